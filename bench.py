@@ -1,0 +1,166 @@
+"""Benchmark of the bucketed CAGRA-style graph build on one MI355X.
+
+A step is one whole graph build -- 3 rounds of (centroids -> probe table ->
+top-2 assignment -> fused MFMA kNN over all buckets -> cross-round merge),
+sanitize, CAGRA prune, reverse-edge merge -- of configuration C2
+(1,000,000 x 128 fp32 integer-valued points, L2, 256 buckets, M 64 -> K 32)
+with the dataset already resident in HBM.  Prints one JSON line.
+
+    python bench.py [--gpus 1] [--steps 3] [--warmup 1] [--config C2]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "gpu-talored-ann_amd"))
+
+PEAK_FP32_MFMA = 157.3e12   # MI355X dense fp32 matrix, FLOP/s
+PEAK_HBM = 8.0e12           # MI355X HBM3E, B/s
+
+
+def recall_at(approx, exact, k):
+    return float(np.mean([len(np.intersect1d(approx[i, :k], exact[i, :k])) / k for i in range(len(exact))]))
+
+
+def cpu_baseline(X, knn_ids, K, n_sample):
+    """The CPU restatement of the reference path (exact kNN -> sanitize ->
+    CAGRA prune -> reverse merge, oracle/gt_oracle.c) timed on this host on a
+    bounded sample and extrapolated to the whole build."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import gt_oracle as O
+    N = len(X)
+    rng = np.random.default_rng(1)
+    q = np.sort(rng.choice(N, n_sample, replace=False))
+    t0 = time.perf_counter()
+    O.knn_exact(X, knn_ids.shape[1], queries=q)
+    t_knn = (time.perf_counter() - t0) * N / n_sample
+    # prune of the sampled rows needs every row they reference: time the
+    # whole-table sanitize + prune + merge on the GPU's own kNN table
+    t0 = time.perf_counter()
+    san = O.sanitize(knn_ids)
+    fwd, rc, _ = O.cagra_prune(san, K)
+    t_prune = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    O.reverse_merge(fwd)
+    t_merge = time.perf_counter() - t0
+    total = t_knn + t_prune + t_merge
+    return {
+        "value": N / total / 1e6, "unit": "Mpts/s", "cores": O.num_threads(), "kind": "port",
+        "sample": f"exact kNN of {n_sample} random queries vs all {N} points, extrapolated x{N / n_sample:.0f} "
+                  f"({t_knn:.1f} s); sanitize+prune ({t_prune:.1f} s) and reverse merge ({t_merge:.1f} s) "
+                  f"measured on the full table",
+        "seconds_extrapolated": total,
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--config", default="C2")
+    ap.add_argument("--rounds", type=int, default=3)
+    ap.add_argument("--cpu-sample", type=int, default=2000)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+              f"(the bucketed build shards by bucket, see DESIGN.md, but no multi-GPU path exists)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import gtann
+    import synth
+
+    cfg = synth.CONFIGS[args.config]
+    X, _ = synth.generate(args.config)
+    N, D = X.shape
+    Xd = torch.from_numpy(X).cuda()
+    torch.cuda.synchronize()
+    ctx = gtann.Context(0)
+    kw = dict(n_buckets=cfg.buckets, M=cfg.M, K=cfg.K, rounds=args.rounds, metric=cfg.metric)
+    for _ in range(args.warmup):
+        ctx.build_graph(Xd, **kw)
+    torch.cuda.synchronize()
+    stats = []
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        res = ctx.build_graph(Xd, **kw)
+        stats.append(res.stats)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / args.steps
+
+    # quality: recall of the pre-prune table vs exact kNN on 10,000 sampled points
+    q = np.random.default_rng(0).choice(N, 10000, replace=False)
+    ex_i, _ = ctx.knn_exact(Xd, 64, queries=torch.from_numpy(q).cuda(), metric=cfg.metric)
+    ex_i = ex_i.cpu().numpy()
+    knn = res.knn_ids.cpu().numpy()
+    rec = {f"recall@{k}": recall_at(knn[q], ex_i, k) for k in (1, 10, 32, 64)}
+    graph = res.graph.cpu().numpy().view(np.uint32)
+    structural = {
+        "bad_ids": int((graph >= N).sum()),
+        "self_loops": int((graph == np.arange(N, dtype=np.uint32)[:, None]).sum()),
+        "dup_edges": int(sum(len(r) - len(np.unique(r)) for r in graph[:20000])),
+        "degree": int(graph.shape[1]),
+    }
+
+    s = {k: float(np.mean([st[k] for st in stats])) for k in stats[0]}
+    launches = args.rounds
+    knn_launch_s = s["t_knn"] / launches
+    flops_launch = s["knn_flops"] / launches
+    achieved = flops_launch / knn_launch_s
+    prune_bytes = N * (4 * cfg.M + 4 * cfg.M * (cfg.M - 1) + 4 * cfg.K)
+    merge_bytes = 28 * N * cfg.K
+
+    out = {
+        "metric": f"graph build Mpts/s at {N // 1000000 if N >= 1000000 else N}"
+                  f"{'M' if N >= 1000000 else ''}x{D} fp32 deg{cfg.K} (build seconds = ms_per_step/1000)",
+        "value": N / wall / 1e6,
+        "unit": "Mpts/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": wall * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic (seeded Gaussian mixture, gpu-talored-ann_amd/synth.py)",
+        "config": {
+            "workload": f"{args.config}: {N} x {D} {cfg.dtype}, {cfg.metric.upper()}, {cfg.buckets} buckets, "
+                        f"M {cfg.M} -> K {cfg.K}, {args.rounds} rounds, nprobe ceil(20000/avg bucket)",
+            "points": N, "dim": D, "buckets": cfg.buckets, "M": cfg.M, "K": cfg.K, "rounds": args.rounds,
+        },
+        "build_seconds": wall,
+        **rec,
+        "structural": structural,
+        "stages_s": {k: s[k] for k in ("t_prepare", "t_bucketing", "t_knn", "t_merge", "t_refine", "t_prune",
+                                       "t_revmerge", "t_download", "t_total")},
+        "roofline": {
+            "kernel": "knn_fused_kernel<128> (one launch per round)",
+            "bound": "mfma", "achieved": achieved / 1e12, "peak": PEAK_FP32_MFMA / 1e12, "unit": "TFLOP/s",
+            "frac": achieved / PEAK_FP32_MFMA, "traffic": None,
+            "flops_per_launch": flops_launch, "launch_ms": knn_launch_s * 1e3,
+        },
+        "roofline_prune": {"bound": "hbm", "achieved": prune_bytes / s["t_prune"] / 1e9, "peak": 8000.0,
+                           "unit": "GB/s", "frac": prune_bytes / s["t_prune"] / PEAK_HBM,
+                           "bytes": prune_bytes, "includes": "sanitize + prune"},
+        "roofline_revmerge": {"bound": "hbm", "achieved": merge_bytes / s["t_revmerge"] / 1e9, "peak": 8000.0,
+                              "unit": "GB/s", "frac": merge_bytes / s["t_revmerge"] / PEAK_HBM,
+                              "bytes": merge_bytes, "includes": "count + scan + scatter + merge"},
+        "max_pool": int(s["max_pool"]), "max_bucket": int(s["max_bucket"]),
+    }
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(X, knn, cfg.K, args.cpu_sample)
+    ctx.close()
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

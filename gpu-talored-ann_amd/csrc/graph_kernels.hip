@@ -1,0 +1,614 @@
+// graph_kernels.hip -- integer graph stages of the build on gfx950:
+// sanitize, CAGRA rank-based detour-count prune, reverse-edge merge,
+// cross-round list merge, id translation, plus layout helpers.
+//
+// All of them are deterministic: no result depends on the order in which
+// atomics land (atomics only count, or fill slots that are re-ordered by a
+// total key before use).
+#include "gtann_common.hpp"
+
+#include <climits>
+#include <cmath>
+
+namespace gtann {
+
+__device__ __forceinline__ void wave_sync_g()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ bool key_less_g(float da, int32_t ia, float db, int32_t ib)
+{
+    return da < db || (da == db && ia < ib);
+}
+
+__device__ __forceinline__ int lower_bound_g(const float* ad, const int32_t* ai, int n, float kd, int32_t ki)
+{
+    int lo = 0, hi = n;
+    while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (key_less_g(ad[mid], ai[mid], kd, ki)) lo = mid + 1;
+        else hi = mid;
+    }
+    return lo;
+}
+
+// ------------------------------------------------------------------ layout
+
+template <typename T>
+__global__ void pad_convert_kernel(const T* __restrict__ src, float* __restrict__ dst, int64_t N, int D, int Dp)
+{
+    const int64_t total = N * Dp;
+    for (int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < total;
+         e += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int64_t r = e / Dp;
+        const int c = static_cast<int>(e - r * Dp);
+        dst[e] = c < D ? static_cast<float>(src[r * D + c]) : 0.f;
+    }
+}
+
+// |x|^2 per row, one wave per row; summed in a fixed order.
+__global__ void __launch_bounds__(256) row_norms_kernel(const float* __restrict__ X, int64_t N, int Dp,
+                                                        float* __restrict__ norms)
+{
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= N) return;
+    float s = 0.f;
+    for (int c = lane; c < Dp; c += 64) {
+        const float v = X[row * Dp + c];
+        s = fmaf(v, v, s);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+    if (lane == 0) norms[row] = s;
+}
+
+// pool list of every bucket = concatenation of member ranges (copy tasks).
+struct CopyTask { int64_t src; int64_t dst; int64_t n; };
+__global__ void copy_ranges_kernel(const CopyTask* __restrict__ tasks, const int32_t* __restrict__ members,
+                                   int32_t* __restrict__ pool)
+{
+    const CopyTask t = tasks[blockIdx.x];
+    for (int64_t e = threadIdx.x; e < t.n; e += blockDim.x) pool[t.dst + e] = members[t.src + e];
+}
+
+__global__ void negate_kernel(float* __restrict__ d, int64_t n)
+{
+    const int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (e < n) d[e] = -d[e];
+}
+
+// ------------------------------------------------------------------ sanitize
+// src/optimize.cu:89-134: -1 / out-of-range / self -> first valid entry of the
+// row, else (i+1) % N.  One wave per row.
+__global__ void __launch_bounds__(256) sanitize_kernel(const int32_t* __restrict__ in, int64_t N, int M,
+                                                       uint32_t* __restrict__ out)
+{
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (i >= N) return;
+    int first = INT_MAX;
+    for (int k = lane; k < M; k += 64) {
+        const int32_t v = in[i * M + k];
+        if (v >= 0 && v < N && v != i) { first = k; break; }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) first = min(first, __shfl_xor(first, o));
+    const uint32_t fallback = first == INT_MAX ? static_cast<uint32_t>((i + 1) % N)
+                                               : static_cast<uint32_t>(in[i * M + first]);
+    for (int k = lane; k < M; k += 64) {
+        const int32_t v = in[i * M + k];
+        out[i * M + k] = (v < 0 || v >= N || v == i) ? fallback : static_cast<uint32_t>(v);
+    }
+}
+
+// ------------------------------------------------------------------ prune
+// CAGRA detour-count prune of one point per wave.
+// count[kAB] = #{kAD < kAB : D = row[kAD] in [0,N), row[kAB] in row(D)},
+// each (kAD, kAB) once, duplicate ids of the row as separate ranks
+// (src/prune_windowed_core.hpp:189-232); output = first K valid entries in
+// (count, rank) order (src/prune_windowed_core.hpp:238-263).
+constexpr int kPruneMaxM = 128;
+constexpr int kPruneCap = 256;   // open-addressing slots, >= 2*M
+
+__global__ void __launch_bounds__(256) cagra_prune_kernel(const int32_t* __restrict__ G, int64_t N, int M, int K,
+                                                          uint32_t* __restrict__ out,
+                                                          unsigned long long* __restrict__ bad_row)
+{
+    __shared__ int32_t hkey[4][kPruneCap];
+    __shared__ int32_t hrank[4][kPruneCap];
+    __shared__ int32_t stamp[4][kPruneMaxM];
+    __shared__ uint32_t cnt[4][kPruneMaxM];
+    __shared__ int32_t sA[4][kPruneMaxM];
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int64_t a = static_cast<int64_t>(blockIdx.x) * 4 + w;
+    if (a >= N) return;
+
+    uint32_t cap = 16;
+    while (cap < 2u * static_cast<uint32_t>(M)) cap <<= 1;
+    const uint32_t mask = cap - 1;
+    for (uint32_t s = lane; s < cap; s += 64) hkey[w][s] = -1;
+    int32_t A[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        const int k = lane + 64 * e;
+        A[e] = k < M ? G[a * M + k] : -1;
+        if (k < M) { stamp[w][k] = -1; cnt[w][k] = 0; sA[w][k] = A[e]; }
+    }
+    wave_sync_g();
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        const int k = lane + 64 * e;
+        if (k < M && A[e] >= 0) {
+            uint32_t h = (static_cast<uint32_t>(A[e]) * 2654435761u) & mask;
+            while (true) {
+                const int32_t old = atomicCAS(&hkey[w][h], -1, A[e]);
+                if (old == -1) { hrank[w][h] = k; break; }
+                h = (h + 1) & mask;
+            }
+        }
+    }
+    wave_sync_g();
+
+    // detour sources, one neighbour row per step, next row prefetched
+    int32_t bcur[2], bnext[2];
+    int kd = 0;
+    auto fetch = [&](int kAD, int32_t (&b)[2]) {
+        const int32_t d = sA[w][kAD];
+        const bool ok = d >= 0 && d < N;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int k = lane + 64 * e;
+            b[e] = (ok && k < M) ? G[static_cast<int64_t>(d) * M + k] : -1;
+        }
+    };
+    if (M > 1) fetch(0, bcur);
+    for (kd = 0; kd < M - 1; ++kd) {
+        if (kd + 1 < M - 1) fetch(kd + 1, bnext);
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int32_t b = bcur[e];
+            if (b < 0) continue;
+            for (uint32_t h = (static_cast<uint32_t>(b) * 2654435761u) & mask; hkey[w][h] != -1; h = (h + 1) & mask) {
+                if (hkey[w][h] != b) continue;
+                const int kab = hrank[w][h];
+                if (kab > kd && atomicExch(&stamp[w][kab], kd) != kd) atomicAdd(&cnt[w][kab], 1u);
+            }
+        }
+        bcur[0] = bnext[0];
+        bcur[1] = bnext[1];
+    }
+    wave_sync_g();
+
+    int nvalid = 0;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        const int k = lane + 64 * e;
+        nvalid += __popcll(__ballot(k < M && A[e] >= 0));
+    }
+    if (nvalid < K) {
+        if (lane == 0) atomicMin(bad_row, static_cast<unsigned long long>(a));
+        return;
+    }
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        const int k = lane + 64 * e;
+        if (k < M && A[e] >= 0) {
+            const uint32_t c = cnt[w][k];
+            int pos = 0;
+            for (int q = 0; q < M; ++q) {
+                const uint32_t cq = cnt[w][q];
+                pos += (sA[w][q] >= 0) && (cq < c || (cq == c && q < k));
+            }
+            if (pos < K) out[a * K + pos] = static_cast<uint32_t>(A[e]);
+        }
+    }
+}
+
+// ------------------------------------------------------------------ reverse merge
+// Reverse edges {dst = fwd[i][k], src = i, rank = k} (src/optimize_chunked.cu:372-407)
+// grouped per dst, ordered by (rank, src) (src/edge_chunk_accumulator.hpp:235-284),
+// and merged into the dst's forward row with K/2 protected slots
+// (src/edge_chunk_accumulator.hpp:471-494).
+
+__global__ void rev_count_kernel(const uint32_t* __restrict__ fwd, int64_t E, int64_t N, uint32_t* __restrict__ deg,
+                                 int* __restrict__ err)
+{
+    const int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (e >= E) return;
+    const uint32_t j = fwd[e];
+    if (j >= N) { atomicExch(err, 1); return; }
+    atomicAdd(&deg[j], 1u);
+}
+
+__global__ void rev_scatter_kernel(const uint32_t* __restrict__ fwd, int64_t E, int64_t N, int K,
+                                   uint32_t* __restrict__ cursor, unsigned long long* __restrict__ keys)
+{
+    const int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (e >= E) return;
+    const uint32_t j = fwd[e];
+    if (j >= N) return;
+    const int64_t i = e / K;
+    const uint32_t k = static_cast<uint32_t>(e - i * K);
+    const uint32_t slot = atomicAdd(&cursor[j], 1u);
+    keys[slot] = (static_cast<unsigned long long>(k) << 32) | static_cast<uint32_t>(i);
+}
+
+// Exclusive scan of n uint32 counts into out[0..n] (out[n] = total).
+constexpr int kScanBlock = 1024;
+__global__ void __launch_bounds__(256) scan_block_kernel(const uint32_t* __restrict__ in, int64_t n,
+                                                         uint32_t* __restrict__ out, uint32_t* __restrict__ sums)
+{
+    __shared__ uint32_t s[256];
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * kScanBlock;
+    uint32_t v[4];
+    uint32_t local = 0;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int64_t e = base + threadIdx.x * 4 + u;
+        v[u] = e < n ? in[e] : 0u;
+        local += v[u];
+    }
+    s[threadIdx.x] = local;
+    __syncthreads();
+    for (int off = 1; off < 256; off <<= 1) {
+        const uint32_t t = threadIdx.x >= off ? s[threadIdx.x - off] : 0u;
+        __syncthreads();
+        s[threadIdx.x] += t;
+        __syncthreads();
+    }
+    uint32_t run = s[threadIdx.x] - local;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int64_t e = base + threadIdx.x * 4 + u;
+        if (e < n) out[e] = run;
+        run += v[u];
+    }
+    if (threadIdx.x == 255) sums[blockIdx.x] = s[255];
+}
+
+__global__ void __launch_bounds__(256) scan_sums_kernel(uint32_t* __restrict__ sums, int64_t nb,
+                                                        uint32_t* __restrict__ total)
+{
+    __shared__ uint32_t s[256];
+    uint32_t carry = 0;
+    for (int64_t b0 = 0; b0 < nb; b0 += 256) {
+        const int64_t e = b0 + threadIdx.x;
+        const uint32_t v = e < nb ? sums[e] : 0u;
+        s[threadIdx.x] = v;
+        __syncthreads();
+        for (int off = 1; off < 256; off <<= 1) {
+            const uint32_t t = threadIdx.x >= off ? s[threadIdx.x - off] : 0u;
+            __syncthreads();
+            s[threadIdx.x] += t;
+            __syncthreads();
+        }
+        if (e < nb) sums[e] = carry + s[threadIdx.x] - v;
+        const uint32_t blk = s[255];
+        __syncthreads();
+        carry += blk;
+    }
+    if (threadIdx.x == 0) *total = carry;
+}
+
+__global__ void scan_add_kernel(uint32_t* __restrict__ out, int64_t n, const uint32_t* __restrict__ sums)
+{
+    const int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (e < n) out[e] += sums[e / kScanBlock];
+}
+
+__device__ __forceinline__ unsigned long long wave_min_u64(unsigned long long v)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const unsigned long long t = __shfl_xor(v, o);
+        v = t < v ? t : v;
+    }
+    return v;
+}
+
+// One wave per dst row.  The final row is
+//   protected S = fwd[j][0..P)  ++  R  ++  (O minus the first occurrence of each r in R)
+// truncated to K, where O = fwd[j][P..K) and R = the distinct sources not in
+// S, by strongest (rank, src) key, at most L = K-P of them.  This is the
+// fixed point of the weakest-first move-to-front insertion of
+// merge_rank_ordered_into_row (an accessed source moves to slot P; absent
+// ones push the last slot out).
+constexpr int kRevMaxK = 64;
+__global__ void __launch_bounds__(256) rev_merge_kernel(const uint32_t* __restrict__ fwd, int64_t N, int K,
+                                                        const uint32_t* __restrict__ off,
+                                                        const unsigned long long* __restrict__ keys,
+                                                        uint32_t* __restrict__ out)
+{
+    __shared__ uint32_t sR[4][kRevMaxK];
+    __shared__ uint32_t sSrc[4][64];
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int64_t j = static_cast<int64_t>(blockIdx.x) * 4 + w;
+    if (j >= N) return;
+    const int P = K / 2, L = K - P;
+    const uint32_t rowv = lane < K ? fwd[j * K + lane] : 0xffffffffu;
+    const uint32_t lo = off[j], hi = off[j + 1];
+    const uint32_t n = hi - lo;
+    const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    int nR = 0;
+
+    auto protected_src = [&](uint32_t s) {
+        bool p = false;
+        for (int q = 0; q < P; ++q) p |= (__shfl(rowv, q) == s);
+        return p;
+    };
+
+    if (n <= 64) {
+        unsigned long long key = lane < static_cast<int>(n) ? keys[lo + lane] : ~0ull;
+        // bitonic sort ascending (keys are unique; sentinels equal)
+#pragma unroll
+        for (int k2 = 2; k2 <= 64; k2 <<= 1) {
+#pragma unroll
+            for (int s = k2 >> 1; s > 0; s >>= 1) {
+                const unsigned long long o = __shfl_xor(key, s);
+                const bool ascending = (lane & k2) == 0;
+                const bool lower = (lane & s) == 0;
+                const bool take = (lower == ascending) ? (o < key) : (o > key);
+                if (take) key = o;
+            }
+        }
+        const bool valid = key != ~0ull;
+        const uint32_t src = static_cast<uint32_t>(key);
+        // cross-lane reads must run with every lane active: a ds_bpermute
+        // from an inactive lane does not return that lane's value
+        const bool prot = protected_src(src);
+        bool keep = valid && !prot;
+        sSrc[w][lane] = src;
+        wave_sync_g();
+        bool dup = false;
+        for (int l2 = 0; l2 < 64; ++l2) dup |= (l2 < lane) && sSrc[w][l2] == src && (l2 < static_cast<int>(n));
+        keep = keep && !dup;
+        const unsigned long long km = __ballot(keep);
+        const int r = __popcll(km & below);
+        if (keep && r < L) sR[w][r] = src;
+        nR = min(L, __popcll(km));
+    } else {
+        unsigned long long last = 0;
+        bool first = true;
+        while (nR < L) {
+            unsigned long long m = ~0ull;
+            for (uint32_t e = lane; e < n; e += 64) {
+                const unsigned long long v = keys[lo + e];
+                if ((first || v > last) && v < m) m = v;
+            }
+            m = wave_min_u64(m);
+            if (m == ~0ull) break;
+            first = false;
+            last = m;
+            const uint32_t src = static_cast<uint32_t>(m);
+            bool skip = protected_src(src);
+            for (int q = 0; q < nR; ++q) skip |= (sR[w][q] == src);
+            if (!skip) {
+                if (lane == 0) sR[w][nR] = src;
+                wave_sync_g();
+                ++nR;
+            }
+        }
+    }
+    wave_sync_g();
+
+    if (lane < P) out[j * K + lane] = rowv;
+    if (lane < nR) out[j * K + P + lane] = sR[w][lane];
+    if (nR < L) {
+        // O entries, in order, minus the first occurrence of each element of R
+        bool inR = false;
+        for (int q = 0; q < nR; ++q) inR |= (sR[w][q] == rowv);
+        bool earlier = false;
+        for (int x = P; x < K; ++x) {
+            const uint32_t vx = __shfl(rowv, x);   // all lanes active (see above)
+            earlier |= (x < lane) && (vx == rowv);
+        }
+        const bool consumed = inR && !earlier;
+        const bool keepO = lane >= P && lane < K && !consumed;
+        const unsigned long long km = __ballot(keepO);
+        const int pos = P + nR + __popcll(km & below);
+        if (keepO && pos < K) out[j * K + pos] = rowv;
+    }
+}
+
+// ------------------------------------------------------------------ cross-round merge
+// top-M by (distance, id) of run U new, an id of new already present in run
+// dropped (src/bucket.cu:5021-5053, ties by id).  One wave per row; both
+// inputs ascending with (-1, +inf) padding at the end.
+constexpr int kMergeMaxM = 128;
+__global__ void __launch_bounds__(256) merge_rounds_kernel(const int32_t* __restrict__ ri, const float* __restrict__ rd,
+                                                           const int32_t* __restrict__ ni, const float* __restrict__ nd,
+                                                           int64_t N, int M, int32_t* __restrict__ oi,
+                                                           float* __restrict__ od)
+{
+    __shared__ float sRd[4][kMergeMaxM], sNd[4][kMergeMaxM];
+    __shared__ int32_t sRi[4][kMergeMaxM], sNi[4][kMergeMaxM];
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + w;
+    if (row >= N) return;
+    float rdv[2], ndv[2];
+    int32_t riv[2], niv[2];
+    int nr = 0;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        const int k = lane + 64 * e;
+        riv[e] = k < M ? ri[row * M + k] : -1;
+        rdv[e] = riv[e] >= 0 ? rd[row * M + k] : INFINITY;
+        niv[e] = k < M ? ni[row * M + k] : -1;
+        ndv[e] = niv[e] >= 0 ? nd[row * M + k] : INFINITY;
+        if (riv[e] < 0) riv[e] = INT_MAX;
+        if (k < kMergeMaxM) { sRd[w][k] = rdv[e]; sRi[w][k] = riv[e]; }
+        nr += __popcll(__ballot(riv[e] != INT_MAX));
+    }
+    wave_sync_g();
+    // drop new ids already in run; compact the survivors (order preserved)
+    bool keep[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        bool dup = false;
+        if (niv[e] >= 0)
+            for (int q = 0; q < nr; ++q) dup |= (sRi[w][q] == niv[e]);
+        keep[e] = niv[e] >= 0 && !dup;
+    }
+    const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    const unsigned long long k0 = __ballot(keep[0]), k1 = __ballot(keep[1]);
+    const int c0 = static_cast<int>(__popcll(k0));
+    const int nn = c0 + static_cast<int>(__popcll(k1));
+    const int cidx[2] = {static_cast<int>(__popcll(k0 & below)), c0 + static_cast<int>(__popcll(k1 & below))};
+#pragma unroll
+    for (int e = 0; e < 2; ++e)
+        if (keep[e]) { sNd[w][cidx[e]] = ndv[e]; sNi[w][cidx[e]] = niv[e]; }
+    wave_sync_g();
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        const int k = lane + 64 * e;
+        if (k < nr) {
+            const int pos = k + lower_bound_g(sNd[w], sNi[w], nn, rdv[e], riv[e]);
+            if (pos < M) { oi[row * M + pos] = riv[e]; od[row * M + pos] = rdv[e]; }
+        }
+        if (keep[e]) {
+            const int pos = cidx[e] + lower_bound_g(sRd[w], sRi[w], nr, ndv[e], niv[e]);
+            if (pos < M) { oi[row * M + pos] = niv[e]; od[row * M + pos] = ndv[e]; }
+        }
+    }
+    for (int p = nr + nn + lane; p < M; p += 64) { oi[row * M + p] = -1; od[row * M + p] = INFINITY; }
+}
+
+// ------------------------------------------------------------------ translate
+// final[inv[i]][k] = inv[g[i][k]] (src/translate_graph_ids.hpp:75); rows hit
+// are counted so the caller can check inv is a permutation.
+__global__ void translate_kernel(const uint32_t* __restrict__ g, const uint32_t* __restrict__ inv, int64_t N, int K,
+                                 uint32_t* __restrict__ out, uint32_t* __restrict__ hits, int* __restrict__ err)
+{
+    const int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (e >= N * K) return;
+    const int64_t i = e / K;
+    const int k = static_cast<int>(e - i * K);
+    const uint32_t r = inv[i];
+    const uint32_t v = g[e];
+    if (r >= N || v >= N) { atomicExch(err, 1); return; }
+    out[static_cast<int64_t>(r) * K + k] = inv[v];
+    if (k == 0) atomicAdd(&hits[r], 1u);
+}
+
+__global__ void check_hits_kernel(const uint32_t* __restrict__ hits, int64_t N, int* __restrict__ err)
+{
+    const int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (e < N && hits[e] != 1u) atomicExch(err, 1);
+}
+
+// ------------------------------------------------------------------ launchers
+
+static unsigned grid_for(int64_t n, int per_block)
+{
+    return static_cast<unsigned>((n + per_block - 1) / per_block);
+}
+
+void launch_pad_convert(const void* src, int dtype, float* dst, int64_t N, int D, int Dp, hipStream_t s)
+{
+    const int64_t total = N * Dp;
+    const unsigned grid = static_cast<unsigned>(std::min<int64_t>((total + 255) / 256, 65536));
+    if (total == 0) return;
+    if (dtype == 0)
+        hipLaunchKernelGGL(pad_convert_kernel<float>, dim3(grid), dim3(256), 0, s, static_cast<const float*>(src), dst, N, D, Dp);
+    else if (dtype == 1)
+        hipLaunchKernelGGL(pad_convert_kernel<uint8_t>, dim3(grid), dim3(256), 0, s, static_cast<const uint8_t*>(src), dst, N, D, Dp);
+    else
+        hipLaunchKernelGGL(pad_convert_kernel<int8_t>, dim3(grid), dim3(256), 0, s, static_cast<const int8_t*>(src), dst, N, D, Dp);
+    GT_HIP(hipGetLastError());
+}
+
+void launch_row_norms(const float* X, int64_t N, int Dp, float* norms, hipStream_t s)
+{
+    if (N <= 0) return;
+    hipLaunchKernelGGL(row_norms_kernel, dim3(grid_for(N, 4)), dim3(256), 0, s, X, N, Dp, norms);
+    GT_HIP(hipGetLastError());
+}
+
+void launch_copy_ranges(const void* tasks, int64_t ntasks, const int32_t* members, int32_t* pool, hipStream_t s)
+{
+    if (ntasks <= 0) return;
+    hipLaunchKernelGGL(copy_ranges_kernel, dim3(static_cast<unsigned>(ntasks)), dim3(256), 0, s,
+                       static_cast<const CopyTask*>(tasks), members, pool);
+    GT_HIP(hipGetLastError());
+}
+
+void launch_negate(float* d, int64_t n, hipStream_t s)
+{
+    if (n <= 0) return;
+    hipLaunchKernelGGL(negate_kernel, dim3(grid_for(n, 256)), dim3(256), 0, s, d, n);
+    GT_HIP(hipGetLastError());
+}
+
+void launch_sanitize(const int32_t* in, int64_t N, int M, uint32_t* out, hipStream_t s)
+{
+    if (N <= 0) return;
+    hipLaunchKernelGGL(sanitize_kernel, dim3(grid_for(N, 4)), dim3(256), 0, s, in, N, M, out);
+    GT_HIP(hipGetLastError());
+}
+
+void launch_cagra_prune(const int32_t* G, int64_t N, int M, int K, uint32_t* out, unsigned long long* bad_row,
+                        hipStream_t s)
+{
+    GT_REQUIRE(M >= 1 && M <= kPruneMaxM, "prune supports intermediate degree <= 128");
+    if (N <= 0) return;
+    hipLaunchKernelGGL(cagra_prune_kernel, dim3(grid_for(N, 4)), dim3(256), 0, s, G, N, M, K, out, bad_row);
+    GT_HIP(hipGetLastError());
+}
+
+void launch_rev_count(const uint32_t* fwd, int64_t N, int K, uint32_t* deg, int* err, hipStream_t s)
+{
+    const int64_t E = N * K;
+    if (E <= 0) return;
+    hipLaunchKernelGGL(rev_count_kernel, dim3(grid_for(E, 256)), dim3(256), 0, s, fwd, E, N, deg, err);
+    GT_HIP(hipGetLastError());
+}
+
+void launch_exclusive_scan(const uint32_t* in, int64_t n, uint32_t* out, uint32_t* sums, hipStream_t s)
+{
+    const int64_t nb = (n + kScanBlock - 1) / kScanBlock;
+    if (n > 0) hipLaunchKernelGGL(scan_block_kernel, dim3(static_cast<unsigned>(nb)), dim3(256), 0, s, in, n, out, sums);
+    hipLaunchKernelGGL(scan_sums_kernel, dim3(1), dim3(256), 0, s, sums, nb, out + n);
+    if (n > 0) hipLaunchKernelGGL(scan_add_kernel, dim3(grid_for(n, 256)), dim3(256), 0, s, out, n, sums);
+    GT_HIP(hipGetLastError());
+}
+
+void launch_rev_scatter(const uint32_t* fwd, int64_t N, int K, uint32_t* cursor, unsigned long long* keys, hipStream_t s)
+{
+    const int64_t E = N * K;
+    if (E <= 0) return;
+    hipLaunchKernelGGL(rev_scatter_kernel, dim3(grid_for(E, 256)), dim3(256), 0, s, fwd, E, N, K, cursor, keys);
+    GT_HIP(hipGetLastError());
+}
+
+void launch_rev_merge(const uint32_t* fwd, int64_t N, int K, const uint32_t* off, const unsigned long long* keys,
+                      uint32_t* out, hipStream_t s)
+{
+    GT_REQUIRE(K >= 1 && K <= kRevMaxK, "reverse merge supports output degree <= 64");
+    if (N <= 0) return;
+    hipLaunchKernelGGL(rev_merge_kernel, dim3(grid_for(N, 4)), dim3(256), 0, s, fwd, N, K, off, keys, out);
+    GT_HIP(hipGetLastError());
+}
+
+void launch_merge_rounds(const int32_t* ri, const float* rd, const int32_t* ni, const float* nd, int64_t N, int M,
+                         int32_t* oi, float* od, hipStream_t s)
+{
+    GT_REQUIRE(M >= 1 && M <= kMergeMaxM, "merge supports list length <= 128");
+    if (N <= 0) return;
+    hipLaunchKernelGGL(merge_rounds_kernel, dim3(grid_for(N, 4)), dim3(256), 0, s, ri, rd, ni, nd, N, M, oi, od);
+    GT_HIP(hipGetLastError());
+}
+
+void launch_translate(const uint32_t* g, const uint32_t* inv, int64_t N, int K, uint32_t* out, uint32_t* hits,
+                      int* err, hipStream_t s)
+{
+    if (N * K <= 0) return;
+    hipLaunchKernelGGL(translate_kernel, dim3(grid_for(N * K, 256)), dim3(256), 0, s, g, inv, N, K, out, hits, err);
+    hipLaunchKernelGGL(check_hits_kernel, dim3(grid_for(N, 256)), dim3(256), 0, s, hits, N, err);
+    GT_HIP(hipGetLastError());
+}
+
+}  // namespace gtann

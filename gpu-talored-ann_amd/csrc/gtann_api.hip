@@ -1,0 +1,996 @@
+// gtann_api.hip -- host orchestration and the C ABI of include/gtann.h.
+//
+// Host C++ owns the control flow (bucketing decisions, work lists, error
+// handling); every data-parallel stage is one of the hand-written kernels of
+// knn_kernels.hip / graph_kernels.hip / refine_kernel.hip on the context's
+// stream.
+#include "gtann_common.hpp"
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstring>
+#include <memory>
+#include <numeric>
+#include <unordered_set>
+#include <vector>
+
+namespace gtann {
+// knn_kernels.hip
+void launch_knn_fused(const KnnArgs& a, hipStream_t stream);
+void launch_merge_partials(const int32_t* pids, const float* pd, int64_t nq, int splits, int M, int32_t* out_ids,
+                           float* out_d, hipStream_t stream);
+// graph_kernels.hip
+void launch_pad_convert(const void* src, int dtype, float* dst, int64_t N, int D, int Dp, hipStream_t s);
+void launch_row_norms(const float* X, int64_t N, int Dp, float* norms, hipStream_t s);
+void launch_copy_ranges(const void* tasks, int64_t ntasks, const int32_t* members, int32_t* pool, hipStream_t s);
+void launch_negate(float* d, int64_t n, hipStream_t s);
+void launch_sanitize(const int32_t* in, int64_t N, int M, uint32_t* out, hipStream_t s);
+void launch_cagra_prune(const int32_t* G, int64_t N, int M, int K, uint32_t* out, unsigned long long* bad_row,
+                        hipStream_t s);
+void launch_rev_count(const uint32_t* fwd, int64_t N, int K, uint32_t* deg, int* err, hipStream_t s);
+void launch_exclusive_scan(const uint32_t* in, int64_t n, uint32_t* out, uint32_t* sums, hipStream_t s);
+void launch_rev_scatter(const uint32_t* fwd, int64_t N, int K, uint32_t* cursor, unsigned long long* keys,
+                        hipStream_t s);
+void launch_rev_merge(const uint32_t* fwd, int64_t N, int K, const uint32_t* off, const unsigned long long* keys,
+                      uint32_t* out, hipStream_t s);
+void launch_merge_rounds(const int32_t* ri, const float* rd, const int32_t* ni, const float* nd, int64_t N, int M,
+                         int32_t* oi, float* od, hipStream_t s);
+void launch_translate(const uint32_t* g, const uint32_t* inv, int64_t N, int K, uint32_t* out, uint32_t* hits,
+                      int* err, hipStream_t s);
+// refine_kernel.hip
+void launch_refine_2hop(const float* X, const float* norms, int64_t N, int Dp, int metric, const int32_t* in_ids,
+                        const float* in_d, int M, int S, int32_t* out_ids, float* out_d, hipStream_t s);
+void launch_centroid_sums(const float* X, int Dp, const int32_t* members, const int64_t* offsets, int64_t C,
+                          float* centroids, hipStream_t s);
+
+struct CopyTaskH { int64_t src; int64_t dst; int64_t n; };
+
+// ---------------------------------------------------------------- device memory
+
+struct DevBuf {
+    void* p = nullptr;
+    size_t cap = 0;
+    DevBuf() = default;
+    DevBuf(const DevBuf&) = delete;
+    DevBuf& operator=(const DevBuf&) = delete;
+    ~DevBuf() { if (p) (void)hipFree(p); }
+    void* ensure(size_t bytes) {
+        if (bytes <= cap) return p;
+        if (p) GT_HIP(hipFree(p));
+        p = nullptr;
+        cap = 0;
+        GT_HIP(hipMalloc(&p, std::max<size_t>(bytes, 256)));
+        cap = std::max<size_t>(bytes, 256);
+        return p;
+    }
+    template <typename T> T* as(size_t n) { return static_cast<T*>(ensure(n * sizeof(T))); }
+};
+
+static bool is_device_ptr(const void* p)
+{
+    if (!p) return false;
+    hipPointerAttribute_t attr;
+    if (hipPointerGetAttributes(&attr, p) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    return attr.type == hipMemoryTypeDevice;
+}
+
+struct Timer {
+    std::chrono::steady_clock::time_point t0 = std::chrono::steady_clock::now();
+    double sec() const { return std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count(); }
+};
+
+}  // namespace gtann
+
+struct gt_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::string err;
+    // named workspaces, grow-only (one slot per role, see gtann::Ws)
+    gtann::DevBuf ws[40];
+    hipEvent_t ev0 = nullptr, ev1 = nullptr;
+};
+
+namespace gtann {
+
+enum Ws {
+    W_X, W_XRAW, W_NORMS, W_C, W_CRAW, W_CNORMS, W_IDS, W_D, W_IDS2, W_D2, W_IDS3, W_D3, W_ITEMS, W_QROWS, W_PROWS,
+    W_MEMBERS, W_TASKS, W_POOL, W_PART_I, W_PART_D, W_G1, W_G2, W_G3, W_DEG, W_OFF, W_CUR, W_KEYS, W_SUMS, W_FLAG,
+    W_TMP, W_OUT, W_IN, W_PROBE_I, W_PROBE_D, W_COUNT_
+};
+static_assert(W_COUNT_ <= 40, "workspace slots");
+
+struct Ctx {
+    gt_ctx* c;
+    hipStream_t s;
+    explicit Ctx(gt_ctx* cc) : c(cc), s(cc->stream) {}
+    template <typename T> T* ws(int slot, size_t n) { return c->ws[slot].as<T>(n); }
+    void sync() { GT_HIP(hipStreamSynchronize(s)); }
+    void h2d(void* dst, const void* src, size_t bytes) {
+        if (bytes) GT_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, s));
+    }
+    void d2h(void* dst, const void* src, size_t bytes) {
+        if (bytes) GT_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, s));
+    }
+    void d2d(void* dst, const void* src, size_t bytes) {
+        if (bytes && dst != src) GT_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, s));
+    }
+    // device view of a caller buffer: the pointer itself if it is device
+    // memory, otherwise a workspace (uploaded when `upload`).
+    template <typename T> T* in(int slot, const T* user, size_t n, bool upload = true) {
+        if (is_device_ptr(user)) return const_cast<T*>(user);
+        T* d = ws<T>(slot, n);
+        if (upload) h2d(d, user, n * sizeof(T));
+        return d;
+    }
+    template <typename T> void out(T* user, const T* dev, size_t n) {
+        if (static_cast<const void*>(user) == static_cast<const void*>(dev)) return;
+        if (is_device_ptr(user)) d2d(user, dev, n * sizeof(T));
+        else d2h(user, dev, n * sizeof(T));
+    }
+    // device-event timing of the work enqueued by f
+    template <typename F> double timed(F&& f) {
+        GT_HIP(hipEventRecord(c->ev0, s));
+        f();
+        GT_HIP(hipEventRecord(c->ev1, s));
+        GT_HIP(hipEventSynchronize(c->ev1));
+        float ms = 0.f;
+        GT_HIP(hipEventElapsedTime(&ms, c->ev0, c->ev1));
+        return ms * 1e-3;
+    }
+};
+
+static int pad_dim(int D) { return (D + 31) / 32 * 32; }
+
+static size_t dtype_size(int dtype)
+{
+    GT_REQUIRE(dtype == GT_DTYPE_F32 || dtype == GT_DTYPE_U8 || dtype == GT_DTYPE_I8, "unknown dtype");
+    return dtype == GT_DTYPE_F32 ? 4 : 1;
+}
+
+struct DevMatrix {
+    const float* data = nullptr;
+    const float* norms = nullptr;
+    int64_t N = 0;
+    int Dp = 0;
+};
+
+// padded fp32 device copy (or the caller's own device buffer when it already
+// has that layout) plus row norms
+static DevMatrix prepare(Ctx& c, int slot_x, int slot_raw, int slot_norms, const void* X, int64_t N, int D, int dtype)
+{
+    GT_REQUIRE(X != nullptr && N > 0 && D > 0, "empty dataset");
+    GT_REQUIRE(N < (int64_t(1) << 31), "N must be < 2^31");
+    const int Dp = pad_dim(D);
+    GT_REQUIRE(Dp <= 256, "dimension > 256 is not supported by this build");
+    const size_t es = dtype_size(dtype);
+    DevMatrix m;
+    m.N = N;
+    m.Dp = Dp;
+    const bool dev = is_device_ptr(X);
+    if (dev && dtype == GT_DTYPE_F32 && D == Dp) {
+        m.data = static_cast<const float*>(X);
+    } else {
+        const void* src = X;
+        if (!dev) {
+            void* raw = c.c->ws[slot_raw].ensure(static_cast<size_t>(N) * D * es);
+            c.h2d(raw, X, static_cast<size_t>(N) * D * es);
+            src = raw;
+        }
+        float* xp = c.ws<float>(slot_x, static_cast<size_t>(N) * Dp);
+        launch_pad_convert(src, dtype, xp, N, D, Dp, c.s);
+        m.data = xp;
+    }
+    float* nrm = c.ws<float>(slot_norms, static_cast<size_t>(N));
+    launch_row_norms(m.data, N, Dp, nrm, c.s);
+    m.norms = nrm;
+    return m;
+}
+
+// Fused kNN of a query list against a pool list, optionally split over the
+// pool for parallelism (partial lists merged afterwards).  Output rows:
+// out_by_id ? query row id : query index.
+struct KnnJob {
+    const DevMatrix* Q;
+    const DevMatrix* P;
+    const int32_t* q_rows = nullptr;   // device, nullptr = identity
+    int64_t nq = 0;
+    const int32_t* p_rows = nullptr;   // device, nullptr = identity
+    int64_t np = 0;
+    int M = 0;
+    int metric = 0;
+    bool exclude_self = true;
+    bool out_pos = false;
+    int32_t* out_ids = nullptr;        // device (nq x M)
+    float* out_d = nullptr;
+};
+
+static void run_knn_flat(Ctx& c, const KnnJob& j, int min_items = 2048)
+{
+    const int64_t qtiles = ceil_div(j.nq, kQueriesPerBlock);
+    int splits = 1;
+    if (qtiles < min_items && j.np > 4096) {
+        const int64_t want = ceil_div(min_items, qtiles);
+        const int64_t by_pool = j.np / 2048;
+        splits = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>({want, by_pool, 2048 / j.M, 64})));
+    }
+    const int64_t chunk = ceil_div(j.np, splits);
+    std::vector<WorkItem> items;
+    items.reserve(static_cast<size_t>(qtiles * splits));
+    for (int s = 0; s < splits; ++s) {
+        const int64_t p0 = s * chunk;
+        const int64_t pc = std::min<int64_t>(chunk, j.np - p0);
+        for (int64_t t = 0; t < qtiles; ++t) {
+            WorkItem it;
+            it.q_begin = t * kQueriesPerBlock;
+            it.q_count = static_cast<int32_t>(std::min<int64_t>(kQueriesPerBlock, j.nq - it.q_begin));
+            it.p_begin = p0;
+            it.p_count = static_cast<int32_t>(std::max<int64_t>(pc, 0));
+            it.out_base = static_cast<int64_t>(s) * j.nq + it.q_begin;
+            items.push_back(it);
+        }
+    }
+    WorkItem* d_items = c.ws<WorkItem>(W_ITEMS, items.size());
+    c.h2d(d_items, items.data(), items.size() * sizeof(WorkItem));
+    int32_t* oi = j.out_ids;
+    float* od = j.out_d;
+    if (splits > 1) {
+        oi = c.ws<int32_t>(W_PART_I, static_cast<size_t>(splits) * j.nq * j.M);
+        od = c.ws<float>(W_PART_D, static_cast<size_t>(splits) * j.nq * j.M);
+    }
+    KnnArgs a{};
+    a.Xq = j.Q->data;
+    a.Xp = j.P->data;
+    a.nq = j.Q->norms;
+    a.np = j.P->norms;
+    a.q_rows = j.q_rows;
+    a.p_rows = j.p_rows;
+    a.items = d_items;
+    a.n_items = static_cast<int32_t>(items.size());
+    a.Dp = j.Q->Dp;
+    a.M = j.M;
+    a.metric = j.metric;
+    a.exclude_self = j.exclude_self ? 1 : 0;
+    a.out_pos = j.out_pos ? 1 : 0;
+    a.out_ids = oi;
+    a.out_d = od;
+    launch_knn_fused(a, c.s);
+    if (splits > 1) launch_merge_partials(oi, od, j.nq, splits, j.M, j.out_ids, j.out_d, c.s);
+}
+
+// ---------------------------------------------------------------- bucketing
+
+static uint64_t splitmix64(uint64_t& x)
+{
+    uint64_t z = (x += 0x9E3779B97F4A7C15ull);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+// C distinct ids of [0, N), ascending (Floyd's sampling, seeded)
+static std::vector<int32_t> sample_ids(int64_t N, int64_t C, uint64_t seed)
+{
+    std::unordered_set<int64_t> chosen;
+    chosen.reserve(static_cast<size_t>(C) * 2);
+    uint64_t st = seed * 0x9E3779B97F4A7C15ull + 0x632BE59BD9B4E019ull;
+    for (int64_t jj = N - C; jj < N; ++jj) {
+        const int64_t t = static_cast<int64_t>(splitmix64(st) % static_cast<uint64_t>(jj + 1));
+        if (!chosen.insert(t).second) chosen.insert(jj);
+    }
+    std::vector<int32_t> ids(chosen.begin(), chosen.end());
+    std::sort(ids.begin(), ids.end());
+    return ids;
+}
+
+struct Buckets {
+    std::vector<int64_t> offsets;   // C+1
+    std::vector<int32_t> members;   // N
+    std::vector<int32_t> probe;     // C x P (bucket indices, -1 = none)
+    int P = 0;
+};
+
+// Two-choice assignment (src/bucket.cu:2276-2302): point i goes to its 2nd
+// nearest centroid if that bucket is smaller than balance x the nearest
+// one's, sizes counted in point order.  Centroids that are data points sit
+// in their own bucket from the start.
+static void assign_two_choice(const std::vector<uint32_t>& top2, int64_t N, int64_t C, float balance,
+                              const std::vector<int32_t>* centroid_ids, std::vector<int32_t>& bucket_of)
+{
+    bucket_of.assign(static_cast<size_t>(N), -1);
+    std::vector<int64_t> size(static_cast<size_t>(C), 0);
+    if (centroid_ids) {
+        for (int64_t c = 0; c < C; ++c) {
+            bucket_of[static_cast<size_t>((*centroid_ids)[static_cast<size_t>(c)])] = static_cast<int32_t>(c);
+            size[static_cast<size_t>(c)] = 1;
+        }
+    }
+    for (int64_t i = 0; i < N; ++i) {
+        if (bucket_of[static_cast<size_t>(i)] >= 0) continue;
+        const uint32_t c1 = top2[static_cast<size_t>(2 * i)];
+        const uint32_t c2 = top2[static_cast<size_t>(2 * i + 1)];
+        GT_REQUIRE(c1 < static_cast<uint64_t>(C), "top-2 assignment returned an invalid centroid");
+        uint32_t chosen = c1;
+        if (balance > 0.f && c2 < static_cast<uint64_t>(C) &&
+            static_cast<double>(size[c2]) < static_cast<double>(balance) * static_cast<double>(size[c1]))
+            chosen = c2;
+        bucket_of[static_cast<size_t>(i)] = static_cast<int32_t>(chosen);
+        size[chosen]++;
+    }
+}
+
+static void csr_from_assignment(const std::vector<int32_t>& bucket_of, int64_t C, Buckets& b)
+{
+    const int64_t N = static_cast<int64_t>(bucket_of.size());
+    b.offsets.assign(static_cast<size_t>(C + 1), 0);
+    for (int64_t i = 0; i < N; ++i) b.offsets[static_cast<size_t>(bucket_of[static_cast<size_t>(i)]) + 1]++;
+    for (int64_t c = 0; c < C; ++c) b.offsets[static_cast<size_t>(c + 1)] += b.offsets[static_cast<size_t>(c)];
+    std::vector<int64_t> cur(b.offsets.begin(), b.offsets.end() - 1);
+    b.members.resize(static_cast<size_t>(N));
+    for (int64_t i = 0; i < N; ++i)
+        b.members[static_cast<size_t>(cur[static_cast<size_t>(bucket_of[static_cast<size_t>(i)])]++)] =
+            static_cast<int32_t>(i);
+}
+
+// One round of pooled kNN into (out_ids, out_d) rows by global id.
+// seed_d (device, optional) caps kept keys at the running M-th distance.
+static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M, int metric, const float* seed_d,
+                             int32_t* out_ids, float* out_d, int64_t* max_pool, int64_t* max_bucket,
+                             double* pairs)
+{
+    const int64_t C = static_cast<int64_t>(b.offsets.size()) - 1;
+    const int64_t N = X.N;
+    std::vector<CopyTaskH> tasks;
+    std::vector<int64_t> pool_off(static_cast<size_t>(C + 1), 0);
+    int64_t total = 0;
+    std::vector<int64_t> segs;
+    for (int64_t bb = 0; bb < C; ++bb) {
+        pool_off[static_cast<size_t>(bb)] = total;
+        segs.clear();
+        segs.push_back(bb);
+        for (int p = 0; p < b.P; ++p) {
+            const int64_t pb = b.probe[static_cast<size_t>(bb * b.P + p)];
+            if (pb < 0 || pb >= C) continue;
+            if (std::find(segs.begin(), segs.end(), pb) != segs.end()) continue;
+            segs.push_back(pb);
+        }
+        for (int64_t sb : segs) {
+            const int64_t lo = b.offsets[static_cast<size_t>(sb)], n = b.offsets[static_cast<size_t>(sb + 1)] - lo;
+            if (n == 0) continue;
+            tasks.push_back({lo, total, n});
+            total += n;
+        }
+    }
+    pool_off[static_cast<size_t>(C)] = total;
+
+    int32_t* d_members = c.ws<int32_t>(W_MEMBERS, static_cast<size_t>(N));
+    c.h2d(d_members, b.members.data(), static_cast<size_t>(N) * sizeof(int32_t));
+    CopyTaskH* d_tasks = c.ws<CopyTaskH>(W_TASKS, tasks.size());
+    c.h2d(d_tasks, tasks.data(), tasks.size() * sizeof(CopyTaskH));
+    int32_t* d_pool = c.ws<int32_t>(W_POOL, static_cast<size_t>(std::max<int64_t>(total, 1)));
+    launch_copy_ranges(d_tasks, static_cast<int64_t>(tasks.size()), d_members, d_pool, c.s);
+
+    std::vector<WorkItem> items;
+    int64_t mp = 0, mb = 0;
+    double pr = 0.0;
+    for (int64_t bb = 0; bb < C; ++bb) {
+        const int64_t q0 = b.offsets[static_cast<size_t>(bb)], nqb = b.offsets[static_cast<size_t>(bb + 1)] - q0;
+        const int64_t p0 = pool_off[static_cast<size_t>(bb)], npb = pool_off[static_cast<size_t>(bb + 1)] - p0;
+        mp = std::max(mp, npb);
+        mb = std::max(mb, nqb);
+        pr += static_cast<double>(nqb) * static_cast<double>(npb);
+        for (int64_t t = 0; t < nqb; t += kQueriesPerBlock) {
+            WorkItem it;
+            it.q_begin = q0 + t;
+            it.q_count = static_cast<int32_t>(std::min<int64_t>(kQueriesPerBlock, nqb - t));
+            it.p_begin = p0;
+            it.p_count = static_cast<int32_t>(npb);
+            it.out_base = -1;
+            items.push_back(it);
+        }
+    }
+    GT_REQUIRE(mp < (int64_t(1) << 31), "pool too large");
+    WorkItem* d_items = c.ws<WorkItem>(W_ITEMS, items.size());
+    c.h2d(d_items, items.data(), items.size() * sizeof(WorkItem));
+
+    KnnArgs a{};
+    a.Xq = X.data;
+    a.Xp = X.data;
+    a.nq = X.norms;
+    a.np = X.norms;
+    a.q_rows = d_members;
+    a.p_rows = d_pool;
+    a.items = d_items;
+    a.n_items = static_cast<int32_t>(items.size());
+    a.Dp = X.Dp;
+    a.M = M;
+    a.metric = metric;
+    a.exclude_self = 1;
+    a.out_pos = 0;
+    a.seed_d = seed_d;
+    a.seed_ld = M;
+    a.out_ids = out_ids;
+    a.out_d = out_d;
+    const double t = c.timed([&] { launch_knn_fused(a, c.s); });
+    if (max_pool) *max_pool = std::max(*max_pool, mp);
+    if (max_bucket) *max_bucket = std::max(*max_bucket, mb);
+    if (pairs) *pairs += pr;
+    return t;
+}
+
+// Centroids + probe table + two-choice assignment of one round.
+static void make_buckets(Ctx& c, const DevMatrix& X, int64_t C, int nprobe, int metric, float balance,
+                         int kmeans_iters, uint64_t seed, Buckets& b)
+{
+    const int64_t N = X.N;
+    C = std::max<int64_t>(1, std::min<int64_t>(C, N));
+    std::vector<int32_t> cid = sample_ids(N, C, seed);
+    int32_t* d_cid = c.ws<int32_t>(W_PROWS, static_cast<size_t>(C));
+    c.h2d(d_cid, cid.data(), static_cast<size_t>(C) * sizeof(int32_t));
+
+    // centroid matrix: the sampled rows themselves, optionally moved to the
+    // means of their members by Lloyd iterations
+    DevMatrix Cm;
+    Cm.N = C;
+    Cm.Dp = X.Dp;
+    float* d_cm = c.ws<float>(W_C, static_cast<size_t>(C) * X.Dp);
+    float* d_cn = c.ws<float>(W_CNORMS, static_cast<size_t>(C));
+    // gather centroid rows via the pool-copy kernel on a float view: row r of
+    // X is Dp floats; copy as int32 words (bit-exact)
+    {
+        std::vector<CopyTaskH> tasks(static_cast<size_t>(C));
+        for (int64_t k = 0; k < C; ++k)
+            tasks[static_cast<size_t>(k)] = {static_cast<int64_t>(cid[static_cast<size_t>(k)]) * X.Dp, k * X.Dp, X.Dp};
+        CopyTaskH* d_tasks = c.ws<CopyTaskH>(W_TASKS, tasks.size());
+        c.h2d(d_tasks, tasks.data(), tasks.size() * sizeof(CopyTaskH));
+        launch_copy_ranges(d_tasks, C, reinterpret_cast<const int32_t*>(X.data), reinterpret_cast<int32_t*>(d_cm),
+                           c.s);
+    }
+    launch_row_norms(d_cm, C, X.Dp, d_cn, c.s);
+    Cm.data = d_cm;
+    Cm.norms = d_cn;
+
+    std::vector<uint32_t> top2(static_cast<size_t>(2 * N));
+    int32_t* d_t2 = c.ws<int32_t>(W_IDS3, static_cast<size_t>(2 * N));
+    float* d_t2d = c.ws<float>(W_D3, static_cast<size_t>(2 * N));
+    std::vector<int32_t> bucket_of;
+    const bool data_points = kmeans_iters <= 0;
+    for (int it = 0; it <= std::max(0, kmeans_iters); ++it) {
+        KnnJob j;
+        j.Q = &X;
+        j.P = &Cm;
+        j.nq = N;
+        j.np = C;
+        j.M = std::min<int64_t>(2, C);
+        j.metric = metric;
+        j.exclude_self = false;
+        j.out_pos = true;
+        j.out_ids = d_t2;
+        j.out_d = d_t2d;
+        if (j.M == 2) {
+            run_knn_flat(c, j, 1);
+            c.d2h(top2.data(), d_t2, top2.size() * sizeof(uint32_t));
+            c.sync();
+        } else {
+            std::fill(top2.begin(), top2.end(), 0u);
+            for (int64_t i = 0; i < N; ++i) top2[static_cast<size_t>(2 * i + 1)] = 0xffffffffu;
+        }
+        if (it < kmeans_iters) {
+            // Lloyd step: nearest-centroid assignment, then member means
+            std::vector<int32_t> nearest(static_cast<size_t>(N));
+            for (int64_t i = 0; i < N; ++i) nearest[static_cast<size_t>(i)] = static_cast<int32_t>(top2[static_cast<size_t>(2 * i)]);
+            Buckets tmp;
+            csr_from_assignment(nearest, C, tmp);
+            int32_t* d_mem = c.ws<int32_t>(W_MEMBERS, static_cast<size_t>(N));
+            c.h2d(d_mem, tmp.members.data(), static_cast<size_t>(N) * sizeof(int32_t));
+            int64_t* d_off = c.ws<int64_t>(W_OFF, static_cast<size_t>(C + 1));
+            c.h2d(d_off, tmp.offsets.data(), static_cast<size_t>(C + 1) * sizeof(int64_t));
+            launch_centroid_sums(X.data, X.Dp, d_mem, d_off, C, d_cm, c.s);
+            launch_row_norms(d_cm, C, X.Dp, d_cn, c.s);
+        }
+    }
+    assign_two_choice(top2, N, C, balance, data_points ? &cid : nullptr, bucket_of);
+    csr_from_assignment(bucket_of, C, b);
+
+    // probe table: nprobe nearest other centroids
+    b.P = static_cast<int>(std::min<int64_t>(nprobe, C - 1));
+    b.probe.assign(static_cast<size_t>(C) * std::max(b.P, 0), -1);
+    if (b.P > 0) {
+        int32_t* d_pi = c.ws<int32_t>(W_PROBE_I, static_cast<size_t>(C) * b.P);
+        float* d_pd = c.ws<float>(W_PROBE_D, static_cast<size_t>(C) * b.P);
+        KnnJob j;
+        j.Q = &Cm;
+        j.P = &Cm;
+        j.nq = C;
+        j.np = C;
+        j.M = b.P;
+        j.metric = metric;
+        j.exclude_self = true;
+        j.out_pos = true;
+        j.out_ids = d_pi;
+        j.out_d = d_pd;
+        run_knn_flat(c, j, 1);
+        c.d2h(b.probe.data(), d_pi, b.probe.size() * sizeof(int32_t));
+        c.sync();
+    }
+}
+
+// ---------------------------------------------------------------- graph stages
+
+static void prune_device(Ctx& c, const int32_t* G, int64_t N, int M, int K, uint32_t* out)
+{
+    GT_REQUIRE(K >= 1 && K <= M, "output degree must be in [1, M]");
+    unsigned long long* bad = c.ws<unsigned long long>(W_FLAG, 1);
+    const unsigned long long init = ~0ull;
+    c.h2d(bad, &init, sizeof(init));
+    launch_cagra_prune(G, N, M, K, out, bad, c.s);
+    unsigned long long h = 0;
+    c.d2h(&h, bad, sizeof(h));
+    c.sync();
+    if (h != ~0ull)
+        throw Error(GT_EFEWCAND, "prune: row " + std::to_string(h) +
+                                     " has fewer than output_degree valid candidates");
+}
+
+static void reverse_merge_device(Ctx& c, const uint32_t* fwd, int64_t N, int K, uint32_t* out)
+{
+    GT_REQUIRE(K >= 1 && K <= 64, "output degree must be in [1, 64]");
+    GT_REQUIRE(N * K < (int64_t(1) << 32), "too many edges for 32-bit offsets");
+    uint32_t* deg = c.ws<uint32_t>(W_DEG, static_cast<size_t>(N));
+    uint32_t* off = c.ws<uint32_t>(W_OFF, static_cast<size_t>(N + 1));
+    uint32_t* cur = c.ws<uint32_t>(W_CUR, static_cast<size_t>(N + 1));
+    uint32_t* sums = c.ws<uint32_t>(W_SUMS, static_cast<size_t>(ceil_div(N, 1024) + 1));
+    unsigned long long* keys = c.ws<unsigned long long>(W_KEYS, static_cast<size_t>(N * K));
+    int* err = c.ws<int>(W_TMP, 1);
+    GT_HIP(hipMemsetAsync(deg, 0, static_cast<size_t>(N) * sizeof(uint32_t), c.s));
+    GT_HIP(hipMemsetAsync(err, 0, sizeof(int), c.s));
+    launch_rev_count(fwd, N, K, deg, err, c.s);
+    launch_exclusive_scan(deg, N, off, sums, c.s);
+    c.d2d(cur, off, static_cast<size_t>(N) * sizeof(uint32_t));
+    launch_rev_scatter(fwd, N, K, cur, keys, c.s);
+    launch_rev_merge(fwd, N, K, off, keys, out, c.s);
+    int h = 0;
+    c.d2h(&h, err, sizeof(int));
+    c.sync();
+    if (h) throw Error(GT_EINVAL, "reverse merge: forward graph holds an id >= N");
+}
+
+}  // namespace gtann
+
+using namespace gtann;
+
+template <typename F>
+static int guarded(gt_ctx* ctx, F&& f)
+{
+    if (!ctx) return GT_EINVAL;
+    try {
+        GT_HIP(hipSetDevice(ctx->device));
+        ctx->err.clear();
+        f();
+        return GT_OK;
+    } catch (const Error& e) {
+        ctx->err = e.what();
+        (void)hipStreamSynchronize(ctx->stream);
+        return e.code;
+    } catch (const std::exception& e) {
+        ctx->err = e.what();
+        return GT_EINVAL;
+    } catch (...) {
+        ctx->err = "unknown error";
+        return GT_EINVAL;
+    }
+}
+
+extern "C" {
+
+const char* gt_version(void) { return "gtann-gfx950 0.1"; }
+
+int gt_create(int device, gt_ctx** out)
+{
+    if (!out) return GT_EINVAL;
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || device < 0 || device >= n) return GT_EDEVICE;
+    gt_ctx* c = new (std::nothrow) gt_ctx();
+    if (!c) return GT_ENOMEM;
+    c->device = device;
+    if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreate(&c->ev0) != hipSuccess || hipEventCreate(&c->ev1) != hipSuccess) {
+        delete c;
+        return GT_EDEVICE;
+    }
+    *out = c;
+    return GT_OK;
+}
+
+void gt_destroy(gt_ctx* ctx)
+{
+    if (!ctx) return;
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    for (auto& b : ctx->ws) {
+        if (b.p) (void)hipFree(b.p);
+        b.p = nullptr;
+        b.cap = 0;
+    }
+    if (ctx->ev0) (void)hipEventDestroy(ctx->ev0);
+    if (ctx->ev1) (void)hipEventDestroy(ctx->ev1);
+    if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+}
+
+const char* gt_last_error(const gt_ctx* ctx) { return ctx ? ctx->err.c_str() : "null context"; }
+
+void gt_build_params_default(gt_build_params* p)
+{
+    if (!p) return;
+    p->metric = GT_METRIC_L2;
+    p->n_buckets = 0;   // 0 = N / 4000
+    p->nprobe = -1;     // -1 = ceil(20000 / avg bucket) (sk/scripts/dataset_env.py:12,56)
+    p->M = 64;
+    p->K = 32;
+    p->rounds = 3;
+    p->refine_passes = 0;
+    p->refine_sample = 16;
+    p->kmeans_iters = 0;
+    p->balance = 0.8f;
+    p->seed = 42;
+}
+
+int gt_knn_exact(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtype, int metric, const int64_t* queries,
+                 int64_t nq, int32_t k, int32_t* ids, float* dists)
+{
+    return guarded(ctx, [&] {
+        GT_REQUIRE(ids && dists && k >= 1 && k <= 128, "k must be in [1, 128]");
+        GT_REQUIRE(metric == GT_METRIC_L2 || metric == GT_METRIC_IP, "unknown metric");
+        GT_REQUIRE(queries || nq == N, "nq must equal N when queries is NULL");
+        Ctx c(ctx);
+        DevMatrix Xm = prepare(c, W_X, W_XRAW, W_NORMS, X, N, D, dtype);
+        int32_t* d_q = nullptr;
+        if (queries) {
+            std::vector<int64_t> hq(static_cast<size_t>(nq));
+            if (is_device_ptr(queries)) {
+                c.d2h(hq.data(), queries, static_cast<size_t>(nq) * sizeof(int64_t));
+                c.sync();
+            } else {
+                std::memcpy(hq.data(), queries, static_cast<size_t>(nq) * sizeof(int64_t));
+            }
+            std::vector<int32_t> q32(static_cast<size_t>(nq));
+            for (int64_t i = 0; i < nq; ++i) {
+                GT_REQUIRE(hq[static_cast<size_t>(i)] >= 0 && hq[static_cast<size_t>(i)] < N, "query id out of range");
+                q32[static_cast<size_t>(i)] = static_cast<int32_t>(hq[static_cast<size_t>(i)]);
+            }
+            d_q = c.ws<int32_t>(W_QROWS, static_cast<size_t>(nq));
+            c.h2d(d_q, q32.data(), q32.size() * sizeof(int32_t));
+        }
+        if (nq == 0) return;
+        int32_t* oi = c.in<int32_t>(W_IDS, ids, static_cast<size_t>(nq) * k, false);
+        float* od = c.in<float>(W_D, dists, static_cast<size_t>(nq) * k, false);
+        KnnJob j;
+        j.Q = &Xm;
+        j.P = &Xm;
+        j.q_rows = d_q;
+        j.nq = nq;
+        j.np = N;
+        j.M = k;
+        j.metric = metric;
+        j.exclude_self = true;
+        j.out_ids = oi;
+        j.out_d = od;
+        run_knn_flat(c, j);
+        if (metric == GT_METRIC_IP) launch_negate(od, nq * k, c.s);
+        c.out(ids, oi, static_cast<size_t>(nq) * k);
+        c.out(dists, od, static_cast<size_t>(nq) * k);
+        c.sync();
+    });
+}
+
+int gt_assign_top2(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtype, int metric, const void* C,
+                   int64_t nC, uint32_t* top2, float* d2)
+{
+    return guarded(ctx, [&] {
+        GT_REQUIRE(top2 && d2 && nC >= 1, "bad arguments");
+        Ctx c(ctx);
+        DevMatrix Xm = prepare(c, W_X, W_XRAW, W_NORMS, X, N, D, dtype);
+        DevMatrix Cm = prepare(c, W_C, W_CRAW, W_CNORMS, C, nC, D, dtype);
+        int32_t* oi = c.in<int32_t>(W_IDS, reinterpret_cast<int32_t*>(top2), static_cast<size_t>(N) * 2, false);
+        float* od = c.in<float>(W_D, d2, static_cast<size_t>(N) * 2, false);
+        KnnJob j;
+        j.Q = &Xm;
+        j.P = &Cm;
+        j.nq = N;
+        j.np = nC;
+        j.M = 2;
+        j.metric = metric;
+        j.exclude_self = false;
+        j.out_pos = true;
+        j.out_ids = oi;
+        j.out_d = od;
+        run_knn_flat(c, j, 1);
+        if (metric == GT_METRIC_IP) launch_negate(od, N * 2, c.s);
+        c.out(reinterpret_cast<int32_t*>(top2), oi, static_cast<size_t>(N) * 2);
+        c.out(d2, od, static_cast<size_t>(N) * 2);
+        c.sync();
+    });
+}
+
+int gt_knn_bucketed(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtype, int metric, const int64_t* offsets,
+                    const int32_t* members, int64_t nB, const int32_t* probe, int32_t P, int32_t M, int32_t* ids,
+                    float* dists, int merge)
+{
+    return guarded(ctx, [&] {
+        GT_REQUIRE(offsets && members && ids && dists && nB >= 1 && M >= 1 && M <= 128 && P >= 0, "bad arguments");
+        GT_REQUIRE(P == 0 || probe, "probe table missing");
+        Ctx c(ctx);
+        Buckets b;
+        b.offsets.resize(static_cast<size_t>(nB + 1));
+        b.members.resize(static_cast<size_t>(N));
+        b.probe.resize(static_cast<size_t>(nB) * P);
+        b.P = P;
+        auto fetch = [&](void* dst, const void* src, size_t bytes) {
+            if (is_device_ptr(src)) { c.d2h(dst, src, bytes); c.sync(); }
+            else std::memcpy(dst, src, bytes);
+        };
+        fetch(b.offsets.data(), offsets, b.offsets.size() * sizeof(int64_t));
+        fetch(b.members.data(), members, b.members.size() * sizeof(int32_t));
+        if (P > 0) fetch(b.probe.data(), probe, b.probe.size() * sizeof(int32_t));
+        GT_REQUIRE(b.offsets[0] == 0 && b.offsets[static_cast<size_t>(nB)] == N, "offsets must span all N points");
+        {
+            std::vector<uint8_t> seen(static_cast<size_t>(N), 0);
+            for (int64_t bb = 0; bb < nB; ++bb)
+                GT_REQUIRE(b.offsets[static_cast<size_t>(bb + 1)] >= b.offsets[static_cast<size_t>(bb)], "offsets must be non-decreasing");
+            for (int64_t i = 0; i < N; ++i) {
+                const int32_t m = b.members[static_cast<size_t>(i)];
+                GT_REQUIRE(m >= 0 && m < N && !seen[static_cast<size_t>(m)], "members must be a permutation of [0, N)");
+                seen[static_cast<size_t>(m)] = 1;
+            }
+        }
+        DevMatrix Xm = prepare(c, W_X, W_XRAW, W_NORMS, X, N, D, dtype);
+        const size_t nm = static_cast<size_t>(N) * M;
+        int32_t* cur_i = c.ws<int32_t>(W_IDS, nm);
+        float* cur_d = c.ws<float>(W_D, nm);
+        const float* seed = nullptr;
+        int32_t* run_i = nullptr;
+        float* run_d = nullptr;
+        if (merge) {
+            run_i = c.in<int32_t>(W_IDS2, ids, nm);
+            run_d = c.in<float>(W_D2, dists, nm);
+            if (metric == GT_METRIC_IP) {
+                float* tmp = c.ws<float>(W_D3, nm);
+                c.d2d(tmp, run_d, nm * sizeof(float));
+                launch_negate(tmp, static_cast<int64_t>(nm), c.s);
+                run_d = tmp;
+            }
+            seed = run_d;
+        }
+        bucketed_round(c, Xm, b, M, metric, seed, cur_i, cur_d, nullptr, nullptr, nullptr);
+        int32_t* res_i = cur_i;
+        float* res_d = cur_d;
+        if (merge) {
+            int32_t* mi = c.ws<int32_t>(W_G1, nm);
+            float* md = c.ws<float>(W_G2, nm);
+            launch_merge_rounds(run_i, run_d, cur_i, cur_d, N, M, mi, md, c.s);
+            res_i = mi;
+            res_d = md;
+        }
+        if (metric == GT_METRIC_IP) launch_negate(res_d, static_cast<int64_t>(nm), c.s);
+        c.out(ids, res_i, nm);
+        c.out(dists, res_d, nm);
+        c.sync();
+    });
+}
+
+int gt_merge_rounds(gt_ctx* ctx, const int32_t* run_ids, const float* run_d, const int32_t* new_ids,
+                    const float* new_d, int64_t N, int32_t M, int32_t* out_ids, float* out_d)
+{
+    return guarded(ctx, [&] {
+        GT_REQUIRE(run_ids && run_d && new_ids && new_d && out_ids && out_d && N >= 0 && M >= 1 && M <= 128,
+                   "bad arguments");
+        Ctx c(ctx);
+        const size_t nm = static_cast<size_t>(N) * M;
+        const int32_t* ri = c.in<int32_t>(W_IDS, run_ids, nm);
+        const float* rd = c.in<float>(W_D, run_d, nm);
+        const int32_t* ni = c.in<int32_t>(W_IDS2, new_ids, nm);
+        const float* nd = c.in<float>(W_D2, new_d, nm);
+        int32_t* oi = c.ws<int32_t>(W_G1, nm);
+        float* od = c.ws<float>(W_G2, nm);
+        launch_merge_rounds(ri, rd, ni, nd, N, M, oi, od, c.s);
+        c.out(out_ids, oi, nm);
+        c.out(out_d, od, nm);
+        c.sync();
+    });
+}
+
+int gt_refine_2hop(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtype, int metric, int32_t M, int32_t S,
+                   int32_t passes, int32_t* ids, float* dists)
+{
+    return guarded(ctx, [&] {
+        GT_REQUIRE(ids && dists && M >= 1 && M <= 128 && S >= 1 && S <= M && S * S <= 1024 && passes >= 0,
+                   "bad arguments (need 1 <= S <= M, S*S <= 1024)");
+        Ctx c(ctx);
+        DevMatrix Xm = prepare(c, W_X, W_XRAW, W_NORMS, X, N, D, dtype);
+        const size_t nm = static_cast<size_t>(N) * M;
+        int32_t* ai = c.ws<int32_t>(W_IDS, nm);
+        float* ad = c.ws<float>(W_D, nm);
+        c.d2d(ai, c.in<int32_t>(W_IDS2, ids, nm), nm * sizeof(int32_t));
+        c.d2d(ad, c.in<float>(W_D2, dists, nm), nm * sizeof(float));
+        if (metric == GT_METRIC_IP) launch_negate(ad, static_cast<int64_t>(nm), c.s);
+        int32_t* bi = c.ws<int32_t>(W_G1, nm);
+        float* bd = c.ws<float>(W_G2, nm);
+        for (int p = 0; p < passes; ++p) {
+            launch_refine_2hop(Xm.data, Xm.norms, N, Xm.Dp, metric, ai, ad, M, S, bi, bd, c.s);
+            std::swap(ai, bi);
+            std::swap(ad, bd);
+        }
+        if (metric == GT_METRIC_IP) launch_negate(ad, static_cast<int64_t>(nm), c.s);
+        c.out(ids, ai, nm);
+        c.out(dists, ad, nm);
+        c.sync();
+    });
+}
+
+int gt_sanitize(gt_ctx* ctx, const int32_t* knn, int64_t N, int32_t M, uint32_t* out)
+{
+    return guarded(ctx, [&] {
+        GT_REQUIRE(knn && out && N >= 1 && M >= 1, "bad arguments");
+        Ctx c(ctx);
+        const size_t nm = static_cast<size_t>(N) * M;
+        const int32_t* in = c.in<int32_t>(W_IN, knn, nm);
+        uint32_t* o = c.ws<uint32_t>(W_OUT, nm);
+        launch_sanitize(in, N, M, o, c.s);
+        c.out(out, o, nm);
+        c.sync();
+    });
+}
+
+int gt_cagra_prune(gt_ctx* ctx, const uint32_t* knn, int64_t N, int32_t M, int32_t K, uint32_t* out)
+{
+    return guarded(ctx, [&] {
+        GT_REQUIRE(knn && out && N >= 1 && M >= 1, "bad arguments");
+        GT_REQUIRE(N < (int64_t(1) << 31), "N must be < 2^31");
+        Ctx c(ctx);
+        const size_t nm = static_cast<size_t>(N) * M;
+        const uint32_t* in = c.in<uint32_t>(W_IN, knn, nm);
+        uint32_t* o = c.ws<uint32_t>(W_OUT, static_cast<size_t>(N) * K);
+        prune_device(c, reinterpret_cast<const int32_t*>(in), N, M, K, o);
+        c.out(out, o, static_cast<size_t>(N) * K);
+        c.sync();
+    });
+}
+
+int gt_reverse_merge(gt_ctx* ctx, const uint32_t* fwd, int64_t N, int32_t K, uint32_t* out)
+{
+    return guarded(ctx, [&] {
+        GT_REQUIRE(fwd && out && N >= 1 && K >= 1, "bad arguments");
+        Ctx c(ctx);
+        const size_t nk = static_cast<size_t>(N) * K;
+        const uint32_t* in = c.in<uint32_t>(W_IN, fwd, nk);
+        uint32_t* o = c.ws<uint32_t>(W_OUT, nk);
+        reverse_merge_device(c, in, N, K, o);
+        c.out(out, o, nk);
+        c.sync();
+    });
+}
+
+int gt_optimize(gt_ctx* ctx, const uint32_t* knn, int64_t N, int32_t M, int32_t K, uint32_t* out)
+{
+    return guarded(ctx, [&] {
+        GT_REQUIRE(knn && out && N >= 1 && M >= 1, "bad arguments");
+        Ctx c(ctx);
+        const size_t nm = static_cast<size_t>(N) * M, nk = static_cast<size_t>(N) * K;
+        const uint32_t* in = c.in<uint32_t>(W_IN, knn, nm);
+        uint32_t* f = c.ws<uint32_t>(W_G3, nk);
+        prune_device(c, reinterpret_cast<const int32_t*>(in), N, M, K, f);
+        uint32_t* o = c.ws<uint32_t>(W_OUT, nk);
+        reverse_merge_device(c, f, N, K, o);
+        c.out(out, o, nk);
+        c.sync();
+    });
+}
+
+int gt_translate(gt_ctx* ctx, const uint32_t* g, const uint32_t* inv, int64_t N, int32_t K, uint32_t* out)
+{
+    return guarded(ctx, [&] {
+        GT_REQUIRE(g && inv && out && N >= 1 && K >= 1, "bad arguments");
+        Ctx c(ctx);
+        const size_t nk = static_cast<size_t>(N) * K;
+        const uint32_t* dg = c.in<uint32_t>(W_IN, g, nk);
+        const uint32_t* dinv = c.in<uint32_t>(W_CUR, inv, static_cast<size_t>(N));
+        uint32_t* o = c.ws<uint32_t>(W_OUT, nk);
+        uint32_t* hits = c.ws<uint32_t>(W_DEG, static_cast<size_t>(N));
+        int* err = c.ws<int>(W_TMP, 1);
+        GT_HIP(hipMemsetAsync(hits, 0, static_cast<size_t>(N) * sizeof(uint32_t), c.s));
+        GT_HIP(hipMemsetAsync(err, 0, sizeof(int), c.s));
+        launch_translate(dg, dinv, N, K, o, hits, err, c.s);
+        int h = 0;
+        c.d2h(&h, err, sizeof(int));
+        c.sync();
+        if (h) throw Error(GT_EINVAL, "translate: ids out of range or inverse_perm is not a permutation");
+        c.out(out, o, nk);
+        c.sync();
+    });
+}
+
+int gt_build_graph(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtype, const gt_build_params* params,
+                   int32_t* knn_ids, float* knn_dists, uint32_t* graph, gt_build_stats* stats)
+{
+    return guarded(ctx, [&] {
+        GT_REQUIRE(params && graph, "bad arguments");
+        gt_build_params p = *params;
+        GT_REQUIRE(p.metric == GT_METRIC_L2 || p.metric == GT_METRIC_IP, "unknown metric");
+        GT_REQUIRE(p.M >= 1 && p.M <= 128 && p.K >= 1 && p.K <= std::min(p.M, 64) && p.rounds >= 1, "bad degrees");
+        GT_REQUIRE(N > p.M, "need N > M");
+        Timer total;
+        gt_build_stats st{};
+        Ctx c(ctx);
+        Timer tp;
+        DevMatrix Xm = prepare(c, W_X, W_XRAW, W_NORMS, X, N, D, dtype);
+        c.sync();
+        st.t_prepare = tp.sec();
+        int64_t C = p.n_buckets > 0 ? p.n_buckets : std::max<int64_t>(1, N / 4000);
+        C = std::min<int64_t>(C, N);
+        int nprobe = p.nprobe;
+        if (nprobe < 0) nprobe = static_cast<int>(std::ceil(20000.0 / (static_cast<double>(N) / C)));
+        nprobe = static_cast<int>(std::min<int64_t>(nprobe, C - 1));
+
+        const size_t nm = static_cast<size_t>(N) * p.M;
+        int32_t* run_i = c.ws<int32_t>(W_G1, nm);
+        float* run_d = c.ws<float>(W_G2, nm);
+        int32_t* cur_i = c.ws<int32_t>(W_IDS, nm);
+        float* cur_d = c.ws<float>(W_D, nm);
+        int32_t* tmp_i = c.ws<int32_t>(W_IDS2, nm);
+        float* tmp_d = c.ws<float>(W_D2, nm);
+        for (int r = 0; r < p.rounds; ++r) {
+            Timer tb;
+            Buckets b;
+            make_buckets(c, Xm, C, nprobe, p.metric, p.balance, p.kmeans_iters, p.seed + static_cast<uint64_t>(r), b);
+            st.t_bucketing += tb.sec();
+            if (r == 0) {
+                st.t_knn += bucketed_round(c, Xm, b, p.M, p.metric, nullptr, run_i, run_d, &st.max_pool,
+                                           &st.max_bucket, &st.knn_pairs);
+            } else {
+                st.t_knn += bucketed_round(c, Xm, b, p.M, p.metric, run_d, cur_i, cur_d, &st.max_pool,
+                                           &st.max_bucket, &st.knn_pairs);
+                st.t_merge += c.timed([&] { launch_merge_rounds(run_i, run_d, cur_i, cur_d, N, p.M, tmp_i, tmp_d, c.s); });
+                std::swap(run_i, tmp_i);
+                std::swap(run_d, tmp_d);
+            }
+        }
+        if (p.refine_passes > 0) {
+            GT_REQUIRE(p.refine_sample >= 1 && p.refine_sample <= p.M && p.refine_sample * p.refine_sample <= 1024,
+                       "bad refine sample");
+            for (int pass = 0; pass < p.refine_passes; ++pass) {
+                st.t_refine += c.timed([&] {
+                    launch_refine_2hop(Xm.data, Xm.norms, N, Xm.Dp, p.metric, run_i, run_d, p.M, p.refine_sample,
+                                       tmp_i, tmp_d, c.s);
+                });
+                std::swap(run_i, tmp_i);
+                std::swap(run_d, tmp_d);
+            }
+        }
+        st.knn_flops = 2.0 * D * st.knn_pairs;
+        // sanitize + prune + reverse merge
+        uint32_t* san = c.ws<uint32_t>(W_OUT, nm);
+        uint32_t* fwd = c.ws<uint32_t>(W_G3, static_cast<size_t>(N) * p.K);
+        uint32_t* fin = c.ws<uint32_t>(W_IN, static_cast<size_t>(N) * p.K);
+        st.t_prune = c.timed([&] { launch_sanitize(run_i, N, p.M, san, c.s); });
+        st.t_prune += c.timed([&] { prune_device(c, reinterpret_cast<const int32_t*>(san), N, p.M, p.K, fwd); });
+        st.t_revmerge = c.timed([&] { reverse_merge_device(c, fwd, N, p.K, fin); });
+        Timer td;
+        if (knn_ids) c.out(knn_ids, run_i, nm);
+        if (knn_dists) {
+            if (p.metric == GT_METRIC_IP) launch_negate(run_d, static_cast<int64_t>(nm), c.s);
+            c.out(knn_dists, run_d, nm);
+        }
+        c.out(graph, fin, static_cast<size_t>(N) * p.K);
+        c.sync();
+        st.t_download = td.sec();
+        st.t_total = total.sec();
+        if (stats) *stats = st;
+    });
+}
+
+}  // extern "C"

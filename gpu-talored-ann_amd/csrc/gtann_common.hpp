@@ -1,0 +1,73 @@
+// gtann_common.hpp -- shared definitions of the gfx950 graph-build library.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "../../include/gtann.h"
+
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+
+namespace gtann {
+
+struct Error : std::runtime_error {
+    int code;
+    Error(int c, const std::string& m) : std::runtime_error(m), code(c) {}
+};
+
+#define GT_HIP(call)                                                                         \
+    do {                                                                                     \
+        hipError_t e_ = (call);                                                              \
+        if (e_ != hipSuccess)                                                                \
+            throw ::gtann::Error(e_ == hipErrorOutOfMemory ? GT_ENOMEM                        \
+                                                           : GT_EDEVICE,                     \
+                                 std::string(#call) + ": " + hipGetErrorString(e_) + " at " + \
+                                     __FILE__ + ":" + std::to_string(__LINE__));             \
+    } while (0)
+
+#define GT_REQUIRE(cond, msg)                                                  \
+    do {                                                                       \
+        if (!(cond)) throw ::gtann::Error(GT_EINVAL, std::string(msg));          \
+    } while (0)
+
+// One unit of work of the fused distance/top-M kernel: a tile of up to
+// kQueriesPerBlock query rows (a contiguous slice of the query list) scanned
+// against a contiguous slice of the pool list.
+struct WorkItem {
+    int64_t q_begin;    // first index into the query list
+    int64_t p_begin;    // first index into the pool list
+    int64_t out_base;   // >= 0: output row of query q_begin (partial lists); < 0: row = query id
+    int32_t q_count;
+    int32_t p_count;
+};
+
+constexpr int kQueriesPerWave = 32;
+constexpr int kWaves = 4;
+constexpr int kQueriesPerBlock = kQueriesPerWave * kWaves;   // 128
+constexpr int kPoolTile = 32;
+
+// Arguments of the fused distance + top-M kernel.
+struct KnnArgs {
+    const float* Xq;        // query vectors, row stride Dp (zero padded)
+    const float* Xp;        // pool vectors, row stride Dp
+    const float* nq;        // |x|^2 of query rows (indexed by query row id)
+    const float* np;        // |x|^2 of pool rows (indexed by pool row id)
+    const int32_t* q_rows;  // query list (row ids into Xq); nullptr = identity
+    const int32_t* p_rows;  // pool list (row ids into Xp); nullptr = identity
+    const WorkItem* items;
+    int32_t n_items;
+    int32_t Dp;
+    int32_t M;              // list length
+    int32_t metric;         // 0 = L2, 1 = inner product (key = -<x,y>)
+    int32_t exclude_self;   // drop pool entries whose row id equals the query row id
+    int32_t out_pos;        // write pool-list positions instead of row ids
+    const float* seed_d;    // optional per-query cap on kept keys: seed_d[qid * seed_ld + seed_ld - 1]
+    int32_t seed_ld;
+    int32_t* out_ids;       // (rows, M)
+    float* out_d;           // (rows, M)
+};
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace gtann

@@ -1,0 +1,411 @@
+// knn_kernels.hip -- per-bucket brute-force kNN for gfx950.
+//
+// One workgroup (4 waves) scans a contiguous slice of a pool list for a tile
+// of 128 query rows.  The |x|^2 - 2x.y contraction runs on the fp32 matrix
+// cores (v_mfma_f32_32x32x2_f32) with the pool tile staged through LDS and
+// each wave's 32 query rows held in registers; the 32x32 distance block is
+// filtered in registers against each query's current M-th key and only the
+// survivors are appended to a per-query LDS buffer, which is merged into the
+// query's sorted list when it fills.  The (queries x pool) distance matrix
+// never reaches HBM.
+//
+// Semantics follow the reference's top-M (src/bucket.cu:4101-4265): self is
+// excluded, padding is (-1, +inf), distance reported = |q|^2 + |p|^2 - 2 q.p.
+// Ties are ordered by id (total order (key, id)), so the kept set and its
+// order are unique.
+#include "gtann_common.hpp"
+
+#include <climits>
+#include <cmath>
+
+namespace gtann {
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+constexpr int kCB = 32;      // candidate-buffer slots per query (>= 32 = one tile's worth per query)
+constexpr int kMaxM = 128;   // longest list the kernel keeps
+
+__device__ __forceinline__ bool key_less(float da, int32_t ia, float db, int32_t ib)
+{
+    return da < db || (da == db && ia < ib);
+}
+
+// Orders LDS traffic of one wave across lanes (no s_barrier needed inside a wave).
+__device__ __forceinline__ void wave_sync()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// number of entries of the sorted (d, i) array [0, n) that are < (kd, ki)
+__device__ __forceinline__ int lower_bound_lds(const float* ad, const int32_t* ai, int n, float kd, int32_t ki)
+{
+    int lo = 0, hi = n;
+    while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (key_less(ad[mid], ai[mid], kd, ki)) lo = mid + 1;
+        else hi = mid;
+    }
+    return lo;
+}
+
+// 64-lane bitonic sort, ascending in (d, i).
+__device__ __forceinline__ void wave_bitonic_sort(float& d, int32_t& i, int lane)
+{
+#pragma unroll
+    for (int k = 2; k <= 64; k <<= 1) {
+#pragma unroll
+        for (int s = k >> 1; s > 0; s >>= 1) {
+            const float od = __shfl_xor(d, s);
+            const int32_t oi = __shfl_xor(i, s);
+            const bool ascending = (lane & k) == 0;
+            const bool lower = (lane & s) == 0;
+            const bool other_less = key_less(od, oi, d, i);
+            const bool other_greater = key_less(d, i, od, oi);
+            const bool take = (lower == ascending) ? other_less : other_greater;
+            if (take) { d = od; i = oi; }
+        }
+    }
+}
+
+template <int DP>
+struct KnnSmem {
+    float tile[2][kPoolTile][DP + 4];   // +4 floats: rows land on distinct bank groups
+    float tnorm[2][kPoolTile];
+    int32_t trow[2][kPoolTile];         // pool row id, -1 past the slice end
+    float bd[kQueriesPerBlock][kCB];
+    int32_t bi[kQueriesPerBlock][kCB];
+    float sBd[kWaves][64];
+    int32_t sBi[kWaves][64];
+    float sLd[kWaves][kMaxM];
+    int32_t sLi[kWaves][kMaxM];
+    float sthr[kWaves];
+};
+
+// Per-lane view of one query's state.  Lanes j and j+32 of a wave hold the
+// same query (both halves of the MFMA's k split) and keep identical copies.
+struct QueryState {
+    float thr;     // keep a candidate iff key <= thr
+    float seed;    // cap from the caller (previous round's M-th) or +inf
+    int32_t cnt;   // entries in the LDS buffer
+    int32_t nL;    // entries in the sorted list (stored in the output row)
+    int64_t orow;  // output row
+};
+
+// Merges the buffer of query q (0..31 of this wave) into its sorted list
+// (output row), recomputing its threshold.  Called by all 64 lanes.
+template <int DP>
+__device__ void wave_merge(KnnSmem<DP>& sm, const KnnArgs& a, int w, int lane, int q, QueryState& st)
+{
+    const int nB = __shfl(st.cnt, q);
+    const int nL = __shfl(st.nL, q);
+    const int64_t orow = __shfl(st.orow, q);
+    const int M = a.M;
+    const int ql = w * kQueriesPerWave + q;
+
+    float bd = INFINITY;
+    int32_t bi = INT_MAX;
+    if (lane < nB) { bd = sm.bd[ql][lane]; bi = sm.bi[ql][lane]; }
+    wave_bitonic_sort(bd, bi, lane);
+    sm.sBd[w][lane] = bd;
+    sm.sBi[w][lane] = bi;
+
+    float ld[2];
+    int32_t li[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        const int idx = lane + 64 * e;
+        ld[e] = INFINITY;
+        li[e] = INT_MAX;
+        if (idx < nL) {
+            ld[e] = a.out_d[orow * M + idx];
+            li[e] = a.out_ids[orow * M + idx];
+        }
+        if (idx < kMaxM) { sm.sLd[w][idx] = ld[e]; sm.sLi[w][idx] = li[e]; }
+    }
+    wave_sync();
+
+    const int total = nL + nB;
+    if (lane < nB) {
+        const int pos = lane + lower_bound_lds(sm.sLd[w], sm.sLi[w], nL, bd, bi);
+        if (pos < M) {
+            a.out_d[orow * M + pos] = bd;
+            a.out_ids[orow * M + pos] = bi;
+            if (pos == M - 1) sm.sthr[w] = bd;
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        const int idx = lane + 64 * e;
+        if (idx < nL) {
+            const int pos = idx + lower_bound_lds(sm.sBd[w], sm.sBi[w], nB, ld[e], li[e]);
+            if (pos < M) {
+                a.out_d[orow * M + pos] = ld[e];
+                a.out_ids[orow * M + pos] = li[e];
+                if (pos == M - 1) sm.sthr[w] = ld[e];
+            }
+        }
+    }
+    wave_sync();
+    const float mth = sm.sthr[w];
+    const int newn = total < M ? total : M;
+    if ((lane & 31) == q) {
+        st.cnt = 0;
+        st.nL = newn;
+        st.thr = (newn == M) ? fminf(st.seed, mth) : st.seed;
+    }
+    // the list rows written above are read back by this wave's next merge
+    __threadfence_block();
+}
+
+template <int DP>
+__global__ void __launch_bounds__(256, 2) knn_fused_kernel(KnnArgs a)
+{
+    constexpr int DH = DP / 2;                    // k-steps of 2 dims (one per half wave)
+    constexpr int F4_ROW = DP / 4;
+    constexpr int F4_THREAD = kPoolTile * F4_ROW / 256;
+    static_assert(DP % 32 == 0, "row stride must be a multiple of 32 floats");
+    __shared__ KnnSmem<DP> sm;
+
+    // XCD-aware order: hardware deals consecutive workgroups round-robin over
+    // the 8 XCDs, so give each XCD a contiguous run of work items (same
+    // bucket => same pool rows => shared L2).
+    const int per = (a.n_items + 7) / 8;
+    const int item_idx = static_cast<int>(blockIdx.x % 8) * per + static_cast<int>(blockIdx.x / 8);
+    if (item_idx >= a.n_items) return;
+    const WorkItem it = a.items[item_idx];
+
+    const int tid = threadIdx.x;
+    const int w = tid >> 6, lane = tid & 63, j = lane & 31, h = lane >> 5;
+    const int qlocal = w * kQueriesPerWave + j;
+    const bool qvalid = qlocal < it.q_count;
+    const int64_t qi = it.q_begin + qlocal;
+    const int32_t qrow = qvalid ? (a.q_rows ? a.q_rows[qi] : static_cast<int32_t>(qi)) : 0;
+    const float qn = (qvalid && a.metric == 0) ? a.nq[qrow] : 0.f;
+
+    QueryState st;
+    st.seed = INFINITY;
+    if (qvalid && a.seed_d) st.seed = a.seed_d[static_cast<int64_t>(qrow) * a.seed_ld + a.seed_ld - 1];
+    st.thr = qvalid ? st.seed : -INFINITY;
+    st.cnt = 0;
+    st.nL = 0;
+    st.orow = it.out_base >= 0 ? it.out_base + qlocal : static_cast<int64_t>(qrow);
+
+    // query fragment: dims [h*DH, h*DH + DH) of query row qrow
+    float qf[DH];
+    {
+        const float4* src = reinterpret_cast<const float4*>(a.Xq + static_cast<int64_t>(qrow) * DP + h * DH);
+#pragma unroll
+        for (int s = 0; s < DH / 4; ++s) {
+            const float4 v = qvalid ? src[s] : make_float4(0.f, 0.f, 0.f, 0.f);
+            qf[4 * s + 0] = v.x; qf[4 * s + 1] = v.y; qf[4 * s + 2] = v.z; qf[4 * s + 3] = v.w;
+        }
+    }
+
+    const int ntiles = static_cast<int>((it.p_count + kPoolTile - 1) / kPoolTile);
+    float4 pre[F4_THREAD];
+    int32_t pre_row = -1;
+    float pre_norm = 0.f;
+
+    auto load_tile = [&](int t) {
+#pragma unroll
+        for (int u = 0; u < F4_THREAD; ++u) {
+            const int e = tid + 256 * u;
+            const int r = e / F4_ROW, c4 = e % F4_ROW;
+            const int p = t * kPoolTile + r;
+            pre[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (p < it.p_count) {
+                const int64_t pl = it.p_begin + p;
+                const int32_t prow = a.p_rows ? a.p_rows[pl] : static_cast<int32_t>(pl);
+                pre[u] = reinterpret_cast<const float4*>(a.Xp + static_cast<int64_t>(prow) * DP)[c4];
+            }
+        }
+        if (tid < kPoolTile) {
+            const int p = t * kPoolTile + tid;
+            pre_row = -1;
+            pre_norm = 0.f;
+            if (p < it.p_count) {
+                const int64_t pl = it.p_begin + p;
+                pre_row = a.p_rows ? a.p_rows[pl] : static_cast<int32_t>(pl);
+                pre_norm = a.metric == 0 ? a.np[pre_row] : 0.f;
+            }
+        }
+    };
+    auto store_tile = [&](int buf) {
+#pragma unroll
+        for (int u = 0; u < F4_THREAD; ++u) {
+            const int e = tid + 256 * u;
+            const int r = e / F4_ROW, c4 = e % F4_ROW;
+            *reinterpret_cast<float4*>(&sm.tile[buf][r][4 * c4]) = pre[u];
+        }
+        if (tid < kPoolTile) { sm.trow[buf][tid] = pre_row; sm.tnorm[buf][tid] = pre_norm; }
+    };
+
+    if (ntiles > 0) {
+        load_tile(0);
+        store_tile(0);
+    }
+    __syncthreads();
+
+    for (int t = 0; t < ntiles; ++t) {
+        const int buf = t & 1;
+        if (t + 1 < ntiles) load_tile(t + 1);
+
+        // D[i][j] = sum_k pool[i][k] * query[j][k]; lane supplies A[i=lane%32][k=lane/32]
+        // (pool row j, dim h*DH+s) and B[k=lane/32][j=lane%32] (query j, same dim).
+        floatx16 acc;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+        const float* arow = &sm.tile[buf][j][h * DH];
+#pragma unroll
+        for (int s = 0; s < DH / 4; ++s) {
+            const float4 av = *reinterpret_cast<const float4*>(arow + 4 * s);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.x, qf[4 * s + 0], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.y, qf[4 * s + 1], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.z, qf[4 * s + 2], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.w, qf[4 * s + 3], acc, 0, 0, 0);
+        }
+
+        // acc[r] is D[i][j] with i = 8*(r/4) + 4*h + r%4 (pool row of the tile).
+        float dv[16];
+        uint32_t okmask = 0;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int i = 8 * (r >> 2) + 4 * h + (r & 3);
+            const int32_t prow = sm.trow[buf][i];
+            const float d = a.metric == 0 ? fmaf(-2.f, acc[r], sm.tnorm[buf][i] + qn) : -acc[r];
+            dv[r] = d;
+            const bool ok = prow >= 0 && !(a.exclude_self && prow == qrow);
+            okmask |= static_cast<uint32_t>(ok) << r;
+        }
+        uint32_t pass = 0;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) pass |= static_cast<uint32_t>(dv[r] <= st.thr) << r;
+        pass &= okmask;
+        int np_ = __popc(pass);
+        int np_o = __shfl_xor(np_, 32);
+        const bool need = qvalid && (st.cnt + np_ + np_o > kCB);
+        uint64_t needmask = __ballot(need) & 0xffffffffull;
+        if (needmask) {
+            while (needmask) {
+                const int q = __ffsll(static_cast<unsigned long long>(needmask)) - 1;
+                needmask &= needmask - 1;
+                wave_merge<DP>(sm, a, w, lane, q, st);
+            }
+            pass = 0;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) pass |= static_cast<uint32_t>(dv[r] <= st.thr) << r;
+            pass &= okmask;
+            np_ = __popc(pass);
+            np_o = __shfl_xor(np_, 32);
+        }
+        if (qvalid) {
+            int off = st.cnt + (h ? np_o : 0);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                if ((pass >> r) & 1u) {
+                    const int i = 8 * (r >> 2) + 4 * h + (r & 3);
+                    sm.bd[qlocal][off] = dv[r];
+                    sm.bi[qlocal][off] = a.out_pos ? t * kPoolTile + i : sm.trow[buf][i];
+                    ++off;
+                }
+            }
+            st.cnt += np_ + np_o;
+        }
+
+        if (t + 1 < ntiles) store_tile(buf ^ 1);
+        __syncthreads();
+    }
+
+    // flush the remaining buffers
+    uint64_t rem = __ballot(qvalid && st.cnt > 0) & 0xffffffffull;
+    while (rem) {
+        const int q = __ffsll(static_cast<unsigned long long>(rem)) - 1;
+        rem &= rem - 1;
+        wave_merge<DP>(sm, a, w, lane, q, st);
+    }
+    if (qvalid) {
+        for (int p = st.nL + h; p < a.M; p += 2) {
+            a.out_ids[st.orow * a.M + p] = -1;
+            a.out_d[st.orow * a.M + p] = INFINITY;
+        }
+    }
+}
+
+// Merges `splits` sorted partial lists per query (rows s*nq + q of parts)
+// into rows out_base + q.  One wave per query; lists staged in LDS.
+constexpr int kMergeMaxEntries = 2048;
+__global__ void __launch_bounds__(64) merge_partials_kernel(const int32_t* __restrict__ pids,
+                                                            const float* __restrict__ pd, int64_t nq,
+                                                            int splits, int M, int32_t* out_ids,
+                                                            float* out_d)
+{
+    __shared__ float sd[kMergeMaxEntries];
+    __shared__ int32_t si[kMergeMaxEntries];
+    __shared__ int scount[64];
+    const int64_t q = blockIdx.x;
+    if (q >= nq) return;
+    const int lane = threadIdx.x;
+    const int total = splits * M;
+    for (int e = lane; e < total; e += 64) {
+        const int s = e / M, idx = e % M;
+        const int32_t id = pids[(static_cast<int64_t>(s) * nq + q) * M + idx];
+        sd[e] = id >= 0 ? pd[(static_cast<int64_t>(s) * nq + q) * M + idx] : INFINITY;
+        si[e] = id >= 0 ? id : INT_MAX;
+    }
+    __syncthreads();
+    int valid = 0;
+    for (int e = lane; e < total; e += 64) valid += si[e] != INT_MAX;
+    scount[lane] = valid;
+    __syncthreads();
+    int nvalid = 0;
+    for (int l = 0; l < 64; ++l) nvalid += scount[l];
+    for (int e = lane; e < total; e += 64) {
+        if (si[e] == INT_MAX) continue;
+        const int s = e / M, idx = e % M;
+        int rank = idx;
+        for (int s2 = 0; s2 < splits; ++s2)
+            if (s2 != s) rank += lower_bound_lds(sd + s2 * M, si + s2 * M, M, sd[e], si[e]);
+        if (rank < M) {
+            out_ids[q * M + rank] = si[e];
+            out_d[q * M + rank] = sd[e];
+        }
+    }
+    for (int p = nvalid + lane; p < M; p += 64) {
+        out_ids[q * M + p] = -1;
+        out_d[q * M + p] = INFINITY;
+    }
+}
+
+void launch_knn_fused(const KnnArgs& a, hipStream_t stream)
+{
+    if (a.n_items <= 0) return;
+    GT_REQUIRE(a.M >= 1 && a.M <= kMaxM, "list length must be in [1, 128]");
+    const int per = (a.n_items + 7) / 8;
+    const dim3 grid(static_cast<unsigned>(per * 8));
+    switch (a.Dp) {
+    case 32:  hipLaunchKernelGGL(knn_fused_kernel<32>, grid, dim3(256), 0, stream, a); break;
+    case 64:  hipLaunchKernelGGL(knn_fused_kernel<64>, grid, dim3(256), 0, stream, a); break;
+    case 96:  hipLaunchKernelGGL(knn_fused_kernel<96>, grid, dim3(256), 0, stream, a); break;
+    case 128: hipLaunchKernelGGL(knn_fused_kernel<128>, grid, dim3(256), 0, stream, a); break;
+    case 160: hipLaunchKernelGGL(knn_fused_kernel<160>, grid, dim3(256), 0, stream, a); break;
+    case 192: hipLaunchKernelGGL(knn_fused_kernel<192>, grid, dim3(256), 0, stream, a); break;
+    case 224: hipLaunchKernelGGL(knn_fused_kernel<224>, grid, dim3(256), 0, stream, a); break;
+    case 256: hipLaunchKernelGGL(knn_fused_kernel<256>, grid, dim3(256), 0, stream, a); break;
+    default: GT_REQUIRE(false, "padded dimension " + std::to_string(a.Dp) + " not supported (D <= 256)");
+    }
+    GT_HIP(hipGetLastError());
+}
+
+void launch_merge_partials(const int32_t* pids, const float* pd, int64_t nq, int splits, int M,
+                           int32_t* out_ids, float* out_d, hipStream_t stream)
+{
+    if (nq <= 0) return;
+    GT_REQUIRE(static_cast<int64_t>(splits) * M <= kMergeMaxEntries, "too many partial lists");
+    hipLaunchKernelGGL(merge_partials_kernel, dim3(static_cast<unsigned>(nq)), dim3(64), 0, stream, pids, pd,
+                       nq, splits, M, out_ids, out_d);
+    GT_HIP(hipGetLastError());
+}
+
+}  // namespace gtann

@@ -1,0 +1,300 @@
+"""ctypes binding of libgtann.so (include/gtann.h) -- the gfx950 graph build.
+
+Arrays may be numpy arrays (host memory) or torch tensors (host or device
+memory of the context's GPU); device tensors are used in place by the
+library.  Every call goes to the HIP library; there is no CPU fallback, and
+a missing library raises immediately.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from dataclasses import dataclass
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libgtann.so")
+
+GT_OK, GT_EINVAL, GT_ENOMEM, GT_EDEVICE, GT_EFEWCAND = 0, -1, -2, -3, -4
+DTYPES = {"f32": 0, "u8": 1, "i8": 2}
+METRICS = {"l2": 0, "ip": 1}
+
+# symbols the C ABI must export (checked by the CPU tests)
+EXPORTS = (
+    "gt_create", "gt_destroy", "gt_last_error", "gt_version", "gt_knn_exact", "gt_assign_top2",
+    "gt_knn_bucketed", "gt_merge_rounds", "gt_refine_2hop", "gt_sanitize", "gt_cagra_prune",
+    "gt_reverse_merge", "gt_optimize", "gt_translate", "gt_build_params_default", "gt_build_graph",
+)
+
+
+class GtannError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"gtann error {code}: {msg}")
+        self.code = code
+
+
+class BuildParams(C.Structure):
+    _fields_ = [
+        ("metric", C.c_int32), ("n_buckets", C.c_int32), ("nprobe", C.c_int32), ("M", C.c_int32),
+        ("K", C.c_int32), ("rounds", C.c_int32), ("refine_passes", C.c_int32), ("refine_sample", C.c_int32),
+        ("kmeans_iters", C.c_int32), ("balance", C.c_float), ("seed", C.c_uint64),
+    ]
+
+
+class BuildStats(C.Structure):
+    _fields_ = [
+        ("t_total", C.c_double), ("t_prepare", C.c_double), ("t_bucketing", C.c_double), ("t_knn", C.c_double),
+        ("t_merge", C.c_double), ("t_refine", C.c_double), ("t_prune", C.c_double), ("t_revmerge", C.c_double),
+        ("t_download", C.c_double), ("knn_flops", C.c_double), ("knn_pairs", C.c_double),
+        ("max_pool", C.c_int64), ("max_bucket", C.c_int64),
+    ]
+
+    def as_dict(self):
+        return {name: getattr(self, name) for name, _ in self._fields_}
+
+
+_lib = None
+
+
+def lib():
+    """Loads libgtann.so; raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"HIP library missing: {LIB_PATH} (run __graft_entry__.build())")
+        L = C.CDLL(LIB_PATH)
+        vp, i64, i32 = C.c_void_p, C.c_int64, C.c_int32
+        L.gt_create.argtypes = [C.c_int, C.POINTER(vp)]
+        L.gt_destroy.argtypes = [vp]
+        L.gt_destroy.restype = None
+        L.gt_last_error.argtypes = [vp]
+        L.gt_last_error.restype = C.c_char_p
+        L.gt_version.restype = C.c_char_p
+        L.gt_knn_exact.argtypes = [vp, vp, i64, i32, C.c_int, C.c_int, vp, i64, i32, vp, vp]
+        L.gt_assign_top2.argtypes = [vp, vp, i64, i32, C.c_int, C.c_int, vp, i64, vp, vp]
+        L.gt_knn_bucketed.argtypes = [vp, vp, i64, i32, C.c_int, C.c_int, vp, vp, i64, vp, i32, i32, vp, vp, C.c_int]
+        L.gt_merge_rounds.argtypes = [vp, vp, vp, vp, vp, i64, i32, vp, vp]
+        L.gt_refine_2hop.argtypes = [vp, vp, i64, i32, C.c_int, C.c_int, i32, i32, i32, vp, vp]
+        L.gt_sanitize.argtypes = [vp, vp, i64, i32, vp]
+        L.gt_cagra_prune.argtypes = [vp, vp, i64, i32, i32, vp]
+        L.gt_reverse_merge.argtypes = [vp, vp, i64, i32, vp]
+        L.gt_optimize.argtypes = [vp, vp, i64, i32, i32, vp]
+        L.gt_translate.argtypes = [vp, vp, vp, i64, i32, vp]
+        L.gt_build_params_default.argtypes = [C.POINTER(BuildParams)]
+        L.gt_build_params_default.restype = None
+        L.gt_build_graph.argtypes = [vp, vp, i64, i32, C.c_int, C.POINTER(BuildParams), vp, vp, vp,
+                                     C.POINTER(BuildStats)]
+        _lib = L
+    return _lib
+
+
+def _is_torch(a):
+    return type(a).__module__.startswith("torch")
+
+
+def _ptr(a):
+    if a is None:
+        return None
+    if _is_torch(a):
+        if not a.is_contiguous():
+            raise ValueError("tensor must be contiguous")
+        return C.c_void_p(a.data_ptr())
+    if not a.flags["C_CONTIGUOUS"]:
+        raise ValueError("array must be C-contiguous")
+    return C.c_void_p(a.ctypes.data)
+
+
+def _np(a, dtype):
+    return np.ascontiguousarray(a, dtype=dtype)
+
+
+def _dtype_code(X):
+    if _is_torch(X):
+        import torch
+        m = {torch.float32: 0, torch.uint8: 1, torch.int8: 2}
+    else:
+        m = {np.dtype(np.float32): 0, np.dtype(np.uint8): 1, np.dtype(np.int8): 2}
+    if X.dtype not in m:
+        raise ValueError(f"unsupported dtype {X.dtype} (float32, uint8, int8)")
+    return m[X.dtype]
+
+
+def _empty_like_input(X, shape, dtype):
+    """Output buffer on the same side (host/device) as the input."""
+    if _is_torch(X):
+        import torch
+        tmap = {np.int32: torch.int32, np.float32: torch.float32, np.uint32: torch.int32, np.int64: torch.int64}
+        return torch.empty(shape, dtype=tmap[dtype], device=X.device)
+    return np.empty(shape, dtype=dtype)
+
+
+def _as_u32(a):
+    if _is_torch(a):
+        return a
+    return a.view(np.uint32) if a.dtype == np.int32 else _np(a, np.uint32)
+
+
+@dataclass
+class BuildResult:
+    graph: object
+    knn_ids: object
+    knn_dists: object
+    stats: dict
+
+
+class Context:
+    """One device + stream + workspaces (gt_create / gt_destroy)."""
+
+    def __init__(self, device: int = 0):
+        self._h = C.c_void_p()
+        rc = lib().gt_create(device, C.byref(self._h))
+        if rc != GT_OK:
+            raise GtannError(rc, f"gt_create(device={device}) failed")
+
+    def close(self):
+        if self._h:
+            lib().gt_destroy(self._h)
+            self._h = C.c_void_p()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _check(self, rc, what):
+        if rc != GT_OK:
+            msg = lib().gt_last_error(self._h)
+            raise GtannError(rc, f"{what}: {msg.decode() if msg else ''}")
+
+    # ---------------------------------------------------------------- stages
+
+    def knn_exact(self, X, k, queries=None, metric="l2"):
+        if not _is_torch(X):
+            X = np.ascontiguousarray(X)
+        N, D = X.shape
+        q = None
+        nq = N
+        if queries is not None:
+            q = queries if _is_torch(queries) else _np(queries, np.int64)
+            nq = int(q.shape[0])
+        ids = _empty_like_input(X, (nq, k), np.int32)
+        d = _empty_like_input(X, (nq, k), np.float32)
+        self._check(lib().gt_knn_exact(self._h, _ptr(X), N, D, _dtype_code(X), METRICS[metric], _ptr(q), nq, k,
+                                       _ptr(ids), _ptr(d)), "gt_knn_exact")
+        return ids, d
+
+    def assign_top2(self, X, Cm, metric="l2"):
+        if not _is_torch(X):
+            X = np.ascontiguousarray(X)
+            Cm = np.ascontiguousarray(Cm, dtype=X.dtype)
+        N, D = X.shape
+        top2 = _empty_like_input(X, (N, 2), np.int32)
+        d2 = _empty_like_input(X, (N, 2), np.float32)
+        self._check(lib().gt_assign_top2(self._h, _ptr(X), N, D, _dtype_code(X), METRICS[metric], _ptr(Cm),
+                                         int(Cm.shape[0]), _ptr(top2), _ptr(d2)), "gt_assign_top2")
+        return top2, d2
+
+    def knn_bucketed(self, X, offsets, members, probe, M, metric="l2", running=None):
+        if not _is_torch(X):
+            X = np.ascontiguousarray(X)
+        N, D = X.shape
+        offsets = _np(offsets, np.int64)
+        members = _np(members, np.int32)
+        probe = _np(probe, np.int32)
+        P = probe.shape[1] if probe.ndim == 2 else 0
+        if running is None:
+            ids = _empty_like_input(X, (N, M), np.int32)
+            d = _empty_like_input(X, (N, M), np.float32)
+            merge = 0
+        else:
+            ids = running[0].copy() if not _is_torch(running[0]) else running[0].clone()
+            d = running[1].copy() if not _is_torch(running[1]) else running[1].clone()
+            merge = 1
+        self._check(lib().gt_knn_bucketed(self._h, _ptr(X), N, D, _dtype_code(X), METRICS[metric], _ptr(offsets),
+                                          _ptr(members), len(offsets) - 1, _ptr(probe), P, M, _ptr(ids), _ptr(d),
+                                          merge), "gt_knn_bucketed")
+        return ids, d
+
+    def merge_rounds(self, run_ids, run_d, new_ids, new_d):
+        run_ids, new_ids = _np(run_ids, np.int32), _np(new_ids, np.int32)
+        run_d, new_d = _np(run_d, np.float32), _np(new_d, np.float32)
+        N, M = run_ids.shape
+        oi = np.empty((N, M), np.int32)
+        od = np.empty((N, M), np.float32)
+        self._check(lib().gt_merge_rounds(self._h, _ptr(run_ids), _ptr(run_d), _ptr(new_ids), _ptr(new_d), N, M,
+                                          _ptr(oi), _ptr(od)), "gt_merge_rounds")
+        return oi, od
+
+    def refine_2hop(self, X, ids, d, S, passes=1, metric="l2"):
+        X = np.ascontiguousarray(X)
+        N, D = X.shape
+        ids = _np(ids, np.int32).copy()
+        d = _np(d, np.float32).copy()
+        M = ids.shape[1]
+        self._check(lib().gt_refine_2hop(self._h, _ptr(X), N, D, _dtype_code(X), METRICS[metric], M, S, passes,
+                                         _ptr(ids), _ptr(d)), "gt_refine_2hop")
+        return ids, d
+
+    def sanitize(self, knn):
+        knn = _np(knn, np.int32)
+        N, M = knn.shape
+        out = np.empty((N, M), np.uint32)
+        self._check(lib().gt_sanitize(self._h, _ptr(knn), N, M, _ptr(out)), "gt_sanitize")
+        return out
+
+    def cagra_prune(self, knn, K):
+        knn = _as_u32(knn)
+        N, M = knn.shape
+        out = np.empty((N, K), np.uint32)
+        self._check(lib().gt_cagra_prune(self._h, _ptr(knn), N, M, K, _ptr(out)), "gt_cagra_prune")
+        return out
+
+    def reverse_merge(self, fwd):
+        fwd = _np(fwd, np.uint32)
+        N, K = fwd.shape
+        out = np.empty((N, K), np.uint32)
+        self._check(lib().gt_reverse_merge(self._h, _ptr(fwd), N, K, _ptr(out)), "gt_reverse_merge")
+        return out
+
+    def optimize(self, knn, K):
+        knn = _as_u32(knn)
+        N, M = knn.shape
+        out = np.empty((N, K), np.uint32)
+        self._check(lib().gt_optimize(self._h, _ptr(knn), N, M, K, _ptr(out)), "gt_optimize")
+        return out
+
+    def translate(self, g, inv):
+        g = _np(g, np.uint32)
+        inv = _np(inv, np.uint32)
+        N, K = g.shape
+        out = np.empty((N, K), np.uint32)
+        self._check(lib().gt_translate(self._h, _ptr(g), _ptr(inv), N, K, _ptr(out)), "gt_translate")
+        return out
+
+    def build_graph(self, X, *, n_buckets=0, nprobe=-1, M=64, K=32, rounds=3, refine_passes=0, refine_sample=16,
+                    kmeans_iters=0, balance=0.8, seed=42, metric="l2", return_knn=True):
+        if not _is_torch(X):
+            X = np.ascontiguousarray(X)
+        N, D = X.shape
+        p = BuildParams()
+        lib().gt_build_params_default(C.byref(p))
+        p.metric, p.n_buckets, p.nprobe, p.M, p.K = METRICS[metric], n_buckets, nprobe, M, K
+        p.rounds, p.refine_passes, p.refine_sample, p.kmeans_iters = rounds, refine_passes, refine_sample, kmeans_iters
+        p.balance, p.seed = balance, seed
+        graph = _empty_like_input(X, (N, K), np.uint32)
+        ids = _empty_like_input(X, (N, M), np.int32) if return_knn else None
+        d = _empty_like_input(X, (N, M), np.float32) if return_knn else None
+        st = BuildStats()
+        self._check(lib().gt_build_graph(self._h, _ptr(X), N, D, _dtype_code(X), C.byref(p), _ptr(ids), _ptr(d),
+                                         _ptr(graph), C.byref(st)), "gt_build_graph")
+        if not _is_torch(graph):
+            graph = graph.view(np.uint32)
+        return BuildResult(graph=graph, knn_ids=ids, knn_dists=d, stats=st.as_dict())

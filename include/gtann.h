@@ -1,0 +1,150 @@
+/*
+ * gtann.h -- C ABI of the MI355X (gfx950) bucketed CAGRA-style graph build.
+ *
+ * Every entry point takes plain pointers and sizes.  Pointers may refer to
+ * host memory or to device memory of the context's GPU (detected per
+ * pointer): host buffers are staged through the device and the call
+ * returns after the results are back; device buffers are used in place.
+ * Calls are synchronous on the context's stream.  One context per host
+ * thread; distinct contexts may be used concurrently.
+ *
+ * Return value: GT_OK (0) or a negative error code; gt_last_error() gives
+ * the message.  No C++ exception crosses this boundary.
+ *
+ * Conventions: kNN rows are ascending by (distance, id), padding is
+ * (-1, +inf).  L2 distances are squared.  For GT_METRIC_IP rows are
+ * descending by inner product and the distance slots hold the inner
+ * product (padding -inf).
+ */
+#ifndef GTANN_H
+#define GTANN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct gt_ctx gt_ctx;
+
+enum { GT_OK = 0, GT_EINVAL = -1, GT_ENOMEM = -2, GT_EDEVICE = -3, GT_EFEWCAND = -4 };
+enum { GT_DTYPE_F32 = 0, GT_DTYPE_U8 = 1, GT_DTYPE_I8 = 2 };
+enum { GT_METRIC_L2 = 0, GT_METRIC_IP = 1 };
+
+/* Context owning a device, a stream and reusable workspaces.
+ * Replaces the GpuResidentKnn constructor/destructor
+ * (src/bucket.cu:5216-5241, :5650) and the cuVS raft::resources handle. */
+int gt_create(int device, gt_ctx** out);
+void gt_destroy(gt_ctx* ctx);
+const char* gt_last_error(const gt_ctx* ctx);
+const char* gt_version(void);
+
+/* Exact kNN of the query rows `queries[0..nq)` (all N rows when queries is
+ * NULL, then nq must be N) against all N rows, self excluded.
+ * ids/dists: nq x k.  Replaces bd/build_knn.py:98-149 (build_exact_knn). */
+int gt_knn_exact(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtype, int metric,
+                 const int64_t* queries, int64_t nq, int32_t k, int32_t* ids, float* dists);
+
+/* Exact top-2 nearest of nC centroid rows C (nC x D, same dtype as X) for
+ * each of the N rows of X; ties by lower centroid index.
+ * Replaces step4_top2_kernel + its cuBLAS GEMM (src/bucket.cu:1230, :2061-2177). */
+int gt_assign_top2(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtype, int metric,
+                   const void* C, int64_t nC, uint32_t* top2, float* d2);
+
+/* One round of bucketed kNN.  Bucket b owns members[offsets[b]..offsets[b+1])
+ * (every point in exactly one bucket); its pool is its own members followed
+ * by the members of probe[b*P .. b*P+P) (ids >= nB skipped).  Each point gets
+ * the M nearest pool points other than itself.  merge = 0: ids/dists (N x M)
+ * are outputs.  merge = 1: ids/dists hold the running table on input and the
+ * merged table (top-M of both, duplicates once) on output.
+ * Replaces GpuResidentKnn::run_round (src/bucket.cu:5310-5546). */
+int gt_knn_bucketed(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtype, int metric,
+                    const int64_t* offsets, const int32_t* members, int64_t nB,
+                    const int32_t* probe, int32_t P, int32_t M,
+                    int32_t* ids, float* dists, int merge);
+
+/* Cross-round merge of two N x M tables into out (may alias run).
+ * Replaces resident_merge_kernel (src/bucket.cu:5021-5130). */
+int gt_merge_rounds(gt_ctx* ctx, const int32_t* run_ids, const float* run_d,
+                    const int32_t* new_ids, const float* new_d, int64_t N, int32_t M,
+                    int32_t* out_ids, float* out_d);
+
+/* `passes` passes of 2-hop local-join refinement of an N x M table in place
+ * (S = neighbours sampled per hop, S*S <= 1024).
+ * Replaces GpuResidentKnn::refine_local_join / a1_pull_join_kernel
+ * (src/bucket.cu:5591-5648, :4754-4850). */
+int gt_refine_2hop(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtype, int metric,
+                   int32_t M, int32_t S, int32_t passes, int32_t* ids, float* dists);
+
+/* -1 / out-of-range / self entries -> first valid entry of the row, else
+ * (i+1) % N.  Replaces sanitize_to_uint32_inplace (src/optimize.cu:89-134). */
+int gt_sanitize(gt_ctx* ctx, const int32_t* knn, int64_t N, int32_t M, uint32_t* out);
+
+/* CAGRA rank-based detour-count prune of rows already in rank order
+ * (entries >= 2^31 as int32 are padding).  GT_EFEWCAND if a row has fewer
+ * than K valid candidates.  Replaces prune_windowed_gpu::run
+ * (src/prune_windowed_gpu.hpp:7-39, src/prune_windowed_gpu.cu:422-498) with a
+ * full window, and the prune half of cuVS helpers::optimize
+ * (src/optimize.cu:396). */
+int gt_cagra_prune(gt_ctx* ctx, const uint32_t* knn, int64_t N, int32_t M, int32_t K, uint32_t* out);
+
+/* Reverse-edge merge of a forward graph (N x K, K <= 64) with K/2
+ * protected slots.  Replaces optimize_chunked -m E Phase 1+2
+ * (src/optimize_chunked.cu:372-407, :1421-1471). */
+int gt_reverse_merge(gt_ctx* ctx, const uint32_t* fwd, int64_t N, int32_t K, uint32_t* out);
+
+/* prune then reverse merge.  Replaces cuvs::neighbors::cagra::helpers::optimize
+ * (src/optimize.cu:395-397, src/bucket.cu:8470). */
+int gt_optimize(gt_ctx* ctx, const uint32_t* knn, int64_t N, int32_t M, int32_t K, uint32_t* out);
+
+/* out[inv[i]][k] = inv[g[i][k]]; GT_EINVAL unless inv is a permutation.
+ * Replaces translate_ids::translate_graph_to_original_order
+ * (src/translate_graph_ids.hpp:75). */
+int gt_translate(gt_ctx* ctx, const uint32_t* g, const uint32_t* inv, int64_t N, int32_t K, uint32_t* out);
+
+typedef struct gt_build_params {
+    int32_t metric;         /* GT_METRIC_L2 / GT_METRIC_IP */
+    int32_t n_buckets;      /* buckets per round (--centroid-ratio * N) */
+    int32_t nprobe;         /* probe buckets per bucket (--nprobe) */
+    int32_t M;              /* intermediate degree (--neighbors-m) */
+    int32_t K;              /* output degree (--fused-optimize-degree) */
+    int32_t rounds;         /* rounds with fresh buckets (-t) */
+    int32_t refine_passes;  /* 2-hop refinement passes (BUCKET2_A1_PASSES) */
+    int32_t refine_sample;  /* S of the refinement (BUCKET2_A1_SAMPLE) */
+    int32_t kmeans_iters;   /* Lloyd iterations on the sampled centroids (0 = data points) */
+    float balance;          /* two-choice factor: 2nd bucket if size2 < balance*size1 (<= 0 off) */
+    uint64_t seed;          /* --seed; round r uses seed + r */
+} gt_build_params;
+
+typedef struct gt_build_stats {
+    double t_total;         /* wall seconds of the whole call */
+    double t_prepare;       /* upload / convert / norms */
+    double t_bucketing;     /* centroids, probe table, top-2, balance, pools */
+    double t_knn;           /* fused kNN kernels (device time) */
+    double t_merge;         /* cross-round merges (device time) */
+    double t_refine;        /* refinement (device time) */
+    double t_prune;         /* sanitize + prune (device time) */
+    double t_revmerge;      /* reverse-edge merge (device time) */
+    double t_download;      /* results to host */
+    double knn_flops;       /* algorithmic flops of the distance contraction (2*D per pair) */
+    double knn_pairs;       /* (query, pool) pairs scanned */
+    int64_t max_pool;
+    int64_t max_bucket;
+} gt_build_stats;
+
+void gt_build_params_default(gt_build_params* p);
+
+/* The whole bucketed build: `rounds` rounds of (centroids -> probe table ->
+ * top-2 assignment with two-choice balance -> pooled kNN -> merge), optional
+ * refinement, sanitize, CAGRA prune, reverse merge.  knn_ids/knn_dists
+ * (N x M, optional, NULL to skip) receive the pre-prune table, graph
+ * (N x K) the final graph.  Replaces bucket2's GPU-resident path
+ * (src/bucket.cu:8729-9842 with --fused-optimize-degree). */
+int gt_build_graph(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtype,
+                   const gt_build_params* params, int32_t* knn_ids, float* knn_dists,
+                   uint32_t* graph, gt_build_stats* stats);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* GTANN_H */

@@ -1,0 +1,271 @@
+"""CPU oracle for the bucketed CAGRA-style graph build -- TEST INFRASTRUCTURE.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s CPU-baseline
+leg may import this module, and only as the checker / the timed CPU
+baseline.  The shipped library never routes through it.
+
+ctypes bindings over ``oracle/liboracle_gt.so`` (built from gt_oracle.c by
+``oracle/Makefile``) plus optional bindings over ``oracle/_ref/libgtann_ref.so``
+(the reference's own headers compiled in place, present only where
+/root/reference was available at build time).
+
+How each oracle function is pinned (what checks it besides itself):
+
+* ``knn_exact`` -- brute force restatement of bd/build_knn.py:17-149.  Pinned by
+  closed forms in tests/test_oracle.py: a 1-D line with hand-computed
+  neighbours, the IP/L2 identity on unit vectors (<x,y> = 1 - |x-y|^2/2),
+  duplicated points giving distance 0, and an independent numpy brute force
+  on integer data.
+* ``knn_bucketed`` -- restates src/bucket.cu:5331-5347 + 4101-4265.  Pinned by
+  the identity "all buckets probed == exact kNN" (config C1 has nprobe =
+  buckets-1) and by a numpy per-bucket brute force.
+* ``merge_rounds`` -- src/bucket.cu:5021-5053.  Pinned by the identity
+  merge(exact, anything-from-the-same-distance-function) == exact, and by a
+  numpy union/dedup/sort restatement on random tables.
+* ``sanitize`` -- src/optimize.cu:89-134.  Pinned by hand-written known
+  answers (padding, self, out-of-range, empty row fallback (i+1)%N).
+* ``cagra_prune`` / ``detour_counts`` -- src/prune_windowed_core.hpp:177-263.
+  Pinned bit-exactly against the reference header itself (``ref_*``) on
+  random graphs incl. duplicates and padding, and the reference's KAT
+  (detour {0,0,1,1,2} -> ids {10,11,12}, test_prune_windowed_core.cpp:93-105).
+* ``reverse_merge`` / ``merge_row`` -- src/edge_chunk_accumulator.hpp:235-284,
+  471-494.  Pinned against the reference header (``ref_reverse_merge``) and
+  its truncation KAT (test_edge_chunk_accumulator.cpp:185-220).
+* ``refine_2hop`` -- src/bucket.cu:4754-4850.  Pinned by invariants: on exact
+  kNN input it is a fixed point; its output is never worse (elementwise
+  distance) than its input; on a table whose rows are all the same bucket's
+  members it equals the brute-force restriction.
+* ``translate`` -- src/translate_graph_ids.hpp:75.  Pinned against the
+  reference header (``ref_translate``).
+* ``prune_occlusion`` -- bd/prune.py:8-83.  Pinned by a hand-computed 1-D
+  example; the tie order of np.argsort and float32 summation order of the
+  reference are "parity unpinned" (only an import would pin them), so tests
+  use integer data without distance ties.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle_gt.so")
+_REF_PATH = os.path.join(_HERE, "_ref", "libgtann_ref.so")
+
+OR_OK, OR_EINVAL, OR_ENOMEM, OR_EFEWCAND = 0, -1, -2, -4
+
+_lib = None
+_ref = None
+
+
+def _p(a):
+    return a.ctypes.data_as(C.c_void_p)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            raise RuntimeError(f"oracle not built: {_LIB_PATH} (run `make -C oracle`)")
+        L = C.CDLL(_LIB_PATH)
+        vp, i64, i32 = C.c_void_p, C.c_int64, C.c_int
+        L.or_knn_exact.argtypes = [vp, i64, i64, i32, vp, i64, i32, i32, vp, vp]
+        L.or_knn_bucketed.argtypes = [vp, i64, i64, i32, vp, vp, i64, vp, i32, i32, vp, vp]
+        L.or_merge_rounds.argtypes = [vp, vp, vp, vp, i64, i32, vp, vp]
+        L.or_sanitize.argtypes = [vp, i64, i32, vp]
+        L.or_sanitize.restype = i64
+        L.or_cagra_prune.argtypes = [vp, i64, i32, i32, vp, vp]
+        L.or_detour_counts.argtypes = [vp, i64, i32, i64, vp]
+        L.or_reverse_merge.argtypes = [vp, i64, i32, vp]
+        L.or_merge_row.argtypes = [vp, vp, C.c_uint32, C.c_uint32]
+        L.or_merge_row.restype = None
+        L.or_refine_2hop.argtypes = [vp, i64, i64, i32, vp, vp, i32, i32, vp, vp]
+        L.or_translate.argtypes = [vp, vp, i64, i32, vp]
+        L.or_prune_occlusion.argtypes = [vp, i64, i64, vp, i32, i32, vp]
+        L.or_num_threads.restype = i32
+        _lib = L
+    return _lib
+
+
+def ref_available() -> bool:
+    return os.path.exists(_REF_PATH)
+
+
+def ref():
+    global _ref
+    if _ref is None:
+        if not ref_available():
+            raise RuntimeError(f"reference harness not built: {_REF_PATH}")
+        R = C.CDLL(_REF_PATH)
+        vp, i64, i32 = C.c_void_p, C.c_int64, C.c_int32
+        R.ref_cagra_prune.argtypes = [vp, i64, i32, i32, vp]
+        R.ref_detour_counts.argtypes = [vp, i64, i32, i64, vp]
+        R.ref_reverse_merge.argtypes = [vp, i64, i32, vp]
+        R.ref_translate.argtypes = [vp, vp, i64, i32, vp]
+        _ref = R
+    return _ref
+
+
+def _f32(X):
+    return np.ascontiguousarray(X, dtype=np.float32)
+
+
+def _check(rc, what):
+    if rc != OR_OK:
+        raise RuntimeError(f"{what} failed with code {rc}")
+
+
+def num_threads() -> int:
+    return int(lib().or_num_threads())
+
+
+def knn_exact(X, k, queries=None, metric=0, exclude_self=True):
+    X = _f32(X)
+    N, D = X.shape
+    q = np.arange(N, dtype=np.int64) if queries is None else np.ascontiguousarray(queries, dtype=np.int64)
+    ids = np.empty((len(q), k), np.int32)
+    d = np.empty((len(q), k), np.float32)
+    _check(lib().or_knn_exact(_p(X), N, D, metric, _p(q), len(q), k, int(exclude_self), _p(ids), _p(d)),
+           "or_knn_exact")
+    return ids, d
+
+
+def knn_bucketed(X, offsets, members, probe, M, metric=0):
+    X = _f32(X)
+    N, D = X.shape
+    offsets = np.ascontiguousarray(offsets, dtype=np.int64)
+    members = np.ascontiguousarray(members, dtype=np.int32)
+    probe = np.ascontiguousarray(probe, dtype=np.int32)
+    nB = len(offsets) - 1
+    P = probe.shape[1] if probe.ndim == 2 else 0
+    ids = np.empty((N, M), np.int32)
+    d = np.empty((N, M), np.float32)
+    _check(lib().or_knn_bucketed(_p(X), N, D, metric, _p(offsets), _p(members), nB, _p(probe), P, M,
+                                 _p(ids), _p(d)), "or_knn_bucketed")
+    return ids, d
+
+
+def merge_rounds(run_ids, run_d, new_ids, new_d):
+    run_ids = np.ascontiguousarray(run_ids, np.int32)
+    new_ids = np.ascontiguousarray(new_ids, np.int32)
+    run_d = np.ascontiguousarray(run_d, np.float32)
+    new_d = np.ascontiguousarray(new_d, np.float32)
+    N, M = run_ids.shape
+    oi = np.empty((N, M), np.int32)
+    od = np.empty((N, M), np.float32)
+    _check(lib().or_merge_rounds(_p(run_ids), _p(run_d), _p(new_ids), _p(new_d), N, M, _p(oi), _p(od)),
+           "or_merge_rounds")
+    return oi, od
+
+
+def sanitize(knn):
+    knn = np.ascontiguousarray(knn, np.int32)
+    N, M = knn.shape
+    out = np.empty((N, M), np.uint32)
+    lib().or_sanitize(_p(knn), N, M, _p(out))
+    return out
+
+
+def cagra_prune(G, K):
+    """Returns (out, rc, bad_row)."""
+    G = np.ascontiguousarray(G).view(np.int32) if np.asarray(G).dtype == np.uint32 else \
+        np.ascontiguousarray(G, np.int32)
+    N, M = G.shape
+    out = np.zeros((N, K), np.uint32)
+    bad = np.zeros(1, np.int64)
+    rc = lib().or_cagra_prune(_p(G), N, M, K, _p(out), _p(bad))
+    return out, rc, int(bad[0])
+
+
+def detour_counts(G, a):
+    G = np.ascontiguousarray(G).view(np.int32) if np.asarray(G).dtype == np.uint32 else \
+        np.ascontiguousarray(G, np.int32)
+    N, M = G.shape
+    cnt = np.empty(M, np.uint32)
+    _check(lib().or_detour_counts(_p(G), N, M, a, _p(cnt)), "or_detour_counts")
+    return cnt
+
+
+def reverse_merge(fwd):
+    fwd = np.ascontiguousarray(fwd, np.uint32)
+    N, K = fwd.shape
+    out = np.empty((N, K), np.uint32)
+    _check(lib().or_reverse_merge(_p(fwd), N, K, _p(out)), "or_reverse_merge")
+    return out
+
+
+def merge_row(row, rank_sorted_src):
+    row = np.array(row, dtype=np.uint32)
+    src = np.ascontiguousarray(rank_sorted_src, np.uint32)
+    lib().or_merge_row(_p(row), _p(src), len(src), len(row))
+    return row
+
+
+def refine_2hop(X, ids, d, S, metric=0):
+    X = _f32(X)
+    N, D = X.shape
+    ids = np.ascontiguousarray(ids, np.int32)
+    d = np.ascontiguousarray(d, np.float32)
+    M = ids.shape[1]
+    oi = np.empty_like(ids)
+    od = np.empty_like(d)
+    _check(lib().or_refine_2hop(_p(X), N, D, metric, _p(ids), _p(d), M, S, _p(oi), _p(od)), "or_refine_2hop")
+    return oi, od
+
+
+def translate(g, inv):
+    g = np.ascontiguousarray(g, np.uint32)
+    inv = np.ascontiguousarray(inv, np.uint32)
+    N, K = g.shape
+    out = np.empty((N, K), np.uint32)
+    _check(lib().or_translate(_p(g), _p(inv), N, K, _p(out)), "or_translate")
+    return out
+
+
+def prune_occlusion(X, nb, max_degree):
+    X = _f32(X)
+    N, D = X.shape
+    nb = np.ascontiguousarray(nb, np.int64)
+    M = nb.shape[1]
+    out = np.empty((N, M), np.int64)
+    _check(lib().or_prune_occlusion(_p(X), N, D, _p(nb), M, int(max_degree or 0), _p(out)),
+           "or_prune_occlusion")
+    return out
+
+
+# ---- the reference's own code, compiled in place (test-time only) ----
+
+def ref_cagra_prune(G, K):
+    G = np.ascontiguousarray(G).view(np.int32) if np.asarray(G).dtype == np.uint32 else \
+        np.ascontiguousarray(G, np.int32)
+    N, M = G.shape
+    out = np.zeros((N, K), np.uint32)
+    rc = ref().ref_cagra_prune(_p(G), N, M, K, _p(out))
+    return out, rc
+
+
+def ref_detour_counts(G, a):
+    G = np.ascontiguousarray(G).view(np.int32) if np.asarray(G).dtype == np.uint32 else \
+        np.ascontiguousarray(G, np.int32)
+    N, M = G.shape
+    cnt = np.empty(M, np.uint32)
+    _check(ref().ref_detour_counts(_p(G), N, M, a, _p(cnt)), "ref_detour_counts")
+    return cnt
+
+
+def ref_reverse_merge(fwd):
+    fwd = np.ascontiguousarray(fwd, np.uint32)
+    N, K = fwd.shape
+    out = np.empty((N, K), np.uint32)
+    _check(ref().ref_reverse_merge(_p(fwd), N, K, _p(out)), "ref_reverse_merge")
+    return out
+
+
+def ref_translate(g, inv):
+    g = np.ascontiguousarray(g, np.uint32)
+    inv = np.ascontiguousarray(inv, np.uint32)
+    N, K = g.shape
+    out = np.empty((N, K), np.uint32)
+    _check(ref().ref_translate(_p(g), _p(inv), N, K, _p(out)), "ref_translate")
+    return out

@@ -1,0 +1,123 @@
+// ref_harness.cpp -- C entry points over the reference's own CUDA-free
+// headers, compiled in place from /root/reference by oracle/Makefile into
+// oracle/_ref/libgtann_ref.so.  Test infrastructure only: it lets the tests
+// check the CPU restatement (gt_oracle.c) and write golden fixtures against
+// the reference implementation itself.  Nothing here is shipped.
+//
+// Wrapped reference functions:
+//   prune_windowed::compute_detour_counts / select_pruned_row
+//       (src/prune_windowed_core.hpp:189-263), full window via WindowLookup
+//       (src/prune_windowed_core.hpp:50-75), rows taken in the given order;
+//   edge_chunk::build_rank_ordered_csr + merge_rank_ordered_into_row
+//       (src/edge_chunk_accumulator.hpp:235-284, 471-494), fed the reverse
+//       edges {dst = fwd[i][k], src = i, rank = k} of
+//       src/optimize_chunked.cu:372-407;
+//   translate_ids::translate_graph_to_original_order
+//       (src/translate_graph_ids.hpp:75), through temporary files.
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <filesystem>
+#include <stdexcept>
+#include <string>
+#include <vector>
+#include <unistd.h>
+
+#include "prune_windowed_core.hpp"
+#include "edge_chunk_accumulator.hpp"
+#include "graph_io.hpp"
+#include "translate_graph_ids.hpp"
+
+extern "C" {
+
+// 0 = ok, -4 = fewer than K valid candidates in some row, -1 = other error
+int ref_cagra_prune(const int32_t* G, int64_t N, int32_t M, int32_t K, uint32_t* out)
+{
+    try {
+        prune_windowed::WindowLookup w;
+        w.reserve(static_cast<size_t>(N));
+        static const float dummy = 0.f;
+        for (int64_t i = 0; i < N; ++i)
+            w.add(static_cast<uint32_t>(i), G + i * M, &dummy);
+        std::vector<uint32_t> detour;
+        for (int64_t a = 0; a < N; ++a) {
+            prune_windowed::compute_detour_counts(G + a * M, M, w, detour);
+            prune_windowed::select_pruned_row(G + a * M, M, detour, K, out + a * K);
+        }
+        return 0;
+    } catch (const std::runtime_error& e) {
+        return std::string(e.what()).find("fewer than output_degree") != std::string::npos ? -4 : -1;
+    } catch (...) {
+        return -1;
+    }
+}
+
+int ref_detour_counts(const int32_t* G, int64_t N, int32_t M, int64_t a, uint32_t* counts)
+{
+    try {
+        prune_windowed::WindowLookup w;
+        static const float dummy = 0.f;
+        for (int64_t i = 0; i < N; ++i)
+            w.add(static_cast<uint32_t>(i), G + i * M, &dummy);
+        std::vector<uint32_t> detour;
+        prune_windowed::compute_detour_counts(G + a * M, M, w, detour);
+        for (int32_t k = 0; k < M; ++k) counts[k] = detour[static_cast<size_t>(k)];
+        return 0;
+    } catch (...) {
+        return -1;
+    }
+}
+
+int ref_reverse_merge(const uint32_t* fwd, int64_t N, int32_t K, uint32_t* out)
+{
+    try {
+        std::vector<edge_chunk::EdgeRecord> edges;
+        edges.reserve(static_cast<size_t>(N) * K);
+        for (int64_t i = 0; i < N; ++i)
+            for (int32_t k = 0; k < K; ++k)
+                edges.push_back(edge_chunk::EdgeRecord{fwd[i * K + k], static_cast<uint32_t>(i),
+                                                       static_cast<uint16_t>(k)});
+        auto csr = edge_chunk::build_rank_ordered_csr(edges, 0, static_cast<uint32_t>(N));
+        for (int64_t j = 0; j < N; ++j) {
+            uint32_t* row = out + j * K;
+            for (int32_t k = 0; k < K; ++k) row[k] = fwd[j * K + k];
+            const uint32_t lo = csr.row_offsets[static_cast<size_t>(j)];
+            const uint32_t hi = csr.row_offsets[static_cast<size_t>(j) + 1];
+            edge_chunk::merge_rank_ordered_into_row(row, csr.src.data() + lo, hi - lo,
+                                                    static_cast<uint32_t>(K));
+        }
+        return 0;
+    } catch (...) {
+        return -1;
+    }
+}
+
+int ref_translate(const uint32_t* g, const uint32_t* inv, int64_t N, int32_t K, uint32_t* out)
+{
+    try {
+        char tmpl[] = "/tmp/gtann_ref_XXXXXX";
+        char* dir = mkdtemp(tmpl);
+        if (!dir) return -1;
+        const std::string d(dir);
+        graph_io::write_graph(d + "/g.bin", g, N, K);
+        {
+            FILE* f = std::fopen((d + "/inv.bin").c_str(), "wb");
+            if (!f) return -1;
+            std::fwrite(inv, sizeof(uint32_t), static_cast<size_t>(N), f);
+            std::fclose(f);
+        }
+        translate_ids::translate_graph_to_original_order(d + "/g.bin", d + "/inv.bin", d + "/o.bin");
+        std::vector<uint32_t> res;
+        int64_t n2 = 0;
+        int32_t k2 = 0;
+        graph_io::read_forward_graph(d + "/o.bin", res, n2, k2);
+        std::filesystem::remove_all(d);
+        if (n2 != N || k2 != K) return -1;
+        for (size_t i = 0; i < res.size(); ++i) out[i] = res[i];
+        return 0;
+    } catch (...) {
+        return -1;
+    }
+}
+
+}  // extern "C"

@@ -1,0 +1,155 @@
+"""GPU parity of the integer graph stages (sanitize, CAGRA prune, reverse-edge
+merge, translate, end-to-end build) against the CPU oracle and the
+reference's golden fixtures.  All bit-exact."""
+import os
+
+import numpy as np
+import pytest
+
+import gt_oracle as O
+import synth
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def _rand_graph(rng, N, M, pad=0.0, dup=True):
+    if dup:
+        G = rng.integers(0, N, size=(N, M)).astype(np.int32)
+    else:
+        G = np.stack([rng.permutation(np.delete(np.arange(N), i))[:M] for i in range(N)]).astype(np.int32)
+    if pad:
+        G[rng.random((N, M)) < pad] = -1
+    return G
+
+
+def test_sanitize_gpu(ctx):
+    rng = np.random.default_rng(1)
+    G = rng.integers(-1, 600, size=(500, 64)).astype(np.int32)
+    G[3] = -1
+    G[4] = 4
+    np.testing.assert_array_equal(ctx.sanitize(G), O.sanitize(G))
+
+
+def test_prune_golden(ctx):
+    z = np.load(os.path.join(GOLDEN, "prune_golden.npz"))
+    import gtann
+    for c in range(6):
+        G, K = z[f"prune{c}_G"], int(z[f"prune{c}_K"])
+        if int(z[f"prune{c}_rc"]) == 0:
+            np.testing.assert_array_equal(ctx.cagra_prune(G, K), z[f"prune{c}_out"])
+        else:
+            with pytest.raises(gtann.GtannError) as e:
+                ctx.cagra_prune(G, K)
+            assert e.value.code == gtann.GT_EFEWCAND
+
+
+@pytest.mark.parametrize("N,M,K,pad,dup", [(2000, 64, 32, 0.0, False), (1500, 64, 32, 0.0, True),
+                                           (1000, 96, 48, 0.0, True), (800, 128, 64, 0.0, True),
+                                           (3000, 32, 16, 0.001, True), (50, 7, 3, 0.0, True)])
+def test_prune_random(ctx, N, M, K, pad, dup):
+    rng = np.random.default_rng(N + M)
+    G = _rand_graph(rng, N, M, pad, dup)
+    ref, rc, _ = O.cagra_prune(G, K)
+    assert rc == 0
+    np.testing.assert_array_equal(ctx.cagra_prune(G, K), ref)
+
+
+def test_prune_few_candidates_error(ctx):
+    import gtann
+    G = np.array([[1, -1, -1], [0, 2, -1], [0, 1, -1]], np.int32)
+    with pytest.raises(gtann.GtannError) as e:
+        ctx.cagra_prune(G, 2)
+    assert e.value.code == gtann.GT_EFEWCAND
+
+
+def _assert_rows_equal(got, ref, F):
+    bad = np.nonzero((got != ref).any(axis=1))[0]
+    if len(bad):
+        j = int(bad[0])
+        raise AssertionError(f"{len(bad)} rows differ, first {j} (in-degree {int((F == j).sum())}):\n"
+                             f"fwd {F[j].tolist()}\nref {ref[j].tolist()}\ngot {got[j].tolist()}")
+
+
+def test_reverse_merge_golden(ctx):
+    z = np.load(os.path.join(GOLDEN, "revmerge_golden.npz"))
+    for c in range(4):
+        F = z[f"rev{c}_F"]
+        _assert_rows_equal(ctx.reverse_merge(F), z[f"rev{c}_out"], F)
+
+
+@pytest.mark.parametrize("N,K,hub", [(5000, 32, False), (3000, 48, True), (2000, 64, True), (700, 1, False),
+                                     (1000, 7, True), (30, 16, False), (100, 32, True), (60000, 32, True)])
+def test_reverse_merge_random(ctx, N, K, hub):
+    rng = np.random.default_rng(N * K)
+    F = rng.integers(0, N, size=(N, K)).astype(np.uint32)
+    if hub:
+        F[rng.random((N, K)) < 0.2] = 3
+        F[rng.random((N, K)) < 0.05] = 5
+    _assert_rows_equal(ctx.reverse_merge(F), O.reverse_merge(F), F)
+
+
+def test_reverse_merge_out_of_range(ctx):
+    import gtann
+    F = np.zeros((10, 4), np.uint32)
+    F[2, 1] = 10
+    with pytest.raises(gtann.GtannError):
+        ctx.reverse_merge(F)
+
+
+def test_optimize_equals_prune_then_merge(ctx):
+    rng = np.random.default_rng(5)
+    G = _rand_graph(rng, 3000, 64, 0.0, False).view(np.uint32)
+    ref, rc, _ = O.cagra_prune(G, 32)
+    ref = O.reverse_merge(ref)
+    np.testing.assert_array_equal(ctx.optimize(G, 32), ref)
+
+
+def test_translate_gpu(ctx):
+    z = np.load(os.path.join(GOLDEN, "translate_golden.npz"))
+    for c in range(2):
+        np.testing.assert_array_equal(ctx.translate(z[f"tr{c}_g"], z[f"tr{c}_inv"]), z[f"tr{c}_out"])
+    import gtann
+    with pytest.raises(gtann.GtannError):
+        ctx.translate(np.zeros((3, 2), np.uint32), np.array([0, 0, 1], np.uint32))
+
+
+def _structural(graph, N, K):
+    assert graph.shape == (N, K)
+    assert (graph < N).all()
+    assert (graph != np.arange(N)[:, None]).all(), "self loop"
+
+
+def test_build_graph_c1_end_to_end(ctx):
+    """The whole build on C1 with every bucket probed: the pre-prune table is the
+    exact kNN and the final graph equals oracle prune + merge of it."""
+    X, _ = synth.generate("C1")
+    X = np.rint(X * 8).astype(np.float32)   # integer-valued C1: exact distances
+    res = ctx.build_graph(X, n_buckets=16, nprobe=15, M=64, K=32, rounds=1)
+    ex_i, ex_d = O.knn_exact(X, 64)
+    np.testing.assert_array_equal(res.knn_ids, ex_i)
+    np.testing.assert_array_equal(res.knn_dists, ex_d)
+    san = O.sanitize(res.knn_ids)
+    fwd, rc, _ = O.cagra_prune(san, 32)
+    assert rc == 0
+    np.testing.assert_array_equal(res.graph, O.reverse_merge(fwd))
+    _structural(res.graph, len(X), 32)
+
+
+def test_build_graph_recall_c2_small(ctx):
+    X, _ = synth.generate("C2", n=60000)
+    res = ctx.build_graph(X, n_buckets=16, M=64, K=32, rounds=2)
+    q = np.random.default_rng(0).choice(len(X), 500, replace=False)
+    ex_i, _ = O.knn_exact(X, 32, queries=q)
+    rec = np.mean([len(np.intersect1d(res.knn_ids[qq, :32], ex_i[r])) / 32 for r, qq in enumerate(q)])
+    assert rec > 0.9, rec
+    _structural(res.graph, len(X), 32)
+    # the final graph is exactly oracle(prune + merge) of the returned table
+    san = O.sanitize(res.knn_ids)
+    np.testing.assert_array_equal(ctx.sanitize(res.knn_ids), san)
+    fwd, rc, _ = O.cagra_prune(san, 32)
+    assert rc == 0
+    gfwd = ctx.cagra_prune(san, 32)
+    _assert_rows_equal(gfwd, fwd, san)
+    _assert_rows_equal(ctx.reverse_merge(fwd), O.reverse_merge(fwd), fwd)
+    _assert_rows_equal(res.graph, O.reverse_merge(fwd), fwd)

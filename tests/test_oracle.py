@@ -1,0 +1,290 @@
+"""Pins the CPU oracle (oracle/gt_oracle.c) before it is trusted as the checker.
+
+Each oracle function is checked against something other than itself: the
+reference's golden fixtures (tests/golden/, written from the reference's own
+headers), hand-computed known answers, closed forms, and independent numpy
+brute force on integer data.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import gt_oracle as O
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def _np_knn(X, k, metric="l2"):
+    """independent brute force: int64 arithmetic on integer data, lexsort by (d, id)"""
+    Xi = X.astype(np.int64)
+    N = len(X)
+    ids = np.empty((N, k), np.int64)
+    ds = np.empty((N, k), np.int64)
+    for q in range(N):
+        if metric == "ip":
+            d = -(Xi @ Xi[q])
+        else:
+            d = ((Xi - Xi[q]) ** 2).sum(axis=1)
+        order = np.lexsort((np.arange(N), d))
+        order = order[order != q][:k]
+        ids[q], ds[q] = order, d[order]
+    return ids, ds
+
+
+# ---------------------------------------------------------------- kNN
+
+def test_knn_exact_line_known_answer():
+    # points on a line at 0, 1, 3, 6, 10: neighbours of x=3 are 1 (d=4), then
+    # 0 and 6 tied at d=9 (lower id first), then 10 (d=49)
+    X = np.array([[0], [1], [3], [6], [10]], np.float32)
+    ids, d = O.knn_exact(X, 4)
+    assert ids[2].tolist() == [1, 0, 3, 4]
+    assert d[2].tolist() == [4.0, 9.0, 9.0, 49.0]
+    assert ids[0].tolist() == [1, 2, 3, 4] and d[0].tolist() == [1, 9, 36, 100]
+
+
+def test_knn_exact_matches_numpy_bruteforce_integer():
+    rng = np.random.default_rng(3)
+    X = rng.integers(0, 256, size=(300, 128)).astype(np.float32)
+    X[7] = X[11]   # duplicate point: distance 0
+    ids, d = O.knn_exact(X, 20)
+    rid, rd = _np_knn(X, 20)
+    np.testing.assert_array_equal(ids, rid)
+    np.testing.assert_array_equal(d, rd.astype(np.float32))
+    assert ids[7, 0] == 11 and d[7, 0] == 0.0
+
+
+def test_knn_exact_ip_equals_l2_on_unit_vectors():
+    # <x,y> = 1 - |x-y|^2 / 2 on the unit sphere: identical rankings
+    rng = np.random.default_rng(4)
+    X = rng.standard_normal((400, 32)).astype(np.float32)
+    X /= np.linalg.norm(X, axis=1, keepdims=True)
+    i_ip, d_ip = O.knn_exact(X, 10, metric=1)
+    i_l2, d_l2 = O.knn_exact(X, 10, metric=0)
+    np.testing.assert_allclose(-d_ip, 1 - d_l2 / 2, atol=1e-6)
+    assert (i_ip == i_l2).mean() > 0.99
+
+
+def test_knn_exact_query_subset_and_keep_self():
+    rng = np.random.default_rng(5)
+    X = rng.integers(0, 50, size=(120, 16)).astype(np.float32)
+    q = np.array([5, 17, 100])
+    ids, d = O.knn_exact(X, 5, queries=q)
+    full, fd = O.knn_exact(X, 5)
+    np.testing.assert_array_equal(ids, full[q])
+    ids2, d2 = O.knn_exact(X, 5, queries=q, exclude_self=False)
+    assert (ids2[:, 0] == q).all() and (d2[:, 0] == 0).all()
+
+
+def _buckets(rng, N, B):
+    lab = rng.integers(0, B, size=N)
+    lab[:B] = np.arange(B)
+    order = np.argsort(lab, kind="stable")
+    offsets = np.zeros(B + 1, np.int64)
+    np.add.at(offsets, lab + 1, 1)
+    return np.cumsum(offsets), order.astype(np.int32), lab
+
+
+def test_knn_bucketed_all_probed_equals_exact():
+    # config C1's rule: nprobe = buckets - 1 makes the pooled kNN exact
+    rng = np.random.default_rng(6)
+    X = rng.integers(0, 256, size=(500, 64)).astype(np.float32)
+    off, mem, _ = _buckets(rng, 500, 8)
+    probe = np.array([[b2 for b2 in range(8) if b2 != b] for b in range(8)], np.int32)
+    ids, d = O.knn_bucketed(X, off, mem, probe, 16)
+    eids, ed = O.knn_exact(X, 16)
+    np.testing.assert_array_equal(ids, eids)
+    np.testing.assert_array_equal(d, ed)
+
+
+def test_knn_bucketed_matches_numpy_per_bucket():
+    rng = np.random.default_rng(7)
+    N, B, P, M = 400, 10, 2, 12
+    X = rng.integers(0, 100, size=(N, 32)).astype(np.float32)
+    off, mem, lab = _buckets(rng, N, B)
+    probe = np.stack([rng.permutation(np.delete(np.arange(B), b))[:P] for b in range(B)]).astype(np.int32)
+    ids, d = O.knn_bucketed(X, off, mem, probe, M)
+    Xi = X.astype(np.int64)
+    for q in range(0, N, 7):
+        b = lab[q]
+        pool = np.concatenate([np.nonzero(lab == bb)[0] for bb in [b, *probe[b]]])
+        pool = pool[pool != q]
+        dd = ((Xi[pool] - Xi[q]) ** 2).sum(axis=1)
+        o = np.lexsort((pool, dd))[:M]
+        np.testing.assert_array_equal(ids[q], pool[o])
+        np.testing.assert_array_equal(d[q], dd[o].astype(np.float32))
+
+
+def test_merge_rounds_union_dedup():
+    rng = np.random.default_rng(8)
+    X = rng.integers(0, 60, size=(300, 16)).astype(np.float32)
+    ex_i, ex_d = O.knn_exact(X, 10)
+    # two "rounds" each seeing a random half of the true neighbours plus junk
+    Xi = X.astype(np.int64)
+    rounds = []
+    for r in range(2):
+        ri = np.full((300, 10), -1, np.int32)
+        rd = np.full((300, 10), np.inf, np.float32)
+        for q in range(300):
+            cand = rng.choice(np.delete(np.arange(300), q), size=14, replace=False)
+            cand = np.union1d(cand, ex_i[q][rng.random(10) < 0.6])
+            dd = ((Xi[cand] - Xi[q]) ** 2).sum(axis=1)
+            o = np.lexsort((cand, dd))[:10]
+            ri[q, :len(o)], rd[q, :len(o)] = cand[o], dd[o]
+        rounds.append((ri, rd))
+    mi, md = O.merge_rounds(*rounds[0], *rounds[1])
+    for q in range(300):
+        u = np.union1d(rounds[0][0][q], rounds[1][0][q])
+        u = u[u >= 0]
+        dd = ((Xi[u] - Xi[q]) ** 2).sum(axis=1)
+        o = np.lexsort((u, dd))[:10]
+        np.testing.assert_array_equal(mi[q, :len(o)], u[o])
+    # merging the exact table with anything drawn from the same distances is a no-op
+    mi2, md2 = O.merge_rounds(ex_i, ex_d, *rounds[0])
+    np.testing.assert_array_equal(mi2, ex_i)
+
+
+# ---------------------------------------------------------------- sanitize
+
+def test_sanitize_known_answers():
+    knn = np.array([[-1, 2, 0, 5],      # row 0: -1 -> 2, self 0 -> 2, 5 out of range -> 2
+                    [1, -1, -1, -1],    # row 1: only self -> fallback (1+1)%3 = 2
+                    [0, 1, -1, 2]], np.int32)
+    out = O.sanitize(knn)
+    assert out.tolist() == [[2, 2, 2, 2], [2, 2, 2, 2], [0, 1, 0, 0]]
+
+
+# ---------------------------------------------------------------- prune
+
+def test_prune_select_known_answer():
+    # point 0 ranks ids 1..5; rows of 1,2 are built so the detour counts are
+    # {0,0,1,1,2} (test_prune_windowed_core.cpp:93-105 pattern): K=3 keeps ranks 0,1,2
+    G = np.zeros((6, 5), np.int32)
+    G[0] = [1, 2, 3, 4, 5]
+    G[1] = [3, 5, 0, 0, 0]
+    G[2] = [4, 5, 0, 0, 0]
+    assert O.detour_counts(G, 0).tolist() == [0, 0, 1, 1, 2]
+    out, rc, _ = O.cagra_prune(G, 3)
+    assert rc == 0 and out[0].tolist() == [1, 2, 3]
+    out, rc, _ = O.cagra_prune(G, 5)
+    assert out[0].tolist() == [1, 2, 3, 4, 5]
+
+
+def _naive_counts(G, a):
+    """direct triple loop of test_prune_windowed_core.cpp:42-63"""
+    M = G.shape[1]
+    row = G[a]
+    cnt = np.zeros(M, np.int64)
+    for kad in range(M - 1):
+        d = row[kad]
+        if d < 0 or d >= len(G):
+            continue
+        for kab in range(kad + 1, M):
+            if row[kab] >= 0 and row[kab] in G[d]:
+                cnt[kab] += 1
+    return cnt
+
+
+def test_prune_counts_match_naive_definition():
+    rng = np.random.default_rng(9)
+    G = rng.integers(-1, 50, size=(50, 10)).astype(np.int32)
+    for a in range(50):
+        np.testing.assert_array_equal(O.detour_counts(G, a), _naive_counts(G, a))
+
+
+def test_prune_fewer_candidates_error():
+    G = np.array([[1, -1, -1], [0, 2, -1], [0, 1, -1]], np.int32)
+    out, rc, bad = O.cagra_prune(G, 2)
+    assert rc == O.OR_EFEWCAND and bad == 0
+
+
+def test_prune_matches_reference_golden():
+    z = np.load(os.path.join(GOLDEN, "prune_golden.npz"))
+    for c in range(6):
+        G, K = z[f"prune{c}_G"], int(z[f"prune{c}_K"])
+        out, rc, _ = O.cagra_prune(G, K)
+        assert rc == int(z[f"prune{c}_rc"])
+        if rc == 0:
+            np.testing.assert_array_equal(out, z[f"prune{c}_out"])
+        np.testing.assert_array_equal(O.detour_counts(G, 0), z[f"prune{c}_counts0"])
+
+
+@pytest.mark.skipif(not O.ref_available(), reason="reference harness not built here")
+def test_prune_matches_reference_random():
+    rng = np.random.default_rng(10)
+    for t in range(20):
+        N, M = int(rng.integers(20, 120)), int(rng.integers(3, 40))
+        K = int(rng.integers(1, M + 1))
+        G = rng.integers(-1, N, size=(N, M)).astype(np.int32)
+        a, rc, _ = O.cagra_prune(G, K)
+        b, rc2 = O.ref_cagra_prune(G, K)
+        assert rc == rc2
+        if rc == 0:
+            np.testing.assert_array_equal(a, b)
+
+
+# ---------------------------------------------------------------- reverse merge
+
+def test_merge_row_truncation_known_answer():
+    # test_edge_chunk_accumulator.cpp:185-220: 5 candidates for 3 free slots
+    row = O.merge_row([0, 1, 2, 3, 4, 5], [13, 11, 14, 12, 10])
+    assert row.tolist() == [0, 1, 2, 13, 11, 14]
+
+
+def test_reverse_merge_matches_reference_golden():
+    z = np.load(os.path.join(GOLDEN, "revmerge_golden.npz"))
+    for c in range(4):
+        np.testing.assert_array_equal(O.reverse_merge(z[f"rev{c}_F"]), z[f"rev{c}_out"])
+
+
+@pytest.mark.skipif(not O.ref_available(), reason="reference harness not built here")
+def test_reverse_merge_matches_reference_random():
+    rng = np.random.default_rng(11)
+    for t in range(20):
+        N, K = int(rng.integers(5, 200)), int(rng.integers(1, 40))
+        F = rng.integers(0, N, size=(N, K)).astype(np.uint32)
+        np.testing.assert_array_equal(O.reverse_merge(F), O.ref_reverse_merge(F))
+
+
+def test_translate_matches_reference_golden():
+    z = np.load(os.path.join(GOLDEN, "translate_golden.npz"))
+    for c in range(2):
+        np.testing.assert_array_equal(O.translate(z[f"tr{c}_g"], z[f"tr{c}_inv"]), z[f"tr{c}_out"])
+
+
+def test_translate_rejects_non_permutation():
+    with pytest.raises(RuntimeError):
+        O.translate(np.zeros((3, 2), np.uint32), np.array([0, 0, 1], np.uint32))
+
+
+# ---------------------------------------------------------------- refine
+
+def test_refine_fixed_point_and_monotone():
+    rng = np.random.default_rng(12)
+    X = rng.integers(0, 40, size=(300, 16)).astype(np.float32)
+    ex_i, ex_d = O.knn_exact(X, 12)
+    ri, rd = O.refine_2hop(X, ex_i, ex_d, 6)
+    np.testing.assert_array_equal(ri, ex_i)     # exact kNN is a fixed point
+    # a damaged table only improves, elementwise
+    bi, bd = ex_i.copy(), ex_d.copy()
+    bi[:, 6:], bd[:, 6:] = -1, np.inf
+    ri, rd = O.refine_2hop(X, bi, bd, 6)
+    assert (rd <= bd).all()
+    assert ((ri >= 0).sum(axis=1) >= (bi >= 0).sum(axis=1)).all()
+    for q in range(0, 300, 13):                 # every kept distance is exact
+        v = ri[q][ri[q] >= 0]
+        np.testing.assert_array_equal(rd[q][:len(v)], ((X[v] - X[q]) ** 2).sum(axis=1))
+
+
+# ---------------------------------------------------------------- occlusion prune
+
+def test_occlusion_prune_line_known_answer():
+    # v = 0 at x=0 with neighbours at 1, 2, -3: sorted 1 (d=1), 2 (d=4), -3 (d=9);
+    # 2 is occluded by 1 (d(1,2)=1 < 4); -3 is not (d(1,-3)=16 > 9)
+    X = np.array([[0], [1], [2], [-3]], np.float32)
+    nb = np.array([[2, 1, 3], [0, 2, 3], [1, 0, 3], [0, 1, 2]], np.int64)
+    out = O.prune_occlusion(X, nb, 0)
+    assert out[0].tolist() == [1, 3, -1]
+    out = O.prune_occlusion(X, nb, 1)
+    assert out[0].tolist() == [1, -1, -1]
