@@ -145,6 +145,40 @@ struct Ctx {
 
 static int pad_dim(int D) { return (D + 31) / 32 * 32; }
 
+// Lays out work items XCD-major for knn_fused_kernel: groups of items (one
+// group per bucket, sharing its pool) are dealt to the 8 XCDs longest-first
+// onto the least-loaded XCD (cost = query rows x pool rows), each XCD runs
+// its groups biggest-first, and every XCD list is padded with empty items to
+// the same length.
+static std::vector<WorkItem> layout_xcd(const std::vector<std::vector<WorkItem>>& groups)
+{
+    constexpr int kXcd = 8;
+    std::vector<double> cost(groups.size(), 0.0);
+    for (size_t g = 0; g < groups.size(); ++g)
+        for (const WorkItem& it : groups[g]) cost[g] += static_cast<double>(it.q_count) * it.p_count;
+    std::vector<size_t> order(groups.size());
+    std::iota(order.begin(), order.end(), size_t(0));
+    std::stable_sort(order.begin(), order.end(), [&](size_t x, size_t y) { return cost[x] > cost[y]; });
+    std::vector<std::vector<WorkItem>> lists(kXcd);
+    std::vector<double> load(kXcd, 0.0);
+    for (size_t g : order) {
+        const int x = static_cast<int>(std::min_element(load.begin(), load.end()) - load.begin());
+        load[static_cast<size_t>(x)] += cost[g];
+        lists[static_cast<size_t>(x)].insert(lists[static_cast<size_t>(x)].end(), groups[g].begin(), groups[g].end());
+    }
+    size_t per = 0;
+    for (const auto& l : lists) per = std::max(per, l.size());
+    WorkItem empty{};
+    empty.q_count = 0;
+    std::vector<WorkItem> out;
+    out.reserve(per * kXcd);
+    for (auto& l : lists) {
+        l.resize(per, empty);
+        out.insert(out.end(), l.begin(), l.end());
+    }
+    return out;
+}
+
 static size_t dtype_size(int dtype)
 {
     GT_REQUIRE(dtype == GT_DTYPE_F32 || dtype == GT_DTYPE_U8 || dtype == GT_DTYPE_I8, "unknown dtype");
@@ -218,8 +252,8 @@ static void run_knn_flat(Ctx& c, const KnnJob& j, int min_items = 2048)
         splits = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>({want, by_pool, 2048 / j.M, 64})));
     }
     const int64_t chunk = ceil_div(j.np, splits);
-    std::vector<WorkItem> items;
-    items.reserve(static_cast<size_t>(qtiles * splits));
+    std::vector<std::vector<WorkItem>> groups;
+    groups.reserve(static_cast<size_t>(qtiles * splits));
     for (int s = 0; s < splits; ++s) {
         const int64_t p0 = s * chunk;
         const int64_t pc = std::min<int64_t>(chunk, j.np - p0);
@@ -230,9 +264,10 @@ static void run_knn_flat(Ctx& c, const KnnJob& j, int min_items = 2048)
             it.p_begin = p0;
             it.p_count = static_cast<int32_t>(std::max<int64_t>(pc, 0));
             it.out_base = static_cast<int64_t>(s) * j.nq + it.q_begin;
-            items.push_back(it);
+            groups.push_back({it});
         }
     }
+    const std::vector<WorkItem> items = layout_xcd(groups);
     WorkItem* d_items = c.ws<WorkItem>(W_ITEMS, items.size());
     c.h2d(d_items, items.data(), items.size() * sizeof(WorkItem));
     int32_t* oi = j.out_ids;
@@ -373,7 +408,7 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
     int32_t* d_pool = c.ws<int32_t>(W_POOL, static_cast<size_t>(std::max<int64_t>(total, 1)));
     launch_copy_ranges(d_tasks, static_cast<int64_t>(tasks.size()), d_members, d_pool, c.s);
 
-    std::vector<WorkItem> items;
+    std::vector<std::vector<WorkItem>> groups(static_cast<size_t>(C));
     int64_t mp = 0, mb = 0;
     double pr = 0.0;
     for (int64_t bb = 0; bb < C; ++bb) {
@@ -389,10 +424,11 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
             it.p_begin = p0;
             it.p_count = static_cast<int32_t>(npb);
             it.out_base = -1;
-            items.push_back(it);
+            groups[static_cast<size_t>(bb)].push_back(it);
         }
     }
     GT_REQUIRE(mp < (int64_t(1) << 31), "pool too large");
+    const std::vector<WorkItem> items = layout_xcd(groups);
     WorkItem* d_items = c.ws<WorkItem>(W_ITEMS, items.size());
     c.h2d(d_items, items.data(), items.size() * sizeof(WorkItem));
 

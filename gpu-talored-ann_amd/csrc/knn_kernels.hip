@@ -15,6 +15,7 @@
 // order are unique.
 #include "gtann_common.hpp"
 
+#include <cfloat>
 #include <climits>
 #include <cmath>
 
@@ -72,8 +73,8 @@ __device__ __forceinline__ void wave_bitonic_sort(float& d, int32_t& i, int lane
 template <int DP>
 struct KnnSmem {
     float tile[2][kPoolTile][DP + 4];   // +4 floats: rows land on distinct bank groups
-    float tnorm[2][kPoolTile];
-    int32_t trow[2][kPoolTile];         // pool row id, -1 past the slice end
+    float tnorm[3][kPoolTile];          // |p|^2 (L2) or 0 (IP); +inf past the slice end
+    int32_t trow[3][kPoolTile];         // pool row id, -1 past the slice end
     float bd[kQueriesPerBlock][kCB];
     int32_t bi[kQueriesPerBlock][kCB];
     float sBd[kWaves][64];
@@ -86,27 +87,35 @@ struct KnnSmem {
 // Per-lane view of one query's state.  Lanes j and j+32 of a wave hold the
 // same query (both halves of the MFMA's k split) and keep identical copies.
 struct QueryState {
-    float thr;     // keep a candidate iff key <= thr
-    float seed;    // cap from the caller (previous round's M-th) or +inf
+    float thr;     // keep a candidate iff key <= thr (finite: never admits a +inf key)
+    float seed;    // cap from the caller (previous round's M-th), FLT_MAX if none
     int32_t cnt;   // entries in the LDS buffer
     int32_t nL;    // entries in the sorted list (stored in the output row)
+    int32_t self;  // id that must not be kept (the query itself), -2 if none
     int64_t orow;  // output row
 };
 
 // Merges the buffer of query q (0..31 of this wave) into its sorted list
-// (output row), recomputing its threshold.  Called by all 64 lanes.
+// (output row), dropping the query's own id, and recomputes its threshold.
+// Called by all 64 lanes.
 template <int DP>
 __device__ void wave_merge(KnnSmem<DP>& sm, const KnnArgs& a, int w, int lane, int q, QueryState& st)
 {
-    const int nB = __shfl(st.cnt, q);
+    const int nBraw = __shfl(st.cnt, q);
     const int nL = __shfl(st.nL, q);
+    const int32_t self = __shfl(st.self, q);
     const int64_t orow = __shfl(st.orow, q);
     const int M = a.M;
     const int ql = w * kQueriesPerWave + q;
 
     float bd = INFINITY;
     int32_t bi = INT_MAX;
-    if (lane < nB) { bd = sm.bd[ql][lane]; bi = sm.bi[ql][lane]; }
+    if (lane < nBraw) {
+        bd = sm.bd[ql][lane];
+        bi = sm.bi[ql][lane];
+        if (bi == self) { bd = INFINITY; bi = INT_MAX; }
+    }
+    const int nB = static_cast<int>(__popcll(__ballot(bi != INT_MAX)));
     wave_bitonic_sort(bd, bi, lane);
     sm.sBd[w][lane] = bd;
     sm.sBi[w][lane] = bi;
@@ -159,7 +168,55 @@ __device__ void wave_merge(KnnSmem<DP>& sm, const KnnArgs& a, int w, int lane, i
     __threadfence_block();
 }
 
-template <int DP>
+// Filter + append of one finished 32x32 tile (rows of tile `tp`), the slow
+// path taken only when some lane of the wave has a candidate <= its threshold.
+template <int DP, int METRIC>
+__device__ void tile_append(KnnSmem<DP>& sm, const KnnArgs& a, const floatx16& acc, int tp, int w, int lane,
+                            int h, int qlocal, bool qvalid, float qn, QueryState& st)
+{
+    const int b3 = tp % 3;
+    float dv[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int i = 8 * (r >> 2) + 4 * h + (r & 3);
+        const float pn = sm.tnorm[b3][i];
+        dv[r] = METRIC == 0 ? fmaf(-2.f, acc[r], pn + qn) : fmaf(-1.f, acc[r], pn);
+    }
+    uint32_t pass = 0;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) pass |= static_cast<uint32_t>(dv[r] <= st.thr) << r;
+    int np_ = __popc(pass);
+    int np_o = __shfl_xor(np_, 32);
+    const bool need = qvalid && (st.cnt + np_ + np_o > kCB);
+    uint64_t needmask = __ballot(need) & 0xffffffffull;
+    if (needmask) {
+        while (needmask) {
+            const int q = __ffsll(static_cast<unsigned long long>(needmask)) - 1;
+            needmask &= needmask - 1;
+            wave_merge<DP>(sm, a, w, lane, q, st);
+        }
+        pass = 0;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) pass |= static_cast<uint32_t>(dv[r] <= st.thr) << r;
+        np_ = __popc(pass);
+        np_o = __shfl_xor(np_, 32);
+    }
+    if (qvalid) {
+        int off = st.cnt + (h ? np_o : 0);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            if ((pass >> r) & 1u) {
+                const int i = 8 * (r >> 2) + 4 * h + (r & 3);
+                sm.bd[qlocal][off] = dv[r];
+                sm.bi[qlocal][off] = a.out_pos ? tp * kPoolTile + i : sm.trow[b3][i];
+                ++off;
+            }
+        }
+        st.cnt += np_ + np_o;
+    }
+}
+
+template <int DP, int METRIC>
 __global__ void __launch_bounds__(256, 2) knn_fused_kernel(KnnArgs a)
 {
     constexpr int DH = DP / 2;                    // k-steps of 2 dims (one per half wave)
@@ -168,13 +225,14 @@ __global__ void __launch_bounds__(256, 2) knn_fused_kernel(KnnArgs a)
     static_assert(DP % 32 == 0, "row stride must be a multiple of 32 floats");
     __shared__ KnnSmem<DP> sm;
 
-    // XCD-aware order: hardware deals consecutive workgroups round-robin over
-    // the 8 XCDs, so give each XCD a contiguous run of work items (same
-    // bucket => same pool rows => shared L2).
-    const int per = (a.n_items + 7) / 8;
+    // Work items are laid out XCD-major by the host: the hardware deals
+    // consecutive workgroups round-robin over the 8 XCDs, so XCD x runs items
+    // [x*per, (x+1)*per) in order (same bucket => same pool rows => shared L2).
+    const int per = a.n_items / 8;
     const int item_idx = static_cast<int>(blockIdx.x % 8) * per + static_cast<int>(blockIdx.x / 8);
     if (item_idx >= a.n_items) return;
     const WorkItem it = a.items[item_idx];
+    if (it.q_count <= 0) return;
 
     const int tid = threadIdx.x;
     const int w = tid >> 6, lane = tid & 63, j = lane & 31, h = lane >> 5;
@@ -182,14 +240,15 @@ __global__ void __launch_bounds__(256, 2) knn_fused_kernel(KnnArgs a)
     const bool qvalid = qlocal < it.q_count;
     const int64_t qi = it.q_begin + qlocal;
     const int32_t qrow = qvalid ? (a.q_rows ? a.q_rows[qi] : static_cast<int32_t>(qi)) : 0;
-    const float qn = (qvalid && a.metric == 0) ? a.nq[qrow] : 0.f;
+    const float qn = (qvalid && METRIC == 0) ? a.nq[qrow] : 0.f;
 
     QueryState st;
-    st.seed = INFINITY;
-    if (qvalid && a.seed_d) st.seed = a.seed_d[static_cast<int64_t>(qrow) * a.seed_ld + a.seed_ld - 1];
+    st.seed = FLT_MAX;
+    if (qvalid && a.seed_d) st.seed = fminf(a.seed_d[static_cast<int64_t>(qrow) * a.seed_ld + a.seed_ld - 1], FLT_MAX);
     st.thr = qvalid ? st.seed : -INFINITY;
     st.cnt = 0;
     st.nL = 0;
+    st.self = a.exclude_self ? qrow : -2;
     st.orow = it.out_base >= 0 ? it.out_base + qlocal : static_cast<int64_t>(qrow);
 
     // query fragment: dims [h*DH, h*DH + DH) of query row qrow
@@ -203,54 +262,67 @@ __global__ void __launch_bounds__(256, 2) knn_fused_kernel(KnnArgs a)
         }
     }
 
-    const int ntiles = static_cast<int>((it.p_count + kPoolTile - 1) / kPoolTile);
+    const int pcount = it.p_count;
+    const int ntiles = (pcount + kPoolTile - 1) / kPoolTile;
+    auto pool_row = [&](int p) -> int32_t {
+        if (p >= pcount) return -1;
+        const int64_t pl = it.p_begin + p;
+        return a.p_rows ? a.p_rows[pl] : static_cast<int32_t>(pl);
+    };
+    auto row_norm = [&](int32_t row) -> float {
+        if (row < 0) return INFINITY;
+        return METRIC == 0 ? a.np[row] : 0.f;
+    };
+
+    // Pool tiles flow through three stages: ids (two tiles ahead) -> row
+    // data in registers (one tile ahead) -> LDS.  Thread tid loads float4 c4_u
+    // of tile row r_u; threads < 32 also carry the id and norm of row tid.
+    int32_t idn[F4_THREAD];
     float4 pre[F4_THREAD];
-    int32_t pre_row = -1;
-    float pre_norm = 0.f;
-
-    auto load_tile = [&](int t) {
+    int32_t rid_next = -1;   // id of row tid of the next tile to load (tid < 32)
+    auto load_ids = [&](int t) {
+#pragma unroll
+        for (int u = 0; u < F4_THREAD; ++u) idn[u] = pool_row(t * kPoolTile + (tid + 256 * u) / F4_ROW);
+        if (tid < kPoolTile) rid_next = pool_row(t * kPoolTile + tid);
+    };
+    auto load_rows = [&]() {
+#pragma unroll
+        for (int u = 0; u < F4_THREAD; ++u) {
+            const int c4 = (tid + 256 * u) % F4_ROW;
+            pre[u] = idn[u] >= 0 ? reinterpret_cast<const float4*>(a.Xp + static_cast<int64_t>(idn[u]) * DP)[c4]
+                                 : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    };
+    auto store_rows = [&](int buf) {
 #pragma unroll
         for (int u = 0; u < F4_THREAD; ++u) {
             const int e = tid + 256 * u;
-            const int r = e / F4_ROW, c4 = e % F4_ROW;
-            const int p = t * kPoolTile + r;
-            pre[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (p < it.p_count) {
-                const int64_t pl = it.p_begin + p;
-                const int32_t prow = a.p_rows ? a.p_rows[pl] : static_cast<int32_t>(pl);
-                pre[u] = reinterpret_cast<const float4*>(a.Xp + static_cast<int64_t>(prow) * DP)[c4];
-            }
+            *reinterpret_cast<float4*>(&sm.tile[buf][e / F4_ROW][4 * (e % F4_ROW)]) = pre[u];
         }
-        if (tid < kPoolTile) {
-            const int p = t * kPoolTile + tid;
-            pre_row = -1;
-            pre_norm = 0.f;
-            if (p < it.p_count) {
-                const int64_t pl = it.p_begin + p;
-                pre_row = a.p_rows ? a.p_rows[pl] : static_cast<int32_t>(pl);
-                pre_norm = a.metric == 0 ? a.np[pre_row] : 0.f;
-            }
-        }
-    };
-    auto store_tile = [&](int buf) {
-#pragma unroll
-        for (int u = 0; u < F4_THREAD; ++u) {
-            const int e = tid + 256 * u;
-            const int r = e / F4_ROW, c4 = e % F4_ROW;
-            *reinterpret_cast<float4*>(&sm.tile[buf][r][4 * c4]) = pre[u];
-        }
-        if (tid < kPoolTile) { sm.trow[buf][tid] = pre_row; sm.tnorm[buf][tid] = pre_norm; }
     };
 
-    if (ntiles > 0) {
-        load_tile(0);
-        store_tile(0);
-    }
+    if (tid < kPoolTile) { sm.tnorm[2][tid] = INFINITY; sm.trow[2][tid] = -1; }
+    load_ids(0);
+    load_rows();
+    int32_t rid_cur = rid_next;
+    float rn_cur = tid < kPoolTile ? row_norm(rid_cur) : 0.f;
+    store_rows(0);
+    if (tid < kPoolTile) { sm.trow[0][tid] = rid_cur; sm.tnorm[0][tid] = rn_cur; }
+    load_ids(1);
     __syncthreads();
+
+    floatx16 acc_prev;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc_prev[r] = 0.f;
 
     for (int t = 0; t < ntiles; ++t) {
         const int buf = t & 1;
-        if (t + 1 < ntiles) load_tile(t + 1);
+        // next tile: rows (ids arrived during the previous tile) and norms
+        load_rows();
+        rid_cur = rid_next;
+        rn_cur = tid < kPoolTile ? row_norm(rid_cur) : 0.f;
+        // tile after next: ids
+        load_ids(t + 2);
 
         // D[i][j] = sum_k pool[i][k] * query[j][k]; lane supplies A[i=lane%32][k=lane/32]
         // (pool row j, dim h*DH+s) and B[k=lane/32][j=lane%32] (query j, same dim).
@@ -267,55 +339,41 @@ __global__ void __launch_bounds__(256, 2) knn_fused_kernel(KnnArgs a)
             acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.w, qf[4 * s + 3], acc, 0, 0, 0);
         }
 
-        // acc[r] is D[i][j] with i = 8*(r/4) + 4*h + r%4 (pool row of the tile).
-        float dv[16];
-        uint32_t okmask = 0;
+        // Fast filter of the previous tile (t-1), independent of the MFMA
+        // chain above: min key per lane.  acc_prev[r] is D[i][j] with
+        // i = 8*(r/4) + 4*h + r%4.  Rows past the slice have +inf norm.
+        const int pb3 = (t + 2) % 3;   // (t-1) mod 3
+        float mkey = INFINITY;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const float4 pn = *reinterpret_cast<const float4*>(&sm.tnorm[pb3][8 * g + 4 * h]);
+            const float n4[4] = {pn.x, pn.y, pn.z, pn.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float d = METRIC == 0 ? fmaf(-2.f, acc_prev[4 * g + e], n4[e] + qn)
+                                            : fmaf(-1.f, acc_prev[4 * g + e], n4[e]);
+                mkey = fminf(mkey, d);
+            }
+        }
+        if (t > 0 && __ballot(mkey <= st.thr))
+            tile_append<DP, METRIC>(sm, a, acc_prev, t - 1, w, lane, h, qlocal, qvalid, qn, st);
+
+        store_rows(buf ^ 1);
+        if (tid < kPoolTile) { sm.trow[(t + 1) % 3][tid] = rid_cur; sm.tnorm[(t + 1) % 3][tid] = rn_cur; }
+        __syncthreads();
+        acc_prev = acc;
+    }
+    if (ntiles > 0) {
+        const int pb3 = (ntiles - 1) % 3;
+        float mkey = INFINITY;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int i = 8 * (r >> 2) + 4 * h + (r & 3);
-            const int32_t prow = sm.trow[buf][i];
-            const float d = a.metric == 0 ? fmaf(-2.f, acc[r], sm.tnorm[buf][i] + qn) : -acc[r];
-            dv[r] = d;
-            const bool ok = prow >= 0 && !(a.exclude_self && prow == qrow);
-            okmask |= static_cast<uint32_t>(ok) << r;
+            const float pn = sm.tnorm[pb3][i];
+            mkey = fminf(mkey, METRIC == 0 ? fmaf(-2.f, acc_prev[r], pn + qn) : fmaf(-1.f, acc_prev[r], pn));
         }
-        uint32_t pass = 0;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) pass |= static_cast<uint32_t>(dv[r] <= st.thr) << r;
-        pass &= okmask;
-        int np_ = __popc(pass);
-        int np_o = __shfl_xor(np_, 32);
-        const bool need = qvalid && (st.cnt + np_ + np_o > kCB);
-        uint64_t needmask = __ballot(need) & 0xffffffffull;
-        if (needmask) {
-            while (needmask) {
-                const int q = __ffsll(static_cast<unsigned long long>(needmask)) - 1;
-                needmask &= needmask - 1;
-                wave_merge<DP>(sm, a, w, lane, q, st);
-            }
-            pass = 0;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) pass |= static_cast<uint32_t>(dv[r] <= st.thr) << r;
-            pass &= okmask;
-            np_ = __popc(pass);
-            np_o = __shfl_xor(np_, 32);
-        }
-        if (qvalid) {
-            int off = st.cnt + (h ? np_o : 0);
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                if ((pass >> r) & 1u) {
-                    const int i = 8 * (r >> 2) + 4 * h + (r & 3);
-                    sm.bd[qlocal][off] = dv[r];
-                    sm.bi[qlocal][off] = a.out_pos ? t * kPoolTile + i : sm.trow[buf][i];
-                    ++off;
-                }
-            }
-            st.cnt += np_ + np_o;
-        }
-
-        if (t + 1 < ntiles) store_tile(buf ^ 1);
-        __syncthreads();
+        if (__ballot(mkey <= st.thr))
+            tile_append<DP, METRIC>(sm, a, acc_prev, ntiles - 1, w, lane, h, qlocal, qvalid, qn, st);
     }
 
     // flush the remaining buffers
@@ -378,23 +436,31 @@ __global__ void __launch_bounds__(64) merge_partials_kernel(const int32_t* __res
     }
 }
 
+template <int METRIC>
+static void launch_knn_metric(const KnnArgs& a, dim3 grid, hipStream_t stream)
+{
+    switch (a.Dp) {
+    case 32:  hipLaunchKernelGGL((knn_fused_kernel<32, METRIC>), grid, dim3(256), 0, stream, a); break;
+    case 64:  hipLaunchKernelGGL((knn_fused_kernel<64, METRIC>), grid, dim3(256), 0, stream, a); break;
+    case 96:  hipLaunchKernelGGL((knn_fused_kernel<96, METRIC>), grid, dim3(256), 0, stream, a); break;
+    case 128: hipLaunchKernelGGL((knn_fused_kernel<128, METRIC>), grid, dim3(256), 0, stream, a); break;
+    case 160: hipLaunchKernelGGL((knn_fused_kernel<160, METRIC>), grid, dim3(256), 0, stream, a); break;
+    case 192: hipLaunchKernelGGL((knn_fused_kernel<192, METRIC>), grid, dim3(256), 0, stream, a); break;
+    case 224: hipLaunchKernelGGL((knn_fused_kernel<224, METRIC>), grid, dim3(256), 0, stream, a); break;
+    case 256: hipLaunchKernelGGL((knn_fused_kernel<256, METRIC>), grid, dim3(256), 0, stream, a); break;
+    default: GT_REQUIRE(false, "padded dimension " + std::to_string(a.Dp) + " not supported (D <= 256)");
+    }
+}
+
+// n_items must be a multiple of 8 (XCD-major layout, see knn_fused_kernel).
 void launch_knn_fused(const KnnArgs& a, hipStream_t stream)
 {
     if (a.n_items <= 0) return;
     GT_REQUIRE(a.M >= 1 && a.M <= kMaxM, "list length must be in [1, 128]");
-    const int per = (a.n_items + 7) / 8;
-    const dim3 grid(static_cast<unsigned>(per * 8));
-    switch (a.Dp) {
-    case 32:  hipLaunchKernelGGL(knn_fused_kernel<32>, grid, dim3(256), 0, stream, a); break;
-    case 64:  hipLaunchKernelGGL(knn_fused_kernel<64>, grid, dim3(256), 0, stream, a); break;
-    case 96:  hipLaunchKernelGGL(knn_fused_kernel<96>, grid, dim3(256), 0, stream, a); break;
-    case 128: hipLaunchKernelGGL(knn_fused_kernel<128>, grid, dim3(256), 0, stream, a); break;
-    case 160: hipLaunchKernelGGL(knn_fused_kernel<160>, grid, dim3(256), 0, stream, a); break;
-    case 192: hipLaunchKernelGGL(knn_fused_kernel<192>, grid, dim3(256), 0, stream, a); break;
-    case 224: hipLaunchKernelGGL(knn_fused_kernel<224>, grid, dim3(256), 0, stream, a); break;
-    case 256: hipLaunchKernelGGL(knn_fused_kernel<256>, grid, dim3(256), 0, stream, a); break;
-    default: GT_REQUIRE(false, "padded dimension " + std::to_string(a.Dp) + " not supported (D <= 256)");
-    }
+    GT_REQUIRE(a.n_items % 8 == 0, "work list must be padded to a multiple of 8");
+    const dim3 grid(static_cast<unsigned>(a.n_items));
+    if (a.metric == 0) launch_knn_metric<0>(a, grid, stream);
+    else launch_knn_metric<1>(a, grid, stream);
     GT_HIP(hipGetLastError());
 }
 
