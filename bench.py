@@ -1,7 +1,8 @@
 """Benchmark of the bucketed CAGRA-style graph build on one MI355X.
 
-A step is one whole graph build -- 3 rounds of (centroids -> probe table ->
-top-2 assignment -> fused MFMA kNN over all buckets -> cross-round merge),
+A step is one whole graph build -- 2 rounds of (centroids refined by 3 Lloyd
+iterations on a training subset -> probe table -> top-2 assignment -> fused
+MFMA kNN over all buckets -> cross-round merge),
 sanitize, CAGRA prune, reverse-edge merge -- of configuration C2
 (1,000,000 x 128 fp32 integer-valued points, L2, 256 buckets, M 64 -> K 32)
 with the dataset already resident in HBM.  Prints one JSON line.
@@ -64,9 +65,17 @@ def main():
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--config", default="C2")
-    ap.add_argument("--rounds", type=int, default=3)
+    ap.add_argument("--rounds", type=int, default=2)
+    ap.add_argument("--kmeans-iters", type=int, default=3)
+    ap.add_argument("--nprobe", type=int, default=1)
+    ap.add_argument("--reference-knobs", action="store_true",
+                    help="the reference's own bucketing settings: 3 rounds, sampled data points as "
+                         "centroids, nprobe = ceil(20000 / avg bucket)")
     ap.add_argument("--cpu-sample", type=int, default=2000)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="run one device-to-device copy of this many MiB first (calibrates the "
+                         "FETCH_SIZE/WRITE_SIZE counters of rocprofv3 --pmc against known bytes)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -82,9 +91,18 @@ def main():
     X, _ = synth.generate(args.config)
     N, D = X.shape
     Xd = torch.from_numpy(X).cuda()
+    if args.copy_probe_mib:
+        src = torch.empty(args.copy_probe_mib << 18, dtype=torch.float32, device="cuda").fill_(1.0)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        del src, dst
     torch.cuda.synchronize()
     ctx = gtann.Context(0)
-    kw = dict(n_buckets=cfg.buckets, M=cfg.M, K=cfg.K, rounds=args.rounds, metric=cfg.metric)
+    if args.reference_knobs:
+        args.rounds, args.kmeans_iters, args.nprobe = 3, 0, -1
+    kw = dict(n_buckets=cfg.buckets, M=cfg.M, K=cfg.K, rounds=args.rounds, metric=cfg.metric,
+              kmeans_iters=args.kmeans_iters, nprobe=args.nprobe)
     for _ in range(args.warmup):
         ctx.build_graph(Xd, **kw)
     torch.cuda.synchronize()
@@ -134,8 +152,10 @@ def main():
         "data": "synthetic (seeded Gaussian mixture, gpu-talored-ann_amd/synth.py)",
         "config": {
             "workload": f"{args.config}: {N} x {D} {cfg.dtype}, {cfg.metric.upper()}, {cfg.buckets} buckets, "
-                        f"M {cfg.M} -> K {cfg.K}, {args.rounds} rounds, nprobe ceil(20000/avg bucket)",
+                        f"M {cfg.M} -> K {cfg.K}, {args.rounds} rounds, {args.kmeans_iters} Lloyd iterations, "
+                        f"nprobe {args.nprobe if args.nprobe >= 0 else 'ceil(20000/avg bucket)'}",
             "points": N, "dim": D, "buckets": cfg.buckets, "M": cfg.M, "K": cfg.K, "rounds": args.rounds,
+            "kmeans_iters": args.kmeans_iters, "nprobe": args.nprobe,
         },
         "build_seconds": wall,
         **rec,

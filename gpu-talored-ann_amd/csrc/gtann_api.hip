@@ -489,44 +489,68 @@ static void make_buckets(Ctx& c, const DevMatrix& X, int64_t C, int nprobe, int 
     Cm.data = d_cm;
     Cm.norms = d_cn;
 
-    std::vector<uint32_t> top2(static_cast<size_t>(2 * N));
-    int32_t* d_t2 = c.ws<int32_t>(W_IDS3, static_cast<size_t>(2 * N));
-    float* d_t2d = c.ws<float>(W_D3, static_cast<size_t>(2 * N));
-    std::vector<int32_t> bucket_of;
+    // Lloyd iterations on a training subset (the reference's KMeans|| also
+    // trains on a subset, src/bucket.cu:8857-8880): nearest centroid of every
+    // sampled row, then each centroid moves to the mean of its sampled members.
     const bool data_points = kmeans_iters <= 0;
-    for (int it = 0; it <= std::max(0, kmeans_iters); ++it) {
-        KnnJob j;
-        j.Q = &X;
-        j.P = &Cm;
-        j.nq = N;
-        j.np = C;
-        j.M = std::min<int64_t>(2, C);
-        j.metric = metric;
-        j.exclude_self = false;
-        j.out_pos = true;
-        j.out_ids = d_t2;
-        j.out_d = d_t2d;
-        if (j.M == 2) {
+    if (!data_points) {
+        const int64_t S = std::min<int64_t>(N, std::max<int64_t>(65536, 256 * C));
+        std::vector<int32_t> srows = sample_ids(N, S, seed * 0x2545F4914F6CDD1Dull + 7);
+        int32_t* d_srows = c.ws<int32_t>(W_QROWS, static_cast<size_t>(S));
+        c.h2d(d_srows, srows.data(), static_cast<size_t>(S) * sizeof(int32_t));
+        int32_t* d_n1 = c.ws<int32_t>(W_IDS3, static_cast<size_t>(S));
+        float* d_n1d = c.ws<float>(W_D3, static_cast<size_t>(S));
+        std::vector<int32_t> nearest(static_cast<size_t>(S));
+        for (int it = 0; it < kmeans_iters; ++it) {
+            KnnJob j;
+            j.Q = &X;
+            j.P = &Cm;
+            j.q_rows = d_srows;
+            j.nq = S;
+            j.np = C;
+            j.M = 1;
+            j.metric = metric;
+            j.exclude_self = false;
+            j.out_pos = true;
+            j.out_ids = d_n1;
+            j.out_d = d_n1d;
             run_knn_flat(c, j, 1);
-            c.d2h(top2.data(), d_t2, top2.size() * sizeof(uint32_t));
+            c.d2h(nearest.data(), d_n1, static_cast<size_t>(S) * sizeof(int32_t));
             c.sync();
-        } else {
-            std::fill(top2.begin(), top2.end(), 0u);
-            for (int64_t i = 0; i < N; ++i) top2[static_cast<size_t>(2 * i + 1)] = 0xffffffffu;
-        }
-        if (it < kmeans_iters) {
-            // Lloyd step: nearest-centroid assignment, then member means
-            std::vector<int32_t> nearest(static_cast<size_t>(N));
-            for (int64_t i = 0; i < N; ++i) nearest[static_cast<size_t>(i)] = static_cast<int32_t>(top2[static_cast<size_t>(2 * i)]);
             Buckets tmp;
             csr_from_assignment(nearest, C, tmp);
-            int32_t* d_mem = c.ws<int32_t>(W_MEMBERS, static_cast<size_t>(N));
-            c.h2d(d_mem, tmp.members.data(), static_cast<size_t>(N) * sizeof(int32_t));
+            for (auto& m : tmp.members) m = srows[static_cast<size_t>(m)];   // sample index -> row id
+            int32_t* d_mem = c.ws<int32_t>(W_MEMBERS, static_cast<size_t>(S));
+            c.h2d(d_mem, tmp.members.data(), static_cast<size_t>(S) * sizeof(int32_t));
             int64_t* d_off = c.ws<int64_t>(W_OFF, static_cast<size_t>(C + 1));
             c.h2d(d_off, tmp.offsets.data(), static_cast<size_t>(C + 1) * sizeof(int64_t));
             launch_centroid_sums(X.data, X.Dp, d_mem, d_off, C, d_cm, c.s);
             launch_row_norms(d_cm, C, X.Dp, d_cn, c.s);
         }
+    }
+
+    // final assignment of every point: exact top-2 centroids + two-choice rule
+    std::vector<uint32_t> top2(static_cast<size_t>(2 * N), 0xffffffffu);
+    std::vector<int32_t> bucket_of;
+    if (C >= 2) {
+        int32_t* d_t2 = c.ws<int32_t>(W_IDS3, static_cast<size_t>(2 * N));
+        float* d_t2d = c.ws<float>(W_D3, static_cast<size_t>(2 * N));
+        KnnJob j;
+        j.Q = &X;
+        j.P = &Cm;
+        j.nq = N;
+        j.np = C;
+        j.M = 2;
+        j.metric = metric;
+        j.exclude_self = false;
+        j.out_pos = true;
+        j.out_ids = d_t2;
+        j.out_d = d_t2d;
+        run_knn_flat(c, j, 1);
+        c.d2h(top2.data(), d_t2, top2.size() * sizeof(uint32_t));
+        c.sync();
+    } else {
+        for (int64_t i = 0; i < N; ++i) top2[static_cast<size_t>(2 * i)] = 0u;
     }
     assign_two_choice(top2, N, C, balance, data_points ? &cid : nullptr, bucket_of);
     csr_from_assignment(bucket_of, C, b);
@@ -665,13 +689,13 @@ void gt_build_params_default(gt_build_params* p)
     if (!p) return;
     p->metric = GT_METRIC_L2;
     p->n_buckets = 0;   // 0 = N / 4000
-    p->nprobe = -1;     // -1 = ceil(20000 / avg bucket) (sk/scripts/dataset_env.py:12,56)
+    p->nprobe = 1;      // -1 = the reference's rule ceil(20000 / avg bucket) (sk/scripts/dataset_env.py:12,56)
     p->M = 64;
     p->K = 32;
-    p->rounds = 3;
+    p->rounds = 2;
     p->refine_passes = 0;
     p->refine_sample = 16;
-    p->kmeans_iters = 0;
+    p->kmeans_iters = 3;
     p->balance = 0.8f;
     p->seed = 42;
 }

@@ -75,10 +75,7 @@ struct KnnSmem {
     float tile[2][kPoolTile][DP + 4];   // +4 floats: rows land on distinct bank groups
     float tnorm[3][kPoolTile];          // |p|^2 (L2) or 0 (IP); +inf past the slice end
     int32_t trow[3][kPoolTile];         // pool row id, -1 past the slice end
-    float bd[kQueriesPerBlock][kCB];
-    int32_t bi[kQueriesPerBlock][kCB];
-    float sBd[kWaves][64];
-    int32_t sBi[kWaves][64];
+    float2 buf[kQueriesPerBlock][kCB];  // (key, id as bits) candidates awaiting a merge
     float sLd[kWaves][kMaxM];
     int32_t sLi[kWaves][kMaxM];
     float sthr[kWaves];
@@ -95,30 +92,37 @@ struct QueryState {
     int64_t orow;  // output row
 };
 
+// Waits until every vector memory access of this wave has completed: the
+// list rows a merge stores are loaded again by the next merge of the same
+// query, which always comes after one of these waits (tile start, flush).
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }   // vmcnt(0)
+
+// List rows are read from L2 (agent scope), never from a possibly stale L1 line.
+__device__ __forceinline__ float load_list_d(const float* p)
+{
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int32_t load_list_i(const int32_t* p)
+{
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Merges the buffer of query q (0..31 of this wave) into its sorted list
 // (output row), dropping the query's own id, and recomputes its threshold.
+// Positions come from rank counting: a buffer entry's position is its rank
+// among the buffer plus the number of list entries before it; a list entry's
+// position is its index plus the number of buffer entries before it.
 // Called by all 64 lanes.
 template <int DP>
 __device__ void wave_merge(KnnSmem<DP>& sm, const KnnArgs& a, int w, int lane, int q, QueryState& st)
 {
-    const int nBraw = __shfl(st.cnt, q);
+    const int nB = __shfl(st.cnt, q);
     const int nL = __shfl(st.nL, q);
     const int32_t self = __shfl(st.self, q);
     const int64_t orow = __shfl(st.orow, q);
     const int M = a.M;
     const int ql = w * kQueriesPerWave + q;
-
-    float bd = INFINITY;
-    int32_t bi = INT_MAX;
-    if (lane < nBraw) {
-        bd = sm.bd[ql][lane];
-        bi = sm.bi[ql][lane];
-        if (bi == self) { bd = INFINITY; bi = INT_MAX; }
-    }
-    const int nB = static_cast<int>(__popcll(__ballot(bi != INT_MAX)));
-    wave_bitonic_sort(bd, bi, lane);
-    sm.sBd[w][lane] = bd;
-    sm.sBi[w][lane] = bi;
+    float2* B = sm.buf[ql];
 
     float ld[2];
     int32_t li[2];
@@ -128,16 +132,32 @@ __device__ void wave_merge(KnnSmem<DP>& sm, const KnnArgs& a, int w, int lane, i
         ld[e] = INFINITY;
         li[e] = INT_MAX;
         if (idx < nL) {
-            ld[e] = a.out_d[orow * M + idx];
-            li[e] = a.out_ids[orow * M + idx];
+            ld[e] = load_list_d(a.out_d + orow * M + idx);
+            li[e] = load_list_i(a.out_ids + orow * M + idx);
         }
         if (idx < kMaxM) { sm.sLd[w][idx] = ld[e]; sm.sLi[w][idx] = li[e]; }
     }
+    // the query's own id never enters the list
+    if (lane < nB && __float_as_int(B[lane].y) == self) B[lane] = make_float2(INFINITY, __int_as_float(INT_MAX));
     wave_sync();
 
-    const int total = nL + nB;
-    if (lane < nB) {
-        const int pos = lane + lower_bound_lds(sm.sLd[w], sm.sLi[w], nL, bd, bi);
+    float bd = INFINITY;
+    int32_t bi = INT_MAX;
+    if (lane < nB) { const float2 v = B[lane]; bd = v.x; bi = __float_as_int(v.y); }
+    int rb = 0;              // rank of this lane's buffer entry among the buffer
+    int cl0 = 0, cl1 = 0;    // buffer entries before list entries lane, lane+64
+    for (int k = 0; k < nB; ++k) {
+        const float2 v = B[k];
+        const int32_t vi = __float_as_int(v.y);
+        rb += key_less(v.x, vi, bd, bi);
+        cl0 += key_less(v.x, vi, ld[0], li[0]);
+        cl1 += key_less(v.x, vi, ld[1], li[1]);
+    }
+    const bool bvalid = lane < nB && bi != INT_MAX;
+    const int nBv = static_cast<int>(__popcll(__ballot(bvalid)));
+    const int total = nL + nBv;
+    if (bvalid) {
+        const int pos = rb + lower_bound_lds(sm.sLd[w], sm.sLi[w], nL, bd, bi);
         if (pos < M) {
             a.out_d[orow * M + pos] = bd;
             a.out_ids[orow * M + pos] = bi;
@@ -148,7 +168,7 @@ __device__ void wave_merge(KnnSmem<DP>& sm, const KnnArgs& a, int w, int lane, i
     for (int e = 0; e < 2; ++e) {
         const int idx = lane + 64 * e;
         if (idx < nL) {
-            const int pos = idx + lower_bound_lds(sm.sBd[w], sm.sBi[w], nB, ld[e], li[e]);
+            const int pos = idx + (e == 0 ? cl0 : cl1);
             if (pos < M) {
                 a.out_d[orow * M + pos] = ld[e];
                 a.out_ids[orow * M + pos] = li[e];
@@ -164,8 +184,6 @@ __device__ void wave_merge(KnnSmem<DP>& sm, const KnnArgs& a, int w, int lane, i
         st.nL = newn;
         st.thr = (newn == M) ? fminf(st.seed, mth) : st.seed;
     }
-    // the list rows written above are read back by this wave's next merge
-    __threadfence_block();
 }
 
 // Filter + append of one finished 32x32 tile (rows of tile `tp`), the slow
@@ -207,8 +225,8 @@ __device__ void tile_append(KnnSmem<DP>& sm, const KnnArgs& a, const floatx16& a
         for (int r = 0; r < 16; ++r) {
             if ((pass >> r) & 1u) {
                 const int i = 8 * (r >> 2) + 4 * h + (r & 3);
-                sm.bd[qlocal][off] = dv[r];
-                sm.bi[qlocal][off] = a.out_pos ? tp * kPoolTile + i : sm.trow[b3][i];
+                const int32_t id = a.out_pos ? tp * kPoolTile + i : sm.trow[b3][i];
+                sm.buf[qlocal][off] = make_float2(dv[r], __int_as_float(id));
                 ++off;
             }
         }
@@ -317,6 +335,7 @@ __global__ void __launch_bounds__(256, 2) knn_fused_kernel(KnnArgs a)
 
     for (int t = 0; t < ntiles; ++t) {
         const int buf = t & 1;
+        wait_vmem();   // ids of the next tile, and any list rows stored by merges
         // next tile: rows (ids arrived during the previous tile) and norms
         load_rows();
         rid_cur = rid_next;
@@ -364,6 +383,7 @@ __global__ void __launch_bounds__(256, 2) knn_fused_kernel(KnnArgs a)
         acc_prev = acc;
     }
     if (ntiles > 0) {
+        wait_vmem();   // list rows stored by the last iteration's merges
         const int pb3 = (ntiles - 1) % 3;
         float mkey = INFINITY;
 #pragma unroll
@@ -377,6 +397,7 @@ __global__ void __launch_bounds__(256, 2) knn_fused_kernel(KnnArgs a)
     }
 
     // flush the remaining buffers
+    wait_vmem();
     uint64_t rem = __ballot(qvalid && st.cnt > 0) & 0xffffffffull;
     while (rem) {
         const int q = __ffsll(static_cast<unsigned long long>(rem)) - 1;

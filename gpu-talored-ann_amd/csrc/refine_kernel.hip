@@ -146,22 +146,40 @@ __global__ void __launch_bounds__(256) refine_2hop_kernel(const float* __restric
     for (int p = nr + ns + tid; p < M; p += 256) { out_ids[a * M + p] = -1; out_d[a * M + p] = INFINITY; }
 }
 
-// Lloyd update: centroid c = mean of its member rows (fixed summation order);
-// empty buckets keep their centroid.
+// Lloyd update: centroid c = mean of its member rows; empty buckets keep
+// their centroid.  One block per centroid: thread t sums dimension t % Dp over
+// members t / Dp, t / Dp + parts, ... and the parts are added in a fixed
+// order, so the result does not depend on scheduling.
 __global__ void __launch_bounds__(256) centroid_means_kernel(const float* __restrict__ X, int Dp,
                                                              const int32_t* __restrict__ members,
                                                              const int64_t* __restrict__ off, int64_t C,
                                                              float* __restrict__ cent)
 {
+    __shared__ float part[256];
     const int64_t c = blockIdx.x;
     if (c >= C) return;
     const int64_t lo = off[c], hi = off[c + 1];
     if (hi <= lo) return;
-    const float inv = 1.0f / static_cast<float>(hi - lo);
-    for (int d = threadIdx.x; d < Dp; d += blockDim.x) {
-        float s = 0.f;
-        for (int64_t i = lo; i < hi; ++i) s += X[static_cast<int64_t>(members[i]) * Dp + d];
-        cent[c * Dp + d] = s * inv;
+    const int parts = Dp <= 256 ? 256 / Dp : 1;
+    const int d = threadIdx.x % Dp, pidx = threadIdx.x / Dp;
+    float s = 0.f;
+    if (pidx < parts) {
+        int64_t i = lo + pidx;
+        for (; i + 3 * parts < hi; i += 4 * parts) {
+            const float a0 = X[static_cast<int64_t>(members[i]) * Dp + d];
+            const float a1 = X[static_cast<int64_t>(members[i + parts]) * Dp + d];
+            const float a2 = X[static_cast<int64_t>(members[i + 2 * parts]) * Dp + d];
+            const float a3 = X[static_cast<int64_t>(members[i + 3 * parts]) * Dp + d];
+            s += (a0 + a1) + (a2 + a3);
+        }
+        for (; i < hi; i += parts) s += X[static_cast<int64_t>(members[i]) * Dp + d];
+    }
+    part[threadIdx.x] = s;
+    __syncthreads();
+    if (threadIdx.x < Dp) {
+        float t = 0.f;
+        for (int p = 0; p < parts; ++p) t += part[p * Dp + threadIdx.x];
+        cent[c * Dp + threadIdx.x] = t / static_cast<float>(hi - lo);
     }
 }
 

@@ -279,8 +279,8 @@ class Context:
         self._check(lib().gt_translate(self._h, _ptr(g), _ptr(inv), N, K, _ptr(out)), "gt_translate")
         return out
 
-    def build_graph(self, X, *, n_buckets=0, nprobe=-1, M=64, K=32, rounds=3, refine_passes=0, refine_sample=16,
-                    kmeans_iters=0, balance=0.8, seed=42, metric="l2", return_knn=True):
+    def build_graph(self, X, *, n_buckets=0, nprobe=1, M=64, K=32, rounds=2, refine_passes=0, refine_sample=16,
+                    kmeans_iters=3, balance=0.8, seed=42, metric="l2", return_knn=True):
         if not _is_torch(X):
             X = np.ascontiguousarray(X)
         N, D = X.shape

@@ -102,16 +102,20 @@ int gt_optimize(gt_ctx* ctx, const uint32_t* knn, int64_t N, int32_t M, int32_t 
  * (src/translate_graph_ids.hpp:75). */
 int gt_translate(gt_ctx* ctx, const uint32_t* g, const uint32_t* inv, int64_t N, int32_t K, uint32_t* out);
 
+/* Defaults (gt_build_params_default): 2 rounds, 3 Lloyd iterations on a
+ * training subset, nprobe 1, balance 0.8, M 64, K 32, N/4000 buckets, seed 42.
+ * The reference's own settings are rounds 3, kmeans_iters 0 (data points as
+ * centroids), nprobe -1 (sk/scripts/params.sh:12, dataset_env.py:56). */
 typedef struct gt_build_params {
     int32_t metric;         /* GT_METRIC_L2 / GT_METRIC_IP */
-    int32_t n_buckets;      /* buckets per round (--centroid-ratio * N) */
-    int32_t nprobe;         /* probe buckets per bucket (--nprobe) */
+    int32_t n_buckets;      /* buckets per round (--centroid-ratio * N); 0 = N / 4000 */
+    int32_t nprobe;         /* probe buckets per bucket (--nprobe); -1 = ceil(20000 / avg bucket) */
     int32_t M;              /* intermediate degree (--neighbors-m) */
     int32_t K;              /* output degree (--fused-optimize-degree) */
     int32_t rounds;         /* rounds with fresh buckets (-t) */
     int32_t refine_passes;  /* 2-hop refinement passes (BUCKET2_A1_PASSES) */
     int32_t refine_sample;  /* S of the refinement (BUCKET2_A1_SAMPLE) */
-    int32_t kmeans_iters;   /* Lloyd iterations on the sampled centroids (0 = data points) */
+    int32_t kmeans_iters;   /* Lloyd iterations on a training subset (0 = sampled data points) */
     float balance;          /* two-choice factor: 2nd bucket if size2 < balance*size1 (<= 0 off) */
     uint64_t seed;          /* --seed; round r uses seed + r */
 } gt_build_params;
