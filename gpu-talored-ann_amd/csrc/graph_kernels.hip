@@ -153,11 +153,11 @@ __global__ void __launch_bounds__(256) cagra_prune_kernel(const int32_t* __restr
     }
     wave_sync_g();
 
-    // detour sources, one neighbour row per step, next row prefetched
-    int32_t bcur[2], bnext[2];
-    int kd = 0;
+    // detour sources: one neighbour row per step, kPruneDepth rows in flight
+    constexpr int kPruneDepth = 4;
+    int32_t ring[kPruneDepth][2];
     auto fetch = [&](int kAD, int32_t (&b)[2]) {
-        const int32_t d = sA[w][kAD];
+        const int32_t d = kAD < M - 1 ? sA[w][kAD] : -1;
         const bool ok = d >= 0 && d < N;
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
@@ -165,21 +165,26 @@ __global__ void __launch_bounds__(256) cagra_prune_kernel(const int32_t* __restr
             b[e] = (ok && k < M) ? G[static_cast<int64_t>(d) * M + k] : -1;
         }
     };
-    if (M > 1) fetch(0, bcur);
-    for (kd = 0; kd < M - 1; ++kd) {
-        if (kd + 1 < M - 1) fetch(kd + 1, bnext);
+    auto probe = [&](int kd, const int32_t (&b)[2]) {
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
-            const int32_t b = bcur[e];
-            if (b < 0) continue;
-            for (uint32_t h = (static_cast<uint32_t>(b) * 2654435761u) & mask; hkey[w][h] != -1; h = (h + 1) & mask) {
-                if (hkey[w][h] != b) continue;
+            const int32_t v = b[e];
+            if (v < 0) continue;
+            for (uint32_t h = (static_cast<uint32_t>(v) * 2654435761u) & mask; hkey[w][h] != -1; h = (h + 1) & mask) {
+                if (hkey[w][h] != v) continue;
                 const int kab = hrank[w][h];
                 if (kab > kd && atomicExch(&stamp[w][kab], kd) != kd) atomicAdd(&cnt[w][kab], 1u);
             }
         }
-        bcur[0] = bnext[0];
-        bcur[1] = bnext[1];
+    };
+#pragma unroll
+    for (int r = 0; r < kPruneDepth; ++r) fetch(r, ring[r]);
+    for (int kd = 0; kd < M - 1; kd += kPruneDepth) {
+#pragma unroll
+        for (int r = 0; r < kPruneDepth; ++r) {
+            if (kd + r < M - 1) probe(kd + r, ring[r]);
+            fetch(kd + r + kPruneDepth, ring[r]);
+        }
     }
     wave_sync_g();
 
@@ -214,18 +219,22 @@ __global__ void __launch_bounds__(256) cagra_prune_kernel(const int32_t* __restr
 // and merged into the dst's forward row with K/2 protected slots
 // (src/edge_chunk_accumulator.hpp:471-494).
 
+// In-degree of every node; each edge keeps the slot the count gave it inside
+// its destination's segment (any slot order works: segments are re-ordered
+// by the (rank, src) key before use).
 __global__ void rev_count_kernel(const uint32_t* __restrict__ fwd, int64_t E, int64_t N, uint32_t* __restrict__ deg,
-                                 int* __restrict__ err)
+                                 uint32_t* __restrict__ slot, int* __restrict__ err)
 {
     const int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (e >= E) return;
     const uint32_t j = fwd[e];
     if (j >= N) { atomicExch(err, 1); return; }
-    atomicAdd(&deg[j], 1u);
+    slot[e] = atomicAdd(&deg[j], 1u);
 }
 
 __global__ void rev_scatter_kernel(const uint32_t* __restrict__ fwd, int64_t E, int64_t N, int K,
-                                   uint32_t* __restrict__ cursor, unsigned long long* __restrict__ keys)
+                                   const uint32_t* __restrict__ off, const uint32_t* __restrict__ slot,
+                                   unsigned long long* __restrict__ keys)
 {
     const int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (e >= E) return;
@@ -233,8 +242,7 @@ __global__ void rev_scatter_kernel(const uint32_t* __restrict__ fwd, int64_t E, 
     if (j >= N) return;
     const int64_t i = e / K;
     const uint32_t k = static_cast<uint32_t>(e - i * K);
-    const uint32_t slot = atomicAdd(&cursor[j], 1u);
-    keys[slot] = (static_cast<unsigned long long>(k) << 32) | static_cast<uint32_t>(i);
+    keys[off[j] + slot[e]] = (static_cast<unsigned long long>(k) << 32) | static_cast<uint32_t>(i);
 }
 
 // Exclusive scan of n uint32 counts into out[0..n] (out[n] = total).
@@ -559,11 +567,11 @@ void launch_cagra_prune(const int32_t* G, int64_t N, int M, int K, uint32_t* out
     GT_HIP(hipGetLastError());
 }
 
-void launch_rev_count(const uint32_t* fwd, int64_t N, int K, uint32_t* deg, int* err, hipStream_t s)
+void launch_rev_count(const uint32_t* fwd, int64_t N, int K, uint32_t* deg, uint32_t* slot, int* err, hipStream_t s)
 {
     const int64_t E = N * K;
     if (E <= 0) return;
-    hipLaunchKernelGGL(rev_count_kernel, dim3(grid_for(E, 256)), dim3(256), 0, s, fwd, E, N, deg, err);
+    hipLaunchKernelGGL(rev_count_kernel, dim3(grid_for(E, 256)), dim3(256), 0, s, fwd, E, N, deg, slot, err);
     GT_HIP(hipGetLastError());
 }
 
@@ -576,11 +584,12 @@ void launch_exclusive_scan(const uint32_t* in, int64_t n, uint32_t* out, uint32_
     GT_HIP(hipGetLastError());
 }
 
-void launch_rev_scatter(const uint32_t* fwd, int64_t N, int K, uint32_t* cursor, unsigned long long* keys, hipStream_t s)
+void launch_rev_scatter(const uint32_t* fwd, int64_t N, int K, const uint32_t* off, const uint32_t* slot,
+                        unsigned long long* keys, hipStream_t s)
 {
     const int64_t E = N * K;
     if (E <= 0) return;
-    hipLaunchKernelGGL(rev_scatter_kernel, dim3(grid_for(E, 256)), dim3(256), 0, s, fwd, E, N, K, cursor, keys);
+    hipLaunchKernelGGL(rev_scatter_kernel, dim3(grid_for(E, 256)), dim3(256), 0, s, fwd, E, N, K, off, slot, keys);
     GT_HIP(hipGetLastError());
 }
 

@@ -28,10 +28,10 @@ void launch_negate(float* d, int64_t n, hipStream_t s);
 void launch_sanitize(const int32_t* in, int64_t N, int M, uint32_t* out, hipStream_t s);
 void launch_cagra_prune(const int32_t* G, int64_t N, int M, int K, uint32_t* out, unsigned long long* bad_row,
                         hipStream_t s);
-void launch_rev_count(const uint32_t* fwd, int64_t N, int K, uint32_t* deg, int* err, hipStream_t s);
+void launch_rev_count(const uint32_t* fwd, int64_t N, int K, uint32_t* deg, uint32_t* slot, int* err, hipStream_t s);
 void launch_exclusive_scan(const uint32_t* in, int64_t n, uint32_t* out, uint32_t* sums, hipStream_t s);
-void launch_rev_scatter(const uint32_t* fwd, int64_t N, int K, uint32_t* cursor, unsigned long long* keys,
-                        hipStream_t s);
+void launch_rev_scatter(const uint32_t* fwd, int64_t N, int K, const uint32_t* off, const uint32_t* slot,
+                        unsigned long long* keys, hipStream_t s);
 void launch_rev_merge(const uint32_t* fwd, int64_t N, int K, const uint32_t* off, const unsigned long long* keys,
                       uint32_t* out, hipStream_t s);
 void launch_merge_rounds(const int32_t* ri, const float* rd, const int32_t* ni, const float* nd, int64_t N, int M,
@@ -601,16 +601,15 @@ static void reverse_merge_device(Ctx& c, const uint32_t* fwd, int64_t N, int K, 
     GT_REQUIRE(N * K < (int64_t(1) << 32), "too many edges for 32-bit offsets");
     uint32_t* deg = c.ws<uint32_t>(W_DEG, static_cast<size_t>(N));
     uint32_t* off = c.ws<uint32_t>(W_OFF, static_cast<size_t>(N + 1));
-    uint32_t* cur = c.ws<uint32_t>(W_CUR, static_cast<size_t>(N + 1));
+    uint32_t* slot = c.ws<uint32_t>(W_CUR, static_cast<size_t>(N * K));
     uint32_t* sums = c.ws<uint32_t>(W_SUMS, static_cast<size_t>(ceil_div(N, 1024) + 1));
     unsigned long long* keys = c.ws<unsigned long long>(W_KEYS, static_cast<size_t>(N * K));
     int* err = c.ws<int>(W_TMP, 1);
     GT_HIP(hipMemsetAsync(deg, 0, static_cast<size_t>(N) * sizeof(uint32_t), c.s));
     GT_HIP(hipMemsetAsync(err, 0, sizeof(int), c.s));
-    launch_rev_count(fwd, N, K, deg, err, c.s);
+    launch_rev_count(fwd, N, K, deg, slot, err, c.s);
     launch_exclusive_scan(deg, N, off, sums, c.s);
-    c.d2d(cur, off, static_cast<size_t>(N) * sizeof(uint32_t));
-    launch_rev_scatter(fwd, N, K, cur, keys, c.s);
+    launch_rev_scatter(fwd, N, K, off, slot, keys, c.s);
     launch_rev_merge(fwd, N, K, off, keys, out, c.s);
     int h = 0;
     c.d2h(&h, err, sizeof(int));

@@ -39,6 +39,33 @@ __device__ __forceinline__ void wave_sync()
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// Order-preserving packing of (key, id): unsigned comparison of the 64-bit
+// words is the (key, id) order.  ~0 is the sentinel (after every real entry).
+constexpr uint64_t kNoKey = ~0ull;
+__device__ __forceinline__ uint32_t f2o(float f)
+{
+    const uint32_t u = __float_as_uint(f);
+    return u ^ (static_cast<uint32_t>(static_cast<int32_t>(u) >> 31) | 0x80000000u);
+}
+__device__ __forceinline__ float o2f(uint32_t k)
+{
+    return __uint_as_float(k ^ ((k & 0x80000000u) ? 0x80000000u : 0xFFFFFFFFu));
+}
+__device__ __forceinline__ uint64_t pack_key(float d, int32_t id)
+{
+    return (static_cast<uint64_t>(f2o(d)) << 32) | static_cast<uint32_t>(id);
+}
+__device__ __forceinline__ int lower_bound_u64(const uint64_t* a, int n, uint64_t k)
+{
+    int lo = 0, hi = n;
+    while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (a[mid] < k) lo = mid + 1;
+        else hi = mid;
+    }
+    return lo;
+}
+
 // number of entries of the sorted (d, i) array [0, n) that are < (kd, ki)
 __device__ __forceinline__ int lower_bound_lds(const float* ad, const int32_t* ai, int n, float kd, int32_t ki)
 {
@@ -75,9 +102,8 @@ struct KnnSmem {
     float tile[2][kPoolTile][DP + 4];   // +4 floats: rows land on distinct bank groups
     float tnorm[3][kPoolTile];          // |p|^2 (L2) or 0 (IP); +inf past the slice end
     int32_t trow[3][kPoolTile];         // pool row id, -1 past the slice end
-    float2 buf[kQueriesPerBlock][kCB];  // (key, id as bits) candidates awaiting a merge
-    float sLd[kWaves][kMaxM];
-    int32_t sLi[kWaves][kMaxM];
+    uint64_t buf[kQueriesPerBlock][kCB];  // packed (key, id) of candidates awaiting a merge
+    uint64_t sL[kWaves][kMaxM];           // the merging query's list, packed
     float sthr[kWaves];
 };
 
@@ -122,46 +148,40 @@ __device__ void wave_merge(KnnSmem<DP>& sm, const KnnArgs& a, int w, int lane, i
     const int64_t orow = __shfl(st.orow, q);
     const int M = a.M;
     const int ql = w * kQueriesPerWave + q;
-    float2* B = sm.buf[ql];
+    uint64_t* B = sm.buf[ql];
 
-    float ld[2];
-    int32_t li[2];
+    uint64_t lk[2];
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
         const int idx = lane + 64 * e;
-        ld[e] = INFINITY;
-        li[e] = INT_MAX;
-        if (idx < nL) {
-            ld[e] = load_list_d(a.out_d + orow * M + idx);
-            li[e] = load_list_i(a.out_ids + orow * M + idx);
-        }
-        if (idx < kMaxM) { sm.sLd[w][idx] = ld[e]; sm.sLi[w][idx] = li[e]; }
+        lk[e] = kNoKey;
+        if (idx < nL)
+            lk[e] = pack_key(load_list_d(a.out_d + orow * M + idx), load_list_i(a.out_ids + orow * M + idx));
+        if (idx < kMaxM) sm.sL[w][idx] = lk[e];
     }
     // the query's own id never enters the list
-    if (lane < nB && __float_as_int(B[lane].y) == self) B[lane] = make_float2(INFINITY, __int_as_float(INT_MAX));
+    if (lane < nB && static_cast<int32_t>(static_cast<uint32_t>(B[lane])) == self) B[lane] = kNoKey;
     wave_sync();
 
-    float bd = INFINITY;
-    int32_t bi = INT_MAX;
-    if (lane < nB) { const float2 v = B[lane]; bd = v.x; bi = __float_as_int(v.y); }
+    const uint64_t bk = lane < nB ? B[lane] : kNoKey;
     int rb = 0;              // rank of this lane's buffer entry among the buffer
     int cl0 = 0, cl1 = 0;    // buffer entries before list entries lane, lane+64
     for (int k = 0; k < nB; ++k) {
-        const float2 v = B[k];
-        const int32_t vi = __float_as_int(v.y);
-        rb += key_less(v.x, vi, bd, bi);
-        cl0 += key_less(v.x, vi, ld[0], li[0]);
-        cl1 += key_less(v.x, vi, ld[1], li[1]);
+        const uint64_t v = B[k];
+        rb += v < bk;
+        cl0 += v < lk[0];
+        cl1 += v < lk[1];
     }
-    const bool bvalid = lane < nB && bi != INT_MAX;
+    const bool bvalid = bk != kNoKey;
     const int nBv = static_cast<int>(__popcll(__ballot(bvalid)));
     const int total = nL + nBv;
     if (bvalid) {
-        const int pos = rb + lower_bound_lds(sm.sLd[w], sm.sLi[w], nL, bd, bi);
+        const int pos = rb + lower_bound_u64(sm.sL[w], nL, bk);
         if (pos < M) {
-            a.out_d[orow * M + pos] = bd;
-            a.out_ids[orow * M + pos] = bi;
-            if (pos == M - 1) sm.sthr[w] = bd;
+            const float d = o2f(static_cast<uint32_t>(bk >> 32));
+            a.out_d[orow * M + pos] = d;
+            a.out_ids[orow * M + pos] = static_cast<int32_t>(static_cast<uint32_t>(bk));
+            if (pos == M - 1) sm.sthr[w] = d;
         }
     }
 #pragma unroll
@@ -170,9 +190,10 @@ __device__ void wave_merge(KnnSmem<DP>& sm, const KnnArgs& a, int w, int lane, i
         if (idx < nL) {
             const int pos = idx + (e == 0 ? cl0 : cl1);
             if (pos < M) {
-                a.out_d[orow * M + pos] = ld[e];
-                a.out_ids[orow * M + pos] = li[e];
-                if (pos == M - 1) sm.sthr[w] = ld[e];
+                const float d = o2f(static_cast<uint32_t>(lk[e] >> 32));
+                a.out_d[orow * M + pos] = d;
+                a.out_ids[orow * M + pos] = static_cast<int32_t>(static_cast<uint32_t>(lk[e]));
+                if (pos == M - 1) sm.sthr[w] = d;
             }
         }
     }
@@ -226,7 +247,7 @@ __device__ void tile_append(KnnSmem<DP>& sm, const KnnArgs& a, const floatx16& a
             if ((pass >> r) & 1u) {
                 const int i = 8 * (r >> 2) + 4 * h + (r & 3);
                 const int32_t id = a.out_pos ? tp * kPoolTile + i : sm.trow[b3][i];
-                sm.buf[qlocal][off] = make_float2(dv[r], __int_as_float(id));
+                sm.buf[qlocal][off] = pack_key(dv[r], id);
                 ++off;
             }
         }
