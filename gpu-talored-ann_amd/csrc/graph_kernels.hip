@@ -12,13 +12,6 @@
 
 namespace gtann {
 
-__device__ __forceinline__ void wave_sync_g()
-{
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
 __device__ __forceinline__ bool key_less_g(float da, int32_t ia, float db, int32_t ib)
 {
     return da < db || (da == db && ia < ib);
@@ -138,7 +131,7 @@ __global__ void __launch_bounds__(256) cagra_prune_kernel(const int32_t* __restr
         A[e] = k < M ? G[a * M + k] : -1;
         if (k < M) { stamp[w][k] = -1; cnt[w][k] = 0; sA[w][k] = A[e]; }
     }
-    wave_sync_g();
+    wave_sync();
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
         const int k = lane + 64 * e;
@@ -151,7 +144,7 @@ __global__ void __launch_bounds__(256) cagra_prune_kernel(const int32_t* __restr
             }
         }
     }
-    wave_sync_g();
+    wave_sync();
 
     // detour sources: one neighbour row per step, kPruneDepth rows in flight
     constexpr int kPruneDepth = 4;
@@ -186,7 +179,7 @@ __global__ void __launch_bounds__(256) cagra_prune_kernel(const int32_t* __restr
             fetch(kd + r + kPruneDepth, ring[r]);
         }
     }
-    wave_sync_g();
+    wave_sync();
 
     int nvalid = 0;
 #pragma unroll
@@ -370,7 +363,7 @@ __global__ void __launch_bounds__(256) rev_merge_kernel(const uint32_t* __restri
         const bool prot = protected_src(src);
         bool keep = valid && !prot;
         sSrc[w][lane] = src;
-        wave_sync_g();
+        wave_sync();
         bool dup = false;
         for (int l2 = 0; l2 < 64; ++l2) dup |= (l2 < lane) && sSrc[w][l2] == src && (l2 < static_cast<int>(n));
         keep = keep && !dup;
@@ -396,12 +389,12 @@ __global__ void __launch_bounds__(256) rev_merge_kernel(const uint32_t* __restri
             for (int q = 0; q < nR; ++q) skip |= (sR[w][q] == src);
             if (!skip) {
                 if (lane == 0) sR[w][nR] = src;
-                wave_sync_g();
+                wave_sync();
                 ++nR;
             }
         }
     }
-    wave_sync_g();
+    wave_sync();
 
     if (lane < P) out[j * K + lane] = rowv;
     if (lane < nR) out[j * K + P + lane] = sR[w][lane];
@@ -451,7 +444,7 @@ __global__ void __launch_bounds__(256) merge_rounds_kernel(const int32_t* __rest
         if (k < kMergeMaxM) { sRd[w][k] = rdv[e]; sRi[w][k] = riv[e]; }
         nr += __popcll(__ballot(riv[e] != INT_MAX));
     }
-    wave_sync_g();
+    wave_sync();
     // drop new ids already in run; compact the survivors (order preserved)
     bool keep[2];
 #pragma unroll
@@ -469,7 +462,7 @@ __global__ void __launch_bounds__(256) merge_rounds_kernel(const int32_t* __rest
 #pragma unroll
     for (int e = 0; e < 2; ++e)
         if (keep[e]) { sNd[w][cidx[e]] = ndv[e]; sNi[w][cidx[e]] = niv[e]; }
-    wave_sync_g();
+    wave_sync();
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
         const int k = lane + 64 * e;

@@ -34,6 +34,15 @@ void launch_rev_scatter(const uint32_t* fwd, int64_t N, int K, const uint32_t* o
                         unsigned long long* keys, hipStream_t s);
 void launch_rev_merge(const uint32_t* fwd, int64_t N, int K, const uint32_t* off, const unsigned long long* keys,
                       uint32_t* out, hipStream_t s);
+void launch_occlusion_prune(const float* X, int64_t N, int Dp, const int32_t* nb, int M, int max_deg, int32_t* out,
+                            hipStream_t s);
+void launch_rin_worst(const float* d, int64_t N, int M, float* worst, hipStream_t s);
+void launch_rin_count(const int32_t* ids, const float* d, int64_t N, int M, const float* worst, uint32_t* cnt,
+                      uint32_t* slot, int* err, hipStream_t s);
+void launch_rin_scatter(const int32_t* ids, const float* d, int64_t N, int M, const uint32_t* off,
+                        const uint32_t* slot, unsigned long long* keys, hipStream_t s);
+void launch_rin_merge(int32_t* ids, float* d, int64_t N, int M, const uint32_t* off, const unsigned long long* keys,
+                      hipStream_t s);
 void launch_merge_rounds(const int32_t* ri, const float* rd, const int32_t* ni, const float* nd, int64_t N, int M,
                          int32_t* oi, float* od, hipStream_t s);
 void launch_translate(const uint32_t* g, const uint32_t* inv, int64_t N, int K, uint32_t* out, uint32_t* hits,
@@ -99,7 +108,7 @@ namespace gtann {
 enum Ws {
     W_X, W_XRAW, W_NORMS, W_C, W_CRAW, W_CNORMS, W_IDS, W_D, W_IDS2, W_D2, W_IDS3, W_D3, W_ITEMS, W_QROWS, W_PROWS,
     W_MEMBERS, W_TASKS, W_POOL, W_PART_I, W_PART_D, W_G1, W_G2, W_G3, W_DEG, W_OFF, W_CUR, W_KEYS, W_SUMS, W_FLAG,
-    W_TMP, W_OUT, W_IN, W_PROBE_I, W_PROBE_D, W_COUNT_
+    W_TMP, W_OUT, W_IN, W_PROBE_I, W_PROBE_D, W_WORST, W_COUNT_
 };
 static_assert(W_COUNT_ <= 40, "workspace slots");
 
@@ -205,7 +214,7 @@ static DevMatrix prepare(Ctx& c, int slot_x, int slot_raw, int slot_norms, const
     m.N = N;
     m.Dp = Dp;
     const bool dev = is_device_ptr(X);
-    if (dev && dtype == GT_DTYPE_F32 && D == Dp) {
+    if (dev && dtype == GT_DTYPE_F32 && D == Dp && (reinterpret_cast<uintptr_t>(X) & 15) == 0) {
         m.data = static_cast<const float*>(X);
     } else {
         const void* src = X;
@@ -617,6 +626,32 @@ static void reverse_merge_device(Ctx& c, const uint32_t* fwd, int64_t N, int K, 
     if (h) throw Error(GT_EINVAL, "reverse merge: forward graph holds an id >= N");
 }
 
+// bd/build_bucket.py:473-543 on a device table (N x M, ascending rows), in place
+static void reverse_insert_device(Ctx& c, int32_t* ids, float* d, int64_t N, int M)
+{
+    GT_REQUIRE(M >= 1 && M <= 128, "list length must be in [1, 128]");
+    GT_REQUIRE(N * M < (int64_t(1) << 32), "too many edges for 32-bit offsets");
+    const int64_t E = N * M;
+    float* worst = c.ws<float>(W_WORST, static_cast<size_t>(N));
+    uint32_t* cnt = c.ws<uint32_t>(W_DEG, static_cast<size_t>(N));
+    uint32_t* off = c.ws<uint32_t>(W_OFF, static_cast<size_t>(N + 1));
+    uint32_t* slot = c.ws<uint32_t>(W_CUR, static_cast<size_t>(E));
+    uint32_t* sums = c.ws<uint32_t>(W_SUMS, static_cast<size_t>(ceil_div(N, 1024) + 1));
+    unsigned long long* keys = c.ws<unsigned long long>(W_KEYS, static_cast<size_t>(E));
+    int* err = c.ws<int>(W_TMP, 1);
+    GT_HIP(hipMemsetAsync(cnt, 0, static_cast<size_t>(N) * sizeof(uint32_t), c.s));
+    GT_HIP(hipMemsetAsync(err, 0, sizeof(int), c.s));
+    launch_rin_worst(d, N, M, worst, c.s);
+    launch_rin_count(ids, d, N, M, worst, cnt, slot, err, c.s);
+    launch_exclusive_scan(cnt, N, off, sums, c.s);
+    launch_rin_scatter(ids, d, N, M, off, slot, keys, c.s);
+    launch_rin_merge(ids, d, N, M, off, keys, c.s);
+    int h = 0;
+    c.d2h(&h, err, sizeof(int));
+    c.sync();
+    if (h) throw Error(GT_EINVAL, "reverse-edge insertion: table holds an id >= N");
+}
+
 }  // namespace gtann
 
 using namespace gtann;
@@ -697,6 +732,8 @@ void gt_build_params_default(gt_build_params* p)
     p->kmeans_iters = 3;
     p->balance = 0.8f;
     p->seed = 42;
+    p->reverse_edges = 0;
+    p->reserved_ = 0;
 }
 
 int gt_knn_exact(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtype, int metric, const int64_t* queries,
@@ -934,6 +971,38 @@ int gt_reverse_merge(gt_ctx* ctx, const uint32_t* fwd, int64_t N, int32_t K, uin
     });
 }
 
+int gt_prune_occlusion(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtype, const int32_t* nb, int32_t M,
+                       int32_t max_degree, int32_t* out)
+{
+    return guarded(ctx, [&] {
+        GT_REQUIRE(nb && out && M >= 1 && M <= 128, "bad arguments (1 <= M <= 128)");
+        Ctx c(ctx);
+        DevMatrix Xm = prepare(c, W_X, W_XRAW, W_NORMS, X, N, D, dtype);
+        const size_t nm = static_cast<size_t>(N) * M;
+        const int32_t* in = c.in<int32_t>(W_IN, nb, nm);
+        int32_t* o = c.ws<int32_t>(W_OUT, nm);
+        launch_occlusion_prune(Xm.data, N, Xm.Dp, in, M, max_degree, o, c.s);
+        c.out(out, o, nm);
+        c.sync();
+    });
+}
+
+int gt_reverse_insert(gt_ctx* ctx, int32_t* ids, float* dists, int64_t N, int32_t M)
+{
+    return guarded(ctx, [&] {
+        GT_REQUIRE(ids && dists && N >= 1 && M >= 1, "bad arguments");
+        GT_REQUIRE(N < (int64_t(1) << 31), "N must be < 2^31");
+        Ctx c(ctx);
+        const size_t nm = static_cast<size_t>(N) * M;
+        int32_t* di = c.in<int32_t>(W_IDS, ids, nm);
+        float* dd = c.in<float>(W_D, dists, nm);
+        reverse_insert_device(c, di, dd, N, M);
+        c.out(ids, di, nm);
+        c.out(dists, dd, nm);
+        c.sync();
+    });
+}
+
 int gt_optimize(gt_ctx* ctx, const uint32_t* knn, int64_t N, int32_t M, int32_t K, uint32_t* out)
 {
     return guarded(ctx, [&] {
@@ -977,10 +1046,11 @@ int gt_build_graph(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtype, 
                    int32_t* knn_ids, float* knn_dists, uint32_t* graph, gt_build_stats* stats)
 {
     return guarded(ctx, [&] {
-        GT_REQUIRE(params && graph, "bad arguments");
+        GT_REQUIRE(params && (graph || knn_ids || knn_dists), "bad arguments");
         gt_build_params p = *params;
         GT_REQUIRE(p.metric == GT_METRIC_L2 || p.metric == GT_METRIC_IP, "unknown metric");
-        GT_REQUIRE(p.M >= 1 && p.M <= 128 && p.K >= 1 && p.K <= std::min(p.M, 64) && p.rounds >= 1, "bad degrees");
+        GT_REQUIRE(p.M >= 1 && p.M <= 128 && p.rounds >= 1, "bad degrees");
+        GT_REQUIRE(!graph || (p.K >= 1 && p.K <= std::min(p.M, 64)), "bad output degree");
         GT_REQUIRE(N > p.M, "need N > M");
         Timer total;
         gt_build_stats st{};
@@ -1007,7 +1077,19 @@ int gt_build_graph(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtype, 
             Buckets b;
             make_buckets(c, Xm, C, nprobe, p.metric, p.balance, p.kmeans_iters, p.seed + static_cast<uint64_t>(r), b);
             st.t_bucketing += tb.sec();
-            if (r == 0) {
+            if (p.reverse_edges) {
+                // the Python pipeline's round: full table, reverse edges, then the merge
+                int32_t* oi = r == 0 ? run_i : cur_i;
+                float* od = r == 0 ? run_d : cur_d;
+                st.t_knn += bucketed_round(c, Xm, b, p.M, p.metric, nullptr, oi, od, &st.max_pool, &st.max_bucket,
+                                           &st.knn_pairs);
+                st.t_merge += c.timed([&] { reverse_insert_device(c, oi, od, N, p.M); });
+                if (r > 0) {
+                    st.t_merge += c.timed([&] { launch_merge_rounds(run_i, run_d, cur_i, cur_d, N, p.M, tmp_i, tmp_d, c.s); });
+                    std::swap(run_i, tmp_i);
+                    std::swap(run_d, tmp_d);
+                }
+            } else if (r == 0) {
                 st.t_knn += bucketed_round(c, Xm, b, p.M, p.metric, nullptr, run_i, run_d, &st.max_pool,
                                            &st.max_bucket, &st.knn_pairs);
             } else {
@@ -1032,19 +1114,22 @@ int gt_build_graph(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtype, 
         }
         st.knn_flops = 2.0 * D * st.knn_pairs;
         // sanitize + prune + reverse merge
-        uint32_t* san = c.ws<uint32_t>(W_OUT, nm);
-        uint32_t* fwd = c.ws<uint32_t>(W_G3, static_cast<size_t>(N) * p.K);
-        uint32_t* fin = c.ws<uint32_t>(W_IN, static_cast<size_t>(N) * p.K);
-        st.t_prune = c.timed([&] { launch_sanitize(run_i, N, p.M, san, c.s); });
-        st.t_prune += c.timed([&] { prune_device(c, reinterpret_cast<const int32_t*>(san), N, p.M, p.K, fwd); });
-        st.t_revmerge = c.timed([&] { reverse_merge_device(c, fwd, N, p.K, fin); });
+        uint32_t* fin = nullptr;
+        if (graph) {
+            uint32_t* san = c.ws<uint32_t>(W_OUT, nm);
+            uint32_t* fwd = c.ws<uint32_t>(W_G3, static_cast<size_t>(N) * p.K);
+            fin = c.ws<uint32_t>(W_IN, static_cast<size_t>(N) * p.K);
+            st.t_prune = c.timed([&] { launch_sanitize(run_i, N, p.M, san, c.s); });
+            st.t_prune += c.timed([&] { prune_device(c, reinterpret_cast<const int32_t*>(san), N, p.M, p.K, fwd); });
+            st.t_revmerge = c.timed([&] { reverse_merge_device(c, fwd, N, p.K, fin); });
+        }
         Timer td;
         if (knn_ids) c.out(knn_ids, run_i, nm);
         if (knn_dists) {
             if (p.metric == GT_METRIC_IP) launch_negate(run_d, static_cast<int64_t>(nm), c.s);
             c.out(knn_dists, run_d, nm);
         }
-        c.out(graph, fin, static_cast<size_t>(N) * p.K);
+        if (graph) c.out(graph, fin, static_cast<size_t>(N) * p.K);
         c.sync();
         st.t_download = td.sec();
         st.t_total = total.sec();

@@ -31,30 +31,6 @@ __device__ __forceinline__ bool key_less(float da, int32_t ia, float db, int32_t
     return da < db || (da == db && ia < ib);
 }
 
-// Orders LDS traffic of one wave across lanes (no s_barrier needed inside a wave).
-__device__ __forceinline__ void wave_sync()
-{
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-// Order-preserving packing of (key, id): unsigned comparison of the 64-bit
-// words is the (key, id) order.  ~0 is the sentinel (after every real entry).
-constexpr uint64_t kNoKey = ~0ull;
-__device__ __forceinline__ uint32_t f2o(float f)
-{
-    const uint32_t u = __float_as_uint(f);
-    return u ^ (static_cast<uint32_t>(static_cast<int32_t>(u) >> 31) | 0x80000000u);
-}
-__device__ __forceinline__ float o2f(uint32_t k)
-{
-    return __uint_as_float(k ^ ((k & 0x80000000u) ? 0x80000000u : 0xFFFFFFFFu));
-}
-__device__ __forceinline__ uint64_t pack_key(float d, int32_t id)
-{
-    return (static_cast<uint64_t>(f2o(d)) << 32) | static_cast<uint32_t>(id);
-}
 __device__ __forceinline__ int lower_bound_u64(const uint64_t* a, int n, uint64_t k)
 {
     int lo = 0, hi = n;

@@ -25,6 +25,7 @@ EXPORTS = (
     "gt_create", "gt_destroy", "gt_last_error", "gt_version", "gt_knn_exact", "gt_assign_top2",
     "gt_knn_bucketed", "gt_merge_rounds", "gt_refine_2hop", "gt_sanitize", "gt_cagra_prune",
     "gt_reverse_merge", "gt_optimize", "gt_translate", "gt_build_params_default", "gt_build_graph",
+    "gt_prune_occlusion", "gt_reverse_insert",
 )
 
 
@@ -39,6 +40,7 @@ class BuildParams(C.Structure):
         ("metric", C.c_int32), ("n_buckets", C.c_int32), ("nprobe", C.c_int32), ("M", C.c_int32),
         ("K", C.c_int32), ("rounds", C.c_int32), ("refine_passes", C.c_int32), ("refine_sample", C.c_int32),
         ("kmeans_iters", C.c_int32), ("balance", C.c_float), ("seed", C.c_uint64),
+        ("reverse_edges", C.c_int32), ("reserved_", C.c_int32),
     ]
 
 
@@ -81,6 +83,8 @@ def lib():
         L.gt_reverse_merge.argtypes = [vp, vp, i64, i32, vp]
         L.gt_optimize.argtypes = [vp, vp, i64, i32, i32, vp]
         L.gt_translate.argtypes = [vp, vp, vp, i64, i32, vp]
+        L.gt_prune_occlusion.argtypes = [vp, vp, i64, i32, C.c_int, vp, i32, i32, vp]
+        L.gt_reverse_insert.argtypes = [vp, vp, vp, i64, i32]
         L.gt_build_params_default.argtypes = [C.POINTER(BuildParams)]
         L.gt_build_params_default.restype = None
         L.gt_build_graph.argtypes = [vp, vp, i64, i32, C.c_int, C.POINTER(BuildParams), vp, vp, vp,
@@ -271,6 +275,28 @@ class Context:
         self._check(lib().gt_optimize(self._h, _ptr(knn), N, M, K, _ptr(out)), "gt_optimize")
         return out
 
+    def prune_occlusion(self, X, nb, max_degree=0):
+        """Occlusion prune (bd/prune.py:8-83); returns int32 (N, M), -1 padded."""
+        if not _is_torch(X):
+            X = np.ascontiguousarray(X)
+        N, D = X.shape
+        nb = _np(nb, np.int32)
+        if nb.ndim != 2 or nb.shape[0] != N:
+            raise ValueError(f"neighbors must be ({N}, M), got {nb.shape}")
+        M = nb.shape[1]
+        out = np.empty((N, M), np.int32)
+        self._check(lib().gt_prune_occlusion(self._h, _ptr(X), N, D, _dtype_code(X), _ptr(nb), M,
+                                             int(max_degree or 0), _ptr(out)), "gt_prune_occlusion")
+        return out
+
+    def reverse_insert(self, ids, d):
+        """Reverse-edge insertion (bd/build_bucket.py:473-543); returns new (ids, d)."""
+        ids = _np(ids, np.int32).copy()
+        d = _np(d, np.float32).copy()
+        N, M = ids.shape
+        self._check(lib().gt_reverse_insert(self._h, _ptr(ids), _ptr(d), N, M), "gt_reverse_insert")
+        return ids, d
+
     def translate(self, g, inv):
         g = _np(g, np.uint32)
         inv = _np(inv, np.uint32)
@@ -280,7 +306,8 @@ class Context:
         return out
 
     def build_graph(self, X, *, n_buckets=0, nprobe=1, M=64, K=32, rounds=2, refine_passes=0, refine_sample=16,
-                    kmeans_iters=3, balance=0.8, seed=42, metric="l2", return_knn=True):
+                    kmeans_iters=3, balance=0.8, seed=42, metric="l2", return_knn=True, reverse_edges=False,
+                    prune=True):
         if not _is_torch(X):
             X = np.ascontiguousarray(X)
         N, D = X.shape
@@ -288,13 +315,13 @@ class Context:
         lib().gt_build_params_default(C.byref(p))
         p.metric, p.n_buckets, p.nprobe, p.M, p.K = METRICS[metric], n_buckets, nprobe, M, K
         p.rounds, p.refine_passes, p.refine_sample, p.kmeans_iters = rounds, refine_passes, refine_sample, kmeans_iters
-        p.balance, p.seed = balance, seed
-        graph = _empty_like_input(X, (N, K), np.uint32)
+        p.balance, p.seed, p.reverse_edges = balance, seed, int(bool(reverse_edges))
+        graph = _empty_like_input(X, (N, K), np.uint32) if prune else None
         ids = _empty_like_input(X, (N, M), np.int32) if return_knn else None
         d = _empty_like_input(X, (N, M), np.float32) if return_knn else None
         st = BuildStats()
         self._check(lib().gt_build_graph(self._h, _ptr(X), N, D, _dtype_code(X), C.byref(p), _ptr(ids), _ptr(d),
                                          _ptr(graph), C.byref(st)), "gt_build_graph")
-        if not _is_torch(graph):
+        if graph is not None and not _is_torch(graph):
             graph = graph.view(np.uint32)
         return BuildResult(graph=graph, knn_ids=ids, knn_dists=d, stats=st.as_dict())

@@ -93,6 +93,23 @@ int gt_cagra_prune(gt_ctx* ctx, const uint32_t* knn, int64_t N, int32_t M, int32
  * (src/optimize_chunked.cu:372-407, :1421-1471). */
 int gt_reverse_merge(gt_ctx* ctx, const uint32_t* fwd, int64_t N, int32_t K, uint32_t* out);
 
+/* Occlusion prune of bd/prune.py:8-83 (prune_graph), L2: per point the valid
+ * candidates of nb (N x M; -1, out-of-range and self dropped) in order of
+ * distance to the point (ties by column); a candidate is dropped when an
+ * earlier kept one is strictly closer to it than the point is.  out (N x M)
+ * holds the kept ids left-aligned, at most max_degree of them (<= 0: no
+ * cap), then -1.  M <= 128.  Replaces prune.prune_graph (bd/prune.py:8-19). */
+int gt_prune_occlusion(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtype, const int32_t* nb, int32_t M,
+                       int32_t max_degree, int32_t* out);
+
+/* Reverse-edge insertion of bd/build_bucket.py:473-543 on an N x M table
+ * (rows ascending), in place: every edge a -> b with distance d strictly below
+ * the largest distance of b's row is offered to b; sources already in b's
+ * row are dropped; a row that receives an offer becomes the M smallest of
+ * (row, offers) by (distance, id).  M <= 128.
+ * Replaces _apply_reverse_edges (bd/build_bucket.py:473). */
+int gt_reverse_insert(gt_ctx* ctx, int32_t* ids, float* dists, int64_t N, int32_t M);
+
 /* prune then reverse merge.  Replaces cuvs::neighbors::cagra::helpers::optimize
  * (src/optimize.cu:395-397, src/bucket.cu:8470). */
 int gt_optimize(gt_ctx* ctx, const uint32_t* knn, int64_t N, int32_t M, int32_t K, uint32_t* out);
@@ -118,6 +135,9 @@ typedef struct gt_build_params {
     int32_t kmeans_iters;   /* Lloyd iterations on a training subset (0 = sampled data points) */
     float balance;          /* two-choice factor: 2nd bucket if size2 < balance*size1 (<= 0 off) */
     uint64_t seed;          /* --seed; round r uses seed + r */
+    int32_t reverse_edges;  /* 1: each round's full table gets gt_reverse_insert before the
+                               cross-round merge (bd/build_bucket.py:628); 0: rounds seeded */
+    int32_t reserved_;
 } gt_build_params;
 
 typedef struct gt_build_stats {
@@ -142,7 +162,7 @@ void gt_build_params_default(gt_build_params* p);
  * top-2 assignment with two-choice balance -> pooled kNN -> merge), optional
  * refinement, sanitize, CAGRA prune, reverse merge.  knn_ids/knn_dists
  * (N x M, optional, NULL to skip) receive the pre-prune table, graph
- * (N x K) the final graph.  Replaces bucket2's GPU-resident path
+ * (N x K, NULL = stop after the table) the final graph.  Replaces bucket2's GPU-resident path
  * (src/bucket.cu:8729-9842 with --fused-optimize-degree). */
 int gt_build_graph(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtype,
                    const gt_build_params* params, int32_t* knn_ids, float* knn_dists,

@@ -566,6 +566,89 @@ int or_prune_occlusion(const float* X, int64_t N, int64_t D, const int64_t* nb, 
     return OR_OK;
 }
 
+/*
+ * Reverse-edge insertion of bd/build_bucket.py:473-543 (_apply_reverse_edges),
+ * in place on an N x M table whose rows are ascending.  All offers are taken
+ * from the table as it was on entry (:485-492).  Edge a -> b (distance d, from
+ * a's row) is offered to b when d < max(b's row) (the per-target skip at
+ * :517-519 keeps exactly these); offers whose source is already in b's row are
+ * dropped (:522-524); repeated offers are kept (:527-529).  A row with a
+ * surviving offer becomes the first M of (row, offers) in (distance, id)
+ * order, ids compared as unsigned so -1 padding sorts last among equal
+ * distances (torch.topk's order among ties, :533, is not specified; this
+ * order is ours).  Returns OR_EINVAL if an id is >= N.
+ */
+typedef struct { float d; uint32_t id; } rin_t;
+
+static int rin_cmp(const void* x, const void* y)
+{
+    const rin_t* a = (const rin_t*)x;
+    const rin_t* b = (const rin_t*)y;
+    if (a->d < b->d) return -1;
+    if (a->d > b->d) return 1;
+    return a->id < b->id ? -1 : (a->id > b->id);
+}
+
+int or_reverse_insert(int32_t* ids, float* d, int64_t N, int M)
+{
+    if (!ids || !d || N <= 0 || M <= 0) return OR_EINVAL;
+    const int64_t E = N * M;
+    for (int64_t e = 0; e < E; ++e)
+        if (ids[e] >= N) return OR_EINVAL;
+    float* worst = (float*)malloc(sizeof(float) * (size_t)N);
+    int64_t* off = (int64_t*)calloc((size_t)N + 1, sizeof(int64_t));
+    for (int64_t b = 0; b < N; ++b) {
+        float w = -INFINITY;
+        for (int k = 0; k < M; ++k) w = fmaxf(w, d[b * M + k]);
+        worst[b] = w;
+    }
+    for (int64_t e = 0; e < E; ++e)
+        if (ids[e] >= 0 && d[e] < worst[ids[e]]) off[ids[e] + 1]++;
+    for (int64_t b = 0; b < N; ++b) off[b + 1] += off[b];
+    rin_t* offers = (rin_t*)malloc(sizeof(rin_t) * (size_t)(off[N] + 1));
+    int64_t* fill = (int64_t*)malloc(sizeof(int64_t) * (size_t)N);
+    memcpy(fill, off, sizeof(int64_t) * (size_t)N);
+    for (int64_t e = 0; e < E; ++e) {
+        const int32_t b = ids[e];
+        if (b >= 0 && d[e] < worst[b]) {
+            offers[fill[b]].d = d[e];
+            offers[fill[b]].id = (uint32_t)(e / M);
+            fill[b]++;
+        }
+    }
+    int32_t* new_ids = (int32_t*)malloc(sizeof(int32_t) * (size_t)E);
+    float* new_d = (float*)malloc(sizeof(float) * (size_t)E);
+    memcpy(new_ids, ids, sizeof(int32_t) * (size_t)E);
+    memcpy(new_d, d, sizeof(float) * (size_t)E);
+    #pragma omp parallel
+    {
+        rin_t* buf = NULL;
+        int64_t cap = 0;
+        #pragma omp for schedule(dynamic, 256)
+        for (int64_t b = 0; b < N; ++b) {
+            const int64_t n = off[b + 1] - off[b];
+            if (n == 0) continue;
+            if (n + M > cap) { cap = n + M; buf = (rin_t*)realloc(buf, sizeof(rin_t) * (size_t)cap); }
+            int64_t cnt = 0;
+            for (int k = 0; k < M; ++k) { buf[cnt].d = d[b * M + k]; buf[cnt].id = (uint32_t)ids[b * M + k]; ++cnt; }
+            int64_t added = 0;
+            for (int64_t t = off[b]; t < off[b + 1]; ++t) {
+                int in_row = 0;
+                for (int k = 0; k < M; ++k) in_row |= (uint32_t)ids[b * M + k] == offers[t].id;
+                if (!in_row) { buf[cnt++] = offers[t]; ++added; }
+            }
+            if (added == 0) continue;
+            qsort(buf, (size_t)cnt, sizeof(rin_t), rin_cmp);
+            for (int k = 0; k < M; ++k) { new_ids[b * M + k] = (int32_t)buf[k].id; new_d[b * M + k] = buf[k].d; }
+        }
+        free(buf);
+    }
+    memcpy(ids, new_ids, sizeof(int32_t) * (size_t)E);
+    memcpy(d, new_d, sizeof(float) * (size_t)E);
+    free(worst); free(off); free(offers); free(fill); free(new_ids); free(new_d);
+    return OR_OK;
+}
+
 int or_num_threads(void)
 {
 #ifdef _OPENMP

@@ -41,6 +41,12 @@ How each oracle function is pinned (what checks it besides itself):
   example; the tie order of np.argsort and float32 summation order of the
   reference are "parity unpinned" (only an import would pin them), so tests
   use integer data without distance ties.
+* ``reverse_insert`` -- bd/build_bucket.py:473-543.  Pinned by a hand-computed
+  1-D known answer, by the fixed point "an exact kNN table with distinct
+  distances does not change", and by the characterisation of each new row
+  as the M smallest of (row, surviving offers) -- every offer left out is
+  not below the row's last key.  torch.topk's order among equal distances is
+  "parity unpinned"; the oracle orders ties by id.
 """
 from __future__ import annotations
 
@@ -78,6 +84,7 @@ def lib():
         L.or_cagra_prune.argtypes = [vp, i64, i32, i32, vp, vp]
         L.or_detour_counts.argtypes = [vp, i64, i32, i64, vp]
         L.or_reverse_merge.argtypes = [vp, i64, i32, vp]
+        L.or_reverse_insert.argtypes = [vp, vp, i64, i32]
         L.or_merge_row.argtypes = [vp, vp, C.c_uint32, C.c_uint32]
         L.or_merge_row.restype = None
         L.or_refine_2hop.argtypes = [vp, i64, i64, i32, vp, vp, i32, i32, vp, vp]
@@ -185,6 +192,15 @@ def detour_counts(G, a):
     cnt = np.empty(M, np.uint32)
     _check(lib().or_detour_counts(_p(G), N, M, a, _p(cnt)), "or_detour_counts")
     return cnt
+
+
+def reverse_insert(ids, d):
+    """bd/build_bucket.py:473-543 on a copy of (ids, d); returns (ids, d)."""
+    ids = np.ascontiguousarray(ids, np.int32).copy()
+    d = np.ascontiguousarray(d, np.float32).copy()
+    N, M = ids.shape
+    _check(lib().or_reverse_insert(_p(ids), _p(d), N, M), "or_reverse_insert")
+    return ids, d
 
 
 def reverse_merge(fwd):

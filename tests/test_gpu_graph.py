@@ -153,3 +153,125 @@ def test_build_graph_recall_c2_small(ctx):
     _assert_rows_equal(gfwd, fwd, san)
     _assert_rows_equal(ctx.reverse_merge(fwd), O.reverse_merge(fwd), fwd)
     _assert_rows_equal(res.graph, O.reverse_merge(fwd), fwd)
+
+
+# ------------------------------------------------------- Python-pipeline stages
+
+def _int_data(rng, N, D, hi=255):
+    return rng.integers(0, hi + 1, size=(N, D)).astype(np.float32)
+
+
+@pytest.mark.parametrize("N,D,M,maxdeg", [(3000, 128, 64, 32), (2000, 100, 64, 0), (1500, 32, 20, 8),
+                                          (1200, 64, 96, 48), (900, 96, 128, 64), (64, 32, 40, 0)])
+def test_prune_occlusion_matches_oracle(ctx, N, D, M, maxdeg):
+    rng = np.random.default_rng(N + M)
+    X = _int_data(rng, N, D)
+    nb = rng.integers(-1, N + 5, size=(N, M)).astype(np.int32)    # padding, out of range
+    nb[::7, 0] = np.arange(0, N, 7)                                # self
+    nb[::5, 3] = nb[::5, 2]                                        # duplicates
+    print(f"occlusion N={N} D={D} M={M} maxdeg={maxdeg}", flush=True)
+    got = ctx.prune_occlusion(X, nb, maxdeg)
+    want = O.prune_occlusion(X, nb.astype(np.int64), maxdeg)
+    np.testing.assert_array_equal(got, want)
+
+
+def test_prune_occlusion_on_knn_lists_u8(ctx):
+    rng = np.random.default_rng(3)
+    X = rng.integers(0, 256, size=(4000, 128)).astype(np.uint8)
+    ids, _ = O.knn_exact(X.astype(np.float32), 64)
+    got = ctx.prune_occlusion(X, ids, 32)
+    want = O.prune_occlusion(X.astype(np.float32), ids.astype(np.int64), 32)
+    np.testing.assert_array_equal(got, want)
+
+
+def test_prune_occlusion_float_data(ctx):
+    # non-integer data: a decision can flip only on a near-tie of fp32 sums
+    X, _ = synth.generate("C1", n=3000)
+    ids, _ = O.knn_exact(X, 48)
+    got = ctx.prune_occlusion(X, ids, 24)
+    want = O.prune_occlusion(X, ids.astype(np.int64), 24)
+    assert (got == want).all(axis=1).mean() >= 0.999
+
+
+def _offer_table(rng, X, M):
+    ids, d = O.knn_exact(X, M)
+    # degrade: drop some true neighbours so that offers exist
+    N = len(X)
+    keep = rng.random((N, M)) < 0.7
+    far = rng.integers(0, N, size=(N, M)).astype(np.int32)
+    Xi = X.astype(np.int64)
+    ids = np.where(keep, ids, far).astype(np.int32)
+    d = ((Xi[ids] - Xi[:, None, :]) ** 2).sum(axis=2).astype(np.float32)
+    d[ids == np.arange(N)[:, None]] = np.inf
+    ids[ids == np.arange(N)[:, None]] = -1
+    o = np.lexsort((ids.view(np.uint32), d), axis=1)
+    return np.take_along_axis(ids, o, 1), np.take_along_axis(d, o, 1)
+
+
+@pytest.mark.parametrize("N,D,M", [(3000, 32, 64), (2000, 16, 32), (1000, 8, 128), (500, 4, 16)])
+def test_reverse_insert_matches_oracle(ctx, N, D, M):
+    rng = np.random.default_rng(N * 3 + M)
+    X = _int_data(rng, N, D, 15)
+    ids, d = _offer_table(rng, X, M)
+    print(f"reverse insert N={N} D={D} M={M}", flush=True)
+    gi, gd = ctx.reverse_insert(ids, d)
+    oi, od = O.reverse_insert(ids, d)
+    np.testing.assert_array_equal(gi, oi)
+    np.testing.assert_array_equal(gd, od)
+
+
+def test_reverse_insert_hub_and_repeats(ctx):
+    # one target offered by nearly every row (>> 64 offers: several chunks),
+    # repeated offers of the same source, padded rows
+    rng = np.random.default_rng(9)
+    N, M = 1500, 16
+    ids = rng.integers(0, N, size=(N, M)).astype(np.int32)
+    d = np.sort(rng.integers(1, 50, size=(N, M)).astype(np.float32), axis=1)
+    ids[:, 0] = 7
+    d[:, 0] = rng.integers(0, 3, size=N)
+    ids[::3, 1] = ids[::3, 0]
+    d[::3, 1] = d[::3, 0]
+    d[7] = 1000.0
+    ids[11, 8:], d[11, 8:] = -1, np.inf
+    o = np.lexsort((ids.view(np.uint32), d), axis=1)
+    ids, d = np.take_along_axis(ids, o, 1), np.take_along_axis(d, o, 1)
+    gi, gd = ctx.reverse_insert(ids, d)
+    oi, od = O.reverse_insert(ids, d)
+    np.testing.assert_array_equal(gi, oi)
+    np.testing.assert_array_equal(gd, od)
+
+
+def test_reverse_insert_out_of_range(ctx):
+    import gtann
+    ids = np.zeros((10, 4), np.int32)
+    ids[3, 2] = 10
+    with pytest.raises(gtann.GtannError) as e:
+        ctx.reverse_insert(ids, np.ones((10, 4), np.float32))
+    assert e.value.code == gtann.GT_EINVAL
+
+
+def test_build_graph_reverse_edges_rounds(ctx):
+    # the Python pipeline's rounds (full table + reverse edges + merge) equal
+    # the oracle's composition of the same steps on the GPU's own round tables
+    X, _ = synth.generate("C1", n=4000)
+    X = np.rint(X * 8).astype(np.float32)   # integer-valued: exact, symmetric distances
+    r = ctx.build_graph(X, n_buckets=8, nprobe=7, M=32, K=16, rounds=2, kmeans_iters=0, reverse_edges=True,
+                        prune=False)
+    ex_i, ex_d = O.knn_exact(X, 32)
+    # the probes cover every bucket, so each round's table is exact, and an
+    # offer below a row's worst is then already in the row: the result is
+    # the exact table
+    np.testing.assert_array_equal(r.knn_ids, ex_i)
+    np.testing.assert_array_equal(r.knn_dists, ex_d)
+    assert r.graph is None
+    # one probe: the rounds are approximate; the merged table keeps its
+    # invariants (sorted, no self, no duplicates, exact distances)
+    r2 = ctx.build_graph(X, n_buckets=8, nprobe=1, M=32, K=16, rounds=2, kmeans_iters=0, reverse_edges=True,
+                         prune=False)
+    d2 = r2.knn_dists
+    assert (np.diff(d2, axis=1) >= 0).all()
+    assert (d2 >= ex_d).all()
+    for q in range(0, len(X), 97):
+        v = r2.knn_ids[q][r2.knn_ids[q] >= 0]
+        assert len(set(v.tolist())) == len(v) and q not in v
+        np.testing.assert_array_equal(d2[q][:len(v)], ((X[v] - X[q]) ** 2).sum(axis=1))

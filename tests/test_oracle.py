@@ -288,3 +288,59 @@ def test_occlusion_prune_line_known_answer():
     assert out[0].tolist() == [1, 3, -1]
     out = O.prune_occlusion(X, nb, 1)
     assert out[0].tolist() == [1, -1, -1]
+
+
+# ---------------------------------------------------------------- reverse-edge insertion
+
+def test_reverse_insert_line_known_answer():
+    # points at 0, 1, 3, 7 (squared distances); an approximate table in which
+    # row 2 misses 1 (d=4) and row 0 misses 2 (d=9).  Offers: 1->2 (4 < 16)
+    # enters row 2; 2->0 (9 < 49) enters row 0; 3->2 (16) is not below row 2's
+    # worst (16); offers already in the target row are dropped.
+    ids = np.array([[1, 3], [0, 2], [0, 3], [2, 1]], np.int32)
+    d = np.array([[1, 49], [1, 4], [9, 16], [16, 36]], np.float32)
+    ri, rd = O.reverse_insert(ids, d)
+    assert ri.tolist() == [[1, 2], [0, 2], [1, 0], [2, 1]]
+    assert rd.tolist() == [[1, 9], [1, 4], [4, 9], [16, 36]]
+
+
+def test_reverse_insert_exact_table_is_fixed_point():
+    # with distinct distances every offer below b's worst is one of b's exact
+    # nearest neighbours, so it is already in b's row
+    rng = np.random.default_rng(5)
+    X = rng.standard_normal((600, 8)).astype(np.float32)
+    ids, d = O.knn_exact(X, 12)
+    ri, rd = O.reverse_insert(ids, d)
+    np.testing.assert_array_equal(ri, ids)
+    np.testing.assert_array_equal(rd, d)
+
+
+def test_reverse_insert_rows_are_m_smallest_of_row_and_offers():
+    rng = np.random.default_rng(6)
+    N, M = 400, 10
+    ids = np.stack([rng.permutation(N)[:M] for _ in range(N)]).astype(np.int32)
+    d = np.sort(rng.integers(0, 1000, size=(N, M)).astype(np.float32), axis=1)
+    ids[rng.random((N, M)) < 0.05] = -1
+    d[ids < 0] = np.inf
+    o = np.argsort(d, axis=1, kind="stable")
+    ids, d = np.take_along_axis(ids, o, 1), np.take_along_axis(d, o, 1)
+    ri, rd = O.reverse_insert(ids, d)
+    worst = d.max(axis=1)
+    offers = [[] for _ in range(N)]
+    for a in range(N):
+        for k in range(M):
+            b = ids[a, k]
+            if b >= 0 and d[a, k] < worst[b] and a not in ids[b]:
+                offers[b].append((float(d[a, k]), a))
+    for b in range(N):
+        pool = sorted([(float(x), int(i) & 0xFFFFFFFF) for x, i in zip(d[b], ids[b])] + offers[b])
+        if not offers[b]:
+            assert ri[b].tolist() == ids[b].tolist()
+            continue
+        got = [(float(x), int(i) & 0xFFFFFFFF) for x, i in zip(rd[b], ri[b])]
+        assert got == sorted(got)
+        # every entry left out is not below the last kept one
+        left = list(pool)
+        for g in got:
+            left.remove(g)
+        assert all(x >= got[-1] for x in left)
