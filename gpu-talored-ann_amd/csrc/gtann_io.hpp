@@ -1,0 +1,190 @@
+// gtann_io.hpp -- readers and writers of the pipeline's on-disk files.
+//
+// Layouts (byte-identical with the reference's files):
+//   dataset   .fbin/.bin  int32 N, int32 D, N*D float32     (src/load.hpp:67-84)
+//             .u8bin      int32 N, int32 D, N*D uint8       (src/load.hpp:94-117)
+//             .i8bin      int32 N, int32 D, N*D int8, signed (src/load.hpp:86-92)
+//   vector_knn.bin        int64 N, int32 M, int32[N*M], -1 = padding
+//                         (src/graph_io.hpp:26-30, 286-329)
+//   vector_dists.bin      int64 N, int32 M, float32[N*M] (src/bucket.cu:5563-5573)
+//   graph / final_graph   int64 N, int32 K, uint32[N*K]  (src/graph_io.hpp:8-11, 50-96)
+//   inverse_perm.bin      uint32[N], no header           (src/graph_io.hpp:369-377)
+//   *.npy                 NumPy format 1.0, C order, little endian (src/load.hpp:535-590)
+//
+// Errors throw std::runtime_error naming the file.
+#pragma once
+
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+namespace gtann_io {
+
+enum class Elem { F32, U8, I8 };
+
+inline size_t elem_size(Elem e) { return e == Elem::F32 ? 4 : 1; }
+
+inline bool ends_with(const std::string& s, const char* suf)
+{
+    const size_t n = std::strlen(suf);
+    return s.size() >= n && s.compare(s.size() - n, n, suf) == 0;
+}
+
+// element type a dataset path stands for, by extension
+inline Elem dataset_elem(const std::string& path)
+{
+    if (ends_with(path, ".fbin") || ends_with(path, ".bin")) return Elem::F32;
+    if (ends_with(path, ".u8bin")) return Elem::U8;
+    if (ends_with(path, ".i8bin")) return Elem::I8;
+    throw std::runtime_error("unsupported dataset extension (.fbin/.bin/.u8bin/.i8bin): " + path);
+}
+
+class File {
+public:
+    File(const std::string& path, const char* mode) : path_(path), f_(std::fopen(path.c_str(), mode))
+    {
+        if (!f_) throw std::runtime_error("cannot open " + path);
+    }
+    ~File() { if (f_) std::fclose(f_); }
+    File(const File&) = delete;
+    File& operator=(const File&) = delete;
+    void read(void* p, size_t bytes, const char* what)
+    {
+        if (bytes && std::fread(p, 1, bytes, f_) != bytes)
+            throw std::runtime_error(std::string("short read of ") + what + ": " + path_);
+    }
+    void write(const void* p, size_t bytes)
+    {
+        if (bytes && std::fwrite(p, 1, bytes, f_) != bytes) throw std::runtime_error("write failed: " + path_);
+    }
+    void close()
+    {
+        if (f_ && std::fclose(f_) != 0) { f_ = nullptr; throw std::runtime_error("close failed: " + path_); }
+        f_ = nullptr;
+    }
+    int64_t size()
+    {
+        const long cur = std::ftell(f_);
+        std::fseek(f_, 0, SEEK_END);
+        const long end = std::ftell(f_);
+        std::fseek(f_, cur, SEEK_SET);
+        return end;
+    }
+
+private:
+    std::string path_;
+    std::FILE* f_;
+};
+
+struct Dataset {
+    int32_t N = 0, D = 0;
+    Elem elem = Elem::F32;
+    std::vector<uint8_t> bytes;   // N*D elements as stored in the file
+    const void* data() const { return bytes.data(); }
+};
+
+inline Dataset read_dataset(const std::string& path)
+{
+    Dataset ds;
+    ds.elem = dataset_elem(path);
+    File f(path, "rb");
+    int32_t hdr[2];
+    f.read(hdr, sizeof(hdr), "header");
+    if (hdr[0] <= 0 || hdr[1] <= 0) throw std::runtime_error("bad header (N, D) in " + path);
+    ds.N = hdr[0];
+    ds.D = hdr[1];
+    ds.bytes.resize(static_cast<size_t>(ds.N) * ds.D * elem_size(ds.elem));
+    f.read(ds.bytes.data(), ds.bytes.size(), "payload");
+    return ds;
+}
+
+inline void write_dataset(const std::string& path, const void* data, int32_t N, int32_t D, Elem elem)
+{
+    File f(path, "wb");
+    const int32_t hdr[2] = {N, D};
+    f.write(hdr, sizeof(hdr));
+    f.write(data, static_cast<size_t>(N) * D * elem_size(elem));
+    f.close();
+}
+
+// int64 N, int32 W, T[N*W]: vector_knn.bin (int32), vector_dists.bin (float),
+// graphs (uint32)
+template <typename T>
+struct Table {
+    int64_t N = 0;
+    int32_t W = 0;
+    std::vector<T> v;
+};
+
+template <typename T>
+inline Table<T> read_table(const std::string& path)
+{
+    Table<T> t;
+    File f(path, "rb");
+    f.read(&t.N, sizeof(t.N), "header");
+    f.read(&t.W, sizeof(t.W), "header");
+    if (t.N <= 0 || t.W <= 0) throw std::runtime_error("bad header (N, width) in " + path);
+    t.v.resize(static_cast<size_t>(t.N) * t.W);
+    f.read(t.v.data(), t.v.size() * sizeof(T), "payload");
+    return t;
+}
+
+template <typename T>
+inline void write_table(const std::string& path, const T* v, int64_t N, int32_t W)
+{
+    File f(path, "wb");
+    f.write(&N, sizeof(N));
+    f.write(&W, sizeof(W));
+    f.write(v, static_cast<size_t>(N) * W * sizeof(T));
+    f.close();
+}
+
+inline std::vector<uint32_t> read_inverse_perm(const std::string& path)
+{
+    File f(path, "rb");
+    const int64_t bytes = f.size();
+    if (bytes <= 0 || bytes % 4) throw std::runtime_error("inverse permutation size is not a multiple of 4: " + path);
+    std::vector<uint32_t> p(static_cast<size_t>(bytes / 4));
+    f.read(p.data(), static_cast<size_t>(bytes), "payload");
+    return p;
+}
+
+inline void write_inverse_perm(const std::string& path, const uint32_t* p, int64_t N)
+{
+    File f(path, "wb");
+    f.write(p, static_cast<size_t>(N) * 4);
+    f.close();
+}
+
+template <typename T> inline const char* npy_descr();
+template <> inline const char* npy_descr<int64_t>() { return "<i8"; }
+template <> inline const char* npy_descr<int32_t>() { return "<i4"; }
+template <> inline const char* npy_descr<uint32_t>() { return "<u4"; }
+template <> inline const char* npy_descr<float>() { return "<f4"; }
+
+// NumPy format 1.0: magic, version, uint16 header length, a dict padded with
+// spaces and a newline so that the data starts at a multiple of 64 bytes
+template <typename T>
+inline void write_npy(const std::string& path, const T* v, int64_t rows, int64_t cols)
+{
+    std::string dict = std::string("{'descr': '") + npy_descr<T>() + "', 'fortran_order': False, 'shape': (" +
+                       std::to_string(rows) + ", " + std::to_string(cols) + "), }";
+    const size_t pre = 10;
+    size_t total = pre + dict.size() + 1;
+    const size_t pad = (64 - total % 64) % 64;
+    dict.append(pad, ' ');
+    dict.push_back('\n');
+    const uint16_t hlen = static_cast<uint16_t>(dict.size());
+    File f(path, "wb");
+    const char magic[8] = {'\x93', 'N', 'U', 'M', 'P', 'Y', 1, 0};
+    f.write(magic, 8);
+    f.write(&hlen, 2);
+    f.write(dict.data(), dict.size());
+    f.write(v, static_cast<size_t>(rows * cols) * sizeof(T));
+    f.close();
+}
+
+}  // namespace gtann_io

@@ -1,0 +1,370 @@
+// gtann_main.cpp -- command-line front end of libgtann.so, one subcommand per
+// executable of the reference pipeline (sk/scripts/run_pipeline.sh:111-148):
+//
+//   gtann bucket2 -i BASE -o OUT [--centroid-ratio R] [--seed S] [--knn-k K]
+//         [--nprobe P] [--neighbors-m M] [-t T] [--fused-optimize-degree K]
+//         [--skip-dists] [--skip-npy] [--kmeans-iters I] [--balance F]
+//         [--refine-passes P] [--refine-sample S]
+//       the GPU-resident build (src/bucket.cu:9900-9990 options).  Writes, under
+//       OUT/k<knn-k>p<nprobe>m<M>t<T>/ (src/bucket.cu:8545-8556):
+//       vector_knn.bin, vector_dists.bin, neighbors.npy (int64), and with
+//       --fused-optimize-degree K > 0 final_graph.bin.  Ids are the input's
+//       own order: inverse_perm.bin is the identity and data_reordered<ext>
+//       links to the input, so the out-of-core tools below read them as usual.
+//   gtann optimize -i DATA -g KNN -o OUT --output-degree K [--skip-sort]
+//       sanitize + CAGRA prune + reverse merge (src/optimize.cu); exit 2 when
+//       the device cannot hold the tables (the reference's "use the other
+//       path" code, src/optimize.cu:300-308).
+//   gtann prune_windowed -k KNN -i DATA -o FWD --output-degree K
+//       sanitize + CAGRA prune with the whole table resident (src/prune_windowed.cpp).
+//   gtann optimize_chunked -g FWD -o OUT [-m E] [--inverse-perm P --final-output F]
+//       reverse-edge merge (Method E), optionally translated to original ids.
+//   gtann translate_ids -g G -p P -o OUT
+//       out[inv[i]][k] = inv[g[i][k]] (src/translate_ids.cpp).
+//   gtann knn -i DATA -o OUTDIR -k K
+//       exact self-excluded kNN (bd/build_knn.py) as vector_knn.bin/vector_dists.bin.
+//
+// Options of the reference that tune its host/out-of-core memory use are
+// accepted and ignored (the tables are resident in HBM).  Errors print
+// "FATAL: <message>" and exit 1.
+#include "gtann.h"
+#include "gtann_io.hpp"
+
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <map>
+#include <set>
+#include <string>
+#include <vector>
+
+namespace {
+
+using namespace gtann_io;
+
+struct Exit {
+    int code;
+    std::string msg;
+};
+
+class Args {
+public:
+    // value options (long names, aliases "a,b"), switches, ignored value options
+    Args(int argc, char** argv, std::initializer_list<const char*> values, std::initializer_list<const char*> switches,
+         std::initializer_list<const char*> ignored = {})
+    {
+        std::map<std::string, std::string> alias;
+        auto reg = [&](const char* spec, std::set<std::string>& into) {
+            std::string s(spec);
+            const size_t c = s.find(',');
+            const std::string name = s.substr(0, c);
+            into.insert(name);
+            alias["--" + name] = name;
+            if (c != std::string::npos) alias["-" + s.substr(c + 1)] = name;
+        };
+        std::set<std::string> vals, sws, ign;
+        for (const char* v : values) reg(v, vals);
+        for (const char* v : switches) reg(v, sws);
+        for (const char* v : ignored) reg(v, ign);
+        for (int i = 0; i < argc; ++i) {
+            std::string a = argv[i], val;
+            bool has_val = false;
+            const size_t eq = a.find('=');
+            if (a.rfind("--", 0) == 0 && eq != std::string::npos) {
+                val = a.substr(eq + 1);
+                a = a.substr(0, eq);
+                has_val = true;
+            }
+            auto it = alias.find(a);
+            if (it == alias.end()) throw Exit{1, "unknown option " + a};
+            const std::string& name = it->second;
+            if (sws.count(name)) {
+                flags_.insert(name);
+                continue;
+            }
+            if (!has_val) {
+                if (i + 1 >= argc) throw Exit{1, "option " + a + " needs a value"};
+                val = argv[++i];
+            }
+            if (!ign.count(name)) kv_[name] = val;
+        }
+    }
+    bool has(const std::string& k) const { return kv_.count(k) > 0; }
+    bool flag(const std::string& k) const { return flags_.count(k) > 0; }
+    std::string str(const std::string& k) const
+    {
+        auto it = kv_.find(k);
+        if (it == kv_.end()) throw Exit{1, "missing required option --" + k};
+        return it->second;
+    }
+    long long num(const std::string& k, long long def) const { return has(k) ? std::stoll(str(k)) : def; }
+    double real(const std::string& k, double def) const { return has(k) ? std::stod(str(k)) : def; }
+
+private:
+    std::map<std::string, std::string> kv_;
+    std::set<std::string> flags_;
+};
+
+struct Lib {
+    gt_ctx* ctx = nullptr;
+    Lib()
+    {
+        if (gt_create(0, &ctx) != GT_OK) throw Exit{1, "cannot create a GPU context (gt_create)"};
+    }
+    ~Lib() { gt_destroy(ctx); }
+    void check(int rc, const char* what) const
+    {
+        if (rc == GT_OK) return;
+        const std::string m = std::string(what) + ": " + gt_last_error(ctx);
+        throw Exit{rc == GT_ENOMEM ? 2 : 1, m};
+    }
+};
+
+int dtype_code(Elem e) { return e == Elem::F32 ? GT_DTYPE_F32 : e == Elem::U8 ? GT_DTYPE_U8 : GT_DTYPE_I8; }
+
+double now()
+{
+    return std::chrono::duration<double>(std::chrono::steady_clock::now().time_since_epoch()).count();
+}
+
+void mkdirs(const std::string& path)
+{
+    std::string cur;
+    for (size_t i = 0; i <= path.size(); ++i) {
+        if (i == path.size() || path[i] == '/') {
+            if (!cur.empty()) mkdir(cur.c_str(), 0755);
+        }
+        if (i < path.size()) cur.push_back(path[i]);
+    }
+    struct stat st;
+    if (stat(path.c_str(), &st) != 0 || !S_ISDIR(st.st_mode)) throw Exit{1, "cannot create directory " + path};
+}
+
+std::string abs_path(const std::string& p)
+{
+    if (!p.empty() && p[0] == '/') return p;
+    char buf[4096];
+    if (!getcwd(buf, sizeof(buf))) return p;
+    return std::string(buf) + "/" + p;
+}
+
+std::string ext_of(const std::string& p)
+{
+    const size_t dot = p.find_last_of('.');
+    const size_t slash = p.find_last_of('/');
+    if (dot == std::string::npos || (slash != std::string::npos && dot < slash)) return "";
+    return p.substr(dot);
+}
+
+std::vector<int64_t> widen(const int32_t* v, size_t n)
+{
+    return std::vector<int64_t>(v, v + n);
+}
+
+// vector_knn.bin -> uint32 table in rank order (src/optimize.cu:89-134)
+std::vector<uint32_t> sanitized(const Lib& L, const Table<int32_t>& knn)
+{
+    std::vector<uint32_t> s(knn.v.size());
+    L.check(gt_sanitize(L.ctx, knn.v.data(), knn.N, knn.W, s.data()), "gt_sanitize");
+    return s;
+}
+
+int cmd_bucket2(int argc, char** argv)
+{
+    Args a(argc, argv,
+           {"input,i", "output,o", "centroid-ratio", "seed", "knn-k", "nprobe", "neighbors-m", "iterations,t",
+            "fused-optimize-degree", "kmeans-iters", "balance", "refine-passes", "refine-sample"},
+           {"skip-dists", "skip-npy", "out-of-core"},
+           {"cpu-limit", "gpu-limit", "bucket-vec-buffer", "sample-rate", "use-pq", "kmeans-train-fraction", "bucket-mem-mb",
+            "gpu-bucket-cache-mb", "pq-bits-start", "pq-bits-min", "search-iters", "order-window", "cache-mb"});
+    const std::string in = a.str("input"), root = a.str("output");
+    const int knn_k = static_cast<int>(a.num("knn-k", 32));
+    const int np_arg = static_cast<int>(a.num("nprobe", 0));
+    const int nprobe = np_arg > 0 ? np_arg : knn_k;
+    const int M = static_cast<int>(a.num("neighbors-m", 0));
+    const int T = static_cast<int>(a.num("iterations", 1));
+    const int K = static_cast<int>(a.num("fused-optimize-degree", 0));
+    if (M <= 0) throw Exit{1, "--neighbors-m must be > 0 (this build always runs the per-vector kNN)"};
+    if (nprobe > 256) throw Exit{1, "nprobe exceeds 256"};
+    if (T < 1) throw Exit{1, "iterations must be >= 1"};
+    const double t0 = now();
+    Dataset ds = read_dataset(in);
+    const double t_read = now() - t0;
+    const double ratio = a.real("centroid-ratio", 0.01);
+    gt_build_params p;
+    gt_build_params_default(&p);
+    p.n_buckets = static_cast<int32_t>(std::max<double>(1.0, std::llround(ds.N * ratio)));
+    p.nprobe = nprobe;
+    p.M = M;
+    p.K = K > 0 ? K : std::min(M, 32);
+    p.rounds = T;
+    p.seed = static_cast<uint64_t>(a.num("seed", 42));
+    p.kmeans_iters = static_cast<int32_t>(a.num("kmeans-iters", p.kmeans_iters));
+    p.balance = static_cast<float>(a.real("balance", p.balance));
+    p.refine_passes = static_cast<int32_t>(a.num("refine-passes", 0));
+    p.refine_sample = static_cast<int32_t>(a.num("refine-sample", p.refine_sample));
+    const std::string dir = root + "/k" + std::to_string(knn_k) + "p" + std::to_string(nprobe) + "m" +
+                            std::to_string(M) + "t" + std::to_string(T);
+    mkdirs(dir);
+    std::printf("Output subdir: %s\n", dir.c_str());
+    const size_t nm = static_cast<size_t>(ds.N) * M;
+    std::vector<int32_t> ids(nm);
+    std::vector<float> dists(nm);
+    std::vector<uint32_t> graph(K > 0 ? static_cast<size_t>(ds.N) * K : 0);
+    gt_build_stats st;
+    Lib L;
+    L.check(gt_build_graph(L.ctx, ds.data(), ds.N, ds.D, dtype_code(ds.elem), &p, ids.data(), dists.data(),
+                           K > 0 ? graph.data() : nullptr, &st),
+            "gt_build_graph");
+    const double t1 = now();
+    write_table<int32_t>(dir + "/vector_knn.bin", ids.data(), ds.N, M);
+    if (!a.flag("skip-dists")) write_table<float>(dir + "/vector_dists.bin", dists.data(), ds.N, M);
+    if (!a.flag("skip-npy")) {
+        const std::vector<int64_t> w = widen(ids.data(), ids.size());
+        write_npy<int64_t>(dir + "/neighbors.npy", w.data(), ds.N, M);
+    }
+    if (K > 0) write_table<uint32_t>(dir + "/final_graph.bin", graph.data(), ds.N, K);
+    std::vector<uint32_t> ident(static_cast<size_t>(ds.N));
+    for (size_t i = 0; i < ident.size(); ++i) ident[i] = static_cast<uint32_t>(i);
+    write_inverse_perm(dir + "/inverse_perm.bin", ident.data(), ds.N);
+    const std::string link = dir + "/data_reordered" + ext_of(in);
+    unlink(link.c_str());
+    if (symlink(abs_path(in).c_str(), link.c_str()) != 0) std::fprintf(stderr, "[warn] cannot link %s\n", link.c_str());
+    const double t_write = now() - t1;
+    std::printf("[bucket2] N=%d D=%d buckets=%d nprobe=%d M=%d K=%d t=%d\n", ds.N, ds.D, p.n_buckets, nprobe, M, K, T);
+    std::printf("[bucket2] read %.3f s  build %.3f s (bucketing %.3f, knn %.3f, merge %.3f, refine %.3f, prune %.3f, "
+                "revmerge %.3f)  write %.3f s\n",
+                t_read, st.t_total, st.t_bucketing, st.t_knn, st.t_merge, st.t_refine, st.t_prune, st.t_revmerge,
+                t_write);
+    return 0;
+}
+
+int cmd_optimize(int argc, char** argv)
+{
+    Args a(argc, argv, {"input,i", "knn-graph,g", "output,o", "output-degree"},
+           {"skip-sort", "save-npy", "force-chunked"}, {"gpu-fit-margin"});
+    const int K = static_cast<int>(a.num("output-degree", 32));
+    if (!a.flag("skip-sort"))
+        std::fprintf(stderr, "[optimize] rows are taken in their stored (rank) order, as with --skip-sort\n");
+    Table<int32_t> knn = read_table<int32_t>(a.str("knn-graph"));
+    Lib L;
+    std::vector<uint32_t> s = sanitized(L, knn);
+    std::vector<uint32_t> out(static_cast<size_t>(knn.N) * K);
+    L.check(gt_optimize(L.ctx, s.data(), knn.N, knn.W, K, out.data()), "gt_optimize");
+    write_table<uint32_t>(a.str("output"), out.data(), knn.N, K);
+    if (a.flag("save-npy")) {
+        std::vector<int64_t> w(out.begin(), out.end());
+        write_npy<int64_t>(a.str("output") + ".npy", w.data(), knn.N, K);
+    }
+    return 0;
+}
+
+int cmd_prune_windowed(int argc, char** argv)
+{
+    Args a(argc, argv, {"vector-knn-reordered,k", "dataset,i", "output,o", "output-degree"}, {"save-npy"},
+           {"bucket-offsets", "bucket-process-order", "centroid-knn,c", "order-window", "cache-mb", "pool-graph",
+            "dists"});
+    const int K = static_cast<int>(a.num("output-degree", 32));
+    Table<int32_t> knn = read_table<int32_t>(a.str("vector-knn-reordered"));
+    Lib L;
+    std::vector<uint32_t> s = sanitized(L, knn);
+    std::vector<uint32_t> out(static_cast<size_t>(knn.N) * K);
+    L.check(gt_cagra_prune(L.ctx, s.data(), knn.N, knn.W, K, out.data()), "gt_cagra_prune");
+    write_table<uint32_t>(a.str("output"), out.data(), knn.N, K);
+    return 0;
+}
+
+int cmd_optimize_chunked(int argc, char** argv)
+{
+    Args a(argc, argv, {"forward-graph,g", "output,o", "method,m", "inverse-perm", "final-output"}, {"save-npy"},
+           {"gpu-budget-mb", "host-budget-mb", "edge-buffer-mb", "tmp-dir", "bucket-offsets", "rev-degree-cap"});
+    if (a.has("method") && a.str("method") != "E") throw Exit{1, "only method E is provided"};
+    Table<uint32_t> fwd = read_table<uint32_t>(a.str("forward-graph"));
+    Lib L;
+    std::vector<uint32_t> out(fwd.v.size());
+    L.check(gt_reverse_merge(L.ctx, fwd.v.data(), fwd.N, fwd.W, out.data()), "gt_reverse_merge");
+    write_table<uint32_t>(a.str("output"), out.data(), fwd.N, fwd.W);
+    if (a.has("inverse-perm") && a.has("final-output")) {
+        std::vector<uint32_t> inv = read_inverse_perm(a.str("inverse-perm"));
+        if (static_cast<int64_t>(inv.size()) != fwd.N) throw Exit{1, "inverse permutation length != N"};
+        std::vector<uint32_t> fin(out.size());
+        L.check(gt_translate(L.ctx, out.data(), inv.data(), fwd.N, fwd.W, fin.data()), "gt_translate");
+        write_table<uint32_t>(a.str("final-output"), fin.data(), fwd.N, fwd.W);
+    }
+    return 0;
+}
+
+int cmd_translate(int argc, char** argv)
+{
+    Args a(argc, argv, {"graph,g", "inverse-perm,p", "output,o"}, {}, {"out-buffer-mb"});
+    Table<uint32_t> g = read_table<uint32_t>(a.str("graph"));
+    std::vector<uint32_t> inv = read_inverse_perm(a.str("inverse-perm"));
+    if (static_cast<int64_t>(inv.size()) != g.N) throw Exit{1, "inverse permutation length != N"};
+    Lib L;
+    std::vector<uint32_t> out(g.v.size());
+    L.check(gt_translate(L.ctx, g.v.data(), inv.data(), g.N, g.W, out.data()), "gt_translate");
+    write_table<uint32_t>(a.str("output"), out.data(), g.N, g.W);
+    return 0;
+}
+
+int cmd_knn(int argc, char** argv)
+{
+    Args a(argc, argv, {"input,i", "output,o", "k,k"}, {"skip-npy"});
+    const int k = static_cast<int>(a.num("k", 32));
+    Dataset ds = read_dataset(a.str("input"));
+    Lib L;
+    const size_t nk = static_cast<size_t>(ds.N) * k;
+    std::vector<int32_t> ids(nk);
+    std::vector<float> d(nk);
+    L.check(gt_knn_exact(L.ctx, ds.data(), ds.N, ds.D, dtype_code(ds.elem), GT_METRIC_L2, nullptr, ds.N, k,
+                         ids.data(), d.data()),
+            "gt_knn_exact");
+    const std::string dir = a.str("output");
+    mkdirs(dir);
+    write_table<int32_t>(dir + "/vector_knn.bin", ids.data(), ds.N, k);
+    write_table<float>(dir + "/vector_dists.bin", d.data(), ds.N, k);
+    if (!a.flag("skip-npy")) {
+        const std::vector<int64_t> w = widen(ids.data(), ids.size());
+        write_npy<int64_t>(dir + "/exact_knn_idx.npy", w.data(), ds.N, k);
+        write_npy<float>(dir + "/exact_knn_dist.npy", d.data(), ds.N, k);
+    }
+    return 0;
+}
+
+void usage()
+{
+    std::fprintf(stderr,
+                 "usage: gtann <bucket2|optimize|prune_windowed|optimize_chunked|translate_ids|knn> [options]\n");
+}
+
+}  // namespace
+
+int main(int argc, char** argv)
+{
+    if (argc < 2) {
+        usage();
+        return 1;
+    }
+    const std::string cmd = argv[1];
+    try {
+        if (cmd == "bucket2") return cmd_bucket2(argc - 2, argv + 2);
+        if (cmd == "optimize") return cmd_optimize(argc - 2, argv + 2);
+        if (cmd == "prune_windowed") return cmd_prune_windowed(argc - 2, argv + 2);
+        if (cmd == "optimize_chunked") return cmd_optimize_chunked(argc - 2, argv + 2);
+        if (cmd == "translate_ids") return cmd_translate(argc - 2, argv + 2);
+        if (cmd == "knn") return cmd_knn(argc - 2, argv + 2);
+        usage();
+        return 1;
+    } catch (const Exit& e) {
+        std::fprintf(stderr, "FATAL: %s\n", e.msg.c_str());
+        return e.code;
+    } catch (const std::exception& e) {
+        std::fprintf(stderr, "FATAL: %s\n", e.what());
+        return 1;
+    }
+}

@@ -110,6 +110,13 @@ def ref():
         R.ref_detour_counts.argtypes = [vp, i64, i32, i64, vp]
         R.ref_reverse_merge.argtypes = [vp, i64, i32, vp]
         R.ref_translate.argtypes = [vp, vp, i64, i32, vp]
+        cp = C.c_char_p
+        R.ref_write_graph.argtypes = [cp, vp, i64, i32]
+        R.ref_write_vector_knn.argtypes = [cp, vp, i64, i32]
+        R.ref_write_u32_vector.argtypes = [cp, vp, i64]
+        R.ref_read_graph.argtypes = [cp, vp, i64, C.POINTER(i64), C.POINTER(i32)]
+        R.ref_read_vector_knn.argtypes = [cp, vp, i64, C.POINTER(i64), C.POINTER(i32)]
+        R.ref_read_dataset.argtypes = [cp, vp, i64, C.POINTER(i32), C.POINTER(i32)]
         _ref = R
     return _ref
 
@@ -285,3 +292,41 @@ def ref_translate(g, inv):
     out = np.empty((N, K), np.uint32)
     _check(ref().ref_translate(_p(g), _p(inv), N, K, _p(out)), "ref_translate")
     return out
+
+
+# ---- on-disk formats through the reference's own writers/readers (src/graph_io.hpp, src/load.hpp)
+
+def ref_write_graph(path, g):
+    g = np.ascontiguousarray(g, np.uint32)
+    _check(ref().ref_write_graph(str(path).encode(), _p(g), g.shape[0], g.shape[1]), "ref_write_graph")
+
+
+def ref_write_vector_knn(path, ids):
+    ids = np.ascontiguousarray(ids, np.int32)
+    _check(ref().ref_write_vector_knn(str(path).encode(), _p(ids), ids.shape[0], ids.shape[1]),
+           "ref_write_vector_knn")
+
+
+def ref_write_u32_vector(path, v):
+    v = np.ascontiguousarray(v, np.uint32)
+    _check(ref().ref_write_u32_vector(str(path).encode(), _p(v), v.size), "ref_write_u32_vector")
+
+
+def _ref_read(fn, path, dtype, cap, nt, wt):
+    buf = np.empty(cap, dtype)
+    n, w = nt(), wt()
+    _check(fn(str(path).encode(), _p(buf), cap, C.byref(n), C.byref(w)), fn.__name__)
+    return buf[: int(n.value) * int(w.value)].reshape(int(n.value), int(w.value))
+
+
+def ref_read_graph(path, cap=1 << 24):
+    return _ref_read(ref().ref_read_graph, path, np.uint32, cap, C.c_int64, C.c_int32)
+
+
+def ref_read_vector_knn(path, cap=1 << 24):
+    return _ref_read(ref().ref_read_vector_knn, path, np.int32, cap, C.c_int64, C.c_int32)
+
+
+def ref_read_dataset(path, cap=1 << 24):
+    """float32 (N, D) as the C++ pipeline reads it (.i8bin signed)."""
+    return _ref_read(ref().ref_read_dataset, path, np.float32, cap, C.c_int32, C.c_int32)

@@ -13,7 +13,11 @@
 //       edges {dst = fwd[i][k], src = i, rank = k} of
 //       src/optimize_chunked.cu:372-407;
 //   translate_ids::translate_graph_to_original_order
-//       (src/translate_graph_ids.hpp:75), through temporary files.
+//       (src/translate_graph_ids.hpp:75), through temporary files;
+//   graph_io::write_graph / write_vector_knn / write_vector_bin /
+//       read_forward_graph / read_vector_knn (src/graph_io.hpp) and
+//       load::read_fbin_f32 / read_u8bin_to_f32 (src/load.hpp:67-117): the
+//       on-disk formats, for byte-level checks of this build's writers.
 #include <cstdint>
 #include <cstdio>
 #include <cstdlib>
@@ -27,6 +31,7 @@
 #include "edge_chunk_accumulator.hpp"
 #include "graph_io.hpp"
 #include "translate_graph_ids.hpp"
+#include "load.hpp"
 
 extern "C" {
 
@@ -114,6 +119,83 @@ int ref_translate(const uint32_t* g, const uint32_t* inv, int64_t N, int32_t K, 
         std::filesystem::remove_all(d);
         if (n2 != N || k2 != K) return -1;
         for (size_t i = 0; i < res.size(); ++i) out[i] = res[i];
+        return 0;
+    } catch (...) {
+        return -1;
+    }
+}
+
+int ref_write_graph(const char* path, const uint32_t* g, int64_t N, int32_t K)
+{
+    try {
+        graph_io::write_graph(path, g, N, K);
+        return 0;
+    } catch (...) {
+        return -1;
+    }
+}
+
+int ref_write_vector_knn(const char* path, const int32_t* g, int64_t N, int32_t M)
+{
+    try {
+        graph_io::write_vector_knn(path, std::vector<int32_t>(g, g + N * M), N, M);
+        return 0;
+    } catch (...) {
+        return -1;
+    }
+}
+
+int ref_write_u32_vector(const char* path, const uint32_t* v, int64_t n)
+{
+    try {
+        graph_io::write_vector_bin(path, std::vector<uint32_t>(v, v + n));
+        return 0;
+    } catch (...) {
+        return -1;
+    }
+}
+
+// reads a graph file into out (capacity cap entries); N, K returned
+int ref_read_graph(const char* path, uint32_t* out, int64_t cap, int64_t* N, int32_t* K)
+{
+    try {
+        std::vector<uint32_t> g;
+        graph_io::read_forward_graph(path, g, *N, *K);
+        if (static_cast<int64_t>(g.size()) > cap) return -1;
+        for (size_t i = 0; i < g.size(); ++i) out[i] = g[i];
+        return 0;
+    } catch (...) {
+        return -1;
+    }
+}
+
+int ref_read_vector_knn(const char* path, int32_t* out, int64_t cap, int64_t* N, int32_t* M)
+{
+    try {
+        graph_io::VectorKnn vk = graph_io::read_vector_knn(path);
+        if (static_cast<int64_t>(vk.graph.size()) > cap) return -1;
+        *N = vk.N;
+        *M = vk.M;
+        for (size_t i = 0; i < vk.graph.size(); ++i) out[i] = vk.graph[i];
+        return 0;
+    } catch (...) {
+        return -1;
+    }
+}
+
+// dataset reader of the C++ pipeline: .fbin/.bin as float, .u8bin/.i8bin
+// converted by extension (.i8bin signed)
+int ref_read_dataset(const char* path, float* out, int64_t cap, int32_t* N, int32_t* D)
+{
+    try {
+        std::vector<float> v;
+        const std::string p(path);
+        if (p.size() >= 5 && (p.compare(p.size() - 5, 5, ".fbin") == 0 || p.compare(p.size() - 4, 4, ".bin") == 0))
+            load::read_fbin_f32(p, v, *N, *D);
+        else
+            load::read_u8bin_to_f32(p, v, *N, *D);
+        if (static_cast<int64_t>(v.size()) > cap) return -1;
+        for (size_t i = 0; i < v.size(); ++i) out[i] = v[i];
         return 0;
     } catch (...) {
         return -1;
