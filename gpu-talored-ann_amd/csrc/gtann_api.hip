@@ -208,7 +208,7 @@ static DevMatrix prepare(Ctx& c, int slot_x, int slot_raw, int slot_norms, const
     GT_REQUIRE(X != nullptr && N > 0 && D > 0, "empty dataset");
     GT_REQUIRE(N < (int64_t(1) << 31), "N must be < 2^31");
     const int Dp = pad_dim(D);
-    GT_REQUIRE(Dp <= 256, "dimension > 256 is not supported by this build");
+    GT_REQUIRE(Dp <= 1024, "dimension > 1024 is not supported by this build");
     const size_t es = dtype_size(dtype);
     DevMatrix m;
     m.N = N;

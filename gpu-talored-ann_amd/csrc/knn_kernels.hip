@@ -73,14 +73,19 @@ __device__ __forceinline__ void wave_bitonic_sort(float& d, int32_t& i, int lane
     }
 }
 
+// Per-block candidate buffers and merge scratch, shared by both kernels.
+struct KnnLists {
+    uint64_t buf[kQueriesPerBlock][kCB];  // packed (key, id) of candidates awaiting a merge
+    uint64_t sL[kWaves][kMaxM];           // the merging query's list, packed
+    float sthr[kWaves];
+};
+
 template <int DP>
 struct KnnSmem {
     float tile[2][kPoolTile][DP + 4];   // +4 floats: rows land on distinct bank groups
     float tnorm[3][kPoolTile];          // |p|^2 (L2) or 0 (IP); +inf past the slice end
     int32_t trow[3][kPoolTile];         // pool row id, -1 past the slice end
-    uint64_t buf[kQueriesPerBlock][kCB];  // packed (key, id) of candidates awaiting a merge
-    uint64_t sL[kWaves][kMaxM];           // the merging query's list, packed
-    float sthr[kWaves];
+    KnnLists L;
 };
 
 // Per-lane view of one query's state.  Lanes j and j+32 of a wave hold the
@@ -115,8 +120,7 @@ __device__ __forceinline__ int32_t load_list_i(const int32_t* p)
 // among the buffer plus the number of list entries before it; a list entry's
 // position is its index plus the number of buffer entries before it.
 // Called by all 64 lanes.
-template <int DP>
-__device__ void wave_merge(KnnSmem<DP>& sm, const KnnArgs& a, int w, int lane, int q, QueryState& st)
+__device__ void wave_merge(KnnLists& sm, const KnnArgs& a, int w, int lane, int q, QueryState& st)
 {
     const int nB = __shfl(st.cnt, q);
     const int nL = __shfl(st.nL, q);
@@ -183,18 +187,19 @@ __device__ void wave_merge(KnnSmem<DP>& sm, const KnnArgs& a, int w, int lane, i
     }
 }
 
-// Filter + append of one finished 32x32 tile (rows of tile `tp`), the slow
+// Filter + append of one finished 32x32 tile whose pool rows have norms
+// tn[0..32) and ids tr[0..32) (tbase = pool-list position of row 0), the slow
 // path taken only when some lane of the wave has a candidate <= its threshold.
-template <int DP, int METRIC>
-__device__ void tile_append(KnnSmem<DP>& sm, const KnnArgs& a, const floatx16& acc, int tp, int w, int lane,
-                            int h, int qlocal, bool qvalid, float qn, QueryState& st)
+template <int METRIC>
+__device__ __forceinline__ void tile_append(KnnLists& sm, const KnnArgs& a, const floatx16& acc, const float* tn,
+                            const int32_t* tr, int tbase, int w, int lane, int h, int qlocal, bool qvalid, float qn,
+                            QueryState& st)
 {
-    const int b3 = tp % 3;
     float dv[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
         const int i = 8 * (r >> 2) + 4 * h + (r & 3);
-        const float pn = sm.tnorm[b3][i];
+        const float pn = tn[i];
         dv[r] = METRIC == 0 ? fmaf(-2.f, acc[r], pn + qn) : fmaf(-1.f, acc[r], pn);
     }
     uint32_t pass = 0;
@@ -208,7 +213,7 @@ __device__ void tile_append(KnnSmem<DP>& sm, const KnnArgs& a, const floatx16& a
         while (needmask) {
             const int q = __ffsll(static_cast<unsigned long long>(needmask)) - 1;
             needmask &= needmask - 1;
-            wave_merge<DP>(sm, a, w, lane, q, st);
+            wave_merge(sm, a, w, lane, q, st);
         }
         pass = 0;
 #pragma unroll
@@ -222,7 +227,7 @@ __device__ void tile_append(KnnSmem<DP>& sm, const KnnArgs& a, const floatx16& a
         for (int r = 0; r < 16; ++r) {
             if ((pass >> r) & 1u) {
                 const int i = 8 * (r >> 2) + 4 * h + (r & 3);
-                const int32_t id = a.out_pos ? tp * kPoolTile + i : sm.trow[b3][i];
+                const int32_t id = a.out_pos ? tbase + i : tr[i];
                 sm.buf[qlocal][off] = pack_key(dv[r], id);
                 ++off;
             }
@@ -372,7 +377,8 @@ __global__ void __launch_bounds__(256, 2) knn_fused_kernel(KnnArgs a)
             }
         }
         if (t > 0 && __ballot(mkey <= st.thr))
-            tile_append<DP, METRIC>(sm, a, acc_prev, t - 1, w, lane, h, qlocal, qvalid, qn, st);
+            tile_append<METRIC>(sm.L, a, acc_prev, sm.tnorm[pb3], sm.trow[pb3], (t - 1) * kPoolTile, w, lane, h,
+                                qlocal, qvalid, qn, st);
 
         store_rows(buf ^ 1);
         if (tid < kPoolTile) { sm.trow[(t + 1) % 3][tid] = rid_cur; sm.tnorm[(t + 1) % 3][tid] = rn_cur; }
@@ -390,7 +396,8 @@ __global__ void __launch_bounds__(256, 2) knn_fused_kernel(KnnArgs a)
             mkey = fminf(mkey, METRIC == 0 ? fmaf(-2.f, acc_prev[r], pn + qn) : fmaf(-1.f, acc_prev[r], pn));
         }
         if (__ballot(mkey <= st.thr))
-            tile_append<DP, METRIC>(sm, a, acc_prev, ntiles - 1, w, lane, h, qlocal, qvalid, qn, st);
+            tile_append<METRIC>(sm.L, a, acc_prev, sm.tnorm[pb3], sm.trow[pb3], (ntiles - 1) * kPoolTile, w, lane,
+                                h, qlocal, qvalid, qn, st);
     }
 
     // flush the remaining buffers
@@ -399,7 +406,208 @@ __global__ void __launch_bounds__(256, 2) knn_fused_kernel(KnnArgs a)
     while (rem) {
         const int q = __ffsll(static_cast<unsigned long long>(rem)) - 1;
         rem &= rem - 1;
-        wave_merge<DP>(sm, a, w, lane, q, st);
+        wave_merge(sm.L, a, w, lane, q, st);
+    }
+    if (qvalid) {
+        for (int p = st.nL + h; p < a.M; p += 2) {
+            a.out_ids[st.orow * a.M + p] = -1;
+            a.out_d[st.orow * a.M + p] = INFINITY;
+        }
+    }
+}
+
+// ------------------------------------------------------------ wide rows
+//
+// Rows longer than 256 floats do not fit a wave's registers as a query
+// fragment.  The wide kernel accumulates a 32-query x 128-pool-row block per
+// wave over chunks of 32 dimensions instead: the pool chunk (128 rows x 32
+// dims) is staged through LDS and shared by the block's 4 waves, each wave
+// reads its 32 queries' chunk into registers, and the block's four 32x32
+// accumulator tiles are filtered once the last chunk is in.  Query rows are
+// re-read once per 128 pool rows (from L2 / Infinity Cache).
+__device__ __forceinline__ float4 keep_or_zero(bool keep, float4 v)
+{
+    return make_float4(keep ? v.x : 0.f, keep ? v.y : 0.f, keep ? v.z : 0.f, keep ? v.w : 0.f);
+}
+
+constexpr int kWideRows = 128;   // pool rows per super-tile
+constexpr int kWideChunk = 32;   // dimensions per chunk
+
+struct KnnWideSmem {
+    float tile[2][kWideRows][kWideChunk + 4];
+    float tnorm[2][kWideRows];
+    int32_t trow[2][kWideRows];
+    KnnLists L;
+};
+
+template <int METRIC>
+__global__ void __launch_bounds__(256, 2) knn_wide_kernel(KnnArgs a)
+{
+    __shared__ KnnWideSmem sm;
+    const int per = a.n_items / 8;
+    const int item_idx = static_cast<int>(blockIdx.x % 8) * per + static_cast<int>(blockIdx.x / 8);
+    if (item_idx >= a.n_items) return;
+    const WorkItem it = a.items[item_idx];
+    if (it.q_count <= 0) return;
+
+    const int Dp = a.Dp;
+    const int nch = Dp / kWideChunk;
+    const int tid = threadIdx.x;
+    const int w = tid >> 6, lane = tid & 63, j = lane & 31, h = lane >> 5;
+    const int qlocal = w * kQueriesPerWave + j;
+    const bool qvalid = qlocal < it.q_count;
+    const int64_t qi = it.q_begin + qlocal;
+    const int32_t qrow = qvalid ? (a.q_rows ? a.q_rows[qi] : static_cast<int32_t>(qi)) : 0;
+    const float qn = (qvalid && METRIC == 0) ? a.nq[qrow] : 0.f;
+
+    QueryState st;
+    st.seed = FLT_MAX;
+    if (qvalid && a.seed_d) st.seed = fminf(a.seed_d[static_cast<int64_t>(qrow) * a.seed_ld + a.seed_ld - 1], FLT_MAX);
+    st.thr = qvalid ? st.seed : -INFINITY;
+    st.cnt = 0;
+    st.nL = 0;
+    st.self = a.exclude_self ? qrow : -2;
+    st.orow = it.out_base >= 0 ? it.out_base + qlocal : static_cast<int64_t>(qrow);
+
+    const int pcount = it.p_count;
+    const int nst = (pcount + kWideRows - 1) / kWideRows;
+    auto pool_row = [&](int p) -> int32_t {
+        if (p >= pcount) return -1;
+        const int64_t pl = it.p_begin + p;
+        return a.p_rows ? a.p_rows[pl] : static_cast<int32_t>(pl);
+    };
+    auto row_norm = [&](int32_t row) -> float {
+        if (row < 0) return INFINITY;
+        return METRIC == 0 ? a.np[row] : 0.f;
+    };
+
+    // thread tid stages float4 (tid & 7) of super-tile rows (tid >> 3) + 32u
+    const int c4 = tid & 7, r0 = tid >> 3;
+    int32_t rid[4], rid_n[4];
+    float4 pre[4];
+    auto set_ids = [&](int stile, int32_t (&ids)[4]) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) ids[u] = stile < nst ? pool_row(stile * kWideRows + r0 + 32 * u) : -1;
+    };
+    // chunk c of the current super-tile's rows, or of the next one's
+    auto load_pool = [&](bool next, int c) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            // branch-free: rows past the slice read row 0 and are zeroed
+            const int32_t id = next ? rid_n[u] : rid[u];
+            const float4 v = *reinterpret_cast<const float4*>(a.Xp + static_cast<int64_t>(id >= 0 ? id : 0) * Dp +
+                                                              c * kWideChunk + 4 * c4);
+            pre[u] = keep_or_zero(id >= 0, v);
+        }
+    };
+    auto store_pool = [&](int buf) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) *reinterpret_cast<float4*>(&sm.tile[buf][r0 + 32 * u][4 * c4]) = pre[u];
+    };
+    // query chunk c: dims c*32 + h*16 + [0, 16)
+    const float* qsrc = a.Xq + static_cast<int64_t>(qrow) * Dp + h * (kWideChunk / 2);
+    float4 qc[4], qx[4];
+    auto load_q = [&](int c, float4 (&dst)[4]) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const float4 v = *reinterpret_cast<const float4*>(qsrc + c * kWideChunk + 4 * s);   // qrow 0 if invalid
+            dst[s] = keep_or_zero(qvalid, v);
+        }
+    };
+
+    set_ids(0, rid);
+    set_ids(1, rid_n);
+    if (tid < kWideRows) {
+        const int32_t r = pool_row(tid);
+        sm.trow[0][tid] = r;
+        sm.tnorm[0][tid] = row_norm(r);
+    }
+    load_pool(false, 0);
+    store_pool(0);
+    load_q(0, qc);
+    __syncthreads();
+
+    int g = 0;
+    for (int stile = 0; stile < nst; ++stile) {
+        floatx16 acc[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[u][r] = 0.f;
+        // ids and norms of the next super-tile's rows (read by its filter)
+        int32_t nrow = -1;
+        float nnrm = INFINITY;
+        if (tid < kWideRows && stile + 1 < nst) {
+            nrow = pool_row((stile + 1) * kWideRows + tid);
+            nnrm = row_norm(nrow);
+        }
+        for (int c = 0; c < nch; ++c) {
+            const int buf = g & 1;
+            const bool last = c + 1 == nch;
+            const bool more = !last || stile + 1 < nst;
+            if (more) load_pool(last, last ? 0 : c + 1);
+            load_q(last ? 0 : c + 1, qx);
+            // A = pool row u*32 + (lane%32), B = query lane%32, k = dims h*16 + s.
+            // Each chunk is summed on its own and added to the running dot:
+            // the rounding error grows with sqrt(chunks) instead of sqrt(D/2).
+            const float* arow = &sm.tile[buf][j][h * (kWideChunk / 2)];
+            floatx16 part[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) part[u][r] = 0.f;
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const float4 av = *reinterpret_cast<const float4*>(arow + u * 32 * (kWideChunk + 4) + 4 * s);
+                    part[u] = __builtin_amdgcn_mfma_f32_32x32x2f32(av.x, qc[s].x, part[u], 0, 0, 0);
+                    part[u] = __builtin_amdgcn_mfma_f32_32x32x2f32(av.y, qc[s].y, part[u], 0, 0, 0);
+                    part[u] = __builtin_amdgcn_mfma_f32_32x32x2f32(av.z, qc[s].z, part[u], 0, 0, 0);
+                    part[u] = __builtin_amdgcn_mfma_f32_32x32x2f32(av.w, qc[s].w, part[u], 0, 0, 0);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[u][r] += part[u][r];
+            if (more) store_pool(buf ^ 1);
+            __syncthreads();
+#pragma unroll
+            for (int s = 0; s < 4; ++s) qc[s] = qx[s];
+            ++g;
+        }
+        if (tid < kWideRows) {
+            sm.trow[(stile + 1) & 1][tid] = nrow;
+            sm.tnorm[(stile + 1) & 1][tid] = nnrm;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) rid[u] = rid_n[u];
+        set_ids(stile + 2, rid_n);
+
+        const int sb = stile & 1;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            wait_vmem();   // list rows stored by this wave's previous merges
+            float mkey = INFINITY;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int i = 8 * (r >> 2) + 4 * h + (r & 3);
+                const float pn = sm.tnorm[sb][u * 32 + i];
+                mkey = fminf(mkey, METRIC == 0 ? fmaf(-2.f, acc[u][r], pn + qn) : fmaf(-1.f, acc[u][r], pn));
+            }
+            if (__ballot(mkey <= st.thr))
+                tile_append<METRIC>(sm.L, a, acc[u], &sm.tnorm[sb][u * 32], &sm.trow[sb][u * 32],
+                                    stile * kWideRows + u * 32, w, lane, h, qlocal, qvalid, qn, st);
+        }
+    }
+
+    wait_vmem();
+    uint64_t rem = __ballot(qvalid && st.cnt > 0) & 0xffffffffull;
+    while (rem) {
+        const int q = __ffsll(static_cast<unsigned long long>(rem)) - 1;
+        rem &= rem - 1;
+        wave_merge(sm.L, a, w, lane, q, st);
     }
     if (qvalid) {
         for (int p = st.nL + h; p < a.M; p += 2) {
@@ -466,7 +674,10 @@ static void launch_knn_metric(const KnnArgs& a, dim3 grid, hipStream_t stream)
     case 192: hipLaunchKernelGGL((knn_fused_kernel<192, METRIC>), grid, dim3(256), 0, stream, a); break;
     case 224: hipLaunchKernelGGL((knn_fused_kernel<224, METRIC>), grid, dim3(256), 0, stream, a); break;
     case 256: hipLaunchKernelGGL((knn_fused_kernel<256, METRIC>), grid, dim3(256), 0, stream, a); break;
-    default: GT_REQUIRE(false, "padded dimension " + std::to_string(a.Dp) + " not supported (D <= 256)");
+    default:
+        GT_REQUIRE(a.Dp % kWideChunk == 0 && a.Dp > 256, "padded dimension " + std::to_string(a.Dp) + " not supported");
+        hipLaunchKernelGGL((knn_wide_kernel<METRIC>), grid, dim3(256), 0, stream, a);
+        break;
     }
 }
 

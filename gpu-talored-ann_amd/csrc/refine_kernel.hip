@@ -18,6 +18,7 @@ namespace gtann {
 constexpr int kRefineMaxCand = 1024;   // S*S
 constexpr int kRefineHash = 4096;      // >= 2 * (M + S*S)
 constexpr int kRefineMaxM = 128;
+constexpr int kMaxDp = 1024;           // longest padded row of this build
 
 __device__ __forceinline__ bool rkey_less(float da, int32_t ia, float db, int32_t ib)
 {
@@ -35,7 +36,7 @@ __global__ void __launch_bounds__(256) refine_2hop_kernel(const float* __restric
     __shared__ float cd[kRefineMaxCand];
     __shared__ int32_t row[kRefineMaxM];
     __shared__ float rowd[kRefineMaxM];
-    __shared__ float xa[256];
+    __shared__ float xa[kMaxDp];
     __shared__ int s_nc, s_ns, s_nr;
     const int64_t a = blockIdx.x;
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
@@ -147,9 +148,10 @@ __global__ void __launch_bounds__(256) refine_2hop_kernel(const float* __restric
 }
 
 // Lloyd update: centroid c = mean of its member rows; empty buckets keep
-// their centroid.  One block per centroid: thread t sums dimension t % Dp over
-// members t / Dp, t / Dp + parts, ... and the parts are added in a fixed
-// order, so the result does not depend on scheduling.
+// their centroid.  One block per centroid.  Dp <= 256: thread t sums
+// dimension t % Dp over members t / Dp, t / Dp + parts, ... and the parts are
+// added in a fixed order; Dp > 256: thread t sums dimensions t, t + 256, ...
+// over all members in order.  The result does not depend on scheduling.
 __global__ void __launch_bounds__(256) centroid_means_kernel(const float* __restrict__ X, int Dp,
                                                              const int32_t* __restrict__ members,
                                                              const int64_t* __restrict__ off, int64_t C,
@@ -160,6 +162,14 @@ __global__ void __launch_bounds__(256) centroid_means_kernel(const float* __rest
     if (c >= C) return;
     const int64_t lo = off[c], hi = off[c + 1];
     if (hi <= lo) return;
+    if (Dp > 256) {
+        for (int d = threadIdx.x; d < Dp; d += 256) {
+            float t = 0.f;
+            for (int64_t i = lo; i < hi; ++i) t += X[static_cast<int64_t>(members[i]) * Dp + d];
+            cent[c * Dp + d] = t / static_cast<float>(hi - lo);
+        }
+        return;
+    }
     const int parts = Dp <= 256 ? 256 / Dp : 1;
     const int d = threadIdx.x % Dp, pidx = threadIdx.x / Dp;
     float s = 0.f;
@@ -186,7 +196,7 @@ __global__ void __launch_bounds__(256) centroid_means_kernel(const float* __rest
 void launch_refine_2hop(const float* X, const float* norms, int64_t N, int Dp, int metric, const int32_t* in_ids,
                         const float* in_d, int M, int S, int32_t* out_ids, float* out_d, hipStream_t s)
 {
-    GT_REQUIRE(M <= kRefineMaxM && S * S <= kRefineMaxCand && Dp <= 256, "refine limits: M <= 128, S*S <= 1024");
+    GT_REQUIRE(M <= kRefineMaxM && S * S <= kRefineMaxCand && Dp <= kMaxDp, "refine limits: M <= 128, S*S <= 1024");
     if (N <= 0) return;
     hipLaunchKernelGGL(refine_2hop_kernel, dim3(static_cast<unsigned>(N)), dim3(256), 0, s, X, norms, N, Dp, metric,
                        in_ids, in_d, M, S, out_ids, out_d);

@@ -172,7 +172,7 @@ def test_invalid_arguments_raise(ctx):
     with pytest.raises(gtann.GtannError):
         ctx.knn_exact(X, 0)
     with pytest.raises(gtann.GtannError):
-        ctx.knn_exact(np.zeros((10, 300), np.float32), 4)   # D > 256 not supported yet
+        ctx.knn_exact(np.zeros((10, 1040), np.float32), 4)   # D > 1024 not supported
     off = np.array([0, 50], np.int64)   # does not cover all points
     with pytest.raises(gtann.GtannError):
         ctx.knn_bucketed(X, off, np.arange(100, dtype=np.int32), np.zeros((1, 0), np.int32), 8)
