@@ -88,7 +88,10 @@ def main():
     import synth
 
     cfg = synth.CONFIGS[args.config]
+    t0 = time.perf_counter()
     X, _ = synth.generate(args.config)
+    print(f"[bench] {args.config} generated {X.shape} {X.dtype} in {time.perf_counter() - t0:.1f} s",
+          file=sys.stderr, flush=True)
     N, D = X.shape
     Xd = torch.from_numpy(X).cuda()
     if args.copy_probe_mib:
@@ -106,6 +109,7 @@ def main():
     for _ in range(args.warmup):
         ctx.build_graph(Xd, **kw)
     torch.cuda.synchronize()
+    print("[bench] warmup done", file=sys.stderr, flush=True)
     stats = []
     t0 = time.perf_counter()
     for _ in range(args.steps):
@@ -163,7 +167,8 @@ def main():
         "stages_s": {k: s[k] for k in ("t_prepare", "t_bucketing", "t_knn", "t_merge", "t_refine", "t_prune",
                                        "t_revmerge", "t_download", "t_total")},
         "roofline": {
-            "kernel": "knn_fused_kernel<128> (one launch per round)",
+            "kernel": (f"knn_fused_kernel<{-(-D // 32) * 32}, {1 if cfg.metric == 'ip' else 0}>" if D <= 256 else
+                       f"knn_wide_kernel<{1 if cfg.metric == 'ip' else 0}>") + " (one launch per round)",
             "bound": "mfma", "achieved": achieved / 1e12, "peak": PEAK_FP32_MFMA / 1e12, "unit": "TFLOP/s",
             "frac": achieved / PEAK_FP32_MFMA, "traffic": None,
             "flops_per_launch": flops_launch, "launch_ms": knn_launch_s * 1e3,

@@ -9,9 +9,12 @@
 #include <algorithm>
 #include <chrono>
 #include <cmath>
+#include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <memory>
 #include <numeric>
+#include <thread>
 #include <unordered_set>
 #include <vector>
 
@@ -76,6 +79,31 @@ struct DevBuf {
     template <typename T> T* as(size_t n) { return static_cast<T*>(ensure(n * sizeof(T))); }
 };
 
+// Pinned host staging (hipHostMalloc), grown on demand and reused.
+struct HostBuf {
+    void* p = nullptr;
+    size_t cap = 0;
+    HostBuf() = default;
+    HostBuf(const HostBuf&) = delete;
+    HostBuf& operator=(const HostBuf&) = delete;
+    ~HostBuf() { release(); }
+    void release()
+    {
+        if (p) (void)hipHostFree(p);
+        p = nullptr;
+        cap = 0;
+    }
+    void* ensure(size_t bytes)
+    {
+        if (bytes <= cap) return p;
+        release();
+        GT_HIP(hipHostMalloc(&p, std::max<size_t>(bytes, 4096), hipHostMallocDefault));
+        cap = std::max<size_t>(bytes, 4096);
+        return p;
+    }
+    template <typename T> T* as(size_t n) { return static_cast<T*>(ensure(n * sizeof(T))); }
+};
+
 static bool is_device_ptr(const void* p)
 {
     if (!p) return false;
@@ -92,6 +120,26 @@ struct Timer {
     double sec() const { return std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count(); }
 };
 
+// Stage tracing: with GTANN_TRACE=1 in the environment every mark()
+// synchronises the stream and prints the wall time since the previous mark
+// to stderr.  Off (the default) it costs nothing and adds no synchronisation.
+struct Trace {
+    bool on = false;
+    Timer t;
+    Trace()
+    {
+        const char* e = std::getenv("GTANN_TRACE");
+        on = e && e[0] && e[0] != '0';
+    }
+    void mark(hipStream_t s, const char* what)
+    {
+        if (!on) return;
+        (void)hipStreamSynchronize(s);
+        std::fprintf(stderr, "[gtann] %-28s %9.3f ms\n", what, t.sec() * 1e3);
+        t = Timer();
+    }
+};
+
 }  // namespace gtann
 
 struct gt_ctx {
@@ -100,6 +148,7 @@ struct gt_ctx {
     std::string err;
     // named workspaces, grow-only (one slot per role, see gtann::Ws)
     gtann::DevBuf ws[40];
+    gtann::HostBuf pinned;   // top-2 assignment download
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
 };
 
@@ -318,15 +367,25 @@ static uint64_t splitmix64(uint64_t& x)
 // C distinct ids of [0, N), ascending (Floyd's sampling, seeded)
 static std::vector<int32_t> sample_ids(int64_t N, int64_t C, uint64_t seed)
 {
-    std::unordered_set<int64_t> chosen;
-    chosen.reserve(static_cast<size_t>(C) * 2);
+    // Floyd's sampling of C distinct ids of [0, N), membership in a bitmap
+    std::vector<uint64_t> bits(static_cast<size_t>((N + 63) / 64), 0);
+    auto test_set = [&](int64_t x) {
+        uint64_t& w = bits[static_cast<size_t>(x >> 6)];
+        const uint64_t m = 1ull << (x & 63);
+        const bool had = (w & m) != 0;
+        w |= m;
+        return had;
+    };
     uint64_t st = seed * 0x9E3779B97F4A7C15ull + 0x632BE59BD9B4E019ull;
     for (int64_t jj = N - C; jj < N; ++jj) {
         const int64_t t = static_cast<int64_t>(splitmix64(st) % static_cast<uint64_t>(jj + 1));
-        if (!chosen.insert(t).second) chosen.insert(jj);
+        if (test_set(t)) test_set(jj);
     }
-    std::vector<int32_t> ids(chosen.begin(), chosen.end());
-    std::sort(ids.begin(), ids.end());
+    std::vector<int32_t> ids;
+    ids.reserve(static_cast<size_t>(C));
+    for (size_t wi = 0; wi < bits.size(); ++wi)
+        for (uint64_t w = bits[wi]; w; w &= w - 1)
+            ids.push_back(static_cast<int32_t>(wi * 64 + static_cast<size_t>(__builtin_ctzll(w))));
     return ids;
 }
 
@@ -341,7 +400,7 @@ struct Buckets {
 // nearest centroid if that bucket is smaller than balance x the nearest
 // one's, sizes counted in point order.  Centroids that are data points sit
 // in their own bucket from the start.
-static void assign_two_choice(const std::vector<uint32_t>& top2, int64_t N, int64_t C, float balance,
+static void assign_two_choice(const uint32_t* top2, int64_t N, int64_t C, float balance,
                               const std::vector<int32_t>* centroid_ids, std::vector<int32_t>& bucket_of)
 {
     bucket_of.assign(static_cast<size_t>(N), -1);
@@ -366,17 +425,79 @@ static void assign_two_choice(const std::vector<uint32_t>& top2, int64_t N, int6
     }
 }
 
+// Runs f(t, lo, hi) over T contiguous slices of [0, n) on T threads.
+template <typename F>
+static void parallel_slices(int64_t n, int T, F&& f)
+{
+    if (T <= 1 || n < 65536) {
+        f(0, int64_t(0), n);
+        return;
+    }
+    std::vector<std::thread> th;
+    th.reserve(static_cast<size_t>(T));
+    for (int t = 0; t < T; ++t)
+        th.emplace_back([&, t] { f(t, n * t / T, n * (t + 1) / T); });
+    for (auto& x : th) x.join();
+}
+
+static int host_threads()
+{
+    const unsigned h = std::thread::hardware_concurrency();
+    return static_cast<int>(std::max(1u, std::min(16u, h)));
+}
+
+// Stable counting sort: out = in ordered by key[in[e]] (keys in [0, K)),
+// equal keys keep their order; off (K+1) receives the key offsets.  Each
+// thread counts and scatters its own slice, so the order is the serial one.
+static void counting_sort(const int32_t* in, int64_t n, const int32_t* key, int64_t K, int32_t* out,
+                          std::vector<int64_t>& off)
+{
+    const int T = n < 65536 ? 1 : host_threads();
+    std::vector<int64_t> cnt(static_cast<size_t>(T) * static_cast<size_t>(K), 0);
+    parallel_slices(n, T, [&](int t, int64_t lo, int64_t hi) {
+        int64_t* c = cnt.data() + static_cast<size_t>(t) * K;
+        for (int64_t e = lo; e < hi; ++e) c[key[in ? in[e] : e]]++;
+    });
+    off.assign(static_cast<size_t>(K + 1), 0);
+    int64_t run = 0;
+    for (int64_t k = 0; k < K; ++k) {
+        off[static_cast<size_t>(k)] = run;
+        for (int t = 0; t < T; ++t) {
+            int64_t& c = cnt[static_cast<size_t>(t) * K + k];
+            const int64_t v = c;
+            c = run;
+            run += v;
+        }
+    }
+    off[static_cast<size_t>(K)] = run;
+    parallel_slices(n, T, [&](int t, int64_t lo, int64_t hi) {
+        int64_t* c = cnt.data() + static_cast<size_t>(t) * K;
+        for (int64_t e = lo; e < hi; ++e) {
+            const int32_t v = in ? in[e] : static_cast<int32_t>(e);
+            out[c[key[v]]++] = v;
+        }
+    });
+}
+
+// CSR of an assignment with members ordered by (bucket, key2, id): two stable
+// counting sorts.  key2 = each point's other top-2 centroid, so that points
+// of one bucket near the same neighbouring bucket sit next to each other.
+static void csr_from_assignment_keyed(const std::vector<int32_t>& bucket_of, const std::vector<int32_t>& key2,
+                                      int64_t C, Buckets& b)
+{
+    const int64_t N = static_cast<int64_t>(bucket_of.size());
+    std::vector<int32_t> by_key(static_cast<size_t>(N));
+    std::vector<int64_t> off;
+    counting_sort(nullptr, N, key2.data(), C, by_key.data(), off);
+    b.members.resize(static_cast<size_t>(N));
+    counting_sort(by_key.data(), N, bucket_of.data(), C, b.members.data(), b.offsets);
+}
+
 static void csr_from_assignment(const std::vector<int32_t>& bucket_of, int64_t C, Buckets& b)
 {
     const int64_t N = static_cast<int64_t>(bucket_of.size());
-    b.offsets.assign(static_cast<size_t>(C + 1), 0);
-    for (int64_t i = 0; i < N; ++i) b.offsets[static_cast<size_t>(bucket_of[static_cast<size_t>(i)]) + 1]++;
-    for (int64_t c = 0; c < C; ++c) b.offsets[static_cast<size_t>(c + 1)] += b.offsets[static_cast<size_t>(c)];
-    std::vector<int64_t> cur(b.offsets.begin(), b.offsets.end() - 1);
     b.members.resize(static_cast<size_t>(N));
-    for (int64_t i = 0; i < N; ++i)
-        b.members[static_cast<size_t>(cur[static_cast<size_t>(bucket_of[static_cast<size_t>(i)])]++)] =
-            static_cast<int32_t>(i);
+    counting_sort(nullptr, N, bucket_of.data(), C, b.members.data(), b.offsets);
 }
 
 // One round of pooled kNN into (out_ids, out_d) rows by global id.
@@ -387,6 +508,7 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
 {
     const int64_t C = static_cast<int64_t>(b.offsets.size()) - 1;
     const int64_t N = X.N;
+    Trace tr;
     std::vector<CopyTaskH> tasks;
     std::vector<int64_t> pool_off(static_cast<size_t>(C + 1), 0);
     int64_t total = 0;
@@ -432,6 +554,9 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
             it.q_count = static_cast<int32_t>(std::min<int64_t>(kQueriesPerBlock, nqb - t));
             it.p_begin = p0;
             it.p_count = static_cast<int32_t>(npb);
+            // own bucket = first pool segment: start the scan at these queries'
+            // own rows (members are ordered so that neighbours sit close by)
+            it.p_rot = static_cast<int32_t>(t);
             it.out_base = -1;
             groups[static_cast<size_t>(bb)].push_back(it);
         }
@@ -441,6 +566,7 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
     WorkItem* d_items = c.ws<WorkItem>(W_ITEMS, items.size());
     c.h2d(d_items, items.data(), items.size() * sizeof(WorkItem));
 
+    tr.mark(c.s, "round: pools + work items");
     KnnArgs a{};
     a.Xq = X.data;
     a.Xp = X.data;
@@ -460,6 +586,7 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
     a.out_ids = out_ids;
     a.out_d = out_d;
     const double t = c.timed([&] { launch_knn_fused(a, c.s); });
+    tr.mark(c.s, "round: fused kNN");
     if (max_pool) *max_pool = std::max(*max_pool, mp);
     if (max_bucket) *max_bucket = std::max(*max_bucket, mb);
     if (pairs) *pairs += pr;
@@ -471,6 +598,7 @@ static void make_buckets(Ctx& c, const DevMatrix& X, int64_t C, int nprobe, int 
                          int kmeans_iters, uint64_t seed, Buckets& b)
 {
     const int64_t N = X.N;
+    Trace tr;
     C = std::max<int64_t>(1, std::min<int64_t>(C, N));
     std::vector<int32_t> cid = sample_ids(N, C, seed);
     int32_t* d_cid = c.ws<int32_t>(W_PROWS, static_cast<size_t>(C));
@@ -497,6 +625,7 @@ static void make_buckets(Ctx& c, const DevMatrix& X, int64_t C, int nprobe, int 
     launch_row_norms(d_cm, C, X.Dp, d_cn, c.s);
     Cm.data = d_cm;
     Cm.norms = d_cn;
+    tr.mark(c.s, "bucketing: sample centroids");
 
     // Lloyd iterations on a training subset (the reference's KMeans|| also
     // trains on a subset, src/bucket.cu:8857-8880): nearest centroid of every
@@ -535,11 +664,12 @@ static void make_buckets(Ctx& c, const DevMatrix& X, int64_t C, int nprobe, int 
             c.h2d(d_off, tmp.offsets.data(), static_cast<size_t>(C + 1) * sizeof(int64_t));
             launch_centroid_sums(X.data, X.Dp, d_mem, d_off, C, d_cm, c.s);
             launch_row_norms(d_cm, C, X.Dp, d_cn, c.s);
+            tr.mark(c.s, "bucketing: Lloyd iteration");
         }
     }
 
     // final assignment of every point: exact top-2 centroids + two-choice rule
-    std::vector<uint32_t> top2(static_cast<size_t>(2 * N), 0xffffffffu);
+    uint32_t* top2 = c.c->pinned.as<uint32_t>(static_cast<size_t>(2 * N));
     std::vector<int32_t> bucket_of;
     if (C >= 2) {
         int32_t* d_t2 = c.ws<int32_t>(W_IDS3, static_cast<size_t>(2 * N));
@@ -556,13 +686,31 @@ static void make_buckets(Ctx& c, const DevMatrix& X, int64_t C, int nprobe, int 
         j.out_ids = d_t2;
         j.out_d = d_t2d;
         run_knn_flat(c, j, 1);
-        c.d2h(top2.data(), d_t2, top2.size() * sizeof(uint32_t));
+        tr.mark(c.s, "bucketing: top-2 kNN");
+        c.d2h(top2, d_t2, static_cast<size_t>(2 * N) * sizeof(uint32_t));
         c.sync();
+        tr.mark(c.s, "bucketing: top-2 download");
     } else {
-        for (int64_t i = 0; i < N; ++i) top2[static_cast<size_t>(2 * i)] = 0u;
+        for (int64_t i = 0; i < N; ++i) {
+            top2[2 * i] = 0u;
+            top2[2 * i + 1] = 0xffffffffu;
+        }
     }
     assign_two_choice(top2, N, C, balance, data_points ? &cid : nullptr, bucket_of);
-    csr_from_assignment(bucket_of, C, b);
+    tr.mark(c.s, "bucketing: two-choice");
+    {
+        std::vector<int32_t> key2(static_cast<size_t>(N));
+        parallel_slices(N, host_threads(), [&](int, int64_t lo, int64_t hi) {
+            for (int64_t i = lo; i < hi; ++i) {
+                const uint32_t c1 = top2[static_cast<size_t>(2 * i)], c2 = top2[static_cast<size_t>(2 * i + 1)];
+                const uint32_t other = static_cast<int64_t>(c1) == bucket_of[static_cast<size_t>(i)] ? c2 : c1;
+                key2[static_cast<size_t>(i)] = other < static_cast<uint64_t>(C) ? static_cast<int32_t>(other)
+                                                                                  : bucket_of[static_cast<size_t>(i)];
+            }
+        });
+        csr_from_assignment_keyed(bucket_of, key2, C, b);
+    }
+    tr.mark(c.s, "bucketing: CSR");
 
     // probe table: nprobe nearest other centroids
     b.P = static_cast<int>(std::min<int64_t>(nprobe, C - 1));
@@ -585,6 +733,7 @@ static void make_buckets(Ctx& c, const DevMatrix& X, int64_t C, int nprobe, int 
         c.d2h(b.probe.data(), d_pi, b.probe.size() * sizeof(int32_t));
         c.sync();
     }
+    tr.mark(c.s, "bucketing: probe table");
 }
 
 // ---------------------------------------------------------------- graph stages
@@ -710,6 +859,7 @@ void gt_destroy(gt_ctx* ctx)
         b.p = nullptr;
         b.cap = 0;
     }
+    ctx->pinned.release();
     if (ctx->ev0) (void)hipEventDestroy(ctx->ev0);
     if (ctx->ev1) (void)hipEventDestroy(ctx->ev1);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);

@@ -40,6 +40,7 @@ struct WorkItem {
     int64_t out_base;   // >= 0: output row of query q_begin (partial lists); < 0: row = query id
     int32_t q_count;
     int32_t p_count;
+    int32_t p_rot = 0;  // the scan visits pool positions p_rot, p_rot+1, ... (mod p_count)
 };
 
 constexpr int kQueriesPerWave = 32;

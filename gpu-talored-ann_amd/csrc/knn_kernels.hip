@@ -286,6 +286,8 @@ __global__ void __launch_bounds__(256, 2) knn_fused_kernel(KnnArgs a)
     const int ntiles = (pcount + kPoolTile - 1) / kPoolTile;
     auto pool_row = [&](int p) -> int32_t {
         if (p >= pcount) return -1;
+        p += it.p_rot;
+        if (p >= pcount) p -= pcount;
         const int64_t pl = it.p_begin + p;
         return a.p_rows ? a.p_rows[pl] : static_cast<int32_t>(pl);
     };
@@ -473,6 +475,8 @@ __global__ void __launch_bounds__(256, 2) knn_wide_kernel(KnnArgs a)
     const int nst = (pcount + kWideRows - 1) / kWideRows;
     auto pool_row = [&](int p) -> int32_t {
         if (p >= pcount) return -1;
+        p += it.p_rot;
+        if (p >= pcount) p -= pcount;
         const int64_t pl = it.p_begin + p;
         return a.p_rows ? a.p_rows[pl] : static_cast<int32_t>(pl);
     };
