@@ -502,9 +502,11 @@ static void csr_from_assignment(const std::vector<int32_t>& bucket_of, int64_t C
 
 // One round of pooled kNN into (out_ids, out_d) rows by global id.
 // seed_d (device, optional) caps kept keys at the running M-th distance.
+// own / probes select the pool segments: the bucket's own members and the
+// members of its probe buckets (both by default).
 static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M, int metric, const float* seed_d,
                              int32_t* out_ids, float* out_d, int64_t* max_pool, int64_t* max_bucket,
-                             double* pairs)
+                             double* pairs, bool own = true, bool probes = true)
 {
     const int64_t C = static_cast<int64_t>(b.offsets.size()) - 1;
     const int64_t N = X.N;
@@ -516,10 +518,10 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
     for (int64_t bb = 0; bb < C; ++bb) {
         pool_off[static_cast<size_t>(bb)] = total;
         segs.clear();
-        segs.push_back(bb);
-        for (int p = 0; p < b.P; ++p) {
+        if (own) segs.push_back(bb);
+        for (int p = 0; probes && p < b.P; ++p) {
             const int64_t pb = b.probe[static_cast<size_t>(bb * b.P + p)];
-            if (pb < 0 || pb >= C) continue;
+            if (pb < 0 || pb >= C || pb == bb) continue;
             if (std::find(segs.begin(), segs.end(), pb) != segs.end()) continue;
             segs.push_back(pb);
         }
@@ -556,7 +558,7 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
             it.p_count = static_cast<int32_t>(npb);
             // own bucket = first pool segment: start the scan at these queries'
             // own rows (members are ordered so that neighbours sit close by)
-            it.p_rot = static_cast<int32_t>(t);
+            it.p_rot = own && npb > 0 ? static_cast<int32_t>(t) : 0;
             it.out_base = -1;
             groups[static_cast<size_t>(bb)].push_back(it);
         }
@@ -1239,6 +1241,17 @@ int gt_build_graph(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtype, 
                     std::swap(run_i, tmp_i);
                     std::swap(run_d, tmp_d);
                 }
+            } else if (r == 0 && b.P > 0) {
+                // the own buckets unseeded, then the probe buckets seeded with
+                // that table's M-th distance, merged (disjoint candidate sets:
+                // the same table as one pass over the whole pools)
+                st.t_knn += bucketed_round(c, Xm, b, p.M, p.metric, nullptr, run_i, run_d, &st.max_pool,
+                                           &st.max_bucket, &st.knn_pairs, true, false);
+                st.t_knn += bucketed_round(c, Xm, b, p.M, p.metric, run_d, cur_i, cur_d, &st.max_pool,
+                                           &st.max_bucket, &st.knn_pairs, false, true);
+                st.t_merge += c.timed([&] { launch_merge_rounds(run_i, run_d, cur_i, cur_d, N, p.M, tmp_i, tmp_d, c.s); });
+                std::swap(run_i, tmp_i);
+                std::swap(run_d, tmp_d);
             } else if (r == 0) {
                 st.t_knn += bucketed_round(c, Xm, b, p.M, p.metric, nullptr, run_i, run_d, &st.max_pool,
                                            &st.max_bucket, &st.knn_pairs);

@@ -31,17 +31,6 @@ __device__ __forceinline__ bool key_less(float da, int32_t ia, float db, int32_t
     return da < db || (da == db && ia < ib);
 }
 
-__device__ __forceinline__ int lower_bound_u64(const uint64_t* a, int n, uint64_t k)
-{
-    int lo = 0, hi = n;
-    while (lo < hi) {
-        const int mid = (lo + hi) >> 1;
-        if (a[mid] < k) lo = mid + 1;
-        else hi = mid;
-    }
-    return lo;
-}
-
 // number of entries of the sorted (d, i) array [0, n) that are < (kd, ki)
 __device__ __forceinline__ int lower_bound_lds(const float* ad, const int32_t* ai, int n, float kd, int32_t ki)
 {
@@ -73,11 +62,10 @@ __device__ __forceinline__ void wave_bitonic_sort(float& d, int32_t& i, int lane
     }
 }
 
-// Per-block candidate buffers and merge scratch, shared by both kernels.
+// Per-block candidate buffers and merge staging, shared by both kernels.
 struct KnnLists {
-    uint64_t buf[kQueriesPerBlock][kCB];  // packed (key, id) of candidates awaiting a merge
-    uint64_t sL[kWaves][kMaxM];           // the merging query's list, packed
-    float sthr[kWaves];
+    uint64_t buf[kQueriesPerBlock][kCB];  // packed (key, id) of candidates awaiting a merge (never the query itself)
+    uint64_t lst[kWaves][kMaxM];          // the merging query's list, packed
 };
 
 template <int DP>
@@ -104,81 +92,154 @@ struct QueryState {
 // query, which always comes after one of these waits (tile start, flush).
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }   // vmcnt(0)
 
-// List rows are read from L2 (agent scope), never from a possibly stale L1 line.
+// A list row is only ever stored and loaded by the one wave that owns its
+// query, on one CU: workgroup-scope loads see those stores once they have
+// completed (the vmcnt(0) waits above), and being atomic they are never
+// folded with an earlier load of the same row by the compiler.
 __device__ __forceinline__ float load_list_d(const float* p)
 {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 __device__ __forceinline__ int32_t load_list_i(const int32_t* p)
 {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
 // Merges the buffer of query q (0..31 of this wave) into its sorted list
-// (output row), dropping the query's own id, and recomputes its threshold.
-// Positions come from rank counting: a buffer entry's position is its rank
-// among the buffer plus the number of list entries before it; a list entry's
-// position is its index plus the number of buffer entries before it.
-// Called by all 64 lanes.
+// (output row) and recomputes its threshold.  Positions come from rank
+// counting: a buffer entry's position is its rank among the buffer plus the
+// number of list entries below it; a list entry's position is its index plus
+// the number of buffer entries below it.  Every count is split between the
+// two half-waves (lanes l and l + 32 both hold buffer entry l) over 128-bit
+// LDS broadcast reads and finished with one shuffle, so no step waits on a
+// chain of round trips; the list loads are issued first and land while the
+// buffer is ranked.  Called by all 64 lanes.
 __device__ void wave_merge(KnnLists& sm, const KnnArgs& a, int w, int lane, int q, QueryState& st)
 {
-    const int nB = __shfl(st.cnt, q);
-    const int nL = __shfl(st.nL, q);
-    const int32_t self = __shfl(st.self, q);
-    const int64_t orow = __shfl(st.orow, q);
+    // query q's state, uniform across the wave (scalar registers)
+    const int nB = __builtin_amdgcn_readlane(st.cnt, q);
+    const int nL = __builtin_amdgcn_readlane(st.nL, q);
+    const int64_t orow = static_cast<int64_t>(
+        (static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(st.orow >> 32), q))) << 32) |
+        static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(st.orow), q)));
     const int M = a.M;
-    const int ql = w * kQueriesPerWave + q;
-    uint64_t* B = sm.buf[ql];
+    const int h = lane >> 5;
+    uint64_t* B = sm.buf[w * kQueriesPerWave + q];
+    uint64_t* L = sm.lst[w];
 
-    uint64_t lk[2];
+    float ld0 = 0.f, ld1 = 0.f;
+    int32_t li0 = 0, li1 = 0;
+    if (lane < nL) {
+        ld0 = load_list_d(a.out_d + orow * M + lane);
+        li0 = load_list_i(a.out_ids + orow * M + lane);
+    }
+    if (lane + 64 < nL) {
+        ld1 = load_list_d(a.out_d + orow * M + lane + 64);
+        li1 = load_list_i(a.out_ids + orow * M + lane + 64);
+    }
+
+    // buffer slots past nB hold kNoKey (never below a key)
+    const int bl = lane & 31;
+    const uint64_t bk = B[bl];
+    auto key_at = [](const uint4& x, int odd) -> uint64_t {
+        return odd ? (static_cast<uint64_t>(x.w) << 32) | x.z : (static_cast<uint64_t>(x.y) << 32) | x.x;
+    };
+    // rank of buffer entry bl among the buffer: half h counts entries [16h, 16h + 16)
+    int rb = 0;
+    {
+        const uint4* B4 = reinterpret_cast<const uint4*>(B + 16 * h);
+#pragma unroll 4
+        for (int e = 0; e < 8; ++e) {
+            const uint4 x = B4[e];
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
-        const int idx = lane + 64 * e;
-        lk[e] = kNoKey;
-        if (idx < nL)
-            lk[e] = pack_key(load_list_d(a.out_d + orow * M + idx), load_list_i(a.out_ids + orow * M + idx));
-        if (idx < kMaxM) sm.sL[w][idx] = lk[e];
+            for (int o = 0; o < 2; ++o) rb += key_at(x, o) < bk ? 1 : 0;
+        }
     }
-    // the query's own id never enters the list
-    if (lane < nB && static_cast<int32_t>(static_cast<uint32_t>(B[lane])) == self) B[lane] = kNoKey;
-    wave_sync();
+    rb += __shfl_xor(rb, 32);
 
-    const uint64_t bk = lane < nB ? B[lane] : kNoKey;
-    int rb = 0;              // rank of this lane's buffer entry among the buffer
-    int cl0 = 0, cl1 = 0;    // buffer entries before list entries lane, lane+64
-    for (int k = 0; k < nB; ++k) {
-        const uint64_t v = B[k];
-        rb += v < bk;
-        cl0 += v < lk[0];
-        cl1 += v < lk[1];
+    // buffer entries below list entries lane, lane + 64
+    const uint64_t lk0 = lane < nL ? pack_key(ld0, li0) : kNoKey;
+    const uint64_t lk1 = lane + 64 < nL ? pack_key(ld1, li1) : kNoKey;
+    int cl0 = 0, cl1 = 0;
+    {
+        const uint4* B4 = reinterpret_cast<const uint4*>(B);
+        if (nL > 64) {
+#pragma unroll 4
+            for (int e = 0; e < kCB / 2; ++e) {
+                const uint4 x = B4[e];
+#pragma unroll
+                for (int o = 0; o < 2; ++o) {
+                    const uint64_t v = key_at(x, o);
+                    cl0 += v < lk0 ? 1 : 0;
+                    cl1 += v < lk1 ? 1 : 0;
+                }
+            }
+        } else {
+#pragma unroll 4
+            for (int e = 0; e < kCB / 2; ++e) {
+                const uint4 x = B4[e];
+                cl0 += key_at(x, 0) < lk0 ? 1 : 0;
+                cl1 += key_at(x, 1) < lk0 ? 1 : 0;
+            }
+            cl0 += cl1;
+        }
     }
-    const bool bvalid = bk != kNoKey;
+
+    // list entries below buffer entry bl: the list goes through LDS (padding
+    // entries are kNoKey, never below a key); half h counts entries
+    // [32h, 32h + 32) and, for lists longer than 64, [64 + 32h, 96 + 32h)
+    L[lane] = lk0;
+    if (nL > 64) L[lane + 64] = lk1;
+    wave_sync();
+    int nlb = 0;
+    for (int part = 0; part < (nL > 64 ? 2 : 1); ++part) {
+        const uint4* L4 = reinterpret_cast<const uint4*>(L + 64 * part + 32 * h);
+#pragma unroll 4
+        for (int e = 0; e < 16; ++e) {
+            const uint4 x = L4[e];
+            nlb += key_at(x, 0) < bk ? 1 : 0;
+            nlb += key_at(x, 1) < bk ? 1 : 0;
+        }
+    }
+    nlb += __shfl_xor(nlb, 32);
+    if (h == 0) B[bl] = kNoKey;   // the buffer starts over empty
+
+    const bool bvalid = h == 0 && bk != kNoKey;
     const int nBv = static_cast<int>(__popcll(__ballot(bvalid)));
     const int total = nL + nBv;
+    bool last = false;   // this lane wrote position M-1
+    float dlast = 0.f;
     if (bvalid) {
-        const int pos = rb + lower_bound_u64(sm.sL[w], nL, bk);
+        const int pos = rb + nlb;
         if (pos < M) {
             const float d = o2f(static_cast<uint32_t>(bk >> 32));
             a.out_d[orow * M + pos] = d;
             a.out_ids[orow * M + pos] = static_cast<int32_t>(static_cast<uint32_t>(bk));
-            if (pos == M - 1) sm.sthr[w] = d;
+            if (pos == M - 1) { last = true; dlast = d; }
         }
     }
-#pragma unroll
-    for (int e = 0; e < 2; ++e) {
-        const int idx = lane + 64 * e;
-        if (idx < nL) {
-            const int pos = idx + (e == 0 ? cl0 : cl1);
-            if (pos < M) {
-                const float d = o2f(static_cast<uint32_t>(lk[e] >> 32));
-                a.out_d[orow * M + pos] = d;
-                a.out_ids[orow * M + pos] = static_cast<int32_t>(static_cast<uint32_t>(lk[e]));
-                if (pos == M - 1) sm.sthr[w] = d;
-            }
+    if (lane < nL) {
+        const int pos = lane + cl0;
+        if (pos < M) {
+            a.out_d[orow * M + pos] = ld0;
+            a.out_ids[orow * M + pos] = li0;
+            if (pos == M - 1) { last = true; dlast = ld0; }
         }
     }
-    wave_sync();
-    const float mth = sm.sthr[w];
+    if (lane + 64 < nL) {
+        const int pos = lane + 64 + cl1;
+        if (pos < M) {
+            a.out_d[orow * M + pos] = ld1;
+            a.out_ids[orow * M + pos] = li1;
+            if (pos == M - 1) { last = true; dlast = ld1; }
+        }
+    }
+    const uint64_t lastmask = __ballot(last);
+    float mth = FLT_MAX;
+    if (lastmask) {
+        const int src = static_cast<int>(__ffsll(static_cast<unsigned long long>(lastmask))) - 1;
+        mth = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dlast), src));
+    }
     const int newn = total < M ? total : M;
     if ((lane & 31) == q) {
         st.cnt = 0;
@@ -192,19 +253,32 @@ __device__ void wave_merge(KnnLists& sm, const KnnArgs& a, int w, int lane, int 
 // path taken only when some lane of the wave has a candidate <= its threshold.
 template <int METRIC>
 __device__ __forceinline__ void tile_append(KnnLists& sm, const KnnArgs& a, const floatx16& acc, const float* tn,
-                            const int32_t* tr, int tbase, int w, int lane, int h, int qlocal, bool qvalid, float qn,
-                            QueryState& st)
+                                            const int32_t* tr, int tbase, int w, int lane, int h, int qlocal,
+                                            bool qvalid, float qn, QueryState& st)
 {
+    // rows 8g + 4h + e of the tile, e = 0..3: norms and ids as 128-bit reads
     float dv[16];
+    int32_t idv[16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const int i = 8 * (r >> 2) + 4 * h + (r & 3);
-        const float pn = tn[i];
-        dv[r] = METRIC == 0 ? fmaf(-2.f, acc[r], pn + qn) : fmaf(-1.f, acc[r], pn);
+    for (int g = 0; g < 4; ++g) {
+        const float4 pn = *reinterpret_cast<const float4*>(tn + 8 * g + 4 * h);
+        const int4 pi = *reinterpret_cast<const int4*>(tr + 8 * g + 4 * h);
+        const float n4[4] = {pn.x, pn.y, pn.z, pn.w};
+        const int32_t i4[4] = {pi.x, pi.y, pi.z, pi.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int r = 4 * g + e;
+            dv[r] = METRIC == 0 ? fmaf(-2.f, acc[r], n4[e] + qn) : fmaf(-1.f, acc[r], n4[e]);
+            idv[r] = a.out_pos ? tbase + 8 * g + 4 * h + e : i4[e];
+        }
     }
+    uint32_t keep = 0;   // rows that may enter the list: not the query itself
+#pragma unroll
+    for (int r = 0; r < 16; ++r) keep |= static_cast<uint32_t>(idv[r] != st.self) << r;
     uint32_t pass = 0;
 #pragma unroll
     for (int r = 0; r < 16; ++r) pass |= static_cast<uint32_t>(dv[r] <= st.thr) << r;
+    pass &= keep;
     int np_ = __popc(pass);
     int np_o = __shfl_xor(np_, 32);
     const bool need = qvalid && (st.cnt + np_ + np_o > kCB);
@@ -218,20 +292,17 @@ __device__ __forceinline__ void tile_append(KnnLists& sm, const KnnArgs& a, cons
         pass = 0;
 #pragma unroll
         for (int r = 0; r < 16; ++r) pass |= static_cast<uint32_t>(dv[r] <= st.thr) << r;
+        pass &= keep;
         np_ = __popc(pass);
         np_o = __shfl_xor(np_, 32);
     }
     if (qvalid) {
-        int off = st.cnt + (h ? np_o : 0);
+        // half 0 fills slots [cnt, cnt + np_), half 1 the next np_o
+        const int base = st.cnt + (h ? np_o : 0);
+        uint64_t* row = sm.buf[qlocal];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            if ((pass >> r) & 1u) {
-                const int i = 8 * (r >> 2) + 4 * h + (r & 3);
-                const int32_t id = a.out_pos ? tbase + i : tr[i];
-                sm.buf[qlocal][off] = pack_key(dv[r], id);
-                ++off;
-            }
-        }
+        for (int r = 0; r < 16; ++r)
+            if ((pass >> r) & 1u) row[base + __popc(pass & ((1u << r) - 1u))] = pack_key(dv[r], idv[r]);
         st.cnt += np_ + np_o;
     }
 }
@@ -270,6 +341,8 @@ __global__ void __launch_bounds__(256, 2) knn_fused_kernel(KnnArgs a)
     st.nL = 0;
     st.self = a.exclude_self ? qrow : -2;
     st.orow = it.out_base >= 0 ? it.out_base + qlocal : static_cast<int64_t>(qrow);
+    // this wave's 32 buffer rows start empty: every slot holds kNoKey
+    for (int e = lane; e < kQueriesPerWave * kCB; e += 64) sm.L.buf[w * kQueriesPerWave + e / kCB][e % kCB] = kNoKey;
 
     // query fragment: dims [h*DH, h*DH + DH) of query row qrow
     float qf[DH];
@@ -470,6 +543,8 @@ __global__ void __launch_bounds__(256, 2) knn_wide_kernel(KnnArgs a)
     st.nL = 0;
     st.self = a.exclude_self ? qrow : -2;
     st.orow = it.out_base >= 0 ? it.out_base + qlocal : static_cast<int64_t>(qrow);
+    // this wave's 32 buffer rows start empty: every slot holds kNoKey
+    for (int e = lane; e < kQueriesPerWave * kCB; e += 64) sm.L.buf[w * kQueriesPerWave + e / kCB][e % kCB] = kNoKey;
 
     const int pcount = it.p_count;
     const int nst = (pcount + kWideRows - 1) / kWideRows;
