@@ -64,7 +64,10 @@ __device__ __forceinline__ void wave_bitonic_sort(float& d, int32_t& i, int lane
 
 // Per-block candidate buffers and merge staging, shared by both kernels.
 struct KnnLists {
-    uint64_t buf[kQueriesPerBlock][kCB];  // packed (key, id) of candidates awaiting a merge (never the query itself)
+    // packed (key, id) of candidates awaiting a merge (never the query
+    // itself); slot kCB takes the writes of rows that did not pass (branch-free
+    // appends) and is never read
+    uint64_t buf[kQueriesPerBlock][kCB + 2];
     uint64_t lst[kWaves][kMaxM];          // the merging query's list, packed
 };
 
@@ -297,12 +300,15 @@ __device__ __forceinline__ void tile_append(KnnLists& sm, const KnnArgs& a, cons
         np_o = __shfl_xor(np_, 32);
     }
     if (qvalid) {
-        // half 0 fills slots [cnt, cnt + np_), half 1 the next np_o
+        // half 0 fills slots [cnt, cnt + np_), half 1 the next np_o; rows that
+        // did not pass go to the spare slot kCB
         const int base = st.cnt + (h ? np_o : 0);
         uint64_t* row = sm.buf[qlocal];
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-            if ((pass >> r) & 1u) row[base + __popc(pass & ((1u << r) - 1u))] = pack_key(dv[r], idv[r]);
+        for (int r = 0; r < 16; ++r) {
+            const int slot = ((pass >> r) & 1u) ? base + __popc(pass & ((1u << r) - 1u)) : kCB;
+            row[slot] = pack_key(dv[r], idv[r]);
+        }
         st.cnt += np_ + np_o;
     }
 }
