@@ -105,104 +105,129 @@ __global__ void __launch_bounds__(256) sanitize_kernel(const int32_t* __restrict
 // (src/prune_windowed_core.hpp:189-232); output = first K valid entries in
 // (count, rank) order (src/prune_windowed_core.hpp:238-263).
 constexpr int kPruneMaxM = 128;
-constexpr int kPruneCap = 256;   // open-addressing slots, >= 2*M
+constexpr int kPruneDepth = 16;   // neighbour rows in flight per wave
 
+// One wave per point a.  Row a goes into an LDS rank table (open addressing,
+// entry = id << 32 | rank; a repeated id keeps one entry per occurrence);
+// then every neighbour row kAD < M-1 is streamed through, kPruneDepth rows in
+// flight, and each of its ids is looked up: a hit at rank kAB > kAD counts
+// once per (kAD, kAB) pair (stamp) -- src/prune_windowed_core.hpp:177-232.
+// Finally the first K valid ranks by (count, rank) are written
+// (src/prune_windowed_core.hpp:234-263).  E = list halves of 64, CAP = table slots.
+template <int E, int CAP>
 __global__ void __launch_bounds__(256) cagra_prune_kernel(const int32_t* __restrict__ G, int64_t N, int M, int K,
                                                           uint32_t* __restrict__ out,
                                                           unsigned long long* __restrict__ bad_row)
 {
-    __shared__ int32_t hkey[4][kPruneCap];
-    __shared__ int32_t hrank[4][kPruneCap];
-    __shared__ int32_t stamp[4][kPruneMaxM];
-    __shared__ uint32_t cnt[4][kPruneMaxM];
-    __shared__ int32_t sA[4][kPruneMaxM];
+    constexpr int MM = 64 * E;
+    constexpr uint32_t mask = CAP - 1;
+    __shared__ uint64_t tab[4][CAP];
+    __shared__ int32_t stamp[4][MM];
+    __shared__ uint32_t cnt[4][MM];
+    __shared__ int32_t sA[4][MM];
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int64_t a = static_cast<int64_t>(blockIdx.x) * 4 + w;
     if (a >= N) return;
 
-    uint32_t cap = 16;
-    while (cap < 2u * static_cast<uint32_t>(M)) cap <<= 1;
-    const uint32_t mask = cap - 1;
-    for (uint32_t s = lane; s < cap; s += 64) hkey[w][s] = -1;
-    int32_t A[2];
+    for (int s = lane; s < CAP; s += 64) tab[w][s] = kNoKey;
+    int32_t A[E];
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
+    for (int e = 0; e < E; ++e) {
         const int k = lane + 64 * e;
         A[e] = k < M ? G[a * M + k] : -1;
-        if (k < M) { stamp[w][k] = -1; cnt[w][k] = 0; sA[w][k] = A[e]; }
+        stamp[w][k] = -1;
+        cnt[w][k] = 0;
+        sA[w][k] = A[e];
     }
     wave_sync();
+    // linear probing; every entry ends up at most dmax slots past its home
+    uint32_t disp = 0;
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
+    for (int e = 0; e < E; ++e) {
         const int k = lane + 64 * e;
-        if (k < M && A[e] >= 0) {
-            uint32_t h = (static_cast<uint32_t>(A[e]) * 2654435761u) & mask;
-            while (true) {
-                const int32_t old = atomicCAS(&hkey[w][h], -1, A[e]);
-                if (old == -1) { hrank[w][h] = k; break; }
+        if (A[e] >= 0) {
+            const uint64_t entry = (static_cast<uint64_t>(static_cast<uint32_t>(A[e])) << 32) | static_cast<uint32_t>(k);
+            const uint32_t home = (static_cast<uint32_t>(A[e]) * 2654435761u) & mask;
+            uint32_t h = home;
+            while (atomicCAS(reinterpret_cast<unsigned long long*>(&tab[w][h]), kNoKey, entry) != kNoKey)
                 h = (h + 1) & mask;
-            }
+            disp = max(disp, (h - home) & mask);
         }
     }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) disp = max(disp, static_cast<uint32_t>(__shfl_xor(static_cast<int>(disp), o)));
+    const uint32_t dmax = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(disp)));
     wave_sync();
 
-    // detour sources: one neighbour row per step, kPruneDepth rows in flight
-    constexpr int kPruneDepth = 4;
-    int32_t ring[kPruneDepth][2];
-    auto fetch = [&](int kAD, int32_t (&b)[2]) {
+    // rows in flight: raw ids plus whether the row exists; the mask is
+    // applied when the row is probed, so no load is waited for early
+    int32_t ring[kPruneDepth][E];
+    bool rok[kPruneDepth];
+    auto fetch = [&](int kAD, int32_t (&b)[E], bool& ok) {
         const int32_t d = kAD < M - 1 ? sA[w][kAD] : -1;
-        const bool ok = d >= 0 && d < N;
+        ok = d >= 0 && d < N;
+        const int64_t row = ok ? static_cast<int64_t>(d) : 0;
 #pragma unroll
-        for (int e = 0; e < 2; ++e) {
+        for (int e = 0; e < E; ++e) {
             const int k = lane + 64 * e;
-            b[e] = (ok && k < M) ? G[static_cast<int64_t>(d) * M + k] : -1;
+            b[e] = G[row * M + (k < M ? k : M - 1)];
         }
     };
-    auto probe = [&](int kd, const int32_t (&b)[2]) {
+    // every occurrence of v in row a lies within dmax slots of v's home: a
+    // fixed, wave-uniform number of probes (no divergent loop exits)
+    auto probe = [&](int kd, const int32_t (&b)[E], bool ok) {
+        if (!ok) return;
 #pragma unroll
-        for (int e = 0; e < 2; ++e) {
+        for (int e = 0; e < E; ++e) {
             const int32_t v = b[e];
-            if (v < 0) continue;
-            for (uint32_t h = (static_cast<uint32_t>(v) * 2654435761u) & mask; hkey[w][h] != -1; h = (h + 1) & mask) {
-                if (hkey[w][h] != v) continue;
-                const int kab = hrank[w][h];
-                if (kab > kd && atomicExch(&stamp[w][kab], kd) != kd) atomicAdd(&cnt[w][kab], 1u);
+            const bool valid = lane + 64 * e < M && v >= 0;
+            const uint32_t home = (static_cast<uint32_t>(v) * 2654435761u) & mask;
+            for (uint32_t s = 0; s <= dmax; ++s) {
+                const uint64_t t = tab[w][(home + s) & mask];
+                const int kab = static_cast<int>(static_cast<uint32_t>(t));
+                if (valid && static_cast<uint32_t>(t >> 32) == static_cast<uint32_t>(v) && kab > kd &&
+                    atomicExch(&stamp[w][kab], kd) != kd)
+                    atomicAdd(&cnt[w][kab], 1u);
             }
         }
     };
 #pragma unroll
-    for (int r = 0; r < kPruneDepth; ++r) fetch(r, ring[r]);
+    for (int r = 0; r < kPruneDepth; ++r) fetch(r, ring[r], rok[r]);
     for (int kd = 0; kd < M - 1; kd += kPruneDepth) {
 #pragma unroll
         for (int r = 0; r < kPruneDepth; ++r) {
-            if (kd + r < M - 1) probe(kd + r, ring[r]);
-            fetch(kd + r + kPruneDepth, ring[r]);
+            if (kd + r < M - 1) probe(kd + r, ring[r], rok[r]);
+            fetch(kd + r + kPruneDepth, ring[r], rok[r]);
         }
     }
     wave_sync();
 
     int nvalid = 0;
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
-        const int k = lane + 64 * e;
-        nvalid += __popcll(__ballot(k < M && A[e] >= 0));
-    }
+    for (int e = 0; e < E; ++e) nvalid += __popcll(__ballot(A[e] >= 0));
     if (nvalid < K) {
         if (lane == 0) atomicMin(bad_row, static_cast<unsigned long long>(a));
         return;
     }
+    // position = valid entries before this one in (count, rank) order
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
+    for (int e = 0; e < E; ++e) {
         const int k = lane + 64 * e;
-        if (k < M && A[e] >= 0) {
-            const uint32_t c = cnt[w][k];
-            int pos = 0;
-            for (int q = 0; q < M; ++q) {
-                const uint32_t cq = cnt[w][q];
-                pos += (sA[w][q] >= 0) && (cq < c || (cq == c && q < k));
+        const uint32_t c = cnt[w][k];
+        int pos = 0;
+#pragma unroll 4
+        for (int q4 = 0; q4 < MM / 4; ++q4) {
+            const uint4 cq = *reinterpret_cast<const uint4*>(&cnt[w][4 * q4]);
+            const int4 aq = *reinterpret_cast<const int4*>(&sA[w][4 * q4]);
+            const uint32_t c4[4] = {cq.x, cq.y, cq.z, cq.w};
+            const int32_t a4[4] = {aq.x, aq.y, aq.z, aq.w};
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) {
+                const int q = 4 * q4 + jj;
+                pos += (a4[jj] >= 0 && (c4[jj] < c || (c4[jj] == c && q < k))) ? 1 : 0;
             }
-            if (pos < K) out[a * K + pos] = static_cast<uint32_t>(A[e]);
         }
+        if (A[e] >= 0 && pos < K) out[a * K + pos] = static_cast<uint32_t>(A[e]);
     }
 }
 
@@ -556,7 +581,10 @@ void launch_cagra_prune(const int32_t* G, int64_t N, int M, int K, uint32_t* out
 {
     GT_REQUIRE(M >= 1 && M <= kPruneMaxM, "prune supports intermediate degree <= 128");
     if (N <= 0) return;
-    hipLaunchKernelGGL(cagra_prune_kernel, dim3(grid_for(N, 4)), dim3(256), 0, s, G, N, M, K, out, bad_row);
+    if (M <= 64)
+        hipLaunchKernelGGL((cagra_prune_kernel<1, 512>), dim3(grid_for(N, 4)), dim3(256), 0, s, G, N, M, K, out, bad_row);
+    else
+        hipLaunchKernelGGL((cagra_prune_kernel<2, 512>), dim3(grid_for(N, 4)), dim3(256), 0, s, G, N, M, K, out, bad_row);
     GT_HIP(hipGetLastError());
 }
 
