@@ -350,7 +350,8 @@ __global__ void __launch_bounds__(256) rev_merge_kernel(const uint32_t* __restri
                                                         uint32_t* __restrict__ out)
 {
     __shared__ uint32_t sR[4][kRevMaxK];
-    __shared__ uint32_t sSrc[4][64];
+    __shared__ uint32_t sRow[4][kRevMaxK];
+    __shared__ unsigned long long sK[4][64];
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int64_t j = static_cast<int64_t>(blockIdx.x) * 4 + w;
     if (j >= N) return;
@@ -359,46 +360,53 @@ __global__ void __launch_bounds__(256) rev_merge_kernel(const uint32_t* __restri
     const uint32_t lo = off[j], hi = off[j + 1];
     const uint32_t n = hi - lo;
     const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    sRow[w][lane] = rowv;
     int nR = 0;
 
+    // s among the protected slots fwd[j][0..P) (LDS broadcast reads)
     auto protected_src = [&](uint32_t s) {
         bool p = false;
-        for (int q = 0; q < P; ++q) p |= (__shfl(rowv, q) == s);
+        for (int q4 = 0; q4 < (P + 3) / 4; ++q4) {
+            const uint4 x = *reinterpret_cast<const uint4*>(&sRow[w][4 * q4]);
+            p |= (4 * q4 + 0 < P && x.x == s) || (4 * q4 + 1 < P && x.y == s) || (4 * q4 + 2 < P && x.z == s) ||
+                 (4 * q4 + 3 < P && x.w == s);
+        }
         return p;
     };
 
     if (n <= 64) {
-        unsigned long long key = lane < static_cast<int>(n) ? keys[lo + lane] : ~0ull;
-        // bitonic sort ascending (keys are unique; sentinels equal)
-#pragma unroll
-        for (int k2 = 2; k2 <= 64; k2 <<= 1) {
-#pragma unroll
-            for (int s = k2 >> 1; s > 0; s >>= 1) {
-                const unsigned long long o = __shfl_xor(key, s);
-                const bool ascending = (lane & k2) == 0;
-                const bool lower = (lane & s) == 0;
-                const bool take = (lower == ascending) ? (o < key) : (o > key);
-                if (take) key = o;
-            }
-        }
-        const bool valid = key != ~0ull;
+        // R by counting: a source is kept if not protected and no smaller key
+        // has the same source; its position is the number of kept keys below it
+        const unsigned long long key = lane < static_cast<int>(n) ? keys[lo + lane] : ~0ull;
         const uint32_t src = static_cast<uint32_t>(key);
-        // cross-lane reads must run with every lane active: a ds_bpermute
-        // from an inactive lane does not return that lane's value
-        const bool prot = protected_src(src);
-        bool keep = valid && !prot;
-        sSrc[w][lane] = src;
+        sK[w][lane] = key;
         wave_sync();
         bool dup = false;
-        for (int l2 = 0; l2 < 64; ++l2) dup |= (l2 < lane) && sSrc[w][l2] == src && (l2 < static_cast<int>(n));
-        keep = keep && !dup;
-        const unsigned long long km = __ballot(keep);
-        const int r = __popcll(km & below);
-        if (keep && r < L) sR[w][r] = src;
-        nR = min(L, __popcll(km));
+#pragma unroll 4
+        for (int q2 = 0; q2 < 32; ++q2) {
+            const uint4 x = *reinterpret_cast<const uint4*>(&sK[w][2 * q2]);
+            const unsigned long long k0 = (static_cast<unsigned long long>(x.y) << 32) | x.x;
+            const unsigned long long k1 = (static_cast<unsigned long long>(x.w) << 32) | x.z;
+            dup |= (k0 < key && x.x == src) || (k1 < key && x.z == src);
+        }
+        const bool keep = key != ~0ull && !dup && !protected_src(src);
+        wave_sync();
+        sK[w][lane] = keep ? key : ~0ull;
+        wave_sync();
+        int pos = 0;
+#pragma unroll 4
+        for (int q2 = 0; q2 < 32; ++q2) {
+            const uint4 x = *reinterpret_cast<const uint4*>(&sK[w][2 * q2]);
+            const unsigned long long k0 = (static_cast<unsigned long long>(x.y) << 32) | x.x;
+            const unsigned long long k1 = (static_cast<unsigned long long>(x.w) << 32) | x.z;
+            pos += (k0 < key ? 1 : 0) + (k1 < key ? 1 : 0);
+        }
+        if (keep && pos < L) sR[w][pos] = src;
+        nR = min(L, static_cast<int>(__popcll(__ballot(keep))));
     } else {
         unsigned long long last = 0;
         bool first = true;
+        wave_sync();
         while (nR < L) {
             unsigned long long m = ~0ull;
             for (uint32_t e = lane; e < n; e += 64) {
@@ -428,10 +436,7 @@ __global__ void __launch_bounds__(256) rev_merge_kernel(const uint32_t* __restri
         bool inR = false;
         for (int q = 0; q < nR; ++q) inR |= (sR[w][q] == rowv);
         bool earlier = false;
-        for (int x = P; x < K; ++x) {
-            const uint32_t vx = __shfl(rowv, x);   // all lanes active (see above)
-            earlier |= (x < lane) && (vx == rowv);
-        }
+        for (int x = P; x < K; ++x) earlier |= (x < lane) && (sRow[w][x] == rowv);
         const bool consumed = inR && !earlier;
         const bool keepO = lane >= P && lane < K && !consumed;
         const unsigned long long km = __ballot(keepO);
