@@ -13,6 +13,9 @@
 #include <cstdlib>
 #include <cstring>
 #include <memory>
+#include <condition_variable>
+#include <functional>
+#include <mutex>
 #include <numeric>
 #include <thread>
 #include <unordered_set>
@@ -149,6 +152,9 @@ struct gt_ctx {
     // named workspaces, grow-only (one slot per role, see gtann::Ws)
     gtann::DevBuf ws[40];
     gtann::HostBuf pinned;   // top-2 assignment download
+    // host scratch of the bucketing, reused across calls (no page faults on
+    // fresh N-sized allocations every round)
+    std::vector<int32_t> h_bucket_of, h_key2, h_by_key, h_members;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
 };
 
@@ -403,7 +409,8 @@ struct Buckets {
 static void assign_two_choice(const uint32_t* top2, int64_t N, int64_t C, float balance,
                               const std::vector<int32_t>* centroid_ids, std::vector<int32_t>& bucket_of)
 {
-    bucket_of.assign(static_cast<size_t>(N), -1);
+    bucket_of.resize(static_cast<size_t>(N));
+    std::fill(bucket_of.begin(), bucket_of.end(), -1);
     std::vector<int64_t> size(static_cast<size_t>(C), 0);
     if (centroid_ids) {
         for (int64_t c = 0; c < C; ++c) {
@@ -425,7 +432,67 @@ static void assign_two_choice(const uint32_t* top2, int64_t N, int64_t C, float 
     }
 }
 
-// Runs f(t, lo, hi) over T contiguous slices of [0, n) on T threads.
+// Process-wide pool of host worker threads (created once, never torn down:
+// the threads only ever run host code).  run(T, f) calls f(t) for t in
+// [0, T), t = 0 on the caller, and returns when all have finished; parallel
+// regions of different callers are serialised.
+class HostPool {
+public:
+    static HostPool& get()
+    {
+        static HostPool* p = new HostPool();
+        return *p;
+    }
+    int size() const { return T_; }
+    template <typename F>
+    void run(int T, F&& f)
+    {
+        if (T <= 1) {
+            f(0);
+            return;
+        }
+        std::lock_guard<std::mutex> one(run_m_);
+        std::function<void(int)> job = [&](int t) { f(t); };
+        {
+            std::lock_guard<std::mutex> lk(m_);
+            job_ = &job;
+            ntask_ = T;
+            next_ = 1;
+            pending_ = T - 1;
+        }
+        cv_.notify_all();
+        f(0);
+        std::unique_lock<std::mutex> lk(m_);
+        done_.wait(lk, [&] { return pending_ == 0; });
+        job_ = nullptr;
+    }
+
+private:
+    HostPool() : T_(static_cast<int>(std::max(1u, std::min(16u, std::thread::hardware_concurrency()))))
+    {
+        for (int i = 1; i < T_; ++i) std::thread([this] { loop(); }).detach();
+    }
+    void loop()
+    {
+        std::unique_lock<std::mutex> lk(m_);
+        for (;;) {
+            cv_.wait(lk, [&] { return job_ != nullptr && next_ < ntask_; });
+            const int t = next_++;
+            std::function<void(int)>* job = job_;
+            lk.unlock();
+            (*job)(t);
+            lk.lock();
+            if (--pending_ == 0) done_.notify_all();
+        }
+    }
+    int T_;
+    std::mutex run_m_, m_;
+    std::condition_variable cv_, done_;
+    std::function<void(int)>* job_ = nullptr;
+    int ntask_ = 0, next_ = 0, pending_ = 0;
+};
+
+// Runs f(t, lo, hi) over T contiguous slices of [0, n).
 template <typename F>
 static void parallel_slices(int64_t n, int T, F&& f)
 {
@@ -433,18 +500,10 @@ static void parallel_slices(int64_t n, int T, F&& f)
         f(0, int64_t(0), n);
         return;
     }
-    std::vector<std::thread> th;
-    th.reserve(static_cast<size_t>(T));
-    for (int t = 0; t < T; ++t)
-        th.emplace_back([&, t] { f(t, n * t / T, n * (t + 1) / T); });
-    for (auto& x : th) x.join();
+    HostPool::get().run(T, [&](int t) { f(t, n * t / T, n * (t + 1) / T); });
 }
 
-static int host_threads()
-{
-    const unsigned h = std::thread::hardware_concurrency();
-    return static_cast<int>(std::max(1u, std::min(16u, h)));
-}
+static int host_threads() { return HostPool::get().size(); }
 
 // Stable counting sort: out = in ordered by key[in[e]] (keys in [0, K)),
 // equal keys keep their order; off (K+1) receives the key offsets.  Each
@@ -483,10 +542,10 @@ static void counting_sort(const int32_t* in, int64_t n, const int32_t* key, int6
 // counting sorts.  key2 = each point's other top-2 centroid, so that points
 // of one bucket near the same neighbouring bucket sit next to each other.
 static void csr_from_assignment_keyed(const std::vector<int32_t>& bucket_of, const std::vector<int32_t>& key2,
-                                      int64_t C, Buckets& b)
+                                      int64_t C, Buckets& b, std::vector<int32_t>& by_key)
 {
     const int64_t N = static_cast<int64_t>(bucket_of.size());
-    std::vector<int32_t> by_key(static_cast<size_t>(N));
+    by_key.resize(static_cast<size_t>(N));
     std::vector<int64_t> off;
     counting_sort(nullptr, N, key2.data(), C, by_key.data(), off);
     b.members.resize(static_cast<size_t>(N));
@@ -672,7 +731,7 @@ static void make_buckets(Ctx& c, const DevMatrix& X, int64_t C, int nprobe, int 
 
     // final assignment of every point: exact top-2 centroids + two-choice rule
     uint32_t* top2 = c.c->pinned.as<uint32_t>(static_cast<size_t>(2 * N));
-    std::vector<int32_t> bucket_of;
+    std::vector<int32_t>& bucket_of = c.c->h_bucket_of;
     if (C >= 2) {
         int32_t* d_t2 = c.ws<int32_t>(W_IDS3, static_cast<size_t>(2 * N));
         float* d_t2d = c.ws<float>(W_D3, static_cast<size_t>(2 * N));
@@ -701,7 +760,8 @@ static void make_buckets(Ctx& c, const DevMatrix& X, int64_t C, int nprobe, int 
     assign_two_choice(top2, N, C, balance, data_points ? &cid : nullptr, bucket_of);
     tr.mark(c.s, "bucketing: two-choice");
     {
-        std::vector<int32_t> key2(static_cast<size_t>(N));
+        std::vector<int32_t>& key2 = c.c->h_key2;
+        key2.resize(static_cast<size_t>(N));
         parallel_slices(N, host_threads(), [&](int, int64_t lo, int64_t hi) {
             for (int64_t i = lo; i < hi; ++i) {
                 const uint32_t c1 = top2[static_cast<size_t>(2 * i)], c2 = top2[static_cast<size_t>(2 * i + 1)];
@@ -710,7 +770,7 @@ static void make_buckets(Ctx& c, const DevMatrix& X, int64_t C, int nprobe, int 
                                                                                   : bucket_of[static_cast<size_t>(i)];
             }
         });
-        csr_from_assignment_keyed(bucket_of, key2, C, b);
+        csr_from_assignment_keyed(bucket_of, key2, C, b, c.c->h_by_key);
     }
     tr.mark(c.s, "bucketing: CSR");
 
@@ -1224,9 +1284,10 @@ int gt_build_graph(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtype, 
         float* cur_d = c.ws<float>(W_D, nm);
         int32_t* tmp_i = c.ws<int32_t>(W_IDS2, nm);
         float* tmp_d = c.ws<float>(W_D2, nm);
+        Buckets b;
+        b.members.swap(ctx->h_members);   // reuse the member list's host memory across builds
         for (int r = 0; r < p.rounds; ++r) {
             Timer tb;
-            Buckets b;
             make_buckets(c, Xm, C, nprobe, p.metric, p.balance, p.kmeans_iters, p.seed + static_cast<uint64_t>(r), b);
             st.t_bucketing += tb.sec();
             if (p.reverse_edges) {
@@ -1263,6 +1324,7 @@ int gt_build_graph(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtype, 
                 std::swap(run_d, tmp_d);
             }
         }
+        b.members.swap(ctx->h_members);
         if (p.refine_passes > 0) {
             GT_REQUIRE(p.refine_sample >= 1 && p.refine_sample <= p.M && p.refine_sample * p.refine_sample <= 1024,
                        "bad refine sample");
