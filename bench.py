@@ -2,10 +2,18 @@
 
 A step is one whole graph build -- 2 rounds of (centroids refined by 3 Lloyd
 iterations on a training subset -> probe table -> top-2 assignment -> fused
-MFMA kNN over all buckets -> cross-round merge),
-sanitize, CAGRA prune, reverse-edge merge -- of configuration C2
+MFMA kNN over every bucket's pool (own bucket + 1 probe bucket) -> cross-round
+merge), sanitize, CAGRA prune, reverse-edge merge -- of configuration C2
 (1,000,000 x 128 fp32 integer-valued points, L2, 256 buckets, M 64 -> K 32)
 with the dataset already resident in HBM.  Prints one JSON line.
+
+`roofline` is the fused kNN kernel of the rounds: achieved = the
+algorithmic flops of its launches (2*D per scanned (query, pool row) pair)
+over their summed duration, both measured by the library with HIP events on
+its stream.  `traffic` is read from profiles/knn_fused_C2_traffic.json, the
+rocprofv3 FETCH_SIZE/WRITE_SIZE measurement of the same launches (see
+profiles/knn_fused_C2_build.md for the commands), when the configuration is
+C2 with the default knobs.
 
     python bench.py [--gpus 1] [--steps 3] [--warmup 1] [--config C2]
 """
@@ -133,10 +141,16 @@ def main():
     }
 
     s = {k: float(np.mean([st[k] for st in stats])) for k in stats[0]}
-    launches = args.rounds
+    launches = max(1, int(round(s["knn_launches"])))
     knn_launch_s = s["t_knn"] / launches
     flops_launch = s["knn_flops"] / launches
     achieved = flops_launch / knn_launch_s
+    traffic = None
+    tfile = os.path.join(ROOT, "profiles", f"knn_fused_{args.config}_traffic.json")
+    default_knobs = (args.rounds, args.kmeans_iters, args.nprobe) == (2, 3, 1)
+    if default_knobs and os.path.exists(tfile):
+        with open(tfile) as f:
+            traffic = json.load(f).get("bytes_per_launch")
     prune_bytes = N * (4 * cfg.M + 4 * cfg.M * (cfg.M - 1) + 4 * cfg.K)
     merge_bytes = 28 * N * cfg.K
 
@@ -170,8 +184,8 @@ def main():
             "kernel": (f"knn_fused_kernel<{-(-D // 32) * 32}, {1 if cfg.metric == 'ip' else 0}>" if D <= 256 else
                        f"knn_wide_kernel<{1 if cfg.metric == 'ip' else 0}>") + " (one launch per round)",
             "bound": "mfma", "achieved": achieved / 1e12, "peak": PEAK_FP32_MFMA / 1e12, "unit": "TFLOP/s",
-            "frac": achieved / PEAK_FP32_MFMA, "traffic": None,
-            "flops_per_launch": flops_launch, "launch_ms": knn_launch_s * 1e3,
+            "frac": achieved / PEAK_FP32_MFMA, "traffic": traffic,
+            "flops_per_launch": flops_launch, "launch_ms": knn_launch_s * 1e3, "launches": launches,
         },
         "roofline_prune": {"bound": "hbm", "achieved": prune_bytes / s["t_prune"] / 1e9, "peak": 8000.0,
                            "unit": "GB/s", "frac": prune_bytes / s["t_prune"] / PEAK_HBM,

@@ -155,6 +155,7 @@ struct gt_ctx {
     // host scratch of the bucketing, reused across calls (no page faults on
     // fresh N-sized allocations every round)
     std::vector<int32_t> h_bucket_of, h_key2, h_by_key, h_members;
+    int64_t knn_launches = 0;   // bucketed-round launches of the current build
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
 };
 
@@ -647,6 +648,7 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
     a.out_ids = out_ids;
     a.out_d = out_d;
     const double t = c.timed([&] { launch_knn_fused(a, c.s); });
+    ++c.c->knn_launches;
     tr.mark(c.s, "round: fused kNN");
     if (max_pool) *max_pool = std::max(*max_pool, mp);
     if (max_bucket) *max_bucket = std::max(*max_bucket, mb);
@@ -1284,6 +1286,7 @@ int gt_build_graph(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtype, 
         float* cur_d = c.ws<float>(W_D, nm);
         int32_t* tmp_i = c.ws<int32_t>(W_IDS2, nm);
         float* tmp_d = c.ws<float>(W_D2, nm);
+        ctx->knn_launches = 0;
         Buckets b;
         b.members.swap(ctx->h_members);   // reuse the member list's host memory across builds
         for (int r = 0; r < p.rounds; ++r) {
@@ -1338,6 +1341,7 @@ int gt_build_graph(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtype, 
             }
         }
         st.knn_flops = 2.0 * D * st.knn_pairs;
+        st.knn_launches = ctx->knn_launches;
         // sanitize + prune + reverse merge
         uint32_t* fin = nullptr;
         if (graph) {

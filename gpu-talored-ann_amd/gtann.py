@@ -49,7 +49,7 @@ class BuildStats(C.Structure):
         ("t_total", C.c_double), ("t_prepare", C.c_double), ("t_bucketing", C.c_double), ("t_knn", C.c_double),
         ("t_merge", C.c_double), ("t_refine", C.c_double), ("t_prune", C.c_double), ("t_revmerge", C.c_double),
         ("t_download", C.c_double), ("knn_flops", C.c_double), ("knn_pairs", C.c_double),
-        ("max_pool", C.c_int64), ("max_bucket", C.c_int64),
+        ("max_pool", C.c_int64), ("max_bucket", C.c_int64), ("knn_launches", C.c_int64),
     ]
 
     def as_dict(self):

@@ -154,6 +154,7 @@ typedef struct gt_build_stats {
     double knn_pairs;       /* (query, pool) pairs scanned */
     int64_t max_pool;
     int64_t max_bucket;
+    int64_t knn_launches;   /* fused kNN launches of the rounds (knn_flops / t_knn cover these) */
 } gt_build_stats;
 
 void gt_build_params_default(gt_build_params* p);
