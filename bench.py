@@ -87,7 +87,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
-              f"(the bucketed build shards by bucket, see DESIGN.md, but no multi-GPU path exists)",
+              f"(the bucketed build would shard by bucket, but no multi-GPU path exists)",
               file=sys.stderr)
         sys.exit(2)
 
