@@ -42,6 +42,38 @@ __global__ void pad_convert_kernel(const T* __restrict__ src, float* __restrict_
     }
 }
 
+// int8 rows for the int8 MFMA kernel: uint8 inputs are shifted by -128 (L2
+// distances do not change under a common shift), int8 inputs copied; zero
+// padded to Dp bytes.
+template <typename T>
+__global__ void pad_i8_kernel(const T* __restrict__ src, int8_t* __restrict__ dst, int64_t N, int D, int Dp, int shift)
+{
+    const int64_t total = N * Dp;
+    for (int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < total;
+         e += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int64_t r = e / Dp;
+        const int c = static_cast<int>(e - r * Dp);
+        dst[e] = c < D ? static_cast<int8_t>(static_cast<int>(src[r * D + c]) - shift) : int8_t(0);
+    }
+}
+
+// |x|^2 of int8 rows (exact integer sums), one wave per row
+__global__ void __launch_bounds__(256) row_norms_i8_kernel(const int8_t* __restrict__ X, int64_t N, int Dp,
+                                                           float* __restrict__ norms)
+{
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= N) return;
+    int s = 0;
+    for (int c = lane; c < Dp; c += 64) {
+        const int v = X[row * Dp + c];
+        s += v * v;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+    if (lane == 0) norms[row] = static_cast<float>(s);
+}
+
 // |x|^2 per row, one wave per row; summed in a fixed order.
 __global__ void __launch_bounds__(256) row_norms_kernel(const float* __restrict__ X, int64_t N, int Dp,
                                                         float* __restrict__ norms)
@@ -549,6 +581,25 @@ void launch_pad_convert(const void* src, int dtype, float* dst, int64_t N, int D
         hipLaunchKernelGGL(pad_convert_kernel<uint8_t>, dim3(grid), dim3(256), 0, s, static_cast<const uint8_t*>(src), dst, N, D, Dp);
     else
         hipLaunchKernelGGL(pad_convert_kernel<int8_t>, dim3(grid), dim3(256), 0, s, static_cast<const int8_t*>(src), dst, N, D, Dp);
+    GT_HIP(hipGetLastError());
+}
+
+void launch_pad_i8(const void* src, int dtype, int8_t* dst, int64_t N, int D, int Dp, hipStream_t s)
+{
+    const int64_t total = N * Dp;
+    const unsigned grid = static_cast<unsigned>(std::min<int64_t>((total + 255) / 256, 65536));
+    if (total == 0) return;
+    if (dtype == 1)
+        hipLaunchKernelGGL(pad_i8_kernel<uint8_t>, dim3(grid), dim3(256), 0, s, static_cast<const uint8_t*>(src), dst, N, D, Dp, 128);
+    else
+        hipLaunchKernelGGL(pad_i8_kernel<int8_t>, dim3(grid), dim3(256), 0, s, static_cast<const int8_t*>(src), dst, N, D, Dp, 0);
+    GT_HIP(hipGetLastError());
+}
+
+void launch_row_norms_i8(const int8_t* X, int64_t N, int Dp, float* norms, hipStream_t s)
+{
+    if (N <= 0) return;
+    hipLaunchKernelGGL(row_norms_i8_kernel, dim3(grid_for(N, 4)), dim3(256), 0, s, X, N, Dp, norms);
     GT_HIP(hipGetLastError());
 }
 

@@ -29,6 +29,8 @@ void launch_merge_partials(const int32_t* pids, const float* pd, int64_t nq, int
 // graph_kernels.hip
 void launch_pad_convert(const void* src, int dtype, float* dst, int64_t N, int D, int Dp, hipStream_t s);
 void launch_row_norms(const float* X, int64_t N, int Dp, float* norms, hipStream_t s);
+void launch_pad_i8(const void* src, int dtype, int8_t* dst, int64_t N, int D, int Dp, hipStream_t s);
+void launch_row_norms_i8(const int8_t* X, int64_t N, int Dp, float* norms, hipStream_t s);
 void launch_copy_ranges(const void* tasks, int64_t ntasks, const int32_t* members, int32_t* pool, hipStream_t s);
 void launch_negate(float* d, int64_t n, hipStream_t s);
 void launch_sanitize(const int32_t* in, int64_t N, int M, uint32_t* out, hipStream_t s);
@@ -164,7 +166,7 @@ namespace gtann {
 enum Ws {
     W_X, W_XRAW, W_NORMS, W_C, W_CRAW, W_CNORMS, W_IDS, W_D, W_IDS2, W_D2, W_IDS3, W_D3, W_ITEMS, W_QROWS, W_PROWS,
     W_MEMBERS, W_TASKS, W_POOL, W_PART_I, W_PART_D, W_G1, W_G2, W_G3, W_DEG, W_OFF, W_CUR, W_KEYS, W_SUMS, W_FLAG,
-    W_TMP, W_OUT, W_IN, W_PROBE_I, W_PROBE_D, W_WORST, W_COUNT_
+    W_TMP, W_OUT, W_IN, W_PROBE_I, W_PROBE_D, W_WORST, W_X8, W_NORMS8, W_COUNT_
 };
 static_assert(W_COUNT_ <= 40, "workspace slots");
 
@@ -255,11 +257,26 @@ struct DevMatrix {
     const float* norms = nullptr;
     int64_t N = 0;
     int Dp = 0;
+    // int8 rows of integer-typed inputs (uint8 shifted by -shift), stride
+    // Dp8 bytes, with their exact |x|^2; null for fp32 inputs
+    const int8_t* data8 = nullptr;
+    const float* norms8 = nullptr;
+    int Dp8 = 0;
+    int shift = 0;
 };
 
+// The int8 kernel runs a (query, pool) pair when both sides have int8 rows
+// with the same shift and the metric is unchanged by it (L2, or IP unshifted).
+static bool use_i8(const DevMatrix& q, const DevMatrix& p, int metric)
+{
+    return q.data8 && p.data8 && q.shift == p.shift && q.Dp8 == p.Dp8 && (metric == GT_METRIC_L2 || q.shift == 0);
+}
+
 // padded fp32 device copy (or the caller's own device buffer when it already
-// has that layout) plus row norms
-static DevMatrix prepare(Ctx& c, int slot_x, int slot_raw, int slot_norms, const void* X, int64_t N, int D, int dtype)
+// has that layout) plus row norms; with_i8: also int8 rows for integer inputs
+// of at most 256 dimensions
+static DevMatrix prepare(Ctx& c, int slot_x, int slot_raw, int slot_norms, const void* X, int64_t N, int D, int dtype,
+                         bool with_i8 = false)
 {
     GT_REQUIRE(X != nullptr && N > 0 && D > 0, "empty dataset");
     GT_REQUIRE(N < (int64_t(1) << 31), "N must be < 2^31");
@@ -270,10 +287,10 @@ static DevMatrix prepare(Ctx& c, int slot_x, int slot_raw, int slot_norms, const
     m.N = N;
     m.Dp = Dp;
     const bool dev = is_device_ptr(X);
+    const void* src = X;   // device copy of the caller's rows
     if (dev && dtype == GT_DTYPE_F32 && D == Dp && (reinterpret_cast<uintptr_t>(X) & 15) == 0) {
         m.data = static_cast<const float*>(X);
     } else {
-        const void* src = X;
         if (!dev) {
             void* raw = c.c->ws[slot_raw].ensure(static_cast<size_t>(N) * D * es);
             c.h2d(raw, X, static_cast<size_t>(N) * D * es);
@@ -286,7 +303,35 @@ static DevMatrix prepare(Ctx& c, int slot_x, int slot_raw, int slot_norms, const
     float* nrm = c.ws<float>(slot_norms, static_cast<size_t>(N));
     launch_row_norms(m.data, N, Dp, nrm, c.s);
     m.norms = nrm;
+    if (with_i8 && (dtype == GT_DTYPE_U8 || dtype == GT_DTYPE_I8) && Dp <= 256) {
+        m.Dp8 = Dp;
+        m.shift = dtype == GT_DTYPE_U8 ? 128 : 0;
+        int8_t* x8 = c.ws<int8_t>(W_X8, static_cast<size_t>(N) * Dp);
+        launch_pad_i8(src, dtype, x8, N, D, Dp, c.s);
+        float* n8 = c.ws<float>(W_NORMS8, static_cast<size_t>(N));
+        launch_row_norms_i8(x8, N, Dp, n8, c.s);
+        m.data8 = x8;
+        m.norms8 = n8;
+    }
     return m;
+}
+
+// Operands of one kNN launch: int8 rows where use_i8 allows, else fp32.
+static void set_operands(KnnArgs& a, const DevMatrix& q, const DevMatrix& p, int metric)
+{
+    if (use_i8(q, p, metric)) {
+        a.Xq8 = q.data8;
+        a.Xp8 = p.data8;
+        a.nq = q.norms8;
+        a.np = p.norms8;
+        a.Dp = q.Dp8;
+    } else {
+        a.Xq = q.data;
+        a.Xp = p.data;
+        a.nq = q.norms;
+        a.np = p.norms;
+        a.Dp = q.Dp;
+    }
 }
 
 // Fused kNN of a query list against a pool list, optionally split over the
@@ -342,15 +387,11 @@ static void run_knn_flat(Ctx& c, const KnnJob& j, int min_items = 2048)
         od = c.ws<float>(W_PART_D, static_cast<size_t>(splits) * j.nq * j.M);
     }
     KnnArgs a{};
-    a.Xq = j.Q->data;
-    a.Xp = j.P->data;
-    a.nq = j.Q->norms;
-    a.np = j.P->norms;
+    set_operands(a, *j.Q, *j.P, j.metric);
     a.q_rows = j.q_rows;
     a.p_rows = j.p_rows;
     a.items = d_items;
     a.n_items = static_cast<int32_t>(items.size());
-    a.Dp = j.Q->Dp;
     a.M = j.M;
     a.metric = j.metric;
     a.exclude_self = j.exclude_self ? 1 : 0;
@@ -630,15 +671,11 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
 
     tr.mark(c.s, "round: pools + work items");
     KnnArgs a{};
-    a.Xq = X.data;
-    a.Xp = X.data;
-    a.nq = X.norms;
-    a.np = X.norms;
+    set_operands(a, X, X, metric);
     a.q_rows = d_members;
     a.p_rows = d_pool;
     a.items = d_items;
     a.n_items = static_cast<int32_t>(items.size());
-    a.Dp = X.Dp;
     a.M = M;
     a.metric = metric;
     a.exclude_self = 1;
@@ -958,7 +995,7 @@ int gt_knn_exact(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtype, in
         GT_REQUIRE(metric == GT_METRIC_L2 || metric == GT_METRIC_IP, "unknown metric");
         GT_REQUIRE(queries || nq == N, "nq must equal N when queries is NULL");
         Ctx c(ctx);
-        DevMatrix Xm = prepare(c, W_X, W_XRAW, W_NORMS, X, N, D, dtype);
+        DevMatrix Xm = prepare(c, W_X, W_XRAW, W_NORMS, X, N, D, dtype, true);
         int32_t* d_q = nullptr;
         if (queries) {
             std::vector<int64_t> hq(static_cast<size_t>(nq));
@@ -1058,7 +1095,7 @@ int gt_knn_bucketed(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtype,
                 seen[static_cast<size_t>(m)] = 1;
             }
         }
-        DevMatrix Xm = prepare(c, W_X, W_XRAW, W_NORMS, X, N, D, dtype);
+        DevMatrix Xm = prepare(c, W_X, W_XRAW, W_NORMS, X, N, D, dtype, true);
         const size_t nm = static_cast<size_t>(N) * M;
         int32_t* cur_i = c.ws<int32_t>(W_IDS, nm);
         float* cur_d = c.ws<float>(W_D, nm);
@@ -1270,7 +1307,7 @@ int gt_build_graph(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtype, 
         gt_build_stats st{};
         Ctx c(ctx);
         Timer tp;
-        DevMatrix Xm = prepare(c, W_X, W_XRAW, W_NORMS, X, N, D, dtype);
+        DevMatrix Xm = prepare(c, W_X, W_XRAW, W_NORMS, X, N, D, dtype, true);
         c.sync();
         st.t_prepare = tp.sec();
         int64_t C = p.n_buckets > 0 ? p.n_buckets : std::max<int64_t>(1, N / 4000);

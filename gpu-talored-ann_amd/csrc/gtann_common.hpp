@@ -67,6 +67,10 @@ struct KnnArgs {
     int32_t seed_ld;
     int32_t* out_ids;       // (rows, M)
     float* out_d;           // (rows, M)
+    // int8 operands (integer-typed inputs): when set, the int8 kernel runs
+    // on these rows (stride Dp bytes) and nq/np are their |x|^2
+    const int8_t* Xq8;
+    const int8_t* Xp8;
 };
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }

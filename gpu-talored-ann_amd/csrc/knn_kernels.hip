@@ -120,7 +120,6 @@ __device__ __forceinline__ int32_t load_list_i(const int32_t* p)
 __device__ void wave_merge(KnnLists& sm, const KnnArgs& a, int w, int lane, int q, QueryState& st)
 {
     // query q's state, uniform across the wave (scalar registers)
-    const int nB = __builtin_amdgcn_readlane(st.cnt, q);
     const int nL = __builtin_amdgcn_readlane(st.nL, q);
     const int64_t orow = static_cast<int64_t>(
         (static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(st.orow >> 32), q))) << 32) |
@@ -497,6 +496,207 @@ __global__ void __launch_bounds__(256, 2) knn_fused_kernel(KnnArgs a)
     }
 }
 
+// ------------------------------------------------------------ int8 rows
+//
+// Integer-typed inputs (int8, or uint8 shifted by -128) run on the int8
+// matrix cores: v_mfma_i32_32x32x32_i8 contracts 32 dimensions per step with
+// exact int32 sums, so a 32x32 tile of D = 128 is 4 MFMAs instead of 64.
+// Each lane holds its query's bytes [32s + 16h, 32s + 16h + 16) for every
+// step s (the pool rows in LDS are read with the same split), so the two
+// half-waves cover the row between them.  Keys are exact: |p|^2 + |q|^2 -
+// 2 p.q < 2^24.  Filtering, appends and merges are the fp32 kernel's.
+typedef int intx4 __attribute__((ext_vector_type(4)));
+typedef int intx16 __attribute__((ext_vector_type(16)));
+
+template <int DP>
+struct KnnSmemI8 {
+    int8_t tile[2][kPoolTile][DP + 16];   // +16 bytes: rows land on distinct bank groups
+    float tnorm[3][kPoolTile];
+    int32_t trow[3][kPoolTile];
+    KnnLists L;
+};
+
+__device__ __forceinline__ floatx16 to_float(const intx16& v)
+{
+    floatx16 f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) f[r] = static_cast<float>(v[r]);
+    return f;
+}
+
+template <int DP, int METRIC>
+__global__ void __launch_bounds__(256, 2) knn_i8_kernel(KnnArgs a)
+{
+    constexpr int KS = DP / 32;                      // MFMA steps per tile
+    constexpr int U4_ROW = DP / 16;                  // 16-byte pieces per row
+    constexpr int U4_TILE = kPoolTile * U4_ROW;
+    constexpr int U4_THREAD = (U4_TILE + 255) / 256;
+    static_assert(DP % 32 == 0, "row stride must be a multiple of 32 bytes");
+    __shared__ KnnSmemI8<DP> sm;
+
+    const int per = a.n_items / 8;
+    const int item_idx = static_cast<int>(blockIdx.x % 8) * per + static_cast<int>(blockIdx.x / 8);
+    if (item_idx >= a.n_items) return;
+    const WorkItem it = a.items[item_idx];
+    if (it.q_count <= 0) return;
+
+    const int tid = threadIdx.x;
+    const int w = tid >> 6, lane = tid & 63, j = lane & 31, h = lane >> 5;
+    const int qlocal = w * kQueriesPerWave + j;
+    const bool qvalid = qlocal < it.q_count;
+    const int64_t qi = it.q_begin + qlocal;
+    const int32_t qrow = qvalid ? (a.q_rows ? a.q_rows[qi] : static_cast<int32_t>(qi)) : 0;
+    const float qn = (qvalid && METRIC == 0) ? a.nq[qrow] : 0.f;
+
+    QueryState st;
+    st.seed = FLT_MAX;
+    if (qvalid && a.seed_d) st.seed = fminf(a.seed_d[static_cast<int64_t>(qrow) * a.seed_ld + a.seed_ld - 1], FLT_MAX);
+    st.thr = qvalid ? st.seed : -INFINITY;
+    st.cnt = 0;
+    st.nL = 0;
+    st.self = a.exclude_self ? qrow : -2;
+    st.orow = it.out_base >= 0 ? it.out_base + qlocal : static_cast<int64_t>(qrow);
+    for (int e = lane; e < kQueriesPerWave * kCB; e += 64) sm.L.buf[w * kQueriesPerWave + e / kCB][e % kCB] = kNoKey;
+
+    intx4 qf[KS];
+    {
+        const int8_t* qsrc = a.Xq8 + static_cast<int64_t>(qrow) * DP + 16 * h;   // qrow 0 if invalid
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+            const intx4 v = *reinterpret_cast<const intx4*>(qsrc + 32 * s);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) qf[s][e] = qvalid ? v[e] : 0;
+        }
+    }
+
+    const int pcount = it.p_count;
+    const int ntiles = (pcount + kPoolTile - 1) / kPoolTile;
+    auto pool_row = [&](int p) -> int32_t {
+        if (p >= pcount) return -1;
+        p += it.p_rot;
+        if (p >= pcount) p -= pcount;
+        const int64_t pl = it.p_begin + p;
+        return a.p_rows ? a.p_rows[pl] : static_cast<int32_t>(pl);
+    };
+    auto row_norm = [&](int32_t row) -> float {
+        if (row < 0) return INFINITY;
+        return METRIC == 0 ? a.np[row] : 0.f;
+    };
+
+    int32_t idn[U4_THREAD];
+    uint4 pre[U4_THREAD];
+    int32_t rid_next = -1;
+    auto load_ids = [&](int t) {
+#pragma unroll
+        for (int u = 0; u < U4_THREAD; ++u) {
+            const int e = tid + 256 * u;
+            idn[u] = e < U4_TILE ? pool_row(t * kPoolTile + e / U4_ROW) : -1;
+        }
+        if (tid < kPoolTile) rid_next = pool_row(t * kPoolTile + tid);
+    };
+    auto load_rows = [&]() {
+#pragma unroll
+        for (int u = 0; u < U4_THREAD; ++u) {
+            const int e = tid + 256 * u;
+            const int32_t id = idn[u];
+            const uint4 v = *reinterpret_cast<const uint4*>(a.Xp8 + static_cast<int64_t>(id >= 0 ? id : 0) * DP +
+                                                            16 * (e % U4_ROW));
+            pre[u] = id >= 0 ? v : make_uint4(0u, 0u, 0u, 0u);
+        }
+    };
+    auto store_rows = [&](int buf) {
+#pragma unroll
+        for (int u = 0; u < U4_THREAD; ++u) {
+            const int e = tid + 256 * u;
+            if (e < U4_TILE) *reinterpret_cast<uint4*>(&sm.tile[buf][e / U4_ROW][16 * (e % U4_ROW)]) = pre[u];
+        }
+    };
+
+    if (tid < kPoolTile) { sm.tnorm[2][tid] = INFINITY; sm.trow[2][tid] = -1; }
+    load_ids(0);
+    load_rows();
+    int32_t rid_cur = rid_next;
+    float rn_cur = tid < kPoolTile ? row_norm(rid_cur) : 0.f;
+    store_rows(0);
+    if (tid < kPoolTile) { sm.trow[0][tid] = rid_cur; sm.tnorm[0][tid] = rn_cur; }
+    load_ids(1);
+    __syncthreads();
+
+    intx16 acc_prev;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc_prev[r] = 0;
+
+    for (int t = 0; t < ntiles; ++t) {
+        const int buf = t & 1;
+        wait_vmem();
+        load_rows();
+        rid_cur = rid_next;
+        rn_cur = tid < kPoolTile ? row_norm(rid_cur) : 0.f;
+        load_ids(t + 2);
+
+        intx16 acc;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[r] = 0;
+        const int8_t* arow = &sm.tile[buf][j][16 * h];
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+            const intx4 av = *reinterpret_cast<const intx4*>(arow + 32 * s);
+            acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, qf[s], acc, 0, 0, 0);
+        }
+
+        const int pb3 = (t + 2) % 3;
+        float mkey = INFINITY;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const float4 pn = *reinterpret_cast<const float4*>(&sm.tnorm[pb3][8 * g + 4 * h]);
+            const float n4[4] = {pn.x, pn.y, pn.z, pn.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float dot = static_cast<float>(acc_prev[4 * g + e]);
+                const float d = METRIC == 0 ? fmaf(-2.f, dot, n4[e] + qn) : fmaf(-1.f, dot, n4[e]);
+                mkey = fminf(mkey, d);
+            }
+        }
+        if (t > 0 && __ballot(mkey <= st.thr))
+            tile_append<METRIC>(sm.L, a, to_float(acc_prev), sm.tnorm[pb3], sm.trow[pb3], (t - 1) * kPoolTile, w,
+                                lane, h, qlocal, qvalid, qn, st);
+
+        store_rows(buf ^ 1);
+        if (tid < kPoolTile) { sm.trow[(t + 1) % 3][tid] = rid_cur; sm.tnorm[(t + 1) % 3][tid] = rn_cur; }
+        __syncthreads();
+        acc_prev = acc;
+    }
+    if (ntiles > 0) {
+        wait_vmem();
+        const int pb3 = (ntiles - 1) % 3;
+        float mkey = INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int i = 8 * (r >> 2) + 4 * h + (r & 3);
+            const float pn = sm.tnorm[pb3][i];
+            const float dot = static_cast<float>(acc_prev[r]);
+            mkey = fminf(mkey, METRIC == 0 ? fmaf(-2.f, dot, pn + qn) : fmaf(-1.f, dot, pn));
+        }
+        if (__ballot(mkey <= st.thr))
+            tile_append<METRIC>(sm.L, a, to_float(acc_prev), sm.tnorm[pb3], sm.trow[pb3], (ntiles - 1) * kPoolTile, w,
+                                lane, h, qlocal, qvalid, qn, st);
+    }
+
+    wait_vmem();
+    uint64_t rem = __ballot(qvalid && st.cnt > 0) & 0xffffffffull;
+    while (rem) {
+        const int q = __ffsll(static_cast<unsigned long long>(rem)) - 1;
+        rem &= rem - 1;
+        wave_merge(sm.L, a, w, lane, q, st);
+    }
+    if (qvalid) {
+        for (int p = st.nL + h; p < a.M; p += 2) {
+            a.out_ids[st.orow * a.M + p] = -1;
+            a.out_d[st.orow * a.M + p] = INFINITY;
+        }
+    }
+}
+
 // ------------------------------------------------------------ wide rows
 //
 // Rows longer than 256 floats do not fit a wave's registers as a query
@@ -766,6 +966,22 @@ static void launch_knn_metric(const KnnArgs& a, dim3 grid, hipStream_t stream)
     }
 }
 
+template <int METRIC>
+static void launch_knn_i8(const KnnArgs& a, dim3 grid, hipStream_t stream)
+{
+    switch (a.Dp) {
+    case 32:  hipLaunchKernelGGL((knn_i8_kernel<32, METRIC>), grid, dim3(256), 0, stream, a); break;
+    case 64:  hipLaunchKernelGGL((knn_i8_kernel<64, METRIC>), grid, dim3(256), 0, stream, a); break;
+    case 96:  hipLaunchKernelGGL((knn_i8_kernel<96, METRIC>), grid, dim3(256), 0, stream, a); break;
+    case 128: hipLaunchKernelGGL((knn_i8_kernel<128, METRIC>), grid, dim3(256), 0, stream, a); break;
+    case 160: hipLaunchKernelGGL((knn_i8_kernel<160, METRIC>), grid, dim3(256), 0, stream, a); break;
+    case 192: hipLaunchKernelGGL((knn_i8_kernel<192, METRIC>), grid, dim3(256), 0, stream, a); break;
+    case 224: hipLaunchKernelGGL((knn_i8_kernel<224, METRIC>), grid, dim3(256), 0, stream, a); break;
+    case 256: hipLaunchKernelGGL((knn_i8_kernel<256, METRIC>), grid, dim3(256), 0, stream, a); break;
+    default: GT_REQUIRE(false, "int8 kernel: padded dimension " + std::to_string(a.Dp) + " not supported");
+    }
+}
+
 // n_items must be a multiple of 8 (XCD-major layout, see knn_fused_kernel).
 void launch_knn_fused(const KnnArgs& a, hipStream_t stream)
 {
@@ -773,8 +989,14 @@ void launch_knn_fused(const KnnArgs& a, hipStream_t stream)
     GT_REQUIRE(a.M >= 1 && a.M <= kMaxM, "list length must be in [1, 128]");
     GT_REQUIRE(a.n_items % 8 == 0, "work list must be padded to a multiple of 8");
     const dim3 grid(static_cast<unsigned>(a.n_items));
-    if (a.metric == 0) launch_knn_metric<0>(a, grid, stream);
-    else launch_knn_metric<1>(a, grid, stream);
+    if (a.Xq8 && a.Xp8) {
+        if (a.metric == 0) launch_knn_i8<0>(a, grid, stream);
+        else launch_knn_i8<1>(a, grid, stream);
+    } else if (a.metric == 0) {
+        launch_knn_metric<0>(a, grid, stream);
+    } else {
+        launch_knn_metric<1>(a, grid, stream);
+    }
     GT_HIP(hipGetLastError());
 }
 
