@@ -29,6 +29,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "gpu-talored-ann_amd"))
 
 PEAK_FP32_MFMA = 157.3e12   # MI355X dense fp32 matrix, FLOP/s
+PEAK_INT8_MFMA = 5.0e15     # MI355X dense int8 matrix, OP/s
 PEAK_HBM = 8.0e12           # MI355X HBM3E, B/s
 
 
@@ -154,9 +155,20 @@ def main():
     prune_bytes = N * (4 * cfg.M + 4 * cfg.M * (cfg.M - 1) + 4 * cfg.K)
     merge_bytes = 28 * N * cfg.K
 
+    # integer datasets of up to 256 dimensions run the int8 kernel
+    int8 = cfg.dtype in ("i8", "u8") and D <= 256
+    dtype = "i8" if int8 else "fp32"
+    mip = 1 if cfg.metric == "ip" else 0
+    if int8:
+        kname, peak, punit = f"knn_i8_kernel<{-(-D // 32) * 32}, {mip}>", PEAK_INT8_MFMA, "TOP/s"
+    elif D <= 256:
+        kname, peak, punit = f"knn_fused_kernel<{-(-D // 32) * 32}, {mip}>", PEAK_FP32_MFMA, "TFLOP/s"
+    else:
+        kname, peak, punit = f"knn_wide_kernel<{mip}>", PEAK_FP32_MFMA, "TFLOP/s"
     out = {
         "metric": f"graph build Mpts/s at {N // 1000000 if N >= 1000000 else N}"
-                  f"{'M' if N >= 1000000 else ''}x{D} fp32 deg{cfg.K} (build seconds = ms_per_step/1000)",
+                  f"{'M' if N >= 1000000 else ''}x{D} {cfg.dtype if int8 else 'fp32'} deg{cfg.K} "
+                  f"(build seconds = ms_per_step/1000)",
         "value": N / wall / 1e6,
         "unit": "Mpts/s",
         "n_gpus": 1,
@@ -166,7 +178,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp32",
+        "dtype": dtype,
         "data": "synthetic (seeded Gaussian mixture, gpu-talored-ann_amd/synth.py)",
         "config": {
             "workload": f"{args.config}: {N} x {D} {cfg.dtype}, {cfg.metric.upper()}, {cfg.buckets} buckets, "
@@ -181,10 +193,9 @@ def main():
         "stages_s": {k: s[k] for k in ("t_prepare", "t_bucketing", "t_knn", "t_merge", "t_refine", "t_prune",
                                        "t_revmerge", "t_download", "t_total")},
         "roofline": {
-            "kernel": (f"knn_fused_kernel<{-(-D // 32) * 32}, {1 if cfg.metric == 'ip' else 0}>" if D <= 256 else
-                       f"knn_wide_kernel<{1 if cfg.metric == 'ip' else 0}>") + " (one launch per round)",
-            "bound": "mfma", "achieved": achieved / 1e12, "peak": PEAK_FP32_MFMA / 1e12, "unit": "TFLOP/s",
-            "frac": achieved / PEAK_FP32_MFMA, "traffic": traffic,
+            "kernel": kname + " (one launch per round; round 1 split in two when probing)",
+            "bound": "mfma", "achieved": achieved / 1e12, "peak": peak / 1e12, "unit": punit,
+            "frac": achieved / peak, "traffic": traffic,
             "flops_per_launch": flops_launch, "launch_ms": knn_launch_s * 1e3, "launches": launches,
         },
         "roofline_prune": {"bound": "hbm", "achieved": prune_bytes / s["t_prune"] / 1e9, "peak": 8000.0,

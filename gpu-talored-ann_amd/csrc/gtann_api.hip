@@ -33,6 +33,8 @@ void launch_pad_i8(const void* src, int dtype, int8_t* dst, int64_t N, int D, in
 void launch_row_norms_i8(const int8_t* X, int64_t N, int Dp, float* norms, hipStream_t s);
 void launch_copy_ranges(const void* tasks, int64_t ntasks, const int32_t* members, int32_t* pool, hipStream_t s);
 void launch_negate(float* d, int64_t n, hipStream_t s);
+void launch_graph_search(const SearchArgs& a, int64_t grid, hipStream_t s);
+size_t search_lds_bytes(int CC, int efr, int Dp, int H);
 void launch_sanitize(const int32_t* in, int64_t N, int M, uint32_t* out, hipStream_t s);
 void launch_cagra_prune(const int32_t* G, int64_t N, int M, int K, uint32_t* out, unsigned long long* bad_row,
                         hipStream_t s);
@@ -985,6 +987,148 @@ void gt_build_params_default(gt_build_params* p)
     p->seed = 42;
     p->reverse_edges = 0;
     p->reserved_ = 0;
+}
+
+void gt_search_params_default(gt_search_params* p)
+{
+    if (!p) return;
+    p->topk = 10;
+    p->ef = 200;
+    p->num_entry = 4;
+    p->metric = GT_METRIC_L2;
+    p->seed = 42;
+    p->visited_slots = 0;
+    p->reserved_ = 0;
+}
+
+int gt_search(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtype, const uint32_t* graph, int32_t degree,
+              const void* Q, int64_t nq, const int32_t* entries, int32_t n_entry, const gt_search_params* params,
+              int32_t* out_ids, float* out_d, gt_search_stats* stats)
+{
+    return guarded(ctx, [&] {
+        GT_REQUIRE(params && graph && out_ids && out_d && nq >= 0, "bad arguments");
+        const gt_search_params& p = *params;
+        GT_REQUIRE(degree >= 1, "degree must be >= 1");
+        GT_REQUIRE(p.topk >= 1 && p.topk <= 2048, "topk must be in [1, 2048]");
+        const int ef = std::max(p.ef, p.topk);
+        GT_REQUIRE(ef <= 2048, "ef must be <= 2048");
+        GT_REQUIRE(p.metric == GT_METRIC_L2 || p.metric == GT_METRIC_IP, "unknown metric");
+        GT_REQUIRE(N < (int64_t(1) << 31) - 1, "N must be < 2^31 - 1");
+        Timer tt;
+        Ctx c(ctx);
+        DevMatrix Xm = prepare(c, W_X, W_XRAW, W_NORMS, X, N, D, dtype);
+        gt_search_stats st{};
+        if (nq > 0) {
+            GT_REQUIRE(Q != nullptr, "no queries");
+            DevMatrix Qm = prepare(c, W_C, W_CRAW, W_CNORMS, Q, nq, D, dtype);
+            const uint32_t* g = c.in<uint32_t>(W_IN, graph, static_cast<size_t>(N) * degree);
+            int E = n_entry;
+            const int32_t* d_ent = nullptr;
+            if (entries) {
+                GT_REQUIRE(n_entry >= 1 && n_entry <= 64, "1 <= n_entry <= 64");
+                d_ent = c.in<int32_t>(W_PROBE_I, entries, static_cast<size_t>(nq) * E);
+            } else {
+                E = p.num_entry;
+                GT_REQUIRE(E >= 1 && E <= 64, "1 <= num_entry <= 64");
+                // E draws per query from a splitmix64 stream, sorted and distinct
+                std::vector<int32_t> he(static_cast<size_t>(nq) * E, -1);
+                parallel_slices(nq, host_threads(), [&](int, int64_t lo, int64_t hi) {
+                    std::vector<int32_t> tmp(static_cast<size_t>(E));
+                    for (int64_t q = lo; q < hi; ++q) {
+                        for (int e = 0; e < E; ++e) {
+                            uint64_t z = p.seed + 0x9E3779B97F4A7C15ull * static_cast<uint64_t>(q * E + e + 1);
+                            z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+                            z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+                            z ^= z >> 31;
+                            tmp[static_cast<size_t>(e)] = static_cast<int32_t>(z % static_cast<uint64_t>(N));
+                        }
+                        std::sort(tmp.begin(), tmp.end());
+                        const auto end = std::unique(tmp.begin(), tmp.end());
+                        std::copy(tmp.begin(), end, he.begin() + q * E);
+                    }
+                });
+                int32_t* d = c.ws<int32_t>(W_PROBE_I, he.size());
+                c.h2d(d, he.data(), he.size() * sizeof(int32_t));
+                c.sync();   // he is released at the end of this scope
+                d_ent = d;
+            }
+            const size_t nr = static_cast<size_t>(nq) * p.topk;
+            int32_t* oi = c.in<int32_t>(W_IDS, out_ids, nr, false);
+            float* od = c.in<float>(W_D, out_d, nr, false);
+            int32_t* d_status = c.ws<int32_t>(W_FLAG, static_cast<size_t>(nq));
+            int32_t* d_exp = c.ws<int32_t>(W_DEG, static_cast<size_t>(nq));
+
+            SearchArgs a{};
+            a.X = Xm.data;
+            a.N = N;
+            a.D = D;
+            a.Dp = Xm.Dp;
+            a.graph = g;
+            a.deg = degree;
+            a.Q = Qm.data;
+            a.entries = d_ent;
+            a.n_entry = E;
+            a.n_run = nq;
+            a.topk = p.topk;
+            a.ef = ef;
+            a.metric = p.metric;
+            a.efr = static_cast<int32_t>(ceil_div(ef, 64) * 64);
+            a.CC = a.efr + 256;
+            a.out_ids = oi;
+            a.out_d = od;
+            a.status = d_status;
+            a.expansions = d_exp;
+            // visited table: about 32 slots per result slot, within 64 KiB of LDS per query
+            int H = p.visited_slots;
+            if (H == 0) {
+                H = 512;
+                while (H < 32 * ef && search_lds_bytes(a.CC, a.efr, a.Dp, 2 * H) <= 65536) H *= 2;
+            }
+            GT_REQUIRE(H >= 512 && (H & (H - 1)) == 0, "visited_slots must be a power of two >= 512");
+            GT_REQUIRE(search_lds_bytes(a.CC, a.efr, a.Dp, H) <= 65536, "ef / dimension too large for one query's LDS");
+            a.H = H;
+            st.t_search = c.timed([&] { launch_graph_search(a, nq, c.s); });
+
+            std::vector<int32_t> hs(static_cast<size_t>(nq)), hx(static_cast<size_t>(nq));
+            c.d2h(hs.data(), d_status, hs.size() * sizeof(int32_t));
+            c.sync();
+            std::vector<int32_t> redo;
+            for (int64_t q = 0; q < nq; ++q) {
+                GT_REQUIRE(hs[static_cast<size_t>(q)] != 2,
+                           "search: more candidates tie at the ef-th distance than fit (query " + std::to_string(q) + ")");
+                if (hs[static_cast<size_t>(q)] == 1) redo.push_back(static_cast<int32_t>(q));
+            }
+            if (!redo.empty()) {
+                // queries that outgrew the on-chip table: a bitmap of N bits per wave in HBM
+                const int64_t words = ceil_div(N, 32);
+                const int64_t by_mem = std::max<int64_t>(1, (int64_t(4) << 30) / (words * 4));
+                const int64_t slots = std::min<int64_t>({static_cast<int64_t>(redo.size()), 2048, by_mem});
+                uint32_t* bmp = c.ws<uint32_t>(W_TMP, static_cast<size_t>(slots * words));
+                GT_HIP(hipMemsetAsync(bmp, 0, static_cast<size_t>(slots * words) * 4, c.s));
+                int32_t* d_redo = c.ws<int32_t>(W_QROWS, redo.size());
+                c.h2d(d_redo, redo.data(), redo.size() * sizeof(int32_t));
+                a.q_list = d_redo;
+                a.n_run = static_cast<int64_t>(redo.size());
+                a.H = 0;
+                a.bitmap = bmp;
+                a.bm_words = words;
+                st.t_search += c.timed([&] { launch_graph_search(a, slots, c.s); });
+                c.d2h(hs.data(), d_status, hs.size() * sizeof(int32_t));
+                c.sync();
+                for (int32_t q : redo)
+                    GT_REQUIRE(hs[static_cast<size_t>(q)] == 0,
+                               "search: more candidates tie at the ef-th distance than fit (query " + std::to_string(q) + ")");
+                st.requeued = static_cast<int64_t>(redo.size());
+            }
+            c.d2h(hx.data(), d_exp, hx.size() * sizeof(int32_t));
+            c.out(out_ids, oi, nr);
+            c.out(out_d, od, nr);
+            c.sync();
+            for (int32_t x : hx) st.expansions += x;
+        }
+        st.t_total = tt.sec();
+        if (stats) *stats = st;
+    });
 }
 
 int gt_knn_exact(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtype, int metric, const int64_t* queries,

@@ -73,6 +73,33 @@ struct KnnArgs {
     const int8_t* Xp8;
 };
 
+// Arguments of the graph search kernel (one wave per query).
+struct SearchArgs {
+    const float* X;           // base rows, stride Dp, zero padded
+    int64_t N;
+    int32_t D;
+    int32_t Dp;
+    const uint32_t* graph;    // (N, deg); entries >= N are skipped
+    int32_t deg;
+    const float* Q;           // query rows, stride Dp
+    const int32_t* entries;   // (nq, n_entry), processed in order; < 0 or >= N skipped
+    int32_t n_entry;          // <= 64
+    const int32_t* q_list;    // queries to run; nullptr = 0 .. n_run-1
+    int64_t n_run;
+    int32_t topk;
+    int32_t ef;
+    int32_t metric;           // 0 = L2, 1 = inner product (key = -<q,x>)
+    int32_t H;                // LDS visited table slots (power of two >= 512); 0 = bitmap mode
+    int32_t CC;               // candidate capacity (multiple of 64)
+    int32_t efr;              // ef rounded up to a multiple of 64
+    uint32_t* bitmap;         // bitmap mode: gridDim.x slots of bm_words words, zero on entry
+    int64_t bm_words;
+    int32_t* out_ids;         // (nq, topk)
+    float* out_d;             // (nq, topk)
+    int32_t* status;          // (nq): 0 done, 1 visited table full, 2 candidate capacity exceeded
+    int32_t* expansions;      // (nq)
+};
+
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // Orders LDS traffic of one wave across its lanes (no s_barrier needed

@@ -25,7 +25,7 @@ EXPORTS = (
     "gt_create", "gt_destroy", "gt_last_error", "gt_version", "gt_knn_exact", "gt_assign_top2",
     "gt_knn_bucketed", "gt_merge_rounds", "gt_refine_2hop", "gt_sanitize", "gt_cagra_prune",
     "gt_reverse_merge", "gt_optimize", "gt_translate", "gt_build_params_default", "gt_build_graph",
-    "gt_prune_occlusion", "gt_reverse_insert",
+    "gt_prune_occlusion", "gt_reverse_insert", "gt_search_params_default", "gt_search",
 )
 
 
@@ -51,6 +51,21 @@ class BuildStats(C.Structure):
         ("t_download", C.c_double), ("knn_flops", C.c_double), ("knn_pairs", C.c_double),
         ("max_pool", C.c_int64), ("max_bucket", C.c_int64), ("knn_launches", C.c_int64),
     ]
+
+    def as_dict(self):
+        return {name: getattr(self, name) for name, _ in self._fields_}
+
+
+class SearchParams(C.Structure):
+    _fields_ = [
+        ("topk", C.c_int32), ("ef", C.c_int32), ("num_entry", C.c_int32), ("metric", C.c_int32),
+        ("seed", C.c_uint64), ("visited_slots", C.c_int32), ("reserved_", C.c_int32),
+    ]
+
+
+class SearchStats(C.Structure):
+    _fields_ = [("t_total", C.c_double), ("t_search", C.c_double), ("expansions", C.c_int64),
+                ("requeued", C.c_int64)]
 
     def as_dict(self):
         return {name: getattr(self, name) for name, _ in self._fields_}
@@ -89,6 +104,10 @@ def lib():
         L.gt_build_params_default.restype = None
         L.gt_build_graph.argtypes = [vp, vp, i64, i32, C.c_int, C.POINTER(BuildParams), vp, vp, vp,
                                      C.POINTER(BuildStats)]
+        L.gt_search_params_default.argtypes = [C.POINTER(SearchParams)]
+        L.gt_search_params_default.restype = None
+        L.gt_search.argtypes = [vp, vp, i64, i32, C.c_int, vp, i32, vp, i64, vp, i32, C.POINTER(SearchParams),
+                                vp, vp, C.POINTER(SearchStats)]
         _lib = L
     return _lib
 
@@ -325,3 +344,43 @@ class Context:
         if graph is not None and not _is_torch(graph):
             graph = graph.view(np.uint32)
         return BuildResult(graph=graph, knn_ids=ids, knn_dists=d, stats=st.as_dict())
+
+    def search(self, X, graph, Q, *, topk=10, ef=200, num_entry=4, entries=None, metric="l2", seed=42,
+               visited_slots=0):
+        """Beam search (bd/search.py:20-90 per query) of the rows of Q over
+        `graph` (N, degree); ids outside [0, N) in the graph are skipped.
+        entries: (nq, E) int entry points in processing order (< 0 skipped),
+        or None to let the library draw `num_entry` per query.  Returns
+        (ids int32 (nq, topk), dists float32, stats dict)."""
+        if not _is_torch(X):
+            X = np.ascontiguousarray(X)
+            Q = np.ascontiguousarray(Q, dtype=X.dtype)
+        N, D = X.shape
+        if Q.shape[1] != D:
+            raise ValueError(f"query dimension {Q.shape[1]} != base dimension {D}")
+        if _is_torch(graph):
+            g = graph
+        else:
+            g = np.asarray(graph)
+            if g.dtype != np.uint32:
+                g64 = g.astype(np.int64)
+                g = np.where((g64 >= 0) & (g64 < N), g64, 0xFFFFFFFF).astype(np.uint32)
+            g = np.ascontiguousarray(g)
+        if g.shape[0] != N:
+            raise ValueError(f"graph must have {N} rows, got {g.shape[0]}")
+        nq = int(Q.shape[0])
+        E = 0
+        ent = None
+        if entries is not None:
+            ent = entries if _is_torch(entries) else _np(np.asarray(entries).reshape(nq, -1), np.int32)
+            E = int(ent.shape[1])
+        p = SearchParams()
+        lib().gt_search_params_default(C.byref(p))
+        p.topk, p.ef, p.num_entry, p.metric = topk, ef, num_entry, METRICS[metric]
+        p.seed, p.visited_slots = seed, visited_slots
+        ids = _empty_like_input(X, (nq, topk), np.int32)
+        d = _empty_like_input(X, (nq, topk), np.float32)
+        st = SearchStats()
+        self._check(lib().gt_search(self._h, _ptr(X), N, D, _dtype_code(X), _ptr(g), int(g.shape[1]), _ptr(Q), nq,
+                                    _ptr(ent), E, C.byref(p), _ptr(ids), _ptr(d), C.byref(st)), "gt_search")
+        return ids, d, st.as_dict()

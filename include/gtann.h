@@ -169,6 +169,45 @@ int gt_build_graph(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtype,
                    const gt_build_params* params, int32_t* knn_ids, float* knn_dists,
                    uint32_t* graph, gt_build_stats* stats);
 
+/* Beam (ef) search.  Defaults (gt_search_params_default) are the reference
+ * CLI's: topk 10, ef 200, num_entry 4 (bd/search.py:280-283), L2, seed 42. */
+typedef struct gt_search_params {
+    int32_t topk;           /* results per query (--topk) */
+    int32_t ef;             /* beam width (--ef), raised to topk as bd/search.py:164 does; <= 2048 */
+    int32_t num_entry;      /* entry points per query drawn when `entries` is NULL (--num-entry), <= 64 */
+    int32_t metric;         /* GT_METRIC_L2 (the reference's only metric) or GT_METRIC_IP */
+    uint64_t seed;          /* entry draw when `entries` is NULL */
+    int32_t visited_slots;  /* 0 = automatic; else the on-chip visited table per query (power of two
+                               >= 512); a query that outgrows it is run again with an HBM bitmap */
+    int32_t reserved_;
+} gt_search_params;
+
+typedef struct gt_search_stats {
+    double t_total;         /* wall seconds of the whole call */
+    double t_search;        /* search kernels (device time) */
+    int64_t expansions;     /* nodes popped and expanded, all queries */
+    int64_t requeued;       /* queries run a second time with the HBM bitmap */
+} gt_search_stats;
+
+void gt_search_params_default(gt_search_params* p);
+
+/* Beam search of nq queries Q (nq x D, same dtype as X) over a graph
+ * (N x degree ids; ids >= N, e.g. 0xFFFFFFFF padding, are skipped): per query
+ * the sequential best-first search of bd/search.py:20-90
+ * (graph_search_single) -- entry points in order, pop the smallest
+ * (distance, id) candidate, stop when ef results are held and the popped
+ * distance exceeds their maximum, a strictly closer point replaces the first
+ * slot holding the maximum.  entries: (nq x n_entry) int32 entry points
+ * (< 0 skipped), or NULL to draw params->num_entry per query (sorted,
+ * distinct, seeded; not numpy's generator -- the Python mirror passes
+ * numpy's draws).  out_ids / out_d: (nq x topk) ascending in distance, ties
+ * in result-slot order, padded with -1 / +inf; with GT_METRIC_IP out_d is the
+ * inner product (descending).  Replaces the per-query loop of
+ * search_graph_recall (bd/search.py:165-174, bd/search.cpp:305-320). */
+int gt_search(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtype, const uint32_t* graph,
+              int32_t degree, const void* Q, int64_t nq, const int32_t* entries, int32_t n_entry,
+              const gt_search_params* params, int32_t* out_ids, float* out_d, gt_search_stats* stats);
+
 #ifdef __cplusplus
 }
 #endif

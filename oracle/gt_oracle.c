@@ -657,3 +657,155 @@ int or_num_threads(void)
     return 1;
 #endif
 }
+
+/* ------------------------------------------------------------------ search
+ * Beam (ef) search over a graph, one query at a time, as
+ * bd/search.py:20-90 (graph_search_single):
+ *   - entry points in the given order (the Python pipeline passes
+ *     np.unique(rng.integers(0, N, num_entry)), bd/search.py:41-42), each
+ *     visited and inserted like a neighbour (:43-54);
+ *   - pop the candidate with the smallest (distance, id) -- heapq's tuple
+ *     order (:56-57); stop when the best list holds ef points and the popped
+ *     distance exceeds its maximum (:58-62);
+ *   - expand the popped node's row in order, skipping ids outside [0, N)
+ *     and visited ones (:64-71); every newly visited point becomes a
+ *     candidate (:72);
+ *   - the best list is an array of at most ef slots: append while short,
+ *     else a strictly closer point replaces the first slot holding the
+ *     maximum (np.argmax, :74-81);
+ *   - output: the best list sorted by distance with ties in slot order (a
+ *     stable argsort; the reference's np.argsort is numpy's unstable sort,
+ *     :87-89), first topk, padded with (-1, +inf) (:171-174).
+ * Distances: sum over dims of (q - x)^2 accumulated in dimension order with
+ * fmaf (bd/search.py:12-14 l2sqr), or -sum q*x for the inner product.
+ */
+typedef struct { float d; uint32_t id; } sc_t;
+
+static int sc_less(sc_t a, sc_t b) { return a.d < b.d || (a.d == b.d && a.id < b.id); }
+
+static void sc_push(sc_t* h, int64_t* n, sc_t x)
+{
+    int64_t i = (*n)++;
+    while (i > 0) {
+        const int64_t p = (i - 1) / 2;
+        if (!sc_less(x, h[p])) break;
+        h[i] = h[p];
+        i = p;
+    }
+    h[i] = x;
+}
+
+static sc_t sc_pop(sc_t* h, int64_t* n)
+{
+    const sc_t top = h[0];
+    const sc_t x = h[--(*n)];
+    int64_t i = 0;
+    for (;;) {
+        int64_t c = 2 * i + 1;
+        if (c >= *n) break;
+        if (c + 1 < *n && sc_less(h[c + 1], h[c])) ++c;
+        if (!sc_less(h[c], x)) break;
+        h[i] = h[c];
+        i = c;
+    }
+    if (*n > 0) h[i] = x;
+    return top;
+}
+
+static float search_dist(const float* q, const float* x, int64_t D, int metric)
+{
+    float s = 0.f;
+    if (metric == 1) {
+        for (int64_t k = 0; k < D; ++k) s = fmaf(q[k], x[k], s);
+        return -s;
+    }
+    for (int64_t k = 0; k < D; ++k) {
+        const float t = q[k] - x[k];
+        s = fmaf(t, t, s);
+    }
+    return s;
+}
+
+int or_search(const float* X, int64_t N, int64_t D, const uint32_t* graph, int deg, const float* Q, int64_t nq,
+              const int32_t* entries, int n_entry, int topk, int ef, int metric, int32_t* out_ids, float* out_d,
+              int64_t* expansions)
+{
+    if (N <= 0 || D <= 0 || deg < 0 || n_entry < 1 || topk < 1 || ef < topk) return OR_EINVAL;
+    int err = OR_OK;
+    #pragma omp parallel
+    {
+        uint8_t* seen = (uint8_t*)calloc((size_t)N, 1);
+        int64_t hcap = 1024, vcap = 1024;
+        sc_t* heap = (sc_t*)malloc(sizeof(sc_t) * (size_t)hcap);
+        uint32_t* vis = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)vcap);
+        float* bd = (float*)malloc(sizeof(float) * (size_t)ef);
+        uint32_t* bi = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)ef);
+        int* ord = (int*)malloc(sizeof(int) * (size_t)ef);
+        if (!seen || !heap || !vis || !bd || !bi || !ord) {
+            #pragma omp atomic write
+            err = OR_ENOMEM;
+        }
+        #pragma omp for schedule(dynamic, 4)
+        for (int64_t qi = 0; qi < nq; ++qi) {
+            if (err) continue;
+            const float* q = Q + qi * D;
+            int64_t nh = 0, nv = 0, nexp = 0;
+            int nb = 0;
+            /* visit v: mark, distance, candidate, best list (bd/search.py:70-81) */
+#define OR_VISIT(vv)                                                                                  \
+            do {                                                                                      \
+                const uint32_t v_ = (vv);                                                             \
+                seen[v_] = 1;                                                                         \
+                if (nv == vcap) { vcap *= 2; vis = (uint32_t*)realloc(vis, sizeof(uint32_t) * (size_t)vcap); } \
+                vis[nv++] = v_;                                                                       \
+                const float dv_ = search_dist(q, X + (int64_t)v_ * D, D, metric);                     \
+                if (nh == hcap) { hcap *= 2; heap = (sc_t*)realloc(heap, sizeof(sc_t) * (size_t)hcap); } \
+                sc_t c_ = {dv_, v_};                                                                  \
+                sc_push(heap, &nh, c_);                                                               \
+                if (nb < ef) { bd[nb] = dv_; bi[nb] = v_; ++nb; }                                     \
+                else {                                                                                \
+                    int w_ = 0;                                                                       \
+                    for (int t_ = 1; t_ < nb; ++t_) if (bd[t_] > bd[w_]) w_ = t_;                     \
+                    if (dv_ < bd[w_]) { bd[w_] = dv_; bi[w_] = v_; }                                  \
+                }                                                                                     \
+            } while (0)
+            for (int e = 0; e < n_entry; ++e) {
+                const int32_t s = entries[qi * n_entry + e];
+                if (s < 0 || s >= N || seen[s]) continue;
+                OR_VISIT((uint32_t)s);
+            }
+            while (nh > 0) {
+                const sc_t u = sc_pop(heap, &nh);
+                if (nb >= ef) {
+                    float worst = bd[0];
+                    for (int t = 1; t < nb; ++t) worst = bd[t] > worst ? bd[t] : worst;
+                    if (u.d > worst) break;
+                }
+                ++nexp;
+                const uint32_t* row = graph + (int64_t)u.id * deg;
+                for (int j = 0; j < deg; ++j) {
+                    const uint32_t v = row[j];
+                    if (v >= (uint64_t)N || seen[v]) continue;
+                    OR_VISIT(v);
+                }
+            }
+#undef OR_VISIT
+            /* stable order of the best list by distance */
+            for (int t = 0; t < nb; ++t) ord[t] = t;
+            for (int t = 1; t < nb; ++t) {
+                const int x = ord[t];
+                int p = t;
+                while (p > 0 && bd[ord[p - 1]] > bd[x]) { ord[p] = ord[p - 1]; --p; }
+                ord[p] = x;
+            }
+            for (int t = 0; t < topk; ++t) {
+                out_ids[qi * topk + t] = t < nb ? (int32_t)bi[ord[t]] : -1;
+                out_d[qi * topk + t] = t < nb ? bd[ord[t]] : INFINITY;
+            }
+            if (expansions) expansions[qi] = nexp;
+            for (int64_t t = 0; t < nv; ++t) seen[vis[t]] = 0;
+        }
+        free(seen); free(heap); free(vis); free(bd); free(bi); free(ord);
+    }
+    return err;
+}

@@ -47,6 +47,16 @@ How each oracle function is pinned (what checks it besides itself):
   as the M smallest of (row, surviving offers) -- every offer left out is
   not below the row's last key.  torch.topk's order among equal distances is
   "parity unpinned"; the oracle orders ties by id.
+* ``search`` -- bd/search.py:20-90 (graph_search_single).  Pinned by two
+  hand-traced known answers (a tie at the ef-th distance is still expanded,
+  ``>`` not ``>=``; a closer point replaces the FIRST slot holding the
+  maximum), by the closed form "ef >= N on a connected graph returns the
+  exact top-k", and against the reference's own C++ search
+  (bd/search.cpp:33-137, compiled in place into ``_ref/``) on tie-free float
+  data with one entry point, where the two reference versions agree.  The
+  reference's np.argsort order among equal distances and its BLAS float32
+  summation order are "parity unpinned"; the oracle sorts ties by slot and
+  sums in dimension order.
 """
 from __future__ import annotations
 
@@ -58,11 +68,13 @@ import numpy as np
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIB_PATH = os.path.join(_HERE, "liboracle_gt.so")
 _REF_PATH = os.path.join(_HERE, "_ref", "libgtann_ref.so")
+_REF_SEARCH_PATH = os.path.join(_HERE, "_ref", "libgtann_ref_search.so")
 
 OR_OK, OR_EINVAL, OR_ENOMEM, OR_EFEWCAND = 0, -1, -2, -4
 
 _lib = None
 _ref = None
+_ref_search = None
 
 
 def _p(a):
@@ -90,6 +102,7 @@ def lib():
         L.or_refine_2hop.argtypes = [vp, i64, i64, i32, vp, vp, i32, i32, vp, vp]
         L.or_translate.argtypes = [vp, vp, i64, i32, vp]
         L.or_prune_occlusion.argtypes = [vp, i64, i64, vp, i32, i32, vp]
+        L.or_search.argtypes = [vp, i64, i64, vp, i32, vp, i64, vp, i32, i32, i32, i32, vp, vp, vp]
         L.or_num_threads.restype = i32
         _lib = L
     return _lib
@@ -257,7 +270,57 @@ def prune_occlusion(X, nb, max_degree):
     return out
 
 
+def search(X, graph, Q, entries, topk, ef, metric=0):
+    """(ids int32 (nq, topk), keys float32, expansions int64 (nq,)); entries
+    (nq, E) int32 in processing order, -1 = none.  ef is raised to topk as
+    bd/search.py:164 does."""
+    X = _f32(X)
+    Q = _f32(Q)
+    N, D = X.shape
+    g = np.ascontiguousarray(graph).astype(np.int64)
+    g = np.where((g >= 0) & (g < N), g, 0xFFFFFFFF).astype(np.uint32)
+    deg = g.shape[1]
+    ent = np.ascontiguousarray(entries, np.int32)
+    if ent.ndim == 1:
+        ent = ent[:, None]
+    nq = Q.shape[0]
+    ef = max(int(ef), int(topk))
+    ids = np.empty((nq, topk), np.int32)
+    d = np.empty((nq, topk), np.float32)
+    ex = np.empty(nq, np.int64)
+    _check(lib().or_search(_p(X), N, D, _p(g), deg, _p(Q), nq, _p(ent), ent.shape[1], topk, ef, metric,
+                           _p(ids), _p(d), _p(ex)), "or_search")
+    return ids, d, ex
+
+
 # ---- the reference's own code, compiled in place (test-time only) ----
+
+def ref_search_available() -> bool:
+    return os.path.exists(_REF_SEARCH_PATH)
+
+
+def ref_search(X, graph, Q, topk, ef, num_entry, seed=42):
+    """bd/search.cpp's graph_search_single over every query with one
+    std::mt19937(seed) as its search_graph_recall does, plus the entry points
+    it drew (nq, num_entry; -1 past the distinct ones, in draw order)."""
+    global _ref_search
+    if _ref_search is None:
+        R = C.CDLL(_REF_SEARCH_PATH)
+        vp, i32 = C.c_void_p, C.c_int32
+        R.ref_graph_search.argtypes = [vp, i32, i32, vp, i32, vp, i32, i32, i32, i32, C.c_uint32, vp, vp, vp]
+        _ref_search = R
+    X = _f32(X)
+    Q = _f32(Q)
+    N, D = X.shape
+    g = np.ascontiguousarray(graph, np.int64)
+    nq = Q.shape[0]
+    ids = np.empty((nq, topk), np.int64)
+    d = np.empty((nq, topk), np.float32)
+    ent = np.empty((nq, num_entry), np.int32)
+    _check(_ref_search.ref_graph_search(_p(X), N, D, _p(g), g.shape[1], _p(Q), nq, topk, ef, num_entry, seed,
+                                        _p(ids), _p(d), _p(ent)), "ref_graph_search")
+    return ids, d, ent
+
 
 def ref_cagra_prune(G, K):
     G = np.ascontiguousarray(G).view(np.int32) if np.asarray(G).dtype == np.uint32 else \

@@ -1,0 +1,146 @@
+"""GPU beam search (gt_search) against the CPU restatement of
+bd/search.py:20-90, through the C ABI.
+
+Both sides accumulate each distance over the dimensions in order with fmaf,
+so ids, distances (bit for bit) and the number of expanded nodes agree on
+integer and on float data.
+"""
+import numpy as np
+import pytest
+
+import gt_oracle as O
+import synth
+
+pytestmark = pytest.mark.gpu
+
+
+def _line(xs):
+    return np.asarray(xs, np.float32)[:, None]
+
+
+def _compare(ctx, X, g, Q, ent, topk, ef, metric="l2", **kw):
+    ids, d, st = ctx.search(X, g, Q, topk=topk, ef=ef, entries=ent, metric=metric, **kw)
+    rid, rd, rex = O.search(X.astype(np.float32), g, Q.astype(np.float32), ent, topk, ef,
+                            metric=1 if metric == "ip" else 0)
+    np.testing.assert_array_equal(ids, rid)
+    dd = -d if metric == "ip" else d
+    np.testing.assert_array_equal(dd.view(np.uint32), rd.view(np.uint32))
+    assert st["expansions"] == int(rex.sum())
+    return st
+
+
+def test_known_answers(ctx):
+    # a tie at the ef-th distance is still expanded (stop on ">", not ">=")
+    X = _line([5, 3, -3, 1])
+    g = np.array([[1, 2], [0, -1], [3, -1], [-1, -1]])
+    ids, d, st = ctx.search(X, g, _line([0]), topk=1, ef=1, entries=[[0]])
+    assert ids.tolist() == [[3]] and d.tolist() == [[1.0]] and st["expansions"] == 4
+    # a closer point replaces the first slot holding the maximum
+    X = _line([50, 2, -2, 1])
+    g = np.array([[-1], [3], [-1], [-1]])
+    ids, d, _ = ctx.search(X, g, _line([0]), topk=2, ef=2, entries=[[1, 2]])
+    assert ids.tolist() == [[3, 2]] and d.tolist() == [[1.0, 4.0]]
+
+
+@pytest.mark.parametrize("N,D,deg,nq,topk,ef,E", [
+    (5000, 128, 32, 300, 10, 64, 4),
+    (5000, 128, 32, 200, 10, 200, 4),
+    (3000, 96, 16, 200, 20, 20, 1),
+    (4000, 64, 96, 100, 10, 100, 8),       # rows longer than a wave
+    (2000, 100, 24, 150, 32, 300, 64),     # D not a multiple of 4 after padding
+])
+def test_integer_data_matches_oracle(ctx, N, D, deg, nq, topk, ef, E):
+    rng = np.random.default_rng(N + deg + ef)
+    X = rng.integers(0, 64, size=(N, D)).astype(np.float32)
+    knn, _ = O.knn_exact(X, deg - 4)
+    g = np.concatenate([knn, rng.integers(0, N, size=(N, 4))], axis=1)
+    Q = rng.integers(0, 64, size=(nq, D)).astype(np.float32)
+    ent = np.sort(rng.integers(0, N, size=(nq, E)), axis=1).astype(np.int32)
+    print(f"search N={N} D={D} deg={deg} nq={nq} topk={topk} ef={ef} E={E}", flush=True)
+    _compare(ctx, X, g, Q, ent, topk, ef)
+
+
+def test_float_data_matches_oracle(ctx):
+    X, _ = synth.generate("C1", n=6000)
+    rng = np.random.default_rng(3)
+    knn, _ = O.knn_exact(X, 32)
+    Q = X[rng.choice(6000, 200, replace=False)] + rng.standard_normal((200, X.shape[1])).astype(np.float32)
+    ent = rng.integers(0, 6000, size=(200, 4)).astype(np.int32)
+    _compare(ctx, X, knn, Q, ent, 10, 128)
+
+
+def test_inner_product(ctx):
+    X, _ = synth.generate("C3", n=4000)
+    knn, _ = O.knn_exact(X, 24, metric=1)
+    rng = np.random.default_rng(4)
+    Q = X[rng.choice(4000, 100, replace=False)]
+    ent = rng.integers(0, 4000, size=(100, 2)).astype(np.int32)
+    _compare(ctx, X, knn, Q, ent, 10, 64, metric="ip")
+
+
+def test_padding_duplicates_and_out_of_range(ctx):
+    rng = np.random.default_rng(5)
+    N, D = 3000, 32
+    X = rng.integers(0, 16, size=(N, D)).astype(np.float32)   # many equal distances
+    g = rng.integers(0, N, size=(N, 20)).astype(np.int64)
+    g[:, 5] = g[:, 2]                       # repeated id in every row
+    g[::3, 10:] = -1                        # padding
+    g[1::7, 0] = N + 5                      # out of range
+    Q = rng.integers(0, 16, size=(120, D)).astype(np.float32)
+    ent = rng.integers(-1, N, size=(120, 3)).astype(np.int32)   # -1 entries skipped
+    _compare(ctx, X, g, Q, ent, 16, 48)
+
+
+def test_small_visited_table_requeues_on_hbm_bitmap(ctx):
+    rng = np.random.default_rng(6)
+    N, D = 20000, 32
+    X = rng.integers(0, 64, size=(N, D)).astype(np.float32)
+    knn, _ = O.knn_exact(X, 32)
+    Q = rng.integers(0, 64, size=(64, D)).astype(np.float32)
+    ent = rng.integers(0, N, size=(64, 4)).astype(np.int32)
+    st = _compare(ctx, X, knn, Q, ent, 10, 400, visited_slots=512)
+    assert st["requeued"] > 0
+    # a second call reuses the (re-zeroed) bitmaps
+    st2 = _compare(ctx, X, knn, Q[::-1].copy(), ent[::-1].copy(), 10, 400, visited_slots=512)
+    assert st2["requeued"] > 0
+
+
+@pytest.mark.parametrize("dtype", [np.uint8, np.int8])
+def test_integer_typed_inputs(ctx, dtype):
+    rng = np.random.default_rng(7)
+    lo, hi = (0, 256) if dtype == np.uint8 else (-128, 128)
+    X = rng.integers(lo, hi, size=(3000, 128)).astype(dtype)
+    Q = rng.integers(lo, hi, size=(100, 128)).astype(dtype)
+    knn, _ = O.knn_exact(X.astype(np.float32), 24)
+    ent = rng.integers(0, 3000, size=(100, 4)).astype(np.int32)
+    _compare(ctx, X, knn, Q, ent, 10, 64)
+
+
+def test_library_entries_and_built_graph_recall(ctx):
+    """End to end: build a graph, search it with library-drawn entries; the
+    results are valid, ascending, and recall@10 vs exact is high."""
+    X, _ = synth.generate("C2", n=50000)
+    res = ctx.build_graph(X, n_buckets=16, M=64, K=32, rounds=2)
+    rng = np.random.default_rng(8)
+    qi = rng.choice(len(X), 500, replace=False)
+    Q = X[qi] + rng.integers(-3, 4, size=(500, X.shape[1])).astype(np.float32)
+    ids, d, st = ctx.search(X, res.graph, Q, topk=10, ef=128, num_entry=4)
+    assert (ids >= 0).all() and (ids < len(X)).all()
+    assert (np.diff(d, axis=1) >= 0).all()
+    ex = np.stack([np.argsort(((X - q) ** 2).sum(1), kind="stable")[:10] for q in Q.astype(np.float64)])
+    rec = np.mean([len(np.intersect1d(ids[i], ex[i])) / 10 for i in range(500)])
+    print(f"search recall@10 = {rec:.4f}, expansions/query = {st['expansions'] / 500:.1f}")
+    assert rec > 0.95
+
+
+def test_invalid_arguments(ctx):
+    X = np.zeros((100, 8), np.float32)
+    g = np.zeros((100, 4), np.int64)
+    Q = np.zeros((2, 8), np.float32)
+    import gtann
+    with pytest.raises(gtann.GtannError):
+        ctx.search(X, g, Q, topk=10, ef=5000)
+    with pytest.raises(gtann.GtannError):
+        ctx.search(X, g, Q, entries=np.zeros((2, 65), np.int32))
+    with pytest.raises(gtann.GtannError):
+        ctx.search(X, g, Q, visited_slots=1000)
