@@ -187,4 +187,78 @@ inline void write_npy(const std::string& path, const T* v, int64_t rows, int64_t
     f.close();
 }
 
+// 2-D .npy of int64, int32 or uint32 (format 1.x/2.x, C order, little
+// endian), widened to int64: neighbors.npy and exact-kNN indices, the files
+// bd/load.hpp:103 (read_npy_int64_2d) reads.
+inline std::vector<int64_t> read_npy_2d(const std::string& path, int64_t& rows, int64_t& cols)
+{
+    File f(path, "rb");
+    char magic[8];
+    f.read(magic, 8, "npy magic");
+    if (static_cast<unsigned char>(magic[0]) != 0x93 || std::string(magic + 1, 5) != "NUMPY")
+        throw std::runtime_error("not a .npy file: " + path);
+    uint32_t hlen = 0;
+    if (magic[6] == 1) {
+        uint16_t h16;
+        f.read(&h16, 2, "npy header length");
+        hlen = h16;
+    } else if (magic[6] == 2 || magic[6] == 3) {
+        f.read(&hlen, 4, "npy header length");
+    } else {
+        throw std::runtime_error("unsupported .npy version in " + path);
+    }
+    std::string h(hlen, '\0');
+    f.read(&h[0], hlen, "npy header");
+    auto field = [&](const char* key) -> std::string {
+        const size_t k = h.find(key);
+        if (k == std::string::npos) throw std::runtime_error(std::string("no ") + key + " in .npy header: " + path);
+        return h.substr(k + std::strlen(key));
+    };
+    const std::string descr = field("'descr':");
+    const std::string order = field("'fortran_order':");
+    if (order.find("True") < order.find(',')) throw std::runtime_error("Fortran-order .npy not supported: " + path);
+    size_t esz = 0;
+    int kind = 0;   // 0 i8, 1 i4, 2 u4
+    if (descr.find("'<i8'") < descr.find(',')) { esz = 8; kind = 0; }
+    else if (descr.find("'<i4'") < descr.find(',')) { esz = 4; kind = 1; }
+    else if (descr.find("'<u4'") < descr.find(',')) { esz = 4; kind = 2; }
+    else throw std::runtime_error("unsupported .npy dtype (int64, int32, uint32): " + path);
+    const std::string shape = field("'shape':");
+    const size_t o = shape.find('('), c = shape.find(')');
+    if (o == std::string::npos || c == std::string::npos) throw std::runtime_error("bad .npy shape: " + path);
+    const std::string dims = shape.substr(o + 1, c - o - 1);
+    const size_t comma = dims.find(',');
+    if (comma == std::string::npos) throw std::runtime_error(".npy array is not 2-D: " + path);
+    rows = std::stoll(dims.substr(0, comma));
+    const std::string rest = dims.substr(comma + 1);
+    if (rest.find_first_of("0123456789") == std::string::npos) throw std::runtime_error(".npy array is not 2-D: " + path);
+    cols = std::stoll(rest);
+    if (rows <= 0 || cols <= 0) throw std::runtime_error("empty .npy array: " + path);
+    const size_t n = static_cast<size_t>(rows) * static_cast<size_t>(cols);
+    std::vector<int64_t> out(n);
+    if (kind == 0) {
+        f.read(out.data(), n * 8, "npy payload");
+    } else {
+        std::vector<uint32_t> tmp(n);
+        f.read(tmp.data(), n * esz, "npy payload");
+        for (size_t i = 0; i < n; ++i)
+            out[i] = kind == 1 ? static_cast<int64_t>(static_cast<int32_t>(tmp[i])) : static_cast<int64_t>(tmp[i]);
+    }
+    return out;
+}
+
+// ground truth .ibin: int32 N, int32 K, int32[N*K] (bd/load.py:43-58)
+inline std::vector<int32_t> read_ibin(const std::string& path, int32_t& N, int32_t& K)
+{
+    File f(path, "rb");
+    int32_t hdr[2];
+    f.read(hdr, sizeof(hdr), "header");
+    if (hdr[0] <= 0 || hdr[1] <= 0) throw std::runtime_error("bad header (N, K) in " + path);
+    N = hdr[0];
+    K = hdr[1];
+    std::vector<int32_t> v(static_cast<size_t>(N) * K);
+    f.read(v.data(), v.size() * 4, "payload");
+    return v;
+}
+
 }  // namespace gtann_io

@@ -23,6 +23,15 @@
 //       out[inv[i]][k] = inv[g[i][k]] (src/translate_ids.cpp).
 //   gtann knn -i DATA -o OUTDIR -k K
 //       exact self-excluded kNN (bd/build_knn.py) as vector_knn.bin/vector_dists.bin.
+//   gtann search --base B --query Q --index IDX --gt GT [--topk 10] [--ef 200]
+//         [--num-entry 4] [--normalize]
+//       beam search of every query and recall against the ground truth, as
+//       bd/search.cpp's `search` (options, file readers, entry draw with
+//       std::mt19937(42), recall definitions and report lines); the search
+//       itself is gt_search.  IDX: .npy (int64/int32/uint32) or a graph .bin.
+//   gtann compare --index1 A --index2 B [--k-cmp K] [--save-csv F]
+//       set-wise comparison of two indices (bd/search.cpp compare, with the
+//       per-node CSV of bd/search.py:238-262).
 //
 // Options of the reference that tune its host/out-of-core memory use are
 // accepted and ignored (the tables are resident in HBM).  Errors print
@@ -35,6 +44,8 @@
 
 #include <algorithm>
 #include <chrono>
+#include <random>
+#include <unordered_set>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -336,10 +347,227 @@ int cmd_knn(int argc, char** argv)
     return 0;
 }
 
+// Base / query files as bd/search.cpp:227-245 reads them: .u8bin and .i8bin
+// bytes as uint8, .ibin as int32 converted to float, anything else float32.
+struct SearchData {
+    int32_t N = 0, D = 0;
+    int dtype = GT_DTYPE_F32;
+    std::vector<uint8_t> u8;
+    std::vector<float> f32;
+    const void* data() const { return dtype == GT_DTYPE_U8 ? static_cast<const void*>(u8.data())
+                                                           : static_cast<const void*>(f32.data()); }
+    void to_float()
+    {
+        if (dtype == GT_DTYPE_F32) return;
+        f32.assign(u8.begin(), u8.end());
+        u8.clear();
+        dtype = GT_DTYPE_F32;
+    }
+};
+
+SearchData read_search_data(const std::string& path)
+{
+    SearchData s;
+    const std::string ext = ext_of(path);
+    File f(path, "rb");
+    int32_t hdr[2];
+    f.read(hdr, sizeof(hdr), "header");
+    if (hdr[0] <= 0 || hdr[1] <= 0) throw Exit{1, "bad header (N, D) in " + path};
+    s.N = hdr[0];
+    s.D = hdr[1];
+    const size_t n = static_cast<size_t>(s.N) * s.D;
+    if (ext == ".u8bin" || ext == ".i8bin") {
+        s.dtype = GT_DTYPE_U8;
+        s.u8.resize(n);
+        f.read(s.u8.data(), n, "payload");
+    } else if (ext == ".ibin") {
+        std::vector<int32_t> t(n);
+        f.read(t.data(), n * 4, "payload");
+        s.f32.assign(t.begin(), t.end());
+    } else {
+        s.f32.resize(n);
+        f.read(s.f32.data(), n * 4, "payload");
+    }
+    return s;
+}
+
+// rows scaled to unit length as bd/search.cpp:280-296 does
+void normalize_rows(SearchData& s)
+{
+    s.to_float();
+    for (int64_t i = 0; i < s.N; ++i) {
+        float* r = s.f32.data() + i * s.D;
+        float norm = 0.f;
+        for (int j = 0; j < s.D; ++j) norm += r[j] * r[j];
+        norm = std::sqrt(norm + 1e-12f);
+        for (int j = 0; j < s.D; ++j) r[j] /= norm;
+    }
+}
+
+std::vector<uint32_t> read_index(const std::string& path, int64_t N, int32_t& deg)
+{
+    std::vector<uint32_t> g;
+    if (ext_of(path) == ".npy") {
+        int64_t rows = 0, cols = 0;
+        const std::vector<int64_t> v = read_npy_2d(path, rows, cols);
+        if (rows != N) throw Exit{1, "Index N mismatch with base"};
+        g.resize(v.size());
+        for (size_t i = 0; i < v.size(); ++i)
+            g[i] = (v[i] >= 0 && v[i] < N) ? static_cast<uint32_t>(v[i]) : 0xFFFFFFFFu;
+        deg = static_cast<int32_t>(cols);
+    } else {
+        Table<uint32_t> t = read_table<uint32_t>(path);
+        if (t.N != N) throw Exit{1, "Index N mismatch with base"};
+        g = std::move(t.v);
+        deg = t.W;
+    }
+    return g;
+}
+
+int cmd_search(int argc, char** argv)
+{
+    Args a(argc, argv, {"base", "query", "index", "gt", "topk", "ef", "num-entry"}, {"normalize"});
+    const int topk = static_cast<int>(a.num("topk", 10));
+    int ef = static_cast<int>(a.num("ef", 200));
+    const int num_entry = static_cast<int>(a.num("num-entry", 4));
+    if (topk < 1 || num_entry < 1 || num_entry > 64) throw Exit{1, "need topk >= 1 and 1 <= num-entry <= 64"};
+    std::printf("[eval] Loading data...\n");
+    SearchData base = read_search_data(a.str("base"));
+    std::printf("  base shape: (%d, %d)\n", base.N, base.D);
+    SearchData Q = read_search_data(a.str("query"));
+    std::printf("  query shape: (%d, %d)\n", Q.N, Q.D);
+    if (Q.D != base.D) throw Exit{1, "Dimension mismatch between base and query"};
+    int32_t deg = 0;
+    const std::vector<uint32_t> g = read_index(a.str("index"), base.N, deg);
+    std::printf("  index shape: (%d, %d)\n", base.N, deg);
+    int32_t gt_nq = 0, k_gt = 0;
+    const std::vector<int32_t> gt = read_ibin(a.str("gt"), gt_nq, k_gt);
+    std::printf("  GT shape: (%d, %d)\n", gt_nq, k_gt);
+    if (gt_nq != Q.N) throw Exit{1, "GT nq mismatch with query"};
+    if (a.flag("normalize")) {
+        std::printf("[eval] L2-normalizing base & queries\n");
+        normalize_rows(base);
+        normalize_rows(Q);
+    }
+    if (base.dtype != Q.dtype) {   // one side .u8bin, the other float: search in float
+        base.to_float();
+        Q.to_float();
+    }
+    ef = std::max(ef, topk);
+    // entry points as bd/search.cpp:51-59 draws them: one generator for all
+    // queries, distinct ids in draw order
+    std::mt19937 rng(42);
+    std::uniform_int_distribution<int> pick(0, base.N - 1);
+    std::vector<int32_t> entries(static_cast<size_t>(Q.N) * num_entry, -1);
+    for (int32_t i = 0; i < Q.N; ++i) {
+        int n = 0;
+        for (int e = 0; e < num_entry; ++e) {
+            const int s = pick(rng);
+            int32_t* row = entries.data() + static_cast<size_t>(i) * num_entry;
+            if (std::find(row, row + n, s) == row + n) row[n++] = s;
+        }
+    }
+    std::printf("[eval] start searching ...\n");
+    std::fflush(stdout);
+    Lib L;
+    gt_search_params p;
+    gt_search_params_default(&p);
+    p.topk = topk;
+    p.ef = ef;
+    p.num_entry = num_entry;
+    std::vector<int32_t> ids(static_cast<size_t>(Q.N) * topk);
+    std::vector<float> d(ids.size());
+    gt_search_stats st{};
+    L.check(gt_search(L.ctx, base.data(), base.N, base.D, base.dtype, g.data(), deg, Q.data(), Q.N, entries.data(),
+                      num_entry, &p, ids.data(), d.data(), &st),
+            "gt_search");
+    // recall_vs_gt of bd/search.cpp:150-208
+    int hit_first = 0, hit_any = 0;
+    float total_overlap = 0.f;
+    for (int32_t i = 0; i < Q.N; ++i) {
+        const int32_t* pr = ids.data() + static_cast<size_t>(i) * topk;
+        const int32_t* gr = gt.data() + static_cast<size_t>(i) * k_gt;
+        if (gr[0] >= 0 && std::find(pr, pr + topk, gr[0]) != pr + topk) ++hit_first;
+        std::unordered_set<int32_t> gs;
+        for (int j = 0; j < k_gt; ++j)
+            if (gr[j] >= 0) gs.insert(gr[j]);
+        if (!gs.empty()) {
+            int h = 0;
+            for (int j = 0; j < topk; ++j) h += gs.count(pr[j]) ? 1 : 0;
+            if (h > 0) ++hit_any;
+        }
+        const int k = std::min({topk, static_cast<int>(gs.size()), static_cast<int>(k_gt)});
+        if (k > 0) {
+            std::unordered_set<int32_t> ps;
+            for (int j = 0; j < k; ++j)
+                if (pr[j] >= 0) ps.insert(pr[j]);
+            int ov = 0;
+            for (int32_t v : ps) ov += gs.count(v) ? 1 : 0;
+            total_overlap += ov / static_cast<float>(k);
+        }
+    }
+    const float nqf = static_cast<float>(Q.N > 0 ? Q.N : 1);
+    std::printf("\n======== Recall vs GT ========\n");
+    std::printf("Recall@%d (hit GT[:,0])         : %.6f\n", topk, hit_first / nqf);
+    std::printf("Recall@%d (hit any of GT[:,:]) : %.6f\n", topk, hit_any / nqf);
+    std::printf("Recall@%d (recall mean overlap): %.6f\n", topk, total_overlap / nqf);
+    std::printf("[eval] %d queries in %.3f s on the GPU (%.0f QPS), %.1f expansions per query\n", Q.N, st.t_search,
+                Q.N / std::max(st.t_search, 1e-9), st.expansions / static_cast<double>(std::max(Q.N, 1)));
+    return 0;
+}
+
+int cmd_compare(int argc, char** argv)
+{
+    Args a(argc, argv, {"index1", "index2", "k-cmp", "k_cmp", "save-csv", "save_csv"}, {});
+    int64_t Na = 0, Ma = 0, Nb = 0, Mb = 0;
+    const std::vector<int64_t> A = read_npy_2d(a.str("index1"), Na, Ma);
+    const std::vector<int64_t> B = read_npy_2d(a.str("index2"), Nb, Mb);
+    if (Na != Nb) throw Exit{1, "N mismatch between indices"};
+    const long long kc = a.has("k-cmp") ? a.num("k-cmp", -1) : a.num("k_cmp", -1);
+    int64_t k = kc > 0 ? kc : std::min(Ma, Mb);
+    k = std::min(k, std::min(Ma, Mb));
+    if (k <= 0) throw Exit{1, "k_cmp must be > 0"};
+    const std::string csv = a.has("save-csv") ? a.str("save-csv") : a.has("save_csv") ? a.str("save_csv") : "";
+    std::FILE* fc = nullptr;
+    if (!csv.empty()) {
+        fc = std::fopen(csv.c_str(), "w");
+        if (!fc) throw Exit{1, "cannot write " + csv};
+        std::fprintf(fc, "node,intersect_size,deg_A,deg_B,overlap\n");
+    }
+    int64_t hits_any = 0, set_equal = 0;
+    float total = 0.f;
+    for (int64_t i = 0; i < Na; ++i) {
+        std::unordered_set<int64_t> SA, SB;
+        for (int64_t j = 0; j < k; ++j) {
+            if (A[static_cast<size_t>(i * Ma + j)] >= 0) SA.insert(A[static_cast<size_t>(i * Ma + j)]);
+            if (B[static_cast<size_t>(i * Mb + j)] >= 0) SB.insert(B[static_cast<size_t>(i * Mb + j)]);
+        }
+        int64_t inter = 0;
+        for (int64_t v : SA) inter += SB.count(v) ? 1 : 0;
+        const float ov = inter / static_cast<float>(k);
+        total += ov;
+        if (inter >= 1) ++hits_any;
+        if (static_cast<int64_t>(SA.size()) == k && static_cast<int64_t>(SB.size()) == k && inter == k) ++set_equal;
+        if (fc) std::fprintf(fc, "%lld,%lld,%zu,%zu,%.6f\n", static_cast<long long>(i), static_cast<long long>(inter),
+                             SA.size(), SB.size(), ov);
+    }
+    if (fc) std::fclose(fc);
+    const float n = static_cast<float>(Na > 0 ? Na : 1);
+    std::printf("\n======= Index Comparison (set-wise) =======\n");
+    std::printf("N=%lld, k=%lld (A:%lld, B:%lld)\n", static_cast<long long>(Na), static_cast<long long>(k),
+                static_cast<long long>(Ma), static_cast<long long>(Mb));
+    std::printf("MeanOverlap@%lld (|A\u2229B|/k) : %.6f\n", static_cast<long long>(k), total / n);
+    std::printf("HitsAny@%lld               : %.6f\n", static_cast<long long>(k), hits_any / n);
+    std::printf("SetEqual@%lld              : %.6f\n", static_cast<long long>(k), set_equal / n);
+    if (!csv.empty()) std::printf("[compare] per-node stats saved to: %s\n", csv.c_str());
+    return 0;
+}
+
 void usage()
 {
     std::fprintf(stderr,
-                 "usage: gtann <bucket2|optimize|prune_windowed|optimize_chunked|translate_ids|knn> [options]\n");
+                 "usage: gtann <bucket2|optimize|prune_windowed|optimize_chunked|translate_ids|knn|search|compare> "
+                 "[options]\n");
 }
 
 }  // namespace
@@ -358,6 +586,8 @@ int main(int argc, char** argv)
         if (cmd == "optimize_chunked") return cmd_optimize_chunked(argc - 2, argv + 2);
         if (cmd == "translate_ids") return cmd_translate(argc - 2, argv + 2);
         if (cmd == "knn") return cmd_knn(argc - 2, argv + 2);
+        if (cmd == "search") return cmd_search(argc - 2, argv + 2);
+        if (cmd == "compare") return cmd_compare(argc - 2, argv + 2);
         usage();
         return 1;
     } catch (const Exit& e) {

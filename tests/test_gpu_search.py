@@ -5,6 +5,8 @@ Both sides accumulate each distance over the dimensions in order with fmaf,
 so ids, distances (bit for bit) and the number of expanded nodes agree on
 integer and on float data.
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -144,3 +146,70 @@ def test_invalid_arguments(ctx):
         ctx.search(X, g, Q, entries=np.zeros((2, 65), np.int32))
     with pytest.raises(gtann.GtannError):
         ctx.search(X, g, Q, visited_slots=1000)
+
+
+def _write_ibin(path, a):
+    a = np.ascontiguousarray(a, np.int32)
+    with open(path, "wb") as f:
+        np.array(a.shape, np.int32).tofile(f)
+        a.tofile(f)
+
+
+def _exact_gt(X, Q, k):
+    d = ((Q[:, None, :].astype(np.float64) - X[None, :, :].astype(np.float64)) ** 2).sum(-1)
+    return np.argsort(d, axis=1, kind="stable")[:, :k].astype(np.int32)
+
+
+def test_python_mirror_search_graph_recall(tmp_path, ctx):
+    """search.py search_graph_recall == the oracle run from the reference's own
+    entry draws (np.random.default_rng(42), bd/search.py:41-42,163)."""
+    import gtann_io as io
+    import search as S
+    rng = np.random.default_rng(9)
+    N, D, nq = 5000, 64, 200
+    X = rng.integers(0, 64, size=(N, D)).astype(np.float32)
+    Q = rng.integers(0, 64, size=(nq, D)).astype(np.float32)
+    g, _ = O.knn_exact(X, 24)
+    gt = _exact_gt(X, Q, 10)
+    io.write_dataset(str(tmp_path / "b.fbin"), X)
+    io.write_dataset(str(tmp_path / "q.fbin"), Q)
+    np.save(tmp_path / "idx.npy", g.astype(np.int64))
+    _write_ibin(tmp_path / "gt.ibin", gt)
+    got = S.search_graph_recall(str(tmp_path / "b.fbin"), str(tmp_path / "q.fbin"), str(tmp_path / "idx.npy"),
+                                str(tmp_path / "gt.ibin"), topk=10, ef=64, num_entry=4, ctx=ctx)
+    ent = S.draw_entries(np.random.default_rng(42), N, nq, 4)
+    rid, _, _ = O.search(X, g, Q, ent, 10, 64)
+    assert got == S.recall_vs_gt(rid.astype(np.int64), gt, 10)
+    # single-query form, same generator stream
+    r2 = np.random.default_rng(42)
+    i0, d0 = S.graph_search_single(Q[0], X, g, 10, 64, r2, num_entry=4, ctx=ctx)
+    np.testing.assert_array_equal(i0, rid[0][rid[0] >= 0])
+
+
+def test_cli_search(tmp_path):
+    import subprocess
+    import gtann_io as io
+    exe = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "gpu-talored-ann_amd", "bin",
+                       "gtann")
+    rng = np.random.default_rng(10)
+    N, D, nq = 1500, 32, 50
+    X = rng.standard_normal((N, D)).astype(np.float32)
+    Q = rng.standard_normal((nq, D)).astype(np.float32)
+    knn, _ = O.knn_exact(X, 15)
+    g = np.concatenate([knn, ((np.arange(N) + 1) % N)[:, None]], axis=1).astype(np.int64)   # connected
+    io.write_dataset(str(tmp_path / "b.fbin"), X)
+    io.write_dataset(str(tmp_path / "q.fbin"), Q)
+    np.save(tmp_path / "idx.npy", g)
+    _write_ibin(tmp_path / "gt.ibin", _exact_gt(X, Q, 10))
+
+    def run(ef):
+        r = subprocess.run([exe, "search", "--base", str(tmp_path / "b.fbin"), "--query", str(tmp_path / "q.fbin"),
+                            "--index", str(tmp_path / "idx.npy"), "--gt", str(tmp_path / "gt.ibin"), "--topk", "10",
+                            "--ef", str(ef), "--num-entry", "2"], capture_output=True, text=True, timeout=120)
+        assert r.returncode == 0, r.stderr + r.stdout
+        print(r.stdout)
+        return [float(ln.split(":")[-1]) for ln in r.stdout.splitlines() if ln.startswith("Recall@10")]
+
+    assert run(2000) == [1.0, 1.0, 1.0]      # ef >= N on a connected graph: exact
+    rec = run(48)
+    assert len(rec) == 3 and rec[2] > 0.8
