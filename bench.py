@@ -15,6 +15,14 @@ rocprofv3 FETCH_SIZE/WRITE_SIZE measurement of the same launches (see
 profiles/knn_fused_C2_build.md for the commands), when the configuration is
 C2 with the default knobs.
 
+`search` (after the build) runs the search entry point on workload S2 (the
+C2 shape with a 16-dimensional latent structure: a connected graph, unlike
+the clustered C mixtures, whose graphs split per cluster): the S2 graph is
+built with the same knobs, then 10,000 held-out queries, topk 10, 4 entry
+points, ef 64 and the reference CLI's 200; QPS from the device time of the
+search kernels, recall@10 against the exact top-10 among the base points,
+and the CPU restatement timed on a sample of the queries beside it.
+
     python bench.py [--gpus 1] [--steps 3] [--warmup 1] [--config C2]
 """
 import argparse
@@ -68,6 +76,60 @@ def cpu_baseline(X, knn_ids, K, n_sample):
     }
 
 
+def search_leg(ctx, torch, name, nq, kw, efs, cpu_sample):
+    """The search entry point on a graph built from workload `name`: nq
+    held-out queries of the same distribution, the reference CLI's topk 10 /
+    num_entry 4 (bd/search.py:280-283), recall@10 against the exact top-10
+    among the base points, device time of the search kernels from the
+    library; the CPU restatement (oracle/gt_oracle.c) timed on cpu_sample
+    queries at the largest ef."""
+    import synth
+    cfg = synth.CONFIGS[name]
+    X, Q = synth.generate(name, queries=nq)
+    Xd = torch.from_numpy(X).cuda()
+    graph = ctx.build_graph(Xd, n_buckets=cfg.buckets, M=cfg.M, K=cfg.K, metric=cfg.metric, **kw).graph
+    N, D = Xd.shape
+    nq = len(Q)
+    Qd = torch.from_numpy(Q).cuda()
+    qids = torch.arange(N, N + nq, device="cuda", dtype=torch.int64)
+    ex_i, _ = ctx.knn_exact(torch.cat([Xd, Qd]), 32, queries=qids, metric=cfg.metric)
+    ex = ex_i.cpu().numpy()
+    gt = [row[(row >= 0) & (row < N)][:10] for row in ex]
+    deg = int(graph.shape[1])
+    runs = []
+    for ef in efs:
+        ctx.search(Xd, graph, Qd, topk=10, ef=ef, num_entry=4, metric=cfg.metric)   # warm-up
+        ids, _, st = ctx.search(Xd, graph, Qd, topk=10, ef=ef, num_entry=4, metric=cfg.metric)
+        ids = ids.cpu().numpy()
+        rec = float(np.mean([len(np.intersect1d(ids[i], gt[i])) / 10 for i in range(nq)]))
+        # algorithmic bytes: one graph row per expansion, one fp32 row per distance
+        nbytes = st["expansions"] * deg * 4 + st["visited"] * D * 4 + nq * D * 4
+        runs.append({
+            "ef": ef, "qps": nq / st["t_search"], "ms": st["t_search"] * 1e3, "recall@10": rec,
+            "expansions_per_query": st["expansions"] / nq, "visited_per_query": st["visited"] / nq,
+            "requeued": st["requeued"],
+            "roofline": {"bound": "hbm", "achieved": nbytes / st["t_search"] / 1e9, "peak": 8000.0, "unit": "GB/s",
+                         "frac": nbytes / st["t_search"] / PEAK_HBM, "bytes": nbytes,
+                         "note": "one wave per query, latency-bound (serial best-first steps)"},
+        })
+        print(f"[bench] search ef={ef}: {runs[-1]['qps']:.0f} QPS, recall@10 {rec:.4f}", file=sys.stderr,
+              flush=True)
+    out = {"kernel": "graph_search_kernel", "workload": f"{name}: {N} x {D} {cfg.dtype}, graph degree {deg}",
+           "queries": nq, "topk": 10, "num_entry": 4, "runs": runs}
+    if cpu_sample:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import gt_oracle as O
+        rng = np.random.default_rng(2)
+        ent = rng.integers(0, N, size=(cpu_sample, 4)).astype(np.int32)
+        g = graph.cpu().numpy().view(np.uint32)
+        t0 = time.perf_counter()
+        O.search(X, g, Q[:cpu_sample], ent, 10, efs[-1], metric=1 if cfg.metric == "ip" else 0)
+        t = time.perf_counter() - t0
+        out["cpu_baseline"] = {"value": cpu_sample / t, "unit": "QPS", "cores": O.num_threads(), "kind": "port",
+                               "sample": f"{cpu_sample} queries at ef {efs[-1]}"}
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -82,6 +144,9 @@ def main():
                          "centroids, nprobe = ceil(20000 / avg bucket)")
     ap.add_argument("--cpu-sample", type=int, default=2000)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--search-queries", type=int, default=10000,
+                    help="held-out queries of the search leg (0 = skip it)")
+    ap.add_argument("--search-config", default="S2", help="workload of the search leg")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="run one device-to-device copy of this many MiB first (calibrates the "
                          "FETCH_SIZE/WRITE_SIZE counters of rocprofv3 --pmc against known bytes)")
@@ -206,6 +271,11 @@ def main():
                               "bytes": merge_bytes, "includes": "count + scan + scatter + merge"},
         "max_pool": int(s["max_pool"]), "max_bucket": int(s["max_bucket"]),
     }
+    if args.search_queries > 0:
+        del Xd, res
+        out["search"] = search_leg(ctx, torch, args.search_config, args.search_queries,
+                                   dict(rounds=args.rounds, kmeans_iters=args.kmeans_iters, nprobe=args.nprobe),
+                                   (64, 200), 0 if args.no_cpu else 500)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(X, knn, cfg.K, args.cpu_sample)
     ctx.close()

@@ -1057,6 +1057,7 @@ int gt_search(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtype, const
             float* od = c.in<float>(W_D, out_d, nr, false);
             int32_t* d_status = c.ws<int32_t>(W_FLAG, static_cast<size_t>(nq));
             int32_t* d_exp = c.ws<int32_t>(W_DEG, static_cast<size_t>(nq));
+            int32_t* d_vis = c.ws<int32_t>(W_CUR, static_cast<size_t>(nq));
 
             SearchArgs a{};
             a.X = Xm.data;
@@ -1078,18 +1079,21 @@ int gt_search(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtype, const
             a.out_d = od;
             a.status = d_status;
             a.expansions = d_exp;
-            // visited table: about 32 slots per result slot, within 64 KiB of LDS per query
+            a.visits = d_vis;
+            // visited table: a query visits up to about degree x ef points; the
+            // table holds 3/4 of its slots, within 64 KiB of LDS per query
             int H = p.visited_slots;
             if (H == 0) {
+                const int64_t want = static_cast<int64_t>(degree) * ef * 4 / 3;
                 H = 512;
-                while (H < 32 * ef && search_lds_bytes(a.CC, a.efr, a.Dp, 2 * H) <= 65536) H *= 2;
+                while (H < want && search_lds_bytes(a.CC, a.efr, a.Dp, 2 * H) <= 65536) H *= 2;
             }
             GT_REQUIRE(H >= 512 && (H & (H - 1)) == 0, "visited_slots must be a power of two >= 512");
             GT_REQUIRE(search_lds_bytes(a.CC, a.efr, a.Dp, H) <= 65536, "ef / dimension too large for one query's LDS");
             a.H = H;
             st.t_search = c.timed([&] { launch_graph_search(a, nq, c.s); });
 
-            std::vector<int32_t> hs(static_cast<size_t>(nq)), hx(static_cast<size_t>(nq));
+            std::vector<int32_t> hs(static_cast<size_t>(nq)), hx(static_cast<size_t>(nq)), hv(static_cast<size_t>(nq));
             c.d2h(hs.data(), d_status, hs.size() * sizeof(int32_t));
             c.sync();
             std::vector<int32_t> redo;
@@ -1121,10 +1125,12 @@ int gt_search(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtype, const
                 st.requeued = static_cast<int64_t>(redo.size());
             }
             c.d2h(hx.data(), d_exp, hx.size() * sizeof(int32_t));
+            c.d2h(hv.data(), d_vis, hv.size() * sizeof(int32_t));
             c.out(out_ids, oi, nr);
             c.out(out_d, od, nr);
             c.sync();
             for (int32_t x : hx) st.expansions += x;
+            for (int32_t x : hv) st.visited += x;
         }
         st.t_total = tt.sec();
         if (stats) *stats = st;

@@ -98,6 +98,7 @@ struct SearchArgs {
     float* out_d;             // (nq, topk)
     int32_t* status;          // (nq): 0 done, 1 visited table full, 2 candidate capacity exceeded
     int32_t* expansions;      // (nq)
+    int32_t* visits;          // (nq): points whose distance was computed
 };
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }

@@ -8,8 +8,9 @@
 //   * expand: lane j takes neighbour j of the popped row (rows longer than 64
 //     in chunks), drops ids outside [0, N) and repeats of an earlier lane in
 //     the same row, tests-and-sets the visited table, and computes the
-//     distance of its new point (one row per lane, dimensions in order with
-//     fmaf, so the value is the CPU restatement's bit for bit);
+//     distance of its new point (one row per lane, four fmaf chains by
+//     dimension mod 4, the CPU restatement's order, so the value is bit for
+//     bit the same);
 //   * best list: new points are applied in row order -- appended while the
 //     list is short, then each strictly closer point replaces the first slot
 //     holding the maximum (np.argmax), the maximum recomputed by a wave max
@@ -53,7 +54,6 @@ __global__ void __launch_bounds__(64) graph_search_kernel(SearchArgs a)
     uint32_t* bm = a.bitmap ? a.bitmap + static_cast<int64_t>(blockIdx.x) * a.bm_words : nullptr;
     const int hshift = a.H ? 32 - (31 - __clz(a.H)) : 0;
     const int hlimit = a.H - a.H / 4;
-    const int D4 = a.D >> 2;
 
     for (int64_t r = blockIdx.x; r < a.n_run; r += gridDim.x) {
         const int64_t q = a.q_list ? a.q_list[r] : r;
@@ -85,34 +85,40 @@ __global__ void __launch_bounds__(64) graph_search_kernel(SearchArgs a)
             wpos = static_cast<int>(~static_cast<uint32_t>(best));
         };
 
+        // Four partial sums, one per dimension mod 4 (the float4 lanes), over
+        // the zero-padded row (padding adds exact zeros), combined as
+        // (s0 + s1) + (s2 + s3).  Up to 32 float4 loads are issued before the
+        // first use, so a row of up to 128 dimensions costs one memory latency.
         auto distance = [&](uint32_t v) -> float {
-            const float* xr = a.X + static_cast<int64_t>(v) * a.Dp;
-            float s = 0.f;
-            if (a.metric == 0) {
-                for (int k = 0; k < D4; ++k) {
-                    const float4 x = reinterpret_cast<const float4*>(xr)[k];
-                    const float4 y = reinterpret_cast<const float4*>(qv)[k];
-                    float t = y.x - x.x; s = fmaf(t, t, s);
-                    t = y.y - x.y; s = fmaf(t, t, s);
-                    t = y.z - x.z; s = fmaf(t, t, s);
-                    t = y.w - x.w; s = fmaf(t, t, s);
+            const float4* xr = reinterpret_cast<const float4*>(a.X + static_cast<int64_t>(v) * a.Dp);
+            const float4* qr = reinterpret_cast<const float4*>(qv);
+            const int n4 = a.Dp >> 2;
+            float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+            for (int base = 0; base < n4; base += 32) {
+                float4 x[32];
+#pragma unroll
+                for (int k = 0; k < 32; ++k) x[k] = xr[min(base + k, n4 - 1)];
+#pragma unroll
+                for (int k = 0; k < 32; ++k) {
+                    const bool in = base + k < n4;
+                    const float4 y = qr[min(base + k, n4 - 1)];
+                    if (a.metric == 0) {
+                        const float t0 = in ? y.x - x[k].x : 0.f, t1 = in ? y.y - x[k].y : 0.f;
+                        const float t2 = in ? y.z - x[k].z : 0.f, t3 = in ? y.w - x[k].w : 0.f;
+                        s0 = fmaf(t0, t0, s0);
+                        s1 = fmaf(t1, t1, s1);
+                        s2 = fmaf(t2, t2, s2);
+                        s3 = fmaf(t3, t3, s3);
+                    } else {
+                        s0 = fmaf(in ? y.x : 0.f, x[k].x, s0);
+                        s1 = fmaf(in ? y.y : 0.f, x[k].y, s1);
+                        s2 = fmaf(in ? y.z : 0.f, x[k].z, s2);
+                        s3 = fmaf(in ? y.w : 0.f, x[k].w, s3);
+                    }
                 }
-                for (int k = 4 * D4; k < a.D; ++k) {
-                    const float t = qv[k] - xr[k];
-                    s = fmaf(t, t, s);
-                }
-                return s;
             }
-            for (int k = 0; k < D4; ++k) {
-                const float4 x = reinterpret_cast<const float4*>(xr)[k];
-                const float4 y = reinterpret_cast<const float4*>(qv)[k];
-                s = fmaf(y.x, x.x, s);
-                s = fmaf(y.y, x.y, s);
-                s = fmaf(y.z, x.z, s);
-                s = fmaf(y.w, x.w, s);
-            }
-            for (int k = 4 * D4; k < a.D; ++k) s = fmaf(qv[k], xr[k], s);
-            return -s;
+            const float s = (s0 + s1) + (s2 + s3);
+            return a.metric == 0 ? s : -s;
         };
 
         // Visits the ids held by the lanes in lane order (the reference's
@@ -257,6 +263,7 @@ __global__ void __launch_bounds__(64) graph_search_kernel(SearchArgs a)
         if (lane == 0) {
             a.status[q] = st;
             a.expansions[q] = nexp;
+            a.visits[q] = nvis;
         }
         if (bm) {
             for (int64_t k = lane; k < a.bm_words; k += 64) bm[k] = 0u;

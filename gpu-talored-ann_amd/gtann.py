@@ -65,7 +65,7 @@ class SearchParams(C.Structure):
 
 class SearchStats(C.Structure):
     _fields_ = [("t_total", C.c_double), ("t_search", C.c_double), ("expansions", C.c_int64),
-                ("requeued", C.c_int64)]
+                ("visited", C.c_int64), ("requeued", C.c_int64)]
 
     def as_dict(self):
         return {name: getattr(self, name) for name, _ in self._fields_}

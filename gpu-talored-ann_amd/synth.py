@@ -12,6 +12,14 @@ Parameters the benchmark description leaves open are fixed here:
   C4  1,000,000 x 960 fp32, 200 centres U[0,1]^960, sigma 0.1, L2, 512 buckets, 96 -> 48
   C5  10,000,000 x 128 int8, 4,096 centres U[-100,100]^128, sigma 15, rounded and
       clipped to [-127,127], L2, 2,048 buckets, 64 -> 32
+  S2  the search workload: 1,000,000 x 128 fp32 integer-valued, a 16-dimensional
+      latent Gaussian (sd 24 per latent axis) through a random orthonormal
+      128 x 16 map, plus N(0, 2^2) noise, centred at 128, rounded and clipped
+      to [0,255]; L2, 256 buckets, 64 -> 32.  The C configurations are
+      mixtures of well separated clusters, so any kNN-derived graph of them
+      splits into one component per cluster and a search from random entry
+      points only reaches its query's cluster by chance; S2 has the low
+      intrinsic dimension and the connected graph of real descriptor sets.
 
 Points are assigned to clusters uniformly at random.  `n` scales a
 configuration down (same recipe, first `n` points of the stream) for tests.
@@ -43,6 +51,7 @@ CONFIGS = {
     "C3": Config("C3", 1_000_000, 96, "ip", 256, 64, 32, "f32"),
     "C4": Config("C4", 1_000_000, 960, "l2", 512, 96, 48, "f32"),
     "C5": Config("C5", 10_000_000, 128, "l2", 2048, 64, 32, "i8"),
+    "S2": Config("S2", 1_000_000, 128, "l2", 256, 64, 32, "f32"),
 }
 
 
@@ -80,6 +89,15 @@ def generate(cfg: str, n: int | None = None, queries: int = 0):
     elif cfg == "C4":
         centres = rng.uniform(0, 1, size=(200, c.dim)).astype(np.float32)
         X = _mixture(rng, n + queries, centres, 0.1)
+    elif cfg == "S2":
+        basis, _ = np.linalg.qr(rng.standard_normal((c.dim, 16)))
+        basis = basis.astype(np.float32)
+        X = np.empty((n + queries, c.dim), np.float32)
+        for s in range(0, n + queries, 1 << 18):
+            e = min(n + queries, s + (1 << 18))
+            z = 24.0 * rng.standard_normal((e - s, 16), dtype=np.float32)
+            X[s:e] = 128.0 + z @ basis.T + 2.0 * rng.standard_normal((e - s, c.dim), dtype=np.float32)
+        X = np.clip(np.rint(X), 0, 255).astype(np.float32)
     elif cfg == "C5":
         centres = rng.uniform(-100, 100, size=(4096, c.dim)).astype(np.float32)
         X = np.clip(np.rint(_mixture(rng, n + queries, centres, 15.0)), -127, 127).astype(np.int8)

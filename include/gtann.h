@@ -186,6 +186,7 @@ typedef struct gt_search_stats {
     double t_total;         /* wall seconds of the whole call */
     double t_search;        /* search kernels (device time) */
     int64_t expansions;     /* nodes popped and expanded, all queries */
+    int64_t visited;        /* distances computed, all queries */
     int64_t requeued;       /* queries run a second time with the HBM bitmap */
 } gt_search_stats;
 

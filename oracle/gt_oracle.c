@@ -676,8 +676,10 @@ int or_num_threads(void)
  *   - output: the best list sorted by distance with ties in slot order (a
  *     stable argsort; the reference's np.argsort is numpy's unstable sort,
  *     :87-89), first topk, padded with (-1, +inf) (:171-174).
- * Distances: sum over dims of (q - x)^2 accumulated in dimension order with
- * fmaf (bd/search.py:12-14 l2sqr), or -sum q*x for the inner product.
+ * Distances: sum over dims of (q - x)^2 (bd/search.py:12-14 l2sqr), or
+ * -sum q*x for the inner product, as four fmaf partial sums by dimension
+ * mod 4 combined as (s0 + s1) + (s2 + s3) -- the GPU kernel's order (the
+ * reference's own order is its BLAS's).
  */
 typedef struct { float d; uint32_t id; } sc_t;
 
@@ -714,16 +716,18 @@ static sc_t sc_pop(sc_t* h, int64_t* n)
 
 static float search_dist(const float* q, const float* x, int64_t D, int metric)
 {
-    float s = 0.f;
-    if (metric == 1) {
-        for (int64_t k = 0; k < D; ++k) s = fmaf(q[k], x[k], s);
-        return -s;
-    }
+    /* four partial sums by dimension mod 4, combined as (s0 + s1) + (s2 + s3) */
+    float s[4] = {0.f, 0.f, 0.f, 0.f};
     for (int64_t k = 0; k < D; ++k) {
-        const float t = q[k] - x[k];
-        s = fmaf(t, t, s);
+        if (metric == 1) {
+            s[k & 3] = fmaf(q[k], x[k], s[k & 3]);
+        } else {
+            const float t = q[k] - x[k];
+            s[k & 3] = fmaf(t, t, s[k & 3]);
+        }
     }
-    return s;
+    const float r = (s[0] + s[1]) + (s[2] + s[3]);
+    return metric == 1 ? -r : r;
 }
 
 int or_search(const float* X, int64_t N, int64_t D, const uint32_t* graph, int deg, const float* Q, int64_t nq,

@@ -56,7 +56,7 @@ How each oracle function is pinned (what checks it besides itself):
   data with one entry point, where the two reference versions agree.  The
   reference's np.argsort order among equal distances and its BLAS float32
   summation order are "parity unpinned"; the oracle sorts ties by slot and
-  sums in dimension order.
+  sums in four partial sums by dimension mod 4 (the kernel's order).
 """
 from __future__ import annotations
 
