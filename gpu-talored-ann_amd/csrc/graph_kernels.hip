@@ -563,6 +563,52 @@ __global__ void check_hits_kernel(const uint32_t* __restrict__ hits, int64_t N, 
     if (e < N && hits[e] != 1u) atomicExch(err, 1);
 }
 
+// ------------------------------------------------------------------ reorder
+//
+// Reordered dataset: out row n = in row inv[n] (bucket-contiguous new ids,
+// src/bucket.cu:9253-9400).  One wave per row, 16-byte words when the row
+// length allows, else 4-byte words, else bytes.
+template <typename W>
+__global__ void __launch_bounds__(256) permute_rows_kernel(const W* __restrict__ in, const uint32_t* __restrict__ inv,
+                                                           int64_t N, int64_t words, W* __restrict__ out)
+{
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= N) return;
+    const uint32_t src = inv[row];
+    if (src >= static_cast<uint64_t>(N)) return;   // rejected by the permutation check
+    const W* a = in + static_cast<int64_t>(src) * words;
+    W* b = out + row * words;
+    for (int64_t k = lane; k < words; k += 64) b[k] = a[k];
+}
+
+// perm[inv[n]] = n, counting hits so that a non-permutation is reported
+__global__ void invert_perm_kernel(const uint32_t* __restrict__ inv, int64_t N, uint32_t* __restrict__ perm,
+                                   uint32_t* __restrict__ hits, int* __restrict__ err)
+{
+    const int64_t n = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (n >= N) return;
+    const uint32_t r = inv[n];
+    if (r >= static_cast<uint64_t>(N)) { atomicExch(err, 1); return; }
+    perm[r] = static_cast<uint32_t>(n);
+    atomicAdd(&hits[r], 1u);
+}
+
+// Table in new ids: out[n][k] = perm[ids[inv[n]][k]], -1 (any id outside
+// [0, N)) kept as -1.
+__global__ void remap_table_kernel(const int32_t* __restrict__ ids, const uint32_t* __restrict__ inv,
+                                   const uint32_t* __restrict__ perm, int64_t N, int M, int32_t* __restrict__ out)
+{
+    const int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (e >= N * M) return;
+    const int64_t n = e / M;
+    const int k = static_cast<int>(e - n * M);
+    const uint32_t src = inv[n];
+    if (src >= static_cast<uint64_t>(N)) return;
+    const int32_t v = ids[static_cast<int64_t>(src) * M + k];
+    out[e] = (v >= 0 && v < N) ? static_cast<int32_t>(perm[v]) : -1;
+}
+
 // ------------------------------------------------------------------ launchers
 
 static unsigned grid_for(int64_t n, int per_block)
@@ -685,6 +731,39 @@ void launch_merge_rounds(const int32_t* ri, const float* rd, const int32_t* ni, 
     GT_REQUIRE(M >= 1 && M <= kMergeMaxM, "merge supports list length <= 128");
     if (N <= 0) return;
     hipLaunchKernelGGL(merge_rounds_kernel, dim3(grid_for(N, 4)), dim3(256), 0, s, ri, rd, ni, nd, N, M, oi, od);
+    GT_HIP(hipGetLastError());
+}
+
+void launch_invert_perm(const uint32_t* inv, int64_t N, uint32_t* perm, uint32_t* hits, int* err, hipStream_t s)
+{
+    if (N <= 0) return;
+    hipLaunchKernelGGL(invert_perm_kernel, dim3(grid_for(N, 256)), dim3(256), 0, s, inv, N, perm, hits, err);
+    hipLaunchKernelGGL(check_hits_kernel, dim3(grid_for(N, 256)), dim3(256), 0, s, hits, N, err);
+    GT_HIP(hipGetLastError());
+}
+
+void launch_permute_rows(const void* in, const uint32_t* inv, int64_t N, int64_t row_bytes, void* out, hipStream_t s)
+{
+    if (N <= 0 || row_bytes <= 0) return;
+    const dim3 grid(grid_for(N, 4));
+    const uintptr_t al = reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(out);
+    if (row_bytes % 16 == 0 && al % 16 == 0)
+        hipLaunchKernelGGL(permute_rows_kernel<uint4>, grid, dim3(256), 0, s, static_cast<const uint4*>(in), inv, N,
+                           row_bytes / 16, static_cast<uint4*>(out));
+    else if (row_bytes % 4 == 0 && al % 4 == 0)
+        hipLaunchKernelGGL(permute_rows_kernel<uint32_t>, grid, dim3(256), 0, s, static_cast<const uint32_t*>(in),
+                           inv, N, row_bytes / 4, static_cast<uint32_t*>(out));
+    else
+        hipLaunchKernelGGL(permute_rows_kernel<uint8_t>, grid, dim3(256), 0, s, static_cast<const uint8_t*>(in), inv,
+                           N, row_bytes, static_cast<uint8_t*>(out));
+    GT_HIP(hipGetLastError());
+}
+
+void launch_remap_table(const int32_t* ids, const uint32_t* inv, const uint32_t* perm, int64_t N, int M, int32_t* out,
+                        hipStream_t s)
+{
+    if (N * M <= 0) return;
+    hipLaunchKernelGGL(remap_table_kernel, dim3(grid_for(N * M, 256)), dim3(256), 0, s, ids, inv, perm, N, M, out);
     GT_HIP(hipGetLastError());
 }
 

@@ -7,6 +7,7 @@
 #include "gtann_common.hpp"
 
 #include <algorithm>
+#include <atomic>
 #include <chrono>
 #include <cmath>
 #include <cstdio>
@@ -34,6 +35,10 @@ void launch_row_norms_i8(const int8_t* X, int64_t N, int Dp, float* norms, hipSt
 void launch_copy_ranges(const void* tasks, int64_t ntasks, const int32_t* members, int32_t* pool, hipStream_t s);
 void launch_negate(float* d, int64_t n, hipStream_t s);
 void launch_graph_search(const SearchArgs& a, int64_t grid, hipStream_t s);
+void launch_invert_perm(const uint32_t* inv, int64_t N, uint32_t* perm, uint32_t* hits, int* err, hipStream_t s);
+void launch_permute_rows(const void* in, const uint32_t* inv, int64_t N, int64_t row_bytes, void* out, hipStream_t s);
+void launch_remap_table(const int32_t* ids, const uint32_t* inv, const uint32_t* perm, int64_t N, int M, int32_t* out,
+                        hipStream_t s);
 size_t search_lds_bytes(int CC, int efr, int Dp, int H);
 void launch_sanitize(const int32_t* in, int64_t N, int M, uint32_t* out, hipStream_t s);
 void launch_cagra_prune(const int32_t* G, int64_t N, int M, int K, uint32_t* out, unsigned long long* bad_row,
@@ -697,7 +702,8 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
 
 // Centroids + probe table + two-choice assignment of one round.
 static void make_buckets(Ctx& c, const DevMatrix& X, int64_t C, int nprobe, int metric, float balance,
-                         int kmeans_iters, uint64_t seed, Buckets& b)
+                         int kmeans_iters, uint64_t seed, Buckets& b, std::vector<int32_t>* cknn = nullptr,
+                         int cknn_k = 0)
 {
     const int64_t N = X.N;
     Trace tr;
@@ -837,6 +843,27 @@ static void make_buckets(Ctx& c, const DevMatrix& X, int64_t C, int nprobe, int 
         c.sync();
     }
     tr.mark(c.s, "bucketing: probe table");
+    if (cknn && cknn_k > 0) {
+        // exact self-kNN of the centroids (self excluded), centroid indices
+        GT_REQUIRE(cknn_k <= C - 1 && cknn_k <= 128, "centroid_knn_k must be <= min(buckets - 1, 128)");
+        int32_t* d_ki = c.ws<int32_t>(W_PROBE_I, static_cast<size_t>(C) * cknn_k);
+        float* d_kd = c.ws<float>(W_PROBE_D, static_cast<size_t>(C) * cknn_k);
+        KnnJob j;
+        j.Q = &Cm;
+        j.P = &Cm;
+        j.nq = C;
+        j.np = C;
+        j.M = cknn_k;
+        j.metric = metric;
+        j.exclude_self = true;
+        j.out_pos = true;
+        j.out_ids = d_ki;
+        j.out_d = d_kd;
+        run_knn_flat(c, j, 1);
+        cknn->resize(static_cast<size_t>(C) * cknn_k);
+        c.d2h(cknn->data(), d_ki, cknn->size() * sizeof(int32_t));
+        c.sync();
+    }
 }
 
 // ---------------------------------------------------------------- graph stages
@@ -930,6 +957,54 @@ static int guarded(gt_ctx* ctx, F&& f)
     }
 }
 
+// Host-only entry points (bucket order / reorder) also run without a
+// context on host buffers; their errors then go to this thread's message,
+// which gt_last_error(NULL) returns.
+thread_local std::string g_host_err;
+
+template <typename F>
+static int guarded_host(gt_ctx* ctx, F&& f)
+{
+    if (ctx) return guarded(ctx, [&] { f(ctx); });
+    try {
+        g_host_err.clear();
+        f(nullptr);
+        return GT_OK;
+    } catch (const Error& e) {
+        g_host_err = e.what();
+        return e.code;
+    } catch (const std::exception& e) {
+        g_host_err = e.what();
+        return GT_EINVAL;
+    }
+}
+
+// copies between a caller buffer (host, or device when ctx is given) and host memory
+template <typename T>
+static void fetch_host(gt_ctx* ctx, T* dst, const T* src, size_t n)
+{
+    if (!n) return;
+    if (ctx && is_device_ptr(src)) {
+        Ctx c(ctx);
+        c.d2h(dst, src, n * sizeof(T));
+        c.sync();
+    } else {
+        std::memcpy(dst, src, n * sizeof(T));
+    }
+}
+template <typename T>
+static void store_host(gt_ctx* ctx, T* dst, const T* src, size_t n)
+{
+    if (!n) return;
+    if (ctx && is_device_ptr(dst)) {
+        Ctx c(ctx);
+        c.h2d(dst, src, n * sizeof(T));
+        c.sync();
+    } else {
+        std::memcpy(dst, src, n * sizeof(T));
+    }
+}
+
 extern "C" {
 
 const char* gt_version(void) { return "gtann-gfx950 0.1"; }
@@ -969,7 +1044,11 @@ void gt_destroy(gt_ctx* ctx)
     delete ctx;
 }
 
-const char* gt_last_error(const gt_ctx* ctx) { return ctx ? ctx->err.c_str() : "null context"; }
+const char* gt_last_error(const gt_ctx* ctx)
+{
+    if (ctx) return ctx->err.c_str();
+    return g_host_err.empty() ? "null context" : g_host_err.c_str();
+}
 
 void gt_build_params_default(gt_build_params* p)
 {
@@ -1446,6 +1525,276 @@ int gt_translate(gt_ctx* ctx, const uint32_t* g, const uint32_t* inv, int64_t N,
 int gt_build_graph(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtype, const gt_build_params* params,
                    int32_t* knn_ids, float* knn_dists, uint32_t* graph, gt_build_stats* stats)
 {
+    return gt_build_graph_ex(ctx, X, N, D, dtype, params, knn_ids, knn_dists, graph, stats, nullptr);
+}
+
+// Host-side DiskJoin processing order over a CSR bucket graph; the
+// candidates live in a max-heap on (score, id) with one entry per bucket,
+// updated in place as the window slides.
+namespace {
+class ScoreHeap {
+public:
+    explicit ScoreHeap(const std::vector<int64_t>& score) : sc_(score), at_(score.size(), -1) {}
+    bool empty() const { return h_.empty(); }
+    void touch(int32_t v)
+    {
+        if (at_[static_cast<size_t>(v)] < 0) {
+            at_[static_cast<size_t>(v)] = static_cast<int32_t>(h_.size());
+            h_.push_back(v);
+        }
+        up(at_[static_cast<size_t>(v)]);
+        down(at_[static_cast<size_t>(v)]);
+    }
+    int32_t pop()
+    {
+        const int32_t top = h_[0];
+        at_[static_cast<size_t>(top)] = -1;
+        const int32_t last = h_.back();
+        h_.pop_back();
+        if (!h_.empty()) {
+            h_[0] = last;
+            at_[static_cast<size_t>(last)] = 0;
+            down(0);
+        }
+        return top;
+    }
+
+private:
+    bool above(int32_t a, int32_t b) const   // a before b: larger score, then larger id
+    {
+        const int64_t x = sc_[static_cast<size_t>(a)], y = sc_[static_cast<size_t>(b)];
+        return x != y ? x > y : a > b;
+    }
+    void place(int32_t i, int32_t v)
+    {
+        h_[static_cast<size_t>(i)] = v;
+        at_[static_cast<size_t>(v)] = i;
+    }
+    void up(int32_t i)
+    {
+        const int32_t v = h_[static_cast<size_t>(i)];
+        while (i > 0) {
+            const int32_t p = (i - 1) / 2;
+            if (!above(v, h_[static_cast<size_t>(p)])) break;
+            place(i, h_[static_cast<size_t>(p)]);
+            i = p;
+        }
+        place(i, v);
+    }
+    void down(int32_t i)
+    {
+        const int32_t n = static_cast<int32_t>(h_.size());
+        const int32_t v = h_[static_cast<size_t>(i)];
+        for (;;) {
+            int32_t c = 2 * i + 1;
+            if (c >= n) break;
+            if (c + 1 < n && above(h_[static_cast<size_t>(c + 1)], h_[static_cast<size_t>(c)])) ++c;
+            if (!above(h_[static_cast<size_t>(c)], v)) break;
+            place(i, h_[static_cast<size_t>(c)]);
+            i = c;
+        }
+        place(i, v);
+    }
+    const std::vector<int64_t>& sc_;
+    std::vector<int32_t> at_;
+    std::vector<int32_t> h_;
+};
+}  // namespace
+
+static std::vector<int32_t> diskjoin_order(const uint32_t* g, int64_t B, int32_t K, int32_t window)
+{
+    std::vector<int32_t> order;
+    if (B <= 0) return order;
+    order.reserve(static_cast<size_t>(B));
+    window = std::max<int32_t>(1, window);
+    // out-neighbours (row order, repeats kept) and their reverse lists
+    std::vector<int64_t> ao(static_cast<size_t>(B + 1), 0), ro(static_cast<size_t>(B + 1), 0);
+    std::vector<int32_t> adj;
+    adj.reserve(static_cast<size_t>(B) * std::max(K, 0));
+    for (int64_t v = 0; v < B; ++v) {
+        for (int32_t k = 0; k < K; ++k) {
+            const uint32_t u = g[static_cast<size_t>(v) * K + k];
+            if (static_cast<int64_t>(u) != v && static_cast<int64_t>(u) < B) {
+                adj.push_back(static_cast<int32_t>(u));
+                ro[static_cast<size_t>(u) + 1]++;
+            }
+        }
+        ao[static_cast<size_t>(v) + 1] = static_cast<int64_t>(adj.size());
+    }
+    for (int64_t u = 0; u < B; ++u) ro[static_cast<size_t>(u) + 1] += ro[static_cast<size_t>(u)];
+    std::vector<int32_t> rev(adj.size());
+    {
+        std::vector<int64_t> cur(ro.begin(), ro.end() - 1);
+        for (int64_t v = 0; v < B; ++v)
+            for (int64_t e = ao[static_cast<size_t>(v)]; e < ao[static_cast<size_t>(v) + 1]; ++e)
+                rev[static_cast<size_t>(cur[static_cast<size_t>(adj[static_cast<size_t>(e)])]++)] = static_cast<int32_t>(v);
+    }
+    int32_t start = 0;
+    for (int64_t v = 1; v < B; ++v)
+        if (ao[static_cast<size_t>(v) + 1] - ao[static_cast<size_t>(v)] >
+            ao[static_cast<size_t>(start) + 1] - ao[static_cast<size_t>(start)])
+            start = static_cast<int32_t>(v);
+    std::vector<uint8_t> placed(static_cast<size_t>(B), 0);
+    std::vector<int64_t> score(static_cast<size_t>(B), 0);   // summed neighbour overlap with the window
+    ScoreHeap heap(score);
+    auto slide = [&](int32_t p, int64_t delta) {
+        for (int64_t e = ao[static_cast<size_t>(p)]; e < ao[static_cast<size_t>(p) + 1]; ++e) {
+            const int32_t u = adj[static_cast<size_t>(e)];
+            for (int64_t r = ro[static_cast<size_t>(u)]; r < ro[static_cast<size_t>(u) + 1]; ++r) {
+                const int32_t v = rev[static_cast<size_t>(r)];
+                if (placed[static_cast<size_t>(v)]) continue;
+                score[static_cast<size_t>(v)] += delta;
+                heap.touch(v);
+            }
+        }
+    };
+    int64_t lowest = 0;
+    auto put = [&](int32_t v) {
+        order.push_back(v);
+        placed[static_cast<size_t>(v)] = 1;
+        slide(v, +1);
+    };
+    put(start);
+    for (int64_t i = 1; i < B; ++i) {
+        if (i > window) slide(order[static_cast<size_t>(i - window - 1)], -1);
+        int32_t pick;
+        if (!heap.empty()) {
+            pick = heap.pop();
+        } else {
+            while (placed[static_cast<size_t>(lowest)]) ++lowest;
+            pick = static_cast<int32_t>(lowest);
+        }
+        put(pick);
+    }
+    return order;
+}
+
+int gt_bucket_order(gt_ctx* ctx, const uint32_t* graph, int64_t B, int32_t K, int32_t window, int32_t* order)
+{
+    return guarded_host(ctx, [&](gt_ctx* cx) {
+        GT_REQUIRE(order && B >= 0 && B < (int64_t(1) << 31) && K >= 0 && (B == 0 || K == 0 || graph),
+                   "bad arguments");
+        std::vector<uint32_t> hg(static_cast<size_t>(B) * static_cast<size_t>(K));
+        fetch_host(cx, hg.data(), graph, hg.size());
+        const std::vector<int32_t> o = diskjoin_order(hg.data(), B, K, window);
+        store_host(cx, order, o.data(), o.size());
+    });
+}
+
+int gt_bucket_reorder(gt_ctx* ctx, const int32_t* assignment, int64_t N, int64_t n_buckets, const int32_t* order,
+                      const int64_t* cids, int64_t n_cids, uint32_t* inverse_perm, uint32_t* bucket_offsets,
+                      uint32_t* cids_new)
+{
+    return guarded_host(ctx, [&](gt_ctx* cx) {
+        GT_REQUIRE(assignment && order && inverse_perm && bucket_offsets && N >= 1 && N < (int64_t(1) << 31) &&
+                       n_buckets >= 1 && n_buckets < (int64_t(1) << 31) && n_cids >= 0 &&
+                       (n_cids == 0 || (cids && cids_new)),
+                   "bad arguments");
+        std::vector<int32_t> ord(static_cast<size_t>(n_buckets)), asg(static_cast<size_t>(N));
+        fetch_host(cx, ord.data(), order, ord.size());
+        fetch_host(cx, asg.data(), assignment, asg.size());
+        // processing position of every bucket; order must be a permutation
+        std::vector<int32_t> pos(static_cast<size_t>(n_buckets), -1);
+        for (int64_t q = 0; q < n_buckets; ++q) {
+            const int32_t b = ord[static_cast<size_t>(q)];
+            GT_REQUIRE(b >= 0 && b < n_buckets && pos[static_cast<size_t>(b)] < 0,
+                       "order is not a permutation of the buckets");
+            pos[static_cast<size_t>(b)] = static_cast<int32_t>(q);
+        }
+        std::vector<int32_t> key(static_cast<size_t>(N));
+        std::atomic<int64_t> bad{-1};
+        parallel_slices(N, host_threads(), [&](int, int64_t lo, int64_t hi) {
+            for (int64_t i = lo; i < hi; ++i) {
+                const int32_t b = asg[static_cast<size_t>(i)];
+                if (b < 0 || b >= n_buckets) {
+                    bad = i;
+                    continue;
+                }
+                key[static_cast<size_t>(i)] = pos[static_cast<size_t>(b)];
+            }
+        });
+        GT_REQUIRE(bad.load() < 0, "point " + std::to_string(bad.load()) + " has no bucket in [0, n_buckets)");
+        // new ids: buckets in processing order, each bucket's points in old-id order
+        std::vector<int32_t> inv(static_cast<size_t>(N));
+        std::vector<int64_t> off;
+        counting_sort(nullptr, N, key.data(), n_buckets, inv.data(), off);
+        const std::vector<uint32_t> off32(off.begin(), off.end());
+        store_host(cx, inverse_perm, reinterpret_cast<const uint32_t*>(inv.data()), inv.size());
+        store_host(cx, bucket_offsets, off32.data(), off32.size());
+        if (n_cids > 0) {
+            std::vector<uint32_t> perm(static_cast<size_t>(N));
+            parallel_slices(N, host_threads(), [&](int, int64_t lo, int64_t hi) {
+                for (int64_t n = lo; n < hi; ++n)
+                    perm[static_cast<size_t>(inv[static_cast<size_t>(n)])] = static_cast<uint32_t>(n);
+            });
+            std::vector<int64_t> hc(static_cast<size_t>(n_cids));
+            fetch_host(cx, hc.data(), cids, hc.size());
+            std::vector<uint32_t> out(static_cast<size_t>(n_cids));
+            for (int64_t k = 0; k < n_cids; ++k) {
+                const int64_t o = hc[static_cast<size_t>(k)];
+                out[static_cast<size_t>(k)] = (o >= 0 && o < N) ? perm[static_cast<size_t>(o)] : 0xFFFFFFFFu;
+            }
+            store_host(cx, cids_new, out.data(), out.size());
+        }
+    });
+}
+
+// inverse_perm on the device, checked to be a permutation; perm (old -> new) on request
+static const uint32_t* checked_perm(Ctx& c, const uint32_t* inverse_perm, int64_t N, uint32_t** perm_out)
+{
+    const uint32_t* dinv = c.in<uint32_t>(W_CUR, inverse_perm, static_cast<size_t>(N));
+    uint32_t* perm = c.ws<uint32_t>(W_OFF, static_cast<size_t>(N));
+    uint32_t* hits = c.ws<uint32_t>(W_DEG, static_cast<size_t>(N));
+    int* err = c.ws<int>(W_FLAG, 1);
+    GT_HIP(hipMemsetAsync(hits, 0, static_cast<size_t>(N) * sizeof(uint32_t), c.s));
+    GT_HIP(hipMemsetAsync(err, 0, sizeof(int), c.s));
+    launch_invert_perm(dinv, N, perm, hits, err, c.s);
+    int h = 0;
+    c.d2h(&h, err, sizeof(int));
+    c.sync();
+    if (h) throw Error(GT_EINVAL, "inverse_perm is not a permutation of [0, N)");
+    if (perm_out) *perm_out = perm;
+    return dinv;
+}
+
+int gt_permute_rows(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtype, const uint32_t* inverse_perm,
+                    void* out)
+{
+    return guarded(ctx, [&] {
+        GT_REQUIRE(X && inverse_perm && out && N >= 1 && N < (int64_t(1) << 32) && D >= 1, "bad arguments");
+        GT_REQUIRE(dtype == GT_DTYPE_F32 || dtype == GT_DTYPE_U8 || dtype == GT_DTYPE_I8, "unknown dtype");
+        Ctx c(ctx);
+        const int64_t rb = static_cast<int64_t>(D) * static_cast<int64_t>(dtype_size(dtype));
+        const size_t bytes = static_cast<size_t>(N) * static_cast<size_t>(rb);
+        const uint32_t* dinv = checked_perm(c, inverse_perm, N, nullptr);
+        const uint8_t* dx = c.in<uint8_t>(W_XRAW, static_cast<const uint8_t*>(X), bytes);
+        uint8_t* o = c.in<uint8_t>(W_TMP, static_cast<uint8_t*>(out), bytes, false);
+        launch_permute_rows(dx, dinv, N, rb, o, c.s);
+        c.out(static_cast<uint8_t*>(out), o, bytes);
+        c.sync();
+    });
+}
+
+int gt_remap_table(gt_ctx* ctx, const int32_t* ids, int64_t N, int32_t M, const uint32_t* inverse_perm, int32_t* out)
+{
+    return guarded(ctx, [&] {
+        GT_REQUIRE(ids && inverse_perm && out && N >= 1 && N < (int64_t(1) << 31) && M >= 1, "bad arguments");
+        Ctx c(ctx);
+        const size_t nm = static_cast<size_t>(N) * M;
+        uint32_t* perm = nullptr;
+        const uint32_t* dinv = checked_perm(c, inverse_perm, N, &perm);
+        const int32_t* di = c.in<int32_t>(W_IN, ids, nm);
+        int32_t* o = c.in<int32_t>(W_OUT, out, nm, false);
+        launch_remap_table(di, dinv, perm, N, M, o, c.s);
+        c.out(out, o, nm);
+        c.sync();
+    });
+}
+
+int gt_build_graph_ex(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtype, const gt_build_params* params,
+                      int32_t* knn_ids, float* knn_dists, uint32_t* graph, gt_build_stats* stats,
+                      const gt_build_extras* extras)
+{
     return guarded(ctx, [&] {
         GT_REQUIRE(params && (graph || knn_ids || knn_dists), "bad arguments");
         gt_build_params p = *params;
@@ -1478,7 +1827,22 @@ int gt_build_graph(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtype, 
         b.members.swap(ctx->h_members);   // reuse the member list's host memory across builds
         for (int r = 0; r < p.rounds; ++r) {
             Timer tb;
-            make_buckets(c, Xm, C, nprobe, p.metric, p.balance, p.kmeans_iters, p.seed + static_cast<uint64_t>(r), b);
+            std::vector<int32_t> cknn;
+            const bool want_cknn = r == 0 && extras && extras->centroid_knn && extras->centroid_knn_k > 0;
+            make_buckets(c, Xm, C, nprobe, p.metric, p.balance, p.kmeans_iters, p.seed + static_cast<uint64_t>(r), b,
+                         want_cknn ? &cknn : nullptr, want_cknn ? extras->centroid_knn_k : 0);
+            if (r == 0 && extras) {
+                if (extras->round1_bucket) {
+                    const std::vector<int32_t>& bo = c.c->h_bucket_of;
+                    if (is_device_ptr(extras->round1_bucket)) c.h2d(extras->round1_bucket, bo.data(), bo.size() * sizeof(int32_t));
+                    else std::memcpy(extras->round1_bucket, bo.data(), bo.size() * sizeof(int32_t));
+                }
+                if (want_cknn) {
+                    if (is_device_ptr(extras->centroid_knn)) c.h2d(extras->centroid_knn, cknn.data(), cknn.size() * sizeof(int32_t));
+                    else std::memcpy(extras->centroid_knn, cknn.data(), cknn.size() * sizeof(int32_t));
+                }
+                c.sync();
+            }
             st.t_bucketing += tb.sec();
             if (p.reverse_edges) {
                 // the Python pipeline's round: full table, reverse edges, then the merge

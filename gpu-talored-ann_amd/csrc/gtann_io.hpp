@@ -187,6 +187,48 @@ inline void write_npy(const std::string& path, const T* v, int64_t rows, int64_t
     f.close();
 }
 
+// bucket_offsets.bin: int32 n_buckets, uint32[n_buckets + 1], indexed by
+// processing position (src/graph_io.hpp:13-17, 178-205)
+inline void write_bucket_offsets(const std::string& path, const uint32_t* off, int32_t n_buckets)
+{
+    File f(path, "wb");
+    f.write(&n_buckets, sizeof(n_buckets));
+    f.write(off, (static_cast<size_t>(n_buckets) + 1) * sizeof(uint32_t));
+    f.close();
+}
+
+inline std::vector<uint32_t> read_bucket_offsets(const std::string& path)
+{
+    File f(path, "rb");
+    int32_t n = 0;
+    f.read(&n, sizeof(n), "header");
+    if (n <= 0) throw std::runtime_error("bad bucket-offsets header: " + path);
+    std::vector<uint32_t> v(static_cast<size_t>(n) + 1);
+    f.read(v.data(), v.size() * sizeof(uint32_t), "payload");
+    return v;
+}
+
+// bucket_process_order.bin: int32 n, int32[n] = bucket id at each
+// processing position (src/graph_io.hpp:207-244)
+inline void write_bucket_process_order(const std::string& path, const int32_t* order, int32_t n)
+{
+    File f(path, "wb");
+    f.write(&n, sizeof(n));
+    f.write(order, static_cast<size_t>(n) * sizeof(int32_t));
+    f.close();
+}
+
+inline std::vector<int32_t> read_bucket_process_order(const std::string& path)
+{
+    File f(path, "rb");
+    int32_t n = 0;
+    f.read(&n, sizeof(n), "header");
+    if (n <= 0) throw std::runtime_error("bad bucket-process-order header: " + path);
+    std::vector<int32_t> v(static_cast<size_t>(n));
+    f.read(v.data(), v.size() * sizeof(int32_t), "payload");
+    return v;
+}
+
 // 2-D .npy of int64, int32 or uint32 (format 1.x/2.x, C order, little
 // endian), widened to int64: neighbors.npy and exact-kNN indices, the files
 // bd/load.hpp:103 (read_npy_int64_2d) reads.

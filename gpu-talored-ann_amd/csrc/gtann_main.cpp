@@ -3,14 +3,17 @@
 //
 //   gtann bucket2 -i BASE -o OUT [--centroid-ratio R] [--seed S] [--knn-k K]
 //         [--nprobe P] [--neighbors-m M] [-t T] [--fused-optimize-degree K]
-//         [--skip-dists] [--skip-npy] [--kmeans-iters I] [--balance F]
-//         [--refine-passes P] [--refine-sample S]
-//       the GPU-resident build (src/bucket.cu:9900-9990 options).  Writes, under
-//       OUT/k<knn-k>p<nprobe>m<M>t<T>/ (src/bucket.cu:8545-8556):
-//       vector_knn.bin, vector_dists.bin, neighbors.npy (int64), and with
-//       --fused-optimize-degree K > 0 final_graph.bin.  Ids are the input's
-//       own order: inverse_perm.bin is the identity and data_reordered<ext>
-//       links to the input, so the out-of-core tools below read them as usual.
+//         [--order-window W] [--skip-dists] [--skip-npy] [--kmeans-iters I]
+//         [--balance F] [--refine-passes P] [--refine-sample S]
+//       the GPU-resident build (src/bucket.cu:9900-9990 options) with the
+//       inline reorder of round 1 (src/bucket.cu:9160-9460): new ids are
+//       bucket-contiguous, buckets in the DiskJoin order of the round-1
+//       centroid kNN graph.  Writes, under OUT/k<knn-k>p<nprobe>m<M>t<T>/
+//       (src/bucket.cu:8545-8556): data_reordered<ext>, inverse_perm.bin,
+//       bucket_offsets.bin, bucket_process_order.bin, centroid_knn.bin,
+//       centroid_pool.bin (with --nprobe), vector_knn.bin, vector_dists.bin
+//       and neighbors.npy in new ids, and with --fused-optimize-degree K > 0
+//       final_graph.bin in the input's ids.
 //   gtann optimize -i DATA -g KNN -o OUT --output-degree K [--skip-sort]
 //       sanitize + CAGRA prune + reverse merge (src/optimize.cu); exit 2 when
 //       the device cannot hold the tables (the reference's "use the other
@@ -189,10 +192,10 @@ int cmd_bucket2(int argc, char** argv)
 {
     Args a(argc, argv,
            {"input,i", "output,o", "centroid-ratio", "seed", "knn-k", "nprobe", "neighbors-m", "iterations,t",
-            "fused-optimize-degree", "kmeans-iters", "balance", "refine-passes", "refine-sample"},
+            "fused-optimize-degree", "kmeans-iters", "balance", "refine-passes", "refine-sample", "order-window"},
            {"skip-dists", "skip-npy", "out-of-core"},
            {"cpu-limit", "gpu-limit", "bucket-vec-buffer", "sample-rate", "use-pq", "kmeans-train-fraction", "bucket-mem-mb",
-            "gpu-bucket-cache-mb", "pq-bits-start", "pq-bits-min", "search-iters", "order-window", "cache-mb"});
+            "gpu-bucket-cache-mb", "pq-bits-start", "pq-bits-min", "search-iters", "cache-mb"});
     const std::string in = a.str("input"), root = a.str("output");
     const int knn_k = static_cast<int>(a.num("knn-k", 32));
     const int np_arg = static_cast<int>(a.num("nprobe", 0));
@@ -200,9 +203,11 @@ int cmd_bucket2(int argc, char** argv)
     const int M = static_cast<int>(a.num("neighbors-m", 0));
     const int T = static_cast<int>(a.num("iterations", 1));
     const int K = static_cast<int>(a.num("fused-optimize-degree", 0));
+    const int ow_arg = static_cast<int>(a.num("order-window", 0));
     if (M <= 0) throw Exit{1, "--neighbors-m must be > 0 (this build always runs the per-vector kNN)"};
     if (nprobe > 256) throw Exit{1, "nprobe exceeds 256"};
     if (T < 1) throw Exit{1, "iterations must be >= 1"};
+    if (knn_k < 1) throw Exit{1, "--knn-k must be >= 1"};
     const double t0 = now();
     Dataset ds = read_dataset(in);
     const double t_read = now() - t0;
@@ -219,6 +224,12 @@ int cmd_bucket2(int argc, char** argv)
     p.balance = static_cast<float>(a.real("balance", p.balance));
     p.refine_passes = static_cast<int32_t>(a.num("refine-passes", 0));
     p.refine_sample = static_cast<int32_t>(a.num("refine-sample", p.refine_sample));
+    const int64_t C = std::min<int64_t>(p.n_buckets, ds.N);
+    // round-1 centroid self-kNN: knn-k columns for the processing order
+    // (centroid_knn.bin), nprobe columns for centroid_pool.bin when given
+    // (src/bucket.cu:8976-9001)
+    const int ck = std::max(knn_k, np_arg);
+    if (ck > C - 1) throw Exit{1, "knn-k / nprobe must be < the number of buckets (" + std::to_string(C) + ")"};
     const std::string dir = root + "/k" + std::to_string(knn_k) + "p" + std::to_string(nprobe) + "m" +
                             std::to_string(M) + "t" + std::to_string(T);
     mkdirs(dir);
@@ -227,31 +238,71 @@ int cmd_bucket2(int argc, char** argv)
     std::vector<int32_t> ids(nm);
     std::vector<float> dists(nm);
     std::vector<uint32_t> graph(K > 0 ? static_cast<size_t>(ds.N) * K : 0);
+    std::vector<int32_t> round1(static_cast<size_t>(ds.N));
+    std::vector<uint32_t> cknn(static_cast<size_t>(C) * ck);
+    gt_build_extras ex{};
+    ex.round1_bucket = round1.data();
+    ex.centroid_knn = cknn.data();
+    ex.centroid_knn_k = ck;
     gt_build_stats st;
     Lib L;
-    L.check(gt_build_graph(L.ctx, ds.data(), ds.N, ds.D, dtype_code(ds.elem), &p, ids.data(), dists.data(),
-                           K > 0 ? graph.data() : nullptr, &st),
-            "gt_build_graph");
+    L.check(gt_build_graph_ex(L.ctx, ds.data(), ds.N, ds.D, dtype_code(ds.elem), &p, ids.data(), dists.data(),
+                              K > 0 ? graph.data() : nullptr, &st, &ex),
+            "gt_build_graph_ex");
+
+    // inline reorder of round 1 (src/bucket.cu:9160-9460): buckets in the
+    // DiskJoin order of the centroid graph, new ids bucket-contiguous
     const double t1 = now();
-    write_table<int32_t>(dir + "/vector_knn.bin", ids.data(), ds.N, M);
-    if (!a.flag("skip-dists")) write_table<float>(dir + "/vector_dists.bin", dists.data(), ds.N, M);
+    auto columns = [&](int w) {
+        std::vector<uint32_t> g(static_cast<size_t>(C) * w);
+        for (int64_t c = 0; c < C; ++c)
+            std::copy(cknn.begin() + c * ck, cknn.begin() + c * ck + w, g.begin() + c * w);
+        return g;
+    };
+    const std::vector<uint32_t> cgraph = columns(knn_k);
+    const int window = ow_arg > 0 ? ow_arg : std::max(4 * knn_k, 16);
+    std::vector<int32_t> order(static_cast<size_t>(C));
+    L.check(gt_bucket_order(L.ctx, cgraph.data(), C, knn_k, window, order.data()), "gt_bucket_order");
+    std::vector<uint32_t> inv(static_cast<size_t>(ds.N)), offsets(static_cast<size_t>(C) + 1);
+    L.check(gt_bucket_reorder(L.ctx, round1.data(), ds.N, C, order.data(), nullptr, 0, inv.data(), offsets.data(),
+                              nullptr),
+            "gt_bucket_reorder");
+    std::vector<uint8_t> reordered(ds.bytes.size());
+    L.check(gt_permute_rows(L.ctx, ds.data(), ds.N, ds.D, dtype_code(ds.elem), inv.data(), reordered.data()),
+            "gt_permute_rows");
+    std::vector<int32_t> ids_new(nm);
+    L.check(gt_remap_table(L.ctx, ids.data(), ds.N, M, inv.data(), ids_new.data()), "gt_remap_table");
+    const double t_reorder = now() - t1;
+
+    const double t2 = now();
+    write_dataset(dir + "/data_reordered" + ext_of(in), reordered.data(), ds.N, ds.D, ds.elem);
+    write_inverse_perm(dir + "/inverse_perm.bin", inv.data(), ds.N);
+    write_bucket_offsets(dir + "/bucket_offsets.bin", offsets.data(), static_cast<int32_t>(C));
+    write_bucket_process_order(dir + "/bucket_process_order.bin", order.data(), static_cast<int32_t>(C));
+    write_table<uint32_t>(dir + "/centroid_knn.bin", cgraph.data(), C, knn_k);
+    if (np_arg > 0) {
+        const std::vector<uint32_t> pool = columns(np_arg);
+        write_table<uint32_t>(dir + "/centroid_pool.bin", pool.data(), C, np_arg);
+    }
+    write_table<int32_t>(dir + "/vector_knn.bin", ids_new.data(), ds.N, M);
+    if (!a.flag("skip-dists")) {
+        std::vector<float> d_new(nm);
+        L.check(gt_permute_rows(L.ctx, dists.data(), ds.N, M, GT_DTYPE_F32, inv.data(), d_new.data()),
+                "gt_permute_rows");
+        write_table<float>(dir + "/vector_dists.bin", d_new.data(), ds.N, M);
+    }
     if (!a.flag("skip-npy")) {
-        const std::vector<int64_t> w = widen(ids.data(), ids.size());
+        const std::vector<int64_t> w = widen(ids_new.data(), ids_new.size());
         write_npy<int64_t>(dir + "/neighbors.npy", w.data(), ds.N, M);
     }
-    if (K > 0) write_table<uint32_t>(dir + "/final_graph.bin", graph.data(), ds.N, K);
-    std::vector<uint32_t> ident(static_cast<size_t>(ds.N));
-    for (size_t i = 0; i < ident.size(); ++i) ident[i] = static_cast<uint32_t>(i);
-    write_inverse_perm(dir + "/inverse_perm.bin", ident.data(), ds.N);
-    const std::string link = dir + "/data_reordered" + ext_of(in);
-    unlink(link.c_str());
-    if (symlink(abs_path(in).c_str(), link.c_str()) != 0) std::fprintf(stderr, "[warn] cannot link %s\n", link.c_str());
-    const double t_write = now() - t1;
-    std::printf("[bucket2] N=%d D=%d buckets=%d nprobe=%d M=%d K=%d t=%d\n", ds.N, ds.D, p.n_buckets, nprobe, M, K, T);
+    if (K > 0) write_table<uint32_t>(dir + "/final_graph.bin", graph.data(), ds.N, K);   // original ids
+    const double t_write = now() - t2;
+    std::printf("[bucket2] N=%d D=%d buckets=%lld nprobe=%d M=%d K=%d t=%d order-window=%d\n", ds.N, ds.D,
+                static_cast<long long>(C), nprobe, M, K, T, window);
     std::printf("[bucket2] read %.3f s  build %.3f s (bucketing %.3f, knn %.3f, merge %.3f, refine %.3f, prune %.3f, "
-                "revmerge %.3f)  write %.3f s\n",
+                "revmerge %.3f)  reorder %.3f s  write %.3f s\n",
                 t_read, st.t_total, st.t_bucketing, st.t_knn, st.t_merge, st.t_refine, st.t_prune, st.t_revmerge,
-                t_write);
+                t_reorder, t_write);
     return 0;
 }
 

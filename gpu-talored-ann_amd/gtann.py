@@ -25,7 +25,8 @@ EXPORTS = (
     "gt_create", "gt_destroy", "gt_last_error", "gt_version", "gt_knn_exact", "gt_assign_top2",
     "gt_knn_bucketed", "gt_merge_rounds", "gt_refine_2hop", "gt_sanitize", "gt_cagra_prune",
     "gt_reverse_merge", "gt_optimize", "gt_translate", "gt_build_params_default", "gt_build_graph",
-    "gt_prune_occlusion", "gt_reverse_insert", "gt_search_params_default", "gt_search",
+    "gt_prune_occlusion", "gt_reverse_insert", "gt_search_params_default", "gt_search", "gt_build_graph_ex",
+    "gt_bucket_order", "gt_bucket_reorder", "gt_permute_rows", "gt_remap_table",
 )
 
 
@@ -54,6 +55,11 @@ class BuildStats(C.Structure):
 
     def as_dict(self):
         return {name: getattr(self, name) for name, _ in self._fields_}
+
+
+class BuildExtras(C.Structure):
+    _fields_ = [("round1_bucket", C.c_void_p), ("centroid_knn", C.c_void_p), ("centroid_knn_k", C.c_int32),
+                ("reserved_", C.c_int32)]
 
 
 class SearchParams(C.Structure):
@@ -104,6 +110,12 @@ def lib():
         L.gt_build_params_default.restype = None
         L.gt_build_graph.argtypes = [vp, vp, i64, i32, C.c_int, C.POINTER(BuildParams), vp, vp, vp,
                                      C.POINTER(BuildStats)]
+        L.gt_build_graph_ex.argtypes = [vp, vp, i64, i32, C.c_int, C.POINTER(BuildParams), vp, vp, vp,
+                                        C.POINTER(BuildStats), C.POINTER(BuildExtras)]
+        L.gt_bucket_order.argtypes = [vp, vp, i64, i32, i32, vp]
+        L.gt_bucket_reorder.argtypes = [vp, vp, i64, i64, vp, vp, i64, vp, vp, vp]
+        L.gt_permute_rows.argtypes = [vp, vp, i64, i32, C.c_int, vp, vp]
+        L.gt_remap_table.argtypes = [vp, vp, i64, i32, vp, vp]
         L.gt_search_params_default.argtypes = [C.POINTER(SearchParams)]
         L.gt_search_params_default.restype = None
         L.gt_search.argtypes = [vp, vp, i64, i32, C.c_int, vp, i32, vp, i64, vp, i32, C.POINTER(SearchParams),
@@ -164,6 +176,40 @@ class BuildResult:
     knn_ids: object
     knn_dists: object
     stats: dict
+    round1_bucket: object = None
+    centroid_knn: object = None
+
+
+def _host_check(rc, what):
+    if rc != GT_OK:
+        msg = lib().gt_last_error(None)
+        raise GtannError(rc, f"{what}: {msg.decode() if msg else ''}")
+
+
+def bucket_order(graph, window):
+    """DiskJoin processing order of the flat (B, K) bucket graph
+    (src/bucket_order.hpp:161-262); host-side, no GPU needed."""
+    g = _np(graph, np.uint32)
+    B, K = g.shape
+    out = np.empty(B, np.int32)
+    _host_check(lib().gt_bucket_order(None, _ptr(g), B, K, int(window), _ptr(out)), "gt_bucket_order")
+    return out
+
+
+def bucket_reorder(assignment, n_buckets, order, cids=None):
+    """(inverse_perm uint32 (N,), bucket_offsets uint32 (n_buckets + 1,),
+    new ids of `cids` or None) -- compute_bucket_reorder
+    (src/bucket.cu:8363-8412); host-side, no GPU needed."""
+    a = _np(assignment, np.int32)
+    o = _np(order, np.int32)
+    N = len(a)
+    inv = np.empty(N, np.uint32)
+    off = np.empty(n_buckets + 1, np.uint32)
+    c = None if cids is None else _np(cids, np.int64)
+    cn = None if c is None else np.empty(len(c), np.uint32)
+    _host_check(lib().gt_bucket_reorder(None, _ptr(a), N, n_buckets, _ptr(o), _ptr(c), 0 if c is None else len(c),
+                                        _ptr(inv), _ptr(off), _ptr(cn)), "gt_bucket_reorder")
+    return inv, off, cn
 
 
 class Context:
@@ -326,7 +372,7 @@ class Context:
 
     def build_graph(self, X, *, n_buckets=0, nprobe=1, M=64, K=32, rounds=2, refine_passes=0, refine_sample=16,
                     kmeans_iters=3, balance=0.8, seed=42, metric="l2", return_knn=True, reverse_edges=False,
-                    prune=True):
+                    prune=True, centroid_knn_k=0, round1_bucket=False):
         if not _is_torch(X):
             X = np.ascontiguousarray(X)
         N, D = X.shape
@@ -339,11 +385,44 @@ class Context:
         ids = _empty_like_input(X, (N, M), np.int32) if return_knn else None
         d = _empty_like_input(X, (N, M), np.float32) if return_knn else None
         st = BuildStats()
-        self._check(lib().gt_build_graph(self._h, _ptr(X), N, D, _dtype_code(X), C.byref(p), _ptr(ids), _ptr(d),
-                                         _ptr(graph), C.byref(st)), "gt_build_graph")
+        ex = BuildExtras()
+        nb = min(max(1, n_buckets if n_buckets > 0 else N // 4000), N)
+        r1 = np.empty(N, np.int32) if round1_bucket else None
+        ck = np.empty((nb, centroid_knn_k), np.uint32) if centroid_knn_k > 0 else None
+        ex.round1_bucket = None if r1 is None else r1.ctypes.data
+        ex.centroid_knn = None if ck is None else ck.ctypes.data
+        ex.centroid_knn_k = centroid_knn_k
+        self._check(lib().gt_build_graph_ex(self._h, _ptr(X), N, D, _dtype_code(X), C.byref(p), _ptr(ids), _ptr(d),
+                                            _ptr(graph), C.byref(st), C.byref(ex)), "gt_build_graph_ex")
         if graph is not None and not _is_torch(graph):
             graph = graph.view(np.uint32)
-        return BuildResult(graph=graph, knn_ids=ids, knn_dists=d, stats=st.as_dict())
+        return BuildResult(graph=graph, knn_ids=ids, knn_dists=d, stats=st.as_dict(), round1_bucket=r1,
+                           centroid_knn=ck)
+
+    def permute_rows(self, X, inverse_perm):
+        """out row n = X row inverse_perm[n] (data_reordered)."""
+        if not _is_torch(X):
+            X = np.ascontiguousarray(X)
+        N, D = X.shape
+        inv = _np(inverse_perm, np.uint32)
+        out = np.empty_like(X) if not _is_torch(X) else X.new_empty(X.shape)
+        if _is_torch(X):
+            import torch
+            codes = {torch.float32: 0, torch.uint8: 1, torch.int8: 2}
+        else:
+            codes = {np.dtype(np.float32): 0, np.dtype(np.uint8): 1, np.dtype(np.int8): 2}
+        self._check(lib().gt_permute_rows(self._h, _ptr(X), N, D, codes[X.dtype], _ptr(inv), _ptr(out)),
+                    "gt_permute_rows")
+        return out
+
+    def remap_table(self, ids, inverse_perm):
+        """Per-point id table in new ids: out[n] = perm[ids[inverse_perm[n]]]."""
+        ids = _np(ids, np.int32)
+        N, M = ids.shape
+        inv = _np(inverse_perm, np.uint32)
+        out = np.empty_like(ids)
+        self._check(lib().gt_remap_table(self._h, _ptr(ids), N, M, _ptr(inv), _ptr(out)), "gt_remap_table")
+        return out
 
     def search(self, X, graph, Q, *, topk=10, ef=200, num_entry=4, entries=None, metric="l2", seed=42,
                visited_slots=0):

@@ -14,6 +14,9 @@ Byte layouts, identical with the reference's files:
   (src/graph_io.hpp:8-11, 50-96).
 * ``inverse_perm.bin``: raw ``uint32[N]`` (src/graph_io.hpp:369-377).
 * ground truth ``.ibin``: ``int32 N, int32 K, int32[N*K]`` (bd/load.py:43-58).
+* ``bucket_offsets.bin``: ``int32 n_buckets, uint32[n_buckets+1]`` and
+  ``bucket_process_order.bin``: ``int32 n, int32[n]`` (src/graph_io.hpp:178-244);
+  ``centroid_knn.bin`` / ``centroid_pool.bin`` use the graph layout.
 """
 from __future__ import annotations
 
@@ -128,3 +131,39 @@ def read_ibin(path: str) -> np.ndarray:
     if a.size != N * K:
         raise ValueError(f"size mismatch for ibin: {path}")
     return a.reshape(N, K)
+
+
+def write_bucket_offsets(path: str, off: np.ndarray) -> None:
+    off = np.ascontiguousarray(off, dtype=np.uint32)
+    with open(path, "wb") as f:
+        f.write(struct.pack("<i", len(off) - 1))
+        off.tofile(f)
+
+
+def read_bucket_offsets(path: str) -> np.ndarray:
+    with open(path, "rb") as f:
+        (n,) = _read_header(f, "i", path)
+        if n <= 0:
+            raise ValueError(f"bad bucket-offsets header: {path}")
+        a = np.fromfile(f, dtype=np.uint32, count=n + 1)
+    if a.size != n + 1:
+        raise ValueError(f"short payload: {path}")
+    return a
+
+
+def write_bucket_process_order(path: str, order: np.ndarray) -> None:
+    order = np.ascontiguousarray(order, dtype=np.int32)
+    with open(path, "wb") as f:
+        f.write(struct.pack("<i", len(order)))
+        order.tofile(f)
+
+
+def read_bucket_process_order(path: str) -> np.ndarray:
+    with open(path, "rb") as f:
+        (n,) = _read_header(f, "i", path)
+        if n <= 0:
+            raise ValueError(f"bad bucket-process-order header: {path}")
+        a = np.fromfile(f, dtype=np.int32, count=n)
+    if a.size != n:
+        raise ValueError(f"short payload: {path}")
+    return a

@@ -36,6 +36,9 @@ enum { GT_METRIC_L2 = 0, GT_METRIC_IP = 1 };
  * (src/bucket.cu:5216-5241, :5650) and the cuVS raft::resources handle. */
 int gt_create(int device, gt_ctx** out);
 void gt_destroy(gt_ctx* ctx);
+/* The message of the context's last error; with ctx NULL, that of this
+ * thread's last failed host-only call (gt_bucket_order, gt_bucket_reorder,
+ * which accept a NULL context for host buffers), else "null context". */
 const char* gt_last_error(const gt_ctx* ctx);
 const char* gt_version(void);
 
@@ -168,6 +171,56 @@ void gt_build_params_default(gt_build_params* p);
 int gt_build_graph(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtype,
                    const gt_build_params* params, int32_t* knn_ids, float* knn_dists,
                    uint32_t* graph, gt_build_stats* stats);
+
+/* Optional outputs of gt_build_graph_ex about round 1, from which bucket2's
+ * reorder artifacts are made.  C = the bucket count (params->n_buckets, or
+ * N / 4000 when 0, clamped to [1, N]). */
+typedef struct gt_build_extras {
+    int32_t* round1_bucket;   /* N, or NULL: round-1 bucket of every point */
+    uint32_t* centroid_knn;   /* C x centroid_knn_k, or NULL: exact self-kNN of the round-1
+                                 centroids (self excluded, ascending distance), as
+                                 centroid_self_knn_bf (src/bucket.cu:3241, 8976-8986) */
+    int32_t centroid_knn_k;   /* <= min(C - 1, 128) */
+    int32_t reserved_;
+} gt_build_extras;
+
+/* gt_build_graph plus the round-1 extras (NULL = none). */
+int gt_build_graph_ex(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtype,
+                      const gt_build_params* params, int32_t* knn_ids, float* knn_dists,
+                      uint32_t* graph, gt_build_stats* stats, const gt_build_extras* extras);
+
+/* DiskJoin bucket processing order over the flat (B x K) bucket graph
+ * (entries equal to the row or >= B are dropped): start at the bucket of
+ * largest out-degree (ties: smallest id), then repeatedly place the
+ * unplaced bucket, among those sharing a neighbour with the last `window`
+ * placed ones, of largest summed neighbour overlap with them (ties: larger
+ * id), else the smallest unplaced id.  Host-side.  Replaces
+ * bucket_order::compute_bucket_processing_order(adjacency_from_flat_graph(...))
+ * (src/bucket_order.hpp:161-238, 247-262). */
+int gt_bucket_order(gt_ctx* ctx, const uint32_t* graph, int64_t B, int32_t K, int32_t window, int32_t* order);
+/* (ctx may be NULL for host buffers, here and in gt_bucket_reorder.) */
+
+/* New-id layout of round-1 buckets in processing order: inverse_perm (N,
+ * new id -> old id: each bucket's points in increasing old id, buckets in
+ * `order`), bucket_offsets (n_buckets + 1, by processing position) and, for
+ * n_cids given old ids (e.g. centroid rows), their new ids (or NULL).
+ * Every point must have a bucket in [0, n_buckets).  Host-side.  Replaces
+ * compute_bucket_reorder (src/bucket.cu:8363-8412). */
+int gt_bucket_reorder(gt_ctx* ctx, const int32_t* assignment, int64_t N, int64_t n_buckets, const int32_t* order,
+                      const int64_t* cids, int64_t n_cids, uint32_t* inverse_perm, uint32_t* bucket_offsets,
+                      uint32_t* cids_new);
+
+/* Rows in new-id order: out row n = X row inverse_perm[n] (dtype element
+ * size x D bytes per row); data_reordered.<ext> (src/bucket.cu:9253-9400).
+ * Also reorders any per-point table (e.g. vector_dists.bin rows as F32, D = M). */
+int gt_permute_rows(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtype, const uint32_t* inverse_perm,
+                    void* out);
+
+/* A per-point id table in new ids: out[n][k] = perm[ids[inverse_perm[n]][k]]
+ * with perm the inverse permutation; ids outside [0, N) become -1 (the
+ * vector_knn.bin of the reordered coordinate system). */
+int gt_remap_table(gt_ctx* ctx, const int32_t* ids, int64_t N, int32_t M, const uint32_t* inverse_perm,
+                   int32_t* out);
 
 /* Beam (ef) search.  Defaults (gt_search_params_default) are the reference
  * CLI's: topk 10, ef 200, num_entry 4 (bd/search.py:280-283), L2, seed 42. */

@@ -813,3 +813,33 @@ int or_search(const float* X, int64_t N, int64_t D, const uint32_t* graph, int d
     }
     return err;
 }
+
+/* ------------------------------------------------------------- bucket reorder
+ * compute_bucket_reorder (src/bucket.cu:8363-8412): bucket b's range of new
+ * ids starts after the points of every bucket placed before it in `order`;
+ * old ids are dealt in increasing order to their bucket's next new id.
+ * inverse_perm[new] = old, offsets[pos + 1] = end of position pos's range.
+ * Points without a bucket in [0, nb) are skipped (the reference counts them
+ * as unassigned); returns the number placed.
+ */
+int64_t or_bucket_reorder(const int32_t* assign, int64_t N, int64_t nb, const int32_t* order, uint32_t* inverse_perm,
+                          uint32_t* offsets)
+{
+    int64_t* count = (int64_t*)calloc((size_t)nb, sizeof(int64_t));
+    uint32_t* cursor = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)nb);
+    if (!count || !cursor) { free(count); free(cursor); return OR_ENOMEM; }
+    for (int64_t i = 0; i < N; ++i)
+        if (assign[i] >= 0 && assign[i] < nb) count[assign[i]]++;
+    uint32_t run = 0;
+    offsets[0] = 0;
+    for (int64_t q = 0; q < nb; ++q) {
+        cursor[order[q]] = run;
+        run += (uint32_t)count[order[q]];
+        offsets[q + 1] = run;
+    }
+    for (int64_t i = 0; i < N; ++i)
+        if (assign[i] >= 0 && assign[i] < nb) inverse_perm[cursor[assign[i]]++] = (uint32_t)i;
+    free(count);
+    free(cursor);
+    return (int64_t)run;
+}

@@ -57,6 +57,11 @@ How each oracle function is pinned (what checks it besides itself):
   reference's np.argsort order among equal distances and its BLAS float32
   summation order are "parity unpinned"; the oracle sorts ties by slot and
   sums in four partial sums by dimension mod 4 (the kernel's order).
+* ``bucket_reorder`` -- src/bucket.cu:8363-8412 (compute_bucket_reorder).
+  Pinned by the closed form "inverse_perm = stable argsort of each point's
+  processing position, offsets = running sums of bucket sizes in processing
+  order" on random assignments.  The bucket order itself is checked against
+  the reference header (``ref_bucket_order``, src/bucket_order.hpp:161-262).
 """
 from __future__ import annotations
 
@@ -103,6 +108,8 @@ def lib():
         L.or_translate.argtypes = [vp, vp, i64, i32, vp]
         L.or_prune_occlusion.argtypes = [vp, i64, i64, vp, i32, i32, vp]
         L.or_search.argtypes = [vp, i64, i64, vp, i32, vp, i64, vp, i32, i32, i32, i32, vp, vp, vp]
+        L.or_bucket_reorder.argtypes = [vp, i64, i64, vp, vp, vp]
+        L.or_bucket_reorder.restype = i64
         L.or_num_threads.restype = i32
         _lib = L
     return _lib
@@ -130,6 +137,11 @@ def ref():
         R.ref_read_graph.argtypes = [cp, vp, i64, C.POINTER(i64), C.POINTER(i32)]
         R.ref_read_vector_knn.argtypes = [cp, vp, i64, C.POINTER(i64), C.POINTER(i32)]
         R.ref_read_dataset.argtypes = [cp, vp, i64, C.POINTER(i32), C.POINTER(i32)]
+        R.ref_bucket_order.argtypes = [vp, i64, i32, i32, vp]
+        R.ref_write_bucket_offsets.argtypes = [cp, vp, i64]
+        R.ref_write_bucket_process_order.argtypes = [cp, vp, i64]
+        R.ref_read_bucket_offsets.argtypes = [cp, vp, i64, C.POINTER(i64)]
+        R.ref_read_bucket_process_order.argtypes = [cp, vp, i64, C.POINTER(i64)]
         _ref = R
     return _ref
 
@@ -293,6 +305,19 @@ def search(X, graph, Q, entries, topk, ef, metric=0):
     return ids, d, ex
 
 
+def bucket_reorder(assign, nb, order):
+    """(inverse_perm uint32 (placed,), offsets uint32 (nb + 1,))."""
+    assign = np.ascontiguousarray(assign, np.int32)
+    order = np.ascontiguousarray(order, np.int32)
+    N = len(assign)
+    inv = np.empty(N, np.uint32)
+    off = np.empty(nb + 1, np.uint32)
+    placed = lib().or_bucket_reorder(_p(assign), N, nb, _p(order), _p(inv), _p(off))
+    if placed < 0:
+        raise RuntimeError(f"or_bucket_reorder failed: {placed}")
+    return inv[:placed], off
+
+
 # ---- the reference's own code, compiled in place (test-time only) ----
 
 def ref_search_available() -> bool:
@@ -393,3 +418,37 @@ def ref_read_vector_knn(path, cap=1 << 24):
 def ref_read_dataset(path, cap=1 << 24):
     """float32 (N, D) as the C++ pipeline reads it (.i8bin signed)."""
     return _ref_read(ref().ref_read_dataset, path, np.float32, cap, C.c_int32, C.c_int32)
+
+
+def ref_bucket_order(graph, window):
+    g = np.ascontiguousarray(graph, np.uint32)
+    B, K = g.shape
+    out = np.empty(B, np.int32)
+    _check(ref().ref_bucket_order(_p(g), B, K, window, _p(out)), "ref_bucket_order")
+    return out
+
+
+def ref_write_bucket_offsets(path, off):
+    off = np.ascontiguousarray(off, np.uint32)
+    _check(ref().ref_write_bucket_offsets(str(path).encode(), _p(off), len(off)), "ref_write_bucket_offsets")
+
+
+def ref_write_bucket_process_order(path, order):
+    order = np.ascontiguousarray(order, np.int32)
+    _check(ref().ref_write_bucket_process_order(str(path).encode(), _p(order), len(order)),
+           "ref_write_bucket_process_order")
+
+
+def _ref_read_vec(fn, path, dtype, cap):
+    out = np.empty(cap, dtype)
+    n = C.c_int64()
+    _check(fn(str(path).encode(), _p(out), cap, C.byref(n)), fn.__name__)
+    return out[:n.value].copy()
+
+
+def ref_read_bucket_offsets(path, cap=1 << 22):
+    return _ref_read_vec(ref().ref_read_bucket_offsets, path, np.uint32, cap)
+
+
+def ref_read_bucket_process_order(path, cap=1 << 22):
+    return _ref_read_vec(ref().ref_read_bucket_process_order, path, np.int32, cap)

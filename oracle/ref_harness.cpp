@@ -17,7 +17,11 @@
 //   graph_io::write_graph / write_vector_knn / write_vector_bin /
 //       read_forward_graph / read_vector_knn (src/graph_io.hpp) and
 //       load::read_fbin_f32 / read_u8bin_to_f32 (src/load.hpp:67-117): the
-//       on-disk formats, for byte-level checks of this build's writers.
+//       on-disk formats, for byte-level checks of this build's writers;
+//   bucket_order::compute_bucket_processing_order over
+//       adjacency_from_flat_graph (src/bucket_order.hpp:161-262), and
+//       graph_io::write/read_bucket_offsets, write/read_bucket_process_order
+//       (src/graph_io.hpp:178-244).
 #include <cstdint>
 #include <cstdio>
 #include <cstdlib>
@@ -32,6 +36,7 @@
 #include "graph_io.hpp"
 #include "translate_graph_ids.hpp"
 #include "load.hpp"
+#include "bucket_order.hpp"
 
 extern "C" {
 
@@ -119,6 +124,65 @@ int ref_translate(const uint32_t* g, const uint32_t* inv, int64_t N, int32_t K, 
         std::filesystem::remove_all(d);
         if (n2 != N || k2 != K) return -1;
         for (size_t i = 0; i < res.size(); ++i) out[i] = res[i];
+        return 0;
+    } catch (...) {
+        return -1;
+    }
+}
+
+int ref_bucket_order(const uint32_t* g, int64_t B, int32_t K, int32_t window, int32_t* order)
+{
+    try {
+        const std::vector<int32_t> o = bucket_order::compute_bucket_processing_order(
+            bucket_order::adjacency_from_flat_graph(g, B, K), window);
+        std::copy(o.begin(), o.end(), order);
+        return 0;
+    } catch (...) {
+        return -1;
+    }
+}
+
+int ref_write_bucket_offsets(const char* path, const uint32_t* off, int64_t n_plus_1)
+{
+    try {
+        graph_io::write_bucket_offsets(path, std::vector<uint32_t>(off, off + n_plus_1));
+        return 0;
+    } catch (...) {
+        return -1;
+    }
+}
+
+int ref_write_bucket_process_order(const char* path, const int32_t* order, int64_t n)
+{
+    try {
+        graph_io::write_bucket_process_order(path, std::vector<int32_t>(order, order + n));
+        return 0;
+    } catch (...) {
+        return -1;
+    }
+}
+
+// readers: the count is returned through n (entries written to out, capacity cap)
+int ref_read_bucket_offsets(const char* path, uint32_t* out, int64_t cap, int64_t* n)
+{
+    try {
+        const std::vector<uint32_t> v = graph_io::read_bucket_offsets(path);
+        if (static_cast<int64_t>(v.size()) > cap) return -2;
+        std::copy(v.begin(), v.end(), out);
+        *n = static_cast<int64_t>(v.size());
+        return 0;
+    } catch (...) {
+        return -1;
+    }
+}
+
+int ref_read_bucket_process_order(const char* path, int32_t* out, int64_t cap, int64_t* n)
+{
+    try {
+        const std::vector<int32_t> v = graph_io::read_bucket_process_order(path);
+        if (static_cast<int64_t>(v.size()) > cap) return -2;
+        std::copy(v.begin(), v.end(), out);
+        *n = static_cast<int64_t>(v.size());
         return 0;
     } catch (...) {
         return -1;

@@ -45,6 +45,14 @@ int main(int argc, char** argv)
             write_dataset(arg + "/x.i8bin", i8.data(), static_cast<int32_t>(N), D, Elem::I8);
             write_npy<int64_t>(arg + "/ids.npy", i64.data(), N, W);
             write_npy<float>(arg + "/dist.npy", dist.data(), N, W);
+            std::vector<uint32_t> boff(12);
+            std::vector<int32_t> bord(11);
+            for (int b = 0; b < 11; ++b) {
+                boff[b + 1] = boff[b] + static_cast<uint32_t>((b * 3) % 5);
+                bord[b] = (b * 7) % 11;
+            }
+            write_bucket_offsets(arg + "/bucket_offsets.bin", boff.data(), 11);
+            write_bucket_process_order(arg + "/bucket_process_order.bin", bord.data(), 11);
             return 0;
         }
         if (mode == "read") {

@@ -31,41 +31,83 @@ def _run(args, **kw):
     return r
 
 
-def test_cli_bucket2_and_pipeline_tools(tmp_path):
+def test_cli_bucket2_and_pipeline_tools(tmp_path, ctx):
+    import gtann
     X = _c1_int()
     N = len(X)
     data = tmp_path / "base.fbin"
     io.write_dataset(data, X)
     # 16 buckets, every bucket probed: the table is the exact kNN
-    _run(["bucket2", "-i", data, "-o", tmp_path / "out", "--centroid-ratio", 16 / N, "--nprobe", 15,
+    _run(["bucket2", "-i", data, "-o", tmp_path / "out", "--centroid-ratio", 16 / N, "--nprobe", 15, "--knn-k", 8,
           "--neighbors-m", 64, "-t", 1, "--fused-optimize-degree", 32, "--kmeans-iters", 0, "--cache-mb", 64])
-    d = tmp_path / "out" / "k32p15m64t1"
+    d = tmp_path / "out" / "k8p15m64t1"
     ex_i, ex_d = O.knn_exact(X, 64)
-    np.testing.assert_array_equal(io.read_vector_knn(d / "vector_knn.bin"), ex_i)
-    np.testing.assert_array_equal(io.read_vector_dists(d / "vector_dists.bin"), ex_d)
-    np.testing.assert_array_equal(np.load(d / "neighbors.npy"), ex_i.astype(np.int64))
     fwd, rc, _ = O.cagra_prune(O.sanitize(ex_i), 32)
     assert rc == 0
     final = O.reverse_merge(fwd)
-    np.testing.assert_array_equal(io.read_graph(d / "final_graph.bin"), final)
-    np.testing.assert_array_equal(io.read_inverse_perm(d / "inverse_perm.bin"), np.arange(N, dtype=np.uint32))
-    assert os.path.realpath(d / "data_reordered.fbin") == os.path.realpath(data)
-    # optimize (prune + reverse merge) from the written table
+    np.testing.assert_array_equal(io.read_graph(d / "final_graph.bin"), final)   # the input's ids
+
+    # round-1 reorder artifacts: the same build through the library, then the
+    # processing order and the new-id layout
+    res = ctx.build_graph(X, n_buckets=16, nprobe=15, M=64, K=32, rounds=1, kmeans_iters=0, prune=False,
+                          round1_bucket=True, centroid_knn_k=15)
+    np.testing.assert_array_equal(io.read_graph(d / "centroid_pool.bin"), res.centroid_knn)
+    cg = np.ascontiguousarray(res.centroid_knn[:, :8])
+    np.testing.assert_array_equal(io.read_graph(d / "centroid_knn.bin"), cg)
+    order = gtann.bucket_order(cg, 32)                     # window: 4 x knn-k
+    np.testing.assert_array_equal(io.read_bucket_process_order(d / "bucket_process_order.bin"), order)
+    inv, off, _ = gtann.bucket_reorder(res.round1_bucket, 16, order)
+    np.testing.assert_array_equal(io.read_inverse_perm(d / "inverse_perm.bin"), inv)
+    np.testing.assert_array_equal(io.read_bucket_offsets(d / "bucket_offsets.bin"), off)
+    for q in range(16):   # position q's range holds bucket order[q]
+        assert (res.round1_bucket[inv[off[q]:off[q + 1]]] == order[q]).all()
+    perm = np.empty(N, np.int64)
+    perm[inv] = np.arange(N)
+    np.testing.assert_array_equal(io.read_dataset(str(d / "data_reordered.fbin")), X[inv])
+    ids_new = io.read_vector_knn(d / "vector_knn.bin")
+    np.testing.assert_array_equal(ids_new, perm[ex_i[inv]].astype(np.int32))
+    np.testing.assert_array_equal(io.read_vector_dists(d / "vector_dists.bin"), ex_d[inv])
+    np.testing.assert_array_equal(np.load(d / "neighbors.npy"), ids_new.astype(np.int64))
+
+    # optimize (prune + reverse merge) of the reordered table
+    fwd_n, rc, _ = O.cagra_prune(O.sanitize(ids_new), 32)
+    final_n = O.reverse_merge(fwd_n)
     _run(["optimize", "-i", d / "data_reordered.fbin", "-g", d / "vector_knn.bin", "-o", tmp_path / "g2.bin",
           "--output-degree", 32, "--skip-sort"])
-    np.testing.assert_array_equal(io.read_graph(tmp_path / "g2.bin"), final)
-    # the out-of-core path's tools: prune_windowed -> optimize_chunked -m E (+ translate)
+    np.testing.assert_array_equal(io.read_graph(tmp_path / "g2.bin"), final_n)
+    # the out-of-core path's tools: prune_windowed -> optimize_chunked -m E (+ translate to the input's ids)
     _run(["prune_windowed", "-k", d / "vector_knn.bin", "-i", d / "data_reordered.fbin", "-o", tmp_path / "fwd.bin",
-          "--output-degree", 32, "--bucket-offsets", "x", "--cache-mb", 8])
-    np.testing.assert_array_equal(io.read_graph(tmp_path / "fwd.bin"), fwd)
-    perm = np.random.default_rng(1).permutation(N).astype(np.uint32)
-    io.write_inverse_perm(tmp_path / "perm.bin", perm)
+          "--output-degree", 32, "--bucket-offsets", d / "bucket_offsets.bin", "--cache-mb", 8])
+    np.testing.assert_array_equal(io.read_graph(tmp_path / "fwd.bin"), fwd_n)
     _run(["optimize_chunked", "-g", tmp_path / "fwd.bin", "-o", tmp_path / "e.bin", "-m", "E",
-          "--inverse-perm", tmp_path / "perm.bin", "--final-output", tmp_path / "final.bin"])
-    np.testing.assert_array_equal(io.read_graph(tmp_path / "e.bin"), final)
-    np.testing.assert_array_equal(io.read_graph(tmp_path / "final.bin"), O.translate(final, perm))
-    _run(["translate_ids", "-g", tmp_path / "e.bin", "-p", tmp_path / "perm.bin", "-o", tmp_path / "t.bin"])
-    np.testing.assert_array_equal(io.read_graph(tmp_path / "t.bin"), O.translate(final, perm))
+          "--inverse-perm", d / "inverse_perm.bin", "--final-output", tmp_path / "final.bin"])
+    np.testing.assert_array_equal(io.read_graph(tmp_path / "e.bin"), final_n)
+    np.testing.assert_array_equal(io.read_graph(tmp_path / "final.bin"), O.translate(final_n, inv))
+    _run(["translate_ids", "-g", tmp_path / "e.bin", "-p", d / "inverse_perm.bin", "-o", tmp_path / "t.bin"])
+    np.testing.assert_array_equal(io.read_graph(tmp_path / "t.bin"), O.translate(final_n, inv))
+
+
+def test_permute_rows_and_remap_table(ctx):
+    import gtann
+    rng = np.random.default_rng(12)
+    N = 5000
+    inv = rng.permutation(N).astype(np.uint32)
+    perm = np.empty(N, np.int64)
+    perm[inv] = np.arange(N)
+    for X in (rng.standard_normal((N, 37)).astype(np.float32), rng.integers(0, 256, (N, 13)).astype(np.uint8),
+              rng.integers(-128, 128, (N, 64)).astype(np.int8), rng.standard_normal((N, 128)).astype(np.float32)):
+        np.testing.assert_array_equal(ctx.permute_rows(X, inv), X[inv])
+    ids = rng.integers(-1, N, size=(N, 24)).astype(np.int32)
+    ids[5, 3] = N + 7   # out of range -> -1
+    exp = np.where(ids[inv] >= 0, perm[np.clip(ids[inv], 0, N - 1)], -1)
+    exp[np.nonzero(inv == 5)[0][0], 3] = -1
+    np.testing.assert_array_equal(ctx.remap_table(ids, inv), exp.astype(np.int32))
+    bad = inv.copy()
+    bad[0] = bad[1]
+    with pytest.raises(gtann.GtannError, match="permutation"):
+        ctx.permute_rows(np.zeros((N, 4), np.float32), bad)
+    with pytest.raises(gtann.GtannError, match="permutation"):
+        ctx.remap_table(ids, bad)
 
 
 def test_cli_knn_u8_and_i8(tmp_path):
@@ -84,14 +126,17 @@ def test_cli_bucket2_multi_round_recall(tmp_path):
     X, _ = synth.generate("C2", n=50000)
     io.write_dataset(tmp_path / "c2.fbin", X)
     r = _run(["bucket2", "-i", tmp_path / "c2.fbin", "-o", tmp_path / "o", "--centroid-ratio", 0.00032,
-              "--nprobe", 1, "--neighbors-m", 64, "-t", 2, "--fused-optimize-degree", 32, "--skip-npy"])
+              "--nprobe", 1, "--knn-k", 8, "--neighbors-m", 64, "-t", 2, "--fused-optimize-degree", 32, "--skip-npy"])
     assert "build" in r.stdout
-    d = tmp_path / "o" / "k32p1m64t2"
-    ids = io.read_vector_knn(d / "vector_knn.bin")
+    d = tmp_path / "o" / "k8p1m64t2"
+    ids = io.read_vector_knn(d / "vector_knn.bin")          # new ids
+    inv = io.read_inverse_perm(d / "inverse_perm.bin")
+    perm = np.empty(len(X), np.int64)
+    perm[inv] = np.arange(len(X))
     assert not (d / "neighbors.npy").exists()
     q = np.arange(0, len(X), 173)
     ex_i, _ = O.knn_exact(X, 32, queries=q)
-    rec = np.mean([len(np.intersect1d(ids[qq, :32], ex_i[j])) / 32 for j, qq in enumerate(q)])
+    rec = np.mean([len(np.intersect1d(inv[ids[perm[qq], :32]], ex_i[j])) / 32 for j, qq in enumerate(q)])
     assert rec > 0.9, rec
     g = io.read_graph(d / "final_graph.bin")
     assert g.shape == (len(X), 32) and (g < len(X)).all()

@@ -163,3 +163,28 @@ def test_cli_rejects_bad_arguments():
     assert r.returncode == 1 and "only method E" in r.stderr
     r = subprocess.run([exe], capture_output=True, text=True)
     assert r.returncode == 1
+
+
+def _bucket_contents():
+    """the bucket files tests/io_driver.cpp writes"""
+    boff = np.concatenate([[0], np.cumsum([(b * 3) % 5 for b in range(11)])]).astype(np.uint32)
+    bord = np.array([(b * 7) % 11 for b in range(11)], np.int32)
+    return boff, bord
+
+
+@needs_ref
+def test_bucket_files_match_reference_bytes(driver, tmp_path):
+    _, out = driver
+    boff, bord = _bucket_contents()
+    O.ref_write_bucket_offsets(tmp_path / "o.bin", boff)
+    O.ref_write_bucket_process_order(tmp_path / "p.bin", bord)
+    assert _bytes(out / "bucket_offsets.bin") == _bytes(tmp_path / "o.bin")
+    assert _bytes(out / "bucket_process_order.bin") == _bytes(tmp_path / "p.bin")
+    io.write_bucket_offsets(tmp_path / "o2.bin", boff)
+    io.write_bucket_process_order(tmp_path / "p2.bin", bord)
+    assert _bytes(tmp_path / "o2.bin") == _bytes(tmp_path / "o.bin")
+    assert _bytes(tmp_path / "p2.bin") == _bytes(tmp_path / "p.bin")
+    np.testing.assert_array_equal(O.ref_read_bucket_offsets(out / "bucket_offsets.bin"), boff)
+    np.testing.assert_array_equal(O.ref_read_bucket_process_order(out / "bucket_process_order.bin"), bord)
+    np.testing.assert_array_equal(io.read_bucket_offsets(tmp_path / "o.bin"), boff)
+    np.testing.assert_array_equal(io.read_bucket_process_order(tmp_path / "p.bin"), bord)
