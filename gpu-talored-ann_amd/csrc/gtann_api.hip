@@ -694,6 +694,9 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
     const double t = c.timed([&] { launch_knn_fused(a, c.s); });
     ++c.c->knn_launches;
     tr.mark(c.s, "round: fused kNN");
+    if (tr.on)
+        std::fprintf(stderr, "[gtann]   pairs %.4g (own %d, probes %d, seeded %d), %.1f ms device\n", pr, own ? 1 : 0,
+                     probes ? 1 : 0, seed_d ? 1 : 0, t * 1e3);
     if (max_pool) *max_pool = std::max(*max_pool, mp);
     if (max_bucket) *max_bucket = std::max(*max_bucket, mb);
     if (pairs) *pairs += pr;
