@@ -250,10 +250,78 @@ __device__ void wave_merge(KnnLists& sm, const KnnArgs& a, int w, int lane, int 
     }
 }
 
+// Lists of at most kSmallM entries (top-2 assignment, Lloyd, narrow probe
+// tables) are merged for every query of the wave at once, one lane per
+// query (lanes 0..31): the list goes into registers and each buffer entry is
+// inserted by one compare-exchange pass.  A wave-wide merge per query would
+// cost as much as the whole scan of such a short pool.
+constexpr int kSmallM = 4;
+
+__device__ void small_merge_all(KnnLists& sm, const KnnArgs& a, int w, int lane, uint64_t mask, QueryState& st)
+{
+    const int M = a.M;
+    if (lane < 32 && ((mask >> lane) & 1ull)) {
+        const int64_t row = st.orow * M;
+        uint64_t k[kSmallM];
+#pragma unroll
+        for (int i = 0; i < kSmallM; ++i)
+            k[i] = i < st.nL ? pack_key(load_list_d(a.out_d + row + i), load_list_i(a.out_ids + row + i)) : kNoKey;
+        uint64_t* B = sm.buf[w * kQueriesPerWave + lane];
+        for (int e = 0; e < st.cnt; ++e) {
+            uint64_t x = B[e];
+            B[e] = kNoKey;   // the buffer starts over empty
+#pragma unroll
+            for (int i = 0; i < kSmallM; ++i) {
+                const bool lt = x < k[i];
+                const uint64_t lo = lt ? x : k[i];
+                x = lt ? k[i] : x;
+                k[i] = lo;
+            }
+        }
+        const int newn = min(st.nL + st.cnt, M);
+        float mth = 0.f;
+#pragma unroll
+        for (int i = 0; i < kSmallM; ++i) {
+            if (i < newn) {
+                const float d = o2f(static_cast<uint32_t>(k[i] >> 32));
+                a.out_d[row + i] = d;
+                a.out_ids[row + i] = static_cast<int32_t>(static_cast<uint32_t>(k[i]));
+                if (i == M - 1) mth = d;
+            }
+        }
+        st.cnt = 0;
+        st.nL = newn;
+        st.thr = newn == M ? fminf(st.seed, mth) : st.seed;
+    }
+    // the second half-wave holds the same queries' state
+    st.cnt = __shfl(st.cnt, lane & 31);
+    st.nL = __shfl(st.nL, lane & 31);
+    st.thr = __shfl(st.thr, lane & 31);
+    wave_sync();
+}
+
+// Merges the buffers of the queries in `mask` (bit q = query q of the wave).
+// SMALL: the launch may have lists of at most kSmallM entries (the int8
+// kernel never does: its registers stay below the three-wave limit).
+template <bool SMALL>
+__device__ __forceinline__ void merge_queries(KnnLists& sm, const KnnArgs& a, int w, int lane, uint64_t mask,
+                                              QueryState& st)
+{
+    if (SMALL && a.M <= kSmallM) {
+        small_merge_all(sm, a, w, lane, mask, st);
+        return;
+    }
+    while (mask) {
+        const int q = __ffsll(static_cast<unsigned long long>(mask)) - 1;
+        mask &= mask - 1;
+        wave_merge(sm, a, w, lane, q, st);
+    }
+}
+
 // Filter + append of one finished 32x32 tile whose pool rows have norms
 // tn[0..32) and ids tr[0..32) (tbase = pool-list position of row 0), the slow
 // path taken only when some lane of the wave has a candidate <= its threshold.
-template <int METRIC>
+template <int METRIC, bool SMALL>
 __device__ __forceinline__ void tile_append(KnnLists& sm, const KnnArgs& a, const floatx16& acc, const float* tn,
                                             const int32_t* tr, int tbase, int w, int lane, int h, int qlocal,
                                             bool qvalid, float qn, QueryState& st)
@@ -286,11 +354,7 @@ __device__ __forceinline__ void tile_append(KnnLists& sm, const KnnArgs& a, cons
     const bool need = qvalid && (st.cnt + np_ + np_o > kCB);
     uint64_t needmask = __ballot(need) & 0xffffffffull;
     if (needmask) {
-        while (needmask) {
-            const int q = __ffsll(static_cast<unsigned long long>(needmask)) - 1;
-            needmask &= needmask - 1;
-            wave_merge(sm, a, w, lane, q, st);
-        }
+        merge_queries<SMALL>(sm, a, w, lane, needmask, st);
         pass = 0;
 #pragma unroll
         for (int r = 0; r < 16; ++r) pass |= static_cast<uint32_t>(dv[r] <= st.thr) << r;
@@ -457,7 +521,7 @@ __global__ void __launch_bounds__(256, 2) knn_fused_kernel(KnnArgs a)
             }
         }
         if (t > 0 && __ballot(mkey <= st.thr))
-            tile_append<METRIC>(sm.L, a, acc_prev, sm.tnorm[pb3], sm.trow[pb3], (t - 1) * kPoolTile, w, lane, h,
+            tile_append<METRIC, true>(sm.L, a, acc_prev, sm.tnorm[pb3], sm.trow[pb3], (t - 1) * kPoolTile, w, lane, h,
                                 qlocal, qvalid, qn, st);
 
         store_rows(buf ^ 1);
@@ -476,18 +540,13 @@ __global__ void __launch_bounds__(256, 2) knn_fused_kernel(KnnArgs a)
             mkey = fminf(mkey, METRIC == 0 ? fmaf(-2.f, acc_prev[r], pn + qn) : fmaf(-1.f, acc_prev[r], pn));
         }
         if (__ballot(mkey <= st.thr))
-            tile_append<METRIC>(sm.L, a, acc_prev, sm.tnorm[pb3], sm.trow[pb3], (ntiles - 1) * kPoolTile, w, lane,
+            tile_append<METRIC, true>(sm.L, a, acc_prev, sm.tnorm[pb3], sm.trow[pb3], (ntiles - 1) * kPoolTile, w, lane,
                                 h, qlocal, qvalid, qn, st);
     }
 
     // flush the remaining buffers
     wait_vmem();
-    uint64_t rem = __ballot(qvalid && st.cnt > 0) & 0xffffffffull;
-    while (rem) {
-        const int q = __ffsll(static_cast<unsigned long long>(rem)) - 1;
-        rem &= rem - 1;
-        wave_merge(sm.L, a, w, lane, q, st);
-    }
+    merge_queries<true>(sm.L, a, w, lane, __ballot(qvalid && st.cnt > 0) & 0xffffffffull, st);
     if (qvalid) {
         for (int p = st.nL + h; p < a.M; p += 2) {
             a.out_ids[st.orow * a.M + p] = -1;
@@ -658,7 +717,7 @@ __global__ void __launch_bounds__(256, 2) knn_i8_kernel(KnnArgs a)
             }
         }
         if (t > 0 && __ballot(mkey <= st.thr))
-            tile_append<METRIC>(sm.L, a, to_float(acc_prev), sm.tnorm[pb3], sm.trow[pb3], (t - 1) * kPoolTile, w,
+            tile_append<METRIC, false>(sm.L, a, to_float(acc_prev), sm.tnorm[pb3], sm.trow[pb3], (t - 1) * kPoolTile, w,
                                 lane, h, qlocal, qvalid, qn, st);
 
         store_rows(buf ^ 1);
@@ -678,17 +737,12 @@ __global__ void __launch_bounds__(256, 2) knn_i8_kernel(KnnArgs a)
             mkey = fminf(mkey, METRIC == 0 ? fmaf(-2.f, dot, pn + qn) : fmaf(-1.f, dot, pn));
         }
         if (__ballot(mkey <= st.thr))
-            tile_append<METRIC>(sm.L, a, to_float(acc_prev), sm.tnorm[pb3], sm.trow[pb3], (ntiles - 1) * kPoolTile, w,
+            tile_append<METRIC, false>(sm.L, a, to_float(acc_prev), sm.tnorm[pb3], sm.trow[pb3], (ntiles - 1) * kPoolTile, w,
                                 lane, h, qlocal, qvalid, qn, st);
     }
 
     wait_vmem();
-    uint64_t rem = __ballot(qvalid && st.cnt > 0) & 0xffffffffull;
-    while (rem) {
-        const int q = __ffsll(static_cast<unsigned long long>(rem)) - 1;
-        rem &= rem - 1;
-        wave_merge(sm.L, a, w, lane, q, st);
-    }
+    merge_queries<false>(sm.L, a, w, lane, __ballot(qvalid && st.cnt > 0) & 0xffffffffull, st);
     if (qvalid) {
         for (int p = st.nL + h; p < a.M; p += 2) {
             a.out_ids[st.orow * a.M + p] = -1;
@@ -882,18 +936,13 @@ __global__ void __launch_bounds__(256, 2) knn_wide_kernel(KnnArgs a)
                 mkey = fminf(mkey, METRIC == 0 ? fmaf(-2.f, acc[u][r], pn + qn) : fmaf(-1.f, acc[u][r], pn));
             }
             if (__ballot(mkey <= st.thr))
-                tile_append<METRIC>(sm.L, a, acc[u], &sm.tnorm[sb][u * 32], &sm.trow[sb][u * 32],
+                tile_append<METRIC, true>(sm.L, a, acc[u], &sm.tnorm[sb][u * 32], &sm.trow[sb][u * 32],
                                     stile * kWideRows + u * 32, w, lane, h, qlocal, qvalid, qn, st);
         }
     }
 
     wait_vmem();
-    uint64_t rem = __ballot(qvalid && st.cnt > 0) & 0xffffffffull;
-    while (rem) {
-        const int q = __ffsll(static_cast<unsigned long long>(rem)) - 1;
-        rem &= rem - 1;
-        wave_merge(sm.L, a, w, lane, q, st);
-    }
+    merge_queries<true>(sm.L, a, w, lane, __ballot(qvalid && st.cnt > 0) & 0xffffffffull, st);
     if (qvalid) {
         for (int p = st.nL + h; p < a.M; p += 2) {
             a.out_ids[st.orow * a.M + p] = -1;

@@ -28,6 +28,19 @@ def test_knn_exact_integer_bitexact(ctx, n, d, k):
     assert_knn_equal(ids, dist, rid, rd)
 
 
+@pytest.mark.parametrize("k", [1, 2, 3, 4, 5])
+def test_knn_exact_short_lists(ctx, k):
+    # lists of at most 4 entries are merged one lane per query; 5 takes the wave-wide merge
+    X = _int_data(3000, 64, seed=40 + k, hi=8)      # many ties
+    ids, dist = ctx.knn_exact(X, k)
+    rid, rd = O.knn_exact(X, k)
+    assert_knn_equal(ids, dist, rid, rd)
+    q = np.random.default_rng(k).choice(3000, size=100, replace=False)
+    ids, dist = ctx.knn_exact(np.tile(X, (8, 1)), k, queries=q)   # pool split + partial merge
+    rid, rd = O.knn_exact(np.tile(X, (8, 1)), k, queries=q)
+    assert_knn_equal(ids, dist, rid, rd)
+
+
 def test_knn_exact_query_subset_split_pool(ctx):
     # few queries, large pool: exercises the pool-split + partial-merge path
     X = _int_data(40000, 128, seed=1)
