@@ -219,6 +219,9 @@ struct Ctx {
 
 static int pad_dim(int D) { return (D + 31) / 32 * 32; }
 
+// longest list the fused kNN kernels keep per query
+constexpr int kMaxListM = 128;
+
 // Lays out work items XCD-major for knn_fused_kernel: groups of items (one
 // group per bucket, sharing its pool) are dealt to the 8 XCDs longest-first
 // onto the least-loaded XCD (cost = query rows x pool rows), each XCD runs
@@ -827,7 +830,33 @@ static void make_buckets(Ctx& c, const DevMatrix& X, int64_t C, int nprobe, int 
     // probe table: nprobe nearest other centroids
     b.P = static_cast<int>(std::min<int64_t>(nprobe, C - 1));
     b.probe.assign(static_cast<size_t>(C) * std::max(b.P, 0), -1);
-    if (b.P > 0) {
+    if (b.P > kMaxListM) {
+        // wider than a kernel list (the reference allows nprobe up to 256):
+        // exact top-P of the centroid distances on the host, (distance, id) order
+        std::vector<float> hc(static_cast<size_t>(C) * X.Dp);
+        c.d2h(hc.data(), d_cm, hc.size() * sizeof(float));
+        c.sync();
+        parallel_slices(C, std::min<int64_t>(host_threads(), C), [&](int, int64_t lo, int64_t hi) {
+            std::vector<std::pair<double, int32_t>> row(static_cast<size_t>(C - 1));
+            for (int64_t q = lo; q < hi; ++q) {
+                const float* xq = hc.data() + q * X.Dp;
+                size_t n = 0;
+                for (int64_t o = 0; o < C; ++o) {
+                    if (o == q) continue;
+                    const float* xo = hc.data() + o * X.Dp;
+                    double d = 0.0;
+                    for (int k = 0; k < X.Dp; ++k) {
+                        if (metric == GT_METRIC_IP) d -= static_cast<double>(xq[k]) * xo[k];
+                        else d += (static_cast<double>(xq[k]) - xo[k]) * (static_cast<double>(xq[k]) - xo[k]);
+                    }
+                    row[n++] = {d, static_cast<int32_t>(o)};
+                }
+                std::partial_sort(row.begin(), row.begin() + b.P, row.begin() + static_cast<std::ptrdiff_t>(n));
+                for (int p = 0; p < b.P; ++p)
+                    b.probe[static_cast<size_t>(q * b.P + p)] = row[static_cast<size_t>(p)].second;
+            }
+        });
+    } else if (b.P > 0) {
         int32_t* d_pi = c.ws<int32_t>(W_PROBE_I, static_cast<size_t>(C) * b.P);
         float* d_pd = c.ws<float>(W_PROBE_D, static_cast<size_t>(C) * b.P);
         KnnJob j;

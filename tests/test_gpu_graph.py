@@ -275,3 +275,14 @@ def test_build_graph_reverse_edges_rounds(ctx):
         v = r2.knn_ids[q][r2.knn_ids[q] >= 0]
         assert len(set(v.tolist())) == len(v) and q not in v
         np.testing.assert_array_equal(d2[q][:len(v)], ((X[v] - X[q]) ** 2).sum(axis=1))
+
+
+def test_build_graph_wide_probe_table(ctx):
+    """nprobe above the kernels' list length (probe table computed exactly on
+    the host): with every other bucket probed the table is the exact kNN."""
+    rng = np.random.default_rng(31)
+    X = rng.integers(0, 40, size=(12000, 32)).astype(np.float32)
+    res = ctx.build_graph(X, n_buckets=160, nprobe=159, M=32, K=16, rounds=1, kmeans_iters=1)
+    ex_i, ex_d = O.knn_exact(X, 32)
+    np.testing.assert_array_equal(res.knn_ids, ex_i)
+    np.testing.assert_array_equal(res.knn_dists, ex_d)
