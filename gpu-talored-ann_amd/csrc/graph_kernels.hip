@@ -57,6 +57,18 @@ __global__ void pad_i8_kernel(const T* __restrict__ src, int8_t* __restrict__ ds
     }
 }
 
+// int8 copy of float rows (centroids of an integer dataset): the value
+// minus the dataset's shift, rounded and clamped; padding stays 0.
+__global__ void quantize_i8_kernel(const float* __restrict__ src, int64_t N, int D, int Dp, int shift,
+                                   int8_t* __restrict__ dst)
+{
+    const int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (e >= N * Dp) return;
+    const int c = static_cast<int>(e % Dp);
+    const float v = c < D ? rintf(src[e] - static_cast<float>(shift)) : 0.f;
+    dst[e] = static_cast<int8_t>(fminf(fmaxf(v, -128.f), 127.f));
+}
+
 // |x|^2 of int8 rows (exact integer sums), one wave per row
 __global__ void __launch_bounds__(256) row_norms_i8_kernel(const int8_t* __restrict__ X, int64_t N, int Dp,
                                                            float* __restrict__ norms)
@@ -639,6 +651,13 @@ void launch_pad_i8(const void* src, int dtype, int8_t* dst, int64_t N, int D, in
         hipLaunchKernelGGL(pad_i8_kernel<uint8_t>, dim3(grid), dim3(256), 0, s, static_cast<const uint8_t*>(src), dst, N, D, Dp, 128);
     else
         hipLaunchKernelGGL(pad_i8_kernel<int8_t>, dim3(grid), dim3(256), 0, s, static_cast<const int8_t*>(src), dst, N, D, Dp, 0);
+    GT_HIP(hipGetLastError());
+}
+
+void launch_quantize_i8(const float* src, int64_t N, int D, int Dp, int shift, int8_t* dst, hipStream_t s)
+{
+    if (N * Dp <= 0) return;
+    hipLaunchKernelGGL(quantize_i8_kernel, dim3(grid_for(N * Dp, 256)), dim3(256), 0, s, src, N, D, Dp, shift, dst);
     GT_HIP(hipGetLastError());
 }
 

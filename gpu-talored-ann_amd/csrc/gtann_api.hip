@@ -32,6 +32,7 @@ void launch_pad_convert(const void* src, int dtype, float* dst, int64_t N, int D
 void launch_row_norms(const float* X, int64_t N, int Dp, float* norms, hipStream_t s);
 void launch_pad_i8(const void* src, int dtype, int8_t* dst, int64_t N, int D, int Dp, hipStream_t s);
 void launch_row_norms_i8(const int8_t* X, int64_t N, int Dp, float* norms, hipStream_t s);
+void launch_quantize_i8(const float* src, int64_t N, int D, int Dp, int shift, int8_t* dst, hipStream_t s);
 void launch_copy_ranges(const void* tasks, int64_t ntasks, const int32_t* members, int32_t* pool, hipStream_t s);
 void launch_negate(float* d, int64_t n, hipStream_t s);
 void launch_graph_search(const SearchArgs& a, int64_t grid, hipStream_t s);
@@ -173,7 +174,7 @@ namespace gtann {
 enum Ws {
     W_X, W_XRAW, W_NORMS, W_C, W_CRAW, W_CNORMS, W_IDS, W_D, W_IDS2, W_D2, W_IDS3, W_D3, W_ITEMS, W_QROWS, W_PROWS,
     W_MEMBERS, W_TASKS, W_POOL, W_PART_I, W_PART_D, W_G1, W_G2, W_G3, W_DEG, W_OFF, W_CUR, W_KEYS, W_SUMS, W_FLAG,
-    W_TMP, W_OUT, W_IN, W_PROBE_I, W_PROBE_D, W_WORST, W_X8, W_NORMS8, W_COUNT_
+    W_TMP, W_OUT, W_IN, W_PROBE_I, W_PROBE_D, W_WORST, W_X8, W_NORMS8, W_C8, W_CNORMS8, W_COUNT_
 };
 static_assert(W_COUNT_ <= 40, "workspace slots");
 
@@ -266,6 +267,7 @@ struct DevMatrix {
     const float* data = nullptr;
     const float* norms = nullptr;
     int64_t N = 0;
+    int D = 0;
     int Dp = 0;
     // int8 rows of integer-typed inputs (uint8 shifted by -shift), stride
     // Dp8 bytes, with their exact |x|^2; null for fp32 inputs
@@ -295,6 +297,7 @@ static DevMatrix prepare(Ctx& c, int slot_x, int slot_raw, int slot_norms, const
     const size_t es = dtype_size(dtype);
     DevMatrix m;
     m.N = N;
+    m.D = D;
     m.Dp = Dp;
     const bool dev = is_device_ptr(X);
     const void* src = X;   // device copy of the caller's rows
@@ -737,8 +740,25 @@ static void make_buckets(Ctx& c, const DevMatrix& X, int64_t C, int nprobe, int 
                            c.s);
     }
     launch_row_norms(d_cm, C, X.Dp, d_cn, c.s);
+    Cm.N = C;
+    Cm.D = X.D;
     Cm.data = d_cm;
     Cm.norms = d_cn;
+    // an integer dataset's assignment runs on the int8 kernel against the
+    // centroids rounded to the dataset's values (the buckets only need
+    // near centroids; every distance is then exact for those)
+    auto refresh_c8 = [&]() {
+        if (!X.data8) return;
+        int8_t* c8 = c.ws<int8_t>(W_C8, static_cast<size_t>(C) * X.Dp8);
+        float* cn8 = c.ws<float>(W_CNORMS8, static_cast<size_t>(C));
+        launch_quantize_i8(d_cm, C, X.D, X.Dp8, X.shift, c8, c.s);
+        launch_row_norms_i8(c8, C, X.Dp8, cn8, c.s);
+        Cm.data8 = c8;
+        Cm.norms8 = cn8;
+        Cm.Dp8 = X.Dp8;
+        Cm.shift = X.shift;
+    };
+    refresh_c8();
     tr.mark(c.s, "bucketing: sample centroids");
 
     // Lloyd iterations on a training subset (the reference's KMeans|| also
@@ -778,6 +798,7 @@ static void make_buckets(Ctx& c, const DevMatrix& X, int64_t C, int nprobe, int 
             c.h2d(d_off, tmp.offsets.data(), static_cast<size_t>(C + 1) * sizeof(int64_t));
             launch_centroid_sums(X.data, X.Dp, d_mem, d_off, C, d_cm, c.s);
             launch_row_norms(d_cm, C, X.Dp, d_cn, c.s);
+            refresh_c8();
             tr.mark(c.s, "bucketing: Lloyd iteration");
         }
     }

@@ -583,7 +583,7 @@ __device__ __forceinline__ floatx16 to_float(const intx16& v)
     return f;
 }
 
-template <int DP, int METRIC>
+template <int DP, int METRIC, bool SMALL>
 __global__ void __launch_bounds__(256, 2) knn_i8_kernel(KnnArgs a)
 {
     constexpr int KS = DP / 32;                      // MFMA steps per tile
@@ -717,7 +717,7 @@ __global__ void __launch_bounds__(256, 2) knn_i8_kernel(KnnArgs a)
             }
         }
         if (t > 0 && __ballot(mkey <= st.thr))
-            tile_append<METRIC, false>(sm.L, a, to_float(acc_prev), sm.tnorm[pb3], sm.trow[pb3], (t - 1) * kPoolTile, w,
+            tile_append<METRIC, SMALL>(sm.L, a, to_float(acc_prev), sm.tnorm[pb3], sm.trow[pb3], (t - 1) * kPoolTile, w,
                                 lane, h, qlocal, qvalid, qn, st);
 
         store_rows(buf ^ 1);
@@ -737,12 +737,12 @@ __global__ void __launch_bounds__(256, 2) knn_i8_kernel(KnnArgs a)
             mkey = fminf(mkey, METRIC == 0 ? fmaf(-2.f, dot, pn + qn) : fmaf(-1.f, dot, pn));
         }
         if (__ballot(mkey <= st.thr))
-            tile_append<METRIC, false>(sm.L, a, to_float(acc_prev), sm.tnorm[pb3], sm.trow[pb3], (ntiles - 1) * kPoolTile, w,
+            tile_append<METRIC, SMALL>(sm.L, a, to_float(acc_prev), sm.tnorm[pb3], sm.trow[pb3], (ntiles - 1) * kPoolTile, w,
                                 lane, h, qlocal, qvalid, qn, st);
     }
 
     wait_vmem();
-    merge_queries<false>(sm.L, a, w, lane, __ballot(qvalid && st.cnt > 0) & 0xffffffffull, st);
+    merge_queries<SMALL>(sm.L, a, w, lane, __ballot(qvalid && st.cnt > 0) & 0xffffffffull, st);
     if (qvalid) {
         for (int p = st.nL + h; p < a.M; p += 2) {
             a.out_ids[st.orow * a.M + p] = -1;
@@ -1015,20 +1015,29 @@ static void launch_knn_metric(const KnnArgs& a, dim3 grid, hipStream_t stream)
     }
 }
 
+// SMALL: lists of at most kSmallM entries (assignment against centroids);
+// the other variant keeps its registers below the three-wave limit.
+template <int METRIC, bool SMALL>
+static void launch_knn_i8_v(const KnnArgs& a, dim3 grid, hipStream_t stream)
+{
+    switch (a.Dp) {
+    case 32:  hipLaunchKernelGGL((knn_i8_kernel<32, METRIC, SMALL>), grid, dim3(256), 0, stream, a); break;
+    case 64:  hipLaunchKernelGGL((knn_i8_kernel<64, METRIC, SMALL>), grid, dim3(256), 0, stream, a); break;
+    case 96:  hipLaunchKernelGGL((knn_i8_kernel<96, METRIC, SMALL>), grid, dim3(256), 0, stream, a); break;
+    case 128: hipLaunchKernelGGL((knn_i8_kernel<128, METRIC, SMALL>), grid, dim3(256), 0, stream, a); break;
+    case 160: hipLaunchKernelGGL((knn_i8_kernel<160, METRIC, SMALL>), grid, dim3(256), 0, stream, a); break;
+    case 192: hipLaunchKernelGGL((knn_i8_kernel<192, METRIC, SMALL>), grid, dim3(256), 0, stream, a); break;
+    case 224: hipLaunchKernelGGL((knn_i8_kernel<224, METRIC, SMALL>), grid, dim3(256), 0, stream, a); break;
+    case 256: hipLaunchKernelGGL((knn_i8_kernel<256, METRIC, SMALL>), grid, dim3(256), 0, stream, a); break;
+    default: GT_REQUIRE(false, "int8 kernel: padded dimension " + std::to_string(a.Dp) + " not supported");
+    }
+}
+
 template <int METRIC>
 static void launch_knn_i8(const KnnArgs& a, dim3 grid, hipStream_t stream)
 {
-    switch (a.Dp) {
-    case 32:  hipLaunchKernelGGL((knn_i8_kernel<32, METRIC>), grid, dim3(256), 0, stream, a); break;
-    case 64:  hipLaunchKernelGGL((knn_i8_kernel<64, METRIC>), grid, dim3(256), 0, stream, a); break;
-    case 96:  hipLaunchKernelGGL((knn_i8_kernel<96, METRIC>), grid, dim3(256), 0, stream, a); break;
-    case 128: hipLaunchKernelGGL((knn_i8_kernel<128, METRIC>), grid, dim3(256), 0, stream, a); break;
-    case 160: hipLaunchKernelGGL((knn_i8_kernel<160, METRIC>), grid, dim3(256), 0, stream, a); break;
-    case 192: hipLaunchKernelGGL((knn_i8_kernel<192, METRIC>), grid, dim3(256), 0, stream, a); break;
-    case 224: hipLaunchKernelGGL((knn_i8_kernel<224, METRIC>), grid, dim3(256), 0, stream, a); break;
-    case 256: hipLaunchKernelGGL((knn_i8_kernel<256, METRIC>), grid, dim3(256), 0, stream, a); break;
-    default: GT_REQUIRE(false, "int8 kernel: padded dimension " + std::to_string(a.Dp) + " not supported");
-    }
+    if (a.M <= kSmallM) launch_knn_i8_v<METRIC, true>(a, grid, stream);
+    else launch_knn_i8_v<METRIC, false>(a, grid, stream);
 }
 
 // n_items must be a multiple of 8 (XCD-major layout, see knn_fused_kernel).

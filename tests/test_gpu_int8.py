@@ -114,9 +114,10 @@ def test_build_graph_all_probed_is_exact(ctx):
 
 def test_build_graph_int8_matches_fp32(ctx):
     # same values as int8 and as float: the int8 kernel and the fp32 kernel
-    # build the same graph (all keys exact, all launches see the same pools)
+    # build the same graph (all keys exact, all launches see the same pools:
+    # the centroids are data points, so rounding them to int8 changes nothing)
     X = _data(20000, 128, np.int8, seed=22, lo=-60, hi=61)
-    kw = dict(n_buckets=16, nprobe=1, M=64, K=32, rounds=2, kmeans_iters=2)
+    kw = dict(n_buckets=16, nprobe=1, M=64, K=32, rounds=2, kmeans_iters=0)
     a = ctx.build_graph(X, **kw)
     b = ctx.build_graph(X.astype(np.float32), **kw)
     np.testing.assert_array_equal(a.knn_ids, b.knn_ids)
@@ -129,3 +130,16 @@ def test_long_rows_keep_fp32_kernel(ctx):
     ids, dist = ctx.knn_exact(X, 16)
     rid, rd = O.knn_exact(X.astype(np.float32), 16)
     assert_knn_equal(ids, dist, rid, rd)
+
+
+def test_build_graph_int8_with_lloyd_recall(ctx):
+    # Lloyd-moved centroids are rounded to int8 for the assignment: a valid
+    # bucketing, checked through the recall of the built table
+    X = _data(30000, 64, np.uint8, seed=23)
+    X[:, :8] = (np.arange(30000)[:, None] % 7 * 30).astype(np.uint8)   # some structure
+    res = ctx.build_graph(X, n_buckets=24, nprobe=2, M=32, K=16, rounds=2, kmeans_iters=3)
+    q = np.arange(0, 30000, 97)
+    ex, _ = O.knn_exact(X.astype(np.float32), 32, queries=q)
+    rec = np.mean([len(np.intersect1d(res.knn_ids[qq], ex[j])) / 32 for j, qq in enumerate(q)])
+    assert rec > 0.5, rec
+    assert (res.graph < 30000).all()
