@@ -16,6 +16,7 @@
 #include <memory>
 #include <condition_variable>
 #include <functional>
+#include <future>
 #include <mutex>
 #include <numeric>
 #include <thread>
@@ -161,10 +162,10 @@ struct gt_ctx {
     std::string err;
     // named workspaces, grow-only (one slot per role, see gtann::Ws)
     gtann::DevBuf ws[40];
-    gtann::HostBuf pinned;   // top-2 assignment download
+    gtann::HostBuf pinned[2];   // top-2 assignment downloads of two consecutive rounds
     // host scratch of the bucketing, reused across calls (no page faults on
     // fresh N-sized allocations every round)
-    std::vector<int32_t> h_bucket_of, h_key2, h_by_key, h_members;
+    std::vector<int32_t> h_bucket_of, h_key2, h_by_key, h_members[2];
     int64_t knn_launches = 0;   // bucketed-round launches of the current build
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
 };
@@ -709,15 +710,31 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
     return t;
 }
 
-// Centroids + probe table + two-choice assignment of one round.
-static void make_buckets(Ctx& c, const DevMatrix& X, int64_t C, int nprobe, int metric, float balance,
-                         int kmeans_iters, uint64_t seed, Buckets& b, std::vector<int32_t>* cknn = nullptr,
-                         int cknn_k = 0)
+// The device half of one round's bucketing: centroids (sampled rows, moved by
+// the Lloyd iterations), every point's exact top-2 centroids downloaded into
+// pinned host memory, the probe table and the optional centroid self-kNN.
+// The host half (bucket_host) only reads this plan, so it can run on another
+// thread while the device works on the next round.
+struct BucketPlan {
+    int64_t N = 0, C = 0;
+    std::vector<int32_t> cid;       // sampled centroid row ids, ascending
+    bool data_points = true;        // centroids are data points (no Lloyd)
+    const uint32_t* top2 = nullptr; // pinned, 2N: nearest and 2nd nearest centroid
+    std::vector<int32_t> probe;     // C x P
+    int P = 0;
+};
+
+static void bucket_device(Ctx& c, const DevMatrix& X, int64_t C, int nprobe, int metric, int kmeans_iters,
+                          uint64_t seed, HostBuf& pin, BucketPlan& bp, std::vector<int32_t>* cknn = nullptr,
+                          int cknn_k = 0)
 {
     const int64_t N = X.N;
     Trace tr;
     C = std::max<int64_t>(1, std::min<int64_t>(C, N));
-    std::vector<int32_t> cid = sample_ids(N, C, seed);
+    bp.N = N;
+    bp.C = C;
+    bp.cid = sample_ids(N, C, seed);
+    std::vector<int32_t>& cid = bp.cid;
     int32_t* d_cid = c.ws<int32_t>(W_PROWS, static_cast<size_t>(C));
     c.h2d(d_cid, cid.data(), static_cast<size_t>(C) * sizeof(int32_t));
 
@@ -803,9 +820,10 @@ static void make_buckets(Ctx& c, const DevMatrix& X, int64_t C, int nprobe, int 
         }
     }
 
-    // final assignment of every point: exact top-2 centroids + two-choice rule
-    uint32_t* top2 = c.c->pinned.as<uint32_t>(static_cast<size_t>(2 * N));
-    std::vector<int32_t>& bucket_of = c.c->h_bucket_of;
+    // exact top-2 centroids of every point
+    bp.data_points = data_points;
+    uint32_t* top2 = pin.as<uint32_t>(static_cast<size_t>(2 * N));
+    bp.top2 = top2;
     if (C >= 2) {
         int32_t* d_t2 = c.ws<int32_t>(W_IDS3, static_cast<size_t>(2 * N));
         float* d_t2d = c.ws<float>(W_D3, static_cast<size_t>(2 * N));
@@ -831,27 +849,11 @@ static void make_buckets(Ctx& c, const DevMatrix& X, int64_t C, int nprobe, int 
             top2[2 * i + 1] = 0xffffffffu;
         }
     }
-    assign_two_choice(top2, N, C, balance, data_points ? &cid : nullptr, bucket_of);
-    tr.mark(c.s, "bucketing: two-choice");
-    {
-        std::vector<int32_t>& key2 = c.c->h_key2;
-        key2.resize(static_cast<size_t>(N));
-        parallel_slices(N, host_threads(), [&](int, int64_t lo, int64_t hi) {
-            for (int64_t i = lo; i < hi; ++i) {
-                const uint32_t c1 = top2[static_cast<size_t>(2 * i)], c2 = top2[static_cast<size_t>(2 * i + 1)];
-                const uint32_t other = static_cast<int64_t>(c1) == bucket_of[static_cast<size_t>(i)] ? c2 : c1;
-                key2[static_cast<size_t>(i)] = other < static_cast<uint64_t>(C) ? static_cast<int32_t>(other)
-                                                                                  : bucket_of[static_cast<size_t>(i)];
-            }
-        });
-        csr_from_assignment_keyed(bucket_of, key2, C, b, c.c->h_by_key);
-    }
-    tr.mark(c.s, "bucketing: CSR");
 
     // probe table: nprobe nearest other centroids
-    b.P = static_cast<int>(std::min<int64_t>(nprobe, C - 1));
-    b.probe.assign(static_cast<size_t>(C) * std::max(b.P, 0), -1);
-    if (b.P > kMaxListM) {
+    bp.P = static_cast<int>(std::min<int64_t>(nprobe, C - 1));
+    bp.probe.assign(static_cast<size_t>(C) * std::max(bp.P, 0), -1);
+    if (bp.P > kMaxListM) {
         // wider than a kernel list (the reference allows nprobe up to 256):
         // exact top-P of the centroid distances on the host, (distance, id) order
         std::vector<float> hc(static_cast<size_t>(C) * X.Dp);
@@ -872,27 +874,27 @@ static void make_buckets(Ctx& c, const DevMatrix& X, int64_t C, int nprobe, int 
                     }
                     row[n++] = {d, static_cast<int32_t>(o)};
                 }
-                std::partial_sort(row.begin(), row.begin() + b.P, row.begin() + static_cast<std::ptrdiff_t>(n));
-                for (int p = 0; p < b.P; ++p)
-                    b.probe[static_cast<size_t>(q * b.P + p)] = row[static_cast<size_t>(p)].second;
+                std::partial_sort(row.begin(), row.begin() + bp.P, row.begin() + static_cast<std::ptrdiff_t>(n));
+                for (int p = 0; p < bp.P; ++p)
+                    bp.probe[static_cast<size_t>(q * bp.P + p)] = row[static_cast<size_t>(p)].second;
             }
         });
-    } else if (b.P > 0) {
-        int32_t* d_pi = c.ws<int32_t>(W_PROBE_I, static_cast<size_t>(C) * b.P);
-        float* d_pd = c.ws<float>(W_PROBE_D, static_cast<size_t>(C) * b.P);
+    } else if (bp.P > 0) {
+        int32_t* d_pi = c.ws<int32_t>(W_PROBE_I, static_cast<size_t>(C) * bp.P);
+        float* d_pd = c.ws<float>(W_PROBE_D, static_cast<size_t>(C) * bp.P);
         KnnJob j;
         j.Q = &Cm;
         j.P = &Cm;
         j.nq = C;
         j.np = C;
-        j.M = b.P;
+        j.M = bp.P;
         j.metric = metric;
         j.exclude_self = true;
         j.out_pos = true;
         j.out_ids = d_pi;
         j.out_d = d_pd;
         run_knn_flat(c, j, 1);
-        c.d2h(b.probe.data(), d_pi, b.probe.size() * sizeof(int32_t));
+        c.d2h(bp.probe.data(), d_pi, bp.probe.size() * sizeof(int32_t));
         c.sync();
     }
     tr.mark(c.s, "bucketing: probe table");
@@ -917,6 +919,34 @@ static void make_buckets(Ctx& c, const DevMatrix& X, int64_t C, int nprobe, int 
         c.d2h(cknn->data(), d_ki, cknn->size() * sizeof(int32_t));
         c.sync();
     }
+}
+
+// The host half: two-choice rule over the downloaded top-2 lists, then the
+// members ordered by (bucket, other top-2 centroid, id).  Host code only (no
+// HIP calls), so the build runs it on a worker thread.
+static void bucket_host(const BucketPlan& bp, float balance, Buckets& b, std::vector<int32_t>& bucket_of,
+                        std::vector<int32_t>& key2, std::vector<int32_t>& by_key)
+{
+    const int64_t N = bp.N, C = bp.C;
+    const uint32_t* top2 = bp.top2;
+    Trace tr;
+    assign_two_choice(top2, N, C, balance, bp.data_points ? &bp.cid : nullptr, bucket_of);
+    const double t_tc = tr.t.sec();
+    key2.resize(static_cast<size_t>(N));
+    parallel_slices(N, host_threads(), [&](int, int64_t lo, int64_t hi) {
+        for (int64_t i = lo; i < hi; ++i) {
+            const uint32_t c1 = top2[static_cast<size_t>(2 * i)], c2 = top2[static_cast<size_t>(2 * i + 1)];
+            const uint32_t other = static_cast<int64_t>(c1) == bucket_of[static_cast<size_t>(i)] ? c2 : c1;
+            key2[static_cast<size_t>(i)] = other < static_cast<uint64_t>(C) ? static_cast<int32_t>(other)
+                                                                              : bucket_of[static_cast<size_t>(i)];
+        }
+    });
+    csr_from_assignment_keyed(bucket_of, key2, C, b, by_key);
+    b.P = bp.P;
+    b.probe = bp.probe;
+    if (tr.on)
+        std::fprintf(stderr, "[gtann] bucketing (host thread): two-choice %.3f ms, CSR %.3f ms\n", t_tc * 1e3,
+                     (tr.t.sec() - t_tc) * 1e3);
 }
 
 // ---------------------------------------------------------------- graph stages
@@ -1090,7 +1120,7 @@ void gt_destroy(gt_ctx* ctx)
         b.p = nullptr;
         b.cap = 0;
     }
-    ctx->pinned.release();
+    for (auto& pb : ctx->pinned) pb.release();
     if (ctx->ev0) (void)hipEventDestroy(ctx->ev0);
     if (ctx->ev1) (void)hipEventDestroy(ctx->ev1);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
@@ -1876,14 +1906,39 @@ int gt_build_graph_ex(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtyp
         int32_t* tmp_i = c.ws<int32_t>(W_IDS2, nm);
         float* tmp_d = c.ws<float>(W_D2, nm);
         ctx->knn_launches = 0;
-        Buckets b;
-        b.members.swap(ctx->h_members);   // reuse the member list's host memory across builds
-        for (int r = 0; r < p.rounds; ++r) {
+        // Round r's bucketing = bucket_device (device work + downloads, on
+        // this thread) then bucket_host (two-choice + CSR, on a worker
+        // thread).  The host half of round r runs while the device computes
+        // round r+1's centroids and top-2 lists, and the host half of round
+        // r+1 while the device runs round r's kNN; every device stage stays
+        // on the context's stream in one order.
+        Buckets bk[2];
+        BucketPlan plans[2];
+        for (int i = 0; i < 2; ++i) bk[i].members.swap(ctx->h_members[i]);   // reuse host memory across builds
+        std::vector<int32_t> cknn;
+        const bool want_cknn = extras && extras->centroid_knn && extras->centroid_knn_k > 0;
+        auto device_part = [&](int r) {
             Timer tb;
-            std::vector<int32_t> cknn;
-            const bool want_cknn = r == 0 && extras && extras->centroid_knn && extras->centroid_knn_k > 0;
-            make_buckets(c, Xm, C, nprobe, p.metric, p.balance, p.kmeans_iters, p.seed + static_cast<uint64_t>(r), b,
-                         want_cknn ? &cknn : nullptr, want_cknn ? extras->centroid_knn_k : 0);
+            bucket_device(c, Xm, C, nprobe, p.metric, p.kmeans_iters, p.seed + static_cast<uint64_t>(r),
+                          ctx->pinned[r & 1], plans[r & 1], r == 0 && want_cknn ? &cknn : nullptr,
+                          r == 0 && want_cknn ? extras->centroid_knn_k : 0);
+            st.t_bucketing += tb.sec();
+        };
+        std::future<void> host_job;   // declared after everything it references
+        auto start_host = [&](int r) {
+            host_job = std::async(std::launch::async, [&, r] {
+                bucket_host(plans[r & 1], p.balance, bk[r & 1], ctx->h_bucket_of, ctx->h_key2, ctx->h_by_key);
+            });
+        };
+        device_part(0);
+        start_host(0);
+        for (int r = 0; r < p.rounds; ++r) {
+            if (r + 1 < p.rounds) device_part(r + 1);
+            {
+                Timer tw;
+                host_job.get();   // rethrows the host half's errors
+                st.t_bucketing += tw.sec();
+            }
             if (r == 0 && extras) {
                 if (extras->round1_bucket) {
                     const std::vector<int32_t>& bo = c.c->h_bucket_of;
@@ -1896,7 +1951,8 @@ int gt_build_graph_ex(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtyp
                 }
                 c.sync();
             }
-            st.t_bucketing += tb.sec();
+            if (r + 1 < p.rounds) start_host(r + 1);
+            const Buckets& b = bk[r & 1];
             if (p.reverse_edges) {
                 // the Python pipeline's round: full table, reverse edges, then the merge
                 int32_t* oi = r == 0 ? run_i : cur_i;
@@ -1931,7 +1987,7 @@ int gt_build_graph_ex(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtyp
                 std::swap(run_d, tmp_d);
             }
         }
-        b.members.swap(ctx->h_members);
+        for (int i = 0; i < 2; ++i) bk[i].members.swap(ctx->h_members[i]);
         if (p.refine_passes > 0) {
             GT_REQUIRE(p.refine_sample >= 1 && p.refine_sample <= p.M && p.refine_sample * p.refine_sample <= 1024,
                        "bad refine sample");
