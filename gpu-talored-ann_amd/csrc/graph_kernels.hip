@@ -380,112 +380,390 @@ __device__ __forceinline__ unsigned long long wave_min_u64(unsigned long long v)
     return v;
 }
 
-// One wave per dst row.  The final row is
+// One dst row j, by one wave.  The final row is
 //   protected S = fwd[j][0..P)  ++  R  ++  (O minus the first occurrence of each r in R)
 // truncated to K, where O = fwd[j][P..K) and R = the distinct sources not in
 // S, by strongest (rank, src) key, at most L = K-P of them.  This is the
 // fixed point of the weakest-first move-to-front insertion of
 // merge_rank_ordered_into_row (an accessed source moves to slot P; absent
-// ones push the last slot out).
+// ones push the last slot out).  keys: the row's n reverse keys
+// (rank << 32 | src) in any order; sR, sRow, sK: the wave's LDS scratch.
 constexpr int kRevMaxK = 64;
-__global__ void __launch_bounds__(256) rev_merge_kernel(const uint32_t* __restrict__ fwd, int64_t N, int K,
-                                                        const uint32_t* __restrict__ off,
-                                                        const unsigned long long* __restrict__ keys,
-                                                        uint32_t* __restrict__ out)
+
+// The global reads of one row, issued ahead of its merge: the forward row
+// (one id per lane) and, for at most 64 keys, one key per lane.
+struct RevRow {
+    uint32_t rowv;
+    unsigned long long key;
+    const unsigned long long* keys;
+    uint32_t n;
+};
+
+__device__ __forceinline__ RevRow rev_row_load(const uint32_t* __restrict__ fwd, int64_t j, int K,
+                                               const unsigned long long* keys, uint32_t n, int lane)
 {
-    __shared__ uint32_t sR[4][kRevMaxK];
-    __shared__ uint32_t sRow[4][kRevMaxK];
-    __shared__ unsigned long long sK[4][64];
-    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int64_t j = static_cast<int64_t>(blockIdx.x) * 4 + w;
-    if (j >= N) return;
+    RevRow r;
+    r.rowv = lane < K ? fwd[j * K + lane] : 0xffffffffu;
+    r.key = n <= 64 && lane < static_cast<int>(n) ? keys[lane] : ~0ull;
+    r.keys = keys;
+    r.n = n;
+    return r;
+}
+
+// v among a[lo, min(hi, lim)), a: 64 LDS words, 16-byte aligned; lo and hi
+// wave-uniform (hi <= 64), lim per lane.  Reads go out 16 words at a time.
+__device__ __forceinline__ bool lds_has(const uint32_t* a, int lo, int hi, int lim, uint32_t v)
+{
+    bool f = false;
+    for (int b = lo & ~15; b < hi; b += 16) {
+        uint4 x[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) x[u] = *reinterpret_cast<const uint4*>(a + b + 4 * u);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int i = b + 4 * u;
+            const uint32_t e[4] = {x[u].x, x[u].y, x[u].z, x[u].w};
+#pragma unroll
+            for (int c = 0; c < 4; ++c) f |= i + c >= lo && i + c < hi && i + c < lim && e[c] == v;
+        }
+    }
+    return f;
+}
+
+// Number of the first 2*npair entries of sK (64 keys, 16-byte aligned)
+// below key; dup: one of those has src's id.  Eight keys per batch of reads.
+__device__ __forceinline__ int keys_below(const unsigned long long* sK, int npair, unsigned long long key,
+                                          uint32_t src, bool& dup)
+{
+    int pos = 0;
+    bool d = false;
+    for (int q = 0; q < npair; q += 4) {
+        uint4 x[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) x[u] = *reinterpret_cast<const uint4*>(&sK[2 * (q + u)]);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const unsigned long long k0 = (static_cast<unsigned long long>(x[u].y) << 32) | x[u].x;
+            const unsigned long long k1 = (static_cast<unsigned long long>(x[u].w) << 32) | x[u].z;
+            const bool l0 = k0 < key, l1 = k1 < key;
+            pos += (l0 ? 1 : 0) + (l1 ? 1 : 0);
+            d |= (l0 && x[u].x == src) || (l1 && x[u].z == src);
+        }
+    }
+    dup = d;
+    return pos;
+}
+
+__device__ __forceinline__ void rev_merge_row(const RevRow& in, int64_t j, int K, uint32_t* __restrict__ out,
+                                              uint32_t* sR, uint32_t* sRow, unsigned long long* sK, int lane)
+{
     const int P = K / 2, L = K - P;
-    const uint32_t rowv = lane < K ? fwd[j * K + lane] : 0xffffffffu;
-    const uint32_t lo = off[j], hi = off[j + 1];
-    const uint32_t n = hi - lo;
+    const uint32_t rowv = in.rowv;
+    const uint32_t n = in.n;
+    const unsigned long long* keys = in.keys;
     const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-    sRow[w][lane] = rowv;
+    wave_sync();   // the wave's previous row is done with the scratch
+    sRow[lane] = rowv;
+    wave_sync();
     int nR = 0;
 
     // s among the protected slots fwd[j][0..P) (LDS broadcast reads)
-    auto protected_src = [&](uint32_t s) {
-        bool p = false;
-        for (int q4 = 0; q4 < (P + 3) / 4; ++q4) {
-            const uint4 x = *reinterpret_cast<const uint4*>(&sRow[w][4 * q4]);
-            p |= (4 * q4 + 0 < P && x.x == s) || (4 * q4 + 1 < P && x.y == s) || (4 * q4 + 2 < P && x.z == s) ||
-                 (4 * q4 + 3 < P && x.w == s);
-        }
-        return p;
-    };
+    auto protected_src = [&](uint32_t s) { return lds_has(sRow, 0, P, 64, s); };
 
     if (n <= 64) {
-        // R by counting: a source is kept if not protected and no smaller key
-        // has the same source; its position is the number of kept keys below it
-        const unsigned long long key = lane < static_cast<int>(n) ? keys[lo + lane] : ~0ull;
+        // R by counting: protected sources drop out first; a key's position
+        // is the number of smaller remaining keys.  A source repeated in the
+        // keys keeps only its strongest key (then the positions are counted
+        // again without the weaker copies).
+        unsigned long long key = in.key;
         const uint32_t src = static_cast<uint32_t>(key);
-        sK[w][lane] = key;
+        if (key != ~0ull && protected_src(src)) key = ~0ull;
+        sK[lane] = key;
         wave_sync();
+        const int npair = static_cast<int>(n + 1) / 2;
         bool dup = false;
-#pragma unroll 4
-        for (int q2 = 0; q2 < 32; ++q2) {
-            const uint4 x = *reinterpret_cast<const uint4*>(&sK[w][2 * q2]);
-            const unsigned long long k0 = (static_cast<unsigned long long>(x.y) << 32) | x.x;
-            const unsigned long long k1 = (static_cast<unsigned long long>(x.w) << 32) | x.z;
-            dup |= (k0 < key && x.x == src) || (k1 < key && x.z == src);
+        int pos = keys_below(sK, npair, key, src, dup);
+        bool keep = key != ~0ull;
+        if (__ballot(keep && dup)) {
+            keep = keep && !dup;
+            wave_sync();
+            sK[lane] = keep ? key : ~0ull;
+            wave_sync();
+            bool unused = false;
+            pos = keys_below(sK, npair, key, src, unused);
         }
-        const bool keep = key != ~0ull && !dup && !protected_src(src);
-        wave_sync();
-        sK[w][lane] = keep ? key : ~0ull;
-        wave_sync();
-        int pos = 0;
-#pragma unroll 4
-        for (int q2 = 0; q2 < 32; ++q2) {
-            const uint4 x = *reinterpret_cast<const uint4*>(&sK[w][2 * q2]);
-            const unsigned long long k0 = (static_cast<unsigned long long>(x.y) << 32) | x.x;
-            const unsigned long long k1 = (static_cast<unsigned long long>(x.w) << 32) | x.z;
-            pos += (k0 < key ? 1 : 0) + (k1 < key ? 1 : 0);
-        }
-        if (keep && pos < L) sR[w][pos] = src;
+        if (keep && pos < L) sR[pos] = src;
         nR = min(L, static_cast<int>(__popcll(__ballot(keep))));
     } else {
-        unsigned long long last = 0;
-        bool first = true;
-        wave_sync();
-        while (nR < L) {
-            unsigned long long m = ~0ull;
-            for (uint32_t e = lane; e < n; e += 64) {
-                const unsigned long long v = keys[lo + e];
-                if ((first || v > last) && v < m) m = v;
+        // long lists, 64 keys at a time: the best L keys so far stay sorted
+        // in sB (over sR's memory); a chunk's keys below the L-th best are
+        // ranked against them and against each other
+        unsigned long long* sB = reinterpret_cast<unsigned long long*>(sR);
+        if (lane < 32) sB[lane] = ~0ull;
+        int nb = 0;
+        unsigned long long thr = ~0ull;
+        for (uint32_t c = 0; c < n; c += 64) {
+            const unsigned long long key = c + lane < n ? keys[c + lane] : ~0ull;
+            bool cand = key < thr;
+            if (cand) cand = !protected_src(static_cast<uint32_t>(key));
+            const unsigned long long cm = __ballot(cand);
+            if (cm == 0) continue;
+            const int nc = static_cast<int>(__popcll(cm));
+            wave_sync();
+            if (cand) sK[__popcll(cm & below)] = key;
+            wave_sync();
+            const unsigned long long mc = lane < nc ? sK[lane] : ~0ull;
+            const unsigned long long mb = lane < nb ? sB[lane] : ~0ull;
+            int pc = 0, pb = lane;
+            for (int q = 0; q < nc; ++q) {
+                const unsigned long long x = sK[q];
+                pc += x < mc ? 1 : 0;
+                pb += x < mb ? 1 : 0;
             }
-            m = wave_min_u64(m);
-            if (m == ~0ull) break;
-            first = false;
-            last = m;
-            const uint32_t src = static_cast<uint32_t>(m);
-            bool skip = protected_src(src);
-            for (int q = 0; q < nR; ++q) skip |= (sR[w][q] == src);
-            if (!skip) {
-                if (lane == 0) sR[w][nR] = src;
-                wave_sync();
-                ++nR;
+            for (int q = 0; q < nb; ++q) pc += sB[q] < mc ? 1 : 0;
+            wave_sync();
+            if (lane < nb && pb < L) sB[pb] = mb;
+            if (lane < nc && pc < L) sB[pc] = mc;
+            nb = min(L, nb + nc);
+            wave_sync();
+            thr = nb == L ? sB[L - 1] : ~0ull;
+        }
+        // a source twice among the chosen keys (a forward row that repeats
+        // an id): the exact scan below decides instead
+        wave_sync();
+        const unsigned long long mb = lane < nb ? sB[lane] : ~0ull;
+        bool dupb = false;
+        for (int q = 0; q < nb; ++q) {
+            const unsigned long long x = sB[q];
+            dupb |= x < mb && static_cast<uint32_t>(x) == static_cast<uint32_t>(mb);
+        }
+        const bool any_dup = __ballot(dupb) != 0;
+        wave_sync();
+        if (!any_dup) {
+            if (lane < nb) sR[lane] = static_cast<uint32_t>(mb);
+            nR = nb;
+        } else {
+            // the strongest remaining key by wave minimum, L times
+            unsigned long long last = 0;
+            bool first = true;
+            while (nR < L) {
+                unsigned long long m = ~0ull;
+                for (uint32_t e = lane; e < n; e += 64) {
+                    const unsigned long long v = keys[e];
+                    if ((first || v > last) && v < m) m = v;
+                }
+                m = wave_min_u64(m);
+                if (m == ~0ull) break;
+                first = false;
+                last = m;
+                const uint32_t src = static_cast<uint32_t>(m);
+                bool skip = protected_src(src);
+                for (int q = 0; q < nR; ++q) skip |= (sR[q] == src);
+                if (!skip) {
+                    if (lane == 0) sR[nR] = src;
+                    wave_sync();
+                    ++nR;
+                }
             }
         }
     }
     wave_sync();
 
     if (lane < P) out[j * K + lane] = rowv;
-    if (lane < nR) out[j * K + P + lane] = sR[w][lane];
+    if (lane < nR) out[j * K + P + lane] = sR[lane];
     if (nR < L) {
         // O entries, in order, minus the first occurrence of each element of R
-        bool inR = false;
-        for (int q = 0; q < nR; ++q) inR |= (sR[w][q] == rowv);
-        bool earlier = false;
-        for (int x = P; x < K; ++x) earlier |= (x < lane) && (sRow[w][x] == rowv);
+        const bool inR = lds_has(sR, 0, nR, 64, rowv);
+        const bool earlier = lds_has(sRow, P, K, lane, rowv);
         const bool consumed = inR && !earlier;
         const bool keepO = lane >= P && lane < K && !consumed;
         const unsigned long long km = __ballot(keepO);
         const int pos = P + nR + __popcll(km & below);
         if (keepO && pos < K) out[j * K + pos] = rowv;
+    }
+}
+
+// Rows grouped through a CSR built with global atomics (rev_count/scatter):
+// the path for graphs beyond the binned path's size limit.
+__global__ void __launch_bounds__(256) rev_merge_kernel(const uint32_t* __restrict__ fwd, int64_t N, int K,
+                                                        const uint32_t* __restrict__ off,
+                                                        const unsigned long long* __restrict__ keys,
+                                                        uint32_t* __restrict__ out)
+{
+    __shared__ __align__(16) uint32_t sR[4][kRevMaxK];
+    __shared__ __align__(16) uint32_t sRow[4][kRevMaxK];
+    __shared__ __align__(16) unsigned long long sK[4][64];
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int64_t j = static_cast<int64_t>(blockIdx.x) * 4 + w;
+    if (j >= N) return;
+    const uint32_t lo = off[j];
+    const RevRow in = rev_row_load(fwd, j, K, keys + lo, off[j + 1] - lo, lane);
+    rev_merge_row(in, j, K, out, sR[w], sRow[w], sK[w], lane);
+}
+
+// Binned reverse merge (no global atomics).  Rows are cut into bins of
+// 2^shift consecutive dst ids.  (1) every block of edges counts its edges per
+// bin in LDS; (2) an exclusive scan of the counts in (bin, block) order gives
+// every (bin, block) pair its output range; (3) every block scatters its
+// edges through LDS cursors, as (dst within bin << 40 | rank << 32 | src);
+// (4) one workgroup per bin groups its keys by dst (LDS counting sort into a
+// second buffer) and merges each of its rows.  The key order inside a row is
+// irrelevant to rev_merge_row, so the result equals the CSR path's.
+constexpr int kRevBinThreads = 512;
+constexpr int kRevMaxBins = 16384;      // (1)-(3): one LDS counter per bin
+constexpr int kRevMaxBinShift = 12;     // (4): rows per bin <= 4096
+
+__global__ void __launch_bounds__(kRevBinThreads) rev_bin_count_kernel(const uint32_t* __restrict__ fwd, int64_t E,
+                                                                       int64_t N, int64_t chunk, int shift, int nbins,
+                                                                       uint32_t* __restrict__ hist,
+                                                                       int* __restrict__ err)
+{
+    __shared__ uint32_t h[kRevMaxBins];
+    for (int i = threadIdx.x; i < nbins; i += kRevBinThreads) h[i] = 0u;
+    __syncthreads();
+    const int64_t e0 = static_cast<int64_t>(blockIdx.x) * chunk, e1 = min(E, e0 + chunk);
+    bool bad = false;
+    for (int64_t e = e0 + threadIdx.x; e < e1; e += 4 * kRevBinThreads) {
+        uint32_t v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int64_t x = e + u * kRevBinThreads;
+            v[u] = x < e1 ? fwd[x] : 0xffffffffu;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            if (e + u * kRevBinThreads >= e1) continue;
+            if (v[u] >= N) bad = true;
+            else atomicAdd(&h[v[u] >> shift], 1u);
+        }
+    }
+    if (bad) atomicExch(err, 1);
+    __syncthreads();
+    for (int i = threadIdx.x; i < nbins; i += kRevBinThreads)
+        hist[static_cast<int64_t>(i) * gridDim.x + blockIdx.x] = h[i];
+}
+
+__global__ void __launch_bounds__(kRevBinThreads) rev_bin_scatter_kernel(const uint32_t* __restrict__ fwd, int64_t E,
+                                                                         int64_t N, int K, int64_t chunk, int shift,
+                                                                         int nbins, const uint32_t* __restrict__ offs,
+                                                                         unsigned long long* __restrict__ part)
+{
+    __shared__ uint32_t cur[kRevMaxBins];
+    for (int i = threadIdx.x; i < nbins; i += kRevBinThreads)
+        cur[i] = offs[static_cast<int64_t>(i) * gridDim.x + blockIdx.x];
+    __syncthreads();
+    const int64_t e0 = static_cast<int64_t>(blockIdx.x) * chunk, e1 = min(E, e0 + chunk);
+    const uint32_t mask = (1u << shift) - 1u;
+    const uint32_t uK = static_cast<uint32_t>(K);
+    for (int64_t e = e0 + threadIdx.x; e < e1; e += 4 * kRevBinThreads) {
+        uint32_t v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int64_t x = e + u * kRevBinThreads;
+            v[u] = x < e1 ? fwd[x] : 0xffffffffu;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            if (v[u] >= N) continue;   // also the lanes past e1
+            const uint32_t eu = static_cast<uint32_t>(e + u * kRevBinThreads);   // E < 2^32
+            const uint32_t i = eu / uK, k = eu - i * uK;
+            const uint32_t slot = atomicAdd(&cur[v[u] >> shift], 1u);
+            part[slot] = (static_cast<unsigned long long>(v[u] & mask) << 40) |
+                         (static_cast<unsigned long long>(k) << 32) | i;
+        }
+    }
+}
+
+__global__ void __launch_bounds__(kRevBinThreads) rev_bin_merge_kernel(const uint32_t* __restrict__ fwd, int64_t N,
+                                                                       int K, int shift, int nblk,
+                                                                       const uint32_t* __restrict__ offs,
+                                                                       const unsigned long long* __restrict__ part,
+                                                                       unsigned long long* __restrict__ grouped,
+                                                                       uint32_t* __restrict__ out)
+{
+    constexpr int kW = kRevBinThreads / 64;
+    constexpr int kU = 4;   // keys in flight per thread while grouping
+    extern __shared__ uint32_t dyn[];   // start[2^shift + 1], cur[2^shift]
+    __shared__ uint32_t wtot[kW + 1];
+    __shared__ __align__(16) uint32_t sR[kW][kRevMaxK];
+    __shared__ __align__(16) uint32_t sRow[kW][kRevMaxK];
+    __shared__ __align__(16) unsigned long long sK[kW][64];
+    uint32_t* start = dyn;
+    uint32_t* cur = dyn + (1 << shift) + 1;
+    const int t = threadIdx.x, w = t >> 6, lane = t & 63;
+    const int64_t j0 = static_cast<int64_t>(blockIdx.x) << shift;
+    const int rows = static_cast<int>(min<int64_t>(int64_t(1) << shift, N - j0));
+    const uint32_t lo = offs[static_cast<int64_t>(blockIdx.x) * nblk];
+    const uint32_t hi = offs[static_cast<int64_t>(blockIdx.x + 1) * nblk];
+    for (int r = t; r < rows; r += kRevBinThreads) cur[r] = 0u;
+    __syncthreads();
+    for (uint32_t e = lo + t; e < hi; e += kU * kRevBinThreads) {
+        unsigned long long k[kU];
+#pragma unroll
+        for (int u = 0; u < kU; ++u) k[u] = e + u * kRevBinThreads < hi ? part[e + u * kRevBinThreads] : ~0ull;
+#pragma unroll
+        for (int u = 0; u < kU; ++u)
+            if (k[u] != ~0ull) atomicAdd(&cur[static_cast<uint32_t>(k[u] >> 40)], 1u);
+    }
+    __syncthreads();
+
+    // exclusive scan of the row counts: per thread a run of rows, then the
+    // runs' totals by wave scans
+    const int per = (rows + kRevBinThreads - 1) / kRevBinThreads;
+    const int r0 = t * per;
+    uint32_t loc = 0;
+    for (int q = 0; q < per; ++q)
+        if (r0 + q < rows) loc += cur[r0 + q];
+    uint32_t inc = loc;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t x = __shfl_up(inc, o);
+        if (lane >= o) inc += x;
+    }
+    if (lane == 63) wtot[w] = inc;
+    __syncthreads();
+    if (t == 0) {
+        uint32_t run = 0;
+        for (int q = 0; q < kW; ++q) {
+            const uint32_t v = wtot[q];
+            wtot[q] = run;
+            run += v;
+        }
+        wtot[kW] = run;
+    }
+    __syncthreads();
+    uint32_t run = wtot[w] + inc - loc;
+    for (int q = 0; q < per; ++q)
+        if (r0 + q < rows) {
+            const uint32_t c = cur[r0 + q];
+            start[r0 + q] = run;
+            cur[r0 + q] = run;
+            run += c;
+        }
+    if (t == 0) start[rows] = wtot[kW];
+    __syncthreads();
+
+    for (uint32_t e = lo + t; e < hi; e += kU * kRevBinThreads) {
+        unsigned long long k[kU];
+#pragma unroll
+        for (int u = 0; u < kU; ++u) k[u] = e + u * kRevBinThreads < hi ? part[e + u * kRevBinThreads] : ~0ull;
+#pragma unroll
+        for (int u = 0; u < kU; ++u)
+            if (k[u] != ~0ull) {
+                const uint32_t slot = atomicAdd(&cur[static_cast<uint32_t>(k[u] >> 40)], 1u);
+                grouped[lo + slot] = k[u] & 0xFFFFFFFFFFull;
+            }
+    }
+    __syncthreads();   // the block's own global writes are visible to the block after the barrier
+    // one wave per row, the next row's reads in flight during each merge
+    int r = w;
+    if (r >= rows) return;
+    RevRow nxt = rev_row_load(fwd, j0 + r, K, grouped + lo + start[r], start[r + 1] - start[r], lane);
+    for (; r < rows; r += kW) {
+        const RevRow in = nxt;
+        const int rn = r + kW;
+        if (rn < rows) nxt = rev_row_load(fwd, j0 + rn, K, grouped + lo + start[rn], start[rn + 1] - start[rn], lane);
+        rev_merge_row(in, j0 + r, K, out, sR[w], sRow[w], sK[w], lane);
     }
 }
 
@@ -732,6 +1010,38 @@ void launch_rev_scatter(const uint32_t* fwd, int64_t N, int K, const uint32_t* o
     const int64_t E = N * K;
     if (E <= 0) return;
     hipLaunchKernelGGL(rev_scatter_kernel, dim3(grid_for(E, 256)), dim3(256), 0, s, fwd, E, N, K, off, slot, keys);
+    GT_HIP(hipGetLastError());
+}
+
+// Bin shift of the binned path, or -1 when N is beyond its limits.
+int rev_bin_shift(int64_t N)
+{
+    int sh = 5;
+    while (sh < kRevMaxBinShift && ceil_div(N, int64_t(1) << sh) > 4096) ++sh;
+    return ceil_div(N, int64_t(1) << sh) <= kRevMaxBins ? sh : -1;
+}
+
+int rev_bin_blocks(int64_t E) { return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(512, ceil_div(E, 8192)))); }
+
+void launch_rev_binned(const uint32_t* fwd, int64_t N, int K, uint32_t* hist, uint32_t* offs, uint32_t* sums,
+                       unsigned long long* part, unsigned long long* grouped, uint32_t* out, int* err, hipStream_t s)
+{
+    GT_REQUIRE(K >= 1 && K <= kRevMaxK, "reverse merge supports output degree <= 64");
+    const int shift = rev_bin_shift(N);
+    GT_REQUIRE(shift >= 0, "binned reverse merge: too many rows");
+    const int64_t E = N * K;
+    if (E <= 0) return;
+    const int nbins = static_cast<int>(ceil_div(N, int64_t(1) << shift));
+    const int nblk = rev_bin_blocks(E);
+    const int64_t chunk = ceil_div(E, nblk);
+    hipLaunchKernelGGL(rev_bin_count_kernel, dim3(nblk), dim3(kRevBinThreads), 0, s, fwd, E, N, chunk, shift, nbins,
+                       hist, err);
+    launch_exclusive_scan(hist, static_cast<int64_t>(nbins) * nblk, offs, sums, s);
+    hipLaunchKernelGGL(rev_bin_scatter_kernel, dim3(nblk), dim3(kRevBinThreads), 0, s, fwd, E, N, K, chunk, shift,
+                       nbins, offs, part);
+    const size_t lds = (2 * (size_t(1) << shift) + 1) * sizeof(uint32_t);
+    hipLaunchKernelGGL(rev_bin_merge_kernel, dim3(nbins), dim3(kRevBinThreads), lds, s, fwd, N, K, shift, nblk, offs,
+                       part, grouped, out);
     GT_HIP(hipGetLastError());
 }
 

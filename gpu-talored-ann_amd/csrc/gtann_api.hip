@@ -49,6 +49,10 @@ void launch_rev_count(const uint32_t* fwd, int64_t N, int K, uint32_t* deg, uint
 void launch_exclusive_scan(const uint32_t* in, int64_t n, uint32_t* out, uint32_t* sums, hipStream_t s);
 void launch_rev_scatter(const uint32_t* fwd, int64_t N, int K, const uint32_t* off, const uint32_t* slot,
                         unsigned long long* keys, hipStream_t s);
+int rev_bin_shift(int64_t N);
+int rev_bin_blocks(int64_t E);
+void launch_rev_binned(const uint32_t* fwd, int64_t N, int K, uint32_t* hist, uint32_t* offs, uint32_t* sums,
+                       unsigned long long* part, unsigned long long* grouped, uint32_t* out, int* err, hipStream_t s);
 void launch_rev_merge(const uint32_t* fwd, int64_t N, int K, const uint32_t* off, const unsigned long long* keys,
                       uint32_t* out, hipStream_t s);
 void launch_occlusion_prune(const float* X, int64_t N, int Dp, const int32_t* nb, int M, int max_deg, int32_t* out,
@@ -970,18 +974,33 @@ static void reverse_merge_device(Ctx& c, const uint32_t* fwd, int64_t N, int K, 
 {
     GT_REQUIRE(K >= 1 && K <= 64, "output degree must be in [1, 64]");
     GT_REQUIRE(N * K < (int64_t(1) << 32), "too many edges for 32-bit offsets");
-    uint32_t* deg = c.ws<uint32_t>(W_DEG, static_cast<size_t>(N));
-    uint32_t* off = c.ws<uint32_t>(W_OFF, static_cast<size_t>(N + 1));
-    uint32_t* slot = c.ws<uint32_t>(W_CUR, static_cast<size_t>(N * K));
-    uint32_t* sums = c.ws<uint32_t>(W_SUMS, static_cast<size_t>(ceil_div(N, 1024) + 1));
-    unsigned long long* keys = c.ws<unsigned long long>(W_KEYS, static_cast<size_t>(N * K));
     int* err = c.ws<int>(W_TMP, 1);
-    GT_HIP(hipMemsetAsync(deg, 0, static_cast<size_t>(N) * sizeof(uint32_t), c.s));
     GT_HIP(hipMemsetAsync(err, 0, sizeof(int), c.s));
-    launch_rev_count(fwd, N, K, deg, slot, err, c.s);
-    launch_exclusive_scan(deg, N, off, sums, c.s);
-    launch_rev_scatter(fwd, N, K, off, slot, keys, c.s);
-    launch_rev_merge(fwd, N, K, off, keys, out, c.s);
+    // GTANN_REVMERGE_CSR=1 selects the global-atomic CSR path at any size
+    // (the path of graphs beyond the binned path's limits; tests cover both)
+    const char* force_csr = std::getenv("GTANN_REVMERGE_CSR");
+    const int shift = force_csr && force_csr[0] == '1' ? -1 : rev_bin_shift(N);
+    if (shift >= 0) {
+        // binned path: LDS histograms and cursors, no global atomics
+        const int64_t nh = ceil_div(N, int64_t(1) << shift) * rev_bin_blocks(N * K);
+        uint32_t* hist = c.ws<uint32_t>(W_DEG, static_cast<size_t>(nh));
+        uint32_t* offs = c.ws<uint32_t>(W_OFF, static_cast<size_t>(nh + 1));
+        uint32_t* sums = c.ws<uint32_t>(W_SUMS, static_cast<size_t>(ceil_div(nh, 1024) + 1));
+        unsigned long long* part = c.ws<unsigned long long>(W_KEYS, static_cast<size_t>(N * K));
+        unsigned long long* grouped = c.ws<unsigned long long>(W_CUR, static_cast<size_t>(N * K));
+        launch_rev_binned(fwd, N, K, hist, offs, sums, part, grouped, out, err, c.s);
+    } else {
+        uint32_t* deg = c.ws<uint32_t>(W_DEG, static_cast<size_t>(N));
+        uint32_t* off = c.ws<uint32_t>(W_OFF, static_cast<size_t>(N + 1));
+        uint32_t* slot = c.ws<uint32_t>(W_CUR, static_cast<size_t>(N * K));
+        uint32_t* sums = c.ws<uint32_t>(W_SUMS, static_cast<size_t>(ceil_div(N, 1024) + 1));
+        unsigned long long* keys = c.ws<unsigned long long>(W_KEYS, static_cast<size_t>(N * K));
+        GT_HIP(hipMemsetAsync(deg, 0, static_cast<size_t>(N) * sizeof(uint32_t), c.s));
+        launch_rev_count(fwd, N, K, deg, slot, err, c.s);
+        launch_exclusive_scan(deg, N, off, sums, c.s);
+        launch_rev_scatter(fwd, N, K, off, slot, keys, c.s);
+        launch_rev_merge(fwd, N, K, off, keys, out, c.s);
+    }
     int h = 0;
     c.d2h(&h, err, sizeof(int));
     c.sync();

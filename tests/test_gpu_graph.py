@@ -89,6 +89,47 @@ def test_reverse_merge_random(ctx, N, K, hub):
     _assert_rows_equal(ctx.reverse_merge(F), O.reverse_merge(F), F)
 
 
+def test_reverse_merge_csr_path(ctx, monkeypatch):
+    """The global-atomic CSR path (graphs beyond the binned path's limits),
+    forced by GTANN_REVMERGE_CSR=1, gives the same rows."""
+    monkeypatch.setenv("GTANN_REVMERGE_CSR", "1")
+    for N, K in [(5000, 32), (3000, 48), (700, 1)]:
+        rng = np.random.default_rng(N + K)
+        F = rng.integers(0, N, size=(N, K)).astype(np.uint32)
+        F[rng.random((N, K)) < 0.2] = 3
+        _assert_rows_equal(ctx.reverse_merge(F), O.reverse_merge(F), F)
+
+
+@pytest.mark.parametrize("N,K", [(200000, 32), (70000, 64), (33, 8), (4097 * 32, 16)])
+def test_reverse_merge_bin_edges(ctx, N, K):
+    # sizes around the bin boundaries (a last bin of one row; many bins),
+    # long in-lists (> 64 keys) and rows without any reverse edge
+    rng = np.random.default_rng(N ^ K)
+    F = rng.integers(0, N, size=(N, K)).astype(np.uint32)
+    F[rng.random((N, K)) < 0.01] = N - 1
+    F[:, K // 2:][rng.random((N, K - K // 2)) < 0.3] = 0
+    _assert_rows_equal(ctx.reverse_merge(F), O.reverse_merge(F), F)
+
+
+def test_reverse_merge_distinct_rows_with_hubs(ctx):
+    # rows without repeated ids (as the prune writes them) and a skewed
+    # in-degree: the long in-lists take the chunked selection, not the
+    # repeated-source fallback
+    rng = np.random.default_rng(17)
+    N, K = 30000, 32
+    w = 1.0 / (1.0 + np.arange(N)) ** 0.9
+    w /= w.sum()
+    draws = rng.choice(N, size=(N, 6 * K), p=w)
+    rows = []
+    for r in draws:
+        u, first = np.unique(r, return_index=True)
+        rows.append(u[np.argsort(first)][:K])   # distinct ids in draw order
+    assert min(len(r) for r in rows) == K
+    F = np.stack(rows).astype(np.uint32)[rng.permutation(N)]
+    assert np.bincount(F.ravel(), minlength=N).max() > 1000
+    _assert_rows_equal(ctx.reverse_merge(F), O.reverse_merge(F), F)
+
+
 def test_reverse_merge_out_of_range(ctx):
     import gtann
     F = np.zeros((10, 4), np.uint32)
