@@ -151,51 +151,67 @@ __global__ void __launch_bounds__(256) sanitize_kernel(const int32_t* __restrict
 constexpr int kPruneMaxM = 128;
 constexpr int kPruneDepth = 16;   // neighbour rows in flight per wave
 
-// One wave per point a.  Row a goes into an LDS rank table (open addressing,
-// entry = id << 32 | rank; a repeated id keeps one entry per occurrence);
-// then every neighbour row kAD < M-1 is streamed through, kPruneDepth rows in
-// flight, and each of its ids is looked up: a hit at rank kAB > kAD counts
-// once per (kAD, kAB) pair (stamp) -- src/prune_windowed_core.hpp:177-232.
-// Finally the first K valid ranks by (count, rank) are written
-// (src/prune_windowed_core.hpp:234-263).  E = list halves of 64, CAP = table slots.
-template <int E, int CAP>
+// One wave per point a.  Row a's ids go into an LDS hash table of 4-slot
+// buckets (2*MM buckets; a full bucket spills into the next one, no
+// wrap-around; a repeated id takes one slot per occurrence); each lane
+// remembers the slots of its own entries.  Every neighbour row kAD < M-1 is
+// then streamed through, kPruneDepth rows in flight: a lane whose id matches
+// a slot (one 16-byte read per bucket probed) tags that slot with kAD + 1 (an
+// id repeated in the neighbour row tags the same slot again, so each
+// (kAD, kAB) pair counts once), and the lane owning rank kAB > kAD counts the
+// row when its slot carries the tag -- src/prune_windowed_core.hpp:177-232.
+// The counts stay in registers; the neighbour row's id is wave-uniform, so
+// its address is scalar work.  Finally the first K valid ranks by
+// (count, rank) are written (src/prune_windowed_core.hpp:234-263).
+// E = list halves of 64.
+__device__ __forceinline__ uint32_t prune_hash(int32_t v, uint32_t mask)
+{
+    return ((static_cast<uint32_t>(v) * 0x9E3779B1u) >> 15) & mask;
+}
+
+template <int E>
 __global__ void __launch_bounds__(256) cagra_prune_kernel(const int32_t* __restrict__ G, int64_t N, int M, int K,
                                                           uint32_t* __restrict__ out,
                                                           unsigned long long* __restrict__ bad_row)
 {
     constexpr int MM = 64 * E;
-    constexpr uint32_t mask = CAP - 1;
-    __shared__ uint64_t tab[4][CAP];
-    __shared__ int32_t stamp[4][MM];
-    __shared__ uint32_t cnt[4][MM];
+    constexpr int NBK = 2 * MM;               // home buckets
+    constexpr int BK = NBK + MM / 4 + 1;      // + spill room: at most MM entries
+    constexpr int SLOTS = 4 * BK;
+    constexpr uint32_t mask = NBK - 1;
+    constexpr uint32_t kEmpty = 0xffffffffu;
+    __shared__ __align__(16) uint32_t tab[4][SLOTS];
+    __shared__ uint32_t tag[4][SLOTS + 64];   // + one scratch word per lane for misses
+    __shared__ __align__(16) uint32_t skey[4][MM];
     __shared__ int32_t sA[4][MM];
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int64_t a = static_cast<int64_t>(blockIdx.x) * 4 + w;
     if (a >= N) return;
 
-    for (int s = lane; s < CAP; s += 64) tab[w][s] = kNoKey;
+    for (int s = lane; s < SLOTS; s += 64) tab[w][s] = kEmpty;
+    for (int s = lane; s < SLOTS + 64; s += 64) tag[w][s] = 0u;
     int32_t A[E];
+    int col[E];
 #pragma unroll
     for (int e = 0; e < E; ++e) {
         const int k = lane + 64 * e;
+        col[e] = k < M ? k : M - 1;
         A[e] = k < M ? G[a * M + k] : -1;
-        stamp[w][k] = -1;
-        cnt[w][k] = 0;
         sA[w][k] = A[e];
     }
     wave_sync();
-    // linear probing; every entry ends up at most dmax slots past its home
+    // insertion; every entry ends up at most dmax buckets past its home
+    int slot[E];
     uint32_t disp = 0;
 #pragma unroll
     for (int e = 0; e < E; ++e) {
-        const int k = lane + 64 * e;
+        slot[e] = SLOTS + lane;   // scratch word: an invalid entry counts nothing that is used
         if (A[e] >= 0) {
-            const uint64_t entry = (static_cast<uint64_t>(static_cast<uint32_t>(A[e])) << 32) | static_cast<uint32_t>(k);
-            const uint32_t home = (static_cast<uint32_t>(A[e]) * 2654435761u) & mask;
-            uint32_t h = home;
-            while (atomicCAS(reinterpret_cast<unsigned long long*>(&tab[w][h]), kNoKey, entry) != kNoKey)
-                h = (h + 1) & mask;
-            disp = max(disp, (h - home) & mask);
+            const uint32_t home = prune_hash(A[e], mask);
+            uint32_t h = 4 * home;
+            while (atomicCAS(&tab[w][h], kEmpty, static_cast<uint32_t>(A[e])) != kEmpty) ++h;
+            slot[e] = static_cast<int>(h);
+            disp = max(disp, h / 4 - home);
         }
     }
 #pragma unroll
@@ -203,37 +219,51 @@ __global__ void __launch_bounds__(256) cagra_prune_kernel(const int32_t* __restr
     const uint32_t dmax = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(disp)));
     wave_sync();
 
-    // rows in flight: raw ids plus whether the row exists; the mask is
-    // applied when the row is probed, so no load is waited for early
+    // rows in flight: raw ids plus whether the row exists; the ids are
+    // checked when the row is probed, so no load is waited for early
     int32_t ring[kPruneDepth][E];
     bool rok[kPruneDepth];
     auto fetch = [&](int kAD, int32_t (&b)[E], bool& ok) {
-        const int32_t d = kAD < M - 1 ? sA[w][kAD] : -1;
+        const int32_t d = __builtin_amdgcn_readfirstlane(kAD < M - 1 ? sA[w][kAD] : -1);
         ok = d >= 0 && d < N;
-        const int64_t row = ok ? static_cast<int64_t>(d) : 0;
+        const int32_t* row = G + (ok ? static_cast<int64_t>(d) : int64_t(0)) * M;
 #pragma unroll
-        for (int e = 0; e < E; ++e) {
-            const int k = lane + 64 * e;
-            b[e] = G[row * M + (k < M ? k : M - 1)];
-        }
+        for (int e = 0; e < E; ++e) b[e] = row[col[e]];
     };
-    // every occurrence of v in row a lies within dmax slots of v's home: a
-    // fixed, wave-uniform number of probes (no divergent loop exits)
+    uint32_t c[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) c[e] = 0;
+    // every occurrence of v in row a lies within dmax buckets of v's home:
+    // a fixed, wave-uniform number of bucket reads; a miss writes the lane's
+    // scratch word, so the common case has no divergent branch
     auto probe = [&](int kd, const int32_t (&b)[E], bool ok) {
         if (!ok) return;
+        const uint32_t t = static_cast<uint32_t>(kd + 1);
 #pragma unroll
         for (int e = 0; e < E; ++e) {
-            const int32_t v = b[e];
-            const bool valid = lane + 64 * e < M && v >= 0;
-            const uint32_t home = (static_cast<uint32_t>(v) * 2654435761u) & mask;
+            const uint32_t v = static_cast<uint32_t>(b[e]);
+            const bool valid = lane + 64 * e < M && b[e] >= 0;
+            const uint32_t home = prune_hash(b[e], mask);
             for (uint32_t s = 0; s <= dmax; ++s) {
-                const uint64_t t = tab[w][(home + s) & mask];
-                const int kab = static_cast<int>(static_cast<uint32_t>(t));
-                if (valid && static_cast<uint32_t>(t >> 32) == static_cast<uint32_t>(v) && kab > kd &&
-                    atomicExch(&stamp[w][kab], kd) != kd)
-                    atomicAdd(&cnt[w][kab], 1u);
+                const uint32_t base = 4 * (home + s);
+                const uint4 x = *reinterpret_cast<const uint4*>(&tab[w][base]);
+                const bool m0 = valid & (x.x == v), m1 = valid & (x.y == v), m2 = valid & (x.z == v),
+                           m3 = valid & (x.w == v);
+                const uint32_t j = m0 ? 0u : m1 ? 1u : m2 ? 2u : 3u;
+                const bool any = m0 | m1 | m2 | m3;
+                tag[w][any ? base + j : static_cast<uint32_t>(SLOTS + lane)] = t;
+                // an id of row a repeated inside one bucket: tag the other copies
+                const bool more = (m0 & (m1 | m2 | m3)) | (m1 & (m2 | m3)) | (m2 & m3);
+                if (__ballot(more)) {
+                    if (m1 && j < 1) tag[w][base + 1] = t;
+                    if (m2 && j < 2) tag[w][base + 2] = t;
+                    if (m3 && j < 3) tag[w][base + 3] = t;
+                }
             }
         }
+        wave_sync();
+#pragma unroll
+        for (int e = 0; e < E; ++e) c[e] += (lane + 64 * e > kd && tag[w][slot[e]] == t) ? 1u : 0u;
     };
 #pragma unroll
     for (int r = 0; r < kPruneDepth; ++r) fetch(r, ring[r], rok[r]);
@@ -244,7 +274,6 @@ __global__ void __launch_bounds__(256) cagra_prune_kernel(const int32_t* __restr
             fetch(kd + r + kPruneDepth, ring[r], rok[r]);
         }
     }
-    wave_sync();
 
     int nvalid = 0;
 #pragma unroll
@@ -253,26 +282,29 @@ __global__ void __launch_bounds__(256) cagra_prune_kernel(const int32_t* __restr
         if (lane == 0) atomicMin(bad_row, static_cast<unsigned long long>(a));
         return;
     }
-    // position = valid entries before this one in (count, rank) order
+    // position = valid entries before this one in (count, rank) order; one
+    // key per entry, count << 8 | rank (counts < 128), invalid = all ones
+    uint32_t key[E];
 #pragma unroll
     for (int e = 0; e < E; ++e) {
-        const int k = lane + 64 * e;
-        const uint32_t c = cnt[w][k];
-        int pos = 0;
-#pragma unroll 4
-        for (int q4 = 0; q4 < MM / 4; ++q4) {
-            const uint4 cq = *reinterpret_cast<const uint4*>(&cnt[w][4 * q4]);
-            const int4 aq = *reinterpret_cast<const int4*>(&sA[w][4 * q4]);
-            const uint32_t c4[4] = {cq.x, cq.y, cq.z, cq.w};
-            const int32_t a4[4] = {aq.x, aq.y, aq.z, aq.w};
-#pragma unroll
-            for (int jj = 0; jj < 4; ++jj) {
-                const int q = 4 * q4 + jj;
-                pos += (a4[jj] >= 0 && (c4[jj] < c || (c4[jj] == c && q < k))) ? 1 : 0;
-            }
-        }
-        if (A[e] >= 0 && pos < K) out[a * K + pos] = static_cast<uint32_t>(A[e]);
+        key[e] = A[e] >= 0 ? (c[e] << 8) | static_cast<uint32_t>(lane + 64 * e) : 0xffffffffu;
+        skey[w][lane + 64 * e] = key[e];
     }
+    wave_sync();
+    int pos[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) pos[e] = 0;
+#pragma unroll 4
+    for (int q4 = 0; q4 < MM / 4; ++q4) {
+        const uint4 kq = *reinterpret_cast<const uint4*>(&skey[w][4 * q4]);
+#pragma unroll
+        for (int e = 0; e < E; ++e)
+            pos[e] += (kq.x < key[e] ? 1 : 0) + (kq.y < key[e] ? 1 : 0) + (kq.z < key[e] ? 1 : 0) +
+                      (kq.w < key[e] ? 1 : 0);
+    }
+#pragma unroll
+    for (int e = 0; e < E; ++e)
+        if (A[e] >= 0 && pos[e] < K) out[a * K + pos[e]] = static_cast<uint32_t>(A[e]);
 }
 
 // ------------------------------------------------------------------ reverse merge
@@ -981,9 +1013,9 @@ void launch_cagra_prune(const int32_t* G, int64_t N, int M, int K, uint32_t* out
     GT_REQUIRE(M >= 1 && M <= kPruneMaxM, "prune supports intermediate degree <= 128");
     if (N <= 0) return;
     if (M <= 64)
-        hipLaunchKernelGGL((cagra_prune_kernel<1, 512>), dim3(grid_for(N, 4)), dim3(256), 0, s, G, N, M, K, out, bad_row);
+        hipLaunchKernelGGL((cagra_prune_kernel<1>), dim3(grid_for(N, 4)), dim3(256), 0, s, G, N, M, K, out, bad_row);
     else
-        hipLaunchKernelGGL((cagra_prune_kernel<2, 512>), dim3(grid_for(N, 4)), dim3(256), 0, s, G, N, M, K, out, bad_row);
+        hipLaunchKernelGGL((cagra_prune_kernel<2>), dim3(grid_for(N, 4)), dim3(256), 0, s, G, N, M, K, out, bad_row);
     GT_HIP(hipGetLastError());
 }
 

@@ -568,12 +568,82 @@ typedef int intx4 __attribute__((ext_vector_type(4)));
 typedef int intx16 __attribute__((ext_vector_type(16)));
 
 template <int DP>
-struct KnnSmemI8 {
+struct KnnSmemI8Tiles {
     int8_t tile[2][kPoolTile][DP + 16];   // +16 bytes: rows land on distinct bank groups
     float tnorm[3][kPoolTile];
     int32_t trow[3][kPoolTile];
+};
+
+template <int DP, bool LISTS>
+struct KnnSmemI8 : KnnSmemI8Tiles<DP> {
     KnnLists L;
 };
+
+template <int DP>
+struct KnnSmemI8<DP, false> : KnnSmemI8Tiles<DP> {};
+
+// Lists of at most kSmallM entries in registers: every lane keeps the best
+// keys among the pool rows it holds (its half of each tile); the two halves
+// of a query are merged once, at the end.  No LDS buffer, no merges.
+struct SmallList {
+    uint64_t k[kSmallM];   // ascending, kNoKey = empty
+    float kth;             // a candidate is kept iff its distance <= kth
+};
+
+__device__ __forceinline__ void small_insert(SmallList& L, uint64_t x)
+{
+#pragma unroll
+    for (int i = 0; i < kSmallM; ++i) {
+        const bool lt = x < L.k[i];
+        const uint64_t lo = lt ? x : L.k[i];
+        x = lt ? L.k[i] : x;
+        L.k[i] = lo;
+    }
+}
+
+__device__ __forceinline__ void small_update_kth(SmallList& L, int M, float seed)
+{
+    const uint64_t km = M <= 1 ? L.k[0] : M == 2 ? L.k[1] : M == 3 ? L.k[2] : L.k[3];
+    L.kth = km == kNoKey ? seed : fminf(seed, o2f(static_cast<uint32_t>(km >> 32)));
+}
+
+// One finished 32x32 tile into the lane's register list.
+template <int METRIC>
+__device__ __forceinline__ void small_tile(const KnnArgs& a, const intx16& acc, const float* tn, const int32_t* tr,
+                                           int tbase, int h, bool qvalid, float qn, const QueryState& st,
+                                           SmallList& L)
+{
+    float dv[16];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const float4 pn = *reinterpret_cast<const float4*>(tn + 8 * g + 4 * h);
+        const float n4[4] = {pn.x, pn.y, pn.z, pn.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float dot = static_cast<float>(acc[4 * g + e]);
+            dv[4 * g + e] = METRIC == 0 ? fmaf(-2.f, dot, n4[e] + qn) : fmaf(-1.f, dot, n4[e]);
+        }
+    }
+    uint32_t pass = 0;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) pass |= static_cast<uint32_t>(qvalid && dv[r] <= L.kth) << r;
+    if (!__ballot(pass != 0u)) return;
+    int32_t idv[16];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const int4 pi = *reinterpret_cast<const int4*>(tr + 8 * g + 4 * h);
+        const int32_t i4[4] = {pi.x, pi.y, pi.z, pi.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) idv[4 * g + e] = a.out_pos ? tbase + 8 * g + 4 * h + e : i4[e];
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) pass &= ~(static_cast<uint32_t>(idv[r] == st.self) << r);
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+        if (__ballot((pass >> r) & 1u))
+            if ((pass >> r) & 1u) small_insert(L, pack_key(dv[r], idv[r]));
+    small_update_kth(L, a.M, st.seed);
+}
 
 __device__ __forceinline__ floatx16 to_float(const intx16& v)
 {
@@ -591,7 +661,7 @@ __global__ void __launch_bounds__(256, 2) knn_i8_kernel(KnnArgs a)
     constexpr int U4_TILE = kPoolTile * U4_ROW;
     constexpr int U4_THREAD = (U4_TILE + 255) / 256;
     static_assert(DP % 32 == 0, "row stride must be a multiple of 32 bytes");
-    __shared__ KnnSmemI8<DP> sm;
+    __shared__ KnnSmemI8<DP, !SMALL> sm;
 
     const int per = a.n_items / 8;
     const int item_idx = static_cast<int>(blockIdx.x % 8) * per + static_cast<int>(blockIdx.x / 8);
@@ -615,7 +685,14 @@ __global__ void __launch_bounds__(256, 2) knn_i8_kernel(KnnArgs a)
     st.nL = 0;
     st.self = a.exclude_self ? qrow : -2;
     st.orow = it.out_base >= 0 ? it.out_base + qlocal : static_cast<int64_t>(qrow);
-    for (int e = lane; e < kQueriesPerWave * kCB; e += 64) sm.L.buf[w * kQueriesPerWave + e / kCB][e % kCB] = kNoKey;
+    SmallList SL;
+    if constexpr (SMALL) {
+#pragma unroll
+        for (int i = 0; i < kSmallM; ++i) SL.k[i] = kNoKey;
+        SL.kth = st.thr;
+    } else {
+        for (int e = lane; e < kQueriesPerWave * kCB; e += 64) sm.L.buf[w * kQueriesPerWave + e / kCB][e % kCB] = kNoKey;
+    }
 
     intx4 qf[KS];
     {
@@ -704,49 +781,77 @@ __global__ void __launch_bounds__(256, 2) knn_i8_kernel(KnnArgs a)
         }
 
         const int pb3 = (t + 2) % 3;
-        float mkey = INFINITY;
+        if constexpr (SMALL) {
+            if (t > 0)
+                small_tile<METRIC>(a, acc_prev, sm.tnorm[pb3], sm.trow[pb3], (t - 1) * kPoolTile, h, qvalid, qn, st,
+                                   SL);
+        } else {
+            float mkey = INFINITY;
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const float4 pn = *reinterpret_cast<const float4*>(&sm.tnorm[pb3][8 * g + 4 * h]);
-            const float n4[4] = {pn.x, pn.y, pn.z, pn.w};
+            for (int g = 0; g < 4; ++g) {
+                const float4 pn = *reinterpret_cast<const float4*>(&sm.tnorm[pb3][8 * g + 4 * h]);
+                const float n4[4] = {pn.x, pn.y, pn.z, pn.w};
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float dot = static_cast<float>(acc_prev[4 * g + e]);
-                const float d = METRIC == 0 ? fmaf(-2.f, dot, n4[e] + qn) : fmaf(-1.f, dot, n4[e]);
-                mkey = fminf(mkey, d);
+                for (int e = 0; e < 4; ++e) {
+                    const float dot = static_cast<float>(acc_prev[4 * g + e]);
+                    const float d = METRIC == 0 ? fmaf(-2.f, dot, n4[e] + qn) : fmaf(-1.f, dot, n4[e]);
+                    mkey = fminf(mkey, d);
+                }
             }
+            if (t > 0 && __ballot(mkey <= st.thr))
+                tile_append<METRIC, false>(sm.L, a, to_float(acc_prev), sm.tnorm[pb3], sm.trow[pb3],
+                                           (t - 1) * kPoolTile, w, lane, h, qlocal, qvalid, qn, st);
         }
-        if (t > 0 && __ballot(mkey <= st.thr))
-            tile_append<METRIC, SMALL>(sm.L, a, to_float(acc_prev), sm.tnorm[pb3], sm.trow[pb3], (t - 1) * kPoolTile, w,
-                                lane, h, qlocal, qvalid, qn, st);
 
         store_rows(buf ^ 1);
         if (tid < kPoolTile) { sm.trow[(t + 1) % 3][tid] = rid_cur; sm.tnorm[(t + 1) % 3][tid] = rn_cur; }
         __syncthreads();
         acc_prev = acc;
     }
-    if (ntiles > 0) {
-        wait_vmem();
-        const int pb3 = (ntiles - 1) % 3;
-        float mkey = INFINITY;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int i = 8 * (r >> 2) + 4 * h + (r & 3);
-            const float pn = sm.tnorm[pb3][i];
-            const float dot = static_cast<float>(acc_prev[r]);
-            mkey = fminf(mkey, METRIC == 0 ? fmaf(-2.f, dot, pn + qn) : fmaf(-1.f, dot, pn));
+    if constexpr (SMALL) {
+        if (ntiles > 0) {
+            wait_vmem();
+            const int pb3 = (ntiles - 1) % 3;
+            small_tile<METRIC>(a, acc_prev, sm.tnorm[pb3], sm.trow[pb3], (ntiles - 1) * kPoolTile, h, qvalid, qn, st,
+                               SL);
         }
-        if (__ballot(mkey <= st.thr))
-            tile_append<METRIC, SMALL>(sm.L, a, to_float(acc_prev), sm.tnorm[pb3], sm.trow[pb3], (ntiles - 1) * kPoolTile, w,
-                                lane, h, qlocal, qvalid, qn, st);
-    }
+        // the second half's keys join the first half's list
+        uint64_t other[kSmallM];
+#pragma unroll
+        for (int i = 0; i < kSmallM; ++i) other[i] = __shfl(SL.k[i], j + 32);
+        if (qvalid && h == 0) {
+#pragma unroll
+            for (int i = 0; i < kSmallM; ++i) small_insert(SL, other[i]);
+            for (int p = 0; p < a.M; ++p) {
+                const uint64_t kp = p == 0 ? SL.k[0] : p == 1 ? SL.k[1] : p == 2 ? SL.k[2] : SL.k[3];
+                a.out_ids[st.orow * a.M + p] = kp == kNoKey ? -1 : static_cast<int32_t>(static_cast<uint32_t>(kp));
+                a.out_d[st.orow * a.M + p] = kp == kNoKey ? INFINITY : o2f(static_cast<uint32_t>(kp >> 32));
+            }
+        }
+    } else {
+        if (ntiles > 0) {
+            wait_vmem();
+            const int pb3 = (ntiles - 1) % 3;
+            float mkey = INFINITY;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int i = 8 * (r >> 2) + 4 * h + (r & 3);
+                const float pn = sm.tnorm[pb3][i];
+                const float dot = static_cast<float>(acc_prev[r]);
+                mkey = fminf(mkey, METRIC == 0 ? fmaf(-2.f, dot, pn + qn) : fmaf(-1.f, dot, pn));
+            }
+            if (__ballot(mkey <= st.thr))
+                tile_append<METRIC, false>(sm.L, a, to_float(acc_prev), sm.tnorm[pb3], sm.trow[pb3],
+                                           (ntiles - 1) * kPoolTile, w, lane, h, qlocal, qvalid, qn, st);
+        }
 
-    wait_vmem();
-    merge_queries<SMALL>(sm.L, a, w, lane, __ballot(qvalid && st.cnt > 0) & 0xffffffffull, st);
-    if (qvalid) {
-        for (int p = st.nL + h; p < a.M; p += 2) {
-            a.out_ids[st.orow * a.M + p] = -1;
-            a.out_d[st.orow * a.M + p] = INFINITY;
+        wait_vmem();
+        merge_queries<false>(sm.L, a, w, lane, __ballot(qvalid && st.cnt > 0) & 0xffffffffull, st);
+        if (qvalid) {
+            for (int p = st.nL + h; p < a.M; p += 2) {
+                a.out_ids[st.orow * a.M + p] = -1;
+                a.out_d[st.orow * a.M + p] = INFINITY;
+            }
         }
     }
 }

@@ -50,6 +50,22 @@ def test_knn_exact_ip(ctx, dtype):
     np.testing.assert_array_equal(-dist, rd)
 
 
+@pytest.mark.parametrize("dtype", [np.int8, np.uint8])
+@pytest.mark.parametrize("k", [1, 2, 3, 4])
+def test_knn_exact_short_lists(ctx, dtype, k):
+    # lists of at most 4 entries stay in registers (one partial list per
+    # half-wave, merged at the end); ties are frequent on a narrow range
+    X = _data(3000, 128, dtype, seed=40 + k, lo=0 if dtype == np.uint8 else -3, hi=4)
+    ids, dist = ctx.knn_exact(X, k)
+    rid, rd = O.knn_exact(X.astype(np.float32), k)
+    assert_knn_equal(ids, dist, rid, rd)
+    q = np.arange(0, 3000, 7)
+    ids, dist = ctx.knn_exact(X, k, queries=q, metric="ip")
+    rid, rd = O.knn_exact(X.astype(np.float32), k, queries=q, metric=1)
+    np.testing.assert_array_equal(ids, rid)
+    np.testing.assert_array_equal(-dist, rd)
+
+
 def test_knn_exact_query_subset_split_pool(ctx):
     X = _data(40000, 128, np.int8, seed=1)
     q = np.random.default_rng(2).choice(40000, size=300, replace=False)
