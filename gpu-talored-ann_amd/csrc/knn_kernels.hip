@@ -72,12 +72,19 @@ struct KnnLists {
 };
 
 template <int DP>
-struct KnnSmem {
+struct KnnSmemTiles {
     float tile[2][kPoolTile][DP + 4];   // +4 floats: rows land on distinct bank groups
     float tnorm[3][kPoolTile];          // |p|^2 (L2) or 0 (IP); +inf past the slice end
     int32_t trow[3][kPoolTile];         // pool row id, -1 past the slice end
+};
+
+template <int DP, bool LISTS = true>
+struct KnnSmem : KnnSmemTiles<DP> {
     KnnLists L;
 };
+
+template <int DP>
+struct KnnSmem<DP, false> : KnnSmemTiles<DP> {};
 
 // Per-lane view of one query's state.  Lanes j and j+32 of a wave hold the
 // same query (both halves of the MFMA's k split) and keep identical copies.
@@ -318,6 +325,87 @@ __device__ __forceinline__ void merge_queries(KnnLists& sm, const KnnArgs& a, in
     }
 }
 
+// Lists of at most kSmallM entries in registers: every lane keeps the best
+// keys among the pool rows it holds (its half of each tile); the two halves
+// of a query are merged once, at the end.  No LDS buffer, no merges.
+struct SmallList {
+    uint64_t k[kSmallM];   // ascending, kNoKey = empty
+    float kth;             // a candidate is kept iff its distance <= kth
+};
+
+__device__ __forceinline__ void small_insert(SmallList& L, uint64_t x)
+{
+#pragma unroll
+    for (int i = 0; i < kSmallM; ++i) {
+        const bool lt = x < L.k[i];
+        const uint64_t lo = lt ? x : L.k[i];
+        x = lt ? L.k[i] : x;
+        L.k[i] = lo;
+    }
+}
+
+__device__ __forceinline__ void small_update_kth(SmallList& L, int M, float seed)
+{
+    const uint64_t km = M <= 1 ? L.k[0] : M == 2 ? L.k[1] : M == 3 ? L.k[2] : L.k[3];
+    L.kth = km == kNoKey ? seed : fminf(seed, o2f(static_cast<uint32_t>(km >> 32)));
+}
+
+// One finished 32x32 tile into the lane's register list.
+template <int METRIC, typename Acc>
+__device__ __forceinline__ void small_tile(const KnnArgs& a, const Acc& acc, const float* tn, const int32_t* tr,
+                                           int tbase, int h, bool qvalid, float qn, const QueryState& st,
+                                           SmallList& L)
+{
+    float dv[16];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const float4 pn = *reinterpret_cast<const float4*>(tn + 8 * g + 4 * h);
+        const float n4[4] = {pn.x, pn.y, pn.z, pn.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float dot = static_cast<float>(acc[4 * g + e]);
+            dv[4 * g + e] = METRIC == 0 ? fmaf(-2.f, dot, n4[e] + qn) : fmaf(-1.f, dot, n4[e]);
+        }
+    }
+    uint32_t pass = 0;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) pass |= static_cast<uint32_t>(qvalid && dv[r] <= L.kth) << r;
+    if (!__ballot(pass != 0u)) return;
+    int32_t idv[16];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const int4 pi = *reinterpret_cast<const int4*>(tr + 8 * g + 4 * h);
+        const int32_t i4[4] = {pi.x, pi.y, pi.z, pi.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) idv[4 * g + e] = a.out_pos ? tbase + 8 * g + 4 * h + e : i4[e];
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) pass &= ~(static_cast<uint32_t>(idv[r] == st.self) << r);
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+        if (__ballot((pass >> r) & 1u))
+            if ((pass >> r) & 1u) small_insert(L, pack_key(dv[r], idv[r]));
+    small_update_kth(L, a.M, st.seed);
+}
+
+// The second half-wave's keys join the first half's list, which lane j
+// writes to output row orow (padding -1 / +inf).
+__device__ __forceinline__ void small_finish(const KnnArgs& a, SmallList& L, int j, int h, bool qvalid, int64_t orow)
+{
+    uint64_t other[kSmallM];
+#pragma unroll
+    for (int i = 0; i < kSmallM; ++i) other[i] = __shfl(L.k[i], j + 32);
+    if (qvalid && h == 0) {
+#pragma unroll
+        for (int i = 0; i < kSmallM; ++i) small_insert(L, other[i]);
+        for (int p = 0; p < a.M; ++p) {
+            const uint64_t kp = p == 0 ? L.k[0] : p == 1 ? L.k[1] : p == 2 ? L.k[2] : L.k[3];
+            a.out_ids[orow * a.M + p] = kp == kNoKey ? -1 : static_cast<int32_t>(static_cast<uint32_t>(kp));
+            a.out_d[orow * a.M + p] = kp == kNoKey ? INFINITY : o2f(static_cast<uint32_t>(kp >> 32));
+        }
+    }
+}
+
 // Filter + append of one finished 32x32 tile whose pool rows have norms
 // tn[0..32) and ids tr[0..32) (tbase = pool-list position of row 0), the slow
 // path taken only when some lane of the wave has a candidate <= its threshold.
@@ -376,14 +464,15 @@ __device__ __forceinline__ void tile_append(KnnLists& sm, const KnnArgs& a, cons
     }
 }
 
-template <int DP, int METRIC>
+// SMALL: lists of at most kSmallM entries, kept in registers (SmallList).
+template <int DP, int METRIC, bool SMALL>
 __global__ void __launch_bounds__(256, 2) knn_fused_kernel(KnnArgs a)
 {
     constexpr int DH = DP / 2;                    // k-steps of 2 dims (one per half wave)
     constexpr int F4_ROW = DP / 4;
     constexpr int F4_THREAD = kPoolTile * F4_ROW / 256;
     static_assert(DP % 32 == 0, "row stride must be a multiple of 32 floats");
-    __shared__ KnnSmem<DP> sm;
+    __shared__ KnnSmem<DP, !SMALL> sm;
 
     // Work items are laid out XCD-major by the host: the hardware deals
     // consecutive workgroups round-robin over the 8 XCDs, so XCD x runs items
@@ -410,8 +499,15 @@ __global__ void __launch_bounds__(256, 2) knn_fused_kernel(KnnArgs a)
     st.nL = 0;
     st.self = a.exclude_self ? qrow : -2;
     st.orow = it.out_base >= 0 ? it.out_base + qlocal : static_cast<int64_t>(qrow);
-    // this wave's 32 buffer rows start empty: every slot holds kNoKey
-    for (int e = lane; e < kQueriesPerWave * kCB; e += 64) sm.L.buf[w * kQueriesPerWave + e / kCB][e % kCB] = kNoKey;
+    SmallList SL;
+    if constexpr (SMALL) {
+#pragma unroll
+        for (int i = 0; i < kSmallM; ++i) SL.k[i] = kNoKey;
+        SL.kth = st.thr;
+    } else {
+        // this wave's 32 buffer rows start empty: every slot holds kNoKey
+        for (int e = lane; e < kQueriesPerWave * kCB; e += 64) sm.L.buf[w * kQueriesPerWave + e / kCB][e % kCB] = kNoKey;
+    }
 
     // query fragment: dims [h*DH, h*DH + DH) of query row qrow
     float qf[DH];
@@ -508,49 +604,65 @@ __global__ void __launch_bounds__(256, 2) knn_fused_kernel(KnnArgs a)
         // chain above: min key per lane.  acc_prev[r] is D[i][j] with
         // i = 8*(r/4) + 4*h + r%4.  Rows past the slice have +inf norm.
         const int pb3 = (t + 2) % 3;   // (t-1) mod 3
-        float mkey = INFINITY;
+        if constexpr (SMALL) {
+            if (t > 0)
+                small_tile<METRIC>(a, acc_prev, sm.tnorm[pb3], sm.trow[pb3], (t - 1) * kPoolTile, h, qvalid, qn, st,
+                                   SL);
+        } else {
+            float mkey = INFINITY;
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const float4 pn = *reinterpret_cast<const float4*>(&sm.tnorm[pb3][8 * g + 4 * h]);
-            const float n4[4] = {pn.x, pn.y, pn.z, pn.w};
+            for (int g = 0; g < 4; ++g) {
+                const float4 pn = *reinterpret_cast<const float4*>(&sm.tnorm[pb3][8 * g + 4 * h]);
+                const float n4[4] = {pn.x, pn.y, pn.z, pn.w};
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float d = METRIC == 0 ? fmaf(-2.f, acc_prev[4 * g + e], n4[e] + qn)
-                                            : fmaf(-1.f, acc_prev[4 * g + e], n4[e]);
-                mkey = fminf(mkey, d);
+                for (int e = 0; e < 4; ++e) {
+                    const float d = METRIC == 0 ? fmaf(-2.f, acc_prev[4 * g + e], n4[e] + qn)
+                                                : fmaf(-1.f, acc_prev[4 * g + e], n4[e]);
+                    mkey = fminf(mkey, d);
+                }
             }
+            if (t > 0 && __ballot(mkey <= st.thr))
+                tile_append<METRIC, true>(sm.L, a, acc_prev, sm.tnorm[pb3], sm.trow[pb3], (t - 1) * kPoolTile, w,
+                                           lane, h, qlocal, qvalid, qn, st);
         }
-        if (t > 0 && __ballot(mkey <= st.thr))
-            tile_append<METRIC, true>(sm.L, a, acc_prev, sm.tnorm[pb3], sm.trow[pb3], (t - 1) * kPoolTile, w, lane, h,
-                                qlocal, qvalid, qn, st);
 
         store_rows(buf ^ 1);
         if (tid < kPoolTile) { sm.trow[(t + 1) % 3][tid] = rid_cur; sm.tnorm[(t + 1) % 3][tid] = rn_cur; }
         __syncthreads();
         acc_prev = acc;
     }
-    if (ntiles > 0) {
-        wait_vmem();   // list rows stored by the last iteration's merges
-        const int pb3 = (ntiles - 1) % 3;
-        float mkey = INFINITY;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int i = 8 * (r >> 2) + 4 * h + (r & 3);
-            const float pn = sm.tnorm[pb3][i];
-            mkey = fminf(mkey, METRIC == 0 ? fmaf(-2.f, acc_prev[r], pn + qn) : fmaf(-1.f, acc_prev[r], pn));
+    if constexpr (SMALL) {
+        if (ntiles > 0) {
+            wait_vmem();
+            const int pb3 = (ntiles - 1) % 3;
+            small_tile<METRIC>(a, acc_prev, sm.tnorm[pb3], sm.trow[pb3], (ntiles - 1) * kPoolTile, h, qvalid, qn, st,
+                               SL);
         }
-        if (__ballot(mkey <= st.thr))
-            tile_append<METRIC, true>(sm.L, a, acc_prev, sm.tnorm[pb3], sm.trow[pb3], (ntiles - 1) * kPoolTile, w, lane,
-                                h, qlocal, qvalid, qn, st);
-    }
+        small_finish(a, SL, j, h, qvalid, st.orow);
+    } else {
+        if (ntiles > 0) {
+            wait_vmem();   // list rows stored by the last iteration's merges
+            const int pb3 = (ntiles - 1) % 3;
+            float mkey = INFINITY;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int i = 8 * (r >> 2) + 4 * h + (r & 3);
+                const float pn = sm.tnorm[pb3][i];
+                mkey = fminf(mkey, METRIC == 0 ? fmaf(-2.f, acc_prev[r], pn + qn) : fmaf(-1.f, acc_prev[r], pn));
+            }
+            if (__ballot(mkey <= st.thr))
+                tile_append<METRIC, true>(sm.L, a, acc_prev, sm.tnorm[pb3], sm.trow[pb3], (ntiles - 1) * kPoolTile, w,
+                                           lane, h, qlocal, qvalid, qn, st);
+        }
 
-    // flush the remaining buffers
-    wait_vmem();
-    merge_queries<true>(sm.L, a, w, lane, __ballot(qvalid && st.cnt > 0) & 0xffffffffull, st);
-    if (qvalid) {
-        for (int p = st.nL + h; p < a.M; p += 2) {
-            a.out_ids[st.orow * a.M + p] = -1;
-            a.out_d[st.orow * a.M + p] = INFINITY;
+        // flush the remaining buffers
+        wait_vmem();
+        merge_queries<true>(sm.L, a, w, lane, __ballot(qvalid && st.cnt > 0) & 0xffffffffull, st);
+        if (qvalid) {
+            for (int p = st.nL + h; p < a.M; p += 2) {
+                a.out_ids[st.orow * a.M + p] = -1;
+                a.out_d[st.orow * a.M + p] = INFINITY;
+            }
         }
     }
 }
@@ -582,68 +694,6 @@ struct KnnSmemI8 : KnnSmemI8Tiles<DP> {
 template <int DP>
 struct KnnSmemI8<DP, false> : KnnSmemI8Tiles<DP> {};
 
-// Lists of at most kSmallM entries in registers: every lane keeps the best
-// keys among the pool rows it holds (its half of each tile); the two halves
-// of a query are merged once, at the end.  No LDS buffer, no merges.
-struct SmallList {
-    uint64_t k[kSmallM];   // ascending, kNoKey = empty
-    float kth;             // a candidate is kept iff its distance <= kth
-};
-
-__device__ __forceinline__ void small_insert(SmallList& L, uint64_t x)
-{
-#pragma unroll
-    for (int i = 0; i < kSmallM; ++i) {
-        const bool lt = x < L.k[i];
-        const uint64_t lo = lt ? x : L.k[i];
-        x = lt ? L.k[i] : x;
-        L.k[i] = lo;
-    }
-}
-
-__device__ __forceinline__ void small_update_kth(SmallList& L, int M, float seed)
-{
-    const uint64_t km = M <= 1 ? L.k[0] : M == 2 ? L.k[1] : M == 3 ? L.k[2] : L.k[3];
-    L.kth = km == kNoKey ? seed : fminf(seed, o2f(static_cast<uint32_t>(km >> 32)));
-}
-
-// One finished 32x32 tile into the lane's register list.
-template <int METRIC>
-__device__ __forceinline__ void small_tile(const KnnArgs& a, const intx16& acc, const float* tn, const int32_t* tr,
-                                           int tbase, int h, bool qvalid, float qn, const QueryState& st,
-                                           SmallList& L)
-{
-    float dv[16];
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-        const float4 pn = *reinterpret_cast<const float4*>(tn + 8 * g + 4 * h);
-        const float n4[4] = {pn.x, pn.y, pn.z, pn.w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const float dot = static_cast<float>(acc[4 * g + e]);
-            dv[4 * g + e] = METRIC == 0 ? fmaf(-2.f, dot, n4[e] + qn) : fmaf(-1.f, dot, n4[e]);
-        }
-    }
-    uint32_t pass = 0;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) pass |= static_cast<uint32_t>(qvalid && dv[r] <= L.kth) << r;
-    if (!__ballot(pass != 0u)) return;
-    int32_t idv[16];
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-        const int4 pi = *reinterpret_cast<const int4*>(tr + 8 * g + 4 * h);
-        const int32_t i4[4] = {pi.x, pi.y, pi.z, pi.w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) idv[4 * g + e] = a.out_pos ? tbase + 8 * g + 4 * h + e : i4[e];
-    }
-#pragma unroll
-    for (int r = 0; r < 16; ++r) pass &= ~(static_cast<uint32_t>(idv[r] == st.self) << r);
-#pragma unroll
-    for (int r = 0; r < 16; ++r)
-        if (__ballot((pass >> r) & 1u))
-            if ((pass >> r) & 1u) small_insert(L, pack_key(dv[r], idv[r]));
-    small_update_kth(L, a.M, st.seed);
-}
 
 __device__ __forceinline__ floatx16 to_float(const intx16& v)
 {
@@ -815,19 +865,7 @@ __global__ void __launch_bounds__(256, 2) knn_i8_kernel(KnnArgs a)
             small_tile<METRIC>(a, acc_prev, sm.tnorm[pb3], sm.trow[pb3], (ntiles - 1) * kPoolTile, h, qvalid, qn, st,
                                SL);
         }
-        // the second half's keys join the first half's list
-        uint64_t other[kSmallM];
-#pragma unroll
-        for (int i = 0; i < kSmallM; ++i) other[i] = __shfl(SL.k[i], j + 32);
-        if (qvalid && h == 0) {
-#pragma unroll
-            for (int i = 0; i < kSmallM; ++i) small_insert(SL, other[i]);
-            for (int p = 0; p < a.M; ++p) {
-                const uint64_t kp = p == 0 ? SL.k[0] : p == 1 ? SL.k[1] : p == 2 ? SL.k[2] : SL.k[3];
-                a.out_ids[st.orow * a.M + p] = kp == kNoKey ? -1 : static_cast<int32_t>(static_cast<uint32_t>(kp));
-                a.out_d[st.orow * a.M + p] = kp == kNoKey ? INFINITY : o2f(static_cast<uint32_t>(kp >> 32));
-            }
-        }
+        small_finish(a, SL, j, h, qvalid, st.orow);
     } else {
         if (ntiles > 0) {
             wait_vmem();
@@ -1101,23 +1139,38 @@ __global__ void __launch_bounds__(64) merge_partials_kernel(const int32_t* __res
     }
 }
 
-template <int METRIC>
-static void launch_knn_metric(const KnnArgs& a, dim3 grid, hipStream_t stream)
+template <int METRIC, bool SMALL>
+static void launch_knn_fused_v(const KnnArgs& a, dim3 grid, hipStream_t stream)
 {
     switch (a.Dp) {
-    case 32:  hipLaunchKernelGGL((knn_fused_kernel<32, METRIC>), grid, dim3(256), 0, stream, a); break;
-    case 64:  hipLaunchKernelGGL((knn_fused_kernel<64, METRIC>), grid, dim3(256), 0, stream, a); break;
-    case 96:  hipLaunchKernelGGL((knn_fused_kernel<96, METRIC>), grid, dim3(256), 0, stream, a); break;
-    case 128: hipLaunchKernelGGL((knn_fused_kernel<128, METRIC>), grid, dim3(256), 0, stream, a); break;
-    case 160: hipLaunchKernelGGL((knn_fused_kernel<160, METRIC>), grid, dim3(256), 0, stream, a); break;
-    case 192: hipLaunchKernelGGL((knn_fused_kernel<192, METRIC>), grid, dim3(256), 0, stream, a); break;
-    case 224: hipLaunchKernelGGL((knn_fused_kernel<224, METRIC>), grid, dim3(256), 0, stream, a); break;
-    case 256: hipLaunchKernelGGL((knn_fused_kernel<256, METRIC>), grid, dim3(256), 0, stream, a); break;
+    case 32:  hipLaunchKernelGGL((knn_fused_kernel<32, METRIC, SMALL>), grid, dim3(256), 0, stream, a); break;
+    case 64:  hipLaunchKernelGGL((knn_fused_kernel<64, METRIC, SMALL>), grid, dim3(256), 0, stream, a); break;
+    case 96:  hipLaunchKernelGGL((knn_fused_kernel<96, METRIC, SMALL>), grid, dim3(256), 0, stream, a); break;
+    case 128: hipLaunchKernelGGL((knn_fused_kernel<128, METRIC, SMALL>), grid, dim3(256), 0, stream, a); break;
+    case 160: hipLaunchKernelGGL((knn_fused_kernel<160, METRIC, SMALL>), grid, dim3(256), 0, stream, a); break;
+    case 192: hipLaunchKernelGGL((knn_fused_kernel<192, METRIC, SMALL>), grid, dim3(256), 0, stream, a); break;
+    case 224:
+        if constexpr (!SMALL) hipLaunchKernelGGL((knn_fused_kernel<224, METRIC, false>), grid, dim3(256), 0, stream, a);
+        else GT_REQUIRE(false, "short lists in registers: rows up to 192");
+        break;
+    case 256:
+        if constexpr (!SMALL) hipLaunchKernelGGL((knn_fused_kernel<256, METRIC, false>), grid, dim3(256), 0, stream, a);
+        else GT_REQUIRE(false, "short lists in registers: rows up to 192");
+        break;
     default:
         GT_REQUIRE(a.Dp % kWideChunk == 0 && a.Dp > 256, "padded dimension " + std::to_string(a.Dp) + " not supported");
         hipLaunchKernelGGL((knn_wide_kernel<METRIC>), grid, dim3(256), 0, stream, a);
         break;
     }
+}
+
+template <int METRIC>
+static void launch_knn_metric(const KnnArgs& a, dim3 grid, hipStream_t stream)
+{
+    // register lists would spill beside the query fragments of rows longer
+    // than 192: those keep the LDS-buffer path (with its short-list merge)
+    if (a.M <= kSmallM && a.Dp <= 192) launch_knn_fused_v<METRIC, true>(a, grid, stream);
+    else launch_knn_fused_v<METRIC, false>(a, grid, stream);
 }
 
 // SMALL: lists of at most kSmallM entries (assignment against centroids);
