@@ -220,8 +220,10 @@ def main():
     prune_bytes = N * (4 * cfg.M + 4 * cfg.M * (cfg.M - 1) + 4 * cfg.K)
     merge_bytes = 28 * N * cfg.K
 
-    # integer datasets of up to 256 dimensions run the int8 kernel
-    int8 = cfg.dtype in ("i8", "u8") and D <= 256
+    # integer-typed datasets of up to 256 dimensions run the int8 kernel, and
+    # so do float datasets whose values are all integers in [-128, 127] or
+    # [0, 255] (the library's int_exact: exact, the fp32 kernel's keys)
+    int8 = bool(round(s["knn_int8"]))
     dtype = "i8" if int8 else "fp32"
     mip = 1 if cfg.metric == "ip" else 0
     if int8:
@@ -232,7 +234,7 @@ def main():
         kname, peak, punit = f"knn_wide_kernel<{mip}>", PEAK_FP32_MFMA, "TFLOP/s"
     out = {
         "metric": f"graph build Mpts/s at {N // 1000000 if N >= 1000000 else N}"
-                  f"{'M' if N >= 1000000 else ''}x{D} {cfg.dtype if int8 else 'fp32'} deg{cfg.K} "
+                  f"{'M' if N >= 1000000 else ''}x{D} {'fp32' if cfg.dtype == 'f32' else cfg.dtype} deg{cfg.K} "
                   f"(build seconds = ms_per_step/1000)",
         "value": N / wall / 1e6,
         "unit": "Mpts/s",
@@ -243,7 +245,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": dtype,
+        "dtype": dtype if cfg.dtype != "f32" or not int8 else "i8 (exact: integer-valued fp32 rows, int32 sums)",
         "data": "synthetic (seeded Gaussian mixture, gpu-talored-ann_amd/synth.py)",
         "config": {
             "workload": f"{args.config}: {N} x {D} {cfg.dtype}, {cfg.metric.upper()}, {cfg.buckets} buckets, "
@@ -271,6 +273,33 @@ def main():
                               "bytes": merge_bytes, "includes": "count + scan + scatter + merge"},
         "max_pool": int(s["max_pool"]), "max_bucket": int(s["max_bucket"]),
     }
+    if int8 and cfg.dtype == "f32":
+        # the same build on the fp32 kernel (int_exact off): its time, its
+        # fraction of the fp32 matrix peak, and the check that both paths
+        # return the same table and graph
+        kw32 = dict(kw, int_exact=False)
+        ctx.build_graph(Xd, **kw32)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        st32 = []
+        for _ in range(max(1, min(args.steps, 3))):
+            r32 = ctx.build_graph(Xd, **kw32)
+            st32.append(r32.stats)
+        torch.cuda.synchronize()
+        wall32 = (time.perf_counter() - t1) / len(st32)
+        s32 = {k: float(np.mean([st[k] for st in st32])) for k in st32[0]}
+        l32 = max(1, int(round(s32["knn_launches"])))
+        ach32 = (s32["knn_flops"] / l32) / (s32["t_knn"] / l32)
+        same = bool(torch.equal(r32.knn_ids, res.knn_ids) and torch.equal(r32.graph, res.graph))
+        out["fp32_path"] = {
+            "note": "int_exact=0: same dataset on knn_fused_kernel (fp32 matrix cores)",
+            "value": N / wall32 / 1e6, "unit": "Mpts/s", "ms_per_step": wall32 * 1e3,
+            "identical_table_and_graph": same,
+            "roofline": {"kernel": f"knn_fused_kernel<{-(-D // 32) * 32}, {mip}>", "bound": "mfma",
+                         "achieved": ach32 / 1e12, "peak": PEAK_FP32_MFMA / 1e12, "unit": "TFLOP/s",
+                         "frac": ach32 / PEAK_FP32_MFMA, "launch_ms": s32["t_knn"] / l32 * 1e3},
+        }
+        del r32
     if args.search_queries > 0:
         del Xd, res
         out["search"] = search_leg(ctx, torch, args.search_config, args.search_queries,

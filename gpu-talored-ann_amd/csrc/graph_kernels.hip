@@ -59,6 +59,36 @@ __global__ void pad_i8_kernel(const T* __restrict__ src, int8_t* __restrict__ ds
 
 // int8 copy of float rows (centroids of an integer dataset): the value
 // minus the dataset's shift, rounded and clamped; padding stays 0.
+// Whether every value of a float matrix is an integer, and the range of the
+// values: out[0] |= 1 on a non-integer or non-finite value; out[1] / out[2]
+// = min / max as ints (atomics; the host starts them at INT_MAX / INT_MIN).
+__global__ void __launch_bounds__(256) int_range_kernel(const float* __restrict__ X, int64_t n,
+                                                        int* __restrict__ out)
+{
+    float lo = INFINITY, hi = -INFINITY;
+    bool bad = false;
+    for (int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < n;
+         e += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const float v = X[e];
+        bad |= !(v == rintf(v)) || !(fabsf(v) < 1e9f);   // NaN and +-inf fail too
+        lo = fminf(lo, v);
+        hi = fmaxf(hi, v);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        lo = fminf(lo, __shfl_xor(lo, o));
+        hi = fmaxf(hi, __shfl_xor(hi, o));
+    }
+    const bool any_bad = __ballot(bad) != 0;
+    if ((threadIdx.x & 63) == 0) {
+        if (any_bad) atomicOr(&out[0], 1);
+        if (lo <= hi && !any_bad) {
+            atomicMin(&out[1], static_cast<int>(lo));
+            atomicMax(&out[2], static_cast<int>(hi));
+        }
+    }
+}
+
 __global__ void quantize_i8_kernel(const float* __restrict__ src, int64_t N, int D, int Dp, int shift,
                                    int8_t* __restrict__ dst)
 {
@@ -961,6 +991,14 @@ void launch_pad_i8(const void* src, int dtype, int8_t* dst, int64_t N, int D, in
         hipLaunchKernelGGL(pad_i8_kernel<uint8_t>, dim3(grid), dim3(256), 0, s, static_cast<const uint8_t*>(src), dst, N, D, Dp, 128);
     else
         hipLaunchKernelGGL(pad_i8_kernel<int8_t>, dim3(grid), dim3(256), 0, s, static_cast<const int8_t*>(src), dst, N, D, Dp, 0);
+    GT_HIP(hipGetLastError());
+}
+
+void launch_int_range(const float* X, int64_t n, int* out, hipStream_t s)
+{
+    if (n <= 0) return;
+    const unsigned grid = static_cast<unsigned>(std::min<int64_t>(4096, (n + 2047) / 2048));
+    hipLaunchKernelGGL(int_range_kernel, dim3(grid), dim3(256), 0, s, X, n, out);
     GT_HIP(hipGetLastError());
 }
 

@@ -9,6 +9,7 @@
 #include <algorithm>
 #include <atomic>
 #include <chrono>
+#include <climits>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -34,6 +35,7 @@ void launch_row_norms(const float* X, int64_t N, int Dp, float* norms, hipStream
 void launch_pad_i8(const void* src, int dtype, int8_t* dst, int64_t N, int D, int Dp, hipStream_t s);
 void launch_row_norms_i8(const int8_t* X, int64_t N, int Dp, float* norms, hipStream_t s);
 void launch_quantize_i8(const float* src, int64_t N, int D, int Dp, int shift, int8_t* dst, hipStream_t s);
+void launch_int_range(const float* X, int64_t n, int* out, hipStream_t s);
 void launch_copy_ranges(const void* tasks, int64_t ntasks, const int32_t* members, int32_t* pool, hipStream_t s);
 void launch_negate(float* d, int64_t n, hipStream_t s);
 void launch_graph_search(const SearchArgs& a, int64_t grid, hipStream_t s);
@@ -275,11 +277,13 @@ struct DevMatrix {
     int D = 0;
     int Dp = 0;
     // int8 rows of integer-typed inputs (uint8 shifted by -shift), stride
-    // Dp8 bytes, with their exact |x|^2; null for fp32 inputs
+    // Dp8 bytes, with their exact |x|^2; null for fp32 inputs unless every
+    // value is an integer in [-128, 127] or [0, 255] (from_float)
     const int8_t* data8 = nullptr;
     const float* norms8 = nullptr;
     int Dp8 = 0;
     int shift = 0;
+    bool from_float = false;
 };
 
 // The int8 kernel runs a (query, pool) pair when both sides have int8 rows
@@ -292,8 +296,12 @@ static bool use_i8(const DevMatrix& q, const DevMatrix& p, int metric)
 // padded fp32 device copy (or the caller's own device buffer when it already
 // has that layout) plus row norms; with_i8: also int8 rows for integer inputs
 // of at most 256 dimensions
+// with_i8: also an int8 copy for the int8 matrix cores, for integer-typed
+// inputs and (int_exact) for float inputs whose values are all integers in
+// [-128, 127] or [0, 255] -- there every distance is an exact integer below
+// 2^24 in both kernels, so the int8 kernel returns the fp32 kernel's keys.
 static DevMatrix prepare(Ctx& c, int slot_x, int slot_raw, int slot_norms, const void* X, int64_t N, int D, int dtype,
-                         bool with_i8 = false)
+                         bool with_i8 = false, bool int_exact = false)
 {
     GT_REQUIRE(X != nullptr && N > 0 && D > 0, "empty dataset");
     GT_REQUIRE(N < (int64_t(1) << 31), "N must be < 2^31");
@@ -330,6 +338,26 @@ static DevMatrix prepare(Ctx& c, int slot_x, int slot_raw, int slot_norms, const
         launch_row_norms_i8(x8, N, Dp, n8, c.s);
         m.data8 = x8;
         m.norms8 = n8;
+    } else if (with_i8 && int_exact && dtype == GT_DTYPE_F32 && Dp <= 256) {
+        int* fl = c.ws<int>(W_FLAG, 4);
+        const int init[3] = {0, INT_MAX, INT_MIN};
+        c.h2d(fl, init, sizeof(init));
+        launch_int_range(m.data, N * Dp, fl, c.s);   // padding columns are zeros
+        int h[3];
+        c.d2h(h, fl, sizeof(h));
+        c.sync();
+        const int shift = h[0] ? -1 : (h[1] >= -128 && h[2] <= 127) ? 0 : (h[1] >= 0 && h[2] <= 255) ? 128 : -1;
+        if (shift >= 0) {
+            m.Dp8 = Dp;
+            m.shift = shift;
+            m.from_float = true;
+            int8_t* x8 = c.ws<int8_t>(W_X8, static_cast<size_t>(N) * Dp);
+            launch_quantize_i8(m.data, N, D, Dp, shift, x8, c.s);   // exact: integers minus the shift; padding 0
+            float* n8 = c.ws<float>(W_NORMS8, static_cast<size_t>(N));
+            launch_row_norms_i8(x8, N, Dp, n8, c.s);
+            m.data8 = x8;
+            m.norms8 = n8;
+        }
     }
     return m;
 }
@@ -769,7 +797,9 @@ static void bucket_device(Ctx& c, const DevMatrix& X, int64_t C, int nprobe, int
     // centroids rounded to the dataset's values (the buckets only need
     // near centroids; every distance is then exact for those)
     auto refresh_c8 = [&]() {
-        if (!X.data8) return;
+        // integer-typed inputs only: float inputs keep fp32 centroids, so
+        // their buckets do not depend on whether the int8 copy exists
+        if (!X.data8 || X.from_float) return;
         int8_t* c8 = c.ws<int8_t>(W_C8, static_cast<size_t>(C) * X.Dp8);
         float* cn8 = c.ws<float>(W_CNORMS8, static_cast<size_t>(C));
         launch_quantize_i8(d_cm, C, X.D, X.Dp8, X.shift, c8, c.s);
@@ -1167,7 +1197,7 @@ void gt_build_params_default(gt_build_params* p)
     p->balance = 0.8f;
     p->seed = 42;
     p->reverse_edges = 0;
-    p->reserved_ = 0;
+    p->int_exact = 1;
 }
 
 void gt_search_params_default(gt_search_params* p)
@@ -1326,7 +1356,7 @@ int gt_knn_exact(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtype, in
         GT_REQUIRE(metric == GT_METRIC_L2 || metric == GT_METRIC_IP, "unknown metric");
         GT_REQUIRE(queries || nq == N, "nq must equal N when queries is NULL");
         Ctx c(ctx);
-        DevMatrix Xm = prepare(c, W_X, W_XRAW, W_NORMS, X, N, D, dtype, true);
+        DevMatrix Xm = prepare(c, W_X, W_XRAW, W_NORMS, X, N, D, dtype, true, true);
         int32_t* d_q = nullptr;
         if (queries) {
             std::vector<int64_t> hq(static_cast<size_t>(nq));
@@ -1426,7 +1456,7 @@ int gt_knn_bucketed(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtype,
                 seen[static_cast<size_t>(m)] = 1;
             }
         }
-        DevMatrix Xm = prepare(c, W_X, W_XRAW, W_NORMS, X, N, D, dtype, true);
+        DevMatrix Xm = prepare(c, W_X, W_XRAW, W_NORMS, X, N, D, dtype, true, true);
         const size_t nm = static_cast<size_t>(N) * M;
         int32_t* cur_i = c.ws<int32_t>(W_IDS, nm);
         float* cur_d = c.ws<float>(W_D, nm);
@@ -1908,7 +1938,7 @@ int gt_build_graph_ex(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtyp
         gt_build_stats st{};
         Ctx c(ctx);
         Timer tp;
-        DevMatrix Xm = prepare(c, W_X, W_XRAW, W_NORMS, X, N, D, dtype, true);
+        DevMatrix Xm = prepare(c, W_X, W_XRAW, W_NORMS, X, N, D, dtype, true, p.int_exact != 0);
         c.sync();
         st.t_prepare = tp.sec();
         int64_t C = p.n_buckets > 0 ? p.n_buckets : std::max<int64_t>(1, N / 4000);
@@ -2021,6 +2051,7 @@ int gt_build_graph_ex(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtyp
         }
         st.knn_flops = 2.0 * D * st.knn_pairs;
         st.knn_launches = ctx->knn_launches;
+        st.knn_int8 = use_i8(Xm, Xm, p.metric) ? 1 : 0;
         // sanitize + prune + reverse merge
         uint32_t* fin = nullptr;
         if (graph) {

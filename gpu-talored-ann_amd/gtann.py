@@ -41,7 +41,7 @@ class BuildParams(C.Structure):
         ("metric", C.c_int32), ("n_buckets", C.c_int32), ("nprobe", C.c_int32), ("M", C.c_int32),
         ("K", C.c_int32), ("rounds", C.c_int32), ("refine_passes", C.c_int32), ("refine_sample", C.c_int32),
         ("kmeans_iters", C.c_int32), ("balance", C.c_float), ("seed", C.c_uint64),
-        ("reverse_edges", C.c_int32), ("reserved_", C.c_int32),
+        ("reverse_edges", C.c_int32), ("int_exact", C.c_int32),
     ]
 
 
@@ -50,7 +50,7 @@ class BuildStats(C.Structure):
         ("t_total", C.c_double), ("t_prepare", C.c_double), ("t_bucketing", C.c_double), ("t_knn", C.c_double),
         ("t_merge", C.c_double), ("t_refine", C.c_double), ("t_prune", C.c_double), ("t_revmerge", C.c_double),
         ("t_download", C.c_double), ("knn_flops", C.c_double), ("knn_pairs", C.c_double),
-        ("max_pool", C.c_int64), ("max_bucket", C.c_int64), ("knn_launches", C.c_int64),
+        ("max_pool", C.c_int64), ("max_bucket", C.c_int64), ("knn_launches", C.c_int64), ("knn_int8", C.c_int64),
     ]
 
     def as_dict(self):
@@ -372,7 +372,7 @@ class Context:
 
     def build_graph(self, X, *, n_buckets=0, nprobe=1, M=64, K=32, rounds=2, refine_passes=0, refine_sample=16,
                     kmeans_iters=3, balance=0.8, seed=42, metric="l2", return_knn=True, reverse_edges=False,
-                    prune=True, centroid_knn_k=0, round1_bucket=False):
+                    prune=True, centroid_knn_k=0, round1_bucket=False, int_exact=True):
         if not _is_torch(X):
             X = np.ascontiguousarray(X)
         N, D = X.shape
@@ -381,6 +381,7 @@ class Context:
         p.metric, p.n_buckets, p.nprobe, p.M, p.K = METRICS[metric], n_buckets, nprobe, M, K
         p.rounds, p.refine_passes, p.refine_sample, p.kmeans_iters = rounds, refine_passes, refine_sample, kmeans_iters
         p.balance, p.seed, p.reverse_edges = balance, seed, int(bool(reverse_edges))
+        p.int_exact = int(bool(int_exact))
         graph = _empty_like_input(X, (N, K), np.uint32) if prune else None
         ids = _empty_like_input(X, (N, M), np.int32) if return_knn else None
         d = _empty_like_input(X, (N, M), np.float32) if return_knn else None

@@ -140,7 +140,10 @@ typedef struct gt_build_params {
     uint64_t seed;          /* --seed; round r uses seed + r */
     int32_t reverse_edges;  /* 1: each round's full table gets gt_reverse_insert before the
                                cross-round merge (bd/build_bucket.py:628); 0: rounds seeded */
-    int32_t reserved_;
+    int32_t int_exact;      /* 1 (default): float rows whose values are all integers in [-128, 127]
+                               or [0, 255] (D <= 256) run the point kNN on the int8 matrix cores;
+                               every distance is an exact integer in both kernels, so the table and
+                               graph are the fp32 kernel's, bit for bit.  0: always fp32 */
 } gt_build_params;
 
 typedef struct gt_build_stats {
@@ -158,6 +161,8 @@ typedef struct gt_build_stats {
     int64_t max_pool;
     int64_t max_bucket;
     int64_t knn_launches;   /* fused kNN launches of the rounds (knn_flops / t_knn cover these) */
+    int64_t knn_int8;       /* 1: the rounds ran on the int8 matrix cores (integer-typed rows, or
+                               integer-valued float rows with int_exact), 0: fp32 */
 } gt_build_stats;
 
 void gt_build_params_default(gt_build_params* p);
