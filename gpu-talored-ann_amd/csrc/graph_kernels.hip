@@ -994,6 +994,61 @@ void launch_pad_i8(const void* src, int dtype, int8_t* dst, int64_t N, int D, in
     GT_HIP(hipGetLastError());
 }
 
+// Counting sort of each segment [off[g], off[g+1]) of members by key
+// (keys < 1024), one workgroup per segment; segments shorter than min_n are
+// copied unchanged.  The order inside a key is not fixed.
+__global__ void __launch_bounds__(256) segment_sort_kernel(const int32_t* __restrict__ members,
+                                                           const int32_t* __restrict__ key,
+                                                           const int64_t* __restrict__ off, int min_n,
+                                                           int32_t* __restrict__ out)
+{
+    constexpr int kKeys = 1024;
+    __shared__ uint32_t cnt[kKeys];
+    __shared__ uint32_t wsum[4];
+    const int64_t lo = off[blockIdx.x], hi = off[blockIdx.x + 1];
+    const int t = threadIdx.x;
+    if (hi - lo < min_n) {
+        for (int64_t e = lo + t; e < hi; e += 256) out[e] = members[e];
+        return;
+    }
+    for (int k = t; k < kKeys; k += 256) cnt[k] = 0u;
+    __syncthreads();
+    for (int64_t e = lo + t; e < hi; e += 256) atomicAdd(&cnt[static_cast<uint32_t>(key[e]) & (kKeys - 1)], 1u);
+    __syncthreads();
+    // exclusive scan: 4 counters per thread, then the 256 partial sums
+    uint32_t v[4], loc = 0;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) { v[u] = cnt[4 * t + u]; loc += v[u]; }
+    const int lane = t & 63, w = t >> 6;
+    uint32_t inc = loc;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t x = __shfl_up(inc, o);
+        if (lane >= o) inc += x;
+    }
+    if (lane == 63) wsum[w] = inc;
+    __syncthreads();
+    uint32_t base = 0;
+    for (int q = 0; q < w; ++q) base += wsum[q];
+    uint32_t run = base + inc - loc;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) { cnt[4 * t + u] = run; run += v[u]; }
+    __syncthreads();
+    for (int64_t e = lo + t; e < hi; e += 256) {
+        const uint32_t slot = atomicAdd(&cnt[static_cast<uint32_t>(key[e]) & (kKeys - 1)], 1u);
+        out[lo + slot] = members[e];
+    }
+}
+
+void launch_segment_sort(const int32_t* members, const int32_t* key, const int64_t* off, int64_t nseg, int min_n,
+                         int32_t* out, hipStream_t s)
+{
+    if (nseg <= 0) return;
+    hipLaunchKernelGGL(segment_sort_kernel, dim3(static_cast<unsigned>(nseg)), dim3(256), 0, s, members, key, off,
+                       min_n, out);
+    GT_HIP(hipGetLastError());
+}
+
 void launch_int_range(const float* X, int64_t n, int* out, hipStream_t s)
 {
     if (n <= 0) return;

@@ -36,6 +36,8 @@ void launch_pad_i8(const void* src, int dtype, int8_t* dst, int64_t N, int D, in
 void launch_row_norms_i8(const int8_t* X, int64_t N, int Dp, float* norms, hipStream_t s);
 void launch_quantize_i8(const float* src, int64_t N, int D, int Dp, int shift, int8_t* dst, hipStream_t s);
 void launch_int_range(const float* X, int64_t n, int* out, hipStream_t s);
+void launch_segment_sort(const int32_t* members, const int32_t* key, const int64_t* off, int64_t nseg, int min_n,
+                         int32_t* out, hipStream_t s);
 void launch_copy_ranges(const void* tasks, int64_t ntasks, const int32_t* members, int32_t* pool, hipStream_t s);
 void launch_negate(float* d, int64_t n, hipStream_t s);
 void launch_graph_search(const SearchArgs& a, int64_t grid, hipStream_t s);
@@ -167,7 +169,7 @@ struct gt_ctx {
     hipStream_t stream = nullptr;
     std::string err;
     // named workspaces, grow-only (one slot per role, see gtann::Ws)
-    gtann::DevBuf ws[40];
+    gtann::DevBuf ws[48];
     gtann::HostBuf pinned[2];   // top-2 assignment downloads of two consecutive rounds
     // host scratch of the bucketing, reused across calls (no page faults on
     // fresh N-sized allocations every round)
@@ -181,9 +183,10 @@ namespace gtann {
 enum Ws {
     W_X, W_XRAW, W_NORMS, W_C, W_CRAW, W_CNORMS, W_IDS, W_D, W_IDS2, W_D2, W_IDS3, W_D3, W_ITEMS, W_QROWS, W_PROWS,
     W_MEMBERS, W_TASKS, W_POOL, W_PART_I, W_PART_D, W_G1, W_G2, W_G3, W_DEG, W_OFF, W_CUR, W_KEYS, W_SUMS, W_FLAG,
-    W_TMP, W_OUT, W_IN, W_PROBE_I, W_PROBE_D, W_WORST, W_X8, W_NORMS8, W_C8, W_CNORMS8, W_COUNT_
+    W_TMP, W_OUT, W_IN, W_PROBE_I, W_PROBE_D, W_WORST, W_X8, W_NORMS8, W_C8, W_CNORMS8,
+    W_SUBROWS, W_SUBID, W_SUBD, W_SUBOFF, W_MEMBERS2, W_COUNT_
 };
-static_assert(W_COUNT_ <= 40, "workspace slots");
+static_assert(W_COUNT_ <= 48, "workspace slots");
 
 struct Ctx {
     gt_ctx* c;
@@ -647,6 +650,74 @@ static void csr_from_assignment(const std::vector<int32_t>& bucket_of, int64_t C
     counting_sort(nullptr, N, bucket_of.data(), C, b.members.data(), b.offsets);
 }
 
+// Orders each bucket's members by their nearest sub-centroid (every
+// kSubSize-th member of the bucket, by the fused kernel with lists of one):
+// an unseeded pass that starts at a query's own tile then meets the query's
+// nearest rows first, so its threshold tightens within a few tiles and few
+// candidates reach the list merges.  The kNN result does not depend on the
+// order of the pool.
+constexpr int kSubSize = 128;     // members per sub-centroid
+constexpr int kSubMax = 1024;     // sub-centroids per bucket (LDS counters of the sort)
+// GTANN_SUB_ORDER=0 keeps the two-choice order (comparisons; same results)
+static bool sub_order_enabled()
+{
+    const char* e = std::getenv("GTANN_SUB_ORDER");
+    return !(e && e[0] == '0');
+}
+
+static void sub_order_members(Ctx& c, const DevMatrix& X, const Buckets& b, int metric, int32_t* d_members)
+{
+    const int64_t C = static_cast<int64_t>(b.offsets.size()) - 1;
+    const int64_t N = X.N;
+    std::vector<int32_t> subrows;
+    std::vector<std::vector<WorkItem>> groups(static_cast<size_t>(C));
+    bool any = false;
+    for (int64_t bb = 0; bb < C; ++bb) {
+        const int64_t lo = b.offsets[static_cast<size_t>(bb)], n = b.offsets[static_cast<size_t>(bb + 1)] - lo;
+        if (n < 2 * kSubSize) continue;   // left as it is (the sort copies it)
+        const int64_t s = std::min<int64_t>(kSubMax, ceil_div(n, kSubSize));
+        const int64_t p0 = static_cast<int64_t>(subrows.size());
+        for (int64_t i = 0; i < s; ++i) subrows.push_back(b.members[static_cast<size_t>(lo + i * n / s)]);
+        for (int64_t t = 0; t < n; t += kQueriesPerBlock) {
+            WorkItem it;
+            it.q_begin = lo + t;
+            it.q_count = static_cast<int32_t>(std::min<int64_t>(kQueriesPerBlock, n - t));
+            it.p_begin = p0;
+            it.p_count = static_cast<int32_t>(s);
+            it.p_rot = 0;
+            it.out_base = lo + t;   // one key per member position
+            groups[static_cast<size_t>(bb)].push_back(it);
+        }
+        any = true;
+    }
+    if (!any) return;
+    int32_t* d_sub = c.ws<int32_t>(W_SUBROWS, subrows.size());
+    c.h2d(d_sub, subrows.data(), subrows.size() * sizeof(int32_t));
+    const std::vector<WorkItem> items = layout_xcd(groups);
+    WorkItem* d_items = c.ws<WorkItem>(W_ITEMS, items.size());
+    c.h2d(d_items, items.data(), items.size() * sizeof(WorkItem));
+    int32_t* d_key = c.ws<int32_t>(W_SUBID, static_cast<size_t>(N));
+    float* d_kd = c.ws<float>(W_SUBD, static_cast<size_t>(N));
+    KnnArgs a{};
+    set_operands(a, X, X, metric);
+    a.q_rows = d_members;
+    a.p_rows = d_sub;
+    a.items = d_items;
+    a.n_items = static_cast<int32_t>(items.size());
+    a.M = 1;
+    a.metric = metric;
+    a.exclude_self = 0;
+    a.out_pos = 1;   // sub-centroid index within the bucket
+    a.out_ids = d_key;
+    a.out_d = d_kd;
+    launch_knn_fused(a, c.s);
+    int64_t* d_off = c.ws<int64_t>(W_SUBOFF, static_cast<size_t>(C + 1));
+    c.h2d(d_off, b.offsets.data(), static_cast<size_t>(C + 1) * sizeof(int64_t));
+    int32_t* d_m2 = c.ws<int32_t>(W_MEMBERS2, static_cast<size_t>(N));
+    launch_segment_sort(d_members, d_key, d_off, C, 2 * kSubSize, d_m2, c.s);
+    c.d2d(d_members, d_m2, static_cast<size_t>(N) * sizeof(int32_t));
+}
+
 // One round of pooled kNN into (out_ids, out_d) rows by global id.
 // seed_d (device, optional) caps kept keys at the running M-th distance.
 // own / probes select the pool segments: the bucket's own members and the
@@ -683,6 +754,7 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
 
     int32_t* d_members = c.ws<int32_t>(W_MEMBERS, static_cast<size_t>(N));
     c.h2d(d_members, b.members.data(), static_cast<size_t>(N) * sizeof(int32_t));
+    if (own && !seed_d && sub_order_enabled()) sub_order_members(c, X, b, metric, d_members);
     CopyTaskH* d_tasks = c.ws<CopyTaskH>(W_TASKS, tasks.size());
     c.h2d(d_tasks, tasks.data(), tasks.size() * sizeof(CopyTaskH));
     int32_t* d_pool = c.ws<int32_t>(W_POOL, static_cast<size_t>(std::max<int64_t>(total, 1)));

@@ -327,3 +327,23 @@ def test_build_graph_wide_probe_table(ctx):
     ex_i, ex_d = O.knn_exact(X, 32)
     np.testing.assert_array_equal(res.knn_ids, ex_i)
     np.testing.assert_array_equal(res.knn_dists, ex_d)
+
+
+def test_sub_centroid_order_does_not_change_the_build(ctx, monkeypatch):
+    """The unseeded own-bucket pass scans members ordered by nearest
+    sub-centroid; the exact top-M does not depend on the order of the pool,
+    so the two-choice order (GTANN_SUB_ORDER=0) gives the same table and graph."""
+    import synth
+    X, _ = synth.generate("C2", n=40000)
+    kw = dict(n_buckets=12, nprobe=2, M=64, K=32, rounds=2)
+    a = ctx.build_graph(X, **kw)
+    monkeypatch.setenv("GTANN_SUB_ORDER", "0")
+    b = ctx.build_graph(X, **kw)
+    np.testing.assert_array_equal(a.knn_ids, b.knn_ids)
+    np.testing.assert_array_equal(a.knn_dists, b.knn_dists)
+    np.testing.assert_array_equal(a.graph, b.graph)
+    c = ctx.build_graph(X.astype(np.float32) + 0.25, **kw)   # float rows: the fp32 kernel
+    monkeypatch.setenv("GTANN_SUB_ORDER", "1")
+    d = ctx.build_graph(X.astype(np.float32) + 0.25, **kw)
+    np.testing.assert_array_equal(c.knn_ids, d.knn_ids)
+    np.testing.assert_array_equal(c.graph, d.graph)
