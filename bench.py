@@ -212,7 +212,8 @@ def main():
     flops_launch = s["knn_flops"] / launches
     achieved = flops_launch / knn_launch_s
     traffic = None
-    tfile = os.path.join(ROOT, "profiles", f"knn_fused_{args.config}_traffic.json")
+    kbase = "knn_i8" if bool(round(s["knn_int8"])) else ("knn_fused" if D <= 256 else "knn_wide")
+    tfile = os.path.join(ROOT, "profiles", f"{kbase}_{args.config}_traffic.json")
     default_knobs = (args.rounds, args.kmeans_iters, args.nprobe) == (2, 3, 1)
     if default_knobs and os.path.exists(tfile):
         with open(tfile) as f:
