@@ -171,6 +171,7 @@ struct gt_ctx {
     // named workspaces, grow-only (one slot per role, see gtann::Ws)
     gtann::DevBuf ws[48];
     gtann::HostBuf pinned[2];   // top-2 assignment downloads of two consecutive rounds
+    gtann::HostBuf pin_lloyd;   // Lloyd steps: nearest centroids down, CSR up
     // host scratch of the bucketing, reused across calls (no page faults on
     // fresh N-sized allocations every round)
     std::vector<int32_t> h_bucket_of, h_key2, h_by_key, h_members[2];
@@ -484,6 +485,25 @@ static std::vector<int32_t> sample_ids(int64_t N, int64_t C, uint64_t seed)
         for (uint64_t w = bits[wi]; w; w &= w - 1)
             ids.push_back(static_cast<int32_t>(wi * 64 + static_cast<size_t>(__builtin_ctzll(w))));
     return ids;
+}
+
+// The random draws of one round's bucketing (host work that depends only on
+// N, C and the seed, so a build draws every round's at its start, on a
+// worker thread, while the dataset is prepared).
+struct RoundSamples {
+    std::vector<int32_t> cid;     // C centroid rows
+    std::vector<int32_t> srows;   // Lloyd training subset (empty without Lloyd)
+};
+
+static int64_t lloyd_subset(int64_t N, int64_t C) { return std::min<int64_t>(N, std::max<int64_t>(65536, 256 * C)); }
+
+static RoundSamples draw_round(int64_t N, int64_t C, int kmeans_iters, uint64_t seed)
+{
+    RoundSamples r;
+    C = std::max<int64_t>(1, std::min<int64_t>(C, N));
+    r.cid = sample_ids(N, C, seed);
+    if (kmeans_iters > 0) r.srows = sample_ids(N, lloyd_subset(N, C), seed * 0x2545F4914F6CDD1Dull + 7);
+    return r;
 }
 
 struct Buckets {
@@ -829,7 +849,7 @@ struct BucketPlan {
 };
 
 static void bucket_device(Ctx& c, const DevMatrix& X, int64_t C, int nprobe, int metric, int kmeans_iters,
-                          uint64_t seed, HostBuf& pin, BucketPlan& bp, std::vector<int32_t>* cknn = nullptr,
+                          RoundSamples&& draws, HostBuf& pin, BucketPlan& bp, std::vector<int32_t>* cknn = nullptr,
                           int cknn_k = 0)
 {
     const int64_t N = X.N;
@@ -837,7 +857,7 @@ static void bucket_device(Ctx& c, const DevMatrix& X, int64_t C, int nprobe, int
     C = std::max<int64_t>(1, std::min<int64_t>(C, N));
     bp.N = N;
     bp.C = C;
-    bp.cid = sample_ids(N, C, seed);
+    bp.cid = std::move(draws.cid);
     std::vector<int32_t>& cid = bp.cid;
     int32_t* d_cid = c.ws<int32_t>(W_PROWS, static_cast<size_t>(C));
     c.h2d(d_cid, cid.data(), static_cast<size_t>(C) * sizeof(int32_t));
@@ -889,13 +909,22 @@ static void bucket_device(Ctx& c, const DevMatrix& X, int64_t C, int nprobe, int
     // sampled row, then each centroid moves to the mean of its sampled members.
     const bool data_points = kmeans_iters <= 0;
     if (!data_points) {
-        const int64_t S = std::min<int64_t>(N, std::max<int64_t>(65536, 256 * C));
-        std::vector<int32_t> srows = sample_ids(N, S, seed * 0x2545F4914F6CDD1Dull + 7);
+        const int64_t S = lloyd_subset(N, C);
+        const std::vector<int32_t> srows = std::move(draws.srows);
+        GT_REQUIRE(static_cast<int64_t>(srows.size()) == S, "Lloyd subset draw");
         int32_t* d_srows = c.ws<int32_t>(W_QROWS, static_cast<size_t>(S));
         c.h2d(d_srows, srows.data(), static_cast<size_t>(S) * sizeof(int32_t));
         int32_t* d_n1 = c.ws<int32_t>(W_IDS3, static_cast<size_t>(S));
         float* d_n1d = c.ws<float>(W_D3, static_cast<size_t>(S));
-        std::vector<int32_t> nearest(static_cast<size_t>(S));
+        // pinned staging: nearest (S) | members (S) | offsets (C + 1, int64)
+        const size_t s4 = (static_cast<size_t>(S) * 4 + 7) / 8 * 8;
+        char* pin = c.c->pin_lloyd.as<char>(2 * s4 + static_cast<size_t>(C + 1) * 8);
+        int32_t* nearest = reinterpret_cast<int32_t*>(pin);
+        int32_t* hmem = reinterpret_cast<int32_t*>(pin + s4);
+        int64_t* hoff = reinterpret_cast<int64_t*>(pin + 2 * s4);
+        int32_t* d_mem = c.ws<int32_t>(W_MEMBERS, static_cast<size_t>(S));
+        int64_t* d_off = c.ws<int64_t>(W_OFF, static_cast<size_t>(C + 1));
+        std::vector<int64_t> off;
         for (int it = 0; it < kmeans_iters; ++it) {
             KnnJob j;
             j.Q = &X;
@@ -910,15 +939,16 @@ static void bucket_device(Ctx& c, const DevMatrix& X, int64_t C, int nprobe, int
             j.out_ids = d_n1;
             j.out_d = d_n1d;
             run_knn_flat(c, j, 1);
-            c.d2h(nearest.data(), d_n1, static_cast<size_t>(S) * sizeof(int32_t));
+            c.d2h(nearest, d_n1, static_cast<size_t>(S) * sizeof(int32_t));
             c.sync();
-            Buckets tmp;
-            csr_from_assignment(nearest, C, tmp);
-            for (auto& m : tmp.members) m = srows[static_cast<size_t>(m)];   // sample index -> row id
-            int32_t* d_mem = c.ws<int32_t>(W_MEMBERS, static_cast<size_t>(S));
-            c.h2d(d_mem, tmp.members.data(), static_cast<size_t>(S) * sizeof(int32_t));
-            int64_t* d_off = c.ws<int64_t>(W_OFF, static_cast<size_t>(C + 1));
-            c.h2d(d_off, tmp.offsets.data(), static_cast<size_t>(C + 1) * sizeof(int64_t));
+            // CSR in sample order (stable counting sort), members as row ids
+            counting_sort(nullptr, S, nearest, C, hmem, off);
+            parallel_slices(S, host_threads(), [&](int, int64_t lo, int64_t hi) {
+                for (int64_t e = lo; e < hi; ++e) hmem[e] = srows[static_cast<size_t>(hmem[e])];
+            });
+            std::copy(off.begin(), off.end(), hoff);
+            c.h2d(d_mem, hmem, static_cast<size_t>(S) * sizeof(int32_t));
+            c.h2d(d_off, hoff, static_cast<size_t>(C + 1) * sizeof(int64_t));
             launch_centroid_sums(X.data, X.Dp, d_mem, d_off, C, d_cm, c.s);
             launch_row_norms(d_cm, C, X.Dp, d_cn, c.s);
             refresh_c8();
@@ -1242,6 +1272,7 @@ void gt_destroy(gt_ctx* ctx)
         b.cap = 0;
     }
     for (auto& pb : ctx->pinned) pb.release();
+    ctx->pin_lloyd.release();
     if (ctx->ev0) (void)hipEventDestroy(ctx->ev0);
     if (ctx->ev1) (void)hipEventDestroy(ctx->ev1);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
@@ -2009,12 +2040,19 @@ int gt_build_graph_ex(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtyp
         Timer total;
         gt_build_stats st{};
         Ctx c(ctx);
+        int64_t C = p.n_buckets > 0 ? p.n_buckets : std::max<int64_t>(1, N / 4000);
+        C = std::min<int64_t>(C, N);
+        // every round's random draws, on a worker thread while the dataset is prepared
+        std::future<std::vector<RoundSamples>> draws_job = std::async(std::launch::async, [N, C, p] {
+            std::vector<RoundSamples> d;
+            for (int r = 0; r < p.rounds; ++r) d.push_back(draw_round(N, C, p.kmeans_iters, p.seed + static_cast<uint64_t>(r)));
+            return d;
+        });
         Timer tp;
         DevMatrix Xm = prepare(c, W_X, W_XRAW, W_NORMS, X, N, D, dtype, true, p.int_exact != 0);
         c.sync();
         st.t_prepare = tp.sec();
-        int64_t C = p.n_buckets > 0 ? p.n_buckets : std::max<int64_t>(1, N / 4000);
-        C = std::min<int64_t>(C, N);
+        std::vector<RoundSamples> draws = draws_job.get();
         int nprobe = p.nprobe;
         if (nprobe < 0) nprobe = static_cast<int>(std::ceil(20000.0 / (static_cast<double>(N) / C)));
         nprobe = static_cast<int>(std::min<int64_t>(nprobe, C - 1));
@@ -2040,7 +2078,7 @@ int gt_build_graph_ex(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtyp
         const bool want_cknn = extras && extras->centroid_knn && extras->centroid_knn_k > 0;
         auto device_part = [&](int r) {
             Timer tb;
-            bucket_device(c, Xm, C, nprobe, p.metric, p.kmeans_iters, p.seed + static_cast<uint64_t>(r),
+            bucket_device(c, Xm, C, nprobe, p.metric, p.kmeans_iters, std::move(draws[static_cast<size_t>(r)]),
                           ctx->pinned[r & 1], plans[r & 1], r == 0 && want_cknn ? &cknn : nullptr,
                           r == 0 && want_cknn ? extras->centroid_knn_k : 0);
             st.t_bucketing += tb.sec();
