@@ -59,36 +59,6 @@ __global__ void pad_i8_kernel(const T* __restrict__ src, int8_t* __restrict__ ds
 
 // int8 copy of float rows (centroids of an integer dataset): the value
 // minus the dataset's shift, rounded and clamped; padding stays 0.
-// Whether every value of a float matrix is an integer, and the range of the
-// values: out[0] |= 1 on a non-integer or non-finite value; out[1] / out[2]
-// = min / max as ints (atomics; the host starts them at INT_MAX / INT_MIN).
-__global__ void __launch_bounds__(256) int_range_kernel(const float* __restrict__ X, int64_t n,
-                                                        int* __restrict__ out)
-{
-    float lo = INFINITY, hi = -INFINITY;
-    bool bad = false;
-    for (int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < n;
-         e += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-        const float v = X[e];
-        bad |= !(v == rintf(v)) || !(fabsf(v) < 1e9f);   // NaN and +-inf fail too
-        lo = fminf(lo, v);
-        hi = fmaxf(hi, v);
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        lo = fminf(lo, __shfl_xor(lo, o));
-        hi = fmaxf(hi, __shfl_xor(hi, o));
-    }
-    const bool any_bad = __ballot(bad) != 0;
-    if ((threadIdx.x & 63) == 0) {
-        if (any_bad) atomicOr(&out[0], 1);
-        if (lo <= hi && !any_bad) {
-            atomicMin(&out[1], static_cast<int>(lo));
-            atomicMax(&out[2], static_cast<int>(hi));
-        }
-    }
-}
-
 __global__ void quantize_i8_kernel(const float* __restrict__ src, int64_t N, int D, int Dp, int shift,
                                    int8_t* __restrict__ dst)
 {
@@ -1049,13 +1019,126 @@ void launch_segment_sort(const int32_t* members, const int32_t* key, const int64
     GT_HIP(hipGetLastError());
 }
 
-void launch_int_range(const float* X, int64_t n, int* out, hipStream_t s)
+// Row norms (the order of row_norms_kernel, so the same bits) plus, per
+// block of 4 rows, whether every value is an integer and their range:
+// part[3b] = 1 on a non-integer / non-finite value, part[3b+1] / part[3b+2]
+// = min / max as ints; int_range_final_kernel folds the blocks into out[3].
+__global__ void __launch_bounds__(256) row_norms_range_kernel(const float* __restrict__ X, int64_t N, int Dp,
+                                                              float* __restrict__ norms, int* __restrict__ part)
 {
-    if (n <= 0) return;
-    const unsigned grid = static_cast<unsigned>(std::min<int64_t>(4096, (n + 2047) / 2048));
-    hipLaunchKernelGGL(int_range_kernel, dim3(grid), dim3(256), 0, s, X, n, out);
+    __shared__ int red[4][3];
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + w;
+    float s = 0.f, lo = INFINITY, hi = -INFINITY;
+    bool bad = false;
+    if (row < N) {
+        for (int c = lane; c < Dp; c += 64) {
+            const float v = X[row * Dp + c];
+            s = fmaf(v, v, s);
+            bad |= !(v == rintf(v)) || !(fabsf(v) < 1e9f);
+            lo = fminf(lo, v);
+            hi = fmaxf(hi, v);
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        s += __shfl_xor(s, o);
+        lo = fminf(lo, __shfl_xor(lo, o));
+        hi = fmaxf(hi, __shfl_xor(hi, o));
+    }
+    const bool any_bad = __ballot(bad) != 0;
+    if (lane == 0) {
+        if (row < N) norms[row] = s;
+        red[w][0] = any_bad ? 1 : 0;
+        red[w][1] = row < N && !any_bad ? static_cast<int>(lo) : INT_MAX;
+        red[w][2] = row < N && !any_bad ? static_cast<int>(hi) : INT_MIN;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int f = 0, mn = INT_MAX, mx = INT_MIN;
+        for (int q = 0; q < 4; ++q) {
+            f |= red[q][0];
+            mn = min(mn, red[q][1]);
+            mx = max(mx, red[q][2]);
+        }
+        part[3 * blockIdx.x] = f;
+        part[3 * blockIdx.x + 1] = mn;
+        part[3 * blockIdx.x + 2] = mx;
+    }
+}
+
+__global__ void __launch_bounds__(1024) int_range_final_kernel(const int* __restrict__ part, int64_t nb,
+                                                               int* __restrict__ out)
+{
+    __shared__ int red[16][3];
+    int f = 0, mn = INT_MAX, mx = INT_MIN;
+    for (int64_t b = threadIdx.x; b < nb; b += 1024) {
+        f |= part[3 * b];
+        mn = min(mn, part[3 * b + 1]);
+        mx = max(mx, part[3 * b + 2]);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        f |= __shfl_xor(f, o);
+        mn = min(mn, __shfl_xor(mn, o));
+        mx = max(mx, __shfl_xor(mx, o));
+    }
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) { red[w][0] = f; red[w][1] = mn; red[w][2] = mx; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int q = 1; q < 16; ++q) { f |= red[q][0]; mn = min(mn, red[q][1]); mx = max(mx, red[q][2]); }
+        out[0] = f;
+        out[1] = mn;
+        out[2] = mx;
+    }
+}
+
+// Exact int8 rows (value - shift, columns >= D zero) and their |x|^2, one
+// wave per row, 4 columns per lane.
+__global__ void __launch_bounds__(256) quantize_norms_i8_kernel(const float* __restrict__ src, int64_t N, int D,
+                                                                int Dp, int shift, int8_t* __restrict__ dst,
+                                                                float* __restrict__ norms)
+{
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= N) return;
+    int s = 0;
+    for (int c0 = 4 * lane; c0 < Dp; c0 += 256) {
+        uint32_t packed = 0;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int c = c0 + u;
+            const float v = c < D ? rintf(src[row * Dp + c] - static_cast<float>(shift)) : 0.f;
+            const int q = static_cast<int>(fminf(fmaxf(v, -128.f), 127.f));
+            s += q * q;
+            packed |= (static_cast<uint32_t>(q) & 0xffu) << (8 * u);
+        }
+        *reinterpret_cast<uint32_t*>(dst + row * Dp + c0) = packed;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+    if (lane == 0) norms[row] = static_cast<float>(s);
+}
+
+void launch_row_norms_range(const float* X, int64_t N, int Dp, float* norms, int* part, int* out, hipStream_t s)
+{
+    if (N <= 0) return;
+    const int64_t nb = (N + 3) / 4;
+    hipLaunchKernelGGL(row_norms_range_kernel, dim3(static_cast<unsigned>(nb)), dim3(256), 0, s, X, N, Dp, norms, part);
+    hipLaunchKernelGGL(int_range_final_kernel, dim3(1), dim3(1024), 0, s, part, nb, out);
     GT_HIP(hipGetLastError());
 }
+
+void launch_quantize_norms_i8(const float* src, int64_t N, int D, int Dp, int shift, int8_t* dst, float* norms,
+                              hipStream_t s)
+{
+    if (N <= 0) return;
+    hipLaunchKernelGGL(quantize_norms_i8_kernel, dim3(grid_for(N, 4)), dim3(256), 0, s, src, N, D, Dp, shift, dst,
+                       norms);
+    GT_HIP(hipGetLastError());
+}
+
 
 void launch_quantize_i8(const float* src, int64_t N, int D, int Dp, int shift, int8_t* dst, hipStream_t s)
 {

@@ -35,7 +35,9 @@ void launch_row_norms(const float* X, int64_t N, int Dp, float* norms, hipStream
 void launch_pad_i8(const void* src, int dtype, int8_t* dst, int64_t N, int D, int Dp, hipStream_t s);
 void launch_row_norms_i8(const int8_t* X, int64_t N, int Dp, float* norms, hipStream_t s);
 void launch_quantize_i8(const float* src, int64_t N, int D, int Dp, int shift, int8_t* dst, hipStream_t s);
-void launch_int_range(const float* X, int64_t n, int* out, hipStream_t s);
+void launch_row_norms_range(const float* X, int64_t N, int Dp, float* norms, int* part, int* out, hipStream_t s);
+void launch_quantize_norms_i8(const float* src, int64_t N, int D, int Dp, int shift, int8_t* dst, float* norms,
+                              hipStream_t s);
 void launch_segment_sort(const int32_t* members, const int32_t* key, const int64_t* off, int64_t nseg, int min_n,
                          int32_t* out, hipStream_t s);
 void launch_copy_ranges(const void* tasks, int64_t ntasks, const int32_t* members, int32_t* pool, hipStream_t s);
@@ -331,7 +333,17 @@ static DevMatrix prepare(Ctx& c, int slot_x, int slot_raw, int slot_norms, const
         m.data = xp;
     }
     float* nrm = c.ws<float>(slot_norms, static_cast<size_t>(N));
-    launch_row_norms(m.data, N, Dp, nrm, c.s);
+    // float rows that may take the exact int8 path: norms and the integer
+    // check in one pass
+    const bool check_int = with_i8 && int_exact && dtype == GT_DTYPE_F32 && Dp <= 256;
+    int* range = nullptr;
+    if (check_int) {
+        int* part = c.ws<int>(W_SUBD, static_cast<size_t>(3 * ((N + 3) / 4)));
+        range = c.ws<int>(W_FLAG, 4);
+        launch_row_norms_range(m.data, N, Dp, nrm, part, range, c.s);
+    } else {
+        launch_row_norms(m.data, N, Dp, nrm, c.s);
+    }
     m.norms = nrm;
     if (with_i8 && (dtype == GT_DTYPE_U8 || dtype == GT_DTYPE_I8) && Dp <= 256) {
         m.Dp8 = Dp;
@@ -342,13 +354,9 @@ static DevMatrix prepare(Ctx& c, int slot_x, int slot_raw, int slot_norms, const
         launch_row_norms_i8(x8, N, Dp, n8, c.s);
         m.data8 = x8;
         m.norms8 = n8;
-    } else if (with_i8 && int_exact && dtype == GT_DTYPE_F32 && Dp <= 256) {
-        int* fl = c.ws<int>(W_FLAG, 4);
-        const int init[3] = {0, INT_MAX, INT_MIN};
-        c.h2d(fl, init, sizeof(init));
-        launch_int_range(m.data, N * Dp, fl, c.s);   // padding columns are zeros
+    } else if (check_int) {
         int h[3];
-        c.d2h(h, fl, sizeof(h));
+        c.d2h(h, range, sizeof(h));   // padding columns are zeros: integers
         c.sync();
         const int shift = h[0] ? -1 : (h[1] >= -128 && h[2] <= 127) ? 0 : (h[1] >= 0 && h[2] <= 255) ? 128 : -1;
         if (shift >= 0) {
@@ -356,9 +364,8 @@ static DevMatrix prepare(Ctx& c, int slot_x, int slot_raw, int slot_norms, const
             m.shift = shift;
             m.from_float = true;
             int8_t* x8 = c.ws<int8_t>(W_X8, static_cast<size_t>(N) * Dp);
-            launch_quantize_i8(m.data, N, D, Dp, shift, x8, c.s);   // exact: integers minus the shift; padding 0
             float* n8 = c.ws<float>(W_NORMS8, static_cast<size_t>(N));
-            launch_row_norms_i8(x8, N, Dp, n8, c.s);
+            launch_quantize_norms_i8(m.data, N, D, Dp, shift, x8, n8, c.s);   // exact; padding 0
             m.data8 = x8;
             m.norms8 = n8;
         }
