@@ -970,6 +970,8 @@ void launch_pad_i8(const void* src, int dtype, int8_t* dst, int64_t N, int D, in
 __global__ void __launch_bounds__(256) segment_sort_kernel(const int32_t* __restrict__ members,
                                                            const int32_t* __restrict__ key,
                                                            const int64_t* __restrict__ off, int min_n,
+                                                           const int32_t* __restrict__ remap,
+                                                           const int64_t* __restrict__ remap_base,
                                                            int32_t* __restrict__ out)
 {
     constexpr int kKeys = 1024;
@@ -981,9 +983,15 @@ __global__ void __launch_bounds__(256) segment_sort_kernel(const int32_t* __rest
         for (int64_t e = lo + t; e < hi; e += 256) out[e] = members[e];
         return;
     }
+    // keys through the segment's remap table when there is one
+    const int32_t* rm = remap ? remap + remap_base[blockIdx.x] : nullptr;
+    auto key_of = [&](int64_t e) -> uint32_t {
+        const uint32_t k = static_cast<uint32_t>(key[e]) & (kKeys - 1);
+        return rm ? static_cast<uint32_t>(rm[k]) & (kKeys - 1) : k;
+    };
     for (int k = t; k < kKeys; k += 256) cnt[k] = 0u;
     __syncthreads();
-    for (int64_t e = lo + t; e < hi; e += 256) atomicAdd(&cnt[static_cast<uint32_t>(key[e]) & (kKeys - 1)], 1u);
+    for (int64_t e = lo + t; e < hi; e += 256) atomicAdd(&cnt[key_of(e)], 1u);
     __syncthreads();
     // exclusive scan: 4 counters per thread, then the 256 partial sums
     uint32_t v[4], loc = 0;
@@ -1005,17 +1013,59 @@ __global__ void __launch_bounds__(256) segment_sort_kernel(const int32_t* __rest
     for (int u = 0; u < 4; ++u) { cnt[4 * t + u] = run; run += v[u]; }
     __syncthreads();
     for (int64_t e = lo + t; e < hi; e += 256) {
-        const uint32_t slot = atomicAdd(&cnt[static_cast<uint32_t>(key[e]) & (kKeys - 1)], 1u);
+        const uint32_t slot = atomicAdd(&cnt[key_of(e)], 1u);
         out[lo + slot] = members[e];
     }
 }
 
+// A greedy nearest-neighbour chain through each segment's sub-centroids:
+// start at sub-centroid 0, step to the first unvisited one of the current
+// one's neighbour list (nn: K entries per sub-centroid, positions within the
+// segment, -1 padded), else to the smallest unvisited one.  pos[base + i] =
+// place of sub-centroid i on the chain.  One wave per segment; lane 0 walks.
+__global__ void __launch_bounds__(64) sub_chain_kernel(const int32_t* __restrict__ nn, int K,
+                                                       const int64_t* __restrict__ base,
+                                                       const int32_t* __restrict__ count, int32_t* __restrict__ pos)
+{
+    __shared__ uint32_t seen[32];   // up to 1024 sub-centroids
+    const int g = blockIdx.x, lane = threadIdx.x;
+    const int n = count[g];
+    if (n <= 0) return;
+    const int64_t b0 = base[g];
+    if (lane < 32) seen[lane] = 0u;
+    __syncthreads();
+    if (lane == 0) {
+        int cur = 0;
+        for (int step = 0; step < n; ++step) {
+            seen[cur >> 5] |= 1u << (cur & 31);
+            pos[b0 + cur] = step;
+            int nxt = -1;
+            for (int k = 0; k < K && nxt < 0; ++k) {
+                const int v = nn[(b0 + cur) * K + k];
+                if (v >= 0 && v < n && !((seen[v >> 5] >> (v & 31)) & 1u)) nxt = v;
+            }
+            for (int v = 0; nxt < 0 && v < n; ++v)
+                if (!((seen[v >> 5] >> (v & 31)) & 1u)) nxt = v;
+            if (nxt < 0) break;
+            cur = nxt;
+        }
+    }
+}
+
 void launch_segment_sort(const int32_t* members, const int32_t* key, const int64_t* off, int64_t nseg, int min_n,
-                         int32_t* out, hipStream_t s)
+                         const int32_t* remap, const int64_t* remap_base, int32_t* out, hipStream_t s)
 {
     if (nseg <= 0) return;
     hipLaunchKernelGGL(segment_sort_kernel, dim3(static_cast<unsigned>(nseg)), dim3(256), 0, s, members, key, off,
-                       min_n, out);
+                       min_n, remap, remap_base, out);
+    GT_HIP(hipGetLastError());
+}
+
+void launch_sub_chain(const int32_t* nn, int K, const int64_t* base, const int32_t* count, int64_t nseg, int32_t* pos,
+                      hipStream_t s)
+{
+    if (nseg <= 0) return;
+    hipLaunchKernelGGL(sub_chain_kernel, dim3(static_cast<unsigned>(nseg)), dim3(64), 0, s, nn, K, base, count, pos);
     GT_HIP(hipGetLastError());
 }
 

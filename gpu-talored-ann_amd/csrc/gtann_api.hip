@@ -39,7 +39,9 @@ void launch_row_norms_range(const float* X, int64_t N, int Dp, float* norms, int
 void launch_quantize_norms_i8(const float* src, int64_t N, int D, int Dp, int shift, int8_t* dst, float* norms,
                               hipStream_t s);
 void launch_segment_sort(const int32_t* members, const int32_t* key, const int64_t* off, int64_t nseg, int min_n,
-                         int32_t* out, hipStream_t s);
+                         const int32_t* remap, const int64_t* remap_base, int32_t* out, hipStream_t s);
+void launch_sub_chain(const int32_t* nn, int K, const int64_t* base, const int32_t* count, int64_t nseg, int32_t* pos,
+                      hipStream_t s);
 void launch_copy_ranges(const void* tasks, int64_t ntasks, const int32_t* members, int32_t* pool, hipStream_t s);
 void launch_negate(float* d, int64_t n, hipStream_t s);
 void launch_graph_search(const SearchArgs& a, int64_t grid, hipStream_t s);
@@ -171,7 +173,7 @@ struct gt_ctx {
     hipStream_t stream = nullptr;
     std::string err;
     // named workspaces, grow-only (one slot per role, see gtann::Ws)
-    gtann::DevBuf ws[48];
+    gtann::DevBuf ws[64];
     gtann::HostBuf pinned[2];   // top-2 assignment downloads of two consecutive rounds
     gtann::HostBuf pin_lloyd;   // Lloyd steps: nearest centroids down, CSR up
     // host scratch of the bucketing, reused across calls (no page faults on
@@ -187,9 +189,9 @@ enum Ws {
     W_X, W_XRAW, W_NORMS, W_C, W_CRAW, W_CNORMS, W_IDS, W_D, W_IDS2, W_D2, W_IDS3, W_D3, W_ITEMS, W_QROWS, W_PROWS,
     W_MEMBERS, W_TASKS, W_POOL, W_PART_I, W_PART_D, W_G1, W_G2, W_G3, W_DEG, W_OFF, W_CUR, W_KEYS, W_SUMS, W_FLAG,
     W_TMP, W_OUT, W_IN, W_PROBE_I, W_PROBE_D, W_WORST, W_X8, W_NORMS8, W_C8, W_CNORMS8,
-    W_SUBROWS, W_SUBID, W_SUBD, W_SUBOFF, W_MEMBERS2, W_COUNT_
+    W_SUBROWS, W_SUBID, W_SUBD, W_SUBOFF, W_MEMBERS2, W_SUBNN, W_SUBNND, W_SUBBASE, W_SUBCNT, W_CHAINPOS, W_COUNT_
 };
-static_assert(W_COUNT_ <= 48, "workspace slots");
+static_assert(W_COUNT_ <= 64, "workspace slots");
 
 struct Ctx {
     gt_ctx* c;
@@ -678,11 +680,13 @@ static void csr_from_assignment(const std::vector<int32_t>& bucket_of, int64_t C
 }
 
 // Orders each bucket's members by their nearest sub-centroid (every
-// kSubSize-th member of the bucket, by the fused kernel with lists of one):
-// an unseeded pass that starts at a query's own tile then meets the query's
-// nearest rows first, so its threshold tightens within a few tiles and few
-// candidates reach the list merges.  The kNN result does not depend on the
-// order of the pool.
+// kSubSize-th member of the bucket, by the fused kernel with lists of one),
+// the sub-centroids themselves along a greedy nearest-neighbour chain: an
+// unseeded pass that starts one sub-centroid's worth of rows before a
+// query's own tile then meets the query's nearest rows first (its own
+// sub-cluster and the two beside it on the chain), so its threshold tightens
+// within a few tiles and few candidates reach the list merges.  The kNN
+// result does not depend on the order of the pool.
 constexpr int kSubSize = 128;     // members per sub-centroid
 constexpr int kSubMax = 1024;     // sub-centroids per bucket (LDS counters of the sort)
 // GTANN_SUB_ORDER=0 keeps the two-choice order (comparisons; same results)
@@ -697,14 +701,28 @@ static void sub_order_members(Ctx& c, const DevMatrix& X, const Buckets& b, int 
     const int64_t C = static_cast<int64_t>(b.offsets.size()) - 1;
     const int64_t N = X.N;
     std::vector<int32_t> subrows;
-    std::vector<std::vector<WorkItem>> groups(static_cast<size_t>(C));
+    std::vector<std::vector<WorkItem>> groups(static_cast<size_t>(C)), sgroups(static_cast<size_t>(C));
+    std::vector<int64_t> sbase(static_cast<size_t>(C), 0);
+    std::vector<int32_t> scount(static_cast<size_t>(C), 0);
     bool any = false;
     for (int64_t bb = 0; bb < C; ++bb) {
         const int64_t lo = b.offsets[static_cast<size_t>(bb)], n = b.offsets[static_cast<size_t>(bb + 1)] - lo;
         if (n < 2 * kSubSize) continue;   // left as it is (the sort copies it)
         const int64_t s = std::min<int64_t>(kSubMax, ceil_div(n, kSubSize));
         const int64_t p0 = static_cast<int64_t>(subrows.size());
+        sbase[static_cast<size_t>(bb)] = p0;
+        scount[static_cast<size_t>(bb)] = static_cast<int32_t>(s);
         for (int64_t i = 0; i < s; ++i) subrows.push_back(b.members[static_cast<size_t>(lo + i * n / s)]);
+        for (int64_t t = 0; t < s; t += kQueriesPerBlock) {   // sub-centroids among themselves
+            WorkItem it;
+            it.q_begin = p0 + t;
+            it.q_count = static_cast<int32_t>(std::min<int64_t>(kQueriesPerBlock, s - t));
+            it.p_begin = p0;
+            it.p_count = static_cast<int32_t>(s);
+            it.p_rot = 0;
+            it.out_base = p0 + t;
+            sgroups[static_cast<size_t>(bb)].push_back(it);
+        }
         for (int64_t t = 0; t < n; t += kQueriesPerBlock) {
             WorkItem it;
             it.q_begin = lo + t;
@@ -738,10 +756,35 @@ static void sub_order_members(Ctx& c, const DevMatrix& X, const Buckets& b, int 
     a.out_ids = d_key;
     a.out_d = d_kd;
     launch_knn_fused(a, c.s);
+
+    // each sub-centroid's nearest sub-centroids of its bucket (itself among
+    // them), then the chain
+    constexpr int kChainK = 9;
+    const int64_t ns = static_cast<int64_t>(subrows.size());
+    const std::vector<WorkItem> sitems = layout_xcd(sgroups);
+    WorkItem* d_sitems = c.ws<WorkItem>(W_TASKS, sitems.size());
+    c.h2d(d_sitems, sitems.data(), sitems.size() * sizeof(WorkItem));
+    int32_t* d_nn = c.ws<int32_t>(W_SUBNN, static_cast<size_t>(ns) * kChainK);
+    float* d_nnd = c.ws<float>(W_SUBNND, static_cast<size_t>(ns) * kChainK);
+    KnnArgs sa = a;
+    sa.q_rows = d_sub;
+    sa.items = d_sitems;
+    sa.n_items = static_cast<int32_t>(sitems.size());
+    sa.M = kChainK;
+    sa.out_ids = d_nn;
+    sa.out_d = d_nnd;
+    launch_knn_fused(sa, c.s);
+    int64_t* d_sbase = c.ws<int64_t>(W_SUBBASE, static_cast<size_t>(C));
+    c.h2d(d_sbase, sbase.data(), static_cast<size_t>(C) * sizeof(int64_t));
+    int32_t* d_scount = c.ws<int32_t>(W_SUBCNT, static_cast<size_t>(C));
+    c.h2d(d_scount, scount.data(), static_cast<size_t>(C) * sizeof(int32_t));
+    int32_t* d_chain = c.ws<int32_t>(W_CHAINPOS, static_cast<size_t>(ns));
+    launch_sub_chain(d_nn, kChainK, d_sbase, d_scount, C, d_chain, c.s);
+
     int64_t* d_off = c.ws<int64_t>(W_SUBOFF, static_cast<size_t>(C + 1));
     c.h2d(d_off, b.offsets.data(), static_cast<size_t>(C + 1) * sizeof(int64_t));
     int32_t* d_m2 = c.ws<int32_t>(W_MEMBERS2, static_cast<size_t>(N));
-    launch_segment_sort(d_members, d_key, d_off, C, 2 * kSubSize, d_m2, c.s);
+    launch_segment_sort(d_members, d_key, d_off, C, 2 * kSubSize, d_chain, d_sbase, d_m2, c.s);
     c.d2d(d_members, d_m2, static_cast<size_t>(N) * sizeof(int32_t));
 }
 
@@ -781,7 +824,8 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
 
     int32_t* d_members = c.ws<int32_t>(W_MEMBERS, static_cast<size_t>(N));
     c.h2d(d_members, b.members.data(), static_cast<size_t>(N) * sizeof(int32_t));
-    if (own && !seed_d && sub_order_enabled()) sub_order_members(c, X, b, metric, d_members);
+    const bool sub_ordered = own && !seed_d && sub_order_enabled();
+    if (sub_ordered) sub_order_members(c, X, b, metric, d_members);
     CopyTaskH* d_tasks = c.ws<CopyTaskH>(W_TASKS, tasks.size());
     c.h2d(d_tasks, tasks.data(), tasks.size() * sizeof(CopyTaskH));
     int32_t* d_pool = c.ws<int32_t>(W_POOL, static_cast<size_t>(std::max<int64_t>(total, 1)));
@@ -803,8 +847,13 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
             it.p_begin = p0;
             it.p_count = static_cast<int32_t>(npb);
             // own bucket = first pool segment: start the scan at these queries'
-            // own rows (members are ordered so that neighbours sit close by)
-            it.p_rot = own && npb > 0 ? static_cast<int32_t>(t) : 0;
+            // own rows (members are ordered so that neighbours sit close by),
+            // for the sub-ordered unseeded pass one sub-cluster earlier (the
+            // chain's previous sub-cluster lies there)
+            int64_t rot = own && npb > 0 ? t : 0;
+            if (sub_ordered && nqb >= 2 * kSubSize && npb >= kSubSize) rot = (t - kSubSize + npb) % npb;   // >= 0
+            GT_REQUIRE(rot >= 0 && (npb == 0 || rot < npb), "pool rotation out of range");
+            it.p_rot = static_cast<int32_t>(rot);
             it.out_base = -1;
             groups[static_cast<size_t>(bb)].push_back(it);
         }
