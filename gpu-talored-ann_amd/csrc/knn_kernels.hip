@@ -679,20 +679,29 @@ __global__ void __launch_bounds__(256, 2) knn_fused_kernel(KnnArgs a)
 typedef int intx4 __attribute__((ext_vector_type(4)));
 typedef int intx16 __attribute__((ext_vector_type(16)));
 
-template <int DP>
+// Pool rows per stage (one barrier, one load round trip): with register
+// short lists a 32x32 tile is a few MFMAs and no LDS list work, too short to
+// hide a load latency, so those launches stage 4 tiles (2 for long rows).
+template <int DP, bool SMALL>
+struct I8Stage {
+    static constexpr int SUB = SMALL ? (DP <= 128 ? 4 : 2) : 1;
+    static constexpr int ROWS = kPoolTile * SUB;
+};
+
+template <int DP, int ROWS>
 struct KnnSmemI8Tiles {
-    int8_t tile[2][kPoolTile][DP + 16];   // +16 bytes: rows land on distinct bank groups
-    float tnorm[3][kPoolTile];
-    int32_t trow[3][kPoolTile];
+    int8_t tile[2][ROWS][DP + 16];   // +16 bytes: rows land on distinct bank groups
+    float tnorm[3][ROWS];
+    int32_t trow[3][ROWS];
 };
 
 template <int DP, bool LISTS>
-struct KnnSmemI8 : KnnSmemI8Tiles<DP> {
+struct KnnSmemI8 : KnnSmemI8Tiles<DP, I8Stage<DP, !LISTS>::ROWS> {
     KnnLists L;
 };
 
 template <int DP>
-struct KnnSmemI8<DP, false> : KnnSmemI8Tiles<DP> {};
+struct KnnSmemI8<DP, false> : KnnSmemI8Tiles<DP, I8Stage<DP, true>::ROWS> {};
 
 
 __device__ __forceinline__ floatx16 to_float(const intx16& v)
@@ -707,9 +716,12 @@ template <int DP, int METRIC, bool SMALL>
 __global__ void __launch_bounds__(256, 2) knn_i8_kernel(KnnArgs a)
 {
     constexpr int KS = DP / 32;                      // MFMA steps per tile
+    constexpr int SUB = I8Stage<DP, SMALL>::SUB;     // tiles per stage
+    constexpr int ST = I8Stage<DP, SMALL>::ROWS;     // pool rows per stage
     constexpr int U4_ROW = DP / 16;                  // 16-byte pieces per row
-    constexpr int U4_TILE = kPoolTile * U4_ROW;
+    constexpr int U4_TILE = ST * U4_ROW;
     constexpr int U4_THREAD = (U4_TILE + 255) / 256;
+    static_assert(ST <= 256, "one row id per thread");
     static_assert(DP % 32 == 0, "row stride must be a multiple of 32 bytes");
     __shared__ KnnSmemI8<DP, !SMALL> sm;
 
@@ -756,7 +768,7 @@ __global__ void __launch_bounds__(256, 2) knn_i8_kernel(KnnArgs a)
     }
 
     const int pcount = it.p_count;
-    const int ntiles = (pcount + kPoolTile - 1) / kPoolTile;
+    const int ntiles = (pcount + ST - 1) / ST;   // stages
     auto pool_row = [&](int p) -> int32_t {
         if (p >= pcount) return -1;
         p += it.p_rot;
@@ -776,9 +788,9 @@ __global__ void __launch_bounds__(256, 2) knn_i8_kernel(KnnArgs a)
 #pragma unroll
         for (int u = 0; u < U4_THREAD; ++u) {
             const int e = tid + 256 * u;
-            idn[u] = e < U4_TILE ? pool_row(t * kPoolTile + e / U4_ROW) : -1;
+            idn[u] = e < U4_TILE ? pool_row(t * ST + e / U4_ROW) : -1;
         }
-        if (tid < kPoolTile) rid_next = pool_row(t * kPoolTile + tid);
+        if (tid < ST) rid_next = pool_row(t * ST + tid);
     };
     auto load_rows = [&]() {
 #pragma unroll
@@ -798,13 +810,13 @@ __global__ void __launch_bounds__(256, 2) knn_i8_kernel(KnnArgs a)
         }
     };
 
-    if (tid < kPoolTile) { sm.tnorm[2][tid] = INFINITY; sm.trow[2][tid] = -1; }
+    if (tid < ST) { sm.tnorm[2][tid] = INFINITY; sm.trow[2][tid] = -1; }
     load_ids(0);
     load_rows();
     int32_t rid_cur = rid_next;
-    float rn_cur = tid < kPoolTile ? row_norm(rid_cur) : 0.f;
+    float rn_cur = tid < ST ? row_norm(rid_cur) : 0.f;
     store_rows(0);
-    if (tid < kPoolTile) { sm.trow[0][tid] = rid_cur; sm.tnorm[0][tid] = rn_cur; }
+    if (tid < ST) { sm.trow[0][tid] = rid_cur; sm.tnorm[0][tid] = rn_cur; }
     load_ids(1);
     __syncthreads();
 
@@ -812,34 +824,18 @@ __global__ void __launch_bounds__(256, 2) knn_i8_kernel(KnnArgs a)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc_prev[r] = 0;
 
-    for (int t = 0; t < ntiles; ++t) {
-        const int buf = t & 1;
-        wait_vmem();
-        load_rows();
-        rid_cur = rid_next;
-        rn_cur = tid < kPoolTile ? row_norm(rid_cur) : 0.f;
-        load_ids(t + 2);
-
-        intx16 acc;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[r] = 0;
-        const int8_t* arow = &sm.tile[buf][j][16 * h];
-#pragma unroll
-        for (int s = 0; s < KS; ++s) {
-            const intx4 av = *reinterpret_cast<const intx4*>(arow + 32 * s);
-            acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, qf[s], acc, 0, 0, 0);
-        }
-
-        const int pb3 = (t + 2) % 3;
+    // tile (t, u) is filtered while tile (t, u + 1)'s MFMAs run; the last
+    // tile of a stage during the first of the next
+    auto filter_tile = [&](int slot3, int u, int tbase) {
+        const float* tn = &sm.tnorm[slot3][kPoolTile * u];
+        const int32_t* tr = &sm.trow[slot3][kPoolTile * u];
         if constexpr (SMALL) {
-            if (t > 0)
-                small_tile<METRIC>(a, acc_prev, sm.tnorm[pb3], sm.trow[pb3], (t - 1) * kPoolTile, h, qvalid, qn, st,
-                                   SL);
+            small_tile<METRIC>(a, acc_prev, tn, tr, tbase, h, qvalid, qn, st, SL);
         } else {
             float mkey = INFINITY;
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-                const float4 pn = *reinterpret_cast<const float4*>(&sm.tnorm[pb3][8 * g + 4 * h]);
+                const float4 pn = *reinterpret_cast<const float4*>(tn + 8 * g + 4 * h);
                 const float n4[4] = {pn.x, pn.y, pn.z, pn.w};
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
@@ -848,41 +844,47 @@ __global__ void __launch_bounds__(256, 2) knn_i8_kernel(KnnArgs a)
                     mkey = fminf(mkey, d);
                 }
             }
-            if (t > 0 && __ballot(mkey <= st.thr))
-                tile_append<METRIC, false>(sm.L, a, to_float(acc_prev), sm.tnorm[pb3], sm.trow[pb3],
-                                           (t - 1) * kPoolTile, w, lane, h, qlocal, qvalid, qn, st);
+            if (__ballot(mkey <= st.thr))
+                tile_append<METRIC, false>(sm.L, a, to_float(acc_prev), tn, tr, tbase, w, lane, h, qlocal, qvalid, qn,
+                                           st);
+        }
+    };
+    for (int t = 0; t < ntiles; ++t) {
+        const int buf = t & 1;
+        wait_vmem();
+        load_rows();
+        rid_cur = rid_next;
+        rn_cur = tid < ST ? row_norm(rid_cur) : 0.f;
+        load_ids(t + 2);
+
+#pragma unroll
+        for (int u = 0; u < SUB; ++u) {
+            intx16 acc;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[r] = 0;
+            const int8_t* arow = &sm.tile[buf][kPoolTile * u + j][16 * h];
+#pragma unroll
+            for (int s = 0; s < KS; ++s) {
+                const intx4 av = *reinterpret_cast<const intx4*>(arow + 32 * s);
+                acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, qf[s], acc, 0, 0, 0);
+            }
+            // the previous tile: (t, u - 1), or (t - 1, SUB - 1)
+            if (u > 0) filter_tile(t % 3, u - 1, t * ST + kPoolTile * (u - 1));
+            else if (t > 0) filter_tile((t + 2) % 3, SUB - 1, (t - 1) * ST + kPoolTile * (SUB - 1));
+            acc_prev = acc;
         }
 
         store_rows(buf ^ 1);
-        if (tid < kPoolTile) { sm.trow[(t + 1) % 3][tid] = rid_cur; sm.tnorm[(t + 1) % 3][tid] = rn_cur; }
+        if (tid < ST) { sm.trow[(t + 1) % 3][tid] = rid_cur; sm.tnorm[(t + 1) % 3][tid] = rn_cur; }
         __syncthreads();
-        acc_prev = acc;
+    }
+    if (ntiles > 0) {
+        wait_vmem();
+        filter_tile((ntiles - 1) % 3, SUB - 1, (ntiles - 1) * ST + kPoolTile * (SUB - 1));
     }
     if constexpr (SMALL) {
-        if (ntiles > 0) {
-            wait_vmem();
-            const int pb3 = (ntiles - 1) % 3;
-            small_tile<METRIC>(a, acc_prev, sm.tnorm[pb3], sm.trow[pb3], (ntiles - 1) * kPoolTile, h, qvalid, qn, st,
-                               SL);
-        }
         small_finish(a, SL, j, h, qvalid, st.orow);
     } else {
-        if (ntiles > 0) {
-            wait_vmem();
-            const int pb3 = (ntiles - 1) % 3;
-            float mkey = INFINITY;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int i = 8 * (r >> 2) + 4 * h + (r & 3);
-                const float pn = sm.tnorm[pb3][i];
-                const float dot = static_cast<float>(acc_prev[r]);
-                mkey = fminf(mkey, METRIC == 0 ? fmaf(-2.f, dot, pn + qn) : fmaf(-1.f, dot, pn));
-            }
-            if (__ballot(mkey <= st.thr))
-                tile_append<METRIC, false>(sm.L, a, to_float(acc_prev), sm.tnorm[pb3], sm.trow[pb3],
-                                           (ntiles - 1) * kPoolTile, w, lane, h, qlocal, qvalid, qn, st);
-        }
-
         wait_vmem();
         merge_queries<false>(sm.L, a, w, lane, __ballot(qvalid && st.cnt > 0) & 0xffffffffull, st);
         if (qvalid) {
