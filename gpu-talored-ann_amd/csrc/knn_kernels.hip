@@ -386,6 +386,10 @@ __device__ __forceinline__ void small_tile(const KnnArgs& a, const Acc& acc, con
         if (__ballot((pass >> r) & 1u))
             if ((pass >> r) & 1u) small_insert(L, pack_key(dv[r], idv[r]));
     small_update_kth(L, a.M, st.seed);
+    // the query's two half-lists each hold M keys at or below their own
+    // M-th distance, so a candidate above the smaller of the two can never
+    // enter the merged top M: both halves filter with it
+    L.kth = fminf(L.kth, __shfl_xor(L.kth, 32));
 }
 
 // The second half-wave's keys join the first half's list, which lane j
