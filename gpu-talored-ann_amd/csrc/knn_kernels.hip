@@ -697,7 +697,29 @@ struct KnnSmemI8Tiles {
     int8_t tile[2][ROWS][DP + 16];   // +16 bytes: rows land on distinct bank groups
     float tnorm[3][ROWS];
     int32_t trow[3][ROWS];
+    int32_t thalf[3][ROWS];          // accumulator start: -floor(|p|^2 / 2) (L2), 0 (IP), kHalfPast past the end
 };
+
+// Accumulator start of a row past the slice end: no dot product (|dot| <
+// 2^22) lifts it to a query's pass floor.
+constexpr int32_t kHalfPast = -(1 << 30);
+
+// Integer pre-filter of the int8 kernel.  Every distance of that kernel is
+// an exact integer below 2^24 (int8 rows, int32 sums, |p|^2 and |q|^2 exact in
+// fp32), and its MFMA accumulators start at -floor(|p|^2 / 2), so they end at
+// v = dot - floor(|p|^2 / 2).  With T = thr - |q|^2, a row passes (L2) iff
+// |p|^2 - 2 dot <= T, i.e. 2v - (|p|^2 mod 2) >= -T, which implies
+// v >= -floor(T / 2): a tile none of whose v reach that floor holds no row
+// that passes.  For the inner product d = -dot = -v, and a row passes iff
+// v >= -thr.  No cap yet (FLT_MAX): every v passes; an invalid query (-inf):
+// none does.
+template <int METRIC>
+__device__ __forceinline__ int32_t i8_pass_floor(float thr, float qn)
+{
+    if (thr > 6.0e7f) return INT_MIN;
+    if (thr < -6.0e7f) return INT_MAX;
+    return METRIC == 0 ? -static_cast<int32_t>(floorf((thr - qn) * 0.5f)) : -static_cast<int32_t>(floorf(thr));
+}
 
 template <int DP, bool LISTS>
 struct KnnSmemI8 : KnnSmemI8Tiles<DP, I8Stage<DP, !LISTS>::ROWS> {
@@ -708,6 +730,33 @@ template <int DP>
 struct KnnSmemI8<DP, false> : KnnSmemI8Tiles<DP, I8Stage<DP, true>::ROWS> {};
 
 
+// One finished 32x32 tile of an int8 list launch: acc holds v = dot -
+// floor(|p|^2 / 2) (L2) or dot (IP) for pool rows with norms tn, ids tr and
+// accumulator starts th.  Tiles with no v at the query's pass floor lo are
+// dropped; the others go through tile_append with the exact dot products,
+// after which lo follows the query's (possibly lowered) threshold.
+template <int METRIC>
+__device__ __forceinline__ void i8_filter_tile(KnnLists& L, const KnnArgs& a, const intx16& acc, const float* tn,
+                                               const int32_t* tr, const int32_t* th, int tbase, int w, int lane, int h,
+                                               int qlocal, bool qvalid, float qn, QueryState& st, int32_t& lo)
+{
+    int32_t vmax = INT_MIN;
+#pragma unroll
+    for (int r = 0; r < 16; r += 2) vmax = max(vmax, max(acc[r], acc[r + 1]));
+    if (__ballot(vmax >= lo)) {
+        floatx16 dot;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int4 hv = *reinterpret_cast<const int4*>(th + 8 * g + 4 * h);
+            const int32_t h4[4] = {hv.x, hv.y, hv.z, hv.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) dot[4 * g + e] = static_cast<float>(acc[4 * g + e] - h4[e]);
+        }
+        tile_append<METRIC, false>(L, a, dot, tn, tr, tbase, w, lane, h, qlocal, qvalid, qn, st);
+        lo = i8_pass_floor<METRIC>(st.thr, qn);
+    }
+}
+
 __device__ __forceinline__ floatx16 to_float(const intx16& v)
 {
     floatx16 f;
@@ -716,8 +765,11 @@ __device__ __forceinline__ floatx16 to_float(const intx16& v)
     return f;
 }
 
+// Three waves per SIMD for the list launches (at most 168 VGPRs), two for
+// the register short lists.
 template <int DP, int METRIC, bool SMALL>
-__global__ void __launch_bounds__(256, 2) knn_i8_kernel(KnnArgs a)
+__global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(SMALL ? 2 : 3)))
+knn_i8_kernel(KnnArgs a)
 {
     constexpr int KS = DP / 32;                      // MFMA steps per tile
     constexpr int SUB = I8Stage<DP, SMALL>::SUB;     // tiles per stage
@@ -814,19 +866,23 @@ __global__ void __launch_bounds__(256, 2) knn_i8_kernel(KnnArgs a)
         }
     };
 
-    if (tid < ST) { sm.tnorm[2][tid] = INFINITY; sm.trow[2][tid] = -1; }
+    auto row_half = [&](int32_t row, float rn) -> int32_t {
+        return row < 0 ? kHalfPast : -(static_cast<int32_t>(rn) >> 1);
+    };
+    if (tid < ST) { sm.tnorm[2][tid] = INFINITY; sm.trow[2][tid] = -1; sm.thalf[2][tid] = kHalfPast; }
     load_ids(0);
     load_rows();
     int32_t rid_cur = rid_next;
     float rn_cur = tid < ST ? row_norm(rid_cur) : 0.f;
     store_rows(0);
-    if (tid < ST) { sm.trow[0][tid] = rid_cur; sm.tnorm[0][tid] = rn_cur; }
+    if (tid < ST) { sm.trow[0][tid] = rid_cur; sm.tnorm[0][tid] = rn_cur; sm.thalf[0][tid] = row_half(rid_cur, rn_cur); }
     load_ids(1);
     __syncthreads();
 
     intx16 acc_prev;
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc_prev[r] = 0;
+    int32_t lo = i8_pass_floor<METRIC>(st.thr, qn);
 
     // tile (t, u) is filtered while tile (t, u + 1)'s MFMAs run; the last
     // tile of a stage during the first of the next
@@ -836,21 +892,8 @@ __global__ void __launch_bounds__(256, 2) knn_i8_kernel(KnnArgs a)
         if constexpr (SMALL) {
             small_tile<METRIC>(a, acc_prev, tn, tr, tbase, h, qvalid, qn, st, SL);
         } else {
-            float mkey = INFINITY;
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const float4 pn = *reinterpret_cast<const float4*>(tn + 8 * g + 4 * h);
-                const float n4[4] = {pn.x, pn.y, pn.z, pn.w};
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float dot = static_cast<float>(acc_prev[4 * g + e]);
-                    const float d = METRIC == 0 ? fmaf(-2.f, dot, n4[e] + qn) : fmaf(-1.f, dot, n4[e]);
-                    mkey = fminf(mkey, d);
-                }
-            }
-            if (__ballot(mkey <= st.thr))
-                tile_append<METRIC, false>(sm.L, a, to_float(acc_prev), tn, tr, tbase, w, lane, h, qlocal, qvalid, qn,
-                                           st);
+            i8_filter_tile<METRIC>(sm.L, a, acc_prev, tn, tr, &sm.thalf[slot3][kPoolTile * u], tbase, w, lane, h,
+                                   qlocal, qvalid, qn, st, lo);
         }
     };
     for (int t = 0; t < ntiles; ++t) {
@@ -864,8 +907,17 @@ __global__ void __launch_bounds__(256, 2) knn_i8_kernel(KnnArgs a)
 #pragma unroll
         for (int u = 0; u < SUB; ++u) {
             intx16 acc;
+            if constexpr (SMALL) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) acc[r] = 0;
+                for (int r = 0; r < 16; ++r) acc[r] = 0;
+            } else {
+                const int32_t* th = &sm.thalf[t % 3][kPoolTile * u];
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int4 hv = *reinterpret_cast<const int4*>(th + 8 * g + 4 * h);
+                    acc[4 * g] = hv.x; acc[4 * g + 1] = hv.y; acc[4 * g + 2] = hv.z; acc[4 * g + 3] = hv.w;
+                }
+            }
             const int8_t* arow = &sm.tile[buf][kPoolTile * u + j][16 * h];
 #pragma unroll
             for (int s = 0; s < KS; ++s) {
@@ -879,7 +931,11 @@ __global__ void __launch_bounds__(256, 2) knn_i8_kernel(KnnArgs a)
         }
 
         store_rows(buf ^ 1);
-        if (tid < ST) { sm.trow[(t + 1) % 3][tid] = rid_cur; sm.tnorm[(t + 1) % 3][tid] = rn_cur; }
+        if (tid < ST) {
+            sm.trow[(t + 1) % 3][tid] = rid_cur;
+            sm.tnorm[(t + 1) % 3][tid] = rn_cur;
+            sm.thalf[(t + 1) % 3][tid] = row_half(rid_cur, rn_cur);
+        }
         __syncthreads();
     }
     if (ntiles > 0) {
