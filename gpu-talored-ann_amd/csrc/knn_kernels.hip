@@ -115,6 +115,20 @@ __device__ __forceinline__ int32_t load_list_i(const int32_t* p)
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
+// Inclusive prefix sum across the 64 lanes: row shifts by 1, 2, 4 and 8 sum
+// within each row of 16 lanes, then rows 1 and 3 add the last lane of the row
+// before them, rows 2 and 3 the last lane of row 1.
+__device__ __forceinline__ int wave_incl_scan(int x)
+{
+    x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);   // row_shr:1
+    x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);   // row_shr:2
+    x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);   // row_shr:4
+    x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);   // row_shr:8
+    x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);   // row_bcast:15
+    x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);   // row_bcast:31
+    return x;
+}
+
 // Merges the buffer of query q (0..31 of this wave) into its sorted list
 // (output row) and recomputes its threshold.  Positions come from rank
 // counting: a buffer entry's position is its rank among the buffer plus the
@@ -166,37 +180,11 @@ __device__ void wave_merge(KnnLists& sm, const KnnArgs& a, int w, int lane, int 
     }
     rb += __shfl_xor(rb, 32);
 
-    // buffer entries below list entries lane, lane + 64
-    const uint64_t lk0 = lane < nL ? pack_key(ld0, li0) : kNoKey;
-    const uint64_t lk1 = lane + 64 < nL ? pack_key(ld1, li1) : kNoKey;
-    int cl0 = 0, cl1 = 0;
-    {
-        const uint4* B4 = reinterpret_cast<const uint4*>(B);
-        if (nL > 64) {
-#pragma unroll 4
-            for (int e = 0; e < kCB / 2; ++e) {
-                const uint4 x = B4[e];
-#pragma unroll
-                for (int o = 0; o < 2; ++o) {
-                    const uint64_t v = key_at(x, o);
-                    cl0 += v < lk0 ? 1 : 0;
-                    cl1 += v < lk1 ? 1 : 0;
-                }
-            }
-        } else {
-#pragma unroll 4
-            for (int e = 0; e < kCB / 2; ++e) {
-                const uint4 x = B4[e];
-                cl0 += key_at(x, 0) < lk0 ? 1 : 0;
-                cl1 += key_at(x, 1) < lk0 ? 1 : 0;
-            }
-            cl0 += cl1;
-        }
-    }
-
     // list entries below buffer entry bl: the list goes through LDS (padding
     // entries are kNoKey, never below a key); half h counts entries
     // [32h, 32h + 32) and, for lists longer than 64, [64 + 32h, 96 + 32h)
+    const uint64_t lk0 = lane < nL ? pack_key(ld0, li0) : kNoKey;
+    const uint64_t lk1 = lane + 64 < nL ? pack_key(ld1, li1) : kNoKey;
     L[lane] = lk0;
     if (nL > 64) L[lane + 64] = lk1;
     wave_sync();
@@ -213,7 +201,20 @@ __device__ void wave_merge(KnnLists& sm, const KnnArgs& a, int w, int lane, int 
     nlb += __shfl_xor(nlb, 32);
     if (h == 0) B[bl] = kNoKey;   // the buffer starts over empty
 
+    // buffer entries below list entry i: those with nlb <= i (the list is
+    // sorted and keys are distinct), i.e. a prefix sum over i of the
+    // histogram of nlb, kept in the list's staging area once read
     const bool bvalid = h == 0 && bk != kNoKey;
+    int* H = reinterpret_cast<int*>(L);   // counters 0..128
+    H[lane] = 0;
+    H[lane + 64] = 0;
+    if (lane == 0) H[128] = 0;
+    wave_sync();
+    if (bvalid) atomicAdd(&H[nlb], 1);
+    wave_sync();
+    const int cl0 = wave_incl_scan(H[lane]);
+    const int cl1 = nL > 64 ? __builtin_amdgcn_readlane(cl0, 63) + wave_incl_scan(H[lane + 64]) : 0;
+
     const int nBv = static_cast<int>(__popcll(__ballot(bvalid)));
     const int total = nL + nBv;
     bool last = false;   // this lane wrote position M-1
