@@ -180,40 +180,39 @@ __device__ void wave_merge(KnnLists& sm, const KnnArgs& a, int w, int lane, int 
     }
     rb += __shfl_xor(rb, 32);
 
-    // list entries below buffer entry bl: the list goes through LDS (padding
-    // entries are kNoKey, never below a key); half h counts entries
-    // [32h, 32h + 32) and, for lists longer than 64, [64 + 32h, 96 + 32h)
+    // the buffer in key order through LDS (slots past the valid entries
+    // hold kNoKey): S[rank] = key
+    const bool bvalid = h == 0 && bk != kNoKey;
+    uint64_t* S = L;
+    if (h == 0) S[bl] = kNoKey;
+    if (bvalid) S[rb] = bk;
+    if (h == 0) B[bl] = kNoKey;   // the buffer starts over empty
+    wave_sync();
+
+    // buffer entries below list entries lane, lane + 64: lower bounds in S,
+    // over S[0, 31) in five halvings, then S[31]
     const uint64_t lk0 = lane < nL ? pack_key(ld0, li0) : kNoKey;
     const uint64_t lk1 = lane + 64 < nL ? pack_key(ld1, li1) : kNoKey;
-    L[lane] = lk0;
-    if (nL > 64) L[lane + 64] = lk1;
-    wave_sync();
-    int nlb = 0;
-    for (int part = 0; part < (nL > 64 ? 2 : 1); ++part) {
-        const uint4* L4 = reinterpret_cast<const uint4*>(L + 64 * part + 32 * h);
-#pragma unroll 4
-        for (int e = 0; e < 16; ++e) {
-            const uint4 x = L4[e];
-            nlb += key_at(x, 0) < bk ? 1 : 0;
-            nlb += key_at(x, 1) < bk ? 1 : 0;
-        }
+    int cl0 = 0, cl1 = 0;
+#pragma unroll
+    for (int step = 16; step > 0; step >>= 1) {
+        if (S[cl0 + step - 1] < lk0) cl0 += step;
+        if (nL > 64 && S[cl1 + step - 1] < lk1) cl1 += step;
     }
-    nlb += __shfl_xor(nlb, 32);
-    if (h == 0) B[bl] = kNoKey;   // the buffer starts over empty
+    cl0 += S[cl0] < lk0 ? 1 : 0;
+    if (nL > 64) cl1 += S[cl1] < lk1 ? 1 : 0;
 
-    // buffer entries below list entry i: those with nlb <= i (the list is
-    // sorted and keys are distinct), i.e. a prefix sum over i of the
-    // histogram of nlb, kept in the list's staging area once read
-    const bool bvalid = h == 0 && bk != kNoKey;
-    int* H = reinterpret_cast<int*>(L);   // counters 0..128
-    H[lane] = 0;
-    H[lane + 64] = 0;
-    if (lane == 0) H[128] = 0;
+    // list entries below the buffer entry of rank r: those with cl <= r (the
+    // list is sorted and keys are distinct), a prefix sum over r of the
+    // histogram of cl, kept in LDS after S
+    int* H = reinterpret_cast<int*>(L + 32);   // counters 0..32
+    if (lane <= 32) H[lane] = 0;
     wave_sync();
-    if (bvalid) atomicAdd(&H[nlb], 1);
+    if (lane < nL) atomicAdd(&H[cl0], 1);
+    if (lane + 64 < nL) atomicAdd(&H[cl1], 1);
     wave_sync();
-    const int cl0 = wave_incl_scan(H[lane]);
-    const int cl1 = nL > 64 ? __builtin_amdgcn_readlane(cl0, 63) + wave_incl_scan(H[lane + 64]) : 0;
+    const int below = wave_incl_scan(lane <= 32 ? H[lane] : 0);
+    const int nlb = __shfl(below, rb);
 
     const int nBv = static_cast<int>(__popcll(__ballot(bvalid)));
     const int total = nL + nBv;
