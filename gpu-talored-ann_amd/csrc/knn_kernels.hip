@@ -130,14 +130,17 @@ __device__ __forceinline__ int wave_incl_scan(int x)
 }
 
 // Merges the buffer of query q (0..31 of this wave) into its sorted list
-// (output row) and recomputes its threshold.  Positions come from rank
-// counting: a buffer entry's position is its rank among the buffer plus the
-// number of list entries below it; a list entry's position is its index plus
-// the number of buffer entries below it.  Every count is split between the
-// two half-waves (lanes l and l + 32 both hold buffer entry l) over 128-bit
-// LDS broadcast reads and finished with one shuffle, so no step waits on a
-// chain of round trips; the list loads are issued first and land while the
-// buffer is ranked.  Called by all 64 lanes.
+// (output row) and recomputes its threshold.  A buffer entry goes to its rank
+// among the buffer plus the number of list entries below it; a list entry to
+// its index plus the number of buffer entries below it.  The buffer ranks
+// come from counting (split between the two half-waves, lanes l and l + 32
+// both holding buffer entry l, over 128-bit LDS broadcast reads); the buffer
+// then sits in LDS in rank order, each list entry finds its count by a lower
+// bound in it, and the list entries below the buffer entry of rank r are
+// those whose lower bound is at most r: a prefix sum (DPP) over a histogram
+// of the lower bounds.  Keys are distinct, so no count is ambiguous.  The
+// list loads are issued first and land while the buffer is ranked.  Called by
+// all 64 lanes.
 __device__ void wave_merge(KnnLists& sm, const KnnArgs& a, int w, int lane, int q, QueryState& st)
 {
     // query q's state, uniform across the wave (scalar registers)
