@@ -7,13 +7,15 @@ merge), sanitize, CAGRA prune, reverse-edge merge -- of configuration C2
 (1,000,000 x 128 fp32 integer-valued points, L2, 256 buckets, M 64 -> K 32)
 with the dataset already resident in HBM.  Prints one JSON line.
 
-`roofline` is the fused kNN kernel of the rounds: achieved = the
-algorithmic flops of its launches (2*D per scanned (query, pool row) pair)
-over their summed duration, both measured by the library with HIP events on
-its stream.  `traffic` is read from profiles/knn_fused_C2_traffic.json, the
-rocprofv3 FETCH_SIZE/WRITE_SIZE measurement of the same launches (see
-profiles/knn_fused_C2_build.md for the commands), when the configuration is
-C2 with the default knobs.
+`roofline` is the kNN kernel of the rounds (knn_i8_kernel when the rows are
+integers, as C2's are; knn_fused_kernel / knn_wide_kernel otherwise):
+achieved = the algorithmic ops of its launches (2*D per scanned (query, pool
+row) pair) over their summed duration, both measured by the library with HIP
+events on its stream.  `traffic` is read from
+profiles/<kernel>_<config>_traffic.json (knn_i8_C2_traffic.json for the
+default run), the rocprofv3 FETCH_SIZE/WRITE_SIZE measurement of the same
+launches (commands in profiles/knn_i8_C2_build.md), when the knobs are the
+defaults.
 
 `search` (after the build) runs the search entry point on workload S2 (the
 C2 shape with a 16-dimensional latent structure: a connected graph, unlike
