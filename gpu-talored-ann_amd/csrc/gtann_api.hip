@@ -81,6 +81,9 @@ void launch_refine_2hop(const float* X, const float* norms, int64_t N, int Dp, i
                         const float* in_d, int M, int S, int32_t* out_ids, float* out_d, hipStream_t s);
 void launch_centroid_sums(const float* X, int Dp, const int32_t* members, const int64_t* offsets, int64_t C,
                           float* centroids, hipStream_t s);
+int csr_blocks(int64_t S);
+void launch_sample_csr(const int32_t* key, const int32_t* val, int64_t S, int C, uint32_t* hist, uint32_t* offs,
+                       uint32_t* sums, int32_t* members, int64_t* off, hipStream_t s);
 
 struct CopyTaskH { int64_t src; int64_t dst; int64_t n; };
 
@@ -189,7 +192,8 @@ enum Ws {
     W_X, W_XRAW, W_NORMS, W_C, W_CRAW, W_CNORMS, W_IDS, W_D, W_IDS2, W_D2, W_IDS3, W_D3, W_ITEMS, W_QROWS, W_PROWS,
     W_MEMBERS, W_TASKS, W_POOL, W_PART_I, W_PART_D, W_G1, W_G2, W_G3, W_DEG, W_OFF, W_CUR, W_KEYS, W_SUMS, W_FLAG,
     W_TMP, W_OUT, W_IN, W_PROBE_I, W_PROBE_D, W_WORST, W_X8, W_NORMS8, W_C8, W_CNORMS8,
-    W_SUBROWS, W_SUBID, W_SUBD, W_SUBOFF, W_MEMBERS2, W_SUBNN, W_SUBNND, W_SUBBASE, W_SUBCNT, W_CHAINPOS, W_COUNT_
+    W_SUBROWS, W_SUBID, W_SUBD, W_SUBOFF, W_MEMBERS2, W_SUBNN, W_SUBNND, W_SUBBASE, W_SUBCNT, W_CHAINPOS,
+    W_LHIST, W_LOFFS, W_LSUMS, W_COUNT_
 };
 static_assert(W_COUNT_ <= 64, "workspace slots");
 
@@ -687,6 +691,14 @@ static void csr_from_assignment(const std::vector<int32_t>& bucket_of, int64_t C
 // sub-cluster and the two beside it on the chain), so its threshold tightens
 // within a few tiles and few candidates reach the list merges.  The kNN
 // result does not depend on the order of the pool.
+// GTANN_LLOYD_HOST=1 groups the Lloyd samples on the host (download, counting
+// sort, upload) instead of on the device (comparisons; the same CSR)
+static bool lloyd_host_csr()
+{
+    const char* e = std::getenv("GTANN_LLOYD_HOST");
+    return e && e[0] == '1';
+}
+
 constexpr int kSubSize = 128;     // members per sub-centroid
 constexpr int kSubMax = 1024;     // sub-centroids per bucket (LDS counters of the sort)
 // GTANN_SUB_ORDER=0 keeps the two-choice order (comparisons; same results)
@@ -981,6 +993,12 @@ static void bucket_device(Ctx& c, const DevMatrix& X, int64_t C, int nprobe, int
         int32_t* d_mem = c.ws<int32_t>(W_MEMBERS, static_cast<size_t>(S));
         int64_t* d_off = c.ws<int64_t>(W_OFF, static_cast<size_t>(C + 1));
         std::vector<int64_t> off;
+        // the CSR on the device: no host round trip per iteration
+        const bool host_csr = lloyd_host_csr() || C > 16384;
+        const int64_t nh = C * csr_blocks(S);
+        uint32_t* d_lhist = host_csr ? nullptr : c.ws<uint32_t>(W_LHIST, static_cast<size_t>(nh));
+        uint32_t* d_loffs = host_csr ? nullptr : c.ws<uint32_t>(W_LOFFS, static_cast<size_t>(nh + 1));
+        uint32_t* d_lsums = host_csr ? nullptr : c.ws<uint32_t>(W_LSUMS, static_cast<size_t>(nh / 1024 + 2));
         for (int it = 0; it < kmeans_iters; ++it) {
             KnnJob j;
             j.Q = &X;
@@ -995,16 +1013,20 @@ static void bucket_device(Ctx& c, const DevMatrix& X, int64_t C, int nprobe, int
             j.out_ids = d_n1;
             j.out_d = d_n1d;
             run_knn_flat(c, j, 1);
-            c.d2h(nearest, d_n1, static_cast<size_t>(S) * sizeof(int32_t));
-            c.sync();
-            // CSR in sample order (stable counting sort), members as row ids
-            counting_sort(nullptr, S, nearest, C, hmem, off);
-            parallel_slices(S, host_threads(), [&](int, int64_t lo, int64_t hi) {
-                for (int64_t e = lo; e < hi; ++e) hmem[e] = srows[static_cast<size_t>(hmem[e])];
-            });
-            std::copy(off.begin(), off.end(), hoff);
-            c.h2d(d_mem, hmem, static_cast<size_t>(S) * sizeof(int32_t));
-            c.h2d(d_off, hoff, static_cast<size_t>(C + 1) * sizeof(int64_t));
+            if (!host_csr) {
+                // CSR in sample order (stable counting sort), members as row ids
+                launch_sample_csr(d_n1, d_srows, S, static_cast<int>(C), d_lhist, d_loffs, d_lsums, d_mem, d_off, c.s);
+            } else {
+                c.d2h(nearest, d_n1, static_cast<size_t>(S) * sizeof(int32_t));
+                c.sync();
+                counting_sort(nullptr, S, nearest, C, hmem, off);
+                parallel_slices(S, host_threads(), [&](int, int64_t lo, int64_t hi) {
+                    for (int64_t e = lo; e < hi; ++e) hmem[e] = srows[static_cast<size_t>(hmem[e])];
+                });
+                std::copy(off.begin(), off.end(), hoff);
+                c.h2d(d_mem, hmem, static_cast<size_t>(S) * sizeof(int32_t));
+                c.h2d(d_off, hoff, static_cast<size_t>(C + 1) * sizeof(int64_t));
+            }
             launch_centroid_sums(X.data, X.Dp, d_mem, d_off, C, d_cm, c.s);
             launch_row_norms(d_cm, C, X.Dp, d_cn, c.s);
             refresh_c8();

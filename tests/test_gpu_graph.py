@@ -347,3 +347,24 @@ def test_sub_centroid_order_does_not_change_the_build(ctx, monkeypatch):
     d = ctx.build_graph(X.astype(np.float32) + 0.25, **kw)
     np.testing.assert_array_equal(c.knn_ids, d.knn_ids)
     np.testing.assert_array_equal(c.graph, d.graph)
+
+
+@pytest.mark.parametrize("dtype,n_buckets", [("f32", 37), ("i8", 24), ("f32", 300)])
+def test_lloyd_device_csr_matches_host(ctx, monkeypatch, dtype, n_buckets):
+    """The Lloyd steps group the sampled rows by nearest centroid on the
+    device (stable counting sort); the host's counting sort
+    (GTANN_LLOYD_HOST=1) gives the same CSR, hence the same centroids and the
+    same build.  300 buckets over 40,000 rows leaves some centroids with few
+    or no sampled members."""
+    import synth
+    X, _ = synth.generate("C2", n=40000)
+    if dtype == "i8":
+        X = (X.astype(np.int64) - 128).clip(-128, 127).astype(np.int8)
+    print(f"lloyd csr {dtype} buckets={n_buckets}", flush=True)
+    kw = dict(n_buckets=n_buckets, nprobe=1, M=32, K=16, rounds=2, kmeans_iters=3)
+    a = ctx.build_graph(X, **kw)
+    monkeypatch.setenv("GTANN_LLOYD_HOST", "1")
+    b = ctx.build_graph(X, **kw)
+    np.testing.assert_array_equal(a.knn_ids, b.knn_ids)
+    np.testing.assert_array_equal(a.knn_dists, b.knn_dists)
+    np.testing.assert_array_equal(a.graph, b.graph)
