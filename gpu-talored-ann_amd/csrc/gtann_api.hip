@@ -683,14 +683,6 @@ static void csr_from_assignment(const std::vector<int32_t>& bucket_of, int64_t C
     counting_sort(nullptr, N, bucket_of.data(), C, b.members.data(), b.offsets);
 }
 
-// Orders each bucket's members by their nearest sub-centroid (every
-// kSubSize-th member of the bucket, by the fused kernel with lists of one),
-// the sub-centroids themselves along a greedy nearest-neighbour chain: an
-// unseeded pass that starts one sub-centroid's worth of rows before a
-// query's own tile then meets the query's nearest rows first (its own
-// sub-cluster and the two beside it on the chain), so its threshold tightens
-// within a few tiles and few candidates reach the list merges.  The kNN
-// result does not depend on the order of the pool.
 // GTANN_LLOYD_HOST=1 groups the Lloyd samples on the host (download, counting
 // sort, upload) instead of on the device (comparisons; the same CSR)
 static bool lloyd_host_csr()
@@ -699,6 +691,14 @@ static bool lloyd_host_csr()
     return e && e[0] == '1';
 }
 
+// Orders each bucket's members by their nearest sub-centroid (every
+// kSubSize-th member of the bucket, by the fused kernel with lists of one),
+// the sub-centroids themselves along a greedy nearest-neighbour chain: an
+// unseeded pass that starts one sub-centroid's worth of rows before a
+// query's own tile then meets the query's nearest rows first (its own
+// sub-cluster and the two beside it on the chain), so its threshold tightens
+// within a few tiles and few candidates reach the list merges.  The kNN
+// result does not depend on the order of the pool.
 constexpr int kSubSize = 128;     // members per sub-centroid
 constexpr int kSubMax = 1024;     // sub-centroids per bucket (LDS counters of the sort)
 // GTANN_SUB_ORDER=0 keeps the two-choice order (comparisons; same results)
