@@ -183,6 +183,7 @@ struct gt_ctx {
     // fresh N-sized allocations every round)
     std::vector<int32_t> h_bucket_of, h_key2, h_by_key, h_members[2];
     int64_t knn_launches = 0;   // bucketed-round launches of the current build
+    uint64_t members_gen = 0;   // bucketing whose members W_MEMBERS holds (0: none)
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
 };
 
@@ -273,6 +274,19 @@ static std::vector<WorkItem> layout_xcd(const std::vector<std::vector<WorkItem>>
         l.resize(per, empty);
         out.insert(out.end(), l.begin(), l.end());
     }
+    return out;
+}
+
+// layout_xcd for groups of one item each of (nearly) equal cost: dealt
+// round-robin to the XCDs in order, lists padded to the same length.
+static std::vector<WorkItem> layout_flat(const std::vector<WorkItem>& items)
+{
+    constexpr size_t kXcd = 8;
+    const size_t per = (items.size() + kXcd - 1) / kXcd;
+    WorkItem empty{};
+    empty.q_count = 0;
+    std::vector<WorkItem> out(per * kXcd, empty);
+    for (size_t i = 0; i < items.size(); ++i) out[(i % kXcd) * per + i / kXcd] = items[i];
     return out;
 }
 
@@ -425,8 +439,8 @@ static void run_knn_flat(Ctx& c, const KnnJob& j, int min_items = 2048)
         splits = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>({want, by_pool, 2048 / j.M, 64})));
     }
     const int64_t chunk = ceil_div(j.np, splits);
-    std::vector<std::vector<WorkItem>> groups;
-    groups.reserve(static_cast<size_t>(qtiles * splits));
+    std::vector<WorkItem> flat;
+    flat.reserve(static_cast<size_t>(qtiles * splits));
     for (int s = 0; s < splits; ++s) {
         const int64_t p0 = s * chunk;
         const int64_t pc = std::min<int64_t>(chunk, j.np - p0);
@@ -437,10 +451,10 @@ static void run_knn_flat(Ctx& c, const KnnJob& j, int min_items = 2048)
             it.p_begin = p0;
             it.p_count = static_cast<int32_t>(std::max<int64_t>(pc, 0));
             it.out_base = static_cast<int64_t>(s) * j.nq + it.q_begin;
-            groups.push_back({it});
+            flat.push_back(it);
         }
     }
-    const std::vector<WorkItem> items = layout_xcd(groups);
+    const std::vector<WorkItem> items = layout_flat(flat);
     WorkItem* d_items = c.ws<WorkItem>(W_ITEMS, items.size());
     c.h2d(d_items, items.data(), items.size() * sizeof(WorkItem));
     int32_t* oi = j.out_ids;
@@ -524,7 +538,15 @@ struct Buckets {
     std::vector<int32_t> members;   // N
     std::vector<int32_t> probe;     // C x P (bucket indices, -1 = none)
     int P = 0;
+    uint64_t gen = 0;               // which bucketing (0: none recorded)
 };
+
+// generation of a host bucketing, never 0
+static uint64_t next_bucket_gen()
+{
+    static std::atomic<uint64_t> g{0};
+    return ++g;
+}
 
 // Two-choice assignment (src/bucket.cu:2276-2302): point i goes to its 2nd
 // nearest centroid if that bucket is smaller than balance x the nearest
@@ -834,8 +856,14 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
     }
     pool_off[static_cast<size_t>(C)] = total;
 
+    // the members go up once per bucketing: a later pass over the same
+    // buckets finds them in place (perhaps reordered within each bucket by
+    // the sub-centroid order, which changes no result)
     int32_t* d_members = c.ws<int32_t>(W_MEMBERS, static_cast<size_t>(N));
-    c.h2d(d_members, b.members.data(), static_cast<size_t>(N) * sizeof(int32_t));
+    if (b.gen == 0 || c.c->members_gen != b.gen) {
+        c.h2d(d_members, b.members.data(), static_cast<size_t>(N) * sizeof(int32_t));
+        c.c->members_gen = b.gen;
+    }
     const bool sub_ordered = own && !seed_d && sub_order_enabled();
     if (sub_ordered) sub_order_members(c, X, b, metric, d_members);
     CopyTaskH* d_tasks = c.ws<CopyTaskH>(W_TASKS, tasks.size());
@@ -991,6 +1019,7 @@ static void bucket_device(Ctx& c, const DevMatrix& X, int64_t C, int nprobe, int
         int32_t* hmem = reinterpret_cast<int32_t*>(pin + s4);
         int64_t* hoff = reinterpret_cast<int64_t*>(pin + 2 * s4);
         int32_t* d_mem = c.ws<int32_t>(W_MEMBERS, static_cast<size_t>(S));
+        c.c->members_gen = 0;   // W_MEMBERS no longer holds a bucketing's members
         int64_t* d_off = c.ws<int64_t>(W_OFF, static_cast<size_t>(C + 1));
         std::vector<int64_t> off;
         // the CSR on the device: no host round trip per iteration
@@ -1158,6 +1187,7 @@ static void bucket_host(const BucketPlan& bp, float balance, Buckets& b, std::ve
     csr_from_assignment_keyed(bucket_of, key2, C, b, by_key);
     b.P = bp.P;
     b.probe = bp.probe;
+    b.gen = next_bucket_gen();
     if (tr.on)
         std::fprintf(stderr, "[gtann] bucketing (host thread): two-choice %.3f ms, CSR %.3f ms\n", t_tc * 1e3,
                      (tr.t.sec() - t_tc) * 1e3);
