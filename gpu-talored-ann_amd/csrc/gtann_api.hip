@@ -171,6 +171,27 @@ struct Trace {
 
 }  // namespace gtann
 
+namespace gtann {
+
+// Allocator over pinned host memory (hipHostMalloc): a vector whose upload
+// is a DMA transfer the host does not wait for.
+template <class T> struct PinnedAlloc {
+    using value_type = T;
+    PinnedAlloc() = default;
+    template <class U> PinnedAlloc(const PinnedAlloc<U>&) {}
+    T* allocate(size_t n) {
+        void* p = nullptr;
+        if (hipHostMalloc(&p, n * sizeof(T), hipHostMallocDefault) != hipSuccess) throw std::bad_alloc();
+        return static_cast<T*>(p);
+    }
+    void deallocate(T* p, size_t) { (void)hipHostFree(p); }
+    template <class U> bool operator==(const PinnedAlloc<U>&) const { return true; }
+    template <class U> bool operator!=(const PinnedAlloc<U>&) const { return false; }
+};
+using PinnedI32 = std::vector<int32_t, PinnedAlloc<int32_t>>;
+
+}  // namespace gtann
+
 struct gt_ctx {
     int device = 0;
     hipStream_t stream = nullptr;
@@ -181,7 +202,9 @@ struct gt_ctx {
     gtann::HostBuf pin_lloyd;   // Lloyd steps: nearest centroids down, CSR up
     // host scratch of the bucketing, reused across calls (no page faults on
     // fresh N-sized allocations every round)
-    std::vector<int32_t> h_bucket_of, h_key2, h_by_key, h_members[2];
+    std::vector<int32_t> h_bucket_of, h_key2, h_by_key, h_bkt;
+    gtann::PinnedI32 h_members[2];
+    hipEvent_t members_up[2] = {nullptr, nullptr};   // after the last upload of h_members[i]
     int64_t knn_launches = 0;   // bucketed-round launches of the current build
     uint64_t members_gen = 0;   // bucketing whose members W_MEMBERS holds (0: none)
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
@@ -535,10 +558,11 @@ static RoundSamples draw_round(int64_t N, int64_t C, int kmeans_iters, uint64_t 
 
 struct Buckets {
     std::vector<int64_t> offsets;   // C+1
-    std::vector<int32_t> members;   // N
+    PinnedI32 members;              // N
     std::vector<int32_t> probe;     // C x P (bucket indices, -1 = none)
     int P = 0;
     uint64_t gen = 0;               // which bucketing (0: none recorded)
+    hipEvent_t uploaded = nullptr;  // recorded after each upload of members, if set
 };
 
 // generation of a host bucketing, never 0
@@ -684,18 +708,56 @@ static void counting_sort(const int32_t* in, int64_t n, const int32_t* key, int6
     });
 }
 
+// Stable counting sort of positions e in [0, n) by key[e] (keys in [0, K)):
+// out[pos] = val ? val[e] : e, and out_carry[pos] = carry[e] when carry is
+// given; off (K+1) receives the key offsets.  Each thread counts and
+// scatters its own slice, so the order is the serial one.
+static void counting_sort_kv(const int32_t* key, const int32_t* val, int64_t n, int64_t K, int32_t* out,
+                             const int32_t* carry, int32_t* out_carry, std::vector<int64_t>& off)
+{
+    const int T = n < 65536 ? 1 : host_threads();
+    std::vector<int64_t> cnt(static_cast<size_t>(T) * static_cast<size_t>(K), 0);
+    parallel_slices(n, T, [&](int t, int64_t lo, int64_t hi) {
+        int64_t* c = cnt.data() + static_cast<size_t>(t) * K;
+        for (int64_t e = lo; e < hi; ++e) c[key[e]]++;
+    });
+    off.assign(static_cast<size_t>(K + 1), 0);
+    int64_t run = 0;
+    for (int64_t k = 0; k < K; ++k) {
+        off[static_cast<size_t>(k)] = run;
+        for (int t = 0; t < T; ++t) {
+            int64_t& c = cnt[static_cast<size_t>(t) * K + k];
+            const int64_t v = c;
+            c = run;
+            run += v;
+        }
+    }
+    off[static_cast<size_t>(K)] = run;
+    parallel_slices(n, T, [&](int t, int64_t lo, int64_t hi) {
+        int64_t* c = cnt.data() + static_cast<size_t>(t) * K;
+        for (int64_t e = lo; e < hi; ++e) {
+            const int64_t pos = c[key[e]]++;
+            out[pos] = val ? val[e] : static_cast<int32_t>(e);
+            if (carry) out_carry[pos] = carry[e];
+        }
+    });
+}
+
 // CSR of an assignment with members ordered by (bucket, key2, id): two stable
 // counting sorts.  key2 = each point's other top-2 centroid, so that points
 // of one bucket near the same neighbouring bucket sit next to each other.
 static void csr_from_assignment_keyed(const std::vector<int32_t>& bucket_of, const std::vector<int32_t>& key2,
-                                      int64_t C, Buckets& b, std::vector<int32_t>& by_key)
+                                      int64_t C, Buckets& b, std::vector<int32_t>& by_key, std::vector<int32_t>& bkt)
 {
     const int64_t N = static_cast<int64_t>(bucket_of.size());
     by_key.resize(static_cast<size_t>(N));
+    bkt.resize(static_cast<size_t>(N));
     std::vector<int64_t> off;
-    counting_sort(nullptr, N, key2.data(), C, by_key.data(), off);
+    // the ids by key2, each carrying its bucket, then by bucket: both passes
+    // read their keys in order
+    counting_sort_kv(key2.data(), nullptr, N, C, by_key.data(), bucket_of.data(), bkt.data(), off);
     b.members.resize(static_cast<size_t>(N));
-    counting_sort(by_key.data(), N, bucket_of.data(), C, b.members.data(), b.offsets);
+    counting_sort_kv(bkt.data(), by_key.data(), N, C, b.members.data(), nullptr, nullptr, b.offsets);
 }
 
 static void csr_from_assignment(const std::vector<int32_t>& bucket_of, int64_t C, Buckets& b)
@@ -862,6 +924,7 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
     int32_t* d_members = c.ws<int32_t>(W_MEMBERS, static_cast<size_t>(N));
     if (b.gen == 0 || c.c->members_gen != b.gen) {
         c.h2d(d_members, b.members.data(), static_cast<size_t>(N) * sizeof(int32_t));
+        if (b.uploaded) GT_HIP(hipEventRecord(b.uploaded, c.s));
         c.c->members_gen = b.gen;
     }
     const bool sub_ordered = own && !seed_d && sub_order_enabled();
@@ -1168,7 +1231,7 @@ static void bucket_device(Ctx& c, const DevMatrix& X, int64_t C, int nprobe, int
 // members ordered by (bucket, other top-2 centroid, id).  Host code only (no
 // HIP calls), so the build runs it on a worker thread.
 static void bucket_host(const BucketPlan& bp, float balance, Buckets& b, std::vector<int32_t>& bucket_of,
-                        std::vector<int32_t>& key2, std::vector<int32_t>& by_key)
+                        std::vector<int32_t>& key2, std::vector<int32_t>& by_key, std::vector<int32_t>& bkt)
 {
     const int64_t N = bp.N, C = bp.C;
     const uint32_t* top2 = bp.top2;
@@ -1184,7 +1247,7 @@ static void bucket_host(const BucketPlan& bp, float balance, Buckets& b, std::ve
                                                                               : bucket_of[static_cast<size_t>(i)];
         }
     });
-    csr_from_assignment_keyed(bucket_of, key2, C, b, by_key);
+    csr_from_assignment_keyed(bucket_of, key2, C, b, by_key, bkt);
     b.P = bp.P;
     b.probe = bp.probe;
     b.gen = next_bucket_gen();
@@ -1361,7 +1424,8 @@ int gt_create(int device, gt_ctx** out)
     if (!c) return GT_ENOMEM;
     c->device = device;
     if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess ||
-        hipEventCreate(&c->ev0) != hipSuccess || hipEventCreate(&c->ev1) != hipSuccess) {
+        hipEventCreate(&c->ev0) != hipSuccess || hipEventCreate(&c->ev1) != hipSuccess ||
+        hipEventCreate(&c->members_up[0]) != hipSuccess || hipEventCreate(&c->members_up[1]) != hipSuccess) {
         delete c;
         return GT_EDEVICE;
     }
@@ -1383,6 +1447,8 @@ void gt_destroy(gt_ctx* ctx)
     ctx->pin_lloyd.release();
     if (ctx->ev0) (void)hipEventDestroy(ctx->ev0);
     if (ctx->ev1) (void)hipEventDestroy(ctx->ev1);
+    for (hipEvent_t e : ctx->members_up)
+        if (e) (void)hipEventDestroy(e);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
     delete ctx;
 }
@@ -2181,7 +2247,10 @@ int gt_build_graph_ex(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtyp
         // on the context's stream in one order.
         Buckets bk[2];
         BucketPlan plans[2];
-        for (int i = 0; i < 2; ++i) bk[i].members.swap(ctx->h_members[i]);   // reuse host memory across builds
+        for (int i = 0; i < 2; ++i) {
+            bk[i].members.swap(ctx->h_members[i]);   // reuse host memory across builds
+            bk[i].uploaded = ctx->members_up[i];
+        }
         std::vector<int32_t> cknn;
         const bool want_cknn = extras && extras->centroid_knn && extras->centroid_knn_k > 0;
         auto device_part = [&](int r) {
@@ -2193,8 +2262,12 @@ int gt_build_graph_ex(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtyp
         };
         std::future<void> host_job;   // declared after everything it references
         auto start_host = [&](int r) {
+            // the previous upload of these buckets' members (two rounds ago)
+            // has been read before the host half rewrites them
+            GT_HIP(hipEventSynchronize(bk[r & 1].uploaded));
             host_job = std::async(std::launch::async, [&, r] {
-                bucket_host(plans[r & 1], p.balance, bk[r & 1], ctx->h_bucket_of, ctx->h_key2, ctx->h_by_key);
+                bucket_host(plans[r & 1], p.balance, bk[r & 1], ctx->h_bucket_of, ctx->h_key2, ctx->h_by_key,
+                            ctx->h_bkt);
             });
         };
         device_part(0);
