@@ -57,6 +57,60 @@ __global__ void pad_i8_kernel(const T* __restrict__ src, int8_t* __restrict__ ds
     }
 }
 
+// One pass over integer-typed rows (D <= Dp <= 256): the float copy and the
+// int8 copy (minus shift: 128 for uint8, 0 for int8), both zero padded to
+// Dp, and both squared norms.  The norms are integers below 2^24, so they
+// are exact in float whatever the summation order.  2^lpr_log2 lanes per row
+// (at least Dp / 4), four columns per lane.
+template <typename T, bool VEC>
+__global__ void __launch_bounds__(256) prepare_int_kernel(const T* __restrict__ src, int64_t N, int D, int Dp,
+                                                          int shift, int lpr_log2, float* __restrict__ xf,
+                                                          float* __restrict__ nf, int8_t* __restrict__ x8,
+                                                          float* __restrict__ n8)
+{
+    const int64_t gt = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    const int64_t row = gt >> lpr_log2;
+    const int c0 = 4 * static_cast<int>(gt & ((1 << lpr_log2) - 1));
+    int sf = 0, s8 = 0;
+    if (row < N && c0 < Dp) {
+        int v[4];
+        if constexpr (VEC) {
+            // D % 4 == 0: the four columns are one aligned word, all in the row or all padding
+            uint32_t wv = 0;
+            if (c0 < D) wv = *reinterpret_cast<const uint32_t*>(src + row * D + c0);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const uint32_t b = (wv >> (8 * u)) & 0xffu;
+                v[u] = sizeof(T) == 1 && static_cast<T>(-1) < 0 ? static_cast<int>(static_cast<int8_t>(b))
+                                                                 : static_cast<int>(b);
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) v[u] = c0 + u < D ? static_cast<int>(src[row * D + c0 + u]) : 0;
+        }
+        uint32_t q = 0;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int qv = c0 + u < D ? v[u] - shift : 0;
+            sf += v[u] * v[u];
+            s8 += qv * qv;
+            q |= (static_cast<uint32_t>(qv) & 0xffu) << (8 * u);
+        }
+        *reinterpret_cast<float4*>(xf + row * Dp + c0) =
+            make_float4(static_cast<float>(v[0]), static_cast<float>(v[1]), static_cast<float>(v[2]),
+                        static_cast<float>(v[3]));
+        *reinterpret_cast<uint32_t*>(x8 + row * Dp + c0) = q;
+    }
+    for (int o = 1 << (lpr_log2 - 1); o > 0; o >>= 1) {
+        sf += __shfl_xor(sf, o);
+        s8 += __shfl_xor(s8, o);
+    }
+    if (row < N && c0 == 0) {
+        nf[row] = static_cast<float>(sf);
+        n8[row] = static_cast<float>(s8);
+    }
+}
+
 // int8 copy of float rows (centroids of an integer dataset): the value
 // minus the dataset's shift, rounded and clamped; padding stays 0.
 __global__ void quantize_i8_kernel(const float* __restrict__ src, int64_t N, int D, int Dp, int shift,
@@ -949,6 +1003,29 @@ void launch_pad_convert(const void* src, int dtype, float* dst, int64_t N, int D
         hipLaunchKernelGGL(pad_convert_kernel<uint8_t>, dim3(grid), dim3(256), 0, s, static_cast<const uint8_t*>(src), dst, N, D, Dp);
     else
         hipLaunchKernelGGL(pad_convert_kernel<int8_t>, dim3(grid), dim3(256), 0, s, static_cast<const int8_t*>(src), dst, N, D, Dp);
+    GT_HIP(hipGetLastError());
+}
+
+void launch_prepare_int(const void* src, int dtype, int64_t N, int D, int Dp, float* xf, float* nf, int8_t* x8,
+                        float* n8, hipStream_t s)
+{
+    GT_REQUIRE((dtype == 1 || dtype == 2) && D >= 1 && D <= Dp && Dp <= 256 && Dp % 4 == 0,
+               "integer rows of at most 256 columns");
+    if (N <= 0) return;
+    int lg = 0;
+    while ((1 << lg) < Dp / 4) ++lg;
+    const int64_t threads = N << lg;
+    const unsigned grid = static_cast<unsigned>((threads + 255) / 256);
+    const bool vec = D % 4 == 0 && (reinterpret_cast<uintptr_t>(src) & 3) == 0;
+    if (dtype == 1) {
+        const uint8_t* p = static_cast<const uint8_t*>(src);
+        if (vec) hipLaunchKernelGGL((prepare_int_kernel<uint8_t, true>), dim3(grid), dim3(256), 0, s, p, N, D, Dp, 128, lg, xf, nf, x8, n8);
+        else hipLaunchKernelGGL((prepare_int_kernel<uint8_t, false>), dim3(grid), dim3(256), 0, s, p, N, D, Dp, 128, lg, xf, nf, x8, n8);
+    } else {
+        const int8_t* p = static_cast<const int8_t*>(src);
+        if (vec) hipLaunchKernelGGL((prepare_int_kernel<int8_t, true>), dim3(grid), dim3(256), 0, s, p, N, D, Dp, 0, lg, xf, nf, x8, n8);
+        else hipLaunchKernelGGL((prepare_int_kernel<int8_t, false>), dim3(grid), dim3(256), 0, s, p, N, D, Dp, 0, lg, xf, nf, x8, n8);
+    }
     GT_HIP(hipGetLastError());
 }
 

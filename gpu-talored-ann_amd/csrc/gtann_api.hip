@@ -33,6 +33,8 @@ void launch_merge_partials(const int32_t* pids, const float* pd, int64_t nq, int
 void launch_pad_convert(const void* src, int dtype, float* dst, int64_t N, int D, int Dp, hipStream_t s);
 void launch_row_norms(const float* X, int64_t N, int Dp, float* norms, hipStream_t s);
 void launch_pad_i8(const void* src, int dtype, int8_t* dst, int64_t N, int D, int Dp, hipStream_t s);
+void launch_prepare_int(const void* src, int dtype, int64_t N, int D, int Dp, float* xf, float* nf, int8_t* x8,
+                        float* n8, hipStream_t s);
 void launch_row_norms_i8(const int8_t* X, int64_t N, int Dp, float* norms, hipStream_t s);
 void launch_quantize_i8(const float* src, int64_t N, int D, int Dp, int shift, int8_t* dst, hipStream_t s);
 void launch_row_norms_range(const float* X, int64_t N, int Dp, float* norms, int* part, int* out, hipStream_t s);
@@ -363,6 +365,26 @@ static DevMatrix prepare(Ctx& c, int slot_x, int slot_raw, int slot_norms, const
     m.Dp = Dp;
     const bool dev = is_device_ptr(X);
     const void* src = X;   // device copy of the caller's rows
+    if (with_i8 && (dtype == GT_DTYPE_U8 || dtype == GT_DTYPE_I8) && Dp <= 256) {
+        // integer rows: float copy, int8 copy and both norms in one pass
+        if (!dev) {
+            void* raw = c.c->ws[slot_raw].ensure(static_cast<size_t>(N) * D * es);
+            c.h2d(raw, X, static_cast<size_t>(N) * D * es);
+            src = raw;
+        }
+        float* xp = c.ws<float>(slot_x, static_cast<size_t>(N) * Dp);
+        float* nrm = c.ws<float>(slot_norms, static_cast<size_t>(N));
+        int8_t* x8 = c.ws<int8_t>(W_X8, static_cast<size_t>(N) * Dp);
+        float* n8 = c.ws<float>(W_NORMS8, static_cast<size_t>(N));
+        launch_prepare_int(src, dtype, N, D, Dp, xp, nrm, x8, n8, c.s);
+        m.data = xp;
+        m.norms = nrm;
+        m.Dp8 = Dp;
+        m.shift = dtype == GT_DTYPE_U8 ? 128 : 0;
+        m.data8 = x8;
+        m.norms8 = n8;
+        return m;
+    }
     if (dev && dtype == GT_DTYPE_F32 && D == Dp && (reinterpret_cast<uintptr_t>(X) & 15) == 0) {
         m.data = static_cast<const float*>(X);
     } else {
