@@ -43,25 +43,6 @@ __device__ __forceinline__ int lower_bound_lds(const float* ad, const int32_t* a
     return lo;
 }
 
-// 64-lane bitonic sort, ascending in (d, i).
-__device__ __forceinline__ void wave_bitonic_sort(float& d, int32_t& i, int lane)
-{
-#pragma unroll
-    for (int k = 2; k <= 64; k <<= 1) {
-#pragma unroll
-        for (int s = k >> 1; s > 0; s >>= 1) {
-            const float od = __shfl_xor(d, s);
-            const int32_t oi = __shfl_xor(i, s);
-            const bool ascending = (lane & k) == 0;
-            const bool lower = (lane & s) == 0;
-            const bool other_less = key_less(od, oi, d, i);
-            const bool other_greater = key_less(d, i, od, oi);
-            const bool take = (lower == ascending) ? other_less : other_greater;
-            if (take) { d = od; i = oi; }
-        }
-    }
-}
-
 // Per-block candidate buffers and merge staging, shared by both kernels.
 struct KnnLists {
     // packed (key, id) of candidates awaiting a merge (never the query
@@ -758,14 +739,6 @@ __device__ __forceinline__ void i8_filter_tile(KnnLists& L, const KnnArgs& a, co
         tile_append<METRIC, false>(L, a, dot, tn, tr, tbase, w, lane, h, qlocal, qvalid, qn, st);
         lo = i8_pass_floor<METRIC>(st.thr, qn);
     }
-}
-
-__device__ __forceinline__ floatx16 to_float(const intx16& v)
-{
-    floatx16 f;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) f[r] = static_cast<float>(v[r]);
-    return f;
 }
 
 // Three waves per SIMD for the list launches (at most 168 VGPRs), two for
