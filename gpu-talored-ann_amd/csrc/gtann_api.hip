@@ -782,13 +782,6 @@ static void csr_from_assignment_keyed(const std::vector<int32_t>& bucket_of, con
     counting_sort_kv(bkt.data(), by_key.data(), N, C, b.members.data(), nullptr, nullptr, b.offsets);
 }
 
-static void csr_from_assignment(const std::vector<int32_t>& bucket_of, int64_t C, Buckets& b)
-{
-    const int64_t N = static_cast<int64_t>(bucket_of.size());
-    b.members.resize(static_cast<size_t>(N));
-    counting_sort(nullptr, N, bucket_of.data(), C, b.members.data(), b.offsets);
-}
-
 // GTANN_LLOYD_HOST=1 groups the Lloyd samples on the host (download, counting
 // sort, upload) instead of on the device (comparisons; the same CSR)
 static bool lloyd_host_csr()

@@ -159,14 +159,6 @@ void mkdirs(const std::string& path)
     if (stat(path.c_str(), &st) != 0 || !S_ISDIR(st.st_mode)) throw Exit{1, "cannot create directory " + path};
 }
 
-std::string abs_path(const std::string& p)
-{
-    if (!p.empty() && p[0] == '/') return p;
-    char buf[4096];
-    if (!getcwd(buf, sizeof(buf))) return p;
-    return std::string(buf) + "/" + p;
-}
-
 std::string ext_of(const std::string& p)
 {
     const size_t dot = p.find_last_of('.');
