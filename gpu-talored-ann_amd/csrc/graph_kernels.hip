@@ -203,21 +203,25 @@ __global__ void __launch_bounds__(256) sanitize_kernel(const int32_t* __restrict
 // (src/prune_windowed_core.hpp:189-232); output = first K valid entries in
 // (count, rank) order (src/prune_windowed_core.hpp:238-263).
 constexpr int kPruneMaxM = 128;
-constexpr int kPruneDepth = 16;   // neighbour rows in flight per wave
+constexpr int kPruneDepth = 8;    // neighbour rows in flight per wave
 
 // One wave per point a.  Row a's ids go into an LDS hash table of 4-slot
 // buckets (2*MM buckets; a full bucket spills into the next one, no
 // wrap-around; a repeated id takes one slot per occurrence); each lane
 // remembers the slots of its own entries.  Every neighbour row kAD < M-1 is
 // then streamed through, kPruneDepth rows in flight: a lane whose id matches
-// a slot (one 16-byte read per bucket probed) tags that slot with kAD + 1 (an
-// id repeated in the neighbour row tags the same slot again, so each
-// (kAD, kAB) pair counts once), and the lane owning rank kAB > kAD counts the
-// row when its slot carries the tag -- src/prune_windowed_core.hpp:177-232.
-// The counts stay in registers; the neighbour row's id is wave-uniform, so
-// its address is scalar work.  Finally the first K valid ranks by
-// (count, rank) are written (src/prune_windowed_core.hpp:234-263).
-// E = list halves of 64.
+// a slot (one 16-byte read per bucket probed) sets bit kAD - kd0 of that
+// slot's tag word (kd0: the first row of the group of kPruneDepth rows; an id
+// repeated in the neighbour row sets the same bit, so each (kAD, kAB) pair
+// counts once).  After each group the lane owning rank kAB counts the bits of
+// rows kAD < kAB in its slot's word and clears it -- one tag read per group
+// instead of one per row, and no wait between a row's tag writes and the
+// next row's bucket reads (src/prune_windowed_core.hpp:177-232).  Only slots
+// that hold an id of row a are ever tagged, and each belongs to one lane, so
+// the clears leave the whole tag array zero.  The counts stay in registers;
+// the neighbour row's id is read from row a's registers by readlane, so its
+// address is scalar work.  Finally the first K valid ranks by (count, rank)
+// are written (src/prune_windowed_core.hpp:234-263).  E = list halves of 64.
 __device__ __forceinline__ uint32_t prune_hash(int32_t v, uint32_t mask)
 {
     return ((static_cast<uint32_t>(v) * 0x9E3779B1u) >> 15) & mask;
@@ -234,10 +238,10 @@ __global__ void __launch_bounds__(256) cagra_prune_kernel(const int32_t* __restr
     constexpr int SLOTS = 4 * BK;
     constexpr uint32_t mask = NBK - 1;
     constexpr uint32_t kEmpty = 0xffffffffu;
+    constexpr int RG = 2 / E;                 // bucket reads issued together (rows)
+    static_assert(kPruneDepth <= 32 && kPruneDepth % RG == 0, "tag bits per group");
     __shared__ __align__(16) uint32_t tab[4][SLOTS];
-    __shared__ uint32_t tag[4][SLOTS + 64];   // + one scratch word per lane for misses
-    __shared__ __align__(16) uint32_t skey[4][MM];
-    __shared__ int32_t sA[4][MM];
+    __shared__ uint32_t tag[4][SLOTS + 64];   // + one never-tagged word per lane (invalid entries)
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int64_t a = static_cast<int64_t>(blockIdx.x) * 4 + w;
     if (a >= N) return;
@@ -251,7 +255,6 @@ __global__ void __launch_bounds__(256) cagra_prune_kernel(const int32_t* __restr
         const int k = lane + 64 * e;
         col[e] = k < M ? k : M - 1;
         A[e] = k < M ? G[a * M + k] : -1;
-        sA[w][k] = A[e];
     }
     wave_sync();
     // insertion; every entry ends up at most dmax buckets past its home
@@ -259,7 +262,7 @@ __global__ void __launch_bounds__(256) cagra_prune_kernel(const int32_t* __restr
     uint32_t disp = 0;
 #pragma unroll
     for (int e = 0; e < E; ++e) {
-        slot[e] = SLOTS + lane;   // scratch word: an invalid entry counts nothing that is used
+        slot[e] = SLOTS + lane;
         if (A[e] >= 0) {
             const uint32_t home = prune_hash(A[e], mask);
             uint32_t h = 4 * home;
@@ -278,7 +281,12 @@ __global__ void __launch_bounds__(256) cagra_prune_kernel(const int32_t* __restr
     int32_t ring[kPruneDepth][E];
     bool rok[kPruneDepth];
     auto fetch = [&](int kAD, int32_t (&b)[E], bool& ok) {
-        const int32_t d = __builtin_amdgcn_readfirstlane(kAD < M - 1 ? sA[w][kAD] : -1);
+        int32_t d = -1;
+        if (kAD < M - 1) {
+#pragma unroll
+            for (int e = 0; e < E; ++e)
+                if ((kAD >> 6) == e) d = __builtin_amdgcn_readlane(A[e], kAD & 63);
+        }
         ok = d >= 0 && d < N;
         const int32_t* row = G + (ok ? static_cast<int64_t>(d) : int64_t(0)) * M;
 #pragma unroll
@@ -287,47 +295,82 @@ __global__ void __launch_bounds__(256) cagra_prune_kernel(const int32_t* __restr
     uint32_t c[E];
 #pragma unroll
     for (int e = 0; e < E; ++e) c[e] = 0;
-    // every occurrence of v in row a lies within dmax buckets of v's home:
-    // a fixed, wave-uniform number of bucket reads; a miss writes the lane's
-    // scratch word, so the common case has no divergent branch
-    auto probe = [&](int kd, const int32_t (&b)[E], bool ok) {
-        if (!ok) return;
-        const uint32_t t = static_cast<uint32_t>(kd + 1);
+    // bit `bit` on every slot of bucket x (at base) holding v
+    auto tag_bucket = [&](const uint4& x, uint32_t v, bool valid, uint32_t base, uint32_t bit) {
+        const bool m0 = valid & (x.x == v), m1 = valid & (x.y == v), m2 = valid & (x.z == v),
+                   m3 = valid & (x.w == v);
+        const uint32_t j = m0 ? 0u : m1 ? 1u : m2 ? 2u : 3u;
+        if (m0 | m1 | m2 | m3) atomicOr(&tag[w][base + j], bit);
+        // an id of row a repeated inside one bucket: tag the other copies
+        const bool more = (m0 & (m1 | m2 | m3)) | (m1 & (m2 | m3)) | (m2 & m3);
+        if (__ballot(more)) {
+            if (m1 && j < 1) atomicOr(&tag[w][base + 1], bit);
+            if (m2 && j < 2) atomicOr(&tag[w][base + 2], bit);
+            if (m3 && j < 3) atomicOr(&tag[w][base + 3], bit);
+        }
+    };
+    // rows kd0 .. kd0 + kPruneDepth - 1 of the ring (row kd0 + r in slot r);
+    // each slot is refilled with row kd0 + r + kPruneDepth once probed
+    auto probe_group = [&](int kd0) {
+        if (dmax == 0) {
+            // every entry sits in its home bucket: one read per id, RG rows
+            // of reads issued before any is used
 #pragma unroll
-        for (int e = 0; e < E; ++e) {
-            const uint32_t v = static_cast<uint32_t>(b[e]);
-            const bool valid = lane + 64 * e < M && b[e] >= 0;
-            const uint32_t home = prune_hash(b[e], mask);
-            for (uint32_t s = 0; s <= dmax; ++s) {
-                const uint32_t base = 4 * (home + s);
-                const uint4 x = *reinterpret_cast<const uint4*>(&tab[w][base]);
-                const bool m0 = valid & (x.x == v), m1 = valid & (x.y == v), m2 = valid & (x.z == v),
-                           m3 = valid & (x.w == v);
-                const uint32_t j = m0 ? 0u : m1 ? 1u : m2 ? 2u : 3u;
-                const bool any = m0 | m1 | m2 | m3;
-                tag[w][any ? base + j : static_cast<uint32_t>(SLOTS + lane)] = t;
-                // an id of row a repeated inside one bucket: tag the other copies
-                const bool more = (m0 & (m1 | m2 | m3)) | (m1 & (m2 | m3)) | (m2 & m3);
-                if (__ballot(more)) {
-                    if (m1 && j < 1) tag[w][base + 1] = t;
-                    if (m2 && j < 2) tag[w][base + 2] = t;
-                    if (m3 && j < 3) tag[w][base + 3] = t;
+            for (int g = 0; g < kPruneDepth; g += RG) {
+                uint4 x[RG][E];
+                uint32_t base[RG][E];
+#pragma unroll
+                for (int r = 0; r < RG; ++r)
+#pragma unroll
+                    for (int e = 0; e < E; ++e) {
+                        base[r][e] = 4 * prune_hash(ring[g + r][e], mask);
+                        x[r][e] = *reinterpret_cast<const uint4*>(&tab[w][base[r][e]]);
+                    }
+#pragma unroll
+                for (int r = 0; r < RG; ++r) {
+                    if (!rok[g + r]) continue;
+#pragma unroll
+                    for (int e = 0; e < E; ++e)
+                        tag_bucket(x[r][e], static_cast<uint32_t>(ring[g + r][e]),
+                                   lane + 64 * e < M && ring[g + r][e] >= 0, base[r][e], 1u << (g + r));
                 }
+#pragma unroll
+                for (int r = 0; r < RG; ++r) fetch(kd0 + g + r + kPruneDepth, ring[g + r], rok[g + r]);
+            }
+        } else {
+            // every occurrence of v in row a lies within dmax buckets of v's
+            // home: a fixed, wave-uniform number of bucket reads
+#pragma unroll
+            for (int r = 0; r < kPruneDepth; ++r) {
+                if (rok[r]) {
+#pragma unroll
+                    for (int e = 0; e < E; ++e) {
+                        const uint32_t v = static_cast<uint32_t>(ring[r][e]);
+                        const bool valid = lane + 64 * e < M && ring[r][e] >= 0;
+                        const uint32_t home = prune_hash(ring[r][e], mask);
+                        for (uint32_t s = 0; s <= dmax; ++s) {
+                            const uint32_t base = 4 * (home + s);
+                            tag_bucket(*reinterpret_cast<const uint4*>(&tab[w][base]), v, valid, base, 1u << r);
+                        }
+                    }
+                }
+                fetch(kd0 + r + kPruneDepth, ring[r], rok[r]);
             }
         }
         wave_sync();
 #pragma unroll
-        for (int e = 0; e < E; ++e) c[e] += (lane + 64 * e > kd && tag[w][slot[e]] == t) ? 1u : 0u;
+        for (int e = 0; e < E; ++e) {
+            const uint32_t t = tag[w][slot[e]];
+            const int m = lane + 64 * e - kd0;   // rows kd0 + r < kAB count
+            const uint32_t below = m <= 0 ? 0u : m >= 32 ? 0xffffffffu : (1u << m) - 1u;
+            c[e] += static_cast<uint32_t>(__popc(t & below));
+            tag[w][slot[e]] = 0u;
+        }
+        wave_sync();
     };
 #pragma unroll
     for (int r = 0; r < kPruneDepth; ++r) fetch(r, ring[r], rok[r]);
-    for (int kd = 0; kd < M - 1; kd += kPruneDepth) {
-#pragma unroll
-        for (int r = 0; r < kPruneDepth; ++r) {
-            if (kd + r < M - 1) probe(kd + r, ring[r], rok[r]);
-            fetch(kd + r + kPruneDepth, ring[r], rok[r]);
-        }
-    }
+    for (int kd = 0; kd < M - 1; kd += kPruneDepth) probe_group(kd);
 
     int nvalid = 0;
 #pragma unroll
@@ -337,12 +380,15 @@ __global__ void __launch_bounds__(256) cagra_prune_kernel(const int32_t* __restr
         return;
     }
     // position = valid entries before this one in (count, rank) order; one
-    // key per entry, count << 8 | rank (counts < 128), invalid = all ones
+    // key per entry, count << 8 | rank (counts < 128), invalid = all ones,
+    // kept in the hash table's LDS (no longer read); fewer LDS bytes per
+    // block let one more block share a CU
+    uint32_t* skey = tab[w];
     uint32_t key[E];
 #pragma unroll
     for (int e = 0; e < E; ++e) {
         key[e] = A[e] >= 0 ? (c[e] << 8) | static_cast<uint32_t>(lane + 64 * e) : 0xffffffffu;
-        skey[w][lane + 64 * e] = key[e];
+        skey[lane + 64 * e] = key[e];
     }
     wave_sync();
     int pos[E];
@@ -350,7 +396,7 @@ __global__ void __launch_bounds__(256) cagra_prune_kernel(const int32_t* __restr
     for (int e = 0; e < E; ++e) pos[e] = 0;
 #pragma unroll 4
     for (int q4 = 0; q4 < MM / 4; ++q4) {
-        const uint4 kq = *reinterpret_cast<const uint4*>(&skey[w][4 * q4]);
+        const uint4 kq = *reinterpret_cast<const uint4*>(&skey[4 * q4]);
 #pragma unroll
         for (int e = 0; e < E; ++e)
             pos[e] += (kq.x < key[e] ? 1 : 0) + (kq.y < key[e] ? 1 : 0) + (kq.z < key[e] ? 1 : 0) +

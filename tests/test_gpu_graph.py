@@ -55,6 +55,24 @@ def test_prune_random(ctx, N, M, K, pad, dup):
     np.testing.assert_array_equal(ctx.cagra_prune(G, K), ref)
 
 
+@pytest.mark.parametrize("M,K,nbk", [(64, 32, 128), (128, 64, 256)])
+def test_prune_spilled_buckets(ctx, M, K, nbk):
+    # rows drawn from ids that share a handful of home buckets of the
+    # kernel's per-row hash table (multiplicative hash, bits 15.. of
+    # v * 0x9E3779B1 mod 2^32): full buckets spill into the next ones, so
+    # lookups probe several buckets (the path random rows rarely reach)
+    rng = np.random.default_rng(M)
+    N = 40000
+    v = np.arange(N, dtype=np.uint64)
+    home = ((v * 0x9E3779B1) % (1 << 32) >> 15) & (nbk - 1)
+    pool = np.flatnonzero(home < 3)
+    G = rng.choice(pool, size=(N, M)).astype(np.int32)
+    G[::5, 1] = G[::5, 0]                        # repeated ids
+    ref, rc, _ = O.cagra_prune(G, K)
+    assert rc == 0
+    np.testing.assert_array_equal(ctx.cagra_prune(G, K), ref)
+
+
 def test_prune_few_candidates_error(ctx):
     import gtann
     G = np.array([[1, -1, -1], [0, 2, -1], [0, 1, -1]], np.int32)
