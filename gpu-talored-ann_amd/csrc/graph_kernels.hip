@@ -750,7 +750,7 @@ __global__ void __launch_bounds__(kRevBinThreads) rev_bin_count_kernel(const uin
                                                                        uint32_t* __restrict__ hist,
                                                                        int* __restrict__ err)
 {
-    __shared__ uint32_t h[kRevMaxBins];
+    extern __shared__ uint32_t h[];   // nbins counters
     for (int i = threadIdx.x; i < nbins; i += kRevBinThreads) h[i] = 0u;
     __syncthreads();
     const int64_t e0 = static_cast<int64_t>(blockIdx.x) * chunk, e1 = min(E, e0 + chunk);
@@ -780,7 +780,7 @@ __global__ void __launch_bounds__(kRevBinThreads) rev_bin_scatter_kernel(const u
                                                                          int nbins, const uint32_t* __restrict__ offs,
                                                                          unsigned long long* __restrict__ part)
 {
-    __shared__ uint32_t cur[kRevMaxBins];
+    extern __shared__ uint32_t cur[];   // nbins cursors
     for (int i = threadIdx.x; i < nbins; i += kRevBinThreads)
         cur[i] = offs[static_cast<int64_t>(i) * gridDim.x + blockIdx.x];
     __syncthreads();
@@ -1415,11 +1415,13 @@ void launch_rev_binned(const uint32_t* fwd, int64_t N, int K, uint32_t* hist, ui
     const int nbins = static_cast<int>(ceil_div(N, int64_t(1) << shift));
     const int nblk = rev_bin_blocks(E);
     const int64_t chunk = ceil_div(E, nblk);
-    hipLaunchKernelGGL(rev_bin_count_kernel, dim3(nblk), dim3(kRevBinThreads), 0, s, fwd, E, N, chunk, shift, nbins,
-                       hist, err);
+    // LDS of (1)-(3) sized to the bins in use, so that several blocks share a CU
+    const size_t lds_bins = static_cast<size_t>(nbins) * sizeof(uint32_t);
+    hipLaunchKernelGGL(rev_bin_count_kernel, dim3(nblk), dim3(kRevBinThreads), lds_bins, s, fwd, E, N, chunk, shift,
+                       nbins, hist, err);
     launch_exclusive_scan(hist, static_cast<int64_t>(nbins) * nblk, offs, sums, s);
-    hipLaunchKernelGGL(rev_bin_scatter_kernel, dim3(nblk), dim3(kRevBinThreads), 0, s, fwd, E, N, K, chunk, shift,
-                       nbins, offs, part);
+    hipLaunchKernelGGL(rev_bin_scatter_kernel, dim3(nblk), dim3(kRevBinThreads), lds_bins, s, fwd, E, N, K, chunk,
+                       shift, nbins, offs, part);
     const size_t lds = (2 * (size_t(1) << shift) + 1) * sizeof(uint32_t);
     hipLaunchKernelGGL(rev_bin_merge_kernel, dim3(nbins), dim3(kRevBinThreads), lds, s, fwd, N, K, shift, nblk, offs,
                        part, grouped, out);
