@@ -238,8 +238,7 @@ __global__ void __launch_bounds__(256) cagra_prune_kernel(const int32_t* __restr
     constexpr int SLOTS = 4 * BK;
     constexpr uint32_t mask = NBK - 1;
     constexpr uint32_t kEmpty = 0xffffffffu;
-    constexpr int RG = 2 / E;                 // bucket reads issued together (rows)
-    static_assert(kPruneDepth <= 32 && kPruneDepth % RG == 0, "tag bits per group");
+    static_assert(kPruneDepth <= 32, "one tag bit per row of a group");
     __shared__ __align__(16) uint32_t tab[4][SLOTS];
     __shared__ uint32_t tag[4][SLOTS + 64];   // + one never-tagged word per lane (invalid entries)
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -313,29 +312,18 @@ __global__ void __launch_bounds__(256) cagra_prune_kernel(const int32_t* __restr
     // each slot is refilled with row kd0 + r + kPruneDepth once probed
     auto probe_group = [&](int kd0) {
         if (dmax == 0) {
-            // every entry sits in its home bucket: one read per id, RG rows
-            // of reads issued before any is used
+            // every entry sits in its home bucket: one bucket read per id
 #pragma unroll
-            for (int g = 0; g < kPruneDepth; g += RG) {
-                uint4 x[RG][E];
-                uint32_t base[RG][E];
+            for (int r = 0; r < kPruneDepth; ++r) {
 #pragma unroll
-                for (int r = 0; r < RG; ++r)
-#pragma unroll
-                    for (int e = 0; e < E; ++e) {
-                        base[r][e] = 4 * prune_hash(ring[g + r][e], mask);
-                        x[r][e] = *reinterpret_cast<const uint4*>(&tab[w][base[r][e]]);
-                    }
-#pragma unroll
-                for (int r = 0; r < RG; ++r) {
-                    if (!rok[g + r]) continue;
-#pragma unroll
-                    for (int e = 0; e < E; ++e)
-                        tag_bucket(x[r][e], static_cast<uint32_t>(ring[g + r][e]),
-                                   lane + 64 * e < M && ring[g + r][e] >= 0, base[r][e], 1u << (g + r));
+                for (int e = 0; e < E; ++e) {
+                    const uint32_t base = 4 * prune_hash(ring[r][e], mask);
+                    const uint4 x = *reinterpret_cast<const uint4*>(&tab[w][base]);
+                    if (rok[r])
+                        tag_bucket(x, static_cast<uint32_t>(ring[r][e]), lane + 64 * e < M && ring[r][e] >= 0, base,
+                                   1u << r);
                 }
-#pragma unroll
-                for (int r = 0; r < RG; ++r) fetch(kd0 + g + r + kPruneDepth, ring[g + r], rok[g + r]);
+                fetch(kd0 + r + kPruneDepth, ring[r], rok[r]);
             }
         } else {
             // every occurrence of v in row a lies within dmax buckets of v's
