@@ -211,14 +211,15 @@ constexpr int kPruneDepth = 8;    // neighbour rows in flight per wave
 // remembers the slots of its own entries.  Every neighbour row kAD < M-1 is
 // then streamed through, kPruneDepth rows in flight: a lane whose id matches
 // a slot (one 16-byte read per bucket probed) sets bit kAD - kd0 of that
-// slot's tag word (kd0: the first row of the group of kPruneDepth rows; an id
-// repeated in the neighbour row sets the same bit, so each (kAD, kAB) pair
-// counts once).  After each group the lane owning rank kAB counts the bits of
-// rows kAD < kAB in its slot's word and clears it -- one tag read per group
-// instead of one per row, and no wait between a row's tag writes and the
-// next row's bucket reads (src/prune_windowed_core.hpp:177-232).  Only slots
-// that hold an id of row a are ever tagged, and each belongs to one lane, so
-// the clears leave the whole tag array zero.  The counts stay in registers;
+// slot's 8-bit tag (kd0: the first row of the group of kPruneDepth rows; an
+// id repeated in the neighbour row sets the same bit, so each (kAD, kAB) pair
+// counts once); a bucket's four tags share one word.  After each group the
+// lane owning rank kAB counts the bits of rows kAD < kAB in its slot's tag,
+// and once every lane has read, the owners clear their words -- one tag read
+// per group instead of one per row, and no wait between a row's tag writes
+// and the next row's bucket reads (src/prune_windowed_core.hpp:177-232).
+// Only slots that hold an id of row a are ever tagged, and each belongs to
+// one lane, so the clears leave the whole tag array zero.  The counts stay in registers;
 // the neighbour row's id is read from row a's registers by readlane, so its
 // address is scalar work.  Finally the first K valid ranks by (count, rank)
 // are written (src/prune_windowed_core.hpp:234-263).  E = list halves of 64.
@@ -238,15 +239,16 @@ __global__ void __launch_bounds__(256) cagra_prune_kernel(const int32_t* __restr
     constexpr int SLOTS = 4 * BK;
     constexpr uint32_t mask = NBK - 1;
     constexpr uint32_t kEmpty = 0xffffffffu;
-    static_assert(kPruneDepth <= 32, "one tag bit per row of a group");
+    static_assert(kPruneDepth <= 8, "one tag bit per row of a group, 8-bit tags");
+    constexpr int TAGW = BK + 16;             // + 64 never-tagged tags (invalid entries)
     __shared__ __align__(16) uint32_t tab[4][SLOTS];
-    __shared__ uint32_t tag[4][SLOTS + 64];   // + one never-tagged word per lane (invalid entries)
+    __shared__ uint32_t tag[4][TAGW];         // slot s: bits 8*(s%4).. of word s/4
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int64_t a = static_cast<int64_t>(blockIdx.x) * 4 + w;
     if (a >= N) return;
 
     for (int s = lane; s < SLOTS; s += 64) tab[w][s] = kEmpty;
-    for (int s = lane; s < SLOTS + 64; s += 64) tag[w][s] = 0u;
+    for (int s = lane; s < TAGW; s += 64) tag[w][s] = 0u;
     int32_t A[E];
     int col[E];
 #pragma unroll
@@ -294,18 +296,19 @@ __global__ void __launch_bounds__(256) cagra_prune_kernel(const int32_t* __restr
     uint32_t c[E];
 #pragma unroll
     for (int e = 0; e < E; ++e) c[e] = 0;
-    // bit `bit` on every slot of bucket x (at base) holding v
+    // bit `bit` of the tag of every slot of bucket x (at base) holding v
     auto tag_bucket = [&](const uint4& x, uint32_t v, bool valid, uint32_t base, uint32_t bit) {
         const bool m0 = valid & (x.x == v), m1 = valid & (x.y == v), m2 = valid & (x.z == v),
                    m3 = valid & (x.w == v);
         const uint32_t j = m0 ? 0u : m1 ? 1u : m2 ? 2u : 3u;
-        if (m0 | m1 | m2 | m3) atomicOr(&tag[w][base + j], bit);
+        uint32_t* tw = &tag[w][base / 4];
+        if (m0 | m1 | m2 | m3) atomicOr(tw, bit << (8 * j));
         // an id of row a repeated inside one bucket: tag the other copies
         const bool more = (m0 & (m1 | m2 | m3)) | (m1 & (m2 | m3)) | (m2 & m3);
         if (__ballot(more)) {
-            if (m1 && j < 1) atomicOr(&tag[w][base + 1], bit);
-            if (m2 && j < 2) atomicOr(&tag[w][base + 2], bit);
-            if (m3 && j < 3) atomicOr(&tag[w][base + 3], bit);
+            const uint32_t rest = ((m1 && j < 1) ? bit << 8 : 0u) | ((m2 && j < 2) ? bit << 16 : 0u) |
+                                  ((m3 && j < 3) ? bit << 24 : 0u);
+            if (rest) atomicOr(tw, rest);
         }
     };
     // rows kd0 .. kd0 + kPruneDepth - 1 of the ring (row kd0 + r in slot r);
@@ -346,13 +349,17 @@ __global__ void __launch_bounds__(256) cagra_prune_kernel(const int32_t* __restr
             }
         }
         wave_sync();
+        uint32_t t[E];
+#pragma unroll
+        for (int e = 0; e < E; ++e) t[e] = tag[w][slot[e] / 4];
+        wave_sync();   // every tag word read before any is cleared
 #pragma unroll
         for (int e = 0; e < E; ++e) {
-            const uint32_t t = tag[w][slot[e]];
+            const uint32_t mine = (t[e] >> (8 * (slot[e] % 4))) & 0xffu;
             const int m = lane + 64 * e - kd0;   // rows kd0 + r < kAB count
-            const uint32_t below = m <= 0 ? 0u : m >= 32 ? 0xffffffffu : (1u << m) - 1u;
-            c[e] += static_cast<uint32_t>(__popc(t & below));
-            tag[w][slot[e]] = 0u;
+            const uint32_t below = m <= 0 ? 0u : m >= 8 ? 0xffu : (1u << m) - 1u;
+            c[e] += static_cast<uint32_t>(__popc(mine & below));
+            tag[w][slot[e] / 4] = 0u;
         }
         wave_sync();
     };
