@@ -1438,7 +1438,11 @@ int gt_create(int device, gt_ctx** out)
     gt_ctx* c = new (std::nothrow) gt_ctx();
     if (!c) return GT_ENOMEM;
     c->device = device;
-    if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess ||
+    // A blocking stream: every call's work is ordered after work already
+    // queued on the device's legacy null stream (PyTorch's default stream),
+    // so a device buffer produced there asynchronously is complete before
+    // the library reads it.
+    if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&c->stream, hipStreamDefault) != hipSuccess ||
         hipEventCreate(&c->ev0) != hipSuccess || hipEventCreate(&c->ev1) != hipSuccess ||
         hipEventCreate(&c->members_up[0]) != hipSuccess || hipEventCreate(&c->members_up[1]) != hipSuccess) {
         delete c;

@@ -80,12 +80,33 @@ class SearchStats(C.Structure):
 _lib = None
 
 
+def _torch_hip_runtime():
+    """Path of the HIP runtime bundled with PyTorch-ROCm, or None."""
+    import importlib.util
+    spec = importlib.util.find_spec("torch")
+    if spec is None or not spec.submodule_search_locations:
+        return None
+    path = os.path.join(list(spec.submodule_search_locations)[0], "lib", "libamdhip64.so")
+    return path if os.path.exists(path) else None
+
+
 def lib():
-    """Loads libgtann.so; raises if it has not been built."""
+    """Loads libgtann.so; raises if it has not been built.
+
+    One HIP runtime per process: PyTorch-ROCm ships its own libamdhip64
+    (soname libamdhip64.so.7, the same as /opt/rocm's) and asks for it by a
+    different name, so a process that loaded /opt/rocm's runtime through this
+    library first would get a second runtime from torch, which cannot acquire
+    the GPU.  When torch is installed its runtime is loaded first (without
+    importing torch), and libgtann.so binds to it; with torch imported
+    earlier this is the runtime already in the process."""
     global _lib
     if _lib is None:
         if not os.path.exists(LIB_PATH):
             raise RuntimeError(f"HIP library missing: {LIB_PATH} (run __graft_entry__.build())")
+        rt = _torch_hip_runtime()
+        if rt is not None:
+            C.CDLL(rt, mode=C.RTLD_GLOBAL)
         L = C.CDLL(LIB_PATH)
         vp, i64, i32 = C.c_void_p, C.c_int64, C.c_int32
         L.gt_create.argtypes = [C.c_int, C.POINTER(vp)]

@@ -8,6 +8,13 @@
  * Calls are synchronous on the context's stream.  One context per host
  * thread; distinct contexts may be used concurrently.
  *
+ * Ordering of device buffers: the context's stream is a blocking stream, so
+ * a call's reads come after all work queued before the call on the device's
+ * legacy null (default) stream -- the stream PyTorch and most HIP callers
+ * use by default.  A caller that produces an input on another non-blocking
+ * stream must synchronise that stream (or the device) before the call.
+ * Every call has finished writing its outputs when it returns.
+ *
  * Return value: GT_OK (0) or a negative error code; gt_last_error() gives
  * the message.  No C++ exception crosses this boundary.
  *

@@ -31,22 +31,32 @@ How each oracle function is pinned (what checks it besides itself):
 * ``reverse_merge`` / ``merge_row`` -- src/edge_chunk_accumulator.hpp:235-284,
   471-494.  Pinned against the reference header (``ref_reverse_merge``) and
   its truncation KAT (test_edge_chunk_accumulator.cpp:185-220).
-* ``refine_2hop`` -- src/bucket.cu:4754-4850.  Pinned by invariants: on exact
-  kNN input it is a fixed point; its output is never worse (elementwise
-  distance) than its input; on a table whose rows are all the same bucket's
-  members it equals the brute-force restriction.
+* ``refine_2hop`` -- src/bucket.cu:4754-4850.  Pinned by a hand-traced known
+  answer on eight 2-D integer points (tests/test_oracle.py, REFINE_KAT_*)
+  that a no-op, an S cutoff off by one on either the hop or the column
+  index, ``<=`` in place of ``<`` against the row's M-th distance, and a
+  missing dedup against the row each fail; by the two-hop property on random
+  integer tables (every 2-hop candidate is in the new row or not below its
+  last distance; every new entry comes from the old row or the candidates,
+  with its exact distance); by the fixed point on exact kNN input and by
+  monotone distances.
 * ``translate`` -- src/translate_graph_ids.hpp:75.  Pinned against the
   reference header (``ref_translate``).
 * ``prune_occlusion`` -- bd/prune.py:8-83.  Pinned by a hand-computed 1-D
-  example; the tie order of np.argsort and float32 summation order of the
-  reference are "parity unpinned" (only an import would pin them), so tests
-  use integer data without distance ties.
-* ``reverse_insert`` -- bd/build_bucket.py:473-543.  Pinned by a hand-computed
-  1-D known answer, by the fixed point "an exact kNN table with distinct
-  distances does not change", and by the characterisation of each new row
-  as the M smallest of (row, surviving offers) -- every offer left out is
-  not below the row's last key.  torch.topk's order among equal distances is
-  "parity unpinned"; the oracle orders ties by id.
+  example and bit for bit against the reference's own ``prune_graph``
+  (imported in the build container by tests/golden/make_golden_py.py;
+  fixtures in tests/golden/pyref_golden.npz): integer cases with distinct
+  candidate distances (one on a coarse 2-D grid where d(u,z) == d(v,z) is
+  frequent, so ``<`` is pinned) and float cases at least 1e-3 relative from
+  every tie.  np.argsort's order among equal distances and float32 summation
+  order on near-ties stay "parity unpinned"; the oracle orders ties by column.
+* ``reverse_insert`` -- bd/build_bucket.py:473-543.  Pinned bit for bit
+  against the reference's own ``_apply_reverse_edges`` (same fixture file:
+  tie-free tables, padded rows), by a hand-computed 1-D known answer, by the
+  fixed point "an exact kNN table with distinct distances does not change",
+  and by the characterisation of each new row as the M smallest of (row,
+  surviving offers).  torch.topk's order among equal distances is "parity
+  unpinned"; the oracle orders ties by id.
 * ``search`` -- bd/search.py:20-90 (graph_search_single).  Pinned by two
   hand-traced known answers (a tie at the ef-th distance is still expanded,
   ``>`` not ``>=``; a closer point replaces the FIRST slot holding the

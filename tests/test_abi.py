@@ -60,3 +60,15 @@ def test_null_context_is_rejected():
     d = np.zeros((4, 2), np.float32)
     rc = lib.gt_knn_exact(None, X.ctypes.data, 4, 8, 0, 0, None, 4, 2, ids.ctypes.data, d.ctypes.data)
     assert rc == gtann.GT_EINVAL
+
+
+def test_one_hip_runtime_with_torch():
+    # libgtann.so and PyTorch must share one HIP runtime, whichever is loaded
+    # first (two runtimes in one process cannot both acquire the GPU)
+    import subprocess
+    import sys
+    code = ("import sys; sys.path.insert(0, %r); import gtann; gtann.lib(); import torch; "
+            "m = {l.split()[-1] for l in open('/proc/self/maps') if 'libamdhip64' in l}; print(len(m))"
+            % os.path.join(ROOT, "gpu-talored-ann_amd"))
+    out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, check=True)
+    assert out.stdout.strip() == "1"

@@ -252,6 +252,28 @@ def test_prune_occlusion_float_data(ctx):
     assert (got == want).all(axis=1).mean() >= 0.999
 
 
+def test_prune_occlusion_matches_reference_python(ctx):
+    # fixtures written by bd/prune.py:prune_graph itself (tests/golden/make_golden_py.py):
+    # integer cases exact, float cases at least 1e-3 relative from every tie
+    z = np.load(os.path.join(GOLDEN, "pyref_golden.npz"))
+    n = len([k for k in z.files if k.endswith("_nb")])
+    for c in range(n):
+        print(f"occlusion vs prune_graph case {c} ({z[f'occ{c}_kind']})", flush=True)
+        got = ctx.prune_occlusion(z[f"occ{c}_X"], z[f"occ{c}_nb"].astype(np.int32), int(z[f"occ{c}_maxdeg"]))
+        np.testing.assert_array_equal(got.astype(np.int64), z[f"occ{c}_out"], err_msg=f"case {c}")
+
+
+def test_reverse_insert_matches_reference_python(ctx):
+    # fixtures written by bd/build_bucket.py:_apply_reverse_edges itself, tie-free tables
+    z = np.load(os.path.join(GOLDEN, "pyref_golden.npz"))
+    n = len([k for k in z.files if k.startswith("rin") and k.endswith("_out_ids")])
+    for c in range(n):
+        print(f"reverse insert vs _apply_reverse_edges case {c}", flush=True)
+        gi, gd = ctx.reverse_insert(z[f"rin{c}_ids"], z[f"rin{c}_d"])
+        np.testing.assert_array_equal(gi, z[f"rin{c}_out_ids"], err_msg=f"case {c}")
+        np.testing.assert_array_equal(gd, z[f"rin{c}_out_d"], err_msg=f"case {c}")
+
+
 def _offer_table(rng, X, M):
     ids, d = O.knn_exact(X, M)
     # degrade: drop some true neighbours so that offers exist

@@ -179,6 +179,14 @@ def test_refine_2hop_gpu(ctx):
     assert_knn_equal(gi, gd, ri, rd)
 
 
+def test_refine_hand_traced_known_answer_gpu(ctx):
+    from test_oracle import REFINE_KAT_OUT_D, REFINE_KAT_OUT_IDS, refine_kat_input
+    X, ids, d = refine_kat_input()
+    gi, gd = ctx.refine_2hop(X, ids, d, S=2, passes=1)
+    assert gi.tolist() == REFINE_KAT_OUT_IDS
+    assert gd.tolist() == REFINE_KAT_OUT_D
+
+
 def test_invalid_arguments_raise(ctx):
     import gtann
     X = _int_data(100, 16, seed=18)

@@ -277,6 +277,107 @@ def test_refine_fixed_point_and_monotone():
         np.testing.assert_array_equal(rd[q][:len(v)], ((X[v] - X[q]) ** 2).sum(axis=1))
 
 
+# Hand-traced known answer of one refinement pass (src/bucket.cu:4754-4850),
+# M = 3, S = 2, eight 2-D integer points.  Each input row holds ids sorted by
+# their true squared distance (not the exact kNN).  The candidates of a are
+# columns 0..S-1 of the rows of its first S neighbours; self, ids already in
+# a's row and repeated candidates drop out; a candidate enters only if its
+# distance is strictly below a's 3rd distance; the row becomes the first 3 of
+# row + candidates by (distance, id).
+REFINE_KAT_X = np.array([[0, 0], [3, 0], [4, 0], [20, 20], [-1, 0], [0, 1], [0, 6], [6, 0]], np.float32)
+REFINE_KAT_IDS = np.array([[1, 2, 7],    # a=0: kth 36
+                           [2, 0, 4],    # col 0 = 2 is in row 0 (dedup); col 2 = 4 (d0 = 1) lies beyond S
+                           [1, 6, 3],    # col 1 = 6: d(0,6) = 36 = row 0's kth, id 6 < 7 (strict <)
+                           [7, 2, 1],
+                           [0, 5, 7],
+                           [0, 4, 1],
+                           [5, 0, 1],
+                           [0, 5, 6]],   # row 7 is row 0's 3rd neighbour (hop beyond S): its 5 has d0 = 1
+                          np.int32)
+REFINE_KAT_OUT_IDS = [[1, 2, 7],   # nothing enters: 2 dedup, 0 self, 1 dedup, 6 tied with kth
+                      [2, 0, 4],   # 6 (45) not below 16; 0 and 2 self / in row
+                      [1, 0, 5],   # 0 (16) via hop 1, 5 (17) via hop 6; 0 again via 6 is a repeat
+                      [6, 7, 2],   # 6 (596) via hop 2 ties 7 (596): lower id first; 0 (800), 5 (761) too far
+                      [0, 5, 1],   # 1 (16) and 2 (25) via hop 0, both below 49
+                      [0, 4, 1],   # 2 (17) not below 10
+                      [5, 0, 4],   # 4 (37) via hop 5; 2 (52) not below 45
+                      [2, 1, 0]]   # 1 (9), 2 (4) via hop 0, 4 (49) via hop 5, all below 72
+REFINE_KAT_OUT_D = [[9, 16, 36], [1, 9, 16], [1, 16, 17], [596, 596, 656],
+                    [1, 2, 16], [1, 2, 10], [25, 36, 37], [4, 9, 36]]
+
+
+def refine_kat_input():
+    X = REFINE_KAT_X
+    d = np.array([[((X[a] - X[v]) ** 2).sum() for v in REFINE_KAT_IDS[a]] for a in range(8)], np.float32)
+    return X, REFINE_KAT_IDS.copy(), d
+
+
+def test_refine_hand_traced_known_answer():
+    X, ids, d = refine_kat_input()
+    assert (np.diff(d, axis=1) >= 0).all()
+    ri, rd = O.refine_2hop(X, ids, d, 2)
+    assert ri.tolist() == REFINE_KAT_OUT_IDS
+    assert rd.tolist() == REFINE_KAT_OUT_D
+
+
+def test_refine_two_hop_property():
+    """After one pass, every 2-hop candidate v of a (column < S of the row of
+    one of a's first S neighbours, v != a) is in a's new row unless its
+    distance is not below the new row's last distance; and every entry of the
+    new row is either from a's old row or such a candidate, with its exact
+    distance."""
+    rng = np.random.default_rng(13)
+    N, D, M, S = 400, 6, 10, 4
+    X = rng.integers(0, 200, size=(N, D)).astype(np.float32)
+    X64 = X.astype(np.float64)
+    ids = np.stack([rng.permutation(np.delete(np.arange(N), a))[:M] for a in range(N)]).astype(np.int32)
+    d = np.array([((X64[ids[a]] - X64[a]) ** 2).sum(1) for a in range(N)], np.float32)
+    o = np.argsort(d, axis=1, kind="stable")
+    ids, d = np.take_along_axis(ids, o, 1), np.take_along_axis(d, o, 1)
+    ri, rd = O.refine_2hop(X, ids, d, S)
+    changed = 0
+    for a in range(N):
+        cand = {int(v) for u in ids[a, :S] for v in ids[u, :S] if v != a}
+        allowed = cand | set(ids[a].tolist())
+        assert set(ri[a].tolist()) <= allowed
+        assert len(set(ri[a].tolist())) == M
+        np.testing.assert_array_equal(rd[a], ((X64[ri[a]] - X64[a]) ** 2).sum(1).astype(np.float32))
+        for v in cand:
+            dv = float(((X64[v] - X64[a]) ** 2).sum())
+            assert v in ri[a] or dv >= rd[a, -1]
+        changed += int((ri[a] != ids[a]).any())
+    assert changed > N // 2
+
+
+# ---------------------------------------------------------------- fixtures from the reference's Python
+# tests/golden/pyref_golden.npz is written by tests/golden/make_golden_py.py,
+# which imports bd/prune.py:prune_graph and bd/build_bucket.py:_apply_reverse_edges
+# in the build container, on inputs whose results no tie order or float32
+# summation order can change.
+
+def _pyref():
+    return np.load(os.path.join(GOLDEN, "pyref_golden.npz"))
+
+
+def test_occlusion_prune_matches_reference_python():
+    z = _pyref()
+    n = len([k for k in z.files if k.endswith("_nb")])
+    assert n >= 7
+    for c in range(n):
+        got = O.prune_occlusion(z[f"occ{c}_X"], z[f"occ{c}_nb"], int(z[f"occ{c}_maxdeg"]))
+        np.testing.assert_array_equal(got, z[f"occ{c}_out"], err_msg=f"case {c} ({z[f'occ{c}_kind']})")
+
+
+def test_reverse_insert_matches_reference_python():
+    z = _pyref()
+    n = len([k for k in z.files if k.startswith("rin") and k.endswith("_out_ids")])
+    assert n >= 4
+    for c in range(n):
+        ri, rd = O.reverse_insert(z[f"rin{c}_ids"], z[f"rin{c}_d"])
+        np.testing.assert_array_equal(ri, z[f"rin{c}_out_ids"], err_msg=f"case {c}")
+        np.testing.assert_array_equal(rd, z[f"rin{c}_out_d"], err_msg=f"case {c}")
+
+
 # ---------------------------------------------------------------- occlusion prune
 
 def test_occlusion_prune_line_known_answer():
