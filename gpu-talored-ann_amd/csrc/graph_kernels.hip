@@ -1344,6 +1344,20 @@ void launch_negate(float* d, int64_t n, hipStream_t s)
     GT_HIP(hipGetLastError());
 }
 
+__global__ void init_flags_kernel(unsigned long long* __restrict__ bad_row, int* __restrict__ err)
+{
+    if (threadIdx.x == 0) {
+        *bad_row = ~0ull;
+        *err = 0;
+    }
+}
+
+void launch_init_flags(unsigned long long* bad_row, int* err, hipStream_t s)
+{
+    hipLaunchKernelGGL(init_flags_kernel, dim3(1), dim3(64), 0, s, bad_row, err);
+    GT_HIP(hipGetLastError());
+}
+
 void launch_sanitize(const int32_t* in, int64_t N, int M, uint32_t* out, hipStream_t s)
 {
     if (N <= 0) return;

@@ -53,6 +53,7 @@ void launch_remap_table(const int32_t* ids, const uint32_t* inv, const uint32_t*
                         hipStream_t s);
 size_t search_lds_bytes(int CC, int efr, int Dp, int H);
 void launch_sanitize(const int32_t* in, int64_t N, int M, uint32_t* out, hipStream_t s);
+void launch_init_flags(unsigned long long* bad_row, int* err, hipStream_t s);
 void launch_cagra_prune(const int32_t* G, int64_t N, int M, int K, uint32_t* out, unsigned long long* bad_row,
                         hipStream_t s);
 void launch_rev_count(const uint32_t* fwd, int64_t N, int K, uint32_t* deg, uint32_t* slot, int* err, hipStream_t s);
@@ -210,6 +211,8 @@ struct gt_ctx {
     int64_t knn_launches = 0;   // bucketed-round launches of the current build
     uint64_t members_gen = 0;   // bucketing whose members W_MEMBERS holds (0: none)
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
+    void* scratch = nullptr;    // this device's fixed scratch array (gt_optimize_noalloc), or null
+    std::string scratch_err;    // why it is null
 };
 
 namespace gtann {
@@ -1355,6 +1358,81 @@ static void reverse_insert_device(Ctx& c, int32_t* ids, float* d, int64_t N, int
 
 using namespace gtann;
 
+// ---------------------------------------------------------------- fixed scratch of gt_optimize_noalloc
+// One array per GPU, allocated with the code object and held until the
+// process ends.  Host code never uses the name `scratch` as an address (on
+// the host it only stands for the symbol): gt_create looks up each device's
+// own address with hipGetSymbolAddress, once per device, and every use goes
+// through that pointer.
+static __device__ __align__(256) unsigned char scratch[GT_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+std::string g_scratch_err[kMaxDevices];
+
+// with `device` current
+void* scratch_for_device(int device, std::string& why)
+{
+    if (device < 0 || device >= kMaxDevices) {
+        why = "device index beyond the scratch table";
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[device] && g_scratch_err[device].empty()) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            g_scratch_err[device] = std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e);
+            (void)hipGetLastError();
+        } else {
+            g_scratch_ptr[device] = p;
+        }
+    }
+    why = g_scratch_err[device];
+    return g_scratch_ptr[device];
+}
+
+// Byte offsets of gt_optimize_noalloc's buffers inside the scratch array
+// (each 256-byte aligned): the forward graph, the two flags, and the binned
+// reverse merge's histogram, offsets, scan sums, partitioned and grouped keys.
+struct NoAllocLayout {
+    size_t fwd, bad, err, hist, offs, sums, part, grouped, bytes;
+};
+
+NoAllocLayout noalloc_layout(int64_t N, int K)
+{
+    const int64_t E = N * K;
+    const int shift = rev_bin_shift(N);
+    const int64_t nh = ceil_div(N, int64_t(1) << shift) * rev_bin_blocks(E);
+    auto up = [](size_t x) { return (x + 255) / 256 * 256; };
+    NoAllocLayout L{};
+    size_t o = 0;
+    L.fwd = o;     o += up(static_cast<size_t>(E) * sizeof(uint32_t));
+    L.bad = o;     o += up(sizeof(unsigned long long));
+    L.err = o;     o += up(sizeof(int));
+    L.hist = o;    o += up(static_cast<size_t>(nh) * sizeof(uint32_t));
+    L.offs = o;    o += up(static_cast<size_t>(nh + 1) * sizeof(uint32_t));
+    L.sums = o;    o += up(static_cast<size_t>(ceil_div(nh, 1024) + 1) * sizeof(uint32_t));
+    L.part = o;    o += up(static_cast<size_t>(E) * sizeof(unsigned long long));
+    L.grouped = o; o += up(static_cast<size_t>(E) * sizeof(unsigned long long));
+    L.bytes = o;
+    return L;
+}
+
+bool on_device(const void* p, int device)
+{
+    if (!p) return false;
+    hipPointerAttribute_t attr;
+    if (hipPointerGetAttributes(&attr, p) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    return attr.type == hipMemoryTypeDevice && attr.device == device;
+}
+}  // namespace
+
 template <typename F>
 static int guarded(gt_ctx* ctx, F&& f)
 {
@@ -1448,6 +1526,9 @@ int gt_create(int device, gt_ctx** out)
         delete c;
         return GT_EDEVICE;
     }
+    // this device's scratch address (looked up once per device); a failure
+    // only disables gt_optimize_noalloc
+    c->scratch = scratch_for_device(device, c->scratch_err);
     *out = c;
     return GT_OK;
 }
@@ -1924,6 +2005,45 @@ int gt_optimize(gt_ctx* ctx, const uint32_t* knn, int64_t N, int32_t M, int32_t 
         reverse_merge_device(c, f, N, K, o);
         c.out(out, o, nk);
         c.sync();
+    });
+}
+
+int gt_optimize_noalloc(gt_ctx* ctx, const uint32_t* knn, int64_t N, int32_t M, int32_t K, uint32_t* out)
+{
+    return guarded(ctx, [&] {
+        GT_REQUIRE(knn && out && N >= 1 && M >= 1 && M <= 128 && K >= 1 && K <= M && K <= 64,
+                   "gt_optimize_noalloc: bad arguments (need 1 <= K <= min(M, 64), M <= 128)");
+        GT_REQUIRE(N * K <= GT_NOALLOC_MAX_EDGES,
+                   "gt_optimize_noalloc: N * K = " + std::to_string(N * K) + " edges exceeds the scratch maximum of " +
+                       std::to_string(GT_NOALLOC_MAX_EDGES) + " (use gt_optimize)");
+        GT_REQUIRE(on_device(knn, ctx->device) && on_device(out, ctx->device),
+                   "gt_optimize_noalloc: knn and out must be device memory of the context's GPU");
+        if (!ctx->scratch) throw Error(GT_EDEVICE, "gt_optimize_noalloc: no scratch array: " + ctx->scratch_err);
+        const NoAllocLayout L = noalloc_layout(N, K);
+        GT_REQUIRE(L.bytes <= GT_NOALLOC_SCRATCH_BYTES, "gt_optimize_noalloc: scratch layout too large");
+        unsigned char* base = static_cast<unsigned char*>(ctx->scratch);
+        auto at = [&](size_t off) { return static_cast<void*>(base + off); };
+        uint32_t* fwd = static_cast<uint32_t*>(at(L.fwd));
+        unsigned long long* bad = static_cast<unsigned long long*>(at(L.bad));
+        int* err = static_cast<int*>(at(L.err));
+        hipStream_t s = ctx->stream;
+        // the array keeps the previous call's contents: reset the flags (a
+        // kernel, not a memset node); everything else is written before it is read
+        launch_init_flags(bad, err, s);
+        launch_cagra_prune(reinterpret_cast<const int32_t*>(knn), N, M, K, fwd, bad, s);
+        unsigned long long h_bad = 0;
+        GT_HIP(hipMemcpyAsync(&h_bad, bad, sizeof(h_bad), hipMemcpyDeviceToHost, s));
+        GT_HIP(hipStreamSynchronize(s));
+        if (h_bad != ~0ull)
+            throw Error(GT_EFEWCAND, "prune: row " + std::to_string(h_bad) +
+                                         " has fewer than output_degree valid candidates");
+        launch_rev_binned(fwd, N, K, static_cast<uint32_t*>(at(L.hist)), static_cast<uint32_t*>(at(L.offs)),
+                          static_cast<uint32_t*>(at(L.sums)), static_cast<unsigned long long*>(at(L.part)),
+                          static_cast<unsigned long long*>(at(L.grouped)), out, err, s);
+        int h_err = 0;
+        GT_HIP(hipMemcpyAsync(&h_err, err, sizeof(h_err), hipMemcpyDeviceToHost, s));
+        GT_HIP(hipStreamSynchronize(s));
+        if (h_err) throw Error(GT_EINVAL, "reverse merge: forward graph holds an id >= N");
     });
 }
 

@@ -26,7 +26,7 @@ EXPORTS = (
     "gt_knn_bucketed", "gt_merge_rounds", "gt_refine_2hop", "gt_sanitize", "gt_cagra_prune",
     "gt_reverse_merge", "gt_optimize", "gt_translate", "gt_build_params_default", "gt_build_graph",
     "gt_prune_occlusion", "gt_reverse_insert", "gt_search_params_default", "gt_search", "gt_build_graph_ex",
-    "gt_bucket_order", "gt_bucket_reorder", "gt_permute_rows", "gt_remap_table",
+    "gt_bucket_order", "gt_bucket_reorder", "gt_permute_rows", "gt_remap_table", "gt_optimize_noalloc",
 )
 
 
@@ -124,6 +124,7 @@ def lib():
         L.gt_cagra_prune.argtypes = [vp, vp, i64, i32, i32, vp]
         L.gt_reverse_merge.argtypes = [vp, vp, i64, i32, vp]
         L.gt_optimize.argtypes = [vp, vp, i64, i32, i32, vp]
+        L.gt_optimize_noalloc.argtypes = [vp, vp, i64, i32, i32, vp]
         L.gt_translate.argtypes = [vp, vp, vp, i64, i32, vp]
         L.gt_prune_occlusion.argtypes = [vp, vp, i64, i32, C.c_int, vp, i32, i32, vp]
         L.gt_reverse_insert.argtypes = [vp, vp, vp, i64, i32]
@@ -359,6 +360,18 @@ class Context:
         N, M = knn.shape
         out = np.empty((N, K), np.uint32)
         self._check(lib().gt_optimize(self._h, _ptr(knn), N, M, K, _ptr(out)), "gt_optimize")
+        return out
+
+    def optimize_noalloc(self, knn, K, out=None):
+        """gt_optimize_noalloc: knn (N, M) int32/uint32 and out (N, K) must be
+        device tensors of this context's GPU; the library allocates nothing."""
+        if not (_is_torch(knn) and knn.is_cuda):
+            raise ValueError("optimize_noalloc needs a device tensor")
+        N, M = knn.shape
+        if out is None:
+            import torch
+            out = torch.empty((N, K), dtype=torch.int32, device=knn.device)
+        self._check(lib().gt_optimize_noalloc(self._h, _ptr(knn), N, M, K, _ptr(out)), "gt_optimize_noalloc")
         return out
 
     def prune_occlusion(self, X, nb, max_degree=0):

@@ -124,6 +124,21 @@ int gt_reverse_insert(gt_ctx* ctx, int32_t* ids, float* dists, int64_t N, int32_
  * (src/optimize.cu:395-397, src/bucket.cu:8470). */
 int gt_optimize(gt_ctx* ctx, const uint32_t* knn, int64_t N, int32_t M, int32_t K, uint32_t* out);
 
+/* gt_optimize without any allocation.  No counterpart in the reference: for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  knn (N x M) and out
+ * (N x K) must be device memory of the context's GPU (GT_EINVAL otherwise).
+ * The forward graph, the error flags and the reverse merge's bins and keys
+ * live in one fixed device array per GPU (GT_NOALLOC_SCRATCH_BYTES, held by
+ * every GPU the library runs on until the process ends), which limits the
+ * call to N * K <= GT_NOALLOC_MAX_EDGES (GT_EINVAL beyond).  Every call on a
+ * GPU shares that GPU's array: calls that overlap on one GPU (other threads,
+ * other contexts) race and must be serialised by the caller.  Same results
+ * as gt_optimize, bit for bit. */
+#define GT_NOALLOC_MAX_EDGES (1 << 20)
+#define GT_NOALLOC_SCRATCH_BYTES (25u << 20)
+int gt_optimize_noalloc(gt_ctx* ctx, const uint32_t* knn, int64_t N, int32_t M, int32_t K, uint32_t* out);
+
 /* out[inv[i]][k] = inv[g[i][k]]; GT_EINVAL unless inv is a permutation.
  * Replaces translate_ids::translate_graph_to_original_order
  * (src/translate_graph_ids.hpp:75). */
