@@ -48,7 +48,6 @@
 #include <algorithm>
 #include <chrono>
 #include <random>
-#include <unordered_set>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -467,6 +466,32 @@ std::vector<uint32_t> read_index(const std::string& path, int64_t N, int32_t& de
     return g;
 }
 
+// Distinct ids >= 0 of row[0..n), ascending.
+template <typename T>
+static std::vector<T> distinct_valid(const T* row, int64_t n)
+{
+    std::vector<T> v;
+    v.reserve(static_cast<size_t>(std::max<int64_t>(n, 0)));
+    for (int64_t j = 0; j < n; ++j)
+        if (row[j] >= 0) v.push_back(row[j]);
+    std::sort(v.begin(), v.end());
+    v.erase(std::unique(v.begin(), v.end()), v.end());
+    return v;
+}
+
+// |a ∩ b| of two ascending distinct lists, by one merge pass.
+template <typename T>
+static int64_t common_count(const std::vector<T>& a, const std::vector<T>& b)
+{
+    int64_t n = 0;
+    for (size_t i = 0, j = 0; i < a.size() && j < b.size();) {
+        if (a[i] < b[j]) ++i;
+        else if (b[j] < a[i]) ++j;
+        else { ++n; ++i; ++j; }
+    }
+    return n;
+}
+
 int cmd_search(int argc, char** argv)
 {
     Args a(argc, argv, {"base", "query", "index", "gt", "topk", "ef", "num-entry"}, {"normalize"});
@@ -524,30 +549,22 @@ int cmd_search(int argc, char** argv)
     L.check(gt_search(L.ctx, base.data(), base.N, base.D, base.dtype, g.data(), deg, Q.data(), Q.N, entries.data(),
                       num_entry, &p, ids.data(), d.data(), &st),
             "gt_search");
-    // recall_vs_gt of bd/search.cpp:150-208
+    // The figures of bd/search.cpp:147-208 (recall_vs_gt): hit GT[:,0] =
+    // the first ground-truth id (when valid) is among the predictions; hit
+    // any = some prediction is a valid ground-truth id; overlap = distinct
+    // valid predictions among the first k that are ground-truth ids, over k,
+    // k = min(topk, distinct valid ground-truth ids, k_gt).
     int hit_first = 0, hit_any = 0;
     float total_overlap = 0.f;
     for (int32_t i = 0; i < Q.N; ++i) {
         const int32_t* pr = ids.data() + static_cast<size_t>(i) * topk;
         const int32_t* gr = gt.data() + static_cast<size_t>(i) * k_gt;
-        if (gr[0] >= 0 && std::find(pr, pr + topk, gr[0]) != pr + topk) ++hit_first;
-        std::unordered_set<int32_t> gs;
-        for (int j = 0; j < k_gt; ++j)
-            if (gr[j] >= 0) gs.insert(gr[j]);
-        if (!gs.empty()) {
-            int h = 0;
-            for (int j = 0; j < topk; ++j) h += gs.count(pr[j]) ? 1 : 0;
-            if (h > 0) ++hit_any;
-        }
+        const std::vector<int32_t> gs = distinct_valid(gr, k_gt);
+        const std::vector<int32_t> ps = distinct_valid(pr, topk);
+        hit_first += gr[0] >= 0 && std::binary_search(ps.begin(), ps.end(), gr[0]);
+        hit_any += common_count(ps, gs) > 0;
         const int k = std::min({topk, static_cast<int>(gs.size()), static_cast<int>(k_gt)});
-        if (k > 0) {
-            std::unordered_set<int32_t> ps;
-            for (int j = 0; j < k; ++j)
-                if (pr[j] >= 0) ps.insert(pr[j]);
-            int ov = 0;
-            for (int32_t v : ps) ov += gs.count(v) ? 1 : 0;
-            total_overlap += ov / static_cast<float>(k);
-        }
+        if (k > 0) total_overlap += common_count(distinct_valid(pr, k), gs) / static_cast<float>(k);
     }
     const float nqf = static_cast<float>(Q.N > 0 ? Q.N : 1);
     std::printf("\n======== Recall vs GT ========\n");
@@ -580,17 +597,13 @@ int cmd_compare(int argc, char** argv)
     int64_t hits_any = 0, set_equal = 0;
     float total = 0.f;
     for (int64_t i = 0; i < Na; ++i) {
-        std::unordered_set<int64_t> SA, SB;
-        for (int64_t j = 0; j < k; ++j) {
-            if (A[static_cast<size_t>(i * Ma + j)] >= 0) SA.insert(A[static_cast<size_t>(i * Ma + j)]);
-            if (B[static_cast<size_t>(i * Mb + j)] >= 0) SB.insert(B[static_cast<size_t>(i * Mb + j)]);
-        }
-        int64_t inter = 0;
-        for (int64_t v : SA) inter += SB.count(v) ? 1 : 0;
+        const std::vector<int64_t> SA = distinct_valid(A.data() + static_cast<size_t>(i * Ma), k);
+        const std::vector<int64_t> SB = distinct_valid(B.data() + static_cast<size_t>(i * Mb), k);
+        const int64_t inter = common_count(SA, SB);
         const float ov = inter / static_cast<float>(k);
         total += ov;
-        if (inter >= 1) ++hits_any;
-        if (static_cast<int64_t>(SA.size()) == k && static_cast<int64_t>(SB.size()) == k && inter == k) ++set_equal;
+        hits_any += inter >= 1;
+        set_equal += static_cast<int64_t>(SA.size()) == k && static_cast<int64_t>(SB.size()) == k && inter == k;
         if (fc) std::fprintf(fc, "%lld,%lld,%zu,%zu,%.6f\n", static_cast<long long>(i), static_cast<long long>(inter),
                              SA.size(), SB.size(), ov);
     }

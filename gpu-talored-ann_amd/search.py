@@ -21,7 +21,7 @@ from __future__ import annotations
 import argparse
 import os
 import time
-from typing import List, Optional, Tuple
+from typing import Optional, Tuple
 
 import numpy as np
 
@@ -38,11 +38,6 @@ def _context(ctx=None):
     if _ctx is None:
         _ctx = gtann.Context()
     return _ctx
-
-
-def l2sqr(a: np.ndarray, b: np.ndarray) -> float:
-    diff = a - b
-    return float(diff.dot(diff))
 
 
 def draw_entries(rng: np.random.Generator, N: int, nq: int, num_entry: int) -> np.ndarray:
@@ -83,52 +78,84 @@ def graph_search_single(
     return ids[0][keep], d[0][keep].astype(np.float32)
 
 
+# ---------------------------------------------------------------- set arithmetic over padded id rows
+
+_SENT = np.iinfo(np.int64).min
+
+
+def _distinct_rows(x: np.ndarray, valid_only: bool, side: int) -> np.ndarray:
+    """Each row sorted, with repeats (and negative ids when valid_only)
+    replaced by sentinels that are unique per position and per side, so they
+    never pair with anything."""
+    s = np.sort(np.asarray(x, np.int64), axis=1)
+    drop = np.zeros(s.shape, bool)
+    drop[:, 1:] = s[:, 1:] == s[:, :-1]
+    if valid_only:
+        drop |= s < 0
+    sent = _SENT + side + 2 * np.arange(s.shape[1], dtype=np.int64)[None, :]
+    return np.where(drop, sent, s)
+
+
+def _set_sizes(a: np.ndarray, b: np.ndarray, valid_only: bool = True, chunk: int = 65536):
+    """Per row i: (|A_i ∩ B_i|, |A_i|, |B_i|) over the distinct values of
+    a[i] and b[i] (ids >= 0 only when valid_only).  A value common to both
+    rows appears exactly twice in the sorted concatenation of the two
+    distinct rows, as a pair of equal neighbours."""
+    n = a.shape[0]
+    inter = np.empty(n, np.int64)
+    na = np.empty(n, np.int64)
+    nb = np.empty(n, np.int64)
+    for r0 in range(0, n, chunk):
+        da = _distinct_rows(a[r0:r0 + chunk], valid_only, 0)
+        db = _distinct_rows(b[r0:r0 + chunk], valid_only, 1)
+        na[r0:r0 + chunk] = (da > _SENT + 2 * da.shape[1]).sum(axis=1)
+        nb[r0:r0 + chunk] = (db > _SENT + 2 * db.shape[1]).sum(axis=1)
+        both = np.sort(np.concatenate([da, db], axis=1), axis=1)
+        inter[r0:r0 + chunk] = (both[:, 1:] == both[:, :-1]).sum(axis=1)
+    return inter, na, nb
+
+
 def recall_vs_gt(pred: np.ndarray, gt: np.ndarray, topk: int) -> Tuple[float, float, float]:
-    """bd/search.py:95-127: (hit GT[:,0], hit any of GT, mean overlap of the
-    first min(topk, pred width, gt width) columns, -1 ignored)."""
+    """The three figures of bd/search.py:95-127:
+      * hit GT[:,0]: the query's first ground-truth id is among its predictions;
+      * hit any:     the prediction row and the ground-truth row share a value;
+      * mean overlap: |distinct valid ids of pred[:, :k] ∩ those of gt[:, :k]| / k,
+        k = min(topk, prediction width, ground-truth width), averaged over queries."""
+    pred = np.asarray(pred, np.int64)
+    gt = np.asarray(gt, np.int64)
     nq = pred.shape[0]
-    hit_first = 0
-    hit_any = 0
-    for i in range(nq):
-        if gt[i, 0] in pred[i]:
-            hit_first += 1
-        if np.intersect1d(pred[i], gt[i], assume_unique=False).size > 0:
-            hit_any += 1
-    r_first = hit_first / float(nq) if nq > 0 else 0.0
-    r_any = hit_any / float(nq) if nq > 0 else 0.0
+    if nq == 0:
+        return 0.0, 0.0, float("nan")
+    r_first = float((pred == gt[:, :1]).any(axis=1).mean())
+    r_any = float((_set_sizes(pred, gt, valid_only=False)[0] > 0).mean())
     k = min(topk, pred.shape[1], gt.shape[1])
-    total = 0.0
-    for i in range(nq):
-        a = pred[i, :k]
-        b = gt[i, :k]
-        a = a[a >= 0]
-        b = b[b >= 0]
-        total += len(set(a.tolist()).intersection(set(b.tolist()))) / float(k)
-    recall = total / float(nq)
-    return r_first, r_any, recall
+    overlap = _set_sizes(pred[:, :k], gt[:, :k])[0]
+    return r_first, r_any, float((overlap / float(k)).mean())
+
+
+def _load_search_inputs(base_path: str, query_path: str, index_path: str, gt_path: str):
+    """(base, queries, graph, ground truth), shapes checked against each
+    other with the reference's messages."""
+    base, N, D = load_bigann_to_f32(base_path)
+    Q, nq, dq = load_bigann_to_f32(query_path)
+    graph = load_neighbors(index_path)
+    GT, gt_nq, _ = load_ibin(gt_path)
+    for ok, msg in ((dq == D, f"Dim mismatch: base D={D}, query D={dq}"),
+                    (graph.shape[0] == N, "Index N mismatch with base"),
+                    (gt_nq == nq, "GT nq mismatch with query")):
+        if not ok:
+            raise ValueError(msg)
+    return base, Q, graph, GT
 
 
 def search_graph_recall(base_path: str, query_path: str, index_path: str, gt_path: str, topk: int, ef: int,
                         num_entry: int, normalize: bool = False, ctx=None):
-    base, N, D = load_bigann_to_f32(base_path)
-    Q, nq, dq = load_bigann_to_f32(query_path)
-    if dq != D:
-        raise ValueError(f"Dim mismatch: base D={D}, query D={dq}")
-    neighbors = load_neighbors(index_path)
-    if neighbors.shape[0] != N:
-        raise ValueError("Index N mismatch with base")
-    GT, gt_nq, k_gt = load_ibin(gt_path)
-    if gt_nq != nq:
-        raise ValueError("GT nq mismatch with query")
-
-    if normalize:
+    base, Q, neighbors, GT = _load_search_inputs(base_path, query_path, index_path, gt_path)
+    nq = Q.shape[0]
+    if normalize:   # cosine search: unit rows (the 1e-12 keeps zero rows finite)
         print("[eval] L2-normalizing base & queries")
-
-        def norm_rows(X):
-            n = np.linalg.norm(X, axis=1, keepdims=True) + 1e-12
-            X /= n
-        norm_rows(base)
-        norm_rows(Q)
+        for X in (base, Q):
+            X /= np.linalg.norm(X, axis=1, keepdims=True) + 1e-12
 
     rng = np.random.default_rng(42)
     ef = max(ef, topk)
@@ -160,25 +187,11 @@ def compare_indices_setwise(index_a_path: str, index_b_path: str, k_cmp: Optiona
     k = min(Ma, Mb) if k_cmp is None else min(int(k_cmp), Ma, Mb)
     if k <= 0:
         raise ValueError("k_cmp must be > 0")
-    Ak = A[:, :k].astype(np.int64, copy=False)
-    Bk = B[:, :k].astype(np.int64, copy=False)
-    overlaps = np.empty(N, dtype=np.float32)
-    hits_any = 0
-    set_equal = 0
-    rows: List[tuple] = []
-    for i in range(N):
-        a = Ak[i][Ak[i] >= 0]
-        b = Bk[i][Bk[i] >= 0]
-        SA, SB = set(a.tolist()), set(b.tolist())
-        inter = len(SA & SB)
-        overlaps[i] = inter / float(k)
-        hits_any += inter >= 1
-        set_equal += len(SA) == len(SB) == k and inter == k
-        if save_csv is not None:
-            rows.append((i, inter, len(SA), len(SB), overlaps[i]))
+    inter, deg_a, deg_b = _set_sizes(A[:, :k], B[:, :k])
+    overlaps = (inter / float(k)).astype(np.float32)
     mean_overlap = float(overlaps.mean()) if N > 0 else 0.0
-    hits_any_rate = hits_any / float(N) if N > 0 else 0.0
-    set_equal_rate = set_equal / float(N) if N > 0 else 0.0
+    hits_any_rate = float((inter >= 1).mean()) if N > 0 else 0.0
+    set_equal_rate = float(((deg_a == k) & (deg_b == k) & (inter == k)).mean()) if N > 0 else 0.0
     print("\n======= Index Comparison (set-wise) =======")
     print(f"N={N}, k={k} (A:{Ma}, B:{Mb})")
     print(f"MeanOverlap@{k} (|A∩B|/k) : {mean_overlap:.6f}")
@@ -188,8 +201,8 @@ def compare_indices_setwise(index_a_path: str, index_b_path: str, k_cmp: Optiona
         os.makedirs(os.path.dirname(save_csv) or ".", exist_ok=True)
         with open(save_csv, "w") as f:
             f.write("node,intersect_size,deg_A,deg_B,overlap\n")
-            for (i, inter, la, lb, ov) in rows:
-                f.write(f"{i},{inter},{la},{lb},{ov:.6f}\n")
+            f.writelines(f"{i},{c},{x},{y},{o:.6f}\n" for i, (c, x, y, o) in
+                         enumerate(zip(inter.tolist(), deg_a.tolist(), deg_b.tolist(), overlaps.tolist())))
         print(f"[compare] per-node stats saved to: {save_csv}")
     return {"mean_overlap": mean_overlap, "hits_any": hits_any_rate, "set_equal": set_equal_rate, "k": k}
 

@@ -72,3 +72,23 @@ def test_cli_compare_matches_mirror(tmp_path):
 def test_cli_search_rejects_bad_options(tmp_path):
     r = subprocess.run([EXE, "search", "--bogus", "1"], capture_output=True, text=True, timeout=60)
     assert r.returncode == 1 and "unknown option" in r.stderr
+
+
+def test_vectorised_metrics_equal_per_row_set_definitions():
+    # rows with -1 padding and repeated ids on both sides
+    rng = np.random.default_rng(8)
+    pred = rng.integers(-1, 40, size=(500, 10))
+    gt = rng.integers(-1, 40, size=(500, 25))
+    r_first, r_any, rec = search.recall_vs_gt(pred, gt, 10)
+    k = 10
+    first = np.mean([gt[i, 0] in pred[i].tolist() for i in range(500)])
+    anyh = np.mean([len(set(pred[i].tolist()) & set(gt[i].tolist())) > 0 for i in range(500)])
+    ov = np.mean([len({v for v in pred[i, :k] if v >= 0} & {v for v in gt[i, :k] if v >= 0}) / k
+                  for i in range(500)])
+    assert (r_first, r_any) == (first, anyh)
+    assert abs(rec - ov) < 1e-12
+    inter, na, nb = search._set_sizes(pred, gt)
+    for i in range(500):
+        A = {v for v in pred[i] if v >= 0}
+        B = {v for v in gt[i] if v >= 0}
+        assert (inter[i], na[i], nb[i]) == (len(A & B), len(A), len(B))
