@@ -64,6 +64,9 @@ int rev_bin_shift(int64_t N);
 int rev_bin_blocks(int64_t E);
 void launch_rev_binned(const uint32_t* fwd, int64_t N, int K, uint32_t* hist, uint32_t* offs, uint32_t* sums,
                        unsigned long long* part, unsigned long long* grouped, uint32_t* out, int* err, hipStream_t s);
+bool rv_plan(int64_t N, int K, RvPlan& p);
+void launch_rv(const uint32_t* fwd, int64_t N, int K, const RvPlan& p, uint32_t* part, uint32_t* meta_cnt,
+               uint32_t* meta_off, uint32_t* out, int* err, uint32_t* slow_rows, uint32_t* slow_count, hipStream_t s);
 void launch_rev_merge(const uint32_t* fwd, int64_t N, int K, const uint32_t* off, const unsigned long long* keys,
                       uint32_t* out, hipStream_t s);
 void launch_occlusion_prune(const float* X, int64_t N, int Dp, const int32_t* nb, int M, int max_deg, int32_t* out,
@@ -1297,11 +1300,22 @@ static void reverse_merge_device(Ctx& c, const uint32_t* fwd, int64_t N, int K, 
     GT_REQUIRE(N * K < (int64_t(1) << 32), "too many edges for 32-bit offsets");
     int* err = c.ws<int>(W_TMP, 1);
     GT_HIP(hipMemsetAsync(err, 0, sizeof(int), c.s));
-    // GTANN_REVMERGE_CSR=1 selects the global-atomic CSR path at any size
-    // (the path of graphs beyond the binned path's limits; tests cover both)
-    const char* force_csr = std::getenv("GTANN_REVMERGE_CSR");
-    const int shift = force_csr && force_csr[0] == '1' ? -1 : rev_bin_shift(N);
-    if (shift >= 0) {
+    // Three paths give the same rows: the two-kernel merge over block-local
+    // key regions (graphs up to 2^11 * 8192 rows), the binned merge through
+    // global grouping (up to 2^26 rows), the global-atomic CSR merge beyond.
+    // GTANN_REVMERGE_PATH=binned|csr selects a later path at any size (tests).
+    const char* force = std::getenv("GTANN_REVMERGE_PATH");
+    const std::string forced = force ? force : "";
+    RvPlan rp{};
+    const int shift = forced == "csr" ? -1 : rev_bin_shift(N);
+    if (forced.empty() && rv_plan(N, K, rp)) {
+        const size_t nm = static_cast<size_t>(rp.nbins) * rp.nblk;
+        uint32_t* part = c.ws<uint32_t>(W_KEYS, static_cast<size_t>(N) * K);
+        uint32_t* mcnt = c.ws<uint32_t>(W_DEG, nm);
+        uint32_t* moff = c.ws<uint32_t>(W_OFF, nm);
+        uint32_t* slow = c.ws<uint32_t>(W_CUR, static_cast<size_t>(N) + 1);   // [0]: count, then rows
+        launch_rv(fwd, N, K, rp, part, mcnt, moff, out, err, slow + 1, slow, c.s);
+    } else if (shift >= 0) {
         // binned path: LDS histograms and cursors, no global atomics
         const int64_t nh = ceil_div(N, int64_t(1) << shift) * rev_bin_blocks(N * K);
         uint32_t* hist = c.ws<uint32_t>(W_DEG, static_cast<size_t>(nh));

@@ -103,6 +103,18 @@ struct SearchArgs {
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// Launch plan of the two-kernel reverse merge (revmerge_kernels.hip).
+struct RvPlan {
+    int cshift;     // rows per destination bin = 2^cshift
+    int nbins;
+    int nblk;       // scatter blocks, each owning spb consecutive source rows
+    int64_t spb;
+    int kbits, sbits, nbits;   // bits of rank, source within block, source id
+    int rp;         // rows per merge pass (= merge block size)
+    int cap;        // keys grouped in LDS per pass
+    int ubuf;       // LDS words of the bin's key copy, later the forward-row stages
+};
+
 // Orders LDS traffic of one wave across its lanes (no s_barrier needed
 // inside a wave).
 __device__ __forceinline__ void wave_sync()

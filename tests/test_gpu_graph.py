@@ -109,10 +109,21 @@ def test_reverse_merge_random(ctx, N, K, hub):
 
 def test_reverse_merge_csr_path(ctx, monkeypatch):
     """The global-atomic CSR path (graphs beyond the binned path's limits),
-    forced by GTANN_REVMERGE_CSR=1, gives the same rows."""
-    monkeypatch.setenv("GTANN_REVMERGE_CSR", "1")
+    forced by GTANN_REVMERGE_PATH=csr, gives the same rows."""
+    monkeypatch.setenv("GTANN_REVMERGE_PATH", "csr")
     for N, K in [(5000, 32), (3000, 48), (700, 1)]:
         rng = np.random.default_rng(N + K)
+        F = rng.integers(0, N, size=(N, K)).astype(np.uint32)
+        F[rng.random((N, K)) < 0.2] = 3
+        _assert_rows_equal(ctx.reverse_merge(F), O.reverse_merge(F), F)
+
+
+def test_reverse_merge_binned_path(ctx, monkeypatch):
+    """The binned merge through global grouping (graphs between the two-kernel
+    merge's 2^11 * 8192 rows and 2^26), forced by GTANN_REVMERGE_PATH=binned."""
+    monkeypatch.setenv("GTANN_REVMERGE_PATH", "binned")
+    for N, K in [(5000, 32), (3000, 48), (700, 1), (20000, 16)]:
+        rng = np.random.default_rng(N * 7 + K)
         F = rng.integers(0, N, size=(N, K)).astype(np.uint32)
         F[rng.random((N, K)) < 0.2] = 3
         _assert_rows_equal(ctx.reverse_merge(F), O.reverse_merge(F), F)
