@@ -25,6 +25,17 @@ points, ef 64 and the reference CLI's 200; QPS from the device time of the
 search kernels, recall@10 against the exact top-10 among the base points,
 and the CPU restatement timed on a sample of the queries beside it.
 
+Beside `value` (dataset resident in HBM), the line carries the other two
+build-time definitions: `host_to_host` (dataset in host memory, graph and
+table back in host memory) and `file_io` (the gtann CLI's bucket2 from a
+.fbin file to the reference's output files, a separate process);
+`reference_knobs` (3 rounds, data points as centroids, nprobe = ceil(20000 /
+avg bucket)) on the same data; `configs` (C1, C3, C4, C5 with the default
+knobs: build time, recall@32, kernel fraction of peak); and `cpu_baseline`,
+the reference's CPU path on this host (numpy BLAS blocked kNN as
+bd/build_knn.py, the reference's own prune and merge headers compiled in
+place) on a bounded sample.
+
     python bench.py [--gpus 1] [--steps 3] [--warmup 1] [--config C2]
 """
 import argparse
@@ -47,33 +58,71 @@ def recall_at(approx, exact, k):
     return float(np.mean([len(np.intersect1d(approx[i, :k], exact[i, :k])) / k for i in range(len(exact))]))
 
 
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(X, knn_ids, K, n_sample):
-    """The CPU restatement of the reference path (exact kNN -> sanitize ->
-    CAGRA prune -> reverse merge, oracle/gt_oracle.c) timed on this host on a
-    bounded sample and extrapolated to the whole build."""
+    """The reference's CPU path timed on this host: exact kNN as
+    bd/build_knn.py:17-149 computes it (numpy: BLAS A @ B.T over 262,144-row
+    base blocks, argpartition + argsort per block and per merge;
+    oracle/gt_oracle.py knn_exact_blas) on a bounded sample of queries,
+    extrapolated to all N; then sanitize and the reference's own prune and
+    rank-ordered reverse merge (src/prune_windowed_core.hpp,
+    src/edge_chunk_accumulator.hpp compiled in place into oracle/_ref, rows over
+    OpenMP threads as src/prune_windowed.cpp:97 runs them) on the GPU's whole
+    kNN table; the CPU restatement in oracle/gt_oracle.c when the reference
+    build is absent."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import gt_oracle as O
     N = len(X)
+    M = knn_ids.shape[1]
     rng = np.random.default_rng(1)
     q = np.sort(rng.choice(N, n_sample, replace=False))
     t0 = time.perf_counter()
-    O.knn_exact(X, knn_ids.shape[1], queries=q)
-    t_knn = (time.perf_counter() - t0) * N / n_sample
-    # prune of the sampled rows needs every row they reference: time the
-    # whole-table sanitize + prune + merge on the GPU's own kNN table
-    t0 = time.perf_counter()
+    O.knn_exact_blas(X, M, queries=q, query_chunk=n_sample)
+    t_knn_sample = time.perf_counter() - t0
+    t_knn = t_knn_sample * N / n_sample
     san = O.sanitize(knn_ids)
-    fwd, rc, _ = O.cagra_prune(san, K)
+    ref = O.ref_available()
+    t0 = time.perf_counter()
+    if ref:
+        fwd, rc = O.ref_cagra_prune_omp(san, K)
+    else:
+        fwd, rc, _ = O.cagra_prune(san, K)
     t_prune = time.perf_counter() - t0
     t0 = time.perf_counter()
-    O.reverse_merge(fwd)
+    if ref:
+        O.ref_reverse_merge_omp(fwd)
+    else:
+        O.reverse_merge(fwd)
     t_merge = time.perf_counter() - t0
     total = t_knn + t_prune + t_merge
+    try:
+        from threadpoolctl import threadpool_info
+        blas = [(i.get("internal_api"), i.get("num_threads")) for i in threadpool_info() if i.get("user_api") == "blas"]
+    except Exception:
+        blas = []
+    threads = O.num_threads()
     return {
-        "value": N / total / 1e6, "unit": "Mpts/s", "cores": O.num_threads(), "kind": "port",
-        "sample": f"exact kNN of {n_sample} random queries vs all {N} points, extrapolated x{N / n_sample:.0f} "
-                  f"({t_knn:.1f} s); sanitize+prune ({t_prune:.1f} s) and reverse merge ({t_merge:.1f} s) "
-                  f"measured on the full table",
+        "value": N / total / 1e6, "unit": "Mpts/s", "cores": threads, "kind": "port",
+        "cpu": cpu_model(), "host_cpus": os.cpu_count(), "blas": blas,
+        "parts": {"knn": "port: numpy restatement of bd/build_knn.py:17-149 (BLAS GEMM; argpartition/argsort "
+                         "on one thread, as the reference)",
+                  "prune_merge": ("reference: prune_windowed_core.hpp + edge_chunk_accumulator.hpp compiled in "
+                                  "place (oracle/_ref), OpenMP over rows") if ref else
+                                 "port: oracle/gt_oracle.c (reference build absent)"},
+        "sample": f"exact kNN of {n_sample} random queries vs all {N} points ({t_knn_sample:.1f} s), extrapolated "
+                  f"x{N / n_sample:.0f}; sanitize + prune ({t_prune:.1f} s) and reverse merge ({t_merge:.1f} s) "
+                  f"on the whole table",
+        "stages_s": {"knn_extrapolated": t_knn, "prune": t_prune, "reverse_merge": t_merge},
         "seconds_extrapolated": total,
     }
 
@@ -132,6 +181,150 @@ def search_leg(ctx, torch, name, nq, kw, efs, cpu_sample):
     return out
 
 
+def knn_roofline(s, D, metric):
+    """Roofline of the round launches of the kNN kernel from the library's
+    own event times (mean build stats s)."""
+    launches = max(1, int(round(s["knn_launches"])))
+    launch_s = s["t_knn"] / launches
+    flops = s["knn_flops"] / launches
+    int8 = bool(round(s["knn_int8"]))
+    mip = 1 if metric == "ip" else 0
+    if int8:
+        kname, peak, unit = f"knn_i8_kernel<{-(-D // 32) * 32}, {mip}>", PEAK_INT8_MFMA, "TOP/s"
+    elif D <= 256:
+        kname, peak, unit = f"knn_fused_kernel<{-(-D // 32) * 32}, {mip}>", PEAK_FP32_MFMA, "TFLOP/s"
+    else:
+        kname, peak, unit = f"knn_wide_kernel<{mip}>", PEAK_FP32_MFMA, "TFLOP/s"
+    return {"kernel": kname, "bound": "mfma", "achieved": flops / launch_s / 1e12, "peak": peak / 1e12,
+            "unit": unit, "frac": flops / launch_s / peak, "flops_per_launch": flops,
+            "launch_ms": launch_s * 1e3, "launches": launches}
+
+
+def traffic_file(kernel, config):
+    """rocprofv3 FETCH+WRITE bytes per round launch of `kernel` on `config`
+    (profiles/<kernel>_<config>_traffic.json), or None."""
+    base = kernel.split("<")[0].replace("_kernel", "")
+    path = os.path.join(ROOT, "profiles", f"{base}_{config}_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        d = json.load(f)
+    return {"bytes_per_launch": d.get("bytes_per_launch"), "mfma_busy_pct": d.get("mfma_busy_pct"),
+            "source": d.get("source")}
+
+
+def mean_stats(stats):
+    return {k: float(np.mean([st[k] for st in stats])) for k in stats[0]}
+
+
+def timed_builds(ctx, torch, X, kw, steps, warmup=1):
+    for _ in range(warmup):
+        ctx.build_graph(X, **kw)
+    torch.cuda.synchronize()
+    stats = []
+    t0 = time.perf_counter()
+    res = None
+    for _ in range(steps):
+        res = ctx.build_graph(X, **kw)
+        stats.append(res.stats)
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps, mean_stats(stats), res
+
+
+def host_to_host_leg(ctx, torch, X, kw, steps):
+    """Build seconds with the dataset in host memory and the graph and the
+    pre-prune table (ids and distances) back in host memory: the upload,
+    the download and pageable-memory staging included."""
+    wall, s, res = timed_builds(ctx, torch, X, kw, steps)
+    N = len(X)
+    return {"ms_per_step": wall * 1e3, "value": N / wall / 1e6, "unit": "Mpts/s",
+            "prepare_incl_upload_ms": s["t_prepare"] * 1e3, "download_ms": s["t_download"] * 1e3,
+            "outputs": "graph (N x K uint32) + pre-prune table (N x M int32 ids, float32 distances), host memory",
+            "input": "dataset as a host numpy array (pageable memory)"}, res
+
+
+def file_io_leg(X, cfg, args):
+    """Build seconds from a .fbin file to the reference's output files: the
+    gtann CLI's bucket2 subcommand (read the dataset, build, inline reorder,
+    write data_reordered, inverse_perm, bucket files, centroid kNN,
+    vector_knn, vector_dists, neighbors.npy and final_graph), as a separate
+    process; wall time includes process start and GPU initialisation."""
+    import re
+    import shutil
+    import subprocess
+    import tempfile
+    import gtann_io
+    exe = os.path.join(ROOT, "gpu-talored-ann_amd", "bin", "gtann")
+    if not os.path.exists(exe):
+        return {"skipped": "gtann CLI not built"}
+    N = len(X)
+    tmp = tempfile.mkdtemp(prefix="gtann_bench_", dir=os.environ.get("TMPDIR", "/tmp"))
+    try:
+        path = os.path.join(tmp, "base.fbin")
+        gtann_io.write_dataset(path, X)
+        cmd = [exe, "bucket2", "-i", path, "-o", os.path.join(tmp, "out"), "--centroid-ratio", repr(cfg.buckets / N),
+               "--nprobe", str(args.nprobe if args.nprobe > 0 else 1), "--neighbors-m", str(cfg.M),
+               "--fused-optimize-degree", str(cfg.K), "-t", str(args.rounds), "--kmeans-iters",
+               str(args.kmeans_iters), "--knn-k", "32"]
+        t0 = time.perf_counter()
+        r = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
+        wall = time.perf_counter() - t0
+        if r.returncode != 0:
+            return {"error": f"gtann bucket2 exited {r.returncode}: {r.stderr.strip()[-300:]}"}
+        m = re.search(r"read ([0-9.]+) s\s+build ([0-9.]+) s.*reorder ([0-9.]+) s\s+write ([0-9.]+) s", r.stdout)
+        out = {"wall_s": wall, "value": N / wall / 1e6, "unit": "Mpts/s", "command": " ".join(
+            ["gtann"] + cmd[1:3] + ["base.fbin"] + cmd[4:5] + ["out"] + cmd[6:])}
+        if m:
+            rd, bd, ro, wr = (float(m.group(k)) for k in range(1, 5))
+            out.update({"read_s": rd, "build_s": bd, "reorder_s": ro, "write_s": wr,
+                        "process_and_init_s": wall - rd - bd - ro - wr})
+        files = os.listdir(os.path.join(tmp, "out"))
+        out["output_dir"] = files[0] if files else None
+        return out
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+
+
+def recall32(ctx, torch, Xd, knn, metric, n_sample=10000):
+    N = Xd.shape[0]
+    q = np.random.default_rng(0).choice(N, min(N, n_sample), replace=False)
+    ex_i, _ = ctx.knn_exact(Xd, 32, queries=torch.from_numpy(q).cuda(), metric=metric)
+    return recall_at(knn[q], ex_i.cpu().numpy(), 32)
+
+
+def configs_leg(ctx, torch, names, steps):
+    """Every other BASELINE configuration once more with the default knobs:
+    build time, recall@32 on a 10,000-point sample (all of C1) against the
+    exact kNN, and the kNN kernel's fraction of its matrix peak."""
+    import synth
+    out = {}
+    for name in names:
+        cfg = synth.CONFIGS[name]
+        t0 = time.perf_counter()
+        X, _ = synth.generate(name)
+        tg = time.perf_counter() - t0
+        Xd = torch.from_numpy(X).cuda()
+        N, D = Xd.shape
+        kw = dict(n_buckets=cfg.buckets, M=cfg.M, K=cfg.K, metric=cfg.metric, rounds=2, kmeans_iters=3, nprobe=1)
+        wall, s, res = timed_builds(ctx, torch, Xd, kw, steps)
+        knn = res.knn_ids.cpu().numpy()
+        rec = recall32(ctx, torch, Xd, knn, cfg.metric)
+        out[name] = {"workload": f"{name}: {N} x {D} {cfg.dtype}, {cfg.metric.upper()}, {cfg.buckets} buckets, "
+                                 f"M {cfg.M} -> K {cfg.K}, 2 rounds, 3 Lloyd iterations, nprobe 1",
+                     "ms_per_step": wall * 1e3, "value": N / wall / 1e6, "unit": "Mpts/s", "recall@32": rec,
+                     "knn_roofline": dict(knn_roofline(s, D, cfg.metric),
+                                          rocprof=traffic_file(knn_roofline(s, D, cfg.metric)["kernel"], name)),
+                     "prune_frac_hbm": N * (4 * cfg.M + 4 * cfg.M * (cfg.M - 1) + 4 * cfg.K) / s["t_prune"] / PEAK_HBM,
+                     "revmerge_frac_hbm": 28 * N * cfg.K / s["t_revmerge"] / PEAK_HBM,
+                     "stages_s": {k: s[k] for k in ("t_prepare", "t_bucketing", "t_knn", "t_merge", "t_prune",
+                                                    "t_revmerge", "t_total")}}
+        print(f"[bench] {name}: {wall * 1e3:.1f} ms, recall@32 {rec:.4f} (data generated in {tg:.1f} s)",
+              file=sys.stderr, flush=True)
+        del Xd, res, X
+        torch.cuda.empty_cache()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -142,10 +335,14 @@ def main():
     ap.add_argument("--kmeans-iters", type=int, default=3)
     ap.add_argument("--nprobe", type=int, default=1)
     ap.add_argument("--reference-knobs", action="store_true",
-                    help="the reference's own bucketing settings: 3 rounds, sampled data points as "
-                         "centroids, nprobe = ceil(20000 / avg bucket)")
-    ap.add_argument("--cpu-sample", type=int, default=2000)
+                    help="headline at the reference's own bucketing settings: 3 rounds, sampled data points as "
+                         "centroids, nprobe = ceil(20000 / avg bucket) (also reported as reference_knobs)")
+    ap.add_argument("--no-ref-knobs", action="store_true", help="skip the reference_knobs builds")
+    ap.add_argument("--cpu-sample", type=int, default=2048)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-io", action="store_true", help="skip the host-to-host and file-I/O legs")
+    ap.add_argument("--configs", default="C1,C3,C4,C5",
+                    help="other configurations built once more with the default knobs ('' = none)")
     ap.add_argument("--search-queries", type=int, default=10000,
                     help="held-out queries of the search leg (0 = skip it)")
     ap.add_argument("--search-config", default="S2", help="workload of the search leg")
@@ -178,21 +375,13 @@ def main():
         del src, dst
     torch.cuda.synchronize()
     ctx = gtann.Context(0)
+    ref_kw = dict(rounds=3, kmeans_iters=0, nprobe=-1)
     if args.reference_knobs:
-        args.rounds, args.kmeans_iters, args.nprobe = 3, 0, -1
-    kw = dict(n_buckets=cfg.buckets, M=cfg.M, K=cfg.K, rounds=args.rounds, metric=cfg.metric,
-              kmeans_iters=args.kmeans_iters, nprobe=args.nprobe)
-    for _ in range(args.warmup):
-        ctx.build_graph(Xd, **kw)
-    torch.cuda.synchronize()
-    print("[bench] warmup done", file=sys.stderr, flush=True)
-    stats = []
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        res = ctx.build_graph(Xd, **kw)
-        stats.append(res.stats)
-    torch.cuda.synchronize()
-    wall = (time.perf_counter() - t0) / args.steps
+        args.rounds, args.kmeans_iters, args.nprobe = ref_kw["rounds"], ref_kw["kmeans_iters"], ref_kw["nprobe"]
+    base_kw = dict(n_buckets=cfg.buckets, M=cfg.M, K=cfg.K, metric=cfg.metric)
+    kw = dict(base_kw, rounds=args.rounds, kmeans_iters=args.kmeans_iters, nprobe=args.nprobe)
+    wall, s, res = timed_builds(ctx, torch, Xd, kw, args.steps, args.warmup)
+    print("[bench] timed builds done", file=sys.stderr, flush=True)
 
     # quality: recall of the pre-prune table vs exact kNN on 10,000 sampled points
     q = np.random.default_rng(0).choice(N, 10000, replace=False)
@@ -208,13 +397,10 @@ def main():
         "degree": int(graph.shape[1]),
     }
 
-    s = {k: float(np.mean([st[k] for st in stats])) for k in stats[0]}
-    launches = max(1, int(round(s["knn_launches"])))
-    knn_launch_s = s["t_knn"] / launches
-    flops_launch = s["knn_flops"] / launches
-    achieved = flops_launch / knn_launch_s
+    roof = knn_roofline(s, D, cfg.metric)
     traffic = None
-    kbase = "knn_i8" if bool(round(s["knn_int8"])) else ("knn_fused" if D <= 256 else "knn_wide")
+    int8 = bool(round(s["knn_int8"]))
+    kbase = "knn_i8" if int8 else ("knn_fused" if D <= 256 else "knn_wide")
     tfile = os.path.join(ROOT, "profiles", f"{kbase}_{args.config}_traffic.json")
     default_knobs = (args.rounds, args.kmeans_iters, args.nprobe) == (2, 3, 1)
     if default_knobs and os.path.exists(tfile):
@@ -222,19 +408,10 @@ def main():
             traffic = json.load(f).get("bytes_per_launch")
     prune_bytes = N * (4 * cfg.M + 4 * cfg.M * (cfg.M - 1) + 4 * cfg.K)
     merge_bytes = 28 * N * cfg.K
-
     # integer-typed datasets of up to 256 dimensions run the int8 kernel, and
     # so do float datasets whose values are all integers in [-128, 127] or
     # [0, 255] (the library's int_exact: exact, the fp32 kernel's keys)
-    int8 = bool(round(s["knn_int8"]))
     dtype = "i8" if int8 else "fp32"
-    mip = 1 if cfg.metric == "ip" else 0
-    if int8:
-        kname, peak, punit = f"knn_i8_kernel<{-(-D // 32) * 32}, {mip}>", PEAK_INT8_MFMA, "TOP/s"
-    elif D <= 256:
-        kname, peak, punit = f"knn_fused_kernel<{-(-D // 32) * 32}, {mip}>", PEAK_FP32_MFMA, "TFLOP/s"
-    else:
-        kname, peak, punit = f"knn_wide_kernel<{mip}>", PEAK_FP32_MFMA, "TFLOP/s"
     out = {
         "metric": f"graph build Mpts/s at {N // 1000000 if N >= 1000000 else N}"
                   f"{'M' if N >= 1000000 else ''}x{D} {'fp32' if cfg.dtype == 'f32' else cfg.dtype} deg{cfg.K} "
@@ -256,58 +433,64 @@ def main():
                         f"nprobe {args.nprobe if args.nprobe >= 0 else 'ceil(20000/avg bucket)'}",
             "points": N, "dim": D, "buckets": cfg.buckets, "M": cfg.M, "K": cfg.K, "rounds": args.rounds,
             "kmeans_iters": args.kmeans_iters, "nprobe": args.nprobe,
+            "timed_region": "dataset resident in HBM (torch tensor) to graph and table in HBM",
         },
         "build_seconds": wall,
         **rec,
         "structural": structural,
         "stages_s": {k: s[k] for k in ("t_prepare", "t_bucketing", "t_knn", "t_merge", "t_refine", "t_prune",
                                        "t_revmerge", "t_download", "t_total")},
-        "roofline": {
-            "kernel": kname + " (one launch per round; round 1 split in two when probing)",
-            "bound": "mfma", "achieved": achieved / 1e12, "peak": peak / 1e12, "unit": punit,
-            "frac": achieved / peak, "traffic": traffic,
-            "flops_per_launch": flops_launch, "launch_ms": knn_launch_s * 1e3, "launches": launches,
-        },
+        "roofline": dict(roof, kernel=roof["kernel"] + " (one launch per round; round 1 split in two when probing)",
+                         traffic=traffic),
         "roofline_prune": {"bound": "hbm", "achieved": prune_bytes / s["t_prune"] / 1e9, "peak": 8000.0,
                            "unit": "GB/s", "frac": prune_bytes / s["t_prune"] / PEAK_HBM,
                            "bytes": prune_bytes, "includes": "sanitize + prune"},
         "roofline_revmerge": {"bound": "hbm", "achieved": merge_bytes / s["t_revmerge"] / 1e9, "peak": 8000.0,
                               "unit": "GB/s", "frac": merge_bytes / s["t_revmerge"] / PEAK_HBM,
-                              "bytes": merge_bytes, "includes": "count + scan + scatter + merge"},
+                              "bytes": merge_bytes, "includes": "scatter + merge (+ slow rows)"},
         "max_pool": int(s["max_pool"]), "max_bucket": int(s["max_bucket"]),
     }
     if int8 and cfg.dtype == "f32":
         # the same build on the fp32 kernel (int_exact off): its time, its
         # fraction of the fp32 matrix peak, and the check that both paths
         # return the same table and graph
-        kw32 = dict(kw, int_exact=False)
-        ctx.build_graph(Xd, **kw32)
-        torch.cuda.synchronize()
-        t1 = time.perf_counter()
-        st32 = []
-        for _ in range(max(1, min(args.steps, 3))):
-            r32 = ctx.build_graph(Xd, **kw32)
-            st32.append(r32.stats)
-        torch.cuda.synchronize()
-        wall32 = (time.perf_counter() - t1) / len(st32)
-        s32 = {k: float(np.mean([st[k] for st in st32])) for k in st32[0]}
-        l32 = max(1, int(round(s32["knn_launches"])))
-        ach32 = (s32["knn_flops"] / l32) / (s32["t_knn"] / l32)
+        w32, s32, r32 = timed_builds(ctx, torch, Xd, dict(kw, int_exact=False), max(1, min(args.steps, 3)))
         same = bool(torch.equal(r32.knn_ids, res.knn_ids) and torch.equal(r32.graph, res.graph))
+        r = knn_roofline(s32, D, cfg.metric)
         out["fp32_path"] = {
             "note": "int_exact=0: same dataset on knn_fused_kernel (fp32 matrix cores)",
-            "value": N / wall32 / 1e6, "unit": "Mpts/s", "ms_per_step": wall32 * 1e3,
+            "value": N / w32 / 1e6, "unit": "Mpts/s", "ms_per_step": w32 * 1e3,
             "identical_table_and_graph": same,
-            "roofline": {"kernel": f"knn_fused_kernel<{-(-D // 32) * 32}, {mip}>", "bound": "mfma",
-                         "achieved": ach32 / 1e12, "peak": PEAK_FP32_MFMA / 1e12, "unit": "TFLOP/s",
-                         "frac": ach32 / PEAK_FP32_MFMA, "launch_ms": s32["t_knn"] / l32 * 1e3},
+            "roofline": dict({k: r[k] for k in ("kernel", "bound", "achieved", "peak", "unit", "frac", "launch_ms")},
+                             rocprof=traffic_file(r["kernel"], args.config)),
         }
         del r32
+    if not args.reference_knobs and not args.no_ref_knobs:
+        # the reference's own knobs on the same data
+        wr, sr, rr = timed_builds(ctx, torch, Xd, dict(base_kw, **ref_kw), max(1, min(args.steps, 2)))
+        out["reference_knobs"] = {
+            "knobs": "3 rounds, sampled data points as centroids (no Lloyd), nprobe = ceil(20000 / avg bucket) "
+                     "(sk/scripts/params.sh:12, sk/scripts/dataset_env.py:56)",
+            "ms_per_step": wr * 1e3, "value": N / wr / 1e6, "unit": "Mpts/s",
+            "recall@32": recall_at(rr.knn_ids.cpu().numpy()[q], ex_i, 32),
+            "knn_roofline": knn_roofline(sr, D, cfg.metric)}
+        del rr
+    if not args.no_io:
+        h2h, rh = host_to_host_leg(ctx, torch, X, kw, max(1, min(args.steps, 2)))
+        h2h["identical_graph_to_device_run"] = bool((rh.graph == graph).all())
+        out["host_to_host"] = h2h
+        del rh
+        out["file_io"] = file_io_leg(X, cfg, args)
+        print("[bench] host-to-host and file-I/O legs done", file=sys.stderr, flush=True)
     if args.search_queries > 0:
         del Xd, res
+        torch.cuda.empty_cache()
         out["search"] = search_leg(ctx, torch, args.search_config, args.search_queries,
                                    dict(rounds=args.rounds, kmeans_iters=args.kmeans_iters, nprobe=args.nprobe),
                                    (64, 200), 0 if args.no_cpu else 500)
+    names = [c for c in args.configs.split(",") if c and c != args.config]
+    if names:
+        out["configs"] = configs_leg(ctx, torch, names, max(1, min(args.steps, 2)))
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(X, knn, cfg.K, args.cpu_sample)
     ctx.close()

@@ -1301,14 +1301,18 @@ static void reverse_merge_device(Ctx& c, const uint32_t* fwd, int64_t N, int K, 
     int* err = c.ws<int>(W_TMP, 1);
     GT_HIP(hipMemsetAsync(err, 0, sizeof(int), c.s));
     // Three paths give the same rows: the two-kernel merge over block-local
-    // key regions (graphs up to 2^11 * 8192 rows), the binned merge through
-    // global grouping (up to 2^26 rows), the global-atomic CSR merge beyond.
-    // GTANN_REVMERGE_PATH=binned|csr selects a later path at any size (tests).
+    // key regions (256-row bins, output degree <= 32: graphs up to 2^21
+    // rows; where it is faster), the binned merge through global grouping
+    // (up to 2^26 rows), the global-atomic CSR merge beyond.
+    // GTANN_REVMERGE_PATH=rv|binned|csr selects a path (tests; rv wherever
+    // it applies).
     const char* force = std::getenv("GTANN_REVMERGE_PATH");
     const std::string forced = force ? force : "";
     RvPlan rp{};
     const int shift = forced == "csr" ? -1 : rev_bin_shift(N);
-    if (forced.empty() && rv_plan(N, K, rp)) {
+    const bool rv_ok = rv_plan(N, K, rp);
+    const bool use_rv = forced == "rv" ? rv_ok : forced.empty() && rv_ok && rp.cshift == 8 && K <= 32;
+    if (use_rv) {
         const size_t nm = static_cast<size_t>(rp.nbins) * rp.nblk;
         uint32_t* part = c.ws<uint32_t>(W_KEYS, static_cast<size_t>(N) * K);
         uint32_t* mcnt = c.ws<uint32_t>(W_DEG, nm);

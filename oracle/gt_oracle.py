@@ -137,6 +137,8 @@ def ref():
         R = C.CDLL(_REF_PATH)
         vp, i64, i32 = C.c_void_p, C.c_int64, C.c_int32
         R.ref_cagra_prune.argtypes = [vp, i64, i32, i32, vp]
+        R.ref_cagra_prune_omp.argtypes = [vp, i64, i32, i32, vp]
+        R.ref_reverse_merge_omp.argtypes = [vp, i64, i32, vp]
         R.ref_detour_counts.argtypes = [vp, i64, i32, i64, vp]
         R.ref_reverse_merge.argtypes = [vp, i64, i32, vp]
         R.ref_translate.argtypes = [vp, vp, i64, i32, vp]
@@ -178,6 +180,48 @@ def knn_exact(X, k, queries=None, metric=0, exclude_self=True):
     _check(lib().or_knn_exact(_p(X), N, D, metric, _p(q), len(q), k, int(exclude_self), _p(ids), _p(d)),
            "or_knn_exact")
     return ids, d
+
+
+def knn_exact_blas(X, k, queries=None, base_chunk=262144, query_chunk=8192):
+    """The reference's CPU exact kNN, bd/build_knn.py:17-149, restated in
+    numpy: per query block and base block, dots by BLAS (A @ B.T, float32),
+    d = |a|^2 + |b|^2 - 2 a.b, self (same global id) set to +inf, the block's
+    top-k by np.argpartition + np.argsort, merged into the running top-k the
+    same way (_merge_topk).  Returns (ids int64, dists float32) for `queries`
+    (global ids, default all rows).  The timed CPU baseline of bench.py; the
+    order among equal distances is numpy's, as in the reference."""
+    X = np.ascontiguousarray(X, np.float32)
+    N = X.shape[0]
+    norms = np.sum(X ** 2, axis=1).astype(np.float32)
+    q = np.arange(N) if queries is None else np.asarray(queries, np.int64)
+    out_i = np.full((len(q), k), -1, np.int64)
+    out_d = np.full((len(q), k), np.inf, np.float32)
+    for a0 in range(0, len(q), query_chunk):
+        qa = q[a0:a0 + query_chunk]
+        A, a2 = X[qa], norms[qa]
+        cur_i = np.full((len(qa), k), -1, np.int64)
+        cur_d = np.full((len(qa), k), np.inf, np.float32)
+        for b0 in range(0, N, base_chunk):
+            b1 = min(N, b0 + base_chunk)
+            dist = a2[:, None] + norms[b0:b1][None, :] - 2.0 * (A @ X[b0:b1].T)
+            own = (qa >= b0) & (qa < b1)
+            dist[np.nonzero(own)[0], qa[own] - b0] = np.inf
+            if k < dist.shape[1]:
+                part = np.argpartition(dist, kth=k - 1, axis=1)[:, :k]
+            else:
+                part = np.tile(np.arange(dist.shape[1]), (dist.shape[0], 1))
+            row = np.arange(dist.shape[0])[:, None]
+            cd, ci = dist[row, part], part + b0
+            o = np.argsort(cd, axis=1)
+            add_d, add_i = np.take_along_axis(cd, o, 1), np.take_along_axis(ci, o, 1)
+            cat_i, cat_d = np.hstack([cur_i, add_i]), np.hstack([cur_d, add_d])
+            sel = np.argpartition(cat_d, kth=k - 1, axis=1)[:, :k]
+            cur_i, cur_d = cat_i[row, sel], cat_d[row, sel]
+            o = np.argsort(cur_d, axis=1)
+            cur_i, cur_d = np.take_along_axis(cur_i, o, 1), np.take_along_axis(cur_d, o, 1)
+        out_i[a0:a0 + len(qa)] = cur_i
+        out_d[a0:a0 + len(qa)] = cur_d
+    return out_i, out_d
 
 
 def knn_bucketed(X, offsets, members, probe, M, metric=0):
@@ -364,6 +408,25 @@ def ref_cagra_prune(G, K):
     out = np.zeros((N, K), np.uint32)
     rc = ref().ref_cagra_prune(_p(G), N, M, K, _p(out))
     return out, rc
+
+
+def ref_cagra_prune_omp(G, K):
+    """The reference's prune as its CLI runs it: rows over OpenMP threads
+    (src/prune_windowed.cpp:97); same output as ref_cagra_prune."""
+    G = np.ascontiguousarray(G).view(np.int32) if np.asarray(G).dtype == np.uint32 else \
+        np.ascontiguousarray(G, np.int32)
+    N, M = G.shape
+    out = np.zeros((N, K), np.uint32)
+    rc = ref().ref_cagra_prune_omp(_p(G), N, M, K, _p(out))
+    return out, rc
+
+
+def ref_reverse_merge_omp(fwd):
+    fwd = np.ascontiguousarray(fwd, np.uint32)
+    N, K = fwd.shape
+    out = np.empty((N, K), np.uint32)
+    _check(ref().ref_reverse_merge_omp(_p(fwd), N, K, _p(out)), "ref_reverse_merge_omp")
+    return out
 
 
 def ref_detour_counts(G, a):

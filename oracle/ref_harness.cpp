@@ -62,6 +62,63 @@ int ref_cagra_prune(const int32_t* G, int64_t N, int32_t M, int32_t K, uint32_t*
     }
 }
 
+// The reference CPU prune as its CLI runs it (src/prune_windowed.cpp:97):
+// rows in parallel over OpenMP threads, one detour buffer per thread; the
+// timed CPU baseline of bench.py.  Same output as ref_cagra_prune.
+int ref_cagra_prune_omp(const int32_t* G, int64_t N, int32_t M, int32_t K, uint32_t* out)
+{
+    try {
+        prune_windowed::WindowLookup w;
+        w.reserve(static_cast<size_t>(N));
+        static const float dummy = 0.f;
+        for (int64_t i = 0; i < N; ++i)
+            w.add(static_cast<uint32_t>(i), G + i * M, &dummy);
+        int64_t n_fail = 0;
+        #pragma omp parallel reduction(+:n_fail)
+        {
+            std::vector<uint32_t> detour;
+            #pragma omp for schedule(dynamic, 256)
+            for (int64_t a = 0; a < N; ++a) {
+                try {
+                    prune_windowed::compute_detour_counts(G + a * M, M, w, detour);
+                    prune_windowed::select_pruned_row(G + a * M, M, detour, K, out + a * K);
+                } catch (...) {
+                    ++n_fail;
+                }
+            }
+        }
+        return n_fail ? -4 : 0;
+    } catch (...) {
+        return -1;
+    }
+}
+
+// The reference's rank-ordered reverse merge with its own OpenMP CSR build
+// (src/edge_chunk_accumulator.hpp:235-284) and the rows merged in parallel.
+int ref_reverse_merge_omp(const uint32_t* fwd, int64_t N, int32_t K, uint32_t* out)
+{
+    try {
+        std::vector<edge_chunk::EdgeRecord> edges(static_cast<size_t>(N) * K);
+        #pragma omp parallel for schedule(static)
+        for (int64_t i = 0; i < N; ++i)
+            for (int32_t k = 0; k < K; ++k)
+                edges[static_cast<size_t>(i * K + k)] =
+                    edge_chunk::EdgeRecord{fwd[i * K + k], static_cast<uint32_t>(i), static_cast<uint16_t>(k)};
+        auto csr = edge_chunk::build_rank_ordered_csr(edges, 0, static_cast<uint32_t>(N));
+        #pragma omp parallel for schedule(dynamic, 1024)
+        for (int64_t j = 0; j < N; ++j) {
+            uint32_t* row = out + j * K;
+            for (int32_t k = 0; k < K; ++k) row[k] = fwd[j * K + k];
+            const uint32_t lo = csr.row_offsets[static_cast<size_t>(j)];
+            const uint32_t hi = csr.row_offsets[static_cast<size_t>(j) + 1];
+            edge_chunk::merge_rank_ordered_into_row(row, csr.src.data() + lo, hi - lo, static_cast<uint32_t>(K));
+        }
+        return 0;
+    } catch (...) {
+        return -1;
+    }
+}
+
 int ref_detour_counts(const int32_t* G, int64_t N, int32_t M, int64_t a, uint32_t* counts)
 {
     try {

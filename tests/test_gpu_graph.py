@@ -118,6 +118,22 @@ def test_reverse_merge_csr_path(ctx, monkeypatch):
         _assert_rows_equal(ctx.reverse_merge(F), O.reverse_merge(F), F)
 
 
+def test_reverse_merge_two_kernel_path_forced(ctx, monkeypatch):
+    """The two-kernel merge wherever it applies (GTANN_REVMERGE_PATH=rv),
+    including the output degrees and bin widths the default leaves to the
+    binned merge (K > 32, 2^11-row bins) and rows beyond its LDS capacity."""
+    monkeypatch.setenv("GTANN_REVMERGE_PATH", "rv")
+    for N, K, hub in [(3000, 48, True), (2000, 64, True), (70000, 48, False), (700, 1, False),
+                      (5000, 32, True), (60000, 32, True), (2200000, 2, False)]:
+        rng = np.random.default_rng(N * 11 + K)
+        F = rng.integers(0, N, size=(N, K)).astype(np.uint32)
+        if hub:
+            F[rng.random((N, K)) < 0.2] = 3
+            F[rng.random((N, K)) < 0.05] = 5
+        print(f"rv path N={N} K={K} hub={hub}", flush=True)
+        _assert_rows_equal(ctx.reverse_merge(F), O.reverse_merge(F), F)
+
+
 def test_reverse_merge_binned_path(ctx, monkeypatch):
     """The binned merge through global grouping (graphs between the two-kernel
     merge's 2^11 * 8192 rows and 2^26), forced by GTANN_REVMERGE_PATH=binned."""

@@ -445,3 +445,30 @@ def test_reverse_insert_rows_are_m_smallest_of_row_and_offers():
         for g in got:
             left.remove(g)
         assert all(x >= got[-1] for x in left)
+
+
+# ---------------------------------------------------------------- the timed CPU baseline
+
+def test_knn_exact_blas_port_matches_oracle():
+    # bd/build_knn.py's blocked BLAS kNN restated in numpy (the CPU baseline of
+    # bench.py): tie-free float data, several query and base blocks
+    rng = np.random.default_rng(21)
+    X = rng.standard_normal((2500, 24)).astype(np.float32)
+    bi, bd = O.knn_exact_blas(X, 16, base_chunk=600, query_chunk=700)
+    oi, od = O.knn_exact(X, 16)
+    np.testing.assert_array_equal(bi, oi)
+    np.testing.assert_allclose(bd, od, rtol=1e-5, atol=1e-5)
+    q = np.array([0, 5, 2499, 1200])
+    si, _ = O.knn_exact_blas(X, 16, queries=q, base_chunk=1000, query_chunk=4)
+    np.testing.assert_array_equal(si, oi[q])
+
+
+@pytest.mark.skipif(not O.ref_available(), reason="reference harness not built here")
+def test_reference_openmp_prune_and_merge_equal_serial():
+    rng = np.random.default_rng(22)
+    G = rng.integers(0, 4000, size=(4000, 32)).astype(np.int32)
+    a, rc = O.ref_cagra_prune(G, 16)
+    b, rc2 = O.ref_cagra_prune_omp(G, 16)
+    assert rc == rc2 == 0
+    np.testing.assert_array_equal(a, b)
+    np.testing.assert_array_equal(O.ref_reverse_merge(a), O.ref_reverse_merge_omp(a))
