@@ -27,6 +27,9 @@
 namespace gtann {
 // knn_kernels.hip
 void launch_knn_fused(const KnnArgs& a, hipStream_t stream);
+// knn_collect.hip
+bool knn_collect_supported(const KnnArgs& a);
+void launch_knn_collect_select(const KnnArgs& a, int64_t rows, hipStream_t stream);
 void launch_merge_partials(const int32_t* pids, const float* pd, int64_t nq, int splits, int M, int32_t* out_ids,
                            float* out_d, hipStream_t stream);
 // graph_kernels.hip
@@ -225,7 +228,7 @@ enum Ws {
     W_MEMBERS, W_TASKS, W_POOL, W_PART_I, W_PART_D, W_G1, W_G2, W_G3, W_DEG, W_OFF, W_CUR, W_KEYS, W_SUMS, W_FLAG,
     W_TMP, W_OUT, W_IN, W_PROBE_I, W_PROBE_D, W_WORST, W_X8, W_NORMS8, W_C8, W_CNORMS8,
     W_SUBROWS, W_SUBID, W_SUBD, W_SUBOFF, W_MEMBERS2, W_SUBNN, W_SUBNND, W_SUBBASE, W_SUBCNT, W_CHAINPOS,
-    W_LHIST, W_LOFFS, W_LSUMS, W_COUNT_
+    W_LHIST, W_LOFFS, W_LSUMS, W_CAND, W_CANDCNT, W_STATS, W_COUNT_
 };
 static_assert(W_COUNT_ <= 64, "workspace slots");
 
@@ -1002,12 +1005,35 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
     a.seed_ld = M;
     a.out_ids = out_ids;
     a.out_d = out_d;
-    const double t = c.timed([&] { launch_knn_fused(a, c.s); });
+    // lists of at most 64 keys on int8 rows: collect + select (every point
+    // is the query of exactly one work item, so rows = N)
+    const bool collect = knn_collect_supported(a);
+    if (collect) {
+        a.cand = c.ws<uint64_t>(W_CAND, static_cast<size_t>(N) * kCollectCap);
+        a.cand_cnt = c.ws<int32_t>(W_CANDCNT, static_cast<size_t>(N));
+        const char* se = std::getenv("GTANN_KNN_STATS");
+        if (tr.on && se && se[0] == '1') {   // counters of the collect launch (slow), printed below
+            a.stats = c.ws<unsigned long long>(W_STATS, 4);
+            GT_HIP(hipMemsetAsync(a.stats, 0, 4 * sizeof(unsigned long long), c.s));
+        }
+    }
+    const double t = c.timed([&] {
+        if (collect) launch_knn_collect_select(a, N, c.s);
+        else launch_knn_fused(a, c.s);
+    });
     ++c.c->knn_launches;
     tr.mark(c.s, "round: fused kNN");
     if (tr.on)
         std::fprintf(stderr, "[gtann]   pairs %.4g (own %d, probes %d, seeded %d), %.1f ms device\n", pr, own ? 1 : 0,
                      probes ? 1 : 0, seed_d ? 1 : 0, t * 1e3);
+    if (tr.on && a.stats) {
+        unsigned long long h[4];
+        c.d2h(h, a.stats, sizeof(h));
+        c.sync();
+        std::fprintf(stderr, "[gtann]   collect: %.3g keys (%.1f per query), %llu compactions, %.3g of %.3g wave tiles past the pre-filter\n",
+                     static_cast<double>(h[0]), static_cast<double>(h[0]) / static_cast<double>(N), h[1],
+                     static_cast<double>(h[2]), static_cast<double>(h[3]));
+    }
     if (max_pool) *max_pool = std::max(*max_pool, mp);
     if (max_bucket) *max_bucket = std::max(*max_bucket, mb);
     if (pairs) *pairs += pr;

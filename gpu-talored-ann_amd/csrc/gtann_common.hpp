@@ -71,7 +71,15 @@ struct KnnArgs {
     // on these rows (stride Dp bytes) and nq/np are their |x|^2
     const int8_t* Xq8;
     const int8_t* Xp8;
+    // collect launches (knn_collect.hip): the keys of a query at or below its
+    // threshold go to cand[row * kCollectCap ...), their number to cand_cnt[row]
+    uint64_t* cand;
+    int32_t* cand_cnt;
+    unsigned long long* stats;   // optional: [0] keys collected, [1] compactions, [2] tiles past the
+                                 // pre-filter, [3] tiles filtered (per wave)
 };
+
+constexpr int kCollectCap = 256;   // candidate slots per query of a collect launch
 
 // Arguments of the graph search kernel (one wave per query).
 struct SearchArgs {

@@ -1,0 +1,517 @@
+// knn_collect.hip -- per-bucket brute-force kNN on int8 rows as collect +
+// select, for lists of at most 64 keys (src/bucket.cu:4101-4265 top-M
+// semantics: self excluded, (-1, +inf) padding, ties by id).
+//
+// knn_i8_collect_kernel scans a tile of 128 queries against a pool slice like
+// knn_i8_kernel (int8 MFMA, LDS pool tiles, integer pre-filter) but keeps no
+// list: every key at or below the query's threshold is appended to the
+// query's candidate slots in HBM.  The threshold is the caller's cap (the
+// running M-th distance of a seeded pass) or, in an unseeded pass, a bound
+// taken from the first kWindow tiles of the scan: each lane keeps the 32
+// smallest distances among the pool rows it holds in those tiles (a sorting
+// network on registers), and the larger of the pair's ceil(M/2)-th smallest
+// bounds the pool's M-th smallest from above (those are M distinct rows).
+// The scan then visits the whole slice (the window's tiles last).  A query
+// whose slots fill up is compacted by its wave: the M-th smallest of its keys
+// is found by a radix descent over the 64 key bits, the keys above it are
+// dropped and it becomes the threshold.  The kept set always contains the
+// pool's M smallest keys at or below the cap, so the selection that follows
+// gives the same list as a scan that merges as it goes.
+//
+// knn_select_kernel sorts each query's candidates into its top-M list: two
+// lanes per query merge 32 keys at a time into a sorted register list
+// (pair_merge32).
+#include "knn_device.hpp"
+
+#include <cstdlib>
+
+namespace gtann {
+
+constexpr int kWindow = 16;   // tiles (of kPoolTile pool rows) of the unseeded threshold pass
+
+// Per-wave staging of a tile's candidates: every lane's 16 accumulators
+// (16-byte chunks swizzled by lane so that a wave's 128-bit stores spread
+// over the banks), one 16-bit code (lane << 4 | element) per accumulator at
+// or above its lane's pass floor, the wave's queries' slot counters and the
+// query state the dense pass reads.
+struct CollectWave {
+    int32_t stash[64 * 16];
+    uint16_t code[64 * 16];
+    int32_t qcnt[kQueriesPerWave];
+    float4 qst[kQueriesPerWave];          // |q|^2, threshold, threshold id (bits), self (bits)
+    int64_t qrow_out[kQueriesPerWave];    // output row
+};
+
+template <int DP>
+struct CollectSmem {
+    int8_t tile[2][kPoolTile][DP + 16];   // +16 bytes: rows land on distinct bank groups
+    float tnorm[3][kPoolTile];
+    int32_t trow[3][kPoolTile];
+    int32_t thalf[3][kPoolTile];          // accumulator start: -floor(|p|^2 / 2) (L2), 0 (IP), kHalfPast past the end
+    CollectWave wv[kWaves];
+};
+
+__device__ __forceinline__ int stash_index(int lane, int r)
+{
+    return lane * 16 + (((r >> 2) ^ ((lane >> 1) & 3)) << 2) + (r & 3);
+}
+
+// Per-lane view of one query (lanes j and j + 32 hold identical copies).
+struct CollectState {
+    float thr;          // a key passes iff (d, id) <= (thr, thr_id)
+    uint32_t thr_id;    // 0xffffffff: every id at distance thr
+    int32_t cnt;        // keys in the query's slots
+    int32_t self;       // id that must not be kept (the query itself), -2 if none
+    int64_t orow;       // output row
+};
+
+__device__ __forceinline__ bool key_passes(float d, int32_t id, const CollectState& st)
+{
+    return d < st.thr || (d == st.thr && static_cast<uint32_t>(id) <= st.thr_id);
+}
+
+// Keeps the M smallest of query q's cnt (> M) keys in its slots and makes the
+// M-th its threshold.  Called by all 64 lanes; q is uniform.
+__device__ __forceinline__ void collect_compact(const KnnArgs& a, int lane, int q, CollectState& st)
+{
+    const int cntq = __builtin_amdgcn_readlane(st.cnt, q);
+    const int64_t orow = static_cast<int64_t>(
+        (static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(st.orow >> 32), q))) << 32) |
+        static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(st.orow), q)));
+    uint64_t* slots = a.cand + orow * kCollectCap;
+    // the slots were stored by lanes q and q + 32: complete, then visible to
+    // the wave (workgroup-scope loads)
+    wait_vmem();
+    wave_sync();
+    constexpr int KPL = kCollectCap / 64;   // slots per lane
+    static_assert(kCollectCap % 64 == 0, "whole slots per lane");
+    uint64_t k[KPL];
+#pragma unroll
+    for (int i = 0; i < KPL; ++i)
+        k[i] = lane + 64 * i < cntq
+                   ? __hip_atomic_load(slots + lane + 64 * i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)
+                   : kNoKey;
+    // the M-th smallest key: the largest K with fewer than M keys below it
+    const int M = a.M;
+    uint64_t K = 0;
+    for (int b = 63; b >= 0; --b) {
+        const uint64_t t = K | (1ull << b);
+        int below = 0;
+#pragma unroll
+        for (int i = 0; i < KPL; ++i) below += __popcll(__ballot(k[i] < t));
+        if (below < M) K = t;
+    }
+    const uint64_t lt = (1ull << lane) - 1ull;
+    int base = 0;
+#pragma unroll
+    for (int i = 0; i < KPL; ++i) {
+        const bool p = k[i] <= K;
+        const uint64_t m = __ballot(p);
+        if (p) slots[base + __popcll(m & lt)] = k[i];
+        base += __popcll(m);
+    }
+    if ((lane & 31) == q) {
+        st.cnt = M;
+        st.thr = o2f(static_cast<uint32_t>(K >> 32));
+        st.thr_id = static_cast<uint32_t>(K);
+    }
+    if (a.stats && lane == 0) atomicAdd(a.stats + 1, 1ull);
+}
+
+// The query state the dense pass reads, published by lanes 0..31.
+__device__ __forceinline__ void publish_state(CollectWave& W, int lane, bool qvalid, float qn, const CollectState& st)
+{
+    if (lane < kQueriesPerWave) {
+        W.qst[lane] = make_float4(qn, qvalid ? st.thr : -INFINITY, __uint_as_float(st.thr_id), __int_as_float(st.self));
+        W.qrow_out[lane] = st.orow;
+    }
+}
+
+// One finished 32x32 tile of the collect scan: acc holds v = dot -
+// floor(|p|^2 / 2) (L2) or dot (IP) for the pool rows with norms tn, ids tr
+// and accumulator starts th (tile rows 8g + 4h + e in element 4g + e of lane
+// (j, h)).  Tiles with no v at the lane's pass floor lo are dropped.  For the
+// others the wave writes a code for every (lane, element) at or above the
+// floor (a ballot per element), and then all 64 lanes take one code each:
+// the exact distance, the exact test against the query's (threshold, id)
+// and the append to the query's slots (an LDS counter per query).  A query
+// that could overflow its slots in this tile (more than kCollectCap - 32
+// keys) is compacted first.
+template <int METRIC>
+__device__ __forceinline__ void collect_tile(const KnnArgs& a, CollectWave& W, const intx16& acc, const float* tn,
+                                             const int32_t* tr, const int32_t* th, int lane, bool qvalid, float qn,
+                                             CollectState& st, int32_t& lo)
+{
+    int32_t vmax = INT_MIN;
+#pragma unroll
+    for (int r = 0; r < 16; r += 2) vmax = max(vmax, max(acc[r], acc[r + 1]));
+    if (a.stats && lane == 0) atomicAdd(a.stats + 3, 1ull);
+    if (!__ballot(vmax >= lo)) return;
+    if (a.stats && lane == 0) atomicAdd(a.stats + 2, 1ull);
+    uint64_t need = __ballot(qvalid && st.cnt > kCollectCap - 2 * 16) & 0xffffffffull;
+    if (need) {
+        while (need) {
+            const int q = __ffsll(static_cast<unsigned long long>(need)) - 1;
+            need &= need - 1;
+            collect_compact(a, lane, q, st);
+        }
+        lo = i8_pass_floor<METRIC>(st.thr, qn);
+        publish_state(W, lane, qvalid, qn, st);
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+        *reinterpret_cast<int4*>(&W.stash[stash_index(lane, 4 * c)]) =
+            make_int4(acc[4 * c], acc[4 * c + 1], acc[4 * c + 2], acc[4 * c + 3]);
+    if (lane < kQueriesPerWave) W.qcnt[lane] = st.cnt;
+    int total = 0;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const uint64_t S = __ballot(acc[r] >= lo);
+        if (S) {
+            if (acc[r] >= lo) {
+                const int pos = total + static_cast<int>(__builtin_amdgcn_mbcnt_hi(
+                                            static_cast<uint32_t>(S >> 32),
+                                            __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(S), 0u)));
+                W.code[pos] = static_cast<uint16_t>((lane << 4) | r);
+            }
+            total += __popcll(S);
+        }
+    }
+    wave_sync();
+    for (int k = lane; k - lane < total; k += 64) {
+        if (k < total) {
+            const int code = W.code[k];
+            const int src = code >> 4, r = code & 15;
+            const int v = W.stash[stash_index(src, r)];
+            const int q = src & 31;
+            const int row = 8 * (r >> 2) + 4 * (src >> 5) + (r & 3);
+            const float pn = tn[row];
+            const int32_t id = tr[row];
+            const int32_t hv = th[row];
+            const float4 Q = W.qst[q];
+            const float dot = static_cast<float>(v - hv);
+            const float d = METRIC == 0 ? fmaf(-2.f, dot, pn + Q.x) : fmaf(-1.f, dot, pn);
+            const bool ok = id >= 0 && id != __float_as_int(Q.w) &&
+                            (d < Q.y || (d == Q.y && static_cast<uint32_t>(id) <= __float_as_uint(Q.z)));
+            if (ok) {
+                const int slot = atomicAdd(&W.qcnt[q], 1);
+                a.cand[W.qrow_out[q] * kCollectCap + slot] = pack_key(d, id);
+            }
+        }
+    }
+    wave_sync();
+    st.cnt = W.qcnt[lane & 31];
+}
+
+// The window pass's share of one finished tile: the lane's 16 distances
+// (the query itself and rows past the slice end at +inf) join its sorted 32
+// smallest.
+template <int METRIC>
+__device__ __forceinline__ void window_tile(const intx16& acc, const float* tn, const int32_t* tr, const int32_t* th,
+                                            int h, float qn, int32_t self, float (&T)[32])
+{
+    float s[16];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const float4 pn = *reinterpret_cast<const float4*>(tn + 8 * g + 4 * h);
+        const int4 pi = *reinterpret_cast<const int4*>(tr + 8 * g + 4 * h);
+        const int4 hv = *reinterpret_cast<const int4*>(th + 8 * g + 4 * h);
+        const float n4[4] = {pn.x, pn.y, pn.z, pn.w};
+        const int32_t i4[4] = {pi.x, pi.y, pi.z, pi.w};
+        const int32_t h4[4] = {hv.x, hv.y, hv.z, hv.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float dot = static_cast<float>(acc[4 * g + e] - h4[e]);
+            const float d = METRIC == 0 ? fmaf(-2.f, dot, n4[e] + qn) : fmaf(-1.f, dot, n4[e]);
+            s[4 * g + e] = (i4[e] < 0 || i4[e] == self) ? INFINITY : d;
+        }
+    }
+    oddeven_sort(s);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) T[16 + k] = fminf(T[16 + k], s[15 - k]);
+    bitonic_merge(T);
+}
+
+template <int DP, int METRIC>
+__global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(3)))
+knn_i8_collect_kernel(KnnArgs a)
+{
+    constexpr int KS = DP / 32;                     // MFMA steps per tile
+    constexpr int U4_ROW = DP / 16;                 // 16-byte pieces per row
+    constexpr int U4_TILE = kPoolTile * U4_ROW;
+    constexpr int U4_THREAD = (U4_TILE + 255) / 256;
+    static_assert(DP % 32 == 0, "row stride must be a multiple of 32 bytes");
+    __shared__ CollectSmem<DP> sm;
+
+    const int per = a.n_items / 8;
+    const int item_idx = static_cast<int>(blockIdx.x % 8) * per + static_cast<int>(blockIdx.x / 8);
+    if (item_idx >= a.n_items) return;
+    const WorkItem it = a.items[item_idx];
+    if (it.q_count <= 0) return;
+
+    const int tid = threadIdx.x;
+    const int w = tid >> 6, lane = tid & 63, j = lane & 31, h = lane >> 5;
+    const int qlocal = w * kQueriesPerWave + j;
+    const bool qvalid = qlocal < it.q_count;
+    const int64_t qi = it.q_begin + qlocal;
+    const int32_t qrow = qvalid ? (a.q_rows ? a.q_rows[qi] : static_cast<int32_t>(qi)) : 0;
+    const float qn = (qvalid && METRIC == 0) ? a.nq[qrow] : 0.f;
+
+    CollectState st;
+    float seed = FLT_MAX;
+    if (qvalid && a.seed_d) seed = fminf(a.seed_d[static_cast<int64_t>(qrow) * a.seed_ld + a.seed_ld - 1], FLT_MAX);
+    st.thr = qvalid ? seed : -INFINITY;
+    st.thr_id = 0xffffffffu;
+    st.cnt = 0;
+    st.self = a.exclude_self ? qrow : -2;
+    st.orow = it.out_base >= 0 ? it.out_base + qlocal : static_cast<int64_t>(qrow);
+
+    intx4 qf[KS];
+    {
+        const int8_t* qsrc = a.Xq8 + static_cast<int64_t>(qrow) * DP + 16 * h;   // qrow 0 if invalid
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+            const intx4 v = *reinterpret_cast<const intx4*>(qsrc + 32 * s);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) qf[s][e] = qvalid ? v[e] : 0;
+        }
+    }
+
+    CollectWave& W = sm.wv[w];
+    publish_state(W, lane, qvalid, qn, st);
+
+    const int pcount = it.p_count;
+    const int ntiles = (pcount + kPoolTile - 1) / kPoolTile;
+    // unseeded: the first nwin tiles bound the threshold, then every tile is
+    // scanned (the window's again, last)
+    const int nwin = a.seed_d ? 0 : min(kWindow, ntiles);
+    const int nstages = ntiles + nwin;
+    auto pool_row = [&](int p) -> int32_t {
+        if (p >= pcount) return -1;
+        p += it.p_rot;
+        if (p >= pcount) p -= pcount;
+        const int64_t pl = it.p_begin + p;
+        return a.p_rows ? a.p_rows[pl] : static_cast<int32_t>(pl);
+    };
+    auto tile_of = [&](int s) { return s < ntiles ? s : s - ntiles; };
+    auto row_norm = [&](int32_t row) -> float {
+        if (row < 0) return INFINITY;
+        return METRIC == 0 ? a.np[row] : 0.f;
+    };
+
+    int32_t idn[U4_THREAD];
+    uint4 pre[U4_THREAD];
+    int32_t rid_next = -1;
+    auto load_ids = [&](int s) {
+        const bool live = s < nstages;
+        const int t = live ? tile_of(s) : 0;
+#pragma unroll
+        for (int u = 0; u < U4_THREAD; ++u) {
+            const int e = tid + 256 * u;
+            idn[u] = (live && e < U4_TILE) ? pool_row(t * kPoolTile + e / U4_ROW) : -1;
+        }
+        if (tid < kPoolTile) rid_next = live ? pool_row(t * kPoolTile + tid) : -1;
+    };
+    auto load_rows = [&]() {
+#pragma unroll
+        for (int u = 0; u < U4_THREAD; ++u) {
+            const int e = tid + 256 * u;
+            const int32_t id = idn[u];
+            const uint4 v = *reinterpret_cast<const uint4*>(a.Xp8 + static_cast<int64_t>(id >= 0 ? id : 0) * DP +
+                                                            16 * (e % U4_ROW));
+            pre[u] = id >= 0 ? v : make_uint4(0u, 0u, 0u, 0u);
+        }
+    };
+    auto store_rows = [&](int buf) {
+#pragma unroll
+        for (int u = 0; u < U4_THREAD; ++u) {
+            const int e = tid + 256 * u;
+            if (e < U4_TILE) *reinterpret_cast<uint4*>(&sm.tile[buf][e / U4_ROW][16 * (e % U4_ROW)]) = pre[u];
+        }
+    };
+    auto row_half = [&](int32_t row, float rn) -> int32_t {
+        return row < 0 ? kHalfPast : -(static_cast<int32_t>(rn) >> 1);
+    };
+    if (tid < kPoolTile) { sm.tnorm[2][tid] = INFINITY; sm.trow[2][tid] = -1; sm.thalf[2][tid] = kHalfPast; }
+    load_ids(0);
+    load_rows();
+    int32_t rid_cur = rid_next;
+    float rn_cur = tid < kPoolTile ? row_norm(rid_cur) : 0.f;
+    store_rows(0);
+    if (tid < kPoolTile) { sm.trow[0][tid] = rid_cur; sm.tnorm[0][tid] = rn_cur; sm.thalf[0][tid] = row_half(rid_cur, rn_cur); }
+    load_ids(1);
+    __syncthreads();
+
+    intx16 acc_prev;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc_prev[r] = 0;
+    int32_t lo = i8_pass_floor<METRIC>(st.thr, qn);
+
+    // one stage: the MFMAs of stage s's tile, then filt(s - 1) on the tile
+    // before it (filtered while these MFMAs run)
+    auto stage = [&](int s, auto&& filt) {
+        const int buf = s & 1;
+        wait_vmem();
+        load_rows();
+        rid_cur = rid_next;
+        rn_cur = tid < kPoolTile ? row_norm(rid_cur) : 0.f;
+        load_ids(s + 2);
+
+        intx16 acc;
+        {
+            const int32_t* th = sm.thalf[s % 3];
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int4 hv = *reinterpret_cast<const int4*>(th + 8 * g + 4 * h);
+                acc[4 * g] = hv.x; acc[4 * g + 1] = hv.y; acc[4 * g + 2] = hv.z; acc[4 * g + 3] = hv.w;
+            }
+        }
+        const int8_t* arow = &sm.tile[buf][j][16 * h];
+#pragma unroll
+        for (int k = 0; k < KS; ++k) {
+            const intx4 av = *reinterpret_cast<const intx4*>(arow + 32 * k);
+            acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, qf[k], acc, 0, 0, 0);
+        }
+        if (s > 0) filt(s - 1);
+        acc_prev = acc;
+
+        store_rows(buf ^ 1);
+        if (tid < kPoolTile) {
+            sm.trow[(s + 1) % 3][tid] = rid_cur;
+            sm.tnorm[(s + 1) % 3][tid] = rn_cur;
+            sm.thalf[(s + 1) % 3][tid] = row_half(rid_cur, rn_cur);
+        }
+        __syncthreads();
+    };
+    auto collect = [&](int s) {
+        const int slot3 = s % 3;
+        collect_tile<METRIC>(a, W, acc_prev, sm.tnorm[slot3], sm.trow[slot3], sm.thalf[slot3], lane, qvalid, qn, st,
+                             lo);
+    };
+    // the window's stages (stage nwin filters its last tile), then the rest
+    const int s_win = min(nwin + 1, nstages);
+    {
+        float T[32];
+#pragma unroll
+        for (int i = 0; i < 32; ++i) T[i] = INFINITY;
+        auto window = [&](int s) {
+            const int slot3 = s % 3;
+            window_tile<METRIC>(acc_prev, sm.tnorm[slot3], sm.trow[slot3], sm.thalf[slot3], h, qn, st.self, T);
+            if (s == nwin - 1) {
+                // the pair's ceil(M/2)-th smallest distances: M distinct rows at or below the larger
+                const int m = (a.M + 1) / 2 - 1;
+                float v = T[0];
+#pragma unroll
+                for (int i = 1; i < 32; ++i) v = i == m ? T[i] : v;
+                const float bound = fmaxf(v, __shfl_xor(v, 32));
+                if (qvalid && bound < st.thr) st.thr = bound;
+                lo = i8_pass_floor<METRIC>(st.thr, qn);
+                publish_state(W, lane, qvalid, qn, st);
+            }
+        };
+        for (int s = 0; s < s_win; ++s) stage(s, window);
+    }
+    for (int s = s_win; s < nstages; ++s) stage(s, collect);
+    if (nstages > 0) collect(nstages - 1);   // nstages - 1 >= nwin
+    if (qvalid && h == 0) a.cand_cnt[st.orow] = st.cnt;
+    if (a.stats && qvalid && h == 0) atomicAdd(a.stats, static_cast<unsigned long long>(st.cnt));
+}
+
+// ------------------------------------------------------------ selection
+
+// Each row's top-M of its cnt[row] candidate keys, ascending, into (out_ids,
+// out_d) (padding -1 / +inf).  Two lanes per row, 128 rows per block.
+template <int LM>
+__global__ void __launch_bounds__(256) knn_select_kernel(const uint64_t* __restrict__ cand,
+                                                         const int32_t* __restrict__ cnt, int64_t rows, int M,
+                                                         int32_t* __restrict__ out_ids, float* __restrict__ out_d)
+{
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, h = lane >> 5;
+    const int64_t row = (static_cast<int64_t>(blockIdx.x) * kWaves + w) * kQueriesPerWave + (lane & 31);
+    const bool valid = row < rows;
+    const int n = valid ? min(cnt[row], kCollectCap) : 0;
+    PairList<LM> PL;
+#pragma unroll
+    for (int i = 0; i < LM; ++i) PL.k[i] = kNoKey;
+    const uint64_t* src = cand + (valid ? row : 0) * kCollectCap + 16 * h;
+    for (int c0 = 0; __ballot(c0 < n); c0 += 32) {
+        uint64_t b[16];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int i = c0 + 16 * h + 2 * e;
+            if (i + 1 < n) {
+                const uint4 x = *reinterpret_cast<const uint4*>(src + c0 + 2 * e);
+                b[2 * e] = (static_cast<uint64_t>(x.y) << 32) | x.x;
+                b[2 * e + 1] = (static_cast<uint64_t>(x.w) << 32) | x.z;
+            } else {
+                b[2 * e] = i < n ? src[c0 + 2 * e] : kNoKey;
+                b[2 * e + 1] = kNoKey;
+            }
+        }
+        pair_merge32<LM>(b, PL, h != 0);
+    }
+    if (!valid) return;
+    int32_t* oi = out_ids + row * M;
+    float* od = out_d + row * M;
+#pragma unroll
+    for (int i = 0; i < LM; ++i) {
+        const int p = LM * h + i;
+        if (p < M) {
+            const uint64_t k = PL.k[i];
+            oi[p] = k == kNoKey ? -1 : static_cast<int32_t>(static_cast<uint32_t>(k));
+            od[p] = k == kNoKey ? INFINITY : o2f(static_cast<uint32_t>(k >> 32));
+        }
+    }
+}
+
+// ------------------------------------------------------------ host side
+
+// GTANN_KNN_COLLECT=0 keeps the merging kernel for every list (same results)
+bool knn_collect_supported(const KnnArgs& a)
+{
+    const char* e = std::getenv("GTANN_KNN_COLLECT");
+    if (e && e[0] == '0') return false;
+    return a.Xq8 && a.Xp8 && a.M > 4 && a.M <= 64 && a.out_pos == 0 && a.Dp <= 256 && a.Dp % 32 == 0;
+}
+
+template <int METRIC>
+static void launch_collect_metric(const KnnArgs& a, dim3 grid, hipStream_t stream)
+{
+    switch (a.Dp) {
+    case 32:  hipLaunchKernelGGL((knn_i8_collect_kernel<32, METRIC>), grid, dim3(256), 0, stream, a); break;
+    case 64:  hipLaunchKernelGGL((knn_i8_collect_kernel<64, METRIC>), grid, dim3(256), 0, stream, a); break;
+    case 96:  hipLaunchKernelGGL((knn_i8_collect_kernel<96, METRIC>), grid, dim3(256), 0, stream, a); break;
+    case 128: hipLaunchKernelGGL((knn_i8_collect_kernel<128, METRIC>), grid, dim3(256), 0, stream, a); break;
+    case 160: hipLaunchKernelGGL((knn_i8_collect_kernel<160, METRIC>), grid, dim3(256), 0, stream, a); break;
+    case 192: hipLaunchKernelGGL((knn_i8_collect_kernel<192, METRIC>), grid, dim3(256), 0, stream, a); break;
+    case 224: hipLaunchKernelGGL((knn_i8_collect_kernel<224, METRIC>), grid, dim3(256), 0, stream, a); break;
+    case 256: hipLaunchKernelGGL((knn_i8_collect_kernel<256, METRIC>), grid, dim3(256), 0, stream, a); break;
+    default: GT_REQUIRE(false, "collect kernel: padded dimension " + std::to_string(a.Dp) + " not supported");
+    }
+}
+
+// Every output row in [0, rows) must be the output row of exactly one query
+// of the launch (cand_cnt is read for all of them).
+void launch_knn_collect_select(const KnnArgs& a, int64_t rows, hipStream_t stream)
+{
+    GT_REQUIRE(knn_collect_supported(a), "collect launch: int8 rows, 4 < M <= 64");
+    GT_REQUIRE(a.cand && a.cand_cnt && a.out_ids && a.out_d, "collect launch: buffers missing");
+    GT_REQUIRE(a.n_items % 8 == 0, "work list must be padded to a multiple of 8");
+    if (a.n_items > 0) {
+        const dim3 grid(static_cast<unsigned>(a.n_items));
+        if (a.metric == 0) launch_collect_metric<0>(a, grid, stream);
+        else launch_collect_metric<1>(a, grid, stream);
+        GT_HIP(hipGetLastError());
+    }
+    if (rows <= 0) return;
+    const dim3 sgrid(static_cast<unsigned>(ceil_div(rows, kQueriesPerBlock)));
+    if (a.M <= 32)
+        hipLaunchKernelGGL((knn_select_kernel<16>), sgrid, dim3(256), 0, stream, a.cand, a.cand_cnt, rows, a.M,
+                           a.out_ids, a.out_d);
+    else
+        hipLaunchKernelGGL((knn_select_kernel<32>), sgrid, dim3(256), 0, stream, a.cand, a.cand_cnt, rows, a.M,
+                           a.out_ids, a.out_d);
+    GT_HIP(hipGetLastError());
+}
+
+}  // namespace gtann

@@ -13,7 +13,7 @@
 // excluded, padding is (-1, +inf), distance reported = |q|^2 + |p|^2 - 2 q.p.
 // Ties are ordered by id (total order (key, id)), so the kept set and its
 // order are unique.
-#include "gtann_common.hpp"
+#include "knn_device.hpp"
 
 #include <cfloat>
 #include <climits>
@@ -21,7 +21,6 @@
 
 namespace gtann {
 
-typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int kCB = 32;      // candidate-buffer slots per query (>= 32 = one tile's worth per query)
 constexpr int kMaxM = 128;   // longest list the kernel keeps
@@ -78,10 +77,6 @@ struct QueryState {
     int64_t orow;  // output row
 };
 
-// Waits until every vector memory access of this wave has completed: the
-// list rows a merge stores are loaded again by the next merge of the same
-// query, which always comes after one of these waits (tile start, flush).
-__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }   // vmcnt(0)
 
 // A list row is only ever stored and loaded by the one wave that owns its
 // query, on one CU: workgroup-scope loads see those stores once they have
@@ -664,8 +659,6 @@ __global__ void __launch_bounds__(256, 2) knn_fused_kernel(KnnArgs a)
 // step s (the pool rows in LDS are read with the same split), so the two
 // half-waves cover the row between them.  Keys are exact: |p|^2 + |q|^2 -
 // 2 p.q < 2^24.  Filtering, appends and merges are the fp32 kernel's.
-typedef int intx4 __attribute__((ext_vector_type(4)));
-typedef int intx16 __attribute__((ext_vector_type(16)));
 
 // Pool rows per stage (one barrier, one load round trip): with register
 // short lists a 32x32 tile is a few MFMAs and no LDS list work, too short to
@@ -684,26 +677,7 @@ struct KnnSmemI8Tiles {
     int32_t thalf[3][ROWS];          // accumulator start: -floor(|p|^2 / 2) (L2), 0 (IP), kHalfPast past the end
 };
 
-// Accumulator start of a row past the slice end: no dot product (|dot| <
-// 2^22) lifts it to a query's pass floor.
-constexpr int32_t kHalfPast = -(1 << 30);
 
-// Integer pre-filter of the int8 kernel.  Every distance of that kernel is
-// an exact integer below 2^24 (int8 rows, int32 sums, |p|^2 and |q|^2 exact in
-// fp32), and its MFMA accumulators start at -floor(|p|^2 / 2), so they end at
-// v = dot - floor(|p|^2 / 2).  With T = thr - |q|^2, a row passes (L2) iff
-// |p|^2 - 2 dot <= T, i.e. 2v - (|p|^2 mod 2) >= -T, which implies
-// v >= -floor(T / 2): a tile none of whose v reach that floor holds no row
-// that passes.  For the inner product d = -dot = -v, and a row passes iff
-// v >= -thr.  No cap yet (FLT_MAX): every v passes; an invalid query (-inf):
-// none does.
-template <int METRIC>
-__device__ __forceinline__ int32_t i8_pass_floor(float thr, float qn)
-{
-    if (thr > 6.0e7f) return INT_MIN;
-    if (thr < -6.0e7f) return INT_MAX;
-    return METRIC == 0 ? -static_cast<int32_t>(floorf((thr - qn) * 0.5f)) : -static_cast<int32_t>(floorf(thr));
-}
 
 template <int DP, bool LISTS>
 struct KnnSmemI8 : KnnSmemI8Tiles<DP, I8Stage<DP, !LISTS>::ROWS> {

@@ -1,0 +1,148 @@
+"""The collect + select kNN path (int8 rows, 4 < M <= 64) against the CPU
+oracle and against the merging kernel.
+
+The bucketed passes on int8 rows append every key at or below a query's
+threshold to its candidate slots and select the top-M afterwards; the
+threshold of an unseeded pass comes from the scan's first tiles, and a query
+whose slots fill up is compacted to its M smallest keys.  Integer rows give
+exact distances, so every comparison here is bit-exact, ties included
+(order (distance, id)).
+"""
+import os
+
+import numpy as np
+import pytest
+
+import gt_oracle as O
+from helpers import assert_knn_equal
+
+pytestmark = pytest.mark.gpu
+
+
+def _data(n, d, seed, lo=-128, hi=128):
+    return np.random.default_rng(seed).integers(lo, hi, size=(n, d)).astype(np.int8)
+
+
+def _buckets(rng, N, B, sizes=None):
+    if sizes is None:
+        lab = rng.integers(0, B, size=N)
+        lab[:B] = np.arange(B)
+    else:
+        lab = np.repeat(np.arange(B), sizes)
+        rng.shuffle(lab)
+    order = np.argsort(lab, kind="stable")
+    off = np.zeros(B + 1, np.int64)
+    np.add.at(off, lab + 1, 1)
+    return np.cumsum(off), order.astype(np.int32)
+
+
+def _probe(rng, B, P):
+    if P == 0:
+        return np.zeros((B, 0), np.int32)
+    return np.stack([rng.permutation(np.delete(np.arange(B), b))[:P] for b in range(B)]).astype(np.int32)
+
+
+@pytest.mark.parametrize("N,D,B,P,M,metric", [
+    (6000, 128, 6, 0, 64, "l2"),     # own buckets only, pools of ~1000 rows
+    (6000, 128, 6, 1, 64, "l2"),
+    (5000, 96, 8, 2, 48, "l2"),
+    (4000, 32, 5, 1, 17, "l2"),      # M <= 32: 16-key lanes
+    (3000, 256, 4, 0, 32, "l2"),
+    (3000, 64, 12, 0, 5, "l2"),
+    (4000, 128, 6, 1, 64, "ip"),
+    (3000, 96, 5, 0, 33, "ip"),
+])
+def test_collect_unseeded_matches_oracle(ctx, N, D, B, P, M, metric):
+    rng = np.random.default_rng(N + D + M)
+    X = _data(N, D, seed=D + M)
+    off, mem = _buckets(rng, N, B)
+    probe = _probe(rng, B, P)
+    print(f"collect unseeded N={N} D={D} B={B} P={P} M={M} {metric}", flush=True)
+    ids, dist = ctx.knn_bucketed(X, off, mem, probe, M, metric=metric)
+    ri, rd = O.knn_bucketed(X.astype(np.float32), off, mem, probe, M, metric=1 if metric == "ip" else 0)
+    got_d = -dist if metric == "ip" else dist
+    assert_knn_equal(ids, got_d, ri, rd)
+
+
+def test_collect_small_and_tiny_buckets(ctx):
+    # pools shorter than the threshold window, shorter than M, a single row
+    rng = np.random.default_rng(5)
+    sizes = [1, 2, 30, 63, 64, 65, 200, 257, 900, 2000]
+    N = sum(sizes)
+    X = _data(N, 128, seed=6)
+    off, mem = _buckets(rng, N, len(sizes), sizes)
+    for P in (0, 1):
+        probe = _probe(rng, len(sizes), P)
+        print(f"collect small buckets P={P}", flush=True)
+        ids, dist = ctx.knn_bucketed(X, off, mem, probe, 64)
+        ri, rd = O.knn_bucketed(X.astype(np.float32), off, mem, probe, 64)
+        assert_knn_equal(ids, dist, ri, rd)
+
+
+def test_collect_ties_and_duplicates(ctx):
+    # rows over {0, 1}: few distinct distances, many duplicates at distance 0;
+    # the kept set and its order are decided by ids at every threshold
+    rng = np.random.default_rng(7)
+    N = 5000
+    X = _data(N, 32, seed=8, lo=0, hi=2)
+    X[100:400] = X[99]          # 301 copies of one row
+    off, mem = _buckets(rng, N, 4)
+    probe = _probe(rng, 4, 1)
+    print("collect ties", flush=True)
+    ids, dist = ctx.knn_bucketed(X, off, mem, probe, 64)
+    ri, rd = O.knn_bucketed(X.astype(np.float32), off, mem, probe, 64)
+    np.testing.assert_array_equal(ids, ri)
+    np.testing.assert_array_equal(dist, rd)
+
+
+def test_collect_seeded_without_cap_compacts(ctx):
+    # a running table of padding seeds every query with +inf: every pool row
+    # passes and each query's slots are compacted many times
+    rng = np.random.default_rng(9)
+    N, B, M = 8000, 4, 64
+    X = _data(N, 128, seed=10)
+    off, mem = _buckets(rng, N, B)
+    probe = _probe(rng, B, 1)
+    run = (np.full((N, M), -1, np.int32), np.full((N, M), np.inf, np.float32))
+    print("collect seeded with +inf", flush=True)
+    ids, dist = ctx.knn_bucketed(X, off, mem, probe, M, running=run)
+    ri, rd = O.knn_bucketed(X.astype(np.float32), off, mem, probe, M)
+    assert_knn_equal(ids, dist, ri, rd)
+
+
+def test_collect_rounds_match_oracle(ctx):
+    rng = np.random.default_rng(13)
+    N, B, M = 6000, 8, 64
+    X = _data(N, 128, seed=14, lo=-30, hi=31)
+    Xf = X.astype(np.float32)
+    run = ref = None
+    for r in range(3):
+        off, mem = _buckets(rng, N, B)
+        probe = _probe(rng, B, 1)
+        print(f"collect round {r}", flush=True)
+        ids, dist = ctx.knn_bucketed(X, off, mem, probe, M, running=run)
+        ni, nd = O.knn_bucketed(Xf, off, mem, probe, M)
+        ref = (ni, nd) if ref is None else O.merge_rounds(*ref, ni, nd)
+        run = (ids, dist)
+        assert_knn_equal(ids, dist, *ref)
+
+
+def test_collect_equals_merging_kernel(ctx):
+    # the same passes through the kernel that merges as it scans
+    rng = np.random.default_rng(15)
+    N, B, M = 20000, 16, 64
+    X = _data(N, 128, seed=16, lo=-60, hi=61)
+    off, mem = _buckets(rng, N, B)
+    probe = _probe(rng, B, 1)
+    a = ctx.knn_bucketed(X, off, mem, probe, M)
+    b2 = ctx.knn_bucketed(X, off, mem, probe, M, running=a)
+    os.environ["GTANN_KNN_COLLECT"] = "0"
+    try:
+        print("merging kernel", flush=True)
+        c = ctx.knn_bucketed(X, off, mem, probe, M)
+        c2 = ctx.knn_bucketed(X, off, mem, probe, M, running=c)
+    finally:
+        del os.environ["GTANN_KNN_COLLECT"]
+    for x, y in ((a, c), (b2, c2)):
+        np.testing.assert_array_equal(x[0], y[0])
+        np.testing.assert_array_equal(x[1], y[1])
