@@ -32,11 +32,13 @@ constexpr int kWindow = 16;   // tiles (of kPoolTile pool rows) of the unseeded 
 // Per-wave staging of a tile's candidates: every lane's 16 accumulators
 // (16-byte chunks swizzled by lane so that a wave's 128-bit stores spread
 // over the banks), one 16-bit code (lane << 4 | element) per accumulator at
-// or above its lane's pass floor, the wave's queries' slot counters and the
-// query state the dense pass reads.
+// or above its lane's pass floor (plus a spare slot per lane), the wave's
+// queries' slot counters and the query state the dense pass reads.
+constexpr int kCodeSpare = 64 * 16;   // first of the 64 per-lane spare code slots
+
 struct CollectWave {
     int32_t stash[64 * 16];
-    uint16_t code[64 * 16];
+    uint16_t code[kCodeSpare + 64];
     int32_t qcnt[kQueriesPerWave];
     float4 qst[kQueriesPerWave];          // |q|^2, threshold, threshold id (bits), self (bits)
     int64_t qrow_out[kQueriesPerWave];    // output row
@@ -132,7 +134,8 @@ __device__ __forceinline__ void publish_state(CollectWave& W, int lane, bool qva
 // and accumulator starts th (tile rows 8g + 4h + e in element 4g + e of lane
 // (j, h)).  Tiles with no v at the lane's pass floor lo are dropped.  For the
 // others the wave writes a code for every (lane, element) at or above the
-// floor (a ballot per element), and then all 64 lanes take one code each:
+// floor (a prefix sum of the lanes' counts places them), and then all 64
+// lanes take one code each:
 // the exact distance, the exact test against the query's (threshold, id)
 // and the append to the query's slots (an LDS counter per query).  A query
 // that could overflow its slots in this tile (more than kCollectCap - 32
@@ -145,9 +148,7 @@ __device__ __forceinline__ void collect_tile(const KnnArgs& a, CollectWave& W, c
     int32_t vmax = INT_MIN;
 #pragma unroll
     for (int r = 0; r < 16; r += 2) vmax = max(vmax, max(acc[r], acc[r + 1]));
-    if (a.stats && lane == 0) atomicAdd(a.stats + 3, 1ull);
     if (!__ballot(vmax >= lo)) return;
-    if (a.stats && lane == 0) atomicAdd(a.stats + 2, 1ull);
     uint64_t need = __ballot(qvalid && st.cnt > kCollectCap - 2 * 16) & 0xffffffffull;
     if (need) {
         while (need) {
@@ -163,19 +164,20 @@ __device__ __forceinline__ void collect_tile(const KnnArgs& a, CollectWave& W, c
         *reinterpret_cast<int4*>(&W.stash[stash_index(lane, 4 * c)]) =
             make_int4(acc[4 * c], acc[4 * c + 1], acc[4 * c + 2], acc[4 * c + 3]);
     if (lane < kQueriesPerWave) W.qcnt[lane] = st.cnt;
-    int total = 0;
+    // codes in lane order, branch-free: each lane's candidates go to
+    // [its exclusive prefix, + its count), the other elements to the lane's
+    // spare slot
+    int c = 0;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) c += acc[r] >= lo ? 1 : 0;
+    const int incl = wave_incl_scan(c);
+    const int total = __builtin_amdgcn_readlane(incl, 63);
+    int pos = incl - c;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-        const uint64_t S = __ballot(acc[r] >= lo);
-        if (S) {
-            if (acc[r] >= lo) {
-                const int pos = total + static_cast<int>(__builtin_amdgcn_mbcnt_hi(
-                                            static_cast<uint32_t>(S >> 32),
-                                            __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(S), 0u)));
-                W.code[pos] = static_cast<uint16_t>((lane << 4) | r);
-            }
-            total += __popcll(S);
-        }
+        const bool p = acc[r] >= lo;
+        W.code[p ? pos : kCodeSpare + lane] = static_cast<uint16_t>((lane << 4) | r);
+        pos += p ? 1 : 0;
     }
     wave_sync();
     for (int k = lane; k - lane < total; k += 64) {
@@ -332,26 +334,31 @@ knn_i8_collect_kernel(KnnArgs a)
     auto row_half = [&](int32_t row, float rn) -> int32_t {
         return row < 0 ? kHalfPast : -(static_cast<int32_t>(rn) >> 1);
     };
-    if (tid < kPoolTile) { sm.tnorm[2][tid] = INFINITY; sm.trow[2][tid] = -1; sm.thalf[2][tid] = kHalfPast; }
     load_ids(0);
     load_rows();
     int32_t rid_cur = rid_next;
     float rn_cur = tid < kPoolTile ? row_norm(rid_cur) : 0.f;
-    store_rows(0);
-    if (tid < kPoolTile) { sm.trow[0][tid] = rid_cur; sm.tnorm[0][tid] = rn_cur; sm.thalf[0][tid] = row_half(rid_cur, rn_cur); }
     load_ids(1);
-    __syncthreads();
 
     intx16 acc_prev;
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc_prev[r] = 0;
     int32_t lo = i8_pass_floor<METRIC>(st.thr, qn);
 
-    // one stage: the MFMAs of stage s's tile, then filt(s - 1) on the tile
-    // before it (filtered while these MFMAs run)
+    // one stage: stage s's rows and norms (requested one stage earlier) into
+    // LDS, the barrier, the requests for stage s + 1 (and the pool ids of
+    // s + 2), then the MFMAs of stage s's tile with filt(s - 1) on the tile
+    // before it.  A request is waited for only at the next stage's top, a
+    // whole stage of MFMAs and filtering later.
     auto stage = [&](int s, auto&& filt) {
-        const int buf = s & 1;
-        wait_vmem();
+        const int buf = s & 1, slot = s % 3;
+        store_rows(buf);
+        if (tid < kPoolTile) {
+            sm.trow[slot][tid] = rid_cur;
+            sm.tnorm[slot][tid] = rn_cur;
+            sm.thalf[slot][tid] = row_half(rid_cur, rn_cur);
+        }
+        __syncthreads();
         load_rows();
         rid_cur = rid_next;
         rn_cur = tid < kPoolTile ? row_norm(rid_cur) : 0.f;
@@ -359,7 +366,7 @@ knn_i8_collect_kernel(KnnArgs a)
 
         intx16 acc;
         {
-            const int32_t* th = sm.thalf[s % 3];
+            const int32_t* th = sm.thalf[slot];
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const int4 hv = *reinterpret_cast<const int4*>(th + 8 * g + 4 * h);
@@ -374,14 +381,6 @@ knn_i8_collect_kernel(KnnArgs a)
         }
         if (s > 0) filt(s - 1);
         acc_prev = acc;
-
-        store_rows(buf ^ 1);
-        if (tid < kPoolTile) {
-            sm.trow[(s + 1) % 3][tid] = rid_cur;
-            sm.tnorm[(s + 1) % 3][tid] = rn_cur;
-            sm.thalf[(s + 1) % 3][tid] = row_half(rid_cur, rn_cur);
-        }
-        __syncthreads();
     };
     auto collect = [&](int s) {
         const int slot3 = s % 3;

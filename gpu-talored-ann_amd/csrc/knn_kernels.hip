@@ -91,19 +91,6 @@ __device__ __forceinline__ int32_t load_list_i(const int32_t* p)
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
-// Inclusive prefix sum across the 64 lanes: row shifts by 1, 2, 4 and 8 sum
-// within each row of 16 lanes, then rows 1 and 3 add the last lane of the row
-// before them, rows 2 and 3 the last lane of row 1.
-__device__ __forceinline__ int wave_incl_scan(int x)
-{
-    x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);   // row_shr:1
-    x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);   // row_shr:2
-    x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);   // row_shr:4
-    x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);   // row_shr:8
-    x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);   // row_bcast:15
-    x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);   // row_bcast:31
-    return x;
-}
 
 // Merges the buffer of query q (0..31 of this wave) into its sorted list
 // (output row) and recomputes its threshold.  A buffer entry goes to its rank
