@@ -288,40 +288,38 @@ knn_i8_collect_kernel(KnnArgs a)
     // scanned (the window's again, last)
     const int nwin = a.seed_d ? 0 : min(kWindow, ntiles);
     const int nstages = ntiles + nwin;
-    auto pool_row = [&](int p) -> int32_t {
-        if (p >= pcount) return -1;
-        p += it.p_rot;
+    // Every thread issues the same loads in every stage (positions past the
+    // slice end are clamped to its last row and flagged), so the compiler
+    // can wait for one stage's loads without draining the next's.  The pool
+    // list is the caller's (launch_knn_collect_select requires one).
+    auto pool_pos = [&](int p) -> int64_t {
+        p = min(p, pcount - 1) + it.p_rot;
         if (p >= pcount) p -= pcount;
-        const int64_t pl = it.p_begin + p;
-        return a.p_rows ? a.p_rows[pl] : static_cast<int32_t>(pl);
+        return it.p_begin + p;
     };
     auto tile_of = [&](int s) { return s < ntiles ? s : s - ntiles; };
-    auto row_norm = [&](int32_t row) -> float {
-        if (row < 0) return INFINITY;
-        return METRIC == 0 ? a.np[row] : 0.f;
-    };
 
     int32_t idn[U4_THREAD];
     uint4 pre[U4_THREAD];
-    int32_t rid_next = -1;
+    int32_t rid_next = 0;    // this thread's tile row (threads < kPoolTile), a valid row id
+    bool rvalid_next = false;
     auto load_ids = [&](int s) {
         const bool live = s < nstages;
         const int t = live ? tile_of(s) : 0;
 #pragma unroll
         for (int u = 0; u < U4_THREAD; ++u) {
-            const int e = tid + 256 * u;
-            idn[u] = (live && e < U4_TILE) ? pool_row(t * kPoolTile + e / U4_ROW) : -1;
+            const int e = min(tid + 256 * u, U4_TILE - 1);
+            idn[u] = a.p_rows[pool_pos(t * kPoolTile + e / U4_ROW)];
         }
-        if (tid < kPoolTile) rid_next = live ? pool_row(t * kPoolTile + tid) : -1;
+        const int r = tid & (kPoolTile - 1);
+        rid_next = a.p_rows[pool_pos(t * kPoolTile + r)];
+        rvalid_next = live && t * kPoolTile + r < pcount;
     };
     auto load_rows = [&]() {
 #pragma unroll
         for (int u = 0; u < U4_THREAD; ++u) {
-            const int e = tid + 256 * u;
-            const int32_t id = idn[u];
-            const uint4 v = *reinterpret_cast<const uint4*>(a.Xp8 + static_cast<int64_t>(id >= 0 ? id : 0) * DP +
-                                                            16 * (e % U4_ROW));
-            pre[u] = id >= 0 ? v : make_uint4(0u, 0u, 0u, 0u);
+            const int e = min(tid + 256 * u, U4_TILE - 1);
+            pre[u] = *reinterpret_cast<const uint4*>(a.Xp8 + static_cast<int64_t>(idn[u]) * DP + 16 * (e % U4_ROW));
         }
     };
     auto store_rows = [&](int buf) {
@@ -331,13 +329,11 @@ knn_i8_collect_kernel(KnnArgs a)
             if (e < U4_TILE) *reinterpret_cast<uint4*>(&sm.tile[buf][e / U4_ROW][16 * (e % U4_ROW)]) = pre[u];
         }
     };
-    auto row_half = [&](int32_t row, float rn) -> int32_t {
-        return row < 0 ? kHalfPast : -(static_cast<int32_t>(rn) >> 1);
-    };
     load_ids(0);
     load_rows();
     int32_t rid_cur = rid_next;
-    float rn_cur = tid < kPoolTile ? row_norm(rid_cur) : 0.f;
+    bool rvalid_cur = rvalid_next;
+    float rn_cur = METRIC == 0 ? a.np[rid_cur] : 0.f;
     load_ids(1);
 
     intx16 acc_prev;
@@ -354,14 +350,17 @@ knn_i8_collect_kernel(KnnArgs a)
         const int buf = s & 1, slot = s % 3;
         store_rows(buf);
         if (tid < kPoolTile) {
-            sm.trow[slot][tid] = rid_cur;
-            sm.tnorm[slot][tid] = rn_cur;
-            sm.thalf[slot][tid] = row_half(rid_cur, rn_cur);
+            // rows past the slice end: id -1, norm +inf, accumulator start
+            // kHalfPast keep them out of every result
+            sm.trow[slot][tid] = rvalid_cur ? rid_cur : -1;
+            sm.tnorm[slot][tid] = rvalid_cur ? rn_cur : INFINITY;
+            sm.thalf[slot][tid] = rvalid_cur ? -(static_cast<int32_t>(rn_cur) >> 1) : kHalfPast;
         }
         __syncthreads();
         load_rows();
         rid_cur = rid_next;
-        rn_cur = tid < kPoolTile ? row_norm(rid_cur) : 0.f;
+        rvalid_cur = rvalid_next;
+        rn_cur = METRIC == 0 ? a.np[rid_cur] : 0.f;
         load_ids(s + 2);
 
         intx16 acc;
@@ -494,7 +493,7 @@ static void launch_collect_metric(const KnnArgs& a, dim3 grid, hipStream_t strea
 void launch_knn_collect_select(const KnnArgs& a, int64_t rows, hipStream_t stream)
 {
     GT_REQUIRE(knn_collect_supported(a), "collect launch: int8 rows, 4 < M <= 64");
-    GT_REQUIRE(a.cand && a.cand_cnt && a.out_ids && a.out_d, "collect launch: buffers missing");
+    GT_REQUIRE(a.cand && a.cand_cnt && a.out_ids && a.out_d && a.p_rows, "collect launch: buffers missing");
     GT_REQUIRE(a.n_items % 8 == 0, "work list must be padded to a multiple of 8");
     if (a.n_items > 0) {
         const dim3 grid(static_cast<unsigned>(a.n_items));
