@@ -44,12 +44,15 @@ struct CollectWave {
     int64_t qrow_out[kQueriesPerWave];    // output row
 };
 
+constexpr int kStageTiles = 2;                       // tiles (of kPoolTile pool rows) per pipeline stage
+constexpr int kStageRows = kPoolTile * kStageTiles;
+
 template <int DP>
 struct CollectSmem {
-    int8_t tile[2][kPoolTile][DP + 16];   // +16 bytes: rows land on distinct bank groups
-    float tnorm[3][kPoolTile];
-    int32_t trow[3][kPoolTile];
-    int32_t thalf[3][kPoolTile];          // accumulator start: -floor(|p|^2 / 2) (L2), 0 (IP), kHalfPast past the end
+    int8_t tile[2][kStageRows][DP + 16];   // +16 bytes: rows land on distinct bank groups
+    float tnorm[3][kStageRows];
+    int32_t trow[3][kStageRows];
+    int32_t thalf[3][kStageRows];          // accumulator start: -floor(|p|^2 / 2) (L2), 0 (IP), kHalfPast past the end
     CollectWave wv[kWaves];
 };
 
@@ -240,9 +243,11 @@ knn_i8_collect_kernel(KnnArgs a)
 {
     constexpr int KS = DP / 32;                     // MFMA steps per tile
     constexpr int U4_ROW = DP / 16;                 // 16-byte pieces per row
-    constexpr int U4_TILE = kPoolTile * U4_ROW;
-    constexpr int U4_THREAD = (U4_TILE + 255) / 256;
+    constexpr int ROWS = kStageRows;
+    constexpr int U4_STAGE = ROWS * U4_ROW;
+    constexpr int U4_THREAD = (U4_STAGE + 255) / 256;
     static_assert(DP % 32 == 0, "row stride must be a multiple of 32 bytes");
+    static_assert(ROWS <= 256 && kWindow % kStageTiles == 0, "stage shape");
     __shared__ CollectSmem<DP> sm;
 
     const int per = a.n_items / 8;
@@ -282,52 +287,55 @@ knn_i8_collect_kernel(KnnArgs a)
     CollectWave& W = sm.wv[w];
     publish_state(W, lane, qvalid, qn, st);
 
+    // stages of ROWS pool rows; unseeded, the first nws stages bound the
+    // threshold and are scanned again at the end
     const int pcount = it.p_count;
-    const int ntiles = (pcount + kPoolTile - 1) / kPoolTile;
-    // unseeded: the first nwin tiles bound the threshold, then every tile is
-    // scanned (the window's again, last)
-    const int nwin = a.seed_d ? 0 : min(kWindow, ntiles);
-    const int nstages = ntiles + nwin;
+    const int nps = (pcount + ROWS - 1) / ROWS;
+    const int nws = a.seed_d ? 0 : min(kWindow / kStageTiles, nps);
+    const int nst = nps + nws;
     // Every thread issues the same loads in every stage (positions past the
     // slice end are clamped to its last row and flagged), so the compiler
     // can wait for one stage's loads without draining the next's.  The pool
     // list is the caller's (launch_knn_collect_select requires one).
-    auto pool_pos = [&](int p) -> int64_t {
+    auto pool_pos = [&](int p) __attribute__((always_inline)) -> int64_t {
         p = min(p, pcount - 1) + it.p_rot;
         if (p >= pcount) p -= pcount;
         return it.p_begin + p;
     };
-    auto tile_of = [&](int s) { return s < ntiles ? s : s - ntiles; };
+    auto stage_base = [&](int s) __attribute__((always_inline)) { return (s < nps ? s : s - nps) * ROWS; };
 
-    int32_t idn[U4_THREAD];
-    uint4 pre[U4_THREAD];
-    int32_t rid_next = 0;    // this thread's tile row (threads < kPoolTile), a valid row id
+    // fixed-size register sets indexed only by unrolled loop counters
+    struct Ids {
+        int32_t v[U4_THREAD];
+    } idn;
+    struct Rows {
+        intx4 v[U4_THREAD];   // vector type: register moves, not aggregate copies
+    } pre;
+    int32_t rid_next = 0;    // this thread's stage row (threads < ROWS), a valid row id
     bool rvalid_next = false;
-    auto load_ids = [&](int s) {
-        const bool live = s < nstages;
-        const int t = live ? tile_of(s) : 0;
-#pragma unroll
-        for (int u = 0; u < U4_THREAD; ++u) {
-            const int e = min(tid + 256 * u, U4_TILE - 1);
-            idn[u] = a.p_rows[pool_pos(t * kPoolTile + e / U4_ROW)];
-        }
-        const int r = tid & (kPoolTile - 1);
-        rid_next = a.p_rows[pool_pos(t * kPoolTile + r)];
-        rvalid_next = live && t * kPoolTile + r < pcount;
+    auto load_ids = [&](int s) __attribute__((always_inline)) {
+        const bool live = s < nst;
+        const int base = live ? stage_base(s) : 0;
+        static_for<0, U4_THREAD>([&](auto U) __attribute__((always_inline)) {
+            const int e = min(tid + 256 * U.value, U4_STAGE - 1);
+            idn.v[U.value] = a.p_rows[pool_pos(base + e / U4_ROW)];
+        });
+        const int r = tid & (ROWS - 1);
+        rid_next = a.p_rows[pool_pos(base + r)];
+        rvalid_next = live && base + r < pcount;
     };
-    auto load_rows = [&]() {
-#pragma unroll
-        for (int u = 0; u < U4_THREAD; ++u) {
-            const int e = min(tid + 256 * u, U4_TILE - 1);
-            pre[u] = *reinterpret_cast<const uint4*>(a.Xp8 + static_cast<int64_t>(idn[u]) * DP + 16 * (e % U4_ROW));
-        }
+    auto load_rows = [&]() __attribute__((always_inline)) {
+        static_for<0, U4_THREAD>([&](auto U) __attribute__((always_inline)) {
+            const int e = min(tid + 256 * U.value, U4_STAGE - 1);
+            pre.v[U.value] =
+                *reinterpret_cast<const intx4*>(a.Xp8 + static_cast<int64_t>(idn.v[U.value]) * DP + 16 * (e % U4_ROW));
+        });
     };
-    auto store_rows = [&](int buf) {
-#pragma unroll
-        for (int u = 0; u < U4_THREAD; ++u) {
-            const int e = tid + 256 * u;
-            if (e < U4_TILE) *reinterpret_cast<uint4*>(&sm.tile[buf][e / U4_ROW][16 * (e % U4_ROW)]) = pre[u];
-        }
+    auto store_rows = [&](int buf) __attribute__((always_inline)) {
+        static_for<0, U4_THREAD>([&](auto U) __attribute__((always_inline)) {
+            const int e = tid + 256 * U.value;
+            if (e < U4_STAGE) *reinterpret_cast<intx4*>(&sm.tile[buf][e / U4_ROW][16 * (e % U4_ROW)]) = pre.v[U.value];
+        });
     };
     load_ids(0);
     load_rows();
@@ -340,16 +348,18 @@ knn_i8_collect_kernel(KnnArgs a)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc_prev[r] = 0;
     int32_t lo = i8_pass_floor<METRIC>(st.thr, qn);
+    bool pending = false;   // acc_prev holds tile p_u of stage p_s, not yet filtered
+    int p_s = 0, p_u = 0;
 
     // one stage: stage s's rows and norms (requested one stage earlier) into
     // LDS, the barrier, the requests for stage s + 1 (and the pool ids of
-    // s + 2), then the MFMAs of stage s's tile with filt(s - 1) on the tile
+    // s + 2), then the MFMAs of stage s's tiles, each with filt on the tile
     // before it.  A request is waited for only at the next stage's top, a
     // whole stage of MFMAs and filtering later.
-    auto stage = [&](int s, auto&& filt) {
+    auto stage = [&](int s, auto&& filt) __attribute__((always_inline)) {
         const int buf = s & 1, slot = s % 3;
         store_rows(buf);
-        if (tid < kPoolTile) {
+        if (tid < ROWS) {
             // rows past the slice end: id -1, norm +inf, accumulator start
             // kHalfPast keep them out of every result
             sm.trow[slot][tid] = rvalid_cur ? rid_cur : -1;
@@ -363,54 +373,59 @@ knn_i8_collect_kernel(KnnArgs a)
         rn_cur = METRIC == 0 ? a.np[rid_cur] : 0.f;
         load_ids(s + 2);
 
-        intx16 acc;
-        {
-            const int32_t* th = sm.thalf[slot];
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int4 hv = *reinterpret_cast<const int4*>(th + 8 * g + 4 * h);
-                acc[4 * g] = hv.x; acc[4 * g + 1] = hv.y; acc[4 * g + 2] = hv.z; acc[4 * g + 3] = hv.w;
+        for (int u = 0; u < kStageTiles; ++u) {
+            intx16 acc;
+            {
+                const int32_t* th = &sm.thalf[slot][kPoolTile * u];
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int4 hv = *reinterpret_cast<const int4*>(th + 8 * g + 4 * h);
+                    acc[4 * g] = hv.x; acc[4 * g + 1] = hv.y; acc[4 * g + 2] = hv.z; acc[4 * g + 3] = hv.w;
+                }
             }
-        }
-        const int8_t* arow = &sm.tile[buf][j][16 * h];
+            const int8_t* arow = &sm.tile[buf][kPoolTile * u + j][16 * h];
 #pragma unroll
-        for (int k = 0; k < KS; ++k) {
-            const intx4 av = *reinterpret_cast<const intx4*>(arow + 32 * k);
-            acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, qf[k], acc, 0, 0, 0);
+            for (int k = 0; k < KS; ++k) {
+                const intx4 av = *reinterpret_cast<const intx4*>(arow + 32 * k);
+                acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, qf[k], acc, 0, 0, 0);
+            }
+            if (pending) filt(p_s, p_u);
+            acc_prev = acc;
+            pending = true;
+            p_s = s;
+            p_u = u;
         }
-        if (s > 0) filt(s - 1);
-        acc_prev = acc;
     };
-    auto collect = [&](int s) {
-        const int slot3 = s % 3;
-        collect_tile<METRIC>(a, W, acc_prev, sm.tnorm[slot3], sm.trow[slot3], sm.thalf[slot3], lane, qvalid, qn, st,
-                             lo);
+    auto collect = [&](int s, int u) __attribute__((always_inline)) {
+        const int slot = s % 3;
+        collect_tile<METRIC>(a, W, acc_prev, &sm.tnorm[slot][kPoolTile * u], &sm.trow[slot][kPoolTile * u],
+                             &sm.thalf[slot][kPoolTile * u], lane, qvalid, qn, st, lo);
     };
-    // the window's stages (stage nwin filters its last tile), then the rest
-    const int s_win = min(nwin + 1, nstages);
-    {
+    if (nws > 0) {
         float T[32];
 #pragma unroll
         for (int i = 0; i < 32; ++i) T[i] = INFINITY;
-        auto window = [&](int s) {
-            const int slot3 = s % 3;
-            window_tile<METRIC>(acc_prev, sm.tnorm[slot3], sm.trow[slot3], sm.thalf[slot3], h, qn, st.self, T);
-            if (s == nwin - 1) {
-                // the pair's ceil(M/2)-th smallest distances: M distinct rows at or below the larger
-                const int m = (a.M + 1) / 2 - 1;
-                float v = T[0];
-#pragma unroll
-                for (int i = 1; i < 32; ++i) v = i == m ? T[i] : v;
-                const float bound = fmaxf(v, __shfl_xor(v, 32));
-                if (qvalid && bound < st.thr) st.thr = bound;
-                lo = i8_pass_floor<METRIC>(st.thr, qn);
-                publish_state(W, lane, qvalid, qn, st);
-            }
+        auto window = [&](int s, int u) __attribute__((always_inline)) {
+            const int slot = s % 3;
+            window_tile<METRIC>(acc_prev, &sm.tnorm[slot][kPoolTile * u], &sm.trow[slot][kPoolTile * u],
+                                &sm.thalf[slot][kPoolTile * u], h, qn, st.self, T);
         };
-        for (int s = 0; s < s_win; ++s) stage(s, window);
+        for (int s = 0; s < nws; ++s) stage(s, window);
+        window(p_s, p_u);   // the window's last tile
+        pending = false;
+        // the pair's ceil(M/2)-th smallest distances: M distinct rows at or below the larger
+        const int m = (a.M + 1) / 2 - 1;
+        float v = T[0];
+#pragma unroll
+        for (int i = 1; i < 32; ++i) v = i == m ? T[i] : v;
+        const float bound = fmaxf(v, __shfl_xor(v, 32));
+        if (qvalid && bound < st.thr) st.thr = bound;
+        lo = i8_pass_floor<METRIC>(st.thr, qn);
+        publish_state(W, lane, qvalid, qn, st);
     }
-    for (int s = s_win; s < nstages; ++s) stage(s, collect);
-    if (nstages > 0) collect(nstages - 1);   // nstages - 1 >= nwin
+    for (int s = nws; s < nst; ++s) stage(s, collect);
+    if (pending) collect(p_s, p_u);
     if (qvalid && h == 0) a.cand_cnt[st.orow] = st.cnt;
     if (a.stats && qvalid && h == 0) atomicAdd(a.stats, static_cast<unsigned long long>(st.cnt));
 }

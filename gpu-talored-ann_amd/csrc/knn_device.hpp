@@ -8,12 +8,25 @@
 #include <cfloat>
 #include <climits>
 #include <cmath>
+#include <type_traits>
 
 namespace gtann {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef int intx4 __attribute__((ext_vector_type(4)));
 typedef int intx16 __attribute__((ext_vector_type(16)));
+
+// f(std::integral_constant<int, I>{}) for I = 0 .. N-1: loop counters that
+// are constants before any optimisation runs (register arrays indexed by
+// them never become memory)
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F&& f)
+{
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<I + 1, N>(f);
+    }
+}
 
 // Waits until every vector memory access of this wave has completed: rows a
 // wave stores (list rows, candidate slots) are loaded again by the same wave
