@@ -68,8 +68,9 @@ int rev_bin_blocks(int64_t E);
 void launch_rev_binned(const uint32_t* fwd, int64_t N, int K, uint32_t* hist, uint32_t* offs, uint32_t* sums,
                        unsigned long long* part, unsigned long long* grouped, uint32_t* out, int* err, hipStream_t s);
 bool rv_plan(int64_t N, int K, RvPlan& p);
-void launch_rv(const uint32_t* fwd, int64_t N, int K, const RvPlan& p, uint32_t* part, uint32_t* meta_cnt,
-               uint32_t* meta_off, uint32_t* out, int* err, uint32_t* slow_rows, uint32_t* slow_count, hipStream_t s);
+void launch_rv(const uint32_t* fwd, int64_t N, int K, const RvPlan& p, uint32_t* part, uint16_t* meta_blk,
+               uint16_t* meta, uint32_t* out, int* err, uint32_t* slow_rows, uint32_t* slow_count, uint32_t* big_bins,
+               hipStream_t s);
 void launch_rev_merge(const uint32_t* fwd, int64_t N, int K, const uint32_t* off, const unsigned long long* keys,
                       uint32_t* out, hipStream_t s);
 void launch_occlusion_prune(const float* X, int64_t N, int Dp, const int32_t* nb, int M, int max_deg, int32_t* out,
@@ -1305,27 +1306,60 @@ static void bucket_host(const BucketPlan& bp, float balance, Buckets& b, std::ve
 
 // ---------------------------------------------------------------- graph stages
 
-static void prune_device(Ctx& c, const int32_t* G, int64_t N, int M, int K, uint32_t* out)
+// Each graph stage is enqueued (kernels only, no host round trip, so that a
+// caller's events around it time the device work) and its flag is checked
+// after.  The flags are cleared by a kernel.
+struct StageFlags {
+    unsigned long long* bad = nullptr;   // prune: lowest row with too few candidates, ~0 if none
+    int* err = nullptr;                  // reverse merge: an id >= N
+};
+
+static StageFlags stage_flags(Ctx& c)
+{
+    StageFlags f;
+    f.bad = c.ws<unsigned long long>(W_FLAG, 1);
+    f.err = c.ws<int>(W_TMP, 1);
+    return f;
+}
+
+static void prune_enqueue(Ctx& c, const StageFlags& f, const int32_t* G, int64_t N, int M, int K, uint32_t* out)
 {
     GT_REQUIRE(K >= 1 && K <= M, "output degree must be in [1, M]");
-    unsigned long long* bad = c.ws<unsigned long long>(W_FLAG, 1);
-    const unsigned long long init = ~0ull;
-    c.h2d(bad, &init, sizeof(init));
-    launch_cagra_prune(G, N, M, K, out, bad, c.s);
+    launch_init_flags(f.bad, f.err, c.s);
+    launch_cagra_prune(G, N, M, K, out, f.bad, c.s);
+}
+
+static void prune_check(Ctx& c, const StageFlags& f)
+{
     unsigned long long h = 0;
-    c.d2h(&h, bad, sizeof(h));
+    c.d2h(&h, f.bad, sizeof(h));
     c.sync();
     if (h != ~0ull)
         throw Error(GT_EFEWCAND, "prune: row " + std::to_string(h) +
                                      " has fewer than output_degree valid candidates");
 }
 
-static void reverse_merge_device(Ctx& c, const uint32_t* fwd, int64_t N, int K, uint32_t* out)
+static void prune_device(Ctx& c, const int32_t* G, int64_t N, int M, int K, uint32_t* out)
+{
+    const StageFlags f = stage_flags(c);
+    prune_enqueue(c, f, G, N, M, K, out);
+    prune_check(c, f);
+}
+
+static void reverse_merge_check(Ctx& c, const StageFlags& f)
+{
+    int h = 0;
+    c.d2h(&h, f.err, sizeof(int));
+    c.sync();
+    if (h) throw Error(GT_EINVAL, "reverse merge: forward graph holds an id >= N");
+}
+
+static void reverse_merge_enqueue(Ctx& c, const StageFlags& f, const uint32_t* fwd, int64_t N, int K, uint32_t* out)
 {
     GT_REQUIRE(K >= 1 && K <= 64, "output degree must be in [1, 64]");
     GT_REQUIRE(N * K < (int64_t(1) << 32), "too many edges for 32-bit offsets");
-    int* err = c.ws<int>(W_TMP, 1);
-    GT_HIP(hipMemsetAsync(err, 0, sizeof(int), c.s));
+    int* err = f.err;
+    launch_init_flags(f.bad, f.err, c.s);
     // Three paths give the same rows: the two-kernel merge over block-local
     // key regions (256-row bins, output degree <= 32: graphs up to 2^21
     // rows; where it is faster), the binned merge through global grouping
@@ -1339,12 +1373,13 @@ static void reverse_merge_device(Ctx& c, const uint32_t* fwd, int64_t N, int K, 
     const bool rv_ok = rv_plan(N, K, rp);
     const bool use_rv = forced == "rv" ? rv_ok : forced.empty() && rv_ok && rp.cshift == 8 && K <= 32;
     if (use_rv) {
-        const size_t nm = static_cast<size_t>(rp.nbins) * rp.nblk;
+        const size_t nm = static_cast<size_t>(rp.nbins + 1) * rp.nblk;   // 16-bit run offsets
         uint32_t* part = c.ws<uint32_t>(W_KEYS, static_cast<size_t>(N) * K);
-        uint32_t* mcnt = c.ws<uint32_t>(W_DEG, nm);
-        uint32_t* moff = c.ws<uint32_t>(W_OFF, nm);
+        uint16_t* meta_blk = reinterpret_cast<uint16_t*>(c.ws<uint32_t>(W_DEG, (nm + 1) / 2));
+        uint16_t* meta = reinterpret_cast<uint16_t*>(c.ws<uint32_t>(W_OFF, (nm + 1) / 2));
         uint32_t* slow = c.ws<uint32_t>(W_CUR, static_cast<size_t>(N) + 1);   // [0]: count, then rows
-        launch_rv(fwd, N, K, rp, part, mcnt, moff, out, err, slow + 1, slow, c.s);
+        uint32_t* big = c.ws<uint32_t>(W_SUMS, static_cast<size_t>(rp.nbins) + 1);   // [0]: count, then bins
+        launch_rv(fwd, N, K, rp, part, meta_blk, meta, out, err, slow + 1, slow, big, c.s);
     } else if (shift >= 0) {
         // binned path: LDS histograms and cursors, no global atomics
         const int64_t nh = ceil_div(N, int64_t(1) << shift) * rev_bin_blocks(N * K);
@@ -1366,10 +1401,13 @@ static void reverse_merge_device(Ctx& c, const uint32_t* fwd, int64_t N, int K, 
         launch_rev_scatter(fwd, N, K, off, slot, keys, c.s);
         launch_rev_merge(fwd, N, K, off, keys, out, c.s);
     }
-    int h = 0;
-    c.d2h(&h, err, sizeof(int));
-    c.sync();
-    if (h) throw Error(GT_EINVAL, "reverse merge: forward graph holds an id >= N");
+}
+
+static void reverse_merge_device(Ctx& c, const uint32_t* fwd, int64_t N, int K, uint32_t* out)
+{
+    const StageFlags f = stage_flags(c);
+    reverse_merge_enqueue(c, f, fwd, N, K, out);
+    reverse_merge_check(c, f);
 }
 
 // bd/build_bucket.py:473-543 on a device table (N x M, ascending rows), in place
@@ -2532,9 +2570,14 @@ int gt_build_graph_ex(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtyp
             uint32_t* san = c.ws<uint32_t>(W_OUT, nm);
             uint32_t* fwd = c.ws<uint32_t>(W_G3, static_cast<size_t>(N) * p.K);
             fin = c.ws<uint32_t>(W_IN, static_cast<size_t>(N) * p.K);
-            st.t_prune = c.timed([&] { launch_sanitize(run_i, N, p.M, san, c.s); });
-            st.t_prune += c.timed([&] { prune_device(c, reinterpret_cast<const int32_t*>(san), N, p.M, p.K, fwd); });
-            st.t_revmerge = c.timed([&] { reverse_merge_device(c, fwd, N, p.K, fin); });
+            const StageFlags fl = stage_flags(c);
+            st.t_prune = c.timed([&] {
+                launch_sanitize(run_i, N, p.M, san, c.s);
+                prune_enqueue(c, fl, reinterpret_cast<const int32_t*>(san), N, p.M, p.K, fwd);
+            });
+            prune_check(c, fl);
+            st.t_revmerge = c.timed([&] { reverse_merge_enqueue(c, fl, fwd, N, p.K, fin); });
+            reverse_merge_check(c, fl);
         }
         Timer td;
         if (knn_ids) c.out(knn_ids, run_i, nm);

@@ -120,7 +120,7 @@ struct RvPlan {
     int kbits, sbits, nbits;   // bits of rank, source within block, source id
     int rp;         // rows per merge pass (= merge block size)
     int cap;        // keys grouped in LDS per pass
-    int ubuf;       // LDS words of the bin's key copy, later the forward-row stages
+    int cap_big;    // the same for the deferred (large) bins
 };
 
 // Orders LDS traffic of one wave across its lanes (no s_barrier needed

@@ -10,22 +10,30 @@
 // reference's weakest-first move-to-front insertion.
 //
 // (1) rv_scatter_kernel: each block owns the edges of a contiguous range of
-//     source rows.  It counts them per destination bin (2^cshift consecutive
-//     rows) in LDS, scans the counts, and writes its edges, bin by bin, into
-//     its own contiguous region of `part` as 32-bit keys
-//       (row within bin << (kbits + sbits)) | (rank << sbits) | (source within block).
-//     The region belongs to one block, so its cache lines fill in one XCD's
-//     L2 before they are written back.  Per (bin, block) it records the run
-//     length and offset (meta_cnt / meta_off, bin-major).
-// (2) rv_merge_kernel: one block per bin.  It gathers the bin's runs, counts
-//     keys per row, groups them by row in LDS (as (rank << nbits) | source),
-//     and then merges one row per lane: the row's keys stream through a sorted
-//     register list of the L strongest non-protected keys (a key at or above
-//     the list's L-th costs one compare), duplicate sources are resolved
-//     after the fact, and the row is written through LDS so that both the
-//     forward rows and the output rows move as coalesced blocks.  A bin whose
-//     keys exceed the LDS capacity is merged in several passes over row
-//     ranges; a single row beyond the capacity reads its keys from the runs.
+//     source rows (at most 32,704 edges, 32 per thread, held in registers).
+//     LDS atomics count them per destination bin (2^cshift consecutive
+//     rows); a scan of the counts gives the runs' offsets, a second round of
+//     atomics places every edge, as a 32-bit key
+//       (row within bin << (kbits + sbits)) | (rank << sbits) | (source within block),
+//     at its run's cursor in an LDS stage, and the stage leaves as one
+//     coalesced copy into the block's own region of `part` (runs in bin
+//     order).  The runs' 16-bit offsets (plus the block's total) go to one
+//     row of `meta_blk` per block, written contiguously; a tiled transpose
+//     turns them bin-major (`meta`), so each merge block reads its offsets
+//     as two contiguous rows.
+// (2) rv_merge_kernel: one block per bin, bins dealt XCD-major so that
+//     neighbouring bins -- whose runs and offsets share cache lines -- run on
+//     one XCD.  Fast path (a bin whose keys fit the registers and the LDS):
+//     every thread loads a strided share of the bin's keys (consecutive lanes
+//     read consecutive keys of the concatenated runs), counts them per row
+//     with one LDS atomic each (keeping the returned slot), and after a scan
+//     of the row counts writes each key, as (rank << nbits) | source, to its
+//     row's group in LDS.  Then one lane per row merges: the row's keys stream
+//     through a sorted register list of the L strongest non-protected keys (a
+//     key at or above the list's L-th costs one compare), and the output row
+//     is written straight to `out`.  Larger bins take passes over row ranges
+//     whose keys fit the LDS, re-reading the runs; a single row beyond the
+//     capacity, or one with a repeated source, goes to rv_slow_kernel.
 #include "gtann_common.hpp"
 
 #include <algorithm>
@@ -34,13 +42,14 @@
 
 namespace gtann {
 
-constexpr int kRvScatterThreads = 512;
-// edges staged in LDS per scatter step: 16384 when its LDS (6 bytes per edge
-// plus two counters per bin) fits, else 8192
-constexpr size_t rv_scatter_lds(int nbins, int sc) { return (2 * static_cast<size_t>(nbins) + sc) * 4 + sc * 2; }
-constexpr int kRvMaxBins = 8192;       // LDS counters of the scatter
-constexpr int kRvMaxBinShift = 11;     // rows per bin <= 2048 (LDS row counters of the merge)
-constexpr int kRvGather = 32;          // keys of a run loaded together by the merge
+constexpr int kRvScatterThreads = 1024;
+constexpr int kRvEdgesPerThread = 32;     // a scatter block's edges stay in registers
+constexpr int kRvMaxBlockEdges = 32704;   // its keys plus 8,192 bin counters fill the 160 KB of LDS
+constexpr int kRvMaxBins = 8192;          // LDS counters of the scatter
+constexpr int kRvMaxBinShift = 11;        // rows per bin <= 2048
+constexpr int kRvKeysPerThread = 36;      // merge fast path: a bin's keys held in registers
+constexpr int kRvLdsPerBlock = 40960;     // merge LDS for 4 blocks per CU
+constexpr int kRvBigThreads = 512;        // blocks of the deferred large bins
 
 // Exclusive scan of a[0..n) in LDS by a block of T threads; returns the
 // total (every thread).  wsum: T/64 + 1 words of LDS.
@@ -92,103 +101,98 @@ __device__ __forceinline__ void divmod_small(uint32_t x, uint32_t K, float rK, u
     r = x - q * K;
 }
 
-template <int kRvSubChunk>
 __global__ void __launch_bounds__(kRvScatterThreads) rv_scatter_kernel(
     const uint32_t* __restrict__ fwd, int64_t N, int K, int64_t spb, int cshift, int nbins, int kbits, int sbits,
-    uint32_t* __restrict__ part, uint32_t* __restrict__ meta_cnt, uint32_t* __restrict__ meta_off,
-    int* __restrict__ err, uint32_t* __restrict__ slow_count)
+    uint32_t* __restrict__ part, uint16_t* __restrict__ meta, int* __restrict__ err, uint32_t* __restrict__ slow_count)
 {
     constexpr int T = kRvScatterThreads;
-    constexpr int U = kRvSubChunk / T;   // edges per thread per sub-chunk
-    extern __shared__ uint32_t h[];      // cur[nbins], sub[nbins], stage[kRvSubChunk], sbin[kRvSubChunk] (u16)
-    uint32_t* cur = h;
-    uint32_t* sub = h + nbins;
-    uint32_t* stage = sub + nbins;
-    uint16_t* sbin = reinterpret_cast<uint16_t*>(stage + kRvSubChunk);
+    constexpr int U = kRvEdgesPerThread;
+    extern __shared__ uint32_t lds[];
+    uint32_t* cnt = lds;             // nbins counters, then the runs' cursors
+    uint32_t* stage = lds + nbins;   // the block's keys in bin order
     __shared__ uint32_t wsum[T / 64 + 1];
     const int t = threadIdx.x;
-    const int nblk = gridDim.x;
     if (blockIdx.x == 0 && t == 0) *slow_count = 0u;   // read by the merge and slow kernels after this one
-    for (int i = t; i < nbins; i += T) cur[i] = 0u;
+    for (int i = t; i < nbins; i += T) cnt[i] = 0u;
     __syncthreads();
     const int64_t i0 = static_cast<int64_t>(blockIdx.x) * spb;
     const int64_t i1 = i0 + spb < N ? i0 + spb : N;
-    const uint32_t ne = i1 > i0 ? static_cast<uint32_t>((i1 - i0) * K) : 0u;   // < 2^24
+    const uint32_t ne = static_cast<uint32_t>((i1 - i0) * K);   // <= kRvMaxBlockEdges
     const uint32_t* src = fwd + i0 * K;
     const uint32_t uN = static_cast<uint32_t>(N);
-    // (1) the block's counts per bin
+    uint32_t v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const uint32_t e = t + u * T;
+        v[u] = e < ne ? src[e] : uN;
+    }
     bool bad = false;
-    for (uint32_t e = t; e < ne; e += U * T) {
-        uint32_t v[U];
 #pragma unroll
-        for (int u = 0; u < U; ++u) v[u] = e + u * T < ne ? src[e + u * T] : uN;
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            if (e + u * T >= ne) continue;
-            if (v[u] >= uN) bad = true;
-            else atomicAdd(&cur[v[u] >> cshift], 1u);
-        }
+    for (int u = 0; u < U; ++u) {
+        if (v[u] < uN) atomicAdd(&cnt[v[u] >> cshift], 1u);
+        else bad |= t + u * T < ne;
     }
     if (bad) atomicExch(err, 1);
     __syncthreads();
-    for (int i = t; i < nbins; i += T) meta_cnt[static_cast<int64_t>(i) * nblk + blockIdx.x] = cur[i];
-    block_exclusive_scan<T>(cur, nbins, wsum);
-    for (int i = t; i < nbins; i += T) meta_off[static_cast<int64_t>(i) * nblk + blockIdx.x] = cur[i];
-    __syncthreads();
-    // (2) sub-chunk by sub-chunk: keys sorted by bin in LDS, then stored in
-    // that order, so the lanes of a store instruction write runs of
-    // consecutive words
+    const uint32_t total = block_exclusive_scan<T>(cnt, nbins, wsum);
+    uint16_t* mrow = meta + static_cast<int64_t>(blockIdx.x) * (nbins + 1);
+    for (int i = t; i < nbins; i += T) mrow[i] = static_cast<uint16_t>(cnt[i]);
+    if (t == 0) mrow[nbins] = static_cast<uint16_t>(total);
+    __syncthreads();   // the offsets are read before the placement advances them
     const uint32_t rmask = (1u << cshift) - 1u;
     const int hs = kbits + sbits;
     const float rK = 1.0f / static_cast<float>(K);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        if (v[u] >= uN) continue;
+        uint32_t il, k;
+        divmod_small(t + u * T, static_cast<uint32_t>(K), rK, il, k);
+        stage[atomicAdd(&cnt[v[u] >> cshift], 1u)] = ((v[u] & rmask) << hs) | (k << sbits) | il;
+    }
+    __syncthreads();
     uint32_t* dst = part + i0 * K;
-    for (uint32_t c0 = 0; c0 < ne; c0 += kRvSubChunk) {
-        for (int i = t; i < nbins; i += T) sub[i] = 0u;
-        __syncthreads();
-        uint32_t v[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const uint32_t e = c0 + t + u * T;
-            v[u] = e < ne ? src[e] : uN;
-        }
-        uint32_t rk[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u)
-            rk[u] = v[u] < uN ? atomicAdd(&sub[v[u] >> cshift], 1u) : 0u;
-        __syncthreads();
-        const uint32_t nsub = block_exclusive_scan<T>(sub, nbins, wsum);   // sub = start of each bin's keys
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            if (v[u] >= uN) continue;
-            const uint32_t b = v[u] >> cshift;
-            uint32_t il, k;
-            divmod_small(c0 + t + u * T, static_cast<uint32_t>(K), rK, il, k);
-            const uint32_t pos = sub[b] + rk[u];
-            stage[pos] = ((v[u] & rmask) << hs) | (k << sbits) | il;
-            sbin[pos] = static_cast<uint16_t>(b);
-        }
-        __syncthreads();
-        for (uint32_t q = t; q < nsub; q += T) {
-            const uint32_t b = sbin[q];
-            dst[cur[b] + (q - sub[b])] = stage[q];
-        }
-        __syncthreads();
-        // advance the cursors by this sub-chunk's counts
-        for (uint32_t q = t; q < nsub; q += T) {
-            const uint32_t b = sbin[q];
-            if (q + 1 == nsub || sbin[q + 1] != b) cur[b] += q + 1 - sub[b];
-        }
-        __syncthreads();
+    for (uint32_t q = t; q < total; q += T) dst[q] = stage[q];
+}
+
+// meta (block-major, nblk rows of nbins + 1 offsets) -> metaT (bin-major,
+// nbins + 1 rows of nblk): each merge block then reads two contiguous rows
+// instead of one entry from every block's row.  64 x 64 tiles through LDS.
+__global__ void __launch_bounds__(256) rv_meta_transpose_kernel(const uint16_t* __restrict__ meta, int nblk, int nbins,
+                                                                uint16_t* __restrict__ metaT,
+                                                                uint32_t* __restrict__ big_bins)
+{
+    __shared__ uint16_t tile[64][65];
+    if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) *big_bins = 0u;   // the merge's deferred bins
+    const int cols = nbins + 1;
+    const int c0 = blockIdx.x * 64, q0 = blockIdx.y * 64;
+    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+    for (int r = ty; r < 64; r += 4) {
+        const int q = q0 + r, c = c0 + tx;
+        if (q < nblk && c < cols) tile[r][tx] = meta[static_cast<int64_t>(q) * cols + c];
+    }
+    __syncthreads();
+    for (int r = ty; r < 64; r += 4) {
+        const int c = c0 + r, q = q0 + tx;
+        if (q < nblk && c < cols) metaT[static_cast<int64_t>(c) * nblk + q] = tile[tx][r];
     }
 }
 
+// median of three unsigned words in one instruction
+__device__ __forceinline__ uint32_t med3_u32(uint32_t x, uint32_t lo, uint32_t hi)
+{
+    uint32_t r;
+    asm("v_med3_u32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(lo), "v"(hi));
+    return r;
+}
+
 // Sorted insertion of x into the ascending register list a[0..LM):
-// a'[l] = clamp(x, a[l-1], a[l]) (a[-1] = 0).
+// a'[l] = clamp(x, a[l-1], a[l]) = med3(x, a[l-1], a[l]) (a[-1] = 0), one
+// instruction per slot.
 template <int LM>
 __device__ __forceinline__ void list_insert(uint32_t (&a)[LM], uint32_t x)
 {
 #pragma unroll
-    for (int l = LM - 1; l >= 1; --l) a[l] = min(a[l], max(a[l - 1], x));
+    for (int l = LM - 1; l >= 1; --l) a[l] = med3_u32(x, a[l - 1], a[l]);
     a[0] = min(a[0], x);
 }
 
@@ -343,42 +347,112 @@ __device__ __forceinline__ bool rv_merge_lane(const uint32_t (&fw)[KMAX], int K,
     return true;
 }
 
-// Loads a wave's wrn consecutive rows of src (K words each, one contiguous
-// run) into the wave's LDS stage (row stride K + 1), all loads in flight
-// before the LDS stores; and the reverse.
+// rv_merge_lane for K == KMAX with the output row in registers: S = fw[0..P),
+// R from the keys, then the entries of O = fw[P..K) that are not the first
+// occurrence in O of an element of R, each placed by a compare network (no
+// dynamically indexed register or store), so that the caller writes the row
+// with vector stores.
 template <int KMAX>
-__device__ __forceinline__ void rv_stage_in(const uint32_t* __restrict__ g, int wrn, int K, uint32_t* wst, int lane)
+__device__ __forceinline__ bool rv_merge_full(const uint32_t (&fw)[KMAX], const uint32_t* grouped, uint32_t n,
+                                              int nbits, uint32_t (&o)[KMAX])
 {
-    const uint32_t nw = static_cast<uint32_t>(wrn * K);
-    const float rK = 1.0f / static_cast<float>(K);
-    uint32_t vv[KMAX];
+    constexpr int P = KMAX / 2, L = KMAX - P;
+    static_assert(P == L, "even output degree");
+    const uint32_t gmask = (1u << nbits) - 1u;
+    uint32_t S[P];
+    uint64_t sbloom = 0;
 #pragma unroll
-    for (int m = 0; m < KMAX; ++m) {
-        const uint32_t f = lane + 64u * m;
-        vv[m] = f < nw ? g[f] : 0u;
+    for (int p = 0; p < P; ++p) {
+        S[p] = fw[p];
+        sbloom |= bloom_bit(fw[p]);
+    }
+    uint32_t lst[L];
+#pragma unroll
+    for (int l = 0; l < L; ++l) lst[l] = 0xFFFFFFFFu;
+    auto offer = [&](uint32_t x) {
+        if (x >= lst[L - 1]) return;
+        const uint32_t s = x & gmask;
+        if (sbloom & bloom_bit(s)) {
+            bool prot = false;
+#pragma unroll
+            for (int p = 0; p < P; ++p) prot |= S[p] == s;
+            if (prot) return;
+        }
+        list_insert<L>(lst, x);
+    };
+    uint32_t e = 0;
+    for (; e + 8 <= n; e += 8) {
+        uint32_t x[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) x[u] = grouped[e + u];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) offer(x[u]);
+    }
+    for (; e < n; ++e) offer(grouped[e]);
+    uint32_t Rv[L];
+    int nR = 0;
+#pragma unroll
+    for (int l = 0; l < L; ++l) {
+        Rv[l] = lst[l] != 0xFFFFFFFFu ? (lst[l] & gmask) : (0x80000000u + l);
+        nR += lst[l] != 0xFFFFFFFFu ? 1 : 0;
+    }
+    bool dup = false;
+#pragma unroll
+    for (int l = 1; l < L; ++l)
+#pragma unroll
+        for (int m = 0; m < l; ++m) dup |= Rv[l] == Rv[m];
+    if (dup) return false;
+    // destination of each entry of O that stays (-1: consumed by R)
+    uint64_t rbloom = 0;
+#pragma unroll
+    for (int l = 0; l < L; ++l) rbloom |= l < nR ? bloom_bit(Rv[l]) : 0ull;
+    int dst[L];
+    int pos = P + nR;
+#pragma unroll
+    for (int k = P; k < KMAX; ++k) {
+        const uint32_t x = fw[k];
+        bool consumed = false;
+        if (rbloom & bloom_bit(x)) {
+            bool inR = false;
+#pragma unroll
+            for (int l = 0; l < L; ++l) inR |= Rv[l] == x;
+            bool earlier = false;
+#pragma unroll
+            for (int q = P; q < k; ++q) earlier |= fw[q] == x;
+            consumed = inR && !earlier;
+        }
+        dst[k - P] = consumed ? -1 : pos;
+        pos += consumed ? 0 : 1;
     }
 #pragma unroll
-    for (int m = 0; m < KMAX; ++m) {
-        const uint32_t f = lane + 64u * m;
-        if (f >= nw) continue;
-        uint32_t rr, c;
-        divmod_small(f, static_cast<uint32_t>(K), rK, rr, c);
-        wst[rr * (K + 1) + c] = vv[m];
+    for (int q = 0; q < P; ++q) o[q] = fw[q];
+#pragma unroll
+    for (int q = P; q < KMAX; ++q) {
+        uint32_t v = Rv[q - P];
+#pragma unroll
+        for (int k = 0; k < L; ++k) v = dst[k] == q ? fw[P + k] : v;
+        o[q] = v;
     }
+    return true;
 }
 
+// One forward row (K words) into registers; entries from K on are unused.
 template <int KMAX>
-__device__ __forceinline__ void rv_stage_out(uint32_t* __restrict__ g, int wrn, int K, const uint32_t* wst, int lane)
+__device__ __forceinline__ void rv_load_row(const uint32_t* __restrict__ g, int K, uint32_t (&fw)[KMAX])
 {
-    const uint32_t nw = static_cast<uint32_t>(wrn * K);
-    const float rK = 1.0f / static_cast<float>(K);
+    if ((K & 3) == 0) {
+        const uint4* g4 = reinterpret_cast<const uint4*>(g);
 #pragma unroll
-    for (int m = 0; m < KMAX; ++m) {
-        const uint32_t f = lane + 64u * m;
-        if (f >= nw) continue;
-        uint32_t rr, c;
-        divmod_small(f, static_cast<uint32_t>(K), rK, rr, c);
-        g[f] = wst[rr * (K + 1) + c];
+        for (int m = 0; m < KMAX / 4; ++m) {
+            const uint4 x = 4 * m < K ? g4[m] : make_uint4(~0u, ~0u, ~0u, ~0u);
+            fw[4 * m] = x.x;
+            fw[4 * m + 1] = x.y;
+            fw[4 * m + 2] = x.z;
+            fw[4 * m + 3] = x.w;
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < KMAX; ++k) fw[k] = k < K ? g[k] : ~0u;
     }
 }
 
@@ -390,10 +464,9 @@ __device__ __forceinline__ void rv_stage_out(uint32_t* __restrict__ g, int wrn, 
 // list; every wave ends when the list is done.
 template <int KMAX>
 __global__ void __launch_bounds__(256) rv_slow_kernel(const uint32_t* __restrict__ fwd, int64_t N, int K, int nblk,
-                                                      int64_t spb, int cshift, int kbits, int sbits, int nbits,
-                                                      const uint32_t* __restrict__ part,
-                                                      const uint32_t* __restrict__ meta_cnt,
-                                                      const uint32_t* __restrict__ meta_off,
+                                                      int64_t spb, int cshift, int nbins, int kbits, int sbits,
+                                                      int nbits, const uint32_t* __restrict__ part,
+                                                      const uint16_t* __restrict__ meta,
                                                       const uint32_t* __restrict__ slow_rows,
                                                       const uint32_t* __restrict__ slow_count, uint32_t* __restrict__ out)
 {
@@ -418,7 +491,9 @@ __global__ void __launch_bounds__(256) rv_slow_kernel(const uint32_t* __restrict
         uint32_t carry = 0;
         for (int q0 = 0; q0 < nblk; q0 += 64) {
             const int q = q0 + lane;
-            const uint32_t c = q < nblk ? meta_cnt[b * nblk + q] : 0u;
+            const int qc = q < nblk ? q : 0;
+            const uint32_t o0 = meta[b * nblk + qc];
+            const uint32_t c = q < nblk ? static_cast<uint32_t>(meta[(b + 1) * nblk + qc]) - o0 : 0u;
             uint32_t inc = c;
 #pragma unroll
             for (int o = 1; o < 64; o <<= 1) {
@@ -427,7 +502,7 @@ __global__ void __launch_bounds__(256) rv_slow_kernel(const uint32_t* __restrict
             }
             if (q < nblk) {
                 rs[q] = carry + inc - c;
-                rb[q] = static_cast<uint32_t>(q * spb * K) + meta_off[b * nblk + q];
+                rb[q] = static_cast<uint32_t>(q * spb * K) + o0;
             }
             carry += __shfl(inc, 63);
         }
@@ -509,148 +584,267 @@ __global__ void __launch_bounds__(256) rv_slow_kernel(const uint32_t* __restrict
     }
 }
 
-template <int KMAX, int RP>
-__global__ void __launch_bounds__(RP) rv_merge_kernel(const uint32_t* __restrict__ fwd, int64_t N, int K, int nblk,
-                                                      int64_t spb, int cshift, int kbits, int sbits, int nbits,
-                                                      const uint32_t* __restrict__ part,
-                                                      const uint32_t* __restrict__ meta_cnt,
-                                                      const uint32_t* __restrict__ meta_off, uint32_t* __restrict__ out,
-                                                      int cap, int ubuf, uint32_t* __restrict__ slow_rows,
-                                                      uint32_t* __restrict__ slow_count)
+// LDS words before the row starts: the 16-bit run tables of the key loading,
+// later the row order and its class counters
+__host__ __device__ inline int rv_head_words(int nblk, int rows_max)
 {
-    constexpr int W = RP / 64;
-    extern __shared__ uint32_t lds[];
-    __shared__ uint32_t wsum[W + 1];
-    const int t = threadIdx.x, w = t >> 6, lane = t & 63;
+    const int runs = (2 * nblk + 2) / 2;
+    return runs > rows_max + 65 ? runs : rows_max + 65;
+}
+
+// The merge of bin b by one block of RP threads.  DEFER: a bin that does not
+// fit the fast path is appended to big_bins (for rv_big_kernel) instead of
+// taking the general path, so that a few long blocks do not trail the launch.
+template <int KMAX, int RP, bool DEFER>
+__device__ __forceinline__ void rv_merge_bin(int b, const uint32_t* __restrict__ fwd, int64_t N, int K, int nblk,
+                                             int64_t spb, int cshift, int nbins, int kbits, int sbits, int nbits,
+                                             const uint32_t* __restrict__ part, const uint16_t* __restrict__ meta,
+                                             uint32_t* __restrict__ out, int cap, uint32_t* __restrict__ slow_rows,
+                                             uint32_t* __restrict__ slow_count, uint32_t* __restrict__ big_bins,
+                                             uint32_t* lds, uint32_t* wsum)
+{
+    constexpr int KPT = kRvKeysPerThread;
+    const int t = threadIdx.x;
     const int rows_max = 1 << cshift;
-    uint32_t* rstart = lds;                      // nblk + 1
-    uint32_t* rbase = rstart + nblk + 1;         // nblk
-    uint32_t* rowstart = rbase + nblk;           // rows_max + 1
-    uint32_t* cursor = rowstart + rows_max + 1;  // rows_max
-    uint32_t* grouped = cursor + rows_max;       // cap
-    uint32_t* ubase = grouped + cap;             // ubuf: the bin's keys as read (<= cap of them), later the stages
-    const int b = blockIdx.x;
+    uint16_t* rs = reinterpret_cast<uint16_t*>(lds);                  // nblk + 1: run starts in the bin's keys
+    uint16_t* roff = rs + nblk + 1;                                   // nblk: run offsets in the block regions
+    uint32_t* perm = lds;                                             // later: rows_max rows, longest first
+    uint32_t* pcls = lds + rows_max;                                  // and 65 class counters
+    uint32_t* rowst = lds + rv_head_words(nblk, rows_max);            // rows_max + 1: row starts
+    uint32_t* grouped = rowst + rows_max + 1;                         // cap: keys grouped by row
     const int64_t j0 = static_cast<int64_t>(b) << cshift;
     const int rows = static_cast<int>(N - j0 < rows_max ? N - j0 : rows_max);
     const int hs = kbits + sbits;
     const uint32_t smask = (1u << sbits) - 1u;
     const uint32_t kmask = (1u << kbits) - 1u;
+    const uint32_t region = static_cast<uint32_t>(spb * K);
 
+    // run lengths (in the group buffer's space), scanned into starts
+    const uint16_t* m0 = meta + static_cast<int64_t>(b) * nblk;   // bin-major: this bin's and the next row
     for (int q = t; q < nblk; q += RP) {
-        rstart[q] = meta_cnt[static_cast<int64_t>(b) * nblk + q];
-        rbase[q] = static_cast<uint32_t>(q * spb * K) + meta_off[static_cast<int64_t>(b) * nblk + q];
+        const uint32_t o0 = m0[q];
+        grouped[q] = static_cast<uint32_t>(m0[q + nblk]) - o0;
+        roff[q] = static_cast<uint16_t>(o0);
     }
-    for (int r = t; r < rows; r += RP) rowstart[r] = 0u;
+    for (int r = t; r <= rows_max; r += RP) rowst[r] = 0u;
     __syncthreads();
-    const uint32_t T = block_exclusive_scan<RP>(rstart, nblk, wsum);
-    if (t == 0) rstart[nblk] = T;
-    __syncthreads();
-    // keys per row, one run per thread, a run's keys loaded together; when
-    // the bin's keys fit, they are kept in LDS in run order
-    // (only when the whole bin is one pass: the copy's space later holds the stages)
-    const bool keep = T <= static_cast<uint32_t>(ubuf) && T <= static_cast<uint32_t>(cap) && rows <= RP;
-    for (int q = t; q < nblk; q += RP) {
-        const uint32_t len = rstart[q + 1] - rstart[q];
-        const uint32_t* run = part + rbase[q];
-        const uint32_t at = rstart[q];
-        for (uint32_t j = 0; j < len; j += kRvGather) {
-            uint32_t kk[kRvGather];
+    const uint32_t T = block_exclusive_scan<RP>(grouped, nblk, wsum);
+    auto convert = [&](uint32_t key, uint32_t q) {
+        return (((key >> sbits) & kmask) << nbits) | (q * static_cast<uint32_t>(spb) + (key & smask));
+    };
+
+    if (rows <= RP && T <= static_cast<uint32_t>(cap) && T <= static_cast<uint32_t>(RP * KPT)) {
+        for (int q = t; q <= nblk; q += RP) rs[q] = static_cast<uint16_t>(q < nblk ? grouped[q] : T);
+        __syncthreads();
+        // the run of every key (in the group buffer's space)
+        for (int q = t; q < nblk; q += RP)
+            for (uint32_t e = rs[q]; e < rs[q + 1]; ++e) grouped[e] = static_cast<uint32_t>(q);
+        __syncthreads();
+        uint32_t qq[KPT], key[KPT];
 #pragma unroll
-            for (int u = 0; u < kRvGather; ++u) kk[u] = j + u < len ? run[j + u] : 0u;
+        for (int u = 0; u < KPT; ++u) {
+            const uint32_t e = t + u * RP;
+            qq[u] = e < T ? grouped[e] : 0u;
+        }
 #pragma unroll
-            for (int u = 0; u < kRvGather; ++u) {
-                if (j + u >= len) continue;
-                atomicAdd(&rowstart[kk[u] >> hs], 1u);
-                if (keep) ubase[at + j + u] = kk[u];
+        for (int u = 0; u < KPT; ++u) {
+            const uint32_t e = t + u * RP;
+            key[u] = e < T ? part[qq[u] * region + roff[qq[u]] + (e - rs[qq[u]])] : 0u;
+        }
+        __syncthreads();   // the run tables are dead: the groups go there, the row order in their head
+        for (int c = t; c <= 64; c += RP) pcls[c] = 0u;
+        uint32_t rsl[KPT];   // row << 16 | slot in the row's group
+#pragma unroll
+        for (int u = 0; u < KPT; ++u) {
+            rsl[u] = 0u;
+            if (t + u * RP < T) {
+                const uint32_t row = key[u] >> hs;
+                rsl[u] = (row << 16) | atomicAdd(&rowst[row], 1u);
+                key[u] = convert(key[u], qq[u]);
             }
         }
+        __syncthreads();
+        block_exclusive_scan<RP>(rowst, rows, wsum);
+#pragma unroll
+        for (int u = 0; u < KPT; ++u)
+            if (t + u * RP < T) grouped[rowst[rsl[u] >> 16] + (rsl[u] & 0xFFFFu)] = key[u];
+        if (t == 0) rowst[rows] = T;
+        __syncthreads();
+        // lanes take the rows longest first (by classes of key counts), so
+        // that a wave's loop runs about as long as each of its rows
+        uint32_t cls = 0u, cslot = 0u;
+        if (t < rows) {
+            const uint32_t n = rowst[t + 1] - rowst[t];
+            cls = 63u - (n < 63u ? n : 63u);
+            cslot = atomicAdd(&pcls[cls], 1u);
+        }
+        __syncthreads();
+        if (t < 64) {
+            const uint32_t c = pcls[t];
+            uint32_t inc = c;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const uint32_t x = __shfl_up(inc, o);
+                if (t >= o) inc += x;
+            }
+            pcls[t] = inc - c;
+        }
+        __syncthreads();
+        if (t < rows) perm[pcls[cls] + cslot] = static_cast<uint32_t>(t);
+        __syncthreads();
+        if (t < rows) {
+            const int r = static_cast<int>(perm[t]);
+            const int64_t j = j0 + r;
+            uint32_t fw[KMAX];
+            rv_load_row<KMAX>(fwd + j * K, K, fw);
+            const uint32_t* g = grouped + rowst[r];
+            const uint32_t n = rowst[r + 1] - rowst[r];
+            bool ok;
+            if (K == KMAX) {
+                uint32_t o[KMAX];
+                ok = rv_merge_full<KMAX>(fw, g, n, nbits, o);
+                if (ok) {
+                    uint4* d4 = reinterpret_cast<uint4*>(out + j * K);
+#pragma unroll
+                    for (int m = 0; m < KMAX / 4; ++m)
+                        d4[m] = make_uint4(o[4 * m], o[4 * m + 1], o[4 * m + 2], o[4 * m + 3]);
+                }
+            } else {
+                ok = rv_merge_lane<KMAX>(fw, K, g, n, nbits, out + j * K);
+            }
+            if (!ok) slow_rows[atomicAdd(slow_count, 1u)] = (static_cast<uint32_t>(b) << 11) | static_cast<uint32_t>(r);
+        }
+        return;
+    }
+    if (DEFER) {
+        if (t == 0) big_bins[1 + atomicAdd(&big_bins[0], 1u)] = static_cast<uint32_t>(b);
+        return;
+    }
+
+    // larger bins: the run starts stay in the head of the group buffer (32-bit,
+    // the bin may hold more than 65,535 keys); every pass loads the bin's keys
+    // in the same coalesced order as above (a key's run by binary search) and
+    // groups the rows of one range whose keys fit the rest of the buffer
+    uint32_t* rs32 = grouped;   // nblk + 1, already the scanned run starts
+    if (t == 0) rs32[nblk] = T;
+    uint32_t* gbuf = grouped + nblk + 1;
+    const int gcap = cap - nblk - 1;
+    __syncthreads();
+    // the runs of G keys by G interleaved binary searches (the last run
+    // starting at or before each key), then the G loads
+    constexpr int G = 8;   // keys loaded together per thread
+    int top = 1;
+    while (2 * top <= nblk) top *= 2;
+    auto load_keys = [&](uint32_t e0, uint32_t (&kk)[G], uint32_t (&qq)[G]) {
+        int pos[G];
+#pragma unroll
+        for (int u = 0; u < G; ++u) pos[u] = 0;
+        for (int w = top; w > 0; w >>= 1) {
+#pragma unroll
+            for (int u = 0; u < G; ++u) {
+                const int c = pos[u] + w;
+                if (c < nblk && rs32[c] <= e0 + u * RP) pos[u] = c;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < G; ++u) {
+            const uint32_t e = e0 + u * RP;
+            qq[u] = static_cast<uint32_t>(pos[u]);
+            kk[u] = e < T ? part[qq[u] * region + roff[pos[u]] + (e - rs32[pos[u]])] : 0u;
+        }
+    };
+    for (uint32_t e0 = t; e0 < T; e0 += G * RP) {
+        uint32_t kk[G], qq[G];
+        load_keys(e0, kk, qq);
+#pragma unroll
+        for (int u = 0; u < G; ++u)
+            if (e0 + u * RP < T) atomicAdd(&rowst[kk[u] >> hs], 1u);
     }
     __syncthreads();
-    block_exclusive_scan<RP>(rowstart, rows, wsum);
-    if (t == 0) rowstart[rows] = T;
+    block_exclusive_scan<RP>(rowst, rows, wsum);
+    if (t == 0) rowst[rows] = T;
     __syncthreads();
-
-    const int ST = K + 1;
-    uint32_t* wst = ubase + w * 64 * ST;
     for (int r0 = 0; r0 < rows;) {
-        // the longest row range from r0 whose keys fit in LDS; a row beyond
-        // the capacity goes to the slow kernel
+        // the longest row range from r0 whose keys fit (rows >= r0 still hold their starts)
         int lo = r0 + 1, hi = r0 + RP < rows ? r0 + RP : rows;
         while (lo < hi) {
             const int mid = (lo + hi + 1) >> 1;
-            if (rowstart[mid] - rowstart[r0] <= static_cast<uint32_t>(cap)) lo = mid;
+            if (rowst[mid] - rowst[r0] <= static_cast<uint32_t>(gcap)) lo = mid;
             else hi = mid - 1;
         }
         const int r1 = lo;
-        const bool giant = rowstart[r0 + 1] - rowstart[r0] > static_cast<uint32_t>(cap);
+        const uint32_t base = rowst[r0];
+        const bool giant = rowst[r0 + 1] - base > static_cast<uint32_t>(gcap);
+        __syncthreads();   // every thread has read the starts before the placement moves them
         if (giant) {
             if (t == 0) slow_rows[atomicAdd(slow_count, 1u)] = (static_cast<uint32_t>(b) << 11) | r0;
             r0 = r1;
             continue;
         }
-        for (int r = r0 + t; r < r1; r += RP) cursor[r] = rowstart[r] - rowstart[r0];
-        __syncthreads();
-        if (keep) {
-            // from the LDS copy, one run per thread
-            for (int q = t; q < nblk; q += RP) {
-                const uint32_t* run = ubase + rstart[q];
-                const uint32_t len = rstart[q + 1] - rstart[q];
-                const uint32_t sbase = static_cast<uint32_t>(q * spb);
-                for (uint32_t j = 0; j < len; j += 8) {
-                    uint32_t kk[8], pos[8];
+        // placement: rowst[r] becomes the end of row r (= the old start of row r + 1)
+        for (uint32_t e0 = t; e0 < T; e0 += G * RP) {
+            uint32_t kk[G], qq[G];
+            load_keys(e0, kk, qq);
 #pragma unroll
-                    for (int u = 0; u < 8; ++u) kk[u] = j + u < len ? run[j + u] : 0u;
-#pragma unroll
-                    for (int u = 0; u < 8; ++u) {
-                        const int row = static_cast<int>(kk[u] >> hs);
-                        pos[u] = (j + u < len && row >= r0 && row < r1) ? atomicAdd(&cursor[row], 1u) : 0xFFFFFFFFu;
-                    }
-#pragma unroll
-                    for (int u = 0; u < 8; ++u)
-                        if (pos[u] != 0xFFFFFFFFu)
-                            grouped[pos[u]] = (((kk[u] >> sbits) & kmask) << nbits) | (sbase + (kk[u] & smask));
-                }
-            }
-        } else {
-            for (int q = t; q < nblk; q += RP) {
-                const uint32_t len = rstart[q + 1] - rstart[q];
-                const uint32_t* run = part + rbase[q];
-                const uint32_t sbase = static_cast<uint32_t>(q * spb);
-                for (uint32_t j = 0; j < len; j += kRvGather) {
-                    uint32_t kk[kRvGather];
-#pragma unroll
-                    for (int u = 0; u < kRvGather; ++u) kk[u] = j + u < len ? run[j + u] : 0xFFFFFFFFu;
-#pragma unroll
-                    for (int u = 0; u < kRvGather; ++u) {
-                        if (j + u >= len) continue;
-                        const uint32_t key = kk[u];
-                        const int row = static_cast<int>(key >> hs);
-                        if (row < r0 || row >= r1) continue;
-                        grouped[atomicAdd(&cursor[row], 1u)] =
-                            (((key >> sbits) & kmask) << nbits) | (sbase + (key & smask));
-                    }
-                }
+            for (int u = 0; u < G; ++u) {
+                const int row = static_cast<int>(kk[u] >> hs);
+                if (e0 + u * RP < T && row >= r0 && row < r1)
+                    gbuf[atomicAdd(&rowst[row], 1u) - base] = convert(kk[u], qq[u]);
             }
         }
-        __syncthreads();   // the LDS copy of the keys is dead from here: its space holds the stages
-        const int wr0 = r0 + w * 64;
-        const int wrn = wr0 < r1 ? (r1 - wr0 < 64 ? r1 - wr0 : 64) : 0;
-        rv_stage_in<KMAX>(fwd + (j0 + wr0) * K, wrn, K, wst, lane);
-        wave_sync();
-        if (lane < wrn) {
-            uint32_t* st = wst + lane * ST;
+        __syncthreads();
+        const int r = r0 + t;
+        if (r < r1) {
+            const uint32_t s0 = r == r0 ? base : rowst[r - 1];
+            const int64_t j = j0 + r;
             uint32_t fw[KMAX];
-#pragma unroll
-            for (int k = 0; k < KMAX; ++k) fw[k] = k < K ? st[k] : 0xFFFFFFFFu;
-            const int r = wr0 + lane;
-            if (!rv_merge_lane<KMAX>(fw, K, grouped + (rowstart[r] - rowstart[r0]), rowstart[r + 1] - rowstart[r],
-                                     nbits, st))
-                slow_rows[atomicAdd(slow_count, 1u)] = (static_cast<uint32_t>(b) << 11) | r;
+            rv_load_row<KMAX>(fwd + j * K, K, fw);
+            if (!rv_merge_lane<KMAX>(fw, K, gbuf + (s0 - base), rowst[r] - s0, nbits, out + j * K))
+                slow_rows[atomicAdd(slow_count, 1u)] = (static_cast<uint32_t>(b) << 11) | static_cast<uint32_t>(r);
         }
-        wave_sync();
-        rv_stage_out<KMAX>(out + (j0 + wr0) * K, wrn, K, wst, lane);
-        __syncthreads();
+        __syncthreads();   // the next pass overwrites the groups
         r0 = r1;
+    }
+}
+
+// One block per bin, bins dealt XCD-major (workgroup ids go to the 8 XCDs
+// round robin, so each XCD takes a contiguous range of bins).
+template <int KMAX, int RP>
+__global__ void __launch_bounds__(RP) rv_merge_kernel(const uint32_t* __restrict__ fwd, int64_t N, int K, int nblk,
+                                                      int64_t spb, int cshift, int nbins, int kbits, int sbits,
+                                                      int nbits, const uint32_t* __restrict__ part,
+                                                      const uint16_t* __restrict__ meta, uint32_t* __restrict__ out,
+                                                      int cap, uint32_t* __restrict__ slow_rows,
+                                                      uint32_t* __restrict__ slow_count, uint32_t* __restrict__ big_bins)
+{
+    extern __shared__ uint32_t lds[];
+    __shared__ uint32_t wsum[RP / 64 + 1];
+    const int per_xcd = (nbins + 7) / 8;
+    const int b = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    if (b >= nbins) return;
+    rv_merge_bin<KMAX, RP, true>(b, fwd, N, K, nblk, spb, cshift, nbins, kbits, sbits, nbits, part, meta, out, cap,
+                                 slow_rows, slow_count, big_bins, lds, wsum);
+}
+
+// The bins rv_merge_kernel deferred, by blocks of kRvBigThreads threads with
+// a larger group buffer (fast path up to 18,432 keys, else the general path);
+// a fixed grid walks the list, every block ends when it is done.
+template <int KMAX>
+__global__ void __launch_bounds__(kRvBigThreads) rv_big_kernel(const uint32_t* __restrict__ fwd, int64_t N, int K, int nblk,
+                                                      int64_t spb, int cshift, int nbins, int kbits, int sbits,
+                                                      int nbits, const uint32_t* __restrict__ part,
+                                                      const uint16_t* __restrict__ meta, uint32_t* __restrict__ out,
+                                                      int cap, uint32_t* __restrict__ slow_rows,
+                                                      uint32_t* __restrict__ slow_count,
+                                                      const uint32_t* __restrict__ big_bins)
+{
+    extern __shared__ uint32_t lds[];
+    __shared__ uint32_t wsum[kRvBigThreads / 64 + 1];
+    const uint32_t n = big_bins[0];
+    for (uint32_t i = blockIdx.x; i < n; i += gridDim.x) {
+        rv_merge_bin<KMAX, kRvBigThreads, false>(static_cast<int>(big_bins[1 + i]), fwd, N, K, nblk, spb, cshift, nbins, kbits,
+                                        sbits, nbits, part, meta, out, cap, slow_rows, slow_count, nullptr, lds, wsum);
+        __syncthreads();   // the next bin reuses the LDS
     }
 }
 
@@ -676,61 +870,77 @@ static int bits_for(int64_t n)   // bits of the values 0 .. n-1
     return b;
 }
 
+size_t rv_merge_lds(const RvPlan& p)
+{
+    const size_t words = static_cast<size_t>(rv_head_words(p.nblk, 1 << p.cshift)) + (size_t(1) << p.cshift) + 1 + p.cap;
+    return words * sizeof(uint32_t);
+}
+
 bool rv_plan(int64_t N, int K, RvPlan& p)
 {
     if (N < 1 || K < 1 || K > 64) return false;
     const int64_t E = N * K;
+    if (E >= (int64_t(1) << 32)) return false;
     p.rp = K > 32 ? 128 : 256;
     p.cshift = K > 32 ? 7 : 8;
     while (p.cshift < kRvMaxBinShift && ceil_div(N, int64_t(1) << p.cshift) > kRvMaxBins) ++p.cshift;
     p.nbins = static_cast<int>(ceil_div(N, int64_t(1) << p.cshift));
     if (p.nbins > kRvMaxBins) return false;
-    p.nblk = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(1024, ceil_div(E, 65536))));
-    p.spb = ceil_div(ceil_div(N, p.nblk), 4) * 4;
+    p.spb = std::min<int64_t>(kRvMaxBlockEdges / K, N);
     p.nblk = static_cast<int>(ceil_div(N, p.spb));
     p.kbits = bits_for(K);
     p.sbits = bits_for(p.spb);
     p.nbits = bits_for(N);
-    if (p.spb * K >= (int64_t(1) << 24)) return false;           // divmod_small
     if (p.cshift + p.kbits + p.sbits > 32) return false;
     if (p.kbits + p.nbits > 31) return false;   // 0xFFFFFFFF stays free as the empty marker
-    if (E >= (int64_t(1) << 32)) return false;
+    // group buffer: an average bin + 1/16, more when 4 blocks per CU still fit
     p.cap = p.rp * K * 17 / 16;
-    p.ubuf = std::max(p.cap, p.rp * (K + 1));
-    return true;
+    RvPlan q = p;
+    q.cap = 0;
+    // (less the static scan words and the LDS allocation granule)
+    const int64_t room = (kRvLdsPerBlock - 512 - static_cast<int64_t>(rv_merge_lds(q))) / 4;
+    p.cap = static_cast<int>(std::max<int64_t>(p.cap, std::min<int64_t>(room, int64_t(p.rp) * kRvKeysPerThread)));
+    // the run lengths are scanned in the group buffer, whose head keeps them
+    // in the general path: leave room for the longest rows besides
+    p.cap = std::max(p.cap, p.nblk + 1 + 4 * p.rp);
+    // deferred bins: larger blocks, two per CU
+    const int64_t room_big = (80 * 1024 - 1024 - static_cast<int64_t>(rv_merge_lds(q))) / 4;
+    p.cap_big = static_cast<int>(std::min<int64_t>(room_big, int64_t(kRvBigThreads) * kRvKeysPerThread));
+    if (p.cap_big < p.cap) return false;
+    return rv_merge_lds(p) <= 160 * 1024;
 }
 
-size_t rv_merge_lds(const RvPlan& p, int K)
+void launch_rv(const uint32_t* fwd, int64_t N, int K, const RvPlan& p, uint32_t* part, uint16_t* meta_blk,
+               uint16_t* meta, uint32_t* out, int* err, uint32_t* slow_rows, uint32_t* slow_count, uint32_t* big_bins,
+               hipStream_t s)
 {
-    const size_t words = static_cast<size_t>(2 * p.nblk + 1) + 2 * (size_t(1) << p.cshift) + 1 + p.cap + p.ubuf;
-    return words * sizeof(uint32_t);
-}
-
-void launch_rv(const uint32_t* fwd, int64_t N, int K, const RvPlan& p, uint32_t* part, uint32_t* meta_cnt,
-               uint32_t* meta_off, uint32_t* out, int* err, uint32_t* slow_rows, uint32_t* slow_count, hipStream_t s)
-{
-#define GT_RV_SCATTER(SC)                                                                                      \
-    do {                                                                                                       \
-        const size_t lds_s = rv_scatter_lds(p.nbins, SC);                                                      \
-        ensure_lds(reinterpret_cast<const void*>(&rv_scatter_kernel<SC>), lds_s);                              \
-        hipLaunchKernelGGL((rv_scatter_kernel<SC>), dim3(p.nblk), dim3(kRvScatterThreads), lds_s, s, fwd, N, K,  \
-                           p.spb, p.cshift, p.nbins, p.kbits, p.sbits, part, meta_cnt, meta_off, err, slow_count); \
-    } while (0)
-    if (rv_scatter_lds(p.nbins, 16384) <= 150 * 1024) GT_RV_SCATTER(16384);
-    else GT_RV_SCATTER(8192);
-#undef GT_RV_SCATTER
-    const size_t lds = rv_merge_lds(p, K);
+    const size_t lds_s = (static_cast<size_t>(p.nbins) + kRvMaxBlockEdges) * sizeof(uint32_t);
+    ensure_lds(reinterpret_cast<const void*>(&rv_scatter_kernel), lds_s);
+    hipLaunchKernelGGL(rv_scatter_kernel, dim3(p.nblk), dim3(kRvScatterThreads), lds_s, s, fwd, N, K, p.spb, p.cshift,
+                       p.nbins, p.kbits, p.sbits, part, meta_blk, err, slow_count);
+    hipLaunchKernelGGL(rv_meta_transpose_kernel, dim3(static_cast<unsigned>(ceil_div(p.nbins + 1, 64)),
+                                                      static_cast<unsigned>(ceil_div(p.nblk, 64))),
+                       dim3(256), 0, s, meta_blk, p.nblk, p.nbins, meta, big_bins);
+    const size_t lds = rv_merge_lds(p);
+    RvPlan pb = p;
+    pb.cap = p.cap_big;
+    const size_t lds_big = rv_merge_lds(pb);
+    const int grid = 8 * ((p.nbins + 7) / 8);
 #define GT_RV_MERGE(KM, R)                                                                                       \
     do {                                                                                                         \
         ensure_lds(reinterpret_cast<const void*>(&rv_merge_kernel<KM, R>), lds);                                 \
-        hipLaunchKernelGGL((rv_merge_kernel<KM, R>), dim3(p.nbins), dim3(R), lds, s, fwd, N, K, p.nblk, p.spb,   \
-                           p.cshift, p.kbits, p.sbits, p.nbits, part, meta_cnt, meta_off, out, p.cap, p.ubuf,    \
-                           slow_rows, slow_count);                                                               \
+        hipLaunchKernelGGL((rv_merge_kernel<KM, R>), dim3(grid), dim3(R), lds, s, fwd, N, K, p.nblk, p.spb,      \
+                           p.cshift, p.nbins, p.kbits, p.sbits, p.nbits, part, meta, out, p.cap, slow_rows,      \
+                           slow_count, big_bins);                                                                \
+        ensure_lds(reinterpret_cast<const void*>(&rv_big_kernel<KM>), lds_big);                                  \
+        hipLaunchKernelGGL((rv_big_kernel<KM>), dim3(std::min(p.nbins, 512)), dim3(kRvBigThreads), lds_big, s, fwd, \
+                           N, K,                                                                                 \
+                           p.nblk, p.spb, p.cshift, p.nbins, p.kbits, p.sbits, p.nbits, part, meta, out,         \
+                           p.cap_big, slow_rows, slow_count, big_bins);                                          \
         const size_t lds_w = (2 * static_cast<size_t>(p.nblk) + 1 + 64 * ((KM + 1) / 2) + KM + 1) * 4 * 4;     \
         ensure_lds(reinterpret_cast<const void*>(&rv_slow_kernel<KM>), lds_w);                                   \
         hipLaunchKernelGGL((rv_slow_kernel<KM>), dim3(256), dim3(256), lds_w, s, fwd, N, K, p.nblk, p.spb,       \
-                           p.cshift, p.kbits, p.sbits, p.nbits, part, meta_cnt, meta_off, slow_rows, slow_count, \
-                           out);                                                                                 \
+                           p.cshift, p.nbins, p.kbits, p.sbits, p.nbits, part, meta, slow_rows, slow_count, out); \
     } while (0)
     if (K <= 16) GT_RV_MERGE(16, 256);
     else if (K <= 32) GT_RV_MERGE(32, 256);
