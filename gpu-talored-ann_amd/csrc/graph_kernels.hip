@@ -228,10 +228,34 @@ __device__ __forceinline__ uint32_t prune_hash(int32_t v, uint32_t mask)
     return ((static_cast<uint32_t>(v) * 0x9E3779B1u) >> 15) & mask;
 }
 
-template <int E>
+// Last processing position p with off[p] <= id (positions 0 .. nb - 1).
+__device__ __forceinline__ int prune_pos_of(const uint32_t* __restrict__ off, int nb, uint32_t id)
+{
+    int lo = 0, hi = nb - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (off[mid] <= id) lo = mid;
+        else hi = mid - 1;
+    }
+    return lo;
+}
+
+// ROWS selects where the rows live:
+//   0: the whole table, row r at G + r * M;
+//   1: a chunk's rows and all their neighbours' rows in a compact table, row r
+//      at G + map.cidx[r] * M (every row the chunk reads is loaded);
+//   2: bucket windows (src/prune_windowed_gpu.cu:181-326 semantics): rows are
+//      numbered by processing position, position q owning ids
+//      [off[q], off[q + 1]); row a at position p may count detours only
+//      through neighbours whose position is in p's window (win[p * W ..],
+//      win_len[p] entries) and loaded (cbase[q] >= 0: the compact row of
+//      off[q]); any other neighbour contributes nothing.
+// ROWS 1 and 2 prune rows map.a0 .. map.a0 + map.n - 1 into output rows
+// 0 .. n - 1.
+template <int E, int ROWS>
 __global__ void __launch_bounds__(256) cagra_prune_kernel(const int32_t* __restrict__ G, int64_t N, int M, int K,
                                                           uint32_t* __restrict__ out,
-                                                          unsigned long long* __restrict__ bad_row)
+                                                          unsigned long long* __restrict__ bad_row, PruneMap map)
 {
     constexpr int MM = 64 * E;
     constexpr int NBK = 2 * MM;               // home buckets
@@ -244,8 +268,16 @@ __global__ void __launch_bounds__(256) cagra_prune_kernel(const int32_t* __restr
     __shared__ __align__(16) uint32_t tab[4][SLOTS];
     __shared__ uint32_t tag[4][TAGW];         // slot s: bits 8*(s%4).. of word s/4
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int64_t a = static_cast<int64_t>(blockIdx.x) * 4 + w;
-    if (a >= N) return;
+    const int64_t a0 = ROWS == 0 ? 0 : map.a0;
+    const int64_t a = a0 + static_cast<int64_t>(blockIdx.x) * 4 + w;
+    if (a >= (ROWS == 0 ? N : map.a0 + map.n)) return;
+    int64_t arow = a;
+    int pa = 0;
+    if (ROWS == 1) arow = map.cidx[a];
+    if (ROWS == 2) {
+        pa = prune_pos_of(map.off, map.n_buckets, static_cast<uint32_t>(a));
+        arow = map.cbase[pa] + (a - map.off[pa]);
+    }
 
     for (int s = lane; s < SLOTS; s += 64) tab[w][s] = kEmpty;
     for (int s = lane; s < TAGW; s += 64) tag[w][s] = 0u;
@@ -255,7 +287,24 @@ __global__ void __launch_bounds__(256) cagra_prune_kernel(const int32_t* __restr
     for (int e = 0; e < E; ++e) {
         const int k = lane + 64 * e;
         col[e] = k < M ? k : M - 1;
-        A[e] = k < M ? G[a * M + k] : -1;
+        A[e] = k < M ? G[arow * M + k] : -1;
+    }
+    // the row of each neighbour in G (-1: not to be read)
+    int64_t nrow[E];
+#pragma unroll
+    for (int e = 0; ROWS != 0 && e < E; ++e) {
+        const bool v = A[e] >= 0 && A[e] < N;
+        nrow[e] = v ? static_cast<int64_t>(A[e]) : -1;
+        if (ROWS == 1 && v) nrow[e] = map.cidx[A[e]];
+        if (ROWS == 2 && v) {
+            const int q = prune_pos_of(map.off, map.n_buckets, static_cast<uint32_t>(A[e]));
+            const int32_t* wp = map.win + static_cast<int64_t>(pa) * map.W;
+            const int wl = map.win_len[pa];
+            bool inw = false;
+            for (int i = 0; i < wl; ++i) inw |= wp[i] == q;
+            const int64_t cb = map.cbase[q];
+            nrow[e] = inw && cb >= 0 ? cb + (A[e] - static_cast<int64_t>(map.off[q])) : -1;
+        }
     }
     wave_sync();
     // insertion; every entry ends up at most dmax buckets past its home
@@ -282,14 +331,22 @@ __global__ void __launch_bounds__(256) cagra_prune_kernel(const int32_t* __restr
     int32_t ring[kPruneDepth][E];
     bool rok[kPruneDepth];
     auto fetch = [&](int kAD, int32_t (&b)[E], bool& ok) {
-        int32_t d = -1;
+        int64_t d = -1;
         if (kAD < M - 1) {
 #pragma unroll
             for (int e = 0; e < E; ++e)
-                if ((kAD >> 6) == e) d = __builtin_amdgcn_readlane(A[e], kAD & 63);
+                if ((kAD >> 6) == e) {
+                    if (ROWS == 0) {
+                        d = __builtin_amdgcn_readlane(A[e], kAD & 63);
+                    } else {
+                        const uint32_t lo = __builtin_amdgcn_readlane(static_cast<uint32_t>(nrow[e]), kAD & 63);
+                        const int32_t hi = __builtin_amdgcn_readlane(static_cast<int32_t>(nrow[e] >> 32), kAD & 63);
+                        d = (static_cast<int64_t>(hi) << 32) | lo;
+                    }
+                }
         }
-        ok = d >= 0 && d < N;
-        const int32_t* row = G + (ok ? static_cast<int64_t>(d) : int64_t(0)) * M;
+        ok = ROWS == 0 ? d >= 0 && d < N : d >= 0;
+        const int32_t* row = G + (ok ? d : int64_t(0)) * M;
 #pragma unroll
         for (int e = 0; e < E; ++e) b[e] = row[col[e]];
     };
@@ -374,6 +431,7 @@ __global__ void __launch_bounds__(256) cagra_prune_kernel(const int32_t* __restr
         if (lane == 0) atomicMin(bad_row, static_cast<unsigned long long>(a));
         return;
     }
+    const int64_t orow = a - a0;
     // position = valid entries before this one in (count, rank) order; one
     // key per entry, count << 8 | rank (counts < 128), invalid = all ones,
     // kept in the hash table's LDS (no longer read); fewer LDS bytes per
@@ -399,7 +457,7 @@ __global__ void __launch_bounds__(256) cagra_prune_kernel(const int32_t* __restr
     }
 #pragma unroll
     for (int e = 0; e < E; ++e)
-        if (A[e] >= 0 && pos[e] < K) out[a * K + pos[e]] = static_cast<uint32_t>(A[e]);
+        if (A[e] >= 0 && pos[e] < K) out[orow * K + pos[e]] = static_cast<uint32_t>(A[e]);
 }
 
 // ------------------------------------------------------------------ reverse merge
@@ -1370,10 +1428,33 @@ void launch_cagra_prune(const int32_t* G, int64_t N, int M, int K, uint32_t* out
 {
     GT_REQUIRE(M >= 1 && M <= kPruneMaxM, "prune supports intermediate degree <= 128");
     if (N <= 0) return;
+    const PruneMap none{};
     if (M <= 64)
-        hipLaunchKernelGGL((cagra_prune_kernel<1>), dim3(grid_for(N, 4)), dim3(256), 0, s, G, N, M, K, out, bad_row);
+        hipLaunchKernelGGL((cagra_prune_kernel<1, 0>), dim3(grid_for(N, 4)), dim3(256), 0, s, G, N, M, K, out, bad_row,
+                           none);
     else
-        hipLaunchKernelGGL((cagra_prune_kernel<2>), dim3(grid_for(N, 4)), dim3(256), 0, s, G, N, M, K, out, bad_row);
+        hipLaunchKernelGGL((cagra_prune_kernel<2, 0>), dim3(grid_for(N, 4)), dim3(256), 0, s, G, N, M, K, out, bad_row,
+                           none);
+    GT_HIP(hipGetLastError());
+}
+
+void launch_cagra_prune_mapped(const int32_t* G, int64_t N, int M, int K, uint32_t* out, unsigned long long* bad_row,
+                               const PruneMap& map, int rows_mode, hipStream_t s)
+{
+    GT_REQUIRE(M >= 1 && M <= kPruneMaxM, "prune supports intermediate degree <= 128");
+    GT_REQUIRE(rows_mode == 1 || rows_mode == 2, "bad prune row mode");
+    if (map.n <= 0) return;
+#define GT_PRUNE_MAP(EE, RR)                                                                                   \
+    hipLaunchKernelGGL((cagra_prune_kernel<EE, RR>), dim3(grid_for(map.n, 4)), dim3(256), 0, s, G, N, M, K, out, \
+                       bad_row, map)
+    if (M <= 64) {
+        if (rows_mode == 1) GT_PRUNE_MAP(1, 1);
+        else GT_PRUNE_MAP(1, 2);
+    } else {
+        if (rows_mode == 1) GT_PRUNE_MAP(2, 1);
+        else GT_PRUNE_MAP(2, 2);
+    }
+#undef GT_PRUNE_MAP
     GT_HIP(hipGetLastError());
 }
 

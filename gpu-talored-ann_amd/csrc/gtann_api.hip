@@ -86,6 +86,14 @@ void launch_merge_rounds(const int32_t* ri, const float* rd, const int32_t* ni, 
                          int32_t* oi, float* od, hipStream_t s);
 void launch_translate(const uint32_t* g, const uint32_t* inv, int64_t N, int K, uint32_t* out, uint32_t* hits,
                       int* err, hipStream_t s);
+void launch_cagra_prune_mapped(const int32_t* G, int64_t N, int M, int K, uint32_t* out, unsigned long long* bad_row,
+                               const PruneMap& map, int rows_mode, hipStream_t s);
+// ooc_kernels.hip
+void launch_set_cidx(const int32_t* ids, int64_t n, int32_t* cidx, hipStream_t s);
+void launch_route(const uint32_t* fwd, int64_t nrows, int K, int64_t N, int64_t R, int nchunks, int64_t s0,
+                  uint32_t* counts, uint32_t* cursor, unsigned long long* recs, int* err, bool place, hipStream_t s);
+void launch_rec_group(const unsigned long long* recs, int64_t n, uint32_t* deg, uint32_t* slot, const uint32_t* off,
+                      unsigned long long* keys, bool scatter, hipStream_t s);
 // refine_kernel.hip
 void launch_refine_2hop(const float* X, const float* norms, int64_t N, int Dp, int metric, const int32_t* in_ids,
                         const float* in_d, int M, int S, int32_t* out_ids, float* out_d, hipStream_t s);
@@ -229,7 +237,8 @@ enum Ws {
     W_MEMBERS, W_TASKS, W_POOL, W_PART_I, W_PART_D, W_G1, W_G2, W_G3, W_DEG, W_OFF, W_CUR, W_KEYS, W_SUMS, W_FLAG,
     W_TMP, W_OUT, W_IN, W_PROBE_I, W_PROBE_D, W_WORST, W_X8, W_NORMS8, W_C8, W_CNORMS8,
     W_SUBROWS, W_SUBID, W_SUBD, W_SUBOFF, W_MEMBERS2, W_SUBNN, W_SUBNND, W_SUBBASE, W_SUBCNT, W_CHAINPOS,
-    W_LHIST, W_LOFFS, W_LSUMS, W_CAND, W_CANDCNT, W_STATS, W_COUNT_
+    W_LHIST, W_LOFFS, W_LSUMS, W_CAND, W_CANDCNT, W_STATS,
+    W_OOC_A, W_OOC_B, W_OOC_C, W_OOC_D, W_OOC_E, W_OOC_F, W_OOC_G, W_COUNT_
 };
 static_assert(W_COUNT_ <= 64, "workspace slots");
 
@@ -913,18 +922,26 @@ static void sub_order_members(Ctx& c, const DevMatrix& X, const Buckets& b, int 
 // seed_d (device, optional) caps kept keys at the running M-th distance.
 // own / probes select the pool segments: the bucket's own members and the
 // members of its probe buckets (both by default).
+// With b1 >= 0 only buckets [b0, b1) run and their members' lists go to
+// compact rows (member position - offsets[b0]), seeded from the same rows
+// (the out-of-core build's chunks).
 static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M, int metric, const float* seed_d,
                              int32_t* out_ids, float* out_d, int64_t* max_pool, int64_t* max_bucket,
-                             double* pairs, bool own = true, bool probes = true)
+                             double* pairs, bool own = true, bool probes = true, int64_t b0 = 0, int64_t b1 = -1)
 {
     const int64_t C = static_cast<int64_t>(b.offsets.size()) - 1;
     const int64_t N = X.N;
+    const bool compact = b1 >= 0;
+    if (!compact) b1 = C;
+    GT_REQUIRE(b0 >= 0 && b0 <= b1 && b1 <= C, "bucket range out of bounds");
+    const int64_t qbase = b.offsets[static_cast<size_t>(b0)];
+    const int64_t rows = compact ? b.offsets[static_cast<size_t>(b1)] - qbase : N;
     Trace tr;
     std::vector<CopyTaskH> tasks;
     std::vector<int64_t> pool_off(static_cast<size_t>(C + 1), 0);
     int64_t total = 0;
     std::vector<int64_t> segs;
-    for (int64_t bb = 0; bb < C; ++bb) {
+    for (int64_t bb = b0; bb < b1; ++bb) {
         pool_off[static_cast<size_t>(bb)] = total;
         segs.clear();
         if (own) segs.push_back(bb);
@@ -941,7 +958,7 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
             total += n;
         }
     }
-    pool_off[static_cast<size_t>(C)] = total;
+    pool_off[static_cast<size_t>(b1)] = total;
 
     // the members go up once per bucketing: a later pass over the same
     // buckets finds them in place (perhaps reordered within each bucket by
@@ -952,7 +969,7 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
         if (b.uploaded) GT_HIP(hipEventRecord(b.uploaded, c.s));
         c.c->members_gen = b.gen;
     }
-    const bool sub_ordered = own && !seed_d && sub_order_enabled();
+    const bool sub_ordered = own && !seed_d && !compact && sub_order_enabled();
     if (sub_ordered) sub_order_members(c, X, b, metric, d_members);
     CopyTaskH* d_tasks = c.ws<CopyTaskH>(W_TASKS, tasks.size());
     c.h2d(d_tasks, tasks.data(), tasks.size() * sizeof(CopyTaskH));
@@ -962,7 +979,7 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
     std::vector<std::vector<WorkItem>> groups(static_cast<size_t>(C));
     int64_t mp = 0, mb = 0;
     double pr = 0.0;
-    for (int64_t bb = 0; bb < C; ++bb) {
+    for (int64_t bb = b0; bb < b1; ++bb) {
         const int64_t q0 = b.offsets[static_cast<size_t>(bb)], nqb = b.offsets[static_cast<size_t>(bb + 1)] - q0;
         const int64_t p0 = pool_off[static_cast<size_t>(bb)], npb = pool_off[static_cast<size_t>(bb + 1)] - p0;
         mp = std::max(mp, npb);
@@ -982,7 +999,7 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
             if (sub_ordered && nqb >= 2 * kSubSize && npb >= kSubSize) rot = (t - kSubSize + npb) % npb;   // >= 0
             GT_REQUIRE(rot >= 0 && (npb == 0 || rot < npb), "pool rotation out of range");
             it.p_rot = static_cast<int32_t>(rot);
-            it.out_base = -1;
+            it.out_base = compact ? q0 - qbase + t : -1;
             groups[static_cast<size_t>(bb)].push_back(it);
         }
     }
@@ -1010,8 +1027,8 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
     // is the query of exactly one work item, so rows = N)
     const bool collect = knn_collect_supported(a);
     if (collect) {
-        a.cand = c.ws<uint64_t>(W_CAND, static_cast<size_t>(N) * kCollectCap);
-        a.cand_cnt = c.ws<int32_t>(W_CANDCNT, static_cast<size_t>(N));
+        a.cand = c.ws<uint64_t>(W_CAND, static_cast<size_t>(rows) * kCollectCap);
+        a.cand_cnt = c.ws<int32_t>(W_CANDCNT, static_cast<size_t>(rows));
         const char* se = std::getenv("GTANN_KNN_STATS");
         if (tr.on && se && se[0] == '1') {   // counters of the collect launch (slow), printed below
             a.stats = c.ws<unsigned long long>(W_STATS, 4);
@@ -1019,7 +1036,7 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
         }
     }
     const double t = c.timed([&] {
-        if (collect) launch_knn_collect_select(a, N, c.s);
+        if (collect) launch_knn_collect_select(a, rows, c.s);
         else launch_knn_fused(a, c.s);
     });
     ++c.c->knn_launches;
@@ -1436,6 +1453,388 @@ static void reverse_insert_device(Ctx& c, int32_t* ids, float* d, int64_t N, int
     if (h) throw Error(GT_EINVAL, "reverse-edge insertion: table holds an id >= N");
 }
 
+// ---------------------------------------------------------------- out-of-core stages
+// The N x M table and the N x K graphs stay in host memory; one chunk at a
+// time goes through a device budget (bytes of device memory for the chunk's
+// buffers; the dataset, when a stage needs it, is not counted).  Every stage
+// gives the same rows as its resident counterpart.
+
+// src/optimize.cu:89-134 on a host table (the rule of sanitize_kernel), rows
+// in parallel.
+static void sanitize_host(const int32_t* in, int64_t N, int M, uint32_t* out)
+{
+    parallel_slices(N, host_threads(), [&](int, int64_t lo, int64_t hi) {
+        for (int64_t i = lo; i < hi; ++i) {
+            const int32_t* r = in + i * M;
+            uint32_t* o = out + i * M;
+            int first = -1;
+            for (int k = 0; k < M && first < 0; ++k)
+                if (r[k] >= 0 && r[k] < N && r[k] != i) first = k;
+            const uint32_t fb = first < 0 ? static_cast<uint32_t>((i + 1) % N) : static_cast<uint32_t>(r[first]);
+            for (int k = 0; k < M; ++k)
+                o[k] = (r[k] < 0 || r[k] >= N || r[k] == i) ? fb : static_cast<uint32_t>(r[k]);
+        }
+    });
+}
+
+struct OocReport {
+    int64_t chunks = 0;         // device chunks of the stage
+    double rows_moved = 0.0;    // table rows sent to the device
+};
+
+// Exact CAGRA prune (cagra_prune_kernel) of a sanitized host table san
+// (N x M) into host rows out (N x K).  Rows go in chunks; a chunk's device
+// table holds its own rows and every row they point to (the union, gathered
+// on the host), read through an id -> compact-row map (ROWS 1), so each row
+// counts its detours exactly as in the resident prune.
+static void prune_chunked(Ctx& c, const uint32_t* san, int64_t N, int M, int K, size_t budget, uint32_t* out,
+                          OocReport* rep)
+{
+    GT_REQUIRE(K >= 1 && K <= M && M <= 128, "bad degrees");
+    const size_t fixed = static_cast<size_t>(N) * sizeof(int32_t);   // the id map
+    // per chunk row, at worst: its own row and M neighbour rows, list entries, the output row
+    const size_t per_row = static_cast<size_t>(M + 1) * (static_cast<size_t>(M) * 4 + 4) + static_cast<size_t>(K) * 4;
+    GT_REQUIRE(budget > fixed + 64 * per_row, "device budget too small for the chunked prune (need > " +
+                                                  std::to_string((fixed + 64 * per_row) >> 20) + " MiB)");
+    const int64_t chunk = std::min<int64_t>(N, static_cast<int64_t>((budget - fixed) / per_row));
+    int32_t* cidx = c.ws<int32_t>(W_OOC_A, static_cast<size_t>(N));
+    const size_t umax = static_cast<size_t>(chunk) * (M + 1);
+    uint32_t* Gc = c.ws<uint32_t>(W_OOC_B, umax * M);
+    int32_t* ulist = c.ws<int32_t>(W_OOC_C, umax);
+    uint32_t* dout = c.ws<uint32_t>(W_OOC_D, static_cast<size_t>(chunk) * K);
+    unsigned long long* bad = c.ws<unsigned long long>(W_FLAG, 1);
+    int* err = c.ws<int>(W_TMP, 1);
+    launch_init_flags(bad, err, c.s);
+    HostBuf hrows, hlist, hout;
+    uint32_t* st_rows = hrows.as<uint32_t>(umax * M);
+    int32_t* st_list = hlist.as<int32_t>(umax);
+    uint32_t* st_out = hout.as<uint32_t>(static_cast<size_t>(chunk) * K);
+    std::vector<int32_t> mark(static_cast<size_t>(N), -1);
+    int32_t gen = 0;
+    for (int64_t a0 = 0; a0 < N; a0 += chunk, ++gen) {
+        const int64_t n = std::min(chunk, N - a0);
+        // the union: the chunk's rows, then the rows they point to
+        size_t nu = 0;
+        for (int64_t i = a0; i < a0 + n; ++i) {
+            mark[static_cast<size_t>(i)] = gen;
+            st_list[nu++] = static_cast<int32_t>(i);
+        }
+        for (int64_t i = a0; i < a0 + n; ++i)
+            for (int k = 0; k < M; ++k) {
+                const uint32_t d = san[i * M + k];
+                if (d < N && mark[d] != gen) {
+                    mark[d] = gen;
+                    st_list[nu++] = static_cast<int32_t>(d);
+                }
+            }
+        parallel_slices(static_cast<int64_t>(nu), host_threads(), [&](int, int64_t lo, int64_t hi) {
+            for (int64_t u = lo; u < hi; ++u)
+                std::memcpy(st_rows + u * M, san + static_cast<int64_t>(st_list[u]) * M, static_cast<size_t>(M) * 4);
+        });
+        c.h2d(Gc, st_rows, nu * M * sizeof(uint32_t));
+        c.h2d(ulist, st_list, nu * sizeof(int32_t));
+        launch_set_cidx(ulist, static_cast<int64_t>(nu), cidx, c.s);
+        PruneMap map{};
+        map.a0 = a0;
+        map.n = n;
+        map.cidx = cidx;
+        launch_cagra_prune_mapped(reinterpret_cast<const int32_t*>(Gc), N, M, K, dout, bad, map, 1, c.s);
+        c.d2h(st_out, dout, static_cast<size_t>(n) * K * sizeof(uint32_t));
+        c.sync();   // the staging buffers are refilled by the next chunk
+        std::memcpy(out + a0 * K, st_out, static_cast<size_t>(n) * K * sizeof(uint32_t));
+        if (rep) {
+            rep->chunks++;
+            rep->rows_moved += static_cast<double>(nu);
+        }
+    }
+    unsigned long long h = 0;
+    c.d2h(&h, bad, sizeof(h));
+    c.sync();
+    if (h != ~0ull)
+        throw Error(GT_EFEWCAND, "prune: row " + std::to_string(h) + " has fewer than output_degree valid candidates");
+}
+
+// Multi-chunk reverse merge (Method E, src/optimize_chunked.cu:1548-2057) of a
+// host forward graph fwd (N x K) into host rows out.  Phase 1 streams the
+// forward rows in batches through the device, which routes every edge to its
+// destination chunk as a (rank, row in chunk, source) record; the host keeps
+// each chunk's records.  Phase 2 takes one destination chunk at a time:
+// records and forward rows up, records grouped per row (CSR), rows merged by
+// rev_merge_kernel -- the same rows as gt_reverse_merge.
+static void reverse_merge_chunked(Ctx& c, const uint32_t* fwd, int64_t N, int K, size_t budget, uint32_t* out,
+                                  OocReport* rep)
+{
+    GT_REQUIRE(K >= 1 && K <= 64, "output degree must be in [1, 64]");
+    // phase 2 per destination row: forward and output rows, about K records
+    // (record, key, slot), row count and offset
+    const size_t per_row2 = static_cast<size_t>(K) * (8 + 20) + 12;
+    const size_t per_row1 = static_cast<size_t>(K) * (4 + 8);   // phase 1: a forward row and its records
+    GT_REQUIRE(budget >= 64 * std::max(per_row1, per_row2), "device budget too small for the chunked merge");
+    int64_t R = std::min<int64_t>(N, std::min<int64_t>(int64_t(1) << 26, static_cast<int64_t>(budget / per_row2)));
+    const int64_t nchunks = ceil_div(N, R);
+    GT_REQUIRE(nchunks <= 4096, "device budget too small for the chunked merge (more than 4096 chunks)");
+    const int64_t B = std::min<int64_t>(N, static_cast<int64_t>(budget / per_row1));
+    uint32_t* dfwd = c.ws<uint32_t>(W_OOC_A, static_cast<size_t>(B) * K);
+    unsigned long long* drec = c.ws<unsigned long long>(W_OOC_B, static_cast<size_t>(B) * K);
+    uint32_t* counts = c.ws<uint32_t>(W_OOC_C, static_cast<size_t>(2 * nchunks));
+    uint32_t* cursor = counts + nchunks;
+    int* err = c.ws<int>(W_TMP, 1);
+    unsigned long long* bad = c.ws<unsigned long long>(W_FLAG, 1);
+    launch_init_flags(bad, err, c.s);
+    std::vector<std::vector<uint64_t>> recs(static_cast<size_t>(nchunks));
+    std::vector<uint32_t> h_counts(static_cast<size_t>(nchunks)), h_off(static_cast<size_t>(nchunks));
+    HostBuf hrec;
+    uint64_t* st_rec = hrec.as<uint64_t>(static_cast<size_t>(B) * K);
+    for (int64_t s0 = 0; s0 < N; s0 += B) {
+        const int64_t nb = std::min(B, N - s0);
+        c.h2d(dfwd, fwd + s0 * K, static_cast<size_t>(nb) * K * sizeof(uint32_t));
+        GT_HIP(hipMemsetAsync(counts, 0, static_cast<size_t>(nchunks) * sizeof(uint32_t), c.s));
+        launch_route(dfwd, nb, K, N, R, static_cast<int>(nchunks), s0, counts, cursor, drec, err, false, c.s);
+        c.d2h(h_counts.data(), counts, h_counts.size() * sizeof(uint32_t));
+        c.sync();
+        uint32_t tot = 0;
+        for (int64_t q = 0; q < nchunks; ++q) {
+            h_off[static_cast<size_t>(q)] = tot;
+            tot += h_counts[static_cast<size_t>(q)];
+        }
+        c.h2d(cursor, h_off.data(), h_off.size() * sizeof(uint32_t));
+        launch_route(dfwd, nb, K, N, R, static_cast<int>(nchunks), s0, counts, cursor, drec, err, true, c.s);
+        c.d2h(st_rec, drec, static_cast<size_t>(tot) * sizeof(uint64_t));
+        c.sync();
+        for (int64_t q = 0; q < nchunks; ++q) {
+            std::vector<uint64_t>& v = recs[static_cast<size_t>(q)];
+            const uint64_t* src = st_rec + h_off[static_cast<size_t>(q)];
+            v.insert(v.end(), src, src + h_counts[static_cast<size_t>(q)]);
+        }
+    }
+    int h_err = 0;
+    c.d2h(&h_err, err, sizeof(int));
+    c.sync();
+    if (h_err) throw Error(GT_EINVAL, "reverse merge: forward graph holds an id >= N");
+    HostBuf hout;
+    uint32_t* st_out = hout.as<uint32_t>(static_cast<size_t>(R) * K);
+    for (int64_t q = 0; q < nchunks; ++q) {
+        const int64_t c0 = q * R, nr = std::min(R, N - c0);
+        const std::vector<uint64_t>& v = recs[static_cast<size_t>(q)];
+        const int64_t nrec = static_cast<int64_t>(v.size());
+        unsigned long long* d_rec = c.ws<unsigned long long>(W_OOC_B, static_cast<size_t>(std::max<int64_t>(nrec, 1)));
+        unsigned long long* d_key = c.ws<unsigned long long>(W_OOC_E, static_cast<size_t>(std::max<int64_t>(nrec, 1)));
+        uint32_t* d_slot = c.ws<uint32_t>(W_OOC_F, static_cast<size_t>(std::max<int64_t>(nrec, 1)));
+        uint32_t* d_deg = c.ws<uint32_t>(W_DEG, static_cast<size_t>(nr));
+        uint32_t* d_off = c.ws<uint32_t>(W_OFF, static_cast<size_t>(nr) + 1);
+        uint32_t* d_sums = c.ws<uint32_t>(W_SUMS, static_cast<size_t>(ceil_div(nr, 1024) + 1));
+        uint32_t* d_fwd = c.ws<uint32_t>(W_OOC_A, static_cast<size_t>(nr) * K);
+        uint32_t* d_out = c.ws<uint32_t>(W_OOC_G, static_cast<size_t>(nr) * K);
+        c.h2d(d_rec, v.data(), static_cast<size_t>(nrec) * sizeof(uint64_t));
+        c.h2d(d_fwd, fwd + c0 * K, static_cast<size_t>(nr) * K * sizeof(uint32_t));
+        GT_HIP(hipMemsetAsync(d_deg, 0, static_cast<size_t>(nr) * sizeof(uint32_t), c.s));
+        launch_rec_group(d_rec, nrec, d_deg, d_slot, nullptr, nullptr, false, c.s);
+        launch_exclusive_scan(d_deg, nr, d_off, d_sums, c.s);
+        launch_rec_group(d_rec, nrec, nullptr, d_slot, d_off, d_key, true, c.s);
+        launch_rev_merge(d_fwd, nr, K, d_off, d_key, d_out, c.s);
+        c.d2h(st_out, d_out, static_cast<size_t>(nr) * K * sizeof(uint32_t));
+        c.sync();
+        std::memcpy(out + c0 * K, st_out, static_cast<size_t>(nr) * K * sizeof(uint32_t));
+        if (rep) {
+            rep->chunks++;
+            rep->rows_moved += static_cast<double>(nr);
+        }
+    }
+}
+
+// prune_windowed_gpu::run_chunked (src/prune_windowed_gpu.cu:529-915) with
+// the candidates ranked as given (its --dists ranking of sorted rows):
+// bucket position q owns the ids [off[q], off[q + 1]); row a at position p
+// counts a detour through its neighbour d only when d's position is in p's
+// window (win[p * W ..], win_len[p] entries), otherwise d contributes
+// nothing (src/prune_windowed_core.hpp:177-232).  Positions go in chunks
+// whose window union -- every row of every bucket in the windows -- fits the
+// budget; a chunk's buckets sit in a compact device table (ROWS 2), so the
+// rows do not depend on the chunking.
+static void prune_windowed_chunked(Ctx& c, const int32_t* cand, int64_t N, int M, const uint32_t* off, int nb,
+                                   const int32_t* win, const int32_t* win_len, int W, int K, size_t budget,
+                                   uint32_t* out, OocReport* rep)
+{
+    GT_REQUIRE(K >= 1 && K <= M && M <= 128, "bad degrees");
+    GT_REQUIRE(nb >= 1 && off[0] == 0 && static_cast<int64_t>(off[nb]) == N, "bucket offsets must cover [0, N)");
+    for (int q = 0; q < nb; ++q) GT_REQUIRE(off[q] <= off[q + 1], "bucket offsets must be ascending");
+    for (int q = 0; q < nb; ++q) {
+        GT_REQUIRE(win_len[q] >= 0 && win_len[q] <= W, "window length out of range");
+        for (int i = 0; i < win_len[q]; ++i)
+            GT_REQUIRE(win[static_cast<int64_t>(q) * W + i] >= 0 && win[static_cast<int64_t>(q) * W + i] < nb,
+                       "window position out of range");
+    }
+    const size_t row_bytes = static_cast<size_t>(M) * 4;
+    const size_t fixed = static_cast<size_t>(nb) * (8 + 4 + 4) + static_cast<size_t>(nb) * W * 4;
+    GT_REQUIRE(budget > fixed, "device budget too small for the windowed prune");
+    const int64_t cap_rows = static_cast<int64_t>((budget - fixed) / (row_bytes + static_cast<size_t>(K) * 4));
+    uint32_t* d_off = c.ws<uint32_t>(W_OOC_C, static_cast<size_t>(nb) + 1);
+    int32_t* d_win = c.ws<int32_t>(W_OOC_D, static_cast<size_t>(nb) * W + 1);
+    int32_t* d_wl = c.ws<int32_t>(W_OOC_E, static_cast<size_t>(nb));
+    int64_t* d_cbase = c.ws<int64_t>(W_OOC_F, static_cast<size_t>(nb));
+    c.h2d(d_off, off, (static_cast<size_t>(nb) + 1) * sizeof(uint32_t));
+    c.h2d(d_win, win, static_cast<size_t>(nb) * W * sizeof(int32_t));
+    c.h2d(d_wl, win_len, static_cast<size_t>(nb) * sizeof(int32_t));
+    unsigned long long* bad = c.ws<unsigned long long>(W_FLAG, 1);
+    int* err = c.ws<int>(W_TMP, 1);
+    launch_init_flags(bad, err, c.s);
+    std::vector<int32_t> stamp(static_cast<size_t>(nb), -1);
+    std::vector<int64_t> cbase(static_cast<size_t>(nb));
+    std::vector<int32_t> U;
+    HostBuf hrows, hout;
+    int32_t chunk_id = 0;
+    for (int p0 = 0; p0 < nb; ++chunk_id) {
+        // the longest run of positions from p0 whose window union fits
+        // (always at least one position, which must fit by itself)
+        U.clear();
+        int64_t rows = 0;
+        int p1 = p0;
+        auto add = [&](int q) {
+            if (stamp[static_cast<size_t>(q)] == chunk_id) return;
+            stamp[static_cast<size_t>(q)] = chunk_id;
+            U.push_back(q);
+            rows += static_cast<int64_t>(off[q + 1] - off[q]);
+        };
+        while (p1 < nb) {
+            const size_t u0 = U.size();
+            const int64_t r0 = rows;
+            add(p1);
+            for (int i = 0; i < win_len[p1]; ++i) add(win[static_cast<int64_t>(p1) * W + i]);
+            if (p1 > p0 && rows > cap_rows) {   // undo: p1 starts the next chunk
+                for (size_t i = u0; i < U.size(); ++i) stamp[static_cast<size_t>(U[i])] = -1;
+                U.resize(u0);
+                rows = r0;
+                break;
+            }
+            ++p1;
+        }
+        GT_REQUIRE(rows <= cap_rows || p1 == p0 + 1,
+                   "device budget too small for the windowed prune (one window needs more)");
+        std::fill(cbase.begin(), cbase.end(), int64_t(-1));
+        int64_t at = 0;
+        for (int q : U) {
+            cbase[static_cast<size_t>(q)] = at;
+            at += static_cast<int64_t>(off[q + 1] - off[q]);
+        }
+        int32_t* st_rows = hrows.as<int32_t>(static_cast<size_t>(std::max<int64_t>(at, 1)) * M);
+        parallel_slices(static_cast<int64_t>(U.size()), host_threads(), [&](int, int64_t lo, int64_t hi) {
+            for (int64_t i = lo; i < hi; ++i) {
+                const int q = U[static_cast<size_t>(i)];
+                std::memcpy(st_rows + cbase[static_cast<size_t>(q)] * M, cand + static_cast<int64_t>(off[q]) * M,
+                            static_cast<size_t>(off[q + 1] - off[q]) * row_bytes);
+            }
+        });
+        int32_t* Gc = c.ws<int32_t>(W_OOC_B, static_cast<size_t>(std::max<int64_t>(at, 1)) * M);
+        const int64_t a0 = off[p0], n = static_cast<int64_t>(off[p1]) - a0;
+        uint32_t* dout = c.ws<uint32_t>(W_OOC_G, static_cast<size_t>(std::max<int64_t>(n, 1)) * K);
+        c.h2d(Gc, st_rows, static_cast<size_t>(at) * row_bytes);
+        c.h2d(d_cbase, cbase.data(), cbase.size() * sizeof(int64_t));
+        PruneMap map{};
+        map.a0 = a0;
+        map.n = n;
+        map.off = d_off;
+        map.win = d_win;
+        map.win_len = d_wl;
+        map.cbase = d_cbase;
+        map.n_buckets = nb;
+        map.W = W;
+        launch_cagra_prune_mapped(Gc, N, M, K, dout, bad, map, 2, c.s);
+        uint32_t* st_out = hout.as<uint32_t>(static_cast<size_t>(std::max<int64_t>(n, 1)) * K);
+        c.d2h(st_out, dout, static_cast<size_t>(n) * K * sizeof(uint32_t));
+        c.sync();   // staging and cbase are refilled by the next chunk
+        std::memcpy(out + a0 * K, st_out, static_cast<size_t>(n) * K * sizeof(uint32_t));
+        if (rep) {
+            rep->chunks++;
+            rep->rows_moved += static_cast<double>(at);
+        }
+        p0 = p1;
+    }
+    unsigned long long h = 0;
+    c.d2h(&h, bad, sizeof(h));
+    c.sync();
+    if (h != ~0ull)
+        throw Error(GT_EFEWCAND, "prune: row " + std::to_string(h) + " has fewer than output_degree valid candidates");
+}
+
+// One round of the out-of-core build (src/bucket.cu:5670-6369: the running
+// table in host memory, merged chunk by chunk): buckets in order, grouped
+// into chunks whose members fit the budget (a bucket is the smallest unit).
+// A chunk's members' running rows go up (round > 0), its buckets' lists are
+// computed into compact rows (seeded from the running rows) and merged with
+// them on the device, and the merged rows go back into the host table.  Every
+// row gets the lists and merges of the resident build, so the table is the
+// same.
+static void ooc_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M, int metric, int r, int32_t* h_ids,
+                      float* h_d, size_t budget, gt_build_stats& st, OocReport* rep)
+{
+    const int64_t C = static_cast<int64_t>(b.offsets.size()) - 1;
+    // per member row: running, new and merged lists, the collect launch's candidates
+    const size_t per_row = static_cast<size_t>(M) * 8 * 4 + static_cast<size_t>(kCollectCap) * 8 + 8;
+    const int64_t cap = std::max<int64_t>(kQueriesPerBlock, static_cast<int64_t>(budget / per_row));
+    HostBuf hi, hd;
+    for (int64_t b0 = 0; b0 < C;) {
+        int64_t b1 = b0, rows = 0;
+        while (b1 < C) {
+            const int64_t nb = b.offsets[static_cast<size_t>(b1 + 1)] - b.offsets[static_cast<size_t>(b1)];
+            if (b1 > b0 && rows + nb > cap) break;
+            rows += nb;
+            ++b1;
+        }
+        const int64_t q0 = b.offsets[static_cast<size_t>(b0)];
+        const size_t nm = static_cast<size_t>(std::max<int64_t>(rows, 1)) * M;
+        int32_t* rid = c.ws<int32_t>(W_G1, nm);
+        float* rdd = c.ws<float>(W_G2, nm);
+        int32_t* nid = c.ws<int32_t>(W_IDS, nm);
+        float* ndd = c.ws<float>(W_D, nm);
+        int32_t* mid = c.ws<int32_t>(W_IDS2, nm);
+        float* mdd = c.ws<float>(W_D2, nm);
+        int32_t* sti = hi.as<int32_t>(nm);
+        float* std_ = hd.as<float>(nm);
+        const int32_t* mem = b.members.data() + q0;
+        if (r > 0) {
+            parallel_slices(rows, host_threads(), [&](int, int64_t lo, int64_t hi_) {
+                for (int64_t q = lo; q < hi_; ++q) {
+                    std::memcpy(sti + q * M, h_ids + static_cast<int64_t>(mem[q]) * M, static_cast<size_t>(M) * 4);
+                    std::memcpy(std_ + q * M, h_d + static_cast<int64_t>(mem[q]) * M, static_cast<size_t>(M) * 4);
+                }
+            });
+            c.h2d(rid, sti, static_cast<size_t>(rows) * M * 4);
+            c.h2d(rdd, std_, static_cast<size_t>(rows) * M * 4);
+        }
+        int32_t* oi = mid;
+        float* od = mdd;
+        if (r == 0 && b.P > 0) {
+            // own buckets unseeded, then the probe buckets seeded with their M-th distance, merged
+            st.t_knn += bucketed_round(c, X, b, M, metric, nullptr, rid, rdd, &st.max_pool, &st.max_bucket,
+                                       &st.knn_pairs, true, false, b0, b1);
+            st.t_knn += bucketed_round(c, X, b, M, metric, rdd, nid, ndd, &st.max_pool, &st.max_bucket,
+                                       &st.knn_pairs, false, true, b0, b1);
+            st.t_merge += c.timed([&] { launch_merge_rounds(rid, rdd, nid, ndd, rows, M, mid, mdd, c.s); });
+        } else if (r == 0) {
+            st.t_knn += bucketed_round(c, X, b, M, metric, nullptr, mid, mdd, &st.max_pool, &st.max_bucket,
+                                       &st.knn_pairs, true, true, b0, b1);
+        } else {
+            st.t_knn += bucketed_round(c, X, b, M, metric, rdd, nid, ndd, &st.max_pool, &st.max_bucket,
+                                       &st.knn_pairs, true, true, b0, b1);
+            st.t_merge += c.timed([&] { launch_merge_rounds(rid, rdd, nid, ndd, rows, M, mid, mdd, c.s); });
+        }
+        c.d2h(sti, oi, static_cast<size_t>(rows) * M * 4);
+        c.d2h(std_, od, static_cast<size_t>(rows) * M * 4);
+        c.sync();
+        parallel_slices(rows, host_threads(), [&](int, int64_t lo, int64_t hi_) {
+            for (int64_t q = lo; q < hi_; ++q) {
+                std::memcpy(h_ids + static_cast<int64_t>(mem[q]) * M, sti + q * M, static_cast<size_t>(M) * 4);
+                std::memcpy(h_d + static_cast<int64_t>(mem[q]) * M, std_ + q * M, static_cast<size_t>(M) * 4);
+            }
+        });
+        if (rep) {
+            rep->chunks++;
+            rep->rows_moved += static_cast<double>(rows);
+        }
+        b0 = b1;
+    }
+}
+
 }  // namespace gtann
 
 using namespace gtann;
@@ -1657,6 +2056,38 @@ void gt_build_params_default(gt_build_params* p)
     p->seed = 42;
     p->reverse_edges = 0;
     p->int_exact = 1;
+    p->device_budget_mb = 0;
+}
+
+int gt_reverse_merge_chunked(gt_ctx* ctx, const uint32_t* fwd, int64_t N, int32_t K, int64_t device_budget_bytes,
+                             uint32_t* out)
+{
+    return guarded(ctx, [&] {
+        GT_REQUIRE(fwd && out && N >= 1 && K >= 1 && K <= 64, "bad arguments");
+        GT_REQUIRE(!is_device_ptr(fwd) && !is_device_ptr(out), "gt_reverse_merge_chunked takes host buffers");
+        Ctx c(ctx);
+        const size_t budget = device_budget_bytes > 0 ? static_cast<size_t>(device_budget_bytes)
+                                                      : static_cast<size_t>(N) * K * 64 + (size_t(64) << 20);
+        reverse_merge_chunked(c, fwd, N, K, budget, out, nullptr);
+    });
+}
+
+int gt_prune_windowed(gt_ctx* ctx, const int32_t* cand, int64_t N, int32_t M, const uint32_t* offsets,
+                      int32_t n_buckets, const int32_t* win, const int32_t* win_len, int32_t W, int32_t K,
+                      int64_t device_budget_bytes, uint32_t* out)
+{
+    return guarded(ctx, [&] {
+        GT_REQUIRE(cand && offsets && win && win_len && out && N >= 1 && M >= 1 && n_buckets >= 1 && W >= 1,
+                   "bad arguments");
+        GT_REQUIRE(N < (int64_t(1) << 31), "N must be < 2^31");
+        GT_REQUIRE(!is_device_ptr(cand) && !is_device_ptr(out), "gt_prune_windowed takes host buffers");
+        Ctx c(ctx);
+        const size_t budget = device_budget_bytes > 0
+                                  ? static_cast<size_t>(device_budget_bytes)
+                                  : static_cast<size_t>(N) * (M + K) * 4 + static_cast<size_t>(n_buckets) * (W + 8) * 4 +
+                                        (size_t(1) << 20);
+        prune_windowed_chunked(c, cand, N, M, offsets, n_buckets, win, win_len, W, K, budget, out, nullptr);
+    });
 }
 
 void gt_search_params_default(gt_search_params* p)
@@ -2453,12 +2884,25 @@ int gt_build_graph_ex(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtyp
         nprobe = static_cast<int>(std::min<int64_t>(nprobe, C - 1));
 
         const size_t nm = static_cast<size_t>(N) * p.M;
-        int32_t* run_i = c.ws<int32_t>(W_G1, nm);
-        float* run_d = c.ws<float>(W_G2, nm);
-        int32_t* cur_i = c.ws<int32_t>(W_IDS, nm);
-        float* cur_d = c.ws<float>(W_D, nm);
-        int32_t* tmp_i = c.ws<int32_t>(W_IDS2, nm);
-        float* tmp_d = c.ws<float>(W_D2, nm);
+        // out of core when a device budget is set and the resident tables
+        // (three N x M tables of ids and distances, the collect candidates,
+        // the sanitized table and two graphs) exceed it
+        const size_t budget = static_cast<size_t>(std::max(p.device_budget_mb, 0)) << 20;
+        const size_t resident = nm * 4 * 7 + static_cast<size_t>(N) * kCollectCap * 8 +
+                                (graph ? static_cast<size_t>(N) * p.K * 8 : 0);
+        const bool ooc = budget > 0 && resident > budget;
+        GT_REQUIRE(!ooc || (p.refine_passes == 0 && !p.reverse_edges),
+                   "the out-of-core build (device budget below the tables) supports neither refinement nor "
+                   "per-round reverse-edge insertion");
+        std::vector<int32_t> h_run_i(ooc ? nm : 0);
+        std::vector<float> h_run_d(ooc ? nm : 0);
+        OocReport rep;
+        int32_t* run_i = ooc ? nullptr : c.ws<int32_t>(W_G1, nm);
+        float* run_d = ooc ? nullptr : c.ws<float>(W_G2, nm);
+        int32_t* cur_i = ooc ? nullptr : c.ws<int32_t>(W_IDS, nm);
+        float* cur_d = ooc ? nullptr : c.ws<float>(W_D, nm);
+        int32_t* tmp_i = ooc ? nullptr : c.ws<int32_t>(W_IDS2, nm);
+        float* tmp_d = ooc ? nullptr : c.ws<float>(W_D2, nm);
         ctx->knn_launches = 0;
         // Round r's bucketing = bucket_device (device work + downloads, on
         // this thread) then bucket_host (two-choice + CSR, on a worker
@@ -2514,6 +2958,10 @@ int gt_build_graph_ex(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtyp
             }
             if (r + 1 < p.rounds) start_host(r + 1);
             const Buckets& b = bk[r & 1];
+            if (ooc) {
+                ooc_round(c, Xm, b, p.M, p.metric, r, h_run_i.data(), h_run_d.data(), budget, st, &rep);
+                continue;
+            }
             if (p.reverse_edges) {
                 // the Python pipeline's round: full table, reverse edges, then the merge
                 int32_t* oi = r == 0 ? run_i : cur_i;
@@ -2549,6 +2997,41 @@ int gt_build_graph_ex(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtyp
             }
         }
         for (int i = 0; i < 2; ++i) bk[i].members.swap(ctx->h_members[i]);
+        if (ooc) {
+            st.knn_flops = 2.0 * D * st.knn_pairs;
+            st.knn_launches = ctx->knn_launches;
+            st.knn_int8 = use_i8(Xm, Xm, p.metric) ? 1 : 0;
+            if (graph) {
+                Timer t1;
+                std::vector<uint32_t> san(nm), fwd(static_cast<size_t>(N) * p.K);
+                sanitize_host(h_run_i.data(), N, p.M, san.data());
+                prune_chunked(c, san.data(), N, p.M, p.K, budget, fwd.data(), &rep);
+                st.t_prune = t1.sec();
+                Timer t2;
+                std::vector<uint32_t> fin(static_cast<size_t>(N) * p.K);
+                reverse_merge_chunked(c, fwd.data(), N, p.K, budget, fin.data(), &rep);
+                st.t_revmerge = t2.sec();
+                if (is_device_ptr(graph)) c.h2d(graph, fin.data(), fin.size() * sizeof(uint32_t));
+                else std::memcpy(graph, fin.data(), fin.size() * sizeof(uint32_t));
+            }
+            Timer td;
+            if (p.metric == GT_METRIC_IP)
+                for (float& v : h_run_d) v = -v;
+            if (knn_ids) {
+                if (is_device_ptr(knn_ids)) c.h2d(knn_ids, h_run_i.data(), nm * sizeof(int32_t));
+                else std::memcpy(knn_ids, h_run_i.data(), nm * sizeof(int32_t));
+            }
+            if (knn_dists) {
+                if (is_device_ptr(knn_dists)) c.h2d(knn_dists, h_run_d.data(), nm * sizeof(float));
+                else std::memcpy(knn_dists, h_run_d.data(), nm * sizeof(float));
+            }
+            c.sync();
+            st.t_download = td.sec();
+            st.ooc_chunks = rep.chunks;
+            st.t_total = total.sec();
+            if (stats) *stats = st;
+            return;
+        }
         if (p.refine_passes > 0) {
             GT_REQUIRE(p.refine_sample >= 1 && p.refine_sample <= p.M && p.refine_sample * p.refine_sample <= 1024,
                        "bad refine sample");

@@ -63,7 +63,7 @@ struct KnnArgs {
     int32_t metric;         // 0 = L2, 1 = inner product (key = -<x,y>)
     int32_t exclude_self;   // drop pool entries whose row id equals the query row id
     int32_t out_pos;        // write pool-list positions instead of row ids
-    const float* seed_d;    // optional per-query cap on kept keys: seed_d[qid * seed_ld + seed_ld - 1]
+    const float* seed_d;    // optional per-query cap on kept keys: seed_d[orow * seed_ld + seed_ld - 1], orow = output row
     int32_t seed_ld;
     int32_t* out_ids;       // (rows, M)
     float* out_d;           // (rows, M)
@@ -110,6 +110,18 @@ struct SearchArgs {
 };
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Where the rows of a chunked prune live (cagra_prune_kernel, ROWS 1 and 2).
+struct PruneMap {
+    int64_t a0, n;            // rows pruned: a0 .. a0 + n - 1, output rows 0 .. n - 1
+    const int32_t* cidx;      // ROWS 1: compact row of every id the chunk reads
+    const uint32_t* off;      // ROWS 2: n_buckets + 1 row starts, by processing position
+    const int32_t* win;       // ROWS 2: (n_buckets, W) window positions
+    const int32_t* win_len;   // ROWS 2: (n_buckets)
+    const int64_t* cbase;     // ROWS 2: compact row of off[q], -1 = position q not loaded
+    int32_t n_buckets;
+    int32_t W;
+};
 
 // Launch plan of the two-kernel reverse merge (revmerge_kernels.hip).
 struct RvPlan {

@@ -4,7 +4,7 @@
 //   gtann bucket2 -i BASE -o OUT [--centroid-ratio R] [--seed S] [--knn-k K]
 //         [--nprobe P] [--neighbors-m M] [-t T] [--fused-optimize-degree K]
 //         [--order-window W] [--skip-dists] [--skip-npy] [--kmeans-iters I]
-//         [--balance F] [--refine-passes P] [--refine-sample S]
+//         [--balance F] [--refine-passes P] [--refine-sample S] [--gpu-limit BYTES]
 //       the GPU-resident build (src/bucket.cu:9900-9990 options) with the
 //       inline reorder of round 1 (src/bucket.cu:9160-9460): new ids are
 //       bucket-contiguous, buckets in the DiskJoin order of the round-1
@@ -13,15 +13,24 @@
 //       bucket_offsets.bin, bucket_process_order.bin, centroid_knn.bin,
 //       centroid_pool.bin (with --nprobe), vector_knn.bin, vector_dists.bin
 //       and neighbors.npy in new ids, and with --fused-optimize-degree K > 0
-//       final_graph.bin in the input's ids.
+//       final_graph.bin in the input's ids.  --gpu-limit below the tables:
+//       the out-of-core build (running table in host memory, chunked), same
+//       files.
 //   gtann optimize -i DATA -g KNN -o OUT --output-degree K [--skip-sort]
 //       sanitize + CAGRA prune + reverse merge (src/optimize.cu); exit 2 when
 //       the device cannot hold the tables (the reference's "use the other
 //       path" code, src/optimize.cu:300-308).
 //   gtann prune_windowed -k KNN -i DATA -o FWD --output-degree K
-//       sanitize + CAGRA prune with the whole table resident (src/prune_windowed.cpp).
-//   gtann optimize_chunked -g FWD -o OUT [-m E] [--inverse-perm P --final-output F]
-//       reverse-edge merge (Method E), optionally translated to original ids.
+//         [--bucket-offsets F --bucket-process-order F -c CENTROID_KNN] [--pool-graph F]
+//         [--cache-mb MB]
+//       the windowed CAGRA prune (src/prune_windowed.cpp): each bucket's rows
+//       see only the rows of the buckets in its window, positions chunked
+//       within --cache-mb of device memory; without the bucket files,
+//       sanitize + the full prune.
+//   gtann optimize_chunked -g FWD -o OUT [-m E] [--gpu-budget-mb MB]
+//         [--inverse-perm P --final-output F]
+//       reverse-edge merge (Method E), in destination chunks when the graph
+//       exceeds --gpu-budget-mb, optionally translated to original ids.
 //   gtann translate_ids -g G -p P -o OUT
 //       out[inv[i]][k] = inv[g[i][k]] (src/translate_ids.cpp).
 //   gtann knn -i DATA -o OUTDIR -k K
@@ -36,8 +45,9 @@
 //       set-wise comparison of two indices (bd/search.cpp compare, with the
 //       per-node CSV of bd/search.py:238-262).
 //
-// Options of the reference that tune its host/out-of-core memory use are
-// accepted and ignored (the tables are resident in HBM).  Errors print
+// The reference's device budgets (--gpu-limit, --cache-mb, --gpu-budget-mb)
+// select the out-of-core stages; its other options that tune host memory,
+// disk buffers or its own caches are accepted and ignored.  Errors print
 // "FATAL: <message>" and exit 1.
 #include "gtann.h"
 #include "gtann_io.hpp"
@@ -183,9 +193,10 @@ int cmd_bucket2(int argc, char** argv)
 {
     Args a(argc, argv,
            {"input,i", "output,o", "centroid-ratio", "seed", "knn-k", "nprobe", "neighbors-m", "iterations,t",
-            "fused-optimize-degree", "kmeans-iters", "balance", "refine-passes", "refine-sample", "order-window"},
+            "fused-optimize-degree", "kmeans-iters", "balance", "refine-passes", "refine-sample", "order-window",
+            "gpu-limit"},
            {"skip-dists", "skip-npy", "out-of-core"},
-           {"cpu-limit", "gpu-limit", "bucket-vec-buffer", "sample-rate", "use-pq", "kmeans-train-fraction", "bucket-mem-mb",
+           {"cpu-limit", "bucket-vec-buffer", "sample-rate", "use-pq", "kmeans-train-fraction", "bucket-mem-mb",
             "gpu-bucket-cache-mb", "pq-bits-start", "pq-bits-min", "search-iters", "cache-mb"});
     const std::string in = a.str("input"), root = a.str("output");
     const int knn_k = static_cast<int>(a.num("knn-k", 32));
@@ -215,6 +226,10 @@ int cmd_bucket2(int argc, char** argv)
     p.balance = static_cast<float>(a.real("balance", p.balance));
     p.refine_passes = static_cast<int32_t>(a.num("refine-passes", 0));
     p.refine_sample = static_cast<int32_t>(a.num("refine-sample", p.refine_sample));
+    // --gpu-limit (bytes, 0 = auto): a device budget below the tables runs
+    // the build out of core (the running table in host memory, chunked)
+    if (a.has("gpu-limit") && a.num("gpu-limit", 0) > 0)
+        p.device_budget_mb = static_cast<int32_t>(std::max<int64_t>(1, a.num("gpu-limit", 0) >> 20));
     const int64_t C = std::min<int64_t>(p.n_buckets, ds.N);
     // round-1 centroid self-kNN: knn-k columns for the processing order
     // (centroid_knn.bin), nprobe columns for centroid_pool.bin when given
@@ -317,30 +332,87 @@ int cmd_optimize(int argc, char** argv)
     return 0;
 }
 
+// src/prune_windowed.cpp: the windowed prune of a bucket2 output directory
+// (reordered candidates, bucket_offsets.bin, bucket_process_order.bin,
+// centroid_knn.bin or --pool-graph).  The window of processing position p is
+// p itself plus the positions of its bucket's centroid-kNN (or pool)
+// neighbours, sorted and distinct (src/prune_windowed.cpp:370-385, the
+// neighbours as adjacency_from_flat_graph keeps them); --cache-mb is the
+// device budget of the chunked prune.  Candidates are ranked as stored (the
+// --dists ranking of rows bucket2 wrote sorted).  Without the bucket files
+// the whole table is one window: sanitize + full prune, as optimize does.
 int cmd_prune_windowed(int argc, char** argv)
 {
-    Args a(argc, argv, {"vector-knn-reordered,k", "dataset,i", "output,o", "output-degree"}, {"save-npy"},
-           {"bucket-offsets", "bucket-process-order", "centroid-knn,c", "order-window", "cache-mb", "pool-graph",
-            "dists"});
+    Args a(argc, argv,
+           {"vector-knn-reordered,k", "dataset,i", "output,o", "output-degree", "bucket-offsets",
+            "bucket-process-order", "centroid-knn,c", "cache-mb", "pool-graph"},
+           {"save-npy"}, {"order-window", "dists"});
     const int K = static_cast<int>(a.num("output-degree", 32));
     Table<int32_t> knn = read_table<int32_t>(a.str("vector-knn-reordered"));
+    if (K > knn.W) throw Exit{1, "--output-degree (" + std::to_string(K) + ") > input degree (" +
+                                     std::to_string(knn.W) + ")"};
     Lib L;
-    std::vector<uint32_t> s = sanitized(L, knn);
     std::vector<uint32_t> out(static_cast<size_t>(knn.N) * K);
-    L.check(gt_cagra_prune(L.ctx, s.data(), knn.N, knn.W, K, out.data()), "gt_cagra_prune");
+    if (a.has("bucket-offsets") && a.has("bucket-process-order") && a.has("centroid-knn")) {
+        const std::vector<uint32_t> off = read_bucket_offsets(a.str("bucket-offsets"));
+        const int32_t nb = static_cast<int32_t>(off.size()) - 1;
+        if (nb < 1 || static_cast<int64_t>(off.back()) != knn.N)
+            throw Exit{1, "bucket_offsets does not cover the candidate rows"};
+        const std::vector<int32_t> order = read_bucket_process_order(a.str("bucket-process-order"));
+        if (static_cast<int32_t>(order.size()) != nb)
+            throw Exit{1, "bucket_process_order size (" + std::to_string(order.size()) + ") != n_buckets (" +
+                              std::to_string(nb) + ")"};
+        std::vector<int32_t> pos_of(static_cast<size_t>(nb), -1);
+        for (int32_t p = 0; p < nb; ++p) {
+            if (order[static_cast<size_t>(p)] < 0 || order[static_cast<size_t>(p)] >= nb)
+                throw Exit{1, "bucket_process_order holds an id out of range"};
+            pos_of[static_cast<size_t>(order[static_cast<size_t>(p)])] = p;
+        }
+        const Table<uint32_t> g = read_table<uint32_t>(a.has("pool-graph") ? a.str("pool-graph") : a.str("centroid-knn"));
+        if (g.N != nb) throw Exit{1, "window graph rows (" + std::to_string(g.N) + ") != n_buckets"};
+        const int32_t W = g.W + 1;
+        std::vector<int32_t> win(static_cast<size_t>(nb) * W, 0), wl(static_cast<size_t>(nb), 0);
+        for (int32_t p = 0; p < nb; ++p) {
+            const int32_t bkt = order[static_cast<size_t>(p)];
+            std::vector<int32_t> w{p};
+            for (int32_t k = 0; k < g.W; ++k) {
+                const uint32_t nbk = g.v[static_cast<size_t>(bkt) * g.W + k];
+                if (static_cast<int64_t>(nbk) != bkt && static_cast<int64_t>(nbk) < nb)
+                    w.push_back(pos_of[nbk]);
+            }
+            std::sort(w.begin(), w.end());
+            w.erase(std::unique(w.begin(), w.end()), w.end());
+            std::copy(w.begin(), w.end(), win.begin() + static_cast<int64_t>(p) * W);
+            wl[static_cast<size_t>(p)] = static_cast<int32_t>(w.size());
+        }
+        const int64_t budget = static_cast<int64_t>(a.num("cache-mb", 4000)) << 20;
+        L.check(gt_prune_windowed(L.ctx, knn.v.data(), knn.N, knn.W, off.data(), nb, win.data(), wl.data(), W, K,
+                                  budget, out.data()),
+                "gt_prune_windowed");
+    } else {
+        std::vector<uint32_t> s = sanitized(L, knn);
+        L.check(gt_cagra_prune(L.ctx, s.data(), knn.N, knn.W, K, out.data()), "gt_cagra_prune");
+    }
     write_table<uint32_t>(a.str("output"), out.data(), knn.N, K);
     return 0;
 }
 
 int cmd_optimize_chunked(int argc, char** argv)
 {
-    Args a(argc, argv, {"forward-graph,g", "output,o", "method,m", "inverse-perm", "final-output"}, {"save-npy"},
-           {"gpu-budget-mb", "host-budget-mb", "edge-buffer-mb", "tmp-dir", "bucket-offsets", "rev-degree-cap"});
+    Args a(argc, argv, {"forward-graph,g", "output,o", "method,m", "inverse-perm", "final-output", "gpu-budget-mb"},
+           {"save-npy"}, {"host-budget-mb", "edge-buffer-mb", "tmp-dir", "bucket-offsets", "rev-degree-cap"});
     if (a.has("method") && a.str("method") != "E") throw Exit{1, "only method E is provided"};
     Table<uint32_t> fwd = read_table<uint32_t>(a.str("forward-graph"));
     Lib L;
     std::vector<uint32_t> out(fwd.v.size());
-    L.check(gt_reverse_merge(L.ctx, fwd.v.data(), fwd.N, fwd.W, out.data()), "gt_reverse_merge");
+    // the resident merge when its edge keys and rows fit --gpu-budget-mb, else
+    // destination chunks (src/optimize_chunked.cu:1548-2057)
+    const int64_t budget = static_cast<int64_t>(a.num("gpu-budget-mb", 8000)) << 20;
+    if (static_cast<int64_t>(fwd.v.size()) * 32 <= budget)
+        L.check(gt_reverse_merge(L.ctx, fwd.v.data(), fwd.N, fwd.W, out.data()), "gt_reverse_merge");
+    else
+        L.check(gt_reverse_merge_chunked(L.ctx, fwd.v.data(), fwd.N, fwd.W, budget, out.data()),
+                "gt_reverse_merge_chunked");
     write_table<uint32_t>(a.str("output"), out.data(), fwd.N, fwd.W);
     if (a.has("inverse-perm") && a.has("final-output")) {
         std::vector<uint32_t> inv = read_inverse_perm(a.str("inverse-perm"));

@@ -266,7 +266,9 @@ knn_i8_collect_kernel(KnnArgs a)
 
     CollectState st;
     float seed = FLT_MAX;
-    if (qvalid && a.seed_d) seed = fminf(a.seed_d[static_cast<int64_t>(qrow) * a.seed_ld + a.seed_ld - 1], FLT_MAX);
+    // the seed is read from the output row (the query row unless the item has an out_base)
+    const int64_t orow_seed = it.out_base >= 0 ? it.out_base + qlocal : static_cast<int64_t>(qrow);
+    if (qvalid && a.seed_d) seed = fminf(a.seed_d[orow_seed * a.seed_ld + a.seed_ld - 1], FLT_MAX);
     st.thr = qvalid ? seed : -INFINITY;
     st.thr_id = 0xffffffffu;
     st.cnt = 0;

@@ -463,7 +463,9 @@ __global__ void __launch_bounds__(256, 2) knn_fused_kernel(KnnArgs a)
 
     QueryState st;
     st.seed = FLT_MAX;
-    if (qvalid && a.seed_d) st.seed = fminf(a.seed_d[static_cast<int64_t>(qrow) * a.seed_ld + a.seed_ld - 1], FLT_MAX);
+    // the seed is read from the output row (the query row unless the item has an out_base)
+    const int64_t orow_seed = it.out_base >= 0 ? it.out_base + qlocal : static_cast<int64_t>(qrow);
+    if (qvalid && a.seed_d) st.seed = fminf(a.seed_d[orow_seed * a.seed_ld + a.seed_ld - 1], FLT_MAX);
     st.thr = qvalid ? st.seed : -INFINITY;
     st.cnt = 0;
     st.nL = 0;
@@ -734,7 +736,9 @@ knn_i8_kernel(KnnArgs a)
 
     QueryState st;
     st.seed = FLT_MAX;
-    if (qvalid && a.seed_d) st.seed = fminf(a.seed_d[static_cast<int64_t>(qrow) * a.seed_ld + a.seed_ld - 1], FLT_MAX);
+    // the seed is read from the output row (the query row unless the item has an out_base)
+    const int64_t orow_seed = it.out_base >= 0 ? it.out_base + qlocal : static_cast<int64_t>(qrow);
+    if (qvalid && a.seed_d) st.seed = fminf(a.seed_d[orow_seed * a.seed_ld + a.seed_ld - 1], FLT_MAX);
     st.thr = qvalid ? st.seed : -INFINITY;
     st.cnt = 0;
     st.nL = 0;
@@ -939,7 +943,9 @@ __global__ void __launch_bounds__(256, 2) knn_wide_kernel(KnnArgs a)
 
     QueryState st;
     st.seed = FLT_MAX;
-    if (qvalid && a.seed_d) st.seed = fminf(a.seed_d[static_cast<int64_t>(qrow) * a.seed_ld + a.seed_ld - 1], FLT_MAX);
+    // the seed is read from the output row (the query row unless the item has an out_base)
+    const int64_t orow_seed = it.out_base >= 0 ? it.out_base + qlocal : static_cast<int64_t>(qrow);
+    if (qvalid && a.seed_d) st.seed = fminf(a.seed_d[orow_seed * a.seed_ld + a.seed_ld - 1], FLT_MAX);
     st.thr = qvalid ? st.seed : -INFINITY;
     st.cnt = 0;
     st.nL = 0;

@@ -27,6 +27,7 @@ EXPORTS = (
     "gt_reverse_merge", "gt_optimize", "gt_translate", "gt_build_params_default", "gt_build_graph",
     "gt_prune_occlusion", "gt_reverse_insert", "gt_search_params_default", "gt_search", "gt_build_graph_ex",
     "gt_bucket_order", "gt_bucket_reorder", "gt_permute_rows", "gt_remap_table", "gt_optimize_noalloc",
+    "gt_reverse_merge_chunked", "gt_prune_windowed",
 )
 
 
@@ -41,7 +42,7 @@ class BuildParams(C.Structure):
         ("metric", C.c_int32), ("n_buckets", C.c_int32), ("nprobe", C.c_int32), ("M", C.c_int32),
         ("K", C.c_int32), ("rounds", C.c_int32), ("refine_passes", C.c_int32), ("refine_sample", C.c_int32),
         ("kmeans_iters", C.c_int32), ("balance", C.c_float), ("seed", C.c_uint64),
-        ("reverse_edges", C.c_int32), ("int_exact", C.c_int32),
+        ("reverse_edges", C.c_int32), ("int_exact", C.c_int32), ("device_budget_mb", C.c_int32),
     ]
 
 
@@ -51,6 +52,7 @@ class BuildStats(C.Structure):
         ("t_merge", C.c_double), ("t_refine", C.c_double), ("t_prune", C.c_double), ("t_revmerge", C.c_double),
         ("t_download", C.c_double), ("knn_flops", C.c_double), ("knn_pairs", C.c_double),
         ("max_pool", C.c_int64), ("max_bucket", C.c_int64), ("knn_launches", C.c_int64), ("knn_int8", C.c_int64),
+        ("ooc_chunks", C.c_int64),
     ]
 
     def as_dict(self):
@@ -123,6 +125,8 @@ def lib():
         L.gt_sanitize.argtypes = [vp, vp, i64, i32, vp]
         L.gt_cagra_prune.argtypes = [vp, vp, i64, i32, i32, vp]
         L.gt_reverse_merge.argtypes = [vp, vp, i64, i32, vp]
+        L.gt_reverse_merge_chunked.argtypes = [vp, vp, i64, i32, i64, vp]
+        L.gt_prune_windowed.argtypes = [vp, vp, i64, i32, vp, i32, vp, vp, i32, i32, i64, vp]
         L.gt_optimize.argtypes = [vp, vp, i64, i32, i32, vp]
         L.gt_optimize_noalloc.argtypes = [vp, vp, i64, i32, i32, vp]
         L.gt_translate.argtypes = [vp, vp, vp, i64, i32, vp]
@@ -355,6 +359,35 @@ class Context:
         self._check(lib().gt_reverse_merge(self._h, _ptr(fwd), N, K, _ptr(out)), "gt_reverse_merge")
         return out
 
+    def reverse_merge_chunked(self, fwd, device_budget_bytes=0):
+        """Out-of-core reverse merge (optimize_chunked -m E with several
+        chunks): the same rows as reverse_merge, within a device budget."""
+        fwd = _np(fwd, np.uint32)
+        N, K = fwd.shape
+        out = np.empty((N, K), np.uint32)
+        self._check(lib().gt_reverse_merge_chunked(self._h, _ptr(fwd), N, K, int(device_budget_bytes), _ptr(out)),
+                    "gt_reverse_merge_chunked")
+        return out
+
+    def prune_windowed(self, cand, offsets, win, win_len, K, device_budget_bytes=0):
+        """Windowed CAGRA prune (prune_windowed_gpu::run_chunked, candidates in
+        rank order) of int32 cand (N, M) in the bucket-contiguous id space:
+        offsets (n_buckets + 1) by processing position, win (n_buckets, W)
+        window positions, win_len (n_buckets)."""
+        cand = _np(cand, np.int32)
+        N, M = cand.shape
+        off = _np(offsets, np.uint32)
+        win = _np(win, np.int32)
+        wl = _np(win_len, np.int32)
+        nb = off.shape[0] - 1
+        if win.ndim != 2 or win.shape[0] != nb or wl.shape != (nb,):
+            raise ValueError("win must be (n_buckets, W) and win_len (n_buckets,)")
+        out = np.empty((N, K), np.uint32)
+        self._check(lib().gt_prune_windowed(self._h, _ptr(cand), N, M, _ptr(off), nb, _ptr(win), _ptr(wl),
+                                            win.shape[1], K, int(device_budget_bytes), _ptr(out)),
+                    "gt_prune_windowed")
+        return out
+
     def optimize(self, knn, K):
         knn = _as_u32(knn)
         N, M = knn.shape
@@ -406,7 +439,7 @@ class Context:
 
     def build_graph(self, X, *, n_buckets=0, nprobe=1, M=64, K=32, rounds=2, refine_passes=0, refine_sample=16,
                     kmeans_iters=3, balance=0.8, seed=42, metric="l2", return_knn=True, reverse_edges=False,
-                    prune=True, centroid_knn_k=0, round1_bucket=False, int_exact=True):
+                    prune=True, centroid_knn_k=0, round1_bucket=False, int_exact=True, device_budget_mb=0):
         if not _is_torch(X):
             X = np.ascontiguousarray(X)
         N, D = X.shape
@@ -416,6 +449,7 @@ class Context:
         p.rounds, p.refine_passes, p.refine_sample, p.kmeans_iters = rounds, refine_passes, refine_sample, kmeans_iters
         p.balance, p.seed, p.reverse_edges = balance, seed, int(bool(reverse_edges))
         p.int_exact = int(bool(int_exact))
+        p.device_budget_mb = int(device_budget_mb)
         graph = _empty_like_input(X, (N, K), np.uint32) if prune else None
         ids = _empty_like_input(X, (N, M), np.int32) if return_knn else None
         d = _empty_like_input(X, (N, M), np.float32) if return_knn else None

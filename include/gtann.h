@@ -120,6 +120,32 @@ int gt_prune_occlusion(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dty
  * Replaces _apply_reverse_edges (bd/build_bucket.py:473). */
 int gt_reverse_insert(gt_ctx* ctx, int32_t* ids, float* dists, int64_t N, int32_t M);
 
+/* Reverse merge of a host forward graph (N x K, K <= 64) into host rows out,
+ * out of core: the forward rows stream through the device in batches that
+ * route every edge to its destination chunk, then one destination chunk at a
+ * time is merged, each within device_budget_bytes of device memory (<= 0:
+ * one chunk).  Same rows as gt_reverse_merge.  Replaces run_method_E with
+ * several chunks (src/optimize_chunked.cu:1548-2057; optimize_chunked -m E
+ * --gpu-budget-mb). */
+int gt_reverse_merge_chunked(gt_ctx* ctx, const uint32_t* fwd, int64_t N, int32_t K, int64_t device_budget_bytes,
+                             uint32_t* out);
+
+/* Windowed CAGRA prune (src/prune_windowed_gpu.cu:529-915, run_chunked;
+ * src/prune_windowed_core.hpp:177-263) of host candidate rows cand (N x M,
+ * rank order, -1 = padding) in the bucket-contiguous id space: processing
+ * position q owns ids [offsets[q], offsets[q+1]) (offsets: n_buckets + 1,
+ * offsets[0] = 0, offsets[n_buckets] = N).  A row at position p counts a
+ * detour through its neighbour d only when d's position is one of win[p*W ..
+ * p*W + win_len[p]) (the reference puts p itself and its centroid-kNN or pool
+ * buckets there); a neighbour outside the window contributes nothing (with
+ * every position in every window this is gt_cagra_prune).  Then the first K
+ * by (count, rank).  Positions go in chunks whose window union fits
+ * device_budget_bytes (<= 0: no limit); the rows do not depend on it.  out:
+ * host N x K.  GT_EFEWCAND if a row has fewer than K valid candidates. */
+int gt_prune_windowed(gt_ctx* ctx, const int32_t* cand, int64_t N, int32_t M, const uint32_t* offsets,
+                      int32_t n_buckets, const int32_t* win, const int32_t* win_len, int32_t W, int32_t K,
+                      int64_t device_budget_bytes, uint32_t* out);
+
 /* prune then reverse merge.  Replaces cuvs::neighbors::cagra::helpers::optimize
  * (src/optimize.cu:395-397, src/bucket.cu:8470). */
 int gt_optimize(gt_ctx* ctx, const uint32_t* knn, int64_t N, int32_t M, int32_t K, uint32_t* out);
@@ -166,6 +192,14 @@ typedef struct gt_build_params {
                                or [0, 255] (D <= 256) run the point kNN on the int8 matrix cores;
                                every distance is an exact integer in both kernels, so the table and
                                graph are the fp32 kernel's, bit for bit.  0: always fp32 */
+    int32_t device_budget_mb; /* bucket2's --gpu-limit: 0 (default) = the tables live on the device.
+                               > 0 and the resident tables exceed it: out of core -- the running
+                               N x M table and the graphs stay in host memory and move through this
+                               many MiB of device memory chunk by chunk (buckets for the kNN rounds,
+                               rows plus their neighbours' rows for the prune, destination rows for
+                               the reverse merge); same table and graph.  The dataset stays on the
+                               device and is not counted.  Excludes refine_passes and reverse_edges.
+                               Replaces ChunkedKnnAccumulator (src/bucket.cu:5670-6369) */
 } gt_build_params;
 
 typedef struct gt_build_stats {
@@ -185,6 +219,7 @@ typedef struct gt_build_stats {
     int64_t knn_launches;   /* fused kNN launches of the rounds (knn_flops / t_knn cover these) */
     int64_t knn_int8;       /* 1: the rounds ran on the int8 matrix cores (integer-typed rows, or
                                integer-valued float rows with int_exact), 0: fp32 */
+    int64_t ooc_chunks;     /* device chunks of an out-of-core build (0: resident) */
 } gt_build_stats;
 
 void gt_build_params_default(gt_build_params* p);

@@ -268,7 +268,39 @@ static int cmp_i32(const void* x, const void* y)
     return (a > b) - (a < b);
 }
 
-static void detour_counts(const int32_t* G, int64_t N, int M, int64_t a, uint32_t* count)
+/* Bucket windows (src/prune_windowed_core.hpp:77-124 BucketWindow): ids are
+ * bucket-contiguous, position q owning [off[q], off[q+1]); row a's window is
+ * the positions win[p*W .. p*W + win_len[p]) of a's own position p.  NULL
+ * off: every row is visible (the full prune). */
+typedef struct {
+    const uint32_t* off;
+    int nb;
+    const int32_t* win;
+    const int32_t* win_len;
+    int W;
+} window_t;
+
+static int pos_of(const window_t* w, uint32_t id)   /* last q with off[q] <= id */
+{
+    int lo = 0, hi = w->nb - 1;
+    while (lo < hi) {
+        int mid = (lo + hi + 1) / 2;
+        if (w->off[mid] <= id) lo = mid;
+        else hi = mid - 1;
+    }
+    return lo;
+}
+
+static int visible(const window_t* w, int64_t a, int32_t d)
+{
+    if (!w || !w->off) return 1;
+    int p = pos_of(w, (uint32_t)a), q = pos_of(w, (uint32_t)d);
+    for (int i = 0; i < w->win_len[p]; ++i)
+        if (w->win[(int64_t)p * w->W + i] == q) return 1;
+    return 0;
+}
+
+static void detour_counts_w(const int32_t* G, int64_t N, int M, int64_t a, uint32_t* count, const window_t* win)
 {
     const int32_t* A = G + a * M;
     int32_t drow[512];   /* M <= 512: the row of D, sorted for membership tests */
@@ -276,6 +308,7 @@ static void detour_counts(const int32_t* G, int64_t N, int M, int64_t a, uint32_
     for (int kAD = 0; kAD < M - 1; ++kAD) {
         int32_t d = A[kAD];
         if (d < 0 || (int64_t)d >= N) continue;
+        if (!visible(win, a, d)) continue;   /* outside the window: contributes nothing */
         memcpy(drow, G + (int64_t)d * M, sizeof(int32_t) * (size_t)M);
         qsort(drow, (size_t)M, sizeof(int32_t), cmp_i32);
         for (int kAB = kAD + 1; kAB < M; ++kAB) {
@@ -286,6 +319,11 @@ static void detour_counts(const int32_t* G, int64_t N, int M, int64_t a, uint32_
     }
 }
 
+static void detour_counts(const int32_t* G, int64_t N, int M, int64_t a, uint32_t* count)
+{
+    detour_counts_w(G, N, M, a, count, NULL);
+}
+
 /*
  * CAGRA rank-based prune: rows are already in rank order (no L2 re-sort),
  * detour counts as above, then the first K valid candidates in
@@ -294,7 +332,8 @@ static void detour_counts(const int32_t* G, int64_t N, int M, int64_t a, uint32_
  * row in *bad_row) when a row has fewer than K valid candidates
  * (src/prune_windowed_core.hpp:257-260).
  */
-int or_cagra_prune(const int32_t* G, int64_t N, int M, int K, uint32_t* out, int64_t* bad_row)
+static int cagra_prune_w(const int32_t* G, int64_t N, int M, int K, uint32_t* out, int64_t* bad_row,
+                         const window_t* win)
 {
     if (!G || N <= 0 || M <= 0 || M > 512 || K <= 0 || K > M) return OR_EINVAL;
     int64_t first_bad = -1;
@@ -304,7 +343,7 @@ int or_cagra_prune(const int32_t* G, int64_t N, int M, int K, uint32_t* out, int
         #pragma omp for schedule(dynamic, 64)
         for (int64_t a = 0; a < N; ++a) {
             const int32_t* A = G + a * M;
-            detour_counts(G, N, M, a, cnt);
+            detour_counts_w(G, N, M, a, cnt, win);
             int pk = 0;
             uint32_t level = 0;
             while (pk < K) {
@@ -328,6 +367,26 @@ int or_cagra_prune(const int32_t* G, int64_t N, int M, int K, uint32_t* out, int
     }
     if (bad_row) *bad_row = first_bad;
     return first_bad >= 0 ? OR_EFEWCAND : OR_OK;
+}
+
+int or_cagra_prune(const int32_t* G, int64_t N, int M, int K, uint32_t* out, int64_t* bad_row)
+{
+    return cagra_prune_w(G, N, M, K, out, bad_row, NULL);
+}
+
+/*
+ * Windowed CAGRA prune (src/prune_windowed_core.hpp:177-263 with a
+ * BucketWindow per processing position, src/prune_windowed.cpp:300-420;
+ * src/prune_windowed_gpu.cu:181-326): as or_cagra_prune, but a detour
+ * through D counts only when D's bucket position is in the window of the
+ * pruned row's position.  Rows are taken in the given (rank) order.
+ */
+int or_prune_windowed(const int32_t* G, int64_t N, int M, const uint32_t* off, int nb, const int32_t* win,
+                      const int32_t* win_len, int W, int K, uint32_t* out, int64_t* bad_row)
+{
+    if (!off || nb <= 0 || off[0] != 0 || (int64_t)off[nb] != N || !win || !win_len || W <= 0) return OR_EINVAL;
+    window_t w = {off, nb, win, win_len, W};
+    return cagra_prune_w(G, N, M, K, out, bad_row, &w);
 }
 
 /* detour counts exported for the known-answer tests */

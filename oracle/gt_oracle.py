@@ -109,6 +109,7 @@ def lib():
         L.or_sanitize.argtypes = [vp, i64, i32, vp]
         L.or_sanitize.restype = i64
         L.or_cagra_prune.argtypes = [vp, i64, i32, i32, vp, vp]
+        L.or_prune_windowed.argtypes = [vp, i64, i32, vp, i32, vp, vp, i32, i32, vp, vp]
         L.or_detour_counts.argtypes = [vp, i64, i32, i64, vp]
         L.or_reverse_merge.argtypes = [vp, i64, i32, vp]
         L.or_reverse_insert.argtypes = [vp, vp, i64, i32]
@@ -137,6 +138,7 @@ def ref():
         R = C.CDLL(_REF_PATH)
         vp, i64, i32 = C.c_void_p, C.c_int64, C.c_int32
         R.ref_cagra_prune.argtypes = [vp, i64, i32, i32, vp]
+        R.ref_prune_windowed.argtypes = [vp, i64, i32, vp, i32, vp, vp, i32, i32, vp]
         R.ref_cagra_prune_omp.argtypes = [vp, i64, i32, i32, vp]
         R.ref_reverse_merge_omp.argtypes = [vp, i64, i32, vp]
         R.ref_detour_counts.argtypes = [vp, i64, i32, i64, vp]
@@ -268,6 +270,22 @@ def cagra_prune(G, K):
     out = np.zeros((N, K), np.uint32)
     bad = np.zeros(1, np.int64)
     rc = lib().or_cagra_prune(_p(G), N, M, K, _p(out), _p(bad))
+    return out, rc, int(bad[0])
+
+
+def prune_windowed(G, offsets, win, win_len, K):
+    """Windowed CAGRA prune (src/prune_windowed_core.hpp:177-263 with bucket
+    windows); returns (out, rc, bad_row)."""
+    G = np.ascontiguousarray(G).view(np.int32) if np.asarray(G).dtype == np.uint32 else \
+        np.ascontiguousarray(G, np.int32)
+    N, M = G.shape
+    off = np.ascontiguousarray(offsets, np.uint32)
+    win = np.ascontiguousarray(win, np.int32)
+    wl = np.ascontiguousarray(win_len, np.int32)
+    out = np.zeros((N, K), np.uint32)
+    bad = np.zeros(1, np.int64)
+    rc = lib().or_prune_windowed(_p(G), N, M, _p(off), len(off) - 1, _p(win), _p(wl), win.shape[1], K, _p(out),
+                                 _p(bad))
     return out, rc, int(bad[0])
 
 
@@ -427,6 +445,21 @@ def ref_reverse_merge_omp(fwd):
     out = np.empty((N, K), np.uint32)
     _check(ref().ref_reverse_merge_omp(_p(fwd), N, K, _p(out)), "ref_reverse_merge_omp")
     return out
+
+
+def ref_prune_windowed(G, offsets, win, win_len, K):
+    """The reference's own windowed prune (BucketWindow per position,
+    compute_detour_counts + select_pruned_row), rows in the given order."""
+    R = ref()
+    G = np.ascontiguousarray(G).view(np.int32) if np.asarray(G).dtype == np.uint32 else \
+        np.ascontiguousarray(G, np.int32)
+    N, M = G.shape
+    off = np.ascontiguousarray(offsets, np.uint32)
+    win = np.ascontiguousarray(win, np.int32)
+    wl = np.ascontiguousarray(win_len, np.int32)
+    out = np.zeros((N, K), np.uint32)
+    rc = R.ref_prune_windowed(_p(G), N, M, _p(off), len(off) - 1, _p(win), _p(wl), win.shape[1], K, _p(out))
+    return out, rc
 
 
 def ref_detour_counts(G, a):

@@ -7,7 +7,9 @@
 // Wrapped reference functions:
 //   prune_windowed::compute_detour_counts / select_pruned_row
 //       (src/prune_windowed_core.hpp:189-263), full window via WindowLookup
-//       (src/prune_windowed_core.hpp:50-75), rows taken in the given order;
+//       (src/prune_windowed_core.hpp:50-75), rows taken in the given order,
+//       and with a BucketWindow per processing position
+//       (src/prune_windowed_core.hpp:77-124) for the windowed prune;
 //   edge_chunk::build_rank_ordered_csr + merge_rank_ordered_into_row
 //       (src/edge_chunk_accumulator.hpp:235-284, 471-494), fed the reverse
 //       edges {dst = fwd[i][k], src = i, rank = k} of
@@ -53,6 +55,37 @@ int ref_cagra_prune(const int32_t* G, int64_t N, int32_t M, int32_t K, uint32_t*
         for (int64_t a = 0; a < N; ++a) {
             prune_windowed::compute_detour_counts(G + a * M, M, w, detour);
             prune_windowed::select_pruned_row(G + a * M, M, detour, K, out + a * K);
+        }
+        return 0;
+    } catch (const std::runtime_error& e) {
+        return std::string(e.what()).find("fewer than output_degree") != std::string::npos ? -4 : -1;
+    } catch (...) {
+        return -1;
+    }
+}
+
+// The windowed prune as src/prune_windowed.cpp's batched path runs it: per
+// processing position p a BucketWindow (src/prune_windowed_core.hpp:77-124)
+// holding the buckets win[p*W .. p*W + win_len[p]), then
+// compute_detour_counts + select_pruned_row on each row of p's bucket in the
+// given order (rows already ranked, as the --dists ranking leaves them).
+int ref_prune_windowed(const int32_t* G, int64_t N, int32_t M, const uint32_t* off, int32_t nb, const int32_t* win,
+                       const int32_t* win_len, int32_t W, int32_t K, uint32_t* out)
+{
+    try {
+        prune_windowed::BucketWindow bw(off, nb);
+        static const float dummy = 0.f;
+        std::vector<uint32_t> detour;
+        for (int32_t p = 0; p < nb; ++p) {
+            bw.clear();
+            for (int32_t i = 0; i < win_len[p]; ++i) {
+                const int32_t q = win[static_cast<int64_t>(p) * W + i];
+                bw.add_bucket(q, G + static_cast<int64_t>(off[q]) * M, M, &dummy, 0);
+            }
+            for (int64_t a = off[p]; a < static_cast<int64_t>(off[p + 1]); ++a) {
+                prune_windowed::compute_detour_counts(G + a * M, M, bw, detour);
+                prune_windowed::select_pruned_row(G + a * M, M, detour, K, out + a * K);
+            }
         }
         return 0;
     } catch (const std::runtime_error& e) {

@@ -75,3 +75,33 @@ def assert_knn_close(X, queries, ids, d, ref_ids, ref_d, rtol=1e-5, metric="l2")
             assert (np.abs(true - refd) <= t2).all(), f"row {r}: id mismatch beyond ties at {mis}"
         assert len(set(ids[r, :k].tolist())) == k, f"row {r}: duplicate ids"
     return nmis
+
+
+def bucketed_graph(rng, N, nb, M, W, outside=0.3, pad=0.0):
+    """A candidate table in a bucket-contiguous id space (the layout of the
+    windowed prune): nb buckets of random sizes, each row's candidates drawn
+    mostly from its own bucket and a few others, some padding (-1) and
+    repeated ids; per bucket position a window of itself plus up to W - 1
+    random positions.  Returns (G int32 (N, M), offsets uint32 (nb + 1),
+    win int32 (nb, W), win_len int32 (nb,))."""
+    cuts = np.sort(rng.choice(np.arange(1, N), nb - 1, replace=False))
+    off = np.concatenate([[0], cuts, [N]]).astype(np.uint32)
+    pos = np.searchsorted(off, np.arange(N), side="right") - 1
+    G = np.empty((N, M), np.int32)
+    for a in range(N):
+        lo, hi = int(off[pos[a]]), int(off[pos[a] + 1])
+        own = rng.integers(lo, hi, M)
+        far = rng.integers(0, N, M)
+        row = np.where(rng.random(M) < outside, far, own)
+        row[row == a] = (a + 1) % N
+        G[a] = row
+    if pad:
+        G[rng.random((N, M)) < pad] = -1
+    win = np.zeros((nb, W), np.int32)
+    wl = np.zeros(nb, np.int32)
+    for p in range(nb):
+        ws = [p] + [int(q) for q in rng.integers(0, nb, W - 1) if q != p]
+        ws = sorted(set(ws))[:W]
+        win[p, :len(ws)] = ws
+        wl[p] = len(ws)
+    return G, off, win, wl

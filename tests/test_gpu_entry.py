@@ -82,6 +82,26 @@ def test_cli_bucket2_and_pipeline_tools(tmp_path, ctx):
     _run(["optimize_chunked", "-g", tmp_path / "fwd.bin", "-o", tmp_path / "e.bin", "-m", "E",
           "--inverse-perm", d / "inverse_perm.bin", "--final-output", tmp_path / "final.bin"])
     np.testing.assert_array_equal(io.read_graph(tmp_path / "e.bin"), final_n)
+    # with a budget below the graph: destination chunks, the same rows
+    _run(["optimize_chunked", "-g", tmp_path / "fwd.bin", "-o", tmp_path / "e2.bin", "-m", "E",
+          "--gpu-budget-mb", 1])
+    np.testing.assert_array_equal(io.read_graph(tmp_path / "e2.bin"), final_n)
+    # the windowed prune: position q's window = q + the positions of its
+    # bucket's centroid-kNN neighbours (src/prune_windowed.cpp:370-385)
+    _run(["prune_windowed", "-k", d / "vector_knn.bin", "-i", d / "data_reordered.fbin", "-o", tmp_path / "fw.bin",
+          "--output-degree", 32, "--bucket-offsets", d / "bucket_offsets.bin", "--bucket-process-order",
+          d / "bucket_process_order.bin", "-c", d / "centroid_knn.bin", "--cache-mb", 1])
+    pos_of = np.empty(16, np.int64)
+    pos_of[order] = np.arange(16)
+    win = np.zeros((16, 9), np.int32)
+    wl = np.zeros(16, np.int32)
+    for q in range(16):
+        w = sorted({q} | {int(pos_of[b]) for b in cg[order[q]] if b != order[q] and b < 16})
+        win[q, :len(w)] = w
+        wl[q] = len(w)
+    ref_w, rc, _ = O.prune_windowed(ids_new, off, win, wl, 32)
+    assert rc == 0
+    np.testing.assert_array_equal(io.read_graph(tmp_path / "fw.bin"), ref_w)
     np.testing.assert_array_equal(io.read_graph(tmp_path / "final.bin"), O.translate(final_n, inv))
     _run(["translate_ids", "-g", tmp_path / "e.bin", "-p", d / "inverse_perm.bin", "-o", tmp_path / "t.bin"])
     np.testing.assert_array_equal(io.read_graph(tmp_path / "t.bin"), O.translate(final_n, inv))
@@ -140,6 +160,13 @@ def test_cli_bucket2_multi_round_recall(tmp_path):
     assert rec > 0.9, rec
     g = io.read_graph(d / "final_graph.bin")
     assert g.shape == (len(X), 32) and (g < len(X)).all()
+    # --gpu-limit far below the tables: the out-of-core build writes the same files
+    _run(["bucket2", "-i", tmp_path / "c2.fbin", "-o", tmp_path / "o2", "--centroid-ratio", 0.00032,
+          "--nprobe", 1, "--knn-k", 8, "--neighbors-m", 64, "-t", 2, "--fused-optimize-degree", 32, "--skip-npy",
+          "--gpu-limit", 32 << 20])
+    d2 = tmp_path / "o2" / "k8p1m64t2"
+    np.testing.assert_array_equal(io.read_vector_knn(d2 / "vector_knn.bin"), ids)
+    np.testing.assert_array_equal(io.read_graph(d2 / "final_graph.bin"), g)
 
 
 def test_python_build_knn_mirror(tmp_path, ctx):

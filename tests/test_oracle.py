@@ -226,6 +226,52 @@ def test_prune_matches_reference_random():
 
 # ---------------------------------------------------------------- reverse merge
 
+def test_prune_windowed_known_answer():
+    # two buckets {0, 1, 2} and {3, 4, 5}; row 0 = [1, 3, 4, 2] in rank order.
+    # Full window: D=1 (rank 0) holds 4; D=3 (rank 1, other bucket) holds 4
+    # and 2; D=4 (rank 2) holds 2 -> counts [0, 0, 2, 2] -> K=3: [1, 3, 4].
+    # Window of position 0 = {0}: only D=1 counts -> [0, 0, 1, 0] -> [1, 3, 2].
+    G = np.array([[1, 3, 4, 2], [0, 4, 5, 5], [0, 1, 3, 4], [2, 5, 4, 0], [2, 0, 3, 5], [3, 4, 0, 1]], np.int32)
+    off = np.array([0, 3, 6], np.uint32)
+    own = np.array([[0, 0], [1, 0]], np.int32), np.array([1, 1], np.int32)
+    both = np.array([[0, 1], [0, 1]], np.int32), np.array([2, 2], np.int32)
+    out, rc, _ = O.prune_windowed(G, off, *own, 3)
+    assert rc == 0 and out[0].tolist() == [1, 3, 2]
+    out, rc, _ = O.prune_windowed(G, off, *both, 3)
+    assert rc == 0 and out[0].tolist() == [1, 3, 4]
+    full, _, _ = O.cagra_prune(G, 3)
+    assert (out == full).all()
+
+
+def test_prune_windowed_full_windows_equal_prune():
+    from helpers import bucketed_graph
+    rng = np.random.default_rng(11)
+    G, off, _, _ = bucketed_graph(rng, 2000, 17, 24, 3)
+    nb = len(off) - 1
+    win = np.tile(np.arange(nb, dtype=np.int32), (nb, 1))
+    out, rc, _ = O.prune_windowed(G, off, win, np.full(nb, nb, np.int32), 12)
+    ref, rc2, _ = O.cagra_prune(G, 12)
+    assert rc == rc2 == 0 and (out == ref).all()
+
+
+@pytest.mark.skipif(not O.ref_available(), reason="reference harness not built here")
+@pytest.mark.parametrize("seed,N,nb,M,K,W,pad", [(1, 3000, 30, 32, 16, 4, 0.0), (2, 1500, 9, 64, 32, 2, 0.0),
+                                                 (3, 2500, 40, 20, 10, 6, 0.05)])
+def test_prune_windowed_matches_reference_random(seed, N, nb, M, K, W, pad):
+    """The reference's own BucketWindow prune (src/prune_windowed_core.hpp),
+    compiled in place, on random bucketed tables with padding and repeats."""
+    from helpers import bucketed_graph
+    rng = np.random.default_rng(seed)
+    G, off, win, wl = bucketed_graph(rng, N, nb, M, W, pad=pad)
+    out, rc, _ = O.prune_windowed(G, off, win, wl, K)
+    ref, rrc = O.ref_prune_windowed(G, off, win, wl, K)
+    assert rc == rrc
+    if rc == 0:
+        assert (out == ref).all()
+        full, _, _ = O.cagra_prune(G, K)
+        assert (out != full).any()   # the windows decide some rows
+
+
 def test_merge_row_truncation_known_answer():
     # test_edge_chunk_accumulator.cpp:185-220: 5 candidates for 3 free slots
     row = O.merge_row([0, 1, 2, 3, 4, 5], [13, 11, 14, 12, 10])
