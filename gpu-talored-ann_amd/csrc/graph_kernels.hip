@@ -196,6 +196,39 @@ __global__ void __launch_bounds__(256) sanitize_kernel(const int32_t* __restrict
     }
 }
 
+// The same rule for M in {16, 32, 64, 128}: L = M / 4 lanes per row, each
+// with one 16-byte load and store, 64 / L rows per wave, the row's first
+// valid entry by a min over its lanes.
+template <int L>
+__global__ void __launch_bounds__(256) sanitize_vec_kernel(const int4* __restrict__ in, int64_t N,
+                                                           uint4* __restrict__ out)
+{
+    constexpr int R = 64 / L;   // rows per wave
+    const int lane = threadIdx.x & 63;
+    const int64_t i = (static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * R + lane / L;
+    const int part = lane % L;
+    const bool live = i < N;
+    const int4 v = live ? in[i * L + part] : make_int4(-1, -1, -1, -1);
+    const int32_t e[4] = {v.x, v.y, v.z, v.w};
+    bool ok[4];
+    int first = INT_MAX;
+#pragma unroll
+    for (int u = 3; u >= 0; --u) {
+        ok[u] = e[u] >= 0 && e[u] < N && e[u] != i;
+        if (ok[u]) first = 4 * part + u;
+    }
+#pragma unroll
+    for (int o = 1; o < L; o <<= 1) first = min(first, __shfl_xor(first, o));
+    // the row's first valid entry, from the lane that holds it
+    const int src = (lane & ~(L - 1)) | ((first == INT_MAX ? 0 : first) >> 2);
+    const int sel = (first == INT_MAX ? 0 : first) & 3;
+    const int32_t mine = sel == 0 ? e[0] : sel == 1 ? e[1] : sel == 2 ? e[2] : e[3];
+    const int32_t got = __shfl(mine, src);
+    const uint32_t fb = first == INT_MAX ? static_cast<uint32_t>((i + 1) % N) : static_cast<uint32_t>(got);
+    if (live)
+        out[i * L + part] = make_uint4(ok[0] ? e[0] : fb, ok[1] ? e[1] : fb, ok[2] ? e[2] : fb, ok[3] ? e[3] : fb);
+}
+
 // ------------------------------------------------------------------ prune
 // CAGRA detour-count prune of one point per wave.
 // count[kAB] = #{kAD < kAB : D = row[kAD] in [0,N), row[kAB] in row(D)},
@@ -1419,7 +1452,16 @@ void launch_init_flags(unsigned long long* bad_row, int* err, hipStream_t s)
 void launch_sanitize(const int32_t* in, int64_t N, int M, uint32_t* out, hipStream_t s)
 {
     if (N <= 0) return;
-    hipLaunchKernelGGL(sanitize_kernel, dim3(grid_for(N, 4)), dim3(256), 0, s, in, N, M, out);
+    const bool vec = (reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(out)) % 16 == 0;
+#define GT_SAN_VEC(LL)                                                                                          \
+    hipLaunchKernelGGL((sanitize_vec_kernel<LL>), dim3(grid_for(N, 4 * (64 / LL))), dim3(256), 0, s,            \
+                       reinterpret_cast<const int4*>(in), N, reinterpret_cast<uint4*>(out))
+    if (vec && M == 64) GT_SAN_VEC(16);
+    else if (vec && M == 32) GT_SAN_VEC(8);
+    else if (vec && M == 128) GT_SAN_VEC(32);
+    else if (vec && M == 16) GT_SAN_VEC(4);
+    else hipLaunchKernelGGL(sanitize_kernel, dim3(grid_for(N, 4)), dim3(256), 0, s, in, N, M, out);
+#undef GT_SAN_VEC
     GT_HIP(hipGetLastError());
 }
 

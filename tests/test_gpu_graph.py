@@ -23,11 +23,16 @@ def _rand_graph(rng, N, M, pad=0.0, dup=True):
     return G
 
 
-def test_sanitize_gpu(ctx):
-    rng = np.random.default_rng(1)
-    G = rng.integers(-1, 600, size=(500, 64)).astype(np.int32)
+@pytest.mark.parametrize("M", [64, 32, 128, 16, 48, 7])
+def test_sanitize_gpu(ctx, M):
+    # the vector kernel (M in 16, 32, 64, 128) and the one-wave-per-row kernel
+    rng = np.random.default_rng(M)
+    N = 503
+    G = rng.integers(-1, N + 100, size=(N, M)).astype(np.int32)
     G[3] = -1
     G[4] = 4
+    G[N - 1] = N - 1   # self only: the fallback wraps to row 0
+    G[7, :M // 2] = -5
     np.testing.assert_array_equal(ctx.sanitize(G), O.sanitize(G))
 
 
@@ -220,6 +225,22 @@ def test_build_graph_c1_end_to_end(ctx):
     assert rc == 0
     np.testing.assert_array_equal(res.graph, O.reverse_merge(fwd))
     _structural(res.graph, len(X), 32)
+
+
+@pytest.mark.parametrize("n_buckets,nprobe", [(400, 0), (60, 1)])
+def test_build_graph_padded_table(ctx, n_buckets, nprobe):
+    """Buckets smaller than M + 1: the table carries -1 padding, which the
+    build's sanitize replaces before the prune; the graph equals the oracle's
+    sanitize + prune + merge of the returned table."""
+    X, _ = synth.generate("C1", n=4000)
+    X = np.rint(X * 8).astype(np.float32)
+    res = ctx.build_graph(X, n_buckets=n_buckets, nprobe=nprobe, M=32, K=16, rounds=1, kmeans_iters=0,
+                          balance=0.0)
+    if n_buckets == 400:
+        assert (res.knn_ids < 0).any()
+    fwd, rc, _ = O.cagra_prune(O.sanitize(res.knn_ids), 16)
+    assert rc == 0
+    np.testing.assert_array_equal(res.graph, O.reverse_merge(fwd))
 
 
 def test_build_graph_recall_c2_small(ctx):
