@@ -7,15 +7,19 @@ merge), sanitize, CAGRA prune, reverse-edge merge -- of configuration C2
 (1,000,000 x 128 fp32 integer-valued points, L2, 256 buckets, M 64 -> K 32)
 with the dataset already resident in HBM.  Prints one JSON line.
 
-`roofline` is the kNN kernel of the rounds (knn_i8_kernel when the rows are
-integers, as C2's are; knn_fused_kernel / knn_wide_kernel otherwise):
-achieved = the algorithmic ops of its launches (2*D per scanned (query, pool
-row) pair) over their summed duration, both measured by the library with HIP
-events on its stream.  `traffic` is read from
-profiles/<kernel>_<config>_traffic.json (knn_i8_C2_traffic.json for the
-default run), the rocprofv3 FETCH_SIZE/WRITE_SIZE measurement of the same
-launches (commands in profiles/knn_i8_C2_build.md), when the knobs are the
-defaults.
+`roofline` is the kNN kernel of the rounds (knn_i8_collect_kernel +
+knn_select_kernel when the rows are integers, as C2's are; knn_fused_kernel /
+knn_wide_kernel otherwise): achieved = the algorithmic ops of its launches
+(2*D per scanned (query, pool row) pair) over their summed duration, both
+measured by the library with HIP events on its stream.  `traffic` is read
+from profiles/<kernel>_<config>_traffic.json (knn_i8_collect_C2_traffic.json
+for the default run), the rocprofv3 FETCH_SIZE/WRITE_SIZE measurement of the
+same launches (commands in profiles/knn_i8_collect_C2_build.md), when the
+knobs are the defaults.  `roofline_prune` / `roofline_revmerge`: the
+algorithmic bytes of sanitize + prune and of the reverse merge over their
+event times.  `--refine-passes P` adds a `refine` leg (the same build with P
+refinement passes: ms per pass, recall before and after, refine_2hop_kernel's
+row-gather rate); the `configs` leg reports one pass on C3 and C4.
 
 `search` (after the build) runs the search entry point on workload S2 (the
 C2 shape with a 16-dimensional latent structure: a connected graph, unlike
@@ -181,16 +185,22 @@ def search_leg(ctx, torch, name, nq, kw, efs, cpu_sample):
     return out
 
 
-def knn_roofline(s, D, metric):
+def knn_roofline(s, D, metric, M=64):
     """Roofline of the round launches of the kNN kernel from the library's
-    own event times (mean build stats s)."""
+    own event times (mean build stats s).  Integer rows with lists of at most
+    64 run as two kernels per launch (knn_i8_collect_kernel keeps the pairs
+    under a per-query bound, knn_select_kernel reduces them to the top M);
+    the library times the pair as one launch."""
     launches = max(1, int(round(s["knn_launches"])))
     launch_s = s["t_knn"] / launches
     flops = s["knn_flops"] / launches
     int8 = bool(round(s["knn_int8"]))
     mip = 1 if metric == "ip" else 0
     if int8:
-        kname, peak, unit = f"knn_i8_kernel<{-(-D // 32) * 32}, {mip}>", PEAK_INT8_MFMA, "TOP/s"
+        dp = -(-D // 32) * 32
+        kname = (f"knn_i8_collect_kernel<{dp}, {mip}> + knn_select_kernel" if 4 < M <= 64 and dp <= 256
+                 else f"knn_i8_kernel<{dp}, {mip}>")
+        peak, unit = PEAK_INT8_MFMA, "TOP/s"
     elif D <= 256:
         kname, peak, unit = f"knn_fused_kernel<{-(-D // 32) * 32}, {mip}>", PEAK_FP32_MFMA, "TFLOP/s"
     else:
@@ -292,6 +302,52 @@ def recall32(ctx, torch, Xd, knn, metric, n_sample=10000):
     return recall_at(knn[q], ex_i.cpu().numpy(), 32)
 
 
+def mean_candidates(knn, S, n_sample=2000):
+    """Mean number of distinct 2-hop candidates per point that refinement
+    computes a distance for: the first S neighbours of the first S
+    neighbours, minus invalid ids, the point itself and its own row."""
+    N = knn.shape[0]
+    rows = np.random.default_rng(1).choice(N, min(N, n_sample), replace=False)
+    tot = 0
+    for a in rows:
+        own = knn[a]
+        hop1 = own[:S][(own[:S] >= 0) & (own[:S] < N)]
+        c = knn[hop1, :S].ravel()
+        c = np.setdiff1d(c[(c >= 0) & (c < N) & (c != a)], own)
+        tot += len(c)
+    return tot / len(rows)
+
+
+def refine_leg(ctx, torch, Xd, knn, kw, metric, rec_before, passes=1, S=16, steps=2):
+    """The same build with refinement (passes x 2-hop pull join of sample S)
+    after the rounds: refine ms per pass, recall@32 before and after, and the
+    row-gather rate of refine_2hop_kernel.  Every candidate costs one Dp-float
+    row read (from L2 or the MALL when the candidate's bucket is resident
+    there, else from HBM); a point also reads its row, its list and its S
+    neighbours' lists and writes its list: the HBM minimum of a pass is the
+    dataset plus the two tables."""
+    N, D = Xd.shape
+    Dp = -(-D // 32) * 32
+    M = knn.shape[1]
+    nc = mean_candidates(knn, S)
+    wall, s, res = timed_builds(ctx, torch, Xd, dict(kw, refine_passes=passes, refine_sample=S), steps)
+    t = s["t_refine"] / passes
+    gather = N * nc * Dp * 4
+    hbm_min = N * Dp * 4 + 2 * N * M * 8
+    rec = recall32(ctx, torch, Xd, res.knn_ids.cpu().numpy(), metric)
+    del res
+    return {"passes": passes, "sample": S, "ms_per_build": wall * 1e3, "refine_ms_per_pass": t * 1e3,
+            "recall@32_before": rec_before, "recall@32_after": rec,
+            "candidates_per_point": nc,
+            "roofline_refine": {"kernel": f"refine_2hop_kernel<{2 if Dp <= 256 else 4}>", "bound": "hbm",
+                                "achieved": hbm_min / t / 1e9, "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+                                "frac": hbm_min / t / PEAK_HBM, "bytes": hbm_min,
+                                "row_gather_bytes": gather, "row_gather_GBps": gather / t / 1e9,
+                                "note": "bytes = dataset + table in + table out (the HBM minimum of a pass); the "
+                                        "kernel is bound by its candidate-row gathers (row_gather_GBps, mostly "
+                                        "served by L2 and the MALL: the points go in bucket order)"}}
+
+
 def configs_leg(ctx, torch, names, steps):
     """Every other BASELINE configuration once more with the default knobs:
     build time, recall@32 on a 10,000-point sample (all of C1) against the
@@ -312,12 +368,15 @@ def configs_leg(ctx, torch, names, steps):
         out[name] = {"workload": f"{name}: {N} x {D} {cfg.dtype}, {cfg.metric.upper()}, {cfg.buckets} buckets, "
                                  f"M {cfg.M} -> K {cfg.K}, 2 rounds, 3 Lloyd iterations, nprobe 1",
                      "ms_per_step": wall * 1e3, "value": N / wall / 1e6, "unit": "Mpts/s", "recall@32": rec,
-                     "knn_roofline": dict(knn_roofline(s, D, cfg.metric),
-                                          rocprof=traffic_file(knn_roofline(s, D, cfg.metric)["kernel"], name)),
+                     "knn_roofline": dict(knn_roofline(s, D, cfg.metric, cfg.M),
+                                          rocprof=traffic_file(knn_roofline(s, D, cfg.metric, cfg.M)["kernel"], name)),
                      "prune_frac_hbm": N * (4 * cfg.M + 4 * cfg.M * (cfg.M - 1) + 4 * cfg.K) / s["t_prune"] / PEAK_HBM,
                      "revmerge_frac_hbm": 28 * N * cfg.K / s["t_revmerge"] / PEAK_HBM,
                      "stages_s": {k: s[k] for k in ("t_prepare", "t_bucketing", "t_knn", "t_merge", "t_prune",
                                                     "t_revmerge", "t_total")}}
+        if name in ("C3", "C4"):
+            # refinement after the rounds: one pass of sample 16
+            out[name]["refine"] = refine_leg(ctx, torch, Xd, knn, kw, cfg.metric, rec)
         print(f"[bench] {name}: {wall * 1e3:.1f} ms, recall@32 {rec:.4f} (data generated in {tg:.1f} s)",
               file=sys.stderr, flush=True)
         del Xd, res, X
@@ -346,6 +405,10 @@ def main():
     ap.add_argument("--search-queries", type=int, default=10000,
                     help="held-out queries of the search leg (0 = skip it)")
     ap.add_argument("--search-config", default="S2", help="workload of the search leg")
+    ap.add_argument("--refine-passes", type=int, default=0,
+                    help="also build --config with this many refinement passes after the rounds and report them "
+                         "(the headline build has none)")
+    ap.add_argument("--refine-sample", type=int, default=16)
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="run one device-to-device copy of this many MiB first (calibrates the "
                          "FETCH_SIZE/WRITE_SIZE counters of rocprofv3 --pmc against known bytes)")
@@ -397,15 +460,11 @@ def main():
         "degree": int(graph.shape[1]),
     }
 
-    roof = knn_roofline(s, D, cfg.metric)
-    traffic = None
+    roof = knn_roofline(s, D, cfg.metric, cfg.M)
     int8 = bool(round(s["knn_int8"]))
-    kbase = "knn_i8" if int8 else ("knn_fused" if D <= 256 else "knn_wide")
-    tfile = os.path.join(ROOT, "profiles", f"{kbase}_{args.config}_traffic.json")
     default_knobs = (args.rounds, args.kmeans_iters, args.nprobe) == (2, 3, 1)
-    if default_knobs and os.path.exists(tfile):
-        with open(tfile) as f:
-            traffic = json.load(f).get("bytes_per_launch")
+    tr = traffic_file(roof["kernel"], args.config) if default_knobs else None
+    traffic = tr["bytes_per_launch"] if tr else None
     prune_bytes = N * (4 * cfg.M + 4 * cfg.M * (cfg.M - 1) + 4 * cfg.K)
     merge_bytes = 28 * N * cfg.K
     # integer-typed datasets of up to 256 dimensions run the int8 kernel, and
@@ -456,7 +515,7 @@ def main():
         # return the same table and graph
         w32, s32, r32 = timed_builds(ctx, torch, Xd, dict(kw, int_exact=False), max(1, min(args.steps, 3)))
         same = bool(torch.equal(r32.knn_ids, res.knn_ids) and torch.equal(r32.graph, res.graph))
-        r = knn_roofline(s32, D, cfg.metric)
+        r = knn_roofline(s32, D, cfg.metric, cfg.M)
         out["fp32_path"] = {
             "note": "int_exact=0: same dataset on knn_fused_kernel (fp32 matrix cores)",
             "value": N / w32 / 1e6, "unit": "Mpts/s", "ms_per_step": w32 * 1e3,
@@ -465,6 +524,10 @@ def main():
                              rocprof=traffic_file(r["kernel"], args.config)),
         }
         del r32
+    if args.refine_passes > 0:
+        out["refine"] = refine_leg(ctx, torch, Xd, knn, kw, cfg.metric, rec["recall@32"], args.refine_passes,
+                                   args.refine_sample, max(1, min(args.steps, 2)))
+        print("[bench] refine leg done", file=sys.stderr, flush=True)
     if not args.reference_knobs and not args.no_ref_knobs:
         # the reference's own knobs on the same data
         wr, sr, rr = timed_builds(ctx, torch, Xd, dict(base_kw, **ref_kw), max(1, min(args.steps, 2)))
@@ -473,7 +536,7 @@ def main():
                      "(sk/scripts/params.sh:12, sk/scripts/dataset_env.py:56)",
             "ms_per_step": wr * 1e3, "value": N / wr / 1e6, "unit": "Mpts/s",
             "recall@32": recall_at(rr.knn_ids.cpu().numpy()[q], ex_i, 32),
-            "knn_roofline": knn_roofline(sr, D, cfg.metric)}
+            "knn_roofline": knn_roofline(sr, D, cfg.metric, cfg.M)}
         del rr
     if not args.no_io:
         h2h, rh = host_to_host_leg(ctx, torch, X, kw, max(1, min(args.steps, 2)))

@@ -95,8 +95,9 @@ void launch_route(const uint32_t* fwd, int64_t nrows, int K, int64_t N, int64_t 
 void launch_rec_group(const unsigned long long* recs, int64_t n, uint32_t* deg, uint32_t* slot, const uint32_t* off,
                       unsigned long long* keys, bool scatter, hipStream_t s);
 // refine_kernel.hip
-void launch_refine_2hop(const float* X, const float* norms, int64_t N, int Dp, int metric, const int32_t* in_ids,
-                        const float* in_d, int M, int S, int32_t* out_ids, float* out_d, hipStream_t s);
+void launch_refine_2hop(const float* X, const float* norms, int64_t N, int Dp, int metric, const int32_t* order,
+                        const int32_t* in_ids, const float* in_d, int M, int S, int32_t* out_ids, float* out_d,
+                        hipStream_t s);
 void launch_centroid_sums(const float* X, int Dp, const int32_t* members, const int64_t* offsets, int64_t C,
                           float* centroids, hipStream_t s);
 int csr_blocks(int64_t S);
@@ -2419,7 +2420,7 @@ int gt_refine_2hop(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtype, 
         int32_t* bi = c.ws<int32_t>(W_G1, nm);
         float* bd = c.ws<float>(W_G2, nm);
         for (int p = 0; p < passes; ++p) {
-            launch_refine_2hop(Xm.data, Xm.norms, N, Xm.Dp, metric, ai, ad, M, S, bi, bd, c.s);
+            launch_refine_2hop(Xm.data, Xm.norms, N, Xm.Dp, metric, nullptr, ai, ad, M, S, bi, bd, c.s);
             std::swap(ai, bi);
             std::swap(ad, bd);
         }
@@ -3035,10 +3036,14 @@ int gt_build_graph_ex(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtyp
         if (p.refine_passes > 0) {
             GT_REQUIRE(p.refine_sample >= 1 && p.refine_sample <= p.M && p.refine_sample * p.refine_sample <= 1024,
                        "bad refine sample");
+            // points in the last bucketing's member order (W_MEMBERS holds it
+            // after a bucketed round): a bucket's 2-hop candidates stay in L2
+            const int32_t* order =
+                c.c->members_gen != 0 ? c.ws<int32_t>(W_MEMBERS, static_cast<size_t>(N)) : nullptr;
             for (int pass = 0; pass < p.refine_passes; ++pass) {
                 st.t_refine += c.timed([&] {
-                    launch_refine_2hop(Xm.data, Xm.norms, N, Xm.Dp, p.metric, run_i, run_d, p.M, p.refine_sample,
-                                       tmp_i, tmp_d, c.s);
+                    launch_refine_2hop(Xm.data, Xm.norms, N, Xm.Dp, p.metric, order, run_i, run_d, p.M,
+                                       p.refine_sample, tmp_i, tmp_d, c.s);
                 });
                 std::swap(run_i, tmp_i);
                 std::swap(run_d, tmp_d);

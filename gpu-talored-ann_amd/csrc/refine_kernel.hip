@@ -18,32 +18,69 @@ namespace gtann {
 void launch_exclusive_scan(const uint32_t* in, int64_t n, uint32_t* out, uint32_t* sums, hipStream_t s);
 
 constexpr int kRefineMaxCand = 1024;   // S*S
-constexpr int kRefineHash = 4096;      // >= 2 * (M + S*S)
 constexpr int kRefineMaxM = 128;
 constexpr int kMaxDp = 1024;           // longest padded row of this build
+
+// LDS of one block, sized per launch: the point's row (Dp floats), the id
+// hash (H = the power of two >= max(256, 2 (M + S*S)) slots, linear probing
+// at load <= 1/2), candidates and their distances (S*S each), survivors and
+// theirs (P = the power of two >= S*S each: the bitonic sort pads to it), the
+// row and its distances (M each).  At most 37.9 KB (Dp 1024, S*S 1024,
+// M 128); 8.9 KB at Dp 96, S 16, M 64, so that the waves, not the LDS,
+// limit the blocks per CU (a cap of 2 to 6 blocks per CU measured slower on
+// 96- and 960-float rows).
+struct RefineLds {
+    int H, C, P;
+    size_t bytes(int Dp, int M) const { return static_cast<size_t>(Dp + H + 2 * C + 2 * P + 2 * M) * 4; }
+};
+static RefineLds refine_lds(int M, int S)
+{
+    RefineLds l{};
+    l.C = (S * S + 3) / 4 * 4;
+    l.P = 1;
+    while (l.P < S * S) l.P <<= 1;
+    l.H = 256;
+    while (l.H < 2 * (M + S * S)) l.H <<= 1;
+    return l;
+}
 
 __device__ __forceinline__ bool rkey_less(float da, int32_t ia, float db, int32_t ib)
 {
     return da < db || (da == db && ia < ib);
 }
 
+// One block per point.  Block b takes position q = (b % 8) * per_xcd + b / 8
+// of the processing order (per_xcd = ceil(N / 8)): the workgroups of a
+// launch go round-robin to the 8 XCDs, so each XCD walks its own contiguous
+// eighth of the order and its L2 keeps the rows of the buckets it is on.
+// The order is the last bucketing's member list when there is one (a
+// point's 2-hop candidates sit mostly in its own bucket), else the ids.
+// The output of a point does not depend on the order.
+template <int G>
 __global__ void __launch_bounds__(256) refine_2hop_kernel(const float* __restrict__ X, const float* __restrict__ norms,
                                                           int64_t N, int Dp, int metric,
+                                                          const int32_t* __restrict__ order,
                                                           const int32_t* __restrict__ in_ids,
-                                                          const float* __restrict__ in_d, int M, int S,
-                                                          int32_t* __restrict__ out_ids, float* __restrict__ out_d)
+                                                          const float* __restrict__ in_d, int M, int S, int H,
+                                                          int C, int P, int32_t* __restrict__ out_ids,
+                                                          float* __restrict__ out_d)
 {
-    __shared__ int32_t hkey[kRefineHash];
-    __shared__ int32_t cid[kRefineMaxCand];
-    __shared__ float cd[kRefineMaxCand];
-    __shared__ int32_t row[kRefineMaxM];
-    __shared__ float rowd[kRefineMaxM];
-    __shared__ float xa[kMaxDp];
+    extern __shared__ __align__(16) float lds[];
+    float* xa = lds;                                               // Dp (a multiple of 4)
+    int32_t* hkey = reinterpret_cast<int32_t*>(xa + Dp);           // H
+    int32_t* cid = hkey + H;                                       // C
+    float* cd = reinterpret_cast<float*>(cid + C);                 // C
+    int32_t* sid = reinterpret_cast<int32_t*>(cd + C);             // P
+    float* sdd = reinterpret_cast<float*>(sid + P);                // P
+    int32_t* row = reinterpret_cast<int32_t*>(sdd + P);            // M
+    float* rowd = reinterpret_cast<float*>(row + M);               // M
     __shared__ int s_nc, s_ns, s_nr;
-    const int64_t a = blockIdx.x;
-    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
-    if (a >= N) return;
-    for (int s = tid; s < kRefineHash; s += 256) hkey[s] = -1;
+    const int64_t per_xcd = (N + 7) / 8;
+    const int64_t q = static_cast<int64_t>(blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+    const int tid = threadIdx.x;
+    if (q >= N) return;
+    const int64_t a = order ? order[q] : q;
+    for (int s = tid; s < H; s += 256) hkey[s] = -1;
     for (int k = tid; k < M; k += 256) {
         row[k] = in_ids[a * M + k];
         rowd[k] = in_d[a * M + k];
@@ -53,9 +90,10 @@ __global__ void __launch_bounds__(256) refine_2hop_kernel(const float* __restric
     __syncthreads();
     const float kth = rowd[M - 1];
     const float na = metric == 0 ? norms[a] : 0.f;
-    constexpr uint32_t mask = kRefineHash - 1;
+    const uint32_t mask = static_cast<uint32_t>(H - 1);
+    const int hshift = 33 - __ffs(H);   // the top log2(H) bits of the product
     auto insert = [&](int32_t v) -> bool {   // true if v was not present
-        uint32_t h = (static_cast<uint32_t>(v) * 2654435761u) & mask;
+        uint32_t h = (static_cast<uint32_t>(v) * 2654435761u) >> hshift;
         while (true) {
             const int32_t old = atomicCAS(&hkey[h], -1, v);
             if (old == -1) return true;
@@ -82,19 +120,58 @@ __global__ void __launch_bounds__(256) refine_2hop_kernel(const float* __restric
     }
     __syncthreads();
     const int nc = s_nc;
-    // exact distance of every candidate: one wave per candidate, lanes over dims
-    for (int k = w; k < nc; k += 4) {
-        const int32_t v = cid[k];
-        float dot = 0.f;
-        for (int d = lane; d < Dp; d += 64) dot = fmaf(xa[d], X[static_cast<int64_t>(v) * Dp + d], dot);
+    // exact distance of every candidate: a group of G lanes per candidate
+    // (256 / G candidates in flight per block), lane l of the group reading
+    // 16-byte pieces l, l + G, ... of the candidate's row, the point's row
+    // broadcast from LDS.  Four partial sums over the dims 4i + c of a lane,
+    // (s0 + s1) + (s2 + s3), then a butterfly over the group's lanes.  G = 2
+    // for rows of up to 256 floats, 4 beyond (measured on 96- and 960-float
+    // rows: one lane per row leaves too few requests per row in flight for
+    // long rows, 8 or more lanes too few rows).
+    {
+        const int g = tid / G, gl = tid % G;
+        const int F = Dp / 4;
+        const float4* xq = reinterpret_cast<const float4*>(xa);
+        for (int k0 = 0; k0 < nc; k0 += 256 / G) {
+            const int k = k0 + g;
+            float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+            if (k < nc) {
+                const float4* xv = reinterpret_cast<const float4*>(X + static_cast<int64_t>(cid[k]) * Dp);
+                int f = gl;
+                // 8 loads in flight before the first use
+                for (; f + 7 * G < F; f += 8 * G) {
+                    float4 pv[8];
 #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) dot += __shfl_xor(dot, o);
-        if (lane == 0) cd[k] = metric == 0 ? fmaf(-2.f, dot, norms[v] + na) : -dot;
+                    for (int u = 0; u < 8; ++u) pv[u] = xv[f + u * G];
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) {
+                        const float4 qv = xq[f + u * G];
+                        s0 = fmaf(qv.x, pv[u].x, s0);
+                        s1 = fmaf(qv.y, pv[u].y, s1);
+                        s2 = fmaf(qv.z, pv[u].z, s2);
+                        s3 = fmaf(qv.w, pv[u].w, s3);
+                    }
+                }
+                for (; f < F; f += G) {
+                    const float4 pv = xv[f];
+                    const float4 qv = xq[f];
+                    s0 = fmaf(qv.x, pv.x, s0);
+                    s1 = fmaf(qv.y, pv.y, s1);
+                    s2 = fmaf(qv.z, pv.z, s2);
+                    s3 = fmaf(qv.w, pv.w, s3);
+                }
+            }
+            float dot = (s0 + s1) + (s2 + s3);
+#pragma unroll
+            for (int o = G / 2; o > 0; o >>= 1) dot += __shfl_xor(dot, o);
+            if (k < nc && gl == 0) {
+                const int32_t v = cid[k];
+                cd[k] = metric == 0 ? fmaf(-2.f, dot, norms[v] + na) : -dot;
+            }
+        }
     }
     __syncthreads();
-    // keep d < kth, compact in place (order fixed later by sorting)
-    __shared__ int32_t sid[kRefineMaxCand];
-    __shared__ float sdd[kRefineMaxCand];
+    // keep d < kth (order fixed later by sorting)
     for (int k = tid; k < nc; k += 256) {
         if (cd[k] < kth) {
             const int slot = atomicAdd(&s_ns, 1);
@@ -150,13 +227,13 @@ __global__ void __launch_bounds__(256) refine_2hop_kernel(const float* __restric
 }
 
 // Lloyd update: centroid c = mean of its member rows; empty buckets keep
-// their centroid.  One block per centroid.  Dp <= 256 and a multiple of 4:
-// thread t sums float4 column t % F (F = Dp / 4) over its group t / F of
-// members (members g, g + G, g + 2G, ... for G = 256 / F groups) with four
-// accumulators (members 4k + u of the group into accumulator u), folded as
-// (a0 + a1) + (a2 + a3), and the groups are added in order.  Other Dp:
-// thread t sums dimensions t, t + 256, ... over all members in order.  The
-// result does not depend on scheduling.
+// their centroid.  Block (c, h) sums float4 columns [64h, 64h + F) of
+// centroid c (F = min(64, Dp / 4 - 64h): up to 256 dimensions per block, so
+// long rows spread over several blocks): thread t sums column t % F over its
+// group t / F of members (members g, g + G, g + 2G, ... for G = 256 / F
+// groups) with four accumulators (members 4k + u of the group into
+// accumulator u), folded as (a0 + a1) + (a2 + a3), and the groups are added
+// in order.  The result does not depend on scheduling.
 __global__ void __launch_bounds__(256) centroid_means_kernel(const float* __restrict__ X, int Dp,
                                                              const int32_t* __restrict__ members,
                                                              const int64_t* __restrict__ off, int64_t C,
@@ -167,17 +244,10 @@ __global__ void __launch_bounds__(256) centroid_means_kernel(const float* __rest
     if (c >= C) return;
     const int64_t lo = off[c], hi = off[c + 1];
     if (hi <= lo) return;
-    if (Dp > 256 || Dp % 4 != 0) {
-        for (int d = threadIdx.x; d < Dp; d += 256) {
-            float t = 0.f;
-            for (int64_t i = lo; i < hi; ++i) t += X[static_cast<int64_t>(members[i]) * Dp + d];
-            cent[c * Dp + d] = t / static_cast<float>(hi - lo);
-        }
-        return;
-    }
-    const int F = Dp / 4, G = 256 / F;
+    const int FD = Dp / 4, c0 = static_cast<int>(blockIdx.y) * 64;
+    const int F = min(64, FD - c0), G = 256 / F;
     const int col = threadIdx.x % F, g = threadIdx.x / F;
-    const float4* X4 = reinterpret_cast<const float4*>(X);
+    const float4* X4 = reinterpret_cast<const float4*>(X) + c0 + col;
     float4 a[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) a[u] = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -186,14 +256,14 @@ __global__ void __launch_bounds__(256) centroid_means_kernel(const float* __rest
         for (; i + 3 * G < hi; i += 4 * G) {
             float4 x[4];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) x[u] = X4[static_cast<int64_t>(members[i + u * G]) * F + col];
+            for (int u = 0; u < 4; ++u) x[u] = X4[static_cast<int64_t>(members[i + u * G]) * FD];
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
                 a[u].x += x[u].x; a[u].y += x[u].y; a[u].z += x[u].z; a[u].w += x[u].w;
             }
         }
         for (int u = 0; i < hi; i += G, ++u) {
-            const float4 x = X4[static_cast<int64_t>(members[i]) * F + col];
+            const float4 x = X4[static_cast<int64_t>(members[i]) * FD];
             a[u].x += x.x; a[u].y += x.y; a[u].z += x.z; a[u].w += x.w;
         }
     }
@@ -207,7 +277,7 @@ __global__ void __launch_bounds__(256) centroid_means_kernel(const float* __rest
             t.x += v.x; t.y += v.y; t.z += v.z; t.w += v.w;
         }
         const float n = static_cast<float>(hi - lo);
-        reinterpret_cast<float4*>(cent + c * Dp)[threadIdx.x] = make_float4(t.x / n, t.y / n, t.z / n, t.w / n);
+        reinterpret_cast<float4*>(cent + c * Dp)[c0 + threadIdx.x] = make_float4(t.x / n, t.y / n, t.z / n, t.w / n);
     }
 }
 
@@ -273,13 +343,19 @@ __global__ void csr_offsets_kernel(const uint32_t* __restrict__ offs, int C, int
     if (c <= C) off[c] = offs[static_cast<int64_t>(c) * nblk];
 }
 
-void launch_refine_2hop(const float* X, const float* norms, int64_t N, int Dp, int metric, const int32_t* in_ids,
-                        const float* in_d, int M, int S, int32_t* out_ids, float* out_d, hipStream_t s)
+void launch_refine_2hop(const float* X, const float* norms, int64_t N, int Dp, int metric, const int32_t* order,
+                        const int32_t* in_ids, const float* in_d, int M, int S, int32_t* out_ids, float* out_d,
+                        hipStream_t s)
 {
-    GT_REQUIRE(M <= kRefineMaxM && S * S <= kRefineMaxCand && Dp <= kMaxDp, "refine limits: M <= 128, S*S <= 1024");
+    GT_REQUIRE(M <= kRefineMaxM && S * S <= kRefineMaxCand && Dp <= kMaxDp && Dp % 4 == 0,
+               "refine limits: M <= 128, S*S <= 1024");
     if (N <= 0) return;
-    hipLaunchKernelGGL(refine_2hop_kernel, dim3(static_cast<unsigned>(N)), dim3(256), 0, s, X, norms, N, Dp, metric,
-                       in_ids, in_d, M, S, out_ids, out_d);
+    const dim3 grid(static_cast<unsigned>(8 * ((N + 7) / 8)));
+    const int G = Dp <= 256 ? 2 : 4;
+    auto k = G == 2 ? refine_2hop_kernel<2> : refine_2hop_kernel<4>;
+    const RefineLds l = refine_lds(M, S);
+    hipLaunchKernelGGL(k, grid, dim3(256), l.bytes(Dp, M), s, X, norms, N, Dp, metric, order, in_ids, in_d, M, S, l.H, l.C, l.P,
+                       out_ids, out_d);
     GT_HIP(hipGetLastError());
 }
 
@@ -302,8 +378,10 @@ void launch_centroid_sums(const float* X, int Dp, const int32_t* members, const 
                           float* centroids, hipStream_t s)
 {
     if (C <= 0) return;
-    hipLaunchKernelGGL(centroid_means_kernel, dim3(static_cast<unsigned>(C)), dim3(256), 0, s, X, Dp, members,
-                       offsets, C, centroids);
+    GT_REQUIRE(Dp % 4 == 0, "centroid means: padded rows are multiples of 4 floats");
+    const unsigned chunks = static_cast<unsigned>((Dp / 4 + 63) / 64);
+    hipLaunchKernelGGL(centroid_means_kernel, dim3(static_cast<unsigned>(C), chunks), dim3(256), 0, s, X, Dp,
+                       members, offsets, C, centroids);
     GT_HIP(hipGetLastError());
 }
 
