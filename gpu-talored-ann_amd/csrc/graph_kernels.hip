@@ -302,8 +302,21 @@ __global__ void __launch_bounds__(256) cagra_prune_kernel(const int32_t* __restr
     __shared__ uint32_t tag[4][TAGW];         // slot s: bits 8*(s%4).. of word s/4
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int64_t a0 = ROWS == 0 ? 0 : map.a0;
-    const int64_t a = a0 + static_cast<int64_t>(blockIdx.x) * 4 + w;
-    if (a >= (ROWS == 0 ? N : map.a0 + map.n)) return;
+    int64_t a;
+    if (ROWS == 0) {
+        // block b takes positions 4 (x * per_xcd + b / 8) .. + 3 of the
+        // order, x = b % 8 (per_xcd = gridDim.x / 8): the workgroups go
+        // round-robin to the 8 XCDs, so each XCD walks its own contiguous
+        // eighth of the order, and with the bucket order its L2 keeps the
+        // neighbour rows of the bucket it is on
+        const int64_t per_xcd = gridDim.x / 8;
+        const int64_t q = (static_cast<int64_t>(blockIdx.x % 8) * per_xcd + blockIdx.x / 8) * 4 + w;
+        if (q >= N) return;
+        a = map.order ? map.order[q] : q;
+    } else {
+        a = a0 + static_cast<int64_t>(blockIdx.x) * 4 + w;
+        if (a >= map.a0 + map.n) return;
+    }
     int64_t arow = a;
     int pa = 0;
     if (ROWS == 1) arow = map.cidx[a];
@@ -1466,17 +1479,17 @@ void launch_sanitize(const int32_t* in, int64_t N, int M, uint32_t* out, hipStre
 }
 
 void launch_cagra_prune(const int32_t* G, int64_t N, int M, int K, uint32_t* out, unsigned long long* bad_row,
-                        hipStream_t s)
+                        hipStream_t s, const int32_t* order)
 {
     GT_REQUIRE(M >= 1 && M <= kPruneMaxM, "prune supports intermediate degree <= 128");
     if (N <= 0) return;
-    const PruneMap none{};
+    PruneMap m{};
+    m.order = order;
+    const dim3 grid(static_cast<unsigned>(8 * ceil_div(ceil_div(N, int64_t(4)), int64_t(8))));
     if (M <= 64)
-        hipLaunchKernelGGL((cagra_prune_kernel<1, 0>), dim3(grid_for(N, 4)), dim3(256), 0, s, G, N, M, K, out, bad_row,
-                           none);
+        hipLaunchKernelGGL((cagra_prune_kernel<1, 0>), grid, dim3(256), 0, s, G, N, M, K, out, bad_row, m);
     else
-        hipLaunchKernelGGL((cagra_prune_kernel<2, 0>), dim3(grid_for(N, 4)), dim3(256), 0, s, G, N, M, K, out, bad_row,
-                           none);
+        hipLaunchKernelGGL((cagra_prune_kernel<2, 0>), grid, dim3(256), 0, s, G, N, M, K, out, bad_row, m);
     GT_HIP(hipGetLastError());
 }
 

@@ -58,7 +58,7 @@ size_t search_lds_bytes(int CC, int efr, int Dp, int H);
 void launch_sanitize(const int32_t* in, int64_t N, int M, uint32_t* out, hipStream_t s);
 void launch_init_flags(unsigned long long* bad_row, int* err, hipStream_t s);
 void launch_cagra_prune(const int32_t* G, int64_t N, int M, int K, uint32_t* out, unsigned long long* bad_row,
-                        hipStream_t s);
+                        hipStream_t s, const int32_t* order = nullptr);
 void launch_rev_count(const uint32_t* fwd, int64_t N, int K, uint32_t* deg, uint32_t* slot, int* err, hipStream_t s);
 void launch_exclusive_scan(const uint32_t* in, int64_t n, uint32_t* out, uint32_t* sums, hipStream_t s);
 void launch_rev_scatter(const uint32_t* fwd, int64_t N, int K, const uint32_t* off, const uint32_t* slot,
@@ -1340,11 +1340,14 @@ static StageFlags stage_flags(Ctx& c)
     return f;
 }
 
-static void prune_enqueue(Ctx& c, const StageFlags& f, const int32_t* G, int64_t N, int M, int K, uint32_t* out)
+// order: a permutation of the rows to process them in (rows that share
+// neighbours close together keep those rows in L2), or null
+static void prune_enqueue(Ctx& c, const StageFlags& f, const int32_t* G, int64_t N, int M, int K, uint32_t* out,
+                          const int32_t* order = nullptr)
 {
     GT_REQUIRE(K >= 1 && K <= M, "output degree must be in [1, M]");
     launch_init_flags(f.bad, f.err, c.s);
-    launch_cagra_prune(G, N, M, K, out, f.bad, c.s);
+    launch_cagra_prune(G, N, M, K, out, f.bad, c.s, order);
 }
 
 static void prune_check(Ctx& c, const StageFlags& f)
@@ -3033,13 +3036,14 @@ int gt_build_graph_ex(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtyp
             if (stats) *stats = st;
             return;
         }
+        // refinement and the prune take the points in the last bucketing's
+        // member order (W_MEMBERS holds it after a bucketed round): the rows
+        // they gather (2-hop candidates, neighbour lists) sit mostly in the
+        // point's own bucket, so they stay in L2
+        const int32_t* order = c.c->members_gen != 0 ? c.ws<int32_t>(W_MEMBERS, static_cast<size_t>(N)) : nullptr;
         if (p.refine_passes > 0) {
             GT_REQUIRE(p.refine_sample >= 1 && p.refine_sample <= p.M && p.refine_sample * p.refine_sample <= 1024,
                        "bad refine sample");
-            // points in the last bucketing's member order (W_MEMBERS holds it
-            // after a bucketed round): a bucket's 2-hop candidates stay in L2
-            const int32_t* order =
-                c.c->members_gen != 0 ? c.ws<int32_t>(W_MEMBERS, static_cast<size_t>(N)) : nullptr;
             for (int pass = 0; pass < p.refine_passes; ++pass) {
                 st.t_refine += c.timed([&] {
                     launch_refine_2hop(Xm.data, Xm.norms, N, Xm.Dp, p.metric, order, run_i, run_d, p.M,
@@ -3061,7 +3065,7 @@ int gt_build_graph_ex(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtyp
             const StageFlags fl = stage_flags(c);
             st.t_prune = c.timed([&] {
                 launch_sanitize(run_i, N, p.M, san, c.s);
-                prune_enqueue(c, fl, reinterpret_cast<const int32_t*>(san), N, p.M, p.K, fwd);
+                prune_enqueue(c, fl, reinterpret_cast<const int32_t*>(san), N, p.M, p.K, fwd, order);
             });
             prune_check(c, fl);
             st.t_revmerge = c.timed([&] { reverse_merge_enqueue(c, fl, fwd, N, p.K, fin); });

@@ -113,6 +113,7 @@ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // Where the rows of a chunked prune live (cagra_prune_kernel, ROWS 1 and 2).
 struct PruneMap {
+    const int32_t* order;     // ROWS 0: processing order (a permutation of the rows) or null
     int64_t a0, n;            // rows pruned: a0 .. a0 + n - 1, output rows 0 .. n - 1
     const int32_t* cidx;      // ROWS 1: compact row of every id the chunk reads
     const uint32_t* off;      // ROWS 2: n_buckets + 1 row starts, by processing position
