@@ -256,9 +256,17 @@ constexpr int kPruneDepth = 8;    // neighbour rows in flight per wave
 // the neighbour row's id is read from row a's registers by readlane, so its
 // address is scalar work.  Finally the first K valid ranks by (count, rank)
 // are written (src/prune_windowed_core.hpp:234-263).  E = list halves of 64.
+// Home bucket of an id: a multiplicative hash on the id's low 24 bits
+// (v_mul_u32_u24 issues at full rate, a 32-bit multiply at a quarter); ids
+// that differ only above bit 23 share a home and spill, which costs probes,
+// not results.
 __device__ __forceinline__ uint32_t prune_hash(int32_t v, uint32_t mask)
 {
-    return ((static_cast<uint32_t>(v) * 0x9E3779B1u) >> 15) & mask;
+    uint32_t p;
+    // (the compiler would fold the 24-bit mask into the bit range it keeps
+    // and pick the quarter-rate 32-bit multiply)
+    asm("v_mul_u32_u24 %0, 0x9e3779, %1" : "=v"(p) : "v"(v));
+    return (p >> 15) & mask;
 }
 
 // Last processing position p with off[p] <= id (positions 0 .. nb - 1).
@@ -325,6 +333,8 @@ __global__ void __launch_bounds__(256) cagra_prune_kernel(const int32_t* __restr
         arow = map.cbase[pa] + (a - map.off[pa]);
     }
 
+    // ids below nlim are rows of G (ROWS 0)
+    const uint32_t nlim = static_cast<uint32_t>(min(N, static_cast<int64_t>(0x80000000u)));
     for (int s = lane; s < SLOTS; s += 64) tab[w][s] = kEmpty;
     for (int s = lane; s < TAGW; s += 64) tag[w][s] = 0u;
     int32_t A[E];
@@ -378,12 +388,13 @@ __global__ void __launch_bounds__(256) cagra_prune_kernel(const int32_t* __restr
     bool rok[kPruneDepth];
     auto fetch = [&](int kAD, int32_t (&b)[E], bool& ok) {
         int64_t d = -1;
+        uint32_t du = 0xFFFFFFFFu;   // ROWS 0: the id (negative ids fail du < nlim)
         if (kAD < M - 1) {
 #pragma unroll
             for (int e = 0; e < E; ++e)
                 if ((kAD >> 6) == e) {
                     if (ROWS == 0) {
-                        d = __builtin_amdgcn_readlane(A[e], kAD & 63);
+                        du = __builtin_amdgcn_readlane(static_cast<uint32_t>(A[e]), kAD & 63);
                     } else {
                         const uint32_t lo = __builtin_amdgcn_readlane(static_cast<uint32_t>(nrow[e]), kAD & 63);
                         const int32_t hi = __builtin_amdgcn_readlane(static_cast<int32_t>(nrow[e] >> 32), kAD & 63);
@@ -391,28 +402,30 @@ __global__ void __launch_bounds__(256) cagra_prune_kernel(const int32_t* __restr
                     }
                 }
         }
-        ok = ROWS == 0 ? d >= 0 && d < N : d >= 0;
-        const int32_t* row = G + (ok ? d : int64_t(0)) * M;
+        if (ROWS == 0) {
+            // the id as a 32-bit scalar: the bounds test and the row address
+            // stay on the scalar unit
+            ok = du < nlim;
+            const int32_t* row = G + static_cast<int64_t>(ok ? du : 0u) * M;
 #pragma unroll
-        for (int e = 0; e < E; ++e) b[e] = row[col[e]];
+            for (int e = 0; e < E; ++e) b[e] = row[col[e]];
+        } else {
+            ok = d >= 0;
+            const int32_t* row = G + (ok ? d : int64_t(0)) * M;
+#pragma unroll
+            for (int e = 0; e < E; ++e) b[e] = row[col[e]];
+        }
     };
     uint32_t c[E];
 #pragma unroll
     for (int e = 0; e < E; ++e) c[e] = 0;
-    // bit `bit` of the tag of every slot of bucket x (at base) holding v
+    // bit `bit` of the tag of every slot of bucket x (at base) holding v (an
+    // id repeated in row a has a slot per copy, all tagged); bit is a
+    // constant of the unrolled row loop, so the word is four selects
     auto tag_bucket = [&](const uint4& x, uint32_t v, bool valid, uint32_t base, uint32_t bit) {
-        const bool m0 = valid & (x.x == v), m1 = valid & (x.y == v), m2 = valid & (x.z == v),
-                   m3 = valid & (x.w == v);
-        const uint32_t j = m0 ? 0u : m1 ? 1u : m2 ? 2u : 3u;
-        uint32_t* tw = &tag[w][base / 4];
-        if (m0 | m1 | m2 | m3) atomicOr(tw, bit << (8 * j));
-        // an id of row a repeated inside one bucket: tag the other copies
-        const bool more = (m0 & (m1 | m2 | m3)) | (m1 & (m2 | m3)) | (m2 & m3);
-        if (__ballot(more)) {
-            const uint32_t rest = ((m1 && j < 1) ? bit << 8 : 0u) | ((m2 && j < 2) ? bit << 16 : 0u) |
-                                  ((m3 && j < 3) ? bit << 24 : 0u);
-            if (rest) atomicOr(tw, rest);
-        }
+        const uint32_t t = (x.x == v ? bit : 0u) | (x.y == v ? bit << 8 : 0u) | (x.z == v ? bit << 16 : 0u) |
+                           (x.w == v ? bit << 24 : 0u);
+        if (valid && t != 0u) atomicOr(&tag[w][base / 4], t);
     };
     // rows kd0 .. kd0 + kPruneDepth - 1 of the ring (row kd0 + r in slot r);
     // each slot is refilled with row kd0 + r + kPruneDepth once probed

@@ -435,47 +435,92 @@ knn_i8_collect_kernel(KnnArgs a)
 // ------------------------------------------------------------ selection
 
 // Each row's top-M of its cnt[row] candidate keys, ascending, into (out_ids,
-// out_d) (padding -1 / +inf).  Two lanes per row, 128 rows per block.
+// out_d) (padding -1 / +inf).  Two lanes per row, 128 rows per block; lane
+// (j, h) of a wave keeps positions LM h .. LM h + LM - 1 of row j's list.
+// Keys and results move through a per-wave LDS stage so that every global
+// access is whole rows: each of a wave's 8 loads per step brings 32 keys of
+// 4 rows (16 lanes x 16 bytes per row; a lane skips keys past its row's
+// count), and the wave's 32 output rows, contiguous in out_ids and out_d,
+// leave as 16-byte stores.  Staged rows are 34 keys (results: M + 4 words)
+// apart, so that the 16 lanes of an LDS pass hit distinct banks.  (Loading
+// the stage by LDS DMA, the next step's keys in flight during the merge,
+// measured slower: the merges are VALU-bound and the DMA version fits two
+// waves per SIMD instead of three.)
+constexpr int kSelStride = 2 * 16 + 2;   // keys per staged row
+
 template <int LM>
-__global__ void __launch_bounds__(256) knn_select_kernel(const uint64_t* __restrict__ cand,
+__global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(3))) knn_select_kernel(const uint64_t* __restrict__ cand,
                                                          const int32_t* __restrict__ cnt, int64_t rows, int M,
                                                          int32_t* __restrict__ out_ids, float* __restrict__ out_d)
 {
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, h = lane >> 5;
-    const int64_t row = (static_cast<int64_t>(blockIdx.x) * kWaves + w) * kQueriesPerWave + (lane & 31);
-    const bool valid = row < rows;
-    const int n = valid ? min(cnt[row], kCollectCap) : 0;
+    __shared__ __align__(16) uint64_t stage[kWaves][kQueriesPerWave * kSelStride];
+    __shared__ int scnt[kWaves][kQueriesPerWave];
+    const int lane = threadIdx.x & 63, h = lane >> 5, j = lane & 31;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * kWaves + w) * kQueriesPerWave;
+    if (row0 >= rows) return;   // wave-uniform
+    const int nrows = static_cast<int>(min(static_cast<int64_t>(kQueriesPerWave), rows - row0));
+    const bool valid = j < nrows;
+    const int n = valid ? min(cnt[row0 + j], kCollectCap) : 0;
+    uint64_t* st = stage[w];
+    if (h == 0) scnt[w][j] = n;
+    wave_sync();
     PairList<LM> PL;
 #pragma unroll
     for (int i = 0; i < LM; ++i) PL.k[i] = kNoKey;
-    const uint64_t* src = cand + (valid ? row : 0) * kCollectCap + 16 * h;
+    const int q = lane & 15, rq = lane >> 4;
     for (int c0 = 0; __ballot(c0 < n); c0 += 32) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const int r = 4 * t + rq;
+            if (r < nrows && c0 + 2 * q < scnt[w][r])
+                *reinterpret_cast<uint4*>(st + r * kSelStride + 2 * q) =
+                    *reinterpret_cast<const uint4*>(cand + (row0 + r) * kCollectCap + c0 + 2 * q);
+        }
+        wave_sync();
         uint64_t b[16];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
+            const uint4 x = *reinterpret_cast<const uint4*>(st + j * kSelStride + 16 * h + 2 * e);
             const int i = c0 + 16 * h + 2 * e;
-            if (i + 1 < n) {
-                const uint4 x = *reinterpret_cast<const uint4*>(src + c0 + 2 * e);
-                b[2 * e] = (static_cast<uint64_t>(x.y) << 32) | x.x;
-                b[2 * e + 1] = (static_cast<uint64_t>(x.w) << 32) | x.z;
-            } else {
-                b[2 * e] = i < n ? src[c0 + 2 * e] : kNoKey;
-                b[2 * e + 1] = kNoKey;
-            }
+            b[2 * e] = i < n ? (static_cast<uint64_t>(x.y) << 32) | x.x : kNoKey;
+            b[2 * e + 1] = i + 1 < n ? (static_cast<uint64_t>(x.w) << 32) | x.z : kNoKey;
         }
+        wave_sync();
         pair_merge32<LM>(b, PL, h != 0);
     }
-    if (!valid) return;
-    int32_t* oi = out_ids + row * M;
-    float* od = out_d + row * M;
+    // ids, then distances, through the stage (row stride Ms words)
+    uint32_t* so = reinterpret_cast<uint32_t*>(st);
+    const int Ms = (M + 3) / 4 * 4 + 4;
+    const int total = nrows * M;
+    for (int pass = 0; pass < 2; ++pass) {
+        if (valid) {
 #pragma unroll
-    for (int i = 0; i < LM; ++i) {
-        const int p = LM * h + i;
-        if (p < M) {
-            const uint64_t k = PL.k[i];
-            oi[p] = k == kNoKey ? -1 : static_cast<int32_t>(static_cast<uint32_t>(k));
-            od[p] = k == kNoKey ? INFINITY : o2f(static_cast<uint32_t>(k >> 32));
+            for (int i = 0; i < LM; ++i) {
+                const int p = LM * h + i;
+                if (p < M) {
+                    const uint64_t k = PL.k[i];
+                    so[j * Ms + p] = pass == 0 ? (k == kNoKey ? 0xFFFFFFFFu : static_cast<uint32_t>(k))
+                                               : __float_as_uint(k == kNoKey ? INFINITY
+                                                                             : o2f(static_cast<uint32_t>(k >> 32)));
+                }
+            }
         }
+        wave_sync();
+        uint32_t* dst = pass == 0 ? reinterpret_cast<uint32_t*>(out_ids + row0 * M)
+                                  : reinterpret_cast<uint32_t*>(out_d + row0 * M);
+        if (M % 4 == 0) {
+            for (int v = 4 * lane; v < total; v += 256) {
+                const int r = v / M, p = v - r * M;
+                *reinterpret_cast<uint4*>(dst + v) = *reinterpret_cast<const uint4*>(so + r * Ms + p);
+            }
+        } else {
+            for (int v = lane; v < total; v += 64) {
+                const int r = v / M;
+                dst[v] = so[r * Ms + (v - r * M)];
+            }
+        }
+        wave_sync();   // read out before the distances overwrite it
     }
 }
 

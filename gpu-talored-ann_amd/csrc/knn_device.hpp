@@ -76,7 +76,8 @@ __device__ __forceinline__ int wave_incl_scan(int x)
 // the layers that pair a lane with its partner exchange registers through
 // partner64.
 
-// the value of x held by lane l ^ 32
+// the value of x held by lane l ^ 32 (ds_bpermute: the exchange runs on the
+// LDS unit; v_permlane32_swap + a select made the VALU-bound merges slower)
 __device__ __forceinline__ uint32_t partner32(uint32_t x)
 {
     return static_cast<uint32_t>(__shfl_xor(static_cast<int>(x), 32));
