@@ -1028,7 +1028,9 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
     // is the query of exactly one work item, so rows = N)
     const bool collect = knn_collect_supported(a);
     if (collect) {
-        a.cand = c.ws<uint64_t>(W_CAND, static_cast<size_t>(rows) * kCollectCap);
+        // (+ one wave's rows of slack: the selection reads whole groups of
+        // 32 rows and masks the rows past the last)
+        a.cand = c.ws<uint64_t>(W_CAND, static_cast<size_t>(rows + kQueriesPerWave) * kCollectCap);
         a.cand_cnt = c.ws<int32_t>(W_CANDCNT, static_cast<size_t>(rows));
         const char* se = std::getenv("GTANN_KNN_STATS");
         if (tr.on && se && se[0] == '1') {   // counters of the collect launch (slow), printed below

@@ -439,9 +439,10 @@ knn_i8_collect_kernel(KnnArgs a)
 // (j, h) of a wave keeps positions LM h .. LM h + LM - 1 of row j's list.
 // Keys and results move through a per-wave LDS stage so that every global
 // access is whole rows: each of a wave's 8 loads per step brings 32 keys of
-// 4 rows (16 lanes x 16 bytes per row; a lane skips keys past its row's
-// count), and the wave's 32 output rows, contiguous in out_ids and out_d,
-// leave as 16-byte stores.  Staged rows are 34 keys (results: M + 4 words)
+// 4 rows (16 lanes x 16 bytes per row), all 8 issued before the stage is
+// written, and the wave's 32 output rows, contiguous in out_ids and out_d,
+// leave as 16-byte stores.  `cand` must hold kQueriesPerWave rows of slack
+// past the last row.  Staged rows are 34 keys (results: M + 4 words)
 // apart, so that the 16 lanes of an LDS pass hit distinct banks.  (Loading
 // the stage by LDS DMA, the next step's keys in flight during the merge,
 // measured slower: the merges are VALU-bound and the DMA version fits two
@@ -454,7 +455,6 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_wav
                                                          int32_t* __restrict__ out_ids, float* __restrict__ out_d)
 {
     __shared__ __align__(16) uint64_t stage[kWaves][kQueriesPerWave * kSelStride];
-    __shared__ int scnt[kWaves][kQueriesPerWave];
     const int lane = threadIdx.x & 63, h = lane >> 5, j = lane & 31;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * kWaves + w) * kQueriesPerWave;
@@ -463,22 +463,24 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_wav
     const bool valid = j < nrows;
     const int n = valid ? min(cnt[row0 + j], kCollectCap) : 0;
     uint64_t* st = stage[w];
-    if (h == 0) scnt[w][j] = n;
-    wave_sync();
     PairList<LM> PL;
 #pragma unroll
     for (int i = 0; i < LM; ++i) PL.k[i] = kNoKey;
     const int q = lane & 15, rq = lane >> 4;
-    for (int c0 = 0; __ballot(c0 < n); c0 += 32) {
+    // keys c0 .. c0 + 31 of every row of the wave into b (16 per lane)
+    auto step = [&](int c0, uint64_t (&b)[16]) __attribute__((always_inline)) {
+        // all 8 loads in flight before the stage is written: every lane loads
+        // its 16 bytes of rows rq, rq + 4, ... whatever the rows' counts (the
+        // keys past a count and the rows past the last are masked below; the
+        // buffer holds a wave's rows of slack past the last row)
+        const uint64_t* src = cand + (row0 + rq) * kCollectCap + c0 + 2 * q;
+        uint4 x[8];
 #pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            const int r = 4 * t + rq;
-            if (r < nrows && c0 + 2 * q < scnt[w][r])
-                *reinterpret_cast<uint4*>(st + r * kSelStride + 2 * q) =
-                    *reinterpret_cast<const uint4*>(cand + (row0 + r) * kCollectCap + c0 + 2 * q);
-        }
+        for (int t = 0; t < 8; ++t) x[t] = *reinterpret_cast<const uint4*>(src + 4 * t * kCollectCap);
+        uint64_t* dst = st + rq * kSelStride + 2 * q;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) *reinterpret_cast<uint4*>(dst + 4 * t * kSelStride) = x[t];
         wave_sync();
-        uint64_t b[16];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             const uint4 x = *reinterpret_cast<const uint4*>(st + j * kSelStride + 16 * h + 2 * e);
@@ -486,7 +488,16 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_wav
             b[2 * e] = i < n ? (static_cast<uint64_t>(x.y) << 32) | x.x : kNoKey;
             b[2 * e + 1] = i + 1 < n ? (static_cast<uint64_t>(x.w) << 32) | x.z : kNoKey;
         }
-        wave_sync();
+        wave_sync();   // the stage is read before the next step refills it
+    };
+    if (__ballot(n > 0)) {
+        uint64_t b[16];
+        step(0, b);
+        pair_first32<LM>(b, PL, h != 0);
+    }
+    for (int c0 = 32; __ballot(c0 < n); c0 += 32) {
+        uint64_t b[16];
+        step(c0, b);
         pair_merge32<LM>(b, PL, h != 0);
     }
     // ids, then distances, through the stage (row stride Ms words)
@@ -551,7 +562,8 @@ static void launch_collect_metric(const KnnArgs& a, dim3 grid, hipStream_t strea
 }
 
 // Every output row in [0, rows) must be the output row of exactly one query
-// of the launch (cand_cnt is read for all of them).
+// of the launch (cand_cnt is read for all of them); a.cand holds
+// (rows + kQueriesPerWave) * kCollectCap keys.
 void launch_knn_collect_select(const KnnArgs& a, int64_t rows, hipStream_t stream)
 {
     GT_REQUIRE(knn_collect_supported(a), "collect launch: int8 rows, 4 < M <= 64");

@@ -156,20 +156,12 @@ struct PairList {
     uint64_t k[LM];
 };
 
-// Merges 32 keys, 16 per lane in any order (kNoKey for empty slots), into
-// the pair's list, which keeps the 2 LM smallest keys of both, sorted.  The
-// 32 keys are sorted (16 per lane, then across the pair: an element-wise
-// min / max against the partner's keys reversed, then a bitonic merge within
-// each lane), laid against the list's tail in reverse (the element-wise
-// minimum of an ascending and a descending sequence is bitonic and holds the
-// 2 LM smallest keys of both), and the result is sorted by a bitonic merge
-// whose first layer pairs each lane with its partner.  Both lanes of every
-// pair must call it.
-template <int LM>
-__device__ __forceinline__ void pair_merge32(uint64_t (&b)[16], PairList<LM>& PL, bool hi)
+// Sorts 32 keys, 16 per lane in any order (kNoKey for empty slots), across
+// the lane pair: afterwards lane l holds ranks 0..15 ascending, lane l + 32
+// ranks 16..31 (16 per lane, then an element-wise min / max against the
+// partner's keys reversed and a bitonic merge within each lane).
+__device__ __forceinline__ void pair_sort32(uint64_t (&b)[16], bool hi)
 {
-    static_assert(LM == 16 || LM == 32, "lists of 32 or 64 keys per pair");
-    uint64_t (&L)[LM] = PL.k;
     oddeven_sort(b);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -179,6 +171,41 @@ __device__ __forceinline__ void pair_merge32(uint64_t (&b)[16], PairList<LM>& PL
         b[15 - i] = (lb != hi) ? pb : b[15 - i];
     }
     bitonic_merge(b);
+}
+
+// The first 32 keys of an empty list: the list becomes them, sorted.
+template <int LM>
+__device__ __forceinline__ void pair_first32(uint64_t (&b)[16], PairList<LM>& PL, bool hi)
+{
+    static_assert(LM == 16 || LM == 32, "lists of 32 or 64 keys per pair");
+    pair_sort32(b, hi);
+    if constexpr (LM == 32) {
+        // positions 0..31 in lane l: its ranks 0..15, then the partner's 16..31
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const uint64_t t = partner64(b[k]);
+            PL.k[k] = hi ? kNoKey : b[k];
+            PL.k[16 + k] = hi ? kNoKey : t;
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) PL.k[k] = b[k];
+    }
+}
+
+// Merges 32 keys, 16 per lane in any order (kNoKey for empty slots), into
+// the pair's list, which keeps the 2 LM smallest keys of both, sorted.  The
+// 32 keys are sorted (pair_sort32), laid against the list's tail in reverse
+// (the element-wise minimum of an ascending and a descending sequence is
+// bitonic and holds the 2 LM smallest keys of both), and the result is
+// sorted by a bitonic merge whose first layer pairs each lane with its
+// partner.  Both lanes of every pair must call it.
+template <int LM>
+__device__ __forceinline__ void pair_merge32(uint64_t (&b)[16], PairList<LM>& PL, bool hi)
+{
+    static_assert(LM == 16 || LM == 32, "lists of 32 or 64 keys per pair");
+    uint64_t (&L)[LM] = PL.k;
+    pair_sort32(b, hi);
     if constexpr (LM == 32) {
         // positions 32 + k take min(list, keys[31 - k]): the upper lane's
         // own keys reversed, then the lower lane's
