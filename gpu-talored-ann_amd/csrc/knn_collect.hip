@@ -1,6 +1,7 @@
-// knn_collect.hip -- per-bucket brute-force kNN on int8 rows as collect +
-// select, for lists of at most 64 keys (src/bucket.cu:4101-4265 top-M
-// semantics: self excluded, (-1, +inf) padding, ties by id).
+// knn_collect.hip -- per-bucket brute-force kNN as collect + select, for
+// lists of 5..64 keys on int8 rows (Dp <= 256) and on fp32 rows (Dp <= 160)
+// (src/bucket.cu:4101-4265 top-M semantics: self excluded, (-1, +inf)
+// padding, ties by id).
 //
 // knn_i8_collect_kernel scans a tile of 128 queries against a pool slice like
 // knn_i8_kernel (int8 MFMA, LDS pool tiles, integer pre-filter) but keeps no
@@ -432,6 +433,288 @@ knn_i8_collect_kernel(KnnArgs a)
     if (a.stats && qvalid && h == 0) atomicAdd(a.stats, static_cast<unsigned long long>(st.cnt));
 }
 
+// ------------------------------------------------------------ fp32 rows
+//
+// knn_f32_collect_kernel: the same collect scan on fp32 rows (float data,
+// Dp <= 160).  Its distances are the merging fp32 kernel's (knn_fused_kernel)
+// bit for bit -- the same v_mfma_f32_32x32x2_f32 chain per 32x32 tile
+// (accumulator from 0, dimensions in the same order, lane (j, h) holding
+// dims [h Dp/2, h Dp/2 + Dp/2) of query j) and the same key
+// fmaf(-2, dot, |p|^2 + |q|^2) (L2) or -dot (IP) -- so the selected lists
+// equal the merging kernel's.  One 32-row pool tile per step, double-buffered
+// in LDS as in knn_fused_kernel (a tile is Dp/2 MFMAs per wave, long enough
+// to hide the next tile's loads); rows past the slice end have norm +inf.
+
+template <int DP>
+struct CollectSmemF {
+    float tile[2][kPoolTile][DP + 4];   // +4 floats: rows land on distinct bank groups
+    float tnorm[3][kPoolTile];
+    int32_t trow[3][kPoolTile];
+    CollectWave wv[kWaves];
+};
+
+// The lane's 16 keys of a finished tile (pool row 8g + 4h + e in element
+// 4g + e; rows past the slice end +inf).
+template <int METRIC>
+__device__ __forceinline__ void f32_tile_keys(const floatx16& acc, const float* tn, int h, float qn, float (&d)[16])
+{
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const float4 pn = *reinterpret_cast<const float4*>(tn + 8 * g + 4 * h);
+        const float n4[4] = {pn.x, pn.y, pn.z, pn.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            d[4 * g + e] = METRIC == 0 ? fmaf(-2.f, acc[4 * g + e], n4[e] + qn) : fmaf(-1.f, acc[4 * g + e], n4[e]);
+    }
+}
+
+// collect_tile for fp32 keys: the stash holds the keys themselves; a code is
+// written for every key at or below the query's threshold, and the exact
+// (key, id) test and the append are made per code.
+template <int METRIC>
+__device__ __forceinline__ void collect_tile_f32(const KnnArgs& a, CollectWave& W, const floatx16& acc,
+                                                 const float* tn, const int32_t* tr, int lane, int h, bool qvalid,
+                                                 float qn, CollectState& st)
+{
+    float d[16];
+    f32_tile_keys<METRIC>(acc, tn, h, qn, d);
+    float dmin = d[0];
+#pragma unroll
+    for (int r = 1; r < 16; ++r) dmin = fminf(dmin, d[r]);
+    if (!__ballot(dmin <= st.thr)) return;
+    uint64_t need = __ballot(qvalid && st.cnt > kCollectCap - 2 * 16) & 0xffffffffull;
+    if (need) {
+        while (need) {
+            const int q = __ffsll(static_cast<unsigned long long>(need)) - 1;
+            need &= need - 1;
+            collect_compact(a, lane, q, st);
+        }
+        publish_state(W, lane, qvalid, qn, st);
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+        *reinterpret_cast<int4*>(&W.stash[stash_index(lane, 4 * c)]) =
+            make_int4(__float_as_int(d[4 * c]), __float_as_int(d[4 * c + 1]), __float_as_int(d[4 * c + 2]),
+                      __float_as_int(d[4 * c + 3]));
+    if (lane < kQueriesPerWave) W.qcnt[lane] = st.cnt;
+    int c = 0;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) c += d[r] <= st.thr ? 1 : 0;
+    const int incl = wave_incl_scan(c);
+    const int total = __builtin_amdgcn_readlane(incl, 63);
+    int pos = incl - c;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const bool p = d[r] <= st.thr;
+        W.code[p ? pos : kCodeSpare + lane] = static_cast<uint16_t>((lane << 4) | r);
+        pos += p ? 1 : 0;
+    }
+    wave_sync();
+    for (int k = lane; k - lane < total; k += 64) {
+        if (k < total) {
+            const int code = W.code[k];
+            const int src = code >> 4, r = code & 15;
+            const float dk = __int_as_float(W.stash[stash_index(src, r)]);
+            const int q = src & 31;
+            const int row = 8 * (r >> 2) + 4 * (src >> 5) + (r & 3);
+            const int32_t id = tr[row];
+            const float4 Q = W.qst[q];
+            const bool ok = id >= 0 && id != __float_as_int(Q.w) &&
+                            (dk < Q.y || (dk == Q.y && static_cast<uint32_t>(id) <= __float_as_uint(Q.z)));
+            if (ok) {
+                const int slot = atomicAdd(&W.qcnt[q], 1);
+                a.cand[W.qrow_out[q] * kCollectCap + slot] = pack_key(dk, id);
+            }
+        }
+    }
+    wave_sync();
+    st.cnt = W.qcnt[lane & 31];
+}
+
+// window_tile for fp32 keys.
+template <int METRIC>
+__device__ __forceinline__ void window_tile_f32(const floatx16& acc, const float* tn, const int32_t* tr, int h,
+                                                float qn, int32_t self, float (&T)[32])
+{
+    float s[16];
+    f32_tile_keys<METRIC>(acc, tn, h, qn, s);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const int4 pi = *reinterpret_cast<const int4*>(tr + 8 * g + 4 * h);
+        const int32_t i4[4] = {pi.x, pi.y, pi.z, pi.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) s[4 * g + e] = (i4[e] < 0 || i4[e] == self) ? INFINITY : s[4 * g + e];
+    }
+    oddeven_sort(s);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) T[16 + k] = fminf(T[16 + k], s[15 - k]);
+    bitonic_merge(T);
+}
+
+template <int DP, int METRIC>
+__global__ void __launch_bounds__(256, 2) knn_f32_collect_kernel(KnnArgs a)
+{
+    constexpr int DH = DP / 2;                       // k-steps of 2 dims (one per half wave)
+    constexpr int F4_ROW = DP / 4;
+    constexpr int F4_THREAD = kPoolTile * F4_ROW / 256;
+    static_assert(DP % 32 == 0, "row stride must be a multiple of 32 floats");
+    __shared__ CollectSmemF<DP> sm;
+
+    const int per = a.n_items / 8;
+    const int item_idx = static_cast<int>(blockIdx.x % 8) * per + static_cast<int>(blockIdx.x / 8);
+    if (item_idx >= a.n_items) return;
+    const WorkItem it = a.items[item_idx];
+    if (it.q_count <= 0) return;
+
+    const int tid = threadIdx.x;
+    const int w = tid >> 6, lane = tid & 63, j = lane & 31, h = lane >> 5;
+    const int qlocal = w * kQueriesPerWave + j;
+    const bool qvalid = qlocal < it.q_count;
+    const int64_t qi = it.q_begin + qlocal;
+    const int32_t qrow = qvalid ? (a.q_rows ? a.q_rows[qi] : static_cast<int32_t>(qi)) : 0;
+    const float qn = (qvalid && METRIC == 0) ? a.nq[qrow] : 0.f;
+
+    CollectState st;
+    float seed = FLT_MAX;
+    const int64_t orow_seed = it.out_base >= 0 ? it.out_base + qlocal : static_cast<int64_t>(qrow);
+    if (qvalid && a.seed_d) seed = fminf(a.seed_d[orow_seed * a.seed_ld + a.seed_ld - 1], FLT_MAX);
+    st.thr = qvalid ? seed : -INFINITY;
+    st.thr_id = 0xffffffffu;
+    st.cnt = 0;
+    st.self = a.exclude_self ? qrow : -2;
+    st.orow = it.out_base >= 0 ? it.out_base + qlocal : static_cast<int64_t>(qrow);
+
+    // query fragment: dims [h*DH, h*DH + DH) of query row qrow
+    float qf[DH];
+    {
+        const float4* src = reinterpret_cast<const float4*>(a.Xq + static_cast<int64_t>(qrow) * DP + h * DH);
+#pragma unroll
+        for (int s4 = 0; s4 < DH / 4; ++s4) {
+            const float4 v = qvalid ? src[s4] : make_float4(0.f, 0.f, 0.f, 0.f);
+            qf[4 * s4 + 0] = v.x; qf[4 * s4 + 1] = v.y; qf[4 * s4 + 2] = v.z; qf[4 * s4 + 3] = v.w;
+        }
+    }
+
+    CollectWave& W = sm.wv[w];
+    publish_state(W, lane, qvalid, qn, st);
+
+    // steps: tiles 0 .. ntl - 1, each once; unseeded, the first nwt tiles
+    // bound the threshold first and are scanned again at the end
+    const int pcount = it.p_count;
+    const int ntl = (pcount + kPoolTile - 1) / kPoolTile;
+    const int nwt = a.seed_d ? 0 : min(kWindow, ntl);
+    const int nst = ntl + nwt;
+    auto pool_row = [&](int t, int r) __attribute__((always_inline)) -> int32_t {
+        if (t >= nst) return -1;
+        int p = (t < ntl ? t : t - ntl) * kPoolTile + r;
+        if (p >= pcount) return -1;
+        p += it.p_rot;
+        if (p >= pcount) p -= pcount;
+        return a.p_rows[it.p_begin + p];
+    };
+    auto row_norm = [&](int32_t row) __attribute__((always_inline)) -> float {
+        if (row < 0) return INFINITY;
+        return METRIC == 0 ? a.np[row] : 0.f;
+    };
+    // pool tiles flow through three stages as in knn_fused_kernel: ids (two
+    // steps ahead) -> rows in registers (one step ahead) -> LDS
+    int32_t idn[F4_THREAD];
+    float4 pre[F4_THREAD];
+    int32_t rid_next = -1;
+    auto load_ids = [&](int t) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < F4_THREAD; ++u) idn[u] = pool_row(t, (tid + 256 * u) / F4_ROW);
+        if (tid < kPoolTile) rid_next = pool_row(t, tid);
+    };
+    auto load_rows = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < F4_THREAD; ++u) {
+            const int c4 = (tid + 256 * u) % F4_ROW;
+            pre[u] = idn[u] >= 0 ? reinterpret_cast<const float4*>(a.Xp + static_cast<int64_t>(idn[u]) * DP)[c4]
+                                 : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    };
+    auto store_rows = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < F4_THREAD; ++u) {
+            const int e = tid + 256 * u;
+            *reinterpret_cast<float4*>(&sm.tile[buf][e / F4_ROW][4 * (e % F4_ROW)]) = pre[u];
+        }
+    };
+
+    load_ids(0);
+    load_rows();
+    int32_t rid_cur = rid_next;
+    float rn_cur = tid < kPoolTile ? row_norm(rid_cur) : 0.f;
+    store_rows(0);
+    if (tid < kPoolTile) { sm.trow[0][tid] = rid_cur; sm.tnorm[0][tid] = rn_cur; }
+    load_ids(1);
+    __syncthreads();
+
+    floatx16 acc_prev;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc_prev[r] = 0.f;
+    bool pending = false;   // acc_prev holds step p_t's tile, not yet filtered
+    int p_t = 0;
+    // one step: the next tile's rows requested, the MFMAs of tile t, the
+    // filter of the tile before it, then tile t + 1 into the other buffer
+    auto step = [&](int t, auto&& filt) __attribute__((always_inline)) {
+        const int buf = t & 1;
+        wait_vmem();
+        load_rows();
+        rid_cur = rid_next;
+        rn_cur = tid < kPoolTile ? row_norm(rid_cur) : 0.f;
+        load_ids(t + 2);
+        floatx16 acc;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+        const float* arow = &sm.tile[buf][j][h * DH];
+#pragma unroll
+        for (int s4 = 0; s4 < DH / 4; ++s4) {
+            const float4 av = *reinterpret_cast<const float4*>(arow + 4 * s4);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.x, qf[4 * s4 + 0], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.y, qf[4 * s4 + 1], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.z, qf[4 * s4 + 2], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.w, qf[4 * s4 + 3], acc, 0, 0, 0);
+        }
+        if (pending) filt(p_t);
+        store_rows(buf ^ 1);
+        if (tid < kPoolTile) { sm.trow[(t + 1) % 3][tid] = rid_cur; sm.tnorm[(t + 1) % 3][tid] = rn_cur; }
+        __syncthreads();
+        acc_prev = acc;
+        pending = true;
+        p_t = t;
+    };
+    auto collect = [&](int t) __attribute__((always_inline)) {
+        const int sl = t % 3;
+        collect_tile_f32<METRIC>(a, W, acc_prev, sm.tnorm[sl], sm.trow[sl], lane, h, qvalid, qn, st);
+    };
+    if (nwt > 0) {
+        float T[32];
+#pragma unroll
+        for (int i = 0; i < 32; ++i) T[i] = INFINITY;
+        auto window = [&](int t) __attribute__((always_inline)) {
+            const int sl = t % 3;
+            window_tile_f32<METRIC>(acc_prev, sm.tnorm[sl], sm.trow[sl], h, qn, st.self, T);
+        };
+        for (int t = 0; t < nwt; ++t) step(t, window);
+        window(p_t);   // the window's last tile
+        pending = false;
+        // the pair's ceil(M/2)-th smallest distances: M distinct rows at or below the larger
+        const int m = (a.M + 1) / 2 - 1;
+        float v = T[0];
+#pragma unroll
+        for (int i = 1; i < 32; ++i) v = i == m ? T[i] : v;
+        const float bound = fmaxf(v, __shfl_xor(v, 32));
+        if (qvalid && bound < st.thr) st.thr = bound;
+        publish_state(W, lane, qvalid, qn, st);
+    }
+    for (int t = nwt; t < nst; ++t) step(t, collect);
+    if (pending) collect(p_t);
+    if (qvalid && h == 0) a.cand_cnt[st.orow] = st.cnt;
+    if (a.stats && qvalid && h == 0) atomicAdd(a.stats, static_cast<unsigned long long>(st.cnt));
+}
+
 // ------------------------------------------------------------ selection
 
 // Each row's top-M of its cnt[row] candidate keys, ascending, into (out_ids,
@@ -542,7 +825,22 @@ bool knn_collect_supported(const KnnArgs& a)
 {
     const char* e = std::getenv("GTANN_KNN_COLLECT");
     if (e && e[0] == '0') return false;
-    return a.Xq8 && a.Xp8 && a.M > 4 && a.M <= 64 && a.out_pos == 0 && a.Dp <= 256 && a.Dp % 32 == 0;
+    if (!(a.M > 4 && a.M <= 64 && a.out_pos == 0 && a.Dp % 32 == 0)) return false;
+    if (a.Xq8 && a.Xp8) return a.Dp <= 256;
+    return a.Xq && a.Xp && a.Dp <= 160;   // longer fp32 rows: the query fragment leaves too few registers
+}
+
+template <int METRIC>
+static void launch_collect_f32_metric(const KnnArgs& a, dim3 grid, hipStream_t stream)
+{
+    switch (a.Dp) {
+    case 32:  hipLaunchKernelGGL((knn_f32_collect_kernel<32, METRIC>), grid, dim3(256), 0, stream, a); break;
+    case 64:  hipLaunchKernelGGL((knn_f32_collect_kernel<64, METRIC>), grid, dim3(256), 0, stream, a); break;
+    case 96:  hipLaunchKernelGGL((knn_f32_collect_kernel<96, METRIC>), grid, dim3(256), 0, stream, a); break;
+    case 128: hipLaunchKernelGGL((knn_f32_collect_kernel<128, METRIC>), grid, dim3(256), 0, stream, a); break;
+    case 160: hipLaunchKernelGGL((knn_f32_collect_kernel<160, METRIC>), grid, dim3(256), 0, stream, a); break;
+    default: GT_REQUIRE(false, "fp32 collect kernel: padded dimension " + std::to_string(a.Dp) + " not supported");
+    }
 }
 
 template <int METRIC>
@@ -566,13 +864,16 @@ static void launch_collect_metric(const KnnArgs& a, dim3 grid, hipStream_t strea
 // (rows + kQueriesPerWave) * kCollectCap keys.
 void launch_knn_collect_select(const KnnArgs& a, int64_t rows, hipStream_t stream)
 {
-    GT_REQUIRE(knn_collect_supported(a), "collect launch: int8 rows, 4 < M <= 64");
+    GT_REQUIRE(knn_collect_supported(a), "collect launch: int8 rows (Dp <= 256) or fp32 rows (Dp <= 160), 4 < M <= 64");
     GT_REQUIRE(a.cand && a.cand_cnt && a.out_ids && a.out_d && a.p_rows, "collect launch: buffers missing");
     GT_REQUIRE(a.n_items % 8 == 0, "work list must be padded to a multiple of 8");
     if (a.n_items > 0) {
         const dim3 grid(static_cast<unsigned>(a.n_items));
-        if (a.metric == 0) launch_collect_metric<0>(a, grid, stream);
-        else launch_collect_metric<1>(a, grid, stream);
+        const bool i8 = a.Xq8 && a.Xp8;
+        if (i8 && a.metric == 0) launch_collect_metric<0>(a, grid, stream);
+        else if (i8) launch_collect_metric<1>(a, grid, stream);
+        else if (a.metric == 0) launch_collect_f32_metric<0>(a, grid, stream);
+        else launch_collect_f32_metric<1>(a, grid, stream);
         GT_HIP(hipGetLastError());
     }
     if (rows <= 0) return;
