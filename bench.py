@@ -8,8 +8,9 @@ merge), sanitize, CAGRA prune, reverse-edge merge -- of configuration C2
 with the dataset already resident in HBM.  Prints one JSON line.
 
 `roofline` is the kNN kernel of the rounds (knn_i8_collect_kernel +
-knn_select_kernel when the rows are integers, as C2's are; knn_fused_kernel /
-knn_wide_kernel otherwise): achieved = the algorithmic ops of its launches
+knn_select_kernel when the rows are integers, as C2's are;
+knn_f32_collect_kernel + knn_select_kernel for float rows up to 160
+dimensions, knn_wide_kernel beyond): achieved = the algorithmic ops of its launches
 (2*D per scanned (query, pool row) pair) over their summed duration, both
 measured by the library with HIP events on its stream.  `traffic` is read
 from profiles/<kernel>_<config>_traffic.json (knn_i8_collect_C2_traffic.json
@@ -202,7 +203,10 @@ def knn_roofline(s, D, metric, M=64):
                  else f"knn_i8_kernel<{dp}, {mip}>")
         peak, unit = PEAK_INT8_MFMA, "TOP/s"
     elif D <= 256:
-        kname, peak, unit = f"knn_fused_kernel<{-(-D // 32) * 32}, {mip}>", PEAK_FP32_MFMA, "TFLOP/s"
+        dp = -(-D // 32) * 32
+        kname = (f"knn_f32_collect_kernel<{dp}, {mip}> + knn_select_kernel" if 4 < M <= 64 and dp <= 160
+                 else f"knn_fused_kernel<{dp}, {mip}>")
+        peak, unit = PEAK_FP32_MFMA, "TFLOP/s"
     else:
         kname, peak, unit = f"knn_wide_kernel<{mip}>", PEAK_FP32_MFMA, "TFLOP/s"
     return {"kernel": kname, "bound": "mfma", "achieved": flops / launch_s / 1e12, "peak": peak / 1e12,
@@ -517,7 +521,7 @@ def main():
         same = bool(torch.equal(r32.knn_ids, res.knn_ids) and torch.equal(r32.graph, res.graph))
         r = knn_roofline(s32, D, cfg.metric, cfg.M)
         out["fp32_path"] = {
-            "note": "int_exact=0: same dataset on knn_fused_kernel (fp32 matrix cores)",
+            "note": "int_exact=0: same dataset on the fp32 matrix cores (knn_f32_collect_kernel + knn_select_kernel)",
             "value": N / w32 / 1e6, "unit": "Mpts/s", "ms_per_step": w32 * 1e3,
             "identical_table_and_graph": same,
             "roofline": dict({k: r[k] for k in ("kernel", "bound", "achieved", "peak", "unit", "frac", "launch_ms")},
