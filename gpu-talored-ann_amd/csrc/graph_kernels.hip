@@ -293,11 +293,14 @@ __device__ __forceinline__ int prune_pos_of(const uint32_t* __restrict__ off, in
 //      off[q]); any other neighbour contributes nothing.
 // ROWS 1 and 2 prune rows map.a0 .. map.a0 + map.n - 1 into output rows
 // 0 .. n - 1.
-template <int E, int ROWS>
+// BUF (ROWS 0, tables below 4 GiB): neighbour rows by buffer loads, the
+// row's byte offset a scalar operand of the load.
+template <int E, int ROWS, bool BUF = false>
 __global__ void __launch_bounds__(256) cagra_prune_kernel(const int32_t* __restrict__ G, int64_t N, int M, int K,
                                                           uint32_t* __restrict__ out,
                                                           unsigned long long* __restrict__ bad_row, PruneMap map)
 {
+    static_assert(!BUF || ROWS == 0, "buffer loads address the whole table");
     constexpr int MM = 64 * E;
     constexpr int NBK = 2 * MM;               // home buckets
     constexpr int BK = NBK + MM / 4 + 1;      // + spill room: at most MM entries
@@ -386,35 +389,50 @@ __global__ void __launch_bounds__(256) cagra_prune_kernel(const int32_t* __restr
     // checked when the row is probed, so no load is waited for early
     int32_t ring[kPruneDepth][E];
     bool rok[kPruneDepth];
+    // ROWS 0: row a's ids with the last rank and everything past it -1
+    // (never fetched), so that a fetch needs no rank test
+    int32_t Apad[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) Apad[e] = lane + 64 * e < M - 1 ? A[e] : -1;
+    // (unused without BUF)
+    const __amdgpu_buffer_rsrc_t grsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int32_t*>(G), 0, BUF ? static_cast<int>(N * M * 4) : 0, 0x00020000);
     auto fetch = [&](int kAD, int32_t (&b)[E], bool& ok) {
+        if constexpr (ROWS == 0) {
+            // the id (negative ids and the padding fail du < nlim) and the
+            // row address stay on the scalar unit
+            const int kk = min(kAD, MM - 1);
+            uint32_t du = __builtin_amdgcn_readlane(static_cast<uint32_t>(Apad[0]), kk & 63);
+            if constexpr (E > 1) {
+                const uint32_t d1 = __builtin_amdgcn_readlane(static_cast<uint32_t>(Apad[E - 1]), kk & 63);
+                du = (kk >> 6) ? d1 : du;
+            }
+            ok = du < nlim;
+            if constexpr (BUF) {
+                const uint32_t soff = ok ? du * static_cast<uint32_t>(4 * M) : 0u;
+#pragma unroll
+                for (int e = 0; e < E; ++e) b[e] = __builtin_amdgcn_raw_buffer_load_b32(grsrc, 4 * col[e], soff, 0);
+            } else {
+                const int32_t* row = G + static_cast<int64_t>(ok ? du : 0u) * M;
+#pragma unroll
+                for (int e = 0; e < E; ++e) b[e] = row[col[e]];
+            }
+            return;
+        }
         int64_t d = -1;
-        uint32_t du = 0xFFFFFFFFu;   // ROWS 0: the id (negative ids fail du < nlim)
         if (kAD < M - 1) {
 #pragma unroll
             for (int e = 0; e < E; ++e)
                 if ((kAD >> 6) == e) {
-                    if (ROWS == 0) {
-                        du = __builtin_amdgcn_readlane(static_cast<uint32_t>(A[e]), kAD & 63);
-                    } else {
-                        const uint32_t lo = __builtin_amdgcn_readlane(static_cast<uint32_t>(nrow[e]), kAD & 63);
-                        const int32_t hi = __builtin_amdgcn_readlane(static_cast<int32_t>(nrow[e] >> 32), kAD & 63);
-                        d = (static_cast<int64_t>(hi) << 32) | lo;
-                    }
+                    const uint32_t lo = __builtin_amdgcn_readlane(static_cast<uint32_t>(nrow[e]), kAD & 63);
+                    const int32_t hi = __builtin_amdgcn_readlane(static_cast<int32_t>(nrow[e] >> 32), kAD & 63);
+                    d = (static_cast<int64_t>(hi) << 32) | lo;
                 }
         }
-        if (ROWS == 0) {
-            // the id as a 32-bit scalar: the bounds test and the row address
-            // stay on the scalar unit
-            ok = du < nlim;
-            const int32_t* row = G + static_cast<int64_t>(ok ? du : 0u) * M;
+        ok = d >= 0;
+        const int32_t* row = G + (ok ? d : int64_t(0)) * M;
 #pragma unroll
-            for (int e = 0; e < E; ++e) b[e] = row[col[e]];
-        } else {
-            ok = d >= 0;
-            const int32_t* row = G + (ok ? d : int64_t(0)) * M;
-#pragma unroll
-            for (int e = 0; e < E; ++e) b[e] = row[col[e]];
-        }
+        for (int e = 0; e < E; ++e) b[e] = row[col[e]];
     };
     uint32_t c[E];
 #pragma unroll
@@ -1499,8 +1517,13 @@ void launch_cagra_prune(const int32_t* G, int64_t N, int M, int K, uint32_t* out
     PruneMap m{};
     m.order = order;
     const dim3 grid(static_cast<unsigned>(8 * ceil_div(ceil_div(N, int64_t(4)), int64_t(8))));
-    if (M <= 64)
+    const bool buf = N * M * 4 < (int64_t(1) << 31);   // byte offsets and the buffer size in 31 bits
+    if (M <= 64 && buf)
+        hipLaunchKernelGGL((cagra_prune_kernel<1, 0, true>), grid, dim3(256), 0, s, G, N, M, K, out, bad_row, m);
+    else if (M <= 64)
         hipLaunchKernelGGL((cagra_prune_kernel<1, 0>), grid, dim3(256), 0, s, G, N, M, K, out, bad_row, m);
+    else if (buf)
+        hipLaunchKernelGGL((cagra_prune_kernel<2, 0, true>), grid, dim3(256), 0, s, G, N, M, K, out, bad_row, m);
     else
         hipLaunchKernelGGL((cagra_prune_kernel<2, 0>), grid, dim3(256), 0, s, G, N, M, K, out, bad_row, m);
     GT_HIP(hipGetLastError());
