@@ -123,6 +123,18 @@ __global__ void quantize_i8_kernel(const float* __restrict__ src, int64_t N, int
     dst[e] = static_cast<int8_t>(fminf(fmaxf(v, -128.f), 127.f));
 }
 
+// the same rounding in fp32: rows of integers, each the value quantize_i8
+// stores plus the shift (padding 0)
+__global__ void round_to_int_kernel(const float* __restrict__ src, int64_t N, int D, int Dp, int shift,
+                                    float* __restrict__ dst)
+{
+    const int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (e >= N * Dp) return;
+    const int c = static_cast<int>(e % Dp);
+    const float v = c < D ? rintf(src[e] - static_cast<float>(shift)) : 0.f;
+    dst[e] = c < D ? fminf(fmaxf(v, -128.f), 127.f) + static_cast<float>(shift) : 0.f;
+}
+
 // |x|^2 of int8 rows (exact integer sums), one wave per row
 __global__ void __launch_bounds__(256) row_norms_i8_kernel(const int8_t* __restrict__ X, int64_t N, int Dp,
                                                            float* __restrict__ norms)
@@ -1447,6 +1459,13 @@ void launch_quantize_i8(const float* src, int64_t N, int D, int Dp, int shift, i
 {
     if (N * Dp <= 0) return;
     hipLaunchKernelGGL(quantize_i8_kernel, dim3(grid_for(N * Dp, 256)), dim3(256), 0, s, src, N, D, Dp, shift, dst);
+    GT_HIP(hipGetLastError());
+}
+
+void launch_round_to_int(const float* src, int64_t N, int D, int Dp, int shift, float* dst, hipStream_t s)
+{
+    if (N * Dp <= 0) return;
+    hipLaunchKernelGGL(round_to_int_kernel, dim3(grid_for(N * Dp, 256)), dim3(256), 0, s, src, N, D, Dp, shift, dst);
     GT_HIP(hipGetLastError());
 }
 

@@ -40,6 +40,7 @@ void launch_prepare_int(const void* src, int dtype, int64_t N, int D, int Dp, fl
                         float* n8, hipStream_t s);
 void launch_row_norms_i8(const int8_t* X, int64_t N, int Dp, float* norms, hipStream_t s);
 void launch_quantize_i8(const float* src, int64_t N, int D, int Dp, int shift, int8_t* dst, hipStream_t s);
+void launch_round_to_int(const float* src, int64_t N, int D, int Dp, int shift, float* dst, hipStream_t s);
 void launch_row_norms_range(const float* X, int64_t N, int Dp, float* norms, int* part, int* out, hipStream_t s);
 void launch_quantize_norms_i8(const float* src, int64_t N, int D, int Dp, int shift, int8_t* dst, float* norms,
                               hipStream_t s);
@@ -239,7 +240,7 @@ enum Ws {
     W_TMP, W_OUT, W_IN, W_PROBE_I, W_PROBE_D, W_WORST, W_X8, W_NORMS8, W_C8, W_CNORMS8,
     W_SUBROWS, W_SUBID, W_SUBD, W_SUBOFF, W_MEMBERS2, W_SUBNN, W_SUBNND, W_SUBBASE, W_SUBCNT, W_CHAINPOS,
     W_LHIST, W_LOFFS, W_LSUMS, W_CAND, W_CANDCNT, W_STATS,
-    W_OOC_A, W_OOC_B, W_OOC_C, W_OOC_D, W_OOC_E, W_OOC_F, W_OOC_G, W_COUNT_
+    W_OOC_A, W_OOC_B, W_OOC_C, W_OOC_D, W_OOC_E, W_OOC_F, W_OOC_G, W_CR, W_CRNORMS, W_COUNT_
 };
 static_assert(W_COUNT_ <= 64, "workspace slots");
 
@@ -355,6 +356,9 @@ struct DevMatrix {
     int Dp8 = 0;
     int shift = 0;
     bool from_float = false;
+    // >= 0: every value is an integer in [-128, 127] + iv_shift (integer
+    // inputs; float rows found integer-valued, with or without their int8 copy)
+    int iv_shift = -1;
 };
 
 // The int8 kernel runs a (query, pool) pair when both sides have int8 rows
@@ -401,6 +405,7 @@ static DevMatrix prepare(Ctx& c, int slot_x, int slot_raw, int slot_norms, const
         m.norms = nrm;
         m.Dp8 = Dp;
         m.shift = dtype == GT_DTYPE_U8 ? 128 : 0;
+        m.iv_shift = m.shift;
         m.data8 = x8;
         m.norms8 = n8;
         return m;
@@ -418,9 +423,10 @@ static DevMatrix prepare(Ctx& c, int slot_x, int slot_raw, int slot_norms, const
         m.data = xp;
     }
     float* nrm = c.ws<float>(slot_norms, static_cast<size_t>(N));
-    // float rows that may take the exact int8 path: norms and the integer
-    // check in one pass
-    const bool check_int = with_i8 && int_exact && dtype == GT_DTYPE_F32 && Dp <= 256;
+    // float rows of a build: norms and the integer check in one pass (an
+    // integer-valued dataset takes the exact int8 path with int_exact, and
+    // its bucketing uses integer-rounded centroids either way)
+    const bool check_int = with_i8 && dtype == GT_DTYPE_F32 && Dp <= 256;
     int* range = nullptr;
     if (check_int) {
         int* part = c.ws<int>(W_SUBD, static_cast<size_t>(3 * ((N + 3) / 4)));
@@ -433,6 +439,7 @@ static DevMatrix prepare(Ctx& c, int slot_x, int slot_raw, int slot_norms, const
     if (with_i8 && (dtype == GT_DTYPE_U8 || dtype == GT_DTYPE_I8) && Dp <= 256) {
         m.Dp8 = Dp;
         m.shift = dtype == GT_DTYPE_U8 ? 128 : 0;
+        m.iv_shift = m.shift;
         int8_t* x8 = c.ws<int8_t>(W_X8, static_cast<size_t>(N) * Dp);
         launch_pad_i8(src, dtype, x8, N, D, Dp, c.s);
         float* n8 = c.ws<float>(W_NORMS8, static_cast<size_t>(N));
@@ -444,7 +451,8 @@ static DevMatrix prepare(Ctx& c, int slot_x, int slot_raw, int slot_norms, const
         c.d2h(h, range, sizeof(h));   // padding columns are zeros: integers
         c.sync();
         const int shift = h[0] ? -1 : (h[1] >= -128 && h[2] <= 127) ? 0 : (h[1] >= 0 && h[2] <= 255) ? 128 : -1;
-        if (shift >= 0) {
+        m.iv_shift = shift;
+        if (shift >= 0 && int_exact) {
             m.Dp8 = Dp;
             m.shift = shift;
             m.from_float = true;
@@ -1112,13 +1120,23 @@ static void bucket_device(Ctx& c, const DevMatrix& X, int64_t C, int nprobe, int
     Cm.D = X.D;
     Cm.data = d_cm;
     Cm.norms = d_cn;
-    // an integer dataset's assignment runs on the int8 kernel against the
-    // centroids rounded to the dataset's values (the buckets only need
-    // near centroids; every distance is then exact for those)
+    // an integer-valued dataset's assignment runs against the centroids
+    // rounded to the dataset's values (the buckets only need near
+    // centroids; every distance is then an exact integer): on the int8
+    // kernel when the rows have their int8 copy, else on the fp32 kernel
+    // with the same rounded centroids, so that the buckets do not depend on
+    // which kernel runs
+    float* d_cr = X.iv_shift >= 0 && !X.data8 ? c.ws<float>(W_CR, static_cast<size_t>(C) * X.Dp) : nullptr;
+    float* d_crn = d_cr ? c.ws<float>(W_CRNORMS, static_cast<size_t>(C)) : nullptr;
     auto refresh_c8 = [&]() {
-        // integer-typed inputs only: float inputs keep fp32 centroids, so
-        // their buckets do not depend on whether the int8 copy exists
-        if (!X.data8 || X.from_float) return;
+        if (X.iv_shift < 0) return;   // float data: fp32 centroids
+        if (!X.data8) {
+            launch_round_to_int(d_cm, C, X.D, X.Dp, X.iv_shift, d_cr, c.s);
+            launch_row_norms(d_cr, C, X.Dp, d_crn, c.s);
+            Cm.data = d_cr;
+            Cm.norms = d_crn;
+            return;
+        }
         int8_t* c8 = c.ws<int8_t>(W_C8, static_cast<size_t>(C) * X.Dp8);
         float* cn8 = c.ws<float>(W_CNORMS8, static_cast<size_t>(C));
         launch_quantize_i8(d_cm, C, X.D, X.Dp8, X.shift, c8, c.s);
