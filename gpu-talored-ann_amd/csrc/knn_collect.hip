@@ -275,6 +275,10 @@ knn_i8_collect_kernel(KnnArgs a)
     st.cnt = 0;
     st.self = a.exclude_self ? qrow : -2;
     st.orow = it.out_base >= 0 ? it.out_base + qlocal : static_cast<int64_t>(qrow);
+    if (it.p_count <= 0) {   // an empty pool: no candidates (the stage loads below need a row)
+        if (qvalid && h == 0) a.cand_cnt[st.orow] = 0;
+        return;
+    }
 
     intx4 qf[KS];
     {
