@@ -54,6 +54,7 @@ struct CollectSmem {
     float tnorm[3][kStageRows];
     int32_t trow[3][kStageRows];
     int32_t thalf[3][kStageRows];          // accumulator start: -floor(|p|^2 / 2) (L2), 0 (IP), kHalfPast past the end
+    int32_t sid[2][kStageRows];            // the next stage's pool row ids, for every thread's row requests
     CollectWave wv[kWaves];
 };
 
@@ -300,10 +301,10 @@ knn_i8_collect_kernel(KnnArgs a)
     const int nps = (pcount + ROWS - 1) / ROWS;
     const int nws = a.seed_d ? 0 : min(kWindow / kStageTiles, nps);
     const int nst = nps + nws;
-    // Every thread issues the same loads in every stage (positions past the
-    // slice end are clamped to its last row and flagged), so the compiler
-    // can wait for one stage's loads without draining the next's.  The pool
-    // list is the caller's (launch_knn_collect_select requires one).
+    // Every thread issues the same row loads in every stage (positions past
+    // the slice end are clamped to its last row and flagged), so the
+    // compiler can wait for one stage's loads without draining the next's.
+    // The pool list is the caller's (launch_knn_collect_select requires one).
     auto pool_pos = [&](int p) __attribute__((always_inline)) -> int64_t {
         p = min(p, pcount - 1) + it.p_rot;
         if (p >= pcount) p -= pcount;
@@ -312,30 +313,23 @@ knn_i8_collect_kernel(KnnArgs a)
     auto stage_base = [&](int s) __attribute__((always_inline)) { return (s < nps ? s : s - nps) * ROWS; };
 
     // fixed-size register sets indexed only by unrolled loop counters
-    struct Ids {
-        int32_t v[U4_THREAD];
-    } idn;
     struct Rows {
         intx4 v[U4_THREAD];   // vector type: register moves, not aggregate copies
     } pre;
-    int32_t rid_next = 0;    // this thread's stage row (threads < ROWS), a valid row id
-    bool rvalid_next = false;
-    auto load_ids = [&](int s) __attribute__((always_inline)) {
+    // The threads < ROWS fetch their stage row's pool id (one stage ahead)
+    // and norm; the ids reach every thread's row requests through LDS.
+    const int r_own = tid & (ROWS - 1);
+    auto stage_id = [&](int s, bool& valid) __attribute__((always_inline)) -> int32_t {
         const bool live = s < nst;
         const int base = live ? stage_base(s) : 0;
-        static_for<0, U4_THREAD>([&](auto U) __attribute__((always_inline)) {
-            const int e = min(tid + 256 * U.value, U4_STAGE - 1);
-            idn.v[U.value] = a.p_rows[pool_pos(base + e / U4_ROW)];
-        });
-        const int r = tid & (ROWS - 1);
-        rid_next = a.p_rows[pool_pos(base + r)];
-        rvalid_next = live && base + r < pcount;
+        valid = live && base + r_own < pcount;
+        return a.p_rows[pool_pos(base + r_own)];
     };
-    auto load_rows = [&]() __attribute__((always_inline)) {
+    auto load_rows = [&](const int32_t* ids) __attribute__((always_inline)) {
         static_for<0, U4_THREAD>([&](auto U) __attribute__((always_inline)) {
             const int e = min(tid + 256 * U.value, U4_STAGE - 1);
             pre.v[U.value] =
-                *reinterpret_cast<const intx4*>(a.Xp8 + static_cast<int64_t>(idn.v[U.value]) * DP + 16 * (e % U4_ROW));
+                *reinterpret_cast<const intx4*>(a.Xp8 + static_cast<int64_t>(ids[e / U4_ROW]) * DP + 16 * (e % U4_ROW));
         });
     };
     auto store_rows = [&](int buf) __attribute__((always_inline)) {
@@ -344,12 +338,17 @@ knn_i8_collect_kernel(KnnArgs a)
             if (e < U4_STAGE) *reinterpret_cast<intx4*>(&sm.tile[buf][e / U4_ROW][16 * (e % U4_ROW)]) = pre.v[U.value];
         });
     };
-    load_ids(0);
-    load_rows();
-    int32_t rid_cur = rid_next;
-    bool rvalid_cur = rvalid_next;
-    float rn_cur = METRIC == 0 ? a.np[rid_cur] : 0.f;
-    load_ids(1);
+    int32_t rid_cur = 0, rid_next = 0;   // threads < ROWS: the stage row's id (a valid row) this stage, the next
+    bool rvalid_cur = false, rvalid_next = false;
+    float rn_cur = 0.f;
+    if (tid < ROWS) {
+        rid_cur = stage_id(0, rvalid_cur);
+        sm.sid[0][tid] = rid_cur;
+        rn_cur = METRIC == 0 ? a.np[rid_cur] : 0.f;
+        rid_next = stage_id(1, rvalid_next);
+    }
+    __syncthreads();
+    load_rows(sm.sid[0]);
 
     intx16 acc_prev;
 #pragma unroll
@@ -372,13 +371,16 @@ knn_i8_collect_kernel(KnnArgs a)
             sm.trow[slot][tid] = rvalid_cur ? rid_cur : -1;
             sm.tnorm[slot][tid] = rvalid_cur ? rn_cur : INFINITY;
             sm.thalf[slot][tid] = rvalid_cur ? -(static_cast<int32_t>(rn_cur) >> 1) : kHalfPast;
+            sm.sid[(s + 1) & 1][tid] = rid_next;
         }
         __syncthreads();
-        load_rows();
-        rid_cur = rid_next;
-        rvalid_cur = rvalid_next;
-        rn_cur = METRIC == 0 ? a.np[rid_cur] : 0.f;
-        load_ids(s + 2);
+        load_rows(sm.sid[(s + 1) & 1]);
+        if (tid < ROWS) {
+            rid_cur = rid_next;
+            rvalid_cur = rvalid_next;
+            rn_cur = METRIC == 0 ? a.np[rid_cur] : 0.f;
+            rid_next = stage_id(s + 2, rvalid_next);
+        }
 
 #pragma unroll
         for (int u = 0; u < kStageTiles; ++u) {
