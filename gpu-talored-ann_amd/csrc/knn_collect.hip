@@ -456,6 +456,7 @@ struct CollectSmemF {
     float tile[2][kPoolTile][DP + 4];   // +4 floats: rows land on distinct bank groups
     float tnorm[3][kPoolTile];
     int32_t trow[3][kPoolTile];
+    int32_t sid[2][kPoolTile];   // the next tile's pool row ids (-1 past the end), for every thread's row requests
     CollectWave wv[kWaves];
 };
 
@@ -623,21 +624,17 @@ __global__ void __launch_bounds__(256, 2) knn_f32_collect_kernel(KnnArgs a)
         return METRIC == 0 ? a.np[row] : 0.f;
     };
     // pool tiles flow through three stages as in knn_fused_kernel: ids (two
-    // steps ahead) -> rows in registers (one step ahead) -> LDS
-    int32_t idn[F4_THREAD];
+    // steps ahead, one per row by the threads < kPoolTile, handed to every
+    // thread through LDS) -> rows in registers (one step ahead) -> LDS
     float4 pre[F4_THREAD];
-    int32_t rid_next = -1;
-    auto load_ids = [&](int t) __attribute__((always_inline)) {
-#pragma unroll
-        for (int u = 0; u < F4_THREAD; ++u) idn[u] = pool_row(t, (tid + 256 * u) / F4_ROW);
-        if (tid < kPoolTile) rid_next = pool_row(t, tid);
-    };
-    auto load_rows = [&]() __attribute__((always_inline)) {
+    int32_t rid_next = -1;   // threads < kPoolTile: the row id two tiles ahead
+    auto load_rows = [&](const int32_t* ids) __attribute__((always_inline)) {
 #pragma unroll
         for (int u = 0; u < F4_THREAD; ++u) {
-            const int c4 = (tid + 256 * u) % F4_ROW;
-            pre[u] = idn[u] >= 0 ? reinterpret_cast<const float4*>(a.Xp + static_cast<int64_t>(idn[u]) * DP)[c4]
-                                 : make_float4(0.f, 0.f, 0.f, 0.f);
+            const int e = tid + 256 * u;
+            const int32_t id = ids[e / F4_ROW];
+            pre[u] = id >= 0 ? reinterpret_cast<const float4*>(a.Xp + static_cast<int64_t>(id) * DP)[e % F4_ROW]
+                             : make_float4(0.f, 0.f, 0.f, 0.f);
         }
     };
     auto store_rows = [&](int buf) __attribute__((always_inline)) {
@@ -648,13 +645,18 @@ __global__ void __launch_bounds__(256, 2) knn_f32_collect_kernel(KnnArgs a)
         }
     };
 
-    load_ids(0);
-    load_rows();
-    int32_t rid_cur = rid_next;
-    float rn_cur = tid < kPoolTile ? row_norm(rid_cur) : 0.f;
+    int32_t rid_cur = -1;
+    float rn_cur = 0.f;
+    if (tid < kPoolTile) {
+        rid_cur = pool_row(0, tid);
+        sm.sid[0][tid] = rid_cur;
+        rn_cur = row_norm(rid_cur);
+        rid_next = pool_row(1, tid);
+    }
+    __syncthreads();
+    load_rows(sm.sid[0]);
     store_rows(0);
-    if (tid < kPoolTile) { sm.trow[0][tid] = rid_cur; sm.tnorm[0][tid] = rn_cur; }
-    load_ids(1);
+    if (tid < kPoolTile) { sm.trow[0][tid] = rid_cur; sm.tnorm[0][tid] = rn_cur; sm.sid[1][tid] = rid_next; }
     __syncthreads();
 
     floatx16 acc_prev;
@@ -667,10 +669,12 @@ __global__ void __launch_bounds__(256, 2) knn_f32_collect_kernel(KnnArgs a)
     auto step = [&](int t, auto&& filt) __attribute__((always_inline)) {
         const int buf = t & 1;
         wait_vmem();
-        load_rows();
-        rid_cur = rid_next;
-        rn_cur = tid < kPoolTile ? row_norm(rid_cur) : 0.f;
-        load_ids(t + 2);
+        load_rows(sm.sid[(t + 1) & 1]);
+        if (tid < kPoolTile) {
+            rid_cur = rid_next;
+            rn_cur = row_norm(rid_cur);
+            rid_next = pool_row(t + 2, tid);
+        }
         floatx16 acc;
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[r] = 0.f;
@@ -685,7 +689,11 @@ __global__ void __launch_bounds__(256, 2) knn_f32_collect_kernel(KnnArgs a)
         }
         if (pending) filt(p_t);
         store_rows(buf ^ 1);
-        if (tid < kPoolTile) { sm.trow[(t + 1) % 3][tid] = rid_cur; sm.tnorm[(t + 1) % 3][tid] = rn_cur; }
+        if (tid < kPoolTile) {
+            sm.trow[(t + 1) % 3][tid] = rid_cur;
+            sm.tnorm[(t + 1) % 3][tid] = rn_cur;
+            sm.sid[t & 1][tid] = rid_next;   // tile t + 2's ids
+        }
         __syncthreads();
         acc_prev = acc;
         pending = true;
