@@ -56,6 +56,7 @@ struct KnnSmemTiles {
     float tile[2][kPoolTile][DP + 4];   // +4 floats: rows land on distinct bank groups
     float tnorm[3][kPoolTile];          // |p|^2 (L2) or 0 (IP); +inf past the slice end
     int32_t trow[3][kPoolTile];         // pool row id, -1 past the slice end
+    int32_t sid[2][kPoolTile];          // the next tile's pool row ids, for every thread's row requests
 };
 
 template <int DP, bool LISTS = true>
@@ -506,23 +507,20 @@ __global__ void __launch_bounds__(256, 2) knn_fused_kernel(KnnArgs a)
         return METRIC == 0 ? a.np[row] : 0.f;
     };
 
-    // Pool tiles flow through three stages: ids (two tiles ahead) -> row
-    // data in registers (one tile ahead) -> LDS.  Thread tid loads float4 c4_u
-    // of tile row r_u; threads < 32 also carry the id and norm of row tid.
-    int32_t idn[F4_THREAD];
+    // Pool tiles flow through three stages: ids (two tiles ahead, fetched by
+    // the threads < 32, one per row, and handed to every thread through LDS)
+    // -> row data in registers (one tile ahead) -> LDS.  Thread tid loads
+    // float4 c4_u of tile row r_u; threads < 32 also carry the id and norm of
+    // row tid.
     float4 pre[F4_THREAD];
-    int32_t rid_next = -1;   // id of row tid of the next tile to load (tid < 32)
-    auto load_ids = [&](int t) {
-#pragma unroll
-        for (int u = 0; u < F4_THREAD; ++u) idn[u] = pool_row(t * kPoolTile + (tid + 256 * u) / F4_ROW);
-        if (tid < kPoolTile) rid_next = pool_row(t * kPoolTile + tid);
-    };
-    auto load_rows = [&]() {
+    int32_t rid_next = -1;   // id of row tid two tiles ahead (tid < 32)
+    auto load_rows = [&](const int32_t* ids) {
 #pragma unroll
         for (int u = 0; u < F4_THREAD; ++u) {
-            const int c4 = (tid + 256 * u) % F4_ROW;
-            pre[u] = idn[u] >= 0 ? reinterpret_cast<const float4*>(a.Xp + static_cast<int64_t>(idn[u]) * DP)[c4]
-                                 : make_float4(0.f, 0.f, 0.f, 0.f);
+            const int e = tid + 256 * u;
+            const int32_t id = ids[e / F4_ROW];
+            pre[u] = id >= 0 ? reinterpret_cast<const float4*>(a.Xp + static_cast<int64_t>(id) * DP)[e % F4_ROW]
+                             : make_float4(0.f, 0.f, 0.f, 0.f);
         }
     };
     auto store_rows = [&](int buf) {
@@ -533,14 +531,19 @@ __global__ void __launch_bounds__(256, 2) knn_fused_kernel(KnnArgs a)
         }
     };
 
-    if (tid < kPoolTile) { sm.tnorm[2][tid] = INFINITY; sm.trow[2][tid] = -1; }
-    load_ids(0);
-    load_rows();
-    int32_t rid_cur = rid_next;
-    float rn_cur = tid < kPoolTile ? row_norm(rid_cur) : 0.f;
+    int32_t rid_cur = -1;
+    float rn_cur = 0.f;
+    if (tid < kPoolTile) {
+        sm.tnorm[2][tid] = INFINITY; sm.trow[2][tid] = -1;
+        rid_cur = pool_row(tid);
+        sm.sid[0][tid] = rid_cur;
+        rn_cur = row_norm(rid_cur);
+        rid_next = pool_row(kPoolTile + tid);
+    }
+    __syncthreads();
+    load_rows(sm.sid[0]);
     store_rows(0);
-    if (tid < kPoolTile) { sm.trow[0][tid] = rid_cur; sm.tnorm[0][tid] = rn_cur; }
-    load_ids(1);
+    if (tid < kPoolTile) { sm.trow[0][tid] = rid_cur; sm.tnorm[0][tid] = rn_cur; sm.sid[1][tid] = rid_next; }
     __syncthreads();
 
     floatx16 acc_prev;
@@ -549,13 +552,14 @@ __global__ void __launch_bounds__(256, 2) knn_fused_kernel(KnnArgs a)
 
     for (int t = 0; t < ntiles; ++t) {
         const int buf = t & 1;
-        wait_vmem();   // ids of the next tile, and any list rows stored by merges
-        // next tile: rows (ids arrived during the previous tile) and norms
-        load_rows();
-        rid_cur = rid_next;
-        rn_cur = tid < kPoolTile ? row_norm(rid_cur) : 0.f;
-        // tile after next: ids
-        load_ids(t + 2);
+        wait_vmem();   // ids of the tile after next, and any list rows stored by merges
+        // next tile: rows (their ids in LDS since the previous tile) and norms
+        load_rows(sm.sid[(t + 1) & 1]);
+        if (tid < kPoolTile) {
+            rid_cur = rid_next;
+            rn_cur = row_norm(rid_cur);
+            rid_next = pool_row((t + 2) * kPoolTile + tid);   // tile after next: ids
+        }
 
         // D[i][j] = sum_k pool[i][k] * query[j][k]; lane supplies A[i=lane%32][k=lane/32]
         // (pool row j, dim h*DH+s) and B[k=lane/32][j=lane%32] (query j, same dim).
@@ -599,7 +603,11 @@ __global__ void __launch_bounds__(256, 2) knn_fused_kernel(KnnArgs a)
         }
 
         store_rows(buf ^ 1);
-        if (tid < kPoolTile) { sm.trow[(t + 1) % 3][tid] = rid_cur; sm.tnorm[(t + 1) % 3][tid] = rn_cur; }
+        if (tid < kPoolTile) {
+            sm.trow[(t + 1) % 3][tid] = rid_cur;
+            sm.tnorm[(t + 1) % 3][tid] = rn_cur;
+            sm.sid[t & 1][tid] = rid_next;   // tile t + 2's ids
+        }
         __syncthreads();
         acc_prev = acc;
     }
@@ -664,6 +672,7 @@ struct KnnSmemI8Tiles {
     float tnorm[3][ROWS];
     int32_t trow[3][ROWS];
     int32_t thalf[3][ROWS];          // accumulator start: -floor(|p|^2 / 2) (L2), 0 (IP), kHalfPast past the end
+    int32_t sid[2][ROWS];            // the next stage's pool row ids (-1 past the end), for every thread's row requests
 };
 
 
@@ -778,22 +787,15 @@ knn_i8_kernel(KnnArgs a)
         return METRIC == 0 ? a.np[row] : 0.f;
     };
 
-    int32_t idn[U4_THREAD];
+    // a stage's pool ids: one per row by the threads < ST (two stages
+    // ahead), handed to every thread's row requests through LDS
     uint4 pre[U4_THREAD];
     int32_t rid_next = -1;
-    auto load_ids = [&](int t) {
+    auto load_rows = [&](const int32_t* ids) {
 #pragma unroll
         for (int u = 0; u < U4_THREAD; ++u) {
             const int e = tid + 256 * u;
-            idn[u] = e < U4_TILE ? pool_row(t * ST + e / U4_ROW) : -1;
-        }
-        if (tid < ST) rid_next = pool_row(t * ST + tid);
-    };
-    auto load_rows = [&]() {
-#pragma unroll
-        for (int u = 0; u < U4_THREAD; ++u) {
-            const int e = tid + 256 * u;
-            const int32_t id = idn[u];
+            const int32_t id = e < U4_TILE ? ids[e / U4_ROW] : -1;
             const uint4 v = *reinterpret_cast<const uint4*>(a.Xp8 + static_cast<int64_t>(id >= 0 ? id : 0) * DP +
                                                             16 * (e % U4_ROW));
             pre[u] = id >= 0 ? v : make_uint4(0u, 0u, 0u, 0u);
@@ -810,14 +812,22 @@ knn_i8_kernel(KnnArgs a)
     auto row_half = [&](int32_t row, float rn) -> int32_t {
         return row < 0 ? kHalfPast : -(static_cast<int32_t>(rn) >> 1);
     };
-    if (tid < ST) { sm.tnorm[2][tid] = INFINITY; sm.trow[2][tid] = -1; sm.thalf[2][tid] = kHalfPast; }
-    load_ids(0);
-    load_rows();
-    int32_t rid_cur = rid_next;
-    float rn_cur = tid < ST ? row_norm(rid_cur) : 0.f;
+    int32_t rid_cur = -1;
+    float rn_cur = 0.f;
+    if (tid < ST) {
+        sm.tnorm[2][tid] = INFINITY; sm.trow[2][tid] = -1; sm.thalf[2][tid] = kHalfPast;
+        rid_cur = pool_row(tid);
+        sm.sid[0][tid] = rid_cur;
+        rn_cur = row_norm(rid_cur);
+        rid_next = pool_row(ST + tid);
+    }
+    __syncthreads();
+    load_rows(sm.sid[0]);
     store_rows(0);
-    if (tid < ST) { sm.trow[0][tid] = rid_cur; sm.tnorm[0][tid] = rn_cur; sm.thalf[0][tid] = row_half(rid_cur, rn_cur); }
-    load_ids(1);
+    if (tid < ST) {
+        sm.trow[0][tid] = rid_cur; sm.tnorm[0][tid] = rn_cur; sm.thalf[0][tid] = row_half(rid_cur, rn_cur);
+        sm.sid[1][tid] = rid_next;
+    }
     __syncthreads();
 
     intx16 acc_prev;
@@ -840,10 +850,12 @@ knn_i8_kernel(KnnArgs a)
     for (int t = 0; t < ntiles; ++t) {
         const int buf = t & 1;
         wait_vmem();
-        load_rows();
-        rid_cur = rid_next;
-        rn_cur = tid < ST ? row_norm(rid_cur) : 0.f;
-        load_ids(t + 2);
+        load_rows(sm.sid[(t + 1) & 1]);
+        if (tid < ST) {
+            rid_cur = rid_next;
+            rn_cur = row_norm(rid_cur);
+            rid_next = pool_row((t + 2) * ST + tid);
+        }
 
 #pragma unroll
         for (int u = 0; u < SUB; ++u) {
@@ -876,6 +888,7 @@ knn_i8_kernel(KnnArgs a)
             sm.trow[(t + 1) % 3][tid] = rid_cur;
             sm.tnorm[(t + 1) % 3][tid] = rn_cur;
             sm.thalf[(t + 1) % 3][tid] = row_half(rid_cur, rn_cur);
+            sm.sid[t & 1][tid] = rid_next;   // stage t + 2's ids
         }
         __syncthreads();
     }
