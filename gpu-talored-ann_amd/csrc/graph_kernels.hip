@@ -1043,9 +1043,12 @@ __global__ void __launch_bounds__(kRevBinThreads) rev_bin_merge_kernel(const uin
 
 // ------------------------------------------------------------------ cross-round merge
 // top-M by (distance, id) of run U new, an id of new already present in run
-// dropped (src/bucket.cu:5021-5053, ties by id).  One wave per row; both
-// inputs ascending with (-1, +inf) padding at the end.
+// dropped (src/bucket.cu:5021-5053, ties by id).  One wave per row, each wave
+// taking rows gridDim.x * 4 apart with the next row's four input rows loaded
+// while it merges the current one; both inputs ascending with (-1, +inf)
+// padding at the end.
 constexpr int kMergeMaxM = 128;
+constexpr int kMergeBlocks = 2048;   // 8 blocks of 4 waves per CU
 __global__ void __launch_bounds__(256) merge_rounds_kernel(const int32_t* __restrict__ ri, const float* __restrict__ rd,
                                                            const int32_t* __restrict__ ni, const float* __restrict__ nd,
                                                            int64_t N, int M, int32_t* __restrict__ oi,
@@ -1054,54 +1057,79 @@ __global__ void __launch_bounds__(256) merge_rounds_kernel(const int32_t* __rest
     __shared__ float sRd[4][kMergeMaxM], sNd[4][kMergeMaxM];
     __shared__ int32_t sRi[4][kMergeMaxM], sNi[4][kMergeMaxM];
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + w;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * 4;
+    int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + w;
     if (row >= N) return;
-    float rdv[2], ndv[2];
-    int32_t riv[2], niv[2];
-    int nr = 0;
+    struct In {
+        float rd[2], nd[2];
+        int32_t ri[2], ni[2];
+    };
+    // a row's inputs (distances loaded with the ids, masked after)
+    auto load = [&](int64_t r, In& x) {
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
-        const int k = lane + 64 * e;
-        riv[e] = k < M ? ri[row * M + k] : -1;
-        rdv[e] = riv[e] >= 0 ? rd[row * M + k] : INFINITY;
-        niv[e] = k < M ? ni[row * M + k] : -1;
-        ndv[e] = niv[e] >= 0 ? nd[row * M + k] : INFINITY;
-        if (riv[e] < 0) riv[e] = INT_MAX;
-        if (k < kMergeMaxM) { sRd[w][k] = rdv[e]; sRi[w][k] = riv[e]; }
-        nr += __popcll(__ballot(riv[e] != INT_MAX));
-    }
-    wave_sync();
-    // drop new ids already in run; compact the survivors (order preserved)
-    bool keep[2];
-#pragma unroll
-    for (int e = 0; e < 2; ++e) {
-        bool dup = false;
-        if (niv[e] >= 0)
-            for (int q = 0; q < nr; ++q) dup |= (sRi[w][q] == niv[e]);
-        keep[e] = niv[e] >= 0 && !dup;
-    }
-    const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-    const unsigned long long k0 = __ballot(keep[0]), k1 = __ballot(keep[1]);
-    const int c0 = static_cast<int>(__popcll(k0));
-    const int nn = c0 + static_cast<int>(__popcll(k1));
-    const int cidx[2] = {static_cast<int>(__popcll(k0 & below)), c0 + static_cast<int>(__popcll(k1 & below))};
-#pragma unroll
-    for (int e = 0; e < 2; ++e)
-        if (keep[e]) { sNd[w][cidx[e]] = ndv[e]; sNi[w][cidx[e]] = niv[e]; }
-    wave_sync();
-#pragma unroll
-    for (int e = 0; e < 2; ++e) {
-        const int k = lane + 64 * e;
-        if (k < nr) {
-            const int pos = k + lower_bound_g(sNd[w], sNi[w], nn, rdv[e], riv[e]);
-            if (pos < M) { oi[row * M + pos] = riv[e]; od[row * M + pos] = rdv[e]; }
+        for (int e = 0; e < 2; ++e) {
+            const int k = lane + 64 * e;
+            const bool in = k < M;
+            x.ri[e] = in ? ri[r * M + k] : -1;
+            x.rd[e] = in ? rd[r * M + k] : INFINITY;
+            x.ni[e] = in ? ni[r * M + k] : -1;
+            x.nd[e] = in ? nd[r * M + k] : INFINITY;
         }
-        if (keep[e]) {
-            const int pos = cidx[e] + lower_bound_g(sRd[w], sRi[w], nr, ndv[e], niv[e]);
-            if (pos < M) { oi[row * M + pos] = niv[e]; od[row * M + pos] = ndv[e]; }
+    };
+    In cur;
+    load(row, cur);
+    for (; row < N; row += stride) {
+        In nxt;
+        if (row + stride < N) load(row + stride, nxt);
+        float rdv[2], ndv[2];
+        int32_t riv[2], niv[2];
+        int nr = 0;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int k = lane + 64 * e;
+            riv[e] = cur.ri[e];
+            rdv[e] = riv[e] >= 0 ? cur.rd[e] : INFINITY;
+            niv[e] = cur.ni[e];
+            ndv[e] = niv[e] >= 0 ? cur.nd[e] : INFINITY;
+            if (riv[e] < 0) riv[e] = INT_MAX;
+            if (k < kMergeMaxM) { sRd[w][k] = rdv[e]; sRi[w][k] = riv[e]; }
+            nr += __popcll(__ballot(riv[e] != INT_MAX));
         }
+        wave_sync();
+        // drop new ids already in run; compact the survivors (order preserved)
+        bool keep[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            bool dup = false;
+            if (niv[e] >= 0)
+                for (int q = 0; q < nr; ++q) dup |= (sRi[w][q] == niv[e]);
+            keep[e] = niv[e] >= 0 && !dup;
+        }
+        const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+        const unsigned long long k0 = __ballot(keep[0]), k1 = __ballot(keep[1]);
+        const int c0 = static_cast<int>(__popcll(k0));
+        const int nn = c0 + static_cast<int>(__popcll(k1));
+        const int cidx[2] = {static_cast<int>(__popcll(k0 & below)), c0 + static_cast<int>(__popcll(k1 & below))};
+#pragma unroll
+        for (int e = 0; e < 2; ++e)
+            if (keep[e]) { sNd[w][cidx[e]] = ndv[e]; sNi[w][cidx[e]] = niv[e]; }
+        wave_sync();
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int k = lane + 64 * e;
+            if (k < nr) {
+                const int pos = k + lower_bound_g(sNd[w], sNi[w], nn, rdv[e], riv[e]);
+                if (pos < M) { oi[row * M + pos] = riv[e]; od[row * M + pos] = rdv[e]; }
+            }
+            if (keep[e]) {
+                const int pos = cidx[e] + lower_bound_g(sRd[w], sRi[w], nr, ndv[e], niv[e]);
+                if (pos < M) { oi[row * M + pos] = niv[e]; od[row * M + pos] = ndv[e]; }
+            }
+        }
+        for (int p = nr + nn + lane; p < M; p += 64) { oi[row * M + p] = -1; od[row * M + p] = INFINITY; }
+        wave_sync();   // the lists are read before the next row overwrites them
+        cur = nxt;
     }
-    for (int p = nr + nn + lane; p < M; p += 64) { oi[row * M + p] = -1; od[row * M + p] = INFINITY; }
 }
 
 // ------------------------------------------------------------------ translate
@@ -1642,7 +1670,9 @@ void launch_merge_rounds(const int32_t* ri, const float* rd, const int32_t* ni, 
 {
     GT_REQUIRE(M >= 1 && M <= kMergeMaxM, "merge supports list length <= 128");
     if (N <= 0) return;
-    hipLaunchKernelGGL(merge_rounds_kernel, dim3(grid_for(N, 4)), dim3(256), 0, s, ri, rd, ni, nd, N, M, oi, od);
+    const int64_t g = std::min<int64_t>(grid_for(N, 4), kMergeBlocks);
+    hipLaunchKernelGGL(merge_rounds_kernel, dim3(static_cast<unsigned>(g)), dim3(256), 0, s, ri, rd, ni, nd, N, M,
+                       oi, od);
     GT_HIP(hipGetLastError());
 }
 
