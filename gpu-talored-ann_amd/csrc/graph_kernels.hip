@@ -1363,38 +1363,61 @@ void launch_sub_chain(const int32_t* nn, int K, const int64_t* base, const int32
 }
 
 // Row norms (the order of row_norms_kernel, so the same bits) plus, per
-// block of 4 rows, whether every value is an integer and their range:
-// part[3b] = 1 on a non-integer / non-finite value, part[3b+1] / part[3b+2]
-// = min / max as ints; int_range_final_kernel folds the blocks into out[3].
+// block of kNrBlockRows rows, whether every value is an integer and their
+// range: part[3b] = 1 on a non-integer / non-finite value, part[3b+1] /
+// part[3b+2] = min / max as ints; int_range_final_kernel folds the blocks
+// into out[3].  Each wave takes kNrBlockRows / 4 rows, kNrGroup at a time
+// with all their loads issued together.
+constexpr int kNrBlockRows = 64;
+constexpr int kNrGroup = 8;
 __global__ void __launch_bounds__(256) row_norms_range_kernel(const float* __restrict__ X, int64_t N, int Dp,
                                                               float* __restrict__ norms, int* __restrict__ part)
 {
     __shared__ int red[4][3];
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + w;
-    float s = 0.f, lo = INFINITY, hi = -INFINITY;
+    constexpr int WR = kNrBlockRows / 4;
+    const int64_t r0 = static_cast<int64_t>(blockIdx.x) * kNrBlockRows + w * WR;
+    float lo = INFINITY, hi = -INFINITY;
     bool bad = false;
-    if (row < N) {
+    for (int g = 0; g < WR; g += kNrGroup) {
+        float s[kNrGroup];
+#pragma unroll
+        for (int q = 0; q < kNrGroup; ++q) s[q] = 0.f;
         for (int c = lane; c < Dp; c += 64) {
-            const float v = X[row * Dp + c];
-            s = fmaf(v, v, s);
-            bad |= !(v == rintf(v)) || !(fabsf(v) < 1e9f);
-            lo = fminf(lo, v);
-            hi = fmaxf(hi, v);
+            float v[kNrGroup];
+#pragma unroll
+            for (int q = 0; q < kNrGroup; ++q) {
+                const int64_t row = r0 + g + q;
+                v[q] = row < N ? X[row * Dp + c] : 0.f;
+            }
+#pragma unroll
+            for (int q = 0; q < kNrGroup; ++q) {
+                if (r0 + g + q < N) {
+                    s[q] = fmaf(v[q], v[q], s[q]);
+                    bad |= !(v[q] == rintf(v[q])) || !(fabsf(v[q]) < 1e9f);
+                    lo = fminf(lo, v[q]);
+                    hi = fmaxf(hi, v[q]);
+                }
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < kNrGroup; ++q) {
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) s[q] += __shfl_xor(s[q], o);
+            if (lane == 0 && r0 + g + q < N) norms[r0 + g + q] = s[q];
         }
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
-        s += __shfl_xor(s, o);
         lo = fminf(lo, __shfl_xor(lo, o));
         hi = fmaxf(hi, __shfl_xor(hi, o));
     }
     const bool any_bad = __ballot(bad) != 0;
     if (lane == 0) {
-        if (row < N) norms[row] = s;
+        const bool any_row = r0 < N;
         red[w][0] = any_bad ? 1 : 0;
-        red[w][1] = row < N && !any_bad ? static_cast<int>(lo) : INT_MAX;
-        red[w][2] = row < N && !any_bad ? static_cast<int>(hi) : INT_MIN;
+        red[w][1] = any_row && !any_bad ? static_cast<int>(lo) : INT_MAX;
+        red[w][2] = any_row && !any_bad ? static_cast<int>(hi) : INT_MIN;
     }
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -1464,10 +1487,59 @@ __global__ void __launch_bounds__(256) quantize_norms_i8_kernel(const float* __r
     if (lane == 0) norms[row] = static_cast<float>(s);
 }
 
+// quantize_norms_i8_kernel over float4 loads: a block takes kQnBlockRows
+// contiguous rows as one flat run of float4s (four loads in flight per
+// thread); a row's |x|^2 is summed in LDS (integers, any order).
+constexpr int kQnBlockRows = 64;
+__global__ void __launch_bounds__(256) quantize_norms_i8_vec_kernel(const float4* __restrict__ src, int64_t N, int D,
+                                                                    int Dp, int shift, uint32_t* __restrict__ dst,
+                                                                    float* __restrict__ norms)
+{
+    __shared__ int sn[kQnBlockRows];
+    const int tid = threadIdx.x;
+    const int64_t r0 = static_cast<int64_t>(blockIdx.x) * kQnBlockRows;
+    const int rows = static_cast<int>(N - r0 < kQnBlockRows ? N - r0 : kQnBlockRows);
+    if (tid < kQnBlockRows) sn[tid] = 0;
+    __syncthreads();
+    const int F4 = Dp / 4;
+    const int total = rows * F4;
+    const int64_t base = r0 * F4;
+    const float fs = static_cast<float>(shift);
+    for (int e0 = tid; e0 < total; e0 += 256 * 4) {
+        float4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int e = e0 + 256 * u;
+            v[u] = e < total ? src[base + e] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int e = e0 + 256 * u;
+            if (e < total) {
+                const int row = e / F4, c0 = (e - row * F4) * 4;
+                const float x[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+                uint32_t packed = 0;
+                int sq = 0;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const float t = c0 + k < D ? rintf(x[k] - fs) : 0.f;
+                    const int q = static_cast<int>(fminf(fmaxf(t, -128.f), 127.f));
+                    sq += q * q;
+                    packed |= (static_cast<uint32_t>(q) & 0xffu) << (8 * k);
+                }
+                dst[base + e] = packed;
+                atomicAdd(&sn[row], sq);
+            }
+        }
+    }
+    __syncthreads();
+    if (tid < rows) norms[r0 + tid] = static_cast<float>(sn[tid]);
+}
+
 void launch_row_norms_range(const float* X, int64_t N, int Dp, float* norms, int* part, int* out, hipStream_t s)
 {
     if (N <= 0) return;
-    const int64_t nb = (N + 3) / 4;
+    const int64_t nb = (N + kNrBlockRows - 1) / kNrBlockRows;
     hipLaunchKernelGGL(row_norms_range_kernel, dim3(static_cast<unsigned>(nb)), dim3(256), 0, s, X, N, Dp, norms, part);
     hipLaunchKernelGGL(int_range_final_kernel, dim3(1), dim3(1024), 0, s, part, nb, out);
     GT_HIP(hipGetLastError());
@@ -1477,8 +1549,13 @@ void launch_quantize_norms_i8(const float* src, int64_t N, int D, int Dp, int sh
                               hipStream_t s)
 {
     if (N <= 0) return;
-    hipLaunchKernelGGL(quantize_norms_i8_kernel, dim3(grid_for(N, 4)), dim3(256), 0, s, src, N, D, Dp, shift, dst,
-                       norms);
+    if (Dp % 4 == 0 && reinterpret_cast<uintptr_t>(src) % 16 == 0 && reinterpret_cast<uintptr_t>(dst) % 4 == 0)
+        hipLaunchKernelGGL(quantize_norms_i8_vec_kernel, dim3(static_cast<unsigned>(ceil_div(N, kQnBlockRows))),
+                           dim3(256), 0, s, reinterpret_cast<const float4*>(src), N, D, Dp, shift,
+                           reinterpret_cast<uint32_t*>(dst), norms);
+    else
+        hipLaunchKernelGGL(quantize_norms_i8_kernel, dim3(grid_for(N, 4)), dim3(256), 0, s, src, N, D, Dp, shift,
+                           dst, norms);
     GT_HIP(hipGetLastError());
 }
 
