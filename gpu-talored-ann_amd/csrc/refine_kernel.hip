@@ -289,7 +289,7 @@ __global__ void __launch_bounds__(256) centroid_means_kernel(const float* __rest
 // (centroid, block) pair its output range; (3) it scatters them 64 at a
 // time in sample order, a lane's rank among the lanes of the same centroid
 // found by ballots over the wave's distinct keys.
-constexpr int kCsrChunk = 1024;
+constexpr int kCsrChunk = 256;
 
 __global__ void __launch_bounds__(64) csr_count_kernel(const int32_t* __restrict__ key, int64_t S, int C,
                                                        uint32_t* __restrict__ hist)
