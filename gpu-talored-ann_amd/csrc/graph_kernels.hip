@@ -1316,32 +1316,54 @@ __global__ void __launch_bounds__(256) segment_sort_kernel(const int32_t* __rest
 // one's neighbour list (nn: K entries per sub-centroid, positions within the
 // segment, -1 padded), else to the smallest unvisited one.  pos[base + i] =
 // place of sub-centroid i on the chain.  One wave per segment; lane 0 walks.
+constexpr int kSubChainLds = 1024 * 9;   // neighbour ids of a bucket's sub-centroids held in LDS
 __global__ void __launch_bounds__(64) sub_chain_kernel(const int32_t* __restrict__ nn, int K,
                                                        const int64_t* __restrict__ base,
                                                        const int32_t* __restrict__ count, int32_t* __restrict__ pos)
 {
     __shared__ uint32_t seen[32];   // up to 1024 sub-centroids
+    __shared__ int32_t tbl[kSubChainLds];
     const int g = blockIdx.x, lane = threadIdx.x;
     const int n = count[g];
     if (n <= 0) return;
     const int64_t b0 = base[g];
+    // the bucket's neighbour lists go to LDS first (the walk reads them one
+    // step after another)
+    const bool in_lds = n * K <= kSubChainLds;
+    if (in_lds)
+        for (int e = lane; e < n * K; e += 64) tbl[e] = nn[b0 * K + e];
     if (lane < 32) seen[lane] = 0u;
     __syncthreads();
-    if (lane == 0) {
-        int cur = 0;
-        for (int step = 0; step < n; ++step) {
+    // the whole wave takes each step: lanes < K test the K neighbours (the
+    // first unseen in list order wins), else lanes < 32 test a word of the
+    // seen bits each (the lowest unseen sub-centroid wins)
+    int cur = 0;
+    for (int step = 0; step < n; ++step) {
+        if (lane == 0) {
             seen[cur >> 5] |= 1u << (cur & 31);
             pos[b0 + cur] = step;
-            int nxt = -1;
-            for (int k = 0; k < K && nxt < 0; ++k) {
-                const int v = nn[(b0 + cur) * K + k];
-                if (v >= 0 && v < n && !((seen[v >> 5] >> (v & 31)) & 1u)) nxt = v;
-            }
-            for (int v = 0; nxt < 0 && v < n; ++v)
-                if (!((seen[v >> 5] >> (v & 31)) & 1u)) nxt = v;
-            if (nxt < 0) break;
-            cur = nxt;
         }
+        wave_sync();
+        int v = -1;
+        bool ok = false;
+        if (lane < K) {
+            v = in_lds ? tbl[cur * K + lane] : nn[(b0 + cur) * K + lane];
+            ok = v >= 0 && v < n && !((seen[v >> 5] >> (v & 31)) & 1u);
+        }
+        const uint64_t m = __ballot(ok);
+        if (m) {
+            cur = __shfl(v, __ffsll(static_cast<unsigned long long>(m)) - 1);
+            continue;
+        }
+        uint32_t fr = 0u;
+        if (lane < 32 && lane * 32 < n) {
+            const int left = n - lane * 32;
+            fr = ~seen[lane] & (left >= 32 ? ~0u : ((1u << left) - 1u));
+        }
+        const uint64_t fm = __ballot(fr != 0u);
+        if (!fm) break;
+        const int wl = __ffsll(static_cast<unsigned long long>(fm)) - 1;
+        cur = wl * 32 + __ffs(__shfl(fr, wl)) - 1;
     }
 }
 
@@ -1358,6 +1380,7 @@ void launch_sub_chain(const int32_t* nn, int K, const int64_t* base, const int32
                       hipStream_t s)
 {
     if (nseg <= 0) return;
+    GT_REQUIRE(K >= 1 && K <= 64, "sub-centroid chain: 1..64 neighbours (one lane each)");
     hipLaunchKernelGGL(sub_chain_kernel, dim3(static_cast<unsigned>(nseg)), dim3(64), 0, s, nn, K, base, count, pos);
     GT_HIP(hipGetLastError());
 }
