@@ -771,12 +771,12 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_wav
         // keys past a count and the rows past the last are masked below; the
         // buffer holds a wave's rows of slack past the last row)
         const uint64_t* src = cand + (row0 + rq) * kCollectCap + c0 + 2 * q;
-        uint4 x[8];
+        intx4 x[8];   // vector type: kept in registers (an array of uint4 structs went to scratch)
 #pragma unroll
-        for (int t = 0; t < 8; ++t) x[t] = *reinterpret_cast<const uint4*>(src + 4 * t * kCollectCap);
+        for (int t = 0; t < 8; ++t) x[t] = *reinterpret_cast<const intx4*>(src + 4 * t * kCollectCap);
         uint64_t* dst = st + rq * kSelStride + 2 * q;
 #pragma unroll
-        for (int t = 0; t < 8; ++t) *reinterpret_cast<uint4*>(dst + 4 * t * kSelStride) = x[t];
+        for (int t = 0; t < 8; ++t) *reinterpret_cast<intx4*>(dst + 4 * t * kSelStride) = x[t];
         wave_sync();
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
