@@ -1657,14 +1657,16 @@ void launch_sanitize(const int32_t* in, int64_t N, int M, uint32_t* out, hipStre
 }
 
 void launch_cagra_prune(const int32_t* G, int64_t N, int M, int K, uint32_t* out, unsigned long long* bad_row,
-                        hipStream_t s, const int32_t* order)
+                        hipStream_t s, const int32_t* order, bool flat_rows)
 {
     GT_REQUIRE(M >= 1 && M <= kPruneMaxM, "prune supports intermediate degree <= 128");
     if (N <= 0) return;
     PruneMap m{};
     m.order = order;
     const dim3 grid(static_cast<unsigned>(8 * ceil_div(ceil_div(N, int64_t(4)), int64_t(8))));
-    const bool buf = N * M * 4 < (int64_t(1) << 31);   // byte offsets and the buffer size in 31 bits
+    // buffer loads need byte offsets and the buffer size in 31 bits; larger
+    // tables (and flat_rows) take 64-bit addresses
+    const bool buf = !flat_rows && N * M * 4 < (int64_t(1) << 31);
     if (M <= 64 && buf)
         hipLaunchKernelGGL((cagra_prune_kernel<1, 0, true>), grid, dim3(256), 0, s, G, N, M, K, out, bad_row, m);
     else if (M <= 64)

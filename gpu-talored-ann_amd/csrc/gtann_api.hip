@@ -59,9 +59,17 @@ size_t search_lds_bytes(int CC, int efr, int Dp, int H);
 void launch_sanitize(const int32_t* in, int64_t N, int M, uint32_t* out, hipStream_t s);
 void launch_init_flags(unsigned long long* bad_row, int* err, hipStream_t s);
 void launch_cagra_prune(const int32_t* G, int64_t N, int M, int K, uint32_t* out, unsigned long long* bad_row,
-                        hipStream_t s, const int32_t* order = nullptr);
+                        hipStream_t s, const int32_t* order = nullptr, bool flat_rows = false);
 void launch_rev_count(const uint32_t* fwd, int64_t N, int K, uint32_t* deg, uint32_t* slot, int* err, hipStream_t s);
 void launch_exclusive_scan(const uint32_t* in, int64_t n, uint32_t* out, uint32_t* sums, hipStream_t s);
+void launch_kmpar_init(uint8_t* flag, float* mind, int64_t S, int64_t first, hipStream_t s);
+void launch_kmpar_psi(const float* mind, int64_t S, int64_t target, float* psi, hipStream_t s);
+void launch_kmpar_sample(const float* mind, uint8_t* flag, uint32_t* sel, int64_t S, const float* psi, float lk,
+                         uint64_t seed, hipStream_t s);
+void launch_kmpar_compact(const uint32_t* sel, const uint32_t* pos, const int32_t* rows, int64_t S, int32_t* out,
+                          hipStream_t s);
+void launch_kmpar_min(float* mind, const float* dnew, int64_t S, hipStream_t s);
+void launch_gather_rows_f32(const float* X, int Dp, const int32_t* ids, int64_t n, float* out, hipStream_t s);
 void launch_rev_scatter(const uint32_t* fwd, int64_t N, int K, const uint32_t* off, const uint32_t* slot,
                         unsigned long long* keys, hipStream_t s);
 int rev_bin_shift(int64_t N);
@@ -217,7 +225,7 @@ struct gt_ctx {
     hipStream_t stream = nullptr;
     std::string err;
     // named workspaces, grow-only (one slot per role, see gtann::Ws)
-    gtann::DevBuf ws[64];
+    gtann::DevBuf ws[80];
     gtann::HostBuf pinned[2];   // top-2 assignment downloads of two consecutive rounds
     gtann::HostBuf pin_lloyd;   // Lloyd steps: nearest centroids down, CSR up
     // host scratch of the bucketing, reused across calls (no page faults on
@@ -230,6 +238,7 @@ struct gt_ctx {
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
     void* scratch = nullptr;    // this device's fixed scratch array (gt_optimize_noalloc), or null
     std::string scratch_err;    // why it is null
+    gt_debug_opts dbg{};        // path selection (gt_set_debug)
 };
 
 namespace gtann {
@@ -240,9 +249,11 @@ enum Ws {
     W_TMP, W_OUT, W_IN, W_PROBE_I, W_PROBE_D, W_WORST, W_X8, W_NORMS8, W_C8, W_CNORMS8,
     W_SUBROWS, W_SUBID, W_SUBD, W_SUBOFF, W_MEMBERS2, W_SUBNN, W_SUBNND, W_SUBBASE, W_SUBCNT, W_CHAINPOS,
     W_LHIST, W_LOFFS, W_LSUMS, W_CAND, W_CANDCNT, W_STATS,
-    W_OOC_A, W_OOC_B, W_OOC_C, W_OOC_D, W_OOC_E, W_OOC_F, W_OOC_G, W_CR, W_CRNORMS, W_COUNT_
+    W_OOC_A, W_OOC_B, W_OOC_C, W_OOC_D, W_OOC_E, W_OOC_F, W_OOC_G, W_CR, W_CRNORMS,
+    W_KM_TRAIN, W_KM_MIND, W_KM_FLAG, W_KM_SEL, W_KM_POS, W_KM_SUMS, W_KM_NEW, W_KM_PSI, W_KM_P, W_KM_PN, W_KM_P8,
+    W_KM_PN8, W_KM_OI, W_KM_OD, W_COUNT_
 };
-static_assert(W_COUNT_ <= 64, "workspace slots");
+static_assert(W_COUNT_ <= 80, "workspace slots");
 
 struct Ctx {
     gt_ctx* c;
@@ -591,18 +602,66 @@ static std::vector<int32_t> sample_ids(int64_t N, int64_t C, uint64_t seed)
 // N, C and the seed, so a build draws every round's at its start, on a
 // worker thread, while the dataset is prepared).
 struct RoundSamples {
-    std::vector<int32_t> cid;     // C centroid rows
+    std::vector<int32_t> cid;     // C centroid rows (uniform seeds; empty with KMeans||)
     std::vector<int32_t> srows;   // Lloyd training subset (empty without Lloyd)
+    bool kmpar = false;           // seeds by KMeans|| on the device
+    std::vector<int32_t> train;   // KMeans|| training rows, ascending
+    int64_t first = 0;            // KMeans|| first candidate: index into train
+    uint64_t seed = 0;            // KMeans|| device draws and final subsample
 };
 
 static int64_t lloyd_subset(int64_t N, int64_t C) { return std::min<int64_t>(N, std::max<int64_t>(65536, 256 * C)); }
 
-static RoundSamples draw_round(int64_t N, int64_t C, int kmeans_iters, uint64_t seed)
+// The KMeans|| training subset (src/bucket.cu:8857-8880): every row kept
+// independently with probability frac (gaps between kept rows drawn from the
+// geometric distribution, so the draw costs one step per kept row); all rows
+// when frac >= 1 or when fewer than 4 C rows are kept.
+static std::vector<int32_t> bernoulli_rows(int64_t N, int64_t C, double frac, uint64_t seed)
+{
+    std::vector<int32_t> rows;
+    if (frac < 1.0) {
+        uint64_t st = seed * 0x9E3779B97F4A7C15ull + 1;
+        const double l1 = std::log1p(-frac);
+        rows.reserve(static_cast<size_t>(static_cast<double>(N) * frac * 1.05) + 16);
+        for (int64_t i = -1;;) {
+            const double u = (static_cast<double>(splitmix64(st) >> 11) + 0.5) * (1.0 / 9007199254740992.0);
+            const double gap = std::floor(std::log(u) / l1);
+            if (!(gap < static_cast<double>(N))) break;
+            i += 1 + static_cast<int64_t>(gap);
+            if (i >= N) break;
+            rows.push_back(static_cast<int32_t>(i));
+        }
+    }
+    if (static_cast<int64_t>(rows.size()) < std::min<int64_t>(N, 4 * C) || frac >= 1.0) {
+        rows.resize(static_cast<size_t>(N));
+        std::iota(rows.begin(), rows.end(), 0);
+    }
+    return rows;
+}
+
+static bool seeds_by_kmpar(const gt_build_params& p)
+{
+    return p.seeding == GT_SEED_KMEANS_PAR || (p.seeding == GT_SEED_AUTO && p.kmeans_iters <= 0);
+}
+
+static RoundSamples draw_round(int64_t N, int64_t C, const gt_build_params& p, uint64_t seed)
 {
     RoundSamples r;
     C = std::max<int64_t>(1, std::min<int64_t>(C, N));
-    r.cid = sample_ids(N, C, seed);
-    if (kmeans_iters > 0) r.srows = sample_ids(N, lloyd_subset(N, C), seed * 0x2545F4914F6CDD1Dull + 7);
+    if (seeds_by_kmpar(p)) {
+        // the reference pipeline trains on min(0.1, 1e7 / N) of the rows
+        // (sk/scripts/dataset_env.py:57)
+        const double frac = p.kmeans_train_fraction > 0.f ? static_cast<double>(p.kmeans_train_fraction)
+                                                           : std::min(0.1, 1e7 / static_cast<double>(N));
+        r.kmpar = true;
+        r.seed = seed * 0xD1B54A32D192ED03ull + 0x5851F42D4C957F2Dull;
+        r.train = bernoulli_rows(N, C, frac, seed);
+        uint64_t st = r.seed;
+        r.first = static_cast<int64_t>(splitmix64(st) % static_cast<uint64_t>(r.train.size()));
+    } else {
+        r.cid = sample_ids(N, C, seed);
+    }
+    if (p.kmeans_iters > 0) r.srows = sample_ids(N, lloyd_subset(N, C), seed * 0x2545F4914F6CDD1Dull + 7);
     return r;
 }
 
@@ -810,14 +869,6 @@ static void csr_from_assignment_keyed(const std::vector<int32_t>& bucket_of, con
     counting_sort_kv(bkt.data(), by_key.data(), N, C, b.members.data(), nullptr, nullptr, b.offsets);
 }
 
-// GTANN_LLOYD_HOST=1 groups the Lloyd samples on the host (download, counting
-// sort, upload) instead of on the device (comparisons; the same CSR)
-static bool lloyd_host_csr()
-{
-    const char* e = std::getenv("GTANN_LLOYD_HOST");
-    return e && e[0] == '1';
-}
-
 // Orders each bucket's members by their nearest sub-centroid (every
 // kSubSize-th member of the bucket, by the fused kernel with lists of one),
 // the sub-centroids themselves along a greedy nearest-neighbour chain: an
@@ -828,13 +879,6 @@ static bool lloyd_host_csr()
 // result does not depend on the order of the pool.
 constexpr int kSubSize = 128;     // members per sub-centroid
 constexpr int kSubMax = 1024;     // sub-centroids per bucket (LDS counters of the sort)
-// GTANN_SUB_ORDER=0 keeps the two-choice order (comparisons; same results)
-static bool sub_order_enabled()
-{
-    const char* e = std::getenv("GTANN_SUB_ORDER");
-    return !(e && e[0] == '0');
-}
-
 static void sub_order_members(Ctx& c, const DevMatrix& X, const Buckets& b, int metric, int32_t* d_members)
 {
     const int64_t C = static_cast<int64_t>(b.offsets.size()) - 1;
@@ -978,7 +1022,7 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
         if (b.uploaded) GT_HIP(hipEventRecord(b.uploaded, c.s));
         c.c->members_gen = b.gen;
     }
-    const bool sub_ordered = own && !seed_d && !compact && sub_order_enabled();
+    const bool sub_ordered = own && !seed_d && !compact && c.c->dbg.sub_order != 0;
     if (sub_ordered) sub_order_members(c, X, b, metric, d_members);
     CopyTaskH* d_tasks = c.ws<CopyTaskH>(W_TASKS, tasks.size());
     c.h2d(d_tasks, tasks.data(), tasks.size() * sizeof(CopyTaskH));
@@ -1034,14 +1078,13 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
     a.out_d = out_d;
     // lists of at most 64 keys on int8 rows: collect + select (every point
     // is the query of exactly one work item, so rows = N)
-    const bool collect = knn_collect_supported(a);
+    const bool collect = c.c->dbg.knn_collect != 0 && knn_collect_supported(a);
     if (collect) {
         // (+ one wave's rows of slack: the selection reads whole groups of
         // 32 rows and masks the rows past the last)
         a.cand = c.ws<uint64_t>(W_CAND, static_cast<size_t>(rows + kQueriesPerWave) * kCollectCap);
         a.cand_cnt = c.ws<int32_t>(W_CANDCNT, static_cast<size_t>(rows));
-        const char* se = std::getenv("GTANN_KNN_STATS");
-        if (tr.on && se && se[0] == '1') {   // counters of the collect launch (slow), printed below
+        if (tr.on && c.c->dbg.knn_stats) {   // counters of the collect launch (slow), printed below
             a.stats = c.ws<unsigned long long>(W_STATS, 4);
             GT_HIP(hipMemsetAsync(a.stats, 0, 4 * sizeof(unsigned long long), c.s));
         }
@@ -1083,6 +1126,125 @@ struct BucketPlan {
     int P = 0;
 };
 
+// KMeans|| seeds (src/bucket.cu:2833-3168): C distinct data points.  The
+// first candidate is a uniform training row; in each of 3 rounds every
+// training row that is not yet a candidate is taken with probability
+// l * C * d^2 / psi (l = 0.5, so about 1.5 C candidates over the rounds;
+// d = L2 distance to the nearest candidate, psi estimated from every
+// (S / 16384)-th row, src/bucket.cu:2933-2935, 3003-3016), and the new
+// candidates lower the distances (fused kNN, lists of one).  Then C of the
+// candidates are chosen uniformly (src/bucket.cu:3134-3168).  Where the
+// rounds leave C or fewer candidates the reference keeps them all and
+// builds fewer buckets; here uniform training rows that are not candidates
+// fill the C (the bucket count is a build parameter).  Returns the rows
+// ascending.
+static std::vector<int32_t> kmeans_par_seeds(Ctx& c, const DevMatrix& X, int64_t C, const RoundSamples& d)
+{
+    constexpr int kRounds = 3;
+    constexpr double kOversample = 1.5 / kRounds;
+    constexpr int64_t kPsiRows = 16384;
+    const int64_t S = static_cast<int64_t>(d.train.size());
+    GT_REQUIRE(S >= C && d.first >= 0 && d.first < S, "KMeans||: training subset smaller than the bucket count");
+    int32_t* d_train = c.ws<int32_t>(W_KM_TRAIN, static_cast<size_t>(S));
+    c.h2d(d_train, d.train.data(), static_cast<size_t>(S) * sizeof(int32_t));
+    float* mind = c.ws<float>(W_KM_MIND, static_cast<size_t>(S));
+    uint8_t* flag = c.ws<uint8_t>(W_KM_FLAG, static_cast<size_t>(S));
+    uint32_t* sel = c.ws<uint32_t>(W_KM_SEL, static_cast<size_t>(S));
+    uint32_t* pos = c.ws<uint32_t>(W_KM_POS, static_cast<size_t>(S) + 1);
+    uint32_t* sums = c.ws<uint32_t>(W_KM_SUMS, static_cast<size_t>(ceil_div(S, int64_t(1024)) + 2));
+    int32_t* d_new = c.ws<int32_t>(W_KM_NEW, static_cast<size_t>(S));
+    float* psi = c.ws<float>(W_KM_PSI, 1);
+    float* dnew = c.ws<float>(W_KM_OD, static_cast<size_t>(S));
+    int32_t* oi = c.ws<int32_t>(W_KM_OI, static_cast<size_t>(S));
+    launch_kmpar_init(flag, mind, S, d.first, c.s);
+    // the distances of every training row to the candidates of d_new[0..n)
+    auto lower = [&](int64_t n) {
+        DevMatrix P;
+        P.N = n;
+        P.D = X.D;
+        P.Dp = X.Dp;
+        float* rows = c.ws<float>(W_KM_P, static_cast<size_t>(n) * X.Dp);
+        float* norms = c.ws<float>(W_KM_PN, static_cast<size_t>(n));
+        launch_gather_rows_f32(X.data, X.Dp, d_new, n, rows, c.s);
+        launch_row_norms(rows, n, X.Dp, norms, c.s);
+        P.data = rows;
+        P.norms = norms;
+        if (X.data8) {
+            int8_t* r8 = c.ws<int8_t>(W_KM_P8, static_cast<size_t>(n) * X.Dp8);
+            float* n8 = c.ws<float>(W_KM_PN8, static_cast<size_t>(n));
+            launch_quantize_i8(rows, n, X.D, X.Dp8, X.shift, r8, c.s);   // exact: the rows are data points
+            launch_row_norms_i8(r8, n, X.Dp8, n8, c.s);
+            P.data8 = r8;
+            P.norms8 = n8;
+            P.Dp8 = X.Dp8;
+            P.shift = X.shift;
+            P.from_float = X.from_float;
+        }
+        P.iv_shift = X.iv_shift;
+        KnnJob j;
+        j.Q = &X;
+        j.P = &P;
+        j.q_rows = d_train;
+        j.nq = S;
+        j.np = n;
+        j.M = 1;
+        j.metric = GT_METRIC_L2;
+        j.exclude_self = false;
+        j.out_pos = true;
+        j.out_ids = oi;
+        j.out_d = dnew;
+        run_knn_flat(c, j, 1);
+        launch_kmpar_min(mind, dnew, S, c.s);
+    };
+    std::vector<int32_t> cand{d.train[static_cast<size_t>(d.first)]};
+    c.h2d(d_new, cand.data(), sizeof(int32_t));
+    lower(1);
+    const float lk = static_cast<float>(kOversample * static_cast<double>(C));
+    for (int it = 0; it < kRounds; ++it) {
+        launch_kmpar_psi(mind, S, kPsiRows, psi, c.s);
+        launch_kmpar_sample(mind, flag, sel, S, psi, lk, d.seed + static_cast<uint64_t>(it + 1) * 0xA0761D6478BD642Full,
+                            c.s);
+        launch_exclusive_scan(sel, S, pos, sums, c.s);
+        launch_kmpar_compact(sel, pos, d_train, S, d_new, c.s);
+        uint32_t n_new = 0;
+        c.d2h(&n_new, pos + S, sizeof(n_new));
+        c.sync();
+        if (n_new == 0) break;
+        const size_t old = cand.size();
+        cand.resize(old + n_new);
+        c.d2h(cand.data() + old, d_new, static_cast<size_t>(n_new) * sizeof(int32_t));
+        if (it + 1 < kRounds) lower(n_new);
+        c.sync();
+    }
+    uint64_t st = d.seed ^ 0x6A09E667F3BCC909ull;
+    std::vector<int32_t> cid;
+    if (static_cast<int64_t>(cand.size()) > C) {
+        // C of the candidates, uniformly (a partial Fisher-Yates shuffle)
+        for (int64_t i = 0; i < C; ++i) {
+            const int64_t j = i + static_cast<int64_t>(splitmix64(st) % static_cast<uint64_t>(cand.size() - i));
+            std::swap(cand[static_cast<size_t>(i)], cand[static_cast<size_t>(j)]);
+        }
+        cid.assign(cand.begin(), cand.begin() + C);
+    } else {
+        // every candidate, then uniform training rows that are not candidates
+        cid = cand;
+        std::vector<uint8_t> taken(static_cast<size_t>(S), 0);
+        for (int32_t r : cand)
+            taken[static_cast<size_t>(std::lower_bound(d.train.begin(), d.train.end(), r) - d.train.begin())] = 1;
+        std::vector<int32_t> rest;
+        rest.reserve(static_cast<size_t>(S) - cand.size());
+        for (int64_t i = 0; i < S; ++i)
+            if (!taken[static_cast<size_t>(i)]) rest.push_back(d.train[static_cast<size_t>(i)]);
+        for (int64_t i = 0; static_cast<int64_t>(cid.size()) < C; ++i) {
+            const int64_t j = i + static_cast<int64_t>(splitmix64(st) % static_cast<uint64_t>(rest.size() - i));
+            std::swap(rest[static_cast<size_t>(i)], rest[static_cast<size_t>(j)]);
+            cid.push_back(rest[static_cast<size_t>(i)]);
+        }
+    }
+    std::sort(cid.begin(), cid.end());
+    return cid;
+}
+
 static void bucket_device(Ctx& c, const DevMatrix& X, int64_t C, int nprobe, int metric, int kmeans_iters,
                           RoundSamples&& draws, HostBuf& pin, BucketPlan& bp, std::vector<int32_t>* cknn = nullptr,
                           int cknn_k = 0)
@@ -1092,8 +1254,9 @@ static void bucket_device(Ctx& c, const DevMatrix& X, int64_t C, int nprobe, int
     C = std::max<int64_t>(1, std::min<int64_t>(C, N));
     bp.N = N;
     bp.C = C;
-    bp.cid = std::move(draws.cid);
+    bp.cid = draws.kmpar ? kmeans_par_seeds(c, X, C, draws) : std::move(draws.cid);
     std::vector<int32_t>& cid = bp.cid;
+    GT_REQUIRE(static_cast<int64_t>(cid.size()) == C, "centroid draw");
     int32_t* d_cid = c.ws<int32_t>(W_PROWS, static_cast<size_t>(C));
     c.h2d(d_cid, cid.data(), static_cast<size_t>(C) * sizeof(int32_t));
 
@@ -1172,7 +1335,7 @@ static void bucket_device(Ctx& c, const DevMatrix& X, int64_t C, int nprobe, int
         int64_t* d_off = c.ws<int64_t>(W_OFF, static_cast<size_t>(C + 1));
         std::vector<int64_t> off;
         // the CSR on the device: no host round trip per iteration
-        const bool host_csr = lloyd_host_csr() || C > 16384;
+        const bool host_csr = c.c->dbg.lloyd_host_csr != 0 || C > 16384;
         const int64_t nh = C * csr_blocks(S);
         uint32_t* d_lhist = host_csr ? nullptr : c.ws<uint32_t>(W_LHIST, static_cast<size_t>(nh));
         uint32_t* d_loffs = host_csr ? nullptr : c.ws<uint32_t>(W_LOFFS, static_cast<size_t>(nh + 1));
@@ -1367,7 +1530,7 @@ static void prune_enqueue(Ctx& c, const StageFlags& f, const int32_t* G, int64_t
 {
     GT_REQUIRE(K >= 1 && K <= M, "output degree must be in [1, M]");
     launch_init_flags(f.bad, f.err, c.s);
-    launch_cagra_prune(G, N, M, K, out, f.bad, c.s, order);
+    launch_cagra_prune(G, N, M, K, out, f.bad, c.s, order, c.c->dbg.prune_flat_rows != 0);
 }
 
 static void prune_check(Ctx& c, const StageFlags& f)
@@ -1405,14 +1568,13 @@ static void reverse_merge_enqueue(Ctx& c, const StageFlags& f, const uint32_t* f
     // key regions (256-row bins, output degree <= 32: graphs up to 2^21
     // rows; where it is faster), the binned merge through global grouping
     // (up to 2^26 rows), the global-atomic CSR merge beyond.
-    // GTANN_REVMERGE_PATH=rv|binned|csr selects a path (tests; rv wherever
-    // it applies).
-    const char* force = std::getenv("GTANN_REVMERGE_PATH");
-    const std::string forced = force ? force : "";
+    // The context's revmerge_path selects one (tests; the two-kernel merge
+    // wherever it applies).
+    const int forced = c.c->dbg.revmerge_path;
     RvPlan rp{};
-    const int shift = forced == "csr" ? -1 : rev_bin_shift(N);
+    const int shift = forced == 3 ? -1 : rev_bin_shift(N);
     const bool rv_ok = rv_plan(N, K, rp);
-    const bool use_rv = forced == "rv" ? rv_ok : forced.empty() && rv_ok && rp.cshift == 8 && K <= 32;
+    const bool use_rv = forced == 1 ? rv_ok : forced == 0 && rv_ok && rp.cshift == 8 && K <= 32;
     if (use_rv) {
         const size_t nm = static_cast<size_t>(rp.nbins + 1) * rp.nblk;   // 16-bit run offsets
         uint32_t* part = c.ws<uint32_t>(W_KEYS, static_cast<size_t>(N) * K);
@@ -2021,6 +2183,7 @@ int gt_create(int device, gt_ctx** out)
     gt_ctx* c = new (std::nothrow) gt_ctx();
     if (!c) return GT_ENOMEM;
     c->device = device;
+    gt_debug_opts_default(&c->dbg);
     // A blocking stream: every call's work is ordered after work already
     // queued on the device's legacy null stream (PyTorch's default stream),
     // so a device buffer produced there asynchronously is complete before
@@ -2081,6 +2244,34 @@ void gt_build_params_default(gt_build_params* p)
     p->reverse_edges = 0;
     p->int_exact = 1;
     p->device_budget_mb = 0;
+    p->seeding = GT_SEED_AUTO;
+    p->kmeans_train_fraction = 0.f;
+}
+
+void gt_debug_opts_default(gt_debug_opts* o)
+{
+    if (!o) return;
+    *o = gt_debug_opts{};
+    o->knn_collect = 1;
+    o->revmerge_path = 0;
+    o->sub_order = 1;
+    o->lloyd_host_csr = 0;
+    o->prune_flat_rows = 0;
+    o->knn_stats = 0;
+}
+
+int gt_set_debug(gt_ctx* ctx, const gt_debug_opts* o)
+{
+    if (!ctx) return GT_EINVAL;
+    gt_debug_opts d;
+    gt_debug_opts_default(&d);
+    if (o) d = *o;
+    if (d.revmerge_path < 0 || d.revmerge_path > 3) {
+        ctx->err = "gt_set_debug: revmerge_path must be 0..3";
+        return GT_EINVAL;
+    }
+    ctx->dbg = d;
+    return GT_OK;
 }
 
 int gt_reverse_merge_chunked(gt_ctx* ctx, const uint32_t* fwd, int64_t N, int32_t K, int64_t device_budget_bytes,
@@ -2567,7 +2758,8 @@ int gt_optimize_noalloc(gt_ctx* ctx, const uint32_t* knn, int64_t N, int32_t M, 
         // the array keeps the previous call's contents: reset the flags (a
         // kernel, not a memset node); everything else is written before it is read
         launch_init_flags(bad, err, s);
-        launch_cagra_prune(reinterpret_cast<const int32_t*>(knn), N, M, K, fwd, bad, s);
+        launch_cagra_prune(reinterpret_cast<const int32_t*>(knn), N, M, K, fwd, bad, s, nullptr,
+                           ctx->dbg.prune_flat_rows != 0);
         unsigned long long h_bad = 0;
         GT_HIP(hipMemcpyAsync(&h_bad, bad, sizeof(h_bad), hipMemcpyDeviceToHost, s));
         GT_HIP(hipStreamSynchronize(s));
@@ -2895,7 +3087,7 @@ int gt_build_graph_ex(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtyp
         // every round's random draws, on a worker thread while the dataset is prepared
         std::future<std::vector<RoundSamples>> draws_job = std::async(std::launch::async, [N, C, p] {
             std::vector<RoundSamples> d;
-            for (int r = 0; r < p.rounds; ++r) d.push_back(draw_round(N, C, p.kmeans_iters, p.seed + static_cast<uint64_t>(r)));
+            for (int r = 0; r < p.rounds; ++r) d.push_back(draw_round(N, C, p, p.seed + static_cast<uint64_t>(r)));
             return d;
         });
         Timer tp;
@@ -2977,6 +3169,20 @@ int gt_build_graph_ex(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtyp
                 if (want_cknn) {
                     if (is_device_ptr(extras->centroid_knn)) c.h2d(extras->centroid_knn, cknn.data(), cknn.size() * sizeof(int32_t));
                     else std::memcpy(extras->centroid_knn, cknn.data(), cknn.size() * sizeof(int32_t));
+                }
+                c.sync();
+            }
+            if (r + 1 == p.rounds && extras && (extras->last_bucket || extras->last_centroids)) {
+                if (extras->last_bucket) {
+                    const std::vector<int32_t>& bo = c.c->h_bucket_of;
+                    if (is_device_ptr(extras->last_bucket)) c.h2d(extras->last_bucket, bo.data(), bo.size() * sizeof(int32_t));
+                    else std::memcpy(extras->last_bucket, bo.data(), bo.size() * sizeof(int32_t));
+                }
+                if (extras->last_centroids) {
+                    const std::vector<int32_t>& cid = plans[r & 1].cid;
+                    std::vector<int64_t> w(cid.begin(), cid.end());
+                    if (is_device_ptr(extras->last_centroids)) c.h2d(extras->last_centroids, w.data(), w.size() * sizeof(int64_t));
+                    else std::memcpy(extras->last_centroids, w.data(), w.size() * sizeof(int64_t));
                 }
                 c.sync();
             }

@@ -218,6 +218,49 @@ inline void write_bucket_process_order(const std::string& path, const int32_t* o
     f.close();
 }
 
+// Step 5 of bucket2 (src/bucket.cu:3434-3510): bucket_data.bin holds the
+// point ids of bucket 0, 1, ... as int32 (each bucket's ids ascending);
+// bucket_index.bin is int64 n_buckets, int64 N, then per bucket int64 byte
+// offset into bucket_data.bin and int32 count, packed (12 bytes a record).
+// bucket[i] is point i's bucket; ids outside [0, n_buckets) are left out.
+inline void write_bucket_files(const std::string& index_path, const std::string& data_path, const int32_t* bucket,
+                               int64_t N, int64_t n_buckets)
+{
+    std::vector<int64_t> count(static_cast<size_t>(n_buckets) + 1, 0);
+    for (int64_t i = 0; i < N; ++i)
+        if (bucket[i] >= 0 && bucket[i] < n_buckets) ++count[static_cast<size_t>(bucket[i]) + 1];
+    for (int64_t c = 0; c < n_buckets; ++c) count[static_cast<size_t>(c) + 1] += count[static_cast<size_t>(c)];
+    std::vector<int32_t> ids(static_cast<size_t>(count[static_cast<size_t>(n_buckets)]));
+    std::vector<int64_t> cur(count.begin(), count.end() - 1);
+    for (int64_t i = 0; i < N; ++i)
+        if (bucket[i] >= 0 && bucket[i] < n_buckets) ids[static_cast<size_t>(cur[static_cast<size_t>(bucket[i])]++)] =
+            static_cast<int32_t>(i);
+    File d(data_path, "wb");
+    d.write(ids.data(), ids.size() * sizeof(int32_t));
+    d.close();
+    std::vector<unsigned char> idx(16 + static_cast<size_t>(n_buckets) * 12);
+    std::memcpy(idx.data(), &n_buckets, 8);
+    std::memcpy(idx.data() + 8, &N, 8);
+    for (int64_t c = 0; c < n_buckets; ++c) {
+        const int64_t off = count[static_cast<size_t>(c)] * 4;
+        const int32_t cnt = static_cast<int32_t>(count[static_cast<size_t>(c) + 1] - count[static_cast<size_t>(c)]);
+        std::memcpy(idx.data() + 16 + c * 12, &off, 8);
+        std::memcpy(idx.data() + 16 + c * 12 + 8, &cnt, 4);
+    }
+    File f(index_path, "wb");
+    f.write(idx.data(), idx.size());
+    f.close();
+}
+
+// centroid_global_indices.bin: int64 n, int64[n] (src/bucket.cu:9561-9568)
+inline void write_centroid_indices(const std::string& path, const int64_t* ids, int64_t n)
+{
+    File f(path, "wb");
+    f.write(&n, sizeof(n));
+    f.write(ids, static_cast<size_t>(n) * sizeof(int64_t));
+    f.close();
+}
+
 inline std::vector<int32_t> read_bucket_process_order(const std::string& path)
 {
     File f(path, "rb");

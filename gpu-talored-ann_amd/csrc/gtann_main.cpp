@@ -194,9 +194,9 @@ int cmd_bucket2(int argc, char** argv)
     Args a(argc, argv,
            {"input,i", "output,o", "centroid-ratio", "seed", "knn-k", "nprobe", "neighbors-m", "iterations,t",
             "fused-optimize-degree", "kmeans-iters", "balance", "refine-passes", "refine-sample", "order-window",
-            "gpu-limit"},
+            "gpu-limit", "kmeans-train-fraction"},
            {"skip-dists", "skip-npy", "out-of-core"},
-           {"cpu-limit", "bucket-vec-buffer", "sample-rate", "use-pq", "kmeans-train-fraction", "bucket-mem-mb",
+           {"cpu-limit", "bucket-vec-buffer", "sample-rate", "use-pq", "bucket-mem-mb",
             "gpu-bucket-cache-mb", "pq-bits-start", "pq-bits-min", "search-iters", "cache-mb"});
     const std::string in = a.str("input"), root = a.str("output");
     const int knn_k = static_cast<int>(a.num("knn-k", 32));
@@ -226,6 +226,11 @@ int cmd_bucket2(int argc, char** argv)
     p.balance = static_cast<float>(a.real("balance", p.balance));
     p.refine_passes = static_cast<int32_t>(a.num("refine-passes", 0));
     p.refine_sample = static_cast<int32_t>(a.num("refine-sample", p.refine_sample));
+    if (a.has("kmeans-train-fraction")) {
+        p.kmeans_train_fraction = static_cast<float>(a.real("kmeans-train-fraction", 1.0));
+        if (!(p.kmeans_train_fraction > 0.f && p.kmeans_train_fraction <= 1.f))
+            throw Exit{1, "--kmeans-train-fraction must be in (0, 1]"};
+    }
     // --gpu-limit (bytes, 0 = auto): a device budget below the tables runs
     // the build out of core (the running table in host memory, chunked)
     if (a.has("gpu-limit") && a.num("gpu-limit", 0) > 0)
@@ -246,10 +251,14 @@ int cmd_bucket2(int argc, char** argv)
     std::vector<uint32_t> graph(K > 0 ? static_cast<size_t>(ds.N) * K : 0);
     std::vector<int32_t> round1(static_cast<size_t>(ds.N));
     std::vector<uint32_t> cknn(static_cast<size_t>(C) * ck);
+    std::vector<int32_t> last_bucket(static_cast<size_t>(ds.N));
+    std::vector<int64_t> last_cent(static_cast<size_t>(C));
     gt_build_extras ex{};
     ex.round1_bucket = round1.data();
     ex.centroid_knn = cknn.data();
     ex.centroid_knn_k = ck;
+    ex.last_bucket = last_bucket.data();
+    ex.last_centroids = last_cent.data();
     gt_build_stats st;
     Lib L;
     L.check(gt_build_graph_ex(L.ctx, ds.data(), ds.N, ds.D, dtype_code(ds.elem), &p, ids.data(), dists.data(),
@@ -302,6 +311,18 @@ int cmd_bucket2(int argc, char** argv)
         write_npy<int64_t>(dir + "/neighbors.npy", w.data(), ds.N, M);
     }
     if (K > 0) write_table<uint32_t>(dir + "/final_graph.bin", graph.data(), ds.N, K);   // original ids
+    {
+        // Step 5 (src/bucket.cu:9552-9568): the last round's buckets and
+        // centroid rows, in new ids like every later round of the reference
+        std::vector<uint32_t> perm(static_cast<size_t>(ds.N));
+        for (int64_t n = 0; n < ds.N; ++n) perm[inv[static_cast<size_t>(n)]] = static_cast<uint32_t>(n);
+        std::vector<int32_t> bucket_new(static_cast<size_t>(ds.N));
+        for (int64_t n = 0; n < ds.N; ++n) bucket_new[static_cast<size_t>(n)] = last_bucket[inv[static_cast<size_t>(n)]];
+        write_bucket_files(dir + "/bucket_index.bin", dir + "/bucket_data.bin", bucket_new.data(), ds.N, C);
+        std::vector<int64_t> cent_new(static_cast<size_t>(C));
+        for (int64_t c = 0; c < C; ++c) cent_new[static_cast<size_t>(c)] = perm[static_cast<size_t>(last_cent[static_cast<size_t>(c)])];
+        write_centroid_indices(dir + "/centroid_global_indices.bin", cent_new.data(), C);
+    }
     const double t_write = now() - t2;
     std::printf("[bucket2] N=%d D=%d buckets=%lld nprobe=%d M=%d K=%d t=%d order-window=%d\n", ds.N, ds.D,
                 static_cast<long long>(C), nprobe, M, K, T, window);

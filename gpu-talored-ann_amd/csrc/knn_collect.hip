@@ -834,11 +834,10 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_wav
 
 // ------------------------------------------------------------ host side
 
-// GTANN_KNN_COLLECT=0 keeps the merging kernel for every list (same results)
+// Shapes the collect + select kernels take (the context's knn_collect
+// option can keep the merging kernel for every list; same results)
 bool knn_collect_supported(const KnnArgs& a)
 {
-    const char* e = std::getenv("GTANN_KNN_COLLECT");
-    if (e && e[0] == '0') return false;
     if (!(a.M > 4 && a.M <= 64 && a.out_pos == 0 && a.Dp % 32 == 0)) return false;
     if (a.Xq8 && a.Xp8) return a.Dp <= 256;
     return a.Xq && a.Xp && a.Dp <= 160;   // longer fp32 rows: the query fragment leaves too few registers

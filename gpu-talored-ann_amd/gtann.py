@@ -27,8 +27,10 @@ EXPORTS = (
     "gt_reverse_merge", "gt_optimize", "gt_translate", "gt_build_params_default", "gt_build_graph",
     "gt_prune_occlusion", "gt_reverse_insert", "gt_search_params_default", "gt_search", "gt_build_graph_ex",
     "gt_bucket_order", "gt_bucket_reorder", "gt_permute_rows", "gt_remap_table", "gt_optimize_noalloc",
-    "gt_reverse_merge_chunked", "gt_prune_windowed",
+    "gt_reverse_merge_chunked", "gt_prune_windowed", "gt_debug_opts_default", "gt_set_debug",
 )
+SEEDING = {"auto": 0, "kmeans||": 1, "uniform": 2}
+REVMERGE_PATHS = {"auto": 0, "rv": 1, "binned": 2, "csr": 3}
 
 
 class GtannError(RuntimeError):
@@ -43,6 +45,15 @@ class BuildParams(C.Structure):
         ("K", C.c_int32), ("rounds", C.c_int32), ("refine_passes", C.c_int32), ("refine_sample", C.c_int32),
         ("kmeans_iters", C.c_int32), ("balance", C.c_float), ("seed", C.c_uint64),
         ("reverse_edges", C.c_int32), ("int_exact", C.c_int32), ("device_budget_mb", C.c_int32),
+        ("seeding", C.c_int32), ("kmeans_train_fraction", C.c_float),
+    ]
+
+
+class DebugOpts(C.Structure):
+    _fields_ = [
+        ("knn_collect", C.c_int32), ("revmerge_path", C.c_int32), ("sub_order", C.c_int32),
+        ("lloyd_host_csr", C.c_int32), ("prune_flat_rows", C.c_int32), ("knn_stats", C.c_int32),
+        ("reserved_", C.c_int32 * 2),
     ]
 
 
@@ -61,7 +72,7 @@ class BuildStats(C.Structure):
 
 class BuildExtras(C.Structure):
     _fields_ = [("round1_bucket", C.c_void_p), ("centroid_knn", C.c_void_p), ("centroid_knn_k", C.c_int32),
-                ("reserved_", C.c_int32)]
+                ("reserved_", C.c_int32), ("last_bucket", C.c_void_p), ("last_centroids", C.c_void_p)]
 
 
 class SearchParams(C.Structure):
@@ -146,6 +157,9 @@ def lib():
         L.gt_search_params_default.restype = None
         L.gt_search.argtypes = [vp, vp, i64, i32, C.c_int, vp, i32, vp, i64, vp, i32, C.POINTER(SearchParams),
                                 vp, vp, C.POINTER(SearchStats)]
+        L.gt_debug_opts_default.argtypes = [C.POINTER(DebugOpts)]
+        L.gt_debug_opts_default.restype = None
+        L.gt_set_debug.argtypes = [vp, C.POINTER(DebugOpts)]
         _lib = L
     return _lib
 
@@ -204,6 +218,8 @@ class BuildResult:
     stats: dict
     round1_bucket: object = None
     centroid_knn: object = None
+    last_bucket: object = None
+    last_centroids: object = None
 
 
 def _host_check(rc, what):
@@ -268,6 +284,21 @@ class Context:
         if rc != GT_OK:
             msg = lib().gt_last_error(self._h)
             raise GtannError(rc, f"{what}: {msg.decode() if msg else ''}")
+
+    def set_debug(self, **opts):
+        """Path selection (gt_set_debug): every choice gives the same results.
+        Keywords: knn_collect (bool), revmerge_path ('auto'|'rv'|'binned'|'csr'),
+        sub_order (bool), lloyd_host_csr (bool), prune_flat_rows (bool),
+        knn_stats (bool).  No keywords: the defaults."""
+        o = DebugOpts()
+        lib().gt_debug_opts_default(C.byref(o))
+        for k, v in opts.items():
+            if k == "revmerge_path":
+                v = REVMERGE_PATHS[v] if isinstance(v, str) else int(v)
+            elif k not in {f for f, _ in DebugOpts._fields_} or k == "reserved_":
+                raise ValueError(f"unknown debug option {k!r}")
+            setattr(o, k, int(v))
+        self._check(lib().gt_set_debug(self._h, C.byref(o)), "gt_set_debug")
 
     # ---------------------------------------------------------------- stages
 
@@ -396,14 +427,22 @@ class Context:
         return out
 
     def optimize_noalloc(self, knn, K, out=None):
-        """gt_optimize_noalloc: knn (N, M) int32/uint32 and out (N, K) must be
-        device tensors of this context's GPU; the library allocates nothing."""
+        """gt_optimize_noalloc: knn (N, M) int32/uint32 and out (N, K)
+        int32/uint32 must be contiguous device tensors of one GPU (this
+        context's); the library allocates nothing."""
+        import torch
+        ok_dt = (torch.int32, getattr(torch, "uint32", torch.int32))
         if not (_is_torch(knn) and knn.is_cuda):
             raise ValueError("optimize_noalloc needs a device tensor")
+        if knn.dim() != 2 or knn.dtype not in ok_dt or not knn.is_contiguous():
+            raise ValueError(f"knn must be a contiguous 2-D int32 tensor, got {knn.dtype} {tuple(knn.shape)}")
         N, M = knn.shape
         if out is None:
-            import torch
             out = torch.empty((N, K), dtype=torch.int32, device=knn.device)
+        if not (_is_torch(out) and out.is_cuda and out.device == knn.device):
+            raise ValueError("out must be a device tensor on knn's device")
+        if out.dtype not in ok_dt or tuple(out.shape) != (N, K) or not out.is_contiguous():
+            raise ValueError(f"out must be a contiguous int32 ({N}, {K}) tensor, got {out.dtype} {tuple(out.shape)}")
         self._check(lib().gt_optimize_noalloc(self._h, _ptr(knn), N, M, K, _ptr(out)), "gt_optimize_noalloc")
         return out
 
@@ -439,7 +478,8 @@ class Context:
 
     def build_graph(self, X, *, n_buckets=0, nprobe=1, M=64, K=32, rounds=2, refine_passes=0, refine_sample=16,
                     kmeans_iters=3, balance=0.8, seed=42, metric="l2", return_knn=True, reverse_edges=False,
-                    prune=True, centroid_knn_k=0, round1_bucket=False, int_exact=True, device_budget_mb=0):
+                    prune=True, centroid_knn_k=0, round1_bucket=False, int_exact=True, device_budget_mb=0,
+                    seeding="auto", kmeans_train_fraction=0.0, last_round=False, graph_out=None):
         if not _is_torch(X):
             X = np.ascontiguousarray(X)
         N, D = X.shape
@@ -450,7 +490,14 @@ class Context:
         p.balance, p.seed, p.reverse_edges = balance, seed, int(bool(reverse_edges))
         p.int_exact = int(bool(int_exact))
         p.device_budget_mb = int(device_budget_mb)
-        graph = _empty_like_input(X, (N, K), np.uint32) if prune else None
+        p.seeding = SEEDING[seeding] if isinstance(seeding, str) else int(seeding)
+        p.kmeans_train_fraction = float(kmeans_train_fraction)
+        if graph_out is not None:
+            if tuple(graph_out.shape) != (N, K) or np.dtype(str(graph_out.dtype).replace("torch.", "")).itemsize != 4:
+                raise ValueError(f"graph_out must be a ({N}, {K}) 32-bit array")
+            graph = graph_out
+        else:
+            graph = _empty_like_input(X, (N, K), np.uint32) if prune else None
         ids = _empty_like_input(X, (N, M), np.int32) if return_knn else None
         d = _empty_like_input(X, (N, M), np.float32) if return_knn else None
         st = BuildStats()
@@ -461,12 +508,16 @@ class Context:
         ex.round1_bucket = None if r1 is None else r1.ctypes.data
         ex.centroid_knn = None if ck is None else ck.ctypes.data
         ex.centroid_knn_k = centroid_knn_k
+        lb = np.empty(N, np.int32) if last_round else None
+        lc = np.empty(nb, np.int64) if last_round else None
+        ex.last_bucket = None if lb is None else lb.ctypes.data
+        ex.last_centroids = None if lc is None else lc.ctypes.data
         self._check(lib().gt_build_graph_ex(self._h, _ptr(X), N, D, _dtype_code(X), C.byref(p), _ptr(ids), _ptr(d),
                                             _ptr(graph), C.byref(st), C.byref(ex)), "gt_build_graph_ex")
         if graph is not None and not _is_torch(graph):
             graph = graph.view(np.uint32)
         return BuildResult(graph=graph, knn_ids=ids, knn_dists=d, stats=st.as_dict(), round1_bucket=r1,
-                           centroid_knn=ck)
+                           centroid_knn=ck, last_bucket=lb, last_centroids=lc)
 
     def permute_rows(self, X, inverse_perm):
         """out row n = X row inverse_perm[n] (data_reordered)."""

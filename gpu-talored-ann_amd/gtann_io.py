@@ -17,6 +17,10 @@ Byte layouts, identical with the reference's files:
 * ``bucket_offsets.bin``: ``int32 n_buckets, uint32[n_buckets+1]`` and
   ``bucket_process_order.bin``: ``int32 n, int32[n]`` (src/graph_io.hpp:178-244);
   ``centroid_knn.bin`` / ``centroid_pool.bin`` use the graph layout.
+* ``bucket_index.bin``: ``int64 n_buckets, int64 N``, then per bucket a
+  packed ``int64 byte offset, int32 count``; ``bucket_data.bin``: the int32
+  point ids of each bucket in turn; ``centroid_global_indices.bin``:
+  ``int64 n, int64[n]`` (src/bucket.cu:3434-3510, 9561-9568).
 """
 from __future__ import annotations
 
@@ -167,3 +171,24 @@ def read_bucket_process_order(path: str) -> np.ndarray:
     if a.size != n:
         raise ValueError(f"short payload: {path}")
     return a
+
+
+def read_bucket_files(index_path: str, data_path: str):
+    """(records, buckets): the (offset, count) records of bucket_index.bin and
+    the int32 ids of every bucket from bucket_data.bin."""
+    with open(index_path, "rb") as f:
+        nb, n = struct.unpack("<qq", f.read(16))
+        rec = np.frombuffer(f.read(12 * nb), dtype=[("off", "<i8"), ("count", "<i4")])
+    if len(rec) != nb:
+        raise ValueError(f"{index_path}: truncated index")
+    data = np.fromfile(data_path, dtype="<i4")
+    return rec, [data[o // 4:o // 4 + c] for o, c in zip(rec["off"].tolist(), rec["count"].tolist())]
+
+
+def read_centroid_indices(path: str) -> np.ndarray:
+    with open(path, "rb") as f:
+        (n,) = struct.unpack("<q", f.read(8))
+        v = np.frombuffer(f.read(8 * n), dtype="<i8")
+    if len(v) != n:
+        raise ValueError(f"{path}: truncated")
+    return v.astype(np.int64)

@@ -37,6 +37,7 @@ typedef struct gt_ctx gt_ctx;
 enum { GT_OK = 0, GT_EINVAL = -1, GT_ENOMEM = -2, GT_EDEVICE = -3, GT_EFEWCAND = -4 };
 enum { GT_DTYPE_F32 = 0, GT_DTYPE_U8 = 1, GT_DTYPE_I8 = 2 };
 enum { GT_METRIC_L2 = 0, GT_METRIC_IP = 1 };
+enum { GT_SEED_AUTO = 0, GT_SEED_KMEANS_PAR = 1, GT_SEED_UNIFORM = 2 };
 
 /* Context owning a device, a stream and reusable workspaces.
  * Replaces the GpuResidentKnn constructor/destructor
@@ -151,8 +152,10 @@ int gt_prune_windowed(gt_ctx* ctx, const int32_t* cand, int64_t N, int32_t M, co
 int gt_optimize(gt_ctx* ctx, const uint32_t* knn, int64_t N, int32_t M, int32_t K, uint32_t* out);
 
 /* gt_optimize without any allocation.  No counterpart in the reference: for
- * callers that cannot allocate device memory (code under HIP graph capture,
- * tight serving loops, harnesses that forbid hipMalloc).  knn (N x M) and out
+ * callers that cannot allocate device memory (tight serving loops, harnesses
+ * that forbid hipMalloc).  It is not capturable into a HIP graph: like every
+ * call here it runs on the context's stream and synchronises it (the row
+ * check reads its error flags back).  knn (N x M) and out
  * (N x K) must be device memory of the context's GPU (GT_EINVAL otherwise).
  * The forward graph, the error flags and the reverse merge's bins and keys
  * live in one fixed device array per GPU (GT_NOALLOC_SCRATCH_BYTES, held by
@@ -200,6 +203,13 @@ typedef struct gt_build_params {
                                the reverse merge); same table and graph.  The dataset stays on the
                                device and is not counted.  Excludes refine_passes and reverse_edges.
                                Replaces ChunkedKnnAccumulator (src/bucket.cu:5670-6369) */
+    int32_t seeding;        /* where the centroids start: GT_SEED_AUTO (default) = KMeans|| with
+                               kmeans_iters 0 (the reference's Step 2,
+                               src/bucket.cu:2833-3168), a uniform sample of rows
+                               before Lloyd iterations; GT_SEED_KMEANS_PAR / GT_SEED_UNIFORM force one */
+    float kmeans_train_fraction; /* KMeans|| trains on each row with this probability
+                               (--kmeans-train-fraction; all rows when fewer than 4 x buckets are
+                               kept); <= 0 (default): min(0.1, 1e7 / N), sk/scripts/dataset_env.py:57 */
 } gt_build_params;
 
 typedef struct gt_build_stats {
@@ -235,8 +245,10 @@ int gt_build_graph(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtype,
                    uint32_t* graph, gt_build_stats* stats);
 
 /* Optional outputs of gt_build_graph_ex about round 1, from which bucket2's
- * reorder artifacts are made.  C = the bucket count (params->n_buckets, or
- * N / 4000 when 0, clamped to [1, N]). */
+ * reorder artifacts are made, and about the last round, from which its
+ * Step-5 files are (src/bucket.cu:9552-9568).  C = the bucket count
+ * (params->n_buckets, or N / 4000 when 0, clamped to [1, N]).  Host or
+ * device memory. */
 typedef struct gt_build_extras {
     int32_t* round1_bucket;   /* N, or NULL: round-1 bucket of every point */
     uint32_t* centroid_knn;   /* C x centroid_knn_k, or NULL: exact self-kNN of the round-1
@@ -244,6 +256,10 @@ typedef struct gt_build_extras {
                                  centroid_self_knn_bf (src/bucket.cu:3241, 8976-8986) */
     int32_t centroid_knn_k;   /* <= min(C - 1, 128) */
     int32_t reserved_;
+    int32_t* last_bucket;     /* N, or NULL: last-round bucket of every point (bucket_data.bin) */
+    int64_t* last_centroids;  /* C, or NULL: the data point each last-round centroid is (KMeans||
+                                 seeds) or was seeded from before its Lloyd iterations
+                                 (centroid_global_indices.bin) */
 } gt_build_extras;
 
 /* gt_build_graph plus the round-1 extras (NULL = none). */
@@ -323,6 +339,29 @@ void gt_search_params_default(gt_search_params* p);
 int gt_search(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtype, const uint32_t* graph,
               int32_t degree, const void* Q, int64_t nq, const int32_t* entries, int32_t n_entry,
               const gt_search_params* params, int32_t* out_ids, float* out_d, gt_search_stats* stats);
+
+/* Path selection of a context, for tests and A/B comparisons.  Every choice
+ * gives the same results bit for bit; the defaults (gt_debug_opts_default)
+ * take the fastest path for each shape.  The reference selects its
+ * alternative paths with BUCKET2_* environment variables
+ * (src/bucket.cu:5375, :5507); here they are a typed per-context setting. */
+typedef struct gt_debug_opts {
+    int32_t knn_collect;     /* 1 (default): collect + select kNN where it applies; 0: merging kernels */
+    int32_t revmerge_path;   /* reverse merge: 0 (default) by shape, 1 two-kernel (where it applies),
+                                2 binned, 3 global-atomic CSR */
+    int32_t sub_order;       /* 1 (default): unseeded passes scan members by nearest sub-centroid;
+                                0: the two-choice order */
+    int32_t lloyd_host_csr;  /* 0 (default): Lloyd groups on the device; 1: on the host */
+    int32_t prune_flat_rows; /* 0 (default): the prune fetches neighbour rows by buffer loads when the
+                                table is below 2 GiB; 1: always the flat 64-bit addressing of larger
+                                tables */
+    int32_t knn_stats;       /* 1 with GTANN_TRACE set: per-launch counters of the collect kernel */
+    int32_t reserved_[2];
+} gt_debug_opts;
+
+void gt_debug_opts_default(gt_debug_opts* o);
+/* Sets the context's options (NULL: the defaults). */
+int gt_set_debug(gt_ctx* ctx, const gt_debug_opts* o);
 
 #ifdef __cplusplus
 }

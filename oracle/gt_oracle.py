@@ -241,6 +241,73 @@ def knn_bucketed(X, offsets, members, probe, M, metric=0):
     return ids, d
 
 
+def knn_bucketed_int(X, offsets, members, probe, M, query_chunk=512, threads=None):
+    """``knn_bucketed`` (L2) for integer rows of magnitude <= 255 with
+    D * 255^2 < 2^24 (int8 datasets, integer-valued float rows), restated
+    with BLAS for sizes the C loop cannot finish in seconds: every product
+    sum is an integer below 2^24, so the float32 GEMM is exact, the distance
+    |q|^2 + |p|^2 - 2 q.p is an exact integer, and the int64 key
+    (distance << 32 | id) is the same total order as the C oracle's
+    (distance, id).  Pool = the bucket's members, then those of its probe
+    buckets (out-of-range and repeated probes skipped), the query itself
+    excluded, as src/bucket.cu:5331-5347 + 4101-4265.  Query blocks run on
+    `threads` host threads (default: all), one BLAS thread each.  Pinned
+    against ``knn_bucketed`` in tests/test_oracle.py."""
+    from concurrent.futures import ThreadPoolExecutor
+    Xi = np.asarray(X)
+    if not np.issubdtype(Xi.dtype, np.integer):
+        if not np.array_equal(Xi, np.rint(Xi)):
+            raise ValueError("knn_bucketed_int needs integer-valued rows")
+    if np.abs(Xi).max(initial=0) > 255 or Xi.shape[1] * 255 ** 2 >= 1 << 24:
+        raise ValueError("knn_bucketed_int needs |x| <= 255 and D * 255^2 < 2^24")
+    Xf = np.ascontiguousarray(Xi, np.float32)
+    N = Xf.shape[0]
+    n2 = (Xi.astype(np.int64) ** 2).sum(1)
+    offsets = np.asarray(offsets, np.int64)
+    members = np.asarray(members, np.int64)
+    probe = np.asarray(probe, np.int64).reshape(len(offsets) - 1, -1)
+    nB = len(offsets) - 1
+    ids = np.full((N, M), -1, np.int32)
+    d = np.full((N, M), np.inf, np.float32)
+    big = np.iinfo(np.int64).max
+    pools = []
+    for b in range(nB):
+        segs = [b]
+        for pb in probe[b]:
+            if 0 <= pb < nB and pb not in segs:
+                segs.append(int(pb))
+        pools.append(np.concatenate([members[offsets[s]:offsets[s + 1]] for s in segs]))
+
+    def block(b, q0):
+        pool = pools[b]
+        q = members[offsets[b] + q0:min(offsets[b + 1], offsets[b] + q0 + query_chunk)]
+        kk = min(M, len(pool))
+        dot = (Xf[q] @ Xf[pool].T).astype(np.int64)
+        key = ((n2[q][:, None] + n2[pool][None, :] - 2 * dot) << 32) | pool[None, :]
+        key[np.arange(len(q)), q0 + np.arange(len(q))] = big   # the query itself (own rows come first)
+        if kk < len(pool):
+            key = np.partition(key, kk - 1, axis=1)[:, :kk]
+        key.sort(axis=1)
+        valid = key != big
+        ids[q, :kk] = np.where(valid, key & 0xFFFFFFFF, -1).astype(np.int32)
+        d[q, :kk] = np.where(valid, (key >> 32).astype(np.float32), np.float32(np.inf))
+
+    jobs = [(b, q0) for b in range(nB) for q0 in range(0, int(offsets[b + 1] - offsets[b]), query_chunk)]
+    try:
+        from threadpoolctl import threadpool_limits
+        limit = threadpool_limits(limits=1, user_api="blas")
+    except Exception:
+        limit = None
+    try:
+        with ThreadPoolExecutor(max_workers=threads or os.cpu_count() or 1) as ex:
+            for f in [ex.submit(block, b, q0) for b, q0 in jobs]:
+                f.result()
+    finally:
+        if limit is not None:
+            limit.unregister() if hasattr(limit, "unregister") else limit.__exit__(None, None, None)
+    return ids, d
+
+
 def merge_rounds(run_ids, run_d, new_ids, new_d):
     run_ids = np.ascontiguousarray(run_ids, np.int32)
     new_ids = np.ascontiguousarray(new_ids, np.int32)

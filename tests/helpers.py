@@ -1,5 +1,18 @@
 """Comparison helpers shared by the parity tests."""
+import contextlib
+
 import numpy as np
+
+
+@contextlib.contextmanager
+def debug_opts(ctx, **opts):
+    """The context's path selection (gt_set_debug) for the duration of a
+    block, back to the defaults afterwards."""
+    ctx.set_debug(**opts)
+    try:
+        yield
+    finally:
+        ctx.set_debug()
 
 
 def exact_dist(X, q, ids, metric="l2"):

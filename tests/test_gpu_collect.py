@@ -8,13 +8,12 @@ whose slots fill up is compacted to its M smallest keys.  Integer rows give
 exact distances, so every comparison here is bit-exact, ties included
 (order (distance, id)).
 """
-import os
 
 import numpy as np
 import pytest
 
 import gt_oracle as O
-from helpers import assert_knn_equal
+from helpers import assert_knn_equal, debug_opts
 
 pytestmark = pytest.mark.gpu
 
@@ -136,13 +135,10 @@ def test_collect_equals_merging_kernel(ctx):
     probe = _probe(rng, B, 1)
     a = ctx.knn_bucketed(X, off, mem, probe, M)
     b2 = ctx.knn_bucketed(X, off, mem, probe, M, running=a)
-    os.environ["GTANN_KNN_COLLECT"] = "0"
-    try:
+    with debug_opts(ctx, knn_collect=False):
         print("merging kernel", flush=True)
         c = ctx.knn_bucketed(X, off, mem, probe, M)
         c2 = ctx.knn_bucketed(X, off, mem, probe, M, running=c)
-    finally:
-        del os.environ["GTANN_KNN_COLLECT"]
     for x, y in ((a, c), (b2, c2)):
         np.testing.assert_array_equal(x[0], y[0])
         np.testing.assert_array_equal(x[1], y[1])

@@ -6,13 +6,12 @@ key formula), so every pass here equals the merging kernel's
 (GTANN_KNN_COLLECT=0) exactly -- ids and distances, ties included -- and the
 CPU oracle within the float tolerance of the fp32 path.
 """
-import os
 
 import numpy as np
 import pytest
 
 import gt_oracle as O
-from helpers import assert_knn_close
+from helpers import assert_knn_close, debug_opts
 
 pytestmark = pytest.mark.gpu
 
@@ -44,11 +43,8 @@ def _probe(rng, B, P):
 
 
 def _merging(ctx, *args, **kw):
-    os.environ["GTANN_KNN_COLLECT"] = "0"
-    try:
+    with debug_opts(ctx, knn_collect=False):
         return ctx.knn_bucketed(*args, **kw)
-    finally:
-        del os.environ["GTANN_KNN_COLLECT"]
 
 
 def _equal(x, y):
@@ -135,11 +131,8 @@ def test_f32_build_equals_merging_kernel(ctx):
     kw = dict(n_buckets=24, M=64, K=32, rounds=2, nprobe=1, metric="ip")
     print("f32 collect build", flush=True)
     a = ctx.build_graph(X, **kw)
-    os.environ["GTANN_KNN_COLLECT"] = "0"
-    try:
+    with debug_opts(ctx, knn_collect=False):
         b = ctx.build_graph(X, **kw)
-    finally:
-        del os.environ["GTANN_KNN_COLLECT"]
     np.testing.assert_array_equal(a.knn_ids, b.knn_ids)
     np.testing.assert_array_equal(a.knn_dists, b.knn_dists)
     np.testing.assert_array_equal(a.graph, b.graph)

@@ -69,6 +69,28 @@ def test_cli_bucket2_and_pipeline_tools(tmp_path, ctx):
     np.testing.assert_array_equal(io.read_vector_dists(d / "vector_dists.bin"), ex_d[inv])
     np.testing.assert_array_equal(np.load(d / "neighbors.npy"), ids_new.astype(np.int64))
 
+    # Step 5 files of the last round (src/bucket.cu:3434-3510, 9552-9568), in
+    # new ids: the same build's last-round buckets and centroid rows
+    last = ctx.build_graph(X, n_buckets=16, nprobe=15, M=64, K=32, rounds=1, kmeans_iters=0, prune=False,
+                           last_round=True)
+    assert (last.last_bucket[last.last_centroids] == np.arange(16)).all()   # KMeans|| seeds: data points
+    bnew = last.last_bucket[inv]
+    data_ref = np.concatenate([np.flatnonzero(bnew == c) for c in range(16)]).astype("<i4")
+    counts = np.bincount(bnew, minlength=16)
+    offs = np.concatenate([[0], np.cumsum(counts)[:-1]]) * 4
+    rec = np.zeros(16, dtype=[("off", "<i8"), ("count", "<i4")])   # packed: 12 bytes a record
+    rec["off"], rec["count"] = offs, counts
+    index_ref = np.array([16, N], "<i8").tobytes() + rec.tobytes()
+    assert (d / "bucket_data.bin").read_bytes() == data_ref.tobytes()
+    assert (d / "bucket_index.bin").read_bytes() == index_ref
+    cent_ref = np.concatenate([[16], perm[last.last_centroids]]).astype("<i8")
+    assert (d / "centroid_global_indices.bin").read_bytes() == cent_ref.tobytes()
+    bi, bd = io.read_bucket_files(d / "bucket_index.bin", d / "bucket_data.bin")
+    for c in range(16):
+        np.testing.assert_array_equal(bd[c], np.flatnonzero(bnew == c))
+    np.testing.assert_array_equal(io.read_centroid_indices(d / "centroid_global_indices.bin"),
+                                  perm[last.last_centroids])
+
     # optimize (prune + reverse merge) of the reordered table
     fwd_n, rc, _ = O.cagra_prune(O.sanitize(ids_new), 32)
     final_n = O.reverse_merge(fwd_n)

@@ -8,6 +8,7 @@ import pytest
 
 import gt_oracle as O
 import synth
+from helpers import debug_opts
 
 pytestmark = pytest.mark.gpu
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
@@ -112,42 +113,42 @@ def test_reverse_merge_random(ctx, N, K, hub):
     _assert_rows_equal(ctx.reverse_merge(F), O.reverse_merge(F), F)
 
 
-def test_reverse_merge_csr_path(ctx, monkeypatch):
+def test_reverse_merge_csr_path(ctx):
     """The global-atomic CSR path (graphs beyond the binned path's limits),
-    forced by GTANN_REVMERGE_PATH=csr, gives the same rows."""
-    monkeypatch.setenv("GTANN_REVMERGE_PATH", "csr")
-    for N, K in [(5000, 32), (3000, 48), (700, 1)]:
-        rng = np.random.default_rng(N + K)
-        F = rng.integers(0, N, size=(N, K)).astype(np.uint32)
-        F[rng.random((N, K)) < 0.2] = 3
-        _assert_rows_equal(ctx.reverse_merge(F), O.reverse_merge(F), F)
+    forced by revmerge_path='csr', gives the same rows."""
+    with debug_opts(ctx, revmerge_path="csr"):
+        for N, K in [(5000, 32), (3000, 48), (700, 1)]:
+            rng = np.random.default_rng(N + K)
+            F = rng.integers(0, N, size=(N, K)).astype(np.uint32)
+            F[rng.random((N, K)) < 0.2] = 3
+            _assert_rows_equal(ctx.reverse_merge(F), O.reverse_merge(F), F)
 
 
-def test_reverse_merge_two_kernel_path_forced(ctx, monkeypatch):
-    """The two-kernel merge wherever it applies (GTANN_REVMERGE_PATH=rv),
+def test_reverse_merge_two_kernel_path_forced(ctx):
+    """The two-kernel merge wherever it applies (revmerge_path='rv'),
     including the output degrees and bin widths the default leaves to the
     binned merge (K > 32, 2^11-row bins) and rows beyond its LDS capacity."""
-    monkeypatch.setenv("GTANN_REVMERGE_PATH", "rv")
-    for N, K, hub in [(3000, 48, True), (2000, 64, True), (70000, 48, False), (700, 1, False),
-                      (5000, 32, True), (60000, 32, True), (2200000, 2, False)]:
-        rng = np.random.default_rng(N * 11 + K)
-        F = rng.integers(0, N, size=(N, K)).astype(np.uint32)
-        if hub:
-            F[rng.random((N, K)) < 0.2] = 3
-            F[rng.random((N, K)) < 0.05] = 5
-        print(f"rv path N={N} K={K} hub={hub}", flush=True)
-        _assert_rows_equal(ctx.reverse_merge(F), O.reverse_merge(F), F)
+    with debug_opts(ctx, revmerge_path="rv"):
+        for N, K, hub in [(3000, 48, True), (2000, 64, True), (70000, 48, False), (700, 1, False),
+                          (5000, 32, True), (60000, 32, True), (2200000, 2, False)]:
+            rng = np.random.default_rng(N * 11 + K)
+            F = rng.integers(0, N, size=(N, K)).astype(np.uint32)
+            if hub:
+                F[rng.random((N, K)) < 0.2] = 3
+                F[rng.random((N, K)) < 0.05] = 5
+            print(f"rv path N={N} K={K} hub={hub}", flush=True)
+            _assert_rows_equal(ctx.reverse_merge(F), O.reverse_merge(F), F)
 
 
-def test_reverse_merge_binned_path(ctx, monkeypatch):
+def test_reverse_merge_binned_path(ctx):
     """The binned merge through global grouping (graphs between the two-kernel
-    merge's 2^11 * 8192 rows and 2^26), forced by GTANN_REVMERGE_PATH=binned."""
-    monkeypatch.setenv("GTANN_REVMERGE_PATH", "binned")
-    for N, K in [(5000, 32), (3000, 48), (700, 1), (20000, 16)]:
-        rng = np.random.default_rng(N * 7 + K)
-        F = rng.integers(0, N, size=(N, K)).astype(np.uint32)
-        F[rng.random((N, K)) < 0.2] = 3
-        _assert_rows_equal(ctx.reverse_merge(F), O.reverse_merge(F), F)
+    merge's 2^11 * 8192 rows and 2^26), forced by revmerge_path='binned'."""
+    with debug_opts(ctx, revmerge_path="binned"):
+        for N, K in [(5000, 32), (3000, 48), (700, 1), (20000, 16)]:
+            rng = np.random.default_rng(N * 7 + K)
+            F = rng.integers(0, N, size=(N, K)).astype(np.uint32)
+            F[rng.random((N, K)) < 0.2] = 3
+            _assert_rows_equal(ctx.reverse_merge(F), O.reverse_merge(F), F)
 
 
 @pytest.mark.parametrize("N,K", [(200000, 32), (70000, 64), (33, 8), (4097 * 32, 16)])
@@ -417,31 +418,30 @@ def test_build_graph_wide_probe_table(ctx):
     np.testing.assert_array_equal(res.knn_dists, ex_d)
 
 
-def test_sub_centroid_order_does_not_change_the_build(ctx, monkeypatch):
+def test_sub_centroid_order_does_not_change_the_build(ctx):
     """The unseeded own-bucket pass scans members ordered by nearest
     sub-centroid; the exact top-M does not depend on the order of the pool,
-    so the two-choice order (GTANN_SUB_ORDER=0) gives the same table and graph."""
+    so the two-choice order (sub_order=False) gives the same table and graph."""
     import synth
     X, _ = synth.generate("C2", n=40000)
     kw = dict(n_buckets=12, nprobe=2, M=64, K=32, rounds=2)
     a = ctx.build_graph(X, **kw)
-    monkeypatch.setenv("GTANN_SUB_ORDER", "0")
-    b = ctx.build_graph(X, **kw)
+    with debug_opts(ctx, sub_order=False):
+        b = ctx.build_graph(X, **kw)
+        c = ctx.build_graph(X.astype(np.float32) + 0.25, **kw)   # float rows: the fp32 kernel
     np.testing.assert_array_equal(a.knn_ids, b.knn_ids)
     np.testing.assert_array_equal(a.knn_dists, b.knn_dists)
     np.testing.assert_array_equal(a.graph, b.graph)
-    c = ctx.build_graph(X.astype(np.float32) + 0.25, **kw)   # float rows: the fp32 kernel
-    monkeypatch.setenv("GTANN_SUB_ORDER", "1")
     d = ctx.build_graph(X.astype(np.float32) + 0.25, **kw)
     np.testing.assert_array_equal(c.knn_ids, d.knn_ids)
     np.testing.assert_array_equal(c.graph, d.graph)
 
 
 @pytest.mark.parametrize("dtype,n_buckets", [("f32", 37), ("i8", 24), ("f32", 300)])
-def test_lloyd_device_csr_matches_host(ctx, monkeypatch, dtype, n_buckets):
+def test_lloyd_device_csr_matches_host(ctx, dtype, n_buckets):
     """The Lloyd steps group the sampled rows by nearest centroid on the
     device (stable counting sort); the host's counting sort
-    (GTANN_LLOYD_HOST=1) gives the same CSR, hence the same centroids and the
+    (lloyd_host_csr=True) gives the same CSR, hence the same centroids and the
     same build.  300 buckets over 40,000 rows leaves some centroids with few
     or no sampled members."""
     import synth
@@ -451,8 +451,8 @@ def test_lloyd_device_csr_matches_host(ctx, monkeypatch, dtype, n_buckets):
     print(f"lloyd csr {dtype} buckets={n_buckets}", flush=True)
     kw = dict(n_buckets=n_buckets, nprobe=1, M=32, K=16, rounds=2, kmeans_iters=3)
     a = ctx.build_graph(X, **kw)
-    monkeypatch.setenv("GTANN_LLOYD_HOST", "1")
-    b = ctx.build_graph(X, **kw)
+    with debug_opts(ctx, lloyd_host_csr=True):
+        b = ctx.build_graph(X, **kw)
     np.testing.assert_array_equal(a.knn_ids, b.knn_ids)
     np.testing.assert_array_equal(a.knn_dists, b.knn_dists)
     np.testing.assert_array_equal(a.graph, b.graph)

@@ -116,6 +116,35 @@ def test_knn_bucketed_matches_numpy_per_bucket():
         np.testing.assert_array_equal(d[q], dd[o].astype(np.float32))
 
 
+@pytest.mark.parametrize("N,B,P,M,D,dtype", [(3000, 6, 2, 64, 128, np.int8), (500, 5, 1, 100, 32, np.int8),
+                                             (60, 4, 3, 64, 8, np.int8), (1200, 7, 1, 32, 96, np.float32)])
+def test_knn_bucketed_int_matches_c_oracle(N, B, P, M, D, dtype):
+    """The BLAS restatement for integer rows (used at C5's bucket sizes) equals
+    the C loop bit for bit: duplicated rows (distance-0 ties broken by id),
+    pools shorter than M, an out-of-range probe, a bucket probing itself."""
+    rng = np.random.default_rng(N + M)
+    if dtype == np.int8:
+        X = rng.integers(-127, 128, size=(N, D)).astype(np.int8)
+    else:
+        X = rng.integers(0, 256, size=(N, D)).astype(np.float32)
+    X[5] = X[7]
+    X[11] = X[7]
+    off, mem, _ = _buckets(rng, N, B)
+    probe = np.stack([rng.permutation(np.delete(np.arange(B), b))[:P] for b in range(B)]).astype(np.int32)
+    probe[0, 0] = -1
+    probe[1, 0] = 1
+    a = O.knn_bucketed(X, off, mem, probe, M)
+    b = O.knn_bucketed_int(X, off, mem, probe, M, query_chunk=97)
+    np.testing.assert_array_equal(a[0], b[0])
+    np.testing.assert_array_equal(a[1].view(np.uint32), b[1].view(np.uint32))
+
+
+def test_knn_bucketed_int_rejects_non_integer_rows():
+    X = np.full((10, 4), 0.5, np.float32)
+    with pytest.raises(ValueError):
+        O.knn_bucketed_int(X, np.array([0, 10]), np.arange(10, dtype=np.int32), np.zeros((1, 0), np.int32), 4)
+
+
 def test_merge_rounds_union_dedup():
     rng = np.random.default_rng(8)
     X = rng.integers(0, 60, size=(300, 16)).astype(np.float32)
