@@ -74,7 +74,7 @@ def cpu_model():
     return "unknown"
 
 
-def cpu_baseline(X, knn_ids, K, n_sample):
+def cpu_baseline(X, knn_ids, K, n_sample, graph=None):
     """The reference's CPU path timed on this host: exact kNN as
     bd/build_knn.py:17-149 computes it (numpy: BLAS A @ B.T over 262,144-row
     base blocks, argpartition + argsort per block and per merge;
@@ -84,7 +84,8 @@ def cpu_baseline(X, knn_ids, K, n_sample):
     src/edge_chunk_accumulator.hpp compiled in place into oracle/_ref, rows over
     OpenMP threads as src/prune_windowed.cpp:97 runs them) on the GPU's whole
     kNN table; the CPU restatement in oracle/gt_oracle.c when the reference
-    build is absent."""
+    build is absent.  With the GPU's graph given, also reports whether it
+    equals the CPU path's prune + merge of the same table bit for bit."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import gt_oracle as O
     N = len(X)
@@ -105,10 +106,11 @@ def cpu_baseline(X, knn_ids, K, n_sample):
     t_prune = time.perf_counter() - t0
     t0 = time.perf_counter()
     if ref:
-        O.ref_reverse_merge_omp(fwd)
+        fin = O.ref_reverse_merge_omp(fwd)
     else:
-        O.reverse_merge(fwd)
+        fin = O.reverse_merge(fwd)
     t_merge = time.perf_counter() - t0
+    same = None if graph is None or rc != 0 else bool(np.array_equal(np.asarray(fin).view(np.uint32), graph))
     total = t_knn + t_prune + t_merge
     try:
         from threadpoolctl import threadpool_info
@@ -129,6 +131,7 @@ def cpu_baseline(X, knn_ids, K, n_sample):
                   f"on the whole table",
         "stages_s": {"knn_extrapolated": t_knn, "prune": t_prune, "reverse_merge": t_merge},
         "seconds_extrapolated": total,
+        "gpu_graph_identical_to_cpu_prune_merge": same,
     }
 
 
@@ -255,6 +258,26 @@ def host_to_host_leg(ctx, torch, X, kw, steps):
             "prepare_incl_upload_ms": s["t_prepare"] * 1e3, "download_ms": s["t_download"] * 1e3,
             "outputs": "graph (N x K uint32) + pre-prune table (N x M int32 ids, float32 distances), host memory",
             "input": "dataset as a host numpy array (pageable memory)"}, res
+
+
+def pinned_graph_leg(ctx, torch, X, kw, steps):
+    """Build seconds as the survey defines them: the dataset in (pinned)
+    host memory, the final N x K graph back in (pinned) host memory, no
+    pre-prune table; the upload and the download are inside the timed
+    region."""
+    N = len(X)
+    Xp = torch.from_numpy(X).pin_memory()
+    g = torch.empty((N, kw["K"]), dtype=torch.int32, pin_memory=True)
+    ctx.build_graph(Xp, return_knn=False, graph_out=g, **kw)
+    stats = []
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        stats.append(ctx.build_graph(Xp, return_knn=False, graph_out=g, **kw).stats)
+    wall = (time.perf_counter() - t0) / steps
+    s = mean_stats(stats)
+    return {"ms_per_step": wall * 1e3, "value": N / wall / 1e6, "unit": "Mpts/s",
+            "upload_and_prepare_ms": s["t_prepare"] * 1e3, "download_ms": s["t_download"] * 1e3,
+            "input": "dataset in pinned host memory", "output": "graph (N x K uint32) in pinned host memory"}, g
 
 
 def file_io_leg(X, cfg, args):
@@ -547,6 +570,10 @@ def main():
         h2h["identical_graph_to_device_run"] = bool((rh.graph == graph).all())
         out["host_to_host"] = h2h
         del rh
+        pg, gp = pinned_graph_leg(ctx, torch, X, kw, max(1, min(args.steps, 3)))
+        pg["identical_graph_to_device_run"] = bool((gp.numpy().view(np.uint32) == graph).all())
+        out["host_to_host_graph_pinned"] = pg
+        del gp
         out["file_io"] = file_io_leg(X, cfg, args)
         print("[bench] host-to-host and file-I/O legs done", file=sys.stderr, flush=True)
     if args.search_queries > 0:
@@ -559,8 +586,31 @@ def main():
     if names:
         out["configs"] = configs_leg(ctx, torch, names, max(1, min(args.steps, 2)))
     if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(X, knn, cfg.K, args.cpu_sample)
+        out["cpu_baseline"] = cpu_baseline(X, knn, cfg.K, args.cpu_sample, graph)
     ctx.close()
+    # the north star's gates in one short object at the end of the line
+    ns = {"build_ms": round(wall * 1e3, 3), "Mpts_s": round(N / wall / 1e6, 3),
+          "recall@32": round(rec["recall@32"], 4), "recall_gate_0.95": rec["recall@32"] >= 0.95,
+          "knn_kernel": roof["kernel"].split(" (")[0], "knn_frac_of_peak": round(roof["frac"], 4),
+          "knn_mfma_busy_pct": (tr or {}).get("mfma_busy_pct"),
+          "prune_frac_hbm": round(out["roofline_prune"]["frac"], 4),
+          "revmerge_frac_hbm": round(out["roofline_revmerge"]["frac"], 4)}
+    if "fp32_path" in out:
+        fp = out["fp32_path"]
+        ns["fp32_knn_frac_of_fp32_peak"] = round(fp["roofline"]["frac"], 4)
+        ns["fp32_mfma_busy_pct"] = (fp["roofline"].get("rocprof") or {}).get("mfma_busy_pct")
+        ns["fp32_identical_table_and_graph"] = fp["identical_table_and_graph"]
+    if "cpu_baseline" in out:
+        ns["graph_identical_to_cpu_prune_merge"] = out["cpu_baseline"]["gpu_graph_identical_to_cpu_prune_merge"]
+    if "host_to_host_graph_pinned" in out:
+        ns["host_to_host_graph_pinned_ms"] = round(out["host_to_host_graph_pinned"]["ms_per_step"], 3)
+    if "configs" in out:
+        ns["configs"] = {k: {"ms": round(v["ms_per_step"], 2), "recall@32": round(v["recall@32"], 4),
+                             "knn_frac": round(v["knn_roofline"]["frac"], 3),
+                             "prune_frac_hbm": round(v["prune_frac_hbm"], 3),
+                             "revmerge_frac_hbm": round(v["revmerge_frac_hbm"], 3)} for k, v in out["configs"].items()}
+    out["north_star"] = ns
+    print(f"[bench] north_star {json.dumps(ns)}", file=sys.stderr, flush=True)
     print(json.dumps(out))
 
 

@@ -25,15 +25,20 @@
 //     neighbouring bins -- whose runs and offsets share cache lines -- run on
 //     one XCD.  Fast path (a bin whose keys fit the registers and the LDS):
 //     every thread loads a strided share of the bin's keys (consecutive lanes
-//     read consecutive keys of the concatenated runs), counts them per row
-//     with one LDS atomic each (keeping the returned slot), and after a scan
-//     of the row counts writes each key, as (rank << nbits) | source, to its
-//     row's group in LDS.  Then one lane per row merges: the row's keys stream
-//     through a sorted register list of the L strongest non-protected keys (a
-//     key at or above the list's L-th costs one compare), and the output row
-//     is written straight to `out`.  Larger bins take passes over row ranges
-//     whose keys fit the LDS, re-reading the runs; a single row beyond the
-//     capacity, or one with a repeated source, goes to rv_slow_kernel.
+//     read consecutive keys of the concatenated runs), counts them per (row,
+//     rank group) with one LDS atomic each (keeping the returned slot; the
+//     counters overlay the run tables, which are dead by then), and after a
+//     scan writes each key, as (rank << nbits) | source, to its slot: each
+//     row's keys in ascending rank groups.  Then lane t merges row t: the
+//     keys stream through a sorted register list of the L strongest
+//     non-protected keys (a key at or above the list's L-th costs one
+//     compare), and the scan stops once the list's L-th is at or below the
+//     floor of the next key's group, so a lane reads about L keys whatever
+//     the row's in-degree; the output row is written straight to `out`.
+//     Bins beyond the fast path's LDS go to rv_big_kernel (larger blocks);
+//     larger ones still take passes over row ranges whose keys fit the LDS,
+//     re-reading the runs; a single row beyond the capacity, or one with a
+//     repeated source, goes to rv_slow_kernel.
 #include "gtann_common.hpp"
 
 #include <algorithm>
@@ -49,6 +54,9 @@ constexpr int kRvMaxBins = 8192;          // LDS counters of the scatter
 constexpr int kRvMaxBinShift = 11;        // rows per bin <= 2048
 constexpr int kRvKeysPerThread = 36;      // merge fast path: a bin's keys held in registers
 constexpr int kRvLdsPerBlock = 40960;     // merge LDS for 4 blocks per CU
+constexpr int kRvGroupBits = 2;
+constexpr int kRvGroups = 1 << kRvGroupBits;   // rank groups per row in the merge's LDS grouping
+constexpr bool kRvDefer = true;           // bins beyond the fast path go to rv_big_kernel
 constexpr int kRvBigThreads = 512;        // blocks of the deferred large bins
 
 // Exclusive scan of a[0..n) in LDS by a block of T threads; returns the
@@ -196,9 +204,10 @@ __device__ __forceinline__ void list_insert(uint32_t (&a)[LM], uint32_t x)
     a[0] = min(a[0], x);
 }
 
+// one of 64 bits per id (a filter ahead of exact compares; no multiply)
 __device__ __forceinline__ uint64_t bloom_bit(uint32_t v)
 {
-    return 1ull << ((v * 0x9E3779B1u) >> 26);
+    return 1ull << ((v ^ (v >> 6) ^ (v >> 12)) & 63u);
 }
 
 // Dedup-aware insertion into the lane's sorted list lst[0..L) (LM slots):
@@ -247,7 +256,7 @@ __device__ __forceinline__ void rv_offer_dedup(uint32_t (&lst)[(KMAX + 1) / 2], 
 // a copy of S padded with a value no source takes).
 template <int KMAX>
 __device__ __forceinline__ bool rv_merge_lane(const uint32_t (&fw)[KMAX], int K, const uint32_t* grouped, uint32_t n,
-                                              int nbits, uint32_t* st)
+                                              int nbits, uint32_t* st, uint32_t gfloor = 0u)
 {
     constexpr int LM = (KMAX + 1) / 2;
     constexpr int PM = KMAX / 2;
@@ -277,16 +286,24 @@ __device__ __forceinline__ bool rv_merge_lane(const uint32_t (&fw)[KMAX], int K,
         }
         list_insert<LM>(lst, x);
     };
-    // four LDS reads in flight per step
+    // four LDS reads in flight per step.  With the keys in ascending rank
+    // groups (gfloor != 0 masks a key down to its group's smallest key), the
+    // scan ends once the list's last slot is at or below the floor of the
+    // next key's group: no later key can enter.
     uint32_t e = 0;
     for (; e + 4 <= n; e += 4) {
         uint32_t x[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) x[u] = grouped[e + u];
+        if (gfloor && lst[LM - 1] <= (x[0] & gfloor)) break;
 #pragma unroll
         for (int u = 0; u < 4; ++u) offer(x[u]);
     }
-    for (; e < n; ++e) offer(grouped[e]);
+    for (; e < n; ++e) {
+        const uint32_t x = grouped[e];
+        if (gfloor && lst[LM - 1] <= (x & gfloor)) break;
+        offer(x);
+    }
     // R = the last L slots.  Rv: each slot's source if it is a real entry of
     // R, else a sentinel of its own (>= 2^31, no source takes it).
     uint32_t Rv[LM];
@@ -347,17 +364,18 @@ __device__ __forceinline__ bool rv_merge_lane(const uint32_t (&fw)[KMAX], int K,
     return true;
 }
 
-// rv_merge_lane for K == KMAX with the output row in registers: S = fw[0..P),
-// R from the keys, then the entries of O = fw[P..K) that are not the first
-// occurrence in O of an element of R, each placed by a compare network (no
-// dynamically indexed register or store), so that the caller writes the row
-// with vector stores.
+// rv_merge_lane for K == KMAX, writing the output row orow directly: S =
+// fw[0..P) and the list's sources as 16-byte stores (a short list leaves
+// its tail slots to the next stores), then, when R is short, the entries of
+// O = fw[P..K) that are not the first occurrence in O of an element of R as
+// single stores at their positions.  Nothing is written when R repeats a
+// source (false: the row goes to the slow kernel).
 template <int KMAX>
 __device__ __forceinline__ bool rv_merge_full(const uint32_t (&fw)[KMAX], const uint32_t* grouped, uint32_t n,
-                                              int nbits, uint32_t (&o)[KMAX])
+                                              int nbits, uint32_t* __restrict__ orow, uint32_t gfloor)
 {
     constexpr int P = KMAX / 2, L = KMAX - P;
-    static_assert(P == L, "even output degree");
+    static_assert(P == L && P % 4 == 0, "even output degree, whole 16-byte halves");
     const uint32_t gmask = (1u << nbits) - 1u;
     uint32_t S[P];
     uint64_t sbloom = 0;
@@ -380,15 +398,22 @@ __device__ __forceinline__ bool rv_merge_full(const uint32_t (&fw)[KMAX], const 
         }
         list_insert<L>(lst, x);
     };
+    // keys in ascending rank groups: stop once the list's last slot is at or
+    // below the floor of the next key's group (x & gfloor)
     uint32_t e = 0;
     for (; e + 8 <= n; e += 8) {
         uint32_t x[8];
 #pragma unroll
         for (int u = 0; u < 8; ++u) x[u] = grouped[e + u];
+        if (lst[L - 1] <= (x[0] & gfloor)) break;
 #pragma unroll
         for (int u = 0; u < 8; ++u) offer(x[u]);
     }
-    for (; e < n; ++e) offer(grouped[e]);
+    for (; e < n; ++e) {
+        const uint32_t x = grouped[e];
+        if (lst[L - 1] <= (x & gfloor)) break;
+        offer(x);
+    }
     uint32_t Rv[L];
     int nR = 0;
 #pragma unroll
@@ -402,36 +427,34 @@ __device__ __forceinline__ bool rv_merge_full(const uint32_t (&fw)[KMAX], const 
 #pragma unroll
         for (int m = 0; m < l; ++m) dup |= Rv[l] == Rv[m];
     if (dup) return false;
-    // destination of each entry of O that stays (-1: consumed by R)
-    uint64_t rbloom = 0;
+    uint4* o4 = reinterpret_cast<uint4*>(orow);
 #pragma unroll
-    for (int l = 0; l < L; ++l) rbloom |= l < nR ? bloom_bit(Rv[l]) : 0ull;
-    int dst[L];
-    int pos = P + nR;
+    for (int m = 0; m < P / 4; ++m) o4[m] = make_uint4(fw[4 * m], fw[4 * m + 1], fw[4 * m + 2], fw[4 * m + 3]);
 #pragma unroll
-    for (int k = P; k < KMAX; ++k) {
-        const uint32_t x = fw[k];
-        bool consumed = false;
-        if (rbloom & bloom_bit(x)) {
-            bool inR = false;
+    for (int m = 0; m < L / 4; ++m) o4[P / 4 + m] = make_uint4(Rv[4 * m], Rv[4 * m + 1], Rv[4 * m + 2], Rv[4 * m + 3]);
+    if (nR < L) {
+        // O's entries, minus the first occurrence of each element of R, fill
+        // positions P + nR .. K - 1
+        uint64_t rbloom = 0;
 #pragma unroll
-            for (int l = 0; l < L; ++l) inR |= Rv[l] == x;
-            bool earlier = false;
+        for (int l = 0; l < L; ++l) rbloom |= l < nR ? bloom_bit(Rv[l]) : 0ull;
+        int pos = P + nR;
 #pragma unroll
-            for (int q = P; q < k; ++q) earlier |= fw[q] == x;
-            consumed = inR && !earlier;
+        for (int k = P; k < KMAX; ++k) {
+            const uint32_t x = fw[k];
+            bool consumed = false;
+            if (rbloom & bloom_bit(x)) {
+                bool inR = false;
+#pragma unroll
+                for (int l = 0; l < L; ++l) inR |= Rv[l] == x;
+                bool earlier = false;
+#pragma unroll
+                for (int q = P; q < k; ++q) earlier |= fw[q] == x;
+                consumed = inR && !earlier;
+            }
+            if (!consumed && pos < KMAX) orow[pos] = x;
+            pos += consumed ? 0 : 1;
         }
-        dst[k - P] = consumed ? -1 : pos;
-        pos += consumed ? 0 : 1;
-    }
-#pragma unroll
-    for (int q = 0; q < P; ++q) o[q] = fw[q];
-#pragma unroll
-    for (int q = P; q < KMAX; ++q) {
-        uint32_t v = Rv[q - P];
-#pragma unroll
-        for (int k = 0; k < L; ++k) v = dst[k] == q ? fw[P + k] : v;
-        o[q] = v;
     }
     return true;
 }
@@ -584,12 +607,19 @@ __global__ void __launch_bounds__(256) rv_slow_kernel(const uint32_t* __restrict
     }
 }
 
-// LDS words before the row starts: the 16-bit run tables of the key loading,
-// later the row order and its class counters
-__host__ __device__ inline int rv_head_words(int nblk, int rows_max)
+// LDS words before the row starts: the 16-bit run tables of the key loading
+__host__ __device__ inline int rv_head_words(int nblk) { return (2 * nblk + 2) / 2; }
+
+// LDS words before the group buffer: the run tables and the row starts of
+// the general path (rows_max + 1), which the fast path's (row, rank group)
+// starts (rows_max * kRvGroups + 1, when a bin's rows fit one block of rp
+// threads) overlay once the keys are loaded
+__host__ __device__ inline int rv_pre_words(int nblk, int cshift, int rp)
 {
-    const int runs = (2 * nblk + 2) / 2;
-    return runs > rows_max + 65 ? runs : rows_max + 65;
+    const int rows_max = 1 << cshift;
+    const int general = rv_head_words(nblk) + rows_max + 1;
+    const int fast = rows_max <= rp ? rows_max * kRvGroups + 1 : 0;
+    return general > fast ? general : fast;
 }
 
 // The merge of bin b by one block of RP threads.  DEFER: a bin that does not
@@ -604,20 +634,24 @@ __device__ __forceinline__ void rv_merge_bin(int b, const uint32_t* __restrict__
                                              uint32_t* lds, uint32_t* wsum)
 {
     constexpr int KPT = kRvKeysPerThread;
+    constexpr int G = kRvGroups;
     const int t = threadIdx.x;
     const int rows_max = 1 << cshift;
     uint16_t* rs = reinterpret_cast<uint16_t*>(lds);                  // nblk + 1: run starts in the bin's keys
     uint16_t* roff = rs + nblk + 1;                                   // nblk: run offsets in the block regions
-    uint32_t* perm = lds;                                             // later: rows_max rows, longest first
-    uint32_t* pcls = lds + rows_max;                                  // and 65 class counters
-    uint32_t* rowst = lds + rv_head_words(nblk, rows_max);            // rows_max + 1: row starts
-    uint32_t* grouped = rowst + rows_max + 1;                         // cap: keys grouped by row
+    uint32_t* rowst = lds + rv_head_words(nblk);                      // rows_max + 1: row starts (general path)
+    uint32_t* cnt = lds;                                              // fast path: (row, group) starts
+    uint32_t* grouped = lds + rv_pre_words(nblk, cshift, RP);         // cap: keys grouped by row
     const int64_t j0 = static_cast<int64_t>(b) << cshift;
     const int rows = static_cast<int>(N - j0 < rows_max ? N - j0 : rows_max);
     const int hs = kbits + sbits;
     const uint32_t smask = (1u << sbits) - 1u;
     const uint32_t kmask = (1u << kbits) - 1u;
     const uint32_t region = static_cast<uint32_t>(spb * K);
+    // ranks per group: 2^gsh (G groups cover every rank below 2^kbits)
+    const int gsh = kbits > kRvGroupBits ? kbits - kRvGroupBits : 0;
+    // a converted key's group floor: the key with its rank's low gsh bits and its source cleared
+    const uint32_t gfloor = ~((1u << (nbits + gsh)) - 1u);
 
     // run lengths (in the group buffer's space), scanned into starts
     const uint16_t* m0 = meta + static_cast<int64_t>(b) * nblk;   // bin-major: this bin's and the next row
@@ -633,7 +667,7 @@ __device__ __forceinline__ void rv_merge_bin(int b, const uint32_t* __restrict__
         return (((key >> sbits) & kmask) << nbits) | (q * static_cast<uint32_t>(spb) + (key & smask));
     };
 
-    if (rows <= RP && T <= static_cast<uint32_t>(cap) && T <= static_cast<uint32_t>(RP * KPT)) {
+    if (rows_max <= RP && T <= static_cast<uint32_t>(cap) && T <= static_cast<uint32_t>(RP * KPT)) {
         for (int q = t; q <= nblk; q += RP) rs[q] = static_cast<uint16_t>(q < nblk ? grouped[q] : T);
         __syncthreads();
         // the run of every key (in the group buffer's space)
@@ -651,68 +685,46 @@ __device__ __forceinline__ void rv_merge_bin(int b, const uint32_t* __restrict__
             const uint32_t e = t + u * RP;
             key[u] = e < T ? part[qq[u] * region + roff[qq[u]] + (e - rs[qq[u]])] : 0u;
         }
-        __syncthreads();   // the run tables are dead: the groups go there, the row order in their head
-        for (int c = t; c <= 64; c += RP) pcls[c] = 0u;
-        uint32_t rsl[KPT];   // row << 16 | slot in the row's group
+        // the run tables are dead (every key is loaded): the (row, group)
+        // counters go there
+        __syncthreads();
+        for (int i = t; i <= rows * G; i += RP) cnt[i] = 0u;
+        __syncthreads();
+        // count per (row, rank group), keeping each key's slot: qq becomes
+        // (row * G + group) << 16 | slot, key the converted key
 #pragma unroll
         for (int u = 0; u < KPT; ++u) {
-            rsl[u] = 0u;
             if (t + u * RP < T) {
-                const uint32_t row = key[u] >> hs;
-                rsl[u] = (row << 16) | atomicAdd(&rowst[row], 1u);
+                const uint32_t rg = (key[u] >> hs) * G + (((key[u] >> sbits) & kmask) >> gsh);
+                const uint32_t slot = atomicAdd(&cnt[rg], 1u);
                 key[u] = convert(key[u], qq[u]);
+                qq[u] = (rg << 16) | slot;
             }
         }
         __syncthreads();
-        block_exclusive_scan<RP>(rowst, rows, wsum);
+        block_exclusive_scan<RP>(cnt, rows * G, wsum);
 #pragma unroll
         for (int u = 0; u < KPT; ++u)
-            if (t + u * RP < T) grouped[rowst[rsl[u] >> 16] + (rsl[u] & 0xFFFFu)] = key[u];
-        if (t == 0) rowst[rows] = T;
+            if (t + u * RP < T) grouped[cnt[qq[u] >> 16] + (qq[u] & 0xFFFFu)] = key[u];
+        // the lane's forward row, requested before the barrier
+        const int64_t j = j0 + t;
+        uint32_t fw[KMAX];
+        if (t < rows) rv_load_row<KMAX>(fwd + j * K, K, fw);
+        if (t == 0) cnt[rows * G] = T;
         __syncthreads();
-        // lanes take the rows longest first (by classes of key counts), so
-        // that a wave's loop runs about as long as each of its rows
-        uint32_t cls = 0u, cslot = 0u;
+        // lane t merges row t: its keys in ascending rank groups, so the
+        // scan ends after about L keys whatever the row's in-degree
         if (t < rows) {
-            const uint32_t n = rowst[t + 1] - rowst[t];
-            cls = 63u - (n < 63u ? n : 63u);
-            cslot = atomicAdd(&pcls[cls], 1u);
-        }
-        __syncthreads();
-        if (t < 64) {
-            const uint32_t c = pcls[t];
-            uint32_t inc = c;
-#pragma unroll
-            for (int o = 1; o < 64; o <<= 1) {
-                const uint32_t x = __shfl_up(inc, o);
-                if (t >= o) inc += x;
-            }
-            pcls[t] = inc - c;
-        }
-        __syncthreads();
-        if (t < rows) perm[pcls[cls] + cslot] = static_cast<uint32_t>(t);
-        __syncthreads();
-        if (t < rows) {
-            const int r = static_cast<int>(perm[t]);
-            const int64_t j = j0 + r;
-            uint32_t fw[KMAX];
-            rv_load_row<KMAX>(fwd + j * K, K, fw);
-            const uint32_t* g = grouped + rowst[r];
-            const uint32_t n = rowst[r + 1] - rowst[r];
+            const uint32_t g0 = cnt[t * G];
+            const uint32_t* g = grouped + g0;
+            const uint32_t n = cnt[(t + 1) * G] - g0;
             bool ok;
             if (K == KMAX) {
-                uint32_t o[KMAX];
-                ok = rv_merge_full<KMAX>(fw, g, n, nbits, o);
-                if (ok) {
-                    uint4* d4 = reinterpret_cast<uint4*>(out + j * K);
-#pragma unroll
-                    for (int m = 0; m < KMAX / 4; ++m)
-                        d4[m] = make_uint4(o[4 * m], o[4 * m + 1], o[4 * m + 2], o[4 * m + 3]);
-                }
+                ok = rv_merge_full<KMAX>(fw, g, n, nbits, out + j * K, gfloor);
             } else {
-                ok = rv_merge_lane<KMAX>(fw, K, g, n, nbits, out + j * K);
+                ok = rv_merge_lane<KMAX>(fw, K, g, n, nbits, out + j * K, gfloor);
             }
-            if (!ok) slow_rows[atomicAdd(slow_count, 1u)] = (static_cast<uint32_t>(b) << 11) | static_cast<uint32_t>(r);
+            if (!ok) slow_rows[atomicAdd(slow_count, 1u)] = (static_cast<uint32_t>(b) << 11) | static_cast<uint32_t>(t);
         }
         return;
     }
@@ -730,34 +742,34 @@ __device__ __forceinline__ void rv_merge_bin(int b, const uint32_t* __restrict__
     uint32_t* gbuf = grouped + nblk + 1;
     const int gcap = cap - nblk - 1;
     __syncthreads();
-    // the runs of G keys by G interleaved binary searches (the last run
-    // starting at or before each key), then the G loads
-    constexpr int G = 8;   // keys loaded together per thread
+    // the runs of GL keys by GL interleaved binary searches (the last run
+    // starting at or before each key), then the GL loads
+    constexpr int GL = 8;   // keys loaded together per thread
     int top = 1;
     while (2 * top <= nblk) top *= 2;
-    auto load_keys = [&](uint32_t e0, uint32_t (&kk)[G], uint32_t (&qq)[G]) {
-        int pos[G];
+    auto load_keys = [&](uint32_t e0, uint32_t (&kk)[GL], uint32_t (&qq)[GL]) {
+        int pos[GL];
 #pragma unroll
-        for (int u = 0; u < G; ++u) pos[u] = 0;
+        for (int u = 0; u < GL; ++u) pos[u] = 0;
         for (int w = top; w > 0; w >>= 1) {
 #pragma unroll
-            for (int u = 0; u < G; ++u) {
+            for (int u = 0; u < GL; ++u) {
                 const int c = pos[u] + w;
                 if (c < nblk && rs32[c] <= e0 + u * RP) pos[u] = c;
             }
         }
 #pragma unroll
-        for (int u = 0; u < G; ++u) {
+        for (int u = 0; u < GL; ++u) {
             const uint32_t e = e0 + u * RP;
             qq[u] = static_cast<uint32_t>(pos[u]);
             kk[u] = e < T ? part[qq[u] * region + roff[pos[u]] + (e - rs32[pos[u]])] : 0u;
         }
     };
-    for (uint32_t e0 = t; e0 < T; e0 += G * RP) {
-        uint32_t kk[G], qq[G];
+    for (uint32_t e0 = t; e0 < T; e0 += GL * RP) {
+        uint32_t kk[GL], qq[GL];
         load_keys(e0, kk, qq);
 #pragma unroll
-        for (int u = 0; u < G; ++u)
+        for (int u = 0; u < GL; ++u)
             if (e0 + u * RP < T) atomicAdd(&rowst[kk[u] >> hs], 1u);
     }
     __syncthreads();
@@ -782,11 +794,11 @@ __device__ __forceinline__ void rv_merge_bin(int b, const uint32_t* __restrict__
             continue;
         }
         // placement: rowst[r] becomes the end of row r (= the old start of row r + 1)
-        for (uint32_t e0 = t; e0 < T; e0 += G * RP) {
-            uint32_t kk[G], qq[G];
+        for (uint32_t e0 = t; e0 < T; e0 += GL * RP) {
+            uint32_t kk[GL], qq[GL];
             load_keys(e0, kk, qq);
 #pragma unroll
-            for (int u = 0; u < G; ++u) {
+            for (int u = 0; u < GL; ++u) {
                 const int row = static_cast<int>(kk[u] >> hs);
                 if (e0 + u * RP < T && row >= r0 && row < r1)
                     gbuf[atomicAdd(&rowst[row], 1u) - base] = convert(kk[u], qq[u]);
@@ -822,7 +834,7 @@ __global__ void __launch_bounds__(RP) rv_merge_kernel(const uint32_t* __restrict
     const int per_xcd = (nbins + 7) / 8;
     const int b = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
     if (b >= nbins) return;
-    rv_merge_bin<KMAX, RP, true>(b, fwd, N, K, nblk, spb, cshift, nbins, kbits, sbits, nbits, part, meta, out, cap,
+    rv_merge_bin<KMAX, RP, kRvDefer>(b, fwd, N, K, nblk, spb, cshift, nbins, kbits, sbits, nbits, part, meta, out, cap,
                                  slow_rows, slow_count, big_bins, lds, wsum);
 }
 
@@ -870,9 +882,10 @@ static int bits_for(int64_t n)   // bits of the values 0 .. n-1
     return b;
 }
 
-size_t rv_merge_lds(const RvPlan& p)
+// LDS of a merge block of rp threads with the plan's group buffer
+size_t rv_merge_lds(const RvPlan& p, int rp)
 {
-    const size_t words = static_cast<size_t>(rv_head_words(p.nblk, 1 << p.cshift)) + (size_t(1) << p.cshift) + 1 + p.cap;
+    const size_t words = static_cast<size_t>(rv_pre_words(p.nblk, p.cshift, rp)) + p.cap;
     return words * sizeof(uint32_t);
 }
 
@@ -898,16 +911,18 @@ bool rv_plan(int64_t N, int K, RvPlan& p)
     RvPlan q = p;
     q.cap = 0;
     // (less the static scan words and the LDS allocation granule)
-    const int64_t room = (kRvLdsPerBlock - 512 - static_cast<int64_t>(rv_merge_lds(q))) / 4;
+    const int64_t room = (kRvLdsPerBlock - 512 - static_cast<int64_t>(rv_merge_lds(q, p.rp))) / 4;
     p.cap = static_cast<int>(std::max<int64_t>(p.cap, std::min<int64_t>(room, int64_t(p.rp) * kRvKeysPerThread)));
     // the run lengths are scanned in the group buffer, whose head keeps them
     // in the general path: leave room for the longest rows besides
     p.cap = std::max(p.cap, p.nblk + 1 + 4 * p.rp);
     // deferred bins: larger blocks, two per CU
-    const int64_t room_big = (80 * 1024 - 1024 - static_cast<int64_t>(rv_merge_lds(q))) / 4;
+    const int64_t room_big = (80 * 1024 - 1024 - static_cast<int64_t>(rv_merge_lds(q, kRvBigThreads))) / 4;
     p.cap_big = static_cast<int>(std::min<int64_t>(room_big, int64_t(kRvBigThreads) * kRvKeysPerThread));
     if (p.cap_big < p.cap) return false;
-    return rv_merge_lds(p) <= 160 * 1024;
+    RvPlan b = p;
+    b.cap = p.cap_big;
+    return rv_merge_lds(p, p.rp) <= 160 * 1024 && rv_merge_lds(b, kRvBigThreads) <= 160 * 1024;
 }
 
 void launch_rv(const uint32_t* fwd, int64_t N, int K, const RvPlan& p, uint32_t* part, uint16_t* meta_blk,
@@ -921,10 +936,10 @@ void launch_rv(const uint32_t* fwd, int64_t N, int K, const RvPlan& p, uint32_t*
     hipLaunchKernelGGL(rv_meta_transpose_kernel, dim3(static_cast<unsigned>(ceil_div(p.nbins + 1, 64)),
                                                       static_cast<unsigned>(ceil_div(p.nblk, 64))),
                        dim3(256), 0, s, meta_blk, p.nblk, p.nbins, meta, big_bins);
-    const size_t lds = rv_merge_lds(p);
+    const size_t lds = rv_merge_lds(p, p.rp);
     RvPlan pb = p;
     pb.cap = p.cap_big;
-    const size_t lds_big = rv_merge_lds(pb);
+    const size_t lds_big = rv_merge_lds(pb, kRvBigThreads);
     const int grid = 8 * ((p.nbins + 7) / 8);
 #define GT_RV_MERGE(KM, R)                                                                                       \
     do {                                                                                                         \

@@ -151,6 +151,30 @@ def test_reverse_merge_binned_path(ctx):
             _assert_rows_equal(ctx.reverse_merge(F), O.reverse_merge(F), F)
 
 
+def test_reverse_merge_oversize_bins(ctx):
+    """256-row bins of the two-kernel merge around its fast path's limits
+    (9,087 keys of LDS group buffer at this size, 9,216 in registers): bins
+    beyond them go to the deferred kernel.  In-degrees set exactly: bin 5 36
+    per row (9,216 keys), bin 9 40 (10,240), bin 30 72 in its first half and
+    0 in its second (9,216 keys on 128 rows); every other bin about 8,100."""
+    rng = np.random.default_rng(11)
+    N, K = 256 * 48, 32
+    deg = np.zeros(N, np.int64)
+    deg[256 * 5:256 * 6] = 36
+    deg[256 * 9:256 * 10] = 40
+    deg[256 * 30:256 * 30 + 128] = 72
+    rest = np.ones(N, bool)
+    rest[256 * 5:256 * 6] = rest[256 * 9:256 * 10] = rest[256 * 30:256 * 31] = False
+    left = N * K - deg.sum()
+    idx = np.flatnonzero(rest)
+    deg[idx] = left // len(idx)
+    deg[idx[:left % len(idx)]] += 1
+    F = rng.permutation(np.repeat(np.arange(N), deg)).reshape(N, K).astype(np.uint32)
+    keys = np.bincount(F.ravel() >> 8, minlength=48)
+    assert keys[5] == 9216 and keys[9] == 10240 and keys[30] == 9216
+    _assert_rows_equal(ctx.reverse_merge(F), O.reverse_merge(F), F)
+
+
 @pytest.mark.parametrize("N,K", [(200000, 32), (70000, 64), (33, 8), (4097 * 32, 16)])
 def test_reverse_merge_bin_edges(ctx, N, K):
     # sizes around the bin boundaries (a last bin of one row; many bins),
