@@ -62,6 +62,8 @@ void launch_cagra_prune(const int32_t* G, int64_t N, int M, int K, uint32_t* out
                         hipStream_t s, const int32_t* order = nullptr, bool flat_rows = false);
 void launch_rev_count(const uint32_t* fwd, int64_t N, int K, uint32_t* deg, uint32_t* slot, int* err, hipStream_t s);
 void launch_exclusive_scan(const uint32_t* in, int64_t n, uint32_t* out, uint32_t* sums, hipStream_t s);
+void launch_chunk_bounds(const int8_t* X8, int Dp, const int32_t* pool, const int32_t* cnt, int64_t nch, int8_t* c8,
+                         float* cn, float* cr, hipStream_t s);
 void launch_kmpar_init(uint8_t* flag, float* mind, int64_t S, int64_t first, hipStream_t s);
 void launch_kmpar_psi(const float* mind, int64_t S, int64_t target, float* psi, hipStream_t s);
 void launch_kmpar_sample(const float* mind, uint8_t* flag, uint32_t* sel, int64_t S, const float* psi, float lk,
@@ -225,7 +227,7 @@ struct gt_ctx {
     hipStream_t stream = nullptr;
     std::string err;
     // named workspaces, grow-only (one slot per role, see gtann::Ws)
-    gtann::DevBuf ws[80];
+    gtann::DevBuf ws[96];
     gtann::HostBuf pinned[2];   // top-2 assignment downloads of two consecutive rounds
     gtann::HostBuf pin_lloyd;   // Lloyd steps: nearest centroids down, CSR up
     // host scratch of the bucketing, reused across calls (no page faults on
@@ -234,6 +236,7 @@ struct gt_ctx {
     gtann::PinnedI32 h_members[2];
     hipEvent_t members_up[2] = {nullptr, nullptr};   // after the last upload of h_members[i]
     int64_t knn_launches = 0;   // bucketed-round launches of the current build
+    double knn_pairs_done = 0;  // (query, pool row) pairs the collect kernels computed (chunk pruning skips the rest)
     uint64_t members_gen = 0;   // bucketing whose members W_MEMBERS holds (0: none)
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
     void* scratch = nullptr;    // this device's fixed scratch array (gt_optimize_noalloc), or null
@@ -251,9 +254,9 @@ enum Ws {
     W_LHIST, W_LOFFS, W_LSUMS, W_CAND, W_CANDCNT, W_STATS,
     W_OOC_A, W_OOC_B, W_OOC_C, W_OOC_D, W_OOC_E, W_OOC_F, W_OOC_G, W_CR, W_CRNORMS,
     W_KM_TRAIN, W_KM_MIND, W_KM_FLAG, W_KM_SEL, W_KM_POS, W_KM_SUMS, W_KM_NEW, W_KM_PSI, W_KM_P, W_KM_PN, W_KM_P8,
-    W_KM_PN8, W_KM_OI, W_KM_OD, W_COUNT_
+    W_KM_PN8, W_KM_OI, W_KM_OD, W_CH8, W_CHN, W_CHR, W_CHCNT, W_PAIRS, W_COUNT_
 };
-static_assert(W_COUNT_ <= 80, "workspace slots");
+static_assert(W_COUNT_ <= 96, "workspace slots");
 
 struct Ctx {
     gt_ctx* c;
@@ -991,10 +994,13 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
     const int64_t rows = compact ? b.offsets[static_cast<size_t>(b1)] - qbase : N;
     Trace tr;
     std::vector<CopyTaskH> tasks;
-    std::vector<int64_t> pool_off(static_cast<size_t>(C + 1), 0);
+    // every pool starts at a multiple of kChunkRows in the pool list (the
+    // collect kernel's pruning chunks); pool_cnt: its rows
+    std::vector<int64_t> pool_off(static_cast<size_t>(C + 1), 0), pool_cnt(static_cast<size_t>(C), 0);
     int64_t total = 0;
     std::vector<int64_t> segs;
     for (int64_t bb = b0; bb < b1; ++bb) {
+        total = ceil_div(total, int64_t(kChunkRows)) * kChunkRows;
         pool_off[static_cast<size_t>(bb)] = total;
         segs.clear();
         if (own) segs.push_back(bb);
@@ -1010,6 +1016,7 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
             tasks.push_back({lo, total, n});
             total += n;
         }
+        pool_cnt[static_cast<size_t>(bb)] = total - pool_off[static_cast<size_t>(bb)];
     }
     pool_off[static_cast<size_t>(b1)] = total;
 
@@ -1022,7 +1029,13 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
         if (b.uploaded) GT_HIP(hipEventRecord(b.uploaded, c.s));
         c.c->members_gen = b.gen;
     }
-    const bool sub_ordered = own && !seed_d && !compact && c.c->dbg.sub_order != 0;
+    // members by nearest sub-centroid: for the unseeded pass (its threshold
+    // tightens within a few tiles), and for seeded passes that prune chunks
+    // (a chunk of 64 consecutive members then lies within one sub-cluster,
+    // and so do a block's 128 queries: small spheres, few chunks needed)
+    const bool want_prune = metric == GT_METRIC_L2 && X.data8 && c.c->dbg.knn_prune != 0 && c.c->dbg.knn_collect != 0 &&
+                            (X.Dp8 == 32 || X.Dp8 == 64 || X.Dp8 == 128 || X.Dp8 == 256);
+    const bool sub_ordered = own && !compact && c.c->dbg.sub_order != 0 && (!seed_d || want_prune);
     if (sub_ordered) sub_order_members(c, X, b, metric, d_members);
     CopyTaskH* d_tasks = c.ws<CopyTaskH>(W_TASKS, tasks.size());
     c.h2d(d_tasks, tasks.data(), tasks.size() * sizeof(CopyTaskH));
@@ -1034,7 +1047,7 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
     double pr = 0.0;
     for (int64_t bb = b0; bb < b1; ++bb) {
         const int64_t q0 = b.offsets[static_cast<size_t>(bb)], nqb = b.offsets[static_cast<size_t>(bb + 1)] - q0;
-        const int64_t p0 = pool_off[static_cast<size_t>(bb)], npb = pool_off[static_cast<size_t>(bb + 1)] - p0;
+        const int64_t p0 = pool_off[static_cast<size_t>(bb)], npb = pool_cnt[static_cast<size_t>(bb)];
         mp = std::max(mp, npb);
         mb = std::max(mb, nqb);
         pr += static_cast<double>(nqb) * static_cast<double>(npb);
@@ -1049,7 +1062,7 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
             // for the sub-ordered unseeded pass one sub-cluster earlier (the
             // chain's previous sub-cluster lies there)
             int64_t rot = own && npb > 0 ? t : 0;
-            if (sub_ordered && nqb >= 2 * kSubSize && npb >= kSubSize) rot = (t - kSubSize + npb) % npb;   // >= 0
+            if (sub_ordered && !seed_d && nqb >= 2 * kSubSize && npb >= kSubSize) rot = (t - kSubSize + npb) % npb;   // >= 0
             GT_REQUIRE(rot >= 0 && (npb == 0 || rot < npb), "pool rotation out of range");
             it.p_rot = static_cast<int32_t>(rot);
             it.out_base = compact ? q0 - qbase + t : -1;
@@ -1088,16 +1101,51 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
             a.stats = c.ws<unsigned long long>(W_STATS, 4);
             GT_HIP(hipMemsetAsync(a.stats, 0, 4 * sizeof(unsigned long long), c.s));
         }
+        a.pairs_done = c.ws<unsigned long long>(W_PAIRS, 1);
+        GT_HIP(hipMemsetAsync(a.pairs_done, 0, sizeof(unsigned long long), c.s));
     }
+    // exact chunk pruning (int8 rows, L2): the centre and radius of every
+    // kChunkRows rows of the pool list
+    const bool prune = collect && a.Xq8 && a.Xp8 && metric == GT_METRIC_L2 && c.c->dbg.knn_prune != 0 &&
+                       (X.Dp8 == 32 || X.Dp8 == 64 || X.Dp8 == 128 || X.Dp8 == 256);
+    int64_t nchunk = 0;
+    int32_t* d_chcnt = nullptr;
+    if (prune) {
+        nchunk = ceil_div(total, int64_t(kChunkRows));
+        std::vector<int32_t> cnt(static_cast<size_t>(std::max<int64_t>(nchunk, 1)), 0);
+        for (int64_t bb = b0; bb < b1; ++bb) {
+            const int64_t g0 = pool_off[static_cast<size_t>(bb)] / kChunkRows, n = pool_cnt[static_cast<size_t>(bb)];
+            for (int64_t k = 0; k * kChunkRows < n; ++k)
+                cnt[static_cast<size_t>(g0 + k)] = static_cast<int32_t>(std::min<int64_t>(kChunkRows, n - k * kChunkRows));
+        }
+        d_chcnt = c.ws<int32_t>(W_CHCNT, cnt.size());
+        c.h2d(d_chcnt, cnt.data(), cnt.size() * sizeof(int32_t));
+        a.ch8 = c.ws<int8_t>(W_CH8, static_cast<size_t>(std::max<int64_t>(nchunk, 1)) * X.Dp8);
+        a.chn = c.ws<float>(W_CHN, static_cast<size_t>(std::max<int64_t>(nchunk, 1)));
+        a.chr = c.ws<float>(W_CHR, static_cast<size_t>(std::max<int64_t>(nchunk, 1)));
+    }
+    const double done_before = c.c->knn_pairs_done;
     const double t = c.timed([&] {
+        if (prune)
+            launch_chunk_bounds(X.data8, X.Dp8, d_pool, d_chcnt, nchunk, const_cast<int8_t*>(a.ch8),
+                                const_cast<float*>(a.chn), const_cast<float*>(a.chr), c.s);
         if (collect) launch_knn_collect_select(a, rows, c.s);
         else launch_knn_fused(a, c.s);
     });
+    if (a.pairs_done) {
+        unsigned long long done = 0;
+        c.d2h(&done, a.pairs_done, sizeof(done));
+        c.sync();
+        c.c->knn_pairs_done += static_cast<double>(done);
+    } else {
+        c.c->knn_pairs_done += pr;
+    }
     ++c.c->knn_launches;
     tr.mark(c.s, "round: fused kNN");
     if (tr.on)
-        std::fprintf(stderr, "[gtann]   pairs %.4g (own %d, probes %d, seeded %d), %.1f ms device\n", pr, own ? 1 : 0,
-                     probes ? 1 : 0, seed_d ? 1 : 0, t * 1e3);
+        std::fprintf(stderr, "[gtann]   pairs %.4g, computed %.4g (own %d, probes %d, seeded %d), %.3f ms device\n", pr,
+                     a.pairs_done ? c.c->knn_pairs_done - done_before : pr, own ? 1 : 0, probes ? 1 : 0,
+                     seed_d ? 1 : 0, t * 1e3);
     if (tr.on && a.stats) {
         unsigned long long h[4];
         c.d2h(h, a.stats, sizeof(h));
@@ -2258,6 +2306,7 @@ void gt_debug_opts_default(gt_debug_opts* o)
     o->lloyd_host_csr = 0;
     o->prune_flat_rows = 0;
     o->knn_stats = 0;
+    o->knn_prune = 1;
 }
 
 int gt_set_debug(gt_ctx* ctx, const gt_debug_opts* o)
@@ -3120,6 +3169,7 @@ int gt_build_graph_ex(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtyp
         int32_t* tmp_i = ooc ? nullptr : c.ws<int32_t>(W_IDS2, nm);
         float* tmp_d = ooc ? nullptr : c.ws<float>(W_D2, nm);
         ctx->knn_launches = 0;
+        ctx->knn_pairs_done = 0.0;
         // Round r's bucketing = bucket_device (device work + downloads, on
         // this thread) then bucket_host (two-choice + CSR, on a worker
         // thread).  The host half of round r runs while the device computes
@@ -3230,6 +3280,7 @@ int gt_build_graph_ex(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtyp
         if (ooc) {
             st.knn_flops = 2.0 * D * st.knn_pairs;
             st.knn_launches = ctx->knn_launches;
+            st.knn_pairs_computed = ctx->knn_pairs_done;
             st.knn_int8 = use_i8(Xm, Xm, p.metric) ? 1 : 0;
             if (graph) {
                 Timer t1;
@@ -3281,6 +3332,7 @@ int gt_build_graph_ex(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtyp
         }
         st.knn_flops = 2.0 * D * st.knn_pairs;
         st.knn_launches = ctx->knn_launches;
+        st.knn_pairs_computed = ctx->knn_pairs_done;
         st.knn_int8 = use_i8(Xm, Xm, p.metric) ? 1 : 0;
         // sanitize + prune + reverse merge
         uint32_t* fin = nullptr;

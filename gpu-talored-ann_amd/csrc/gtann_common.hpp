@@ -77,7 +77,19 @@ struct KnnArgs {
     int32_t* cand_cnt;
     unsigned long long* stats;   // optional: [0] keys collected, [1] compactions, [2] tiles past the
                                  // pre-filter, [3] tiles filtered (per wave)
+    // exact chunk pruning of the int8 collect kernel (L2): every pool starts
+    // at a multiple of kChunkRows in the pool list, and chunk g (pool-list
+    // rows [kChunkRows g, kChunkRows g + kChunkRows)) has the rounded centre
+    // ch8[g * Dp ..] (int8), its |c|^2 chn[g] and chr[g] >= the largest
+    // |p - c| of its rows; null = every stage is scanned
+    const int8_t* ch8;
+    const float* chn;
+    const float* chr;
+    unsigned long long* pairs_done;   // optional: += (query, pool row) pairs the MFMAs computed
 };
+
+constexpr int kChunkRows = 64;       // pool rows per pruning chunk (= one collect stage)
+constexpr int kMaxChunkWords = 24;   // pools of up to 24 * 32 chunks (49,152 rows) are pruned
 
 constexpr int kCollectCap = 256;   // candidate slots per query of a collect launch
 

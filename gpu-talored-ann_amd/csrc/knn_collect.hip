@@ -56,7 +56,14 @@ struct CollectSmem {
     int32_t thalf[3][kStageRows];          // accumulator start: -floor(|p|^2 / 2) (L2), 0 (IP), kHalfPast past the end
     int32_t sid[2][kStageRows];            // the next stage's pool row ids, for every thread's row requests
     CollectWave wv[kWaves];
+    // chunk pruning: each wave's chunks needed (bits), the block's, and the
+    // schedule of the stages still to scan
+    uint32_t wmask[kWaves][kMaxChunkWords];
+    uint32_t bmask[kMaxChunkWords];
+    uint16_t slist[kMaxChunkWords * 32 + kWindow / kStageTiles + 2];
+    int32_t nlist;
 };
+static_assert(kChunkRows == kStageRows, "a pruning chunk is one stage of pool rows");
 
 __device__ __forceinline__ int stash_index(int lane, int r)
 {
@@ -301,9 +308,17 @@ knn_i8_collect_kernel(KnnArgs a)
     const int nps = (pcount + ROWS - 1) / ROWS;
     const int nws = a.seed_d ? 0 : min(kWindow / kStageTiles, nps);
     const int nst = nps + nws;
-    // Every thread issues the same row loads in every stage (positions past
-    // the slice end are clamped to its last row and flagged), so the
-    // compiler can wait for one stage's loads without draining the next's.
+    // Chunk pruning (L2, integer rows): once every query of the block has its
+    // threshold, a stage is scanned only if some query may hold a key in it:
+    // with c a chunk's centre and r >= the distance of its rows from c, a row
+    // p of the chunk has |q - p| >= |q - c| - r, so a query with
+    // |q - c| > r + sqrt(thr) has no key at or below thr there.  The steps
+    // after the window follow the schedule sm.slist (the first two, already
+    // requested during the window, unconditionally).
+    const int nch = (pcount + kChunkRows - 1) / kChunkRows;
+    const bool prune = METRIC == 0 && a.ch8 != nullptr && nch <= kMaxChunkWords * 32;
+    int nsteps = nst;     // steps of the scan (stages, in schedule order)
+    bool listed = false;  // the steps from nws on follow sm.slist
     // The pool list is the caller's (launch_knn_collect_select requires one).
     auto pool_pos = [&](int p) __attribute__((always_inline)) -> int64_t {
         p = min(p, pcount - 1) + it.p_rot;
@@ -311,6 +326,11 @@ knn_i8_collect_kernel(KnnArgs a)
         return it.p_begin + p;
     };
     auto stage_base = [&](int s) __attribute__((always_inline)) { return (s < nps ? s : s - nps) * ROWS; };
+    // the stage scanned at step k (-1: none)
+    auto sched = [&](int k) __attribute__((always_inline)) -> int {
+        if (k >= nsteps) return -1;
+        return (!listed || k < nws) ? k : static_cast<int>(sm.slist[k - nws]);
+    };
 
     // fixed-size register sets indexed only by unrolled loop counters
     struct Rows {
@@ -319,10 +339,10 @@ knn_i8_collect_kernel(KnnArgs a)
     // The threads < ROWS fetch their stage row's pool id (one stage ahead)
     // and norm; the ids reach every thread's row requests through LDS.
     const int r_own = tid & (ROWS - 1);
-    auto stage_id = [&](int s, bool& valid) __attribute__((always_inline)) -> int32_t {
-        const bool live = s < nst;
-        const int base = live ? stage_base(s) : 0;
-        valid = live && base + r_own < pcount;
+    auto stage_id = [&](int k, bool& valid) __attribute__((always_inline)) -> int32_t {
+        const int s = sched(k);
+        const int base = s >= 0 ? stage_base(s) : 0;
+        valid = s >= 0 && base + r_own < pcount;
         return a.p_rows[pool_pos(base + r_own)];
     };
     auto load_rows = [&](const int32_t* ids) __attribute__((always_inline)) {
@@ -338,6 +358,102 @@ knn_i8_collect_kernel(KnnArgs a)
             if (e < U4_STAGE) *reinterpret_cast<intx4*>(&sm.tile[buf][e / U4_ROW][16 * (e % U4_ROW)]) = pre.v[U.value];
         });
     };
+
+    // The block's schedule: each wave marks the chunks some query of it may
+    // need (centres staged through tile[0], 32 x 32 MFMA tiles of q.c), the
+    // marks are ORed over the waves, and wave 0 lists the stages from
+    // `from` on that touch a marked chunk (stages before `first_free`
+    // unconditionally).  Called by every thread; tile[0], tnorm[0..1] are free.
+    auto build_schedule = [&](int from, int first_free) __attribute__((always_inline)) {
+        __syncthreads();   // every wave is done with tile[0] and the norm slots
+        const float sthr = st.thr >= 0.f ? sqrtf(st.thr) : -1.f;   // -1: the query needs nothing (invalid)
+        const bool qneed = qvalid && sthr >= 0.f;
+        for (int cb = 0; cb < nch; cb += ROWS) {
+            const int nc = min(ROWS, nch - cb);
+            static_for<0, U4_THREAD>([&](auto U) __attribute__((always_inline)) {
+                const int e = tid + 256 * U.value;
+                if (e < U4_STAGE) {
+                    const int r = e / U4_ROW;
+                    const int g = min(r, nc - 1);
+                    *reinterpret_cast<intx4*>(&sm.tile[0][r][16 * (e % U4_ROW)]) = *reinterpret_cast<const intx4*>(
+                        a.ch8 + (static_cast<int64_t>(it.p_begin / kChunkRows) + cb + g) * DP + 16 * (e % U4_ROW));
+                }
+            });
+            if (tid < ROWS) {
+                const int64_t g = it.p_begin / kChunkRows + cb + min(tid, nc - 1);
+                sm.tnorm[0][tid] = a.chn[g];
+                sm.tnorm[1][tid] = a.chr[g];
+            }
+            __syncthreads();
+#pragma unroll
+            for (int u = 0; u < kStageTiles; ++u) {
+                intx16 acc;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[r] = 0;
+                const int8_t* arow = &sm.tile[0][kPoolTile * u + j][16 * h];
+#pragma unroll
+                for (int k = 0; k < KS; ++k) {
+                    const intx4 av = *reinterpret_cast<const intx4*>(arow + 32 * k);
+                    acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, qf[k], acc, 0, 0, 0);
+                }
+                uint32_t word = 0u;
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int row = kPoolTile * u + 8 * g + 4 * h + e;   // this lane's chunk (in the batch)
+                        const float dqc = qn + sm.tnorm[0][row] - 2.f * static_cast<float>(acc[4 * g + e]);
+                        const float lim = sm.tnorm[1][row] + sthr;
+                        const bool need = qneed && cb + row < nch && dqc <= fmaf(lim, lim, 1.f) * 1.000001f;
+                        const uint64_t bal = __ballot(need);
+                        word |= ((bal & 0xffffffffull) != 0 ? 1u : 0u) << (8 * g + e);
+                        word |= ((bal >> 32) != 0 ? 1u : 0u) << (8 * g + 4 + e);
+                    }
+                }
+                if (lane == 0) sm.wmask[w][(cb + kPoolTile * u) / 32] = word;
+            }
+            __syncthreads();   // tile[0] and tnorm are read before the next batch
+        }
+        if (tid < (nch + 31) / 32)
+            sm.bmask[tid] = sm.wmask[0][tid] | sm.wmask[1][tid] | sm.wmask[2][tid] | sm.wmask[3][tid];
+        __syncthreads();
+        if (w == 0) {
+            const uint64_t lt = (1ull << lane) - 1ull;
+            int n = 0;
+            for (int s0 = from; s0 < nst; s0 += 64) {
+                const int s = s0 + lane;
+                bool need = false;
+                if (s < nst) {
+                    if (s < first_free) {
+                        need = true;
+                    } else {
+                        // the chunks of the stage's first and last positions (a
+                        // stage wrapping past the pool's end touches both ends)
+                        const int base = stage_base(s);
+                        const int p0 = static_cast<int>(pool_pos(base) - it.p_begin);
+                        const int p1 = static_cast<int>(pool_pos(min(base + ROWS - 1, pcount - 1)) - it.p_begin);
+                        const int c0 = p0 / kChunkRows, c1 = p1 / kChunkRows;
+                        auto bit = [&](int c) { return (sm.bmask[c >> 5] >> (c & 31)) & 1u; };
+                        if (c0 <= c1) {
+                            for (int c = c0; c <= c1; ++c) need |= bit(c) != 0u;
+                        } else {
+                            for (int c = c0; c < nch; ++c) need |= bit(c) != 0u;
+                            for (int c = 0; c <= c1; ++c) need |= bit(c) != 0u;
+                        }
+                    }
+                }
+                const uint64_t m = __ballot(need);
+                if (need) sm.slist[n + __popcll(m & lt)] = static_cast<uint16_t>(s);
+                n += __popcll(m);
+            }
+            if (lane == 0) sm.nlist = n;
+        }
+        __syncthreads();
+        nsteps = from + sm.nlist;
+        listed = true;
+    };
+    if (prune && nws == 0) build_schedule(0, 0);   // seeded: the thresholds are known
+
     int32_t rid_cur = 0, rid_next = 0;   // threads < ROWS: the stage row's id (a valid row) this stage, the next
     bool rvalid_cur = false, rvalid_next = false;
     float rn_cur = 0.f;
@@ -354,16 +470,16 @@ knn_i8_collect_kernel(KnnArgs a)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc_prev[r] = 0;
     int32_t lo = i8_pass_floor<METRIC>(st.thr, qn);
-    bool pending = false;   // acc_prev holds tile p_u of stage p_s, not yet filtered
-    int p_s = 0, p_u = 0;
+    bool pending = false;   // acc_prev holds tile p_u of step p_k, not yet filtered
+    int p_k = 0, p_u = 0;
 
-    // one stage: stage s's rows and norms (requested one stage earlier) into
-    // LDS, the barrier, the requests for stage s + 1 (and the pool ids of
-    // s + 2), then the MFMAs of stage s's tiles, each with filt on the tile
-    // before it.  A request is waited for only at the next stage's top, a
+    // one step k: its stage's rows and norms (requested one step earlier)
+    // into LDS, the barrier, the requests for step k + 1 (and the pool ids of
+    // k + 2), then the MFMAs of the stage's tiles, each with filt on the tile
+    // before it.  A request is waited for only at the next step's top, a
     // whole stage of MFMAs and filtering later.
-    auto stage = [&](int s, auto&& filt) __attribute__((always_inline)) {
-        const int buf = s & 1, slot = s % 3;
+    auto stage = [&](int k, auto&& filt) __attribute__((always_inline)) {
+        const int buf = k & 1, slot = k % 3;
         store_rows(buf);
         if (tid < ROWS) {
             // rows past the slice end: id -1, norm +inf, accumulator start
@@ -371,15 +487,15 @@ knn_i8_collect_kernel(KnnArgs a)
             sm.trow[slot][tid] = rvalid_cur ? rid_cur : -1;
             sm.tnorm[slot][tid] = rvalid_cur ? rn_cur : INFINITY;
             sm.thalf[slot][tid] = rvalid_cur ? -(static_cast<int32_t>(rn_cur) >> 1) : kHalfPast;
-            sm.sid[(s + 1) & 1][tid] = rid_next;
+            sm.sid[(k + 1) & 1][tid] = rid_next;
         }
         __syncthreads();
-        load_rows(sm.sid[(s + 1) & 1]);
+        load_rows(sm.sid[(k + 1) & 1]);
         if (tid < ROWS) {
             rid_cur = rid_next;
             rvalid_cur = rvalid_next;
             rn_cur = METRIC == 0 ? a.np[rid_cur] : 0.f;
-            rid_next = stage_id(s + 2, rvalid_next);
+            rid_next = stage_id(k + 2, rvalid_next);
         }
 
 #pragma unroll
@@ -395,19 +511,19 @@ knn_i8_collect_kernel(KnnArgs a)
             }
             const int8_t* arow = &sm.tile[buf][kPoolTile * u + j][16 * h];
 #pragma unroll
-            for (int k = 0; k < KS; ++k) {
-                const intx4 av = *reinterpret_cast<const intx4*>(arow + 32 * k);
-                acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, qf[k], acc, 0, 0, 0);
+            for (int kk = 0; kk < KS; ++kk) {
+                const intx4 av = *reinterpret_cast<const intx4*>(arow + 32 * kk);
+                acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, qf[kk], acc, 0, 0, 0);
             }
-            if (pending) filt(p_s, p_u);
+            if (pending) filt(p_k, p_u);
             acc_prev = acc;
             pending = true;
-            p_s = s;
+            p_k = k;
             p_u = u;
         }
     };
-    auto collect = [&](int s, int u) __attribute__((always_inline)) {
-        const int slot = s % 3;
+    auto collect = [&](int k, int u) __attribute__((always_inline)) {
+        const int slot = k % 3;
         collect_tile<METRIC>(a, W, acc_prev, &sm.tnorm[slot][kPoolTile * u], &sm.trow[slot][kPoolTile * u],
                              &sm.thalf[slot][kPoolTile * u], lane, qvalid, qn, st, lo);
     };
@@ -415,13 +531,13 @@ knn_i8_collect_kernel(KnnArgs a)
         float T[32];
 #pragma unroll
         for (int i = 0; i < 32; ++i) T[i] = INFINITY;
-        auto window = [&](int s, int u) __attribute__((always_inline)) {
-            const int slot = s % 3;
+        auto window = [&](int k, int u) __attribute__((always_inline)) {
+            const int slot = k % 3;
             window_tile<METRIC>(acc_prev, &sm.tnorm[slot][kPoolTile * u], &sm.trow[slot][kPoolTile * u],
                                 &sm.thalf[slot][kPoolTile * u], h, qn, st.self, T);
         };
-        for (int s = 0; s < nws; ++s) stage(s, window);
-        window(p_s, p_u);   // the window's last tile
+        for (int k = 0; k < nws; ++k) stage(k, window);
+        window(p_k, p_u);   // the window's last tile
         pending = false;
         // the pair's ceil(M/2)-th smallest distances: M distinct rows at or below the larger
         const int m = (a.M + 1) / 2 - 1;
@@ -432,11 +548,15 @@ knn_i8_collect_kernel(KnnArgs a)
         if (qvalid && bound < st.thr) st.thr = bound;
         lo = i8_pass_floor<METRIC>(st.thr, qn);
         publish_state(W, lane, qvalid, qn, st);
+        // the steps nws and nws + 1 are requested already: they stay
+        if (prune) build_schedule(nws, nws + 2);
     }
-    for (int s = nws; s < nst; ++s) stage(s, collect);
-    if (pending) collect(p_s, p_u);
+    for (int k = nws; k < nsteps; ++k) stage(k, collect);
+    if (pending) collect(p_k, p_u);
     if (qvalid && h == 0) a.cand_cnt[st.orow] = st.cnt;
     if (a.stats && qvalid && h == 0) atomicAdd(a.stats, static_cast<unsigned long long>(st.cnt));
+    if (a.pairs_done && tid == 0)
+        atomicAdd(a.pairs_done, static_cast<unsigned long long>(nsteps) * ROWS * static_cast<unsigned>(it.q_count));
 }
 
 // ------------------------------------------------------------ fp32 rows
@@ -830,6 +950,107 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_wav
         }
         wave_sync();   // read out before the distances overwrite it
     }
+}
+
+// Per pruning chunk g (pool-list rows [kChunkRows g, + cnt[g])): the
+// rounded mean of its int8 rows as its centre c, |c|^2, and sqrt of the
+// largest |p - c|^2 of its rows (exact integers; the root rounded up by a
+// relative 2^-20), for knn_i8_collect_kernel's stage skipping (Dp a power
+// of two, at most 256).  One wave per chunk, four chunks per block: lane l
+// holds the 16-byte piece l % (Dp / 16) of the rows l / (Dp / 16) + k * RG,
+// all its loads in flight together; the column sums add the lanes of one
+// piece, the row distances the pieces of a row.
+template <int DP>
+__global__ void __launch_bounds__(256) chunk_bounds_kernel(const int8_t* __restrict__ X8,
+                                                           const int32_t* __restrict__ pool,
+                                                           const int32_t* __restrict__ cnt, int64_t nch,
+                                                           int8_t* __restrict__ c8, float* __restrict__ cn,
+                                                           float* __restrict__ cr)
+{
+    constexpr int PC = DP / 16;          // pieces per row
+    constexpr int RG = 64 / PC;          // row groups per wave
+    constexpr int RPT = kChunkRows / RG; // rows per lane
+    static_assert((PC & (PC - 1)) == 0 && PC <= 16, "chunk shape");
+    __shared__ int32_t cs[4][DP];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int64_t g = static_cast<int64_t>(blockIdx.x) * 4 + w;
+    if (g >= nch) return;
+    const int q = lane % PC, rg = lane / PC;
+    const int n = cnt[g];
+    int32_t id[RPT];
+#pragma unroll
+    for (int k = 0; k < RPT; ++k) {
+        const int r = rg + k * RG;
+        id[k] = r < n ? pool[g * kChunkRows + r] : -1;
+    }
+    intx4 x[RPT];
+#pragma unroll
+    for (int k = 0; k < RPT; ++k)
+        x[k] = id[k] >= 0 ? *reinterpret_cast<const intx4*>(X8 + static_cast<int64_t>(id[k]) * DP + 16 * q)
+                          : intx4{0, 0, 0, 0};
+    int sum[16];
+#pragma unroll
+    for (int b = 0; b < 16; ++b) {
+        int sb = 0;
+#pragma unroll
+        for (int k = 0; k < RPT; ++k) sb += static_cast<int8_t>(x[k][b >> 2] >> (8 * (b & 3)));
+        sum[b] = sb;
+    }
+    // the lanes of one piece (stride PC)
+#pragma unroll
+    for (int o = PC; o < 64; o <<= 1)
+#pragma unroll
+        for (int b = 0; b < 16; ++b) sum[b] += __shfl_xor(sum[b], o);
+    int nsum = 0;
+    if (lane < PC) {
+        const float inv = 1.0f / static_cast<float>(n > 0 ? n : 1);
+#pragma unroll
+        for (int b = 0; b < 16; ++b) {
+            const int c = n > 0 ? static_cast<int>(rintf(static_cast<float>(sum[b]) * inv)) : 0;
+            cs[w][16 * q + b] = c;
+            c8[g * DP + 16 * q + b] = static_cast<int8_t>(c);
+            nsum += c * c;
+        }
+    }
+    wave_sync();
+    // each row's |p - c|^2: the PC lanes of a row (consecutive) add
+    int v = 0;
+#pragma unroll
+    for (int k = 0; k < RPT; ++k) {
+        int d = 0;
+#pragma unroll
+        for (int b = 0; b < 16; ++b) {
+            const int e = static_cast<int>(static_cast<int8_t>(x[k][b >> 2] >> (8 * (b & 3)))) - cs[w][16 * q + b];
+            d += e * e;
+        }
+#pragma unroll
+        for (int o = 1; o < PC; o <<= 1) d += __shfl_xor(d, o);
+        if (id[k] >= 0) v = max(v, d);
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        nsum += __shfl_xor(nsum, o);
+        v = max(v, __shfl_xor(v, o));
+    }
+    if (lane == 0) {
+        cn[g] = static_cast<float>(nsum);
+        cr[g] = sqrtf(static_cast<float>(v)) * 1.000001f;
+    }
+}
+
+void launch_chunk_bounds(const int8_t* X8, int Dp, const int32_t* pool, const int32_t* cnt, int64_t nch, int8_t* c8,
+                         float* cn, float* cr, hipStream_t s)
+{
+    if (nch <= 0) return;
+    const dim3 grid(static_cast<unsigned>((nch + 3) / 4));
+    switch (Dp) {
+    case 32: hipLaunchKernelGGL((chunk_bounds_kernel<32>), grid, dim3(256), 0, s, X8, pool, cnt, nch, c8, cn, cr); break;
+    case 64: hipLaunchKernelGGL((chunk_bounds_kernel<64>), grid, dim3(256), 0, s, X8, pool, cnt, nch, c8, cn, cr); break;
+    case 128: hipLaunchKernelGGL((chunk_bounds_kernel<128>), grid, dim3(256), 0, s, X8, pool, cnt, nch, c8, cn, cr); break;
+    case 256: hipLaunchKernelGGL((chunk_bounds_kernel<256>), grid, dim3(256), 0, s, X8, pool, cnt, nch, c8, cn, cr); break;
+    default: GT_REQUIRE(false, "chunk bounds: padded dimension " + std::to_string(Dp) + " not supported");
+    }
+    GT_HIP(hipGetLastError());
 }
 
 // ------------------------------------------------------------ host side

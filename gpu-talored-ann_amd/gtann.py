@@ -53,7 +53,7 @@ class DebugOpts(C.Structure):
     _fields_ = [
         ("knn_collect", C.c_int32), ("revmerge_path", C.c_int32), ("sub_order", C.c_int32),
         ("lloyd_host_csr", C.c_int32), ("prune_flat_rows", C.c_int32), ("knn_stats", C.c_int32),
-        ("reserved_", C.c_int32 * 2),
+        ("knn_prune", C.c_int32), ("reserved_", C.c_int32),
     ]
 
 
@@ -63,7 +63,7 @@ class BuildStats(C.Structure):
         ("t_merge", C.c_double), ("t_refine", C.c_double), ("t_prune", C.c_double), ("t_revmerge", C.c_double),
         ("t_download", C.c_double), ("knn_flops", C.c_double), ("knn_pairs", C.c_double),
         ("max_pool", C.c_int64), ("max_bucket", C.c_int64), ("knn_launches", C.c_int64), ("knn_int8", C.c_int64),
-        ("ooc_chunks", C.c_int64),
+        ("ooc_chunks", C.c_int64), ("knn_pairs_computed", C.c_double),
     ]
 
     def as_dict(self):

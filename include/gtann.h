@@ -230,6 +230,8 @@ typedef struct gt_build_stats {
     int64_t knn_int8;       /* 1: the rounds ran on the int8 matrix cores (integer-typed rows, or
                                integer-valued float rows with int_exact), 0: fp32 */
     int64_t ooc_chunks;     /* device chunks of an out-of-core build (0: resident) */
+    double knn_pairs_computed; /* pairs the distance kernels computed: knn_pairs less the pool chunks
+                               the exact pruning skipped */
 } gt_build_stats;
 
 void gt_build_params_default(gt_build_params* p);
@@ -356,7 +358,9 @@ typedef struct gt_debug_opts {
                                 table is below 2 GiB; 1: always the flat 64-bit addressing of larger
                                 tables */
     int32_t knn_stats;       /* 1 with GTANN_TRACE set: per-launch counters of the collect kernel */
-    int32_t reserved_[2];
+    int32_t knn_prune;       /* 1 (default): the int8 collect kernel skips pool chunks whose bounding
+                                sphere is farther from every query than its threshold (exact); 0: scans all */
+    int32_t reserved_;
 } gt_debug_opts;
 
 void gt_debug_opts_default(gt_debug_opts* o);

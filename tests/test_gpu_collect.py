@@ -142,3 +142,40 @@ def test_collect_equals_merging_kernel(ctx):
     for x, y in ((a, c), (b2, c2)):
         np.testing.assert_array_equal(x[0], y[0])
         np.testing.assert_array_equal(x[1], y[1])
+
+
+@pytest.mark.parametrize("cfg,n,nb,skips", [("C2", 60000, 16, True), ("C5", 80000, 16, False),
+                                            ("C2", 30000, 3, False)])
+def test_chunk_pruning_is_exact(ctx, cfg, n, nb, skips):
+    """The int8 collect kernel skips pool chunks whose bounding sphere is
+    farther from every query of the block than its threshold: the tables and
+    graphs equal a build that scans every chunk, bit for bit.  On the C2
+    mixture (60 rows per cluster here) fewer pairs are computed; an 80,000-row
+    slice of C5's 4,096-cluster mixture has 20 rows per cluster, so chunks
+    span clusters and nothing is skipped."""
+    import synth
+    X, _ = synth.generate(cfg, n=n)
+    kw = dict(n_buckets=nb, nprobe=1, M=64, K=32, rounds=2)
+    print(f"pruning {cfg} n={n} buckets={nb}", flush=True)
+    a = ctx.build_graph(X, **kw)
+    with debug_opts(ctx, knn_prune=False):
+        b = ctx.build_graph(X, **kw)
+    np.testing.assert_array_equal(a.knn_ids, b.knn_ids)
+    np.testing.assert_array_equal(a.knn_dists.view(np.uint32), b.knn_dists.view(np.uint32))
+    np.testing.assert_array_equal(a.graph, b.graph)
+    done, full = a.stats["knn_pairs_computed"], b.stats["knn_pairs_computed"]
+    print(f"  pairs computed {done:.4g} of {full:.4g}", flush=True)
+    if skips:
+        assert done < full
+
+
+def test_chunk_pruning_uniform_rows(ctx):
+    # unclustered rows: chunks' spheres overlap every query; same table
+    rng = np.random.default_rng(21)
+    X = rng.integers(-127, 128, size=(20000, 64)).astype(np.int8)
+    kw = dict(n_buckets=8, nprobe=2, M=32, K=16, rounds=2)
+    a = ctx.build_graph(X, **kw)
+    with debug_opts(ctx, knn_prune=False):
+        b = ctx.build_graph(X, **kw)
+    np.testing.assert_array_equal(a.knn_ids, b.knn_ids)
+    np.testing.assert_array_equal(a.graph, b.graph)
