@@ -12,22 +12,6 @@
 
 namespace gtann {
 
-__device__ __forceinline__ bool key_less_g(float da, int32_t ia, float db, int32_t ib)
-{
-    return da < db || (da == db && ia < ib);
-}
-
-__device__ __forceinline__ int lower_bound_g(const float* ad, const int32_t* ai, int n, float kd, int32_t ki)
-{
-    int lo = 0, hi = n;
-    while (lo < hi) {
-        const int mid = (lo + hi) >> 1;
-        if (key_less_g(ad[mid], ai[mid], kd, ki)) lo = mid + 1;
-        else hi = mid;
-    }
-    return lo;
-}
-
 // ------------------------------------------------------------------ layout
 
 template <typename T>

@@ -251,7 +251,7 @@ enum Ws {
     W_MEMBERS, W_TASKS, W_POOL, W_PART_I, W_PART_D, W_G1, W_G2, W_G3, W_DEG, W_OFF, W_CUR, W_KEYS, W_SUMS, W_FLAG,
     W_TMP, W_OUT, W_IN, W_PROBE_I, W_PROBE_D, W_WORST, W_X8, W_NORMS8, W_C8, W_CNORMS8,
     W_SUBROWS, W_SUBID, W_SUBD, W_SUBOFF, W_MEMBERS2, W_SUBNN, W_SUBNND, W_SUBBASE, W_SUBCNT, W_CHAINPOS,
-    W_LHIST, W_LOFFS, W_LSUMS, W_CAND, W_CANDCNT, W_STATS,
+    W_LHIST, W_LOFFS, W_LSUMS, W_CAND, W_CANDCNT, W_HLIST, W_HCOUNT, W_STATS,
     W_OOC_A, W_OOC_B, W_OOC_C, W_OOC_D, W_OOC_E, W_OOC_F, W_OOC_G, W_CR, W_CRNORMS,
     W_KM_TRAIN, W_KM_MIND, W_KM_FLAG, W_KM_SEL, W_KM_POS, W_KM_SUMS, W_KM_NEW, W_KM_PSI, W_KM_P, W_KM_PN, W_KM_P8,
     W_KM_PN8, W_KM_OI, W_KM_OD, W_CH8, W_CHN, W_CHR, W_CHCNT, W_PAIRS, W_COUNT_
@@ -983,7 +983,8 @@ static void sub_order_members(Ctx& c, const DevMatrix& X, const Buckets& b, int 
 // (the out-of-core build's chunks).
 static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M, int metric, const float* seed_d,
                              int32_t* out_ids, float* out_d, int64_t* max_pool, int64_t* max_bucket,
-                             double* pairs, bool own = true, bool probes = true, int64_t b0 = 0, int64_t b1 = -1)
+                             double* pairs, bool own = true, bool probes = true, int64_t b0 = 0, int64_t b1 = -1,
+                             int32_t* run_ids = nullptr, bool* merged = nullptr)
 {
     const int64_t C = static_cast<int64_t>(b.offsets.size()) - 1;
     const int64_t N = X.N;
@@ -1098,12 +1099,21 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
         a.cand = c.ws<uint64_t>(W_CAND, static_cast<size_t>(rows + kQueriesPerWave) * kCollectCap);
         a.cand_cnt = c.ws<int32_t>(W_CANDCNT, static_cast<size_t>(rows));
         if (tr.on && c.c->dbg.knn_stats) {   // counters of the collect launch (slow), printed below
-            a.stats = c.ws<unsigned long long>(W_STATS, 4);
-            GT_HIP(hipMemsetAsync(a.stats, 0, 4 * sizeof(unsigned long long), c.s));
+            a.stats = c.ws<unsigned long long>(W_STATS, 8);
+            GT_HIP(hipMemsetAsync(a.stats, 0, 8 * sizeof(unsigned long long), c.s));
         }
         a.pairs_done = c.ws<unsigned long long>(W_PAIRS, 1);
         GT_HIP(hipMemsetAsync(a.pairs_done, 0, sizeof(unsigned long long), c.s));
+        // a seeded pass given its running table's ids: the new lists merge
+        // into (run_ids, seed_d) in place
+        if (run_ids && seed_d) {
+            a.run_ids = run_ids;
+            a.run_d = const_cast<float*>(seed_d);
+            a.hl_rows = c.ws<int32_t>(W_HLIST, static_cast<size_t>(rows));
+            a.hl_count = c.ws<uint32_t>(W_HCOUNT, 1);
+        }
     }
+    if (merged) *merged = a.run_ids != nullptr;
     // exact chunk pruning (int8 rows, L2): the centre and radius of every
     // kChunkRows rows of the pool list
     const bool prune = collect && a.Xq8 && a.Xp8 && metric == GT_METRIC_L2 && c.c->dbg.knn_prune != 0 &&
@@ -1147,12 +1157,15 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
                      a.pairs_done ? c.c->knn_pairs_done - done_before : pr, own ? 1 : 0, probes ? 1 : 0,
                      seed_d ? 1 : 0, t * 1e3);
     if (tr.on && a.stats) {
-        unsigned long long h[4];
+        unsigned long long h[8];
         c.d2h(h, a.stats, sizeof(h));
         c.sync();
         std::fprintf(stderr, "[gtann]   collect: %.3g keys (%.1f per query), %llu compactions, %.3g of %.3g wave tiles past the pre-filter\n",
                      static_cast<double>(h[0]), static_cast<double>(h[0]) / static_cast<double>(N), h[1],
                      static_cast<double>(h[2]), static_cast<double>(h[3]));
+        if (a.run_ids)
+            std::fprintf(stderr, "[gtann]   merge: %llu rows with keys, %.3g fresh keys, %llu rows with fresh keys, %llu with more than M\n",
+                         h[4], static_cast<double>(h[5]), h[6], h[7]);
     }
     if (max_pool) *max_pool = std::max(*max_pool, mp);
     if (max_bucket) *max_bucket = std::max(*max_bucket, mb);
@@ -2037,20 +2050,29 @@ static void ooc_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M, int m
         }
         int32_t* oi = mid;
         float* od = mdd;
+        // a pass seeded with the running rows (rid, rdd), merged into them in
+        // place by the collect launch, else through (nid, ndd) into (mid, mdd)
+        auto seeded = [&](bool own, bool probes) {
+            bool merged = false;
+            st.t_knn += bucketed_round(c, X, b, M, metric, rdd, nid, ndd, &st.max_pool, &st.max_bucket,
+                                       &st.knn_pairs, own, probes, b0, b1, rid, &merged);
+            if (merged) {
+                oi = rid;
+                od = rdd;
+            } else {
+                st.t_merge += c.timed([&] { launch_merge_rounds(rid, rdd, nid, ndd, rows, M, mid, mdd, c.s); });
+            }
+        };
         if (r == 0 && b.P > 0) {
             // own buckets unseeded, then the probe buckets seeded with their M-th distance, merged
             st.t_knn += bucketed_round(c, X, b, M, metric, nullptr, rid, rdd, &st.max_pool, &st.max_bucket,
                                        &st.knn_pairs, true, false, b0, b1);
-            st.t_knn += bucketed_round(c, X, b, M, metric, rdd, nid, ndd, &st.max_pool, &st.max_bucket,
-                                       &st.knn_pairs, false, true, b0, b1);
-            st.t_merge += c.timed([&] { launch_merge_rounds(rid, rdd, nid, ndd, rows, M, mid, mdd, c.s); });
+            seeded(false, true);
         } else if (r == 0) {
             st.t_knn += bucketed_round(c, X, b, M, metric, nullptr, mid, mdd, &st.max_pool, &st.max_bucket,
                                        &st.knn_pairs, true, true, b0, b1);
         } else {
-            st.t_knn += bucketed_round(c, X, b, M, metric, rdd, nid, ndd, &st.max_pool, &st.max_bucket,
-                                       &st.knn_pairs, true, true, b0, b1);
-            st.t_merge += c.timed([&] { launch_merge_rounds(rid, rdd, nid, ndd, rows, M, mid, mdd, c.s); });
+            seeded(true, true);
         }
         c.d2h(sti, oi, static_cast<size_t>(rows) * M * 4);
         c.d2h(std_, od, static_cast<size_t>(rows) * M * 4);
@@ -2628,10 +2650,15 @@ int gt_knn_bucketed(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtype,
             }
             seed = run_d;
         }
-        bucketed_round(c, Xm, b, M, metric, seed, cur_i, cur_d, nullptr, nullptr, nullptr);
+        bool merged = false;
+        bucketed_round(c, Xm, b, M, metric, seed, cur_i, cur_d, nullptr, nullptr, nullptr, true, true, 0, -1, run_i,
+                       &merged);
         int32_t* res_i = cur_i;
         float* res_d = cur_d;
-        if (merge) {
+        if (merged) {   // the collect launch merged the new lists into (run_i, run_d)
+            res_i = run_i;
+            res_d = run_d;
+        } else if (merge) {
             int32_t* mi = c.ws<int32_t>(W_G1, nm);
             float* md = c.ws<float>(W_G2, nm);
             launch_merge_rounds(run_i, run_d, cur_i, cur_d, N, M, mi, md, c.s);
@@ -3170,6 +3197,18 @@ int gt_build_graph_ex(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtyp
         float* tmp_d = ooc ? nullptr : c.ws<float>(W_D2, nm);
         ctx->knn_launches = 0;
         ctx->knn_pairs_done = 0.0;
+        // a pass seeded with the running table's M-th distances, its lists
+        // merged into the table: in place by the collect launch (only rows
+        // with keys touched), else into (cur_i, cur_d) and then merged
+        auto seeded = [&](const Buckets& b, bool own, bool probes) {
+            bool merged = false;
+            st.t_knn += bucketed_round(c, Xm, b, p.M, p.metric, run_d, cur_i, cur_d, &st.max_pool, &st.max_bucket,
+                                       &st.knn_pairs, own, probes, 0, -1, run_i, &merged);
+            if (merged) return;
+            st.t_merge += c.timed([&] { launch_merge_rounds(run_i, run_d, cur_i, cur_d, N, p.M, tmp_i, tmp_d, c.s); });
+            std::swap(run_i, tmp_i);
+            std::swap(run_d, tmp_d);
+        };
         // Round r's bucketing = bucket_device (device work + downloads, on
         // this thread) then bucket_host (two-choice + CSR, on a worker
         // thread).  The host half of round r runs while the device computes
@@ -3260,20 +3299,12 @@ int gt_build_graph_ex(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtyp
                 // the same table as one pass over the whole pools)
                 st.t_knn += bucketed_round(c, Xm, b, p.M, p.metric, nullptr, run_i, run_d, &st.max_pool,
                                            &st.max_bucket, &st.knn_pairs, true, false);
-                st.t_knn += bucketed_round(c, Xm, b, p.M, p.metric, run_d, cur_i, cur_d, &st.max_pool,
-                                           &st.max_bucket, &st.knn_pairs, false, true);
-                st.t_merge += c.timed([&] { launch_merge_rounds(run_i, run_d, cur_i, cur_d, N, p.M, tmp_i, tmp_d, c.s); });
-                std::swap(run_i, tmp_i);
-                std::swap(run_d, tmp_d);
+                seeded(b, false, true);
             } else if (r == 0) {
                 st.t_knn += bucketed_round(c, Xm, b, p.M, p.metric, nullptr, run_i, run_d, &st.max_pool,
                                            &st.max_bucket, &st.knn_pairs);
             } else {
-                st.t_knn += bucketed_round(c, Xm, b, p.M, p.metric, run_d, cur_i, cur_d, &st.max_pool,
-                                           &st.max_bucket, &st.knn_pairs);
-                st.t_merge += c.timed([&] { launch_merge_rounds(run_i, run_d, cur_i, cur_d, N, p.M, tmp_i, tmp_d, c.s); });
-                std::swap(run_i, tmp_i);
-                std::swap(run_d, tmp_d);
+                seeded(b, true, true);
             }
         }
         for (int i = 0; i < 2; ++i) bk[i].members.swap(ctx->h_members[i]);

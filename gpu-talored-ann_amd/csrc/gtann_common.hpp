@@ -86,6 +86,13 @@ struct KnnArgs {
     const float* chn;
     const float* chr;
     unsigned long long* pairs_done;   // optional: += (query, pool row) pairs the MFMAs computed
+    // collect launches: when set, the new lists are merged into the running
+    // table (run_ids, run_d) (rows, M) in place instead of written to
+    // (out_ids, out_d), which then hold only the rows the selection took (fp32)
+    int32_t* run_ids;
+    float* run_d;
+    int32_t* hl_rows;      // (rows): int8 merge: the rows left to the selection
+    uint32_t* hl_count;    // their number
 };
 
 constexpr int kChunkRows = 64;       // pool rows per pruning chunk (= one collect stage)
@@ -173,6 +180,23 @@ __device__ __forceinline__ float o2f(uint32_t k)
 __device__ __forceinline__ uint64_t pack_key(float d, int32_t id)
 {
     return (static_cast<uint64_t>(f2o(d)) << 32) | static_cast<uint32_t>(id);
+}
+// (distance, id) order of the cross-round merge: distances as floats, ties
+// by id; lower_bound_g = the number of entries of a list ascending in that
+// order that precede (kd, ki)
+__device__ __forceinline__ bool key_less_g(float da, int32_t ia, float db, int32_t ib)
+{
+    return da < db || (da == db && ia < ib);
+}
+__device__ __forceinline__ int lower_bound_g(const float* ad, const int32_t* ai, int n, float kd, int32_t ki)
+{
+    int lo = 0, hi = n;
+    while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (key_less_g(ad[mid], ai[mid], kd, ki)) lo = mid + 1;
+        else hi = mid;
+    }
+    return lo;
 }
 __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m)
 {

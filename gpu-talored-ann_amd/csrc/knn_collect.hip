@@ -24,7 +24,9 @@
 // (pair_merge32).
 #include "knn_device.hpp"
 
+#include <climits>
 #include <cstdlib>
+#include <type_traits>
 
 namespace gtann {
 
@@ -854,6 +856,9 @@ __global__ void __launch_bounds__(256, 2) knn_f32_collect_kernel(KnnArgs a)
 // Each row's top-M of its cnt[row] candidate keys, ascending, into (out_ids,
 // out_d) (padding -1 / +inf).  Two lanes per row, 128 rows per block; lane
 // (j, h) of a wave keeps positions LM h .. LM h + LM - 1 of row j's list.
+// Rows with at most skip_le keys are neither selected nor written (-1: every
+// row is).  LIST: the rows are rlist[0 .. *rcount) (output row i = list
+// entry i).
 // Keys and results move through a per-wave LDS stage so that every global
 // access is whole rows: each of a wave's 8 loads per step brings 32 keys of
 // 4 rows (16 lanes x 16 bytes per row), all 8 issued before the stage is
@@ -866,19 +871,28 @@ __global__ void __launch_bounds__(256, 2) knn_f32_collect_kernel(KnnArgs a)
 // waves per SIMD instead of three.)
 constexpr int kSelStride = 2 * 16 + 2;   // keys per staged row
 
-template <int LM>
-__global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(3))) knn_select_kernel(const uint64_t* __restrict__ cand,
+template <int LM, bool LIST>
+__global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(LIST ? 2 : 3))) knn_select_kernel(const uint64_t* __restrict__ cand,
                                                          const int32_t* __restrict__ cnt, int64_t rows, int M,
+                                                         int skip_le, const int32_t* __restrict__ rlist,
+                                                         const uint32_t* __restrict__ rcount,
                                                          int32_t* __restrict__ out_ids, float* __restrict__ out_d)
 {
     __shared__ __align__(16) uint64_t stage[kWaves][kQueriesPerWave * kSelStride];
     const int lane = threadIdx.x & 63, h = lane >> 5, j = lane & 31;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (LIST) rows = __builtin_amdgcn_readfirstlane(static_cast<int>(*rcount));
     const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * kWaves + w) * kQueriesPerWave;
     if (row0 >= rows) return;   // wave-uniform
     const int nrows = static_cast<int>(min(static_cast<int64_t>(kQueriesPerWave), rows - row0));
-    const bool valid = j < nrows;
-    const int n = valid ? min(cnt[row0 + j], kCollectCap) : 0;
+    // LIST: the table row of the wave's row j (the loads take row rq + 4 t's
+    // from its lane)
+    const int32_t lrow = LIST ? rlist[min(row0 + j, rows - 1)] : 0;
+    const int n_all = j < nrows ? min(cnt[LIST ? static_cast<int64_t>(lrow) : row0 + j], kCollectCap) : 0;
+    const bool valid = j < nrows && n_all > skip_le;
+    const uint64_t vrows = __ballot(valid && h == 0);   // bit j: row j is written
+    if (vrows == 0) return;                              // wave-uniform
+    const int n = valid ? n_all : 0;
     uint64_t* st = stage[w];
     PairList<LM> PL;
 #pragma unroll
@@ -893,7 +907,10 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_wav
         const uint64_t* src = cand + (row0 + rq) * kCollectCap + c0 + 2 * q;
         intx4 x[8];   // vector type: kept in registers (an array of uint4 structs went to scratch)
 #pragma unroll
-        for (int t = 0; t < 8; ++t) x[t] = *reinterpret_cast<const intx4*>(src + 4 * t * kCollectCap);
+        for (int t = 0; t < 8; ++t)
+            x[t] = LIST ? *reinterpret_cast<const intx4*>(cand + static_cast<int64_t>(__shfl(lrow, rq + 4 * t)) * kCollectCap +
+                                                          c0 + 2 * q)
+                        : *reinterpret_cast<const intx4*>(src + 4 * t * kCollectCap);
         uint64_t* dst = st + rq * kSelStride + 2 * q;
 #pragma unroll
         for (int t = 0; t < 8; ++t) *reinterpret_cast<intx4*>(dst + 4 * t * kSelStride) = x[t];
@@ -940,15 +957,363 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_wav
         if (M % 4 == 0) {
             for (int v = 4 * lane; v < total; v += 256) {
                 const int r = v / M, p = v - r * M;
-                *reinterpret_cast<uint4*>(dst + v) = *reinterpret_cast<const uint4*>(so + r * Ms + p);
+                if ((vrows >> r) & 1)
+                    *reinterpret_cast<uint4*>(dst + v) = *reinterpret_cast<const uint4*>(so + r * Ms + p);
             }
         } else {
             for (int v = lane; v < total; v += 64) {
                 const int r = v / M;
-                dst[v] = so[r * Ms + (v - r * M)];
+                if ((vrows >> r) & 1) dst[v] = so[r * Ms + (v - r * M)];
             }
         }
         wave_sync();   // read out before the distances overwrite it
+    }
+}
+
+// ------------------------------------------------------------ merge into the running table
+
+// The cross-round merge (src/bucket.cu:5021-5053) of a seeded pass, in place:
+// running row r (ascending by (distance, id), padding (-1, +inf) last)
+// becomes the top-M by (distance, id) of itself and the row's new list, a new
+// id already in it dropped -- the rule and arithmetic of merge_rounds_kernel,
+// on the same two lists, so the table is the same bit for bit.  Only rows
+// that received keys are read or written: the merge of a running row with an
+// empty list is the row.  The new list of a row with at most rank_max (<= M)
+// keys is its keys ascending (the selection's list of it), ranked here from
+// the collect buffer; a row with more was selected into (sel_ids, sel_d) by
+// knn_select_kernel (skip_le = rank_max).  With rlist, the rows are
+// rlist[0 .. *rcount) and selected row i is list entry i's.  One wave per
+// rpw (<= 64) rows: the rows with keys one after another, the next one's
+// loads in flight during each merge.
+__global__ void __launch_bounds__(256) knn_merge_run_kernel(const uint64_t* __restrict__ cand,
+                                                            const int32_t* __restrict__ cnt, int64_t rows, int M,
+                                                            int rpw, int rank_max, const int32_t* __restrict__ rlist,
+                                                            const uint32_t* __restrict__ rcount,
+                                                            const int32_t* __restrict__ sel_ids,
+                                                            const float* __restrict__ sel_d, int32_t* run_ids,
+                                                            float* run_d)
+{
+    __shared__ float sRd[kWaves][64], sNd[kWaves][64];
+    __shared__ int32_t sRi[kWaves][64], sNi[kWaves][64];
+    __shared__ uint64_t sK[kWaves][64];
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (rlist) rows = __builtin_amdgcn_readfirstlane(static_cast<int>(*rcount));
+    const int64_t g0 = (static_cast<int64_t>(blockIdx.x) * kWaves + w) * rpw;
+    if (g0 >= rows) return;   // wave-uniform
+    // position g0 + lane's table row
+    const bool mine = lane < rpw && g0 + lane < rows;
+    const int32_t prow = mine ? (rlist ? rlist[g0 + lane] : static_cast<int32_t>(g0 + lane)) : 0;
+    const int nl = mine ? min(cnt[prow], kCollectCap) : 0;
+    uint64_t todo = __ballot(nl > 0);
+    struct In {
+        int32_t ri, ni;
+        float rd, nd;
+        uint64_t key;
+    };
+    // row g0 + r's running entry `lane`, and its new entry `lane` (selected
+    // rows) or key `lane` (rows of at most M keys)
+    auto load = [&](int r, In& x) __attribute__((always_inline)) {
+        const int64_t row = __shfl(prow, r), srow = g0 + r;
+        const int n = __shfl(nl, r);
+        const bool in = lane < M;
+        x.ri = in ? run_ids[row * M + lane] : -1;
+        x.rd = in ? run_d[row * M + lane] : INFINITY;
+        x.ni = -1;
+        x.nd = INFINITY;
+        x.key = kNoKey;
+        if (n > rank_max) {
+            if (in) {
+                x.ni = sel_ids[srow * M + lane];
+                x.nd = sel_d[srow * M + lane];
+            }
+        } else if (lane < n) {
+            x.key = cand[row * kCollectCap + lane];
+        }
+    };
+    if (todo == 0) return;
+    int r = __builtin_ctzll(todo);
+    In cur;
+    load(r, cur);
+    while (true) {
+        todo &= todo - 1;
+        const int rn = todo ? __builtin_ctzll(todo) : -1;
+        In nxt;
+        if (rn >= 0) load(rn, nxt);
+        const int64_t row = __shfl(prow, r);
+        const int n = __shfl(nl, r);
+        int32_t niv = cur.ni;
+        float ndv = cur.nd;
+        if (n <= rank_max) {
+            // the keys ascending: key q goes to its rank among the row's keys
+            // (distinct: one key per pool row)
+            sK[w][lane] = cur.key;
+            wave_sync();
+            int rank = 0;
+            for (int q = 0; q < n; ++q) rank += sK[w][q] < cur.key ? 1 : 0;
+            wave_sync();
+            if (lane < n) sK[w][rank] = cur.key;
+            wave_sync();
+            const uint64_t k = sK[w][lane];
+            const bool has = lane < n;
+            niv = has ? static_cast<int32_t>(static_cast<uint32_t>(k)) : -1;
+            ndv = has ? o2f(static_cast<uint32_t>(k >> 32)) : INFINITY;
+        }
+        // merge_rounds_kernel's steps for one row of at most 64 entries
+        int32_t riv = cur.ri;
+        const float rdv = riv >= 0 ? cur.rd : INFINITY;
+        ndv = niv >= 0 ? ndv : INFINITY;
+        if (riv < 0) riv = INT_MAX;
+        sRd[w][lane] = rdv;
+        sRi[w][lane] = riv;
+        const int nr = static_cast<int>(__popcll(__ballot(riv != INT_MAX)));
+        wave_sync();
+        bool dup = false;
+        if (niv >= 0)
+            for (int q = 0; q < nr; ++q) dup |= (sRi[w][q] == niv);
+        const bool keep = niv >= 0 && !dup;
+        const unsigned long long below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+        const unsigned long long km = __ballot(keep);
+        const int nn = static_cast<int>(__popcll(km));
+        const int cidx = static_cast<int>(__popcll(km & below));
+        if (keep) {
+            sNd[w][cidx] = ndv;
+            sNi[w][cidx] = niv;
+        }
+        wave_sync();
+        if (lane < nr) {
+            const int pos = lane + lower_bound_g(sNd[w], sNi[w], nn, rdv, riv);
+            if (pos < M) {
+                run_ids[row * M + pos] = riv;
+                run_d[row * M + pos] = rdv;
+            }
+        }
+        if (keep) {
+            const int pos = cidx + lower_bound_g(sRd[w], sRi[w], nr, ndv, niv);
+            if (pos < M) {
+                run_ids[row * M + pos] = niv;
+                run_d[row * M + pos] = ndv;
+            }
+        }
+        for (int p = nr + nn + lane; p < M; p += 64) {
+            run_ids[row * M + p] = -1;
+            run_d[row * M + p] = INFINITY;
+        }
+        wave_sync();   // the lists are read before the next row overwrites them
+        if (rn < 0) break;
+        r = rn;
+        cur = nxt;
+    }
+}
+
+// The same in-place merge for int8 rows, with the duplicates dropped before
+// the top M is taken.  A pair's int8 distance is an exact integer, the same
+// in every pass, so an id already in the running row comes back with the
+// same key; and every key of a seeded pass lies at or below the row's
+// running M-th distance, so the running row's own entries within the pass's
+// pools come back (most of a later round's keys).  Dropping the keys whose
+// ids the running row holds before taking the top M leaves the table of
+// select-then-merge unchanged: a key outside the top M of the row's keys has
+// M smaller keys, each in the running row or among the fresh ones.  Per row:
+// the running ids go into two 256-slot LDS tables (slots by two multiplicative
+// hashes); an id that lost both its slots to other ids is compared with the
+// keys from registers (readlane), so a key's id is in the row iff a table
+// slot or a lost id matches it; the fresh keys (at most kCollectCap) are
+// ranked by counting and merged with merge_rounds_kernel's order and
+// positions.  A row without fresh keys is not written; a row with more than
+// M is left to the selection: appended to hl_rows (hl_count, zero on entry),
+// for knn_select_kernel and knn_merge_run_kernel over that list.  Rows with
+// keys are handled in order, RING rows' loads in flight.  The running table's
+// distances must be the library's own (exact) ones.
+constexpr int kFreshSlots = 256;
+constexpr int kFreshRing = 2;   // rows in flight per wave of knn_merge_fresh_kernel
+__device__ __forceinline__ int fresh_h1(int32_t id) { return static_cast<int>((static_cast<uint32_t>(id) * 0x9E3779B1u) >> 24); }
+__device__ __forceinline__ int fresh_h2(int32_t id) { return static_cast<int>((static_cast<uint32_t>(id) * 0x85EBCA6Bu) >> 24); }
+
+template <int RING>
+__global__ void __launch_bounds__(256) knn_merge_fresh_kernel(const uint64_t* __restrict__ cand,
+                                                              const int32_t* __restrict__ cnt, int64_t rows, int M,
+                                                              int32_t* run_ids, float* run_d,
+                                                              int32_t* __restrict__ hl_rows,
+                                                              uint32_t* __restrict__ hl_count,
+                                                              unsigned long long* __restrict__ stats)
+{
+    __shared__ int32_t sT1[kWaves][kFreshSlots], sT2[kWaves][kFreshSlots];
+    __shared__ float sRd[kWaves][64], sNd[kWaves][64];
+    __shared__ int32_t sRi[kWaves][64], sNi[kWaves][64];
+    __shared__ uint64_t sF[kWaves][kCollectCap];
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int64_t g0 = (static_cast<int64_t>(blockIdx.x) * kWaves + w) * 64;
+    if (g0 >= rows) return;   // wave-uniform
+    const int nl = g0 + lane < rows ? min(cnt[g0 + lane], kCollectCap) : 0;
+    uint64_t todo = __ballot(nl > 0), heavy = 0;
+    if (todo == 0) return;
+    for (int i = lane; i < kFreshSlots; i += 64) {
+        sT1[w][i] = -1;
+        sT2[w][i] = -1;
+    }
+    struct In {
+        int32_t ri;
+        float rd;
+        uint64_t key[4];   // keys lane, lane + 64, lane + 128, lane + 192
+    };
+    auto next = [&]() __attribute__((always_inline)) {
+        if (todo == 0) return -1;
+        const int r = __builtin_ctzll(todo);
+        todo &= todo - 1;
+        return r;
+    };
+    // a row's six loads are range-checked buffer loads based at the wave's
+    // first row: a masked lane gets an offset past the range (it reads 0 and
+    // fetches nothing), so every row issues the same loads without a branch
+    // and the loads of the rows in flight are waited for one row at a time
+    const int grows = static_cast<int>(min(static_cast<int64_t>(64), rows - g0));
+    constexpr uint32_t kOut = 0x7FFFFFF0u;
+    const __amdgpu_buffer_rsrc_t rs_i = __builtin_amdgcn_make_buffer_rsrc(run_ids + g0 * M, 0, grows * M * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rs_d = __builtin_amdgcn_make_buffer_rsrc(run_d + g0 * M, 0, grows * M * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rs_c = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint64_t*>(cand) + g0 * kCollectCap, 0, grows * kCollectCap * 8, 0x00020000);
+    // (the raw words only: the masking is applied where the row is merged,
+    // so that nothing waits for a row's loads before then)
+    auto load = [&](int r, In& x) __attribute__((always_inline)) {
+        if (r < 0) return;
+        const int n = __shfl(nl, r);
+        const uint32_t ro = lane < M ? static_cast<uint32_t>((r * M + lane) * 4) : kOut;
+        x.ri = __builtin_amdgcn_raw_buffer_load_b32(rs_i, ro, 0, 0);
+        x.rd = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs_d, ro, 0, 0));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t co = lane + 64 * j < n ? static_cast<uint32_t>((r * kCollectCap + lane + 64 * j) * 8) : kOut;
+            const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs_c, co, 0, 0);
+            x.key[j] = (static_cast<uint64_t>(v[1]) << 32) | v[0];
+        }
+    };
+    const unsigned long long below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+    auto process = [&](int r, const In& raw) __attribute__((always_inline)) {
+        const int64_t row = g0 + r;
+        const int n = __shfl(nl, r);
+        const int nk = (n + 63) >> 6;   // 64-key chunks holding keys (uniform)
+        In cur;   // masked lanes: id -1 / distance +inf, key kNoKey (they read 0)
+        cur.ri = lane < M ? raw.ri : -1;
+        cur.rd = lane < M ? raw.rd : INFINITY;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) cur.key[j] = lane + 64 * j < n ? raw.key[j] : kNoKey;
+        int32_t riv = cur.ri;
+        const float rdv = riv >= 0 ? cur.rd : INFINITY;
+        if (riv < 0) riv = INT_MAX;
+        const bool rv = riv != INT_MAX;
+        const int nr = static_cast<int>(__popcll(__ballot(rv)));
+        const int h1 = fresh_h1(riv), h2 = fresh_h2(riv);
+        if (rv) {
+            sT1[w][h1] = riv;
+            sT2[w][h2] = riv;
+        }
+        sRd[w][lane] = rdv;
+        sRi[w][lane] = riv;
+        wave_sync();
+        int32_t kid[4];
+        bool held[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            kid[j] = static_cast<int32_t>(static_cast<uint32_t>(cur.key[j]));
+            held[j] = false;
+            if (j < nk) held[j] = (sT1[w][fresh_h1(kid[j])] == kid[j]) | (sT2[w][fresh_h2(kid[j])] == kid[j]);
+        }
+        // the running ids that lost both slots, compared from registers
+        uint64_t lost = __ballot(rv & (sT1[w][h1] != riv) & (sT2[w][h2] != riv));
+        while (lost) {
+            const int l = __builtin_ctzll(lost);
+            lost &= lost - 1;
+            const int32_t id = __builtin_amdgcn_readlane(riv, l);
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (j < nk) held[j] |= kid[j] == id;
+        }
+        // fresh keys, compacted in slot order
+        int f = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (j >= nk) break;
+            const bool fresh = (cur.key[j] != kNoKey) & !held[j];
+            const unsigned long long fm = __ballot(fresh);
+            if (fresh) sF[w][f + static_cast<int>(__popcll(fm & below))] = cur.key[j];
+            f += static_cast<int>(__popcll(fm));
+        }
+        if (stats && lane == 0) {   // optional counters: [4] rows, [5] fresh keys, [6] rows with some, [7] > M
+            atomicAdd(stats + 4, 1ull);
+            atomicAdd(stats + 5, static_cast<unsigned long long>(f));
+            if (f > 0) atomicAdd(stats + 6, 1ull);
+            if (f > M) atomicAdd(stats + 7, 1ull);
+        }
+        wave_sync();
+        sT1[w][h1] = -1;   // every slot written for this row back to empty (after the lookups above)
+        sT2[w][h2] = -1;
+        if (f == 0) return;
+        if (f > M) {   // to the selection (listed when the wave ends)
+            heavy |= 1ull << r;
+            return;
+        }
+        // fresh key `lane`'s rank among the fresh keys (distinct)
+        const uint64_t fk = lane < f ? sF[w][lane] : kNoKey;
+        int rk = 0;
+        for (int t = 0; t < f; ++t) rk += sF[w][t] < fk ? 1 : 0;
+        if (lane < f) {
+            sNd[w][rk] = o2f(static_cast<uint32_t>(fk >> 32));
+            sNi[w][rk] = static_cast<int32_t>(static_cast<uint32_t>(fk));
+        }
+        const int nn = f;
+        wave_sync();
+        if (lane < nr) {
+            const int pos = lane + lower_bound_g(sNd[w], sNi[w], nn, rdv, riv);
+            if (pos < M) {
+                run_ids[row * M + pos] = riv;
+                run_d[row * M + pos] = rdv;
+            }
+        }
+        if (lane < nn) {
+            const float nd = sNd[w][lane];
+            const int32_t ni = sNi[w][lane];
+            const int pos = lane + lower_bound_g(sRd[w], sRi[w], nr, nd, ni);
+            if (pos < M) {
+                run_ids[row * M + pos] = ni;
+                run_d[row * M + pos] = nd;
+            }
+        }
+        for (int p = nr + nn + lane; p < M; p += 64) {
+            run_ids[row * M + p] = -1;
+            run_d[row * M + p] = INFINITY;
+        }
+        wave_sync();   // the lists are read before the next row overwrites them
+    };
+    // a ring of RING rows: a slot is refilled with the next row as soon as
+    // its row is merged (rows leave todo in ascending order, so a slot
+    // without a row means no row follows)
+    In buf[RING];
+    int rr[RING];
+#pragma unroll
+    for (int i = 0; i < RING; ++i) {
+        rr[i] = next();
+        load(rr[i], buf[i]);
+    }
+    bool more = true;
+    while (more) {
+#pragma unroll
+        for (int i = 0; i < RING; ++i) {
+            if (more && rr[i] < 0) more = false;
+            if (more) {
+                process(rr[i], buf[i]);
+                rr[i] = next();
+                load(rr[i], buf[i]);
+            }
+        }
+    }
+    // the wave's rows for the selection: one counter update per wave (one
+    // per row serialised on the counter)
+    if (heavy) {
+        uint32_t base = 0;
+        if (lane == 0) base = atomicAdd(hl_count, static_cast<uint32_t>(__popcll(heavy)));
+        base = __shfl(base, 0);
+        if ((heavy >> lane) & 1)
+            hl_rows[base + static_cast<uint32_t>(__popcll(heavy & below))] = static_cast<int32_t>(g0 + lane);
     }
 }
 
@@ -1111,14 +1476,48 @@ void launch_knn_collect_select(const KnnArgs& a, int64_t rows, hipStream_t strea
         GT_HIP(hipGetLastError());
     }
     if (rows <= 0) return;
+    const bool merge = a.run_ids != nullptr;
+    GT_REQUIRE(!merge || (a.run_d && a.seed_d && a.seed_ld == a.M), "collect merge: running table missing");
     const dim3 sgrid(static_cast<unsigned>(ceil_div(rows, kQueriesPerBlock)));
+    const dim3 mgrid(static_cast<unsigned>(ceil_div(rows, int64_t(64) * kWaves)));
+    if (merge && a.Xq8 && a.Xp8) {
+        // int8 rows: duplicates dropped and the rows with at most M fresh keys
+        // merged; the others selected from the list and merged after
+        GT_REQUIRE(a.hl_rows && a.hl_count, "collect merge: row list missing");
+        GT_HIP(hipMemsetAsync(a.hl_count, 0, sizeof(uint32_t), stream));
+        hipLaunchKernelGGL((knn_merge_fresh_kernel<kFreshRing>), mgrid, dim3(256), 0, stream, a.cand, a.cand_cnt,
+                           rows, a.M, a.run_ids, a.run_d, a.hl_rows, a.hl_count, a.stats);
+        GT_HIP(hipGetLastError());
+        if (a.M <= 32)
+            hipLaunchKernelGGL((knn_select_kernel<16, true>), sgrid, dim3(256), 0, stream, a.cand, a.cand_cnt, rows,
+                               a.M, -1, a.hl_rows, a.hl_count, a.out_ids, a.out_d);
+        else
+            hipLaunchKernelGGL((knn_select_kernel<32, true>), sgrid, dim3(256), 0, stream, a.cand, a.cand_cnt, rows,
+                               a.M, -1, a.hl_rows, a.hl_count, a.out_ids, a.out_d);
+        GT_HIP(hipGetLastError());
+        constexpr int kListRpw = 4;   // few rows per wave: the list is short and its rows heavy
+        hipLaunchKernelGGL(knn_merge_run_kernel, dim3(static_cast<unsigned>(ceil_div(rows, int64_t(kListRpw) * kWaves))),
+                           dim3(256), 0, stream, a.cand, a.cand_cnt, rows, a.M, kListRpw, 0, a.hl_rows, a.hl_count,
+                           a.out_ids, a.out_d, a.run_ids, a.run_d);
+        GT_HIP(hipGetLastError());
+        return;
+    }
+    // fp32 rows merged: rows of at most kRankMax keys ranked in the merge,
+    // the others selected first
+    constexpr int kRankMax = 8;
+    const int skip_le = merge ? kRankMax : -1;
     if (a.M <= 32)
-        hipLaunchKernelGGL((knn_select_kernel<16>), sgrid, dim3(256), 0, stream, a.cand, a.cand_cnt, rows, a.M,
-                           a.out_ids, a.out_d);
+        hipLaunchKernelGGL((knn_select_kernel<16, false>), sgrid, dim3(256), 0, stream, a.cand, a.cand_cnt, rows,
+                           a.M, skip_le, nullptr, nullptr, a.out_ids, a.out_d);
     else
-        hipLaunchKernelGGL((knn_select_kernel<32>), sgrid, dim3(256), 0, stream, a.cand, a.cand_cnt, rows, a.M,
-                           a.out_ids, a.out_d);
+        hipLaunchKernelGGL((knn_select_kernel<32, false>), sgrid, dim3(256), 0, stream, a.cand, a.cand_cnt, rows,
+                           a.M, skip_le, nullptr, nullptr, a.out_ids, a.out_d);
     GT_HIP(hipGetLastError());
+    if (merge) {
+        hipLaunchKernelGGL(knn_merge_run_kernel, mgrid, dim3(256), 0, stream, a.cand, a.cand_cnt, rows, a.M, 64,
+                           kRankMax, nullptr, nullptr, a.out_ids, a.out_d, a.run_ids, a.run_d);
+        GT_HIP(hipGetLastError());
+    }
 }
 
 }  // namespace gtann

@@ -66,8 +66,11 @@ int gt_assign_top2(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtype, 
  * (every point in exactly one bucket); its pool is its own members followed
  * by the members of probe[b*P .. b*P+P) (ids >= nB skipped).  Each point gets
  * the M nearest pool points other than itself.  merge = 0: ids/dists (N x M)
- * are outputs.  merge = 1: ids/dists hold the running table on input and the
- * merged table (top-M of both, duplicates once) on output.
+ * are outputs.  merge = 1: ids/dists hold the running table on input (rows
+ * ascending by (distance, id), padding (-1, +inf) last, as this call writes
+ * them) and the merged table (top-M of both, duplicates once) on output; a
+ * row with no new pool point within its running M-th distance keeps its
+ * running list as it is.
  * Replaces GpuResidentKnn::run_round (src/bucket.cu:5310-5546). */
 int gt_knn_bucketed(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtype, int metric,
                     const int64_t* offsets, const int32_t* members, int64_t nB,

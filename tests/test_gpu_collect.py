@@ -126,6 +126,52 @@ def test_collect_rounds_match_oracle(ctx):
         assert_knn_equal(ids, dist, *ref)
 
 
+def _mixed_running(ids, dist, other_ids, other_dist):
+    """Running rows of every shape the in-place merge meets: a pass's own
+    table (its keys come back: no fresh key), padding only (every key fresh,
+    more than M), a short prefix + padding (threshold +inf), the row with a
+    middle stretch removed (+ padding), and the row of another bucketing's
+    table.  Every distance is the pair's exact one, as in a build."""
+    N, M = ids.shape
+    ri, rd = ids.copy(), dist.copy()
+    k = np.arange(N) % 5
+    ri[k == 1], rd[k == 1] = -1, np.inf
+    ri[k == 2, 5:], rd[k == 2, 5:] = -1, np.inf
+    sel = np.flatnonzero(k == 3)
+    keep = np.r_[0:M // 4, M // 2:M]
+    ri[sel, :len(keep)], rd[sel, :len(keep)] = ids[sel][:, keep], dist[sel][:, keep]
+    ri[sel, len(keep):], rd[sel, len(keep):] = -1, np.inf
+    ri[k == 4], rd[k == 4] = other_ids[k == 4], other_dist[k == 4]
+    return ri, rd
+
+
+@pytest.mark.parametrize("M,metric", [(64, "l2"), (33, "l2"), (17, "l2"), (64, "ip")])
+def test_collect_merge_mixed_running_rows(ctx, M, metric):
+    # a seeded pass merged into the running table in place: rows without
+    # keys, rows whose keys all repeat running ids, rows with a few fresh
+    # keys and rows with more than M, all against the oracle's pass +
+    # cross-round merge
+    rng = np.random.default_rng(31 + M)
+    N, B = 7000, 7
+    X = _data(N, 96, seed=32 + M, lo=-40, hi=41)
+    mi = 1 if metric == "ip" else 0
+    sign = -1 if metric == "ip" else 1
+    off, mem = _buckets(rng, N, B)
+    probe = _probe(rng, B, 1)
+    ai, ad = O.knn_bucketed(X.astype(np.float32), off, mem, probe, M, metric=mi)
+    off3, mem3 = _buckets(rng, N, B)
+    bi, bd = O.knn_bucketed(X.astype(np.float32), off3, mem3, _probe(rng, B, 1), M, metric=mi)
+    ri, rd = _mixed_running(ai, ad, bi, bd)
+    off2, mem2 = _buckets(rng, N, B)
+    probe2 = _probe(rng, B, 1)
+    print(f"collect merge into mixed running rows M={M} {metric}", flush=True)
+    ids, dist = ctx.knn_bucketed(X, off2, mem2, probe2, M, metric=metric, running=(ri, sign * rd))
+    ni, nd = O.knn_bucketed(X.astype(np.float32), off2, mem2, probe2, M, metric=mi)
+    ei, ed = O.merge_rounds(ri, rd, ni, nd)
+    np.testing.assert_array_equal(ids, ei)
+    np.testing.assert_array_equal((sign * dist).view(np.uint32), ed.view(np.uint32))
+
+
 def test_collect_equals_merging_kernel(ctx):
     # the same passes through the kernel that merges as it scans
     rng = np.random.default_rng(15)
