@@ -192,12 +192,25 @@ def search_leg(ctx, torch, name, nq, kw, efs, cpu_sample):
 def knn_roofline(s, D, metric, M=64):
     """Roofline of the round launches of the kNN kernel from the library's
     own event times (mean build stats s).  Integer rows with lists of at most
-    64 run as two kernels per launch (knn_i8_collect_kernel keeps the pairs
-    under a per-query bound, knn_select_kernel reduces them to the top M);
-    the library times the pair as one launch."""
+    64 run as one launch of several kernels (chunk_bounds_kernel: the
+    pruning spheres; knn_i8_collect_kernel keeps the pairs under a per-query
+    bound; knn_select_kernel reduces them to the top M, or for a seeded pass
+    knn_merge_fresh_kernel merges them into the running table, the rows with
+    more than M fresh keys through a listed knn_select_kernel +
+    knn_merge_run_kernel); the library times the launch as one.
+
+    `achieved`/`frac`: the algorithmic ops, 2*D per (query, pool row) pair of
+    the bucketed scan (every pair of every pool, what the reference's GEMM
+    computes), over the launch time.  The int8 kernel skips pool chunks whose
+    bounding sphere lies beyond every query's bound, so it multiplies fewer
+    pairs: `ops_executed_per_launch` / `frac_executed` count those (the
+    pairs the MFMAs actually computed, counted on the device)."""
     launches = max(1, int(round(s["knn_launches"])))
     launch_s = s["t_knn"] / launches
     flops = s["knn_flops"] / launches
+    pairs = max(float(s.get("knn_pairs", 0.0)), 1.0)
+    done = float(s.get("knn_pairs_computed", 0.0)) or pairs
+    executed = flops * done / pairs
     int8 = bool(round(s["knn_int8"]))
     mip = 1 if metric == "ip" else 0
     if int8:
@@ -214,6 +227,8 @@ def knn_roofline(s, D, metric, M=64):
         kname, peak, unit = f"knn_wide_kernel<{mip}>", PEAK_FP32_MFMA, "TFLOP/s"
     return {"kernel": kname, "bound": "mfma", "achieved": flops / launch_s / 1e12, "peak": peak / 1e12,
             "unit": unit, "frac": flops / launch_s / peak, "flops_per_launch": flops,
+            "ops_executed_per_launch": executed, "pairs_executed_share": done / pairs,
+            "frac_executed": executed / launch_s / peak,
             "launch_ms": launch_s * 1e3, "launches": launches}
 
 
@@ -592,6 +607,10 @@ def main():
     ns = {"build_ms": round(wall * 1e3, 3), "Mpts_s": round(N / wall / 1e6, 3),
           "recall@32": round(rec["recall@32"], 4), "recall_gate_0.95": rec["recall@32"] >= 0.95,
           "knn_kernel": roof["kernel"].split(" (")[0], "knn_frac_of_peak": round(roof["frac"], 4),
+          "knn_pairs_executed_share": round(roof["pairs_executed_share"], 4),
+          "knn_frac_of_peak_executed": round(roof["frac_executed"], 4),
+          "knn_launch_ms": round(roof["launch_ms"], 3),
+          "knn_traffic_gb_per_launch": round(traffic / 1e9, 3) if traffic else None,
           "knn_mfma_busy_pct": (tr or {}).get("mfma_busy_pct"),
           "prune_frac_hbm": round(out["roofline_prune"]["frac"], 4),
           "revmerge_frac_hbm": round(out["roofline_revmerge"]["frac"], 4)}
@@ -607,6 +626,7 @@ def main():
     if "configs" in out:
         ns["configs"] = {k: {"ms": round(v["ms_per_step"], 2), "recall@32": round(v["recall@32"], 4),
                              "knn_frac": round(v["knn_roofline"]["frac"], 3),
+                             "knn_mfma_busy_pct": ((v["knn_roofline"].get("rocprof") or {}).get("mfma_busy_pct")),
                              "prune_frac_hbm": round(v["prune_frac_hbm"], 3),
                              "revmerge_frac_hbm": round(v["revmerge_frac_hbm"], 3)} for k, v in out["configs"].items()}
     out["north_star"] = ns

@@ -22,3 +22,11 @@ def ctx():
     c = gtann.Context(0)
     yield c
     c.close()
+
+
+def pytest_sessionfinish(session, exitstatus):
+    # the float tolerance's calibration data, when float tests ran
+    import helpers
+    if helpers.ERR_ULPS_MAX:
+        print("\n[floor] largest error in ulps of the operand magnitude, by (metric, D): " +
+              ", ".join(f"{m} D={d}: {v:.2f}" for (m, d), v in sorted(helpers.ERR_ULPS_MAX.items())), flush=True)

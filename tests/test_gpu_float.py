@@ -33,6 +33,9 @@ def _probe(rng, B, P):
     return np.stack([rng.permutation(np.delete(np.arange(B), b))[:P] for b in range(B)]).astype(np.int32)
 
 
+FLOOR_DECIDED_MAX = {"C1": 0.06, "C3": 0.0, "C4": 0.0005}
+
+
 @pytest.mark.parametrize("cfg,N,B,P,M,rounds", [("C1", 6000, 12, 2, 64, 3), ("C3", 6000, 12, 2, 64, 3),
                                                 ("C4", 3000, 8, 2, 96, 2)])
 def test_knn_bucketed_float_rounds_match_oracle(ctx, cfg, N, B, P, M, rounds):
@@ -51,7 +54,11 @@ def test_knn_bucketed_float_rounds_match_oracle(ctx, cfg, N, B, P, M, rounds):
         run = (ids, dist)
         got_d = -dist if metric == "ip" else dist   # the library reports the inner product itself
         assert_knn_close(X, np.arange(N), ids, got_d, ref[0], ref[1], rtol=1e-5, metric=metric)
-    print(f"  floor statistics {cfg}: {floor_report()}", flush=True)
+    st = floor_report()
+    print(f"  floor statistics {cfg}: {st}", flush=True)
+    # share of distance positions whose error exceeds 1e-5 relative (decided
+    # by the floor): measured C1 5.2 % (88 % of rows), C3 none, C4 0.014 %
+    assert st["positions_floor_decided"] <= FLOOR_DECIDED_MAX[cfg]
 
 
 def _check_build(ctx, X, metric, n_buckets, M, K, min_recall, sample=1000):
