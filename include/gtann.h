@@ -70,7 +70,11 @@ int gt_assign_top2(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtype, 
  * ascending by (distance, id), padding (-1, +inf) last, as this call writes
  * them) and the merged table (top-M of both, duplicates once) on output; a
  * row with no new pool point within its running M-th distance keeps its
- * running list as it is.
+ * running list as it is.  On integer rows the running distances must be
+ * the exact ones this library computes (a table from an earlier call or
+ * from gt_knn_exact): the merge drops a new key whose id the running row
+ * holds before taking the top M, which equals the merge of the top M only
+ * when a pair's distance is the same in both.
  * Replaces GpuResidentKnn::run_round (src/bucket.cu:5310-5546). */
 int gt_knn_bucketed(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtype, int metric,
                     const int64_t* offsets, const int32_t* members, int64_t nB,
