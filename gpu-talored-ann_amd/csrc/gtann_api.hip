@@ -114,6 +114,10 @@ void launch_centroid_sums(const float* X, int Dp, const int32_t* members, const 
 int csr_blocks(int64_t S);
 void launch_sample_csr(const int32_t* key, const int32_t* val, int64_t S, int C, uint32_t* hist, uint32_t* offs,
                        uint32_t* sums, int32_t* members, int64_t* off, hipStream_t s);
+void launch_gather_i32(const int32_t* src, const int32_t* idx, int64_t n, int32_t* out, hipStream_t s);
+void launch_bucket_csr(const uint32_t* top2, const int32_t* bucket, int64_t N, int C, int32_t* key2, int32_t* by_key,
+                       int32_t* bkt, uint32_t* hist, uint32_t* offs, uint32_t* sums, int32_t* members, int64_t* off,
+                       hipStream_t s);
 
 struct CopyTaskH { int64_t src; int64_t dst; int64_t n; };
 
@@ -230,6 +234,7 @@ struct gt_ctx {
     gtann::DevBuf ws[96];
     gtann::HostBuf pinned[2];   // top-2 assignment downloads of two consecutive rounds
     gtann::HostBuf pin_lloyd;   // Lloyd steps: nearest centroids down, CSR up
+    gtann::HostBuf pin_bucket[2];   // two-choice buckets of two consecutive rounds (uploaded for the device CSR)
     // host scratch of the bucketing, reused across calls (no page faults on
     // fresh N-sized allocations every round)
     std::vector<int32_t> h_bucket_of, h_key2, h_by_key, h_bkt;
@@ -254,7 +259,8 @@ enum Ws {
     W_LHIST, W_LOFFS, W_LSUMS, W_CAND, W_CANDCNT, W_HLIST, W_HCOUNT, W_STATS,
     W_OOC_A, W_OOC_B, W_OOC_C, W_OOC_D, W_OOC_E, W_OOC_F, W_OOC_G, W_CR, W_CRNORMS,
     W_KM_TRAIN, W_KM_MIND, W_KM_FLAG, W_KM_SEL, W_KM_POS, W_KM_SUMS, W_KM_NEW, W_KM_PSI, W_KM_P, W_KM_PN, W_KM_P8,
-    W_KM_PN8, W_KM_OI, W_KM_OD, W_CH8, W_CHN, W_CHR, W_CHCNT, W_PAIRS, W_COUNT_
+    W_KM_PN8, W_KM_OI, W_KM_OD, W_CH8, W_CHN, W_CHR, W_CHCNT, W_PAIRS, W_TOP2A, W_TOP2B, W_BUCKETD, W_KEY2,
+    W_BYKEY, W_BKTD, W_BOFF, W_SUBPOS, W_COUNT_
 };
 static_assert(W_COUNT_ <= 96, "workspace slots");
 
@@ -590,7 +596,10 @@ static std::vector<int32_t> sample_ids(int64_t N, int64_t C, uint64_t seed)
     };
     uint64_t st = seed * 0x9E3779B97F4A7C15ull + 0x632BE59BD9B4E019ull;
     for (int64_t jj = N - C; jj < N; ++jj) {
-        const int64_t t = static_cast<int64_t>(splitmix64(st) % static_cast<uint64_t>(jj + 1));
+        // uniform in [0, jj] by a 64 x 64 -> 128-bit multiply (Lemire's
+        // reduction) instead of a 64-bit division
+        const int64_t t = static_cast<int64_t>(
+            (static_cast<unsigned __int128>(splitmix64(st)) * static_cast<uint64_t>(jj + 1)) >> 64);
         if (test_set(t)) test_set(jj);
     }
     std::vector<int32_t> ids;
@@ -689,10 +698,9 @@ static uint64_t next_bucket_gen()
 // one's, sizes counted in point order.  Centroids that are data points sit
 // in their own bucket from the start.
 static void assign_two_choice(const uint32_t* top2, int64_t N, int64_t C, float balance,
-                              const std::vector<int32_t>* centroid_ids, std::vector<int32_t>& bucket_of)
+                              const std::vector<int32_t>* centroid_ids, int32_t* bucket_of)
 {
-    bucket_of.resize(static_cast<size_t>(N));
-    std::fill(bucket_of.begin(), bucket_of.end(), -1);
+    std::fill(bucket_of, bucket_of + N, -1);
     std::vector<int64_t> size(static_cast<size_t>(C), 0);
     if (centroid_ids) {
         for (int64_t c = 0; c < C; ++c) {
@@ -700,17 +708,23 @@ static void assign_two_choice(const uint32_t* top2, int64_t N, int64_t C, float 
             size[static_cast<size_t>(c)] = 1;
         }
     }
+    // every nearest centroid valid (checked before the sequential loop)
+    bool bad = false;
+    for (int64_t i = 0; i < N; ++i) bad |= top2[static_cast<size_t>(2 * i)] >= static_cast<uint64_t>(C);
+    GT_REQUIRE(!bad, "top-2 assignment returned an invalid centroid");
+    const double bal = balance > 0.f ? static_cast<double>(balance) : -1.0;   // -1: never the second
+    int64_t* sz = size.data();
     for (int64_t i = 0; i < N; ++i) {
-        if (bucket_of[static_cast<size_t>(i)] >= 0) continue;
+        if (bucket_of[i] >= 0) continue;
         const uint32_t c1 = top2[static_cast<size_t>(2 * i)];
         const uint32_t c2 = top2[static_cast<size_t>(2 * i + 1)];
-        GT_REQUIRE(c1 < static_cast<uint64_t>(C), "top-2 assignment returned an invalid centroid");
-        uint32_t chosen = c1;
-        if (balance > 0.f && c2 < static_cast<uint64_t>(C) &&
-            static_cast<double>(size[c2]) < static_cast<double>(balance) * static_cast<double>(size[c1]))
-            chosen = c2;
-        bucket_of[static_cast<size_t>(i)] = static_cast<int32_t>(chosen);
-        size[chosen]++;
+        // branch-free: the second centroid's size read at c1 when it is missing
+        const bool ok2 = c2 < static_cast<uint64_t>(C);
+        const uint32_t c2s = ok2 ? c2 : c1;
+        const bool take = ok2 && static_cast<double>(sz[c2s]) < bal * static_cast<double>(sz[c1]);
+        const uint32_t chosen = take ? c2 : c1;
+        bucket_of[i] = static_cast<int32_t>(chosen);
+        sz[chosen]++;
     }
 }
 
@@ -858,16 +872,15 @@ static void counting_sort_kv(const int32_t* key, const int32_t* val, int64_t n, 
 // CSR of an assignment with members ordered by (bucket, key2, id): two stable
 // counting sorts.  key2 = each point's other top-2 centroid, so that points
 // of one bucket near the same neighbouring bucket sit next to each other.
-static void csr_from_assignment_keyed(const std::vector<int32_t>& bucket_of, const std::vector<int32_t>& key2,
+static void csr_from_assignment_keyed(const int32_t* bucket_of, int64_t N, const std::vector<int32_t>& key2,
                                       int64_t C, Buckets& b, std::vector<int32_t>& by_key, std::vector<int32_t>& bkt)
 {
-    const int64_t N = static_cast<int64_t>(bucket_of.size());
     by_key.resize(static_cast<size_t>(N));
     bkt.resize(static_cast<size_t>(N));
     std::vector<int64_t> off;
     // the ids by key2, each carrying its bucket, then by bucket: both passes
     // read their keys in order
-    counting_sort_kv(key2.data(), nullptr, N, C, by_key.data(), bucket_of.data(), bkt.data(), off);
+    counting_sort_kv(key2.data(), nullptr, N, C, by_key.data(), bucket_of, bkt.data(), off);
     b.members.resize(static_cast<size_t>(N));
     counting_sort_kv(bkt.data(), by_key.data(), N, C, b.members.data(), nullptr, nullptr, b.offsets);
 }
@@ -898,7 +911,7 @@ static void sub_order_members(Ctx& c, const DevMatrix& X, const Buckets& b, int 
         const int64_t p0 = static_cast<int64_t>(subrows.size());
         sbase[static_cast<size_t>(bb)] = p0;
         scount[static_cast<size_t>(bb)] = static_cast<int32_t>(s);
-        for (int64_t i = 0; i < s; ++i) subrows.push_back(b.members[static_cast<size_t>(lo + i * n / s)]);
+        for (int64_t i = 0; i < s; ++i) subrows.push_back(static_cast<int32_t>(lo + i * n / s));   // positions
         for (int64_t t = 0; t < s; t += kQueriesPerBlock) {   // sub-centroids among themselves
             WorkItem it;
             it.q_begin = p0 + t;
@@ -922,8 +935,12 @@ static void sub_order_members(Ctx& c, const DevMatrix& X, const Buckets& b, int 
         any = true;
     }
     if (!any) return;
+    // the sub-centroid rows: the members at those positions (d_members holds
+    // this bucketing's members in its own order)
+    int32_t* d_subpos = c.ws<int32_t>(W_SUBPOS, subrows.size());
+    c.h2d(d_subpos, subrows.data(), subrows.size() * sizeof(int32_t));
     int32_t* d_sub = c.ws<int32_t>(W_SUBROWS, subrows.size());
-    c.h2d(d_sub, subrows.data(), subrows.size() * sizeof(int32_t));
+    launch_gather_i32(d_members, d_subpos, static_cast<int64_t>(subrows.size()), d_sub, c.s);
     const std::vector<WorkItem> items = layout_xcd(groups);
     WorkItem* d_items = c.ws<WorkItem>(W_ITEMS, items.size());
     c.h2d(d_items, items.data(), items.size() * sizeof(WorkItem));
@@ -1026,6 +1043,7 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
     // the sub-centroid order, which changes no result)
     int32_t* d_members = c.ws<int32_t>(W_MEMBERS, static_cast<size_t>(N));
     if (b.gen == 0 || c.c->members_gen != b.gen) {
+        GT_REQUIRE(static_cast<int64_t>(b.members.size()) == N, "bucket members are on the device only");
         c.h2d(d_members, b.members.data(), static_cast<size_t>(N) * sizeof(int32_t));
         if (b.uploaded) GT_HIP(hipEventRecord(b.uploaded, c.s));
         c.c->members_gen = b.gen;
@@ -1183,6 +1201,7 @@ struct BucketPlan {
     std::vector<int32_t> cid;       // sampled centroid row ids, ascending
     bool data_points = true;        // centroids are data points (no Lloyd)
     const uint32_t* top2 = nullptr; // pinned, 2N: nearest and 2nd nearest centroid
+    const uint32_t* d_top2 = nullptr;   // the same on the device (the round's own buffer), or null
     std::vector<int32_t> probe;     // C x P
     int P = 0;
 };
@@ -1307,8 +1326,8 @@ static std::vector<int32_t> kmeans_par_seeds(Ctx& c, const DevMatrix& X, int64_t
 }
 
 static void bucket_device(Ctx& c, const DevMatrix& X, int64_t C, int nprobe, int metric, int kmeans_iters,
-                          RoundSamples&& draws, HostBuf& pin, BucketPlan& bp, std::vector<int32_t>* cknn = nullptr,
-                          int cknn_k = 0)
+                          RoundSamples&& draws, HostBuf& pin, BucketPlan& bp, int parity,
+                          std::vector<int32_t>* cknn = nullptr, int cknn_k = 0)
 {
     const int64_t N = X.N;
     Trace tr;
@@ -1440,8 +1459,12 @@ static void bucket_device(Ctx& c, const DevMatrix& X, int64_t C, int nprobe, int
     bp.data_points = data_points;
     uint32_t* top2 = pin.as<uint32_t>(static_cast<size_t>(2 * N));
     bp.top2 = top2;
+    bp.d_top2 = nullptr;
     if (C >= 2) {
-        int32_t* d_t2 = c.ws<int32_t>(W_IDS3, static_cast<size_t>(2 * N));
+        // (each round parity its own buffer: the device CSR of a round reads
+        // it after the next round's centroids are computed)
+        int32_t* d_t2 = c.ws<int32_t>(parity ? W_TOP2B : W_TOP2A, static_cast<size_t>(2 * N));
+        bp.d_top2 = reinterpret_cast<const uint32_t*>(d_t2);
         float* d_t2d = c.ws<float>(W_D3, static_cast<size_t>(2 * N));
         KnnJob j;
         j.Q = &X;
@@ -1537,10 +1560,11 @@ static void bucket_device(Ctx& c, const DevMatrix& X, int64_t C, int nprobe, int
     }
 }
 
-// The host half: two-choice rule over the downloaded top-2 lists, then the
-// members ordered by (bucket, other top-2 centroid, id).  Host code only (no
-// HIP calls), so the build runs it on a worker thread.
-static void bucket_host(const BucketPlan& bp, float balance, Buckets& b, std::vector<int32_t>& bucket_of,
+// The host half: two-choice rule over the downloaded top-2 lists into
+// bucket_of (N), then, with csr, the members ordered by (bucket, other top-2
+// centroid, id) (without it the device orders them: launch_bucket_csr).
+// Host code only (no HIP calls), so the build runs it on a worker thread.
+static void bucket_host(const BucketPlan& bp, float balance, Buckets& b, int32_t* bucket_of, bool csr,
                         std::vector<int32_t>& key2, std::vector<int32_t>& by_key, std::vector<int32_t>& bkt)
 {
     const int64_t N = bp.N, C = bp.C;
@@ -1548,6 +1572,14 @@ static void bucket_host(const BucketPlan& bp, float balance, Buckets& b, std::ve
     Trace tr;
     assign_two_choice(top2, N, C, balance, bp.data_points ? &bp.cid : nullptr, bucket_of);
     const double t_tc = tr.t.sec();
+    b.P = bp.P;
+    b.probe = bp.probe;
+    b.gen = next_bucket_gen();
+    if (!csr) {
+        b.members.clear();   // the members live on the device only
+        if (tr.on) std::fprintf(stderr, "[gtann] bucketing (host thread): two-choice %.3f ms\n", t_tc * 1e3);
+        return;
+    }
     key2.resize(static_cast<size_t>(N));
     parallel_slices(N, host_threads(), [&](int, int64_t lo, int64_t hi) {
         for (int64_t i = lo; i < hi; ++i) {
@@ -1557,10 +1589,7 @@ static void bucket_host(const BucketPlan& bp, float balance, Buckets& b, std::ve
                                                                               : bucket_of[static_cast<size_t>(i)];
         }
     });
-    csr_from_assignment_keyed(bucket_of, key2, C, b, by_key, bkt);
-    b.P = bp.P;
-    b.probe = bp.probe;
-    b.gen = next_bucket_gen();
+    csr_from_assignment_keyed(bucket_of, N, key2, C, b, by_key, bkt);
     if (tr.on)
         std::fprintf(stderr, "[gtann] bucketing (host thread): two-choice %.3f ms, CSR %.3f ms\n", t_tc * 1e3,
                      (tr.t.sec() - t_tc) * 1e3);
@@ -2283,6 +2312,7 @@ void gt_destroy(gt_ctx* ctx)
     }
     for (auto& pb : ctx->pinned) pb.release();
     ctx->pin_lloyd.release();
+    for (gtann::HostBuf& b : ctx->pin_bucket) b.release();
     if (ctx->ev0) (void)hipEventDestroy(ctx->ev0);
     if (ctx->ev1) (void)hipEventDestroy(ctx->ev1);
     for (hipEvent_t e : ctx->members_up)
@@ -3160,17 +3190,19 @@ int gt_build_graph_ex(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtyp
         Ctx c(ctx);
         int64_t C = p.n_buckets > 0 ? p.n_buckets : std::max<int64_t>(1, N / 4000);
         C = std::min<int64_t>(C, N);
-        // every round's random draws, on a worker thread while the dataset is prepared
-        std::future<std::vector<RoundSamples>> draws_job = std::async(std::launch::async, [N, C, p] {
-            std::vector<RoundSamples> d;
-            for (int r = 0; r < p.rounds; ++r) d.push_back(draw_round(N, C, p, p.seed + static_cast<uint64_t>(r)));
-            return d;
-        });
+        // every round's random draws, one worker thread per round, while the
+        // dataset is prepared
+        std::vector<std::future<RoundSamples>> draws_jobs;
+        for (int r = 0; r < p.rounds; ++r)
+            draws_jobs.push_back(std::async(std::launch::async, [N, C, p, r] {
+                return draw_round(N, C, p, p.seed + static_cast<uint64_t>(r));
+            }));
         Timer tp;
         DevMatrix Xm = prepare(c, W_X, W_XRAW, W_NORMS, X, N, D, dtype, true, p.int_exact != 0);
         c.sync();
         st.t_prepare = tp.sec();
-        std::vector<RoundSamples> draws = draws_job.get();
+        std::vector<RoundSamples> draws;
+        for (auto& j : draws_jobs) draws.push_back(j.get());
         int nprobe = p.nprobe;
         if (nprobe < 0) nprobe = static_cast<int>(std::ceil(20000.0 / (static_cast<double>(N) / C)));
         nprobe = static_cast<int>(std::min<int64_t>(nprobe, C - 1));
@@ -3226,19 +3258,48 @@ int gt_build_graph_ex(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtyp
         auto device_part = [&](int r) {
             Timer tb;
             bucket_device(c, Xm, C, nprobe, p.metric, p.kmeans_iters, std::move(draws[static_cast<size_t>(r)]),
-                          ctx->pinned[r & 1], plans[r & 1], r == 0 && want_cknn ? &cknn : nullptr,
+                          ctx->pinned[r & 1], plans[r & 1], r & 1, r == 0 && want_cknn ? &cknn : nullptr,
                           r == 0 && want_cknn ? extras->centroid_knn_k : 0);
             st.t_bucketing += tb.sec();
         };
+        // the members' order (bucket, other top-2 centroid, id) is computed on
+        // the device from the round's top-2 lists and the host's two-choice
+        // buckets (the host half then only runs the sequential rule), except
+        // out of core, where the host keeps the members, and where the debug
+        // options ask for the host
+        const bool dev_csr = !ooc && C >= 2 && C <= 16384 && c.c->dbg.bucket_host_csr == 0;
+        auto bucket_of_host = [&](int r) { return ctx->pin_bucket[r & 1].as<int32_t>(static_cast<size_t>(N)); };
         std::future<void> host_job;   // declared after everything it references
         auto start_host = [&](int r) {
-            // the previous upload of these buckets' members (two rounds ago)
-            // has been read before the host half rewrites them
+            // the previous upload of these buckets (two rounds ago) has been
+            // read before the host half rewrites them
             GT_HIP(hipEventSynchronize(bk[r & 1].uploaded));
-            host_job = std::async(std::launch::async, [&, r] {
-                bucket_host(plans[r & 1], p.balance, bk[r & 1], ctx->h_bucket_of, ctx->h_key2, ctx->h_by_key,
-                            ctx->h_bkt);
+            int32_t* bo = bucket_of_host(r);
+            host_job = std::async(std::launch::async, [&, r, bo] {
+                bucket_host(plans[r & 1], p.balance, bk[r & 1], bo, !dev_csr, ctx->h_key2, ctx->h_by_key, ctx->h_bkt);
             });
+        };
+        // round r's members into W_MEMBERS and its offsets to the host
+        auto device_csr = [&](int r) {
+            Timer tc;
+            Buckets& b = bk[r & 1];
+            int32_t* d_bucket = c.ws<int32_t>(W_BUCKETD, static_cast<size_t>(N));
+            c.h2d(d_bucket, bucket_of_host(r), static_cast<size_t>(N) * sizeof(int32_t));
+            if (b.uploaded) GT_HIP(hipEventRecord(b.uploaded, c.s));
+            const int64_t nh = C * csr_blocks(N);
+            int32_t* d_mem = c.ws<int32_t>(W_MEMBERS, static_cast<size_t>(N));
+            int64_t* d_off = c.ws<int64_t>(W_BOFF, static_cast<size_t>(C + 1));
+            launch_bucket_csr(plans[r & 1].d_top2, d_bucket, N, static_cast<int>(C), c.ws<int32_t>(W_KEY2, static_cast<size_t>(N)),
+                              c.ws<int32_t>(W_BYKEY, static_cast<size_t>(N)), c.ws<int32_t>(W_BKTD, static_cast<size_t>(N)),
+                              c.ws<uint32_t>(W_LHIST, static_cast<size_t>(nh)),
+                              c.ws<uint32_t>(W_LOFFS, static_cast<size_t>(nh + 1)),
+                              c.ws<uint32_t>(W_LSUMS, static_cast<size_t>(nh / 1024 + 2)), d_mem, d_off, c.s);
+            b.offsets.resize(static_cast<size_t>(C + 1));
+            c.d2h(b.offsets.data(), d_off, static_cast<size_t>(C + 1) * sizeof(int64_t));
+            c.sync();
+            GT_REQUIRE(b.offsets[0] == 0 && b.offsets[static_cast<size_t>(C)] == N, "device bucket CSR");
+            c.c->members_gen = b.gen;   // W_MEMBERS holds these buckets' members
+            st.t_bucketing += tc.sec();
         };
         device_part(0);
         start_host(0);
@@ -3249,11 +3310,13 @@ int gt_build_graph_ex(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtyp
                 host_job.get();   // rethrows the host half's errors
                 st.t_bucketing += tw.sec();
             }
+            if (dev_csr && plans[r & 1].d_top2) device_csr(r);
+            GT_REQUIRE(!dev_csr || plans[r & 1].d_top2, "device bucket CSR without device top-2 lists");
             if (r == 0 && extras) {
                 if (extras->round1_bucket) {
-                    const std::vector<int32_t>& bo = c.c->h_bucket_of;
-                    if (is_device_ptr(extras->round1_bucket)) c.h2d(extras->round1_bucket, bo.data(), bo.size() * sizeof(int32_t));
-                    else std::memcpy(extras->round1_bucket, bo.data(), bo.size() * sizeof(int32_t));
+                    const int32_t* bo = bucket_of_host(r);
+                    if (is_device_ptr(extras->round1_bucket)) c.h2d(extras->round1_bucket, bo, static_cast<size_t>(N) * sizeof(int32_t));
+                    else std::memcpy(extras->round1_bucket, bo, static_cast<size_t>(N) * sizeof(int32_t));
                 }
                 if (want_cknn) {
                     if (is_device_ptr(extras->centroid_knn)) c.h2d(extras->centroid_knn, cknn.data(), cknn.size() * sizeof(int32_t));
@@ -3263,9 +3326,9 @@ int gt_build_graph_ex(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtyp
             }
             if (r + 1 == p.rounds && extras && (extras->last_bucket || extras->last_centroids)) {
                 if (extras->last_bucket) {
-                    const std::vector<int32_t>& bo = c.c->h_bucket_of;
-                    if (is_device_ptr(extras->last_bucket)) c.h2d(extras->last_bucket, bo.data(), bo.size() * sizeof(int32_t));
-                    else std::memcpy(extras->last_bucket, bo.data(), bo.size() * sizeof(int32_t));
+                    const int32_t* bo = bucket_of_host(r);
+                    if (is_device_ptr(extras->last_bucket)) c.h2d(extras->last_bucket, bo, static_cast<size_t>(N) * sizeof(int32_t));
+                    else std::memcpy(extras->last_bucket, bo, static_cast<size_t>(N) * sizeof(int32_t));
                 }
                 if (extras->last_centroids) {
                     const std::vector<int32_t>& cid = plans[r & 1].cid;

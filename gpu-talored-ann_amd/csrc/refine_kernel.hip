@@ -10,6 +10,8 @@
 // pass's table (no in-place updates), so the result is deterministic.
 #include "gtann_common.hpp"
 
+#include <algorithm>
+
 #include <climits>
 #include <cmath>
 
@@ -281,24 +283,25 @@ __global__ void __launch_bounds__(256) centroid_means_kernel(const float* __rest
     }
 }
 
-// Lloyd CSR on the device: the sampled rows grouped by nearest centroid and,
-// within a centroid, in sample order (a stable counting sort -- the order
-// of the host's counting sort).  Each one-wave block owns kCsrChunk
-// consecutive sample entries: (1) it counts them per centroid in LDS into
-// hist[centroid][block]; (2) an exclusive scan of hist gives every
-// (centroid, block) pair its output range; (3) it scatters them 64 at a
-// time in sample order, a lane's rank among the lanes of the same centroid
-// found by ballots over the wave's distinct keys.
+// Stable counting sort on the device (the Lloyd steps' CSR: the sampled
+// rows grouped by nearest centroid and, within a centroid, in sample order;
+// the bucketing's CSR: two passes, by second key then by bucket) -- the
+// order of the host's counting sort.  Each one-wave block owns `chunk`
+// consecutive entries: (1) it counts them per key in LDS into
+// hist[key][block]; (2) an exclusive scan of hist gives every (key, block)
+// pair its output range; (3) it scatters them 64 at a time in input order,
+// a lane's rank among the lanes of the same key found by ballots over the
+// wave's distinct keys.  out[...] = val[e], or e itself when val is null.
 constexpr int kCsrChunk = 256;
 
 __global__ void __launch_bounds__(64) csr_count_kernel(const int32_t* __restrict__ key, int64_t S, int C,
-                                                       uint32_t* __restrict__ hist)
+                                                       int64_t chunk, uint32_t* __restrict__ hist)
 {
     extern __shared__ uint32_t h[];   // C counters
     const int lane = threadIdx.x;
     for (int i = lane; i < C; i += 64) h[i] = 0u;
     __syncthreads();
-    const int64_t e0 = static_cast<int64_t>(blockIdx.x) * kCsrChunk, e1 = min(S, e0 + kCsrChunk);
+    const int64_t e0 = static_cast<int64_t>(blockIdx.x) * chunk, e1 = min(S, e0 + chunk);
     for (int64_t e = e0 + lane; e < e1; e += 64) {
         const int32_t k = key[e];
         if (k >= 0 && k < C) atomicAdd(&h[k], 1u);
@@ -309,14 +312,15 @@ __global__ void __launch_bounds__(64) csr_count_kernel(const int32_t* __restrict
 
 __global__ void __launch_bounds__(64) csr_scatter_kernel(const int32_t* __restrict__ key,
                                                          const int32_t* __restrict__ val, int64_t S, int C,
-                                                         const uint32_t* __restrict__ offs, int32_t* __restrict__ out)
+                                                         int64_t chunk, const uint32_t* __restrict__ offs,
+                                                         int32_t* __restrict__ out)
 {
     extern __shared__ uint32_t cur[];   // C cursors
     const int lane = threadIdx.x;
     for (int i = lane; i < C; i += 64) cur[i] = offs[static_cast<int64_t>(i) * gridDim.x + blockIdx.x];
     __syncthreads();
     const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
-    const int64_t e0 = static_cast<int64_t>(blockIdx.x) * kCsrChunk, e1 = min(S, e0 + kCsrChunk);
+    const int64_t e0 = static_cast<int64_t>(blockIdx.x) * chunk, e1 = min(S, e0 + chunk);
     for (int64_t base = e0; base < e1; base += 64) {
         const int64_t e = base + lane;
         const int32_t k = e < e1 ? key[e] : -1;
@@ -330,7 +334,7 @@ __global__ void __launch_bounds__(64) csr_scatter_kernel(const int32_t* __restri
             if (valid && k == kl) peers = m;
             todo &= ~m;
         }
-        if (valid) out[cur[k] + __popcll(peers & below)] = val[e];
+        if (valid) out[cur[k] + __popcll(peers & below)] = val ? val[e] : static_cast<int32_t>(e);
         __syncthreads();
         if (valid && (peers >> lane) == 1ull) cur[k] += static_cast<uint32_t>(__popcll(peers));
         __syncthreads();
@@ -359,19 +363,72 @@ void launch_refine_2hop(const float* X, const float* norms, int64_t N, int Dp, i
     GT_HIP(hipGetLastError());
 }
 
-int csr_blocks(int64_t S) { return static_cast<int>((S + kCsrChunk - 1) / kCsrChunk); }
+// entries per block of the stable counting sort: kCsrChunk, more for large
+// inputs so that the (key, block) histogram stays near 4,096 blocks
+int64_t csr_chunk(int64_t S) { return std::max<int64_t>(kCsrChunk, (S + 4095) / 4096 + 63) / 64 * 64; }
+int csr_blocks(int64_t S) { return static_cast<int>((S + csr_chunk(S) - 1) / csr_chunk(S)); }
 
 void launch_sample_csr(const int32_t* key, const int32_t* val, int64_t S, int C, uint32_t* hist, uint32_t* offs,
                        uint32_t* sums, int32_t* members, int64_t* off, hipStream_t s)
 {
     GT_REQUIRE(C >= 1 && C <= 16384, "device CSR: at most 16384 keys");
+    const int64_t chunk = csr_chunk(S);
     const int nblk = csr_blocks(S);
     const size_t lds = static_cast<size_t>(C) * sizeof(uint32_t);
-    if (S > 0) hipLaunchKernelGGL(csr_count_kernel, dim3(nblk), dim3(64), lds, s, key, S, C, hist);
+    if (S > 0) hipLaunchKernelGGL(csr_count_kernel, dim3(nblk), dim3(64), lds, s, key, S, C, chunk, hist);
     launch_exclusive_scan(hist, static_cast<int64_t>(C) * nblk, offs, sums, s);
-    if (S > 0) hipLaunchKernelGGL(csr_scatter_kernel, dim3(nblk), dim3(64), lds, s, key, val, S, C, offs, members);
-    hipLaunchKernelGGL(csr_offsets_kernel, dim3((C + 256) / 256), dim3(256), 0, s, offs, C, nblk, off);
+    if (S > 0)
+        hipLaunchKernelGGL(csr_scatter_kernel, dim3(nblk), dim3(64), lds, s, key, val, S, C, chunk, offs, members);
+    if (off) hipLaunchKernelGGL(csr_offsets_kernel, dim3((C + 256) / 256), dim3(256), 0, s, offs, C, nblk, off);
     GT_HIP(hipGetLastError());
+}
+
+// The bucketing's second key: each point's other top-2 centroid (its own
+// bucket when that is missing), key2[i] for the stable sort by (bucket,
+// key2, id)
+__global__ void bucket_key2_kernel(const uint32_t* __restrict__ top2, const int32_t* __restrict__ bucket, int64_t N,
+                                   int64_t C, int32_t* __restrict__ key2)
+{
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= N) return;
+    const uint32_t c1 = top2[2 * i], c2 = top2[2 * i + 1];
+    const int32_t b = bucket[i];
+    const uint32_t other = static_cast<int64_t>(c1) == b ? c2 : c1;
+    key2[i] = other < static_cast<uint64_t>(C) ? static_cast<int32_t>(other) : b;
+}
+
+// out[i] = src[idx[i]]
+__global__ void gather_i32_kernel(const int32_t* __restrict__ src, const int32_t* __restrict__ idx, int64_t n,
+                                  int32_t* __restrict__ out)
+{
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = src[idx[i]];
+}
+
+void launch_gather_i32(const int32_t* src, const int32_t* idx, int64_t n, int32_t* out, hipStream_t s)
+{
+    if (n <= 0) return;
+    hipLaunchKernelGGL(gather_i32_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, src, idx, n,
+                       out);
+    GT_HIP(hipGetLastError());
+}
+
+// Members of every bucket ordered by (bucket, key2, id) -- the host CSR's
+// order -- from the device top-2 lists and the two-choice buckets: key2, a
+// stable sort of the ids by key2, their buckets gathered, a stable sort by
+// bucket.  members (N) and off (C + 1) out; key2, by_key and bkt (N each)
+// and hist / offs / sums (csr_blocks(N) * C, + 1, / 1024 + 2) are scratch.
+void launch_bucket_csr(const uint32_t* top2, const int32_t* bucket, int64_t N, int C, int32_t* key2, int32_t* by_key,
+                       int32_t* bkt, uint32_t* hist, uint32_t* offs, uint32_t* sums, int32_t* members, int64_t* off,
+                       hipStream_t s)
+{
+    if (N <= 0) return;
+    hipLaunchKernelGGL(bucket_key2_kernel, dim3(static_cast<unsigned>((N + 255) / 256)), dim3(256), 0, s, top2, bucket,
+                       N, static_cast<int64_t>(C), key2);
+    GT_HIP(hipGetLastError());
+    launch_sample_csr(key2, nullptr, N, C, hist, offs, sums, by_key, nullptr, s);
+    launch_gather_i32(bucket, by_key, N, bkt, s);
+    launch_sample_csr(bkt, by_key, N, C, hist, offs, sums, members, off, s);
 }
 
 void launch_centroid_sums(const float* X, int Dp, const int32_t* members, const int64_t* offsets, int64_t C,

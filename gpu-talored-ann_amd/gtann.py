@@ -53,7 +53,7 @@ class DebugOpts(C.Structure):
     _fields_ = [
         ("knn_collect", C.c_int32), ("revmerge_path", C.c_int32), ("sub_order", C.c_int32),
         ("lloyd_host_csr", C.c_int32), ("prune_flat_rows", C.c_int32), ("knn_stats", C.c_int32),
-        ("knn_prune", C.c_int32), ("reserved_", C.c_int32),
+        ("knn_prune", C.c_int32), ("bucket_host_csr", C.c_int32),
     ]
 
 
@@ -289,13 +289,14 @@ class Context:
         """Path selection (gt_set_debug): every choice gives the same results.
         Keywords: knn_collect (bool), revmerge_path ('auto'|'rv'|'binned'|'csr'),
         sub_order (bool), lloyd_host_csr (bool), prune_flat_rows (bool),
-        knn_stats (bool).  No keywords: the defaults."""
+        knn_stats (bool), knn_prune (bool), bucket_host_csr (bool).  No
+        keywords: the defaults."""
         o = DebugOpts()
         lib().gt_debug_opts_default(C.byref(o))
         for k, v in opts.items():
             if k == "revmerge_path":
                 v = REVMERGE_PATHS[v] if isinstance(v, str) else int(v)
-            elif k not in {f for f, _ in DebugOpts._fields_} or k == "reserved_":
+            elif k not in {f for f, _ in DebugOpts._fields_}:
                 raise ValueError(f"unknown debug option {k!r}")
             setattr(o, k, int(v))
         self._check(lib().gt_set_debug(self._h, C.byref(o)), "gt_set_debug")

@@ -367,7 +367,8 @@ typedef struct gt_debug_opts {
     int32_t knn_stats;       /* 1 with GTANN_TRACE set: per-launch counters of the collect kernel */
     int32_t knn_prune;       /* 1 (default): the int8 collect kernel skips pool chunks whose bounding
                                 sphere is farther from every query than its threshold (exact); 0: scans all */
-    int32_t reserved_;
+    int32_t bucket_host_csr; /* 0 (default): the bucket members are ordered on the device (the host
+                                runs only the two-choice rule); 1: on the host (same order) */
 } gt_debug_opts;
 
 void gt_debug_opts_default(gt_debug_opts* o);

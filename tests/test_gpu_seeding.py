@@ -89,3 +89,22 @@ def test_kmeans_par_seeds_lloyd(ctx):
     rec = [np.mean([len(np.intersect1d(r.knn_ids[i], ex[k])) / 32 for k, i in enumerate(q)]) for r in (a, b)]
     print(f"recall@32 kmeans|| + Lloyd {rec[0]:.4f}, uniform + Lloyd {rec[1]:.4f}", flush=True)
     assert rec[0] >= rec[1] - 0.02
+
+
+@pytest.mark.parametrize("rounds,iters,seeding", [(2, 3, "auto"), (3, 0, "auto"), (2, 0, "uniform")])
+def test_device_bucket_csr_matches_host(ctx, rounds, iters, seeding):
+    # the members ordered by (bucket, other top-2 centroid, id) on the device
+    # and on the host: the same buckets, table and graph bit for bit
+    from helpers import debug_opts
+    X, _ = synth.generate("C2", n=40000)
+    kw = dict(n_buckets=24, nprobe=1, M=32, K=16, rounds=rounds, kmeans_iters=iters, seeding=seeding,
+              last_round=True, round1_bucket=True)
+    print(f"device vs host bucket CSR rounds={rounds} iters={iters} {seeding}", flush=True)
+    a = ctx.build_graph(X, **kw)
+    with debug_opts(ctx, bucket_host_csr=True):
+        b = ctx.build_graph(X, **kw)
+    np.testing.assert_array_equal(a.round1_bucket, b.round1_bucket)
+    np.testing.assert_array_equal(a.last_bucket, b.last_bucket)
+    np.testing.assert_array_equal(a.knn_ids, b.knn_ids)
+    np.testing.assert_array_equal(a.knn_dists.view(np.uint32), b.knn_dists.view(np.uint32))
+    np.testing.assert_array_equal(a.graph, b.graph)
