@@ -115,6 +115,7 @@ int csr_blocks(int64_t S);
 void launch_sample_csr(const int32_t* key, const int32_t* val, int64_t S, int C, uint32_t* hist, uint32_t* offs,
                        uint32_t* sums, int32_t* members, int64_t* off, hipStream_t s);
 void launch_gather_i32(const int32_t* src, const int32_t* idx, int64_t n, int32_t* out, hipStream_t s);
+void launch_pack_u16(const uint32_t* in, int64_t n, uint16_t* out, hipStream_t s);
 void launch_bucket_csr(const uint32_t* top2, const int32_t* bucket, int64_t N, int C, int32_t* key2, int32_t* by_key,
                        int32_t* bkt, uint32_t* hist, uint32_t* offs, uint32_t* sums, int32_t* members, int64_t* off,
                        hipStream_t s);
@@ -260,7 +261,7 @@ enum Ws {
     W_OOC_A, W_OOC_B, W_OOC_C, W_OOC_D, W_OOC_E, W_OOC_F, W_OOC_G, W_CR, W_CRNORMS,
     W_KM_TRAIN, W_KM_MIND, W_KM_FLAG, W_KM_SEL, W_KM_POS, W_KM_SUMS, W_KM_NEW, W_KM_PSI, W_KM_P, W_KM_PN, W_KM_P8,
     W_KM_PN8, W_KM_OI, W_KM_OD, W_CH8, W_CHN, W_CHR, W_CHCNT, W_PAIRS, W_TOP2A, W_TOP2B, W_BUCKETD, W_KEY2,
-    W_BYKEY, W_BKTD, W_BOFF, W_SUBPOS, W_COUNT_
+    W_BYKEY, W_BKTD, W_BOFF, W_SUBPOS, W_TOP2H, W_COUNT_
 };
 static_assert(W_COUNT_ <= 96, "workspace slots");
 
@@ -697,7 +698,8 @@ static uint64_t next_bucket_gen()
 // nearest centroid if that bucket is smaller than balance x the nearest
 // one's, sizes counted in point order.  Centroids that are data points sit
 // in their own bucket from the start.
-static void assign_two_choice(const uint32_t* top2, int64_t N, int64_t C, float balance,
+template <typename T>
+static void assign_two_choice(const T* top2, int64_t N, int64_t C, float balance,
                               const std::vector<int32_t>* centroid_ids, int32_t* bucket_of)
 {
     std::fill(bucket_of, bucket_of + N, -1);
@@ -1200,7 +1202,8 @@ struct BucketPlan {
     int64_t N = 0, C = 0;
     std::vector<int32_t> cid;       // sampled centroid row ids, ascending
     bool data_points = true;        // centroids are data points (no Lloyd)
-    const uint32_t* top2 = nullptr; // pinned, 2N: nearest and 2nd nearest centroid
+    const uint32_t* top2 = nullptr; // pinned, 2N: nearest and 2nd nearest centroid (C >= 65535)
+    const uint16_t* top2h = nullptr;    // the same as 16-bit ids (C < 65535; a missing one is 0xFFFF)
     const uint32_t* d_top2 = nullptr;   // the same on the device (the round's own buffer), or null
     std::vector<int32_t> probe;     // C x P
     int P = 0;
@@ -1455,39 +1458,7 @@ static void bucket_device(Ctx& c, const DevMatrix& X, int64_t C, int nprobe, int
         }
     }
 
-    // exact top-2 centroids of every point
     bp.data_points = data_points;
-    uint32_t* top2 = pin.as<uint32_t>(static_cast<size_t>(2 * N));
-    bp.top2 = top2;
-    bp.d_top2 = nullptr;
-    if (C >= 2) {
-        // (each round parity its own buffer: the device CSR of a round reads
-        // it after the next round's centroids are computed)
-        int32_t* d_t2 = c.ws<int32_t>(parity ? W_TOP2B : W_TOP2A, static_cast<size_t>(2 * N));
-        bp.d_top2 = reinterpret_cast<const uint32_t*>(d_t2);
-        float* d_t2d = c.ws<float>(W_D3, static_cast<size_t>(2 * N));
-        KnnJob j;
-        j.Q = &X;
-        j.P = &Cm;
-        j.nq = N;
-        j.np = C;
-        j.M = 2;
-        j.metric = metric;
-        j.exclude_self = false;
-        j.out_pos = true;
-        j.out_ids = d_t2;
-        j.out_d = d_t2d;
-        run_knn_flat(c, j, 1);
-        tr.mark(c.s, "bucketing: top-2 kNN");
-        c.d2h(top2, d_t2, static_cast<size_t>(2 * N) * sizeof(uint32_t));
-        c.sync();
-        tr.mark(c.s, "bucketing: top-2 download");
-    } else {
-        for (int64_t i = 0; i < N; ++i) {
-            top2[2 * i] = 0u;
-            top2[2 * i + 1] = 0xffffffffu;
-        }
-    }
 
     // probe table: nprobe nearest other centroids
     bp.P = static_cast<int>(std::min<int64_t>(nprobe, C - 1));
@@ -1558,6 +1529,55 @@ static void bucket_device(Ctx& c, const DevMatrix& X, int64_t C, int nprobe, int
         c.d2h(cknn->data(), d_ki, cknn->size() * sizeof(int32_t));
         c.sync();
     }
+    // exact top-2 centroids of every point, last: the host half starts as
+    // soon as they are down (16-bit ids when the centroids allow)
+    uint32_t* top2 = nullptr;
+    bp.top2 = nullptr;
+    bp.top2h = nullptr;
+    bp.d_top2 = nullptr;
+    const bool h16 = C < 65535;
+    if (h16) bp.top2h = pin.as<uint16_t>(static_cast<size_t>(2 * N));
+    else bp.top2 = top2 = pin.as<uint32_t>(static_cast<size_t>(2 * N));
+    if (C >= 2) {
+        // (each round parity its own buffer: the device CSR of a round reads
+        // it after the next round's centroids are computed)
+        int32_t* d_t2 = c.ws<int32_t>(parity ? W_TOP2B : W_TOP2A, static_cast<size_t>(2 * N));
+        bp.d_top2 = reinterpret_cast<const uint32_t*>(d_t2);
+        float* d_t2d = c.ws<float>(W_D3, static_cast<size_t>(2 * N));
+        KnnJob j;
+        j.Q = &X;
+        j.P = &Cm;
+        j.nq = N;
+        j.np = C;
+        j.M = 2;
+        j.metric = metric;
+        j.exclude_self = false;
+        j.out_pos = true;
+        j.out_ids = d_t2;
+        j.out_d = d_t2d;
+        run_knn_flat(c, j, 1);
+        tr.mark(c.s, "bucketing: top-2 kNN");
+        if (h16) {
+            uint16_t* d_h = c.ws<uint16_t>(W_TOP2H, static_cast<size_t>(2 * N));
+            launch_pack_u16(reinterpret_cast<const uint32_t*>(d_t2), 2 * N, d_h, c.s);
+            c.d2h(const_cast<uint16_t*>(bp.top2h), d_h, static_cast<size_t>(2 * N) * sizeof(uint16_t));
+        } else {
+            c.d2h(top2, d_t2, static_cast<size_t>(2 * N) * sizeof(uint32_t));
+        }
+        c.sync();
+        tr.mark(c.s, "bucketing: top-2 download");
+    } else {
+        uint16_t* th = const_cast<uint16_t*>(bp.top2h);
+        for (int64_t i = 0; i < N; ++i) {
+            if (h16) {
+                th[2 * i] = 0;
+                th[2 * i + 1] = 0xFFFF;
+            } else {
+                top2[2 * i] = 0u;
+                top2[2 * i + 1] = 0xffffffffu;
+            }
+        }
+    }
 }
 
 // The host half: two-choice rule over the downloaded top-2 lists into
@@ -1568,9 +1588,9 @@ static void bucket_host(const BucketPlan& bp, float balance, Buckets& b, int32_t
                         std::vector<int32_t>& key2, std::vector<int32_t>& by_key, std::vector<int32_t>& bkt)
 {
     const int64_t N = bp.N, C = bp.C;
-    const uint32_t* top2 = bp.top2;
     Trace tr;
-    assign_two_choice(top2, N, C, balance, bp.data_points ? &bp.cid : nullptr, bucket_of);
+    if (bp.top2h) assign_two_choice(bp.top2h, N, C, balance, bp.data_points ? &bp.cid : nullptr, bucket_of);
+    else assign_two_choice(bp.top2, N, C, balance, bp.data_points ? &bp.cid : nullptr, bucket_of);
     const double t_tc = tr.t.sec();
     b.P = bp.P;
     b.probe = bp.probe;
@@ -1583,7 +1603,8 @@ static void bucket_host(const BucketPlan& bp, float balance, Buckets& b, int32_t
     key2.resize(static_cast<size_t>(N));
     parallel_slices(N, host_threads(), [&](int, int64_t lo, int64_t hi) {
         for (int64_t i = lo; i < hi; ++i) {
-            const uint32_t c1 = top2[static_cast<size_t>(2 * i)], c2 = top2[static_cast<size_t>(2 * i + 1)];
+            const size_t e = static_cast<size_t>(2 * i);
+            const uint32_t c1 = bp.top2h ? bp.top2h[e] : bp.top2[e], c2 = bp.top2h ? bp.top2h[e + 1] : bp.top2[e + 1];
             const uint32_t other = static_cast<int64_t>(c1) == bucket_of[static_cast<size_t>(i)] ? c2 : c1;
             key2[static_cast<size_t>(i)] = other < static_cast<uint64_t>(C) ? static_cast<int32_t>(other)
                                                                               : bucket_of[static_cast<size_t>(i)];

@@ -397,6 +397,21 @@ __global__ void bucket_key2_kernel(const uint32_t* __restrict__ top2, const int3
     key2[i] = other < static_cast<uint64_t>(C) ? static_cast<int32_t>(other) : b;
 }
 
+// out[i] = min(in[i], 0xFFFF): top-2 centroid lists of fewer than 65,535
+// centroids for the host (a missing second centroid stays out of range)
+__global__ void pack_u16_kernel(const uint32_t* __restrict__ in, int64_t n, uint16_t* __restrict__ out)
+{
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = static_cast<uint16_t>(min(in[i], 0xFFFFu));
+}
+
+void launch_pack_u16(const uint32_t* in, int64_t n, uint16_t* out, hipStream_t s)
+{
+    if (n <= 0) return;
+    hipLaunchKernelGGL(pack_u16_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, in, n, out);
+    GT_HIP(hipGetLastError());
+}
+
 // out[i] = src[idx[i]]
 __global__ void gather_i32_kernel(const int32_t* __restrict__ src, const int32_t* __restrict__ idx, int64_t n,
                                   int32_t* __restrict__ out)
