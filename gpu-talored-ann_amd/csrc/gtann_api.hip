@@ -79,9 +79,10 @@ int rev_bin_blocks(int64_t E);
 void launch_rev_binned(const uint32_t* fwd, int64_t N, int K, uint32_t* hist, uint32_t* offs, uint32_t* sums,
                        unsigned long long* part, unsigned long long* grouped, uint32_t* out, int* err, hipStream_t s);
 bool rv_plan(int64_t N, int K, RvPlan& p);
-void launch_rv(const uint32_t* fwd, int64_t N, int K, const RvPlan& p, uint32_t* part, uint16_t* meta_blk,
-               uint16_t* meta, uint32_t* out, int* err, uint32_t* slow_rows, uint32_t* slow_count, uint32_t* big_bins,
-               hipStream_t s);
+bool rv_plan2(int64_t N, int K, RvPlan& p);
+RvSizes rv_sizes(int64_t N, int K, const RvPlan& p);
+void launch_rv(const uint32_t* fwd, int64_t N, int K, const RvPlan& p, const RvBufs& bf, uint32_t* out, int* err,
+               uint32_t* slow_rows, uint32_t* slow_count, uint32_t* big_bins, hipStream_t s);
 void launch_rev_merge(const uint32_t* fwd, int64_t N, int K, const uint32_t* off, const unsigned long long* keys,
                       uint32_t* out, hipStream_t s);
 void launch_occlusion_prune(const float* X, int64_t N, int Dp, const int32_t* nb, int M, int max_deg, int32_t* out,
@@ -261,7 +262,7 @@ enum Ws {
     W_OOC_A, W_OOC_B, W_OOC_C, W_OOC_D, W_OOC_E, W_OOC_F, W_OOC_G, W_CR, W_CRNORMS,
     W_KM_TRAIN, W_KM_MIND, W_KM_FLAG, W_KM_SEL, W_KM_POS, W_KM_SUMS, W_KM_NEW, W_KM_PSI, W_KM_P, W_KM_PN, W_KM_P8,
     W_KM_PN8, W_KM_OI, W_KM_OD, W_CH8, W_CHN, W_CHR, W_CHCNT, W_PAIRS, W_TOP2A, W_TOP2B, W_BUCKETD, W_KEY2,
-    W_BYKEY, W_BKTD, W_BOFF, W_SUBPOS, W_TOP2H, W_COUNT_
+    W_BYKEY, W_BKTD, W_BOFF, W_SUBPOS, W_TOP2H, W_RV1, W_RV1M, W_COUNT_
 };
 static_assert(W_COUNT_ <= 96, "workspace slots");
 
@@ -1661,39 +1662,44 @@ static void prune_device(Ctx& c, const int32_t* G, int64_t N, int M, int K, uint
     prune_check(c, f);
 }
 
-static void reverse_merge_check(Ctx& c, const StageFlags& f)
-{
-    int h = 0;
-    c.d2h(&h, f.err, sizeof(int));
-    c.sync();
-    if (h) throw Error(GT_EINVAL, "reverse merge: forward graph holds an id >= N");
-}
-
-static void reverse_merge_enqueue(Ctx& c, const StageFlags& f, const uint32_t* fwd, int64_t N, int K, uint32_t* out)
+static void reverse_merge_enqueue(Ctx& c, const StageFlags& f, const uint32_t* fwd, int64_t N, int K, uint32_t* out,
+                                  int forced = -1)
 {
     GT_REQUIRE(K >= 1 && K <= 64, "output degree must be in [1, 64]");
     GT_REQUIRE(N * K < (int64_t(1) << 32), "too many edges for 32-bit offsets");
     int* err = f.err;
     launch_init_flags(f.bad, f.err, c.s);
-    // Three paths give the same rows: the two-kernel merge over block-local
-    // key regions (256-row bins, output degree <= 32: graphs up to 2^21
-    // rows; where it is faster), the binned merge through global grouping
-    // (up to 2^26 rows), the global-atomic CSR merge beyond.
-    // The context's revmerge_path selects one (tests; the two-kernel merge
-    // wherever it applies).
-    const int forced = c.c->dbg.revmerge_path;
+    // Four paths give the same rows: the two-kernel merge over block-local
+    // key regions (2^8-row bins, output degree <= 48: graphs up to 2^21
+    // rows), the same merge behind a level of superbins (larger graphs), the
+    // binned merge through global grouping (up to 2^26 rows; degrees above
+    // 48), the global-atomic CSR merge beyond.  The context's revmerge_path
+    // forces one (tests).
+    if (forced < 0) forced = c.c->dbg.revmerge_path;
     RvPlan rp{};
     const int shift = forced == 3 ? -1 : rev_bin_shift(N);
-    const bool rv_ok = rv_plan(N, K, rp);
-    const bool use_rv = forced == 1 ? rv_ok : forced == 0 && rv_ok && rp.cshift == 8 && K <= 32;
+    bool use_rv = false;
+    if (forced == 1) {
+        use_rv = rv_plan(N, K, rp);
+    } else if (forced == 4) {
+        use_rv = rv_plan2(N, K, rp);
+    } else if (forced == 0 && K <= 48) {
+        use_rv = rv_plan(N, K, rp) && rp.cshift == 8;
+        if (!use_rv) use_rv = rv_plan2(N, K, rp);
+    }
     if (use_rv) {
-        const size_t nm = static_cast<size_t>(rp.nbins + 1) * rp.nblk;   // 16-bit run offsets
-        uint32_t* part = c.ws<uint32_t>(W_KEYS, static_cast<size_t>(N) * K);
-        uint16_t* meta_blk = reinterpret_cast<uint16_t*>(c.ws<uint32_t>(W_DEG, (nm + 1) / 2));
-        uint16_t* meta = reinterpret_cast<uint16_t*>(c.ws<uint32_t>(W_OFF, (nm + 1) / 2));
+        const RvSizes z = rv_sizes(N, K, rp);
+        RvBufs bf;
+        bf.part = c.ws<uint32_t>(W_KEYS, z.part);
+        bf.meta_blk = reinterpret_cast<uint16_t*>(c.ws<uint32_t>(W_DEG, (z.meta + 1) / 2));
+        bf.meta = reinterpret_cast<uint16_t*>(c.ws<uint32_t>(W_OFF, (z.meta + 1) / 2));
+        if (rp.two) {
+            bf.part1 = c.ws<uint32_t>(W_RV1, z.part1);
+            bf.meta1 = reinterpret_cast<uint16_t*>(c.ws<uint32_t>(W_RV1M, (z.meta1 + 1) / 2));
+        }
         uint32_t* slow = c.ws<uint32_t>(W_CUR, static_cast<size_t>(N) + 1);   // [0]: count, then rows
         uint32_t* big = c.ws<uint32_t>(W_SUMS, static_cast<size_t>(rp.nbins) + 1);   // [0]: count, then bins
-        launch_rv(fwd, N, K, rp, part, meta_blk, meta, out, err, slow + 1, slow, big, c.s);
+        launch_rv(fwd, N, K, rp, bf, out, err, slow + 1, slow, big, c.s);
     } else if (shift >= 0) {
         // binned path: LDS histograms and cursors, no global atomics
         const int64_t nh = ceil_div(N, int64_t(1) << shift) * rev_bin_blocks(N * K);
@@ -1717,11 +1723,30 @@ static void reverse_merge_enqueue(Ctx& c, const StageFlags& f, const uint32_t* f
     }
 }
 
+// Reads the merge's error word after reverse_merge_enqueue: 1 = an id >= N;
+// 2 = a level-two block of the two-level merge held more keys than it takes
+// (destinations concentrated in one superbin), whose rows are then redone by
+// the binned merge.  Returns the seconds of that redo.
+static double reverse_merge_check(Ctx& c, const StageFlags& f, const uint32_t* fwd, int64_t N, int K, uint32_t* out)
+{
+    int h = 0;
+    c.d2h(&h, f.err, sizeof(int));
+    c.sync();
+    double t = 0.0;
+    if (h == 2) {
+        t = c.timed([&] { reverse_merge_enqueue(c, f, fwd, N, K, out, 2); });
+        c.d2h(&h, f.err, sizeof(int));
+        c.sync();
+    }
+    if (h) throw Error(GT_EINVAL, "reverse merge: forward graph holds an id >= N");
+    return t;
+}
+
 static void reverse_merge_device(Ctx& c, const uint32_t* fwd, int64_t N, int K, uint32_t* out)
 {
     const StageFlags f = stage_flags(c);
     reverse_merge_enqueue(c, f, fwd, N, K, out);
-    reverse_merge_check(c, f);
+    reverse_merge_check(c, f, fwd, N, K, out);
 }
 
 // bd/build_bucket.py:473-543 on a device table (N x M, ascending rows), in place
@@ -2388,8 +2413,8 @@ int gt_set_debug(gt_ctx* ctx, const gt_debug_opts* o)
     gt_debug_opts d;
     gt_debug_opts_default(&d);
     if (o) d = *o;
-    if (d.revmerge_path < 0 || d.revmerge_path > 3) {
-        ctx->err = "gt_set_debug: revmerge_path must be 0..3";
+    if (d.revmerge_path < 0 || d.revmerge_path > 4) {
+        ctx->err = "gt_set_debug: revmerge_path must be 0..4";
         return GT_EINVAL;
     }
     ctx->dbg = d;
@@ -3462,7 +3487,7 @@ int gt_build_graph_ex(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtyp
             });
             prune_check(c, fl);
             st.t_revmerge = c.timed([&] { reverse_merge_enqueue(c, fl, fwd, N, p.K, fin); });
-            reverse_merge_check(c, fl);
+            st.t_revmerge += reverse_merge_check(c, fl, fwd, N, p.K, fin);
         }
         Timer td;
         if (knn_ids) c.out(knn_ids, run_i, nm);

@@ -147,12 +147,34 @@ struct PruneMap {
 struct RvPlan {
     int cshift;     // rows per destination bin = 2^cshift
     int nbins;
-    int nblk;       // scatter blocks, each owning spb consecutive source rows
+    int nblk;       // key blocks seen by the merge, each owning spb consecutive source rows
     int64_t spb;
     int kbits, sbits, nbits;   // bits of rank, source within block, source id
     int rp;         // rows per merge pass (= merge block size)
     int cap;        // keys grouped in LDS per pass
     int cap_big;    // the same for the deferred (large) bins
+    int bsh = 31;   // bins per superbin = 2^bsh (two levels; 31: one level)
+    uint32_t region = 0;   // words per key block in the merge's key array
+    // two levels: the scatter first groups by superbin (2^sshift rows, G of
+    // them) in nblk1 blocks of spb1 source rows (sbits1 bits), then regroups
+    // each superbin's runs of F consecutive level-one blocks by bin
+    bool two = false;
+    int sshift = 0, G = 0, F = 0, nblk1 = 0, sbits1 = 0;
+    int64_t spb1 = 0;
+};
+
+// Device buffers of the two-kernel reverse merge: the merge's key blocks and
+// their run offsets (block-major, then bin-major), and with two levels the
+// level-one keys and offsets.  Sizes in elements (rv_sizes).
+struct RvBufs {
+    uint32_t* part = nullptr;
+    uint16_t* meta_blk = nullptr;
+    uint16_t* meta = nullptr;
+    uint32_t* part1 = nullptr;
+    uint16_t* meta1 = nullptr;
+};
+struct RvSizes {
+    size_t part = 0, meta = 0, part1 = 0, meta1 = 0;
 };
 
 // Orders LDS traffic of one wave across its lanes (no s_barrier needed

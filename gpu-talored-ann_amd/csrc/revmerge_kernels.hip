@@ -39,6 +39,11 @@
 //     larger ones still take passes over row ranges whose keys fit the LDS,
 //     re-reading the runs; a single row beyond the capacity, or one with a
 //     repeated source, goes to rv_slow_kernel.
+// Larger graphs (beyond 2^21 rows) would give a (bin, block) run table with
+// about one key per run, so they take two levels: (1) groups by superbin
+// (2^sshift rows) instead of bin, (1b) rv_scatter2_kernel regroups each
+// superbin's runs of F consecutive blocks by bin into blocks of its own, and
+// (2) merges from those, each superbin's run table transposed on its own.
 #include "gtann_common.hpp"
 
 #include <algorithm>
@@ -52,8 +57,12 @@ constexpr int kRvEdgesPerThread = 32;     // a scatter block's edges stay in reg
 constexpr int kRvMaxBlockEdges = 32704;   // its keys plus 8,192 bin counters fill the 160 KB of LDS
 constexpr int kRvMaxBins = 8192;          // LDS counters of the scatter
 constexpr int kRvMaxBinShift = 11;        // rows per bin <= 2048
-constexpr int kRvKeysPerThread = 36;      // merge fast path: a bin's keys held in registers
-constexpr int kRvLdsPerBlock = 40960;     // merge LDS for 4 blocks per CU
+// merge fast path: a bin's keys held in registers, per thread of a block of
+// rp threads (a bin of rp rows holds K keys per thread on average; the
+// 512-thread blocks of the deferred bins hold up to 512 * 36)
+__host__ __device__ constexpr int rv_kpt(int kmax, int rp) { return kmax > 32 && rp < 512 ? 60 : 36; }
+constexpr int kRvLdsPerBlock = 40960;     // merge LDS for 4 blocks per CU (degree <= 32; twice that above,
+                                          // where the registers allow 2 blocks of 256 threads)
 constexpr int kRvGroupBits = 2;
 constexpr int kRvGroups = 1 << kRvGroupBits;   // rank groups per row in the merge's LDS grouping
 constexpr bool kRvDefer = true;           // bins beyond the fast path go to rv_big_kernel
@@ -164,14 +173,19 @@ __global__ void __launch_bounds__(kRvScatterThreads) rv_scatter_kernel(
 
 // meta (block-major, nblk rows of nbins + 1 offsets) -> metaT (bin-major,
 // nbins + 1 rows of nblk): each merge block then reads two contiguous rows
-// instead of one entry from every block's row.  64 x 64 tiles through LDS.
+// instead of one entry from every block's row.  64 x 64 tiles through LDS;
+// blockIdx.z walks the superbins of a two-level merge (one table each).
 __global__ void __launch_bounds__(256) rv_meta_transpose_kernel(const uint16_t* __restrict__ meta, int nblk, int nbins,
                                                                 uint16_t* __restrict__ metaT,
                                                                 uint32_t* __restrict__ big_bins)
 {
     __shared__ uint16_t tile[64][65];
-    if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) *big_bins = 0u;   // the merge's deferred bins
+    if (blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0 && threadIdx.x == 0)
+        *big_bins = 0u;   // the merge's deferred bins
     const int cols = nbins + 1;
+    const int64_t zoff = static_cast<int64_t>(blockIdx.z) * nblk * cols;
+    meta += zoff;
+    metaT += zoff;
     const int c0 = blockIdx.x * 64, q0 = blockIdx.y * 64;
     const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
     for (int r = ty; r < 64; r += 4) {
@@ -183,6 +197,104 @@ __global__ void __launch_bounds__(256) rv_meta_transpose_kernel(const uint16_t* 
         const int c = c0 + r, q = q0 + tx;
         if (q < nblk && c < cols) metaT[static_cast<int64_t>(c) * nblk + q] = tile[tx][r];
     }
+}
+
+// Level two of the two-level merge, for graphs whose (bin, block) run table
+// would outgrow one level: rv_scatter_kernel has grouped every block's edges
+// by superbin (2^sshift destination rows, G of them) with the key layout
+// above; block (q2, g) here concatenates superbin g's runs of level-one
+// blocks [F q2, F q2 + F) -- at most kRvMaxBlockEdges keys, 32 per thread in
+// registers -- and groups them by 2^cshift-row bin into its own region of
+// part2 (kRvMaxBlockEdges words; 16-bit run offsets, block-major, in meta2),
+// the source now counted from the first row of level-one block F q2 (sbits2
+// bits).  A block with more keys sets *err to 2 and leaves its runs empty:
+// the caller then merges by another path.
+__global__ void __launch_bounds__(kRvScatterThreads) rv_scatter2_kernel(
+    const uint32_t* __restrict__ part1, const uint16_t* __restrict__ meta1, int nblk1, int G, int64_t spb, int K,
+    int F, int sshift, int cshift, int kbits, int sbits1, int sbits2, uint32_t* __restrict__ part2,
+    uint16_t* __restrict__ meta2, int nblk2, int* __restrict__ err)
+{
+    constexpr int T = kRvScatterThreads;
+    constexpr int U = kRvEdgesPerThread;
+    extern __shared__ uint32_t lds[];
+    const int nb = 1 << (sshift - cshift);   // bins per superbin
+    uint32_t* cnt = lds;                      // nb counters, then the runs' cursors
+    uint32_t* rst = cnt + nb;                 // F + 1: run starts in the concatenation
+    uint32_t* rof = rst + F + 1;              // F: run offsets in part1
+    uint32_t* stage = rof + F;                // the block's keys in bin order
+    __shared__ uint32_t wsum[T / 64 + 1];
+    const int t = threadIdx.x;
+    const int q2 = blockIdx.x, g = blockIdx.y;
+    const int q1a = q2 * F;
+    const int nr = min(F, nblk1 - q1a);
+    const uint32_t region1 = static_cast<uint32_t>(spb * K);
+    for (int i = t; i < nb; i += T) cnt[i] = 0u;
+    for (int r = t; r < nr; r += T) {
+        const uint16_t* m = meta1 + static_cast<int64_t>(q1a + r) * (G + 1) + g;
+        const uint32_t o0 = m[0];
+        rst[r] = static_cast<uint32_t>(m[1]) - o0;
+        rof[r] = static_cast<uint32_t>(q1a + r) * region1 + o0;
+    }
+    __syncthreads();
+    const uint32_t total = block_exclusive_scan<T>(rst, nr, wsum);
+    uint16_t* mrow = meta2 + (static_cast<int64_t>(g) * nblk2 + q2) * (nb + 1);
+    if (total > static_cast<uint32_t>(kRvMaxBlockEdges)) {   // uniform: every thread leaves
+        for (int i = t; i <= nb; i += T) mrow[i] = 0;
+        if (t == 0) atomicMax(err, 2);
+        return;
+    }
+    if (t == 0) rst[nr] = total;
+    __syncthreads();
+    // thread t's keys t + u T: the run of the first by binary search, then
+    // forward (empty runs are stepped over)
+    int r = 0;
+    {
+        int hi = nr;
+        while (hi - r > 1) {
+            const int mid = (r + hi) >> 1;
+            if (rst[mid] <= static_cast<uint32_t>(t)) r = mid;
+            else hi = mid;
+        }
+    }
+    const int hs1 = kbits + sbits1, hs2 = kbits + sbits2;
+    const uint32_t rmask = (1u << cshift) - 1u, kmask = (1u << kbits) - 1u, smask1 = (1u << sbits1) - 1u;
+    const uint32_t spb32 = static_cast<uint32_t>(spb);
+    // every load issued before any key is decoded (the walk is control flow;
+    // a decode beside each load would wait for it): key = the level-one key,
+    // bin = its run, then both decoded in place
+    uint32_t key[U], bin[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const uint32_t e = t + u * T;
+        bin[u] = 0xFFFFFFFFu;
+        if (e < total) {
+            while (rst[r + 1] <= e) ++r;
+            bin[u] = static_cast<uint32_t>(r);
+            key[u] = part1[rof[r] + (e - rst[r])];
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        if (bin[u] == 0xFFFFFFFFu) continue;
+        const uint32_t k1 = key[u];
+        const uint32_t row = k1 >> hs1;   // row within the superbin
+        key[u] = ((row & rmask) << hs2) | (((k1 >> sbits1) & kmask) << sbits2) | (bin[u] * spb32 + (k1 & smask1));
+        bin[u] = row >> cshift;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+        if (bin[u] != 0xFFFFFFFFu) atomicAdd(&cnt[bin[u]], 1u);
+    __syncthreads();
+    block_exclusive_scan<T>(cnt, nb, wsum);
+    for (int i = t; i < nb; i += T) mrow[i] = static_cast<uint16_t>(cnt[i]);
+    if (t == 0) mrow[nb] = static_cast<uint16_t>(total);
+    __syncthreads();   // the offsets are read before the placement advances them
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+        if (bin[u] != 0xFFFFFFFFu) stage[atomicAdd(&cnt[bin[u]], 1u)] = key[u];
+    __syncthreads();
+    uint32_t* dst = part2 + (static_cast<int64_t>(g) * nblk2 + q2) * kRvMaxBlockEdges;
+    for (uint32_t q = t; q < total; q += T) dst[q] = stage[q];
 }
 
 // median of three unsigned words in one instruction
@@ -487,7 +599,8 @@ __device__ __forceinline__ void rv_load_row(const uint32_t* __restrict__ g, int 
 // list; every wave ends when the list is done.
 template <int KMAX>
 __global__ void __launch_bounds__(256) rv_slow_kernel(const uint32_t* __restrict__ fwd, int64_t N, int K, int nblk,
-                                                      int64_t spb, int cshift, int nbins, int kbits, int sbits,
+                                                      int64_t spb, int bsh, uint32_t region, int cshift, int nbins,
+                                                      int kbits, int sbits,
                                                       int nbits, const uint32_t* __restrict__ part,
                                                       const uint16_t* __restrict__ meta,
                                                       const uint32_t* __restrict__ slow_rows,
@@ -510,13 +623,15 @@ __global__ void __launch_bounds__(256) rv_slow_kernel(const uint32_t* __restrict
         const int64_t b = code >> 11;
         const uint32_t row = code & 2047u;
         const int64_t j = (b << cshift) + row;
+        const int64_t mr = b + (b >> bsh);   // the bin's row of meta
+        const uint32_t qb = static_cast<uint32_t>(b >> bsh) * static_cast<uint32_t>(nblk);
         // the bin's runs: starts by a wave scan
         uint32_t carry = 0;
         for (int q0 = 0; q0 < nblk; q0 += 64) {
             const int q = q0 + lane;
             const int qc = q < nblk ? q : 0;
-            const uint32_t o0 = meta[b * nblk + qc];
-            const uint32_t c = q < nblk ? static_cast<uint32_t>(meta[(b + 1) * nblk + qc]) - o0 : 0u;
+            const uint32_t o0 = meta[mr * nblk + qc];
+            const uint32_t c = q < nblk ? static_cast<uint32_t>(meta[(mr + 1) * nblk + qc]) - o0 : 0u;
             uint32_t inc = c;
 #pragma unroll
             for (int o = 1; o < 64; o <<= 1) {
@@ -525,7 +640,7 @@ __global__ void __launch_bounds__(256) rv_slow_kernel(const uint32_t* __restrict
             }
             if (q < nblk) {
                 rs[q] = carry + inc - c;
-                rb[q] = static_cast<uint32_t>(q * spb * K) + o0;
+                rb[q] = (qb + static_cast<uint32_t>(q)) * region + o0;
             }
             carry += __shfl(inc, 63);
         }
@@ -627,13 +742,14 @@ __host__ __device__ inline int rv_pre_words(int nblk, int cshift, int rp)
 // taking the general path, so that a few long blocks do not trail the launch.
 template <int KMAX, int RP, bool DEFER>
 __device__ __forceinline__ void rv_merge_bin(int b, const uint32_t* __restrict__ fwd, int64_t N, int K, int nblk,
-                                             int64_t spb, int cshift, int nbins, int kbits, int sbits, int nbits,
+                                             int64_t spb, int bsh, uint32_t region, int cshift, int nbins, int kbits,
+                                             int sbits, int nbits,
                                              const uint32_t* __restrict__ part, const uint16_t* __restrict__ meta,
                                              uint32_t* __restrict__ out, int cap, uint32_t* __restrict__ slow_rows,
                                              uint32_t* __restrict__ slow_count, uint32_t* __restrict__ big_bins,
                                              uint32_t* lds, uint32_t* wsum)
 {
-    constexpr int KPT = kRvKeysPerThread;
+    constexpr int KPT = rv_kpt(KMAX, RP);
     constexpr int G = kRvGroups;
     const int t = threadIdx.x;
     const int rows_max = 1 << cshift;
@@ -647,14 +763,15 @@ __device__ __forceinline__ void rv_merge_bin(int b, const uint32_t* __restrict__
     const int hs = kbits + sbits;
     const uint32_t smask = (1u << sbits) - 1u;
     const uint32_t kmask = (1u << kbits) - 1u;
-    const uint32_t region = static_cast<uint32_t>(spb * K);
+    // the bin's runs: block regions qb + q of part (qb = 0 with one level)
+    const uint32_t qb = static_cast<uint32_t>(b >> bsh) * static_cast<uint32_t>(nblk);
     // ranks per group: 2^gsh (G groups cover every rank below 2^kbits)
     const int gsh = kbits > kRvGroupBits ? kbits - kRvGroupBits : 0;
     // a converted key's group floor: the key with its rank's low gsh bits and its source cleared
     const uint32_t gfloor = ~((1u << (nbits + gsh)) - 1u);
 
     // run lengths (in the group buffer's space), scanned into starts
-    const uint16_t* m0 = meta + static_cast<int64_t>(b) * nblk;   // bin-major: this bin's and the next row
+    const uint16_t* m0 = meta + static_cast<int64_t>(b + (b >> bsh)) * nblk;   // bin-major: this bin's and the next row
     for (int q = t; q < nblk; q += RP) {
         const uint32_t o0 = m0[q];
         grouped[q] = static_cast<uint32_t>(m0[q + nblk]) - o0;
@@ -683,7 +800,7 @@ __device__ __forceinline__ void rv_merge_bin(int b, const uint32_t* __restrict__
 #pragma unroll
         for (int u = 0; u < KPT; ++u) {
             const uint32_t e = t + u * RP;
-            key[u] = e < T ? part[qq[u] * region + roff[qq[u]] + (e - rs[qq[u]])] : 0u;
+            key[u] = e < T ? part[(qb + qq[u]) * region + roff[qq[u]] + (e - rs[qq[u]])] : 0u;
         }
         // the run tables are dead (every key is loaded): the (row, group)
         // counters go there
@@ -762,7 +879,7 @@ __device__ __forceinline__ void rv_merge_bin(int b, const uint32_t* __restrict__
         for (int u = 0; u < GL; ++u) {
             const uint32_t e = e0 + u * RP;
             qq[u] = static_cast<uint32_t>(pos[u]);
-            kk[u] = e < T ? part[qq[u] * region + roff[pos[u]] + (e - rs32[pos[u]])] : 0u;
+            kk[u] = e < T ? part[(qb + qq[u]) * region + roff[pos[u]] + (e - rs32[pos[u]])] : 0u;
         }
     };
     for (uint32_t e0 = t; e0 < T; e0 += GL * RP) {
@@ -820,10 +937,12 @@ __device__ __forceinline__ void rv_merge_bin(int b, const uint32_t* __restrict__
 }
 
 // One block per bin, bins dealt XCD-major (workgroup ids go to the 8 XCDs
-// round robin, so each XCD takes a contiguous range of bins).
+// round robin, so each XCD takes a contiguous range of bins).  Registers
+// for 4 waves per SIMD up to degree 32 (the LDS holds 4 blocks per CU).
 template <int KMAX, int RP>
-__global__ void __launch_bounds__(RP) rv_merge_kernel(const uint32_t* __restrict__ fwd, int64_t N, int K, int nblk,
-                                                      int64_t spb, int cshift, int nbins, int kbits, int sbits,
+__global__ void __launch_bounds__(RP) __attribute__((amdgpu_waves_per_eu(KMAX > 32 ? 2 : 4))) rv_merge_kernel(const uint32_t* __restrict__ fwd, int64_t N, int K, int nblk,
+                                                      int64_t spb, int bsh, uint32_t region, int cshift, int nbins,
+                                                      int kbits, int sbits,
                                                       int nbits, const uint32_t* __restrict__ part,
                                                       const uint16_t* __restrict__ meta, uint32_t* __restrict__ out,
                                                       int cap, uint32_t* __restrict__ slow_rows,
@@ -834,16 +953,19 @@ __global__ void __launch_bounds__(RP) rv_merge_kernel(const uint32_t* __restrict
     const int per_xcd = (nbins + 7) / 8;
     const int b = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
     if (b >= nbins) return;
-    rv_merge_bin<KMAX, RP, kRvDefer>(b, fwd, N, K, nblk, spb, cshift, nbins, kbits, sbits, nbits, part, meta, out, cap,
+    rv_merge_bin<KMAX, RP, kRvDefer>(b, fwd, N, K, nblk, spb, bsh, region, cshift, nbins, kbits, sbits, nbits, part,
+                                     meta, out, cap,
                                  slow_rows, slow_count, big_bins, lds, wsum);
 }
 
 // The bins rv_merge_kernel deferred, by blocks of kRvBigThreads threads with
-// a larger group buffer (fast path up to 18,432 keys, else the general path);
+// a larger group buffer (fast path up to 512 * rv_kpt keys as the LDS allows,
+// else the general path);
 // a fixed grid walks the list, every block ends when it is done.
 template <int KMAX>
 __global__ void __launch_bounds__(kRvBigThreads) rv_big_kernel(const uint32_t* __restrict__ fwd, int64_t N, int K, int nblk,
-                                                      int64_t spb, int cshift, int nbins, int kbits, int sbits,
+                                                      int64_t spb, int bsh, uint32_t region, int cshift, int nbins,
+                                                      int kbits, int sbits,
                                                       int nbits, const uint32_t* __restrict__ part,
                                                       const uint16_t* __restrict__ meta, uint32_t* __restrict__ out,
                                                       int cap, uint32_t* __restrict__ slow_rows,
@@ -854,8 +976,9 @@ __global__ void __launch_bounds__(kRvBigThreads) rv_big_kernel(const uint32_t* _
     __shared__ uint32_t wsum[kRvBigThreads / 64 + 1];
     const uint32_t n = big_bins[0];
     for (uint32_t i = blockIdx.x; i < n; i += gridDim.x) {
-        rv_merge_bin<KMAX, kRvBigThreads, false>(static_cast<int>(big_bins[1 + i]), fwd, N, K, nblk, spb, cshift, nbins, kbits,
-                                        sbits, nbits, part, meta, out, cap, slow_rows, slow_count, nullptr, lds, wsum);
+        rv_merge_bin<KMAX, kRvBigThreads, false>(static_cast<int>(big_bins[1 + i]), fwd, N, K, nblk, spb, bsh, region,
+                                                 cshift, nbins, kbits, sbits, nbits, part, meta, out, cap, slow_rows,
+                                                 slow_count, nullptr, lds, wsum);
         __syncthreads();   // the next bin reuses the LDS
     }
 }
@@ -889,13 +1012,41 @@ size_t rv_merge_lds(const RvPlan& p, int rp)
     return words * sizeof(uint32_t);
 }
 
+// the merge instantiation (KMAX) of output degree K
+static int rv_kmax(int K) { return K <= 16 ? 16 : K <= 32 ? 32 : K <= 48 ? 48 : 64; }
+
+// The merge side of a plan (p.rp, p.cshift, p.nblk set): group buffers and
+// the LDS checks
+static bool rv_plan_merge(RvPlan& p, int K)
+{
+    // group buffer: an average bin + 1/16, more when 4 blocks per CU still fit
+    p.cap = p.rp * K * 17 / 16;
+    RvPlan q = p;
+    q.cap = 0;
+    // (less the static scan words and the LDS allocation granule)
+    const int64_t budget = K > 32 && p.rp == 256 ? 2 * kRvLdsPerBlock : kRvLdsPerBlock;
+    const int64_t room = (budget - 512 - static_cast<int64_t>(rv_merge_lds(q, p.rp))) / 4;
+    p.cap = static_cast<int>(std::max<int64_t>(p.cap, std::min<int64_t>(room, int64_t(p.rp) * rv_kpt(rv_kmax(K), p.rp))));
+    // the run lengths are scanned in the group buffer, whose head keeps them
+    // in the general path: leave room for the longest rows besides
+    p.cap = std::max(p.cap, p.nblk + 1 + 4 * p.rp);
+    // deferred bins: larger blocks, two per CU
+    const int64_t room_big = (80 * 1024 - 1024 - static_cast<int64_t>(rv_merge_lds(q, kRvBigThreads))) / 4;
+    p.cap_big = static_cast<int>(std::min<int64_t>(room_big, int64_t(kRvBigThreads) * rv_kpt(rv_kmax(K), kRvBigThreads)));
+    if (p.cap_big < p.cap) return false;
+    RvPlan b = p;
+    b.cap = p.cap_big;
+    return rv_merge_lds(p, p.rp) <= 160 * 1024 && rv_merge_lds(b, kRvBigThreads) <= 160 * 1024;
+}
+
 bool rv_plan(int64_t N, int K, RvPlan& p)
 {
     if (N < 1 || K < 1 || K > 64) return false;
     const int64_t E = N * K;
     if (E >= (int64_t(1) << 32)) return false;
-    p.rp = K > 32 ? 128 : 256;
-    p.cshift = K > 32 ? 7 : 8;
+    p = RvPlan{};
+    p.rp = K > 48 ? 128 : 256;
+    p.cshift = K > 48 ? 7 : 8;
     while (p.cshift < kRvMaxBinShift && ceil_div(N, int64_t(1) << p.cshift) > kRvMaxBins) ++p.cshift;
     p.nbins = static_cast<int>(ceil_div(N, int64_t(1) << p.cshift));
     if (p.nbins > kRvMaxBins) return false;
@@ -904,38 +1055,93 @@ bool rv_plan(int64_t N, int K, RvPlan& p)
     p.kbits = bits_for(K);
     p.sbits = bits_for(p.spb);
     p.nbits = bits_for(N);
+    p.region = static_cast<uint32_t>(p.spb * K);
     if (p.cshift + p.kbits + p.sbits > 32) return false;
     if (p.kbits + p.nbits > 31) return false;   // 0xFFFFFFFF stays free as the empty marker
-    // group buffer: an average bin + 1/16, more when 4 blocks per CU still fit
-    p.cap = p.rp * K * 17 / 16;
-    RvPlan q = p;
-    q.cap = 0;
-    // (less the static scan words and the LDS allocation granule)
-    const int64_t room = (kRvLdsPerBlock - 512 - static_cast<int64_t>(rv_merge_lds(q, p.rp))) / 4;
-    p.cap = static_cast<int>(std::max<int64_t>(p.cap, std::min<int64_t>(room, int64_t(p.rp) * kRvKeysPerThread)));
-    // the run lengths are scanned in the group buffer, whose head keeps them
-    // in the general path: leave room for the longest rows besides
-    p.cap = std::max(p.cap, p.nblk + 1 + 4 * p.rp);
-    // deferred bins: larger blocks, two per CU
-    const int64_t room_big = (80 * 1024 - 1024 - static_cast<int64_t>(rv_merge_lds(q, kRvBigThreads))) / 4;
-    p.cap_big = static_cast<int>(std::min<int64_t>(room_big, int64_t(kRvBigThreads) * kRvKeysPerThread));
-    if (p.cap_big < p.cap) return false;
-    RvPlan b = p;
-    b.cap = p.cap_big;
-    return rv_merge_lds(p, p.rp) <= 160 * 1024 && rv_merge_lds(b, kRvBigThreads) <= 160 * 1024;
+    return rv_plan_merge(p, K);
 }
 
-void launch_rv(const uint32_t* fwd, int64_t N, int K, const RvPlan& p, uint32_t* part, uint16_t* meta_blk,
-               uint16_t* meta, uint32_t* out, int* err, uint32_t* slow_rows, uint32_t* slow_count, uint32_t* big_bins,
-               hipStream_t s)
+// Two levels: superbins as large as the level-one key allows (and small
+// enough that a small graph still gets several), then F level-one blocks per
+// level-two block, sized so that a superbin's runs of F blocks fill about
+// 60 % of a block when destinations spread evenly.
+bool rv_plan2(int64_t N, int K, RvPlan& p)
 {
-    const size_t lds_s = (static_cast<size_t>(p.nbins) + kRvMaxBlockEdges) * sizeof(uint32_t);
-    ensure_lds(reinterpret_cast<const void*>(&rv_scatter_kernel), lds_s);
-    hipLaunchKernelGGL(rv_scatter_kernel, dim3(p.nblk), dim3(kRvScatterThreads), lds_s, s, fwd, N, K, p.spb, p.cshift,
-                       p.nbins, p.kbits, p.sbits, part, meta_blk, err, slow_count);
-    hipLaunchKernelGGL(rv_meta_transpose_kernel, dim3(static_cast<unsigned>(ceil_div(p.nbins + 1, 64)),
-                                                      static_cast<unsigned>(ceil_div(p.nblk, 64))),
-                       dim3(256), 0, s, meta_blk, p.nblk, p.nbins, meta, big_bins);
+    if (N < 1 || K < 1 || K > 64) return false;
+    const int64_t E = N * K;
+    if (E >= (int64_t(1) << 32)) return false;
+    p = RvPlan{};
+    p.two = true;
+    p.rp = K > 48 ? 128 : 256;
+    p.cshift = K > 48 ? 7 : 8;
+    p.kbits = bits_for(K);
+    p.nbits = bits_for(N);
+    if (p.kbits + p.nbits > 31) return false;
+    p.spb1 = std::min<int64_t>(kRvMaxBlockEdges / K, N);
+    p.nblk1 = static_cast<int>(ceil_div(N, p.spb1));
+    p.sbits1 = bits_for(p.spb1);
+    p.sshift = std::min(32 - p.kbits - p.sbits1, std::max(p.cshift + 2, p.nbits - 6));
+    if (p.sshift - p.cshift < 1 || p.sshift - p.cshift > 12) return false;
+    p.G = static_cast<int>(ceil_div(N, int64_t(1) << p.sshift));
+    if (p.G >= kRvMaxBins) return false;
+    const double per_run = static_cast<double>(p.spb1) * K * static_cast<double>(int64_t(1) << p.sshift) / N;
+    p.F = static_cast<int>(std::max(1.0, std::min(512.0, 0.6 * kRvMaxBlockEdges / per_run)));
+    while (p.F > 1 && p.cshift + p.kbits + bits_for(p.F * p.spb1) > 32) --p.F;
+    p.spb = p.F * p.spb1;
+    p.sbits = bits_for(p.spb);
+    if (p.cshift + p.kbits + p.sbits > 32) return false;
+    p.nblk = static_cast<int>(ceil_div(p.nblk1, p.F));
+    p.bsh = p.sshift - p.cshift;
+    p.nbins = static_cast<int>(ceil_div(N, int64_t(1) << p.cshift));
+    p.region = kRvMaxBlockEdges;
+    if (static_cast<int64_t>(p.G) * p.nblk * kRvMaxBlockEdges >= (int64_t(1) << 32)) return false;
+    return rv_plan_merge(p, K);
+}
+
+RvSizes rv_sizes(int64_t N, int K, const RvPlan& p)
+{
+    RvSizes z{};
+    if (p.two) {
+        const int64_t nb = int64_t(1) << p.bsh;
+        z.part = static_cast<size_t>(p.G) * p.nblk * kRvMaxBlockEdges;
+        z.meta = static_cast<size_t>(p.G) * p.nblk * (nb + 1);
+        z.part1 = static_cast<size_t>(N) * K;
+        z.meta1 = static_cast<size_t>(p.nblk1) * (p.G + 1);
+    } else {
+        z.part = static_cast<size_t>(N) * K;
+        z.meta = static_cast<size_t>(p.nbins + 1) * p.nblk;
+    }
+    return z;
+}
+
+void launch_rv(const uint32_t* fwd, int64_t N, int K, const RvPlan& p, const RvBufs& bf, uint32_t* out, int* err,
+               uint32_t* slow_rows, uint32_t* slow_count, uint32_t* big_bins, hipStream_t s)
+{
+    uint32_t* part = bf.part;
+    const uint16_t* meta = bf.meta;
+    if (p.two) {
+        const int nb = 1 << p.bsh;
+        const size_t lds1 = (static_cast<size_t>(p.G) + kRvMaxBlockEdges) * sizeof(uint32_t);
+        ensure_lds(reinterpret_cast<const void*>(&rv_scatter_kernel), lds1);
+        hipLaunchKernelGGL(rv_scatter_kernel, dim3(p.nblk1), dim3(kRvScatterThreads), lds1, s, fwd, N, K, p.spb1,
+                           p.sshift, p.G, p.kbits, p.sbits1, bf.part1, bf.meta1, err, slow_count);
+        const size_t lds2 = (static_cast<size_t>(nb) + 2 * p.F + 1 + kRvMaxBlockEdges) * sizeof(uint32_t);
+        ensure_lds(reinterpret_cast<const void*>(&rv_scatter2_kernel), lds2);
+        hipLaunchKernelGGL(rv_scatter2_kernel, dim3(p.nblk, p.G), dim3(kRvScatterThreads), lds2, s, bf.part1, bf.meta1,
+                           p.nblk1, p.G, p.spb1, K, p.F, p.sshift, p.cshift, p.kbits, p.sbits1, p.sbits, bf.part,
+                           bf.meta_blk, p.nblk, err);
+        hipLaunchKernelGGL(rv_meta_transpose_kernel, dim3(static_cast<unsigned>(ceil_div(nb + 1, 64)),
+                                                          static_cast<unsigned>(ceil_div(p.nblk, 64)), p.G),
+                           dim3(256), 0, s, bf.meta_blk, p.nblk, nb, bf.meta, big_bins);
+    } else {
+        const size_t lds_s = (static_cast<size_t>(p.nbins) + kRvMaxBlockEdges) * sizeof(uint32_t);
+        ensure_lds(reinterpret_cast<const void*>(&rv_scatter_kernel), lds_s);
+        hipLaunchKernelGGL(rv_scatter_kernel, dim3(p.nblk), dim3(kRvScatterThreads), lds_s, s, fwd, N, K, p.spb,
+                           p.cshift, p.nbins, p.kbits, p.sbits, part, bf.meta_blk, err, slow_count);
+        hipLaunchKernelGGL(rv_meta_transpose_kernel, dim3(static_cast<unsigned>(ceil_div(p.nbins + 1, 64)),
+                                                          static_cast<unsigned>(ceil_div(p.nblk, 64))),
+                           dim3(256), 0, s, bf.meta_blk, p.nblk, p.nbins, bf.meta, big_bins);
+    }
     const size_t lds = rv_merge_lds(p, p.rp);
     RvPlan pb = p;
     pb.cap = p.cap_big;
@@ -945,20 +1151,22 @@ void launch_rv(const uint32_t* fwd, int64_t N, int K, const RvPlan& p, uint32_t*
     do {                                                                                                         \
         ensure_lds(reinterpret_cast<const void*>(&rv_merge_kernel<KM, R>), lds);                                 \
         hipLaunchKernelGGL((rv_merge_kernel<KM, R>), dim3(grid), dim3(R), lds, s, fwd, N, K, p.nblk, p.spb,      \
-                           p.cshift, p.nbins, p.kbits, p.sbits, p.nbits, part, meta, out, p.cap, slow_rows,      \
-                           slow_count, big_bins);                                                                \
+                           p.bsh, p.region, p.cshift, p.nbins, p.kbits, p.sbits, p.nbits, part, meta, out, p.cap, \
+                           slow_rows, slow_count, big_bins);                                                     \
         ensure_lds(reinterpret_cast<const void*>(&rv_big_kernel<KM>), lds_big);                                  \
         hipLaunchKernelGGL((rv_big_kernel<KM>), dim3(std::min(p.nbins, 512)), dim3(kRvBigThreads), lds_big, s, fwd, \
                            N, K,                                                                                 \
-                           p.nblk, p.spb, p.cshift, p.nbins, p.kbits, p.sbits, p.nbits, part, meta, out,         \
-                           p.cap_big, slow_rows, slow_count, big_bins);                                          \
+                           p.nblk, p.spb, p.bsh, p.region, p.cshift, p.nbins, p.kbits, p.sbits, p.nbits, part,   \
+                           meta, out, p.cap_big, slow_rows, slow_count, big_bins);                               \
         const size_t lds_w = (2 * static_cast<size_t>(p.nblk) + 1 + 64 * ((KM + 1) / 2) + KM + 1) * 4 * 4;     \
         ensure_lds(reinterpret_cast<const void*>(&rv_slow_kernel<KM>), lds_w);                                   \
         hipLaunchKernelGGL((rv_slow_kernel<KM>), dim3(256), dim3(256), lds_w, s, fwd, N, K, p.nblk, p.spb,       \
-                           p.cshift, p.nbins, p.kbits, p.sbits, p.nbits, part, meta, slow_rows, slow_count, out); \
+                           p.bsh, p.region, p.cshift, p.nbins, p.kbits, p.sbits, p.nbits, part, meta, slow_rows, \
+                           slow_count, out);                                                                     \
     } while (0)
     if (K <= 16) GT_RV_MERGE(16, 256);
     else if (K <= 32) GT_RV_MERGE(32, 256);
+    else if (K <= 48) GT_RV_MERGE(48, 256);
     else GT_RV_MERGE(64, 128);
 #undef GT_RV_MERGE
     GT_HIP(hipGetLastError());

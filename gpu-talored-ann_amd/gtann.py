@@ -30,7 +30,7 @@ EXPORTS = (
     "gt_reverse_merge_chunked", "gt_prune_windowed", "gt_debug_opts_default", "gt_set_debug",
 )
 SEEDING = {"auto": 0, "kmeans||": 1, "uniform": 2}
-REVMERGE_PATHS = {"auto": 0, "rv": 1, "binned": 2, "csr": 3}
+REVMERGE_PATHS = {"auto": 0, "rv": 1, "binned": 2, "csr": 3, "rv2": 4}
 
 
 class GtannError(RuntimeError):
@@ -287,7 +287,7 @@ class Context:
 
     def set_debug(self, **opts):
         """Path selection (gt_set_debug): every choice gives the same results.
-        Keywords: knn_collect (bool), revmerge_path ('auto'|'rv'|'binned'|'csr'),
+        Keywords: knn_collect (bool), revmerge_path ('auto'|'rv'|'binned'|'csr'|'rv2'),
         sub_order (bool), lloyd_host_csr (bool), prune_flat_rows (bool),
         knn_stats (bool), knn_prune (bool), bucket_host_csr (bool).  No
         keywords: the defaults."""

@@ -357,7 +357,7 @@ int gt_search(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtype, const
 typedef struct gt_debug_opts {
     int32_t knn_collect;     /* 1 (default): collect + select kNN where it applies; 0: merging kernels */
     int32_t revmerge_path;   /* reverse merge: 0 (default) by shape, 1 two-kernel (where it applies),
-                                2 binned, 3 global-atomic CSR */
+                                2 binned, 3 global-atomic CSR, 4 two-kernel behind superbins */
     int32_t sub_order;       /* 1 (default): unseeded passes scan members by nearest sub-centroid;
                                 0: the two-choice order */
     int32_t lloyd_host_csr;  /* 0 (default): Lloyd groups on the device; 1: on the host */

@@ -140,6 +140,24 @@ def test_reverse_merge_two_kernel_path_forced(ctx):
             _assert_rows_equal(ctx.reverse_merge(F), O.reverse_merge(F), F)
 
 
+def test_reverse_merge_superbin_path_forced(ctx):
+    """The two-kernel merge behind a level of superbins (revmerge_path='rv2',
+    the default beyond 2^21 rows): several superbins at these sizes, K from 1
+    to 64; the hub graphs send a quarter of all edges to two rows of the first
+    superbin, so its level-two blocks overflow and the rows are redone by the
+    binned merge."""
+    with debug_opts(ctx, revmerge_path="rv2"):
+        for N, K, hub in [(3000, 48, True), (70000, 48, False), (60000, 32, True), (200000, 32, False),
+                          (2000, 64, True), (700, 1, False), (50000, 16, False), (131104, 24, False)]:
+            rng = np.random.default_rng(N * 13 + K)
+            F = rng.integers(0, N, size=(N, K)).astype(np.uint32)
+            if hub:
+                F[rng.random((N, K)) < 0.2] = 3
+                F[rng.random((N, K)) < 0.05] = 5
+            print(f"rv2 path N={N} K={K} hub={hub}", flush=True)
+            _assert_rows_equal(ctx.reverse_merge(F), O.reverse_merge(F), F)
+
+
 def test_reverse_merge_binned_path(ctx):
     """The binned merge through global grouping (graphs between the two-kernel
     merge's 2^11 * 8192 rows and 2^26), forced by revmerge_path='binned'."""
