@@ -374,28 +374,26 @@ __device__ __forceinline__ bool rv_merge_lane(const uint32_t (&fw)[KMAX], int K,
     constexpr int PM = KMAX / 2;
     const int P = K >> 1, L = K - P;
     const uint32_t gmask = (1u << nbits) - 1u;
+    static_assert(PM % 2 == 0, "protected slots in pairs");
     uint32_t S[PM];
-    uint64_t sbloom = 0;
 #pragma unroll
     for (int p = 0; p < PM; ++p) {
         S[p] = p < P ? fw[p] : 0xFFFFFFFFu;
         // an opaque register copy: the per-key compares below then test
         // plain values instead of re-deriving the uniform bound p < P
         asm volatile("" : "+v"(S[p]));
-        sbloom |= p < P ? bloom_bit(fw[p]) : 0ull;
     }
     uint32_t lst[LM];
 #pragma unroll
     for (int l = 0; l < LM; ++l) lst[l] = l < LM - L ? 0u : 0xFFFFFFFFu;
     auto offer = [&](uint32_t x) {
         if (x >= lst[LM - 1]) return;
+        // protected: min_p (S[p] ^ s) == 0 (the padding never matches a source)
         const uint32_t s = x & gmask;
-        if (sbloom & bloom_bit(s)) {
-            bool prot = false;
+        uint32_t m = 0xFFFFFFFFu;
 #pragma unroll
-            for (int p = 0; p < PM; ++p) prot |= S[p] == s;
-            if (prot) return;
-        }
+        for (int p = 0; p < PM; p += 2) m = min(m, min(S[p] ^ s, S[p + 1] ^ s));
+        if (m == 0u) return;
         list_insert<LM>(lst, x);
     };
     // four LDS reads in flight per step.  With the keys in ascending rank
@@ -490,24 +488,20 @@ __device__ __forceinline__ bool rv_merge_full(const uint32_t (&fw)[KMAX], const 
     static_assert(P == L && P % 4 == 0, "even output degree, whole 16-byte halves");
     const uint32_t gmask = (1u << nbits) - 1u;
     uint32_t S[P];
-    uint64_t sbloom = 0;
 #pragma unroll
-    for (int p = 0; p < P; ++p) {
-        S[p] = fw[p];
-        sbloom |= bloom_bit(fw[p]);
-    }
+    for (int p = 0; p < P; ++p) S[p] = fw[p];
     uint32_t lst[L];
 #pragma unroll
     for (int l = 0; l < L; ++l) lst[l] = 0xFFFFFFFFu;
     auto offer = [&](uint32_t x) {
         if (x >= lst[L - 1]) return;
+        // protected: some S[p] == s, i.e. min_p (S[p] ^ s) == 0 -- vector
+        // instructions only (a wave takes the test whenever one lane needs it)
         const uint32_t s = x & gmask;
-        if (sbloom & bloom_bit(s)) {
-            bool prot = false;
+        uint32_t m = 0xFFFFFFFFu;
 #pragma unroll
-            for (int p = 0; p < P; ++p) prot |= S[p] == s;
-            if (prot) return;
-        }
+        for (int p = 0; p < P; p += 2) m = min(m, min(S[p] ^ s, S[p + 1] ^ s));
+        if (m == 0u) return;
         list_insert<L>(lst, x);
     };
     // keys in ascending rank groups: stop once the list's last slot is at or
