@@ -32,6 +32,8 @@ bool knn_collect_supported(const KnnArgs& a);
 void launch_knn_collect_select(const KnnArgs& a, int64_t rows, hipStream_t stream);
 void launch_merge_partials(const int32_t* pids, const float* pd, int64_t nq, int splits, int M, int32_t* out_ids,
                            float* out_d, hipStream_t stream);
+bool resident_supported(const KnnArgs& a, int64_t np);
+void launch_knn_resident(const KnnArgs& a, int64_t nq, int64_t np, hipStream_t stream);
 // graph_kernels.hip
 void launch_pad_convert(const void* src, int dtype, float* dst, int64_t N, int D, int Dp, hipStream_t s);
 void launch_row_norms(const float* X, int64_t N, int Dp, float* norms, hipStream_t s);
@@ -526,6 +528,23 @@ struct KnnJob {
 
 static void run_knn_flat(Ctx& c, const KnnJob& j, int min_items = 2048)
 {
+    if (c.c->dbg.knn_resident) {
+        // short lists of int8 rows against a small pool: the pool in LDS
+        KnnArgs a{};
+        set_operands(a, *j.Q, *j.P, j.metric);
+        a.q_rows = j.q_rows;
+        a.p_rows = j.p_rows;
+        a.M = j.M;
+        a.metric = j.metric;
+        a.exclude_self = j.exclude_self ? 1 : 0;
+        a.out_pos = j.out_pos ? 1 : 0;
+        a.out_ids = j.out_ids;
+        a.out_d = j.out_d;
+        if (resident_supported(a, j.np)) {
+            launch_knn_resident(a, j.nq, j.np, c.s);
+            return;
+        }
+    }
     const int64_t qtiles = ceil_div(j.nq, kQueriesPerBlock);
     int splits = 1;
     if (qtiles < min_items && j.np > 4096) {
@@ -2405,6 +2424,7 @@ void gt_debug_opts_default(gt_debug_opts* o)
     o->prune_flat_rows = 0;
     o->knn_stats = 0;
     o->knn_prune = 1;
+    o->knn_resident = 1;
 }
 
 int gt_set_debug(gt_ctx* ctx, const gt_debug_opts* o)

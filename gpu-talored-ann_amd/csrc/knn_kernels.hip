@@ -15,6 +15,7 @@
 // order are unique.
 #include "knn_device.hpp"
 
+#include <algorithm>
 #include <cfloat>
 #include <climits>
 #include <cmath>
@@ -910,6 +911,108 @@ knn_i8_kernel(KnnArgs a)
     }
 }
 
+// ------------------------------------------------------------ resident pools
+//
+// Short lists (M <= kSmallM) of every row of a flat query set against a pool
+// small enough to sit in LDS: centroid sets of up to resident_rows(Dp) rows
+// (C2's top-2 assignment, Lloyd steps and probe table).  Each block loads the
+// pool once and then walks query tiles blockIdx.x, + gridDim.x, ...: no stage
+// barrier and no row loads inside the scan, the next tile's query bytes in
+// flight during the current one.  Tiles go through small_tile as in
+// knn_i8_kernel's short lists (same keys, same order), so the lists are bit
+// for bit that kernel's.  (Larger pools split into parts would each warm up
+// a list of their own and merge them: measured slower than the staged kernel
+// at 2,048 centroids, so they stay there.)
+constexpr int kResidentLds = 78 * 1024;   // two blocks per CU
+
+static int resident_rows(int dp) { return kResidentLds / (dp + 24) / kPoolTile * kPoolTile; }
+
+template <int DP, int METRIC>
+__global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(2)))
+knn_i8_resident_kernel(KnnArgs a, int64_t nq, int64_t npool, int pc)   // npool <= pc
+{
+    constexpr int KS = DP / 32;
+    constexpr int RS = DP + 16;          // LDS row stride: rows land on distinct bank groups
+    constexpr int U4_ROW = DP / 16;
+    extern __shared__ __align__(16) unsigned char res_lds[];
+    int8_t* tile = reinterpret_cast<int8_t*>(res_lds);
+    float* tn = reinterpret_cast<float*>(res_lds + static_cast<size_t>(pc) * RS);   // |p|^2 (L2), 0 (IP), +inf past the pool
+    int32_t* tr = reinterpret_cast<int32_t*>(tn + pc);                            // pool positions, -1 past the pool
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, j = lane & 31, h = lane >> 5;
+    constexpr int64_t p0 = 0;
+    const int pcnt = static_cast<int>(npool);
+    for (int e = tid; e < pc * U4_ROW; e += 256) {
+        const int r = e / U4_ROW, c = e % U4_ROW;
+        uint4 v = make_uint4(0u, 0u, 0u, 0u);
+        if (r < pcnt) v = *reinterpret_cast<const uint4*>(a.Xp8 + (p0 + r) * DP + 16 * c);
+        *reinterpret_cast<uint4*>(tile + r * RS + 16 * c) = v;
+    }
+    for (int r = tid; r < pc; r += 256) {
+        tn[r] = r < pcnt ? (METRIC == 0 ? a.np[p0 + r] : 0.f) : INFINITY;
+        tr[r] = r < pcnt ? static_cast<int32_t>(p0 + r) : -1;
+    }
+    __syncthreads();
+    const int ntiles = (pcnt + kPoolTile - 1) / kPoolTile;
+    const int64_t nqt = (nq + kQueriesPerBlock - 1) / kQueriesPerBlock;
+    // lane (j, h) holds bytes [32s + 16h, 32s + 16h + 16) of its query for every step s
+    auto load_q = [&](int64_t qt, intx4 (&qf)[KS]) {
+        const int64_t q = qt * kQueriesPerBlock + w * kQueriesPerWave + j;
+        const int8_t* src = a.Xq8 + (q < nq ? q : 0) * DP + 16 * h;
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+            const intx4 v = *reinterpret_cast<const intx4*>(src + 32 * s);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) qf[s][e] = q < nq ? v[e] : 0;
+        }
+    };
+    intx4 qnext[KS];
+    int64_t qt = blockIdx.x;
+    if (qt < nqt) load_q(qt, qnext);
+    for (; qt < nqt; qt += gridDim.x) {
+        intx4 qf[KS];
+#pragma unroll
+        for (int s = 0; s < KS; ++s) qf[s] = qnext[s];
+        if (qt + gridDim.x < nqt) load_q(qt + gridDim.x, qnext);
+        const int64_t q = qt * kQueriesPerBlock + w * kQueriesPerWave + j;
+        const bool qvalid = q < nq;
+        const float qn = (qvalid && METRIC == 0) ? a.nq[q] : 0.f;
+        QueryState st;
+        st.seed = FLT_MAX;
+        st.thr = qvalid ? st.seed : -INFINITY;
+        st.cnt = 0;
+        st.nL = 0;
+        st.self = a.exclude_self ? static_cast<int32_t>(q) : -2;
+        st.orow = q;
+        SmallList SL;
+#pragma unroll
+        for (int i = 0; i < kSmallM; ++i) SL.k[i] = kNoKey;
+        SL.kth = st.thr;
+        // tile t - 1 is filtered while tile t's MFMAs run
+        intx16 acc_prev;
+        for (int t = 0; t < ntiles; ++t) {
+            intx16 acc;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[r] = 0;
+            const int8_t* arow = tile + (t * kPoolTile + j) * RS + 16 * h;
+#pragma unroll
+            for (int s = 0; s < KS; ++s) {
+                const intx4 av = *reinterpret_cast<const intx4*>(arow + 32 * s);
+                acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, qf[s], acc, 0, 0, 0);
+            }
+            if (t > 0) {
+                const int b = (t - 1) * kPoolTile;
+                small_tile<METRIC>(a, acc_prev, tn + b, tr + b, static_cast<int>(p0) + b, h, qvalid, qn, st, SL);
+            }
+            acc_prev = acc;
+        }
+        if (ntiles > 0) {
+            const int b = (ntiles - 1) * kPoolTile;
+            small_tile<METRIC>(a, acc_prev, tn + b, tr + b, static_cast<int>(p0) + b, h, qvalid, qn, st, SL);
+        }
+        small_finish(a, SL, j, h, qvalid, st.orow);
+    }
+}
+
 // ------------------------------------------------------------ wide rows
 //
 // Rows longer than 256 floats do not fit a wave's registers as a query
@@ -1214,6 +1317,46 @@ static void launch_knn_i8(const KnnArgs& a, dim3 grid, hipStream_t stream)
 {
     if (a.M <= kSmallM) launch_knn_i8_v<METRIC, true>(a, grid, stream);
     else launch_knn_i8_v<METRIC, false>(a, grid, stream);
+}
+
+// Whether knn_i8_resident_kernel takes the flat job a against np pool rows:
+// int8 operands, short lists, identity query and pool lists, no seed, and a
+// pool that fits the LDS.
+bool resident_supported(const KnnArgs& a, int64_t np)
+{
+    return a.Xq8 && a.Xp8 && a.M >= 1 && a.M <= kSmallM && !a.q_rows && !a.p_rows && !a.seed_d && a.Dp % 32 == 0 &&
+           a.Dp >= 32 && a.Dp <= 256 && np >= 1 && np <= resident_rows(a.Dp);
+}
+
+void launch_knn_resident(const KnnArgs& a, int64_t nq, int64_t np, hipStream_t stream)
+{
+    GT_REQUIRE(resident_supported(a, np), "resident short-list kNN: unsupported job");
+    if (nq <= 0) return;
+    const int pc = static_cast<int>(ceil_div(np, kPoolTile) * kPoolTile);
+    const int64_t nqt = ceil_div(nq, kQueriesPerBlock);
+    const dim3 grid(static_cast<unsigned>(std::max<int64_t>(1, std::min<int64_t>(nqt, 1024))));
+    const size_t lds = static_cast<size_t>(pc) * (a.Dp + 16) + static_cast<size_t>(pc) * 8;
+#define GT_RES(DPV, MET)                                                                                  \
+    do {                                                                                                  \
+        const void* f = reinterpret_cast<const void*>(&knn_i8_resident_kernel<DPV, MET>);                 \
+        GT_HIP(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds))); \
+        hipLaunchKernelGGL((knn_i8_resident_kernel<DPV, MET>), grid, dim3(256), lds, stream, a, nq, np, pc); \
+    } while (0)
+#define GT_RES_DP(MET)                                                        \
+    switch (a.Dp) {                                                           \
+    case 32: GT_RES(32, MET); break;                                          \
+    case 64: GT_RES(64, MET); break;                                          \
+    case 96: GT_RES(96, MET); break;                                          \
+    case 128: GT_RES(128, MET); break;                                        \
+    case 160: GT_RES(160, MET); break;                                        \
+    case 192: GT_RES(192, MET); break;                                        \
+    case 224: GT_RES(224, MET); break;                                        \
+    default: GT_RES(256, MET); break;                                         \
+    }
+    if (a.metric == 0) GT_RES_DP(0) else GT_RES_DP(1)
+#undef GT_RES_DP
+#undef GT_RES
+    GT_HIP(hipGetLastError());
 }
 
 // n_items must be a multiple of 8 (XCD-major layout, see knn_fused_kernel).

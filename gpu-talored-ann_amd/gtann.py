@@ -53,7 +53,7 @@ class DebugOpts(C.Structure):
     _fields_ = [
         ("knn_collect", C.c_int32), ("revmerge_path", C.c_int32), ("sub_order", C.c_int32),
         ("lloyd_host_csr", C.c_int32), ("prune_flat_rows", C.c_int32), ("knn_stats", C.c_int32),
-        ("knn_prune", C.c_int32), ("bucket_host_csr", C.c_int32),
+        ("knn_prune", C.c_int32), ("bucket_host_csr", C.c_int32), ("knn_resident", C.c_int32),
     ]
 
 
@@ -289,7 +289,8 @@ class Context:
         """Path selection (gt_set_debug): every choice gives the same results.
         Keywords: knn_collect (bool), revmerge_path ('auto'|'rv'|'binned'|'csr'|'rv2'),
         sub_order (bool), lloyd_host_csr (bool), prune_flat_rows (bool),
-        knn_stats (bool), knn_prune (bool), bucket_host_csr (bool).  No
+        knn_stats (bool), knn_prune (bool), bucket_host_csr (bool),
+        knn_resident (bool).  No
         keywords: the defaults."""
         o = DebugOpts()
         lib().gt_debug_opts_default(C.byref(o))

@@ -369,6 +369,10 @@ typedef struct gt_debug_opts {
                                 sphere is farther from every query than its threshold (exact); 0: scans all */
     int32_t bucket_host_csr; /* 0 (default): the bucket members are ordered on the device (the host
                                 runs only the two-choice rule); 1: on the host (same order) */
+    int32_t knn_resident;    /* 1 (default): short lists of int8 rows against a centroid set that fits
+                                the LDS (top-2 assignment, Lloyd steps, probe tables; up to 512
+                                centroids of 128 bytes) with the centroids held there; 0: the
+                                staged-pool kernel */
 } gt_debug_opts;
 
 void gt_debug_opts_default(gt_debug_opts* o);

@@ -197,3 +197,40 @@ def test_invalid_arguments_raise(ctx):
     off = np.array([0, 50], np.int64)   # does not cover all points
     with pytest.raises(gtann.GtannError):
         ctx.knn_bucketed(X, off, np.arange(100, dtype=np.int32), np.zeros((1, 0), np.int32), 8)
+
+
+@pytest.mark.parametrize("n,nb,D,lo,hi", [(30000, 300, 128, -128, 128), (20000, 500, 128, -2, 3),
+                                           (20000, 250, 256, -128, 128), (12000, 40, 32, 0, 2),
+                                           (30000, 900, 128, -128, 128)])
+def test_bucketing_resident_centroids(ctx, n, nb, D, lo, hi):
+    """Lloyd steps, probe table and top-2 assignment of int8 rows with the
+    centroids held in LDS (up to 512 of 128 bytes, 288 of 256; 900 take the
+    staged kernel either way): the staged kernel's build, table and graph bit
+    for bit.  Values in [-2, 3) and [0, 2) give ties among centroids."""
+    from helpers import debug_opts
+    rng = np.random.default_rng(n + nb + D)
+    X = rng.integers(lo, hi, size=(n, D)).astype(np.int8)
+    kw = dict(n_buckets=nb, nprobe=1, M=32, K=16, rounds=2)
+    print(f"resident centroids n={n} buckets={nb} D={D}", flush=True)
+    a = ctx.build_graph(X, **kw)
+    with debug_opts(ctx, knn_resident=False):
+        b = ctx.build_graph(X, **kw)
+    np.testing.assert_array_equal(a.knn_ids, b.knn_ids)
+    np.testing.assert_array_equal(a.knn_dists.view(np.uint32), b.knn_dists.view(np.uint32))
+    np.testing.assert_array_equal(a.graph, b.graph)
+
+
+@pytest.mark.parametrize("k", [1, 3, 4])
+def test_knn_exact_short_lists_resident(ctx, k):
+    # exact kNN of a small int8 set with k <= 4 (self excluded) takes the
+    # LDS-resident kernel: the staged kernel's lists bit for bit
+    from helpers import debug_opts
+    rng = np.random.default_rng(k)
+    X = rng.integers(-3, 4, size=(2500, 64)).astype(np.int8)
+    a = ctx.knn_exact(X, k)
+    with debug_opts(ctx, knn_resident=False):
+        b = ctx.knn_exact(X, k)
+    np.testing.assert_array_equal(a[0], b[0])
+    np.testing.assert_array_equal(a[1].view(np.uint32), b[1].view(np.uint32))
+    rid, rd = O.knn_exact(X.astype(np.float32), k)
+    assert_knn_equal(a[0], a[1], rid, rd)
