@@ -714,6 +714,33 @@ __device__ __forceinline__ void i8_filter_tile(KnnLists& L, const KnnArgs& a, co
     }
 }
 
+// One finished 32x32 tile of the resident short-list kernel, whose
+// accumulators started at -floor(|p|^2 / 2) (L2) or 0 (IP) (th): a tile none
+// of whose v reach the pass floor lo of the list's bound holds no row that
+// small_tile would keep (the same argument as i8_filter_tile's), so it costs
+// a max and a ballot; the others go through small_tile with the exact dot
+// products, after which lo follows the list's (possibly lowered) bound.
+template <int METRIC>
+__device__ __forceinline__ void small_tile_i8(const KnnArgs& a, const intx16& acc, const float* tn, const int32_t* tr,
+                                              const int32_t* th, int tbase, int h, bool qvalid, float qn,
+                                              const QueryState& st, SmallList& L, int32_t& lo)
+{
+    int32_t vmax = INT_MIN;
+#pragma unroll
+    for (int r = 0; r < 16; r += 2) vmax = max(vmax, max(acc[r], acc[r + 1]));
+    if (!__ballot(qvalid && vmax >= lo)) return;
+    intx16 dot;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const int4 hv = *reinterpret_cast<const int4*>(th + 8 * g + 4 * h);
+        const int32_t h4[4] = {hv.x, hv.y, hv.z, hv.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) dot[4 * g + e] = acc[4 * g + e] - h4[e];
+    }
+    small_tile<METRIC>(a, dot, tn, tr, tbase, h, qvalid, qn, st, L);
+    lo = i8_pass_floor<METRIC>(L.kth, qn);
+}
+
 // Three waves per SIMD for the list launches (at most 168 VGPRs), two for
 // the register short lists.
 template <int DP, int METRIC, bool SMALL>
@@ -918,14 +945,14 @@ knn_i8_kernel(KnnArgs a)
 // (C2's top-2 assignment, Lloyd steps and probe table).  Each block loads the
 // pool once and then walks query tiles blockIdx.x, + gridDim.x, ...: no stage
 // barrier and no row loads inside the scan, the next tile's query bytes in
-// flight during the current one.  Tiles go through small_tile as in
+// flight during the current one.  Tiles go through small_tile_i8 as in
 // knn_i8_kernel's short lists (same keys, same order), so the lists are bit
 // for bit that kernel's.  (Larger pools split into parts would each warm up
 // a list of their own and merge them: measured slower than the staged kernel
 // at 2,048 centroids, so they stay there.)
 constexpr int kResidentLds = 78 * 1024;   // two blocks per CU
 
-static int resident_rows(int dp) { return kResidentLds / (dp + 24) / kPoolTile * kPoolTile; }
+static int resident_rows(int dp) { return kResidentLds / (dp + 28) / kPoolTile * kPoolTile; }
 
 template <int DP, int METRIC>
 __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(2)))
@@ -938,6 +965,7 @@ knn_i8_resident_kernel(KnnArgs a, int64_t nq, int64_t npool, int pc)   // npool 
     int8_t* tile = reinterpret_cast<int8_t*>(res_lds);
     float* tn = reinterpret_cast<float*>(res_lds + static_cast<size_t>(pc) * RS);   // |p|^2 (L2), 0 (IP), +inf past the pool
     int32_t* tr = reinterpret_cast<int32_t*>(tn + pc);                            // pool positions, -1 past the pool
+    int32_t* th = tr + pc;   // accumulator starts: -floor(|p|^2 / 2) (L2), 0 (IP), kHalfPast past the pool
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, j = lane & 31, h = lane >> 5;
     constexpr int64_t p0 = 0;
     const int pcnt = static_cast<int>(npool);
@@ -948,8 +976,10 @@ knn_i8_resident_kernel(KnnArgs a, int64_t nq, int64_t npool, int pc)   // npool 
         *reinterpret_cast<uint4*>(tile + r * RS + 16 * c) = v;
     }
     for (int r = tid; r < pc; r += 256) {
-        tn[r] = r < pcnt ? (METRIC == 0 ? a.np[p0 + r] : 0.f) : INFINITY;
+        const float n = r < pcnt ? (METRIC == 0 ? a.np[p0 + r] : 0.f) : INFINITY;
+        tn[r] = n;
         tr[r] = r < pcnt ? static_cast<int32_t>(p0 + r) : -1;
+        th[r] = r < pcnt ? -(static_cast<int32_t>(n) >> 1) : kHalfPast;
     }
     __syncthreads();
     const int ntiles = (pcnt + kPoolTile - 1) / kPoolTile;
@@ -987,12 +1017,16 @@ knn_i8_resident_kernel(KnnArgs a, int64_t nq, int64_t npool, int pc)   // npool 
 #pragma unroll
         for (int i = 0; i < kSmallM; ++i) SL.k[i] = kNoKey;
         SL.kth = st.thr;
+        int32_t lo = i8_pass_floor<METRIC>(st.thr, qn);
         // tile t - 1 is filtered while tile t's MFMAs run
         intx16 acc_prev;
         for (int t = 0; t < ntiles; ++t) {
             intx16 acc;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) acc[r] = 0;
+            for (int g = 0; g < 4; ++g) {
+                const int4 hv = *reinterpret_cast<const int4*>(th + t * kPoolTile + 8 * g + 4 * h);
+                acc[4 * g] = hv.x; acc[4 * g + 1] = hv.y; acc[4 * g + 2] = hv.z; acc[4 * g + 3] = hv.w;
+            }
             const int8_t* arow = tile + (t * kPoolTile + j) * RS + 16 * h;
 #pragma unroll
             for (int s = 0; s < KS; ++s) {
@@ -1001,13 +1035,15 @@ knn_i8_resident_kernel(KnnArgs a, int64_t nq, int64_t npool, int pc)   // npool 
             }
             if (t > 0) {
                 const int b = (t - 1) * kPoolTile;
-                small_tile<METRIC>(a, acc_prev, tn + b, tr + b, static_cast<int>(p0) + b, h, qvalid, qn, st, SL);
+                small_tile_i8<METRIC>(a, acc_prev, tn + b, tr + b, th + b, static_cast<int>(p0) + b, h, qvalid, qn, st,
+                                      SL, lo);
             }
             acc_prev = acc;
         }
         if (ntiles > 0) {
             const int b = (ntiles - 1) * kPoolTile;
-            small_tile<METRIC>(a, acc_prev, tn + b, tr + b, static_cast<int>(p0) + b, h, qvalid, qn, st, SL);
+            small_tile_i8<METRIC>(a, acc_prev, tn + b, tr + b, th + b, static_cast<int>(p0) + b, h, qvalid, qn, st, SL,
+                                  lo);
         }
         small_finish(a, SL, j, h, qvalid, st.orow);
     }
@@ -1335,7 +1371,7 @@ void launch_knn_resident(const KnnArgs& a, int64_t nq, int64_t np, hipStream_t s
     const int pc = static_cast<int>(ceil_div(np, kPoolTile) * kPoolTile);
     const int64_t nqt = ceil_div(nq, kQueriesPerBlock);
     const dim3 grid(static_cast<unsigned>(std::max<int64_t>(1, std::min<int64_t>(nqt, 1024))));
-    const size_t lds = static_cast<size_t>(pc) * (a.Dp + 16) + static_cast<size_t>(pc) * 8;
+    const size_t lds = static_cast<size_t>(pc) * (a.Dp + 16) + static_cast<size_t>(pc) * 12;
 #define GT_RES(DPV, MET)                                                                                  \
     do {                                                                                                  \
         const void* f = reinterpret_cast<const void*>(&knn_i8_resident_kernel<DPV, MET>);                 \
