@@ -1154,6 +1154,10 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
         }
     }
     if (merged) *merged = a.run_ids != nullptr;
+    // the unseeded pass's threshold window: 32 tiles on large builds (C5:
+    // 423 -> about 200 keys per query, kNN 97 -> 80 ms), 16 below (C2: 32
+    // tiles take 0.14 ms more than the 23 % fewer keys save)
+    a.window_tiles = c.c->dbg.knn_window > 0 ? c.c->dbg.knn_window : X.N >= (int64_t(1) << 22) ? 32 : 16;
     // exact chunk pruning (int8 rows, L2): the centre and radius of every
     // kChunkRows rows of the pool list
     const bool prune = collect && a.Xq8 && a.Xp8 && metric == GT_METRIC_L2 && c.c->dbg.knn_prune != 0 &&
@@ -2433,6 +2437,10 @@ int gt_set_debug(gt_ctx* ctx, const gt_debug_opts* o)
     gt_debug_opts d;
     gt_debug_opts_default(&d);
     if (o) d = *o;
+    if (d.knn_window < 0 || d.knn_window > 32 || (d.knn_window & 1)) {
+        ctx->err = "gt_set_debug: knn_window must be 0 or an even number of tiles up to 32";
+        return GT_EINVAL;
+    }
     if (d.revmerge_path < 0 || d.revmerge_path > 4) {
         ctx->err = "gt_set_debug: revmerge_path must be 0..4";
         return GT_EINVAL;

@@ -93,6 +93,7 @@ struct KnnArgs {
     float* run_d;
     int32_t* hl_rows;      // (rows): int8 merge: the rows left to the selection
     uint32_t* hl_count;    // their number
+    int32_t window_tiles;  // collect launches, unseeded: tiles of the threshold window (0: 16)
 };
 
 constexpr int kChunkRows = 64;       // pool rows per pruning chunk (= one collect stage)

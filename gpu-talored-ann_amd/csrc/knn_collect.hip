@@ -8,7 +8,7 @@
 // list: every key at or below the query's threshold is appended to the
 // query's candidate slots in HBM.  The threshold is the caller's cap (the
 // running M-th distance of a seeded pass) or, in an unseeded pass, a bound
-// taken from the first kWindow tiles of the scan: each lane keeps the 32
+// taken from the first tiles of the scan (the window): each lane keeps the 32
 // smallest distances among the pool rows it holds in those tiles (a sorting
 // network on registers), and the larger of the pair's ceil(M/2)-th smallest
 // bounds the pool's M-th smallest from above (those are M distinct rows).
@@ -30,7 +30,14 @@
 
 namespace gtann {
 
-constexpr int kWindow = 16;   // tiles (of kPoolTile pool rows) of the unseeded threshold pass
+// tiles (of kPoolTile pool rows) of the unseeded threshold pass: the
+// caller's KnnArgs::window_tiles (even, at most kWindowMax), else kWindow
+constexpr int kWindow = 16;
+constexpr int kWindowMax = 32;
+__device__ __forceinline__ int window_tiles(const KnnArgs& a)
+{
+    return a.window_tiles > 0 ? min(a.window_tiles, kWindowMax) & ~1 : kWindow;
+}
 
 // Per-wave staging of a tile's candidates: every lane's 16 accumulators
 // (16-byte chunks swizzled by lane so that a wave's 128-bit stores spread
@@ -62,7 +69,7 @@ struct CollectSmem {
     // schedule of the stages still to scan
     uint32_t wmask[kWaves][kMaxChunkWords];
     uint32_t bmask[kMaxChunkWords];
-    uint16_t slist[kMaxChunkWords * 32 + kWindow / kStageTiles + 2];
+    uint16_t slist[kMaxChunkWords * 32 + kWindowMax / kStageTiles + 2];
     int32_t nlist;
 };
 static_assert(kChunkRows == kStageRows, "a pruning chunk is one stage of pool rows");
@@ -258,7 +265,7 @@ knn_i8_collect_kernel(KnnArgs a)
     constexpr int U4_STAGE = ROWS * U4_ROW;
     constexpr int U4_THREAD = (U4_STAGE + 255) / 256;
     static_assert(DP % 32 == 0, "row stride must be a multiple of 32 bytes");
-    static_assert(ROWS <= 256 && kWindow % kStageTiles == 0, "stage shape");
+    static_assert(ROWS <= 256 && kWindow % kStageTiles == 0 && kWindowMax % kStageTiles == 0, "stage shape");
     __shared__ CollectSmem<DP> sm;
 
     const int per = a.n_items / 8;
@@ -308,7 +315,7 @@ knn_i8_collect_kernel(KnnArgs a)
     // threshold and are scanned again at the end
     const int pcount = it.p_count;
     const int nps = (pcount + ROWS - 1) / ROWS;
-    const int nws = a.seed_d ? 0 : min(kWindow / kStageTiles, nps);
+    const int nws = a.seed_d ? 0 : min(window_tiles(a) / kStageTiles, nps);
     const int nst = nps + nws;
     // Chunk pruning (L2, integer rows): once every query of the block has its
     // threshold, a stage is scanned only if some query may hold a key in it:
@@ -731,7 +738,7 @@ __global__ void __launch_bounds__(256, 2) knn_f32_collect_kernel(KnnArgs a)
     // bound the threshold first and are scanned again at the end
     const int pcount = it.p_count;
     const int ntl = (pcount + kPoolTile - 1) / kPoolTile;
-    const int nwt = a.seed_d ? 0 : min(kWindow, ntl);
+    const int nwt = a.seed_d ? 0 : min(window_tiles(a), ntl);
     const int nst = ntl + nwt;
     auto pool_row = [&](int t, int r) __attribute__((always_inline)) -> int32_t {
         if (t >= nst) return -1;

@@ -54,6 +54,7 @@ class DebugOpts(C.Structure):
         ("knn_collect", C.c_int32), ("revmerge_path", C.c_int32), ("sub_order", C.c_int32),
         ("lloyd_host_csr", C.c_int32), ("prune_flat_rows", C.c_int32), ("knn_stats", C.c_int32),
         ("knn_prune", C.c_int32), ("bucket_host_csr", C.c_int32), ("knn_resident", C.c_int32),
+        ("knn_window", C.c_int32),
     ]
 
 
@@ -290,7 +291,7 @@ class Context:
         Keywords: knn_collect (bool), revmerge_path ('auto'|'rv'|'binned'|'csr'|'rv2'),
         sub_order (bool), lloyd_host_csr (bool), prune_flat_rows (bool),
         knn_stats (bool), knn_prune (bool), bucket_host_csr (bool),
-        knn_resident (bool).  No
+        knn_resident (bool), knn_window (even tiles, 0 = by size).  No
         keywords: the defaults."""
         o = DebugOpts()
         lib().gt_debug_opts_default(C.byref(o))

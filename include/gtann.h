@@ -373,6 +373,8 @@ typedef struct gt_debug_opts {
                                 the LDS (top-2 assignment, Lloyd steps, probe tables; up to 512
                                 centroids of 128 bytes) with the centroids held there; 0: the
                                 staged-pool kernel */
+    int32_t knn_window;      /* tiles of 32 pool rows in the unseeded collect pass's threshold window
+                                (2..32, even); 0 (default): 32 on builds of 2^22 rows or more, else 16 */
 } gt_debug_opts;
 
 void gt_debug_opts_default(gt_debug_opts* o);

@@ -225,3 +225,19 @@ def test_chunk_pruning_uniform_rows(ctx):
         b = ctx.build_graph(X, **kw)
     np.testing.assert_array_equal(a.knn_ids, b.knn_ids)
     np.testing.assert_array_equal(a.graph, b.graph)
+
+
+@pytest.mark.parametrize("window", [2, 16, 32])
+def test_collect_threshold_window_sizes(ctx, window):
+    # the unseeded pass's threshold window (32 tiles on builds of 2^22 rows
+    # or more) changes how many keys are collected, never the lists
+    rng = np.random.default_rng(41)
+    N, B = 9000, 3
+    X = _data(N, 128, seed=42, lo=-20, hi=21)
+    off, mem = _buckets(rng, N, B)
+    probe = _probe(rng, B, 1)
+    print(f"collect window {window}", flush=True)
+    with debug_opts(ctx, knn_window=window):
+        ids, dist = ctx.knn_bucketed(X, off, mem, probe, 64)
+    ri, rd = O.knn_bucketed(X.astype(np.float32), off, mem, probe, 64)
+    assert_knn_equal(ids, dist, ri, rd)

@@ -136,3 +136,20 @@ def test_f32_build_equals_merging_kernel(ctx):
     np.testing.assert_array_equal(a.knn_ids, b.knn_ids)
     np.testing.assert_array_equal(a.knn_dists, b.knn_dists)
     np.testing.assert_array_equal(a.graph, b.graph)
+
+
+@pytest.mark.parametrize("window,metric", [(2, "l2"), (32, "l2"), (32, "ip")])
+def test_f32_collect_threshold_window_sizes(ctx, window, metric):
+    # the threshold window's size changes how many keys are collected, never
+    # the lists: the merging kernel's bit for bit
+    rng = np.random.default_rng(window + 5)
+    N, D, B = 8000, 96, 3
+    X = _data(N, D, seed=window)
+    if metric == "ip":
+        X /= np.linalg.norm(X, axis=1, keepdims=True)
+    off, mem = _buckets(rng, N, B)
+    probe = _probe(rng, B, 1)
+    print(f"f32 collect window {window} {metric}", flush=True)
+    with debug_opts(ctx, knn_window=window):
+        got = ctx.knn_bucketed(X, off, mem, probe, 64, metric=metric)
+    _equal(got, _merging(ctx, X, off, mem, probe, 64, metric=metric))
