@@ -34,8 +34,8 @@ Beside `value` (dataset resident in HBM), the line carries the other two
 build-time definitions: `host_to_host` (dataset in host memory, graph and
 table back in host memory) and `file_io` (the gtann CLI's bucket2 from a
 .fbin file to the reference's output files, a separate process);
-`reference_knobs` (3 rounds, data points as centroids, nprobe = ceil(20000 /
-avg bucket)) on the same data; `configs` (C1, C3, C4, C5 with the default
+`reference_knobs` (3 rounds, KMeans|| data-point centroids, nprobe =
+ceil(20000 / avg bucket)) on the same data; `configs` (C1, C3, C4, C5 with the default
 knobs: build time, recall@32, kernel fraction of peak); and `cpu_baseline`,
 the reference's CPU path on this host (numpy BLAS blocked kNN as
 bd/build_knn.py, the reference's own prune and merge headers compiled in
@@ -436,7 +436,7 @@ def main():
     ap.add_argument("--kmeans-iters", type=int, default=3)
     ap.add_argument("--nprobe", type=int, default=1)
     ap.add_argument("--reference-knobs", action="store_true",
-                    help="headline at the reference's own bucketing settings: 3 rounds, sampled data points as "
+                    help="headline at the reference's own bucketing settings: 3 rounds, KMeans|| data-point "
                          "centroids, nprobe = ceil(20000 / avg bucket) (also reported as reference_knobs)")
     ap.add_argument("--no-ref-knobs", action="store_true", help="skip the reference_knobs builds")
     ap.add_argument("--cpu-sample", type=int, default=2048)
@@ -574,8 +574,8 @@ def main():
         # the reference's own knobs on the same data
         wr, sr, rr = timed_builds(ctx, torch, Xd, dict(base_kw, **ref_kw), max(1, min(args.steps, 2)))
         out["reference_knobs"] = {
-            "knobs": "3 rounds, sampled data points as centroids (no Lloyd), nprobe = ceil(20000 / avg bucket) "
-                     "(sk/scripts/params.sh:12, sk/scripts/dataset_env.py:56)",
+            "knobs": "3 rounds, KMeans|| data-point centroids (D^2 oversampling, no Lloyd; src/bucket.cu:2833-3168), "
+                     "nprobe = ceil(20000 / avg bucket) (sk/scripts/params.sh:12, sk/scripts/dataset_env.py:56)",
             "ms_per_step": wr * 1e3, "value": N / wr / 1e6, "unit": "Mpts/s",
             "recall@32": recall_at(rr.knn_ids.cpu().numpy()[q], ex_i, 32),
             "knn_roofline": knn_roofline(sr, D, cfg.metric, cfg.M)}
