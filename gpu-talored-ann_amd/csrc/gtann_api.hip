@@ -1958,9 +1958,9 @@ static void reverse_merge_chunked(Ctx& c, const uint32_t* fwd, int64_t N, int K,
     if (h_err) throw Error(GT_EINVAL, "reverse merge: forward graph holds an id >= N");
     HostBuf hout;
     uint32_t* st_out = hout.as<uint32_t>(static_cast<size_t>(R) * K);
-    for (int64_t q = 0; q < nchunks; ++q) {
-        const int64_t c0 = q * R, nr = std::min(R, N - c0);
-        const std::vector<uint64_t>& v = recs[static_cast<size_t>(q)];
+    // phase 2 on destination rows [c0, c0 + nr) and their records v (row
+    // local to c0)
+    auto merge_rows = [&](int64_t c0, int64_t nr, const std::vector<uint64_t>& v) {
         const int64_t nrec = static_cast<int64_t>(v.size());
         unsigned long long* d_rec = c.ws<unsigned long long>(W_OOC_B, static_cast<size_t>(std::max<int64_t>(nrec, 1)));
         unsigned long long* d_key = c.ws<unsigned long long>(W_OOC_E, static_cast<size_t>(std::max<int64_t>(nrec, 1)));
@@ -1983,6 +1983,34 @@ static void reverse_merge_chunked(Ctx& c, const uint32_t* fwd, int64_t N, int K,
         if (rep) {
             rep->chunks++;
             rep->rows_moved += static_cast<double>(nr);
+        }
+    };
+    // A chunk holds about R * K records (one per forward edge into it), which
+    // the budget was sized for; a chunk whose rows receive more (hub rows) is
+    // merged in row ranges whose records fit, a single row over that alone.
+    const size_t cap = static_cast<size_t>(R) * K;
+    constexpr uint64_t kLocal = 0x3FFFFFFull;   // a record's row within its chunk: bits 32..57
+    for (int64_t q = 0; q < nchunks; ++q) {
+        const int64_t c0 = q * R, nr = std::min(R, N - c0);
+        const std::vector<uint64_t>& v = recs[static_cast<size_t>(q)];
+        if (v.size() <= cap) {
+            merge_rows(c0, nr, v);
+            continue;
+        }
+        std::vector<size_t> cnt(static_cast<size_t>(nr), 0);
+        for (const uint64_t r : v) cnt[static_cast<size_t>((r >> 32) & kLocal)]++;
+        for (int64_t a = 0; a < nr;) {
+            int64_t b = a + 1;
+            size_t sum = cnt[static_cast<size_t>(a)];
+            while (b < nr && sum + cnt[static_cast<size_t>(b)] <= cap) sum += cnt[static_cast<size_t>(b++)];
+            std::vector<uint64_t> sub;
+            sub.reserve(sum);
+            for (const uint64_t r : v) {
+                const int64_t dl = static_cast<int64_t>((r >> 32) & kLocal);
+                if (dl >= a && dl < b) sub.push_back(r - (static_cast<uint64_t>(a) << 32));
+            }
+            merge_rows(c0 + a, b - a, sub);
+            a = b;
         }
     }
 }

@@ -132,7 +132,10 @@ int gt_reverse_insert(gt_ctx* ctx, int32_t* ids, float* dists, int64_t N, int32_
  * out of core: the forward rows stream through the device in batches that
  * route every edge to its destination chunk, then one destination chunk at a
  * time is merged, each within device_budget_bytes of device memory (<= 0:
- * one chunk).  Same rows as gt_reverse_merge.  Replaces run_method_E with
+ * one chunk); a chunk whose rows receive more edges than its share (hub
+ * rows) is merged in row ranges that fit, and a single row with more
+ * in-edges than a chunk's share alone, over the budget by its excess.  Same
+ * rows as gt_reverse_merge.  Replaces run_method_E with
  * several chunks (src/optimize_chunked.cu:1548-2057; optimize_chunked -m E
  * --gpu-budget-mb). */
 int gt_reverse_merge_chunked(gt_ctx* ctx, const uint32_t* fwd, int64_t N, int32_t K, int64_t device_budget_bytes,

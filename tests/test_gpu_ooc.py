@@ -54,13 +54,20 @@ def test_prune_windowed_padding_and_errors(ctx):
 
 
 @pytest.mark.parametrize("N,K,hub,budget", [(60000, 32, True, 2_000_000), (30000, 16, False, 600_000),
-                                            (5000, 48, True, 1_500_000), (100000, 32, False, 0)])
+                                            (5000, 48, True, 1_500_000), (100000, 32, False, 0),
+                                            (40000, 32, "spread", 1_000_000)])
 def test_reverse_merge_chunked_equals_resident(ctx, N, K, hub, budget):
+    """Hubs send a destination chunk more edges than its share of the budget:
+    one row with 10 % of all edges (merged alone), or 30 % of the edges over
+    the first 2,000 rows (merged in row ranges that fit)."""
     rng = np.random.default_rng(N + K)
     F = rng.integers(0, N, size=(N, K)).astype(np.uint32)
-    if hub:
+    if hub == "spread":
+        sel = rng.random((N, K)) < 0.3
+        F[sel] = rng.integers(0, 2000, size=int(sel.sum())).astype(np.uint32)
+    elif hub:
         F[rng.random((N, K)) < 0.1] = 7
-    print(f"chunked merge N={N} K={K} budget={budget}", flush=True)
+    print(f"chunked merge N={N} K={K} hub={hub} budget={budget}", flush=True)
     np.testing.assert_array_equal(ctx.reverse_merge_chunked(F, budget), ctx.reverse_merge(F))
 
 
