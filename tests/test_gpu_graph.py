@@ -158,6 +158,17 @@ def test_reverse_merge_superbin_path_forced(ctx):
             _assert_rows_equal(ctx.reverse_merge(F), O.reverse_merge(F), F)
 
 
+@pytest.mark.parametrize("K", [8, 32])
+def test_reverse_merge_default_beyond_2_21_rows(ctx, K):
+    # graphs beyond 2^21 rows take the superbin path by default (C5's shape
+    # at K 32, 2.2 M rows), checked against the oracle
+    rng = np.random.default_rng(K)
+    N = 2_200_000
+    F = rng.integers(0, N, size=(N, K)).astype(np.uint32)
+    print(f"default path N={N} K={K}", flush=True)
+    _assert_rows_equal(ctx.reverse_merge(F), O.reverse_merge(F), F)
+
+
 def test_reverse_merge_binned_path(ctx):
     """The binned merge through global grouping (graphs between the two-kernel
     merge's 2^11 * 8192 rows and 2^26), forced by revmerge_path='binned'."""
