@@ -54,7 +54,7 @@ class DebugOpts(C.Structure):
         ("knn_collect", C.c_int32), ("revmerge_path", C.c_int32), ("sub_order", C.c_int32),
         ("lloyd_host_csr", C.c_int32), ("prune_flat_rows", C.c_int32), ("knn_stats", C.c_int32),
         ("knn_prune", C.c_int32), ("bucket_host_csr", C.c_int32), ("knn_resident", C.c_int32),
-        ("knn_window", C.c_int32),
+        ("knn_window", C.c_int32), ("knn_screen", C.c_int32),
     ]
 
 
@@ -291,8 +291,8 @@ class Context:
         Keywords: knn_collect (bool), revmerge_path ('auto'|'rv'|'binned'|'csr'|'rv2'),
         sub_order (bool), lloyd_host_csr (bool), prune_flat_rows (bool),
         knn_stats (bool), knn_prune (bool), bucket_host_csr (bool),
-        knn_resident (bool), knn_window (even tiles, 0 = by size).  No
-        keywords: the defaults."""
+        knn_resident (bool), knn_window (even tiles, 0 = by size),
+        knn_screen (bool).  No keywords: the defaults."""
         o = DebugOpts()
         lib().gt_debug_opts_default(C.byref(o))
         for k, v in opts.items():

@@ -240,8 +240,9 @@ typedef struct gt_build_stats {
     int64_t knn_int8;       /* 1: the rounds ran on the int8 matrix cores (integer-typed rows, or
                                integer-valued float rows with int_exact), 0: fp32 */
     int64_t ooc_chunks;     /* device chunks of an out-of-core build (0: resident) */
-    double knn_pairs_computed; /* pairs the distance kernels computed: knn_pairs less the pool chunks
-                               the exact pruning skipped */
+    double knn_pairs_computed; /* pairs the exact distance kernels computed: knn_pairs less the pool
+                               chunks the exact pruning skipped and the pool rows the bf16 screen
+                               dropped (the screen itself computes every pair) */
 } gt_build_stats;
 
 void gt_build_params_default(gt_build_params* p);
@@ -378,6 +379,10 @@ typedef struct gt_debug_opts {
                                 staged-pool kernel */
     int32_t knn_window;      /* tiles of 32 pool rows in the unseeded collect pass's threshold window
                                 (2..32, even); 0 (default): 32 on builds of 2^22 rows or more, else 16 */
+    int32_t knn_screen;      /* 1: seeded collect passes on fp32 rows (Dp <= 160, pools of at most 32768
+                                rows) scan each work item's pool on the bf16 matrix cores first and run
+                                the fp32 pass over the rows that can reach a list (same tables bit for
+                                bit); 0: the fp32 pass over every pool row */
 } gt_debug_opts;
 
 void gt_debug_opts_default(gt_debug_opts* o);
