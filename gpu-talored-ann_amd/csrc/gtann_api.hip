@@ -36,11 +36,12 @@ bool resident_supported(const KnnArgs& a, int64_t np);
 void launch_knn_resident(const KnnArgs& a, int64_t nq, int64_t np, hipStream_t stream);
 // screen_kernels.hip
 bool screen_supported(int Dp, int64_t max_pool);
-void launch_screen_bf16(const float* X, int64_t N, int Dp, uint16_t* Xb, hipStream_t s);
+void launch_screen_prepare(const float* X, const float* nrm, int64_t N, int Dp, unsigned int* sq, uint16_t* Xh,
+                           hipStream_t s);
 void launch_screen(const WorkItem* items, int n_items, const int64_t* ubase, const int32_t* q_rows,
-                   const int32_t* p_rows, const uint16_t* Xb, const float* nrm, int Dp, int metric,
-                   const float* seed_d, int seed_ld, int32_t* union_rows, WorkItem* items_out,
-                   unsigned long long* pairs_done, hipStream_t s);
+                   const int32_t* p_rows, const uint16_t* Xb, const float* nrm, const unsigned int* sq, int Dp,
+                   int metric, const float* seed_d, int seed_ld, int M, int wtiles, float* tq, int32_t* union_rows,
+                   WorkItem* items_out, unsigned long long* pairs_done, hipStream_t s);
 // graph_kernels.hip
 void launch_pad_convert(const void* src, int dtype, float* dst, int64_t N, int D, int Dp, hipStream_t s);
 void launch_row_norms(const float* X, int64_t N, int Dp, float* norms, hipStream_t s);
@@ -271,7 +272,7 @@ enum Ws {
     W_OOC_A, W_OOC_B, W_OOC_C, W_OOC_D, W_OOC_E, W_OOC_F, W_OOC_G, W_CR, W_CRNORMS,
     W_KM_TRAIN, W_KM_MIND, W_KM_FLAG, W_KM_SEL, W_KM_POS, W_KM_SUMS, W_KM_NEW, W_KM_PSI, W_KM_P, W_KM_PN, W_KM_P8,
     W_KM_PN8, W_KM_OI, W_KM_OD, W_CH8, W_CHN, W_CHR, W_CHCNT, W_PAIRS, W_TOP2A, W_TOP2B, W_BUCKETD, W_KEY2,
-    W_BYKEY, W_BKTD, W_BOFF, W_SUBPOS, W_TOP2H, W_RV1, W_RV1M, W_XB, W_UBASE, W_UROWS, W_UITEMS, W_COUNT_
+    W_BYKEY, W_BKTD, W_BOFF, W_SUBPOS, W_TOP2H, W_RV1, W_RV1M, W_XB, W_UBASE, W_UROWS, W_UITEMS, W_TQ, W_SQ, W_COUNT_
 };
 static_assert(W_COUNT_ <= 112, "workspace slots");
 
@@ -1083,9 +1084,10 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
     // and so do a block's 128 queries: small spheres, few chunks needed)
     const bool want_prune = metric == GT_METRIC_L2 && X.data8 && c.c->dbg.knn_prune != 0 && c.c->dbg.knn_collect != 0 &&
                             (X.Dp8 == 32 || X.Dp8 == 64 || X.Dp8 == 128 || X.Dp8 == 256);
-    // and for seeded passes the bf16 screen cuts (each work item's union of
-    // candidate rows is then a few sub-clusters, not the whole pool)
-    const bool want_screen = seed_d && c.c->dbg.knn_screen != 0 && c.c->dbg.knn_collect != 0 && !use_i8(X, X, metric);
+    // and for seeded passes the fp16 screen cuts (each work item's union of
+    // candidate rows is then a few sub-clusters, not the whole pool; the
+    // unseeded pass is sub-ordered either way)
+    const bool want_screen = c.c->dbg.knn_screen != 0 && c.c->dbg.knn_collect != 0 && !use_i8(X, X, metric);
     const bool sub_ordered = own && !compact && c.c->dbg.sub_order != 0 && (!seed_d || want_prune || want_screen);
     if (sub_ordered) sub_order_members(c, X, b, metric, d_members);
     CopyTaskH* d_tasks = c.ws<CopyTaskH>(W_TASKS, tasks.size());
@@ -1164,16 +1166,23 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
         }
     }
     if (merged) *merged = a.run_ids != nullptr;
-    // bf16 screen of a seeded pass on fp32 rows: each work item's pool cut
-    // to the rows whose bf16 key, less a bound on its gap to the fp32 key,
-    // is at or below some query's running M-th distance (a superset of the
-    // rows the fp32 pass keeps, so its lists are unchanged); the fp32 pass
-    // then scans each item's union (items and pool list replaced)
-    bool screen = collect && a.Xq && !a.Xq8 && seed_d && c.c->dbg.knn_screen != 0 && screen_supported(a.Dp, mp);
+    // the unseeded pass's threshold window: 32 tiles on large builds (C5:
+    // 423 -> about 200 keys per query, kNN 97 -> 80 ms), 16 below (C2: 32
+    // tiles take 0.14 ms more than the 23 % fewer keys save)
+    a.window_tiles = c.c->dbg.knn_window > 0 ? c.c->dbg.knn_window : X.N >= (int64_t(1) << 22) ? 32 : 16;
+    // fp16 screen on fp32 rows: each work item's pool cut to the rows whose
+    // fp16 key, less a bound on its gap to the fp32 key, is at or below some
+    // query's threshold -- the running M-th distance of a seeded pass, else
+    // a bound on the pool's M-th smallest key from the screen's own window
+    // -- a superset of the rows the fp32 pass keeps, so its lists are
+    // unchanged; the fp32 pass then scans each item's union (items and pool
+    // list replaced), an unseeded one seeded with the screen's bounds
+    bool screen = collect && a.Xq && !a.Xq8 && c.c->dbg.knn_screen != 0 && screen_supported(a.Dp, mp);
     int64_t* d_ubase = nullptr;
     int32_t* d_urows = nullptr;
     WorkItem* d_uitems = nullptr;
     uint16_t* d_xb = nullptr;
+    float* d_tq = nullptr;
     if (screen) {
         std::vector<int64_t> ub(items.size(), 0);
         int64_t u = 0;
@@ -1190,12 +1199,13 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
             d_xb = c.ws<uint16_t>(W_XB, static_cast<size_t>(N) * X.Dp);
             a.items = d_uitems;
             a.p_rows = d_urows;
+            if (!seed_d) {
+                d_tq = c.ws<float>(W_TQ, static_cast<size_t>(std::max<int64_t>(rows, 1)));
+                a.seed_d = d_tq;
+                a.seed_ld = 1;
+            }
         }
     }
-    // the unseeded pass's threshold window: 32 tiles on large builds (C5:
-    // 423 -> about 200 keys per query, kNN 97 -> 80 ms), 16 below (C2: 32
-    // tiles take 0.14 ms more than the 23 % fewer keys save)
-    a.window_tiles = c.c->dbg.knn_window > 0 ? c.c->dbg.knn_window : X.N >= (int64_t(1) << 22) ? 32 : 16;
     // exact chunk pruning (int8 rows, L2): the centre and radius of every
     // kChunkRows rows of the pool list
     const bool prune = collect && a.Xq8 && a.Xp8 && metric == GT_METRIC_L2 && c.c->dbg.knn_prune != 0 &&
@@ -1222,9 +1232,10 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
             launch_chunk_bounds(X.data8, X.Dp8, d_pool, d_chcnt, nchunk, const_cast<int8_t*>(a.ch8),
                                 const_cast<float*>(a.chn), const_cast<float*>(a.chr), c.s);
         if (screen) {
-            launch_screen_bf16(X.data, N, X.Dp, d_xb, c.s);
-            launch_screen(d_items, a.n_items, d_ubase, d_members, d_pool, d_xb, X.norms, X.Dp, metric, seed_d, M,
-                          d_urows, d_uitems, a.pairs_done, c.s);
+            unsigned int* d_sq = c.ws<unsigned int>(W_SQ, 1);
+            launch_screen_prepare(X.data, X.norms, N, X.Dp, d_sq, d_xb, c.s);
+            launch_screen(d_items, a.n_items, d_ubase, d_members, d_pool, d_xb, X.norms, d_sq, X.Dp, metric, seed_d, M, M,
+                          a.window_tiles, d_tq, d_urows, d_uitems, a.pairs_done, c.s);
         }
         if (collect) launch_knn_collect_select(a, rows, c.s);
         else launch_knn_fused(a, c.s);

@@ -1,90 +1,137 @@
-// screen_kernels.hip -- bf16 screen ahead of a seeded fp32 collect pass.
+// screen_kernels.hip -- fp16 screen ahead of an fp32 collect pass.
 //
-// A seeded pass over fp32 rows collects, for every query q of a 128-query
-// work item, the keys of the item's pool at or below q's running M-th
-// distance T_q, then selects and merges them (knn_f32_collect_kernel).  The
-// screen computes every (q, p) pair of the item on the bf16 matrix cores
-// (v_mfma_f32_32x32x16_bf16: rows rounded to bf16, fp32 sums) and keeps the
-// pool rows p whose bf16 key minus a rigorous bound e(q, p) is at most T_q
-// for some query of the item.  e bounds the gap between the bf16 key and the
-// fp32 path's key, so every row whose fp32 key is at or below T_q is kept;
-// the union of kept rows, in pool order, becomes the item's pool for the fp32
-// collect pass, which therefore collects exactly the keys the full pool would
-// give it (its keys are per pair and ordered by (key, id), so neither the
-// rows it no longer visits nor the visiting order change a list): the merged
-// table is the unscreened pass's bit for bit.
+// A collect pass over fp32 rows collects, for every query q of a 128-query
+// work item, the keys of the item's pool at or below a threshold T_q (the
+// running M-th distance of a seeded pass), then selects the M smallest
+// (knn_f32_collect_kernel).  The screen computes every (q, p) pair of the
+// item on the fp16 matrix cores (v_mfma_f32_32x32x16_f16: rows scaled by one
+// power of two 2^k for the whole matrix, rounded to fp16, fp32 sums) and
+// keeps the pool rows p whose fp16 key minus a rigorous bound e(q, p) on its
+// gap to the fp32 path's key is at most T_q for some query of the item: every
+// row whose fp32 key is at or below T_q is kept.  The union of kept rows, in
+// pool order, becomes the item's pool for the fp32 collect pass, which
+// therefore collects exactly the keys the full pool would give it (its keys
+// are per pair and ordered by (key, id), so neither the rows it no longer
+// visits nor the visiting order change a list).  An unseeded pass first
+// bounds each query's M-th smallest fp32 key from above with fp16 keys plus e
+// over the item's first tiles (the window) and is then screened and collected
+// against that bound: the lists are the unscreened pass's bit for bit.
 //
-// The bound.  S = sum_i |q_i p_i| <= |q| |p| (Cauchy-Schwarz).  Rounding a
-// row to bf16 moves each element by at most 2^-8 of itself, so a product of
-// two rounded elements is within (2^-7 + 2^-16) of the exact one; the bf16
-// products are exact in fp32, and either path's fp32 sums over D <= 160 terms
-// (in any order, each add within 2^-23 of its result: truncating adds
-// included) add at most D 2^-23 (1 + 2^-7) S < 2^-15.6 S each.  The two dot
-// products thus differ by less than (2^-7 + 2^-14) S < c S with
-// c = 2^-7 + 2^-11, which leaves 2^-12 S for matrix-core sums coarser than
-// that.  The fp32 key's own roundings
-// (|q|^2 + |p|^2 then one fma, results of at most 2 (|q|^2 + |p|^2)) and the
-// roundings of the screen's test below add less than 2^-19 (|q|^2 + |p|^2) for
-// L2; 2^-60 absolute covers flushed denormal products.
-//   L2 (key |q|^2 + |p|^2 - 2 q.p):  e = 2 c |q||p| + 2^-19 (|q|^2 + |p|^2)
-//   IP (key -q.p):                    e = (c + 2^-19) |q||p|
+// The scale: k = 15 - E with max_x |x| < 2^E, so every scaled element is
+// below 2^15 (fp16's largest finite value is 65504); products of fp16 values
+// are exact in fp32 and scaled dot products stay below 2^38.  Keys and norms
+// scale by 4^k and 2^k exactly (powers of two) except where they underflow.
+//
+// The bound, in scaled units.  S = sum_i |q_i p_i| <= |q| |p|
+// (Cauchy-Schwarz).  Rounding to fp16 moves an element by at most 2^-11 of
+// itself plus 2^-14 (subnormals, flushed or not), so
+//   |sum q~_i p~_i - sum q_i p_i| <= (2^-10 + 2^-22) S + 2^-14 (1 + 2^-11) (|q|_1 + |p|_1) + D 2^-28
+// with |x|_1 <= sqrt(D) |x| < 16 |x| (D <= 160): below
+// (2^-10 + 2^-22) S + 2^-10 (|q| + |p|) + 2^-20.  Either path's fp32 sums
+// over D terms (in any order, each add within 2^-23 of its result, truncating
+// adds included) add at most D 2^-23 (1 + 2^-10) S < 2^-15.6 S each, so the
+// dot products differ by less than c S + 2^-10 (|q| + |p|) + 2^-20 with
+// c = 2^-10 + 2^-12 (which leaves 2^-12.6 S for matrix-core sums coarser than
+// that).  The fp32 key's own roundings (|q|^2 + |p|^2, then one fma; results
+// of at most 2 (|q|^2 + |p|^2)) and the roundings of the tests below add less
+// than R (|q|^2 + |p|^2), R = 2^-19 (L2).  With d the fp16 dot, A = 2^-20:
+//   L2 (key |q|^2 + |p|^2 - 2 q.p):  e = 2 c |q||p| + 2^-9 (|q| + |p|) + R (|q|^2 + |p|^2) + A
+//   IP (key -q.p):                    e = (c + R) |q||p| + 2^-10 (|q| + |p|) + A
 // |x| is sqrt of the fp32 |x|^2 both paths use (within 2^-23 relative of the
-// true norm, far inside the 2^-11 spare of c).  The test "bf16 key - e <= T"
-// is evaluated as
-//   L2: fma(2, d, fma(2 c |q|, |p|, -(1 - 2^-19) |p|^2)) >= (1 - 2^-19) |q|^2 - T - 2^-60
-//   IP: fma((c + 2^-19) |q|, |p|, d)                      >= -T - 2^-60
-// (d the bf16 dot): two and one vector instructions per pair before the
-// compare, the pool row's two terms staged with its bf16 row.  T = +inf
-// keeps every row.
-#include "gtann_common.hpp"
+// true norm, inside the spare of c).  "fp16 key - e <= T" is evaluated as
+//   L2: fma(2, d, fma(cq, |p|, -(1 - R) |p|^2)) >= (1 - R) |q|^2 - T - A - 2^-9 |q|,   cq = 2 c |q| + 2^-9
+//   IP: fma(cq, |p|, d)                         >= -T - A - 2^-10 |q|,                 cq = (c + R) |q| + 2^-10
+// (two and one vector instructions per pair before the compare), and the
+// window's upper bound "fp16 key + e" as
+//   L2: fma(-2, d, fma(cq, |p|, (1 + R) |p|^2 + (1 + R) |q|^2 + A + 2^-9 |q|))
+//   IP: fma(cq, |p|, A + 2^-10 |q| - d).
+// T = +inf keeps every row; a matrix whose largest norm is not finite or
+// needs |k| > 60 is not screened (every row kept, every window bound +inf).
+#include "knn_device.hpp"
 
 #include <algorithm>
 
 namespace gtann {
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 halfx8 __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int kScreenMaxPool = 32768;   // pool rows an item's LDS bitmap covers
-constexpr float kScreenC = 0x1p-7f + 0x1p-11f;
+constexpr float kScreenC = 0x1p-10f + 0x1p-12f;
 constexpr float kScreenR = 0x1p-19f;
-constexpr float kScreenA = 0x1p-60f;
+constexpr float kScreenA = 0x1p-20f;
+constexpr float kScreenD = 0x1p-10f;   // the subnormal term's factor (per metric: x2 for L2)
+constexpr float kScreenAOut = 0x1p-60f;   // added to a window bound returned unscaled
 
-// fp32 rows (stride Dp) -> bf16 rows (stride Dp), rounded to nearest even
-__global__ void __launch_bounds__(256) screen_bf16_kernel(const float4* __restrict__ X, int64_t n4,
-                                                         uint2* __restrict__ Xb)
+// max over rows of |x|^2 (non-negative floats order as their bit patterns)
+__global__ void __launch_bounds__(256) screen_norm_max_kernel(const float* __restrict__ nrm, int64_t N,
+                                                             unsigned int* __restrict__ out)
 {
+    unsigned int m = 0u;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < N;
+         i += static_cast<int64_t>(gridDim.x) * 256) {
+        const float v = nrm[i];
+        m = max(m, v >= 0.f ? __float_as_uint(v) : 0x7F800000u);   // NaN: not finite
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = max(m, static_cast<unsigned int>(__shfl_xor(static_cast<int>(m), o)));
+    if ((threadIdx.x & 63) == 0) atomicMax(out, m);
+}
+
+// The scale exponent k from the largest |x|^2 (scale[0] = k, scale[1] = 1
+// when the matrix cannot be screened).
+__device__ __forceinline__ void screen_scale(const unsigned int* sq, int& k, bool& off)
+{
+    const float n2 = __uint_as_float(*sq);
+    off = !(n2 < INFINITY);
+    int E = 0;
+    if (!off && n2 > 0.f) {
+        frexpf(sqrtf(n2) * 1.0000002f, &E);   // max |x| < 2^E (the factor: sqrt's rounding)
+    }
+    k = 15 - E;
+    if (k < -60 || k > 60) off = true;
+    if (off) k = 0;
+}
+
+// fp32 rows (stride Dp) -> 2^k-scaled fp16 rows (stride Dp), round to nearest even
+__global__ void __launch_bounds__(256) screen_f16_kernel(const float4* __restrict__ X, int64_t n4,
+                                                        const unsigned int* __restrict__ sq, uint2* __restrict__ Xh)
+{
+    int k;
+    bool off;
+    screen_scale(sq, k, off);
+    const float sc = ldexpf(1.f, k);
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n4;
          i += static_cast<int64_t>(gridDim.x) * 256) {
         const float4 v = X[i];
-        const float f[4] = {v.x, v.y, v.z, v.w};
-        uint32_t o[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const uint32_t u = __float_as_uint(f[e]);
-            o[e] = (u & 0x7FFFFFFFu) > 0x7F800000u ? ((u >> 16) | 0x40u)   // NaN stays NaN
-                                                   : (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
-        }
-        Xb[i] = make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
+        const _Float16 h0 = static_cast<_Float16>(off ? 0.f : v.x * sc);
+        const _Float16 h1 = static_cast<_Float16>(off ? 0.f : v.y * sc);
+        const _Float16 h2 = static_cast<_Float16>(off ? 0.f : v.z * sc);
+        const _Float16 h3 = static_cast<_Float16>(off ? 0.f : v.w * sc);
+        const uint32_t b0 = __builtin_bit_cast(uint16_t, h0), b1 = __builtin_bit_cast(uint16_t, h1);
+        const uint32_t b2 = __builtin_bit_cast(uint16_t, h2), b3 = __builtin_bit_cast(uint16_t, h3);
+        Xh[i] = make_uint2(b0 | (b1 << 16), b2 | (b3 << 16));
     }
 }
 
 // One block per work item (4 waves of 32 queries; lanes j and j + 32 hold
 // query j's dims 16 s + 8 h + [0, 8) of step s, h = lane / 32).  Pool tiles
 // of 32 rows are staged through LDS, double buffered (the next tile's loads
-// in flight during a tile's MFMAs).  With the queries as the MFMA's rows, a
-// tile's accumulator element 4 g + e of lane (j, h) is pool row j against
-// query 8 g + 4 h + e; the 16 compares' lane masks OR into the tile's
-// admitted rows (bit j from lanes j and j + 32), which each wave ORs into
-// word t of the item's LDS bitmap; the set bits, in pool order, become the
-// item's union at union_rows[ubase[item] ...).
-template <int DP, int METRIC>
+// in flight during a tile's MFMAs).  In the admission scan the queries are
+// the MFMA's rows: a tile's accumulator element 4 g + e of lane (j, h) is pool
+// row j against query 8 g + 4 h + e; the 16 compares' lane masks OR into the
+// tile's admitted rows (bit j from lanes j and j + 32), which each wave ORs
+// into word t of the item's LDS bitmap; the set bits, in pool order, become
+// the item's union at union_rows[ubase[item] ...).
+template <int DP, int METRIC, bool WINDOW>
 __global__ void __launch_bounds__(256) knn_screen_kernel(const WorkItem* __restrict__ items,
                                                          const int64_t* __restrict__ ubase,
                                                          const int32_t* __restrict__ q_rows,
                                                          const int32_t* __restrict__ p_rows,
                                                          const uint16_t* __restrict__ Xb, const float* __restrict__ nrm,
-                                                         const float* __restrict__ seed_d, int seed_ld,
+                                                         const unsigned int* __restrict__ sq,
+                                                         const float* __restrict__ seed_d, int seed_ld, int M,
+                                                         int wtiles, float* __restrict__ tq,
                                                          int32_t* __restrict__ union_rows,
                                                          WorkItem* __restrict__ items_out,
                                                          unsigned long long* __restrict__ pairs_done)
@@ -97,8 +144,10 @@ __global__ void __launch_bounds__(256) knn_screen_kernel(const WorkItem* __restr
     constexpr int WPT = kScreenMaxPool / 32 / 256;   // bitmap words per thread in the compaction
     static_assert(DP % 16 == 0 && kPoolTile == 32, "bf16 steps of 16 dims, one bitmap word per tile");
     __shared__ __align__(16) uint16_t tile[2][kPoolTile][RS];
-    __shared__ float tpr[2][kPoolTile];   // |p|
-    __shared__ float tpm[2][kPoolTile];   // -(1 - R) |p|^2
+    __shared__ __align__(16) float tpr[2][kPoolTile];   // |p|
+    __shared__ __align__(16) float tpm[2][kPoolTile];   // -(1 - R) |p|^2
+    __shared__ __align__(16) float tpu[2][kPoolTile];   // (1 + R) |p|^2
+    __shared__ __align__(16) int32_t trow[2][kPoolTile];   // row id, -1 past the pool's end
     __shared__ uint32_t bits[kScreenMaxPool / 32];
     __shared__ uint32_t wsum[kWaves];
 
@@ -106,27 +155,160 @@ __global__ void __launch_bounds__(256) knn_screen_kernel(const WorkItem* __restr
     const WorkItem it = items[item_idx];
     const int tid = threadIdx.x;
     if (it.q_count <= 0) {   // padding
-        if (tid == 0) items_out[item_idx] = it;
+        if (!WINDOW && tid == 0) items_out[item_idx] = it;
         return;
     }
     const int w = tid >> 6, lane = tid & 63, j = lane & 31, h = lane >> 5;
     const int pc = it.p_count;
     const int ntiles = (pc + kPoolTile - 1) / kPoolTile;
-    for (int i = tid; i < ntiles; i += 256) bits[i] = 0u;
+    if (!WINDOW)
+        for (int i = tid; i < ntiles; i += 256) bits[i] = 0u;
 
     const int qlocal = w * kQueriesPerWave + j;
     const bool qvalid = qlocal < it.q_count;
     const int64_t qi = it.q_begin + qlocal;
     const int32_t qrow = qvalid ? (q_rows ? q_rows[qi] : static_cast<int32_t>(qi)) : 0;
-    const int64_t orow_seed = it.out_base >= 0 ? it.out_base + qlocal : static_cast<int64_t>(qrow);
-    const float T = qvalid ? seed_d[orow_seed * seed_ld + seed_ld - 1] : 0.f;
-    const float qn = nrm[qrow];
-    const float qr = sqrtf(qn);
-    const float cq = METRIC == 0 ? 2.f * kScreenC * qr : (kScreenC + kScreenR) * qr;
+    const int64_t orow = it.out_base >= 0 ? it.out_base + qlocal : static_cast<int64_t>(qrow);
+    int k;
+    bool unscreened;   // the matrix's scale is out of range: every row kept
+    screen_scale(sq, k, unscreened);
+    const float s1 = ldexpf(1.f, k), s2 = ldexpf(1.f, 2 * k);   // exact powers of two
+    const float qn = nrm[qrow] * s2;
+    const float qr = sqrtf(nrm[qrow]) * s1;
+    constexpr float kD = METRIC == 0 ? 2.f * kScreenD : kScreenD;
+    const float cq = METRIC == 0 ? fmaf(2.f * kScreenC, qr, kD) : fmaf(kScreenC + kScreenR, qr, kD);
+    halfx8 qf[KS];
+    {
+        const uint4* src = reinterpret_cast<const uint4*>(Xb + static_cast<int64_t>(qrow) * DP + 8 * h);
+#pragma unroll
+        for (int s = 0; s < KS; ++s) qf[s] = __builtin_bit_cast(halfx8, src[2 * s]);
+    }
+
+    // pool tile t: positions rot + 32 t + r (mod pc) for 32 t + r < pc
+    // A three-stage pipeline per tile: row ids (one tile ahead of the row
+    // loads, so the row loads never wait on an id load) -> rows and norms in
+    // registers (one tile ahead) -> LDS.  fetch_ids(t) loads tile t's ids;
+    // load_tile() issues the loads of the tile fetch_ids last named;
+    // store_tile(buf) puts them into LDS.
+    int32_t idq[U4_THREAD];   // ids of the next tile's 16-byte pieces (-1: none)
+    int32_t ridq = -1, ridc = -1;   // threads < 32: the id of the next tile's row tid, of the loaded tile's
+    float pnc = 0.f;
+    uint4 pre[U4_THREAD];
+    auto pos_row = [&](int t, int r, int rot) __attribute__((always_inline)) -> int32_t {
+        int p = t * kPoolTile + r;
+        if (p >= pc) return -1;
+        p += rot;
+        if (p >= pc) p -= pc;
+        return p_rows[it.p_begin + p];
+    };
+    auto fetch_ids = [&](int t, int rot) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < U4_THREAD; ++u) {
+            const int e = tid + 256 * u;
+            idq[u] = e < U4_TILE ? pos_row(t, e / U4_ROW, rot) : -1;
+        }
+        if (tid < kPoolTile) ridq = pos_row(t, tid, rot);
+    };
+    auto load_tile = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < U4_THREAD; ++u) {
+            const int e = tid + 256 * u;
+            pre[u] = idq[u] >= 0 ? reinterpret_cast<const uint4*>(Xb + static_cast<int64_t>(idq[u]) * DP)[e % U4_ROW]
+                                 : make_uint4(0u, 0u, 0u, 0u);
+        }
+        if (tid < kPoolTile) {
+            ridc = ridq;
+            pnc = ridq >= 0 ? nrm[ridq] : 0.f;
+        }
+    };
+    auto store_tile = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < U4_THREAD; ++u) {
+            const int e = tid + 256 * u;
+            if (e < U4_TILE) *reinterpret_cast<uint4*>(&tile[buf][e / U4_ROW][8 * (e % U4_ROW)]) = pre[u];
+        }
+        if (tid < kPoolTile) {
+            tpr[buf][tid] = sqrtf(pnc) * s1;
+            tpm[buf][tid] = -(1.f - kScreenR) * (pnc * s2);
+            tpu[buf][tid] = (1.f + kScreenR) * (pnc * s2);
+            trow[buf][tid] = ridc;
+        }
+    };
+
+    // WINDOW: an upper bound on the M-th smallest fp32 key of the pool from
+    // its first wtiles tiles (from the item's rotation), to tq: each lane
+    // keeps the 32 smallest bounds ub = bf16 key + e >= fp32 key of the rows
+    // it holds (a sorting network on registers), and the larger of the pair's
+    // ceil(M/2)-th smallest bounds ceil(M/2) rows of each lane from above: M
+    // distinct rows, the query itself excluded (+inf if the window has fewer).
+    // Else the admission scan against the query's threshold seed_d (the
+    // running M-th distance, or such a bound; +inf keeps every row).
+    if constexpr (WINDOW) {
+        const float qk = METRIC == 0 ? fmaf(kD, qr, (1.f + kScreenR) * qn + kScreenA) : fmaf(kD, qr, kScreenA);
+        float L[32];
+#pragma unroll
+        for (int i = 0; i < 32; ++i) L[i] = INFINITY;
+        const int nwt = min(wtiles, ntiles);
+        if (nwt > 0) {
+            fetch_ids(0, it.p_rot);
+            load_tile();
+            if (nwt > 1) fetch_ids(1, it.p_rot);
+            store_tile(0);
+        }
+        __syncthreads();
+        for (int t = 0; t < nwt; ++t) {
+            const int buf = t & 1;
+            if (t + 1 < nwt) load_tile();
+            if (t + 2 < nwt) fetch_ids(t + 2, it.p_rot);
+            floatx16 acc;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+            // pool rows as A, queries as B: element 4 g + e of lane (j, h)
+            // is pool row 8 g + 4 h + e against query j
+            const uint16_t* arow = &tile[buf][j][8 * h];
+#pragma unroll
+            for (int s = 0; s < KS; ++s) {
+                const halfx8 av = __builtin_bit_cast(halfx8, *reinterpret_cast<const uint4*>(arow + 16 * s));
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, qf[s], acc, 0, 0, 0);
+            }
+            float ub[16];
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const float4 r4 = *reinterpret_cast<const float4*>(&tpr[buf][8 * g + 4 * h]);
+                const float4 u4 = *reinterpret_cast<const float4*>(&tpu[buf][8 * g + 4 * h]);
+                const int4 i4 = *reinterpret_cast<const int4*>(&trow[buf][8 * g + 4 * h]);
+                const float pr[4] = {r4.x, r4.y, r4.z, r4.w}, pu[4] = {u4.x, u4.y, u4.z, u4.w};
+                const int32_t id[4] = {i4.x, i4.y, i4.z, i4.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float d = acc[4 * g + e];
+                    const float v = METRIC == 0 ? fmaf(-2.f, d, fmaf(cq, pr[e], pu[e] + qk)) : fmaf(cq, pr[e], qk - d);
+                    ub[4 * g + e] = (id[e] < 0 || id[e] == qrow || !(v < INFINITY)) ? INFINITY : v;   // NaN: no bound
+                }
+            }
+            oddeven_sort(ub);
+#pragma unroll
+            for (int k = 0; k < 16; ++k) L[16 + k] = fminf(L[16 + k], ub[15 - k]);
+            bitonic_merge(L);
+            if (t + 1 < nwt) store_tile(buf ^ 1);
+            __syncthreads();
+        }
+        const int m = (M + 1) / 2 - 1;
+        float v = L[0];
+#pragma unroll
+        for (int i = 1; i < 32; ++i) v = i == m ? L[i] : v;
+        v = fmaxf(v, __shfl_xor(v, 32));
+        // unscaled (exact but for underflow, which the added 2^-60 covers)
+        if (qvalid && h == 0) tq[orow] = unscreened ? INFINITY : fmaf(v, ldexpf(1.f, -2 * k), kScreenAOut);
+        return;
+    }
+    const float T = qvalid ? (unscreened ? INFINITY : seed_d[orow * seed_ld + seed_ld - 1] * s2) : 0.f;
     // an invalid query admits nothing (y >= +inf fails for every finite y)
-    const float qa = !qvalid ? INFINITY : METRIC == 0 ? qn * (1.f - kScreenR) - T - kScreenA : -T - kScreenA;
+    const float qa = !qvalid ? INFINITY
+                     : METRIC == 0 ? fmaf(-kD, qr, qn * (1.f - kScreenR) - T - kScreenA)
+                                   : fmaf(-kD, qr, -T - kScreenA);
     // the constants of the queries this lane's accumulator elements hold
-    // (element 4 g + e: query 8 g + 4 h + e of the wave)
+    // in the admission scan (element 4 g + e: query 8 g + 4 h + e)
     float qa_r[16], cq_r[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -134,49 +316,18 @@ __global__ void __launch_bounds__(256) knn_screen_kernel(const WorkItem* __restr
         qa_r[r] = __shfl(qa, src);
         cq_r[r] = __shfl(cq, src);
     }
-    bf16x8 qf[KS];
-    {
-        const uint4* src = reinterpret_cast<const uint4*>(Xb + static_cast<int64_t>(qrow) * DP + 8 * h);
-#pragma unroll
-        for (int s = 0; s < KS; ++s) qf[s] = __builtin_bit_cast(bf16x8, src[2 * s]);
-    }
 
-    uint4 pre[U4_THREAD];
-    auto load_tile = [&](int t) __attribute__((always_inline)) {
-#pragma unroll
-        for (int u = 0; u < U4_THREAD; ++u) {
-            const int e = tid + 256 * u;
-            pre[u] = make_uint4(0u, 0u, 0u, 0u);
-            if (e < U4_TILE) {
-                const int p = t * kPoolTile + e / U4_ROW;
-                if (p < pc) {
-                    const int32_t row = p_rows[it.p_begin + p];
-                    pre[u] = reinterpret_cast<const uint4*>(Xb + static_cast<int64_t>(row) * DP)[e % U4_ROW];
-                }
-            }
-        }
-    };
-    auto store_tile = [&](int t, int buf) __attribute__((always_inline)) {
-#pragma unroll
-        for (int u = 0; u < U4_THREAD; ++u) {
-            const int e = tid + 256 * u;
-            if (e < U4_TILE) *reinterpret_cast<uint4*>(&tile[buf][e / U4_ROW][8 * (e % U4_ROW)]) = pre[u];
-        }
-        if (tid < kPoolTile) {
-            const int p = t * kPoolTile + tid;
-            const float pn = p < pc ? nrm[p_rows[it.p_begin + p]] : 0.f;
-            tpr[buf][tid] = sqrtf(pn);
-            tpm[buf][tid] = -(1.f - kScreenR) * pn;
-        }
-    };
     if (ntiles > 0) {
-        load_tile(0);
-        store_tile(0, 0);
+        fetch_ids(0, 0);
+        load_tile();
+        if (ntiles > 1) fetch_ids(1, 0);
+        store_tile(0);
     }
     __syncthreads();
     for (int t = 0; t < ntiles; ++t) {
         const int buf = t & 1;
-        if (t + 1 < ntiles) load_tile(t + 1);
+        if (t + 1 < ntiles) load_tile();
+        if (t + 2 < ntiles) fetch_ids(t + 2, 0);
         floatx16 acc;
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[r] = 0.f;
@@ -185,8 +336,8 @@ __global__ void __launch_bounds__(256) knn_screen_kernel(const WorkItem* __restr
         const uint16_t* brow = &tile[buf][j][8 * h];
 #pragma unroll
         for (int s = 0; s < KS; ++s) {
-            const bf16x8 bv = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(brow + 16 * s));
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qf[s], bv, acc, 0, 0, 0);
+            const halfx8 bv = __builtin_bit_cast(halfx8, *reinterpret_cast<const uint4*>(brow + 16 * s));
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(qf[s], bv, acc, 0, 0, 0);
         }
         const float pr = tpr[buf][j], pm = tpm[buf][j];
         uint64_t m = 0u;   // lanes whose pool row some query admits
@@ -199,7 +350,7 @@ __global__ void __launch_bounds__(256) knn_screen_kernel(const WorkItem* __restr
         const int left = pc - t * kPoolTile;
         if (left < kPoolTile) tm &= (1u << left) - 1u;
         if (lane == 0 && tm) atomicOr(&bits[t], tm);
-        if (t + 1 < ntiles) store_tile(t + 1, buf ^ 1);
+        if (t + 1 < ntiles) store_tile(buf ^ 1);
         __syncthreads();
     }
     // the set bits, in order, as row ids
@@ -246,47 +397,67 @@ bool screen_supported(int Dp, int64_t max_pool)
     return (Dp == 32 || Dp == 64 || Dp == 96 || Dp == 128 || Dp == 160) && max_pool <= kScreenMaxPool;
 }
 
-void launch_screen_bf16(const float* X, int64_t N, int Dp, uint16_t* Xb, hipStream_t s)
+// Xh: the 2^k-scaled fp16 copy of X (N rows, stride Dp); sq: one unsigned
+// int of device memory for the scale (written here)
+void launch_screen_prepare(const float* X, const float* nrm, int64_t N, int Dp, unsigned int* sq, uint16_t* Xh,
+                           hipStream_t s)
 {
     GT_REQUIRE(Dp % 4 == 0, "screen: rows of whole float4s");
+    if (N <= 0) return;
+    GT_HIP(hipMemsetAsync(sq, 0, sizeof(unsigned int), s));
+    const unsigned g1 = static_cast<unsigned>(std::min<int64_t>(ceil_div(N, int64_t(256)), 1024));
+    hipLaunchKernelGGL(screen_norm_max_kernel, dim3(g1), dim3(256), 0, s, nrm, N, sq);
+    GT_HIP(hipGetLastError());
     const int64_t n4 = N * Dp / 4;
-    if (n4 <= 0) return;
     const unsigned grid = static_cast<unsigned>(std::min<int64_t>(ceil_div(n4, int64_t(256)), 8192));
-    hipLaunchKernelGGL(screen_bf16_kernel, dim3(grid), dim3(256), 0, s, reinterpret_cast<const float4*>(X), n4,
-                       reinterpret_cast<uint2*>(Xb));
+    hipLaunchKernelGGL(screen_f16_kernel, dim3(grid), dim3(256), 0, s, reinterpret_cast<const float4*>(X), n4, sq,
+                       reinterpret_cast<uint2*>(Xh));
     GT_HIP(hipGetLastError());
 }
 
-// items: n_items work items of a seeded pass (every pool at most
-// kScreenMaxPool rows); ubase[i]: item i's first slot of union_rows, which
-// holds at least its pool count from there; items_out: the items with their
-// unions as pools.  Xb: bf16 rows (stride Dp) of the matrix the q_rows and
-// p_rows index, nrm its fp32 |x|^2.  pairs_done (optional) += the (query,
-// union row) pairs left to the fp32 pass.
+// items: n_items work items of a pass (every pool at most kScreenMaxPool
+// rows); ubase[i]: item i's first slot of union_rows, which holds at least
+// its pool count from there; items_out: the items with their unions as
+// pools.  Xb: the scaled fp16 rows (stride Dp) of the matrix the q_rows and
+// p_rows index, sq its scale (launch_screen_prepare), nrm its fp32 |x|^2.  A seeded pass (seed_d: running tables of
+// seed_ld keys per output row) screens against each row's last key; an
+// unseeded one (M keys wanted, 4 < M <= 64) against a bound from the first
+// wtiles tiles of each item's rotated pool, written to tq (one per output
+// row: the pool's M-th smallest fp32 key is at or below it).  pairs_done
+// (optional) += the (query, union row) pairs left to the fp32 pass.
 void launch_screen(const WorkItem* items, int n_items, const int64_t* ubase, const int32_t* q_rows,
-                   const int32_t* p_rows, const uint16_t* Xb, const float* nrm, int Dp, int metric,
-                   const float* seed_d, int seed_ld, int32_t* union_rows, WorkItem* items_out,
-                   unsigned long long* pairs_done, hipStream_t s)
+                   const int32_t* p_rows, const uint16_t* Xb, const float* nrm, const unsigned int* sq, int Dp,
+                   int metric,
+                   const float* seed_d, int seed_ld, int M, int wtiles, float* tq, int32_t* union_rows,
+                   WorkItem* items_out, unsigned long long* pairs_done, hipStream_t s)
 {
     GT_REQUIRE(screen_supported(Dp, 0), "screen: padded dimension not supported");
-    GT_REQUIRE(seed_d != nullptr && seed_ld > 0, "screen: a seeded pass only");
+    GT_REQUIRE(seed_d ? seed_ld > 0 : (tq && M > 4 && M <= 64 && wtiles > 0), "screen: seed or window missing");
     if (n_items <= 0) return;
-#define GT_SCR(DPV)                                                                                           \
+#define GT_SCR(DPV, MET)                                                                                      \
     do {                                                                                                      \
-        if (metric == 0)                                                                                      \
-            hipLaunchKernelGGL((knn_screen_kernel<DPV, 0>), dim3(n_items), dim3(256), 0, s, items, ubase,     \
-                               q_rows, p_rows, Xb, nrm, seed_d, seed_ld, union_rows, items_out, pairs_done);            \
-        else                                                                                                  \
-            hipLaunchKernelGGL((knn_screen_kernel<DPV, 1>), dim3(n_items), dim3(256), 0, s, items, ubase,     \
-                               q_rows, p_rows, Xb, nrm, seed_d, seed_ld, union_rows, items_out, pairs_done);            \
+        if (!seed_d)                                                                                          \
+            hipLaunchKernelGGL((knn_screen_kernel<DPV, MET, true>), dim3(n_items), dim3(256), 0, s, items,    \
+                               ubase, q_rows, p_rows, Xb, nrm, sq, seed_d, seed_ld, M, wtiles, tq, union_rows,    \
+                               items_out, pairs_done);                                                        \
+        const float* sd = seed_d ? seed_d : tq;                                                               \
+        const int sl = seed_d ? seed_ld : 1;                                                                  \
+        hipLaunchKernelGGL((knn_screen_kernel<DPV, MET, false>), dim3(n_items), dim3(256), 0, s, items, ubase, \
+                           q_rows, p_rows, Xb, nrm, sq, sd, sl, M, wtiles, tq, union_rows, items_out, pairs_done); \
+    } while (0)
+#define GT_SCR_M(DPV)                     \
+    do {                                  \
+        if (metric == 0) GT_SCR(DPV, 0);  \
+        else GT_SCR(DPV, 1);              \
     } while (0)
     switch (Dp) {
-    case 32: GT_SCR(32); break;
-    case 64: GT_SCR(64); break;
-    case 96: GT_SCR(96); break;
-    case 128: GT_SCR(128); break;
-    default: GT_SCR(160); break;
+    case 32: GT_SCR_M(32); break;
+    case 64: GT_SCR_M(64); break;
+    case 96: GT_SCR_M(96); break;
+    case 128: GT_SCR_M(128); break;
+    default: GT_SCR_M(160); break;
     }
+#undef GT_SCR_M
 #undef GT_SCR
     GT_HIP(hipGetLastError());
 }

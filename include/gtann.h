@@ -241,7 +241,7 @@ typedef struct gt_build_stats {
                                integer-valued float rows with int_exact), 0: fp32 */
     int64_t ooc_chunks;     /* device chunks of an out-of-core build (0: resident) */
     double knn_pairs_computed; /* pairs the exact distance kernels computed: knn_pairs less the pool
-                               chunks the exact pruning skipped and the pool rows the bf16 screen
+                               chunks the exact pruning skipped and the pool rows the fp16 screen
                                dropped (the screen itself computes every pair) */
 } gt_build_stats;
 
@@ -379,10 +379,11 @@ typedef struct gt_debug_opts {
                                 staged-pool kernel */
     int32_t knn_window;      /* tiles of 32 pool rows in the unseeded collect pass's threshold window
                                 (2..32, even); 0 (default): 32 on builds of 2^22 rows or more, else 16 */
-    int32_t knn_screen;      /* 1: seeded collect passes on fp32 rows (Dp <= 160, pools of at most 32768
-                                rows) scan each work item's pool on the bf16 matrix cores first and run
-                                the fp32 pass over the rows that can reach a list (same tables bit for
-                                bit); 0: the fp32 pass over every pool row */
+    int32_t knn_screen;      /* 1: collect passes on fp32 rows (Dp <= 160, pools of at most 32768 rows)
+                                scan each work item's pool on the fp16 matrix cores first (an unseeded
+                                pass also bounds its thresholds there) and run the fp32 pass over the
+                                rows that can reach a list (same tables bit for bit); 0: the fp32 pass
+                                over every pool row */
 } gt_debug_opts;
 
 void gt_debug_opts_default(gt_debug_opts* o);

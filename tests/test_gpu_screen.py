@@ -1,12 +1,15 @@
-"""The bf16 screen ahead of seeded fp32 collect passes (knn_screen).
+"""The fp16 screen ahead of fp32 collect passes (knn_screen).
 
-The screen keeps, for each 128-query work item, the pool rows whose bf16
+The screen keeps, for each 128-query work item, the pool rows whose fp16
 key less a rigorous bound on its gap to the fp32 key is at or below some
-query's running M-th distance; the fp32 pass then scans only those rows.
-It must change nothing: every seeded pass here is compared with the
+query's threshold -- the running M-th distance of a seeded pass, or in an
+unseeded pass an upper bound on the pool's M-th smallest fp32 key from the
+screen's own window (fp16 key plus the bound); the fp32 pass then scans only
+those rows.  It must change nothing: every pass here is compared with the
 unscreened pass from the same running table, ids and distance bits equal.
 The cases press on the bound: rows far from the origin (the L2 key's
-cancellation, where the norm term of the bound decides), duplicated rows
+cancellation, where the norm term of the bound decides), rows of tiny and
+of huge scale (the power-of-two scale of the fp16 copy), duplicated rows
 (ties at the threshold), inner products of rows of varied norm, running
 tables with padding (+inf thresholds: every row kept), every padded width
 the screen takes (32 .. 160), and whole builds.  The unscreened passes are
@@ -52,6 +55,10 @@ def _data(kind, n, d, seed):
         X = X[rng.permutation(len(X))]
     elif kind == "scaled":    # rows of norms over three orders of magnitude
         X = X * np.exp(rng.uniform(-3.5, 3.5, size=(n, 1))).astype(np.float32)
+    elif kind == "tiny":      # elements near fp16's subnormals before scaling
+        X = X * np.float32(1e-9)
+    elif kind == "huge":      # elements far beyond fp16's range before scaling
+        X = X * np.float32(1e12)
     return np.ascontiguousarray(X, dtype=np.float32)
 
 
@@ -72,15 +79,16 @@ def _equal(x, y):
     ("dup", 4000, 96, 6, 1, 32, "ip"),
     ("scaled", 4000, 128, 6, 1, 32, "ip"),
     ("scaled", 4000, 64, 6, 1, 32, "l2"),
+    ("tiny", 3000, 96, 5, 1, 32, "l2"),
+    ("huge", 3000, 64, 5, 1, 32, "ip"),
 ])
 def test_screened_passes_equal_unscreened(ctx, kind, N, D, B, P, M, metric):
     X = _data(kind, N, D, seed=N + D + M)
     N = len(X)
     rng = np.random.default_rng(7 * N + M)
     print(f"screen rounds {kind} N={N} D={D} B={B} P={P} M={M} {metric}", flush=True)
-    off, mem = _buckets(rng, N, B)
-    run = ctx.knn_bucketed(X, off, mem, _probe(rng, B, P), M, metric=metric)
-    for r in range(2):
+    run = None   # the first pass unseeded: the screen's own window bound
+    for r in range(3):
         off, mem = _buckets(rng, N, B)
         probe = _probe(rng, B, P)
         with debug_opts(ctx, knn_screen=True):
@@ -99,7 +107,11 @@ def test_screen_with_padded_running_lists(ctx, metric):
     N = len(X)
     rng = np.random.default_rng(12)
     off, mem = _buckets(rng, N, 400)
-    run = ctx.knn_bucketed(X, off, mem, _probe(rng, 400, 0), 32, metric=metric)
+    # unseeded pools of fewer than M rows: the window bound is +inf
+    with debug_opts(ctx, knn_screen=True):
+        run = ctx.knn_bucketed(X, off, mem, _probe(rng, 400, 0), 32, metric=metric)
+    with debug_opts(ctx, knn_screen=False):
+        _equal(run, ctx.knn_bucketed(X, off, mem, _probe(rng, 400, 0), 32, metric=metric))
     assert (run[0] < 0).any()
     off, mem = _buckets(rng, N, 6)
     probe = _probe(rng, 6, 1)
