@@ -1087,7 +1087,16 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
     // and for seeded passes the fp16 screen cuts (each work item's union of
     // candidate rows is then a few sub-clusters, not the whole pool; the
     // unseeded pass is sub-ordered either way)
-    const bool want_screen = c.c->dbg.knn_screen != 0 && c.c->dbg.knn_collect != 0 && !use_i8(X, X, metric);
+    // (knn_screen 1: passes of at least 2^27 pairs, below which its launches
+    // cost more than it saves -- C1's 10^7-pair passes measured 0.1 ms slower
+    // each; 2: every pass it can take)
+    double pairs_all = 0.0;
+    for (int64_t bb = b0; bb < b1; ++bb)
+        pairs_all += static_cast<double>(b.offsets[static_cast<size_t>(bb + 1)] - b.offsets[static_cast<size_t>(bb)]) *
+                     static_cast<double>(pool_cnt[static_cast<size_t>(bb)]);
+    const int scr = c.c->dbg.knn_screen;
+    const bool want_screen = c.c->dbg.knn_collect != 0 && !use_i8(X, X, metric) &&
+                             (scr == 2 || (scr == 1 && pairs_all >= static_cast<double>(int64_t(1) << 27)));
     const bool sub_ordered = own && !compact && c.c->dbg.sub_order != 0 && (!seed_d || want_prune || want_screen);
     if (sub_ordered) sub_order_members(c, X, b, metric, d_members);
     CopyTaskH* d_tasks = c.ws<CopyTaskH>(W_TASKS, tasks.size());
@@ -1177,7 +1186,7 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
     // -- a superset of the rows the fp32 pass keeps, so its lists are
     // unchanged; the fp32 pass then scans each item's union (items and pool
     // list replaced), an unseeded one seeded with the screen's bounds
-    bool screen = collect && a.Xq && !a.Xq8 && c.c->dbg.knn_screen != 0 && screen_supported(a.Dp, mp);
+    bool screen = want_screen && collect && a.Xq && !a.Xq8 && screen_supported(a.Dp, mp);
     int64_t* d_ubase = nullptr;
     int32_t* d_urows = nullptr;
     WorkItem* d_uitems = nullptr;
@@ -2526,6 +2535,7 @@ void gt_debug_opts_default(gt_debug_opts* o)
     o->knn_stats = 0;
     o->knn_prune = 1;
     o->knn_resident = 1;
+    o->knn_screen = 1;
 }
 
 int gt_set_debug(gt_ctx* ctx, const gt_debug_opts* o)

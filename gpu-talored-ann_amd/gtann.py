@@ -292,7 +292,8 @@ class Context:
         sub_order (bool), lloyd_host_csr (bool), prune_flat_rows (bool),
         knn_stats (bool), knn_prune (bool), bucket_host_csr (bool),
         knn_resident (bool), knn_window (even tiles, 0 = by size),
-        knn_screen (bool).  No keywords: the defaults."""
+        knn_screen (0 off, 1 by pass size, 2 always).  No keywords: the
+        defaults."""
         o = DebugOpts()
         lib().gt_debug_opts_default(C.byref(o))
         for k, v in opts.items():

@@ -379,11 +379,12 @@ typedef struct gt_debug_opts {
                                 staged-pool kernel */
     int32_t knn_window;      /* tiles of 32 pool rows in the unseeded collect pass's threshold window
                                 (2..32, even); 0 (default): 32 on builds of 2^22 rows or more, else 16 */
-    int32_t knn_screen;      /* 1: collect passes on fp32 rows (Dp <= 160, pools of at most 32768 rows)
-                                scan each work item's pool on the fp16 matrix cores first (an unseeded
-                                pass also bounds its thresholds there) and run the fp32 pass over the
-                                rows that can reach a list (same tables bit for bit); 0: the fp32 pass
-                                over every pool row */
+    int32_t knn_screen;      /* 1 (default): collect passes on fp32 rows (Dp <= 160, pools of at most
+                                32768 rows) of at least 2^27 (query, pool) pairs scan each work item's
+                                pool on the fp16 matrix cores first (an unseeded pass also bounds its
+                                thresholds there) and run the fp32 pass over the rows that can reach a
+                                list (same tables bit for bit); 2: every such pass, whatever its size;
+                                0: the fp32 pass over every pool row */
 } gt_debug_opts;
 
 void gt_debug_opts_default(gt_debug_opts* o);

@@ -1,4 +1,6 @@
-"""The fp16 screen ahead of fp32 collect passes (knn_screen).
+"""The fp16 screen ahead of fp32 collect passes (knn_screen; forced on
+here with knn_screen=2, which also screens passes below the default's size
+threshold).
 
 The screen keeps, for each 128-query work item, the pool rows whose fp16
 key less a rigorous bound on its gap to the fp32 key is at or below some
@@ -91,9 +93,9 @@ def test_screened_passes_equal_unscreened(ctx, kind, N, D, B, P, M, metric):
     for r in range(3):
         off, mem = _buckets(rng, N, B)
         probe = _probe(rng, B, P)
-        with debug_opts(ctx, knn_screen=True):
+        with debug_opts(ctx, knn_screen=2):
             got = ctx.knn_bucketed(X, off, mem, probe, M, metric=metric, running=run)
-        with debug_opts(ctx, knn_screen=False):
+        with debug_opts(ctx, knn_screen=0):
             want = ctx.knn_bucketed(X, off, mem, probe, M, metric=metric, running=run)
         _equal(got, want)
         run = want
@@ -108,16 +110,16 @@ def test_screen_with_padded_running_lists(ctx, metric):
     rng = np.random.default_rng(12)
     off, mem = _buckets(rng, N, 400)
     # unseeded pools of fewer than M rows: the window bound is +inf
-    with debug_opts(ctx, knn_screen=True):
+    with debug_opts(ctx, knn_screen=2):
         run = ctx.knn_bucketed(X, off, mem, _probe(rng, 400, 0), 32, metric=metric)
-    with debug_opts(ctx, knn_screen=False):
+    with debug_opts(ctx, knn_screen=0):
         _equal(run, ctx.knn_bucketed(X, off, mem, _probe(rng, 400, 0), 32, metric=metric))
     assert (run[0] < 0).any()
     off, mem = _buckets(rng, N, 6)
     probe = _probe(rng, 6, 1)
-    with debug_opts(ctx, knn_screen=True):
+    with debug_opts(ctx, knn_screen=2):
         got = ctx.knn_bucketed(X, off, mem, probe, 32, metric=metric, running=run)
-    with debug_opts(ctx, knn_screen=False):
+    with debug_opts(ctx, knn_screen=0):
         want = ctx.knn_bucketed(X, off, mem, probe, 32, metric=metric, running=run)
     _equal(got, want)
 
@@ -128,9 +130,9 @@ def test_screened_build_equals_unscreened(ctx, cfg, N):
     metric = synth.CONFIGS[cfg].metric
     kw = dict(n_buckets=16, nprobe=1, M=64, K=32, rounds=2, metric=metric)
     print(f"screened build {cfg} N={N}", flush=True)
-    with debug_opts(ctx, knn_screen=True):
+    with debug_opts(ctx, knn_screen=2):
         a = ctx.build_graph(X, **kw)
-    with debug_opts(ctx, knn_screen=False):
+    with debug_opts(ctx, knn_screen=0):
         b = ctx.build_graph(X, **kw)
     np.testing.assert_array_equal(a.knn_ids, b.knn_ids)
     np.testing.assert_array_equal(a.knn_dists.view(np.uint32), b.knn_dists.view(np.uint32))
