@@ -204,7 +204,11 @@ def knn_roofline(s, D, metric, M=64):
     computes), over the launch time.  The int8 kernel skips pool chunks whose
     bounding sphere lies beyond every query's bound, so it multiplies fewer
     pairs: `ops_executed_per_launch` / `frac_executed` count those (the
-    pairs the MFMAs actually computed, counted on the device)."""
+    pairs the MFMAs actually computed, counted on the device).  On fp32 rows
+    the fp16 screen (knn_screen_kernel) first computes every pair of each
+    work item on the fp16 matrix cores and the fp32 collect kernel then
+    scans only the item's union of rows that can reach a list: there
+    `pairs_executed_share` is the share of pairs left to the fp32 MFMAs."""
     launches = max(1, int(round(s["knn_launches"])))
     launch_s = s["t_knn"] / launches
     flops = s["knn_flops"] / launches
@@ -223,6 +227,8 @@ def knn_roofline(s, D, metric, M=64):
         kname = (f"knn_f32_collect_kernel<{dp}, {mip}> + knn_select_kernel" if 4 < M <= 64 and dp <= 160
                  else f"knn_fused_kernel<{dp}, {mip}>")
         peak, unit = PEAK_FP32_MFMA, "TFLOP/s"
+        if done < pairs and 4 < M <= 64 and dp <= 160:   # the fp16 screen ran
+            kname = f"knn_screen_kernel<{dp}, {mip}> (fp16) + " + kname
     else:
         kname, peak, unit = f"knn_wide_kernel<{mip}>", PEAK_FP32_MFMA, "TFLOP/s"
     return {"kernel": kname, "bound": "mfma", "achieved": flops / launch_s / 1e12, "peak": peak / 1e12,

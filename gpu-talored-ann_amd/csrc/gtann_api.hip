@@ -1185,7 +1185,7 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
     // a bound on the pool's M-th smallest key from the screen's own window
     // -- a superset of the rows the fp32 pass keeps, so its lists are
     // unchanged; the fp32 pass then scans each item's union (items and pool
-    // list replaced), an unseeded one seeded with the screen's bounds
+    // list replaced)
     bool screen = want_screen && collect && a.Xq && !a.Xq8 && screen_supported(a.Dp, mp);
     int64_t* d_ubase = nullptr;
     int32_t* d_urows = nullptr;
@@ -1208,11 +1208,10 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
             d_xb = c.ws<uint16_t>(W_XB, static_cast<size_t>(N) * X.Dp);
             a.items = d_uitems;
             a.p_rows = d_urows;
-            if (!seed_d) {
-                d_tq = c.ws<float>(W_TQ, static_cast<size_t>(std::max<int64_t>(rows, 1)));
-                a.seed_d = d_tq;
-                a.seed_ld = 1;
-            }
+            // an unseeded pass's bounds serve the screen only: the fp32 pass
+            // takes its own (exact, tighter) window from each union,
+            // rotated to the queries' own rows
+            if (!seed_d) d_tq = c.ws<float>(W_TQ, static_cast<size_t>(std::max<int64_t>(rows, 1)));
         }
     }
     // exact chunk pruning (int8 rows, L2): the centre and radius of every

@@ -150,6 +150,7 @@ __global__ void __launch_bounds__(256) knn_screen_kernel(const WorkItem* __restr
     __shared__ __align__(16) int32_t trow[2][kPoolTile];   // row id, -1 past the pool's end
     __shared__ uint32_t bits[kScreenMaxPool / 32];
     __shared__ uint32_t wsum[kWaves];
+    __shared__ uint32_t urot;
 
     const int item_idx = blockIdx.x;
     const WorkItem it = items[item_idx];
@@ -370,6 +371,15 @@ __global__ void __launch_bounds__(256) knn_screen_kernel(const WorkItem* __restr
     __syncthreads();
     uint32_t off = inc - cnt;
     for (int q = 0; q < w; ++q) off += wsum[q];
+    // the union's rotation: its first row at or after the item's rotation
+    // (an unseeded fp32 pass takes its threshold window from there)
+    const int wr = it.p_rot >> 5;
+    if (pc > 0 && tid == wr / WPT) {
+        uint32_t r = off;
+        for (int wi = tid * WPT; wi < wr; ++wi) r += static_cast<uint32_t>(__popc(bits[wi]));
+        urot = r + static_cast<uint32_t>(__popc(bits[wr] & ((1u << (it.p_rot & 31)) - 1u)));
+    }
+    __syncthreads();
     const int64_t base = ubase[item_idx];
 #pragma unroll
     for (int u = 0; u < WPT; ++u) {
@@ -385,7 +395,7 @@ __global__ void __launch_bounds__(256) knn_screen_kernel(const WorkItem* __restr
         WorkItem o = it;
         o.p_begin = base;
         o.p_count = static_cast<int32_t>(wsum[0] + wsum[1] + wsum[2] + wsum[3]);
-        o.p_rot = 0;
+        o.p_rot = pc > 0 && static_cast<int32_t>(urot) < o.p_count ? static_cast<int32_t>(urot) : 0;
         items_out[item_idx] = o;
         if (pairs_done)
             atomicAdd(pairs_done, static_cast<unsigned long long>(o.p_count) * static_cast<unsigned>(o.q_count));
@@ -417,18 +427,19 @@ void launch_screen_prepare(const float* X, const float* nrm, int64_t N, int Dp, 
 
 // items: n_items work items of a pass (every pool at most kScreenMaxPool
 // rows); ubase[i]: item i's first slot of union_rows, which holds at least
-// its pool count from there; items_out: the items with their unions as
-// pools.  Xb: the scaled fp16 rows (stride Dp) of the matrix the q_rows and
-// p_rows index, sq its scale (launch_screen_prepare), nrm its fp32 |x|^2.  A seeded pass (seed_d: running tables of
-// seed_ld keys per output row) screens against each row's last key; an
-// unseeded one (M keys wanted, 4 < M <= 64) against a bound from the first
-// wtiles tiles of each item's rotated pool, written to tq (one per output
-// row: the pool's M-th smallest fp32 key is at or below it).  pairs_done
-// (optional) += the (query, union row) pairs left to the fp32 pass.
+// its pool count from there; items_out: the items with their unions as pools
+// (rotated to the union's first row at or after the item's rotation).  Xb:
+// the scaled fp16 rows (stride Dp) of the matrix the q_rows and p_rows
+// index, sq its scale (launch_screen_prepare), nrm its fp32 |x|^2.  A seeded
+// pass (seed_d: running tables of seed_ld keys per output row) screens
+// against each row's last key; an unseeded one (M keys wanted, 4 < M <= 64)
+// against a bound from the first wtiles tiles of each item's rotated pool,
+// written to tq (one per output row: the pool's M-th smallest fp32 key is at
+// or below it).  pairs_done (optional) += the (query, union row) pairs left
+// to the fp32 pass.
 void launch_screen(const WorkItem* items, int n_items, const int64_t* ubase, const int32_t* q_rows,
                    const int32_t* p_rows, const uint16_t* Xb, const float* nrm, const unsigned int* sq, int Dp,
-                   int metric,
-                   const float* seed_d, int seed_ld, int M, int wtiles, float* tq, int32_t* union_rows,
+                   int metric, const float* seed_d, int seed_ld, int M, int wtiles, float* tq, int32_t* union_rows,
                    WorkItem* items_out, unsigned long long* pairs_done, hipStream_t s)
 {
     GT_REQUIRE(screen_supported(Dp, 0), "screen: padded dimension not supported");
