@@ -558,20 +558,37 @@ def main():
         "max_pool": int(s["max_pool"]), "max_bucket": int(s["max_bucket"]),
     }
     if int8 and cfg.dtype == "f32":
-        # the same build on the fp32 kernel (int_exact off): its time, its
-        # fraction of the fp32 matrix peak, and the check that both paths
-        # return the same table and graph
-        w32, s32, r32 = timed_builds(ctx, torch, Xd, dict(kw, int_exact=False), max(1, min(args.steps, 3)))
+        # the same build on the fp32 kernel (int_exact off), first without
+        # the fp16 screen (every pair on the fp32 matrix cores: the fp32
+        # distance kernel's own fraction of the fp32 peak), then as the
+        # library runs it by default (behind the screen); both checked to
+        # return the int8 path's table and graph
+        ctx.set_debug(knn_screen=0)
+        try:
+            w32, s32, r32 = timed_builds(ctx, torch, Xd, dict(kw, int_exact=False), max(1, min(args.steps, 3)))
+        finally:
+            ctx.set_debug()
         same = bool(torch.equal(r32.knn_ids, res.knn_ids) and torch.equal(r32.graph, res.graph))
         r = knn_roofline(s32, D, cfg.metric, cfg.M)
+        del r32
+        wsc, ssc, rsc = timed_builds(ctx, torch, Xd, dict(kw, int_exact=False), max(1, min(args.steps, 3)))
+        same_sc = bool(torch.equal(rsc.knn_ids, res.knn_ids) and torch.equal(rsc.graph, res.graph))
+        rs = knn_roofline(ssc, D, cfg.metric, cfg.M)
+        del rsc
         out["fp32_path"] = {
-            "note": "int_exact=0: same dataset on the fp32 matrix cores (knn_f32_collect_kernel + knn_select_kernel)",
+            "note": "int_exact=0, knn_screen=0: same dataset, every pair on the fp32 matrix cores "
+                    "(knn_f32_collect_kernel + knn_select_kernel)",
             "value": N / w32 / 1e6, "unit": "Mpts/s", "ms_per_step": w32 * 1e3,
             "identical_table_and_graph": same,
             "roofline": dict({k: r[k] for k in ("kernel", "bound", "achieved", "peak", "unit", "frac", "launch_ms")},
                              rocprof=traffic_file(r["kernel"], args.config)),
+            "screened": {
+                "note": "int_exact=0 with the default fp16 screen: the fp32 collect kernel scans only each work "
+                        "item's rows that can reach a list",
+                "value": N / wsc / 1e6, "unit": "Mpts/s", "ms_per_step": wsc * 1e3,
+                "identical_table_and_graph": same_sc, "knn_launch_ms": rs["launch_ms"],
+                "fp32_pairs_share": rs["pairs_executed_share"]},
         }
-        del r32
     if args.refine_passes > 0:
         out["refine"] = refine_leg(ctx, torch, Xd, knn, kw, cfg.metric, rec["recall@32"], args.refine_passes,
                                    args.refine_sample, max(1, min(args.steps, 2)))
@@ -625,6 +642,8 @@ def main():
         ns["fp32_knn_frac_of_fp32_peak"] = round(fp["roofline"]["frac"], 4)
         ns["fp32_mfma_busy_pct"] = (fp["roofline"].get("rocprof") or {}).get("mfma_busy_pct")
         ns["fp32_identical_table_and_graph"] = fp["identical_table_and_graph"]
+        ns["fp32_screened_ms"] = round(fp["screened"]["ms_per_step"], 3)
+        ns["fp32_screened_identical_table_and_graph"] = fp["screened"]["identical_table_and_graph"]
     if "cpu_baseline" in out:
         ns["graph_identical_to_cpu_prune_merge"] = out["cpu_baseline"]["gpu_graph_identical_to_cpu_prune_merge"]
     if "host_to_host_graph_pinned" in out:
