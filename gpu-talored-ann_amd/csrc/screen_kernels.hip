@@ -124,7 +124,7 @@ __global__ void __launch_bounds__(256) screen_f16_kernel(const float4* __restric
 // into word t of the item's LDS bitmap; the set bits, in pool order, become
 // the item's union at union_rows[ubase[item] ...).
 template <int DP, int METRIC, bool WINDOW>
-__global__ void __launch_bounds__(256) knn_screen_kernel(const WorkItem* __restrict__ items,
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WINDOW || DP > 128 ? 2 : 4))) knn_screen_kernel(const WorkItem* __restrict__ items,
                                                          const int64_t* __restrict__ ubase,
                                                          const int32_t* __restrict__ q_rows,
                                                          const int32_t* __restrict__ p_rows,
@@ -185,16 +185,23 @@ __global__ void __launch_bounds__(256) knn_screen_kernel(const WorkItem* __restr
         for (int s = 0; s < KS; ++s) qf[s] = __builtin_bit_cast(halfx8, src[2 * s]);
     }
 
-    // pool tile t: positions rot + 32 t + r (mod pc) for 32 t + r < pc
-    // A three-stage pipeline per tile: row ids (one tile ahead of the row
-    // loads, so the row loads never wait on an id load) -> rows and norms in
-    // registers (one tile ahead) -> LDS.  fetch_ids(t) loads tile t's ids;
-    // load_tile() issues the loads of the tile fetch_ids last named;
-    // store_tile(buf) puts them into LDS.
+    // pool tile t: positions rot + 32 t + r (mod pc) for 32 t + r < pc,
+    // flowing through row ids (fetched a tile ahead of the row loads, so a
+    // row load never waits on an id load) -> rows and norms in registers
+    // (two register sets: loaded two tiles ahead of their use) -> LDS (two
+    // buffers).  fetch_ids(t) loads tile t's ids; load_into(set) issues the
+    // loads of the tile fetch_ids last named; store_from(set, buf) puts a set
+    // into LDS.
     int32_t idq[U4_THREAD];   // ids of the next tile's 16-byte pieces (-1: none)
-    int32_t ridq = -1, ridc = -1;   // threads < 32: the id of the next tile's row tid, of the loaded tile's
-    float pnc = 0.f;
-    uint4 pre[U4_THREAD];
+    int32_t ridq = -1;        // threads < 32: the id of the next tile's row tid
+    struct Set {
+        uint4 v[U4_THREAD];
+        int32_t rid;
+        float pn;
+    };
+    Set set0, set1;
+    set0.rid = set1.rid = -1;
+    set0.pn = set1.pn = 0.f;
     auto pos_row = [&](int t, int r, int rot) __attribute__((always_inline)) -> int32_t {
         int p = t * kPoolTile + r;
         if (p >= pc) return -1;
@@ -210,29 +217,62 @@ __global__ void __launch_bounds__(256) knn_screen_kernel(const WorkItem* __restr
         }
         if (tid < kPoolTile) ridq = pos_row(t, tid, rot);
     };
-    auto load_tile = [&]() __attribute__((always_inline)) {
+    auto load_into = [&](Set& S) __attribute__((always_inline)) {
 #pragma unroll
         for (int u = 0; u < U4_THREAD; ++u) {
             const int e = tid + 256 * u;
-            pre[u] = idq[u] >= 0 ? reinterpret_cast<const uint4*>(Xb + static_cast<int64_t>(idq[u]) * DP)[e % U4_ROW]
+            S.v[u] = idq[u] >= 0 ? reinterpret_cast<const uint4*>(Xb + static_cast<int64_t>(idq[u]) * DP)[e % U4_ROW]
                                  : make_uint4(0u, 0u, 0u, 0u);
         }
         if (tid < kPoolTile) {
-            ridc = ridq;
-            pnc = ridq >= 0 ? nrm[ridq] : 0.f;
+            S.rid = ridq;
+            S.pn = ridq >= 0 ? nrm[ridq] : 0.f;
         }
     };
-    auto store_tile = [&](int buf) __attribute__((always_inline)) {
+    auto store_from = [&](const Set& S, int buf) __attribute__((always_inline)) {
 #pragma unroll
         for (int u = 0; u < U4_THREAD; ++u) {
             const int e = tid + 256 * u;
-            if (e < U4_TILE) *reinterpret_cast<uint4*>(&tile[buf][e / U4_ROW][8 * (e % U4_ROW)]) = pre[u];
+            if (e < U4_TILE) *reinterpret_cast<uint4*>(&tile[buf][e / U4_ROW][8 * (e % U4_ROW)]) = S.v[u];
         }
         if (tid < kPoolTile) {
-            tpr[buf][tid] = sqrtf(pnc) * s1;
-            tpm[buf][tid] = -(1.f - kScreenR) * (pnc * s2);
-            tpu[buf][tid] = (1.f + kScreenR) * (pnc * s2);
-            trow[buf][tid] = ridc;
+            tpr[buf][tid] = sqrtf(S.pn) * s1;
+            tpm[buf][tid] = -(1.f - kScreenR) * (S.pn * s2);
+            tpu[buf][tid] = (1.f + kScreenR) * (S.pn * s2);
+            trow[buf][tid] = S.rid;
+        }
+    };
+    // runs body(t, buf) over tiles 0 .. n - 1 (tile t in LDS buffer t & 1),
+    // one barrier per tile
+    auto pipeline = [&](int n, int rot, auto&& body) __attribute__((always_inline)) {
+        if (n > 0) {
+            fetch_ids(0, rot);
+            load_into(set0);
+        }
+        if (n > 1) {
+            fetch_ids(1, rot);
+            load_into(set1);
+        }
+        if (n > 2) fetch_ids(2, rot);
+        if (n > 0) store_from(set0, 0);
+        __syncthreads();
+        for (int t = 0; t < n; t += 2) {
+            if (t + 2 < n) {
+                load_into(set0);
+                if (t + 3 < n) fetch_ids(t + 3, rot);
+            }
+            body(t, 0);
+            if (t + 1 < n) store_from(set1, 1);
+            __syncthreads();
+            if (t + 1 < n) {
+                if (t + 3 < n) {
+                    load_into(set1);
+                    if (t + 4 < n) fetch_ids(t + 4, rot);
+                }
+                body(t + 1, 1);
+                if (t + 2 < n) store_from(set0, 0);
+                __syncthreads();
+            }
         }
     };
 
@@ -250,17 +290,7 @@ __global__ void __launch_bounds__(256) knn_screen_kernel(const WorkItem* __restr
 #pragma unroll
         for (int i = 0; i < 32; ++i) L[i] = INFINITY;
         const int nwt = min(wtiles, ntiles);
-        if (nwt > 0) {
-            fetch_ids(0, it.p_rot);
-            load_tile();
-            if (nwt > 1) fetch_ids(1, it.p_rot);
-            store_tile(0);
-        }
-        __syncthreads();
-        for (int t = 0; t < nwt; ++t) {
-            const int buf = t & 1;
-            if (t + 1 < nwt) load_tile();
-            if (t + 2 < nwt) fetch_ids(t + 2, it.p_rot);
+        pipeline(nwt, it.p_rot, [&](int t, int buf) __attribute__((always_inline)) {
             floatx16 acc;
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[r] = 0.f;
@@ -291,9 +321,7 @@ __global__ void __launch_bounds__(256) knn_screen_kernel(const WorkItem* __restr
 #pragma unroll
             for (int k = 0; k < 16; ++k) L[16 + k] = fminf(L[16 + k], ub[15 - k]);
             bitonic_merge(L);
-            if (t + 1 < nwt) store_tile(buf ^ 1);
-            __syncthreads();
-        }
+        });
         const int m = (M + 1) / 2 - 1;
         float v = L[0];
 #pragma unroll
@@ -318,17 +346,7 @@ __global__ void __launch_bounds__(256) knn_screen_kernel(const WorkItem* __restr
         cq_r[r] = __shfl(cq, src);
     }
 
-    if (ntiles > 0) {
-        fetch_ids(0, 0);
-        load_tile();
-        if (ntiles > 1) fetch_ids(1, 0);
-        store_tile(0);
-    }
-    __syncthreads();
-    for (int t = 0; t < ntiles; ++t) {
-        const int buf = t & 1;
-        if (t + 1 < ntiles) load_tile();
-        if (t + 2 < ntiles) fetch_ids(t + 2, 0);
+    pipeline(ntiles, 0, [&](int t, int buf) __attribute__((always_inline)) {
         floatx16 acc;
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[r] = 0.f;
@@ -351,9 +369,7 @@ __global__ void __launch_bounds__(256) knn_screen_kernel(const WorkItem* __restr
         const int left = pc - t * kPoolTile;
         if (left < kPoolTile) tm &= (1u << left) - 1u;
         if (lane == 0 && tm) atomicOr(&bits[t], tm);
-        if (t + 1 < ntiles) store_tile(buf ^ 1);
-        __syncthreads();
-    }
+    });
     // the set bits, in order, as row ids
     uint32_t cnt = 0u;
 #pragma unroll
