@@ -1187,6 +1187,11 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
     // unchanged; the fp32 pass then scans each item's union (items and pool
     // list replaced)
     bool screen = want_screen && collect && a.Xq && !a.Xq8 && screen_supported(a.Dp, mp);
+    // the screen's own window: 16 tiles (C3: 32, 64 and 128 tiles shrink
+    // the union by 1.7, 3.5 and 6.5 % and cost more than that saves); the
+    // fp32 pass over the unions takes 32 (C3 kNN 22.9 -> 21.9 ms)
+    const int screen_window = a.window_tiles;
+    if (screen && c.c->dbg.knn_window <= 0) a.window_tiles = 32;
     int64_t* d_ubase = nullptr;
     int32_t* d_urows = nullptr;
     WorkItem* d_uitems = nullptr;
@@ -1243,7 +1248,7 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
             unsigned int* d_sq = c.ws<unsigned int>(W_SQ, 1);
             launch_screen_prepare(X.data, X.norms, N, X.Dp, d_sq, d_xb, c.s);
             launch_screen(d_items, a.n_items, d_ubase, d_members, d_pool, d_xb, X.norms, d_sq, X.Dp, metric, seed_d, M, M,
-                          a.window_tiles, d_tq, d_urows, d_uitems, a.pairs_done, c.s);
+                          screen_window, d_tq, d_urows, d_uitems, a.pairs_done, c.s);
         }
         if (collect) launch_knn_collect_select(a, rows, c.s);
         else launch_knn_fused(a, c.s);
