@@ -10,7 +10,8 @@ with the dataset already resident in HBM.  Prints one JSON line.
 `roofline` is the kNN kernel of the rounds (knn_i8_collect_kernel +
 knn_select_kernel when the rows are integers, as C2's are;
 knn_f32_collect_kernel + knn_select_kernel for float rows up to 160
-dimensions, knn_wide_kernel beyond): achieved = the algorithmic ops of its launches
+dimensions, behind the fp16 screen (knn_screen_kernel) on passes of at least
+2^27 pairs; knn_wide_kernel beyond): achieved = the algorithmic ops of its launches
 (2*D per scanned (query, pool row) pair) over their summed duration, both
 measured by the library with HIP events on its stream.  `traffic` is read
 from profiles/<kernel>_<config>_traffic.json (knn_i8_collect_C2_traffic.json
@@ -240,8 +241,11 @@ def knn_roofline(s, D, metric, M=64):
 
 def traffic_file(kernel, config):
     """rocprofv3 FETCH+WRITE bytes per round launch of `kernel` on `config`
-    (profiles/<kernel>_<config>_traffic.json), or None."""
-    base = kernel.split("<")[0].replace("_kernel", "")
+    (profiles/<kernel>_<config>_traffic.json, named for the launch's
+    distance kernel: a leading fp16 screen is part of the same launch), or
+    None."""
+    main = kernel.split(" + ")[1] if kernel.startswith("knn_screen_kernel") else kernel
+    base = main.split("<")[0].replace("_kernel", "")
     path = os.path.join(ROOT, "profiles", f"{base}_{config}_traffic.json")
     if not os.path.exists(path):
         return None
