@@ -14,7 +14,8 @@ cancellation, where the norm term of the bound decides), rows of tiny and
 of huge scale (the power-of-two scale of the fp16 copy), duplicated rows
 (ties at the threshold), inner products of rows of varied norm, running
 tables with padding (+inf thresholds: every row kept), every padded width
-the screen takes (32 .. 160), and whole builds.  The unscreened passes are
+the screen takes (32 .. 160), and whole builds, resident and out of core
+(compact output rows).  The unscreened passes are
 themselves checked against the CPU oracle in tests/test_gpu_collect_f32.py
 and tests/test_gpu_float.py.
 """
@@ -143,3 +144,23 @@ def test_screened_build_equals_unscreened(ctx, cfg, N):
           f"unscreened {sb['knn_pairs_computed']:.4g}", flush=True)
     assert sb["knn_pairs_computed"] == sb["knn_pairs"]
     assert sa["knn_pairs_computed"] < 0.8 * sa["knn_pairs"]
+
+
+@pytest.mark.parametrize("metric", ["l2", "ip"])
+def test_screened_out_of_core_build_equals_unscreened(ctx, metric):
+    # bucket chunks with compact output rows (each work item's rows through
+    # its out_base), seeded from the host-resident running table
+    X = _data("gauss", 40000, 96, seed=21)
+    if metric == "ip":
+        X /= np.linalg.norm(X, axis=1, keepdims=True)
+    kw = dict(n_buckets=24, M=32, K=16, rounds=2, nprobe=1, metric=metric, device_budget_mb=24)
+    print(f"screened out-of-core build {metric}", flush=True)
+    with debug_opts(ctx, knn_screen=2):
+        a = ctx.build_graph(X, **kw)
+    with debug_opts(ctx, knn_screen=0):
+        b = ctx.build_graph(X, **kw)
+    assert a.stats["ooc_chunks"] > 3
+    assert a.stats["knn_pairs_computed"] < a.stats["knn_pairs"]
+    np.testing.assert_array_equal(a.knn_ids, b.knn_ids)
+    np.testing.assert_array_equal(a.knn_dists.view(np.uint32), b.knn_dists.view(np.uint32))
+    np.testing.assert_array_equal(a.graph, b.graph)
