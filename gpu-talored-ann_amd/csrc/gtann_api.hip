@@ -2682,49 +2682,70 @@ int gt_search(gt_ctx* ctx, const void* X, int64_t N, int32_t D, int dtype, const
             a.status = d_status;
             a.expansions = d_exp;
             a.visits = d_vis;
-            // visited table: a query visits up to about degree x ef points; the
-            // table holds 3/4 of its slots, within 64 KiB of LDS per query
+            // visited set: an LDS hash table (a query visits up to about
+            // degree x ef points; the table holds 3/4 of its slots) or, when
+            // that table would leave fewer than five waves per CU (S2 at
+            // ef 200: one wave per SIMD, 19.0 ms against 10.7 ms), a bitmap
+            // of N bits per wave in HBM with a few KiB of LDS per wave
+            constexpr size_t kHashLdsMax = 32768;
             int H = p.visited_slots;
+            bool bitmap_only = H == -1;
             if (H == 0) {
                 const int64_t want = static_cast<int64_t>(degree) * ef * 4 / 3;
                 H = 512;
                 while (H < want && search_lds_bytes(a.CC, a.efr, a.Dp, 2 * H) <= 65536) H *= 2;
+                bitmap_only = search_lds_bytes(a.CC, a.efr, a.Dp, H) > kHashLdsMax;
             }
-            GT_REQUIRE(H >= 512 && (H & (H - 1)) == 0, "visited_slots must be a power of two >= 512");
-            GT_REQUIRE(search_lds_bytes(a.CC, a.efr, a.Dp, H) <= 65536, "ef / dimension too large for one query's LDS");
-            a.H = H;
-            st.t_search = c.timed([&] { launch_graph_search(a, nq, c.s); });
-
-            std::vector<int32_t> hs(static_cast<size_t>(nq)), hx(static_cast<size_t>(nq)), hv(static_cast<size_t>(nq));
-            c.d2h(hs.data(), d_status, hs.size() * sizeof(int32_t));
-            c.sync();
-            std::vector<int32_t> redo;
-            for (int64_t q = 0; q < nq; ++q) {
-                GT_REQUIRE(hs[static_cast<size_t>(q)] != 2,
-                           "search: more candidates tie at the ef-th distance than fit (query " + std::to_string(q) + ")");
-                if (hs[static_cast<size_t>(q)] == 1) redo.push_back(static_cast<int32_t>(q));
-            }
-            if (!redo.empty()) {
-                // queries that outgrew the on-chip table: a bitmap of N bits per wave in HBM
+            // queries (all, or those that outgrew the on-chip table) on the
+            // bitmap path: up to kBitmapWaves waves, each clearing its bitmap
+            // after every query
+            auto run_bitmap = [&](const int32_t* d_list, int64_t n) {
+                constexpr int64_t kBitmapWaves = 2048;   // S2, ef 200: 4096 and 8192 no faster
                 const int64_t words = ceil_div(N, 32);
                 const int64_t by_mem = std::max<int64_t>(1, (int64_t(4) << 30) / (words * 4));
-                const int64_t slots = std::min<int64_t>({static_cast<int64_t>(redo.size()), 2048, by_mem});
+                const int64_t slots = std::min<int64_t>({n, kBitmapWaves, by_mem});
                 uint32_t* bmp = c.ws<uint32_t>(W_TMP, static_cast<size_t>(slots * words));
                 GT_HIP(hipMemsetAsync(bmp, 0, static_cast<size_t>(slots * words) * 4, c.s));
-                int32_t* d_redo = c.ws<int32_t>(W_QROWS, redo.size());
-                c.h2d(d_redo, redo.data(), redo.size() * sizeof(int32_t));
-                a.q_list = d_redo;
-                a.n_run = static_cast<int64_t>(redo.size());
+                a.q_list = d_list;
+                a.n_run = n;
                 a.H = 0;
                 a.bitmap = bmp;
                 a.bm_words = words;
+                GT_REQUIRE(search_lds_bytes(a.CC, a.efr, a.Dp, 0) <= 65536, "ef / dimension too large for one query's LDS");
                 st.t_search += c.timed([&] { launch_graph_search(a, slots, c.s); });
+            };
+            std::vector<int32_t> hs(static_cast<size_t>(nq)), hx(static_cast<size_t>(nq)), hv(static_cast<size_t>(nq));
+            if (bitmap_only) {
+                run_bitmap(nullptr, nq);
                 c.d2h(hs.data(), d_status, hs.size() * sizeof(int32_t));
                 c.sync();
-                for (int32_t q : redo)
+                for (int64_t q = 0; q < nq; ++q)
                     GT_REQUIRE(hs[static_cast<size_t>(q)] == 0,
                                "search: more candidates tie at the ef-th distance than fit (query " + std::to_string(q) + ")");
-                st.requeued = static_cast<int64_t>(redo.size());
+            } else {
+                GT_REQUIRE(H >= 512 && (H & (H - 1)) == 0, "visited_slots must be -1, 0 or a power of two >= 512");
+                GT_REQUIRE(search_lds_bytes(a.CC, a.efr, a.Dp, H) <= 65536, "ef / dimension too large for one query's LDS");
+                a.H = H;
+                st.t_search = c.timed([&] { launch_graph_search(a, nq, c.s); });
+                c.d2h(hs.data(), d_status, hs.size() * sizeof(int32_t));
+                c.sync();
+                std::vector<int32_t> redo;
+                for (int64_t q = 0; q < nq; ++q) {
+                    GT_REQUIRE(hs[static_cast<size_t>(q)] != 2,
+                               "search: more candidates tie at the ef-th distance than fit (query " + std::to_string(q) + ")");
+                    if (hs[static_cast<size_t>(q)] == 1) redo.push_back(static_cast<int32_t>(q));
+                }
+                if (!redo.empty()) {
+                    int32_t* d_redo = c.ws<int32_t>(W_QROWS, redo.size());
+                    c.h2d(d_redo, redo.data(), redo.size() * sizeof(int32_t));
+                    run_bitmap(d_redo, static_cast<int64_t>(redo.size()));
+                    c.d2h(hs.data(), d_status, hs.size() * sizeof(int32_t));
+                    c.sync();
+                    for (int32_t q : redo)
+                        GT_REQUIRE(hs[static_cast<size_t>(q)] == 0,
+                                   "search: more candidates tie at the ef-th distance than fit (query " + std::to_string(q) + ")");
+                    st.requeued = static_cast<int64_t>(redo.size());
+                }
             }
             c.d2h(hx.data(), d_exp, hx.size() * sizeof(int32_t));
             c.d2h(hv.data(), d_vis, hv.size() * sizeof(int32_t));

@@ -321,8 +321,10 @@ typedef struct gt_search_params {
     int32_t num_entry;      /* entry points per query drawn when `entries` is NULL (--num-entry), <= 64 */
     int32_t metric;         /* GT_METRIC_L2 (the reference's only metric) or GT_METRIC_IP */
     uint64_t seed;          /* entry draw when `entries` is NULL */
-    int32_t visited_slots;  /* 0 = automatic; else the on-chip visited table per query (power of two
-                               >= 512); a query that outgrows it is run again with an HBM bitmap */
+    int32_t visited_slots;  /* visited set per query: 0 = automatic (an on-chip hash table, or an HBM
+                               bitmap of N bits per wave when the table would take more than 32 KiB
+                               of LDS); -1 = the HBM bitmap; else the on-chip table's slots (power of
+                               two >= 512), a query that outgrows it run again with the bitmap */
     int32_t reserved_;
 } gt_search_params;
 

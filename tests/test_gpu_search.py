@@ -107,6 +107,22 @@ def test_small_visited_table_requeues_on_hbm_bitmap(ctx):
     assert st2["requeued"] > 0
 
 
+@pytest.mark.parametrize("ef,slots", [(64, -1), (200, -1), (200, 8192)])
+def test_visited_set_paths_match_oracle(ctx, ef, slots):
+    # -1: every query on the HBM bitmap (the automatic choice when the
+    # on-chip table would take more than 32 KiB of LDS, as at ef 200);
+    # 8192: the on-chip table forced where the bitmap would be chosen
+    rng = np.random.default_rng(ef + 7)
+    N, D = 6000, 128
+    X = rng.integers(0, 64, size=(N, D)).astype(np.float32)
+    knn, _ = O.knn_exact(X, 32)
+    Q = rng.integers(0, 64, size=(150, D)).astype(np.float32)
+    ent = rng.integers(0, N, size=(150, 4)).astype(np.int32)
+    print(f"search visited set ef={ef} slots={slots}", flush=True)
+    st = _compare(ctx, X, knn, Q, ent, 10, ef, visited_slots=slots)
+    assert st["requeued"] == 0
+
+
 @pytest.mark.parametrize("dtype", [np.uint8, np.int8])
 def test_integer_typed_inputs(ctx, dtype):
     rng = np.random.default_rng(7)
