@@ -39,7 +39,7 @@ bool screen_supported(int Dp, int64_t max_pool);
 void launch_screen_prepare(const float* X, const float* nrm, int64_t N, int Dp, unsigned int* sq, uint16_t* Xh,
                            hipStream_t s);
 void launch_screen(const WorkItem* items, int n_items, const int64_t* ubase, const int32_t* q_rows,
-                   const int32_t* p_rows, const uint16_t* Xb, const float* nrm, const unsigned int* sq, int Dp,
+                   const int32_t* p_rows, const uint16_t* Xh, const float* nrm, const unsigned int* sq, int Dp,
                    int metric, const float* seed_d, int seed_ld, int M, int wtiles, float* tq, int32_t* union_rows,
                    WorkItem* items_out, unsigned long long* pairs_done, hipStream_t s);
 // graph_kernels.hip
@@ -272,7 +272,7 @@ enum Ws {
     W_OOC_A, W_OOC_B, W_OOC_C, W_OOC_D, W_OOC_E, W_OOC_F, W_OOC_G, W_CR, W_CRNORMS,
     W_KM_TRAIN, W_KM_MIND, W_KM_FLAG, W_KM_SEL, W_KM_POS, W_KM_SUMS, W_KM_NEW, W_KM_PSI, W_KM_P, W_KM_PN, W_KM_P8,
     W_KM_PN8, W_KM_OI, W_KM_OD, W_CH8, W_CHN, W_CHR, W_CHCNT, W_PAIRS, W_TOP2A, W_TOP2B, W_BUCKETD, W_KEY2,
-    W_BYKEY, W_BKTD, W_BOFF, W_SUBPOS, W_TOP2H, W_RV1, W_RV1M, W_XB, W_UBASE, W_UROWS, W_UITEMS, W_TQ, W_SQ, W_COUNT_
+    W_BYKEY, W_BKTD, W_BOFF, W_SUBPOS, W_TOP2H, W_RV1, W_RV1M, W_XH, W_UBASE, W_UROWS, W_UITEMS, W_TQ, W_SQ, W_COUNT_
 };
 static_assert(W_COUNT_ <= 112, "workspace slots");
 
@@ -1195,7 +1195,7 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
     int64_t* d_ubase = nullptr;
     int32_t* d_urows = nullptr;
     WorkItem* d_uitems = nullptr;
-    uint16_t* d_xb = nullptr;
+    uint16_t* d_xh = nullptr;
     float* d_tq = nullptr;
     if (screen) {
         std::vector<int64_t> ub(items.size(), 0);
@@ -1210,7 +1210,7 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
             c.h2d(d_ubase, ub.data(), ub.size() * sizeof(int64_t));
             d_urows = c.ws<int32_t>(W_UROWS, static_cast<size_t>(std::max<int64_t>(u, 1)));
             d_uitems = c.ws<WorkItem>(W_UITEMS, items.size());
-            d_xb = c.ws<uint16_t>(W_XB, static_cast<size_t>(N) * X.Dp);
+            d_xh = c.ws<uint16_t>(W_XH, static_cast<size_t>(N) * X.Dp);
             a.items = d_uitems;
             a.p_rows = d_urows;
             // an unseeded pass's bounds serve the screen only: the fp32 pass
@@ -1246,8 +1246,8 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
                                 const_cast<float*>(a.chn), const_cast<float*>(a.chr), c.s);
         if (screen) {
             unsigned int* d_sq = c.ws<unsigned int>(W_SQ, 1);
-            launch_screen_prepare(X.data, X.norms, N, X.Dp, d_sq, d_xb, c.s);
-            launch_screen(d_items, a.n_items, d_ubase, d_members, d_pool, d_xb, X.norms, d_sq, X.Dp, metric, seed_d, M, M,
+            launch_screen_prepare(X.data, X.norms, N, X.Dp, d_sq, d_xh, c.s);
+            launch_screen(d_items, a.n_items, d_ubase, d_members, d_pool, d_xh, X.norms, d_sq, X.Dp, metric, seed_d, M, M,
                           screen_window, d_tq, d_urows, d_uitems, a.pairs_done, c.s);
         }
         if (collect) launch_knn_collect_select(a, rows, c.s);

@@ -128,7 +128,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WINDOW
                                                          const int64_t* __restrict__ ubase,
                                                          const int32_t* __restrict__ q_rows,
                                                          const int32_t* __restrict__ p_rows,
-                                                         const uint16_t* __restrict__ Xb, const float* __restrict__ nrm,
+                                                         const uint16_t* __restrict__ Xh, const float* __restrict__ nrm,
                                                          const unsigned int* __restrict__ sq,
                                                          const float* __restrict__ seed_d, int seed_ld, int M,
                                                          int wtiles, float* __restrict__ tq,
@@ -137,12 +137,12 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WINDOW
                                                          unsigned long long* __restrict__ pairs_done)
 {
     constexpr int KS = DP / 16;          // MFMA steps per tile
-    constexpr int RS = DP + 8;           // LDS row stride (bf16 elements): rows on distinct bank groups
+    constexpr int RS = DP + 8;           // LDS row stride (fp16 elements): rows on distinct bank groups
     constexpr int U4_ROW = DP / 8;       // 16-byte pieces per row
     constexpr int U4_TILE = kPoolTile * U4_ROW;
     constexpr int U4_THREAD = (U4_TILE + 255) / 256;
     constexpr int WPT = kScreenMaxPool / 32 / 256;   // bitmap words per thread in the compaction
-    static_assert(DP % 16 == 0 && kPoolTile == 32, "bf16 steps of 16 dims, one bitmap word per tile");
+    static_assert(DP % 16 == 0 && kPoolTile == 32, "fp16 steps of 16 dims, one bitmap word per tile");
     __shared__ __align__(16) uint16_t tile[2][kPoolTile][RS];
     __shared__ __align__(16) float tpr[2][kPoolTile];   // |p|
     __shared__ __align__(16) float tpm[2][kPoolTile];   // -(1 - R) |p|^2
@@ -180,7 +180,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WINDOW
     const float cq = METRIC == 0 ? fmaf(2.f * kScreenC, qr, kD) : fmaf(kScreenC + kScreenR, qr, kD);
     halfx8 qf[KS];
     {
-        const uint4* src = reinterpret_cast<const uint4*>(Xb + static_cast<int64_t>(qrow) * DP + 8 * h);
+        const uint4* src = reinterpret_cast<const uint4*>(Xh + static_cast<int64_t>(qrow) * DP + 8 * h);
 #pragma unroll
         for (int s = 0; s < KS; ++s) qf[s] = __builtin_bit_cast(halfx8, src[2 * s]);
     }
@@ -221,7 +221,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WINDOW
 #pragma unroll
         for (int u = 0; u < U4_THREAD; ++u) {
             const int e = tid + 256 * u;
-            S.v[u] = idq[u] >= 0 ? reinterpret_cast<const uint4*>(Xb + static_cast<int64_t>(idq[u]) * DP)[e % U4_ROW]
+            S.v[u] = idq[u] >= 0 ? reinterpret_cast<const uint4*>(Xh + static_cast<int64_t>(idq[u]) * DP)[e % U4_ROW]
                                  : make_uint4(0u, 0u, 0u, 0u);
         }
         if (tid < kPoolTile) {
@@ -278,7 +278,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WINDOW
 
     // WINDOW: an upper bound on the M-th smallest fp32 key of the pool from
     // its first wtiles tiles (from the item's rotation), to tq: each lane
-    // keeps the 32 smallest bounds ub = bf16 key + e >= fp32 key of the rows
+    // keeps the 32 smallest bounds ub = fp16 key + e >= fp32 key of the rows
     // it holds (a sorting network on registers), and the larger of the pair's
     // ceil(M/2)-th smallest bounds ceil(M/2) rows of each lane from above: M
     // distinct rows, the query itself excluded (+inf if the window has fewer).
@@ -444,7 +444,7 @@ void launch_screen_prepare(const float* X, const float* nrm, int64_t N, int Dp, 
 // items: n_items work items of a pass (every pool at most kScreenMaxPool
 // rows); ubase[i]: item i's first slot of union_rows, which holds at least
 // its pool count from there; items_out: the items with their unions as pools
-// (rotated to the union's first row at or after the item's rotation).  Xb:
+// (rotated to the union's first row at or after the item's rotation).  Xh:
 // the scaled fp16 rows (stride Dp) of the matrix the q_rows and p_rows
 // index, sq its scale (launch_screen_prepare), nrm its fp32 |x|^2.  A seeded
 // pass (seed_d: running tables of seed_ld keys per output row) screens
@@ -454,7 +454,7 @@ void launch_screen_prepare(const float* X, const float* nrm, int64_t N, int Dp, 
 // or below it).  pairs_done (optional) += the (query, union row) pairs left
 // to the fp32 pass.
 void launch_screen(const WorkItem* items, int n_items, const int64_t* ubase, const int32_t* q_rows,
-                   const int32_t* p_rows, const uint16_t* Xb, const float* nrm, const unsigned int* sq, int Dp,
+                   const int32_t* p_rows, const uint16_t* Xh, const float* nrm, const unsigned int* sq, int Dp,
                    int metric, const float* seed_d, int seed_ld, int M, int wtiles, float* tq, int32_t* union_rows,
                    WorkItem* items_out, unsigned long long* pairs_done, hipStream_t s)
 {
@@ -465,12 +465,12 @@ void launch_screen(const WorkItem* items, int n_items, const int64_t* ubase, con
     do {                                                                                                      \
         if (!seed_d)                                                                                          \
             hipLaunchKernelGGL((knn_screen_kernel<DPV, MET, true>), dim3(n_items), dim3(256), 0, s, items,    \
-                               ubase, q_rows, p_rows, Xb, nrm, sq, seed_d, seed_ld, M, wtiles, tq, union_rows,    \
+                               ubase, q_rows, p_rows, Xh, nrm, sq, seed_d, seed_ld, M, wtiles, tq, union_rows,    \
                                items_out, pairs_done);                                                        \
         const float* sd = seed_d ? seed_d : tq;                                                               \
         const int sl = seed_d ? seed_ld : 1;                                                                  \
         hipLaunchKernelGGL((knn_screen_kernel<DPV, MET, false>), dim3(n_items), dim3(256), 0, s, items, ubase, \
-                           q_rows, p_rows, Xb, nrm, sq, sd, sl, M, wtiles, tq, union_rows, items_out, pairs_done); \
+                           q_rows, p_rows, Xh, nrm, sq, sd, sl, M, wtiles, tq, union_rows, items_out, pairs_done); \
     } while (0)
 #define GT_SCR_M(DPV)                     \
     do {                                  \
