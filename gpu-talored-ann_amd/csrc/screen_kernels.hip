@@ -152,7 +152,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WINDOW
     __shared__ uint32_t wsum[kWaves];
     __shared__ uint32_t urot;
 
-    const int item_idx = blockIdx.x;
+    // the items are laid out XCD by XCD (n_items / 8 each, a bucket's items
+    // together): block b runs item (b mod 8) n_items / 8 + b / 8, so the
+    // blocks one XCD runs share their pools in its L2
+    const int per = static_cast<int>(gridDim.x) / 8;
+    const int item_idx = static_cast<int>(blockIdx.x % 8) * per + static_cast<int>(blockIdx.x / 8);
     const WorkItem it = items[item_idx];
     const int tid = threadIdx.x;
     if (it.q_count <= 0) {   // padding
@@ -459,6 +463,7 @@ void launch_screen(const WorkItem* items, int n_items, const int64_t* ubase, con
                    WorkItem* items_out, unsigned long long* pairs_done, hipStream_t s)
 {
     GT_REQUIRE(screen_supported(Dp, 0), "screen: padded dimension not supported");
+    GT_REQUIRE(n_items % 8 == 0, "screen: work list must be padded to a multiple of 8 (one eighth per XCD)");
     GT_REQUIRE(seed_d ? seed_ld > 0 : (tq && M > 4 && M <= 64 && wtiles > 0), "screen: seed or window missing");
     if (n_items <= 0) return;
 #define GT_SCR(DPV, MET)                                                                                      \
