@@ -255,6 +255,9 @@ struct gt_ctx {
     int64_t knn_launches = 0;   // bucketed-round launches of the current build
     double knn_pairs_done = 0;  // (query, pool row) pairs the collect kernels computed (chunk pruning skips the rest)
     uint64_t members_gen = 0;   // bucketing whose members W_MEMBERS holds (0: none)
+    uint64_t data_gen = 0;      // bumped whenever W_X / W_NORMS are (re)written
+    uint64_t screen_gen = 0;    // data_gen whose fp16 copy and scale W_XH / W_SQ hold (0: none)
+    const float* screen_src = nullptr;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
     void* scratch = nullptr;    // this device's fixed scratch array (gt_optimize_noalloc), or null
     std::string scratch_err;    // why it is null
@@ -412,6 +415,7 @@ static DevMatrix prepare(Ctx& c, int slot_x, int slot_raw, int slot_norms, const
 {
     GT_REQUIRE(X != nullptr && N > 0 && D > 0, "empty dataset");
     GT_REQUIRE(N < (int64_t(1) << 31), "N must be < 2^31");
+    if (slot_x == W_X) ++c.c->data_gen;   // the screen's fp16 copy of these rows is stale
     const int Dp = pad_dim(D);
     GT_REQUIRE(Dp <= 1024, "dimension > 1024 is not supported by this build");
     const size_t es = dtype_size(dtype);
@@ -1245,8 +1249,14 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
             launch_chunk_bounds(X.data8, X.Dp8, d_pool, d_chcnt, nchunk, const_cast<int8_t*>(a.ch8),
                                 const_cast<float*>(a.chn), const_cast<float*>(a.chr), c.s);
         if (screen) {
+            // the fp16 copy once per prepared dataset (every pass of a build
+            // screens the same rows)
             unsigned int* d_sq = c.ws<unsigned int>(W_SQ, 1);
-            launch_screen_prepare(X.data, X.norms, N, X.Dp, d_sq, d_xh, c.s);
+            if (c.c->screen_gen != c.c->data_gen || c.c->screen_src != X.data) {
+                launch_screen_prepare(X.data, X.norms, N, X.Dp, d_sq, d_xh, c.s);
+                c.c->screen_gen = c.c->data_gen;
+                c.c->screen_src = X.data;
+            }
             launch_screen(d_items, a.n_items, d_ubase, d_members, d_pool, d_xh, X.norms, d_sq, X.Dp, metric, seed_d, M, M,
                           screen_window, d_tq, d_urows, d_uitems, a.pairs_done, c.s);
         }
