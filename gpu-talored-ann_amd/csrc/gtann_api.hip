@@ -38,7 +38,8 @@ void launch_knn_resident(const KnnArgs& a, int64_t nq, int64_t np, hipStream_t s
 bool screen_supported(int Dp, int64_t max_pool);
 void launch_screen_prepare(const float* X, const float* nrm, int64_t N, int Dp, unsigned int* sq, uint16_t* Xh,
                            hipStream_t s);
-void launch_screen(const WorkItem* items, int n_items, const int64_t* ubase, const int32_t* q_rows,
+void launch_screen(const WorkItem* items, int n_items, const int32_t* pairs, int n_pairs, const int64_t* ubase,
+                   const int32_t* q_rows,
                    const int32_t* p_rows, const uint16_t* Xh, const float* nrm, const unsigned int* sq, int Dp,
                    int metric, const float* seed_d, int seed_ld, int M, int wtiles, float* tq, int32_t* union_rows,
                    WorkItem* items_out, unsigned long long* pairs_done, hipStream_t s);
@@ -275,7 +276,7 @@ enum Ws {
     W_OOC_A, W_OOC_B, W_OOC_C, W_OOC_D, W_OOC_E, W_OOC_F, W_OOC_G, W_CR, W_CRNORMS,
     W_KM_TRAIN, W_KM_MIND, W_KM_FLAG, W_KM_SEL, W_KM_POS, W_KM_SUMS, W_KM_NEW, W_KM_PSI, W_KM_P, W_KM_PN, W_KM_P8,
     W_KM_PN8, W_KM_OI, W_KM_OD, W_CH8, W_CHN, W_CHR, W_CHCNT, W_PAIRS, W_TOP2A, W_TOP2B, W_BUCKETD, W_KEY2,
-    W_BYKEY, W_BKTD, W_BOFF, W_SUBPOS, W_TOP2H, W_RV1, W_RV1M, W_XH, W_UBASE, W_UROWS, W_UITEMS, W_TQ, W_SQ, W_COUNT_
+    W_BYKEY, W_BKTD, W_BOFF, W_SUBPOS, W_TOP2H, W_RV1, W_RV1M, W_XH, W_UBASE, W_UROWS, W_UITEMS, W_TQ, W_SQ, W_PAIRS2, W_COUNT_
 };
 static_assert(W_COUNT_ <= 112, "workspace slots");
 
@@ -1201,6 +1202,8 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
     WorkItem* d_uitems = nullptr;
     uint16_t* d_xh = nullptr;
     float* d_tq = nullptr;
+    int32_t* d_pairs = nullptr;
+    int n_pairs = 0;
     if (screen) {
         std::vector<int64_t> ub(items.size(), 0);
         int64_t u = 0;
@@ -1217,6 +1220,27 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
             d_xh = c.ws<uint16_t>(W_XH, static_cast<size_t>(N) * X.Dp);
             a.items = d_uitems;
             a.p_rows = d_urows;
+            // the screen's pairs: consecutive items with queries and the same
+            // pool (a bucket's items sit together), padded to a multiple of 8
+            std::vector<int32_t> pr;
+            int32_t held = -1;
+            for (size_t i = 0; i < items.size(); ++i) {
+                if (items[i].q_count <= 0) continue;
+                if (held >= 0 && items[static_cast<size_t>(held)].p_begin == items[i].p_begin &&
+                    items[static_cast<size_t>(held)].p_count == items[i].p_count) {
+                    pr.push_back(held);
+                    pr.push_back(static_cast<int32_t>(i));
+                    held = -1;
+                } else {
+                    if (held >= 0) { pr.push_back(held); pr.push_back(-1); }
+                    held = static_cast<int32_t>(i);
+                }
+            }
+            if (held >= 0) { pr.push_back(held); pr.push_back(-1); }
+            while ((pr.size() / 2) % 8 != 0) { pr.push_back(-1); pr.push_back(-1); }
+            n_pairs = static_cast<int>(pr.size() / 2);
+            d_pairs = c.ws<int32_t>(W_PAIRS2, std::max<size_t>(pr.size(), 2));
+            c.h2d(d_pairs, pr.data(), pr.size() * sizeof(int32_t));
             // an unseeded pass's bounds serve the screen only: the fp32 pass
             // takes its own (exact, tighter) window from each union,
             // rotated to the queries' own rows
@@ -1257,7 +1281,8 @@ static double bucketed_round(Ctx& c, const DevMatrix& X, const Buckets& b, int M
                 c.c->screen_gen = c.c->data_gen;
                 c.c->screen_src = X.data;
             }
-            launch_screen(d_items, a.n_items, d_ubase, d_members, d_pool, d_xh, X.norms, d_sq, X.Dp, metric, seed_d, M, M,
+            launch_screen(d_items, a.n_items, d_pairs, n_pairs, d_ubase, d_members, d_pool, d_xh, X.norms, d_sq, X.Dp,
+                          metric, seed_d, M, M,
                           screen_window, d_tq, d_urows, d_uitems, a.pairs_done, c.s);
         }
         if (collect) launch_knn_collect_select(a, rows, c.s);

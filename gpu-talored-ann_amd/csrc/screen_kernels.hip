@@ -124,7 +124,8 @@ __global__ void __launch_bounds__(256) screen_f16_kernel(const float4* __restric
 // into word t of the item's LDS bitmap; the set bits, in pool order, become
 // the item's union at union_rows[ubase[item] ...).
 template <int DP, int METRIC, bool WINDOW>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WINDOW || DP > 128 ? 2 : 4))) knn_screen_kernel(const WorkItem* __restrict__ items,
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(WINDOW || DP > 128 ? 2 : 4))) knn_screen_kernel(const WorkItem* __restrict__ items,
+                                                         const int32_t* __restrict__ pairs,
                                                          const int64_t* __restrict__ ubase,
                                                          const int32_t* __restrict__ q_rows,
                                                          const int32_t* __restrict__ p_rows,
@@ -140,7 +141,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WINDOW
     constexpr int RS = DP + 8;           // LDS row stride (fp16 elements): rows on distinct bank groups
     constexpr int U4_ROW = DP / 8;       // 16-byte pieces per row
     constexpr int U4_TILE = kPoolTile * U4_ROW;
-    constexpr int U4_THREAD = (U4_TILE + 255) / 256;
+    constexpr int NT = WINDOW ? 256 : 512;           // threads: one item, or a pair sharing the pool
+    constexpr int U4_THREAD = (U4_TILE + NT - 1) / NT;
     constexpr int WPT = kScreenMaxPool / 32 / 256;   // bitmap words per thread in the compaction
     static_assert(DP % 16 == 0 && kPoolTile == 32, "fp16 steps of 16 dims, one bitmap word per tile");
     __shared__ __align__(16) uint16_t tile[2][kPoolTile][RS];
@@ -148,29 +150,39 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WINDOW
     __shared__ __align__(16) float tpm[2][kPoolTile];   // -(1 - R) |p|^2
     __shared__ __align__(16) float tpu[2][kPoolTile];   // (1 + R) |p|^2
     __shared__ __align__(16) int32_t trow[2][kPoolTile];   // row id, -1 past the pool's end
-    __shared__ uint32_t bits[kScreenMaxPool / 32];
-    __shared__ uint32_t wsum[kWaves];
-    __shared__ uint32_t urot;
+    __shared__ uint32_t bits[2][kScreenMaxPool / 32];   // per item of the pair
+    __shared__ uint32_t wsum[2][kWaves];
+    __shared__ uint32_t urot[2];
 
-    // the items are laid out XCD by XCD (n_items / 8 each, a bucket's items
-    // together): block b runs item (b mod 8) n_items / 8 + b / 8, so the
-    // blocks one XCD runs share their pools in its L2
+    // the items (window) or pairs (admission) are laid out XCD by XCD (an
+    // eighth each, a bucket's together): block b runs entry
+    // (b mod 8) (n / 8) + b / 8, so the blocks one XCD runs share their pools
+    // in its L2.  An admission block runs two items of one pool (waves 0-3
+    // the first, 4-7 the second), each staged pool tile serving both.
     const int per = static_cast<int>(gridDim.x) / 8;
-    const int item_idx = static_cast<int>(blockIdx.x % 8) * per + static_cast<int>(blockIdx.x / 8);
-    const WorkItem it = items[item_idx];
+    const int entry = static_cast<int>(blockIdx.x % 8) * per + static_cast<int>(blockIdx.x / 8);
     const int tid = threadIdx.x;
-    if (it.q_count <= 0) {   // padding
-        if (!WINDOW && tid == 0) items_out[item_idx] = it;
-        return;
-    }
     const int w = tid >> 6, lane = tid & 63, j = lane & 31, h = lane >> 5;
-    const int pc = it.p_count;
+    const int half = WINDOW ? 0 : w >> 2, wq = w & 3;
+    int item_idx, pool_idx;
+    if constexpr (WINDOW) {
+        item_idx = pool_idx = entry;
+    } else {
+        pool_idx = pairs[2 * entry];
+        item_idx = pairs[2 * entry + half];
+        if (pool_idx < 0) return;   // padding
+    }
+    const WorkItem pool = items[pool_idx];
+    const WorkItem it = items[item_idx >= 0 ? item_idx : pool_idx];
+    const int nq = item_idx >= 0 ? it.q_count : 0;   // 0: the pair's missing second item
+    if (WINDOW && nq <= 0) return;   // padding
+    const int pc = pool.p_count;
     const int ntiles = (pc + kPoolTile - 1) / kPoolTile;
     if (!WINDOW)
-        for (int i = tid; i < ntiles; i += 256) bits[i] = 0u;
+        for (int i = tid; i < ntiles; i += NT) bits[0][i] = bits[1][i] = 0u;
 
-    const int qlocal = w * kQueriesPerWave + j;
-    const bool qvalid = qlocal < it.q_count;
+    const int qlocal = wq * kQueriesPerWave + j;
+    const bool qvalid = qlocal < nq;
     const int64_t qi = it.q_begin + qlocal;
     const int32_t qrow = qvalid ? (q_rows ? q_rows[qi] : static_cast<int32_t>(qi)) : 0;
     const int64_t orow = it.out_base >= 0 ? it.out_base + qlocal : static_cast<int64_t>(qrow);
@@ -211,12 +223,12 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WINDOW
         if (p >= pc) return -1;
         p += rot;
         if (p >= pc) p -= pc;
-        return p_rows[it.p_begin + p];
+        return p_rows[pool.p_begin + p];
     };
     auto fetch_ids = [&](int t, int rot) __attribute__((always_inline)) {
 #pragma unroll
         for (int u = 0; u < U4_THREAD; ++u) {
-            const int e = tid + 256 * u;
+            const int e = tid + NT * u;
             idq[u] = e < U4_TILE ? pos_row(t, e / U4_ROW, rot) : -1;
         }
         if (tid < kPoolTile) ridq = pos_row(t, tid, rot);
@@ -224,7 +236,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WINDOW
     auto load_into = [&](Set& S) __attribute__((always_inline)) {
 #pragma unroll
         for (int u = 0; u < U4_THREAD; ++u) {
-            const int e = tid + 256 * u;
+            const int e = tid + NT * u;
             S.v[u] = idq[u] >= 0 ? reinterpret_cast<const uint4*>(Xh + static_cast<int64_t>(idq[u]) * DP)[e % U4_ROW]
                                  : make_uint4(0u, 0u, 0u, 0u);
         }
@@ -236,7 +248,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WINDOW
     auto store_from = [&](const Set& S, int buf) __attribute__((always_inline)) {
 #pragma unroll
         for (int u = 0; u < U4_THREAD; ++u) {
-            const int e = tid + 256 * u;
+            const int e = tid + NT * u;
             if (e < U4_TILE) *reinterpret_cast<uint4*>(&tile[buf][e / U4_ROW][8 * (e % U4_ROW)]) = S.v[u];
         }
         if (tid < kPoolTile) {
@@ -372,14 +384,16 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WINDOW
         uint32_t tm = static_cast<uint32_t>(m) | static_cast<uint32_t>(m >> 32);   // bit j: pool row j
         const int left = pc - t * kPoolTile;
         if (left < kPoolTile) tm &= (1u << left) - 1u;
-        if (lane == 0 && tm) atomicOr(&bits[t], tm);
+        if (lane == 0 && tm) atomicOr(&bits[half][t], tm);
     });
-    // the set bits, in order, as row ids
+    // the set bits of each item's bitmap, in order, as row ids (threads
+    // 256 half .. 256 half + 255 for item half)
+    const int th = tid & 255;
     uint32_t cnt = 0u;
 #pragma unroll
     for (int u = 0; u < WPT; ++u) {
-        const int wi = tid * WPT + u;
-        cnt += wi < ntiles ? static_cast<uint32_t>(__popc(bits[wi])) : 0u;
+        const int wi = th * WPT + u;
+        cnt += wi < ntiles ? static_cast<uint32_t>(__popc(bits[half][wi])) : 0u;
     }
     uint32_t inc = cnt;
 #pragma unroll
@@ -387,35 +401,36 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WINDOW
         const uint32_t x = __shfl_up(inc, o);
         if (lane >= o) inc += x;
     }
-    if (lane == 63) wsum[w] = inc;
+    if (lane == 63) wsum[half][wq] = inc;
     __syncthreads();
     uint32_t off = inc - cnt;
-    for (int q = 0; q < w; ++q) off += wsum[q];
+    for (int q = 0; q < wq; ++q) off += wsum[half][q];
     // the union's rotation: its first row at or after the item's rotation
     // (an unseeded fp32 pass takes its threshold window from there)
     const int wr = it.p_rot >> 5;
-    if (pc > 0 && tid == wr / WPT) {
+    if (item_idx >= 0 && pc > 0 && th == wr / WPT) {
         uint32_t r = off;
-        for (int wi = tid * WPT; wi < wr; ++wi) r += static_cast<uint32_t>(__popc(bits[wi]));
-        urot = r + static_cast<uint32_t>(__popc(bits[wr] & ((1u << (it.p_rot & 31)) - 1u)));
+        for (int wi = th * WPT; wi < wr; ++wi) r += static_cast<uint32_t>(__popc(bits[half][wi]));
+        urot[half] = r + static_cast<uint32_t>(__popc(bits[half][wr] & ((1u << (it.p_rot & 31)) - 1u)));
     }
     __syncthreads();
+    if (item_idx < 0) return;
     const int64_t base = ubase[item_idx];
 #pragma unroll
     for (int u = 0; u < WPT; ++u) {
-        const int wi = tid * WPT + u;
-        uint32_t b = wi < ntiles ? bits[wi] : 0u;
+        const int wi = th * WPT + u;
+        uint32_t b = wi < ntiles ? bits[half][wi] : 0u;
         while (b) {
             const int k = __ffs(b) - 1;
             b &= b - 1u;
-            union_rows[base + off++] = p_rows[it.p_begin + wi * 32 + k];
+            union_rows[base + off++] = p_rows[pool.p_begin + wi * 32 + k];
         }
     }
-    if (tid == 0) {
+    if (th == 0) {
         WorkItem o = it;
         o.p_begin = base;
-        o.p_count = static_cast<int32_t>(wsum[0] + wsum[1] + wsum[2] + wsum[3]);
-        o.p_rot = pc > 0 && static_cast<int32_t>(urot) < o.p_count ? static_cast<int32_t>(urot) : 0;
+        o.p_count = static_cast<int32_t>(wsum[half][0] + wsum[half][1] + wsum[half][2] + wsum[half][3]);
+        o.p_rot = pc > 0 && static_cast<int32_t>(urot[half]) < o.p_count ? static_cast<int32_t>(urot[half]) : 0;
         items_out[item_idx] = o;
         if (pairs_done)
             atomicAdd(pairs_done, static_cast<unsigned long long>(o.p_count) * static_cast<unsigned>(o.q_count));
@@ -446,7 +461,10 @@ void launch_screen_prepare(const float* X, const float* nrm, int64_t N, int Dp, 
 }
 
 // items: n_items work items of a pass (every pool at most kScreenMaxPool
-// rows); ubase[i]: item i's first slot of union_rows, which holds at least
+// rows); pairs: n_pairs entries (first item, second item or -1; -1, -1 for
+// padding) pairing every item that has queries with at most one other item
+// of the same pool, laid out like the items; ubase[i]: item i's first slot
+// of union_rows, which holds at least
 // its pool count from there; items_out: the items with their unions as pools
 // (rotated to the union's first row at or after the item's rotation).  Xh:
 // the scaled fp16 rows (stride Dp) of the matrix the q_rows and p_rows
@@ -457,25 +475,30 @@ void launch_screen_prepare(const float* X, const float* nrm, int64_t N, int Dp, 
 // written to tq (one per output row: the pool's M-th smallest fp32 key is at
 // or below it).  pairs_done (optional) += the (query, union row) pairs left
 // to the fp32 pass.
-void launch_screen(const WorkItem* items, int n_items, const int64_t* ubase, const int32_t* q_rows,
+void launch_screen(const WorkItem* items, int n_items, const int32_t* pairs, int n_pairs, const int64_t* ubase,
+                   const int32_t* q_rows,
                    const int32_t* p_rows, const uint16_t* Xh, const float* nrm, const unsigned int* sq, int Dp,
                    int metric, const float* seed_d, int seed_ld, int M, int wtiles, float* tq, int32_t* union_rows,
                    WorkItem* items_out, unsigned long long* pairs_done, hipStream_t s)
 {
     GT_REQUIRE(screen_supported(Dp, 0), "screen: padded dimension not supported");
-    GT_REQUIRE(n_items % 8 == 0, "screen: work list must be padded to a multiple of 8 (one eighth per XCD)");
+    GT_REQUIRE(n_items % 8 == 0 && n_pairs % 8 == 0, "screen: work lists must be padded to multiples of 8 (one eighth per XCD)");
+    GT_REQUIRE(pairs != nullptr, "screen: item pairs missing");
+    // the items without a pair entry (padding) keep their pools
+    GT_HIP(hipMemcpyAsync(items_out, items, static_cast<size_t>(n_items) * sizeof(WorkItem), hipMemcpyDeviceToDevice, s));
     GT_REQUIRE(seed_d ? seed_ld > 0 : (tq && M > 4 && M <= 64 && wtiles > 0), "screen: seed or window missing");
     if (n_items <= 0) return;
 #define GT_SCR(DPV, MET)                                                                                      \
     do {                                                                                                      \
         if (!seed_d)                                                                                          \
             hipLaunchKernelGGL((knn_screen_kernel<DPV, MET, true>), dim3(n_items), dim3(256), 0, s, items,    \
-                               ubase, q_rows, p_rows, Xh, nrm, sq, seed_d, seed_ld, M, wtiles, tq, union_rows,    \
-                               items_out, pairs_done);                                                        \
+                               nullptr, ubase, q_rows, p_rows, Xh, nrm, sq, seed_d, seed_ld, M, wtiles, tq,    \
+                               union_rows, items_out, pairs_done);                                            \
         const float* sd = seed_d ? seed_d : tq;                                                               \
         const int sl = seed_d ? seed_ld : 1;                                                                  \
-        hipLaunchKernelGGL((knn_screen_kernel<DPV, MET, false>), dim3(n_items), dim3(256), 0, s, items, ubase, \
-                           q_rows, p_rows, Xh, nrm, sq, sd, sl, M, wtiles, tq, union_rows, items_out, pairs_done); \
+        hipLaunchKernelGGL((knn_screen_kernel<DPV, MET, false>), dim3(n_pairs), dim3(512), 0, s, items, pairs, \
+                           ubase, q_rows, p_rows, Xh, nrm, sq, sd, sl, M, wtiles, tq, union_rows, items_out,    \
+                           pairs_done);                                                                       \
     } while (0)
 #define GT_SCR_M(DPV)                     \
     do {                                  \
