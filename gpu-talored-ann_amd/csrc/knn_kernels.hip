@@ -1058,11 +1058,6 @@ knn_i8_resident_kernel(KnnArgs a, int64_t nq, int64_t npool, int pc)   // npool 
 // reads its 32 queries' chunk into registers, and the block's four 32x32
 // accumulator tiles are filtered once the last chunk is in.  Query rows are
 // re-read once per 128 pool rows (from L2 / Infinity Cache).
-__device__ __forceinline__ float4 keep_or_zero(bool keep, float4 v)
-{
-    return make_float4(keep ? v.x : 0.f, keep ? v.y : 0.f, keep ? v.z : 0.f, keep ? v.w : 0.f);
-}
-
 constexpr int kWideRows = 128;   // pool rows per super-tile
 constexpr int kWideChunk = 32;   // dimensions per chunk
 
@@ -1132,11 +1127,15 @@ __global__ void __launch_bounds__(256, 2) knn_wide_kernel(KnnArgs a)
     auto load_pool = [&](bool next, int c) {
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            // branch-free: rows past the slice read row 0 and are zeroed
+            // rows past the slice stage row 0's values: their norm is +inf and
+            // their id -1, so no key of theirs reaches a list (each accumulator
+            // element is one pair's own dot product).  Not zeroing them leaves
+            // the loads' results untouched until the LDS store at the chunk's
+            // end, and the MFMAs run while they are in flight.
             const int32_t id = next ? rid_n[u] : rid[u];
             const float4 v = *reinterpret_cast<const float4*>(a.Xp + static_cast<int64_t>(id >= 0 ? id : 0) * Dp +
                                                               c * kWideChunk + 4 * c4);
-            pre[u] = keep_or_zero(id >= 0, v);
+            pre[u] = make_float4(v.x, v.y, v.z, v.w);   // a value, not a copy through private memory
         }
     };
     auto store_pool = [&](int buf) {
@@ -1148,9 +1147,9 @@ __global__ void __launch_bounds__(256, 2) knn_wide_kernel(KnnArgs a)
     float4 qc[4], qx[4];
     auto load_q = [&](int c, float4 (&dst)[4]) {
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            const float4 v = *reinterpret_cast<const float4*>(qsrc + c * kWideChunk + 4 * s);   // qrow 0 if invalid
-            dst[s] = keep_or_zero(qvalid, v);
+        for (int s = 0; s < 4; ++s) {   // row 0 for an invalid query: its column is never read
+            const float4 v = *reinterpret_cast<const float4*>(qsrc + c * kWideChunk + 4 * s);
+            dst[s] = make_float4(v.x, v.y, v.z, v.w);
         }
     };
 
@@ -1183,9 +1182,14 @@ __global__ void __launch_bounds__(256, 2) knn_wide_kernel(KnnArgs a)
         for (int c = 0; c < nch; ++c) {
             const int buf = g & 1;
             const bool last = c + 1 == nch;
-            const bool more = !last || stile + 1 < nst;
-            if (more) load_pool(last, last ? 0 : c + 1);
+            // the item's last chunk stages row 0 (the ids past the last
+            // super-tile are -1) into the buffer no wave reads again
+            load_pool(last, last ? 0 : c + 1);
             load_q(last ? 0 : c + 1, qx);
+            // the next chunk's loads stay ahead of this chunk's MFMAs (left
+            // to itself the scheduler sinks them below the MFMAs, and the LDS
+            // store then waits out their whole latency every chunk)
+            __builtin_amdgcn_sched_barrier(0);
             // A = pool row u*32 + (lane%32), B = query lane%32, k = dims h*16 + s.
             // Each chunk is summed on its own and added to the running dot:
             // the rounding error grows with sqrt(chunks) instead of sqrt(D/2).
@@ -1210,7 +1214,7 @@ __global__ void __launch_bounds__(256, 2) knn_wide_kernel(KnnArgs a)
             for (int u = 0; u < 4; ++u)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) acc[u][r] += part[u][r];
-            if (more) store_pool(buf ^ 1);
+            store_pool(buf ^ 1);
             __syncthreads();
 #pragma unroll
             for (int s = 0; s < 4; ++s) qc[s] = qx[s];
